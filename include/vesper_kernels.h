@@ -1,0 +1,75 @@
+/* C ABI of the MI355X (gfx950) column sequence mixers: the delta-rule scan and sliding-window
+ * causal attention of Vesper's column, as hand-written HIP kernels.
+ *
+ * Conventions shared by every entry point:
+ *  - Pointers are device pointers to contiguous row-major tensors; sizes are element counts.
+ *  - `stream` is a hipStream_t (NULL = the null stream). Work is enqueued only: no host
+ *    synchronisation, no device-to-host reads and no device allocation happen inside, so every
+ *    call can be captured into a HIP graph. Scratch memory, where a kernel needs it, is passed in.
+ *  - Inputs are never written; outputs may alias their matching input only where stated.
+ *  - `active` (optional, may be NULL) is a uint8 mask [B, T] (1 = active token). Inactive tokens
+ *    still write the recurrent state and stay visible as keys; their outputs are written as 0.
+ *  - Return 0 on success, otherwise a nonzero status with a message in vsp_last_error().
+ *  - Results are bitwise repeatable: no atomics take part in any reduction.
+ */
+#ifndef VESPER_KERNELS_H
+#define VESPER_KERNELS_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define VSP_ABI_VERSION 1
+
+/* Status codes. */
+#define VSP_OK 0
+#define VSP_ERR_ARG 1         /* a size, pointer or combination the kernels do not take */
+#define VSP_ERR_UNSUPPORTED 2 /* a valid request this build has no kernel for */
+#define VSP_ERR_LAUNCH 3      /* the HIP runtime refused the launch */
+
+/* The message of the last failed call on this thread ("" after a success). */
+const char* vsp_last_error(void);
+
+/* VSP_ABI_VERSION of the loaded library. */
+int vsp_abi_version(void);
+
+/* ---- delta-rule scan ------------------------------------------------------------------------
+ * Per batch row b and head h, with the state H [D, D] read as H^T q, each token applies
+ *     H <- (I - beta k k^T) H + beta k v^T,    o = H^T q
+ * q, k, v: [B, T, H, D]; beta: [B, T, H]; state_in, state_out: [B, H, D, D] float32 (may alias).
+ * No query scaling, no in-kernel key normalisation (keys arrive with L2 norm at most one).
+ * Replaces the fla-core 0.5.2 calls behind vesper/kernels/delta_scan.py:122-129 (`_run`):
+ * `chunk_delta_rule` for the bf16 entry (delta_scan.py:132-153) and
+ * `fused_recurrent_delta_rule` for the fp32 entry (delta_scan.py:156-187).
+ * D <= 256. D in {16, 32, 64, 128} runs the chunked WY/UT MFMA path (64-token chunks); other
+ * widths, and T below 16, run the token-serial kernel.
+ * `workspace` holds the per-chunk UT matrices of the chunked path; it needs
+ * vsp_delta_scan_workspace_bytes(...) bytes (0 when the serial path runs; then it may be NULL). */
+size_t vsp_delta_scan_workspace_bytes(int B, int T, int H, int D, int fp32_inputs);
+
+/* bf16 q, k, v, beta; float32 state; bf16 o. */
+int vsp_delta_scan_bf16(const void* q, const void* k, const void* v, const void* beta, const float* state_in,
+                        void* o, float* state_out, void* workspace, size_t workspace_bytes,
+                        const uint8_t* active, int B, int T, int H, int D, void* stream);
+
+/* float32 q, k, v, beta, state and o. */
+int vsp_delta_scan_f32(const float* q, const float* k, const float* v, const float* beta, const float* state_in,
+                       float* o, float* state_out, void* workspace, size_t workspace_bytes,
+                       const uint8_t* active, int B, int T, int H, int D, void* stream);
+
+/* One decoding token per row (the contract of vesper/recurrence.py:143-163, delta_scan_step):
+ * q, k, v: [B, H, D]; beta: [B, H]; state_in, state_out: [B, H, D, D] float32 (may alias, for an
+ * in-place decode); o: [B, H, D]; active: [B] or NULL. */
+int vsp_delta_step_f32(const float* q, const float* k, const float* v, const float* beta, const float* state_in,
+                       float* state_out, float* o, const uint8_t* active, int B, int H, int D, void* stream);
+int vsp_delta_step_bf16(const void* q, const void* k, const void* v, const void* beta, const float* state_in,
+                        float* state_out, void* o, const uint8_t* active, int B, int H, int D, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* VESPER_KERNELS_H */

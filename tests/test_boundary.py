@@ -1,0 +1,81 @@
+"""CPU checks of the boundary: the C-ABI library loads and exports what its header declares, and
+the Python entry points refuse what the contract excludes before any kernel runs."""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+BF16 = torch.bfloat16
+
+
+def test_the_library_exports_every_declared_symbol():
+    from vesper.kernels import _lib
+
+    lib = _lib.library()
+    declared = _lib.header_symbols()
+    assert "vsp_delta_scan_bf16" in declared and "vsp_last_error" in declared
+    for name in declared:
+        assert hasattr(lib, name), name
+        assert name in _lib.SIGNATURES, f"{name} has no ctypes signature"
+    assert lib.vsp_abi_version() == _lib.ABI_VERSION
+
+
+def test_the_workspace_size_covers_every_chunk():
+    from vesper.kernels import _lib
+
+    lib = _lib.library()
+    assert lib.vsp_delta_scan_workspace_bytes(8, 4096, 8, 64, 0) == 8 * 8 * 64 * 64 * 64 * 2
+    assert lib.vsp_delta_scan_workspace_bytes(2, 130, 3, 16, 1) == 2 * 3 * 3 * 64 * 64 * 4
+    assert lib.vsp_delta_scan_workspace_bytes(2, 130, 3, 48, 1) == 0  # token-serial width
+    assert lib.vsp_delta_scan_workspace_bytes(2, 10, 3, 64, 0) == 0  # short sequences are serial
+
+
+def test_a_bad_size_is_an_error_status_not_a_crash():
+    from vesper.kernels import _lib
+
+    lib = _lib.library()
+    status = lib.vsp_delta_scan_f32(None, None, None, None, None, None, None, None, 0, None, 1, 8, 1, 300, None)
+    assert status == 1
+    assert "head dimension 300" in lib.vsp_last_error().decode()
+
+
+def test_refuses_a_cpu_tensor_before_touching_the_kernel():
+    from vesper.contracts import ContractError
+    from vesper.kernels.delta_scan import delta_scan_fused, delta_scan_fused_fp32, delta_scan_step_fused
+
+    z = torch.zeros(1, 4, 1, 8, dtype=BF16)
+    with pytest.raises(ContractError, match="CUDA only"):
+        delta_scan_fused(z, z, z, torch.zeros(1, 4, 1, dtype=BF16), torch.zeros(1, 1, 8, 8))
+    z = torch.zeros(1, 4, 1, 8)
+    with pytest.raises(ContractError, match="CUDA only"):
+        delta_scan_fused_fp32(z, z, z, torch.zeros(1, 4, 1), torch.zeros(1, 1, 8, 8))
+    z = torch.zeros(1, 1, 8)
+    with pytest.raises(ContractError, match="CUDA only"):
+        delta_scan_step_fused(z, z, z, torch.zeros(1, 1), torch.zeros(1, 1, 8, 8))
+
+
+def test_shape_and_dtype_refusals_come_first():
+    from vesper.contracts import ContractError
+    from vesper.kernels.delta_scan import MAX_HEAD_DIM, delta_scan_fused
+
+    assert MAX_HEAD_DIM == 256
+    z = torch.zeros(1, 4, 1, 8, dtype=BF16)
+    with pytest.raises(ContractError, match="dtype"):
+        delta_scan_fused(z.float(), z, z, torch.zeros(1, 4, 1, dtype=BF16), torch.zeros(1, 1, 8, 8))
+    with pytest.raises(ContractError, match="axis"):
+        delta_scan_fused(z, z[:, :2], z, torch.zeros(1, 4, 1, dtype=BF16), torch.zeros(1, 1, 8, 8))
+
+
+def test_the_product_path_does_not_import_the_oracle():
+    import subprocess
+    import sys
+
+    from conftest import PACKAGE_ROOT
+
+    code = (
+        "import sys; sys.path.insert(0, %r); import vesper.kernels.delta_scan, vesper.kernels._lib; "
+        "print(any(m == 'oracle' or m.startswith('oracle.') for m in sys.modules))" % str(PACKAGE_ROOT)
+    )
+    out = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, check=True)
+    assert out.stdout.strip() == "False"

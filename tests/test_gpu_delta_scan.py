@@ -1,0 +1,242 @@
+"""The HIP delta scan (``vesper.kernels.delta_scan``) against the CPU oracle, through the C ABI.
+
+The oracle in float64, fed the same bf16- (or fp32-) valued inputs, is the truth. Tolerances are
+the reference's own (``tests/test_delta_scan_fused.py:34``, ``:255``): relative Frobenius error
+below 1.5e-2 for the bf16 kernel and 1e-5 for the fp32 kernel, on outputs and final states.
+"""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+from conftest import needs_gpu, scan_inputs
+from oracle.delta import delta_scan_chunked, delta_scan_step, normalize_keys, relative_error
+
+pytestmark = [pytest.mark.gpu, needs_gpu]
+
+BF16 = torch.bfloat16
+TOL = 1.5e-2
+TOL_FP32 = 1e-5
+GPU = torch.device("cuda")
+
+# n = 1, one short of a chunk, one past it, two and a partial, 4096 (tests/test_delta_scan_fused.py:71)
+SIZES = [(2, 1, 2, 16), (2, 63, 3, 16), (1, 65, 2, 64), (2, 130, 3, 16), (1, 4096, 2, 64)]
+
+
+def _bf16_inputs(b, n, h, dk, seed=0):
+    q, k, v, beta, h0 = scan_inputs(b, n, h, dk, seed)
+    return [t.to(GPU, BF16) for t in (q, k, v, beta)] + [h0.to(GPU)]
+
+
+def _fp32_inputs(b, n, h, dk, seed=0):
+    q, k, v, beta, h0 = scan_inputs(b, n, h, dk, seed)
+    q, k, v, beta = (t.to(BF16).float() for t in (q, k, v, beta))
+    g = torch.Generator().manual_seed(seed + 100)  # values the bf16 grid cannot hold
+    q = q + 1e-3 * torch.randn(q.shape, generator=g)
+    k = normalize_keys(k + 1e-3 * torch.randn(k.shape, generator=g))
+    v = v + 1e-3 * torch.randn(v.shape, generator=g)
+    return [t.to(GPU) for t in (q, k, v, beta, h0)]
+
+
+def _oracle(q, k, v, beta, h0, active=None):
+    cpu = [t.detach().double().cpu() for t in (q, k, v, beta, h0)]
+    return delta_scan_chunked(*cpu, block=64, active=None if active is None else active.cpu())
+
+
+@pytest.mark.parametrize(("b", "n", "h", "dk"), SIZES)
+def test_bf16_forward_and_state_match_the_oracle(b, n, h, dk):
+    from vesper.kernels.delta_scan import delta_scan_fused
+
+    q, k, v, beta, h0 = _bf16_inputs(b, n, h, dk)
+    o_ref, s_ref = _oracle(q, k, v, beta, h0)
+    o, s = delta_scan_fused(q, k, v, beta, h0)
+    torch.cuda.synchronize()
+    assert o.dtype == BF16 and s.dtype == torch.float32
+    assert relative_error(o, o_ref) < TOL
+    assert relative_error(s, s_ref) < TOL
+
+
+@pytest.mark.parametrize(("b", "n", "h", "dk"), SIZES)
+def test_fp32_forward_and_state_match_the_oracle(b, n, h, dk):
+    from vesper.kernels.delta_scan import delta_scan_fused_fp32
+
+    q, k, v, beta, h0 = _fp32_inputs(b, n, h, dk)
+    o_ref, s_ref = _oracle(q, k, v, beta, h0)
+    o, s = delta_scan_fused_fp32(q, k, v, beta, h0)
+    torch.cuda.synchronize()
+    assert (o.dtype, s.dtype) == (torch.float32, torch.float32)
+    assert relative_error(o, o_ref) < TOL_FP32
+    assert relative_error(s, s_ref) < TOL_FP32
+
+
+@pytest.mark.parametrize("dk", [8, 16, 24, 32, 48, 64, 100, 128, 192, 256])
+@pytest.mark.parametrize("n", [5, 70])
+def test_every_head_width_up_to_the_bound(dk, n):
+    # chunked widths (16/32/64/128) and the token-serial kernel for the rest
+    from vesper.kernels.delta_scan import delta_scan_fused, delta_scan_fused_fp32
+
+    q, k, v, beta, h0 = _fp32_inputs(2, n, 2, dk, seed=dk)
+    o_ref, s_ref = _oracle(q, k, v, beta, h0)
+    o, s = delta_scan_fused_fp32(q, k, v, beta, h0)
+    assert relative_error(o, o_ref) < TOL_FP32 and relative_error(s, s_ref) < TOL_FP32
+    qb, kb, vb, bb, h0b = _bf16_inputs(2, n, 2, dk, seed=dk)
+    o_ref, s_ref = _oracle(qb, kb, vb, bb, h0b)
+    o, s = delta_scan_fused(qb, kb, vb, bb, h0b)
+    assert relative_error(o, o_ref) < TOL and relative_error(s, s_ref) < TOL
+
+
+def test_parity_config_fp32_b2_t512_h4_d64_zero_state():
+    # B=2, T=512, H=4, d=64, chunk 64, q and k L2-normalised, zero initial state
+    from vesper.kernels.delta_scan import delta_scan_fused_fp32
+
+    g = torch.Generator().manual_seed(0)
+    q = normalize_keys(torch.randn(2, 512, 4, 64, generator=g))
+    k = normalize_keys(torch.randn(2, 512, 4, 64, generator=g))
+    v = torch.randn(2, 512, 4, 64, generator=g)
+    beta = torch.sigmoid(torch.randn(2, 512, 4, generator=g))
+    h0 = torch.zeros(2, 4, 64, 64)
+    o_ref, s_ref = delta_scan_chunked(*(t.double() for t in (q, k, v, beta, h0)), block=64)
+    o, s = delta_scan_fused_fp32(*(t.to(GPU) for t in (q, k, v, beta, h0)))
+    assert relative_error(o, o_ref) < 1e-5
+    assert relative_error(s, s_ref) < 1e-5
+
+
+def test_prefill_config_bf16_b8_t4096_h8_d64_full_size():
+    # the headline prefill shape with a nonzero initial state S0 ~ N(0, 0.02^2)
+    from vesper.kernels.delta_scan import delta_scan_fused
+
+    g = torch.Generator().manual_seed(0)
+    q = normalize_keys(torch.randn(8, 4096, 8, 64, generator=g)).to(BF16)
+    k = normalize_keys(torch.randn(8, 4096, 8, 64, generator=g)).to(BF16)
+    v = torch.randn(8, 4096, 8, 64, generator=g).to(BF16)
+    beta = torch.sigmoid(torch.randn(8, 4096, 8, generator=g)).to(BF16)
+    h0 = 0.02 * torch.randn(8, 8, 64, 64, generator=g)
+    o, s = delta_scan_fused(*(t.to(GPU) for t in (q, k, v, beta, h0)))
+    o_ref, s_ref = delta_scan_chunked(*(t.float() for t in (q, k, v, beta, h0)), block=64)
+    assert relative_error(o, o_ref) < 2e-2
+    assert relative_error(s, s_ref) < 2e-2
+
+
+def test_a_carried_state_continues_the_sequence():
+    # 130 tokens at once against 50 then 80: the split falls inside a 64-token chunk
+    from vesper.kernels.delta_scan import delta_scan_fused, delta_scan_fused_fp32
+
+    for fn, make, tol in ((delta_scan_fused, _bf16_inputs, TOL), (delta_scan_fused_fp32, _fp32_inputs, TOL_FP32)):
+        q, k, v, beta, h0 = make(2, 130, 3, 16)
+        o_ref, s_ref = _oracle(q, k, v, beta, h0)
+        oa, sa = fn(q[:, :50], k[:, :50], v[:, :50], beta[:, :50], h0)
+        ob, sb = fn(q[:, 50:], k[:, 50:], v[:, 50:], beta[:, 50:], sa)
+        assert relative_error(torch.cat([oa, ob], 1), o_ref) < tol
+        assert relative_error(sb, s_ref) < tol
+
+
+def test_no_tokens_return_the_state_unchanged():
+    from vesper.kernels.delta_scan import delta_scan_fused, delta_scan_fused_fp32
+
+    q, k, v, beta, h0 = _bf16_inputs(2, 0, 3, 16)
+    o, s = delta_scan_fused(q, k, v, beta, h0)
+    assert o.shape == (2, 0, 3, 16) and s is h0
+    q, k, v, beta, h0 = _fp32_inputs(2, 0, 3, 16)
+    o, s = delta_scan_fused_fp32(q, k, v, beta, h0)
+    assert o is q and s is h0
+
+
+def test_refuses_what_the_contract_excludes():
+    from vesper.contracts import ContractError
+    from vesper.kernels.delta_scan import delta_scan_fused, delta_scan_fused_fp32
+
+    q, k, v, beta, h0 = _bf16_inputs(1, 8, 2, 16)
+    with pytest.raises(ContractError, match="dtype"):
+        delta_scan_fused(q.float(), k, v, beta, h0)
+    with pytest.raises(ContractError, match="dtype"):
+        delta_scan_fused(q, k, v, beta, h0.to(BF16))
+    with pytest.raises(ContractError, match="axis"):
+        delta_scan_fused(q, k[:, :4], v, beta, h0)
+    with pytest.raises(ContractError, match="is on cpu"):
+        delta_scan_fused(q, k, v, beta, h0.cpu())
+    wide = torch.zeros(1, 8, 1, 512, dtype=BF16, device=GPU)
+    with pytest.raises(ContractError, match="exceeds"):
+        delta_scan_fused(wide, wide, wide, torch.zeros(1, 8, 1, dtype=BF16, device=GPU),
+                         torch.zeros(1, 1, 512, 512, device=GPU))
+    with pytest.raises(ContractError, match="dtype"):
+        delta_scan_fused_fp32(q, k, v, beta, h0)
+    with pytest.raises(ContractError, match="forward only"):
+        delta_scan_fused(q.clone().requires_grad_(), k, v, beta, h0)
+
+
+def test_active_mask_zeroes_outputs_and_keeps_every_write():
+    from vesper.kernels.delta_scan import delta_scan_fused, delta_scan_fused_fp32
+
+    act = torch.rand(2, 130, generator=torch.Generator().manual_seed(5)) < 0.7
+    for fn, make, tol in ((delta_scan_fused, _bf16_inputs, TOL), (delta_scan_fused_fp32, _fp32_inputs, TOL_FP32)):
+        q, k, v, beta, h0 = make(2, 130, 3, 64)
+        o_ref, s_ref = _oracle(q, k, v, beta, h0, act)
+        o, s = fn(q, k, v, beta, h0, active=act.to(GPU))
+        o_all, s_all = fn(q, k, v, beta, h0)
+        assert torch.equal(s, s_all)
+        assert torch.equal(o[act.to(GPU)], o_all[act.to(GPU)])
+        assert bool((o[~act.to(GPU)] == 0).all())
+        assert relative_error(o, o_ref) < tol and relative_error(s, s_ref) < tol
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, BF16])
+@pytest.mark.parametrize("dk", [16, 64, 100])
+def test_the_decode_step_matches_the_oracle_step(dtype, dk):
+    from vesper.kernels.delta_scan import delta_scan_step_fused
+
+    g = torch.Generator().manual_seed(dk)
+    b, h = 5, 3
+    q = torch.randn(b, h, dk, generator=g).to(dtype)
+    k = normalize_keys(torch.randn(b, h, dk, generator=g)).to(dtype)
+    v = torch.randn(b, h, dk, generator=g).to(dtype)
+    beta = torch.sigmoid(torch.randn(b, h, generator=g)).to(dtype)
+    s0 = 0.5 * torch.randn(b, h, dk, dk, generator=g)
+    o_ref, s_ref = delta_scan_step(*(t.double() for t in (q, k, v, beta, s0)))
+    dev = [t.to(GPU) for t in (q, k, v, beta, s0)]
+    o, s = delta_scan_step_fused(*dev)
+    tol = 1e-6 if dtype == torch.float32 else 1e-2
+    assert relative_error(o, o_ref) < tol and relative_error(s, s_ref) < 1e-6
+    # in place: the new state overwrites the old one
+    state = dev[4].clone()
+    o2, s2 = delta_scan_step_fused(*dev[:4], state, out_state=state)
+    assert s2 is state and torch.equal(state, s) and torch.equal(o2, o)
+    act = torch.tensor([True, False, True, True, False], device=GPU)
+    o3, s3 = delta_scan_step_fused(*dev, active=act)
+    assert torch.equal(s3, s) and bool((o3[~act] == 0).all()) and torch.equal(o3[act], o[act])
+
+
+def test_bitwise_repeatable_and_exactly_linear_under_power_of_two_scaling():
+    # a size-independent property at the headline width: doubling v and S0 doubles o and S_n
+    # exactly (every rounding is scale-invariant under a power of two), and reruns are bitwise
+    from vesper.kernels.delta_scan import delta_scan_fused
+
+    q, k, v, beta, h0 = _bf16_inputs(2, 1000, 8, 64, seed=3)
+    o1, s1 = delta_scan_fused(q, k, v, beta, h0)
+    o2, s2 = delta_scan_fused(q, k, v, beta, h0)
+    assert torch.equal(o1, o2) and torch.equal(s1, s2)
+    o3, s3 = delta_scan_fused(q, k, 2 * v, beta, 2 * h0)
+    assert torch.equal(o3, 2 * o1) and torch.equal(s3, 2 * s1)
+
+
+def test_graph_replays_equal_the_eager_result():
+    from vesper.kernels.delta_scan import delta_scan_fused
+
+    q, k, v, beta, h0 = _bf16_inputs(2, 300, 4, 64, seed=9)
+    eager_o, eager_s = delta_scan_fused(q, k, v, beta, h0)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for _ in range(2):
+            delta_scan_fused(q, k, v, beta, h0)
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        got_o, got_s = delta_scan_fused(q, k, v, beta, h0)
+    for i in range(3):
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(got_o, eager_o), i
+        assert torch.equal(got_s, eager_s), i
+        _ = delta_scan_fused(q, k, v, beta, h0)  # eager work between replays
+        torch.cuda.synchronize()

@@ -1,0 +1,96 @@
+"""ctypes binding of ``libvesper_kernels.so``: the one place Python meets the C ABI.
+
+The library is the product path. It is loaded from this directory only; when it is missing or its
+ABI version differs, every kernel call raises ``KernelLibraryError`` - there is no fallback. torch
+is imported first so that its HIP runtime (``libamdhip64.so.7``) is the one the library binds to,
+and the streams handed over are torch's.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+
+import torch
+
+HERE = Path(__file__).resolve().parent
+LIBRARY_PATH = HERE / "libvesper_kernels.so"
+HEADER_PATH = HERE.parents[2] / "include" / "vesper_kernels.h"
+ABI_VERSION = 1
+
+P = ctypes.c_void_p
+I = ctypes.c_int
+Z = ctypes.c_size_t
+
+# every entry point of include/vesper_kernels.h: (return type, argument types)
+SIGNATURES: dict[str, tuple[object, list[object]]] = {
+    "vsp_last_error": (ctypes.c_char_p, []),
+    "vsp_abi_version": (I, []),
+    "vsp_delta_scan_workspace_bytes": (Z, [I, I, I, I, I]),
+    "vsp_delta_scan_bf16": (I, [P, P, P, P, P, P, P, P, Z, P, I, I, I, I, P]),
+    "vsp_delta_scan_f32": (I, [P, P, P, P, P, P, P, P, Z, P, I, I, I, I, P]),
+    "vsp_delta_step_f32": (I, [P, P, P, P, P, P, P, P, I, I, I, P]),
+    "vsp_delta_step_bf16": (I, [P, P, P, P, P, P, P, P, I, I, I, P]),
+}
+
+
+class KernelLibraryError(RuntimeError):
+    """The HIP kernel library is missing, stale, or a kernel call failed."""
+
+
+_LIB: ctypes.CDLL | None = None
+
+
+def library() -> ctypes.CDLL:
+    """The loaded library with every signature declared; raises if it is not built."""
+    global _LIB
+    if _LIB is not None:
+        return _LIB
+    if not LIBRARY_PATH.exists():
+        raise KernelLibraryError(
+            f"{LIBRARY_PATH} is not built: run `python -m vesper.kernels.build` (or __graft_entry__.build())"
+        )
+    lib = ctypes.CDLL(str(LIBRARY_PATH))
+    for name, (restype, argtypes) in SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.restype = restype
+        fn.argtypes = argtypes
+    version = lib.vsp_abi_version()
+    if version != ABI_VERSION:
+        raise KernelLibraryError(f"{LIBRARY_PATH} has ABI {version}, this package needs {ABI_VERSION}")
+    _LIB = lib
+    return lib
+
+
+def available() -> bool:
+    """Whether the library loads (it does on a machine without a GPU too)."""
+    try:
+        library()
+    except (KernelLibraryError, OSError):
+        return False
+    return True
+
+
+def header_symbols() -> list[str]:
+    """The function names declared in ``include/vesper_kernels.h``."""
+    text = HEADER_PATH.read_text(encoding="utf-8")
+    return sorted(set(re.findall(r"\b(vsp_[a-z0-9_]+)\s*\(", text)))
+
+
+def ptr(t: torch.Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def stream_of(device: torch.device) -> int:
+    """torch's current stream on ``device`` as a hipStream_t handle."""
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def call(name: str, *args: object) -> None:
+    """Call an entry point and turn a nonzero status into ``KernelLibraryError``."""
+    lib = library()
+    status = getattr(lib, name)(*args)
+    if status != 0:
+        message = lib.vsp_last_error().decode("utf-8", "replace")
+        raise KernelLibraryError(f"{name} returned {status}: {message}")

@@ -1,0 +1,114 @@
+// Shared device helpers for the CDNA4 (gfx950) mixer kernels: element conversions, MFMA tile
+// products with their operand fragment layouts, wave reductions, and the C ABI's error state.
+//
+// MFMA conventions used throughout (64-lane wavefronts, 16x16 output tiles):
+//   v_mfma_f32_16x16x32_bf16 : lane l holds A[l%16][8*(l/16) .. +7] and B[8*(l/16) .. +7][l%16]
+//   v_mfma_f32_16x16x4_f32   : lane l holds A[l%16][l/16]           and B[l/16][l%16]
+//   accumulator (both)       : lane l holds D[4*(l/16) + r][l%16], r = 0..3
+// A and B always use the same lane -> k assignment, so any consistent permutation of k between
+// the two operands leaves the product unchanged.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <stddef.h>
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+
+namespace vsp {
+
+// ---- host-side error state (defined in abi.cpp) ------------------------------------------------
+int fail(int code, const char* fmt, ...);
+int check_launch(const char* what);
+
+enum Status { OK = 0, ERR_ARG = 1, ERR_UNSUPPORTED = 2, ERR_LAUNCH = 3 };
+
+// ---- element conversions ----------------------------------------------------------------------
+__device__ __forceinline__ float to_f32(float x) { return x; }
+__device__ __forceinline__ float to_f32(__bf16 x) { return (float)x; }
+__device__ __forceinline__ float to_f32(_Float16 x) { return (float)x; }
+
+template <typename T> __device__ __forceinline__ T from_f32(float x);
+template <> __device__ __forceinline__ float from_f32<float>(float x) { return x; }
+template <> __device__ __forceinline__ __bf16 from_f32<__bf16>(float x) { return (__bf16)x; }
+template <> __device__ __forceinline__ _Float16 from_f32<_Float16>(float x) { return (_Float16)x; }
+
+// ---- MFMA tile products -----------------------------------------------------------------------
+// Operand element type E selects the instruction: __bf16 -> 16x16x32 bf16, float -> 16x16x4 f32.
+// `a` points at A[r0][k0] of a row-major [row][k] array with pitch lda (elements); `bt` points at
+// B[k0][c0] stored as [col][k] ("k-contiguous") with pitch ldb. K is a multiple of kstep<E>.
+template <typename E> struct Mfma;
+
+template <> struct Mfma<__bf16> {
+  static constexpr int kstep = 32;
+  __device__ __forceinline__ static f32x4 run(const __bf16* a, int lda, const __bf16* bt, int ldb, int K,
+                                              f32x4 acc) {
+    const int l = threadIdx.x & 63;
+    const __bf16* pa = a + (l & 15) * lda + 8 * (l >> 4);
+    const __bf16* pb = bt + (l & 15) * ldb + 8 * (l >> 4);
+    for (int k = 0; k < K; k += 32) {
+      bf16x8 av = *reinterpret_cast<const bf16x8*>(pa + k);
+      bf16x8 bv = *reinterpret_cast<const bf16x8*>(pb + k);
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, bv, acc, 0, 0, 0);
+    }
+    return acc;
+  }
+};
+
+template <> struct Mfma<float> {
+  static constexpr int kstep = 4;
+  __device__ __forceinline__ static f32x4 run(const float* a, int lda, const float* bt, int ldb, int K,
+                                              f32x4 acc) {
+    const int l = threadIdx.x & 63;
+    const float* pa = a + (l & 15) * lda + (l >> 4);
+    const float* pb = bt + (l & 15) * ldb + (l >> 4);
+    for (int k = 0; k < K; k += 4) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(pa[k], pb[k], acc, 0, 0, 0);
+    return acc;
+  }
+};
+
+// fp32 product with B row-major ([k][col], pitch ldb): used by the small triangular solves.
+__device__ __forceinline__ f32x4 mfma_f32_rowmajor_b(const float* a, int lda, const float* b, int ldb, int K,
+                                                     f32x4 acc) {
+  const int l = threadIdx.x & 63;
+  const float* pa = a + (l & 15) * lda + (l >> 4);
+  const float* pb = b + (l >> 4) * ldb + (l & 15);
+  for (int k = 0; k < K; k += 4) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(pa[k], pb[k * ldb], acc, 0, 0, 0);
+  return acc;
+}
+
+__device__ __forceinline__ f32x4 zero4() { return f32x4{0.f, 0.f, 0.f, 0.f}; }
+
+// Store an accumulator tile into a row-major [row][col] array (pitch ld) with conversion to E.
+template <typename E>
+__device__ __forceinline__ void store_tile(E* base, int ld, f32x4 acc) {
+  const int l = threadIdx.x & 63;
+  const int c = l & 15, r0 = 4 * (l >> 4);
+#pragma unroll
+  for (int r = 0; r < 4; ++r) base[(r0 + r) * ld + c] = from_f32<E>(acc[r]);
+}
+
+// Store an accumulator tile transposed: dst[col][row] (pitch ld), i.e. into a k-contiguous B operand.
+template <typename E>
+__device__ __forceinline__ void store_tile_t(E* base, int ld, f32x4 acc) {
+  const int l = threadIdx.x & 63;
+  const int c = l & 15, r0 = 4 * (l >> 4);
+#pragma unroll
+  for (int r = 0; r < 4; ++r) base[c * ld + r0 + r] = from_f32<E>(acc[r]);
+}
+
+// ---- XCD-aware block order --------------------------------------------------------------------
+// Workgroups are dispatched round-robin over the 8 XCDs (block g runs on XCD g % 8), and each XCD
+// has its own L2. Renumber so that consecutive logical ids share an XCD: blocks that read the same
+// data (e.g. the value slices of one head) then hit the same L2.
+__device__ __forceinline__ int xcd_logical_block(int g, int n) {
+  constexpr int kXcd = 8;
+  if (n % kXcd != 0) return g;
+  return (g % kXcd) * (n / kXcd) + g / kXcd;
+}
+
+}  // namespace vsp

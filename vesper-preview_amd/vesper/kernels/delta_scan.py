@@ -1,0 +1,182 @@
+"""The delta-rule scan on MI355X: hand-written HIP kernels behind the reference's contract.
+
+``delta_scan_fused`` and ``delta_scan_fused_fp32`` keep the signatures, tensor contracts and
+refusals of the reference's ``vesper/kernels/delta_scan.py:132-187`` (registry rows
+``docs/registry.md:29-30``): ``q, k, v [b, n, h, dk]``, ``beta [b, n, h]``, the state
+``[b, h, dk, dk]`` in float32 read as ``H^T q`` after the token's own write, no query scaling, keys
+already normalised. Where the reference calls fla-core's Triton kernels, these call
+``libvesper_kernels.so`` through its C ABI (``include/vesper_kernels.h``) on torch's current stream:
+
+- ``delta_scan_fused``: bfloat16 inputs and output, float32 state; the chunked WY/UT scan with
+  bf16 MFMA contractions (``vsp_delta_scan_bf16``).
+- ``delta_scan_fused_fp32``: float32 throughout, fp32 MFMA (``vsp_delta_scan_f32``).
+- ``delta_scan_step_fused``: one token per row, the contract of ``vesper/recurrence.py:143-163``
+  (``delta_scan_step``), for decoding (``vsp_delta_step_f32`` / ``vsp_delta_step_bf16``).
+
+Each takes an optional keyword ``active`` (bool ``[b, n]``, ``[b]`` for the step): inactive tokens
+still write the state; their outputs are zero (``vesper/loop.py:24-26``, ``:441-442``). ``None`` is
+exactly the reference behaviour. The kernels are forward only: inputs that require a gradient are
+refused while grad mode is on.
+"""
+
+from __future__ import annotations
+
+import torch
+from torch import Tensor
+
+from vesper.contracts import ContractError, Dims, check_shape
+from vesper.kernels import _lib
+
+MAX_HEAD_DIM = 256  # delta_scan.py:41 in the reference; the HIP kernels take any width up to it
+INPUT_DTYPE = torch.bfloat16  # delta_scan_fused's q, k, v, beta
+FP32_INPUT_DTYPE = torch.float32  # delta_scan_fused_fp32's q, k, v, beta
+STATE_DTYPE = torch.float32
+
+
+def fused_scan_available() -> bool:
+    """Whether the fused scans can run here: a HIP device and the built kernel library."""
+    return torch.cuda.is_available() and _lib.available()
+
+
+def _checked_length(q: Tensor, k: Tensor, v: Tensor, beta: Tensor, state: Tensor, input_dtype: torch.dtype) -> int:
+    """The one contract check of the scans (reference ``delta_scan.py:93-119``); returns ``n``.
+
+    Raises:
+        ContractError: on a shape or dtype mismatch, a tensor off the GPU or on another device than
+            ``q``, or a head dimension above ``MAX_HEAD_DIM``.
+    """
+    dims: Dims = {}
+    check_shape("q", q, ("b", "n", "h", "dk"), dims, input_dtype)
+    check_shape("k", k, ("b", "n", "h", "dk"), dims, input_dtype)
+    check_shape("v", v, ("b", "n", "h", "dk"), dims, input_dtype)
+    check_shape("beta", beta, ("b", "n", "h"), dims, input_dtype)
+    check_shape("state", state, ("b", "h", "dk", "dk"), dims, STATE_DTYPE)
+    if q.device.type != "cuda":
+        raise ContractError(f"the fused scan runs on CUDA only, got q on {q.device}")
+    for name, tensor in (("k", k), ("v", v), ("beta", beta), ("state", state)):
+        if tensor.device != q.device:
+            raise ContractError(f"{name} is on {tensor.device}, q on {q.device}")
+    if dims["dk"] > MAX_HEAD_DIM:
+        raise ContractError(f"head dimension {dims['dk']} exceeds the kernel's {MAX_HEAD_DIM}")
+    return dims["n"]
+
+
+def _refuse_grad(*tensors: Tensor) -> None:
+    if torch.is_grad_enabled() and any(t.requires_grad for t in tensors):
+        raise ContractError(
+            "the HIP delta scan is forward only (no backward kernel yet): call it under torch.no_grad() "
+            "or on detached inputs"
+        )
+
+
+def _active_mask(active: Tensor | None, lead: tuple[str, ...], dims: Dims, device: torch.device) -> Tensor | None:
+    if active is None:
+        return None
+    check_shape("active", active, lead, dims, torch.bool)
+    if active.device != device:
+        raise ContractError(f"active is on {active.device}, q on {device}")
+    return active.contiguous().view(torch.uint8)
+
+
+def _scan(entry: str, q: Tensor, k: Tensor, v: Tensor, beta: Tensor, state: Tensor, active: Tensor | None,
+          fp32: bool) -> tuple[Tensor, Tensor]:
+    b, n, h, dk = q.shape
+    q, k, v, beta, state = (t.contiguous() for t in (q, k, v, beta, state))
+    mask = _active_mask(active, ("b", "n"), {"b": b, "n": n}, q.device)
+    o = torch.empty_like(q)
+    s_out = torch.empty_like(state)
+    lib = _lib.library()
+    ws_bytes = int(lib.vsp_delta_scan_workspace_bytes(b, n, h, dk, int(fp32)))
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=q.device) if ws_bytes else None
+    with torch.cuda.device(q.device):
+        _lib.call(entry, q.data_ptr(), k.data_ptr(), v.data_ptr(), beta.data_ptr(), state.data_ptr(), o.data_ptr(),
+                  s_out.data_ptr(), _lib.ptr(ws), ws_bytes, _lib.ptr(mask), b, n, h, dk, _lib.stream_of(q.device))
+    return o, s_out
+
+
+def delta_scan_fused(q: Tensor, k: Tensor, v: Tensor, beta: Tensor, state: Tensor, *,
+                     active: Tensor | None = None) -> tuple[Tensor, Tensor]:
+    """Apply ``n`` tokens to the state with the chunked bfloat16 kernel.
+
+    Args:
+        q: ``[b, n, h, dk]`` queries, bfloat16, on the GPU.
+        k: ``[b, n, h, dk]`` keys, bfloat16, L2 norm at most one.
+        v: ``[b, n, h, dk]`` values, bfloat16.
+        beta: ``[b, n, h]`` write strengths in [0, 1], bfloat16.
+        state: ``[b, h, dk, dk]`` the state before the first token, float32.
+        active: optional bool ``[b, n]``; inactive tokens write the state, their outputs are zero.
+
+    Returns:
+        ``(o, state_n)``: ``o [b, n, h, dk]`` bfloat16 and the final state in float32; with no
+        tokens, the empty query tensor and the unchanged state object.
+
+    Raises:
+        ContractError: on a dtype, shape, device or width outside the contract, or inputs needing
+            a gradient, before any kernel runs.
+    """
+    if _checked_length(q, k, v, beta, state, INPUT_DTYPE) == 0:
+        return q, state
+    _refuse_grad(q, k, v, beta, state)
+    return _scan("vsp_delta_scan_bf16", q, k, v, beta, state, active, fp32=False)
+
+
+def delta_scan_fused_fp32(q: Tensor, k: Tensor, v: Tensor, beta: Tensor, state: Tensor, *,
+                          active: Tensor | None = None) -> tuple[Tensor, Tensor]:
+    """Apply ``n`` tokens to the state with float32 inputs, state and arithmetic.
+
+    As ``delta_scan_fused`` with every tensor float32; ``o`` is float32.
+    """
+    if _checked_length(q, k, v, beta, state, FP32_INPUT_DTYPE) == 0:
+        return q, state
+    _refuse_grad(q, k, v, beta, state)
+    return _scan("vsp_delta_scan_f32", q, k, v, beta, state, active, fp32=True)
+
+
+def delta_scan_step_fused(q: Tensor, k: Tensor, v: Tensor, beta: Tensor, state: Tensor, *,
+                          active: Tensor | None = None, out_state: Tensor | None = None) -> tuple[Tensor, Tensor]:
+    """One token per row written then read: ``(H'^T q, H')`` (``vesper/recurrence.py:143-163``).
+
+    Args:
+        q, k, v: ``[b, h, dk]`` float32 or bfloat16 (all three alike, ``beta [b, h]`` too).
+        state: ``[b, h, dk, dk]`` float32.
+        active: optional bool ``[b]``; an inactive row writes the state and reads zero.
+        out_state: optional float32 tensor shaped like ``state`` that receives the new state; it
+            may be ``state`` itself (an in-place decode step).
+
+    Returns:
+        ``(o [b, h, dk], state')`` with ``o`` in the inputs' dtype.
+    """
+    dtype = q.dtype
+    if dtype not in (torch.float32, torch.bfloat16):
+        raise ContractError(f"q: dtype must be torch.float32 or torch.bfloat16, got {dtype}")
+    dims: Dims = {}
+    check_shape("q", q, ("b", "h", "dk"), dims, dtype)
+    check_shape("k", k, ("b", "h", "dk"), dims, dtype)
+    check_shape("v", v, ("b", "h", "dk"), dims, dtype)
+    check_shape("beta", beta, ("b", "h"), dims, dtype)
+    check_shape("state", state, ("b", "h", "dk", "dk"), dims, STATE_DTYPE)
+    if q.device.type != "cuda":
+        raise ContractError(f"the fused scan runs on CUDA only, got q on {q.device}")
+    for name, tensor in (("k", k), ("v", v), ("beta", beta), ("state", state)):
+        if tensor.device != q.device:
+            raise ContractError(f"{name} is on {tensor.device}, q on {q.device}")
+    if dims["dk"] > MAX_HEAD_DIM:
+        raise ContractError(f"head dimension {dims['dk']} exceeds the kernel's {MAX_HEAD_DIM}")
+    _refuse_grad(q, k, v, beta, state)
+    b, h, dk = q.shape
+    q, k, v, beta = (t.contiguous() for t in (q, k, v, beta))
+    if not state.is_contiguous():
+        raise ContractError("state must be contiguous")
+    if out_state is None:
+        out_state = torch.empty_like(state)
+    else:
+        check_shape("out_state", out_state, ("b", "h", "dk", "dk"), dims, STATE_DTYPE)
+        if out_state.device != q.device or not out_state.is_contiguous():
+            raise ContractError("out_state must be a contiguous tensor on q's device")
+    mask = _active_mask(active, ("b",), dims, q.device)
+    o = torch.empty_like(q)
+    entry = "vsp_delta_step_f32" if dtype == torch.float32 else "vsp_delta_step_bf16"
+    with torch.cuda.device(q.device):
+        _lib.call(entry, q.data_ptr(), k.data_ptr(), v.data_ptr(), beta.data_ptr(), state.data_ptr(),
+                  out_state.data_ptr(), o.data_ptr(), _lib.ptr(mask), b, h, dk, _lib.stream_of(q.device))
+    return o, out_state
