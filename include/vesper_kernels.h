@@ -68,6 +68,35 @@ int vsp_delta_step_f32(const float* q, const float* k, const float* v, const flo
 int vsp_delta_step_bf16(const void* q, const void* k, const void* v, const void* beta, const float* state_in,
                         float* state_out, void* o, const uint8_t* active, int B, int H, int D, void* stream);
 
+/* ---- sliding-window causal attention (prefill) -----------------------------------------------
+ * q: [B, N, H, D]; keys, values: [B, M + N, HKV, D], the cache's M rows first; o: [B, N, H, D].
+ * Query i sits at key index M + i and attends key indices [M + i - window + 1, M + i]; softmax in
+ * fp32 with `scale` (1/sqrt(D) for the reference); query head h reads KV head h / (H / HKV).
+ * D in {16, 32, 64, 128}; H a multiple of HKV; active: [B, N] or NULL.
+ * Replaces the fla-core 0.5.2 `parallel_attn` call of vesper/kernels/window_attn.py:27-39
+ * (`window_attention`), without the zero query rows the reference pads the cache with. */
+int vsp_window_attn_bf16(const void* q, const void* keys, const void* values, void* o, const uint8_t* active,
+                         int B, int N, int M, int H, int HKV, int D, int window, float scale, void* stream);
+int vsp_window_attn_f16(const void* q, const void* keys, const void* values, void* o, const uint8_t* active,
+                        int B, int N, int M, int H, int HKV, int D, int window, float scale, void* stream);
+
+/* ---- decode: one new token per row over a KV ring ------------------------------------------
+ * q: [B, H, D]; k, v: [B, HKV, D] (the new token); pos: [B] int64, nonnegative;
+ * ring_k, ring_v: [B, window, HKV, D]; ring_pos: [B, window] int64; ring_valid: [B, window] uint8.
+ * The query at position p attends valid slots with a position in (p - window, p] and the new token
+ * itself; o: [B, H, D]. With `write` nonzero the new token is then written into slot p % window
+ * (keys, values, position, valid flag) in place, after every read of the call (a second launch).
+ * The contract of vesper/attention.py:298-338 (`attend_ring`, without the projections) and
+ * vesper/attention.py:104-139 (`kv_ring_write`); the reference runs masked SDPA there.
+ * D in {16, 32, 64, 128}; at most 8 query heads per KV head; active: [B] or NULL (an inactive row
+ * reads zeros and still writes its token). */
+int vsp_ring_attn_bf16(const void* q, const void* k, const void* v, const int64_t* pos, void* ring_k, void* ring_v,
+                       int64_t* ring_pos, uint8_t* ring_valid, void* o, const uint8_t* active, int B, int H, int HKV,
+                       int D, int window, float scale, int write, void* stream);
+int vsp_ring_attn_f16(const void* q, const void* k, const void* v, const int64_t* pos, void* ring_k, void* ring_v,
+                      int64_t* ring_pos, uint8_t* ring_valid, void* o, const uint8_t* active, int B, int H, int HKV,
+                      int D, int window, float scale, int write, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

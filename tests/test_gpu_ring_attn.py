@@ -1,0 +1,144 @@
+"""The HIP ring attention (``vesper.kernels.ring_attn``) against the CPU oracle, through the C ABI."""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+from conftest import frac_tensor, needs_gpu, reference_vectors
+from oracle import attention as oa
+from oracle.delta import relative_error
+
+pytestmark = [pytest.mark.gpu, needs_gpu]
+
+GPU = torch.device("cuda")
+BF16 = torch.bfloat16
+
+
+def test_a_ring_attends_by_position_not_by_slot_order():
+    # slots hold positions [3, 1, 2] with values [30, 10, 20]; the new token (position 4, value
+    # 40) sees positions 2..4 with equal logits, so every output is 30 (tests/test_attention.py:150-172)
+    from vesper.kernels.ring_attn import RingKVCache, ring_attention
+
+    c = reference_vectors()["ring_by_position"]
+    w, dk = c["window"], 16
+    vals = frac_tensor(c["ring_values"]).reshape(1, w, 1, 1).expand(1, w, 1, dk).to(BF16)
+    ring = RingKVCache(torch.zeros(1, w, 1, dk, dtype=BF16, device=GPU), vals.contiguous().to(GPU),
+                       torch.tensor([c["ring_pos"]], device=GPU), torch.ones(1, w, dtype=torch.bool, device=GPU), w)
+    q = torch.zeros(1, 1, 1, dk, dtype=BF16, device=GPU)
+    v = torch.full((1, 1, 1, dk), float(frac_tensor([c["new_value"]])[0]), dtype=BF16, device=GPU)
+    o, after = ring_attention(q, q, v, torch.tensor([[c["new_pos"]]], device=GPU), ring)
+    assert torch.equal(o.float().cpu(), torch.full((1, 1, 1, dk), float(frac_tensor([c["want"]])[0])))
+    assert after.pos.cpu().tolist() == [c["pos_after_write"]]
+    assert bool(after.valid.all())
+    assert torch.equal(ring.pos.cpu(), torch.tensor([c["ring_pos"]]))  # the functional form copied
+
+
+def _random_ring(b, w, hkv, dk, seed, dtype=BF16):
+    g = torch.Generator().manual_seed(seed)
+    rk = torch.randn(b, w, hkv, dk, generator=g).to(dtype)
+    rv = torch.randn(b, w, hkv, dk, generator=g).to(dtype)
+    p = torch.randint(w, 3 * w, (b, 1), generator=g)
+    # positions spread around the window: some visible, some too old, some in the future
+    rpos = p - torch.randint(-3, w + 5, (b, w), generator=g)
+    valid = torch.rand(b, w, generator=g) < 0.85
+    return rk, rv, rpos, valid, p
+
+
+@pytest.mark.parametrize("dtype", [BF16, torch.float16])
+@pytest.mark.parametrize("dk", [16, 32, 64, 128])
+@pytest.mark.parametrize(("h", "hkv"), [(8, 8), (8, 4), (8, 1), (12, 4)])
+def test_random_rings_match_the_oracle(dtype, dk, h, hkv):
+    from vesper.kernels.ring_attn import RingKVCache, ring_attention
+
+    b, w = 3, 37
+    rk, rv, rpos, valid, p = _random_ring(b, w, hkv, dk, seed=dk + h + hkv, dtype=dtype)
+    g = torch.Generator().manual_seed(5)
+    q = torch.randn(b, 1, h, dk, generator=g).to(dtype)
+    k = torch.randn(b, 1, hkv, dk, generator=g).to(dtype)
+    v = torch.randn(b, 1, hkv, dk, generator=g).to(dtype)
+    want = oa.ring_attend(q.double(), k.double(), v.double(), p, rk.double(), rv.double(), rpos, valid, w)
+    ring = RingKVCache(*(t.to(GPU) for t in (rk, rv, rpos, valid)), w)
+    o, after = ring_attention(q.to(GPU), k.to(GPU), v.to(GPU), p.to(GPU), ring)
+    assert relative_error(o, want) < 1e-2
+    torch.testing.assert_close(o.float().cpu(), want.float(), rtol=3e-2, atol=3e-2)
+    nk, nv, npos, nvalid = oa.kv_ring_write(rk, rv, rpos, valid, k, v, p)
+    assert torch.equal(after.k.cpu(), nk) and torch.equal(after.v.cpu(), nv)
+    assert torch.equal(after.pos.cpu(), npos) and torch.equal(after.valid.cpu(), nvalid)
+
+
+def test_decoding_steps_equal_the_whole_chunk_window():
+    # 3w + 5 single-token steps from an empty ring equal the window attention over the whole chunk
+    from vesper.kernels.ring_attn import kv_ring_empty, ring_attention
+
+    b, h, hkv, dk, w, start = 2, 8, 2, 64, 16, 7
+    steps = 3 * w + 5
+    g = torch.Generator().manual_seed(4)
+    q = torch.randn(b, steps, h, dk, generator=g).to(BF16)
+    k = torch.randn(b, steps, hkv, dk, generator=g).to(BF16)
+    v = torch.randn(b, steps, hkv, dk, generator=g).to(BF16)
+    whole = oa.window_attention(q.double(), k.double(), v.double(), w)
+    ring = kv_ring_empty(b, hkv, dk, w, BF16, GPU)
+    pos = torch.arange(start, start + steps).expand(b, steps).contiguous()
+    outs = []
+    for i in range(steps):
+        sl = slice(i, i + 1)
+        o, ring = ring_attention(q[:, sl].to(GPU), k[:, sl].to(GPU), v[:, sl].to(GPU), pos[:, sl].to(GPU), ring,
+                                 inplace=True)
+        outs.append(o)
+    got = torch.cat(outs, 1)
+    assert relative_error(got, whole) < 1e-2
+    torch.testing.assert_close(got.float().cpu(), whole.float(), rtol=3e-2, atol=3e-2)
+    held = ring.valid[0].cpu()
+    assert sorted(ring.pos[0].cpu()[held].tolist()) == list(range(start + steps - w, start + steps))
+
+
+def test_decode_config_b64_h8_d64_ring512_one_step():
+    from vesper.kernels.ring_attn import RingKVCache, ring_attention
+
+    b, h, dk, w = 64, 8, 64, 512
+    g = torch.Generator().manual_seed(0)
+    rk = torch.randn(b, w, h, dk, generator=g).to(BF16)
+    rv = torch.randn(b, w, h, dk, generator=g).to(BF16)
+    rpos = torch.arange(w).expand(b, w).contiguous()
+    valid = torch.ones(b, w, dtype=torch.bool)
+    q = torch.randn(b, 1, h, dk, generator=g).to(BF16)
+    k = torch.randn(b, 1, h, dk, generator=g).to(BF16)
+    v = torch.randn(b, 1, h, dk, generator=g).to(BF16)
+    p = torch.full((b, 1), w)
+    want = oa.ring_attend(q.float(), k.float(), v.float(), p, rk.float(), rv.float(), rpos, valid, w)
+    ring = RingKVCache(*(t.to(GPU) for t in (rk, rv, rpos, valid)), w)
+    o, after = ring_attention(q.to(GPU), k.to(GPU), v.to(GPU), p.to(GPU), ring, inplace=True)
+    assert relative_error(o, want) < 1e-2
+    assert after is ring and int(ring.pos[0, 0]) == w  # slot 512 % 512 = 0 took the new token
+
+
+def test_an_inactive_row_reads_zero_and_still_writes():
+    from vesper.kernels.ring_attn import RingKVCache, ring_attention
+
+    rk, rv, rpos, valid, p = _random_ring(4, 20, 2, 64, seed=3)
+    g = torch.Generator().manual_seed(6)
+    q = torch.randn(4, 1, 4, 64, generator=g).to(BF16)
+    k = torch.randn(4, 1, 2, 64, generator=g).to(BF16)
+    v = torch.randn(4, 1, 2, 64, generator=g).to(BF16)
+    act = torch.tensor([True, False, True, False])
+    ring = RingKVCache(*(t.to(GPU) for t in (rk, rv, rpos, valid)), 20)
+    o_all, _ = ring_attention(q.to(GPU), k.to(GPU), v.to(GPU), p.to(GPU), ring)
+    o, after = ring_attention(q.to(GPU), k.to(GPU), v.to(GPU), p.to(GPU), ring, active=act.to(GPU))
+    assert torch.equal(o[act.to(GPU)], o_all[act.to(GPU)]) and bool((o[~act.to(GPU)] == 0).all())
+    _, _, npos, _ = oa.kv_ring_write(rk, rv, rpos, valid, k, v, p)
+    assert torch.equal(after.pos.cpu(), npos)
+
+
+def test_refusals():
+    from vesper.contracts import ContractError
+    from vesper.kernels.ring_attn import kv_ring_empty, ring_attention
+
+    ring = kv_ring_empty(1, 1, 64, 8, BF16, GPU)
+    q = torch.zeros(1, 1, 1, 64, dtype=BF16, device=GPU)
+    with pytest.raises(ContractError, match="nonnegative"):
+        ring_attention(q, q, q, torch.tensor([[-1]], device=GPU), ring)
+    with pytest.raises(ContractError, match="dtype"):
+        ring_attention(q.float(), q, q, torch.tensor([[1]], device=GPU), ring)
+    with pytest.raises(ContractError, match="axis"):
+        ring_attention(q, q, q, torch.tensor([[1, 2]], device=GPU), ring)

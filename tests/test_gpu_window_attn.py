@@ -1,0 +1,137 @@
+"""The HIP window attention (``vesper.kernels.window_attn``) against the CPU oracle, through the C ABI.
+
+The oracle runs in float64 (float32 at the full headline size) on the same bf16/fp16-valued inputs.
+Bound: relative Frobenius error below 1e-2, and elementwise within the reference's
+``rtol = atol = 3e-2`` (``tests/test_window_attn.py:78``).
+"""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+from conftest import needs_gpu
+from oracle.attention import window_attention as oracle_window
+from oracle.delta import relative_error
+
+pytestmark = [pytest.mark.gpu, needs_gpu]
+
+GPU = torch.device("cuda")
+BF16 = torch.bfloat16
+
+
+def _inputs(b, n, m, h, hkv, dk, seed=0, dtype=BF16):
+    g = torch.Generator().manual_seed(seed)
+    q = torch.randn(b, n, h, dk, generator=g).to(dtype)
+    keys = torch.randn(b, m + n, hkv, dk, generator=g).to(dtype)
+    values = torch.randn(b, m + n, hkv, dk, generator=g).to(dtype)
+    return q, keys, values
+
+
+def _check(got, want, rel=1e-2):
+    assert relative_error(got, want) < rel
+    torch.testing.assert_close(got.float().cpu(), want.float(), rtol=3e-2, atol=3e-2)
+
+
+# the reference's shapes: h 4, 2 KV heads, dk 64, window 16; chunks shorter and longer than the
+# window with an empty, a partial and a full cache (tests/test_window_attn.py:67-78)
+@pytest.mark.parametrize(("n", "m"), [(8, 0), (40, 0), (8, 5), (40, 5), (8, 16), (40, 16)])
+def test_the_kernel_equals_the_oracle_window(n, m):
+    from vesper.kernels.window_attn import window_attention
+
+    q, keys, values = _inputs(3, n, m, 4, 2, 64, seed=n * 100 + m)
+    want = oracle_window(q.double(), keys.double(), values.double(), 16)
+    got = window_attention(q.to(GPU), keys.to(GPU), values.to(GPU), 16)
+    assert got.dtype == BF16 and got.shape == q.shape
+    _check(got, want)
+
+
+@pytest.mark.parametrize("dtype", [BF16, torch.float16])
+@pytest.mark.parametrize("dk", [16, 32, 64, 128])
+@pytest.mark.parametrize(("n", "m", "w"), [(1, 0, 1), (70, 3, 7), (130, 64, 64), (300, 100, 100), (200, 40, 600)])
+def test_widths_windows_and_offsets(dtype, dk, n, m, w):
+    from vesper.kernels.window_attn import window_attention
+
+    q, keys, values = _inputs(2, n, m, 4, 1, dk, seed=dk + n + w, dtype=dtype)
+    want = oracle_window(q.double(), keys.double(), values.double(), w)
+    got = window_attention(q.to(GPU), keys.to(GPU), values.to(GPU), w)
+    assert got.dtype == dtype
+    _check(got, want)
+
+
+@pytest.mark.parametrize(("h", "hkv"), [(8, 8), (8, 2), (12, 3), (4, 1)])
+def test_grouped_kv_heads(h, hkv):
+    from vesper.kernels.window_attn import window_attention
+
+    q, keys, values = _inputs(2, 100, 20, h, hkv, 64, seed=h * 10 + hkv)
+    want = oracle_window(q.double(), keys.double(), values.double(), 32)
+    _check(window_attention(q.to(GPU), keys.to(GPU), values.to(GPU), 32), want)
+
+
+def test_headline_config_b4_t4096_h8_d64_w512():
+    from vesper.kernels.window_attn import window_attention
+
+    q, keys, values = _inputs(4, 4096, 0, 8, 8, 64, seed=0)
+    got = window_attention(q.to(GPU), keys.to(GPU), values.to(GPU), 512)
+    want = oracle_window(q.float(), keys.float(), values.float(), 512)
+    _check(got, want)
+
+
+def test_active_mask_skips_inactive_queries_only():
+    from vesper.kernels.window_attn import window_attention
+
+    q, keys, values = _inputs(2, 300, 10, 4, 2, 64, seed=4)
+    act = torch.rand(2, 300, generator=torch.Generator().manual_seed(1)) < 0.4
+    act[0, 64:128] = False  # a whole tile of 64 queries inactive
+    dev = [t.to(GPU) for t in (q, keys, values)]
+    full = window_attention(*dev, 48)
+    got = window_attention(*dev, 48, active=act.to(GPU))
+    a = act.to(GPU)
+    assert torch.equal(got[a], full[a])
+    assert bool((got[~a] == 0).all())
+    want = oracle_window(q.double(), keys.double(), values.double(), 48, active=act)
+    _check(got, want)
+
+
+def test_refusals():
+    from vesper.contracts import ContractError
+    from vesper.kernels.window_attn import window_attention
+
+    q, keys, values = _inputs(1, 8, 0, 4, 2, 64)
+    with pytest.raises(ContractError, match="CUDA only"):
+        window_attention(q, keys, values, 4)
+    dq, dk_, dv = (t.to(GPU) for t in (q, keys, values))
+    with pytest.raises(ContractError, match="dtype"):
+        window_attention(dq.float(), dk_.float(), dv.float(), 4)
+    with pytest.raises(ContractError, match="dtype"):
+        window_attention(dq, dk_.half(), dv, 4)
+    with pytest.raises(ContractError, match="multiple"):
+        window_attention(dq[:, :, :3], dk_, dv, 4)
+    with pytest.raises(ContractError, match="fewer"):
+        window_attention(dq, dk_[:, :4], dv[:, :4], 4)
+    with pytest.raises(ContractError, match="forward only"):
+        window_attention(dq.clone().requires_grad_(), dk_, dv, 4)
+    with pytest.raises(ValueError, match="window"):
+        window_attention(dq, dk_, dv, 0)
+
+
+def test_repeatable_and_captured_replays_equal_eager():
+    from vesper.kernels.window_attn import window_attention
+
+    q, keys, values = (t.to(GPU) for t in _inputs(2, 500, 16, 8, 2, 64, seed=7))
+    eager = window_attention(q, keys, values, 64)
+    assert torch.equal(window_attention(q, keys, values, 64), eager)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        window_attention(q, keys, values, 64)
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        out = window_attention(q, keys, values, 64)
+    for i in range(3):
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager), i
+        window_attention(q, keys, values, 64)
+        torch.cuda.synchronize()

@@ -22,6 +22,7 @@ ABI_VERSION = 1
 P = ctypes.c_void_p
 I = ctypes.c_int
 Z = ctypes.c_size_t
+F = ctypes.c_float
 
 # every entry point of include/vesper_kernels.h: (return type, argument types)
 SIGNATURES: dict[str, tuple[object, list[object]]] = {
@@ -32,6 +33,10 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "vsp_delta_scan_f32": (I, [P, P, P, P, P, P, P, P, Z, P, I, I, I, I, P]),
     "vsp_delta_step_f32": (I, [P, P, P, P, P, P, P, P, I, I, I, P]),
     "vsp_delta_step_bf16": (I, [P, P, P, P, P, P, P, P, I, I, I, P]),
+    "vsp_window_attn_bf16": (I, [P, P, P, P, P, I, I, I, I, I, I, I, F, P]),
+    "vsp_window_attn_f16": (I, [P, P, P, P, P, I, I, I, I, I, I, I, F, P]),
+    "vsp_ring_attn_bf16": (I, [P, P, P, P, P, P, P, P, P, P, I, I, I, I, I, F, I, P]),
+    "vsp_ring_attn_f16": (I, [P, P, P, P, P, P, P, P, P, P, I, I, I, I, I, F, I, P]),
 }
 
 

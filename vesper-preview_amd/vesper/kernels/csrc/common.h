@@ -37,6 +37,22 @@ template <> __device__ __forceinline__ float from_f32<float>(float x) { return x
 template <> __device__ __forceinline__ __bf16 from_f32<__bf16>(float x) { return (__bf16)x; }
 template <> __device__ __forceinline__ _Float16 from_f32<_Float16>(float x) { return (_Float16)x; }
 
+// Eight consecutive elements (16-byte aligned) as floats, with one vector load.
+template <typename T>
+__device__ __forceinline__ void load8_f32(const T* p, float* out) {
+  if constexpr (sizeof(T) == 2) {
+    typedef T V8 __attribute__((ext_vector_type(8)));
+    const V8 v = *reinterpret_cast<const V8*>(p);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) out[e] = to_f32(v[e]);
+  } else {
+    const float4 a = reinterpret_cast<const float4*>(p)[0];
+    const float4 b = reinterpret_cast<const float4*>(p)[1];
+    out[0] = a.x; out[1] = a.y; out[2] = a.z; out[3] = a.w;
+    out[4] = b.x; out[5] = b.y; out[6] = b.z; out[7] = b.w;
+  }
+}
+
 // ---- MFMA tile products -----------------------------------------------------------------------
 // Operand element type E selects the instruction: __bf16 -> 16x16x32 bf16, float -> 16x16x4 f32.
 // `a` points at A[r0][k0] of a row-major [row][k] array with pitch lda (elements); `bt` points at

@@ -1,0 +1,86 @@
+"""Sliding-window causal attention on MI355X: a hand-written HIP kernel behind the reference's contract.
+
+``window_attention(q, keys, values, window)`` keeps the signature and semantics of the reference's
+``vesper/kernels/window_attn.py:27-39`` (registry row ``docs/registry.md:108``): the outputs of the
+``n`` newest positions of ``m + n`` consecutive key positions (the cache's ``m`` first), each query
+at index ``i`` attending key indices ``[i - window + 1, i]``, scale ``1 / sqrt(dk)``, query head
+``j`` reading KV head ``j // (h / hkv)``. Where the reference calls fla-core's ``parallel_attn`` on
+a query tensor padded with ``m`` zero rows, this calls ``vsp_window_attn_bf16`` / ``_f16`` through
+the C ABI with the cache offset as an argument, so nothing is padded.
+
+For: bfloat16 or float16 on the GPU with consecutive positions (the window counts indices, as the
+reference's kernel does; ``WindowedAttention.attend`` checks the positions before calling).
+An optional keyword ``active`` (bool ``[b, n]``) skips inactive queries, whose outputs are zero;
+their keys and values stay visible to every other query. Forward only.
+"""
+
+from __future__ import annotations
+
+import math
+
+import torch
+from torch import Tensor
+
+from vesper.contracts import ContractError, Dims, check_shape
+from vesper.kernels import _lib
+
+WINDOW_KERNEL_DTYPES = (torch.bfloat16, torch.float16)
+HEAD_DIMS = (16, 32, 64, 128)
+
+
+def _aligned(t: Tensor) -> Tensor:
+    t = t.contiguous()
+    return t if t.data_ptr() % 16 == 0 else t.clone()
+
+
+def window_attention(q: Tensor, keys: Tensor, values: Tensor, window: int, *, active: Tensor | None = None) -> Tensor:
+    """Outputs ``[b, n, h, dk]`` of ``q`` over ``keys, values [b, m + n, hkv, dk]``.
+
+    Raises:
+        ContractError: on shapes that disagree, a dtype other than bfloat16/float16 (or mixed), a
+            tensor off the GPU, ``h`` not a multiple of ``hkv``, a head width the kernel does not
+            tile, fewer key rows than queries, or inputs needing a gradient.
+        ValueError: if ``window`` is below 1.
+    """
+    if window < 1:
+        raise ValueError(f"window must be at least 1, got {window}")
+    dims: Dims = {}
+    check_shape("q", q, ("b", "n", "h", "dk"), dims)
+    check_shape("keys", keys, ("b", "s", "hkv", "dk"), dims)
+    check_shape("values", values, ("b", "s", "hkv", "dk"), dims)
+    if q.dtype not in WINDOW_KERNEL_DTYPES:
+        raise ContractError(f"q: dtype must be bfloat16 or float16, got {q.dtype}")
+    for name, t in (("keys", keys), ("values", values)):
+        if t.dtype != q.dtype:
+            raise ContractError(f"{name}: dtype must be {q.dtype}, got {t.dtype}")
+    if q.device.type != "cuda":
+        raise ContractError(f"the window attention kernel runs on CUDA only, got q on {q.device}")
+    for name, t in (("keys", keys), ("values", values)):
+        if t.device != q.device:
+            raise ContractError(f"{name} is on {t.device}, q on {q.device}")
+    b, n, h, dk = q.shape
+    s, hkv = dims["s"], dims["hkv"]
+    m = s - n
+    if m < 0:
+        raise ContractError(f"keys hold {s} positions, fewer than the {n} queries")
+    if h % hkv != 0:
+        raise ContractError(f"{h} query heads are not a multiple of {hkv} KV heads")
+    if dk not in HEAD_DIMS:
+        raise ContractError(f"head dimension {dk} is not one the kernel tiles ({HEAD_DIMS})")
+    if torch.is_grad_enabled() and any(t.requires_grad for t in (q, keys, values)):
+        raise ContractError("the HIP window attention is forward only: call it under torch.no_grad()")
+    mask = None
+    if active is not None:
+        check_shape("active", active, ("b", "n"), {"b": b, "n": n}, torch.bool)
+        if active.device != q.device:
+            raise ContractError(f"active is on {active.device}, q on {q.device}")
+        mask = active.contiguous().view(torch.uint8)
+    if n == 0:
+        return q.new_zeros(q.shape)
+    q, keys, values = _aligned(q), _aligned(keys), _aligned(values)
+    o = torch.empty_like(q)
+    entry = "vsp_window_attn_bf16" if q.dtype == torch.bfloat16 else "vsp_window_attn_f16"
+    with torch.cuda.device(q.device):
+        _lib.call(entry, q.data_ptr(), keys.data_ptr(), values.data_ptr(), o.data_ptr(), _lib.ptr(mask), b, n, m, h,
+                  hkv, dk, int(window), 1.0 / math.sqrt(dk), _lib.stream_of(q.device))
+    return o
