@@ -1,0 +1,334 @@
+#!/usr/bin/env python3
+"""Benchmark of Vesper's column sequence mixers on one MI355X.
+
+A step is one prefill pass of both mixers over one batch of synthetic input: the delta-rule scan
+(B=8, T=4096, H=8, d=64; bf16 q/k/v/beta, fp32 state with S0 ~ N(0, 0.02^2), chunk 64) followed by
+sliding-window causal attention over the same batch shape (window 512, bf16). ``value`` is prefill
+tokens/s = B*T / (time of one step), inputs resident in HBM. Beside it the line carries each
+kernel's own rate at its own configuration (attention alone at B=4), the decode rate (256
+single-token steps of batch 64: fp32 delta update of S [64,8,64,64] then attention over a 512-entry
+bf16 KV ring, captured as one HIP graph), the roofline of the dominant kernel measured with HIP
+events on the launch stream inside the timed region, and the CPU oracle timed on a bounded sample
+of the same workload on this host's cores.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import platform
+import statistics
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT / "vesper-preview_amd"))
+
+HBM_PEAK_GBS = 8000.0
+BF16_PEAK_TFLOPS = 2500.0
+
+B, T, H, D, WINDOW = 8, 4096, 8, 64, 512
+ATTN_B = 4
+DEC_B, DEC_W, DEC_STEPS = 64, 512, 256
+
+
+def log(*a: object) -> None:
+    print(*a, file=sys.stderr, flush=True)
+
+
+# ---- algorithmic work (per launch) ---------------------------------------------------------------
+def scan_flops(b: int, t: int, h: int, d: int, chunk: int = 64) -> float:
+    units = b * h * math.ceil(t / chunk)
+    return units * (8 * 2 * chunk * d * d + chunk**3 / 3)
+
+
+def scan_bytes(b: int, t: int, h: int, d: int) -> float:
+    return 4 * b * t * h * d * 2 + b * t * h * 2 + 2 * b * h * d * d * 4  # q,k,v,o bf16; beta; S0, S_n
+
+
+def window_pairs(t: int, w: int) -> int:
+    return sum(min(i + 1, w) for i in range(t))
+
+
+def attn_flops(b: int, t: int, h: int, d: int, w: int) -> float:
+    return 4.0 * d * b * h * window_pairs(t, w)
+
+
+def attn_bytes(b: int, t: int, h: int, hkv: int, d: int) -> float:
+    return 2 * b * t * h * d * 2 + 2 * b * t * hkv * d * 2  # q, o; k, v
+
+
+def decode_step_bytes(b: int, h: int, d: int, w: int) -> float:
+    state = 2 * b * h * d * d * 4  # read + write
+    delta_io = 4 * b * h * d * 4 + b * h * 4  # q, k, v, o fp32; beta
+    ring = 2 * b * w * h * d * 2  # K and V rows read
+    attn_io = 4 * b * h * d * 2 + b * 8  # q, k, v, o bf16; positions
+    ring_write = 2 * b * h * d * 2 + b * 9
+    return state + delta_io + ring + attn_io + ring_write
+
+
+# ---- inputs -------------------------------------------------------------------------------------
+def scan_inputs(torch, dev, b=B, t=T, h=H, d=D, seed=0):
+    from vesper.kernels.delta_scan import INPUT_DTYPE
+
+    g = torch.Generator().manual_seed(seed)
+    q = torch.randn(b, t, h, d, generator=g)
+    k = torch.randn(b, t, h, d, generator=g)
+    q = q / q.norm(dim=-1, keepdim=True).clamp_min(1e-6)
+    k = k / k.norm(dim=-1, keepdim=True).clamp_min(1e-6)
+    v = torch.randn(b, t, h, d, generator=g)
+    beta = torch.sigmoid(torch.randn(b, t, h, generator=g))
+    s0 = 0.02 * torch.randn(b, h, d, d, generator=g)
+    return [x.to(dev, INPUT_DTYPE) for x in (q, k, v, beta)] + [s0.to(dev)]
+
+
+def attn_inputs(torch, dev, b=B, t=T, h=H, d=D, seed=1):
+    g = torch.Generator().manual_seed(seed)
+    return [torch.randn(b, t, h, d, generator=g).to(dev, torch.bfloat16) for _ in range(3)]
+
+
+# ---- GPU legs -------------------------------------------------------------------------------------
+def time_prefill(torch, steps: int, warmup: int) -> dict:
+    from vesper.kernels.delta_scan import delta_scan_fused
+    from vesper.kernels.window_attn import window_attention
+
+    dev = torch.device("cuda:0")
+    q, k, v, beta, s0 = scan_inputs(torch, dev)
+    aq, ak, av = attn_inputs(torch, dev)
+    with torch.no_grad():
+        for _ in range(warmup):
+            delta_scan_fused(q, k, v, beta, s0)
+            window_attention(aq, ak, av, WINDOW)
+        ev = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(steps)]
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for i in range(steps):
+            ev[i][0].record()
+            delta_scan_fused(q, k, v, beta, s0)
+            ev[i][1].record()
+            window_attention(aq, ak, av, WINDOW)
+            ev[i][2].record()
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - t0
+    scan_ms = [e[0].elapsed_time(e[1]) for e in ev]
+    attn_ms = [e[1].elapsed_time(e[2]) for e in ev]
+    step_ms = [e[0].elapsed_time(e[2]) for e in ev]
+    return {"wall_s": wall, "scan_ms": statistics.mean(scan_ms), "attn_ms": statistics.mean(attn_ms),
+            "step_ms": statistics.mean(step_ms), "scan_ms_median": statistics.median(scan_ms),
+            "attn_ms_median": statistics.median(attn_ms)}
+
+
+def time_attention_config(torch, reps: int = 20) -> float:
+    from vesper.kernels.window_attn import window_attention
+
+    dev = torch.device("cuda:0")
+    aq, ak, av = attn_inputs(torch, dev, b=ATTN_B, seed=2)
+    with torch.no_grad():
+        for _ in range(3):
+            window_attention(aq, ak, av, WINDOW)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        e0.record()
+        for _ in range(reps):
+            window_attention(aq, ak, av, WINDOW)
+        e1.record()
+        torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / reps
+
+
+def time_decode(torch, reps: int = 5) -> dict:
+    from vesper.kernels.delta_scan import delta_scan_step_fused
+    from vesper.kernels.ring_attn import RingKVCache, ring_attention
+
+    dev = torch.device("cuda:0")
+    g = torch.Generator().manual_seed(3)
+    b, h, d, w, n = DEC_B, H, D, DEC_W, DEC_STEPS
+    state = (0.02 * torch.randn(b, h, d, d, generator=g)).to(dev)
+    ring = RingKVCache(torch.randn(b, w, h, d, generator=g).to(dev, torch.bfloat16),
+                       torch.randn(b, w, h, d, generator=g).to(dev, torch.bfloat16),
+                       torch.arange(w).expand(b, w).contiguous().to(dev),
+                       torch.ones(b, w, dtype=torch.bool, device=dev), w)
+    pos0, valid0 = ring.pos.clone(), ring.valid.clone()
+    dq = torch.randn(n, b, h, d, generator=g)
+    dk = torch.randn(n, b, h, d, generator=g)
+    dq = (dq / dq.norm(dim=-1, keepdim=True)).to(dev)
+    dk = (dk / dk.norm(dim=-1, keepdim=True)).to(dev)
+    dv = torch.randn(n, b, h, d, generator=g).to(dev)
+    dbeta = torch.sigmoid(torch.randn(n, b, h, generator=g)).to(dev)
+    aq = torch.randn(n, b, 1, h, d, generator=g).to(dev, torch.bfloat16)
+    ak = torch.randn(n, b, 1, h, d, generator=g).to(dev, torch.bfloat16)
+    av = torch.randn(n, b, 1, h, d, generator=g).to(dev, torch.bfloat16)
+    pos = (w + torch.arange(n)).view(n, 1, 1).expand(n, b, 1).contiguous().to(dev)
+
+    def run_all():
+        for s in range(n):
+            delta_scan_step_fused(dq[s], dk[s], dv[s], dbeta[s], state, out_state=state)
+            ring_attention(aq[s], ak[s], av[s], pos[s], ring, inplace=True, check_positions=False)
+
+    with torch.no_grad():
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            run_all()
+        torch.cuda.current_stream().wait_stream(side)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            run_all()
+        times = []
+        for _ in range(reps):
+            ring.pos.copy_(pos0)
+            ring.valid.copy_(valid0)
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            torch.cuda.synchronize()
+            e0.record()
+            graph.replay()
+            e1.record()
+            torch.cuda.synchronize()
+            times.append(e0.elapsed_time(e1))
+    ms = statistics.median(times)
+    return {"ms_256_steps": ms, "tok_s": b * n / (ms / 1e3), "us_per_step": 1e3 * ms / n}
+
+
+# ---- CPU baseline ---------------------------------------------------------------------------------
+def cpu_baseline(torch) -> dict:
+    from oracle.attention import window_attention as oracle_window
+    from oracle.delta import delta_scan_chunked
+
+    threads = max(1, min(16, os.cpu_count() or 1))
+    torch.set_num_threads(threads)
+    sb = B  # the whole step's batch
+    q, k, v, beta, s0 = scan_inputs(torch, torch.device("cpu"), b=sb)
+    aq, ak, av = attn_inputs(torch, torch.device("cpu"), b=sb)
+    q, k, v, beta = (x.float() for x in (q, k, v, beta))
+    aq, ak, av = (x.float() for x in (aq, ak, av))
+    times = []
+    for i in range(6):
+        t0 = time.perf_counter()
+        delta_scan_chunked(q, k, v, beta, s0, 64)
+        oracle_window(aq, ak, av, WINDOW)
+        if i:  # the first run warms up
+            times.append(time.perf_counter() - t0)
+    t = statistics.median(times)
+    model = platform.processor() or "unknown"
+    try:
+        with open("/proc/cpuinfo", encoding="utf-8") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {"value": sb * T / t, "unit": "tok/s", "cores": torch.get_num_threads(), "kind": "port",
+            "sample": f"one full step on the CPU: oracle delta_scan_chunked + window_attention in fp32 on the "
+                      f"same inputs (B={sb}, T={T}, H={H}, d={D}, w={WINDOW}), median of 5 after 1 warm-up, {model}"}
+
+
+def traffic_from_profiles(kernel: str) -> float | None:
+    path = ROOT / "profiles" / "hbm_traffic.json"
+    if not path.exists():
+        return None
+    try:
+        data = json.loads(path.read_text())
+        return float(data[kernel]["bytes_per_launch"])
+    except (KeyError, ValueError, TypeError):
+        return None
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-decode", action="store_true")
+    args = ap.parse_args()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(f"bench.py measures one GPU: the mixers shard over (batch, head) with no exchange, and this build "
+              f"runs no multi-GPU path (asked for --gpus {args.gpus}, WORLD_SIZE {world})", file=sys.stderr)
+        return 2
+
+    import torch
+
+    if not torch.cuda.is_available():
+        log("no HIP device")
+        return 1
+    from vesper.kernels import _lib
+
+    _lib.library()  # fail loudly if the kernels are not built
+
+    pre = time_prefill(torch, args.steps, args.warmup)
+    tok_s = B * T / (pre["step_ms"] / 1e3)
+    s_bytes, s_flops = scan_bytes(B, T, H, D), scan_flops(B, T, H, D)
+    a_bytes, a_flops = attn_bytes(B, T, H, H, D), attn_flops(B, T, H, D, WINDOW)
+    attn4_ms = time_attention_config(torch)
+    dec = None if args.no_decode else time_decode(torch)
+
+    scan_dominant = pre["scan_ms"] >= pre["attn_ms"]
+    if scan_dominant:
+        name, ms, nbytes, flops = "delta_scan (prep + chain kernels)", pre["scan_ms"], s_bytes, s_flops
+        traffic = traffic_from_profiles("delta_scan")
+    else:
+        name, ms, nbytes, flops = "window_attn_kernel", pre["attn_ms"], a_bytes, a_flops
+        traffic = traffic_from_profiles("window_attn")
+    achieved = nbytes / (ms / 1e3) / 1e9
+    roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic, "kernel": name,
+                "algorithmic_bytes": nbytes, "algorithmic_flops": flops,
+                "mfma_frac_bf16": round(flops / (ms / 1e3) / 1e12 / BF16_PEAK_TFLOPS, 4),
+                "avg_launch_ms": round(ms, 4)}
+
+    result = {
+        "metric": "delta-scan+window-attn prefill tok/s @T=4096; decode tok/s; % of roofline",
+        "value": round(tok_s, 1),
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(pre["step_ms"], 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1); q, k L2-normalised; beta = sigmoid(N(0,1)); S0 ~ N(0, 0.02^2))",
+        "config": {
+            "workload": "column mixers prefill: delta scan B8 T4096 H8 d64 chunk 64 (bf16 in, fp32 state) + "
+                        "window attention B8 T4096 H8 D64 w512 (bf16)",
+            "global_batch": B, "seq_len": T, "heads": H, "head_dim": D, "window": WINDOW, "parallelism": "none",
+        },
+        "kernels": {
+            "delta_scan_ms": round(pre["scan_ms"], 4),
+            "delta_scan_tok_s": round(B * T / (pre["scan_ms"] / 1e3), 1),
+            "delta_scan_hbm_frac": round(s_bytes / (pre["scan_ms"] / 1e3) / 1e9 / HBM_PEAK_GBS, 4),
+            "delta_scan_mfma_frac_bf16": round(s_flops / (pre["scan_ms"] / 1e3) / 1e12 / BF16_PEAK_TFLOPS, 4),
+            "window_attn_b8_ms": round(pre["attn_ms"], 4),
+            "window_attn_b4_ms": round(attn4_ms, 4),
+            "window_attn_b4_tok_s": round(ATTN_B * T / (attn4_ms / 1e3), 1),
+            "window_attn_b4_hbm_frac": round(attn_bytes(ATTN_B, T, H, H, D) / (attn4_ms / 1e3) / 1e9 / HBM_PEAK_GBS, 4),
+            "window_attn_b4_mfma_frac_bf16": round(attn_flops(ATTN_B, T, H, D, WINDOW) / (attn4_ms / 1e3) / 1e12 / BF16_PEAK_TFLOPS, 4),
+        },
+        "roofline": roofline,
+    }
+    if dec is not None:
+        step_bytes = decode_step_bytes(DEC_B, H, D, DEC_W)
+        result["decode"] = {
+            "workload": "256 steps, batch 64, H8 d64: fp32 delta step on S [64,8,64,64] + attention over a 512-entry "
+                        "bf16 KV ring, one HIP graph",
+            "tok_s": round(dec["tok_s"], 1), "us_per_step": round(dec["us_per_step"], 3),
+            "hbm_frac": round(step_bytes / (dec["us_per_step"] / 1e6) / 1e9 / HBM_PEAK_GBS, 4),
+            "algorithmic_bytes_per_step": step_bytes,
+        }
+    if not args.no_cpu_baseline:
+        result["cpu_baseline"] = cpu_baseline(torch)
+    log(f"prefill step {pre['step_ms']:.3f} ms (scan {pre['scan_ms']:.3f}, attn {pre['attn_ms']:.3f}), wall {pre['wall_s']:.2f} s")
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())
