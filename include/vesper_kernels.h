@@ -44,8 +44,8 @@ int vsp_abi_version(void);
  * Replaces the fla-core 0.5.2 calls behind vesper/kernels/delta_scan.py:122-129 (`_run`):
  * `chunk_delta_rule` for the bf16 entry (delta_scan.py:132-153) and
  * `fused_recurrent_delta_rule` for the fp32 entry (delta_scan.py:156-187).
- * D <= 256. D in {16, 32, 64, 128} runs the chunked WY/UT MFMA path (64-token chunks); other
- * widths, and T below 16, run the token-serial kernel.
+ * D <= 256. D in {16, 32, 64, 128} (bf16) or {16, 32, 64} (fp32) runs the chunked WY/UT MFMA path
+ * (64-token chunks); other widths, and T below 16, run the token-serial kernel.
  * `workspace` holds the per-chunk UT matrices of the chunked path; it needs
  * vsp_delta_scan_workspace_bytes(...) bytes (0 when the serial path runs; then it may be NULL). */
 size_t vsp_delta_scan_workspace_bytes(int B, int T, int H, int D, int fp32_inputs);

@@ -25,8 +25,10 @@ def test_the_workspace_size_covers_every_chunk():
     from vesper.kernels import _lib
 
     lib = _lib.library()
-    assert lib.vsp_delta_scan_workspace_bytes(8, 4096, 8, 64, 0) == 8 * 8 * 64 * 64 * 64 * 2
-    assert lib.vsp_delta_scan_workspace_bytes(2, 130, 3, 16, 1) == 2 * 3 * 3 * 64 * 64 * 4
+    # ten 16x16 lower tiles of the UT factor per 64-token chunk
+    assert lib.vsp_delta_scan_workspace_bytes(8, 4096, 8, 64, 0) == 8 * 8 * 64 * 2560 * 2
+    assert lib.vsp_delta_scan_workspace_bytes(2, 130, 3, 16, 1) == 2 * 3 * 3 * 2560 * 4
+    assert lib.vsp_delta_scan_workspace_bytes(2, 130, 3, 128, 1) == 0  # fp32 at 128 runs token by token
     assert lib.vsp_delta_scan_workspace_bytes(2, 130, 3, 48, 1) == 0  # token-serial width
     assert lib.vsp_delta_scan_workspace_bytes(2, 10, 3, 64, 0) == 0  # short sequences are serial
 

@@ -128,236 +128,527 @@ __global__ __launch_bounds__(256) void delta_serial_kernel(const TIn* __restrict
 }
 
 // --------------------------------------------------------------------------------------------
-// chunk preparation: T = (I + A)^-1 diag(beta) per 64-token chunk
+// MFMA operand flavours
 // --------------------------------------------------------------------------------------------
-__constant__ int kTriRow[10] = {0, 1, 1, 2, 2, 2, 3, 3, 3, 3};
-__constant__ int kTriCol[10] = {0, 0, 1, 0, 1, 2, 0, 1, 2, 3};
+__device__ __forceinline__ int lane_group() { return (threadIdx.x & 63) >> 4; }
 
-template <typename TIn, typename E, int DK>
-__global__ __launch_bounds__(256) void delta_prep_kernel(const TIn* __restrict__ k, const TIn* __restrict__ beta,
-                                                         E* __restrict__ tmat, int T, int H) {
-  constexpr int KS = Mfma<E>::kstep;
-  constexpr int DKP = DK < KS ? KS : DK;
-  constexpr int PK = DKP + (sizeof(E) == 2 ? 8 : 1);
-  constexpr int PA = 65;
-  __shared__ __align__(16) E sK[64 * PK];
-  __shared__ float sA[64 * PA];
-  __shared__ float sX[64 * PA];
-  __shared__ float sY[4][16 * 17];
-  __shared__ float sB[64];
+// Within a wave, make LDS writes of any lane visible to later LDS reads of any lane.
+__device__ __forceinline__ void wave_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
 
-  const int nc = (T + kChunk - 1) / kChunk;
-  const int g = blockIdx.x;
-  const int c = g % nc, bh = g / nc;
-  const int b = bh / H, h = bh - b * H;
-  const int t0 = c * kChunk, nv = min(kChunk, T - t0);
-  const int w = threadIdx.x >> 6, l = threadIdx.x & 63;
-  const int lc = l & 15, lr = 4 * (l >> 4);
-
-  for (int i = threadIdx.x; i < 64 * DKP; i += 256) {
-    const int r = i / DKP, e = i - r * DKP;
-    const float x = (r < nv && e < DK) ? to_f32(k[(((size_t)b * T + t0 + r) * H + h) * DK + e]) : 0.f;
-    sK[r * PK + e] = from_f32<E>(x);
-  }
-  if (threadIdx.x < 64) sB[threadIdx.x] = (int)threadIdx.x < nv ? to_f32(beta[((size_t)b * T + t0 + threadIdx.x) * H + h]) : 0.f;
-  for (int i = threadIdx.x; i < 64 * PA; i += 256) sX[i] = 0.f;
-  __syncthreads();
-
-  // A = beta_i (K K^T)_ij below the diagonal, lower 16x16 tiles only
-  for (int t = w; t < 10; t += 4) {
-    const int ti = kTriRow[t], tj = kTriCol[t];
-    const f32x4 acc = Mfma<E>::run(sK + 16 * ti * PK, PK, sK + 16 * tj * PK, PK, DKP, zero4());
-    const int cc = 16 * tj + lc;
+// "Acc" flavour: the B operand is a pair of accumulator tiles (rows 16 apart, 32 k values), so a
+// lane of group g supplies k = 4g + r and 16 + 4g + r (r = 0..3); the A operand is read from a
+// row-major LDS row with that same k permutation. Products of two chained contractions never
+// leave registers this way.
+template <typename E> struct Acc;
+template <> struct Acc<__bf16> {
+  struct B { bf16x8 v; };
+  __device__ __forceinline__ static B pack(f32x4 t0, f32x4 t1) {
+    B b;
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      const int rr = 16 * ti + lr + r;
-      sA[rr * PA + cc] = rr > cc ? sB[rr] * acc[r] : 0.f;
+      b.v[r] = (__bf16)t0[r];
+      b.v[4 + r] = (__bf16)t1[r];
     }
+    return b;
   }
-  __syncthreads();
-
-  // diagonal blocks: wave w inverts I + A_ww by forward substitution, one lane per column
-  if (l < 16) {
-    const float* ab = sA + 16 * w * PA + 16 * w;
-    float x[16];
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      float s = (i == l) ? 1.f : 0.f;
-#pragma unroll
-      for (int j = 0; j < i; ++j) s -= ab[i * PA + j] * x[j];
-      x[i] = s;
-    }
-#pragma unroll
-    for (int i = 0; i < 16; ++i) sX[(16 * w + i) * PA + 16 * w + l] = x[i];
+  __device__ __forceinline__ static f32x4 mma(const __bf16* arow, const B& b, f32x4 acc) {
+    const int g = lane_group();
+    const bf16x4 lo = *reinterpret_cast<const bf16x4*>(arow + 4 * g);
+    const bf16x4 hi = *reinterpret_cast<const bf16x4*>(arow + 16 + 4 * g);
+    const bf16x8 a = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b.v, acc, 0, 0, 0);
   }
-  __syncthreads();
-
-  // off-diagonal blocks by distance d: X_ij = -X_ii sum_{m=j}^{i-1} A_im X_mj, i = j + d
-  for (int d = 1; d < 4; ++d) {
-    const int bi = w + d, bj = w;
-    const bool mine = bi < 4;
-    if (mine) {
-      f32x4 y = zero4();
-      for (int m = bj; m < bi; ++m)
-        y = mfma_f32_rowmajor_b(sA + 16 * bi * PA + 16 * m, PA, sX + 16 * m * PA + 16 * bj, PA, 16, y);
-      store_tile<float>(&sY[w][0], 17, y);
-    }
-    __syncthreads();
-    if (mine) {
-      const f32x4 x = mfma_f32_rowmajor_b(sX + 16 * bi * PA + 16 * bi, PA, &sY[w][0], 17, 16, zero4());
-      store_tile<float>(sX + 16 * bi * PA + 16 * bj, PA, -x);
-    }
-    __syncthreads();
+};
+template <> struct Acc<float> {
+  struct B { f32x4 t0, t1; };
+  __device__ __forceinline__ static B pack(f32x4 t0, f32x4 t1) { return B{t0, t1}; }
+  __device__ __forceinline__ static f32x4 mma(const float* arow, const B& b, f32x4 acc) {
+    const int g = lane_group();
+    const f32x4 lo = *reinterpret_cast<const f32x4*>(arow + 4 * g);
+    const f32x4 hi = *reinterpret_cast<const f32x4*>(arow + 16 + 4 * g);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(lo[r], b.t0[r], acc, 0, 0, 0);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(hi[r], b.t1[r], acc, 0, 0, 0);
+    return acc;
   }
+};
 
-  E* out = tmat + (size_t)g * kChunk * kChunk;
-  for (int i = threadIdx.x; i < kChunk * kChunk; i += 256) {
-    const int r = i >> 6, cidx = i & 63;
-    out[i] = from_f32<E>(cidx <= r ? sX[r * PA + cidx] * sB[cidx] : 0.f);
+// "Nat" flavour: rows loaded straight from memory, K values along the row. bf16: lane group g holds
+// k = 32s + 8g + e (s < K/32, e < 8). fp32: k = (K/4) g + 4s + e (s < K/16, e < 4), so each lane
+// reads one contiguous run of its row.
+template <typename E, int K> struct Nat;
+template <int K> struct Nat<__bf16, K> {
+  static constexpr int NREG = K / 32;
+  static constexpr int PER = 8;
+  using R = bf16x8;
+  __device__ __forceinline__ static int feat(int s) { return 32 * s + 8 * lane_group(); }
+  __device__ __forceinline__ static f32x4 mma(const R* a, const R* b, f32x4 acc) {
+#pragma unroll
+    for (int s = 0; s < NREG; ++s) acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[s], b[s], acc, 0, 0, 0);
+    return acc;
+  }
+  __device__ __forceinline__ static f32x4 mma_lds(const __bf16* arow, const R* b, f32x4 acc) {
+#pragma unroll
+    for (int s = 0; s < NREG; ++s) {
+      const R a = *reinterpret_cast<const R*>(arow + feat(s));
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b[s], acc, 0, 0, 0);
+    }
+    return acc;
+  }
+};
+template <int K> struct Nat<float, K> {
+  static constexpr int FPL = K / 4;
+  static constexpr int NREG = FPL / 4;
+  static constexpr int PER = 4;
+  using R = f32x4;
+  __device__ __forceinline__ static int feat(int s) { return FPL * lane_group() + 4 * s; }
+  __device__ __forceinline__ static f32x4 mma(const R* a, const R* b, f32x4 acc) {
+#pragma unroll
+    for (int s = 0; s < NREG; ++s)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[s][e], b[s][e], acc, 0, 0, 0);
+    return acc;
+  }
+  __device__ __forceinline__ static f32x4 mma_lds(const float* arow, const R* b, f32x4 acc) {
+#pragma unroll
+    for (int s = 0; s < NREG; ++s) {
+      const f32x4 a = *reinterpret_cast<const f32x4*>(arow + feat(s));
+#pragma unroll
+      for (int e = 0; e < 4; ++e) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[e], b[s][e], acc, 0, 0, 0);
+    }
+    return acc;
+  }
+};
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+template <typename E>
+__device__ __forceinline__ E elem_of(const u32x4& v, int i) {
+  if constexpr (sizeof(E) == 2) {
+    const uint32_t w = v[i >> 1];
+    const uint16_t hbits = (i & 1) ? (uint16_t)(w >> 16) : (uint16_t)(w & 0xffffu);
+    return __builtin_bit_cast(E, hbits);
+  } else {
+    // through a scalar: a bit_cast applied to the vector element directly was compiled as
+    // element 0 for every i by this toolchain
+    const uint32_t w = v[i];
+    return __uint_as_float(w);
   }
 }
 
+// The compact per-chunk UT factor: the ten 16x16 tiles (i, j), j <= i, of T = (I + A)^-1 diag(beta),
+// tile t = i (i + 1) / 2 + j, each row-major.
+constexpr int kTiles = 10;
+constexpr int kTileElems = 256;
+constexpr int kChunkT = kTiles * kTileElems;
+// constexpr (not __constant__): indices into register arrays must fold at compile time
+constexpr int kTileRow[kTiles] = {0, 1, 1, 2, 2, 2, 3, 3, 3, 3};
+constexpr int kTileCol[kTiles] = {0, 0, 1, 0, 1, 2, 0, 1, 2, 3};
+__device__ __forceinline__ int tile_of(int i, int j) { return i * (i + 1) / 2 + j; }
+
 // --------------------------------------------------------------------------------------------
-// the chunk chain: one (b, h, value slice) per workgroup, chunks in order
+// chunk preparation: one wave per 64-token chunk, no workgroup barriers
 // --------------------------------------------------------------------------------------------
 template <typename TIn, typename E, int DK>
-__global__ __launch_bounds__(256) void delta_chain_kernel(const TIn* __restrict__ q, const TIn* __restrict__ k,
-                                                          const TIn* __restrict__ v, const E* __restrict__ tmat,
-                                                          const float* __restrict__ s_in, float* __restrict__ s_out,
-                                                          TIn* __restrict__ o, const uint8_t* __restrict__ active,
-                                                          int T, int H) {
+__global__ __launch_bounds__(256) void delta_prep_kernel(const TIn* __restrict__ k, const TIn* __restrict__ beta,
+                                                         E* __restrict__ tmat, int T, int H, int total) {
+  constexpr int DKP = DK < 32 ? 32 : DK;
+  using N = Nat<E, DKP>;
+  constexpr int TP = 17;  // pitch of the fp32 16x16 tiles
+  __shared__ float sA[4][kTiles][16 * TP];
+  __shared__ float sXd[4][4][16 * TP];
+
+  const int w = threadIdx.x >> 6, l = threadIdx.x & 63;
+  const int lq = l & 15, g = l >> 4;
+  const int chunk = blockIdx.x * 4 + w;
+  if (chunk >= total) return;  // whole waves only: this kernel has no workgroup barrier
+  const int nc = (T + kChunk - 1) / kChunk;
+  const int c = chunk % nc, bh = chunk / nc;
+  const int b = bh / H, h = bh - b * H;
+  const int t0 = c * kChunk, nv = min(kChunk, T - t0);
+  float* A = &sA[w][0][0];
+  float* Xd = &sXd[w][0][0];
+
+  typename N::R kn[4][N::NREG];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int tok = 16 * i + lq;
+    const TIn* row = k + (((size_t)b * T + t0 + tok) * H + h) * DK;
+#pragma unroll
+    for (int s = 0; s < N::NREG; ++s) {
+      const int f = N::feat(s);
+      if (tok < nv && f < DK) {
+        kn[i][s] = *reinterpret_cast<const typename N::R*>(row + f);
+      } else {
+#pragma unroll
+        for (int e = 0; e < N::PER; ++e) kn[i][s][e] = from_f32<E>(0.f);
+      }
+    }
+  }
+  const float bl = l < nv ? to_f32(beta[((size_t)b * T + t0 + l) * H + h]) : 0.f;
+
+  // A = beta_row (K K^T) strictly below the diagonal, ten lower tiles
+#pragma unroll
+  for (int t = 0; t < kTiles; ++t) {
+    const int ti = kTileRow[t], tj = kTileCol[t];
+    const f32x4 gr = N::mma(kn[ti], kn[tj], zero4());
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int row = 16 * ti + 4 * g + r, col = 16 * tj + lq;
+      const float br = __shfl(bl, row);
+      A[t * 16 * TP + (4 * g + r) * TP + lq] = row > col ? br * gr[r] : 0.f;
+    }
+  }
+  wave_sync();
+
+  // diagonal blocks: lane (blk, col) solves (I + A_bb) x = e_col by forward substitution
+  {
+    const int blk = g, col = lq;
+    const float* ab = A + tile_of(blk, blk) * 16 * TP;
+    float x[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      float s = (i == col) ? 1.f : 0.f;
+#pragma unroll
+      for (int j = 0; j < i; ++j) s -= ab[i * TP + j] * x[j];
+      x[i] = s;
+    }
+#pragma unroll
+    for (int i = 0; i < 16; ++i) Xd[blk * 16 * TP + i * TP + col] = x[i];
+  }
+  wave_sync();
+
+  // fp32 16x16x16 products; k permuted as 4g + r so accumulator tiles serve as B operands
+  auto mm = [&](const float* atile, const float* btile_lds, const f32x4* breg, f32x4 acc) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const float av = atile[lq * TP + 4 * g + r];
+      const float bv = breg ? (*breg)[r] : btile_lds[(4 * g + r) * TP + lq];
+      acc = __builtin_amdgcn_mfma_f32_16x16x4f32(av, bv, acc, 0, 0, 0);
+    }
+    return acc;
+  };
+  const float* Xt0 = Xd;
+  auto xd = [&](int blk) { return Xt0 + blk * 16 * TP; };
+  auto at = [&](int i, int j) { return (const float*)(A + tile_of(i, j) * 16 * TP); };
+
+  f32x4 x1[3], x2[2], x3;
+#pragma unroll
+  for (int bb = 0; bb < 3; ++bb) {
+    const f32x4 y = mm(at(bb + 1, bb), xd(bb), nullptr, zero4());
+    x1[bb] = -mm(xd(bb + 1), nullptr, &y, zero4());
+  }
+#pragma unroll
+  for (int bb = 0; bb < 2; ++bb) {
+    f32x4 y = mm(at(bb + 2, bb), xd(bb), nullptr, zero4());
+    y = mm(at(bb + 2, bb + 1), nullptr, &x1[bb], y);
+    x2[bb] = -mm(xd(bb + 2), nullptr, &y, zero4());
+  }
+  {
+    f32x4 y = mm(at(3, 0), xd(0), nullptr, zero4());
+    y = mm(at(3, 1), nullptr, &x1[0], y);
+    y = mm(at(3, 2), nullptr, &x2[0], y);
+    x3 = -mm(xd(3), nullptr, &y, zero4());
+  }
+
+  // T = X diag(beta), compact tiles
+  E* out = tmat + (size_t)chunk * kChunkT;
+  {
+    const int blk = g, col = lq;
+    const float bc = __shfl(bl, 16 * blk + col);
+#pragma unroll
+    for (int i = 0; i < 16; ++i)
+      out[tile_of(blk, blk) * kTileElems + i * 16 + col] = from_f32<E>(Xd[blk * 16 * TP + i * TP + col] * bc);
+  }
+  auto put = [&](int i, int j, const f32x4& x) {
+    const float bc = __shfl(bl, 16 * j + lq);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) out[tile_of(i, j) * kTileElems + (4 * g + r) * 16 + lq] = from_f32<E>(x[r] * bc);
+  };
+  put(1, 0, x1[0]);
+  put(2, 1, x1[1]);
+  put(3, 2, x1[2]);
+  put(2, 0, x2[0]);
+  put(3, 1, x2[1]);
+  put(3, 0, x3);
+}
+
+// --------------------------------------------------------------------------------------------
+// the chunk chain: wave 0 carries the state of one (b, h, 16-column value slice) through the chunks
+// with every intermediate in registers; waves 1..NH stage chunk data ahead of it, form
+// P^T = tril(Q K^T)^T and write the outputs O^T = H^T Q^T + Delta^T P^T one iteration behind it.
+// --------------------------------------------------------------------------------------------
+// Helper waves per workgroup (= chunks staged ahead of the chain). Seven keep the bf16 chain fed
+// through HBM latency at head width 64; wider heads and fp32 need the registers of a 4-wave group.
+template <typename E, int DK> struct ChainShape {
+  static constexpr int NH = (sizeof(E) == 2 && DK <= 64) ? 7 : 3;
+};
+
+template <typename TIn, typename E, int DK>
+__global__ __launch_bounds__(64 * (ChainShape<E, DK>::NH + 1)) void delta_chain_kernel(
+    const TIn* __restrict__ q, const TIn* __restrict__ k, const TIn* __restrict__ v, const E* __restrict__ tmat,
+    const float* __restrict__ s_in, float* __restrict__ s_out, TIn* __restrict__ o, const uint8_t* __restrict__ active,
+    int T, int H) {
+  constexpr int NH = ChainShape<E, DK>::NH;
+  constexpr int NW = NH + 1;
   constexpr int BV = 16;
   constexpr int NS = DK / BV;
-  constexpr int KS = Mfma<E>::kstep;
-  constexpr int DKP = DK < KS ? KS : DK;
-  constexpr int PAD = sizeof(E) == 2 ? 8 : 1;
+  constexpr bool BF = sizeof(E) == 2;
+  constexpr int DKP = DK < 32 ? 32 : DK;
+  constexpr int PAD = BF ? 8 : 4;
   constexpr int PK = DKP + PAD;
   constexpr int PT = 64 + PAD;
   constexpr int HB = DK / 16;
-  constexpr int HPW = (HB + 3) / 4;
+  constexpr int KBF = DKP / 32;
+  constexpr int EPS = 16 / (int)sizeof(E);               // elements per 16-byte segment
+  constexpr int TSEG = kChunkT * (int)sizeof(E) / 16 / 64;  // compact-T segments per lane
+  constexpr int VSPT = BV * (int)sizeof(E) / 16;            // V segments per token
+  constexpr int VSEG = 64 * VSPT / 64;                      // V segments per lane
+  constexpr bool kKeepQ = false;  // re-read Q (an L2 hit) for the outputs: keeps the helpers under 256 VGPRs
+  using N = Nat<E, DKP>;
+  using AB = typename Acc<E>::B;
+  using NR = typename N::R;
 
-  __shared__ __align__(16) E sQ[64 * PK];
-  __shared__ __align__(16) E sK[64 * PK];
-  __shared__ __align__(16) E sKt[DK * PT];
-  __shared__ __align__(16) E sT[64 * PT];
-  __shared__ __align__(16) E sP[64 * PT];
-  __shared__ __align__(16) E sHt[BV * PK];
-  __shared__ __align__(16) E sRt[BV * PT];
-  __shared__ __align__(16) E sDt[BV * PT];
+  __shared__ __align__(16) E sK[2][64 * PK];
+  __shared__ __align__(16) E sKt[2][DK * PT];
+  __shared__ __align__(16) E sT[2][64 * PT];
+  __shared__ __align__(16) E sVt[2][BV * PT];
+  __shared__ __align__(16) E sHo[2][BV * PK];
+  __shared__ __align__(16) E sDo[2][BV * PT];
 
   const int lg = xcd_logical_block(blockIdx.x, gridDim.x);
   const int slice = lg % NS, bh = lg / NS;
   const int b = bh / H, h = bh - b * H;
   const int v0 = slice * BV;
-  const int w = threadIdx.x >> 6, l = threadIdx.x & 63;
-  const int lc = l & 15, lr = 4 * (l >> 4);
+  const int wave = threadIdx.x >> 6, l = threadIdx.x & 63;
+  const int lq = l & 15, g = l >> 4;
   const int nc = (T + kChunk - 1) / kChunk;
 
-  for (int i = threadIdx.x; i < 64 * PK; i += 256) {
-    sQ[i] = from_f32<E>(0.f);
-    sK[i] = from_f32<E>(0.f);
-  }
-  for (int i = threadIdx.x; i < 64 * PT; i += 256) sP[i] = from_f32<E>(0.f);
-  for (int i = threadIdx.x; i < BV * PK; i += 256) sHt[i] = from_f32<E>(0.f);
-
-  f32x4 hacc[HPW];
+  {
+    const E zero = from_f32<E>(0.f);
+    E* base[6] = {&sK[0][0], &sKt[0][0], &sT[0][0], &sVt[0][0], &sHo[0][0], &sDo[0][0]};
+    const int len[6] = {2 * 64 * PK, 2 * DK * PT, 2 * 64 * PT, 2 * BV * PT, 2 * BV * PK, 2 * BV * PT};
 #pragma unroll
-  for (int m = 0; m < HPW; ++m) {
-    const int rb = w + 4 * m;
-#pragma unroll
-    for (int r = 0; r < 4; ++r)
-      hacc[m][r] = rb < HB ? s_in[((size_t)bh * DK + 16 * rb + lr + r) * DK + v0 + lc] : 0.f;
-  }
-  __syncthreads();
-#pragma unroll
-  for (int m = 0; m < HPW; ++m) {
-    const int rb = w + 4 * m;
-    if (rb < HB) store_tile_t<E>(sHt + 16 * rb, PK, hacc[m]);
+    for (int a = 0; a < 6; ++a)
+      for (int i = threadIdx.x; i < len[a]; i += 64 * NW) base[a][i] = zero;
   }
 
-  const int kend = ((16 * (w + 1) + KS - 1) / KS) * KS;
-  for (int c = 0; c < nc; ++c) {
-    const int t0 = c * kChunk, nv = min(kChunk, T - t0);
-    __syncthreads();
-    for (int i = threadIdx.x; i < 64 * DK; i += 256) {
-      const int r = i / DK, e = i - r * DK;
-      float xq = 0.f, xk = 0.f;
-      if (r < nv) {
-        const size_t off = (((size_t)b * T + t0 + r) * H + h) * DK + e;
-        xq = to_f32(q[off]);
-        xk = to_f32(k[off]);
-      }
-      sQ[r * PK + e] = from_f32<E>(xq);
-      sK[r * PK + e] = from_f32<E>(xk);
-      sKt[e * PT + r] = from_f32<E>(xk);
-    }
-    const E* tsrc = tmat + ((size_t)bh * nc + c) * kChunk * kChunk;
-    for (int i = threadIdx.x; i < kChunk * kChunk; i += 256) sT[(i >> 6) * PT + (i & 63)] = tsrc[i];
-    __syncthreads();
+  // ---- helper state ----
+  const int hj = wave - 1;  // helper index; chunks c with c % NH == hj
+  NR qn[4][N::NREG], kn[4][N::NREG];
+  u32x4 tseg[TSEG], vseg[VSEG];
+  uint8_t actn[4];
+  NR qk[kKeepQ ? 4 : 1][kKeepQ ? N::NREG : 1];  // Q kept for the output of the pending chunk
+  AB pt[6];
+  uint8_t actk[4];
 
-    // stage 1: token rows 16w.. - K H, Q H and the causal tiles of Q K^T
-    const E* kw = sK + 16 * w * PK;
-    const E* qw = sQ + 16 * w * PK;
-    const f32x4 kh = Mfma<E>::run(kw, PK, sHt, PK, DKP, zero4());
-    const f32x4 qh = Mfma<E>::run(qw, PK, sHt, PK, DKP, zero4());
-    for (int j = 0; j <= w; ++j) {
-      const f32x4 p = Mfma<E>::run(qw, PK, sK + 16 * j * PK, PK, DKP, zero4());
-      const int cc = 16 * j + lc;
+  auto token_row = [&](const TIn* base, int c, int tok) {
+    return base + (((size_t)b * T + (size_t)c * kChunk + tok) * H + h) * DK;
+  };
+  auto load_rows = [&](NR (&dst)[4][N::NREG], const TIn* base, int c) {
+    const int nvc = min(kChunk, T - c * kChunk);
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int rr = 16 * w + lr + r;
-        sP[rr * PT + cc] = from_f32<E>(cc <= rr ? p[r] : 0.f);
+    for (int i = 0; i < 4; ++i) {
+      const int tok = 16 * i + lq;
+      const TIn* row = token_row(base, c, tok);
+#pragma unroll
+      for (int s = 0; s < N::NREG; ++s) {
+        const int f = N::feat(s);
+        if (tok < nvc && f < DK) {
+          dst[i][s] = *reinterpret_cast<const NR*>(row + f);
+        } else {
+#pragma unroll
+          for (int e = 0; e < N::PER; ++e) dst[i][s][e] = from_f32<E>(0.f);
+        }
       }
     }
-    f32x4 rv;
+  };
+  auto issue_loads = [&](int c) {
+    load_rows(qn, q, c);
+    load_rows(kn, k, c);
+    const u32x4* ts = reinterpret_cast<const u32x4*>(tmat + ((size_t)bh * nc + c) * kChunkT);
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int t = 16 * w + lr + r;
-      const float vv = t < nv ? to_f32(v[(((size_t)b * T + t0 + t) * H + h) * DK + v0 + lc]) : 0.f;
-      rv[r] = vv - kh[r];
-    }
-    store_tile_t<E>(sRt + 16 * w, PT, rv);
-    __syncthreads();
-
-    // stage 2: Delta = T R for token rows 16w..
-    const f32x4 dl = Mfma<E>::run(sT + 16 * w * PT, PT, sRt, PT, kend, zero4());
-    store_tile_t<E>(sDt + 16 * w, PT, dl);
-    __syncthreads();
-
-    // stage 3: O = Q H + P Delta, then H += K^T Delta
-    const f32x4 ov = Mfma<E>::run(sP + 16 * w * PT, PT, sDt, PT, kend, qh);
+    for (int j = 0; j < TSEG; ++j) tseg[j] = ts[l + 64 * j];
+    const int nvc = min(kChunk, T - c * kChunk);
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int t = 16 * w + lr + r;
-      if (t < nv) {
-        const size_t tok = (size_t)b * T + t0 + t;
-        const bool on = active == nullptr || active[tok] != 0;
-        o[(tok * H + h) * DK + v0 + lc] = from_f32<TIn>(on ? ov[r] : 0.f);
+    for (int j = 0; j < VSEG; ++j) {
+      const int sg = l + 64 * j, tok = sg / VSPT, part = sg - tok * VSPT;
+      if (tok < nvc) {
+        vseg[j] = *reinterpret_cast<const u32x4*>(token_row(v, c, tok) + v0 + part * EPS);
+      } else {
+        vseg[j] = u32x4{0u, 0u, 0u, 0u};
       }
     }
 #pragma unroll
-    for (int m = 0; m < HPW; ++m) {
-      const int rb = w + 4 * m;
-      if (rb < HB) {
-        hacc[m] = Mfma<E>::run(sKt + 16 * rb * PT, PT, sDt, PT, kChunk, hacc[m]);
-        store_tile_t<E>(sHt + 16 * rb, PK, hacc[m]);
+    for (int i = 0; i < 4; ++i) {
+      const int tok = 16 * i + lq;
+      actn[i] = (tok < nvc && (active == nullptr || active[(size_t)b * T + (size_t)c * kChunk + tok] != 0)) ? 1 : 0;
+    }
+  };
+  auto store_chunk = [&](int c) {
+    const int bs = c & 1;
+    E* K = sK[bs];
+    E* Kt = sKt[bs];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int tok = 16 * i + lq;
+#pragma unroll
+      for (int s = 0; s < N::NREG; ++s) {
+        const int f = N::feat(s);
+        *reinterpret_cast<NR*>(K + tok * PK + f) = kn[i][s];
+#pragma unroll
+        for (int e = 0; e < N::PER; ++e)
+          if (f + e < DK) Kt[(f + e) * PT + tok] = kn[i][s][e];
       }
     }
-  }
+    E* Tm = sT[bs];
 #pragma unroll
-  for (int m = 0; m < HPW; ++m) {
-    const int rb = w + 4 * m;
-    if (rb < HB) {
-#pragma unroll
-      for (int r = 0; r < 4; ++r) s_out[((size_t)bh * DK + 16 * rb + lr + r) * DK + v0 + lc] = hacc[m][r];
+    for (int j = 0; j < TSEG; ++j) {
+      const int el = (l + 64 * j) * EPS;
+      const int t = el / kTileElems, within = el - t * kTileElems;
+      const int row = 16 * kTileRow[t] + within / 16, col = 16 * kTileCol[t] + within % 16;
+      *reinterpret_cast<u32x4*>(Tm + row * PT + col) = tseg[j];
     }
+    E* Vt = sVt[bs];
+#pragma unroll
+    for (int j = 0; j < VSEG; ++j) {
+      const int sg = l + 64 * j, tok = sg / VSPT, part = sg - tok * VSPT;
+#pragma unroll
+      for (int e = 0; e < EPS; ++e) Vt[(part * EPS + e) * PT + tok] = elem_of<E>(vseg[j], e);
+    }
+    // P^T tiles (key tile jj, query tile ii), keys after the query masked, packed per k-block;
+    // each tile is formed right before its pack so at most two are live
+    auto ptile = [&](int jj, int ii) {
+      const f32x4 acc = N::mma(kn[jj], qn[ii], zero4());
+      f32x4 r4;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) r4[r] = (16 * jj + 4 * g + r <= 16 * ii + lq) ? acc[r] : 0.f;
+      return r4;
+    };
+    pt[0] = Acc<E>::pack(ptile(0, 0), zero4());
+    pt[1] = Acc<E>::pack(ptile(0, 1), ptile(1, 1));
+    pt[2] = Acc<E>::pack(ptile(0, 2), ptile(1, 2));
+    pt[3] = Acc<E>::pack(ptile(2, 2), zero4());
+    pt[4] = Acc<E>::pack(ptile(0, 3), ptile(1, 3));
+    pt[5] = Acc<E>::pack(ptile(2, 3), ptile(3, 3));
+    if constexpr (kKeepQ) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int s = 0; s < N::NREG; ++s) qk[i][s] = qn[i][s];
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) actk[i] = actn[i];
+  };
+  auto write_output = [&](int c) {
+    const int bs = c & 1;
+    const int nvc = min(kChunk, T - c * kChunk);
+    NR qr[kKeepQ ? 1 : 4][N::NREG];
+    if constexpr (!kKeepQ) load_rows(qr, q, c);
+    const E* ho = sHo[bs] + lq * PK;
+    const E* dd = sDo[bs] + lq * PT;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      f32x4 acc;
+      if constexpr (kKeepQ) {
+        acc = N::mma_lds(ho, qk[i], zero4());
+      } else {
+        acc = N::mma_lds(ho, qr[i], zero4());
+      }
+      acc = Acc<E>::mma(dd, pt[i == 0 ? 0 : (i == 1 ? 1 : (i == 2 ? 2 : 4))], acc);
+      if (i >= 2) acc = Acc<E>::mma(dd + 32, pt[i == 2 ? 3 : 5], acc);
+      const int tok = 16 * i + lq;
+      if (tok < nvc) {
+        TIn* dst = o + (((size_t)b * T + (size_t)c * kChunk + tok) * H + h) * DK + v0 + 4 * g;
+        const bool on = actk[i] != 0;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) dst[r] = from_f32<TIn>(on ? acc[r] : 0.f);
+      }
+    }
+  };
+
+  // ---- chain state ----
+  f32x4 hreg[HB];
+  if (wave == 0) {
+#pragma unroll
+    for (int m = 0; m < HB; ++m)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) hreg[m][r] = s_in[((size_t)bh * DK + 16 * m + 4 * g + r) * DK + v0 + lq];
+  }
+  auto chain_step = [&](int c) {
+    const int bs = c & 1;
+    AB hb[KBF];
+#pragma unroll
+    for (int kb = 0; kb < KBF; ++kb) hb[kb] = Acc<E>::pack(hreg[2 * kb], 2 * kb + 1 < HB ? hreg[2 * kb + 1] : zero4());
+#pragma unroll
+    for (int m = 0; m < HB; ++m)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) sHo[bs][lq * PK + 16 * m + 4 * g + r] = from_f32<E>(hreg[m][r]);
+    const E* K = sK[bs];
+    f32x4 rr[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      f32x4 kh = zero4();
+#pragma unroll
+      for (int kb = 0; kb < KBF; ++kb) kh = Acc<E>::mma(K + (16 * i + lq) * PK + 32 * kb, hb[kb], kh);
+      const E* vt = sVt[bs] + lq * PT + 16 * i + 4 * g;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) rr[i][r] = to_f32(vt[r]) - kh[r];
+    }
+    const AB rb0 = Acc<E>::pack(rr[0], rr[1]);
+    const AB rb1 = Acc<E>::pack(rr[2], rr[3]);
+    const E* Tm = sT[bs];
+    f32x4 dl[4];
+    dl[0] = Acc<E>::mma(Tm + lq * PT, rb0, zero4());
+    dl[1] = Acc<E>::mma(Tm + (16 + lq) * PT, rb0, zero4());
+    dl[2] = Acc<E>::mma(Tm + (32 + lq) * PT + 32, rb1, Acc<E>::mma(Tm + (32 + lq) * PT, rb0, zero4()));
+    dl[3] = Acc<E>::mma(Tm + (48 + lq) * PT + 32, rb1, Acc<E>::mma(Tm + (48 + lq) * PT, rb0, zero4()));
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) sDo[bs][lq * PT + 16 * i + 4 * g + r] = from_f32<E>(dl[i][r]);
+    const AB db0 = Acc<E>::pack(dl[0], dl[1]);
+    const AB db1 = Acc<E>::pack(dl[2], dl[3]);
+    const E* Kt = sKt[bs];
+#pragma unroll
+    for (int m = 0; m < HB; ++m) {
+      hreg[m] = Acc<E>::mma(Kt + (16 * m + lq) * PT, db0, hreg[m]);
+      hreg[m] = Acc<E>::mma(Kt + (16 * m + lq) * PT + 32, db1, hreg[m]);
+    }
+  };
+
+  __syncthreads();  // zeroed buffers
+  if (wave > 0 && hj < nc) issue_loads(hj);
+  for (int it = -1; it < nc; ++it) {
+    if (wave == 0) {
+      if (it >= 0) chain_step(it);
+    } else {
+      const int cs = it + 1, co = it - 1;
+      if (cs < nc && cs % NH == hj) {
+        store_chunk(cs);
+        if (cs + NH < nc) issue_loads(cs + NH);
+      }
+      if (co >= 0 && co % NH == hj) write_output(co);
+    }
+    __syncthreads();
+  }
+  if (wave > 0 && nc >= 1 && (nc - 1) % NH == hj) write_output(nc - 1);
+  if (wave == 0) {
+#pragma unroll
+    for (int m = 0; m < HB; ++m)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) s_out[((size_t)bh * DK + 16 * m + 4 * g + r) * DK + v0 + lq] = hreg[m][r];
   }
 }
-
 // --------------------------------------------------------------------------------------------
 // host side
 // --------------------------------------------------------------------------------------------
-bool chunked_width(int D) { return D == 16 || D == 32 || D == 64 || D == 128; }
+bool chunked_width(int D, bool fp32) { return D == 16 || D == 32 || D == 64 || (D == 128 && !fp32); }
 constexpr int kSerialBelow = 16;  // shorter sequences run token by token
 
 int check_common(const void* q, const void* k, const void* v, const void* beta, const void* s_in, const void* s_out,
@@ -381,19 +672,20 @@ int launch_serial(const TIn* q, const TIn* k, const TIn* v, const TIn* beta, con
 }
 
 size_t workspace_bytes(int B, int T, int H, int D, bool fp32) {
-  if (B <= 0 || H <= 0 || T < kSerialBelow || !chunked_width(D)) return 0;
+  if (B <= 0 || H <= 0 || T < kSerialBelow || !chunked_width(D, fp32)) return 0;
   const size_t nc = (size_t)(T + kChunk - 1) / kChunk;
-  return (size_t)B * H * nc * kChunk * kChunk * (fp32 ? sizeof(float) : sizeof(uint16_t));
+  return (size_t)B * H * nc * kChunkT * (fp32 ? sizeof(float) : sizeof(uint16_t));
 }
 
 template <typename TIn, typename E, int DK>
 void launch_chunked(const TIn* q, const TIn* k, const TIn* v, const TIn* beta, const float* s_in, float* s_out, TIn* o,
                     E* tmat, const uint8_t* active, int B, int T, int H, hipStream_t stream) {
   const int nc = (T + kChunk - 1) / kChunk;
-  hipLaunchKernelGGL((delta_prep_kernel<TIn, E, DK>), dim3((unsigned)(B * H * nc)), dim3(256), 0, stream, k, beta, tmat,
-                     T, H);
-  hipLaunchKernelGGL((delta_chain_kernel<TIn, E, DK>), dim3((unsigned)(B * H * (DK / 16))), dim3(256), 0, stream, q, k,
-                     v, tmat, s_in, s_out, o, active, T, H);
+  const int total = B * H * nc;
+  hipLaunchKernelGGL((delta_prep_kernel<TIn, E, DK>), dim3((unsigned)((total + 3) / 4)), dim3(256), 0, stream, k, beta,
+                     tmat, T, H, total);
+  hipLaunchKernelGGL((delta_chain_kernel<TIn, E, DK>), dim3((unsigned)(B * H * (DK / 16))),
+                     dim3(64 * (ChainShape<E, DK>::NH + 1)), 0, stream, q, k, v, tmat, s_in, s_out, o, active, T, H);
 }
 
 template <typename TIn, typename E>
@@ -419,7 +711,9 @@ int delta_scan(const TIn* q, const TIn* k, const TIn* v, const TIn* beta, const 
     case 16: launch_chunked<TIn, E, 16>(q, k, v, beta, s_in, s_out, o, tmat, active, B, T, H, stream); break;
     case 32: launch_chunked<TIn, E, 32>(q, k, v, beta, s_in, s_out, o, tmat, active, B, T, H, stream); break;
     case 64: launch_chunked<TIn, E, 64>(q, k, v, beta, s_in, s_out, o, tmat, active, B, T, H, stream); break;
-    default: launch_chunked<TIn, E, 128>(q, k, v, beta, s_in, s_out, o, tmat, active, B, T, H, stream); break;
+    default:
+      if constexpr (sizeof(E) == 2) launch_chunked<TIn, E, 128>(q, k, v, beta, s_in, s_out, o, tmat, active, B, T, H, stream);
+      break;
   }
   return check_launch(who);
 }
