@@ -226,6 +226,7 @@ template <int K> struct Nat<float, K> {
 };
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef short s16x4 __attribute__((ext_vector_type(4)));
 
 template <typename E>
 __device__ __forceinline__ E elem_of(const u32x4& v, int i) {
@@ -409,7 +410,9 @@ __global__ __launch_bounds__(64 * (ChainShape<E, DK>::NH + 1)) void delta_chain_
   constexpr int TSEG = kChunkT * (int)sizeof(E) / 16 / 64;  // compact-T segments per lane
   constexpr int VSPT = BV * (int)sizeof(E) / 16;            // V segments per token
   constexpr int VSEG = 64 * VSPT / 64;                      // V segments per lane
-  constexpr bool kKeepQ = false;  // re-read Q (an L2 hit) for the outputs: keeps the helpers under 256 VGPRs
+  // Q for the outputs: bf16 keeps it in three LDS buffers (written when the chunk is staged, read
+  // two iterations later); fp32 re-reads it from L2 in the helper's idle iteration (no LDS left)
+  constexpr bool kQInLds = BF;
   using N = Nat<E, DKP>;
   using AB = typename Acc<E>::B;
   using NR = typename N::R;
@@ -420,6 +423,7 @@ __global__ __launch_bounds__(64 * (ChainShape<E, DK>::NH + 1)) void delta_chain_
   __shared__ __align__(16) E sVt[2][BV * PT];
   __shared__ __align__(16) E sHo[2][BV * PK];
   __shared__ __align__(16) E sDo[2][BV * PT];
+  __shared__ __align__(16) E sQ[kQInLds ? 3 : 1][kQInLds ? 64 * PK : 16];
 
   const int lg = xcd_logical_block(blockIdx.x, gridDim.x);
   const int slice = lg % NS, bh = lg / NS;
@@ -441,26 +445,28 @@ __global__ __launch_bounds__(64 * (ChainShape<E, DK>::NH + 1)) void delta_chain_
   // ---- helper state ----
   const int hj = wave - 1;  // helper index; chunks c with c % NH == hj
   NR qn[4][N::NREG], kn[4][N::NREG];
-  u32x4 tseg[TSEG], vseg[VSEG];
-  uint8_t actn[4];
-  NR qk[kKeepQ ? 4 : 1][kKeepQ ? N::NREG : 1];  // Q kept for the output of the pending chunk
+  u32x4 tseg[TSEG], vseg[BF ? 1 : VSEG];
+  bf16x4 vn[BF ? 4 : 1];  // bf16: V slice rows, value columns 4g..4g+3 (16x16x16 operand layout)
+  uint8_t actraw[4];  // active bytes as loaded; compared only when staged (no wait at issue)
+  NR qr[kQInLds ? 1 : 4][N::NREG];  // fp32: Q re-read for the pending output
   AB pt[6];
   uint8_t actk[4];
 
-  auto token_row = [&](const TIn* base, int c, int tok) {
-    return base + (((size_t)b * T + (size_t)c * kChunk + tok) * H + h) * DK;
-  };
+  // Rows of one (b, h) from a uniform base with 32-bit lane offsets (the host keeps T*H*DK below
+  // 2^31): one VGPR per address keeps the helpers' staging registers from spilling.
+  const int rstride = H * DK;
+  const size_t bh_base = ((size_t)b * T * H + h) * DK;
   auto load_rows = [&](NR (&dst)[4][N::NREG], const TIn* base, int c) {
     const int nvc = min(kChunk, T - c * kChunk);
+    const TIn* cb = base + bh_base + (size_t)c * kChunk * rstride;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int tok = 16 * i + lq;
-      const TIn* row = token_row(base, c, tok);
 #pragma unroll
       for (int s = 0; s < N::NREG; ++s) {
         const int f = N::feat(s);
         if (tok < nvc && f < DK) {
-          dst[i][s] = *reinterpret_cast<const NR*>(row + f);
+          dst[i][s] = *reinterpret_cast<const NR*>(cb + (tok * rstride + f));
         } else {
 #pragma unroll
           for (int e = 0; e < N::PER; ++e) dst[i][s][e] = from_f32<E>(0.f);
@@ -475,19 +481,36 @@ __global__ __launch_bounds__(64 * (ChainShape<E, DK>::NH + 1)) void delta_chain_
 #pragma unroll
     for (int j = 0; j < TSEG; ++j) tseg[j] = ts[l + 64 * j];
     const int nvc = min(kChunk, T - c * kChunk);
+    if constexpr (BF) {
+      const TIn* cb = v + bh_base + (size_t)c * kChunk * rstride + v0;
 #pragma unroll
-    for (int j = 0; j < VSEG; ++j) {
-      const int sg = l + 64 * j, tok = sg / VSPT, part = sg - tok * VSPT;
-      if (tok < nvc) {
-        vseg[j] = *reinterpret_cast<const u32x4*>(token_row(v, c, tok) + v0 + part * EPS);
-      } else {
-        vseg[j] = u32x4{0u, 0u, 0u, 0u};
+      for (int i = 0; i < 4; ++i) {
+        const int tok = 16 * i + lq;
+        if (tok < nvc) {
+          vn[i] = *reinterpret_cast<const bf16x4*>(cb + (tok * rstride + 4 * g));
+        } else {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) vn[i][e] = (__bf16)0.f;
+        }
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < VSEG; ++j) {
+        const int sg = l + 64 * j, tok = sg / VSPT, part = sg - tok * VSPT;
+        if (tok < nvc) {
+          const TIn* cb = v + bh_base + (size_t)c * kChunk * rstride + v0;
+          vseg[j] = *reinterpret_cast<const u32x4*>(cb + (tok * rstride + part * EPS));
+        } else {
+          vseg[j] = u32x4{0u, 0u, 0u, 0u};
+        }
       }
     }
+    if (active != nullptr) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int tok = 16 * i + lq;
-      actn[i] = (tok < nvc && (active == nullptr || active[(size_t)b * T + (size_t)c * kChunk + tok] != 0)) ? 1 : 0;
+      for (int i = 0; i < 4; ++i) {
+        const int tok = min(16 * i + lq, nvc - 1);  // clamped: loaded unconditionally, masked later
+        actraw[i] = active[(size_t)b * T + (size_t)c * kChunk + tok];
+      }
     }
   };
   auto store_chunk = [&](int c) {
@@ -501,9 +524,41 @@ __global__ __launch_bounds__(64 * (ChainShape<E, DK>::NH + 1)) void delta_chain_
       for (int s = 0; s < N::NREG; ++s) {
         const int f = N::feat(s);
         *reinterpret_cast<NR*>(K + tok * PK + f) = kn[i][s];
+        if constexpr (!BF) {
 #pragma unroll
-        for (int e = 0; e < N::PER; ++e)
-          if (f + e < DK) Kt[(f + e) * PT + tok] = kn[i][s][e];
+          for (int e = 0; e < N::PER; ++e)
+            if (f + e < DK) Kt[(f + e) * PT + tok] = kn[i][s][e];
+        }
+      }
+    }
+    if constexpr (BF) {
+      // transposes through the MFMA unit: (rows x 32) . I selects 16 columns and returns them in
+      // the accumulator layout, where a lane holds four consecutive rows of one column - so each
+      // lane writes 8 contiguous bytes of the transposed tile. Exact: products with 1 and 0.
+      bf16x8 eye[2];
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) eye[hh][j] = (__bf16)((8 * g + j == 16 * hh + lq) ? 1.f : 0.f);
+      bf16x4 eye4;  // the 16x16x16 operand: lane group g holds k = 4g..4g+3
+#pragma unroll
+      for (int j = 0; j < 4; ++j) eye4[j] = (__bf16)((4 * g + j == lq) ? 1.f : 0.f);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+#pragma unroll
+        for (int ft = 0; ft < DK / 16; ++ft) {
+          const f32x4 tr = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kn[i][ft / 2], eye[ft % 2], zero4(), 0, 0, 0);
+          bf16x4 w4;
+#pragma unroll
+          for (int r = 0; r < 4; ++r) w4[r] = (__bf16)tr[r];
+          *reinterpret_cast<bf16x4*>(Kt + (16 * ft + lq) * PT + 16 * i + 4 * g) = w4;
+        }
+        const f32x4 tv = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(
+            __builtin_bit_cast(s16x4, vn[i]), __builtin_bit_cast(s16x4, eye4), zero4(), 0, 0, 0);
+        bf16x4 v4;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) v4[r] = (__bf16)tv[r];
+        *reinterpret_cast<bf16x4*>(sVt[bs] + lq * PT + 16 * i + 4 * g) = v4;
       }
     }
     E* Tm = sT[bs];
@@ -511,15 +566,19 @@ __global__ __launch_bounds__(64 * (ChainShape<E, DK>::NH + 1)) void delta_chain_
     for (int j = 0; j < TSEG; ++j) {
       const int el = (l + 64 * j) * EPS;
       const int t = el / kTileElems, within = el - t * kTileElems;
-      const int row = 16 * kTileRow[t] + within / 16, col = 16 * kTileCol[t] + within % 16;
+      // tile t -> (ti, tj) by arithmetic: a lane-varying index into a table would be a memory load
+      const int ti = (t >= 1) + (t >= 3) + (t >= 6), tj = t - ti * (ti + 1) / 2;
+      const int row = 16 * ti + within / 16, col = 16 * tj + within % 16;
       *reinterpret_cast<u32x4*>(Tm + row * PT + col) = tseg[j];
     }
-    E* Vt = sVt[bs];
+    if constexpr (!BF) {
+      E* Vt = sVt[bs];
 #pragma unroll
-    for (int j = 0; j < VSEG; ++j) {
-      const int sg = l + 64 * j, tok = sg / VSPT, part = sg - tok * VSPT;
+      for (int j = 0; j < VSEG; ++j) {
+        const int sg = l + 64 * j, tok = sg / VSPT, part = sg - tok * VSPT;
 #pragma unroll
-      for (int e = 0; e < EPS; ++e) Vt[(part * EPS + e) * PT + tok] = elem_of<E>(vseg[j], e);
+        for (int e = 0; e < EPS; ++e) Vt[(part * EPS + e) * PT + tok] = elem_of<E>(vseg[j], e);
+      }
     }
     // P^T tiles (key tile jj, query tile ii), keys after the query masked, packed per k-block;
     // each tile is formed right before its pack so at most two are live
@@ -536,27 +595,35 @@ __global__ __launch_bounds__(64 * (ChainShape<E, DK>::NH + 1)) void delta_chain_
     pt[3] = Acc<E>::pack(ptile(2, 2), zero4());
     pt[4] = Acc<E>::pack(ptile(0, 3), ptile(1, 3));
     pt[5] = Acc<E>::pack(ptile(2, 3), ptile(3, 3));
-    if constexpr (kKeepQ) {
+    if constexpr (kQInLds) {
+      E* Qs = sQ[c % 3];
 #pragma unroll
       for (int i = 0; i < 4; ++i)
 #pragma unroll
-        for (int s = 0; s < N::NREG; ++s) qk[i][s] = qn[i][s];
+        for (int s = 0; s < N::NREG; ++s) *reinterpret_cast<NR*>(Qs + (16 * i + lq) * PK + N::feat(s)) = qn[i][s];
     }
+    const int nvc = min(kChunk, T - c * kChunk);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) actk[i] = actn[i];
+    for (int i = 0; i < 4; ++i) actk[i] = (16 * i + lq < nvc && (active == nullptr || actraw[i] != 0)) ? 1 : 0;
   };
   auto write_output = [&](int c) {
     const int bs = c & 1;
     const int nvc = min(kChunk, T - c * kChunk);
-    NR qr[kKeepQ ? 1 : 4][N::NREG];
-    if constexpr (!kKeepQ) load_rows(qr, q, c);
+    NR ql[kQInLds ? 4 : 1][N::NREG];
+    if constexpr (kQInLds) {
+      const E* Qs = sQ[c % 3];
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int s = 0; s < N::NREG; ++s) ql[i][s] = *reinterpret_cast<const NR*>(Qs + (16 * i + lq) * PK + N::feat(s));
+    }
     const E* ho = sHo[bs] + lq * PK;
     const E* dd = sDo[bs] + lq * PT;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       f32x4 acc;
-      if constexpr (kKeepQ) {
-        acc = N::mma_lds(ho, qk[i], zero4());
+      if constexpr (kQInLds) {
+        acc = N::mma_lds(ho, ql[i], zero4());
       } else {
         acc = N::mma_lds(ho, qr[i], zero4());
       }
@@ -564,7 +631,7 @@ __global__ __launch_bounds__(64 * (ChainShape<E, DK>::NH + 1)) void delta_chain_
       if (i >= 2) acc = Acc<E>::mma(dd + 32, pt[i == 2 ? 3 : 5], acc);
       const int tok = 16 * i + lq;
       if (tok < nvc) {
-        TIn* dst = o + (((size_t)b * T + (size_t)c * kChunk + tok) * H + h) * DK + v0 + 4 * g;
+        TIn* dst = o + bh_base + (size_t)c * kChunk * rstride + v0 + (tok * rstride + 4 * g);
         const bool on = actk[i] != 0;
 #pragma unroll
         for (int r = 0; r < 4; ++r) dst[r] = from_f32<TIn>(on ? acc[r] : 0.f);
@@ -629,11 +696,12 @@ __global__ __launch_bounds__(64 * (ChainShape<E, DK>::NH + 1)) void delta_chain_
       if (it >= 0) chain_step(it);
     } else {
       const int cs = it + 1, co = it - 1;
-      if (cs < nc && cs % NH == hj) {
-        store_chunk(cs);
-        if (cs + NH < nc) issue_loads(cs + NH);
-      }
+      if (cs < nc && cs % NH == hj) store_chunk(cs);
       if (co >= 0 && co % NH == hj) write_output(co);
+      if (it >= 0 && it % NH == hj) {  // the idle iteration of chunk it's helper
+        if (it + NH < nc) issue_loads(it + NH);
+        if constexpr (!kQInLds) load_rows(qr, q, it);
+      }
     }
     __syncthreads();
   }
@@ -673,6 +741,7 @@ int launch_serial(const TIn* q, const TIn* k, const TIn* v, const TIn* beta, con
 
 size_t workspace_bytes(int B, int T, int H, int D, bool fp32) {
   if (B <= 0 || H <= 0 || T < kSerialBelow || !chunked_width(D, fp32)) return 0;
+  if ((size_t)T * H * D >= ((size_t)1 << 31)) return 0;  // 32-bit row offsets in the chain kernel
   const size_t nc = (size_t)(T + kChunk - 1) / kChunk;
   return (size_t)B * H * nc * kChunkT * (fp32 ? sizeof(float) : sizeof(uint16_t));
 }
