@@ -164,11 +164,13 @@ def time_decode(torch, reps: int = 5) -> dict:
     ak = torch.randn(n, b, 1, h, d, generator=g).to(dev, torch.bfloat16)
     av = torch.randn(n, b, 1, h, d, generator=g).to(dev, torch.bfloat16)
     pos = (w + torch.arange(n)).view(n, 1, 1).expand(n, b, 1).contiguous().to(dev)
+    counters = torch.zeros(b, dtype=torch.int32, device=dev)  # the ring write's arrival counters
 
     def run_all():
         for s in range(n):
             delta_scan_step_fused(dq[s], dk[s], dv[s], dbeta[s], state, out_state=state)
-            ring_attention(aq[s], ak[s], av[s], pos[s], ring, inplace=True, check_positions=False)
+            ring_attention(aq[s], ak[s], av[s], pos[s], ring, inplace=True, check_positions=False,
+                           workspace=counters)
 
     with torch.no_grad():
         side = torch.cuda.Stream()

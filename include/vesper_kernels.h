@@ -22,7 +22,7 @@
 extern "C" {
 #endif
 
-#define VSP_ABI_VERSION 1
+#define VSP_ABI_VERSION 2
 
 /* Status codes. */
 #define VSP_OK 0
@@ -85,17 +85,23 @@ int vsp_window_attn_f16(const void* q, const void* keys, const void* values, voi
  * ring_k, ring_v: [B, window, HKV, D]; ring_pos: [B, window] int64; ring_valid: [B, window] uint8.
  * The query at position p attends valid slots with a position in (p - window, p] and the new token
  * itself; o: [B, H, D]. With `write` nonzero the new token is then written into slot p % window
- * (keys, values, position, valid flag) in place, after every read of the call (a second launch).
+ * (keys, values, position, valid flag) in place, after every read of the call, by the same launch.
  * The contract of vesper/attention.py:298-338 (`attend_ring`, without the projections) and
  * vesper/attention.py:104-139 (`kv_ring_write`); the reference runs masked SDPA there.
- * D in {16, 32, 64, 128}; at most 8 query heads per KV head; active: [B] or NULL (an inactive row
- * reads zeros and still writes its token). */
+ * D in {16, 32, 64, 128}; at most 8 query heads per KV head; q, k, v and the ring's keys and
+ * values 16-byte aligned; active: [B] or NULL (an inactive row reads zeros and still writes its
+ * token). `workspace` (needed when `write` is nonzero) holds vsp_ring_attn_workspace_bytes(B)
+ * bytes of per-row arrival counters: zero before the first call, and every call leaves it zero.
+ * Calls that overlap in time must not share a workspace. */
+size_t vsp_ring_attn_workspace_bytes(int B);
 int vsp_ring_attn_bf16(const void* q, const void* k, const void* v, const int64_t* pos, void* ring_k, void* ring_v,
-                       int64_t* ring_pos, uint8_t* ring_valid, void* o, const uint8_t* active, int B, int H, int HKV,
-                       int D, int window, float scale, int write, void* stream);
+                       int64_t* ring_pos, uint8_t* ring_valid, void* o, const uint8_t* active, void* workspace,
+                       size_t workspace_bytes, int B, int H, int HKV, int D, int window, float scale, int write,
+                       void* stream);
 int vsp_ring_attn_f16(const void* q, const void* k, const void* v, const int64_t* pos, void* ring_k, void* ring_v,
-                      int64_t* ring_pos, uint8_t* ring_valid, void* o, const uint8_t* active, int B, int H, int HKV,
-                      int D, int window, float scale, int write, void* stream);
+                      int64_t* ring_pos, uint8_t* ring_valid, void* o, const uint8_t* active, void* workspace,
+                      size_t workspace_bytes, int B, int H, int HKV, int D, int window, float scale, int write,
+                      void* stream);
 
 #ifdef __cplusplus
 }

@@ -31,6 +31,8 @@ def test_the_workspace_size_covers_every_chunk():
     assert lib.vsp_delta_scan_workspace_bytes(2, 130, 3, 128, 1) == 0  # fp32 at 128 runs token by token
     assert lib.vsp_delta_scan_workspace_bytes(2, 130, 3, 48, 1) == 0  # token-serial width
     assert lib.vsp_delta_scan_workspace_bytes(2, 10, 3, 64, 0) == 0  # short sequences are serial
+    assert lib.vsp_ring_attn_workspace_bytes(64) == 64 * 4  # one arrival counter per row
+    assert lib.vsp_ring_attn_workspace_bytes(0) == 0
 
 
 def test_a_bad_size_is_an_error_status_not_a_crash():

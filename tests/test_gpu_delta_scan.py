@@ -181,7 +181,7 @@ def test_active_mask_zeroes_outputs_and_keeps_every_write():
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, BF16])
-@pytest.mark.parametrize("dk", [16, 64, 100])
+@pytest.mark.parametrize("dk", [16, 32, 64, 100, 128])
 def test_the_decode_step_matches_the_oracle_step(dtype, dk):
     from vesper.kernels.delta_scan import delta_scan_step_fused
 
@@ -204,6 +204,29 @@ def test_the_decode_step_matches_the_oracle_step(dtype, dk):
     act = torch.tensor([True, False, True, True, False], device=GPU)
     o3, s3 = delta_scan_step_fused(*dev, active=act)
     assert torch.equal(s3, s) and bool((o3[~act] == 0).all()) and torch.equal(o3[act], o[act])
+
+
+def test_decode_config_256_steps_b64_h8_d64_equal_the_chunked_scan():
+    # the decode workload: 256 in-place fp32 steps on S [64, 8, 64, 64] ~ N(0, 0.02^2) give the
+    # outputs and final state of one chunked scan over the same 256 tokens (tests/test_decode.py:45-71)
+    from vesper.kernels.delta_scan import delta_scan_step_fused
+
+    b, n, h, dk = 64, 256, 8, 64
+    g = torch.Generator().manual_seed(4)
+    q = normalize_keys(torch.randn(b, n, h, dk, generator=g))
+    k = normalize_keys(torch.randn(b, n, h, dk, generator=g))
+    v = torch.randn(b, n, h, dk, generator=g)
+    beta = torch.sigmoid(torch.randn(b, n, h, generator=g))
+    s0 = 0.02 * torch.randn(b, h, dk, dk, generator=g)
+    o_ref, s_ref = delta_scan_chunked(*(t.double() for t in (q, k, v, beta, s0)), 64)
+    dq, dk_, dv, db = (t.to(GPU) for t in (q, k, v, beta))
+    state = s0.to(GPU)
+    outs = []
+    for t in range(n):
+        o, _ = delta_scan_step_fused(dq[:, t], dk_[:, t], dv[:, t], db[:, t], state, out_state=state)
+        outs.append(o)
+    o = torch.stack(outs, dim=1)
+    assert relative_error(o, o_ref) < 1e-5 and relative_error(state, s_ref) < 1e-5
 
 
 def test_bitwise_repeatable_and_exactly_linear_under_power_of_two_scaling():

@@ -93,6 +93,51 @@ def test_decoding_steps_equal_the_whole_chunk_window():
     assert sorted(ring.pos[0].cpu()[held].tolist()) == list(range(start + steps - w, start + steps))
 
 
+def test_captured_decoding_with_one_workspace_equals_eager_on_every_replay():
+    # eight decoding steps captured in one graph, all sharing one counter workspace: every replay
+    # from the same starting ring gives the eager outputs and ring bitwise, and leaves the counters zero
+    from vesper.kernels.ring_attn import RingKVCache, ring_attention
+
+    b, h, hkv, dk, w, steps = 6, 8, 8, 64, 32, 8
+    rk, rv, rpos, valid, _ = _random_ring(b, w, hkv, dk, seed=11)
+    g = torch.Generator().manual_seed(12)
+    q = torch.randn(steps, b, 1, h, dk, generator=g).to(BF16).to(GPU)
+    k = torch.randn(steps, b, 1, hkv, dk, generator=g).to(BF16).to(GPU)
+    v = torch.randn(steps, b, 1, hkv, dk, generator=g).to(BF16).to(GPU)
+    p0 = torch.randint(2 * w, 3 * w, (b, 1), generator=g)
+    pos = torch.stack([p0 + i for i in range(steps)]).to(GPU)
+    start = [t.to(GPU) for t in (rk, rv, rpos, valid)]
+    counters = torch.zeros(b, dtype=torch.int32, device=GPU)
+
+    def run(ring):
+        return [ring_attention(q[i], k[i], v[i], pos[i], ring, inplace=True, check_positions=False,
+                               workspace=counters)[0] for i in range(steps)]
+
+    eager_ring = RingKVCache(*(t.clone() for t in start), w)
+    eager = run(eager_ring)
+    ring = RingKVCache(*(t.clone() for t in start), w)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        run(RingKVCache(*(t.clone() for t in start), w))
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        got = run(ring)
+    for rep in range(3):
+        for dst, src in zip((ring.k, ring.v, ring.pos, ring.valid), start):
+            dst.copy_(src)
+        graph.replay()
+        torch.cuda.synchronize()
+        for i in range(steps):
+            assert torch.equal(got[i], eager[i]), (rep, i)
+        for a, e in zip((ring.k, ring.v, ring.pos, ring.valid), (eager_ring.k, eager_ring.v, eager_ring.pos, eager_ring.valid)):
+            assert torch.equal(a, e), rep
+        assert int(counters.abs().sum()) == 0, rep
+        run(RingKVCache(*(t.clone() for t in start), w))  # eager work between replays
+        torch.cuda.synchronize()
+
+
 def test_decode_config_b64_h8_d64_ring512_one_step():
     from vesper.kernels.ring_attn import RingKVCache, ring_attention
 

@@ -27,6 +27,14 @@ int check_launch(const char* what);
 
 enum Status { OK = 0, ERR_ARG = 1, ERR_UNSUPPORTED = 2, ERR_LAUNCH = 3 };
 
+// ---- launchers shared between translation units ------------------------------------------------
+// The register-resident single-token delta step (delta_step.hip) for head widths 16, 32, 64 and
+// 128; false when the width or the state's alignment needs the general token-serial kernel.
+bool delta_step_fast_f32(const float* q, const float* k, const float* v, const float* beta, const float* s_in,
+                         float* s_out, float* o, const uint8_t* active, int B, int H, int D, hipStream_t stream);
+bool delta_step_fast_bf16(const __bf16* q, const __bf16* k, const __bf16* v, const __bf16* beta, const float* s_in,
+                          float* s_out, __bf16* o, const uint8_t* active, int B, int H, int D, hipStream_t stream);
+
 // ---- element conversions ----------------------------------------------------------------------
 __device__ __forceinline__ float to_f32(float x) { return x; }
 __device__ __forceinline__ float to_f32(__bf16 x) { return (float)x; }
@@ -115,6 +123,24 @@ __device__ __forceinline__ void store_tile_t(E* base, int ld, f32x4 acc) {
   const int c = l & 15, r0 = 4 * (l >> 4);
 #pragma unroll
   for (int r = 0; r < 4; ++r) base[c * ld + r0 + r] = from_f32<E>(acc[r]);
+}
+
+// ---- lane reductions through DPP (a VALU modifier: no LDS traffic, unlike ds_bpermute) --------
+template <int CTRL>
+__device__ __forceinline__ float dpp_f32(float x) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), CTRL, 0xF, 0xF, true));
+}
+// Sum over aligned groups of N consecutive lanes (N = 1, 2, 4, 8 or 16); every lane of a group
+// gets the group's sum. quad_perm [1,0,3,2] and [2,3,0,1] pair lanes within a quad,
+// row_half_mirror swaps the two quads of 8 lanes, row_mirror the two halves of 16.
+template <int N>
+__device__ __forceinline__ float group_sum(float x) {
+  static_assert(N == 1 || N == 2 || N == 4 || N == 8 || N == 16, "group of 1..16 lanes");
+  if constexpr (N >= 2) x += dpp_f32<0xB1>(x);
+  if constexpr (N >= 4) x += dpp_f32<0x4E>(x);
+  if constexpr (N >= 8) x += dpp_f32<0x141>(x);
+  if constexpr (N >= 16) x += dpp_f32<0x140>(x);
+  return x;
 }
 
 // ---- XCD-aware block order --------------------------------------------------------------------

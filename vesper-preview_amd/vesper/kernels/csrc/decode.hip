@@ -2,17 +2,26 @@
 //
 // Semantics (reference vesper/attention.py:62-139, :298-338): a token at position p lives in slot
 // p % W; slots are not in age order. The query at position p attends the ring slots that are valid
-// and hold a position in (p - W, p], plus the new token itself, which is attended exactly once from
-// its own argument; only then is the new token written into its slot. Query head h reads KV head
-// h / (H / HKV); scale 1/sqrt(D).
+// and hold a position in (p - W, p], plus the new token itself, which is attended exactly once
+// from its own argument; only then is the new token written into its slot (keys, values, position,
+// valid flag). Query head h reads KV head h / (H / HKV); scale 1/sqrt(D) (passed in).
 //
-// ring_attn_kernel (reads only): one workgroup per (b, KV head) serves the G = H / HKV query heads
-// of that group, so each ring row is read from HBM once. D/8 lanes share a key row (16-byte loads);
-// scores go to LDS, the softmax runs per head over W + 1 scores, and the weighted sum of V rows is
-// reduced across lanes, then across waves.
-// ring_write_kernel: writes the new keys, values, position and valid flag after every read of the
-// step has finished (a separate launch on the same stream, so no workgroup can observe a slot half
-// updated by another).
+// ring_attn_kernel: one workgroup per (b, KV head) serves the G = H / HKV query heads of that
+// group, so each ring row is read from HBM once per step. D/8 lanes share a key row (16-byte
+// pieces); a thread takes KPT keys of a batch and issues all of their K and V loads before any
+// arithmetic, so the whole window of the head is in flight at once (W = 512 at D = 64 is one
+// batch). Each thread keeps, per query head, an online softmax over its own keys (running max,
+// sum and weighted values, base-2 exponent); the partial states merge across the key groups of a
+// wave with lane shuffles and across the four waves through LDS, in a fixed order.
+//
+// The write: a workgroup writes its own KV head's key and value into slot p % W after all of its
+// reads (no other workgroup reads that head). The slot's position and valid flag are shared by the
+// HKV workgroups of row b, so the last of them to finish reading the row's positions and flags (a
+// per-row arrival counter in the caller's workspace) writes them and resets the counter to zero:
+// every workgroup of the row has read the old position and flag by then, whatever order the
+// workgroups ran in.
+#include <type_traits>
+
 #include "common.h"
 #include "vesper_kernels.h"
 
@@ -21,226 +30,300 @@ namespace {
 
 constexpr int kMaxGroup = 8;
 
-template <typename T, int D>
+// Dot product of eight 16-bit pairs accumulated in fp32 (v_dot2 on bf16 or f16 pairs).
+template <typename T> struct Dot2;
+template <> struct Dot2<__bf16> {
+  typedef __bf16 P2 __attribute__((ext_vector_type(2)));
+  __device__ __forceinline__ static float run(P2 a, P2 b, float c) { return __builtin_amdgcn_fdot2_f32_bf16(a, b, c, false); }
+};
+template <> struct Dot2<_Float16> {
+  typedef _Float16 P2 __attribute__((ext_vector_type(2)));
+  __device__ __forceinline__ static float run(P2 a, P2 b, float c) { return __builtin_amdgcn_fdot2(a, b, c, false); }
+};
+
+// GM: the query heads per KV head rounded up to a power of two (register arrays are sized by it);
+// wide groups take fewer keys per thread so the per-head softmax states still fit in registers.
+template <typename T, int D, int GM>
 __global__ __launch_bounds__(256) void ring_attn_kernel(const T* __restrict__ q, const T* __restrict__ knew,
                                                         const T* __restrict__ vnew, const int64_t* __restrict__ pos,
-                                                        const T* __restrict__ ring_k, const T* __restrict__ ring_v,
-                                                        const int64_t* __restrict__ ring_pos,
-                                                        const uint8_t* __restrict__ ring_valid, T* __restrict__ o,
-                                                        const uint8_t* __restrict__ active, int H, int HKV, int W,
-                                                        float scale_log2) {
-  constexpr int KL = D / 8;          // lanes per key row
-  constexpr int KPP = 256 / KL;      // keys per pass of the workgroup
-  extern __shared__ float ss[];      // [G][W + 1] scores, then probabilities
-  __shared__ float sq[kMaxGroup][D];
-  __shared__ float sred[4][kMaxGroup];
-  __shared__ float sstat[2][kMaxGroup];
-  __shared__ float sacc[4][kMaxGroup][D];
+                                                        T* ring_k, T* ring_v, int64_t* ring_pos, uint8_t* ring_valid,
+                                                        T* __restrict__ o, const uint8_t* __restrict__ active,
+                                                        uint32_t* __restrict__ counters, int H, int HKV, int W,
+                                                        float scale_log2, int write) {
+  constexpr int KL = D / 8;                // lanes per key row
+  constexpr int KPP = 256 / KL;            // keys per pass of the workgroup
+  constexpr int KPT = GM >= 4 ? 8 : 16;    // keys per thread per batch
+  constexpr int BATCH = KPP * KPT;
+  constexpr int VPT = (BATCH + 255) / 256;  // visibility flags computed per thread per batch
+  constexpr bool kQReg = GM <= 2;          // query pieces in registers (else read from LDS per key)
+  typedef T V8 __attribute__((ext_vector_type(8)));
+  using P2 = typename Dot2<T>::P2;
+  __shared__ __align__(16) T sq[GM][D];
+  __shared__ uint8_t svis[BATCH];
+  __shared__ float smerge[4][GM][2 + D];
 
   const int b = blockIdx.x / HKV, kvh = blockIdx.x - b * HKV;
   const int G = H / HKV;
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int part = tid % KL, kg = tid / KL;
   const int64_t p = pos[b];
-  T* out = o + ((size_t)b * H + (size_t)kvh * G) * D;
-
-  if (active != nullptr && active[b] == 0) {
-    for (int i = tid; i < G * D; i += 256) out[i] = from_f32<T>(0.f);
-    return;
-  }
-  for (int i = tid; i < G * D; i += 256) sq[i / D][i % D] = to_f32(q[((size_t)b * H + (size_t)kvh * G) * D + i]);
-  __syncthreads();
-
-  // scores of the ring slots
   const size_t row_stride = (size_t)HKV * D;
-  const T* kb = ring_k + ((size_t)b * W * HKV + kvh) * D + 8 * part;
-  for (int j = kg; j < W; j += KPP) {
-    const int64_t rp = ring_pos[(size_t)b * W + j];
-    const bool vis = ring_valid[(size_t)b * W + j] != 0 && rp <= p && rp > p - W;
-    float kv8[8];
-    load8_f32(kb + (size_t)j * row_stride, kv8);
-    for (int gi = 0; gi < G; ++gi) {
-      float acc = 0.f;
+  const size_t head_off = ((size_t)b * W * HKV + kvh) * D + 8 * part;
+  T* out = o + ((size_t)b * H + (size_t)kvh * G) * D;
+  // An inactive row is computed like an active one and stores zeros, so no wait on its flag delays
+  // the row's loads; its token is still written.
+  {
+    float m[GM], l[GM], acc[GM][8];
 #pragma unroll
-      for (int e = 0; e < 8; ++e) acc += kv8[e] * sq[gi][8 * part + e];
+    for (int gi = 0; gi < GM; ++gi) {
+      m[gi] = -1e30f;  // finite: a thread that sees no key keeps l = 0 and merges as nothing
+      l[gi] = 0.f;
 #pragma unroll
-      for (int off = 1; off < KL; off <<= 1) acc += __shfl_xor(acc, off);
-      if (part == 0) ss[gi * (W + 1) + j] = vis ? acc * scale_log2 : -INFINITY;
+      for (int e = 0; e < 8; ++e) acc[gi][e] = 0.f;
     }
-  }
-  // the new token's own score
-  if (kg == 0) {
-    float kv8[8];
-    load8_f32(knew + ((size_t)b * HKV + kvh) * D + 8 * part, kv8);
-    for (int gi = 0; gi < G; ++gi) {
-      float acc = 0.f;
+    V8 qr[kQReg ? GM : 1];
+    // one batch of n <= KPT keys of this thread (scores sc, values vr) folded into the running state
+    auto fold = [&](float (&sc)[GM][KPT], const V8* vr, int n) {
 #pragma unroll
-      for (int e = 0; e < 8; ++e) acc += kv8[e] * sq[gi][8 * part + e];
+      for (int gi = 0; gi < GM; ++gi) {
+        float mb = sc[gi][0];
 #pragma unroll
-      for (int off = 1; off < KL; off <<= 1) acc += __shfl_xor(acc, off);
-      if (part == 0) ss[gi * (W + 1) + W] = acc * scale_log2;
-    }
-  }
-  __syncthreads();
+        for (int i = 1; i < KPT; ++i)
+          if (i < n) mb = fmaxf(mb, sc[gi][i]);
+        const float mn = fmaxf(m[gi], mb);
+        const float a = __builtin_amdgcn_exp2f(m[gi] - mn);
+        l[gi] *= a;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc[gi][e] *= a;
+#pragma unroll
+        for (int i = 0; i < KPT; ++i) {
+          if (i < n) {
+            const float pj = __builtin_amdgcn_exp2f(sc[gi][i] - mn);
+            l[gi] += pj;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) acc[gi][e] += pj * to_f32(vr[i][e]);
+          }
+        }
+        m[gi] = mn;
+      }
+    };
+    auto dot = [&](int gi, const V8& kv) {
+      V8 qv;
+      if constexpr (kQReg) {
+        qv = qr[kQReg ? gi : 0];
+      } else {
+        qv = *reinterpret_cast<const V8*>(&sq[gi][8 * part]);
+      }
+      float s = 0.f;
+#pragma unroll
+      for (int e = 0; e < 8; e += 2) s = Dot2<T>::run(P2{kv[e], kv[e + 1]}, P2{qv[e], qv[e + 1]}, s);
+      return group_sum<KL>(s) * scale_log2;
+    };
 
-  // softmax per head over W + 1 scores (the new token is always visible, so the max is finite)
-  for (int gi = 0; gi < G; ++gi) {
-    float* row = ss + gi * (W + 1);
-    float m = -INFINITY;
-    for (int j = tid; j <= W; j += 256) m = fmaxf(m, row[j]);
+    const T* kb = ring_k + head_off;
+    const T* vb = ring_v + head_off;
+    for (int j0 = 0; j0 < W; j0 += BATCH) {
+      // positions and flags first, then every key and value load of the batch: waiting for the
+      // first does not wait for the rest (the load counter retires in order)
+      int64_t rp[VPT];
+      uint8_t rv[VPT];
 #pragma unroll
-    for (int off = 1; off < 64; off <<= 1) m = fmaxf(m, __shfl_xor(m, off));
-    if (lane == 0) sred[wv][gi] = m;
-  }
-  __syncthreads();
-  if (tid < G) sstat[0][tid] = fmaxf(fmaxf(sred[0][tid], sred[1][tid]), fmaxf(sred[2][tid], sred[3][tid]));
-  __syncthreads();
-  for (int gi = 0; gi < G; ++gi) {
-    float* row = ss + gi * (W + 1);
-    const float m = sstat[0][gi];
-    float s = 0.f;
-    for (int j = tid; j <= W; j += 256) {
-      const float e = exp2f(row[j] - m);
-      row[j] = e;
-      s += e;
+      for (int u = 0; u < VPT; ++u) {
+        const int j = min(j0 + tid + 256 * u, W - 1);
+        rp[u] = ring_pos[(size_t)b * W + j];
+        rv[u] = ring_valid[(size_t)b * W + j];
+      }
+      V8 kr[KPT], vr[KPT];
+#pragma unroll
+      for (int i = 0; i < KPT; ++i) {
+        const int j = min(j0 + kg + i * KPP, W - 1);  // keys past W re-read row W - 1, masked below
+        kr[i] = *reinterpret_cast<const V8*>(kb + (size_t)j * row_stride);
+        vr[i] = *reinterpret_cast<const V8*>(vb + (size_t)j * row_stride);
+      }
+      if (j0 == 0) {  // the group's query heads (heads past G are zero: their results are never stored)
+        const T* qb = q + ((size_t)b * H + (size_t)kvh * G) * D;
+        if constexpr (kQReg) {
+#pragma unroll
+          for (int gi = 0; gi < GM; ++gi) {
+            if (gi < G) {
+              qr[gi] = *reinterpret_cast<const V8*>(qb + gi * D + 8 * part);
+            } else {
+#pragma unroll
+              for (int e = 0; e < 8; ++e) qr[gi][e] = from_f32<T>(0.f);
+            }
+          }
+        } else {
+          for (int i = tid; i < GM * D; i += 256) sq[i / D][i % D] = i / D < G ? qb[i] : from_f32<T>(0.f);
+        }
+      }
+      __syncthreads();  // the previous batch's flags are read (and sq is written)
+#pragma unroll
+      for (int u = 0; u < VPT; ++u) {
+        const int jj = tid + 256 * u;
+        if (jj < BATCH) svis[jj] = (j0 + jj < W && rv[u] != 0 && rp[u] <= p && rp[u] > p - W) ? 1 : 0;
+      }
+      __syncthreads();
+      if (write && p >= 0 && tid == 0 && j0 + BATCH >= W) {
+        // This workgroup has read every position and flag of the row it will read (the last batch's
+        // are in LDS now), so it reports in; the row's last workgroup to report writes the slot's
+        // position and flag. No fence is needed on either side: the loads reporting here have
+        // returned (their values were consumed before the barrier), so a store issued after this
+        // increment is observed cannot reach them, and what is written here is read by later
+        // launches only. The counter is a relaxed device-scope atomic, coherent across the XCDs'
+        // L2s (an agent-scope fence would write back the whole L2, dearer than the attention).
+        // Reporting here rather than at the end hides the atomic's round trip behind the K/V loads.
+        const uint32_t arrived = __hip_atomic_fetch_add(&counters[b], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (arrived == (uint32_t)(HKV - 1)) {
+          const int slot = (int)(p % W);
+          ring_pos[(size_t)b * W + slot] = p;
+          ring_valid[(size_t)b * W + slot] = 1;
+          __hip_atomic_store(&counters[b], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+      }
+      float sc[GM][KPT];
+#pragma unroll
+      for (int i = 0; i < KPT; ++i) {
+        const bool vis = svis[kg + i * KPP] != 0;
+#pragma unroll
+        for (int gi = 0; gi < GM; ++gi) {
+          const float sv = dot(gi, kr[i]);
+          sc[gi][i] = vis ? sv : -INFINITY;
+        }
+      }
+      fold(sc, vr, KPT);
     }
+    if (kg == 0) {  // the new token, always visible
+      const V8 kn = *reinterpret_cast<const V8*>(knew + ((size_t)b * HKV + kvh) * D + 8 * part);
+      V8 vn[KPT];
+      vn[0] = *reinterpret_cast<const V8*>(vnew + ((size_t)b * HKV + kvh) * D + 8 * part);
+      float sc[GM][KPT];
 #pragma unroll
-    for (int off = 1; off < 64; off <<= 1) s += __shfl_xor(s, off);
-    if (lane == 0) sred[wv][gi] = s;
-  }
-  __syncthreads();
-  if (tid < G) sstat[1][tid] = (sred[0][tid] + sred[1][tid]) + (sred[2][tid] + sred[3][tid]);
-  __syncthreads();
+      for (int gi = 0; gi < GM; ++gi) sc[gi][0] = dot(gi, kn);
+      fold(sc, vn, 1);
+    }
 
-  // weighted values
-  float acc[kMaxGroup][8];
+    // merge the partial softmax states: key groups of a wave, then the four waves
 #pragma unroll
-  for (int gi = 0; gi < kMaxGroup; ++gi)
+    for (int gi = 0; gi < GM; ++gi) {
 #pragma unroll
-    for (int e = 0; e < 8; ++e) acc[gi][e] = 0.f;
-  const T* vb = ring_v + ((size_t)b * W * HKV + kvh) * D + 8 * part;
-  for (int j = kg; j < W; j += KPP) {
-    float vv[8];
-    load8_f32(vb + (size_t)j * row_stride, vv);
+      for (int off = KL; off < 64; off <<= 1) {
+        const float mo = __shfl_xor(m[gi], off);
+        const float lo = __shfl_xor(l[gi], off);
+        const float mn = fmaxf(m[gi], mo);
+        const float a = __builtin_amdgcn_exp2f(m[gi] - mn), c = __builtin_amdgcn_exp2f(mo - mn);
+        l[gi] = l[gi] * a + lo * c;
 #pragma unroll
-    for (int gi = 0; gi < kMaxGroup; ++gi) {
-      if (gi < G) {
-        const float pj = ss[gi * (W + 1) + j];
+        for (int e = 0; e < 8; ++e) acc[gi][e] = acc[gi][e] * a + __shfl_xor(acc[gi][e], off) * c;
+        m[gi] = mn;
+      }
+      if (lane < KL) {
+        if (part == 0) {
+          smerge[wv][gi][0] = m[gi];
+          smerge[wv][gi][1] = l[gi];
+        }
 #pragma unroll
-        for (int e = 0; e < 8; ++e) acc[gi][e] += pj * vv[e];
+        for (int e = 0; e < 8; ++e) smerge[wv][gi][2 + 8 * part + e] = acc[gi][e];
       }
     }
-  }
-  if (kg == 0) {
-    float vv[8];
-    load8_f32(vnew + ((size_t)b * HKV + kvh) * D + 8 * part, vv);
+    __syncthreads();
+    const bool on = active == nullptr || active[b] != 0;
+    for (int i = tid; i < G * D; i += 256) {
+      const int gi = i / D, d = i - gi * D;
+      float mx = smerge[0][gi][0];
 #pragma unroll
-    for (int gi = 0; gi < kMaxGroup; ++gi) {
-      if (gi < G) {
-        const float pj = ss[gi * (W + 1) + W];
+      for (int w = 1; w < 4; ++w) mx = fmaxf(mx, smerge[w][gi][0]);
+      float lsum = 0.f, num = 0.f;
 #pragma unroll
-        for (int e = 0; e < 8; ++e) acc[gi][e] += pj * vv[e];
+      for (int w = 0; w < 4; ++w) {
+        const float a = __builtin_amdgcn_exp2f(smerge[w][gi][0] - mx);
+        lsum += smerge[w][gi][1] * a;
+        num += smerge[w][gi][2 + d] * a;
       }
+      out[i] = from_f32<T>(on ? num / lsum : 0.f);
     }
   }
-  // reduce over the key groups of a wave, then over the four waves
-#pragma unroll
-  for (int gi = 0; gi < kMaxGroup; ++gi) {
-    if (gi < G) {
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        float x = acc[gi][e];
-#pragma unroll
-        for (int off = KL; off < 64; off <<= 1) x += __shfl_xor(x, off);
-        acc[gi][e] = x;
-      }
-    }
-  }
-  if (lane < KL) {
-#pragma unroll
-    for (int gi = 0; gi < kMaxGroup; ++gi)
-      if (gi < G)
-#pragma unroll
-        for (int e = 0; e < 8; ++e) sacc[wv][gi][8 * lane + e] = acc[gi][e];
-  }
-  __syncthreads();
-  for (int i = tid; i < G * D; i += 256) {
-    const int gi = i / D, d = i - gi * D;
-    const float sum = (sacc[0][gi][d] + sacc[1][gi][d]) + (sacc[2][gi][d] + sacc[3][gi][d]);
-    out[i] = from_f32<T>(sum / sstat[1][gi]);
-  }
-}
 
-template <typename T>
-__global__ __launch_bounds__(256) void ring_write_kernel(const T* __restrict__ knew, const T* __restrict__ vnew,
-                                                         const int64_t* __restrict__ pos, T* __restrict__ ring_k,
-                                                         T* __restrict__ ring_v, int64_t* __restrict__ ring_pos,
-                                                         uint8_t* __restrict__ ring_valid, int HKV, int D, int W) {
-  const int b = blockIdx.x;
-  const int64_t p = pos[b];
-  if (p < 0) return;  // refused by the host wrapper; never index with a negative slot
+  if (!write || p < 0) return;  // a negative position is refused by the host wrapper
+  __syncthreads();              // every read of this workgroup is done
   const int slot = (int)(p % W);
-  const size_t dst = ((size_t)b * W + slot) * HKV * D;
-  const size_t src = (size_t)b * HKV * D;
-  for (int i = threadIdx.x; i < HKV * D; i += blockDim.x) {
-    ring_k[dst + i] = knew[src + i];
-    ring_v[dst + i] = vnew[src + i];
-  }
-  if (threadIdx.x == 0) {
-    ring_pos[(size_t)b * W + slot] = p;
-    ring_valid[(size_t)b * W + slot] = 1;
+  const size_t dst = ((size_t)b * W + slot) * row_stride + (size_t)kvh * D;
+  const size_t src = ((size_t)b * HKV + kvh) * D;
+  if (tid < KL) {
+    *reinterpret_cast<V8*>(ring_k + dst + 8 * tid) = *reinterpret_cast<const V8*>(knew + src + 8 * tid);
+  } else if (tid < 2 * KL) {
+    const int pp = tid - KL;
+    *reinterpret_cast<V8*>(ring_v + dst + 8 * pp) = *reinterpret_cast<const V8*>(vnew + src + 8 * pp);
   }
 }
 
 bool ring_width(int D) { return D == 16 || D == 32 || D == 64 || D == 128; }
 
+bool aligned16(const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15) == 0; }
+
 template <typename T>
 int ring_attn(const T* q, const T* knew, const T* vnew, const int64_t* pos, T* ring_k, T* ring_v, int64_t* ring_pos,
-              uint8_t* ring_valid, T* o, const uint8_t* active, int B, int H, int HKV, int D, int W, float scale,
-              int write, void* stream_ptr, const char* who) {
+              uint8_t* ring_valid, T* o, const uint8_t* active, void* workspace, size_t ws_bytes, int B, int H, int HKV,
+              int D, int W, float scale, int write, void* stream_ptr, const char* who) {
   if (B < 0 || H < 1 || HKV < 1 || W < 1) return fail(ERR_ARG, "%s: bad sizes B=%d H=%d HKV=%d W=%d", who, B, H, HKV, W);
   if (H % HKV != 0) return fail(ERR_ARG, "%s: %d query heads are not a multiple of %d KV heads", who, H, HKV);
   if (H / HKV > kMaxGroup) return fail(ERR_UNSUPPORTED, "%s: %d query heads per KV head (at most %d)", who, H / HKV, kMaxGroup);
   if (!ring_width(D)) return fail(ERR_UNSUPPORTED, "%s: head dimension %d (kernels: 16, 32, 64, 128)", who, D);
-  const size_t smem = (size_t)(H / HKV) * (W + 1) * sizeof(float);
-  if (smem > 96 * 1024) return fail(ERR_UNSUPPORTED, "%s: window %d with %d heads per group needs %zu bytes of LDS", who, W, H / HKV, smem);
   if (B == 0) return OK;
   if (!q || !knew || !vnew || !pos || !ring_k || !ring_v || !ring_pos || !ring_valid || !o)
     return fail(ERR_ARG, "%s: null pointer", who);
+  if (!aligned16(q) || !aligned16(knew) || !aligned16(vnew) || !aligned16(ring_k) || !aligned16(ring_v))
+    return fail(ERR_ARG, "%s: q, k, v and the ring's keys and values must be 16-byte aligned", who);
+  if (write && (workspace == nullptr || ws_bytes < (size_t)B * sizeof(uint32_t)))
+    return fail(ERR_ARG, "%s: workspace of %zu bytes given, %zu needed", who, workspace ? ws_bytes : (size_t)0,
+                (size_t)B * sizeof(uint32_t));
   hipStream_t stream = reinterpret_cast<hipStream_t>(stream_ptr);
   const float scale_log2 = scale * 1.4426950408889634f;
+  uint32_t* counters = static_cast<uint32_t*>(workspace);
   dim3 grid((unsigned)(B * HKV));
+  const int G = H / HKV;
+  auto go = [&](auto kern) {
+    hipLaunchKernelGGL(kern, grid, dim3(256), 0, stream, q, knew, vnew, pos, ring_k, ring_v, ring_pos, ring_valid, o,
+                       active, counters, H, HKV, W, scale_log2, write);
+  };
+  auto by_group = [&](auto dtag) {
+    constexpr int Dc = decltype(dtag)::value;
+    if (G == 1) go(ring_attn_kernel<T, Dc, 1>);
+    else if (G == 2) go(ring_attn_kernel<T, Dc, 2>);
+    else if (G <= 4) go(ring_attn_kernel<T, Dc, 4>);
+    else go(ring_attn_kernel<T, Dc, 8>);
+  };
   switch (D) {
-    case 16: hipLaunchKernelGGL((ring_attn_kernel<T, 16>), grid, dim3(256), smem, stream, q, knew, vnew, pos, ring_k, ring_v, ring_pos, ring_valid, o, active, H, HKV, W, scale_log2); break;
-    case 32: hipLaunchKernelGGL((ring_attn_kernel<T, 32>), grid, dim3(256), smem, stream, q, knew, vnew, pos, ring_k, ring_v, ring_pos, ring_valid, o, active, H, HKV, W, scale_log2); break;
-    case 64: hipLaunchKernelGGL((ring_attn_kernel<T, 64>), grid, dim3(256), smem, stream, q, knew, vnew, pos, ring_k, ring_v, ring_pos, ring_valid, o, active, H, HKV, W, scale_log2); break;
-    default: hipLaunchKernelGGL((ring_attn_kernel<T, 128>), grid, dim3(256), smem, stream, q, knew, vnew, pos, ring_k, ring_v, ring_pos, ring_valid, o, active, H, HKV, W, scale_log2); break;
+    case 16: by_group(std::integral_constant<int, 16>{}); break;
+    case 32: by_group(std::integral_constant<int, 32>{}); break;
+    case 64: by_group(std::integral_constant<int, 64>{}); break;
+    default: by_group(std::integral_constant<int, 128>{}); break;
   }
-  int st = check_launch(who);
-  if (st != OK || !write) return st;
-  hipLaunchKernelGGL((ring_write_kernel<T>), dim3((unsigned)B), dim3(256), 0, stream, knew, vnew, pos, ring_k, ring_v,
-                     ring_pos, ring_valid, HKV, D, W);
   return check_launch(who);
 }
 
 }  // namespace
 }  // namespace vsp
 
+extern "C" size_t vsp_ring_attn_workspace_bytes(int B) { return B > 0 ? (size_t)B * sizeof(uint32_t) : 0; }
+
 extern "C" int vsp_ring_attn_bf16(const void* q, const void* k, const void* v, const int64_t* pos, void* ring_k,
                                   void* ring_v, int64_t* ring_pos, uint8_t* ring_valid, void* o,
-                                  const uint8_t* active, int B, int H, int HKV, int D, int window, float scale,
-                                  int write, void* stream) {
+                                  const uint8_t* active, void* workspace, size_t workspace_bytes, int B, int H, int HKV,
+                                  int D, int window, float scale, int write, void* stream) {
   return vsp::ring_attn<__bf16>(static_cast<const __bf16*>(q), static_cast<const __bf16*>(k),
                                 static_cast<const __bf16*>(v), pos, static_cast<__bf16*>(ring_k),
-                                static_cast<__bf16*>(ring_v), ring_pos, ring_valid, static_cast<__bf16*>(o), active, B,
-                                H, HKV, D, window, scale, write, stream, "vsp_ring_attn_bf16");
+                                static_cast<__bf16*>(ring_v), ring_pos, ring_valid, static_cast<__bf16*>(o), active,
+                                workspace, workspace_bytes, B, H, HKV, D, window, scale, write, stream,
+                                "vsp_ring_attn_bf16");
 }
 
 extern "C" int vsp_ring_attn_f16(const void* q, const void* k, const void* v, const int64_t* pos, void* ring_k,
                                  void* ring_v, int64_t* ring_pos, uint8_t* ring_valid, void* o, const uint8_t* active,
-                                 int B, int H, int HKV, int D, int window, float scale, int write, void* stream) {
+                                 void* workspace, size_t workspace_bytes, int B, int H, int HKV, int D, int window,
+                                 float scale, int write, void* stream) {
   return vsp::ring_attn<_Float16>(static_cast<const _Float16*>(q), static_cast<const _Float16*>(k),
                                   static_cast<const _Float16*>(v), pos, static_cast<_Float16*>(ring_k),
                                   static_cast<_Float16*>(ring_v), ring_pos, ring_valid, static_cast<_Float16*>(o),
-                                  active, B, H, HKV, D, window, scale, write, stream, "vsp_ring_attn_f16");
+                                  active, workspace, workspace_bytes, B, H, HKV, D, window, scale, write, stream,
+                                  "vsp_ring_attn_f16");
 }

@@ -792,8 +792,15 @@ int delta_step(const TIn* q, const TIn* k, const TIn* v, const TIn* beta, const 
                const uint8_t* active, int B, int H, int D, void* stream_ptr, const char* who) {
   int st = check_common(q, k, v, beta, s_in, s_out, o, B, 1, H, D, who);
   if (st != OK || B == 0 || H == 0) return st;
-  return launch_serial<TIn>(q, k, v, beta, s_in, s_out, o, active, B, 1, H, D,
-                            reinterpret_cast<hipStream_t>(stream_ptr), who);
+  hipStream_t stream = reinterpret_cast<hipStream_t>(stream_ptr);
+  bool fast;
+  if constexpr (sizeof(TIn) == 4) {
+    fast = delta_step_fast_f32(q, k, v, beta, s_in, s_out, o, active, B, H, D, stream);
+  } else {
+    fast = delta_step_fast_bf16(q, k, v, beta, s_in, s_out, o, active, B, H, D, stream);
+  }
+  if (fast) return check_launch(who);
+  return launch_serial<TIn>(q, k, v, beta, s_in, s_out, o, active, B, 1, H, D, stream, who);
 }
 
 }  // namespace

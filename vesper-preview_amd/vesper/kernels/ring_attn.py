@@ -28,6 +28,11 @@ HEAD_DIMS = (16, 32, 64, 128)
 MAX_GROUP = 8
 
 
+def _aligned(t: Tensor) -> Tensor:
+    t = t.contiguous()
+    return t if t.data_ptr() % 16 == 0 else t.clone()
+
+
 @dataclass(frozen=True)
 class RingKVCache:
     """A decoding window of ``window`` slots; slot order is not age order."""
@@ -53,7 +58,8 @@ def kv_ring_empty(b: int, hkv: int, dk: int, window: int, dtype: torch.dtype, de
 
 
 def ring_attention(q: Tensor, k: Tensor, v: Tensor, pos: Tensor, cache: RingKVCache, *, active: Tensor | None = None,
-                   inplace: bool = False, check_positions: bool = True) -> tuple[Tensor, RingKVCache]:
+                   inplace: bool = False, check_positions: bool = True,
+                   workspace: Tensor | None = None) -> tuple[Tensor, RingKVCache]:
     """One new token per row over the ring and itself; then the token is written into its slot.
 
     Args:
@@ -64,6 +70,9 @@ def ring_attention(q: Tensor, k: Tensor, v: Tensor, pos: Tensor, cache: RingKVCa
         active: optional bool ``[b]``; an inactive row's output is zero, its token is still written.
         inplace: write into ``cache``'s tensors instead of a copy.
         check_positions: hold ``pos >= 0`` with ``require`` (a device assert under graph capture).
+        workspace: optional int32 tensor of at least ``b`` zeros on q's device, the per-row arrival
+            counters of the in-kernel write; every call leaves it zero, so a decoder can keep one
+            (calls that overlap in time must not share it). By default a fresh one is made.
 
     Returns:
         ``(o [b, 1, h, dk], ring)`` with the ring that holds the new tokens.
@@ -108,11 +117,24 @@ def ring_attention(q: Tensor, k: Tensor, v: Tensor, pos: Tensor, cache: RingKVCa
     for name, t in (("k", ring.k), ("v", ring.v), ("pos", ring.pos), ("valid", ring.valid)):
         if not t.is_contiguous():
             raise ContractError(f"cache.{name} must be contiguous for an in-place ring")
-    q, k, v, pos = (t.contiguous() for t in (q, k, v, pos))
+    q, k, v, pos = (_aligned(t) for t in (q, k, v, pos))
+    for name, t in (("k", ring.k), ("v", ring.v)):
+        if t.data_ptr() % 16 != 0:
+            raise ContractError(f"cache.{name} must be 16-byte aligned for an in-place ring")
     o = torch.empty_like(q)
+    # per-row arrival counters of the in-kernel write: zero before, and the kernel leaves them zero
+    if workspace is None:
+        counters = torch.zeros(max(b, 1), dtype=torch.int32, device=q.device)
+    else:
+        counters = workspace
+        if counters.dtype != torch.int32 or counters.device != q.device or not counters.is_contiguous():
+            raise ContractError("workspace must be a contiguous int32 tensor on q's device")
+        if counters.numel() < b:
+            raise ContractError(f"workspace holds {counters.numel()} counters, {b} rows need {b}")
     entry = "vsp_ring_attn_bf16" if q.dtype == torch.bfloat16 else "vsp_ring_attn_f16"
     with torch.cuda.device(q.device):
         _lib.call(entry, q.data_ptr(), k.data_ptr(), v.data_ptr(), pos.data_ptr(), ring.k.data_ptr(),
-                  ring.v.data_ptr(), ring.pos.data_ptr(), ring.valid.data_ptr(), o.data_ptr(), _lib.ptr(mask), b, h,
-                  hkv, dk, cache.window, 1.0 / math.sqrt(dk), 1, _lib.stream_of(q.device))
+                  ring.v.data_ptr(), ring.pos.data_ptr(), ring.valid.data_ptr(), o.data_ptr(), _lib.ptr(mask),
+                  counters.data_ptr(), counters.numel() * 4, b, h, hkv, dk, cache.window, 1.0 / math.sqrt(dk), 1,
+                  _lib.stream_of(q.device))
     return o, ring
