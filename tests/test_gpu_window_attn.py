@@ -93,6 +93,19 @@ def test_active_mask_skips_inactive_queries_only():
     _check(got, want)
 
 
+def test_large_logits_stay_finite_and_match():
+    # logits with a standard deviation near 100: exp2 overflows unless every tile's running maximum
+    # is the true maximum over the four lane groups of its query (the lazy rescale relies on it)
+    from vesper.kernels.window_attn import window_attention
+
+    q, keys, values = _inputs(2, 300, 20, 4, 2, 64, seed=31)
+    q, keys = (10 * q.float()).to(BF16), (10 * keys.float()).to(BF16)
+    want = oracle_window(q.double(), keys.double(), values.double(), 100)
+    got = window_attention(q.to(GPU), keys.to(GPU), values.to(GPU), 100)
+    assert bool(torch.isfinite(got).all())
+    _check(got, want)
+
+
 def test_refusals():
     from vesper.contracts import ContractError
     from vesper.kernels.window_attn import window_attention

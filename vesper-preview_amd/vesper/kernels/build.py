@@ -64,7 +64,8 @@ def build(verbose: bool = False) -> Path:
     with ThreadPoolExecutor(max_workers=workers) as pool:
         objs = list(pool.map(_compile, srcs))
     tmp = LIBRARY.with_suffix(".so.tmp")
-    cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs)]
+    # --no-undefined: a kernel whose host stub failed to instantiate must fail the build, not the load
+    cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-Wl,--no-undefined", "-o", str(tmp), *map(str, objs)]
     proc = subprocess.run(cmd, capture_output=True, text=True, check=False)
     if proc.returncode != 0:
         raise RuntimeError(f"link failed:\n{proc.stderr[-6000:]}")

@@ -4,17 +4,29 @@
 // [B, M + N, HKV, D] whose first M rows are the cache; query i sits at key index M + i and attends
 // key indices [M + i - W + 1, M + i]; scale 1/sqrt(D); query head h reads KV head h / (H / HKV).
 //
-// One workgroup = 64 queries of one (b, h), four waves of 16 queries. Key tiles of 64 rows walk the
-// window: K is staged row-major in LDS, V transposed ([d][key]). Each wave computes the score tile
-// transposed, S^T = K Q^T (16x16x32 MFMA, Q held in registers as the B operand), so a lane holds
-// one query's scores for 16 keys; the online softmax (running max, exp2, running sum) then needs
-// only a 4-lane reduction, and the probabilities are already laid out as the B operand of
-// O^T += V^T P^T. The next key tile is prefetched into registers while the current one is used.
+// One workgroup = 128 queries of one (b, h): four waves of 32 queries, each as two 16-query
+// blocks, so every K or V fragment read from LDS feeds two MFMAs. Key tiles of 64 rows walk the
+// window through double-buffered LDS (one barrier per tile; the next tile's global loads are in
+// flight while the current one is used). Per tile and query block a wave computes the transposed
+// score tile S^T = K Q^T (16x16x32 MFMA, K rows from LDS as the A operand, Q in registers as the
+// B operand), so a lane holds 16 keys of one query: the row maximum needs two lane swaps
+// (v_permlane16/32_swap) and the probabilities are already laid out as the B operand of
+// O^T += V^T P^T. V stays row-major in LDS; its transposed A fragments come from ds_read_b64_tr_b16.
+// At D >= 64 the tiles go from global memory straight into LDS (global_load_lds_dwordx4), with no
+// staging registers; rows carry one 16-byte pad segment against bank conflicts.
+//
+// Softmax: exp2 with the scale folded into one FMA per score; the running maximum is only moved
+// when a tile's maximum exceeds it by more than kLazy (log2 units), so the O rescale runs about
+// once per query instead of once per tile (probabilities then reach at most 2^kLazy, which bf16
+// P and the fp32 sums hold exactly as well). Only tiles that cross the causal diagonal, the
+// window's lower edge or the end of the keys are masked.
 #include "common.h"
 #include "vesper_kernels.h"
 
 namespace vsp {
 namespace {
+
+constexpr float kLazy = 8.f;
 
 template <typename T> struct Mma;
 template <> struct Mma<__bf16> {
@@ -32,22 +44,59 @@ template <> struct Mma<_Float16> {
   }
 };
 
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+
+// ds_read_b64_tr_b16: within each 16-lane group, lane i receives element i % 4 of the 8-byte
+// pieces addressed by lanes 4e + i / 4 (e = 0..3). Lane j of the group addressing row r0 + j / 4,
+// column c0 + 4 (j % 4) of a row-major tile therefore receives column c0 + i of rows r0 .. r0 + 3.
+template <typename T>
+__device__ __forceinline__ typename Mma<T>::V4 read_tr(const T* p) {
+  const s16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(p));
+  return __builtin_bit_cast(typename Mma<T>::V4, v);
+}
+
+// 16 bytes per lane from global memory straight into LDS (global_load_lds_dwordx4): lane i writes
+// lds + 16 i, so `lds` must be the same for the whole wave. Device pass only: the host pass of a
+// kernel template does not take the builtin.
+__device__ __forceinline__ void load_lds16(const void* src, void* lds) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  __builtin_amdgcn_global_load_lds(src, lds, 16, 0, 0);
+#endif
+}
+
+// max over the four lanes l, l ^ 16, l ^ 32, l ^ 48 (the four lane groups of one query)
+__device__ __forceinline__ float max_over_groups(float x) {
+  const auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  const auto c = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(c[0]), __uint_as_float(c[1]));
+}
+
 template <typename T, int D>
-__global__ __launch_bounds__(256) void window_attn_kernel(const T* __restrict__ q, const T* __restrict__ keys,
-                                                          const T* __restrict__ values, T* __restrict__ o,
-                                                          const uint8_t* __restrict__ active, int N, int M, int H,
-                                                          int HKV, int W, float scale_log2, int nqt) {
+__global__ __launch_bounds__(256, D >= 128 ? 2 : 4) void window_attn_kernel(const T* __restrict__ q, const T* __restrict__ keys,
+                                                             const T* __restrict__ values, T* __restrict__ o,
+                                                             const uint8_t* __restrict__ active, int N, int M, int H,
+                                                             int HKV, int W, float scale_log2, int nqt) {
   using V8 = typename Mma<T>::V8;
   using V4 = typename Mma<T>::V4;
+  constexpr int QT = 128;              // queries per workgroup
+  constexpr int QB = 2;                // 16-query blocks per wave
+  constexpr int KT = 64;               // keys per tile
   constexpr int DP = D < 32 ? 32 : D;  // feature extent padded to the MFMA k step
-  constexpr int PK = DP + 8;           // LDS pitch of K rows
-  constexpr int PV = 64 + 8;           // LDS pitch of V^T rows
   constexpr int DT = DP / 16;          // 16-row tiles of O^T
   constexpr int KSQ = DP / 32;         // k steps over features
-  constexpr int SEG = DP / 8;          // 16-byte segments per key row
-  constexpr int LOADS = (64 * SEG + 255) / 256;
-  __shared__ __align__(16) T sK[64 * PK];
-  __shared__ __align__(16) T sVt[DP * PV];
+  constexpr int SEG = DP / 8;          // 16-byte segments per row
+  constexpr int PK = DP + 8;           // LDS pitch of K and V rows (elements): one pad segment
+  constexpr int PSEG = SEG + 1;        // 16-byte segments per padded row
+  // At D >= 64 the tiles go from global memory straight into LDS: a wave instruction fills 1 KiB
+  // of consecutive segments (pad segments re-read a real one and are never used); narrower heads,
+  // whose rows need zero padding up to the MFMA k step, stage through registers.
+  constexpr bool kDirect = D >= 64;
+  constexpr int NINS = KT * PSEG / 64;  // wave instructions per tile for K (and for V)
+  constexpr int NI = kDirect ? (NINS + 3) / 4 : (KT * SEG + 255) / 256;
+  __shared__ __align__(16) T sK[2][KT * PK];
+  __shared__ __align__(16) T sV[2][KT * PK];
 
   const int lg = xcd_logical_block(blockIdx.x, gridDim.x);
   const int qt = lg % nqt, bh = lg / nqt;
@@ -56,153 +105,224 @@ __global__ __launch_bounds__(256) void window_attn_kernel(const T* __restrict__ 
   const int w = threadIdx.x >> 6, l = threadIdx.x & 63;
   const int lq = l & 15, g = l >> 4;
   const int S = M + N;
-  const int qbase = qt * 64;
-  const int myq = qbase + 16 * w + lq;
-  const bool qok = myq < N;
-  const bool act = qok && (active == nullptr || active[(size_t)b * N + myq] != 0);
-  T* dst = o + (((size_t)b * N + (qok ? myq : 0)) * H + h) * D;
+  const int qbase = qt * QT;
+  const int wq0 = qbase + 32 * w;  // the wave's first query
 
-  if (!__syncthreads_or(act)) {  // every query of the tile is inactive (or past N): zeros
-    if (qok && g == 0)
-      for (int d = 0; d < D; ++d) dst[d] = from_f32<T>(0.f);
+  bool qok[QB], act[QB];
+  bool any = false;
+#pragma unroll
+  for (int qb = 0; qb < QB; ++qb) {
+    const int myq = wq0 + 16 * qb + lq;
+    qok[qb] = myq < N;
+    act[qb] = qok[qb] && (active == nullptr || active[(size_t)b * N + myq] != 0);
+    any |= act[qb];
+  }
+  if (!__syncthreads_or(any)) {  // every query of the tile is inactive (or past N): zeros
+#pragma unroll
+    for (int qb = 0; qb < QB; ++qb) {
+      const int myq = wq0 + 16 * qb + lq;
+      if (qok[qb] && g == 0) {
+        T* dst = o + (((size_t)b * N + myq) * H + h) * D;
+        for (int d = 0; d < D; ++d) dst[d] = from_f32<T>(0.f);
+      }
+    }
     return;
   }
 
-  V8 qf[KSQ];
+  V8 qf[QB][KSQ];
 #pragma unroll
-  for (int s = 0; s < KSQ; ++s) {
-    const int f = 32 * s + 8 * g;
-    if (qok && f < D) {
-      qf[s] = *reinterpret_cast<const V8*>(q + (((size_t)b * N + myq) * H + h) * D + f);
-    } else {
+  for (int qb = 0; qb < QB; ++qb) {
+    const int myq = wq0 + 16 * qb + lq;
 #pragma unroll
-      for (int j = 0; j < 8; ++j) qf[s][j] = from_f32<T>(0.f);
+    for (int s = 0; s < KSQ; ++s) {
+      const int f = 32 * s + 8 * g;
+      if (qok[qb] && f < D) {
+        qf[qb][s] = *reinterpret_cast<const V8*>(q + (((size_t)b * N + myq) * H + h) * D + f);
+      } else {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) qf[qb][s][j] = from_f32<T>(0.f);
+      }
     }
   }
 
   const int kfirst = max(0, M + qbase - W + 1);
-  const int klast = min(S, M + qbase + 64);
-  const int qidx = M + myq;
+  const int klast = min(S, M + qbase + QT);
+  const int ntiles = (klast - kfirst + KT - 1) / KT;
   const size_t kv_row = (size_t)HKV * D;
   const T* kbase = keys + ((size_t)b * S * HKV + kvh) * D;
   const T* vbase = values + ((size_t)b * S * HKV + kvh) * D;
 
-  V8 kreg[LOADS], vreg[LOADS];
-  auto fetch = [&](int k0) {
+  // staging of one 64-key tile; keys past klast re-read key klast - 1 (masked in the scores, weight 0
+  // in the output)
+  V8 kreg[kDirect ? 1 : NI], vreg[kDirect ? 1 : NI];
+  auto fetch = [&](int k0, int buf) {
 #pragma unroll
-    for (int i = 0; i < LOADS; ++i) {
-      const int seg = threadIdx.x + 256 * i;
-      const int row = seg / SEG, part = seg - row * SEG;
-      const int key = k0 + row;
-      const bool ok = seg < 64 * SEG && key < klast && 8 * part < D;
-      if (ok) {
-        kreg[i] = *reinterpret_cast<const V8*>(kbase + (size_t)key * kv_row + 8 * part);
-        vreg[i] = *reinterpret_cast<const V8*>(vbase + (size_t)key * kv_row + 8 * part);
+    for (int j = 0; j < NI; ++j) {
+      if constexpr (kDirect) {
+        const int ins = w + 4 * j;  // this wave's j-th instruction of the tile
+        if (ins < NINS) {
+          const int pos = ins * 64 + l;  // padded segment position in the tile
+          const int row = pos / PSEG;
+          int seg = pos - row * PSEG;
+          seg = seg < SEG ? seg : 0;
+          const size_t goff = (size_t)min(k0 + row, klast - 1) * kv_row + 8 * seg;
+          load_lds16(kbase + goff, &sK[buf][ins * 64 * 8]);
+          load_lds16(vbase + goff, &sV[buf][ins * 64 * 8]);
+        }
       } else {
+        const int sg = threadIdx.x + 256 * j;
+        const int row = sg / SEG, part = sg - row * SEG;
+        const size_t goff = (size_t)min(k0 + row, klast - 1) * kv_row + 8 * part;
+        if (sg < KT * SEG && 8 * part < D) {
+          kreg[j] = *reinterpret_cast<const V8*>(kbase + goff);
+          vreg[j] = *reinterpret_cast<const V8*>(vbase + goff);
+        } else {
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          kreg[i][j] = from_f32<T>(0.f);
-          vreg[i][j] = from_f32<T>(0.f);
+          for (int e = 0; e < 8; ++e) {
+            kreg[j][e] = from_f32<T>(0.f);
+            vreg[j][e] = from_f32<T>(0.f);
+          }
         }
       }
     }
   };
-  auto stash = [&]() {
+  auto stash = [&](int buf) {
+    if constexpr (!kDirect) {
 #pragma unroll
-    for (int i = 0; i < LOADS; ++i) {
-      const int seg = threadIdx.x + 256 * i;
-      if (seg < 64 * SEG) {
-        const int row = seg / SEG, part = seg - row * SEG;
-        *reinterpret_cast<V8*>(sK + row * PK + 8 * part) = kreg[i];
-#pragma unroll
-        for (int j = 0; j < 8; ++j) sVt[(8 * part + j) * PV + row] = vreg[i][j];
+      for (int j = 0; j < NI; ++j) {
+        const int sg = threadIdx.x + 256 * j;
+        if (sg < KT * SEG) {
+          const int row = sg / SEG, part = sg - row * SEG;
+          *reinterpret_cast<V8*>(&sK[buf][row * PK + 8 * part]) = kreg[j];
+          *reinterpret_cast<V8*>(&sV[buf][row * PK + 8 * part]) = vreg[j];
+        }
       }
     }
   };
 
-  float m_run = -1e30f, l_run = 0.f;
-  f32x4 oacc[DT];
+  float m_used[QB], l_run[QB];
+  f32x4 oacc[QB][DT];
 #pragma unroll
-  for (int t = 0; t < DT; ++t) oacc[t] = zero4();
+  for (int qb = 0; qb < QB; ++qb) {
+    m_used[qb] = -1e30f;  // finite: exp2 of a masked score minus it is exactly 0
+    l_run[qb] = 0.f;
+#pragma unroll
+    for (int t = 0; t < DT; ++t) oacc[qb][t] = zero4();
+  }
+  // the wave's queries in key-index space: [wlo, whi]
+  const int wlo = M + wq0, whi = M + wq0 + 31;
 
-  fetch(kfirst);
-  for (int k0 = kfirst; k0 < klast; k0 += 64) {
-    __syncthreads();
-    stash();
-    __syncthreads();
-    if (k0 + 64 < klast) fetch(k0 + 64);
+  fetch(kfirst, 0);
+  stash(0);
+  __syncthreads();
+  for (int it = 0; it < ntiles; ++it) {
+    const int k0 = kfirst + it * KT;
+    const int buf = it & 1;
+    // the other buffer was last read before the previous barrier
+    if (it + 1 < ntiles) fetch(k0 + KT, buf ^ 1);
 
-    float s[4][4];
-    float mt = -INFINITY;
+    // skip a tile this wave's queries cannot see (wave-uniform)
+    const bool seen = k0 <= whi && k0 + KT - 1 > wlo - W;
+    if (seen) {
+      const bool full = k0 + KT - 1 <= wlo && k0 > whi - W && k0 + KT <= klast;
+      const T* Kt = sK[buf];
+      const T* Vt = sV[buf];
+      f32x4 sacc[QB][4];
 #pragma unroll
-    for (int kb = 0; kb < 4; ++kb) {
-      f32x4 acc = zero4();
+      for (int kb = 0; kb < 4; ++kb) {
 #pragma unroll
-      for (int st = 0; st < KSQ; ++st) {
-        const V8 a = *reinterpret_cast<const V8*>(sK + (16 * kb + lq) * PK + 32 * st + 8 * g);
-        acc = Mma<T>::run(a, qf[st], acc);
+        for (int qb = 0; qb < QB; ++qb) sacc[qb][kb] = zero4();
+#pragma unroll
+        for (int st = 0; st < KSQ; ++st) {
+          const V8 a = *reinterpret_cast<const V8*>(Kt + (16 * kb + lq) * PK + 32 * st + 8 * g);
+#pragma unroll
+          for (int qb = 0; qb < QB; ++qb) sacc[qb][kb] = Mma<T>::run(a, qf[qb][st], sacc[qb][kb]);
+        }
       }
+      V8 pb[QB][2];
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int key = k0 + 16 * kb + 4 * g + r;
-        const bool vis = key < klast && key <= qidx && key > qidx - W;
-        s[kb][r] = vis ? acc[r] * scale_log2 : -INFINITY;
-        mt = fmaxf(mt, s[kb][r]);
+      for (int qb = 0; qb < QB; ++qb) {
+        if (!full) {
+          const int qidx = wlo + 16 * qb + lq;
+#pragma unroll
+          for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              const int key = k0 + 16 * kb + 4 * g + r;
+              const bool vis = key < klast && key <= qidx && key > qidx - W;
+              sacc[qb][kb][r] = vis ? sacc[qb][kb][r] : -INFINITY;
+            }
+        }
+        float mt = sacc[qb][0][0];
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) mt = fmaxf(mt, sacc[qb][kb][r]);
+        mt = max_over_groups(mt) * scale_log2;
+        const bool need = mt > m_used[qb] + kLazy;
+        if (__builtin_amdgcn_ballot_w64(need)) {  // some query of the wave moves its maximum
+          const float mn = need ? mt : m_used[qb];
+          const float alpha = __builtin_amdgcn_exp2f(m_used[qb] - mn);
+          l_run[qb] *= alpha;
+#pragma unroll
+          for (int t = 0; t < DT; ++t) oacc[qb][t] *= alpha;
+          m_used[qb] = mn;
+        }
+        float p[4][4];
+        float psum = 0.f;
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            p[kb][r] = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[qb][kb][r], scale_log2, -m_used[qb]));
+            psum += p[kb][r];
+          }
+        l_run[qb] += psum;
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            pb[qb][ks][j] = from_f32<T>(p[2 * ks][j]);
+            pb[qb][ks][4 + j] = from_f32<T>(p[2 * ks + 1][j]);
+          }
       }
-    }
-    mt = fmaxf(mt, __shfl_xor(mt, 16));
-    mt = fmaxf(mt, __shfl_xor(mt, 32));
-    const float m_new = fmaxf(m_run, mt);
-    const float alpha = exp2f(m_run - m_new);
-    float psum = 0.f;
-#pragma unroll
-    for (int kb = 0; kb < 4; ++kb)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const float p = exp2f(s[kb][r] - m_new);
-        s[kb][r] = p;
-        psum += p;
-      }
-    l_run = l_run * alpha + psum;
-    m_run = m_new;
-#pragma unroll
-    for (int t = 0; t < DT; ++t) oacc[t] *= alpha;
-
-#pragma unroll
-    for (int ks = 0; ks < 2; ++ks) {
-      V8 pb;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        pb[j] = from_f32<T>(s[2 * ks][j]);
-        pb[4 + j] = from_f32<T>(s[2 * ks + 1][j]);
-      }
+      // O^T += V^T P^T: A fragments of V^T by transposed LDS reads (lane (lq, g) gets column
+      // 16 t + lq of key rows 32 ks + 4 g .. +3 and 32 ks + 16 + 4 g .. +3)
 #pragma unroll
       for (int t = 0; t < DT; ++t) {
-        const T* row = sVt + (16 * t + lq) * PV + 32 * ks + 4 * g;
-        const V4 lo = *reinterpret_cast<const V4*>(row);
-        const V4 hi = *reinterpret_cast<const V4*>(row + 16);
-        V8 a;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          a[j] = lo[j];
-          a[4 + j] = hi[j];
+        for (int ks = 0; ks < 2; ++ks) {
+          const T* base = Vt + (32 * ks + 4 * g + (lq >> 2)) * PK + 16 * t + 4 * (lq & 3);
+          const V4 lo = read_tr<T>(base);
+          const V4 hi = read_tr<T>(base + 16 * PK);
+          const V8 a = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+#pragma unroll
+          for (int qb = 0; qb < QB; ++qb) oacc[qb][t] = Mma<T>::run(a, pb[qb][ks], oacc[qb][t]);
         }
-        oacc[t] = Mma<T>::run(a, pb, oacc[t]);
       }
     }
+    if (it + 1 < ntiles) stash(buf ^ 1);
+    __syncthreads();  // (the direct loads into buf ^ 1 are waited for before it)
   }
 
-  float lt = l_run + __shfl_xor(l_run, 16);
-  lt += __shfl_xor(lt, 32);
-  const float inv = (act && lt > 0.f) ? 1.f / lt : 0.f;
-  if (qok) {
 #pragma unroll
-    for (int t = 0; t < DT; ++t)
+  for (int qb = 0; qb < QB; ++qb) {
+    float lt = l_run[qb] + __shfl_xor(l_run[qb], 16);
+    lt += __shfl_xor(lt, 32);
+    const float inv = (act[qb] && lt > 0.f) ? 1.f / lt : 0.f;
+    if (qok[qb]) {
+      T* dst = o + (((size_t)b * N + wq0 + 16 * qb + lq) * H + h) * D;
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int d = 16 * t + 4 * g + r;
-        if (d < D) dst[d] = from_f32<T>(oacc[t][r] * inv);
+      for (int t = 0; t < DT; ++t) {
+        const int d = 16 * t + 4 * g;
+        if (d < D) {
+          V4 v;
+#pragma unroll
+          for (int r = 0; r < 4; ++r) v[r] = from_f32<T>(oacc[qb][t][r] * inv);
+          *reinterpret_cast<V4*>(dst + d) = v;
+        }
       }
+    }
   }
 }
 
@@ -214,11 +334,15 @@ int window_attn(const T* q, const T* keys, const T* values, T* o, const uint8_t*
   if (B < 0 || N < 0 || M < 0 || H < 1 || HKV < 1) return fail(ERR_ARG, "%s: bad sizes B=%d N=%d M=%d H=%d HKV=%d", who, B, N, M, H, HKV);
   if (H % HKV != 0) return fail(ERR_ARG, "%s: %d query heads are not a multiple of %d KV heads", who, H, HKV);
   if (W < 1) return fail(ERR_ARG, "%s: window must be at least 1, got %d", who, W);
+  if (!(scale > 0.f)) return fail(ERR_ARG, "%s: the score scale must be positive, got %g", who, (double)scale);
   if (!attn_width(D)) return fail(ERR_UNSUPPORTED, "%s: head dimension %d (kernels: 16, 32, 64, 128)", who, D);
   if (B == 0 || N == 0) return OK;
   if (!q || !keys || !values || !o) return fail(ERR_ARG, "%s: null pointer", who);
+  if ((reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(keys) | reinterpret_cast<uintptr_t>(values) |
+       reinterpret_cast<uintptr_t>(o)) & 15)
+    return fail(ERR_ARG, "%s: q, keys, values and o must be 16-byte aligned", who);
   const float scale_log2 = scale * 1.4426950408889634f;
-  const int nqt = (N + 63) / 64;
+  const int nqt = (N + 127) / 128;
   dim3 grid((unsigned)((size_t)nqt * H * B));
   hipStream_t stream = reinterpret_cast<hipStream_t>(stream_ptr);
   switch (D) {
