@@ -143,6 +143,26 @@ __device__ __forceinline__ float group_sum(float x) {
   return x;
 }
 
+// ---- transposed LDS reads (gfx950 ds_read_b64_tr_b16) ------------------------------------------
+// Within each 16-lane group, lane i receives element i % 4 of the 8-byte pieces addressed by lanes
+// 4e + i / 4 (e = 0..3). So when lane j of a group addresses row r0 + j / 4, column c0 + 4 (j % 4)
+// of a row-major tile of 16-bit elements, lane i receives column c0 + i of rows r0 .. r0 + 3: the
+// k-contiguous operand fragment of an MFMA whose k index runs down the tile's rows.
+typedef short s16x4_t __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) s16x4_t lds_s16x4_t;
+template <typename V4, typename T>
+__device__ __forceinline__ V4 read_tr16(const T* p) {
+  const s16x4_t v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t*)(p));
+  return __builtin_bit_cast(V4, v);
+}
+// The transposed fragment of a row-major tile for lane (lq, g) of a wave: column c0 + lq of rows
+// r0 + 4 g .. r0 + 4 g + 3 (pitch in elements).
+template <typename V4, typename T>
+__device__ __forceinline__ V4 read_tr16_rows(const T* tile, int pitch, int r0, int c0) {
+  const int l = threadIdx.x & 63, lq = l & 15, g = l >> 4;
+  return read_tr16<V4>(tile + (r0 + 4 * g + (lq >> 2)) * pitch + c0 + 4 * (lq & 3));
+}
+
 // ---- XCD-aware block order --------------------------------------------------------------------
 // Workgroups are dispatched round-robin over the 8 XCDs (block g runs on XCD g % 8), and each XCD
 // has its own L2. Renumber so that consecutive logical ids share an XCD: blocks that read the same

@@ -714,6 +714,286 @@ __global__ __launch_bounds__(64 * (ChainShape<E, DK>::NH + 1)) void delta_chain_
   }
 }
 // --------------------------------------------------------------------------------------------
+// the bf16 chunk chain (head widths 32, 64, 128): as delta_chain_kernel, with the helper work
+// spread so that no helper's share of an iteration outlasts the chain step:
+//  * transposed operands (K^T for the state update, the V slice in the accumulator layout) come
+//    from row-major LDS tiles through ds_read_b64_tr_b16, so staging a chunk is plain LDS stores;
+//  * the output of a chunk, O = Q H + tril(Q K^T) Delta, is computed by two idle helpers in the
+//    next iteration, each taking two of the four 16-token row blocks and forming its own causal
+//    Q K^T tiles from the K and Q tiles still in LDS (K and Q are triple-buffered for that).
+// Per iteration it: the chain runs chunk it; helper (it + 1) % 7 stages chunk it + 1; helpers
+// (it - 1) % 7 and (it + 2) % 7 write the outputs of chunk it - 1; helper it % 7 issues the
+// global loads of chunk it + 7 into its registers (six iterations of latency cover).
+// --------------------------------------------------------------------------------------------
+__device__ __forceinline__ f32x4 mfma_bf16(const bf16x8& a, const bf16x8& b, f32x4 acc) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, acc, 0, 0, 0);
+}
+
+template <typename TIn, int DK>
+__global__ __launch_bounds__(512) void delta_chain_bf16_kernel(const TIn* __restrict__ q, const TIn* __restrict__ k,
+                                                               const TIn* __restrict__ v,
+                                                               const __bf16* __restrict__ tmat,
+                                                               const float* __restrict__ s_in, float* __restrict__ s_out,
+                                                               TIn* __restrict__ o, const uint8_t* __restrict__ active,
+                                                               int T, int H) {
+  using E = __bf16;
+  constexpr int NH = 7;                          // helper waves
+  constexpr int BV = 16;                         // value columns per chain
+  constexpr int NS = DK / BV;                    // value slices per head
+  constexpr int PK = DK + 8;                     // pitch of K and Q rows (elements)
+  constexpr int PT = 64 + 8;                     // pitch of T rows and of Delta^T rows
+  constexpr int PV = BV + 8;                     // pitch of V slice rows
+  constexpr int HB = DK / 16;                    // 16-row tiles of the state slice
+  constexpr int KBF = DK / 32;                   // 32-wide k blocks over dk
+  constexpr int TSEG = kChunkT * 2 / 16 / 64;    // 16-byte compact-T segments per lane
+  using N = Nat<E, DK>;
+  using AB = typename Acc<E>::B;
+  using NR = typename N::R;
+
+  __shared__ __align__(16) E sK[3][64 * PK];
+  __shared__ __align__(16) E sQ[3][64 * PK];
+  __shared__ __align__(16) E sT[2][64 * PT];
+  __shared__ __align__(16) E sV[2][64 * PV];
+  __shared__ __align__(16) E sHo[2][BV * PK];  // H^T of the slice: row = value column, column = dk
+  __shared__ __align__(16) E sDo[2][BV * PT];  // Delta^T: row = value column, column = token
+  __shared__ uint8_t sAct[3][64];
+
+  const int lg = xcd_logical_block(blockIdx.x, gridDim.x);
+  const int slice = lg % NS, bh = lg / NS;
+  const int b = bh / H, h = bh - b * H;
+  const int v0 = slice * BV;
+  const int wave = threadIdx.x >> 6, l = threadIdx.x & 63;
+  const int lq = l & 15, g = l >> 4;
+  const int nc = (T + kChunk - 1) / kChunk;
+  const int rstride = H * DK;
+  const size_t bh_base = ((size_t)b * T * H + h) * DK;
+
+  // ---- helper state: one chunk's loads in flight ----
+  const int hj = wave - 1;
+  NR qn[4][N::NREG], kn[4][N::NREG];
+  u32x4 tseg[TSEG];
+  bf16x4 vn[4];
+  uint8_t actraw[4];
+
+  // Rows of one (b, h) from a uniform base with 32-bit lane offsets (the host keeps T*H*DK < 2^31).
+  // Every load is unconditional (rows past the chunk's end re-read its last row and are zeroed when
+  // staged): a load under a branch made the compiler wait for the earlier loads of the batch.
+  auto load_rows = [&](NR (&dst)[4][N::NREG], const TIn* base, int c) {
+    const int nvc = min(kChunk, T - c * kChunk);
+    const TIn* cb = base + bh_base + (size_t)c * kChunk * rstride;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const unsigned tok = (unsigned)min(16 * i + lq, nvc - 1);
+#pragma unroll
+      for (int sgi = 0; sgi < N::NREG; ++sgi)
+        dst[i][sgi] = *reinterpret_cast<const NR*>(cb + (tok * (unsigned)rstride + (unsigned)N::feat(sgi)));
+    }
+  };
+  auto issue_loads = [&](int c) {
+    load_rows(qn, q, c);
+    load_rows(kn, k, c);
+    const u32x4* ts = reinterpret_cast<const u32x4*>(tmat + ((size_t)bh * nc + c) * kChunkT);
+#pragma unroll
+    for (int j = 0; j < TSEG; ++j) tseg[j] = ts[l + 64 * j];
+    const int nvc = min(kChunk, T - c * kChunk);
+    const TIn* cb = v + bh_base + (size_t)c * kChunk * rstride + v0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const unsigned tok = (unsigned)min(16 * i + lq, nvc - 1);
+      vn[i] = *reinterpret_cast<const bf16x4*>(cb + (tok * (unsigned)rstride + 4u * (unsigned)g));
+    }
+    if (active != nullptr) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int tok = min(16 * i + lq, nvc - 1);
+        actraw[i] = active[(size_t)b * T + (size_t)c * kChunk + tok];
+      }
+    }
+  };
+  auto store_chunk = [&](int c) {
+    const int b3 = c % 3, b2 = c & 1;
+    const int nvc = min(kChunk, T - c * kChunk);
+    if (nvc < kChunk) {  // the sequence's last, partial chunk: rows past its end stage as zeros
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        if (16 * i + lq >= nvc) {
+#pragma unroll
+          for (int sgi = 0; sgi < N::NREG; ++sgi) kn[i][sgi] = qn[i][sgi] = NR{};
+          vn[i] = bf16x4{};
+        }
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int tok = 16 * i + lq;
+#pragma unroll
+      for (int sgi = 0; sgi < N::NREG; ++sgi) {
+        *reinterpret_cast<NR*>(&sK[b3][tok * PK + N::feat(sgi)]) = kn[i][sgi];
+        *reinterpret_cast<NR*>(&sQ[b3][tok * PK + N::feat(sgi)]) = qn[i][sgi];
+      }
+      *reinterpret_cast<bf16x4*>(&sV[b2][tok * PV + 4 * g]) = vn[i];
+      if (g == 0) sAct[b3][tok] = (tok < nvc && (active == nullptr || actraw[i] != 0)) ? 1 : 0;
+    }
+#pragma unroll
+    for (int j = 0; j < TSEG; ++j) {
+      const int el = (l + 64 * j) * 8;
+      const int t = el / kTileElems, within = el - t * kTileElems;
+      const int ti = (t >= 1) + (t >= 3) + (t >= 6), tj = t - ti * (ti + 1) / 2;
+      const int row = 16 * ti + within / 16, col = 16 * tj + within % 16;
+      *reinterpret_cast<u32x4*>(&sT[b2][row * PT + col]) = tseg[j];
+    }
+  };
+  // rows 16 blk .. 16 blk + 15 of the output of chunk c: O^T = H^T Q^T + Delta^T P^T with the
+  // causal P^T = tril(Q K^T)^T formed here from the LDS tiles
+  auto write_block = [&](int c, int blk) {
+    const int b3 = c % 3, b2 = c & 1;
+    const int nvc = min(kChunk, T - c * kChunk);
+    NR ql[N::NREG];
+#pragma unroll
+    for (int sgi = 0; sgi < N::NREG; ++sgi)
+      ql[sgi] = *reinterpret_cast<const NR*>(&sQ[b3][(16 * blk + lq) * PK + N::feat(sgi)]);
+    f32x4 acc = N::mma_lds(&sHo[b2][lq * PK], ql, zero4());
+    f32x4 pt[4];
+#pragma unroll
+    for (int jj = 0; jj < 4; ++jj) {
+      if (jj <= blk) {
+        const f32x4 sc = N::mma_lds(&sK[b3][(16 * jj + lq) * PK], ql, zero4());
+#pragma unroll
+        for (int r = 0; r < 4; ++r) pt[jj][r] = (16 * jj + 4 * g + r <= 16 * blk + lq) ? sc[r] : 0.f;
+      } else {
+        pt[jj] = zero4();
+      }
+    }
+    acc = Acc<E>::mma(&sDo[b2][lq * PT], Acc<E>::pack(pt[0], pt[1]), acc);
+    if (blk >= 2) acc = Acc<E>::mma(&sDo[b2][lq * PT + 32], Acc<E>::pack(pt[2], pt[3]), acc);
+    const int tok = 16 * blk + lq;
+    if (tok < nvc) {
+      TIn* dst = o + bh_base + (size_t)c * kChunk * rstride + v0 + (tok * rstride + 4 * g);
+      const bool on = sAct[b3][tok] != 0;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) dst[r] = from_f32<TIn>(on ? acc[r] : 0.f);
+    }
+  };
+
+  // ---- chain state ----
+  f32x4 hreg[HB];
+  if (wave == 0) {
+#pragma unroll
+    for (int m = 0; m < HB; ++m)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) hreg[m][r] = s_in[((size_t)bh * DK + 16 * m + 4 * g + r) * DK + v0 + lq];
+  }
+  // the Acc-layout A fragment of a row-major LDS row: k = 4 g + r and 16 + 4 g + r
+  auto acc_frag = [&](const E* arow) {
+    const bf16x4 lo = *reinterpret_cast<const bf16x4*>(arow + 4 * g);
+    const bf16x4 hi = *reinterpret_cast<const bf16x4*>(arow + 16 + 4 * g);
+    return bf16x8(__builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+  };
+  auto chain_step = [&](int c) {
+    const int b3 = c % 3, b2 = c & 1;
+    const E* K = sK[b3];
+    const E* Tm = sT[b2];
+    // every LDS operand of the step first, in one batch: a single wait instead of one per level
+    bf16x8 kfr[4][KBF], tfr[6], ktf[HB][2];
+    bf16x4 vfr[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+#pragma unroll
+      for (int kb = 0; kb < KBF; ++kb) kfr[i][kb] = acc_frag(K + (16 * i + lq) * PK + 32 * kb);
+      vfr[i] = read_tr16_rows<bf16x4>(sV[b2], PV, 16 * i, 0);
+    }
+    tfr[0] = acc_frag(Tm + lq * PT);
+    tfr[1] = acc_frag(Tm + (16 + lq) * PT);
+    tfr[2] = acc_frag(Tm + (32 + lq) * PT);
+    tfr[3] = acc_frag(Tm + (32 + lq) * PT + 32);
+    tfr[4] = acc_frag(Tm + (48 + lq) * PT);
+    tfr[5] = acc_frag(Tm + (48 + lq) * PT + 32);
+#pragma unroll
+    for (int m = 0; m < HB; ++m)
+#pragma unroll
+      for (int pr = 0; pr < 2; ++pr) {  // K^T: column 16 m + lq of token rows 32 pr + 4 g (+16)
+        const bf16x4 lo = read_tr16_rows<bf16x4>(K, PK, 32 * pr, 16 * m);
+        const bf16x4 hi = read_tr16_rows<bf16x4>(K, PK, 32 * pr + 16, 16 * m);
+        ktf[m][pr] = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+      }
+    __builtin_amdgcn_sched_barrier(0);
+
+    AB hb[KBF];
+#pragma unroll
+    for (int kb = 0; kb < KBF; ++kb) hb[kb] = Acc<E>::pack(hreg[2 * kb], hreg[2 * kb + 1]);
+#pragma unroll
+    for (int m = 0; m < HB; ++m) {
+      bf16x4 w4;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) w4[r] = (__bf16)hreg[m][r];
+      *reinterpret_cast<bf16x4*>(&sHo[b2][lq * PK + 16 * m + 4 * g]) = w4;
+    }
+    f32x4 rr[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      f32x4 kh = zero4();
+#pragma unroll
+      for (int kb = 0; kb < KBF; ++kb) kh = mfma_bf16(kfr[i][kb], hb[kb].v, kh);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) rr[i][r] = (float)vfr[i][r] - kh[r];
+    }
+    const AB rb0 = Acc<E>::pack(rr[0], rr[1]);
+    const AB rb1 = Acc<E>::pack(rr[2], rr[3]);
+    f32x4 dl[4];
+    dl[0] = mfma_bf16(tfr[0], rb0.v, zero4());
+    dl[1] = mfma_bf16(tfr[1], rb0.v, zero4());
+    dl[2] = mfma_bf16(tfr[3], rb1.v, mfma_bf16(tfr[2], rb0.v, zero4()));
+    dl[3] = mfma_bf16(tfr[5], rb1.v, mfma_bf16(tfr[4], rb0.v, zero4()));
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      bf16x4 w4;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) w4[r] = (__bf16)dl[i][r];
+      *reinterpret_cast<bf16x4*>(&sDo[b2][lq * PT + 16 * i + 4 * g]) = w4;
+    }
+    const AB db[2] = {Acc<E>::pack(dl[0], dl[1]), Acc<E>::pack(dl[2], dl[3])};
+#pragma unroll
+    for (int m = 0; m < HB; ++m)
+#pragma unroll
+      for (int pr = 0; pr < 2; ++pr) hreg[m] = mfma_bf16(ktf[m][pr], db[pr].v, hreg[m]);
+  };
+
+  // the upper tiles of T are never staged (the compact factor holds the ten lower ones): zero once
+  for (int i = threadIdx.x; i < 2 * 64 * PT; i += 512) (&sT[0][0])[i] = (__bf16)0.f;
+  __syncthreads();
+  // The chain and the helpers run separate loops with the same barrier sequence, so neither keeps
+  // the other's registers live.
+  if (wave == 0) {
+    for (int it = -1; it <= nc; ++it) {
+      if (it >= 0 && it < nc) chain_step(it);
+      __syncthreads();
+    }
+#pragma unroll
+    for (int m = 0; m < HB; ++m)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) s_out[((size_t)bh * DK + 16 * m + 4 * g + r) * DK + v0 + lq] = hreg[m][r];
+  } else {
+    if (hj < nc) issue_loads(hj);
+    for (int it = -1; it <= nc; ++it) {
+      const int cs = it + 1, co = it - 1;
+      if (cs < nc && cs % NH == hj) store_chunk(cs);
+      if (co >= 0) {
+        if (co % NH == hj) {
+          write_block(co, 0);
+          write_block(co, 3);
+        }
+        if ((co + 3) % NH == hj) {
+          write_block(co, 1);
+          write_block(co, 2);
+        }
+      }
+      if (it >= 0 && it < nc && it % NH == hj && it + NH < nc) issue_loads(it + NH);
+      __syncthreads();
+    }
+  }
+}
+
+// --------------------------------------------------------------------------------------------
 // host side
 // --------------------------------------------------------------------------------------------
 bool chunked_width(int D, bool fp32) { return D == 16 || D == 32 || D == 64 || (D == 128 && !fp32); }
@@ -753,8 +1033,13 @@ void launch_chunked(const TIn* q, const TIn* k, const TIn* v, const TIn* beta, c
   const int total = B * H * nc;
   hipLaunchKernelGGL((delta_prep_kernel<TIn, E, DK>), dim3((unsigned)((total + 3) / 4)), dim3(256), 0, stream, k, beta,
                      tmat, T, H, total);
-  hipLaunchKernelGGL((delta_chain_kernel<TIn, E, DK>), dim3((unsigned)(B * H * (DK / 16))),
-                     dim3(64 * (ChainShape<E, DK>::NH + 1)), 0, stream, q, k, v, tmat, s_in, s_out, o, active, T, H);
+  if constexpr (sizeof(E) == 2 && DK >= 32 && DK <= 64) {  // (at 128 its staging registers would spill)
+    hipLaunchKernelGGL((delta_chain_bf16_kernel<TIn, DK>), dim3((unsigned)(B * H * (DK / 16))), dim3(512), 0, stream, q,
+                       k, v, tmat, s_in, s_out, o, active, T, H);
+  } else {
+    hipLaunchKernelGGL((delta_chain_kernel<TIn, E, DK>), dim3((unsigned)(B * H * (DK / 16))),
+                       dim3(64 * (ChainShape<E, DK>::NH + 1)), 0, stream, q, k, v, tmat, s_in, s_out, o, active, T, H);
+  }
 }
 
 template <typename TIn, typename E>

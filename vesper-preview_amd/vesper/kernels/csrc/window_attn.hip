@@ -44,16 +44,9 @@ template <> struct Mma<_Float16> {
   }
 };
 
-typedef short s16x4 __attribute__((ext_vector_type(4)));
-typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
-
-// ds_read_b64_tr_b16: within each 16-lane group, lane i receives element i % 4 of the 8-byte
-// pieces addressed by lanes 4e + i / 4 (e = 0..3). Lane j of the group addressing row r0 + j / 4,
-// column c0 + 4 (j % 4) of a row-major tile therefore receives column c0 + i of rows r0 .. r0 + 3.
 template <typename T>
 __device__ __forceinline__ typename Mma<T>::V4 read_tr(const T* p) {
-  const s16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(p));
-  return __builtin_bit_cast(typename Mma<T>::V4, v);
+  return read_tr16<typename Mma<T>::V4>(p);
 }
 
 // 16 bytes per lane from global memory straight into LDS (global_load_lds_dwordx4): lane i writes
