@@ -7,7 +7,8 @@ sliding-window causal attention over the same batch shape (window 512, bf16). ``
 tokens/s = B*T / (time of one step), inputs resident in HBM. Beside it the line carries each
 kernel's own rate at its own configuration (attention alone at B=4), the decode rate (256
 single-token steps of batch 64: fp32 delta update of S [64,8,64,64] then attention over a 512-entry
-bf16 KV ring, captured as one HIP graph), the roofline of the dominant kernel measured with HIP
+bf16 KV ring, captured as one HIP graph), the looped column with per-token halting (B4 T2048 d512,
+8 passes), the roofline of the dominant kernel measured with HIP
 events on the launch stream inside the timed region, and the CPU oracle timed on a bounded sample
 of the same workload on this host's cores.
 
@@ -35,6 +36,7 @@ BF16_PEAK_TFLOPS = 2500.0
 B, T, H, D, WINDOW = 8, 4096, 8, 64, 512
 ATTN_B = 4
 DEC_B, DEC_W, DEC_STEPS = 64, 512, 256
+LOOP_B, LOOP_T, LOOP_D, LOOP_PASSES = 4, 2048, 512, 8
 
 
 def log(*a: object) -> None:
@@ -196,6 +198,29 @@ def time_decode(torch, reps: int = 5) -> dict:
     return {"ms_256_steps": ms, "tok_s": b * n / (ms / 1e3), "us_per_step": 1e3 * ms / n}
 
 
+def time_looped(torch, reps: int = 3) -> dict:
+    """The looped column with halting: B4 T2048 d512 H8 d64, 8 passes, window 512, p_halt 0.3."""
+    from vesper.loop import LoopedColumn
+
+    dev = torch.device("cuda:0")
+    b, n, d, h, dk, passes = LOOP_B, LOOP_T, LOOP_D, H, D, LOOP_PASSES
+    column = LoopedColumn.random(d, h, h, dk, WINDOW, passes, seed=11, device=dev)
+    g = torch.Generator().manual_seed(12)
+    x0 = torch.randn(b, n, d, generator=g).to(dev)
+    exits = [(torch.rand(b, n, generator=g) < 0.3).to(dev) for _ in range(passes)]
+    states = [torch.zeros(b, h, dk, dk, device=dev) for _ in range(passes)]
+    column.forward(x0, states, exits)  # warm-up
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    e0.record()
+    for _ in range(reps):
+        out = column.forward(x0, states, exits)
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / reps
+    return {"ms": ms, "tok_s": b * n / (ms / 1e3), "mean_passes": float(out.n_iters.float().mean())}
+
+
 # ---- CPU baseline ---------------------------------------------------------------------------------
 def cpu_baseline(torch) -> dict:
     from oracle.attention import window_attention as oracle_window
@@ -248,6 +273,7 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-decode", action="store_true")
+    ap.add_argument("--no-loop", action="store_true")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -270,6 +296,7 @@ def main() -> int:
     a_bytes, a_flops = attn_bytes(B, T, H, H, D), attn_flops(B, T, H, D, WINDOW)
     attn4_ms = time_attention_config(torch)
     dec = None if args.no_decode else time_decode(torch)
+    looped = None if args.no_loop else time_looped(torch)
 
     scan_dominant = pre["scan_ms"] >= pre["attn_ms"]
     if scan_dominant:
@@ -324,6 +351,14 @@ def main() -> int:
             "tok_s": round(dec["tok_s"], 1), "us_per_step": round(dec["us_per_step"], 3),
             "hbm_frac": round(step_bytes / (dec["us_per_step"] / 1e6) / 1e9 / HBM_PEAK_GBS, 4),
             "algorithmic_bytes_per_step": step_bytes,
+        }
+    if looped is not None:
+        result["looped_column"] = {
+            "workload": "looped column with per-token halting: B4 T2048 d512 H8 d64, 8 passes of delta scan + "
+                        "window attention (w512) with bf16 projections (fixed N(0, 1/512) weights), p_halt 0.3, "
+                        "copy-forward of halted tokens",
+            "tok_s": round(looped["tok_s"], 1), "ms": round(looped["ms"], 3),
+            "mean_active_passes": round(looped["mean_passes"], 3),
         }
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(torch)

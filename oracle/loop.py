@@ -1,0 +1,162 @@
+"""CPU oracle of the looped column with per-token halting (test infrastructure only; see ``oracle/__init__.py``).
+
+Restated from the reference's pass loop and column:
+
+- ``loop_forward`` follows ``Loop.forward`` (``vesper/loop.py:415-453``) with a given exit trace
+  (``TraceRule``, ``vesper/loop.py:203-240``): every pass runs over every token; after a pass the
+  column's outputs at inactive positions are zeroed (``:441-442``); the tokens halting now freeze
+  the projections they wrote (``_merge``, ``:523-537``), which every later pass writes again in
+  their place (copy-forward); a halted token's hidden state is carried forward unchanged
+  (``:452``); the last pass halts every token still active.
+- ``mixer_column_step`` is the column's two mixers as ``Column.step`` orders them
+  (``vesper/column.py:709-812``): recurrent projections, the carry merges of ``k, v, beta``
+  (``:784-789``), the delta scan, the residual; attention projections, the carry merges of the
+  attention keys and values (``:795-796``), window attention, the residual. Norms, the key
+  filter, rotary and the FFN are not part of the mixer path and are left out; queries and keys
+  are L2-normalised (``normalize_keys``) as the scan requires.
+
+Rounding points mirror the GPU path (``vesper/loop.py``): the residual stream stays in the wide
+dtype; every matmul takes bf16-rounded operands and returns a bf16-rounded product; the mixers
+take bf16 inputs and return bf16 outputs; the scan state stays in the wide dtype.
+"""
+
+from __future__ import annotations
+
+from collections.abc import Callable, Sequence
+from dataclasses import dataclass
+
+import torch
+from torch import Tensor
+
+from oracle.attention import window_attention
+from oracle.delta import delta_scan_chunked, normalize_keys
+
+BF16 = torch.bfloat16
+
+
+@dataclass(frozen=True)
+class Written:
+    """What a pass writes per token into its states (``Projections``, ``vesper/column.py:113-137``)."""
+
+    k: Tensor  # [b, n, h, dk]
+    v: Tensor  # [b, n, h, dk]
+    beta: Tensor  # [b, n, h]
+    attn_k: Tensor  # [b, n, hkv, dk]
+    attn_v: Tensor  # [b, n, hkv, dk]
+
+
+# step(x, pass_index, state, carry) -> (out, new_state, written); carry = (active, carried Written)
+ColumnStep = Callable[[Tensor, int, Tensor, "tuple[Tensor, Written] | None"], "tuple[Tensor, Tensor, Written]"]
+
+
+def _where_tokens(mask: Tensor, a: Tensor, b: Tensor) -> Tensor:
+    m = mask.reshape(*mask.shape, *([1] * (a.dim() - mask.dim())))
+    return torch.where(m, a, b)
+
+
+def merge(halts: Tensor, fresh: Written, previous: Written) -> Written:
+    """Tokens halting now freeze their fresh projections; the others keep the previous ones (``loop.py:523-537``)."""
+    return Written(*(_where_tokens(halts, f, p) for f, p in zip(
+        (fresh.k, fresh.v, fresh.beta, fresh.attn_k, fresh.attn_v),
+        (previous.k, previous.v, previous.beta, previous.attn_k, previous.attn_v))))
+
+
+def carry_in(active: Tensor, fresh: Tensor, carried: Tensor) -> Tensor:
+    """``_carry`` (``vesper/column.py:140-143``): fresh where active, the carried value elsewhere."""
+    return _where_tokens(active, fresh, carried)
+
+
+@dataclass(frozen=True)
+class LoopOutput:
+    y: Tensor  # [b, n, d] the hidden state each token halted with
+    states: tuple[Tensor, ...]  # one scan state per pass
+    n_iters: Tensor  # int32 [b, n] passes each token was active in
+    per_pass: tuple[Tensor, ...]  # each pass's column output, zero at inactive positions
+
+
+def loop_forward(x0: Tensor, step: ColumnStep, states: Sequence[Tensor], exits: Sequence[Tensor]) -> LoopOutput:
+    """Run ``len(states)`` passes of one column with exits given per pass (``exits[t]`` bool ``[b, n]``).
+
+    A token that is active at pass ``t`` and has ``exits[t]`` set halts after that pass; the last
+    pass halts every token (``loop.py:443``, ``last=t == runs - 1``).
+    """
+    passes = len(states)
+    if len(exits) < passes:
+        raise ValueError(f"{passes} passes need {passes} exit masks, got {len(exits)}")
+    b, n = x0.shape[0], x0.shape[1]
+    active = torch.ones(b, n, dtype=torch.bool)
+    n_iters = torch.zeros(b, n, dtype=torch.int32)
+    carried: Written | None = None
+    x = x0
+    new_states = list(states)
+    per_pass = []
+    for t in range(passes):
+        carry = None if carried is None else (active, carried)
+        h, new_states[t], written = step(x, t, new_states[t], carry)
+        h = _where_tokens(active, h, torch.zeros_like(h))
+        halts = active & (exits[t] | (t == passes - 1))
+        n_iters = n_iters + active.to(torch.int32)
+        per_pass.append(h)
+        carried = written if carried is None else merge(halts, written, carried)
+        x = _where_tokens(active, h, x)
+        active = active & ~halts
+    return LoopOutput(y=x, states=tuple(new_states), n_iters=n_iters, per_pass=tuple(per_pass))
+
+
+def _bf(t: Tensor) -> Tensor:
+    """Round to bfloat16 and come back to the wide dtype."""
+    return t.to(BF16).to(t.dtype)
+
+
+def _mm(x: Tensor, w: Tensor) -> Tensor:
+    """A bf16 matmul as the GPU path runs it: bf16 operands, a wide product, a bf16 result."""
+    return _bf(_bf(x) @ _bf(w))
+
+
+@dataclass(frozen=True)
+class MixerWeights:
+    """Per-pass projection weights ``[d, out]`` (``x @ w``)."""
+
+    wq: Sequence[Tensor]
+    wk: Sequence[Tensor]
+    wv: Sequence[Tensor]
+    wb: Sequence[Tensor]  # [d, h]: the write-strength logits
+    waq: Sequence[Tensor]
+    wak: Sequence[Tensor]
+    wav: Sequence[Tensor]
+    heads: int
+    kv_heads: int
+    head_dim: int
+    window: int
+
+
+def mixer_column_step(weights: MixerWeights, masked: bool = True) -> ColumnStep:
+    """The config's column: delta scan then window attention, each with its residual (see module doc).
+
+    With ``masked`` the mixers take the active mask (inactive outputs zero, their writes kept);
+    without it they run densely over every token, as the reference's mixers do.
+    """
+    h, hkv, dk, w = weights.heads, weights.kv_heads, weights.head_dim, weights.window
+
+    def step(x: Tensor, t: int, state: Tensor, carry: tuple[Tensor, Written] | None) -> tuple[Tensor, Tensor, Written]:
+        b, n, _ = x.shape
+        active = None if carry is None else carry[0]
+        mask = active if masked else None
+        q = _bf(normalize_keys(_mm(x, weights.wq[t]).view(b, n, h, dk)))
+        k = _bf(normalize_keys(_mm(x, weights.wk[t]).view(b, n, h, dk)))
+        v = _mm(x, weights.wv[t]).view(b, n, h, dk)
+        beta = _bf(torch.sigmoid(_mm(x, weights.wb[t])))
+        if carry is not None:
+            k, v, beta = (carry_in(active, f, c) for f, c in zip((k, v, beta), (carry[1].k, carry[1].v, carry[1].beta)))
+        r, new_state = delta_scan_chunked(q, k, v, beta, state, 64, active=mask)
+        x1 = x + _bf(r).reshape(b, n, h * dk)
+        aq = _mm(x1, weights.waq[t]).view(b, n, h, dk)
+        ak = _mm(x1, weights.wak[t]).view(b, n, hkv, dk)
+        av = _mm(x1, weights.wav[t]).view(b, n, hkv, dk)
+        if carry is not None:
+            ak, av = (carry_in(active, f, c) for f, c in zip((ak, av), (carry[1].attn_k, carry[1].attn_v)))
+        a = window_attention(aq, ak, av, w, active=mask)
+        x2 = x1 + _bf(a).reshape(b, n, h * dk)
+        return x2, new_state, Written(k=k, v=v, beta=beta, attn_k=ak, attn_v=av)
+
+    return step

@@ -1,0 +1,109 @@
+"""The looped column with halting (``vesper.loop``) on the GPU against the loop oracle.
+
+Parity: relative Frobenius error of the halted hidden states and of every pass's scan state below
+3e-2 (the reference's attention bound; eight bf16 mixer passes compound their roundings), the
+per-token pass counts exact. At the full config size: exact size-independent properties
+(determinism, pass counts from the exit trace, early-halting tokens bitwise equal to a one-pass
+run) and an fp32-oracle parity check over two passes.
+"""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+from conftest import needs_gpu
+from oracle import loop as ol
+from oracle.delta import relative_error
+
+pytestmark = [pytest.mark.gpu, needs_gpu]
+
+GPU = torch.device("cuda")
+
+
+def _setup(b, n, d, h, hkv, dk, w, passes, seed, p_halt=0.3):
+    from vesper.loop import LoopedColumn
+
+    column = LoopedColumn.random(d, h, hkv, dk, w, passes, seed, GPU)
+    g = torch.Generator().manual_seed(seed + 1)
+    x0 = torch.randn(b, n, d, generator=g)
+    exits = [torch.rand(b, n, generator=g) < p_halt for _ in range(passes)]
+    states = [0.02 * torch.randn(b, h, dk, dk, generator=g) for _ in range(passes)]
+    return column, x0, exits, states
+
+
+def _oracle(column, x0, exits, states, dtype=torch.float64):
+    ws = {name: [t.to("cpu", dtype) for t in column.w[name]] for name in column.w}
+    weights = ol.MixerWeights(**ws, heads=column.heads, kv_heads=column.kv_heads, head_dim=column.head_dim,
+                              window=column.window)
+    return ol.loop_forward(x0.to(dtype), ol.mixer_column_step(weights), [s.to(dtype) for s in states], exits)
+
+
+def _expected_iters(exits, passes):
+    b, n = exits[0].shape
+    iters = torch.full((b, n), passes, dtype=torch.int32)
+    done = torch.zeros(b, n, dtype=torch.bool)
+    for t in range(passes - 1):
+        now = exits[t] & ~done
+        iters[now] = t + 1
+        done |= now
+    return iters
+
+
+def test_small_loop_matches_the_oracle():
+    b, n, d, h, hkv, dk, w, passes = 2, 200, 128, 2, 2, 64, 64, 4
+    column, x0, exits, states = _setup(b, n, d, h, hkv, dk, w, passes, seed=5)
+    got = column.forward(x0.to(GPU), [s.to(GPU) for s in states], [e.to(GPU) for e in exits])
+    want = _oracle(column, x0, exits, states)
+    assert torch.equal(got.n_iters.cpu(), want.n_iters)
+    assert torch.equal(got.n_iters.cpu(), _expected_iters(exits, passes))
+    assert relative_error(got.y, want.y) < 3e-2
+    for t in range(passes):
+        assert relative_error(got.states[t], want.states[t]) < 3e-2, t
+
+
+def test_config_b4_t2048_d512_h8_eight_passes_properties():
+    from vesper.loop import LoopedColumn
+
+    b, n, d, h, dk, w, passes = 4, 2048, 512, 8, 64, 512, 8
+    column, x0, exits, states = _setup(b, n, d, h, h, dk, w, passes, seed=7)
+    dx0, dst, dex = x0.to(GPU), [s.to(GPU) for s in states], [e.to(GPU) for e in exits]
+    first = column.forward(dx0, dst, dex)
+    second = column.forward(dx0, dst, dex)
+    assert torch.equal(first.y, second.y)
+    assert all(torch.equal(a, c) for a, c in zip(first.states, second.states))
+    assert bool(torch.isfinite(first.y).all())
+    assert torch.equal(first.n_iters.cpu(), _expected_iters(exits, passes))
+    # a token that halts after the first pass keeps its pass-1 hidden state: that of a one-pass run
+    one = LoopedColumn({name: column.w[name][:1] for name in column.w}, h, h, dk, w)
+    single = one.forward(dx0, dst[:1], dex[:1])
+    early = (first.n_iters == 1)
+    assert int(early.sum()) > 0
+    assert torch.equal(first.y[early], single.y[early])
+    assert torch.equal(first.states[0], single.states[0])
+
+
+def test_config_size_two_passes_match_the_fp32_oracle():
+    b, n, d, h, dk, w, passes = 4, 2048, 512, 8, 64, 512, 2
+    column, x0, exits, states = _setup(b, n, d, h, h, dk, w, passes, seed=9)
+    got = column.forward(x0.to(GPU), [s.to(GPU) for s in states], [e.to(GPU) for e in exits])
+    want = _oracle(column, x0, exits, states, dtype=torch.float32)
+    assert relative_error(got.y, want.y) < 3e-2
+    for t in range(passes):
+        assert relative_error(got.states[t], want.states[t]) < 3e-2, t
+
+
+def test_refusals():
+    from vesper.contracts import ContractError
+    from vesper.loop import LoopedColumn
+
+    column = LoopedColumn.random(64, 1, 1, 64, 16, 2, 0, GPU)
+    x0 = torch.zeros(1, 8, 64, device=GPU)
+    states = [torch.zeros(1, 1, 64, 64, device=GPU)] * 2
+    exits = [torch.zeros(1, 8, dtype=torch.bool, device=GPU)] * 2
+    with pytest.raises(ContractError, match="dtype"):
+        column.forward(x0.half(), states, exits)
+    with pytest.raises(ContractError, match="passes"):
+        column.forward(x0, states[:1], exits)
+    with pytest.raises(ContractError, match="axis"):
+        column.forward(x0, states, [torch.zeros(1, 9, dtype=torch.bool, device=GPU)] * 2)

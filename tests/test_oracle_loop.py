@@ -1,0 +1,131 @@
+"""The loop oracle (``oracle.loop``) against the reference's hand-computed copy-forward table.
+
+The scalar column is the one of the reference's pass-state review, section B
+(``tests/test_loop.py:38-79``): one head of width one, unit key and query, value = the input,
+beta 1/2, output = the state read; no attention and no residual, so the rational answers of
+``tests/test_loop.py:126-175`` apply exactly.
+"""
+
+from __future__ import annotations
+
+from fractions import Fraction
+
+import pytest
+import torch
+
+from oracle import loop as ol
+from oracle.delta import delta_scan_chunked
+
+F64 = torch.float64
+
+
+def scalar_step(x, t, state, carry):
+    del t
+    b, n = x.shape[0], x.shape[1]
+    ones = torch.ones(b, n, 1, 1, dtype=x.dtype)
+    k, v = ones, x.reshape(b, n, 1, 1)
+    beta = torch.full((b, n, 1), 0.5, dtype=x.dtype)
+    if carry is not None:
+        active, carried = carry
+        k = ol.carry_in(active, k, carried.k)
+        v = ol.carry_in(active, v, carried.v)
+        beta = ol.carry_in(active, beta, carried.beta)
+    o, new = delta_scan_chunked(ones, k, v, beta, state, 1)
+    empty = torch.zeros(b, n, 1, 1, dtype=x.dtype)
+    return o.reshape(b, n, 1), new, ol.Written(k=k, v=v, beta=beta, attn_k=empty, attn_v=empty)
+
+
+def scalar_states(values):
+    return [torch.full((1, 1, 1, 1), v, dtype=F64) for v in values]
+
+
+def section_b():
+    x0 = torch.tensor([[[2.0], [4.0]]], dtype=F64)
+    exits = [torch.tensor([[True, False]]), torch.tensor([[False, False]])]
+    return ol.loop_forward(x0, scalar_step, scalar_states([0.0, 10.0]), exits)
+
+
+def test_section_b_copy_forward_table():
+    # pass 1: 0 -> 1 -> 5/2; token 1 halts with output 1. Pass 2 writes token 1's saved
+    # (k, v, beta) = (1, 2, 1/2) first: 10/2 + 2/2 = 6, then token 2 with its pass-1 output 5/2:
+    # 6/2 + (5/2)/2 = 17/4, also its pass-2 output (tests/test_loop.py:126-138)
+    out = section_b()
+    assert out.states[0].item() == Fraction(5, 2)
+    assert out.states[1].item() == Fraction(17, 4)
+    assert out.y[0, 0, 0].item() == 1.0
+    assert out.y[0, 1, 0].item() == Fraction(17, 4)
+    assert out.n_iters.tolist() == [[1, 2]]
+    assert out.per_pass[1][0, 0, 0].item() == 0.0  # token 1 produced nothing at pass 2
+
+
+def test_the_inactive_token_still_writes():
+    # tests/test_loop.py:141-150: one token, halting after pass 1: pass 2's state is 10/2 + 2/2
+    x0 = torch.tensor([[[2.0]]], dtype=F64)
+    out = ol.loop_forward(x0, scalar_step, scalar_states([0.0, 10.0]), [torch.tensor([[True]])] * 2)
+    assert out.states[0].item() == 1.0
+    assert out.states[1].item() == 6.0
+
+
+def test_all_tokens_halted_passes_still_update_every_later_state():
+    # tests/test_loop.py:162-175: both tokens halt after pass 1 of three
+    x0 = torch.tensor([[[2.0], [4.0]]], dtype=F64)
+    out = ol.loop_forward(x0, scalar_step, scalar_states([0.0, 10.0, 20.0]), [torch.tensor([[True, True]])] * 3)
+    assert out.n_iters.tolist() == [[1, 1]]
+    assert out.states[1].item() == 5.0  # 10 -> 6 -> 5
+    assert out.states[2].item() == 7.5  # 20 -> 11 -> 7.5
+    assert all(bool((p == 0).all()) for p in out.per_pass[1:])
+
+
+@pytest.mark.parametrize("kind", ["no_carry", "no_write"])
+def test_the_table_catches_planted_mistakes(kind, monkeypatch):
+    if kind == "no_carry":  # halted tokens write their fresh projections instead of the frozen ones
+        monkeypatch.setattr(ol, "carry_in", lambda active, fresh, carried: fresh)
+    else:  # halted tokens stop writing (zero projections, so beta = 0)
+        real = ol.carry_in
+        monkeypatch.setattr(ol, "carry_in", lambda active, fresh, carried: real(active, fresh, torch.zeros_like(carried)))
+    x0 = torch.tensor([[[2.0], [4.0]]], dtype=F64)
+    exits = [torch.tensor([[True, False]]), torch.tensor([[False, False]]), torch.tensor([[False, False]])]
+    out = ol.loop_forward(x0, scalar_step, scalar_states([0.0, 10.0, 20.0]), exits)
+    # the correct third state: 20 -> (20 + 2)/2 = 11 -> (11 + 17/4)/2 = 61/8
+    assert [out.states[1].item(), out.states[2].item()] != [Fraction(17, 4), Fraction(61, 8)]
+
+
+def test_three_pass_table_without_mistakes():
+    x0 = torch.tensor([[[2.0], [4.0]]], dtype=F64)
+    exits = [torch.tensor([[True, False]]), torch.tensor([[False, False]]), torch.tensor([[False, False]])]
+    out = ol.loop_forward(x0, scalar_step, scalar_states([0.0, 10.0, 20.0]), exits)
+    assert [out.states[1].item(), out.states[2].item()] == [Fraction(17, 4), Fraction(61, 8)]
+    assert out.y[0, 1, 0].item() == Fraction(61, 8) and out.n_iters.tolist() == [[1, 3]]
+
+
+def _mixer_weights(d, h, hkv, dk, w, passes, seed):
+    g = torch.Generator().manual_seed(seed)
+
+    def mats(out):
+        return [(torch.randn(d, out, generator=g) / d**0.5).to(torch.bfloat16).double() for _ in range(passes)]
+
+    return ol.MixerWeights(wq=mats(h * dk), wk=mats(h * dk), wv=mats(h * dk), wb=mats(h), waq=mats(h * dk),
+                           wak=mats(hkv * dk), wav=mats(hkv * dk), heads=h, kv_heads=hkv, head_dim=dk, window=w)
+
+
+def test_masked_mixers_equal_dense_mixers_for_every_active_token():
+    # the kernels skip inactive tokens' reads and outputs (loop.py:24-26): running the mixers with
+    # the active mask gives, bit for bit, what the reference's dense mixers give once the loop
+    # has zeroed the inactive outputs and merged the carried projections
+    d, h, dk, passes = 16, 2, 8, 3
+    weights = _mixer_weights(d, h, h, dk, 6, passes, seed=3)
+    g = torch.Generator().manual_seed(4)
+    x0 = torch.randn(2, 19, d, generator=g, dtype=F64)
+    exits = [torch.rand(2, 19, generator=g) < 0.3 for _ in range(passes)]
+    states = [0.1 * torch.randn(2, h, dk, dk, generator=g, dtype=F64) for _ in range(passes)]
+    masked = ol.loop_forward(x0, ol.mixer_column_step(weights), states, exits)
+    dense = ol.loop_forward(x0, ol.mixer_column_step(weights, masked=False), states, exits)
+    assert torch.equal(masked.y, dense.y)
+    assert all(torch.equal(a, b) for a, b in zip(masked.states, dense.states))
+    assert torch.equal(masked.n_iters, dense.n_iters)
+    assert int((masked.n_iters < passes).sum()) > 0  # some tokens did halt early
+    # halted tokens carry forward the hidden state of their halting pass
+    halt_pass = masked.n_iters - 1
+    for t in range(passes):
+        sel = halt_pass == t
+        assert torch.equal(masked.y[sel], masked.per_pass[t][sel])

@@ -1,0 +1,171 @@
+"""The looped column with per-token halting, on MI355X: the caller of the mixers with an active mask.
+
+This is the pass loop of the reference's ``Loop.forward`` (``vesper/loop.py:415-453``) driven by
+a given exit trace (``TraceRule``, ``:203-240``), over a column reduced to its two mixers in the
+order of ``Column.step`` (``vesper/column.py:709-812``):
+
+- recurrent sublayer: projections ``q, k, v, beta`` of the pass input (bf16 matmuls; queries and
+  keys L2-normalised, ``beta = sigmoid``), the carry merges of ``k, v, beta`` for halted tokens
+  (``column.py:784-789``), the delta scan (``vsp_delta_scan_bf16`` with the active mask), the
+  residual;
+- attention sublayer: projections, the carry merges of the attention keys and values
+  (``column.py:795-796``), window attention over the chunk (``vsp_window_attn_bf16`` with the
+  active mask), the residual.
+
+The loop zeroes inactive outputs, freezes the projections of tokens as they halt and writes them
+into every later pass's state (copy-forward), and carries halted tokens' hidden states forward
+unchanged (``loop.py:441-453``, ``:523-537``). All passes run even when no token is active any
+more. Norms, the key filter, rotary embeddings and the FFN are not part of the mixer path and
+are left out. The residual stream stays in float32 (autocast's convention); matmuls and mixers run
+in bfloat16 with the scan state in float32. Forward only.
+"""
+
+from __future__ import annotations
+
+from collections.abc import Sequence
+from dataclasses import dataclass
+
+import torch
+from torch import Tensor
+
+from vesper.contracts import ContractError, Dims, check_shape
+from vesper.kernels.delta_scan import delta_scan_fused
+from vesper.kernels.window_attn import window_attention
+
+BF16 = torch.bfloat16
+KEY_NORM_FLOOR = 1e-6  # vesper/recurrence.py:31
+
+
+def _normalize(x: Tensor) -> Tensor:
+    """``normalize_keys`` (``vesper/recurrence.py:91-115``) in float32: divide by the row's peak
+    magnitude (floored at 1e-6), then by the norm of the scaled row floored at one."""
+    x = x.float()
+    peak = x.abs().amax(dim=-1, keepdim=True).clamp_min(KEY_NORM_FLOOR)
+    unit = x / peak
+    return unit / (unit * unit).sum(dim=-1, keepdim=True).clamp_min(1.0).sqrt()
+
+
+def _where_tokens(mask: Tensor, a: Tensor, b: Tensor) -> Tensor:
+    return torch.where(mask.reshape(*mask.shape, *([1] * (a.dim() - mask.dim()))), a, b)
+
+
+@dataclass(frozen=True)
+class Written:
+    """What a pass writes per token into its states (the mixer part of ``Projections``)."""
+
+    k: Tensor
+    v: Tensor
+    beta: Tensor
+    attn_k: Tensor
+    attn_v: Tensor
+
+    def merged(self, halts: Tensor, previous: Written) -> Written:
+        """Tokens halting now freeze these projections; the others keep ``previous`` (``loop.py:523-537``)."""
+        return Written(*(_where_tokens(halts, a, b) for a, b in zip(
+            (self.k, self.v, self.beta, self.attn_k, self.attn_v),
+            (previous.k, previous.v, previous.beta, previous.attn_k, previous.attn_v))))
+
+
+@dataclass(frozen=True)
+class LoopResult:
+    y: Tensor  # [b, n, d] float32: the hidden state each token halted with
+    states: tuple[Tensor, ...]  # the scan state of every pass, [b, h, dk, dk] float32
+    n_iters: Tensor  # int32 [b, n]: passes each token was active in
+
+
+class LoopedColumn:
+    """One column's mixers run for ``passes`` passes with per-pass projection weights.
+
+    Weights are ``[d, out]`` bfloat16 tensors per pass (``x @ w``): ``wq, wk, wv [d, h*dk]``,
+    ``wb [d, h]``, ``waq [d, h*dk]``, ``wak, wav [d, hkv*dk]``.
+    """
+
+    def __init__(self, weights: dict[str, Sequence[Tensor]], heads: int, kv_heads: int, head_dim: int,
+                 window: int) -> None:
+        names = ("wq", "wk", "wv", "wb", "waq", "wak", "wav")
+        missing = [n for n in names if n not in weights]
+        if missing:
+            raise ValueError(f"missing weights: {missing}")
+        self.passes = len(weights["wq"])
+        if any(len(weights[n]) != self.passes for n in names):
+            raise ValueError("every weight needs one tensor per pass")
+        self.w = {n: list(weights[n]) for n in names}
+        self.heads, self.kv_heads, self.head_dim, self.window = heads, kv_heads, head_dim, window
+
+    @classmethod
+    def random(cls, d: int, heads: int, kv_heads: int, head_dim: int, window: int, passes: int, seed: int,
+               device: torch.device) -> LoopedColumn:
+        """Fixed random weights ~ N(0, 1/d) from a CPU generator (the same values on any device)."""
+        g = torch.Generator().manual_seed(seed)
+        shapes = {"wq": heads * head_dim, "wk": heads * head_dim, "wv": heads * head_dim, "wb": heads,
+                  "waq": heads * head_dim, "wak": kv_heads * head_dim, "wav": kv_heads * head_dim}
+        weights: dict[str, list[Tensor]] = {n: [] for n in shapes}
+        for _ in range(passes):
+            for name, out in shapes.items():
+                weights[name].append((torch.randn(d, out, generator=g) / d**0.5).to(device, BF16))
+        return cls(weights, heads, kv_heads, head_dim, window)
+
+    def _step(self, x: Tensor, t: int, state: Tensor, active: Tensor | None,
+              carried: Written | None) -> tuple[Tensor, Tensor, Written]:
+        b, n, d = x.shape
+        h, hkv, dk = self.heads, self.kv_heads, self.head_dim
+        xb = x.to(BF16)
+        q = _normalize((xb @ self.w["wq"][t]).view(b, n, h, dk)).to(BF16)
+        k = _normalize((xb @ self.w["wk"][t]).view(b, n, h, dk)).to(BF16)
+        v = (xb @ self.w["wv"][t]).view(b, n, h, dk)
+        beta = torch.sigmoid((xb @ self.w["wb"][t]).float()).to(BF16)
+        if carried is not None and active is not None:
+            k = _where_tokens(active, k, carried.k)
+            v = _where_tokens(active, v, carried.v)
+            beta = _where_tokens(active, beta, carried.beta)
+        r, new_state = delta_scan_fused(q, k, v, beta, state, active=active)
+        x1 = x + r.reshape(b, n, h * dk).float()
+        x1b = x1.to(BF16)
+        aq = (x1b @ self.w["waq"][t]).view(b, n, h, dk)
+        ak = (x1b @ self.w["wak"][t]).view(b, n, hkv, dk)
+        av = (x1b @ self.w["wav"][t]).view(b, n, hkv, dk)
+        if carried is not None and active is not None:
+            ak = _where_tokens(active, ak, carried.attn_k)
+            av = _where_tokens(active, av, carried.attn_v)
+        a = window_attention(aq, ak, av, self.window, active=active)
+        x2 = x1 + a.reshape(b, n, h * dk).float()
+        return x2, new_state, Written(k=k, v=v, beta=beta, attn_k=ak, attn_v=av)
+
+    def forward(self, x0: Tensor, states: Sequence[Tensor], exits: Sequence[Tensor]) -> LoopResult:
+        """All passes over ``x0 [b, n, d]`` (float32, on the GPU).
+
+        Args:
+            x0: the chunk's input hidden states.
+            states: one float32 scan state ``[b, h, dk, dk]`` per pass.
+            exits: per pass a bool ``[b, n]``: an active token with its exit set halts after the
+                pass; the last pass halts every token still active.
+
+        Raises:
+            ContractError: on shapes or dtypes outside that contract.
+        """
+        dims: Dims = {"d": self.heads * self.head_dim, "h": self.heads, "dk": self.head_dim}
+        check_shape("x0", x0, ("b", "n", "d"), dims, torch.float32)
+        if len(states) != self.passes or len(exits) < self.passes:
+            raise ContractError(f"{self.passes} passes need {self.passes} states and exit masks")
+        for t in range(self.passes):
+            check_shape(f"states[{t}]", states[t], ("b", "h", "dk", "dk"), dims, torch.float32)
+            check_shape(f"exits[{t}]", exits[t], ("b", "n"), dims, torch.bool)
+        b, n = dims["b"], dims["n"]
+        with torch.no_grad():
+            active = torch.ones(b, n, dtype=torch.bool, device=x0.device)
+            n_iters = torch.zeros(b, n, dtype=torch.int32, device=x0.device)
+            carried: Written | None = None
+            x = x0
+            new_states = list(states)
+            for t in range(self.passes):
+                # pass 0 runs with every token active: the unmasked kernels, as the reference's
+                # carry-free first pass
+                mask = None if carried is None else active
+                h, new_states[t], written = self._step(x, t, new_states[t], mask, carried)
+                h = _where_tokens(active, h, torch.zeros_like(h))
+                halts = active & exits[t] if t < self.passes - 1 else active
+                n_iters += active.to(torch.int32)
+                carried = written if carried is None else written.merged(halts, carried)
+                x = _where_tokens(active, h, x)
+                active = active & ~halts
+        return LoopResult(y=x, states=tuple(new_states), n_iters=n_iters)
