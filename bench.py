@@ -37,6 +37,7 @@ B, T, H, D, WINDOW = 8, 4096, 8, 64, 512
 ATTN_B = 4
 DEC_B, DEC_W, DEC_STEPS = 64, 512, 256
 LOOP_B, LOOP_T, LOOP_D, LOOP_PASSES = 4, 2048, 512, 8
+COPY_BYTES = 256 << 20  # the calibration copy of --traffic-probe
 
 
 def log(*a: object) -> None:
@@ -255,6 +256,42 @@ def cpu_baseline(torch) -> dict:
                       f"same inputs (B={sb}, T={T}, H={H}, d={D}, w={WINDOW}), median of 5 after 1 warm-up, {model}"}
 
 
+def traffic_probe(torch) -> None:
+    """One launch of each bench kernel plus a plain copy of known size, for `rocprofv3 --pmc` runs.
+
+    The copy (torch's `copy_` of COPY_BYTES) reads and writes exactly COPY_BYTES: the ratio of that
+    to what FETCH_SIZE / WRITE_SIZE report for it scales the counters of the other kernels.
+    """
+    from vesper.kernels.delta_scan import delta_scan_fused, delta_scan_step_fused
+    from vesper.kernels.ring_attn import RingKVCache, ring_attention
+    from vesper.kernels.window_attn import window_attention
+
+    dev = torch.device("cuda:0")
+    src = torch.ones(COPY_BYTES // 4, dtype=torch.float32, device=dev)
+    dst = torch.empty_like(src)
+    q, k, v, beta, s0 = scan_inputs(torch, dev)
+    aq, ak, av = attn_inputs(torch, dev)  # the prefill step's shape, B8
+    g = torch.Generator().manual_seed(3)
+    b, h, d, w = DEC_B, H, D, DEC_W
+    state = (0.02 * torch.randn(b, h, d, d, generator=g)).to(dev)
+    ring = RingKVCache(torch.randn(b, w, h, d, generator=g).to(dev, torch.bfloat16),
+                       torch.randn(b, w, h, d, generator=g).to(dev, torch.bfloat16),
+                       torch.arange(w).expand(b, w).contiguous().to(dev),
+                       torch.ones(b, w, dtype=torch.bool, device=dev), w)
+    dq = torch.randn(b, h, d, generator=g).to(dev)
+    dbeta = torch.rand(b, h, generator=g).to(dev)
+    rq = torch.randn(b, 1, h, d, generator=g).to(dev, torch.bfloat16)
+    pos = torch.full((b, 1), w, device=dev)
+    with torch.no_grad():
+        dst.copy_(src)
+        delta_scan_fused(q, k, v, beta, s0)
+        window_attention(aq, ak, av, WINDOW)
+        delta_scan_step_fused(dq, dq, dq, dbeta, state, out_state=state)
+        ring_attention(rq, rq, rq, pos, ring, inplace=True, check_positions=False)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_bytes": COPY_BYTES}), flush=True)
+
+
 def traffic_from_profiles(kernel: str) -> float | None:
     path = ROOT / "profiles" / "hbm_traffic.json"
     if not path.exists():
@@ -274,6 +311,8 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-decode", action="store_true")
     ap.add_argument("--no-loop", action="store_true")
+    ap.add_argument("--traffic-probe", action="store_true",
+                    help="launch each kernel once plus a calibration copy, for rocprofv3 --pmc runs")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -289,6 +328,9 @@ def main() -> int:
     from vesper.kernels import _lib
 
     _lib.library()  # fail loudly if the kernels are not built
+    if args.traffic_probe:
+        traffic_probe(torch)
+        return 0
 
     pre = time_prefill(torch, args.steps, args.warmup)
     tok_s = B * T / (pre["step_ms"] / 1e3)

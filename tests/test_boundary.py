@@ -83,3 +83,18 @@ def test_the_product_path_does_not_import_the_oracle():
     )
     out = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, check=True)
     assert out.stdout.strip() == "False"
+
+
+def test_the_scan_switch_refuses_what_it_cannot_run():
+    # the reference's names and refusals (vesper/column.py:382-405); "reference" is not shipped
+    from vesper.column import SCAN_IMPLS, check_capturable_scan, check_scan
+
+    assert SCAN_IMPLS == ("reference", "fused", "fused-fp32")
+    with pytest.raises(ValueError, match="does not ship"):
+        check_scan("reference", torch.device("cpu"))
+    with pytest.raises(ValueError, match="must be one of"):
+        check_scan("triton", torch.device("cpu"))
+    with pytest.raises(ValueError, match="needs the model on CUDA"):
+        check_scan("fused", torch.device("cpu"))
+    with pytest.raises(ValueError, match="needs the model on CUDA"):
+        check_capturable_scan("fused-fp32", torch.device("cpu"))

@@ -1,0 +1,87 @@
+"""The column's scan switch, for the HIP scans: which delta-rule kernel a recurrent sublayer runs.
+
+Mirrors the reference's backend selection (``vesper/column.py:47-53``, ``:291-326``,
+``:382-426``) with the same names and the same refusals, so a driver written against the
+reference keeps its checks:
+
+- ``ScanImpl`` / ``SCAN_IMPLS`` / ``FUSED_INPUT_DTYPES``: "fused" runs ``delta_scan_fused``
+  (bfloat16 inputs, float32 state), "fused-fp32" runs ``delta_scan_fused_fp32`` (float32
+  throughout). "reference" names the reference's pure-PyTorch scan (``vesper/recurrence.py``),
+  which this build does not ship: asking for it is refused with a message saying so.
+- ``check_scan`` / ``check_capturable_scan``: the device checks of a choice, before any step.
+- ``recurrent_scan``: the kernel part of ``RecurrentSublayer.scan`` (``column.py:308-315``):
+  cast ``q, k, v, beta`` to the choice's input dtype and the state to float32 with autocast off,
+  run the kernel, return the reads in the projections' dtype and the new float32 state. The
+  output projection ``W_o`` stays with the caller.
+"""
+
+from __future__ import annotations
+
+from typing import Literal
+
+import torch
+from torch import Tensor
+
+from vesper.kernels.delta_scan import (
+    FP32_INPUT_DTYPE,
+    INPUT_DTYPE,
+    STATE_DTYPE,
+    delta_scan_fused,
+    delta_scan_fused_fp32,
+    fused_scan_available,
+)
+
+ScanImpl = Literal["reference", "fused", "fused-fp32"]
+SCAN_IMPLS: tuple[ScanImpl, ...] = ("reference", "fused", "fused-fp32")
+# what each HIP scan takes its q, k, v, beta in
+FUSED_INPUT_DTYPES: dict[ScanImpl, torch.dtype] = {
+    "fused": INPUT_DTYPE,
+    "fused-fp32": FP32_INPUT_DTYPE,
+}
+
+
+def check_scan(impl: str, device: torch.device) -> ScanImpl:
+    """The one check of a scan choice against the device it would run on; returns it typed.
+
+    Raises:
+        ValueError: if ``impl`` is not one of ``SCAN_IMPLS``; for "reference" (not shipped by this
+            build); for a HIP scan off the GPU or without the built kernel library.
+    """
+    if impl == "reference":
+        raise ValueError(
+            "the reference scan is the pure-PyTorch path of vesper/recurrence.py, which this build does "
+            "not ship; use fused or fused-fp32"
+        )
+    if impl not in FUSED_INPUT_DTYPES:
+        raise ValueError(f"scan must be one of {SCAN_IMPLS}, got {impl!r}")
+    if device.type != "cuda":
+        raise ValueError(f"the fused scan needs the model on CUDA, got {device}")
+    if not fused_scan_available():
+        raise ValueError("the fused scan needs a HIP device and the built kernel library (libvesper_kernels.so)")
+    return "fused" if impl == "fused" else "fused-fp32"
+
+
+def check_capturable_scan(impl: str, device: torch.device) -> ScanImpl:
+    """``check_scan``: both HIP scans run inside a captured HIP graph (no allocation in the library,
+    no host synchronisation), so every choice that passes it can be captured."""
+    return check_scan(impl, device)
+
+
+def recurrent_scan(impl: str, q: Tensor, k: Tensor, v: Tensor, beta: Tensor, state: Tensor, *,
+                   active: Tensor | None = None) -> tuple[Tensor, Tensor]:
+    """The scan of ``RecurrentSublayer.scan`` without its output projection: ``(o, state')``.
+
+    ``q, k, v [b, n, h, dk]`` and ``beta [b, n, h]`` in the projections' dtype; ``state
+    [b, h, dk, dk]`` in any float dtype. Returns ``o`` in ``q``'s dtype and the state in float32.
+
+    Raises:
+        ValueError: as ``check_scan``.
+        ContractError: from the kernel's contract check.
+    """
+    chosen = check_scan(impl, q.device)
+    kernel = delta_scan_fused if chosen == "fused" else delta_scan_fused_fp32
+    dtype = FUSED_INPUT_DTYPES[chosen]
+    with torch.autocast(device_type=q.device.type, enabled=False):
+        o, new_state = kernel(q.to(dtype), k.to(dtype), v.to(dtype), beta.to(dtype), state.to(STATE_DTYPE),
+                              active=active)
+    return o.to(q.dtype), new_state
