@@ -714,16 +714,18 @@ __global__ __launch_bounds__(64 * (ChainShape<E, DK>::NH + 1)) void delta_chain_
   }
 }
 // --------------------------------------------------------------------------------------------
-// the bf16 chunk chain (head widths 32, 64, 128): as delta_chain_kernel, with the helper work
-// spread so that no helper's share of an iteration outlasts the chain step:
+// the bf16 chunk chain (head widths 32 and 64): as delta_chain_kernel, with its work arranged so
+// that the chain's step, not the helpers or the LDS, sets the pace:
 //  * transposed operands (K^T for the state update, the V slice in the accumulator layout) come
-//    from row-major LDS tiles through ds_read_b64_tr_b16, so staging a chunk is plain LDS stores;
-//  * the output of a chunk, O = Q H + tril(Q K^T) Delta, is computed by two idle helpers in the
-//    next iteration, each taking two of the four 16-token row blocks and forming its own causal
-//    Q K^T tiles from the K and Q tiles still in LDS (K and Q are triple-buffered for that).
-// Per iteration it: the chain runs chunk it; helper (it + 1) % 7 stages chunk it + 1; helpers
-// (it - 1) % 7 and (it + 2) % 7 write the outputs of chunk it - 1; helper it % 7 issues the
-// global loads of chunk it + 7 into its registers (six iterations of latency cover).
+//    from row-major LDS tiles through ds_read_b64_tr_b16, so staging a chunk needs no MFMA;
+//  * the chain issues all of its step's LDS reads in one batch before its first product;
+//  * the helper that stages chunk c keeps Q_c and the causal tiles P^T = tril(Q K^T)^T (formed from
+//    its registers while staging) in registers of their own, issues the loads of chunk c + 7 in the
+//    next iteration (six iterations of latency cover), and writes the output of chunk c one
+//    iteration after the chain ran it, reading only H^T and Delta^T from LDS, once for all four
+//    row blocks.
+// Per iteration it: the chain runs chunk it; helper (it + 1) % 7 stages chunk it + 1; helper
+// it % 7 loads chunk it + 7; helper (it - 1) % 7 writes the outputs of chunk it - 1.
 // --------------------------------------------------------------------------------------------
 __device__ __forceinline__ f32x4 mfma_bf16(const bf16x8& a, const bf16x8& b, f32x4 acc) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, acc, 0, 0, 0);
@@ -740,7 +742,7 @@ __global__ __launch_bounds__(512) void delta_chain_bf16_kernel(const TIn* __rest
   constexpr int NH = 7;                          // helper waves
   constexpr int BV = 16;                         // value columns per chain
   constexpr int NS = DK / BV;                    // value slices per head
-  constexpr int PK = DK + 8;                     // pitch of K and Q rows (elements)
+  constexpr int PK = DK + 8;                     // pitch of K rows and of H^T rows (elements)
   constexpr int PT = 64 + 8;                     // pitch of T rows and of Delta^T rows
   constexpr int PV = BV + 8;                     // pitch of V slice rows
   constexpr int HB = DK / 16;                    // 16-row tiles of the state slice
@@ -750,13 +752,11 @@ __global__ __launch_bounds__(512) void delta_chain_bf16_kernel(const TIn* __rest
   using AB = typename Acc<E>::B;
   using NR = typename N::R;
 
-  __shared__ __align__(16) E sK[3][64 * PK];
-  __shared__ __align__(16) E sQ[3][64 * PK];
+  __shared__ __align__(16) E sK[2][64 * PK];
   __shared__ __align__(16) E sT[2][64 * PT];
   __shared__ __align__(16) E sV[2][64 * PV];
   __shared__ __align__(16) E sHo[2][BV * PK];  // H^T of the slice: row = value column, column = dk
   __shared__ __align__(16) E sDo[2][BV * PT];  // Delta^T: row = value column, column = token
-  __shared__ uint8_t sAct[3][64];
 
   const int lg = xcd_logical_block(blockIdx.x, gridDim.x);
   const int slice = lg % NS, bh = lg / NS;
@@ -768,12 +768,112 @@ __global__ __launch_bounds__(512) void delta_chain_bf16_kernel(const TIn* __rest
   const int rstride = H * DK;
   const size_t bh_base = ((size_t)b * T * H + h) * DK;
 
-  // ---- helper state: one chunk's loads in flight ----
+  // the Acc-layout A fragment of a row-major LDS row: k = 4 g + r and 16 + 4 g + r
+  auto acc_frag = [&](const E* arow) {
+    const bf16x4 lo = *reinterpret_cast<const bf16x4*>(arow + 4 * g);
+    const bf16x4 hi = *reinterpret_cast<const bf16x4*>(arow + 16 + 4 * g);
+    return bf16x8(__builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+  };
+
+  // the upper tiles of T are never staged (the compact factor holds the ten lower ones): zero once
+  for (int i = threadIdx.x; i < 2 * 64 * PT; i += 512) (&sT[0][0])[i] = (__bf16)0.f;
+  __syncthreads();
+
+  // The chain and the helpers run separate loops with the same barrier sequence, so neither keeps
+  // the other's registers live.
+  if (wave == 0) {
+    f32x4 hreg[HB];
+#pragma unroll
+    for (int m = 0; m < HB; ++m)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) hreg[m][r] = s_in[((size_t)bh * DK + 16 * m + 4 * g + r) * DK + v0 + lq];
+    for (int it = -1; it <= nc; ++it) {
+      if (it >= 0 && it < nc) {
+        const int b2 = it & 1;
+        const E* K = sK[b2];
+        const E* Tm = sT[b2];
+        // every LDS operand of the step first, in one batch: a single wait instead of one per level
+        bf16x8 kfr[4][KBF], tfr[6], ktf[HB][2];
+        bf16x4 vfr[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+#pragma unroll
+          for (int kb = 0; kb < KBF; ++kb) kfr[i][kb] = acc_frag(K + (16 * i + lq) * PK + 32 * kb);
+          vfr[i] = read_tr16_rows<bf16x4>(sV[b2], PV, 16 * i, 0);
+        }
+        tfr[0] = acc_frag(Tm + lq * PT);
+        tfr[1] = acc_frag(Tm + (16 + lq) * PT);
+        tfr[2] = acc_frag(Tm + (32 + lq) * PT);
+        tfr[3] = acc_frag(Tm + (32 + lq) * PT + 32);
+        tfr[4] = acc_frag(Tm + (48 + lq) * PT);
+        tfr[5] = acc_frag(Tm + (48 + lq) * PT + 32);
+#pragma unroll
+        for (int m = 0; m < HB; ++m)
+#pragma unroll
+          for (int pr = 0; pr < 2; ++pr) {  // K^T: column 16 m + lq of token rows 32 pr + 4 g (+16)
+            const bf16x4 lo = read_tr16_rows<bf16x4>(K, PK, 32 * pr, 16 * m);
+            const bf16x4 hi = read_tr16_rows<bf16x4>(K, PK, 32 * pr + 16, 16 * m);
+            ktf[m][pr] = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+          }
+        __builtin_amdgcn_sched_barrier(0);
+
+        AB hb[KBF];
+#pragma unroll
+        for (int kb = 0; kb < KBF; ++kb) hb[kb] = Acc<E>::pack(hreg[2 * kb], hreg[2 * kb + 1]);
+#pragma unroll
+        for (int m = 0; m < HB; ++m) {
+          bf16x4 w4;
+#pragma unroll
+          for (int r = 0; r < 4; ++r) w4[r] = (__bf16)hreg[m][r];
+          *reinterpret_cast<bf16x4*>(&sHo[b2][lq * PK + 16 * m + 4 * g]) = w4;
+        }
+        f32x4 rr[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          f32x4 kh = zero4();
+#pragma unroll
+          for (int kb = 0; kb < KBF; ++kb) kh = mfma_bf16(kfr[i][kb], hb[kb].v, kh);
+#pragma unroll
+          for (int r = 0; r < 4; ++r) rr[i][r] = (float)vfr[i][r] - kh[r];
+        }
+        const AB rb0 = Acc<E>::pack(rr[0], rr[1]);
+        const AB rb1 = Acc<E>::pack(rr[2], rr[3]);
+        f32x4 dl[4];
+        dl[0] = mfma_bf16(tfr[0], rb0.v, zero4());
+        dl[1] = mfma_bf16(tfr[1], rb0.v, zero4());
+        dl[2] = mfma_bf16(tfr[3], rb1.v, mfma_bf16(tfr[2], rb0.v, zero4()));
+        dl[3] = mfma_bf16(tfr[5], rb1.v, mfma_bf16(tfr[4], rb0.v, zero4()));
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          bf16x4 w4;
+#pragma unroll
+          for (int r = 0; r < 4; ++r) w4[r] = (__bf16)dl[i][r];
+          *reinterpret_cast<bf16x4*>(&sDo[b2][lq * PT + 16 * i + 4 * g]) = w4;
+        }
+        const AB db[2] = {Acc<E>::pack(dl[0], dl[1]), Acc<E>::pack(dl[2], dl[3])};
+#pragma unroll
+        for (int m = 0; m < HB; ++m)
+#pragma unroll
+          for (int pr = 0; pr < 2; ++pr) hreg[m] = mfma_bf16(ktf[m][pr], db[pr].v, hreg[m]);
+      }
+      __syncthreads();
+    }
+#pragma unroll
+    for (int m = 0; m < HB; ++m)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) s_out[((size_t)bh * DK + 16 * m + 4 * g + r) * DK + v0 + lq] = hreg[m][r];
+    return;
+  }
+
+  // ---- helpers: one chunk in flight each ----
   const int hj = wave - 1;
   NR qn[4][N::NREG], kn[4][N::NREG];
   u32x4 tseg[TSEG];
   bf16x4 vn[4];
   uint8_t actraw[4];
+  NR qo[4][N::NREG];  // Q of the staged chunk, kept for its output while the next loads fly
+  AB pt[6];
+  uint8_t actk[4];
 
   // Rows of one (b, h) from a uniform base with 32-bit lane offsets (the host keeps T*H*DK < 2^31).
   // Every load is unconditional (rows past the chunk's end re-read its last row and are zeroed when
@@ -811,7 +911,7 @@ __global__ __launch_bounds__(512) void delta_chain_bf16_kernel(const TIn* __rest
     }
   };
   auto store_chunk = [&](int c) {
-    const int b3 = c % 3, b2 = c & 1;
+    const int b2 = c & 1;
     const int nvc = min(kChunk, T - c * kChunk);
     if (nvc < kChunk) {  // the sequence's last, partial chunk: rows past its end stage as zeros
 #pragma unroll
@@ -827,12 +927,9 @@ __global__ __launch_bounds__(512) void delta_chain_bf16_kernel(const TIn* __rest
     for (int i = 0; i < 4; ++i) {
       const int tok = 16 * i + lq;
 #pragma unroll
-      for (int sgi = 0; sgi < N::NREG; ++sgi) {
-        *reinterpret_cast<NR*>(&sK[b3][tok * PK + N::feat(sgi)]) = kn[i][sgi];
-        *reinterpret_cast<NR*>(&sQ[b3][tok * PK + N::feat(sgi)]) = qn[i][sgi];
-      }
+      for (int sgi = 0; sgi < N::NREG; ++sgi) *reinterpret_cast<NR*>(&sK[b2][tok * PK + N::feat(sgi)]) = kn[i][sgi];
       *reinterpret_cast<bf16x4*>(&sV[b2][tok * PV + 4 * g]) = vn[i];
-      if (g == 0) sAct[b3][tok] = (tok < nvc && (active == nullptr || actraw[i] != 0)) ? 1 : 0;
+      actk[i] = (tok < nvc && (active == nullptr || actraw[i] != 0)) ? 1 : 0;
     }
 #pragma unroll
     for (int j = 0; j < TSEG; ++j) {
@@ -842,154 +939,62 @@ __global__ __launch_bounds__(512) void delta_chain_bf16_kernel(const TIn* __rest
       const int row = 16 * ti + within / 16, col = 16 * tj + within % 16;
       *reinterpret_cast<u32x4*>(&sT[b2][row * PT + col]) = tseg[j];
     }
+    // P^T tiles (key tile jj, query tile ii), keys after the query masked, packed per k-block
+    auto ptile = [&](int jj, int ii) {
+      const f32x4 acc = N::mma(kn[jj], qn[ii], zero4());
+      f32x4 r4;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) r4[r] = (16 * jj + 4 * g + r <= 16 * ii + lq) ? acc[r] : 0.f;
+      return r4;
+    };
+    pt[0] = Acc<E>::pack(ptile(0, 0), zero4());
+    pt[1] = Acc<E>::pack(ptile(0, 1), ptile(1, 1));
+    pt[2] = Acc<E>::pack(ptile(0, 2), ptile(1, 2));
+    pt[3] = Acc<E>::pack(ptile(2, 2), zero4());
+    pt[4] = Acc<E>::pack(ptile(0, 3), ptile(1, 3));
+    pt[5] = Acc<E>::pack(ptile(2, 3), ptile(3, 3));
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int sgi = 0; sgi < N::NREG; ++sgi) qo[i][sgi] = qn[i][sgi];
   };
-  // rows 16 blk .. 16 blk + 15 of the output of chunk c: O^T = H^T Q^T + Delta^T P^T with the
-  // causal P^T = tril(Q K^T)^T formed here from the LDS tiles
-  auto write_block = [&](int c, int blk) {
-    const int b3 = c % 3, b2 = c & 1;
+  // O^T = H^T Q^T + Delta^T P^T for the four row blocks of chunk c: the H^T and Delta^T fragments
+  // are read from LDS once and serve all four blocks
+  auto write_output = [&](int c) {
+    const int b2 = c & 1;
     const int nvc = min(kChunk, T - c * kChunk);
-    NR ql[N::NREG];
+    NR ho[N::NREG];
 #pragma unroll
-    for (int sgi = 0; sgi < N::NREG; ++sgi)
-      ql[sgi] = *reinterpret_cast<const NR*>(&sQ[b3][(16 * blk + lq) * PK + N::feat(sgi)]);
-    f32x4 acc = N::mma_lds(&sHo[b2][lq * PK], ql, zero4());
-    f32x4 pt[4];
-#pragma unroll
-    for (int jj = 0; jj < 4; ++jj) {
-      if (jj <= blk) {
-        const f32x4 sc = N::mma_lds(&sK[b3][(16 * jj + lq) * PK], ql, zero4());
-#pragma unroll
-        for (int r = 0; r < 4; ++r) pt[jj][r] = (16 * jj + 4 * g + r <= 16 * blk + lq) ? sc[r] : 0.f;
-      } else {
-        pt[jj] = zero4();
-      }
-    }
-    acc = Acc<E>::mma(&sDo[b2][lq * PT], Acc<E>::pack(pt[0], pt[1]), acc);
-    if (blk >= 2) acc = Acc<E>::mma(&sDo[b2][lq * PT + 32], Acc<E>::pack(pt[2], pt[3]), acc);
-    const int tok = 16 * blk + lq;
-    if (tok < nvc) {
-      TIn* dst = o + bh_base + (size_t)c * kChunk * rstride + v0 + (tok * rstride + 4 * g);
-      const bool on = sAct[b3][tok] != 0;
-#pragma unroll
-      for (int r = 0; r < 4; ++r) dst[r] = from_f32<TIn>(on ? acc[r] : 0.f);
-    }
-  };
-
-  // ---- chain state ----
-  f32x4 hreg[HB];
-  if (wave == 0) {
-#pragma unroll
-    for (int m = 0; m < HB; ++m)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) hreg[m][r] = s_in[((size_t)bh * DK + 16 * m + 4 * g + r) * DK + v0 + lq];
-  }
-  // the Acc-layout A fragment of a row-major LDS row: k = 4 g + r and 16 + 4 g + r
-  auto acc_frag = [&](const E* arow) {
-    const bf16x4 lo = *reinterpret_cast<const bf16x4*>(arow + 4 * g);
-    const bf16x4 hi = *reinterpret_cast<const bf16x4*>(arow + 16 + 4 * g);
-    return bf16x8(__builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
-  };
-  auto chain_step = [&](int c) {
-    const int b3 = c % 3, b2 = c & 1;
-    const E* K = sK[b3];
-    const E* Tm = sT[b2];
-    // every LDS operand of the step first, in one batch: a single wait instead of one per level
-    bf16x8 kfr[4][KBF], tfr[6], ktf[HB][2];
-    bf16x4 vfr[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-#pragma unroll
-      for (int kb = 0; kb < KBF; ++kb) kfr[i][kb] = acc_frag(K + (16 * i + lq) * PK + 32 * kb);
-      vfr[i] = read_tr16_rows<bf16x4>(sV[b2], PV, 16 * i, 0);
-    }
-    tfr[0] = acc_frag(Tm + lq * PT);
-    tfr[1] = acc_frag(Tm + (16 + lq) * PT);
-    tfr[2] = acc_frag(Tm + (32 + lq) * PT);
-    tfr[3] = acc_frag(Tm + (32 + lq) * PT + 32);
-    tfr[4] = acc_frag(Tm + (48 + lq) * PT);
-    tfr[5] = acc_frag(Tm + (48 + lq) * PT + 32);
-#pragma unroll
-    for (int m = 0; m < HB; ++m)
-#pragma unroll
-      for (int pr = 0; pr < 2; ++pr) {  // K^T: column 16 m + lq of token rows 32 pr + 4 g (+16)
-        const bf16x4 lo = read_tr16_rows<bf16x4>(K, PK, 32 * pr, 16 * m);
-        const bf16x4 hi = read_tr16_rows<bf16x4>(K, PK, 32 * pr + 16, 16 * m);
-        ktf[m][pr] = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
-      }
+    for (int sgi = 0; sgi < N::NREG; ++sgi) ho[sgi] = *reinterpret_cast<const NR*>(&sHo[b2][lq * PK + N::feat(sgi)]);
+    const bf16x8 d0 = acc_frag(&sDo[b2][lq * PT]);
+    const bf16x8 d1 = acc_frag(&sDo[b2][lq * PT + 32]);
     __builtin_amdgcn_sched_barrier(0);
-
-    AB hb[KBF];
-#pragma unroll
-    for (int kb = 0; kb < KBF; ++kb) hb[kb] = Acc<E>::pack(hreg[2 * kb], hreg[2 * kb + 1]);
-#pragma unroll
-    for (int m = 0; m < HB; ++m) {
-      bf16x4 w4;
-#pragma unroll
-      for (int r = 0; r < 4; ++r) w4[r] = (__bf16)hreg[m][r];
-      *reinterpret_cast<bf16x4*>(&sHo[b2][lq * PK + 16 * m + 4 * g]) = w4;
-    }
-    f32x4 rr[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      f32x4 kh = zero4();
+      f32x4 acc = N::mma(ho, qo[i], zero4());
+      acc = mfma_bf16(d0, pt[i == 0 ? 0 : (i == 1 ? 1 : (i == 2 ? 2 : 4))].v, acc);
+      if (i >= 2) acc = mfma_bf16(d1, pt[i == 2 ? 3 : 5].v, acc);
+      const int tok = 16 * i + lq;
+      if (tok < nvc) {
+        TIn* dst = o + bh_base + (size_t)c * kChunk * rstride + v0 + (tok * rstride + 4 * g);
+        const bool on = actk[i] != 0;
+        typedef TIn O4 __attribute__((ext_vector_type(4)));
+        O4 w4;
 #pragma unroll
-      for (int kb = 0; kb < KBF; ++kb) kh = mfma_bf16(kfr[i][kb], hb[kb].v, kh);
-#pragma unroll
-      for (int r = 0; r < 4; ++r) rr[i][r] = (float)vfr[i][r] - kh[r];
+        for (int r = 0; r < 4; ++r) w4[r] = from_f32<TIn>(on ? acc[r] : 0.f);
+        *reinterpret_cast<O4*>(dst) = w4;  // 8 bytes: the host keeps o 8-byte aligned
+      }
     }
-    const AB rb0 = Acc<E>::pack(rr[0], rr[1]);
-    const AB rb1 = Acc<E>::pack(rr[2], rr[3]);
-    f32x4 dl[4];
-    dl[0] = mfma_bf16(tfr[0], rb0.v, zero4());
-    dl[1] = mfma_bf16(tfr[1], rb0.v, zero4());
-    dl[2] = mfma_bf16(tfr[3], rb1.v, mfma_bf16(tfr[2], rb0.v, zero4()));
-    dl[3] = mfma_bf16(tfr[5], rb1.v, mfma_bf16(tfr[4], rb0.v, zero4()));
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      bf16x4 w4;
-#pragma unroll
-      for (int r = 0; r < 4; ++r) w4[r] = (__bf16)dl[i][r];
-      *reinterpret_cast<bf16x4*>(&sDo[b2][lq * PT + 16 * i + 4 * g]) = w4;
-    }
-    const AB db[2] = {Acc<E>::pack(dl[0], dl[1]), Acc<E>::pack(dl[2], dl[3])};
-#pragma unroll
-    for (int m = 0; m < HB; ++m)
-#pragma unroll
-      for (int pr = 0; pr < 2; ++pr) hreg[m] = mfma_bf16(ktf[m][pr], db[pr].v, hreg[m]);
   };
 
-  // the upper tiles of T are never staged (the compact factor holds the ten lower ones): zero once
-  for (int i = threadIdx.x; i < 2 * 64 * PT; i += 512) (&sT[0][0])[i] = (__bf16)0.f;
-  __syncthreads();
-  // The chain and the helpers run separate loops with the same barrier sequence, so neither keeps
-  // the other's registers live.
-  if (wave == 0) {
-    for (int it = -1; it <= nc; ++it) {
-      if (it >= 0 && it < nc) chain_step(it);
-      __syncthreads();
-    }
-#pragma unroll
-    for (int m = 0; m < HB; ++m)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) s_out[((size_t)bh * DK + 16 * m + 4 * g + r) * DK + v0 + lq] = hreg[m][r];
-  } else {
-    if (hj < nc) issue_loads(hj);
-    for (int it = -1; it <= nc; ++it) {
-      const int cs = it + 1, co = it - 1;
-      if (cs < nc && cs % NH == hj) store_chunk(cs);
-      if (co >= 0) {
-        if (co % NH == hj) {
-          write_block(co, 0);
-          write_block(co, 3);
-        }
-        if ((co + 3) % NH == hj) {
-          write_block(co, 1);
-          write_block(co, 2);
-        }
-      }
-      if (it >= 0 && it < nc && it % NH == hj && it + NH < nc) issue_loads(it + NH);
-      __syncthreads();
-    }
+  if (hj < nc) issue_loads(hj);
+  for (int it = -1; it <= nc; ++it) {
+    const int cs = it + 1, co = it - 1;
+    if (cs < nc && cs % NH == hj) store_chunk(cs);
+    // the iteration between staging and output: loads of the chunk seven on
+    if (it >= 0 && it % NH == hj && it + NH < nc) issue_loads(it + NH);
+    if (co >= 0 && co % NH == hj) write_output(co);
+    __syncthreads();
   }
 }
 
@@ -1033,7 +1038,7 @@ void launch_chunked(const TIn* q, const TIn* k, const TIn* v, const TIn* beta, c
   const int total = B * H * nc;
   hipLaunchKernelGGL((delta_prep_kernel<TIn, E, DK>), dim3((unsigned)((total + 3) / 4)), dim3(256), 0, stream, k, beta,
                      tmat, T, H, total);
-  if constexpr (sizeof(E) == 2 && DK >= 32 && DK <= 64) {  // (at 128 its staging registers would spill)
+  if constexpr (sizeof(E) == 2 && DK >= 32 && DK <= 64) {  // (at 128 the staging registers would spill)
     hipLaunchKernelGGL((delta_chain_bf16_kernel<TIn, DK>), dim3((unsigned)(B * H * (DK / 16))), dim3(512), 0, stream, q,
                        k, v, tmat, s_in, s_out, o, active, T, H);
   } else {
@@ -1060,6 +1065,10 @@ int delta_scan(const TIn* q, const TIn* k, const TIn* v, const TIn* beta, const 
   if (need == 0) return launch_serial<TIn>(q, k, v, beta, s_in, s_out, o, active, B, T, H, D, stream, who);
   if (workspace == nullptr || ws_bytes < need)
     return fail(ERR_ARG, "%s: workspace of %zu bytes given, %zu needed", who, workspace ? ws_bytes : (size_t)0, need);
+  // the chunked kernels move q, k, v, o rows and the workspace in 16-byte pieces
+  if ((reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(k) | reinterpret_cast<uintptr_t>(v) |
+       reinterpret_cast<uintptr_t>(o) | reinterpret_cast<uintptr_t>(workspace)) & 15)
+    return fail(ERR_ARG, "%s: q, k, v, o and the workspace must be 16-byte aligned", who);
   E* tmat = reinterpret_cast<E*>(workspace);
   switch (D) {
     case 16: launch_chunked<TIn, E, 16>(q, k, v, beta, s_in, s_out, o, tmat, active, B, T, H, stream); break;

@@ -78,10 +78,16 @@ def _active_mask(active: Tensor | None, lead: tuple[str, ...], dims: Dims, devic
     return active.contiguous().view(torch.uint8)
 
 
+def _aligned(t: Tensor) -> Tensor:
+    """Contiguous and 16-byte aligned (the kernels move rows in 16-byte pieces)."""
+    t = t.contiguous()
+    return t if t.data_ptr() % 16 == 0 else t.clone()
+
+
 def _scan(entry: str, q: Tensor, k: Tensor, v: Tensor, beta: Tensor, state: Tensor, active: Tensor | None,
           fp32: bool) -> tuple[Tensor, Tensor]:
     b, n, h, dk = q.shape
-    q, k, v, beta, state = (t.contiguous() for t in (q, k, v, beta, state))
+    q, k, v, beta, state = (_aligned(t) for t in (q, k, v, beta, state))
     mask = _active_mask(active, ("b", "n"), {"b": b, "n": n}, q.device)
     o = torch.empty_like(q)
     s_out = torch.empty_like(state)
