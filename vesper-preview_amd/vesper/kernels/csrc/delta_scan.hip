@@ -253,56 +253,50 @@ constexpr int kTileCol[kTiles] = {0, 0, 1, 0, 1, 2, 0, 1, 2, 3};
 __device__ __forceinline__ int tile_of(int i, int j) { return i * (i + 1) / 2 + j; }
 
 // --------------------------------------------------------------------------------------------
-// chunk preparation: one wave per 64-token chunk, no workgroup barriers
+// the UT factor of one chunk, by one wave
 // --------------------------------------------------------------------------------------------
-template <typename TIn, typename E, int DK>
-__global__ __launch_bounds__(256) void delta_prep_kernel(const TIn* __restrict__ k, const TIn* __restrict__ beta,
-                                                         E* __restrict__ tmat, int T, int H, int total) {
-  constexpr int DKP = DK < 32 ? 32 : DK;
+constexpr int kUtPitch = 17;  // pitch of the fp32 16x16 scratch tiles
+constexpr int kUtScratch = 8 * 16 * kUtPitch;  // floats: the four diagonal A tiles, then their inverses
+
+// T = (I + A)^-1 diag(beta) with A = tril(diag(beta) K K^T, -1) for one 64-token chunk, computed
+// by one wave with no workgroup barrier: the Gram matrix on MFMA from the key rows `kn` (Nat
+// layout, zero rows past the chunk's end), the four diagonal 16x16 blocks of the inverse by
+// forward substitution in fp32, the off-diagonal blocks level by level on fp32 MFMA. The six
+// off-diagonal A tiles never leave registers: computed transposed (K_j K_i^T = (K_i K_j^T)^T), an
+// accumulator tile is already the A operand of the fp32 16x16x4 products. Only the diagonal A
+// tiles and their inverses use the LDS scratch `scr` (kUtScratch floats, 8.5 KiB). `bl` is beta
+// of token l on lane l (zero past the end). Element (r, c) of the lower 16x16 tile (ti, tj) of T
+// goes to out(ti, tj, r, c), an LDS or global address that may alias `scr`. Upper tiles are not
+// written. Ends with a wave_sync, so the wave may read LDS tiles back.
+template <typename E, int DKP, typename Out>
+__device__ __forceinline__ void ut_solve(const typename Nat<E, DKP>::R (&kn)[4][Nat<E, DKP>::NREG], float bl,
+                                         float* scr, Out out) {
   using N = Nat<E, DKP>;
-  constexpr int TP = 17;  // pitch of the fp32 16x16 tiles
-  __shared__ float sA[4][kTiles][16 * TP];
-  __shared__ float sXd[4][4][16 * TP];
+  constexpr int TP = kUtPitch;
+  const int l = threadIdx.x & 63, lq = l & 15, g = l >> 4;
+  float* Ad = scr;                // diagonal A tiles, row-major
+  float* Xd = scr + 4 * 16 * TP;  // their inverses (I + A_bb)^-1, row-major
 
-  const int w = threadIdx.x >> 6, l = threadIdx.x & 63;
-  const int lq = l & 15, g = l >> 4;
-  const int chunk = blockIdx.x * 4 + w;
-  if (chunk >= total) return;  // whole waves only: this kernel has no workgroup barrier
-  const int nc = (T + kChunk - 1) / kChunk;
-  const int c = chunk % nc, bh = chunk / nc;
-  const int b = bh / H, h = bh - b * H;
-  const int t0 = c * kChunk, nv = min(kChunk, T - t0);
-  float* A = &sA[w][0][0];
-  float* Xd = &sXd[w][0][0];
-
-  typename N::R kn[4][N::NREG];
+  // A tiles: diagonal ones into LDS (strictly lower part), off-diagonal ones transposed in
+  // registers: aoff holds A[16 i + lq][16 j + 4 g + r] on lane (lq, g)
+  f32x4 aoff[6];  // (1,0) (2,0) (2,1) (3,0) (3,1) (3,2)
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    const int tok = 16 * i + lq;
-    const TIn* row = k + (((size_t)b * T + t0 + tok) * H + h) * DK;
+    const float brow = __shfl(bl, 16 * i + lq);  // beta of row 16 i + lq (the transposed layout's row)
 #pragma unroll
-    for (int s = 0; s < N::NREG; ++s) {
-      const int f = N::feat(s);
-      if (tok < nv && f < DK) {
-        kn[i][s] = *reinterpret_cast<const typename N::R*>(row + f);
-      } else {
+    for (int j = 0; j < i; ++j) {
+      const f32x4 gt = N::mma(kn[j], kn[i], zero4());
+      f32x4 a;
 #pragma unroll
-        for (int e = 0; e < N::PER; ++e) kn[i][s][e] = from_f32<E>(0.f);
-      }
+      for (int r = 0; r < 4; ++r) a[r] = brow * gt[r];
+      aoff[i * (i - 1) / 2 + j] = a;
     }
-  }
-  const float bl = l < nv ? to_f32(beta[((size_t)b * T + t0 + l) * H + h]) : 0.f;
-
-  // A = beta_row (K K^T) strictly below the diagonal, ten lower tiles
-#pragma unroll
-  for (int t = 0; t < kTiles; ++t) {
-    const int ti = kTileRow[t], tj = kTileCol[t];
-    const f32x4 gr = N::mma(kn[ti], kn[tj], zero4());
+    const f32x4 gd = N::mma(kn[i], kn[i], zero4());
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      const int row = 16 * ti + 4 * g + r, col = 16 * tj + lq;
-      const float br = __shfl(bl, row);
-      A[t * 16 * TP + (4 * g + r) * TP + lq] = row > col ? br * gr[r] : 0.f;
+      const int row = 4 * g + r;
+      const float br = __shfl(bl, 16 * i + row);
+      Ad[i * 16 * TP + row * TP + lq] = row > lq ? br * gd[r] : 0.f;
     }
   }
   wave_sync();
@@ -310,14 +304,14 @@ __global__ __launch_bounds__(256) void delta_prep_kernel(const TIn* __restrict__
   // diagonal blocks: lane (blk, col) solves (I + A_bb) x = e_col by forward substitution
   {
     const int blk = g, col = lq;
-    const float* ab = A + tile_of(blk, blk) * 16 * TP;
+    const float* ab = Ad + blk * 16 * TP;
     float x[16];
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
-      float s = (i == col) ? 1.f : 0.f;
+      float sum = (i == col) ? 1.f : 0.f;
 #pragma unroll
-      for (int j = 0; j < i; ++j) s -= ab[i * TP + j] * x[j];
-      x[i] = s;
+      for (int j = 0; j < i; ++j) sum -= ab[i * TP + j] * x[j];
+      x[i] = sum;
     }
 #pragma unroll
     for (int i = 0; i < 16; ++i) Xd[blk * 16 * TP + i * TP + col] = x[i];
@@ -325,51 +319,53 @@ __global__ __launch_bounds__(256) void delta_prep_kernel(const TIn* __restrict__
   wave_sync();
 
   // fp32 16x16x16 products; k permuted as 4g + r so accumulator tiles serve as B operands
-  auto mm = [&](const float* atile, const float* btile_lds, const f32x4* breg, f32x4 acc) {
+  auto mm = [&](const float* atile_lds, const f32x4* areg, const float* btile_lds, const f32x4* breg, f32x4 acc) {
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      const float av = atile[lq * TP + 4 * g + r];
+      const float av = areg ? (*areg)[r] : atile_lds[lq * TP + 4 * g + r];
       const float bv = breg ? (*breg)[r] : btile_lds[(4 * g + r) * TP + lq];
       acc = __builtin_amdgcn_mfma_f32_16x16x4f32(av, bv, acc, 0, 0, 0);
     }
     return acc;
   };
-  const float* Xt0 = Xd;
-  auto xd = [&](int blk) { return Xt0 + blk * 16 * TP; };
-  auto at = [&](int i, int j) { return (const float*)(A + tile_of(i, j) * 16 * TP); };
+  auto xd = [&](int blk) { return (const float*)(Xd + blk * 16 * TP); };
+  auto ao = [&](int i, int j) { return &aoff[i * (i - 1) / 2 + j]; };
 
   f32x4 x1[3], x2[2], x3;
 #pragma unroll
   for (int bb = 0; bb < 3; ++bb) {
-    const f32x4 y = mm(at(bb + 1, bb), xd(bb), nullptr, zero4());
-    x1[bb] = -mm(xd(bb + 1), nullptr, &y, zero4());
+    const f32x4 y = mm(nullptr, ao(bb + 1, bb), xd(bb), nullptr, zero4());
+    x1[bb] = -mm(xd(bb + 1), nullptr, nullptr, &y, zero4());
   }
 #pragma unroll
   for (int bb = 0; bb < 2; ++bb) {
-    f32x4 y = mm(at(bb + 2, bb), xd(bb), nullptr, zero4());
-    y = mm(at(bb + 2, bb + 1), nullptr, &x1[bb], y);
-    x2[bb] = -mm(xd(bb + 2), nullptr, &y, zero4());
+    f32x4 y = mm(nullptr, ao(bb + 2, bb), xd(bb), nullptr, zero4());
+    y = mm(nullptr, ao(bb + 2, bb + 1), nullptr, &x1[bb], y);
+    x2[bb] = -mm(xd(bb + 2), nullptr, nullptr, &y, zero4());
   }
   {
-    f32x4 y = mm(at(3, 0), xd(0), nullptr, zero4());
-    y = mm(at(3, 1), nullptr, &x1[0], y);
-    y = mm(at(3, 2), nullptr, &x2[0], y);
-    x3 = -mm(xd(3), nullptr, &y, zero4());
+    f32x4 y = mm(nullptr, ao(3, 0), xd(0), nullptr, zero4());
+    y = mm(nullptr, ao(3, 1), nullptr, &x1[0], y);
+    y = mm(nullptr, ao(3, 2), nullptr, &x2[0], y);
+    x3 = -mm(xd(3), nullptr, nullptr, &y, zero4());
   }
 
-  // T = X diag(beta), compact tiles
-  E* out = tmat + (size_t)chunk * kChunkT;
+  // T = X diag(beta): the diagonal tiles from the LDS inverses (read before any output write
+  // that may alias them), the off-diagonal ones from registers
+  float dcol[16];
   {
     const int blk = g, col = lq;
     const float bc = __shfl(bl, 16 * blk + col);
 #pragma unroll
-    for (int i = 0; i < 16; ++i)
-      out[tile_of(blk, blk) * kTileElems + i * 16 + col] = from_f32<E>(Xd[blk * 16 * TP + i * TP + col] * bc);
+    for (int i = 0; i < 16; ++i) dcol[i] = Xd[blk * 16 * TP + i * TP + col] * bc;
   }
+  wave_sync();
+#pragma unroll
+  for (int i = 0; i < 16; ++i) *out(g, g, i, lq) = from_f32<E>(dcol[i]);
   auto put = [&](int i, int j, const f32x4& x) {
     const float bc = __shfl(bl, 16 * j + lq);
 #pragma unroll
-    for (int r = 0; r < 4; ++r) out[tile_of(i, j) * kTileElems + (4 * g + r) * 16 + lq] = from_f32<E>(x[r] * bc);
+    for (int r = 0; r < 4; ++r) *out(i, j, 4 * g + r, lq) = from_f32<E>(x[r] * bc);
   };
   put(1, 0, x1[0]);
   put(2, 1, x1[1]);
@@ -377,6 +373,56 @@ __global__ __launch_bounds__(256) void delta_prep_kernel(const TIn* __restrict__
   put(2, 0, x2[0]);
   put(3, 1, x2[1]);
   put(3, 0, x3);
+  wave_sync();
+}
+
+// --------------------------------------------------------------------------------------------
+// chunk preparation: one wave per 64-token chunk, no workgroup barriers
+// --------------------------------------------------------------------------------------------
+template <typename TIn, typename E, int DK>
+__global__ __launch_bounds__(256, 3) void delta_prep_kernel(const TIn* __restrict__ k, const TIn* __restrict__ beta,
+                                                         E* __restrict__ tmat, int T, int H, int total) {
+  constexpr int DKP = DK < 32 ? 32 : DK;
+  using N = Nat<E, DKP>;
+  // the compact factor is staged in LDS for 16-byte global stores: it overlays the scratch
+  constexpr int kScr = kChunkT * (int)sizeof(E) / 4 > kUtScratch ? kChunkT * (int)sizeof(E) / 4 : kUtScratch;
+  __shared__ __align__(16) float sScr[4][kScr];
+
+  const int w = threadIdx.x >> 6, l = threadIdx.x & 63;
+  const int lq = l & 15;
+  const int chunk = blockIdx.x * 4 + w;
+  if (chunk >= total) return;  // whole waves only: this kernel has no workgroup barrier
+  const int nc = (T + kChunk - 1) / kChunk;
+  const int c = chunk % nc, bh = chunk / nc;
+  const int b = bh / H, h = bh - b * H;
+  const int t0 = c * kChunk, nv = min(kChunk, T - t0);
+
+  typename N::R kn[4][N::NREG];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int tok = 16 * i + lq;
+    const TIn* row = k + (((size_t)b * T + t0 + tok) * H + h) * DK;
+#pragma unroll
+    for (int sgi = 0; sgi < N::NREG; ++sgi) {
+      const int f = N::feat(sgi);
+      if (tok < nv && f < DK) {
+        kn[i][sgi] = *reinterpret_cast<const typename N::R*>(row + f);
+      } else {
+#pragma unroll
+        for (int e = 0; e < N::PER; ++e) kn[i][sgi][e] = from_f32<E>(0.f);
+      }
+    }
+  }
+  const float bl = l < nv ? to_f32(beta[((size_t)b * T + t0 + l) * H + h]) : 0.f;
+  E* tc = reinterpret_cast<E*>(&sScr[w][0]);  // compact tiles: tile t = i (i + 1) / 2 + j, row-major
+  ut_solve<E, DKP>(kn, bl, &sScr[w][0],
+                   [&](int ti, int tj, int r, int cc) { return tc + tile_of(ti, tj) * kTileElems + r * 16 + cc; });
+  // the compact factor to global memory in 16-byte pieces
+  typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+  constexpr int SEGS = kChunkT * (int)sizeof(E) / 16;
+  u32x4_t* dst = reinterpret_cast<u32x4_t*>(tmat + (size_t)chunk * kChunkT);
+  const u32x4_t* src = reinterpret_cast<const u32x4_t*>(tc);
+  for (int j = l; j < SEGS; j += 64) dst[j] = src[j];
 }
 
 // --------------------------------------------------------------------------------------------
