@@ -163,6 +163,15 @@ __device__ __forceinline__ V4 read_tr16_rows(const T* tile, int pitch, int r0, i
   return read_tr16<V4>(tile + (r0 + 4 * g + (lq >> 2)) * pitch + c0 + 4 * (lq & 3));
 }
 
+// 16 bytes per lane from global memory straight into LDS (global_load_lds_dwordx4): lane i writes
+// lds + 16 i, so `lds` must be the same for the whole wave. Device pass only: the host pass of a
+// kernel template does not take the builtin.
+__device__ __forceinline__ void load_lds16(const void* src, void* lds) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  __builtin_amdgcn_global_load_lds(src, lds, 16, 0, 0);
+#endif
+}
+
 // ---- XCD-aware block order --------------------------------------------------------------------
 // Workgroups are dispatched round-robin over the 8 XCDs (block g runs on XCD g % 8), and each XCD
 // has its own L2. Renumber so that consecutive logical ids share an XCD: blocks that read the same

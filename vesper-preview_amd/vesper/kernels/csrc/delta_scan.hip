@@ -2,7 +2,7 @@
 //
 // Per batch row b and head h the state H [D, D] (key rows, value columns) is read as H^T q; a token
 // applies H <- (I - beta k k^T) H + beta k v^T and reads o = H^T q (reference vesper/recurrence.py:
-// 1-23, 118-163). Three kernels:
+// 1-23, 118-163). Four kernels (the decode step's register-resident kernel is in delta_step.hip):
 //
 //  * delta_serial_kernel  - token by token, the state of a 64-column block in registers (one lane
 //    per value column, rows split over up to four waves). Any D <= 256; the decode step (T = 1)
@@ -15,7 +15,10 @@
 //    the state slice in MFMA accumulators: R = V - K H, Delta = T R, O = Q H + tril(Q K^T) Delta,
 //    H += K^T Delta (the WY/UT form of recurrence.py:17-23 and :202-216, with Delta = U - W H
 //    written as T (V - K H)). Value columns of the state evolve independently, so slicing them
-//    gives B*H*(D/16) concurrent chains.
+//    gives B*H*(D/16) concurrent chains. fp32 inputs and head widths 16 and 128.
+//  * delta_chain_bf16_kernel - the same chains for bf16 inputs at head widths 32 and 64, with the
+//    state-independent products (W = T K, U = T V, P = tril(Q K^T), the outputs) moved to helper
+//    waves, so the chain wave runs only Delta = U - W H and H += K^T Delta per chunk.
 #include "common.h"
 #include "vesper_kernels.h"
 
@@ -226,6 +229,7 @@ template <int K> struct Nat<float, K> {
 };
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 typedef short s16x4 __attribute__((ext_vector_type(4)));
 
 template <typename E>
@@ -760,21 +764,76 @@ __global__ __launch_bounds__(64 * (ChainShape<E, DK>::NH + 1)) void delta_chain_
   }
 }
 // --------------------------------------------------------------------------------------------
-// the bf16 chunk chain (head widths 32 and 64): as delta_chain_kernel, with its work arranged so
-// that the chain's step, not the helpers or the LDS, sets the pace:
-//  * transposed operands (K^T for the state update, the V slice in the accumulator layout) come
-//    from row-major LDS tiles through ds_read_b64_tr_b16, so staging a chunk needs no MFMA;
-//  * the chain issues all of its step's LDS reads in one batch before its first product;
-//  * the helper that stages chunk c keeps Q_c and the causal tiles P^T = tril(Q K^T)^T (formed from
-//    its registers while staging) in registers of their own, issues the loads of chunk c + 7 in the
-//    next iteration (six iterations of latency cover), and writes the output of chunk c one
-//    iteration after the chain ran it, reading only H^T and Delta^T from LDS, once for all four
-//    row blocks.
-// Per iteration it: the chain runs chunk it; helper (it + 1) % 7 stages chunk it + 1; helper
-// it % 7 loads chunk it + 7; helper (it - 1) % 7 writes the outputs of chunk it - 1.
+// the bf16 chunk chain (head widths 32 and 64)
+// --------------------------------------------------------------------------------------------
+// Per chunk, with W = T K and U = T V (T the chunk's UT factor),
+//   Delta = U - W H,   H' = H + K^T Delta,   O = Q H + P Delta,   P = tril(Q K^T)
+// (the WY/UT form of recurrence.py:17-23 and :202-216). The chain wave runs only the two
+// state-dependent levels, Delta and H', from operands that helper waves have laid out in its MFMA
+// fragment order; the helpers form everything else.
+//  * helper c % 7 owns chunk c: it loads Q, the compact T and the active flags into registers and
+//    K and the V slice straight into its own LDS tiles (issued one chunk period ahead), reads the
+//    token-major fragments of K and V from them (ds_read_b64_tr_b16), forms -W (as the accumulator
+//    tiles of W^T = K^T T^T), U = T V and P^T = tril(K Q^T)^T on MFMA, hands -W, K^T and U to the
+//    chain through one of three LDS slots, and once the chain has run the chunk writes
+//    O^T = H^T Q^T + Delta^T P^T from the chunk's H^T and Delta;
+//  * every product's accumulator tiles serve directly as the next product's operand (the "Acc"
+//    k permutation); slot contents are stored lane by lane in fragment order, so the chain reads
+//    them with conflict-free 16-byte loads;
+//  * the waves hand chunks over through LDS flags, never a workgroup barrier: staged[c % 3] = c once
+//    chunk c's operands are in their slot; done = c once the chain has run chunk c (its slot reads
+//    are performed, and H^T before chunk c and Delta of chunk c are in state slot c % 3);
+//    consumed[c % 3] = c once the helper has read that state slot. The helper of chunk c fills its
+//    slot after done >= c - 3 and writes the output after done >= c; the chain runs chunk c after
+//    staged[c % 3] >= c and consumed[c % 3] >= c - 3. Every wait is on an earlier chain step or on
+//    a helper step that needs only earlier chain steps, so all end.
+// Loads and stores go through buffer resources over each (b, h)'s rows: reads past the sequence's
+// end return zeros and stores there are dropped, so a partial chunk needs no masking.
 // --------------------------------------------------------------------------------------------
 __device__ __forceinline__ f32x4 mfma_bf16(const bf16x8& a, const bf16x8& b, f32x4 acc) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, acc, 0, 0, 0);
+}
+__device__ __forceinline__ bf16x8 join4(const bf16x4& lo, const bf16x4& hi) {
+  return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+}
+// the Acc-permuted operand of a pair of accumulator tiles (rows 16 apart), optionally negated
+__device__ __forceinline__ bf16x8 pack_acc(const f32x4& t0, const f32x4& t1, float sign = 1.f) {
+  bf16x8 b;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    b[r] = (__bf16)(sign * t0[r]);
+    b[4 + r] = (__bf16)(sign * t1[r]);
+  }
+  return b;
+}
+
+// LDS flags of the chunk hand-over. The LDS executes one wave's DS instructions in issue order, so a
+// flag written after a wave's LDS reads and writes is seen by another wave only once those have
+// been performed, and LDS accesses issued after a flag read that returned the awaited value see
+// what the writer did before setting it. Ordering is therefore kept by the compiler alone (signal
+// fences): no wait for the wave's outstanding LDS operations, which would put the LDS queue's
+// latency on the chain's path. (The helpers' direct global-to-LDS loads are not DS instructions;
+// their own vmcnt wait covers them.)
+__device__ __forceinline__ void flag_release(int* f, int value) {
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __hip_atomic_store(f, value, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+__device__ __forceinline__ int flag_peek(const int* f) {
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  const int value = __hip_atomic_load(f, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  return value;
+}
+// Wait until *f >= want, polling every 64 * SLEEP cycles. The spin limit (2^19 polls) is never
+// reached while the hand-over protocol holds; it only keeps a broken protocol from hanging the
+// device.
+template <int SLEEP = 1>
+__device__ __forceinline__ void flag_wait(const int* f, int want) {
+  for (int spin = 0; spin < (1 << 19); ++spin) {
+    if (flag_peek(f) >= want) return;
+    __builtin_amdgcn_s_sleep(SLEEP);
+  }
 }
 
 template <typename TIn, int DK>
@@ -785,30 +844,32 @@ __global__ __launch_bounds__(512) void delta_chain_bf16_kernel(const TIn* __rest
                                                                TIn* __restrict__ o, const uint8_t* __restrict__ active,
                                                                int T, int H) {
   using E = __bf16;
-  constexpr int NH = 7;                          // helper waves
-  constexpr int BV = 16;                         // value columns per chain
-  constexpr int NS = DK / BV;                    // value slices per head
-  constexpr int PK = DK + 8;                     // pitch of K rows and of H^T rows (elements)
-  constexpr int PT = 64 + 8;                     // pitch of T rows and of Delta^T rows
-  constexpr int PV = BV + 8;                     // pitch of V slice rows
-  constexpr int HB = DK / 16;                    // 16-row tiles of the state slice
-  constexpr int KBF = DK / 32;                   // 32-wide k blocks over dk
-  constexpr int TSEG = kChunkT * 2 / 16 / 64;    // 16-byte compact-T segments per lane
-  using N = Nat<E, DK>;
-  using AB = typename Acc<E>::B;
-  using NR = typename N::R;
+  static_assert(sizeof(TIn) == 2, "bf16 inputs");
+  constexpr int NH = 7;          // helper waves: chunks in flight
+  constexpr int NSL = 3;         // LDS slots of chunk operands and of chunk states
+  constexpr int BV = 16;         // value columns per chain
+  constexpr int NS = DK / BV;    // value slices per head
+  constexpr int PK = DK + 8;     // pitch of H^T rows (elements)
+  constexpr int KSEG = DK / 8;   // 16-byte segments of a K row
+  constexpr int HB = DK / 16;    // 16-row tiles over dk
+  constexpr int KBF = DK / 32;   // 32-wide k blocks over dk
+  constexpr int FR = 64 * 8;     // elements of one lane-linear bf16 fragment
 
-  __shared__ __align__(16) E sK[2][64 * PK];
-  __shared__ __align__(16) E sT[2][64 * PT];
-  __shared__ __align__(16) E sV[2][64 * PV];
-  __shared__ __align__(16) E sHo[2][BV * PK];  // H^T of the slice: row = value column, column = dk
-  __shared__ __align__(16) E sDo[2][BV * PT];  // Delta^T: row = value column, column = token
+  __shared__ __align__(16) E hK[NH][64 * DK];         // each helper's K rows (segments swizzled by row)
+  __shared__ __align__(16) E hV[NH][64 * BV];         // each helper's V slice rows
+  __shared__ __align__(16) E sW[NSL][4 * KBF * FR];   // -W: token tile ti, dk block kb
+  __shared__ __align__(16) E sKt[NSL][HB * 2 * FR];   // K^T: dk tile m, token block kb
+  __shared__ __align__(16) float sU[NSL][4 * 64 * 4]; // U: token tile ti, accumulator layout
+  __shared__ __align__(16) E sHo[NSL][BV * PK];       // H^T of the slice before the chunk: row = value column
+  __shared__ __align__(16) E sD[NSL][2 * FR];         // Delta: token block kb, as the output's operand
+  __shared__ int staged[NSL], consumed[NSL], done;
 
   const int lg = xcd_logical_block(blockIdx.x, gridDim.x);
   const int slice = lg % NS, bh = lg / NS;
   const int b = bh / H, h = bh - b * H;
   const int v0 = slice * BV;
-  const int wave = threadIdx.x >> 6, l = threadIdx.x & 63;
+  // the wave index as a scalar: the role branch and the helper's LDS tiles are then wave-uniform
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), l = threadIdx.x & 63;
   const int lq = l & 15, g = l >> 4;
   const int nc = (T + kChunk - 1) / kChunk;
   const int rstride = H * DK;
@@ -816,93 +877,91 @@ __global__ __launch_bounds__(512) void delta_chain_bf16_kernel(const TIn* __rest
 
   // the Acc-layout A fragment of a row-major LDS row: k = 4 g + r and 16 + 4 g + r
   auto acc_frag = [&](const E* arow) {
-    const bf16x4 lo = *reinterpret_cast<const bf16x4*>(arow + 4 * g);
-    const bf16x4 hi = *reinterpret_cast<const bf16x4*>(arow + 16 + 4 * g);
-    return bf16x8(__builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+    return join4(*reinterpret_cast<const bf16x4*>(arow + 4 * g), *reinterpret_cast<const bf16x4*>(arow + 16 + 4 * g));
   };
+  auto frag_at = [&](const E* base, int f) { return *reinterpret_cast<const bf16x8*>(base + f * FR + 8 * l); };
+  auto put_frag = [&](E* base, int f, const bf16x8& x) { *reinterpret_cast<bf16x8*>(base + f * FR + 8 * l) = x; };
 
-  // the upper tiles of T are never staged (the compact factor holds the ten lower ones): zero once
-  for (int i = threadIdx.x; i < 2 * 64 * PT; i += 512) (&sT[0][0])[i] = (__bf16)0.f;
+  if (threadIdx.x < NSL) staged[threadIdx.x] = consumed[threadIdx.x] = -1;
+  if (threadIdx.x == 0) done = -1;
   __syncthreads();
 
-  // The chain and the helpers run separate loops with the same barrier sequence, so neither keeps
-  // the other's registers live.
   if (wave == 0) {
+    // ---- the chain: Delta = U - W H, H <- H + K^T Delta per chunk ----
+    __builtin_amdgcn_s_setprio(2);
     f32x4 hreg[HB];
 #pragma unroll
     for (int m = 0; m < HB; ++m)
 #pragma unroll
       for (int r = 0; r < 4; ++r) hreg[m][r] = s_in[((size_t)bh * DK + 16 * m + 4 * g + r) * DK + v0 + lq];
-    for (int it = -1; it <= nc; ++it) {
-      if (it >= 0 && it < nc) {
-        const int b2 = it & 1;
-        const E* K = sK[b2];
-        const E* Tm = sT[b2];
-        // every LDS operand of the step first, in one batch: a single wait instead of one per level
-        bf16x8 kfr[4][KBF], tfr[6], ktf[HB][2];
-        bf16x4 vfr[4];
+    struct Ops {
+      bf16x8 wf[4][KBF], kt[HB][2];
+      f32x4 u[4];
+    };
+    auto read_ops = [&](int s, Ops& op) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
+      for (int ti = 0; ti < 4; ++ti) {
 #pragma unroll
-          for (int kb = 0; kb < KBF; ++kb) kfr[i][kb] = acc_frag(K + (16 * i + lq) * PK + 32 * kb);
-          vfr[i] = read_tr16_rows<bf16x4>(sV[b2], PV, 16 * i, 0);
-        }
-        tfr[0] = acc_frag(Tm + lq * PT);
-        tfr[1] = acc_frag(Tm + (16 + lq) * PT);
-        tfr[2] = acc_frag(Tm + (32 + lq) * PT);
-        tfr[3] = acc_frag(Tm + (32 + lq) * PT + 32);
-        tfr[4] = acc_frag(Tm + (48 + lq) * PT);
-        tfr[5] = acc_frag(Tm + (48 + lq) * PT + 32);
-#pragma unroll
-        for (int m = 0; m < HB; ++m)
-#pragma unroll
-          for (int pr = 0; pr < 2; ++pr) {  // K^T: column 16 m + lq of token rows 32 pr + 4 g (+16)
-            const bf16x4 lo = read_tr16_rows<bf16x4>(K, PK, 32 * pr, 16 * m);
-            const bf16x4 hi = read_tr16_rows<bf16x4>(K, PK, 32 * pr + 16, 16 * m);
-            ktf[m][pr] = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
-          }
-        __builtin_amdgcn_sched_barrier(0);
-
-        AB hb[KBF];
-#pragma unroll
-        for (int kb = 0; kb < KBF; ++kb) hb[kb] = Acc<E>::pack(hreg[2 * kb], hreg[2 * kb + 1]);
-#pragma unroll
-        for (int m = 0; m < HB; ++m) {
-          bf16x4 w4;
-#pragma unroll
-          for (int r = 0; r < 4; ++r) w4[r] = (__bf16)hreg[m][r];
-          *reinterpret_cast<bf16x4*>(&sHo[b2][lq * PK + 16 * m + 4 * g]) = w4;
-        }
-        f32x4 rr[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          f32x4 kh = zero4();
-#pragma unroll
-          for (int kb = 0; kb < KBF; ++kb) kh = mfma_bf16(kfr[i][kb], hb[kb].v, kh);
-#pragma unroll
-          for (int r = 0; r < 4; ++r) rr[i][r] = (float)vfr[i][r] - kh[r];
-        }
-        const AB rb0 = Acc<E>::pack(rr[0], rr[1]);
-        const AB rb1 = Acc<E>::pack(rr[2], rr[3]);
-        f32x4 dl[4];
-        dl[0] = mfma_bf16(tfr[0], rb0.v, zero4());
-        dl[1] = mfma_bf16(tfr[1], rb0.v, zero4());
-        dl[2] = mfma_bf16(tfr[3], rb1.v, mfma_bf16(tfr[2], rb0.v, zero4()));
-        dl[3] = mfma_bf16(tfr[5], rb1.v, mfma_bf16(tfr[4], rb0.v, zero4()));
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          bf16x4 w4;
-#pragma unroll
-          for (int r = 0; r < 4; ++r) w4[r] = (__bf16)dl[i][r];
-          *reinterpret_cast<bf16x4*>(&sDo[b2][lq * PT + 16 * i + 4 * g]) = w4;
-        }
-        const AB db[2] = {Acc<E>::pack(dl[0], dl[1]), Acc<E>::pack(dl[2], dl[3])};
-#pragma unroll
-        for (int m = 0; m < HB; ++m)
-#pragma unroll
-          for (int pr = 0; pr < 2; ++pr) hreg[m] = mfma_bf16(ktf[m][pr], db[pr].v, hreg[m]);
+        for (int kb = 0; kb < KBF; ++kb) op.wf[ti][kb] = frag_at(sW[s], ti * KBF + kb);
+        op.u[ti] = *reinterpret_cast<const f32x4*>(&sU[s][(ti * 64 + l) * 4]);
       }
-      __syncthreads();
+#pragma unroll
+      for (int m = 0; m < HB; ++m)
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb) op.kt[m][kb] = frag_at(sKt[s], m * 2 + kb);
+    };
+    // Chunk c may run once its operands are staged and its state slot has been read by the helper
+    // of c - NSL. The flags of chunk c are fetched one step early; only when they are not yet set
+    // does the chain poll.
+    auto ready = [&](int c, int st, int cs) {
+      const int s = c % NSL;
+      if (st < c || cs < c - NSL) {
+        flag_wait(&staged[s], c);
+        flag_wait(&consumed[s], c - NSL);
+      }
+    };
+
+    Ops cur;
+    ready(0, -1, -1 - NSL);
+    read_ops(0, cur);
+    for (int it = 0; it < nc; ++it) {
+      const int s = it % NSL, s2 = (it + 1) % NSL;
+      const int st_next = flag_peek(&staged[s2]), cs_next = flag_peek(&consumed[s2]);
+      bf16x8 hb[KBF];
+#pragma unroll
+      for (int kb = 0; kb < KBF; ++kb) hb[kb] = pack_acc(hreg[2 * kb], hreg[2 * kb + 1]);
+#pragma unroll
+      for (int kb = 0; kb < KBF; ++kb) {  // H^T rows: value column lq, dk 32 kb + 4 g (+16)
+        *reinterpret_cast<bf16x4*>(&sHo[s][lq * PK + 32 * kb + 4 * g]) = __builtin_shufflevector(hb[kb], hb[kb], 0, 1, 2, 3);
+        *reinterpret_cast<bf16x4*>(&sHo[s][lq * PK + 32 * kb + 16 + 4 * g]) =
+            __builtin_shufflevector(hb[kb], hb[kb], 4, 5, 6, 7);
+      }
+      f32x4 dt[4];
+#pragma unroll
+      for (int ti = 0; ti < 4; ++ti) {
+        f32x4 acc = cur.u[ti];
+#pragma unroll
+        for (int kb = 0; kb < KBF; ++kb) acc = mfma_bf16(cur.wf[ti][kb], hb[kb], acc);
+        dt[ti] = acc;
+      }
+      const bf16x8 db[2] = {pack_acc(dt[0], dt[1]), pack_acc(dt[2], dt[3])};
+      put_frag(sD[s], 0, db[0]);
+      put_frag(sD[s], 1, db[1]);
+      bf16x8 kt[HB][2];
+#pragma unroll
+      for (int m = 0; m < HB; ++m)
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb) kt[m][kb] = cur.kt[m][kb];
+      flag_release(&done, it);
+      // the next chunk's operands load while this chunk's state update runs
+      if (it + 1 < nc) {
+        ready(it + 1, st_next, cs_next);
+        read_ops(s2, cur);
+      }
+#pragma unroll
+      for (int m = 0; m < HB; ++m)
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb) hreg[m] = mfma_bf16(kt[m][kb], db[kb], hreg[m]);
     }
 #pragma unroll
     for (int m = 0; m < HB; ++m)
@@ -911,136 +970,183 @@ __global__ __launch_bounds__(512) void delta_chain_bf16_kernel(const TIn* __rest
     return;
   }
 
-  // ---- helpers: one chunk in flight each ----
+  // ---- helpers: one chunk each, NH chunks in flight ----
   const int hj = wave - 1;
-  NR qn[4][N::NREG], kn[4][N::NREG];
-  u32x4 tseg[TSEG];
-  bf16x4 vn[4];
+  E* myK = hK[hj];
+  E* myV = hV[hj];
+  // Buffer resources over this (b, h)'s rows: 32-bit offsets from a scalar base; reads past the
+  // sequence's last token return zeros and stores there are dropped.
+  const unsigned head_bytes = (unsigned)(((size_t)(T - 1) * rstride + DK) * sizeof(TIn));
+  auto rsrc = [](const void* base, unsigned bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+  };
+  const __amdgpu_buffer_rsrc_t rq = rsrc(q + bh_base, head_bytes), rk = rsrc(k + bh_base, head_bytes);
+  const __amdgpu_buffer_rsrc_t rv = rsrc(v + bh_base + v0, head_bytes - v0 * (unsigned)sizeof(TIn));
+  const __amdgpu_buffer_rsrc_t ro = rsrc(o + bh_base + v0, head_bytes - v0 * (unsigned)sizeof(TIn));
+  const __amdgpu_buffer_rsrc_t rt = rsrc(tmat + (size_t)bh * nc * kChunkT, (unsigned)(nc * kChunkT * 2));
+  const __amdgpu_buffer_rsrc_t ra = rsrc(active != nullptr ? active + (size_t)b * T : active, (unsigned)T);
+  const unsigned row_bytes = (unsigned)(rstride * sizeof(TIn));
+  // K rows: 64 / KSEG rows per wave instruction, lane l on row l / KSEG, physical segment l % KSEG
+  auto kswz = [](int row) { return KSEG == 8 ? ((((row >> 1) & 3) << 1) | ((row >> 3) & 1)) : ((row >> 2) & 3); };
+  // lane offsets: row lq, features 4 g (q, o); row lq, T tile columns 4 g; the direct-load segments
+  // (K: for even and odd instructions, whose rows differ in the swizzle's row-bit 3)
+  const unsigned off_q = (unsigned)lq * row_bytes + 8u * g;
+  const unsigned off_t = (unsigned)(lq * 16 + 4 * g) * 2u;
+  const unsigned off_k0 = (unsigned)(l / KSEG) * row_bytes + 16u * (unsigned)((l % KSEG) ^ kswz(l / KSEG));
+  const unsigned off_k1 = (unsigned)(l / KSEG) * row_bytes + 16u * (unsigned)((l % KSEG) ^ kswz(64 / KSEG + l / KSEG));
+  const unsigned off_v = (unsigned)(l >> 1) * row_bytes + 16u * (unsigned)(l & 1);
+
+  // Q in the Q^T accumulator layout, qa[J][I] = Q[16 J + lq][16 I + 4 g .. + 3], for two chunks: the
+  // one being formed and written, and the one whose loads are in flight
+  bf16x4 qa0[4][HB], qa1[4][HB];
+  bf16x4 tl[kTiles];  // the compact T tiles: row lq, columns 4 g .. + 3
   uint8_t actraw[4];
-  NR qo[4][N::NREG];  // Q of the staged chunk, kept for its output while the next loads fly
-  AB pt[6];
+  bf16x8 pt[6];       // P^T per (key block, query tile): (0,0) (0,1) (0,2) (1,2) (0,3) (1,3)
   uint8_t actk[4];
 
-  // Rows of one (b, h) from a uniform base with 32-bit lane offsets (the host keeps T*H*DK < 2^31).
-  // Every load is unconditional (rows past the chunk's end re-read its last row and are zeroed when
-  // staged): a load under a branch made the compiler wait for the earlier loads of the batch.
-  auto load_rows = [&](NR (&dst)[4][N::NREG], const TIn* base, int c) {
-    const int nvc = min(kChunk, T - c * kChunk);
-    const TIn* cb = base + bh_base + (size_t)c * kChunk * rstride;
+  // K rows and the V slice go straight into the helper's LDS tiles; Q, T and the active flags into
+  // registers. The tiles are zeroed once first, so no uninitialised LDS is ever read.
+  for (int i = l; i < 64 * DK / 8; i += 64) *reinterpret_cast<bf16x8*>(&myK[8 * i]) = bf16x8{};
+  for (int i = l; i < 64 * BV / 8; i += 64) *reinterpret_cast<bf16x8*>(&myV[8 * i]) = bf16x8{};
+  __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the zeros land before any direct load
+  auto issue_loads = [&](int c, bf16x4 (&qa)[4][HB]) {
+    const unsigned cb = (unsigned)c * kChunk * row_bytes;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const unsigned tok = (unsigned)min(16 * i + lq, nvc - 1);
+    for (int j = 0; j < KSEG; ++j)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (__attribute__((address_space(3))) void*)&myK[512 * j], 16,
+                                               (j & 1) ? off_k1 : off_k0, cb + (unsigned)j * (64 / KSEG) * row_bytes, 0, 0);
 #pragma unroll
-      for (int sgi = 0; sgi < N::NREG; ++sgi)
-        dst[i][sgi] = *reinterpret_cast<const NR*>(cb + (tok * (unsigned)rstride + (unsigned)N::feat(sgi)));
-    }
-  };
-  auto issue_loads = [&](int c) {
-    load_rows(qn, q, c);
-    load_rows(kn, k, c);
-    const u32x4* ts = reinterpret_cast<const u32x4*>(tmat + ((size_t)bh * nc + c) * kChunkT);
-#pragma unroll
-    for (int j = 0; j < TSEG; ++j) tseg[j] = ts[l + 64 * j];
-    const int nvc = min(kChunk, T - c * kChunk);
-    const TIn* cb = v + bh_base + (size_t)c * kChunk * rstride + v0;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const unsigned tok = (unsigned)min(16 * i + lq, nvc - 1);
-      vn[i] = *reinterpret_cast<const bf16x4*>(cb + (tok * (unsigned)rstride + 4u * (unsigned)g));
-    }
-    if (active != nullptr) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int tok = min(16 * i + lq, nvc - 1);
-        actraw[i] = active[(size_t)b * T + (size_t)c * kChunk + tok];
-      }
-    }
-  };
-  auto store_chunk = [&](int c) {
-    const int b2 = c & 1;
-    const int nvc = min(kChunk, T - c * kChunk);
-    if (nvc < kChunk) {  // the sequence's last, partial chunk: rows past its end stage as zeros
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        if (16 * i + lq >= nvc) {
-#pragma unroll
-          for (int sgi = 0; sgi < N::NREG; ++sgi) kn[i][sgi] = qn[i][sgi] = NR{};
-          vn[i] = bf16x4{};
-        }
-      }
-    }
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int tok = 16 * i + lq;
-#pragma unroll
-      for (int sgi = 0; sgi < N::NREG; ++sgi) *reinterpret_cast<NR*>(&sK[b2][tok * PK + N::feat(sgi)]) = kn[i][sgi];
-      *reinterpret_cast<bf16x4*>(&sV[b2][tok * PV + 4 * g]) = vn[i];
-      actk[i] = (tok < nvc && (active == nullptr || actraw[i] != 0)) ? 1 : 0;
-    }
-#pragma unroll
-    for (int j = 0; j < TSEG; ++j) {
-      const int el = (l + 64 * j) * 8;
-      const int t = el / kTileElems, within = el - t * kTileElems;
-      const int ti = (t >= 1) + (t >= 3) + (t >= 6), tj = t - ti * (ti + 1) / 2;
-      const int row = 16 * ti + within / 16, col = 16 * tj + within % 16;
-      *reinterpret_cast<u32x4*>(&sT[b2][row * PT + col]) = tseg[j];
-    }
-    // P^T tiles (key tile jj, query tile ii), keys after the query masked, packed per k-block
-    auto ptile = [&](int jj, int ii) {
-      const f32x4 acc = N::mma(kn[jj], qn[ii], zero4());
-      f32x4 r4;
-#pragma unroll
-      for (int r = 0; r < 4; ++r) r4[r] = (16 * jj + 4 * g + r <= 16 * ii + lq) ? acc[r] : 0.f;
-      return r4;
-    };
-    pt[0] = Acc<E>::pack(ptile(0, 0), zero4());
-    pt[1] = Acc<E>::pack(ptile(0, 1), ptile(1, 1));
-    pt[2] = Acc<E>::pack(ptile(0, 2), ptile(1, 2));
-    pt[3] = Acc<E>::pack(ptile(2, 2), zero4());
-    pt[4] = Acc<E>::pack(ptile(0, 3), ptile(1, 3));
-    pt[5] = Acc<E>::pack(ptile(2, 3), ptile(3, 3));
+    for (int j = 0; j < 2; ++j)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, (__attribute__((address_space(3))) void*)&myV[512 * j], 16, off_v,
+                                               cb + (unsigned)j * 32 * row_bytes, 0, 0);
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll
-      for (int sgi = 0; sgi < N::NREG; ++sgi) qo[i][sgi] = qn[i][sgi];
-  };
-  // O^T = H^T Q^T + Delta^T P^T for the four row blocks of chunk c: the H^T and Delta^T fragments
-  // are read from LDS once and serve all four blocks
-  auto write_output = [&](int c) {
-    const int b2 = c & 1;
-    const int nvc = min(kChunk, T - c * kChunk);
-    NR ho[N::NREG];
+      for (int m = 0; m < HB; ++m)
+        qa[i][m] = __builtin_bit_cast(bf16x4, __builtin_amdgcn_raw_buffer_load_b64(rq, off_q + 32u * m, cb + 16u * i * row_bytes, 0));
+    const unsigned tb = (unsigned)c * kChunkT * 2u;
 #pragma unroll
-    for (int sgi = 0; sgi < N::NREG; ++sgi) ho[sgi] = *reinterpret_cast<const NR*>(&sHo[b2][lq * PK + N::feat(sgi)]);
-    const bf16x8 d0 = acc_frag(&sDo[b2][lq * PT]);
-    const bf16x8 d1 = acc_frag(&sDo[b2][lq * PT + 32]);
-    __builtin_amdgcn_sched_barrier(0);
+    for (int t = 0; t < kTiles; ++t)
+      tl[t] = __builtin_bit_cast(bf16x4, __builtin_amdgcn_raw_buffer_load_b64(rt, off_t + 512u * t, tb, 0));
+    if (active != nullptr) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      f32x4 acc = N::mma(ho, qo[i], zero4());
-      acc = mfma_bf16(d0, pt[i == 0 ? 0 : (i == 1 ? 1 : (i == 2 ? 2 : 4))].v, acc);
-      if (i >= 2) acc = mfma_bf16(d1, pt[i == 2 ? 3 : 5].v, acc);
-      const int tok = 16 * i + lq;
-      if (tok < nvc) {
-        TIn* dst = o + bh_base + (size_t)c * kChunk * rstride + v0 + (tok * rstride + 4 * g);
-        const bool on = actk[i] != 0;
-        typedef TIn O4 __attribute__((ext_vector_type(4)));
-        O4 w4;
-#pragma unroll
-        for (int r = 0; r < 4; ++r) w4[r] = from_f32<TIn>(on ? acc[r] : 0.f);
-        *reinterpret_cast<O4*>(dst) = w4;  // 8 bytes: the host keeps o 8-byte aligned
-      }
+      for (int i = 0; i < 4; ++i) actraw[i] = __builtin_amdgcn_raw_buffer_load_b8(ra, (unsigned)(16 * i + lq), (unsigned)c * kChunk, 0);
     }
   };
 
-  if (hj < nc) issue_loads(hj);
-  for (int it = -1; it <= nc; ++it) {
-    const int cs = it + 1, co = it - 1;
-    if (cs < nc && cs % NH == hj) store_chunk(cs);
-    // the iteration between staging and output: loads of the chunk seven on
-    if (it >= 0 && it % NH == hj && it + NH < nc) issue_loads(it + NH);
-    if (co >= 0 && co % NH == hj) write_output(co);
-    __syncthreads();
+  // element offset of (row, column) in a helper's K tile: unpadded rows, 16-byte segments XOR-swizzled
+  // by row bits so that both the row-fragment and the transposed reads spread over the 64 banks
+  auto kat = [&](int row, int col) { return row * DK + (((col >> 3) ^ kswz(row)) << 3) + (col & 7); };
+  auto kfrag = [&](int row, int kb) {  // the Acc-layout A fragment of K row `row`, dk block kb
+    return join4(*reinterpret_cast<const bf16x4*>(&myK[kat(row, 32 * kb + 4 * g)]),
+                 *reinterpret_cast<const bf16x4*>(&myK[kat(row, 32 * kb + 16 + 4 * g)]));
+  };
+  auto ktr = [&](int r0, int m) {  // column 16 m + lq of token rows r0 + 4 g .. + 3 (transposed read)
+    return read_tr16<bf16x4>(&myK[kat(r0 + 4 * g + (lq >> 2), 16 * m + 4 * (lq & 3))]);
+  };
+
+  // Chunk c's operands into state slot c % NSL (once the chain is done with the slot's previous
+  // chunk); P^T kept in registers for the output
+  auto form = [&](int c, const bf16x4 (&qa)[4][HB]) {
+    const int nvc = min(kChunk, T - c * kChunk);
+    const int s = c % NSL;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) actk[i] = (16 * i + lq < nvc && (active == nullptr || actraw[i] != 0)) ? 1 : 0;
+    // the direct loads of K and V count as outstanding vector loads until they have written LDS
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+    wave_sync();
+    // token-major operands: ktf[m][kb] = column 16 m + lq of token rows 32 kb + 4 g (+16)
+    bf16x8 ktf[HB][2], vtf[2];
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) {
+#pragma unroll
+      for (int m = 0; m < HB; ++m) ktf[m][kb] = join4(ktr(32 * kb, m), ktr(32 * kb + 16, m));
+      vtf[kb] = join4(read_tr16_rows<bf16x4>(myV, BV, 32 * kb, 0), read_tr16_rows<bf16x4>(myV, BV, 32 * kb + 16, 0));
+    }
+    // P^T = tril(K Q^T)^T tiles (key tile jj, query tile ii); only diagonal tiles hold keys after the query
+    auto ptile = [&](int jj, int ii) {
+      f32x4 acc = zero4();
+#pragma unroll
+      for (int kb = 0; kb < KBF; ++kb) acc = mfma_bf16(kfrag(16 * jj + lq, kb), join4(qa[ii][2 * kb], qa[ii][2 * kb + 1]), acc);
+      if (jj == ii) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) acc[r] = (4 * g + r <= lq) ? acc[r] : 0.f;
+      }
+      return acc;
+    };
+    pt[0] = pack_acc(ptile(0, 0), zero4());
+    pt[1] = pack_acc(ptile(0, 1), ptile(1, 1));
+    pt[2] = pack_acc(ptile(0, 2), ptile(1, 2));
+    pt[3] = pack_acc(ptile(2, 2), zero4());
+    pt[4] = pack_acc(ptile(0, 3), ptile(1, 3));
+    pt[5] = pack_acc(ptile(2, 3), ptile(3, 3));
+    // T's operand fragments (row tile, token block): (0,0) (1,0) (2,0) (2,1) (3,0) (3,1)
+    const bf16x4 z4{};
+    const bf16x8 tf[6] = {join4(tl[0], z4), join4(tl[1], tl[2]), join4(tl[3], tl[4]),
+                          join4(tl[5], z4), join4(tl[6], tl[7]), join4(tl[8], tl[9])};
+    flag_wait<4>(&done, c - NSL);  // the chain is done with the slot's previous chunk
+    // W^T = K^T T^T (dk tile m, token tile ti): its tile pairs over dk are the chain's -W operand
+#pragma unroll
+    for (int ti = 0; ti < 4; ++ti) {
+      const int f0 = ti == 0 ? 0 : (ti == 1 ? 1 : (ti == 2 ? 2 : 4));
+      f32x4 wt[HB];
+#pragma unroll
+      for (int m = 0; m < HB; ++m) {
+        wt[m] = mfma_bf16(ktf[m][0], tf[f0], zero4());
+        if (ti >= 2) wt[m] = mfma_bf16(ktf[m][1], tf[f0 + 1], wt[m]);
+      }
+#pragma unroll
+      for (int kb = 0; kb < KBF; ++kb) put_frag(sW[s], ti * KBF + kb, pack_acc(wt[2 * kb], wt[2 * kb + 1], -1.f));
+      // U = T V (token tile ti), in the accumulator layout of Delta
+      f32x4 u = mfma_bf16(tf[f0], vtf[0], zero4());
+      if (ti >= 2) u = mfma_bf16(tf[f0 + 1], vtf[1], u);
+      *reinterpret_cast<f32x4*>(&sU[s][(ti * 64 + l) * 4]) = u;
+    }
+#pragma unroll
+    for (int m = 0; m < HB; ++m)
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb) put_frag(sKt[s], m * 2 + kb, ktf[m][kb]);
+    flag_release(&staged[s], c);
+  };
+
+  // O^T = H^T Q^T + Delta^T P^T for chunk c, from state slot c % NSL; rows past the sequence's end
+  // fall outside the output's buffer range and are dropped
+  auto write_output = [&](int c, const bf16x4 (&qa)[4][HB]) {
+    const int s = c % NSL;
+    bf16x8 hf[KBF];
+#pragma unroll
+    for (int kb = 0; kb < KBF; ++kb) hf[kb] = acc_frag(&sHo[s][lq * PK + 32 * kb]);
+    const bf16x8 d0 = frag_at(sD[s], 0), d1 = frag_at(sD[s], 1);
+    flag_release(&consumed[s], c);  // after the reads above: the chain may reuse the slot
+    const unsigned cb = (unsigned)c * kChunk * row_bytes;
+#pragma unroll
+    for (int J = 0; J < 4; ++J) {
+      const int p0 = J == 0 ? 0 : (J == 1 ? 1 : (J == 2 ? 2 : 4));
+      f32x4 acc = mfma_bf16(d0, pt[p0], zero4());
+      if (J >= 2) acc = mfma_bf16(d1, pt[p0 + 1], acc);
+#pragma unroll
+      for (int kb = 0; kb < KBF; ++kb) acc = mfma_bf16(hf[kb], join4(qa[J][2 * kb], qa[J][2 * kb + 1]), acc);
+      const bool on = actk[J] != 0;
+      typedef TIn O4 __attribute__((ext_vector_type(4)));
+      O4 w4;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) w4[r] = from_f32<TIn>(on ? acc[r] : 0.f);
+      __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, w4), ro, off_q, cb + 16u * J * row_bytes, 0);
+    }
+  };
+
+  // chunk c: form its operands, issue the loads of chunk c + NH (their latency hidden behind the
+  // wait for the chain), then write its output
+  auto run = [&](int c, const bf16x4 (&qc)[4][HB], bf16x4 (&qn)[4][HB]) {
+    form(c, qc);
+    if (c + NH < nc) issue_loads(c + NH, qn);
+    flag_wait<4>(&done, c);
+    write_output(c, qc);
+  };
+  if (hj < nc) issue_loads(hj, qa0);
+  for (int c = hj; c < nc; c += 2 * NH) {
+    run(c, qa0, qa1);
+    if (c + NH < nc) run(c + NH, qa1, qa0);
   }
 }
 

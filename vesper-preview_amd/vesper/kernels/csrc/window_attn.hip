@@ -49,15 +49,6 @@ __device__ __forceinline__ typename Mma<T>::V4 read_tr(const T* p) {
   return read_tr16<typename Mma<T>::V4>(p);
 }
 
-// 16 bytes per lane from global memory straight into LDS (global_load_lds_dwordx4): lane i writes
-// lds + 16 i, so `lds` must be the same for the whole wave. Device pass only: the host pass of a
-// kernel template does not take the builtin.
-__device__ __forceinline__ void load_lds16(const void* src, void* lds) {
-#if defined(__HIP_DEVICE_COMPILE__)
-  __builtin_amdgcn_global_load_lds(src, lds, 16, 0, 0);
-#endif
-}
-
 // max over the four lanes l, l ^ 16, l ^ 32, l ^ 48 (the four lane groups of one query)
 __device__ __forceinline__ float max_over_groups(float x) {
   const auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
