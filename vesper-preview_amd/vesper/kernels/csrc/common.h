@@ -163,12 +163,36 @@ __device__ __forceinline__ V4 read_tr16_rows(const T* tile, int pitch, int r0, i
   return read_tr16<V4>(tile + (r0 + 4 * g + (lq >> 2)) * pitch + c0 + 4 * (lq & 3));
 }
 
+// a.x * b.x + a.y * b.y + c on a pair of 16-bit values, accumulated in fp32 (v_dot2).
+template <typename T> struct Dot2;
+template <> struct Dot2<__bf16> {
+  typedef __bf16 P2 __attribute__((ext_vector_type(2)));
+  __device__ __forceinline__ static float run(P2 a, P2 b, float c) { return __builtin_amdgcn_fdot2_f32_bf16(a, b, c, false); }
+};
+template <> struct Dot2<_Float16> {
+  typedef _Float16 P2 __attribute__((ext_vector_type(2)));
+  __device__ __forceinline__ static float run(P2 a, P2 b, float c) { return __builtin_amdgcn_fdot2(a, b, c, false); }
+};
+
 // 16 bytes per lane from global memory straight into LDS (global_load_lds_dwordx4): lane i writes
 // lds + 16 i, so `lds` must be the same for the whole wave. Device pass only: the host pass of a
 // kernel template does not take the builtin.
 __device__ __forceinline__ void load_lds16(const void* src, void* lds) {
 #if defined(__HIP_DEVICE_COMPILE__)
   __builtin_amdgcn_global_load_lds(src, lds, 16, 0, 0);
+#endif
+}
+
+// Buffer resources (raw, stride 0) over `bytes` bytes from `base`: 32-bit offsets from a scalar
+// base, reads past the range return zeros and writes there are dropped.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* base, unsigned bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+}
+// 16 bytes per lane from a buffer straight into LDS: lane i writes lds + 16 i (`lds` wave-uniform).
+// Device pass only, like load_lds16: the host pass of a kernel template does not take the builtin.
+__device__ __forceinline__ void buffer_load_lds16(__amdgpu_buffer_rsrc_t r, void* lds, unsigned voff, unsigned soff) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 16, voff, soff, 0, 0);
 #endif
 }
 

@@ -30,17 +30,6 @@ namespace {
 
 constexpr int kMaxGroup = 8;
 
-// Dot product of eight 16-bit pairs accumulated in fp32 (v_dot2 on bf16 or f16 pairs).
-template <typename T> struct Dot2;
-template <> struct Dot2<__bf16> {
-  typedef __bf16 P2 __attribute__((ext_vector_type(2)));
-  __device__ __forceinline__ static float run(P2 a, P2 b, float c) { return __builtin_amdgcn_fdot2_f32_bf16(a, b, c, false); }
-};
-template <> struct Dot2<_Float16> {
-  typedef _Float16 P2 __attribute__((ext_vector_type(2)));
-  __device__ __forceinline__ static float run(P2 a, P2 b, float c) { return __builtin_amdgcn_fdot2(a, b, c, false); }
-};
-
 // GM: the query heads per KV head rounded up to a power of two (register arrays are sized by it);
 // wide groups take fewer keys per thread so the per-head softmax states still fit in registers.
 template <typename T, int D, int GM>

@@ -977,9 +977,7 @@ __global__ __launch_bounds__(512) void delta_chain_bf16_kernel(const TIn* __rest
   // Buffer resources over this (b, h)'s rows: 32-bit offsets from a scalar base; reads past the
   // sequence's last token return zeros and stores there are dropped.
   const unsigned head_bytes = (unsigned)(((size_t)(T - 1) * rstride + DK) * sizeof(TIn));
-  auto rsrc = [](const void* base, unsigned bytes) {
-    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
-  };
+  auto rsrc = [](const void* base, unsigned bytes) { return buffer_rsrc(base, bytes); };
   const __amdgpu_buffer_rsrc_t rq = rsrc(q + bh_base, head_bytes), rk = rsrc(k + bh_base, head_bytes);
   const __amdgpu_buffer_rsrc_t rv = rsrc(v + bh_base + v0, head_bytes - v0 * (unsigned)sizeof(TIn));
   const __amdgpu_buffer_rsrc_t ro = rsrc(o + bh_base + v0, head_bytes - v0 * (unsigned)sizeof(TIn));
@@ -1013,12 +1011,10 @@ __global__ __launch_bounds__(512) void delta_chain_bf16_kernel(const TIn* __rest
     const unsigned cb = (unsigned)c * kChunk * row_bytes;
 #pragma unroll
     for (int j = 0; j < KSEG; ++j)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (__attribute__((address_space(3))) void*)&myK[512 * j], 16,
-                                               (j & 1) ? off_k1 : off_k0, cb + (unsigned)j * (64 / KSEG) * row_bytes, 0, 0);
+      buffer_load_lds16(rk, &myK[512 * j], (j & 1) ? off_k1 : off_k0, cb + (unsigned)j * (64 / KSEG) * row_bytes);
 #pragma unroll
     for (int j = 0; j < 2; ++j)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, (__attribute__((address_space(3))) void*)&myV[512 * j], 16, off_v,
-                                               cb + (unsigned)j * 32 * row_bytes, 0, 0);
+      buffer_load_lds16(rv, &myV[512 * j], off_v, cb + (unsigned)j * 32 * row_bytes);
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll

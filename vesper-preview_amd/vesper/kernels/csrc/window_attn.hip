@@ -49,12 +49,16 @@ __device__ __forceinline__ typename Mma<T>::V4 read_tr(const T* p) {
   return read_tr16<typename Mma<T>::V4>(p);
 }
 
+// IEEE maximum (NaN-propagating): v_maximum3_f32 / v_maximum_f32, which need no operand
+// canonicalisation, unlike fmaxf's v_max_f32
+__device__ __forceinline__ float fmax_ieee(float a, float b) { return __builtin_elementwise_maximum(a, b); }
+
 // max over the four lanes l, l ^ 16, l ^ 32, l ^ 48 (the four lane groups of one query)
 __device__ __forceinline__ float max_over_groups(float x) {
   const auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  x = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  x = fmax_ieee(__uint_as_float(a[0]), __uint_as_float(a[1]));
   const auto c = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  return fmaxf(__uint_as_float(c[0]), __uint_as_float(c[1]));
+  return fmax_ieee(__uint_as_float(c[0]), __uint_as_float(c[1]));
 }
 
 template <typename T, int D>
@@ -136,22 +140,29 @@ __global__ __launch_bounds__(256, D >= 128 ? 2 : 4) void window_attn_kernel(cons
   const T* kbase = keys + ((size_t)b * S * HKV + kvh) * D;
   const T* vbase = values + ((size_t)b * S * HKV + kvh) * D;
 
-  // staging of one 64-key tile; keys past klast re-read key klast - 1 (masked in the scores, weight 0
-  // in the output)
+  // staging of one 64-key tile. At D >= 64 through buffer resources over the (b, KV head) rows:
+  // each lane's offset within a tile is fixed (computed once), rows past the last key read zeros,
+  // and keys past klast that do load are masked in the scores (weight 0 in the output). Narrower
+  // heads: keys past klast re-read key klast - 1.
   V8 kreg[kDirect ? 1 : NI], vreg[kDirect ? 1 : NI];
+  const unsigned kv_bytes = (unsigned)(((size_t)(S - 1) * kv_row + D) * sizeof(T));
+  const __amdgpu_buffer_rsrc_t rk = buffer_rsrc(kbase, kv_bytes), rv = buffer_rsrc(vbase, kv_bytes);
+  unsigned lane_off[kDirect ? NI : 1];
+#pragma unroll
+  for (int j = 0; j < (kDirect ? NI : 1); ++j) {
+    const int pos = (w + 4 * j) * 64 + l;  // padded segment position in the tile
+    const int row = pos / PSEG, seg = pos - row * PSEG;
+    lane_off[j] = (unsigned)(row * kv_row + 8 * (seg < SEG ? seg : 0)) * (unsigned)sizeof(T);
+  }
   auto fetch = [&](int k0, int buf) {
 #pragma unroll
     for (int j = 0; j < NI; ++j) {
       if constexpr (kDirect) {
         const int ins = w + 4 * j;  // this wave's j-th instruction of the tile
         if (ins < NINS) {
-          const int pos = ins * 64 + l;  // padded segment position in the tile
-          const int row = pos / PSEG;
-          int seg = pos - row * PSEG;
-          seg = seg < SEG ? seg : 0;
-          const size_t goff = (size_t)min(k0 + row, klast - 1) * kv_row + 8 * seg;
-          load_lds16(kbase + goff, &sK[buf][ins * 64 * 8]);
-          load_lds16(vbase + goff, &sV[buf][ins * 64 * 8]);
+          const unsigned toff = (unsigned)((size_t)k0 * kv_row * sizeof(T));
+          buffer_load_lds16(rk, &sK[buf][ins * 64 * 8], lane_off[j], toff);
+          buffer_load_lds16(rv, &sV[buf][ins * 64 * 8], lane_off[j], toff);
         }
       } else {
         const int sg = threadIdx.x + 256 * j;
@@ -224,44 +235,56 @@ __global__ __launch_bounds__(256, D >= 128 ? 2 : 4) void window_attn_kernel(cons
         }
       }
       V8 pb[QB][2];
+      // both query blocks' maxima first, then one wave-uniform decision on rescaling, so that the
+      // exponentials of the two blocks form one stretch of independent work
+      float mt[QB];
 #pragma unroll
       for (int qb = 0; qb < QB; ++qb) {
         if (!full) {
-          const int qidx = wlo + 16 * qb + lq;
+          // key k0 + 16 kb + 4 g + r is visible to query qidx iff 0 <= qidx - key < W; for every
+          // query that is stored, qidx < klast, so keys at or past klast are never visible
+          const int c0 = wlo + 16 * qb + lq - k0 - 4 * g;
 #pragma unroll
           for (int kb = 0; kb < 4; ++kb)
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-              const int key = k0 + 16 * kb + 4 * g + r;
-              const bool vis = key < klast && key <= qidx && key > qidx - W;
+              const bool vis = (unsigned)(c0 - 16 * kb - r) < (unsigned)W;
               sacc[qb][kb][r] = vis ? sacc[qb][kb][r] : -INFINITY;
             }
         }
-        float mt = sacc[qb][0][0];
+        mt[qb] = sacc[qb][0][0];
 #pragma unroll
         for (int kb = 0; kb < 4; ++kb)
 #pragma unroll
-          for (int r = 0; r < 4; ++r) mt = fmaxf(mt, sacc[qb][kb][r]);
-        mt = max_over_groups(mt) * scale_log2;
-        const bool need = mt > m_used[qb] + kLazy;
-        if (__builtin_amdgcn_ballot_w64(need)) {  // some query of the wave moves its maximum
-          const float mn = need ? mt : m_used[qb];
+          for (int r = 0; r < 4; ++r) mt[qb] = fmax_ieee(mt[qb], sacc[qb][kb][r]);
+      }
+      bool need[QB], any_need = false;
+#pragma unroll
+      for (int qb = 0; qb < QB; ++qb) {
+        mt[qb] = max_over_groups(mt[qb]) * scale_log2;
+        need[qb] = mt[qb] > m_used[qb] + kLazy;
+        any_need |= need[qb];
+      }
+      if (__builtin_amdgcn_ballot_w64(any_need)) {  // some query of the wave moves its maximum
+#pragma unroll
+        for (int qb = 0; qb < QB; ++qb) {
+          const float mn = need[qb] ? mt[qb] : m_used[qb];
           const float alpha = __builtin_amdgcn_exp2f(m_used[qb] - mn);
           l_run[qb] *= alpha;
 #pragma unroll
           for (int t = 0; t < DT; ++t) oacc[qb][t] *= alpha;
           m_used[qb] = mn;
         }
+      }
+      using P2 = typename Dot2<T>::P2;
+      const P2 one2 = {from_f32<T>(1.f), from_f32<T>(1.f)};
+#pragma unroll
+      for (int qb = 0; qb < QB; ++qb) {
         float p[4][4];
-        float psum = 0.f;
 #pragma unroll
         for (int kb = 0; kb < 4; ++kb)
 #pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            p[kb][r] = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[qb][kb][r], scale_log2, -m_used[qb]));
-            psum += p[kb][r];
-          }
-        l_run[qb] += psum;
+          for (int r = 0; r < 4; ++r) p[kb][r] = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[qb][kb][r], scale_log2, -m_used[qb]));
 #pragma unroll
         for (int ks = 0; ks < 2; ++ks)
 #pragma unroll
@@ -269,6 +292,14 @@ __global__ __launch_bounds__(256, D >= 128 ? 2 : 4) void window_attn_kernel(cons
             pb[qb][ks][j] = from_f32<T>(p[2 * ks][j]);
             pb[qb][ks][4 + j] = from_f32<T>(p[2 * ks + 1][j]);
           }
+        // the row sum of the probabilities as rounded for the P V product, two per v_dot2
+        float ps0 = 0.f, ps1 = 0.f;
+#pragma unroll
+        for (int j = 0; j < 8; j += 2) {
+          ps0 = Dot2<T>::run(P2{pb[qb][0][j], pb[qb][0][j + 1]}, one2, ps0);
+          ps1 = Dot2<T>::run(P2{pb[qb][1][j], pb[qb][1][j + 1]}, one2, ps1);
+        }
+        l_run[qb] += ps0 + ps1;
       }
       // O^T += V^T P^T: A fragments of V^T by transposed LDS reads (lane (lq, g) gets column
       // 16 t + lq of key rows 32 ks + 4 g .. +3 and 32 ks + 16 + 4 g .. +3)
@@ -325,6 +356,9 @@ int window_attn(const T* q, const T* keys, const T* values, T* o, const uint8_t*
   if ((reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(keys) | reinterpret_cast<uintptr_t>(values) |
        reinterpret_cast<uintptr_t>(o)) & 15)
     return fail(ERR_ARG, "%s: q, keys, values and o must be 16-byte aligned", who);
+  // one batch row's keys (all KV heads) are addressed with 32-bit byte offsets
+  if ((size_t)(M + N) * HKV * D * sizeof(T) >= ((size_t)1 << 32))
+    return fail(ERR_UNSUPPORTED, "%s: %d keys x %d KV heads x %d features exceed 4 GiB per batch row", who, M + N, HKV, D);
   const float scale_log2 = scale * 1.4426950408889634f;
   const int nqt = (N + 127) / 128;
   dim3 grid((unsigned)((size_t)nqt * H * B));
