@@ -13,7 +13,7 @@
 // (v_permlane16/32_swap) and the probabilities are already laid out as the B operand of
 // O^T += V^T P^T. V stays row-major in LDS; its transposed A fragments come from ds_read_b64_tr_b16.
 // At D >= 64 the tiles go from global memory straight into LDS (global_load_lds_dwordx4), with no
-// staging registers; rows carry one 16-byte pad segment against bank conflicts.
+// staging registers; K rows carry one 16-byte pad segment and V rows two, against bank conflicts.
 //
 // Softmax: exp2 with the scale folded into one FMA per score; the running maximum is only moved
 // when a tile's maximum exceeds it by more than kLazy (log2 units), so the O rescale runs about
@@ -75,16 +75,19 @@ __global__ __launch_bounds__(256, D >= 128 ? 2 : 4) void window_attn_kernel(cons
   constexpr int DT = DP / 16;          // 16-row tiles of O^T
   constexpr int KSQ = DP / 32;         // k steps over features
   constexpr int SEG = DP / 8;          // 16-byte segments per row
-  constexpr int PK = DP + 8;           // LDS pitch of K and V rows (elements): one pad segment
-  constexpr int PSEG = SEG + 1;        // 16-byte segments per padded row
+  // LDS pitches (elements) against bank conflicts on the 64 banks: K rows carry one 16-byte pad
+  // segment (the 16 rows of a 16-byte row-fragment read start 36 banks apart at D 64), V rows two
+  // (the 8 rows of a transposed read start 8, 24 or 40 banks apart and cover all 64 banks)
+  constexpr int PK = DP + 8, PSEG = SEG + 1;
+  constexpr int PV = DP + 16, PSEGV = SEG + 2;
   // At D >= 64 the tiles go from global memory straight into LDS: a wave instruction fills 1 KiB
   // of consecutive segments (pad segments re-read a real one and are never used); narrower heads,
   // whose rows need zero padding up to the MFMA k step, stage through registers.
   constexpr bool kDirect = D >= 64;
-  constexpr int NINS = KT * PSEG / 64;  // wave instructions per tile for K (and for V)
-  constexpr int NI = kDirect ? (NINS + 3) / 4 : (KT * SEG + 255) / 256;
+  constexpr int NINS = KT * PSEG / 64, NINSV = KT * PSEGV / 64;  // wave instructions per K, V tile
+  constexpr int NI = kDirect ? (NINSV + 3) / 4 : (KT * SEG + 255) / 256;
   __shared__ __align__(16) T sK[2][KT * PK];
-  __shared__ __align__(16) T sV[2][KT * PK];
+  __shared__ __align__(16) T sV[2][KT * PV];
 
   const int lg = xcd_logical_block(blockIdx.x, gridDim.x);
   const int qt = lg % nqt, bh = lg / nqt;
@@ -147,23 +150,23 @@ __global__ __launch_bounds__(256, D >= 128 ? 2 : 4) void window_attn_kernel(cons
   V8 kreg[kDirect ? 1 : NI], vreg[kDirect ? 1 : NI];
   const unsigned kv_bytes = (unsigned)(((size_t)(S - 1) * kv_row + D) * sizeof(T));
   const __amdgpu_buffer_rsrc_t rk = buffer_rsrc(kbase, kv_bytes), rv = buffer_rsrc(vbase, kv_bytes);
-  unsigned lane_off[kDirect ? NI : 1];
+  unsigned koff[kDirect ? NI : 1], voff[kDirect ? NI : 1];
 #pragma unroll
   for (int j = 0; j < (kDirect ? NI : 1); ++j) {
     const int pos = (w + 4 * j) * 64 + l;  // padded segment position in the tile
     const int row = pos / PSEG, seg = pos - row * PSEG;
-    lane_off[j] = (unsigned)(row * kv_row + 8 * (seg < SEG ? seg : 0)) * (unsigned)sizeof(T);
+    koff[j] = (unsigned)(row * kv_row + 8 * (seg < SEG ? seg : 0)) * (unsigned)sizeof(T);
+    const int rowv = pos / PSEGV, segv = pos - rowv * PSEGV;
+    voff[j] = (unsigned)(rowv * kv_row + 8 * (segv < SEG ? segv : 0)) * (unsigned)sizeof(T);
   }
   auto fetch = [&](int k0, int buf) {
 #pragma unroll
     for (int j = 0; j < NI; ++j) {
       if constexpr (kDirect) {
         const int ins = w + 4 * j;  // this wave's j-th instruction of the tile
-        if (ins < NINS) {
-          const unsigned toff = (unsigned)((size_t)k0 * kv_row * sizeof(T));
-          buffer_load_lds16(rk, &sK[buf][ins * 64 * 8], lane_off[j], toff);
-          buffer_load_lds16(rv, &sV[buf][ins * 64 * 8], lane_off[j], toff);
-        }
+        const unsigned toff = (unsigned)((size_t)k0 * kv_row * sizeof(T));
+        if (ins < NINS) buffer_load_lds16(rk, &sK[buf][ins * 64 * 8], koff[j], toff);
+        if (ins < NINSV) buffer_load_lds16(rv, &sV[buf][ins * 64 * 8], voff[j], toff);
       } else {
         const int sg = threadIdx.x + 256 * j;
         const int row = sg / SEG, part = sg - row * SEG;
@@ -189,7 +192,7 @@ __global__ __launch_bounds__(256, D >= 128 ? 2 : 4) void window_attn_kernel(cons
         if (sg < KT * SEG) {
           const int row = sg / SEG, part = sg - row * SEG;
           *reinterpret_cast<V8*>(&sK[buf][row * PK + 8 * part]) = kreg[j];
-          *reinterpret_cast<V8*>(&sV[buf][row * PK + 8 * part]) = vreg[j];
+          *reinterpret_cast<V8*>(&sV[buf][row * PV + 8 * part]) = vreg[j];
         }
       }
     }
@@ -307,9 +310,9 @@ __global__ __launch_bounds__(256, D >= 128 ? 2 : 4) void window_attn_kernel(cons
       for (int t = 0; t < DT; ++t) {
 #pragma unroll
         for (int ks = 0; ks < 2; ++ks) {
-          const T* base = Vt + (32 * ks + 4 * g + (lq >> 2)) * PK + 16 * t + 4 * (lq & 3);
+          const T* base = Vt + (32 * ks + 4 * g + (lq >> 2)) * PV + 16 * t + 4 * (lq & 3);
           const V4 lo = read_tr<T>(base);
-          const V4 hi = read_tr<T>(base + 16 * PK);
+          const V4 hi = read_tr<T>(base + 16 * PV);
           const V8 a = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
 #pragma unroll
           for (int qb = 0; qb < QB; ++qb) oacc[qb][t] = Mma<T>::run(a, pb[qb][ks], oacc[qb][t]);
