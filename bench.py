@@ -5,7 +5,8 @@ A step is one prefill pass of both mixers over one batch of synthetic input: the
 (B=8, T=4096, H=8, d=64; bf16 q/k/v/beta, fp32 state with S0 ~ N(0, 0.02^2), chunk 64) followed by
 sliding-window causal attention over the same batch shape (window 512, bf16). ``value`` is prefill
 tokens/s = B*T / (time of one step), inputs resident in HBM. Beside it the line carries each
-kernel's own rate at its own configuration (attention alone at B=4), the decode rate (256
+kernel's own rate at its own configuration (attention alone at B=4), the key filter that feeds the
+scan (B8 T4096 d512 = 8 heads of 64, 4 taps, bf16), the decode rate (256
 single-token steps of batch 64: fp32 delta update of S [64,8,64,64] then attention over a 512-entry
 bf16 KV ring, captured as one HIP graph), the looped column with per-token halting (B4 T2048 d512,
 8 passes), the roofline of the dominant kernel measured with HIP
@@ -37,6 +38,7 @@ B, T, H, D, WINDOW = 8, 4096, 8, 64, 512
 ATTN_B = 4
 DEC_B, DEC_W, DEC_STEPS = 64, 512, 256
 LOOP_B, LOOP_T, LOOP_D, LOOP_PASSES = 4, 2048, 512, 8
+KEY_D, KEY_TAPS = H * D, 4  # the key filter over the prefill batch: d = 8 heads of 64, 4 taps
 COPY_BYTES = 256 << 20  # the calibration copy of --traffic-probe
 
 
@@ -64,6 +66,11 @@ def attn_flops(b: int, t: int, h: int, d: int, w: int) -> float:
 
 def attn_bytes(b: int, t: int, h: int, hkv: int, d: int) -> float:
     return 2 * b * t * h * d * 2 + 2 * b * t * hkv * d * 2  # q, o; k, v
+
+
+def key_filter_bytes(b: int, t: int, d: int, taps: int, elem: int = 2) -> float:
+    """Key inputs read once, keys written once, plus the history rows and the taps (float32)."""
+    return 2.0 * b * t * d * elem + 4.0 * d * (b * (taps - 1) + taps)
 
 
 def decode_step_bytes(b: int, h: int, d: int, w: int) -> float:
@@ -142,6 +149,43 @@ def time_attention_config(torch, reps: int = 20) -> float:
         e1.record()
         torch.cuda.synchronize()
     return e0.elapsed_time(e1) / reps
+
+
+def time_key_filter(torch, reps: int = 50) -> float:
+    """Milliseconds per launch of the key filter at B8 T4096 d512 (8 heads of 64), 4 taps, bf16.
+
+    The launches are captured in one HIP graph and timed on replay: one launch (13 us) is about as
+    long as the host's per-call checks, so a timed loop of eager calls would measure the host.
+    """
+    from vesper.kernels.keys import fused_keys
+
+    dev = torch.device("cuda:0")
+    g = torch.Generator().manual_seed(4)
+    z = torch.randn(B, T, KEY_D, generator=g).to(dev, torch.bfloat16)
+    history = torch.randn(B, KEY_TAPS - 1, KEY_D, generator=g).to(dev)
+    taps = torch.randn(KEY_TAPS, KEY_D, generator=g).to(dev)
+    with torch.no_grad():
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            for _ in range(3):
+                fused_keys(z, history, taps, H)
+        torch.cuda.current_stream().wait_stream(side)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            for _ in range(reps):
+                fused_keys(z, history, taps, H)
+        graph.replay()  # warm
+        times = []
+        for _ in range(5):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            torch.cuda.synchronize()
+            e0.record()
+            graph.replay()
+            e1.record()
+            torch.cuda.synchronize()
+            times.append(e0.elapsed_time(e1) / reps)
+    return statistics.median(times)
 
 
 def time_decode(torch, reps: int = 5) -> dict:
@@ -263,6 +307,7 @@ def traffic_probe(torch) -> None:
     to what FETCH_SIZE / WRITE_SIZE report for it scales the counters of the other kernels.
     """
     from vesper.kernels.delta_scan import delta_scan_fused, delta_scan_step_fused
+    from vesper.kernels.keys import fused_keys
     from vesper.kernels.ring_attn import RingKVCache, ring_attention
     from vesper.kernels.window_attn import window_attention
 
@@ -282,12 +327,16 @@ def traffic_probe(torch) -> None:
     dbeta = torch.rand(b, h, generator=g).to(dev)
     rq = torch.randn(b, 1, h, d, generator=g).to(dev, torch.bfloat16)
     pos = torch.full((b, 1), w, device=dev)
+    kz = torch.randn(B, T, KEY_D, generator=g).to(dev, torch.bfloat16)
+    khist = torch.randn(B, KEY_TAPS - 1, KEY_D, generator=g).to(dev)
+    ktaps = torch.randn(KEY_TAPS, KEY_D, generator=g).to(dev)
     with torch.no_grad():
         dst.copy_(src)
         delta_scan_fused(q, k, v, beta, s0)
         window_attention(aq, ak, av, WINDOW)
         delta_scan_step_fused(dq, dq, dq, dbeta, state, out_state=state)
         ring_attention(rq, rq, rq, pos, ring, inplace=True, check_positions=False)
+        fused_keys(kz, khist, ktaps, H)
     torch.cuda.synchronize()
     print(json.dumps({"copy_bytes": COPY_BYTES}), flush=True)
 
@@ -337,6 +386,7 @@ def main() -> int:
     s_bytes, s_flops = scan_bytes(B, T, H, D), scan_flops(B, T, H, D)
     a_bytes, a_flops = attn_bytes(B, T, H, H, D), attn_flops(B, T, H, D, WINDOW)
     attn4_ms = time_attention_config(torch)
+    keys_ms = time_key_filter(torch)
     dec = None if args.no_decode else time_decode(torch)
     looped = None if args.no_loop else time_looped(torch)
 
@@ -384,6 +434,13 @@ def main() -> int:
             "window_attn_b4_mfma_frac_bf16": round(attn_flops(ATTN_B, T, H, D, WINDOW) / (attn4_ms / 1e3) / 1e12 / BF16_PEAK_TFLOPS, 4),
         },
         "roofline": roofline,
+    }
+    k_bytes = key_filter_bytes(B, T, KEY_D, KEY_TAPS)
+    result["key_filter"] = {
+        "workload": "causal key filter + per-head key normalization: B8 T4096 d512 (8 heads of 64), 4 taps, bf16 "
+                    "keys, float32 history and taps",
+        "us": round(keys_ms * 1e3, 3), "tok_s": round(B * T / (keys_ms / 1e3), 1),
+        "hbm_frac": round(k_bytes / (keys_ms / 1e3) / 1e9 / HBM_PEAK_GBS, 4), "algorithmic_bytes": k_bytes,
     }
     if dec is not None:
         step_bytes = decode_step_bytes(DEC_B, H, D, DEC_W)

@@ -22,7 +22,7 @@
 extern "C" {
 #endif
 
-#define VSP_ABI_VERSION 2
+#define VSP_ABI_VERSION 3
 
 /* Status codes. */
 #define VSP_OK 0
@@ -102,6 +102,23 @@ int vsp_ring_attn_f16(const void* q, const void* k, const void* v, const int64_t
                       int64_t* ring_pos, uint8_t* ring_valid, void* o, const uint8_t* active, void* workspace,
                       size_t workspace_bytes, int B, int H, int HKV, int D, int window, float scale, int write,
                       void* stream);
+
+/* ---- the causal key filter and key normalization (before the scan) --------------------------
+ * z: [B, N, D] key inputs (bf16, f16 or fp32); history: [B, K-1, D] fp32, the K-1 inputs before
+ * the chunk, oldest first (may be NULL when K == 1); taps: [K, D] fp32, tap 0 on the current token.
+ * keys: [B, N, D] = [B, N, heads, D / heads] in z's dtype:
+ *   u[t, j] = sum_{r < K} taps[r, j] * z[t - r, j] (rows before the chunk from the history), then
+ *   per head normalize_keys(u) = s / max(||s||, 1), s = u / max(max |u|, 1e-6).
+ * The contract of vesper/column.py:255-289 (`RecurrentSublayer.keys`; the next history, the newest
+ * K-1 inputs, is the caller's) as vesper/kernels/keys.py:28-32 (`fused_keys`, forward) computes it
+ * on CUDA. K in 1..8; head width D / heads a power of two in 8..512; one batch row of z at most
+ * 2 GiB; z, history, taps and keys 16-byte aligned. */
+int vsp_key_filter_bf16(const void* z, const float* history, const float* taps, void* keys, int B, int N, int D,
+                        int heads, int K, void* stream);
+int vsp_key_filter_f16(const void* z, const float* history, const float* taps, void* keys, int B, int N, int D,
+                       int heads, int K, void* stream);
+int vsp_key_filter_f32(const float* z, const float* history, const float* taps, float* keys, int B, int N, int D,
+                       int heads, int K, void* stream);
 
 #ifdef __cplusplus
 }

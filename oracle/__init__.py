@@ -7,7 +7,9 @@ the algorithms the HIP kernels of ``vesper`` must reproduce:
 - ``oracle.attention``: sliding-window causal attention, the chronological cache and the decode
   ring (reference ``vesper/attention.py``, ``vesper/kernels/window_attn.py``);
 - ``oracle.loop``: the looped column with per-token halting and copy-forward (reference
-  ``vesper/loop.py``, ``vesper/column.py``).
+  ``vesper/loop.py``, ``vesper/column.py``);
+- ``oracle.keys``: the causal key filter and key normalization before the scan (reference
+  ``vesper/column.py``, ``vesper/kernels/keys.py``).
 
 Only ``tests/``, ``__graft_entry__.smoke()`` and the CPU-baseline leg of ``bench.py`` may import
 this package, and only as the checker (or as the timed CPU baseline); the product path never

@@ -98,3 +98,26 @@ def test_the_scan_switch_refuses_what_it_cannot_run():
         check_scan("fused", torch.device("cpu"))
     with pytest.raises(ValueError, match="needs the model on CUDA"):
         check_capturable_scan("fused-fp32", torch.device("cpu"))
+
+
+def test_the_key_filter_refuses_before_launching():
+    from vesper.contracts import ContractError
+    from vesper.kernels import _lib
+    from vesper.kernels.keys import fused_keys
+
+    z = torch.zeros(1, 4, 128)
+    taps = torch.ones(4, 128)
+    with pytest.raises(ContractError, match="CUDA only"):
+        fused_keys(z, torch.zeros(1, 3, 128), taps, 2)
+    with pytest.raises(ContractError, match="dtype"):
+        fused_keys(z.double(), torch.zeros(1, 3, 128), taps, 2)
+    with pytest.raises(ContractError, match="axis"):
+        fused_keys(z, torch.zeros(1, 4, 128), taps, 2)
+    lib = _lib.library()
+    assert lib.vsp_key_filter_bf16(None, None, None, None, 1, 4, 128, 2, 9, None) == 2  # unsupported
+    assert "filter width 9" in lib.vsp_last_error().decode()
+    assert lib.vsp_key_filter_f32(None, None, None, None, 1, 4, 128, 32, 4, None) == 2
+    assert "head width 4" in lib.vsp_last_error().decode()
+    assert lib.vsp_key_filter_f16(None, None, None, None, 1, 4, 128, 2, 4, None) == 1  # bad argument
+    assert "null pointer" in lib.vsp_last_error().decode()
+    assert lib.vsp_key_filter_bf16(None, None, None, None, 0, 4, 128, 2, 4, None) == 0  # nothing to do

@@ -1,0 +1,158 @@
+"""The key filter kernel (``vsp_key_filter_*`` via ``vesper.kernels.keys`` / ``vesper.column``)
+against the key-filter oracle.
+
+Parity bar (the reference's own, ``tests/test_keys_fused.py:70-75``): 2e-5 for float32 key inputs,
+8e-3 for bfloat16 (the key's own final rounding), element-wise against the oracle in float64. At the
+prefill shape (B8 T4096, d 512 = 8 heads of 64, 4 taps) the same bound against the oracle in
+float32, and exact size-independent properties: chunking does not change a key (bitwise), captured
+replays equal eager.
+"""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+from conftest import needs_gpu
+from oracle import keys as ok
+from oracle.delta import normalize_keys
+
+pytestmark = [pytest.mark.gpu, needs_gpu]
+
+GPU = torch.device("cuda")
+K = 4
+
+
+def _taps(d: int, width: int = K) -> torch.Tensor:
+    # asymmetric: every tap and channel differ (tests/test_keys_fused.py:38-43 of the reference)
+    r = torch.arange(width, dtype=torch.float32)[:, None]
+    j = torch.arange(d, dtype=torch.float32)[None, :]
+    return (r + 1) * 0.5 - 0.003 * j + 0.01 * r * j
+
+
+def _bound(dtype: torch.dtype) -> float:
+    return 2e-5 if dtype == torch.float32 else 8e-3
+
+
+def _check(z, history, taps, heads, dtype):
+    from vesper.column import recurrent_keys
+
+    keys, after = recurrent_keys(z.to(GPU), history.to(GPU), taps.to(GPU), heads)
+    want, want_after = ok.filter_keys(z.double(), history.double(), taps.double(), heads)
+    bound = _bound(dtype)
+    torch.testing.assert_close(keys.double().cpu(), want, rtol=bound, atol=bound)
+    assert keys.dtype == dtype
+    torch.testing.assert_close(after.cpu().double(), want_after, rtol=0, atol=0)
+    return keys
+
+
+@pytest.mark.parametrize("n", [1, 2, 3, 257])  # shorter than the filter, and a long chunk
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_the_keys_match_the_oracle(n, dtype):
+    g = torch.Generator().manual_seed(n)
+    z = (torch.randn(3, n, 128, generator=g) * 2).to(dtype)
+    z[0, 0] = 0.0  # a zero key input row: the floor
+    history = torch.randn(3, K - 1, 128, generator=g)
+    _check(z, history, _taps(128), 2, dtype)
+
+
+@pytest.mark.parametrize("head_dim", [8, 16, 32, 64, 128, 256, 512])
+@pytest.mark.parametrize("width", [1, 2, 4, 8])
+def test_every_head_width_and_filter_width(head_dim, width):
+    g = torch.Generator().manual_seed(head_dim + width)
+    heads = max(1, 512 // head_dim)
+    d = heads * head_dim
+    z = torch.randn(2, 45, d, generator=g).to(torch.bfloat16)
+    history = torch.randn(2, width - 1, d, generator=g)
+    _check(z, history, _taps(d, width), heads, torch.bfloat16)
+
+
+def test_the_prefill_shape_b8_t4096_d512_h8_k4():
+    g = torch.Generator().manual_seed(11)
+    z = torch.randn(8, 4096, 512, generator=g).to(torch.bfloat16)
+    history = torch.randn(8, K - 1, 512, generator=g)
+    from vesper.kernels.keys import fused_keys
+
+    keys = fused_keys(z.to(GPU), history.to(GPU), _taps(512).to(GPU), 8)
+    want, _ = ok.filter_keys(z.float(), history, _taps(512), 8)
+    torch.testing.assert_close(keys.float().cpu(), want.float(), rtol=8e-3, atol=8e-3)
+    again = fused_keys(z.to(GPU), history.to(GPU), _taps(512).to(GPU), 8)
+    assert torch.equal(keys, again)
+
+
+def test_chunking_does_not_change_a_key():
+    from vesper.column import recurrent_keys
+
+    g = torch.Generator().manual_seed(3)
+    z = torch.randn(2, 300, 256, generator=g).to(GPU, torch.bfloat16)
+    cold = torch.zeros(2, K - 1, 256, device=GPU)
+    taps = _taps(256).to(GPU)
+    whole, last = recurrent_keys(z, cold, taps, 4)
+    for sizes in ((1,) * 7 + (293,), (2, 0, 3, 1, 294), (100, 100, 100), (0, 4, 296)):
+        history, start, parts = cold, 0, []
+        for size in sizes:
+            keys, history = recurrent_keys(z[:, start:start + size], history, taps, 4)
+            parts.append(keys)
+            start += size
+        assert torch.equal(torch.cat(parts, dim=1), whole), sizes
+        assert torch.equal(history, last)
+
+
+def test_no_filter_is_the_plain_normalization_and_keeps_the_history():
+    from vesper.column import recurrent_keys
+
+    g = torch.Generator().manual_seed(4)
+    z = torch.randn(2, 33, 128, generator=g)
+    none = torch.zeros(2, 0, 128, device=GPU)
+    keys, after = recurrent_keys(z.to(GPU), none, None, 2)
+    assert after is none
+    torch.testing.assert_close(keys.cpu().double(), normalize_keys(z.double().view(2, 33, 2, 64)), rtol=2e-5, atol=2e-5)
+    empty = z[:, :0].to(GPU)
+    history = torch.randn(2, K - 1, 128, device=GPU)
+    keys, after = recurrent_keys(empty, history, _taps(128).to(GPU), 2)
+    assert keys.shape == (2, 0, 2, 64) and after is history
+
+
+def test_captured_replays_equal_eager():
+    from vesper.kernels.keys import fused_keys
+
+    g = torch.Generator().manual_seed(5)
+    z = torch.randn(2, 64, 128, generator=g).to(GPU, torch.bfloat16)
+    history = torch.randn(2, K - 1, 128, generator=g).to(GPU)
+    taps = _taps(128).to(GPU)
+    eager = fused_keys(z, history, taps, 2)
+    out = torch.empty_like(eager)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        out.copy_(fused_keys(z, history, taps, 2))  # warm-up outside the capture
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        out.copy_(fused_keys(z, history, taps, 2))
+    for _ in range(3):
+        out.zero_()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager)
+
+
+def test_refusals():
+    from vesper.contracts import ContractError
+    from vesper.kernels.keys import fused_keys
+
+    z = torch.randn(1, 4, 128, device=GPU)
+    history = torch.zeros(1, K - 1, 128, device=GPU)
+    taps = _taps(128).to(GPU)
+    with pytest.raises(ContractError, match="dtype"):
+        fused_keys(z.double(), history, taps, 2)
+    with pytest.raises(ContractError, match="CUDA only"):
+        fused_keys(z.cpu(), history.cpu(), taps.cpu(), 2)
+    with pytest.raises(ContractError, match="gradient"):
+        fused_keys(z.clone().requires_grad_(), history, taps, 2)
+    with pytest.raises(ContractError, match="taps"):
+        fused_keys(z, torch.zeros(1, 8, 128, device=GPU), _taps(128, 9).to(GPU), 2)
+    with pytest.raises(ContractError, match="head width"):
+        fused_keys(z, history, taps, 32)  # head width 4
+    with pytest.raises(ContractError, match="axis"):
+        fused_keys(z, torch.zeros(1, K, 128, device=GPU), taps, 2)

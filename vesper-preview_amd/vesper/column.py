@@ -13,6 +13,8 @@ reference keeps its checks:
   cast ``q, k, v, beta`` to the choice's input dtype and the state to float32 with autocast off,
   run the kernel, return the reads in the projections' dtype and the new float32 state. The
   output projection ``W_o`` stays with the caller.
+- ``recurrent_keys``: ``RecurrentSublayer.keys`` (``column.py:255-289``) on the key filter kernel:
+  the normalized keys and the next key history, for a filter or none.
 """
 
 from __future__ import annotations
@@ -22,6 +24,7 @@ from typing import Literal
 import torch
 from torch import Tensor
 
+from vesper.kernels.keys import fused_keys
 from vesper.kernels.delta_scan import (
     FP32_INPUT_DTYPE,
     INPUT_DTYPE,
@@ -85,3 +88,27 @@ def recurrent_scan(impl: str, q: Tensor, k: Tensor, v: Tensor, beta: Tensor, sta
         o, new_state = kernel(q.to(dtype), k.to(dtype), v.to(dtype), beta.to(dtype), state.to(STATE_DTYPE),
                               active=active)
     return o.to(q.dtype), new_state
+
+
+def recurrent_keys(z: Tensor, history: Tensor, taps: Tensor | None, heads: int) -> tuple[Tensor, Tensor]:
+    """Normalized keys ``[b, n, heads, d / heads]`` of key inputs ``z [b, n, d]`` and the next history.
+
+    With a filter (``taps [K, d]``) the key of token ``t`` is ``normalize_keys`` per head of
+    ``sum_r taps[r] * z[t - r]``, the positions before the chunk from ``history [b, K-1, d]``
+    (oldest first); the next history is the newest ``K - 1`` inputs of ``(history, z)`` as an owned
+    float32 copy. With no filter (``taps`` None) the key is ``normalize_keys(z)`` and the history
+    object passes through; so it does for an empty chunk.
+
+    Raises:
+        ContractError: as ``fused_keys``.
+    """
+    b, n, d = z.shape
+    if taps is None or n == 0:
+        if n == 0:
+            return z.new_empty(b, 0, heads, d // heads), history
+        ones = torch.ones(1, d, dtype=torch.float32, device=z.device)
+        return fused_keys(z, z.new_empty(b, 0, d, dtype=torch.float32), ones, heads), history
+    width = int(taps.shape[0])
+    keys = fused_keys(z, history, taps, heads)
+    tail = z[:, max(0, n - (width - 1)):].to(torch.float32)
+    return keys, torch.cat([history.to(torch.float32)[:, n:], tail], dim=1)

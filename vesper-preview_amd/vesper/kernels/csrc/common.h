@@ -128,19 +128,43 @@ __device__ __forceinline__ void store_tile_t(E* base, int ld, f32x4 acc) {
 // ---- lane reductions through DPP (a VALU modifier: no LDS traffic, unlike ds_bpermute) --------
 template <int CTRL>
 __device__ __forceinline__ float dpp_f32(float x) {
-  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), CTRL, 0xF, 0xF, true));
+  return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), CTRL, 0xF, 0xF, true));
 }
-// Sum over aligned groups of N consecutive lanes (N = 1, 2, 4, 8 or 16); every lane of a group
-// gets the group's sum. quad_perm [1,0,3,2] and [2,3,0,1] pair lanes within a quad,
-// row_half_mirror swaps the two quads of 8 lanes, row_mirror the two halves of 16.
+// Reduction over aligned groups of N consecutive lanes (N a power of two, 1..64); every lane of a
+// group gets the same result. quad_perm [1,0,3,2] and [2,3,0,1] pair lanes within a quad,
+// row_half_mirror swaps the two quads of 8 lanes, row_mirror the two halves of 16, and
+// v_permlane16_swap / v_permlane32_swap hand each lane the value of lane l ^ 16 / l ^ 32 (the even
+// group's value first, so the last steps combine in one order on every lane).
+template <int N, typename Op>
+__device__ __forceinline__ float group_reduce(float x, Op op) {
+  static_assert(N >= 1 && N <= 64 && (N & (N - 1)) == 0, "group of 1..64 lanes");
+  if constexpr (N >= 2) x = op(x, dpp_f32<0xB1>(x));
+  if constexpr (N >= 4) x = op(x, dpp_f32<0x4E>(x));
+  if constexpr (N >= 8) x = op(x, dpp_f32<0x141>(x));
+  if constexpr (N >= 16) x = op(x, dpp_f32<0x140>(x));
+  if constexpr (N >= 32) {
+    const auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    x = op(__uint_as_float(p[0]), __uint_as_float(p[1]));
+  }
+  if constexpr (N >= 64) {
+    const auto p = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    x = op(__uint_as_float(p[0]), __uint_as_float(p[1]));
+  }
+  return x;
+}
+struct SumOp {
+  __device__ __forceinline__ float operator()(float a, float b) const { return a + b; }
+};
+struct MaxOp {
+  __device__ __forceinline__ float operator()(float a, float b) const { return __builtin_fmaxf(a, b); }
+};
 template <int N>
 __device__ __forceinline__ float group_sum(float x) {
-  static_assert(N == 1 || N == 2 || N == 4 || N == 8 || N == 16, "group of 1..16 lanes");
-  if constexpr (N >= 2) x += dpp_f32<0xB1>(x);
-  if constexpr (N >= 4) x += dpp_f32<0x4E>(x);
-  if constexpr (N >= 8) x += dpp_f32<0x141>(x);
-  if constexpr (N >= 16) x += dpp_f32<0x140>(x);
-  return x;
+  return group_reduce<N>(x, SumOp{});
+}
+template <int N>
+__device__ __forceinline__ float group_max(float x) {
+  return group_reduce<N>(x, MaxOp{});
 }
 
 // ---- transposed LDS reads (gfx950 ds_read_b64_tr_b16) ------------------------------------------

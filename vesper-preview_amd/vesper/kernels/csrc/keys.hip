@@ -1,0 +1,241 @@
+// The causal key filter and key normalization on CDNA4 (gfx950): the step before the scan.
+//
+// Semantics (reference vesper/column.py:255-289, computed on CUDA by vesper/kernels/keys.py:28-32):
+// u[t, j] = sum_{r < K} taps[r, j] * z[t - r, j] (depthwise, r = 0 the current token, positions
+// before the chunk from history [B, K-1, D], oldest first, float32), then per head of width hd the
+// key normalize_keys(u) = s / max(||s||, 1) with s = u / max(max_j |u_j|, 1e-6)
+// (vesper/recurrence.py:91-115), returned in z's dtype.
+//
+// HBM-bound: z is read once (plus a (K-1)-row halo per run of tokens, mostly from L2) and the key
+// written once. A lane owns 8 consecutive features (16-byte loads at bf16); a wave walks a run of
+// consecutive tokens, keeping the previous K-1 input rows in registers; a head's hd / 8 lanes
+// reduce its maximum and squared norm by DPP / permlane exchanges.
+#include "common.h"
+#include "vesper_kernels.h"
+
+namespace vsp {
+namespace {
+
+constexpr float kKeyFloor = 1e-6f;  // normalize_keys' floor (vesper/recurrence.py:31)
+
+// One row segment of 8 features through a buffer resource: the raw load (kept packed until used),
+// its float32 view, and the store of 8 float32 values in TZ.
+typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+template <typename TZ> struct Row8;
+template <> struct Row8<float> {
+  struct Raw {
+    u32x4 a, b;
+  };
+  static constexpr int kRun = 8;  // tokens per wave: 8 rows of 32 bytes in flight per lane
+  __device__ __forceinline__ static Raw load(__amdgpu_buffer_rsrc_t r, unsigned voff, unsigned soff) {
+    return Raw{__builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0), __builtin_amdgcn_raw_buffer_load_b128(r, voff + 16u, soff, 0)};
+  }
+  __device__ __forceinline__ static void unpack(const Raw& r, float (&x)[8]) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      x[e] = __uint_as_float(r.a[e]);
+      x[4 + e] = __uint_as_float(r.b[e]);
+    }
+  }
+  __device__ __forceinline__ static void store(__amdgpu_buffer_rsrc_t r, unsigned voff, unsigned soff, const float (&x)[8]) {
+    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, f32x4{x[0], x[1], x[2], x[3]}), r, voff, soff, 0);
+    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, f32x4{x[4], x[5], x[6], x[7]}), r, voff + 16u, soff, 0);
+  }
+};
+template <typename H8> struct Row8Half {
+  using Raw = u32x4;
+  static constexpr int kRun = 16;  // tokens per wave: 16 rows of 16 bytes in flight per lane
+  __device__ __forceinline__ static Raw load(__amdgpu_buffer_rsrc_t r, unsigned voff, unsigned soff) {
+    return __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0);
+  }
+  __device__ __forceinline__ static void unpack(const Raw& r, float (&x)[8]) {
+    const H8 h = __builtin_bit_cast(H8, r);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) x[e] = (float)h[e];
+  }
+  __device__ __forceinline__ static void store(__amdgpu_buffer_rsrc_t r, unsigned voff, unsigned soff, const float (&x)[8]) {
+    H8 h;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) h[e] = (decltype(h[0] + 0))x[e];
+    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, h), r, voff, soff, 0);
+  }
+};
+template <> struct Row8<__bf16> : Row8Half<bf16x8> {};
+template <> struct Row8<_Float16> : Row8Half<f16x8> {};
+
+// A wave owns a run of Row8<TZ>::kRun consecutive tokens of one batch row and 64 segments of 8
+// features. Every load of the run (its rows, the K - 1 rows before it, the taps) is issued before
+// the first use, so a wave keeps its whole run in flight: the kernel is bound by HBM bandwidth,
+// not by one row's latency per token. z and the keys go through buffer resources over one batch
+// row: the token's row offset is scalar, and a lane past D gets a vector offset beyond the range,
+// so its reads return zeros and its writes are dropped (whole heads idle together: D is a multiple
+// of the head width).
+template <typename TZ, int K, int LPH>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))) void key_filter_kernel(const TZ* __restrict__ z, const float* __restrict__ history,
+                                                         const float* __restrict__ taps, TZ* __restrict__ out, int N,
+                                                         int D) {
+  using Row = Row8<TZ>;
+  constexpr int RUN = Row::kRun;
+  static_assert(RUN >= K - 1, "a run is at least as long as the filter's history");
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), l = threadIdx.x & 63;
+  const int b = blockIdx.z;
+  const int f0 = 8 * (64 * blockIdx.x + l);  // this lane's first feature
+  const bool on = f0 < D;
+  const int t_begin = RUN * (4 * blockIdx.y + wave);
+  if (t_begin >= N) return;  // whole waves only: no workgroup barrier in this kernel
+  const unsigned row_bytes = (unsigned)D * sizeof(TZ);
+  const unsigned batch_bytes = (unsigned)N * row_bytes;  // below 2^31: the host refuses more
+  const auto rz = buffer_rsrc(z + (size_t)b * N * D, batch_bytes);
+  const auto ro = buffer_rsrc(out + (size_t)b * N * D, batch_bytes);
+  constexpr unsigned kPast = 0x80000000u;  // a vector offset past every range (ranges stay below 2^31)
+  const unsigned voff = on ? (unsigned)f0 * sizeof(TZ) : kPast;
+  const int fl = on ? f0 : 0;  // taps: idle lanes read feature 0's (never stored)
+
+  // Loads in the order of use (vmcnt counts in issue order): the taps, the K - 1 rows before the
+  // run, then the run's rows, so token i waits only for its own row.
+  float tp[K][8];
+#pragma unroll
+  for (int r = 0; r < K; ++r) {
+    const f32x4 t0 = *reinterpret_cast<const f32x4*>(taps + (size_t)r * D + fl);
+    const f32x4 t1 = *reinterpret_cast<const f32x4*>(taps + (size_t)r * D + fl + 4);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      tp[r][e] = t0[e];
+      tp[r][4 + e] = t1[e];
+    }
+  }
+  // The rows before the run come from z, or for the batch row's first run (the run is at least
+  // K - 1 tokens long) all from the history. Both are loaded without a branch, the unused one from
+  // past its range (zeros), and joined bitwise: exact, signed zeros included.
+  float win[K > 1 ? K - 1 : 1][8];  // win[r - 1] = input row t - r
+  if constexpr (K > 1) {
+    const bool first = t_begin == 0;
+    const auto rh = buffer_rsrc(history + (size_t)b * (K - 1) * D, (unsigned)(K - 1) * D * 4u);
+    const unsigned vz = first ? kPast : voff;
+    const unsigned vh = (first && on) ? (unsigned)f0 * 4u : kPast;
+#pragma unroll
+    for (int r = 1; r < K; ++r) {
+      float zr[8], hr[8];
+      Row::unpack(Row::load(rz, vz, first ? 0u : (unsigned)(t_begin - r) * row_bytes), zr);
+      Row8<float>::unpack(Row8<float>::load(rh, vh, (unsigned)(K - 1 - r) * D * 4u), hr);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) win[r - 1][e] = __uint_as_float(__float_as_uint(zr[e]) | __float_as_uint(hr[e]));
+    }
+  }
+  typename Row::Raw raw[RUN];  // rows past N (a short last run) re-read row N - 1
+#pragma unroll
+  for (int i = 0; i < RUN; ++i) raw[i] = Row::load(rz, voff, (unsigned)min(t_begin + i, N - 1) * row_bytes);
+
+#pragma unroll
+  for (int i = 0; i < RUN; ++i) {
+    const int t = t_begin + i;  // past N in a short last run: computed, the store dropped
+    float cur[8];
+    Row::unpack(raw[i], cur);
+    // the filter in the reference's order: taps[0] z[t], then + taps[r] z[t - r] for r = 1, 2, ...
+    float u[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      float acc = tp[0][e] * cur[e];
+#pragma unroll
+      for (int r = 1; r < K; ++r) acc = acc + tp[r][e] * win[r - 1][e];
+      u[e] = acc;
+    }
+#pragma unroll
+    for (int r = K - 1; r >= 2; --r)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) win[r - 1][e] = win[r - 2][e];
+    if constexpr (K > 1) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) win[0][e] = cur[e];
+    }
+    // normalize_keys per head: s = u / max(peak, floor), key = s / sqrt(max(|s|^2, 1)); each
+    // division is a reciprocal (v_rcp / v_rsq, 1 ulp) per token and lane times the 8 features,
+    // far inside float32's 2e-5 bound
+    float peak = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) peak = __builtin_fmaxf(peak, fabsf(u[e]));
+    const float inv_scale = __builtin_amdgcn_rcpf(__builtin_fmaxf(group_max<LPH>(peak), kKeyFloor));
+    float ss = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      u[e] = u[e] * inv_scale;
+      ss += u[e] * u[e];
+    }
+    const float inv_den = __builtin_amdgcn_rsqf(__builtin_fmaxf(group_sum<LPH>(ss), 1.f));
+#pragma unroll
+    for (int e = 0; e < 8; ++e) u[e] = u[e] * inv_den;
+    // The row offset goes in the vector offset with soffset 0. With a register soffset the
+    // compiler inserts no wait state between a store of more than 8 bytes and a VALU write of its
+    // data registers, and on gfx950 that write then reached the store's first dword (in lanes
+    // 12..15 of each row of 16); with soffset 0 the wait state is inserted.
+    Row::store(ro, (t < N ? voff : kPast) + (unsigned)min(t, N - 1) * row_bytes, 0u, u);
+  }
+}
+
+template <typename TZ, int K>
+void launch_k(const TZ* z, const float* history, const float* taps, TZ* out, int B, int N, int D, int hd,
+              hipStream_t stream) {
+  constexpr int per_block = 4 * Row8<TZ>::kRun;
+  dim3 grid((unsigned)((D / 8 + 63) / 64), (unsigned)((N + per_block - 1) / per_block), (unsigned)B);
+  switch (hd / 8) {
+    case 1: hipLaunchKernelGGL((key_filter_kernel<TZ, K, 1>), grid, dim3(256), 0, stream, z, history, taps, out, N, D); break;
+    case 2: hipLaunchKernelGGL((key_filter_kernel<TZ, K, 2>), grid, dim3(256), 0, stream, z, history, taps, out, N, D); break;
+    case 4: hipLaunchKernelGGL((key_filter_kernel<TZ, K, 4>), grid, dim3(256), 0, stream, z, history, taps, out, N, D); break;
+    case 8: hipLaunchKernelGGL((key_filter_kernel<TZ, K, 8>), grid, dim3(256), 0, stream, z, history, taps, out, N, D); break;
+    case 16: hipLaunchKernelGGL((key_filter_kernel<TZ, K, 16>), grid, dim3(256), 0, stream, z, history, taps, out, N, D); break;
+    case 32: hipLaunchKernelGGL((key_filter_kernel<TZ, K, 32>), grid, dim3(256), 0, stream, z, history, taps, out, N, D); break;
+    default: hipLaunchKernelGGL((key_filter_kernel<TZ, K, 64>), grid, dim3(256), 0, stream, z, history, taps, out, N, D); break;
+  }
+}
+
+template <typename TZ>
+int key_filter(const TZ* z, const float* history, const float* taps, TZ* out, int B, int N, int D, int heads, int K,
+               void* stream_ptr, const char* who) {
+  if (B < 0 || N < 0 || D < 1 || heads < 1) return fail(ERR_ARG, "%s: bad sizes B=%d N=%d D=%d heads=%d", who, B, N, D, heads);
+  if (K < 1 || K > 8) return fail(ERR_UNSUPPORTED, "%s: filter width %d (kernels: 1..8)", who, K);
+  if (D % heads != 0) return fail(ERR_ARG, "%s: %d features are not a multiple of %d heads", who, D, heads);
+  const int hd = D / heads;
+  if (hd < 8 || hd > 512 || (hd & (hd - 1)) != 0)
+    return fail(ERR_UNSUPPORTED, "%s: head width %d (kernels: powers of two 8..512)", who, hd);
+  if (B == 0 || N == 0) return OK;
+  if (!z || !taps || !out || (K > 1 && !history)) return fail(ERR_ARG, "%s: null pointer", who);
+  if ((N + 4 * Row8<TZ>::kRun - 1) / (4 * Row8<TZ>::kRun) > 65535 || B > 65535)
+    return fail(ERR_UNSUPPORTED, "%s: %d tokens in %d batch rows exceed the launch grid", who, N, B);
+  if ((size_t)N * D * sizeof(TZ) > 0x7FFFFFF0u)
+    return fail(ERR_UNSUPPORTED, "%s: %d tokens of %d features exceed 2 GiB in one batch row", who, N, D);
+  if ((reinterpret_cast<uintptr_t>(z) | reinterpret_cast<uintptr_t>(out) | reinterpret_cast<uintptr_t>(taps) |
+       reinterpret_cast<uintptr_t>(history)) & 15)
+    return fail(ERR_ARG, "%s: z, history, taps and the output must be 16-byte aligned", who);
+  hipStream_t stream = reinterpret_cast<hipStream_t>(stream_ptr);
+  switch (K) {
+    case 1: launch_k<TZ, 1>(z, history, taps, out, B, N, D, hd, stream); break;
+    case 2: launch_k<TZ, 2>(z, history, taps, out, B, N, D, hd, stream); break;
+    case 3: launch_k<TZ, 3>(z, history, taps, out, B, N, D, hd, stream); break;
+    case 4: launch_k<TZ, 4>(z, history, taps, out, B, N, D, hd, stream); break;
+    case 5: launch_k<TZ, 5>(z, history, taps, out, B, N, D, hd, stream); break;
+    case 6: launch_k<TZ, 6>(z, history, taps, out, B, N, D, hd, stream); break;
+    case 7: launch_k<TZ, 7>(z, history, taps, out, B, N, D, hd, stream); break;
+    default: launch_k<TZ, 8>(z, history, taps, out, B, N, D, hd, stream); break;
+  }
+  return check_launch(who);
+}
+
+}  // namespace
+}  // namespace vsp
+
+extern "C" int vsp_key_filter_bf16(const void* z, const float* history, const float* taps, void* keys, int B, int N,
+                                   int D, int heads, int K, void* stream) {
+  return vsp::key_filter<__bf16>(static_cast<const __bf16*>(z), history, taps, static_cast<__bf16*>(keys), B, N, D,
+                                 heads, K, stream, "vsp_key_filter_bf16");
+}
+
+extern "C" int vsp_key_filter_f16(const void* z, const float* history, const float* taps, void* keys, int B, int N,
+                                  int D, int heads, int K, void* stream) {
+  return vsp::key_filter<_Float16>(static_cast<const _Float16*>(z), history, taps, static_cast<_Float16*>(keys), B, N,
+                                   D, heads, K, stream, "vsp_key_filter_f16");
+}
+
+extern "C" int vsp_key_filter_f32(const float* z, const float* history, const float* taps, float* keys, int B, int N,
+                                  int D, int heads, int K, void* stream) {
+  return vsp::key_filter<float>(z, history, taps, keys, B, N, D, heads, K, stream, "vsp_key_filter_f32");
+}
