@@ -73,6 +73,12 @@ def key_filter_bytes(b: int, t: int, d: int, taps: int, elem: int = 2) -> float:
     return 2.0 * b * t * d * elem + 4.0 * d * (b * (taps - 1) + taps)
 
 
+def key_filter_backward_bytes(b: int, t: int, d: int, taps: int, elem: int = 2) -> float:
+    """Key inputs and the keys' gradient read once, the inputs' gradient written once; taps, history
+    and their gradients (float32)."""
+    return 3.0 * b * t * d * elem + 4.0 * d * 2 * (b * (taps - 1) + taps)
+
+
 def decode_step_bytes(b: int, h: int, d: int, w: int) -> float:
     state = 2 * b * h * d * d * 4  # read + write
     delta_io = 4 * b * h * d * 4 + b * h * 4  # q, k, v, o fp32; beta
@@ -151,12 +157,15 @@ def time_attention_config(torch, reps: int = 20) -> float:
     return e0.elapsed_time(e1) / reps
 
 
-def time_key_filter(torch, reps: int = 50) -> float:
-    """Milliseconds per launch of the key filter at B8 T4096 d512 (8 heads of 64), 4 taps, bf16.
+def time_key_filter(torch, reps: int = 50) -> tuple[float, float]:
+    """Milliseconds per launch of the key filter, forward and backward, at B8 T4096 d512 (8 heads of
+    64), 4 taps, bf16.
 
-    The launches are captured in one HIP graph and timed on replay: one launch (13 us) is about as
-    long as the host's per-call checks, so a timed loop of eager calls would measure the host.
+    The launches are captured in one HIP graph each and timed on replay: one launch (13 us) is about
+    as long as the host's per-call checks, so a timed loop of eager calls would measure the host.
+    The backward is the library's entry point (d z, d taps, d history) with its workspace.
     """
+    from vesper.kernels import _lib
     from vesper.kernels.keys import fused_keys
 
     dev = torch.device("cuda:0")
@@ -164,28 +173,46 @@ def time_key_filter(torch, reps: int = 50) -> float:
     z = torch.randn(B, T, KEY_D, generator=g).to(dev, torch.bfloat16)
     history = torch.randn(B, KEY_TAPS - 1, KEY_D, generator=g).to(dev)
     taps = torch.randn(KEY_TAPS, KEY_D, generator=g).to(dev)
+    up = torch.randn(B, T, KEY_D, generator=g).to(dev, torch.bfloat16)
+    grad_z = torch.empty_like(z)
+    grad_taps = torch.empty(KEY_TAPS, KEY_D, device=dev)
+    grad_history = torch.empty_like(history)
+    nbytes = int(_lib.library().vsp_key_filter_backward_workspace_bytes(B, T, KEY_D, KEY_TAPS))
+    workspace = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+
+    def forward():
+        fused_keys(z, history, taps, H)
+
+    def backward():
+        _lib.call("vsp_key_filter_backward_bf16", _lib.ptr(z), _lib.ptr(history), _lib.ptr(taps), _lib.ptr(up),
+                  _lib.ptr(grad_z), _lib.ptr(grad_taps), _lib.ptr(grad_history), _lib.ptr(workspace), nbytes,
+                  B, T, KEY_D, H, KEY_TAPS, _lib.stream_of(dev))
+
+    out = []
     with torch.no_grad():
-        side = torch.cuda.Stream()
-        side.wait_stream(torch.cuda.current_stream())
-        with torch.cuda.stream(side):
-            for _ in range(3):
-                fused_keys(z, history, taps, H)
-        torch.cuda.current_stream().wait_stream(side)
-        graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(graph):
-            for _ in range(reps):
-                fused_keys(z, history, taps, H)
-        graph.replay()  # warm
-        times = []
-        for _ in range(5):
-            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            torch.cuda.synchronize()
-            e0.record()
-            graph.replay()
-            e1.record()
-            torch.cuda.synchronize()
-            times.append(e0.elapsed_time(e1) / reps)
-    return statistics.median(times)
+        for fn in (forward, backward):
+            side = torch.cuda.Stream()
+            side.wait_stream(torch.cuda.current_stream())
+            with torch.cuda.stream(side):
+                for _ in range(3):
+                    fn()
+            torch.cuda.current_stream().wait_stream(side)
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph):
+                for _ in range(reps):
+                    fn()
+            graph.replay()  # warm
+            times = []
+            for _ in range(5):
+                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                torch.cuda.synchronize()
+                e0.record()
+                graph.replay()
+                e1.record()
+                torch.cuda.synchronize()
+                times.append(e0.elapsed_time(e1) / reps)
+            out.append(statistics.median(times))
+    return out[0], out[1]
 
 
 def time_decode(torch, reps: int = 5) -> dict:
@@ -386,7 +413,7 @@ def main() -> int:
     s_bytes, s_flops = scan_bytes(B, T, H, D), scan_flops(B, T, H, D)
     a_bytes, a_flops = attn_bytes(B, T, H, H, D), attn_flops(B, T, H, D, WINDOW)
     attn4_ms = time_attention_config(torch)
-    keys_ms = time_key_filter(torch)
+    keys_ms, keys_bwd_ms = time_key_filter(torch)
     dec = None if args.no_decode else time_decode(torch)
     looped = None if args.no_loop else time_looped(torch)
 
@@ -436,11 +463,15 @@ def main() -> int:
         "roofline": roofline,
     }
     k_bytes = key_filter_bytes(B, T, KEY_D, KEY_TAPS)
+    kb_bytes = key_filter_backward_bytes(B, T, KEY_D, KEY_TAPS)
     result["key_filter"] = {
         "workload": "causal key filter + per-head key normalization: B8 T4096 d512 (8 heads of 64), 4 taps, bf16 "
-                    "keys, float32 history and taps",
+                    "keys, float32 history and taps; backward = d z, d taps, d history from the keys' gradient",
         "us": round(keys_ms * 1e3, 3), "tok_s": round(B * T / (keys_ms / 1e3), 1),
         "hbm_frac": round(k_bytes / (keys_ms / 1e3) / 1e9 / HBM_PEAK_GBS, 4), "algorithmic_bytes": k_bytes,
+        "backward_us": round(keys_bwd_ms * 1e3, 3),
+        "backward_hbm_frac": round(kb_bytes / (keys_bwd_ms / 1e3) / 1e9 / HBM_PEAK_GBS, 4),
+        "backward_algorithmic_bytes": kb_bytes,
     }
     if dec is not None:
         step_bytes = decode_step_bytes(DEC_B, H, D, DEC_W)

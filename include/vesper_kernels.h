@@ -22,7 +22,7 @@
 extern "C" {
 #endif
 
-#define VSP_ABI_VERSION 3
+#define VSP_ABI_VERSION 4
 
 /* Status codes. */
 #define VSP_OK 0
@@ -119,6 +119,24 @@ int vsp_key_filter_f16(const void* z, const float* history, const float* taps, v
                        int heads, int K, void* stream);
 int vsp_key_filter_f32(const float* z, const float* history, const float* taps, float* keys, int B, int N, int D,
                        int heads, int K, void* stream);
+
+/* The key filter's backward (vesper/kernels/keys.py:46-78, `_FusedKeys.backward`, on CUDA
+ * vesper/kernels/keys_triton.py:56-177): from grad_keys [B, N, D] (z's dtype), with the
+ * normalization's peak held constant (vesper/recurrence.py:103-105),
+ *   grad_z [B, N, D] (z's dtype), grad_taps [K, D] fp32, and grad_history [B, K-1, D] fp32 (skipped
+ *   when NULL). Deterministic: no atomics, the taps' partial sums added in a fixed order.
+ * Same shape limits as the forward; workspace of vsp_key_filter_backward_workspace_bytes bytes
+ * (16-byte aligned, contents ignored). B == 0 or N == 0 writes zero gradients. */
+size_t vsp_key_filter_backward_workspace_bytes(int B, int N, int D, int K);
+int vsp_key_filter_backward_bf16(const void* z, const float* history, const float* taps, const void* grad_keys,
+                                 void* grad_z, float* grad_taps, float* grad_history, void* workspace,
+                                 size_t workspace_bytes, int B, int N, int D, int heads, int K, void* stream);
+int vsp_key_filter_backward_f16(const void* z, const float* history, const float* taps, const void* grad_keys,
+                                void* grad_z, float* grad_taps, float* grad_history, void* workspace,
+                                size_t workspace_bytes, int B, int N, int D, int heads, int K, void* stream);
+int vsp_key_filter_backward_f32(const float* z, const float* history, const float* taps, const float* grad_keys,
+                                float* grad_z, float* grad_taps, float* grad_history, void* workspace,
+                                size_t workspace_bytes, int B, int N, int D, int heads, int K, void* stream);
 
 #ifdef __cplusplus
 }

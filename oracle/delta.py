@@ -26,13 +26,15 @@ KEY_NORM_FLOOR = 1e-6  # recurrence.py:31
 def normalize_keys(k: Tensor) -> Tensor:
     """``k / max(||k||, 1e-6)`` computed without squaring out of range (``recurrence.py:91-115``).
 
-    The row is first divided by its largest magnitude (floored at 1e-6), so one component of the
-    scaled row has magnitude one unless the whole row sits under the floor; the squared norm is
-    accumulated in float32 (float64 for float64 rows) and floored at one before the root.
+    The row is first divided by its largest magnitude (floored at 1e-6, and a constant for the
+    gradient), so one component of the scaled row has magnitude one unless the whole row sits under
+    the floor; the squared norm is accumulated in float32 (float64 for float64 rows) and floored at
+    one before the root.
     """
     if k.numel() == 0:
         return k
-    peak = k.abs().amax(dim=-1, keepdim=True).clamp_min(KEY_NORM_FLOOR)
+    # the peak is held constant under autograd (recurrence.py:103-105): it cancels algebraically
+    peak = k.detach().abs().amax(dim=-1, keepdim=True).clamp_min(KEY_NORM_FLOOR)
     unit = k / peak
     wide = torch.float64 if unit.dtype == torch.float64 else torch.float32
     norm2 = (unit.to(wide) ** 2).sum(dim=-1, keepdim=True)

@@ -2,10 +2,11 @@
 against the key-filter oracle.
 
 Parity bar (the reference's own, ``tests/test_keys_fused.py:70-75``): 2e-5 for float32 key inputs,
-8e-3 for bfloat16 (the key's own final rounding), element-wise against the oracle in float64. At the
+8e-3 for bfloat16 (the key's own final rounding), element-wise against the oracle in float64, for
+the keys, the next history and the gradients of the key input, the taps and the history. At the
 prefill shape (B8 T4096, d 512 = 8 heads of 64, 4 taps) the same bound against the oracle in
-float32, and exact size-independent properties: chunking does not change a key (bitwise), captured
-replays equal eager.
+float32, and exact size-independent properties: chunking does not change a key (bitwise), the
+backward repeats bitwise, captured replays equal eager.
 """
 
 from __future__ import annotations
@@ -148,11 +149,119 @@ def test_refusals():
         fused_keys(z.double(), history, taps, 2)
     with pytest.raises(ContractError, match="CUDA only"):
         fused_keys(z.cpu(), history.cpu(), taps.cpu(), 2)
-    with pytest.raises(ContractError, match="gradient"):
-        fused_keys(z.clone().requires_grad_(), history, taps, 2)
     with pytest.raises(ContractError, match="taps"):
         fused_keys(z, torch.zeros(1, 8, 128, device=GPU), _taps(128, 9).to(GPU), 2)
     with pytest.raises(ContractError, match="head width"):
         fused_keys(z, history, taps, 32)  # head width 4
     with pytest.raises(ContractError, match="axis"):
         fused_keys(z, torch.zeros(1, K, 128, device=GPU), taps, 2)
+
+
+def _grads(z, history, taps, heads, up):
+    from vesper.column import recurrent_keys
+
+    zs, hs, ts = (t.detach().clone().to(GPU).requires_grad_() for t in (z, history, taps))
+    keys, _ = recurrent_keys(zs, hs, ts, heads)
+    torch.autograd.backward([(keys.double() * up.to(GPU).double()).sum()])
+    return zs.grad, hs.grad, ts.grad
+
+
+def _check_grads(z, history, taps, heads, up, bound):
+    got = _grads(z, history, taps, heads, up)
+    # the key's gradient reaches the kernel in the key's dtype, as under the reference's autograd
+    g = up.to(z.dtype).double()
+    want = ok.filter_keys_grads(z.double(), history.double(), taps.double(), heads, g)
+    for a, b, name in zip(got, want, ("dz", "dhistory", "dtaps")):
+        assert a is not None, name
+        torch.testing.assert_close(a.double().cpu(), b, rtol=bound, atol=bound, msg=name)
+    return got
+
+
+@pytest.mark.parametrize("n", [1, 2, 3, 257])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_the_gradients_match_the_oracle(n, dtype):
+    g = torch.Generator().manual_seed(100 + n)
+    z = (torch.randn(3, n, 128, generator=g) * 2).to(dtype)
+    z[0, 0] = 0.0
+    history = torch.randn(3, K - 1, 128, generator=g)
+    up = torch.randn(3, n, 2, 64, generator=g)
+    dz, dh, dt = _check_grads(z, history, _taps(128), 2, up, _bound(dtype))
+    assert dz.dtype == dtype and dh.dtype == torch.float32 and dt.dtype == torch.float32
+
+
+@pytest.mark.parametrize("head_dim", [8, 64, 512])
+@pytest.mark.parametrize("width", [1, 2, 3, 4, 5, 8])
+def test_the_gradients_for_every_filter_width(head_dim, width):
+    g = torch.Generator().manual_seed(head_dim * 10 + width)
+    heads = max(1, 512 // head_dim)
+    z = torch.randn(2, 70, 512, generator=g)
+    history = torch.randn(2, width - 1, 512, generator=g)
+    up = torch.randn(2, 70, heads, head_dim, generator=g)
+    _check_grads(z, history, _taps(512, width), heads, up, 2e-5)
+
+
+def test_the_gradients_at_the_prefill_shape_and_they_repeat():
+    from vesper.kernels.keys import fused_keys
+
+    g = torch.Generator().manual_seed(12)
+    z = torch.randn(8, 4096, 512, generator=g).to(torch.bfloat16)
+    history = torch.randn(8, K - 1, 512, generator=g)
+    taps = _taps(512)
+    up = torch.randn(8, 4096, 8, 64, generator=g).to(torch.bfloat16)
+
+    def run():
+        zs, hs, ts = (t.to(GPU).requires_grad_() for t in (z, history, taps))
+        keys = fused_keys(zs, hs, ts, 8)
+        keys.backward(up.to(GPU))
+        return zs.grad, hs.grad, ts.grad
+
+    first = run()
+    again = run()
+    for a, b in zip(first, again):
+        assert torch.equal(a, b)  # deterministic: the taps' sums run in a fixed order
+    want = ok.filter_keys_grads(z.float(), history, taps, 8, up.float())
+    for a, b, name in zip(first, want, ("dz", "dhistory", "dtaps")):
+        torch.testing.assert_close(a.float().cpu(), b, rtol=8e-3, atol=8e-3, msg=name)
+
+
+def test_captured_forward_and_backward_equal_eager():
+    from vesper.kernels.keys import fused_keys
+
+    g = torch.Generator().manual_seed(13)
+    z = torch.randn(2, 100, 128, generator=g).to(GPU, torch.bfloat16).requires_grad_()
+    history = torch.randn(2, K - 1, 128, generator=g).to(GPU).requires_grad_()
+    taps = _taps(128).to(GPU).requires_grad_()
+    up = torch.randn(2, 100, 2, 64, generator=g).to(GPU, torch.bfloat16)
+
+    def step():
+        keys = fused_keys(z, history, taps, 2)
+        return (keys.detach(), *torch.autograd.grad((keys * up).sum(), (z, history, taps)))
+
+    eager = [t.clone() for t in step()]
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        step()  # warm-up outside the capture
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        static = step()
+    for _ in range(3):
+        for t in static:
+            t.zero_()
+        graph.replay()
+        torch.cuda.synchronize()
+        for a, b in zip(static, eager):
+            assert torch.equal(a, b)
+
+
+def test_an_empty_chunk_has_zero_gradients():
+    from vesper.kernels.keys import fused_keys
+
+    z = torch.randn(2, 0, 128, device=GPU, requires_grad=True)
+    history = torch.randn(2, K - 1, 128, device=GPU, requires_grad=True)
+    taps = _taps(128).to(GPU).requires_grad_()
+    keys = fused_keys(z, history, taps, 2)
+    gz, gh, gt = torch.autograd.grad(keys.sum(), (z, history, taps), allow_unused=True)
+    assert gz.shape == z.shape
+    assert torch.equal(gh, torch.zeros_like(gh)) and torch.equal(gt, torch.zeros_like(gt))

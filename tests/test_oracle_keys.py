@@ -119,3 +119,54 @@ def test_low_precision_inputs_filter_in_float32_and_return_their_dtype():
     assert keys.dtype == torch.bfloat16 and after.dtype == torch.float32
     wide, _ = ok.filter_keys_literal(z.double(), history.double(), _taps(8), heads=2)
     assert torch.allclose(keys.double(), wide, rtol=0, atol=8e-3)
+
+
+def test_the_gradients_match_finite_differences():
+    g = torch.Generator().manual_seed(21)
+    z = torch.randn(2, 5, 8, generator=g, dtype=torch.float64)
+    hist = torch.randn(2, 2, 8, generator=g, dtype=torch.float64)
+    taps = torch.randn(3, 8, generator=g, dtype=torch.float64)
+    up = torch.randn(2, 5, 2, 4, generator=g, dtype=torch.float64)
+
+    def loss(zz, hh, tt):
+        keys, _ = ok.filter_keys(zz, hh, tt, 2)
+        return (keys * up).sum()
+
+    assert torch.autograd.gradcheck(loss, (z.requires_grad_(), hist.requires_grad_(), taps.requires_grad_()))
+    dz, dh, dt = ok.filter_keys_grads(z, hist, taps, 2, up)
+    lz, lh, lt = ok.filter_keys_grads_literal(z.detach(), hist.detach(), taps.detach(), 2, up)
+    for a, b in ((dz, lz), (dh, lh), (dt, lt)):
+        torch.testing.assert_close(a, b, rtol=1e-10, atol=1e-12)
+
+
+def test_the_gradients_below_the_unit_norm_and_under_the_floor():
+    # a head whose scaled norm is exactly one (one nonzero component) and a row under the floor
+    z = torch.zeros(1, 3, 4, dtype=torch.float64)
+    z[0, 0, 1] = 2.0
+    z[0, 2] = 1e-8
+    hist = torch.zeros(1, 1, 4, dtype=torch.float64)
+    taps = torch.ones(2, 4, dtype=torch.float64)
+    up = torch.arange(12, dtype=torch.float64).view(1, 3, 1, 4) - 5.0
+    dz, dh, dt = ok.filter_keys_grads(z, hist, taps, 1, up)
+    lz, lh, lt = ok.filter_keys_grads_literal(z, hist, taps, 1, up)
+    for a, b in ((dz, lz), (dh, lh), (dt, lt)):
+        torch.testing.assert_close(a, b, rtol=1e-12, atol=1e-12)
+    # under the floor the key is u / 1e-6 (norm below one): its gradient is up / 1e-6 through the filter
+    want_row2 = up[0, 2, 0] / 1e-6
+    torch.testing.assert_close(dz[0, 2], want_row2, rtol=1e-12, atol=0)  # dz[2] = taps[0] du[2]
+
+
+def test_a_planted_mistake_in_the_literal_gradients_is_caught():
+    g = torch.Generator().manual_seed(22)
+    z = torch.randn(1, 4, 8, generator=g, dtype=torch.float64)
+    hist = torch.randn(1, 2, 8, generator=g, dtype=torch.float64)
+    taps = torch.randn(3, 8, generator=g, dtype=torch.float64)
+    up = torch.randn(1, 4, 2, 4, generator=g, dtype=torch.float64)
+    dz, _, dt = ok.filter_keys_grads(z, hist, taps, 2, up)
+    # the taps' gradient with the input shifted by one token (a plausible indexing slip)
+    full = torch.cat([hist, z], dim=1)
+    _, _, lt = ok.filter_keys_grads_literal(z, hist, taps, 2, up)
+    assert torch.allclose(dt, lt)
+    shifted = torch.cat([hist[:, :1], full[:, :-1]], dim=1)
+    _, _, wrong = ok.filter_keys_grads_literal(shifted[:, 2:], shifted[:, :2], taps, 2, up)
+    assert not torch.allclose(dt, wrong, rtol=1e-3, atol=1e-6)

@@ -10,58 +10,12 @@
 // written once. A lane owns 8 consecutive features (16-byte loads at bf16); a wave walks a run of
 // consecutive tokens, keeping the previous K-1 input rows in registers; a head's hd / 8 lanes
 // reduce its maximum and squared norm by DPP / permlane exchanges.
-#include "common.h"
+#include "keys_rows.h"
+#include "keys_backward.h"
 #include "vesper_kernels.h"
 
 namespace vsp {
 namespace {
-
-constexpr float kKeyFloor = 1e-6f;  // normalize_keys' floor (vesper/recurrence.py:31)
-
-// One row segment of 8 features through a buffer resource: the raw load (kept packed until used),
-// its float32 view, and the store of 8 float32 values in TZ.
-typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
-template <typename TZ> struct Row8;
-template <> struct Row8<float> {
-  struct Raw {
-    u32x4 a, b;
-  };
-  static constexpr int kRun = 8;  // tokens per wave: 8 rows of 32 bytes in flight per lane
-  __device__ __forceinline__ static Raw load(__amdgpu_buffer_rsrc_t r, unsigned voff, unsigned soff) {
-    return Raw{__builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0), __builtin_amdgcn_raw_buffer_load_b128(r, voff + 16u, soff, 0)};
-  }
-  __device__ __forceinline__ static void unpack(const Raw& r, float (&x)[8]) {
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      x[e] = __uint_as_float(r.a[e]);
-      x[4 + e] = __uint_as_float(r.b[e]);
-    }
-  }
-  __device__ __forceinline__ static void store(__amdgpu_buffer_rsrc_t r, unsigned voff, unsigned soff, const float (&x)[8]) {
-    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, f32x4{x[0], x[1], x[2], x[3]}), r, voff, soff, 0);
-    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, f32x4{x[4], x[5], x[6], x[7]}), r, voff + 16u, soff, 0);
-  }
-};
-template <typename H8> struct Row8Half {
-  using Raw = u32x4;
-  static constexpr int kRun = 16;  // tokens per wave: 16 rows of 16 bytes in flight per lane
-  __device__ __forceinline__ static Raw load(__amdgpu_buffer_rsrc_t r, unsigned voff, unsigned soff) {
-    return __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0);
-  }
-  __device__ __forceinline__ static void unpack(const Raw& r, float (&x)[8]) {
-    const H8 h = __builtin_bit_cast(H8, r);
-#pragma unroll
-    for (int e = 0; e < 8; ++e) x[e] = (float)h[e];
-  }
-  __device__ __forceinline__ static void store(__amdgpu_buffer_rsrc_t r, unsigned voff, unsigned soff, const float (&x)[8]) {
-    H8 h;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) h[e] = (decltype(h[0] + 0))x[e];
-    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, h), r, voff, soff, 0);
-  }
-};
-template <> struct Row8<__bf16> : Row8Half<bf16x8> {};
-template <> struct Row8<_Float16> : Row8Half<f16x8> {};
 
 // A wave owns a run of Row8<TZ>::kRun consecutive tokens of one batch row and 64 segments of 8
 // features. Every load of the run (its rows, the K - 1 rows before it, the taps) is issued before
@@ -220,8 +174,83 @@ int key_filter(const TZ* z, const float* history, const float* taps, TZ* out, in
   return check_launch(who);
 }
 
+// out[c] = sum over r < rows of in[r, c], 16 columns per workgroup: 64 row groups (one per lane of
+// a wave's worth of threads per column quad) each add the rows g, g + 64, g + 128, ... in order,
+// eight loads issued before their adds; then groups 0..7 each add eight group sums (g, g + 8, ...)
+// and group 0 adds those eight, all in a fixed order for a shape (deterministic).
+__global__ __launch_bounds__(256) void tap_sum_kernel(const float* __restrict__ in, float* __restrict__ out, int rows,
+                                                      int cols) {
+  constexpr int kGroups = 64, kBatch = 8;
+  __shared__ f32x4 part[kGroups][4];
+  const int cq = threadIdx.x & 3, rg = threadIdx.x >> 2;
+  const int c = 4 * (4 * blockIdx.x + cq);
+  f32x4 s = {0.f, 0.f, 0.f, 0.f};
+  if (c < cols) {
+    int r = rg;
+    for (; r + (kBatch - 1) * kGroups < rows; r += kBatch * kGroups) {
+      f32x4 v[kBatch];
+#pragma unroll
+      for (int u = 0; u < kBatch; ++u) v[u] = *reinterpret_cast<const f32x4*>(in + (size_t)(r + u * kGroups) * cols + c);
+#pragma unroll
+      for (int u = 0; u < kBatch; ++u) s += v[u];
+    }
+    for (; r < rows; r += kGroups) s += *reinterpret_cast<const f32x4*>(in + (size_t)r * cols + c);
+  }
+  part[rg][cq] = s;
+  __syncthreads();
+  if (rg < 8) {
+    f32x4 t = part[rg][cq];
+#pragma unroll
+    for (int g = 1; g < 8; ++g) t += part[rg + 8 * g][cq];
+    part[rg][cq] = t;  // only group rg reads or writes row rg here
+  }
+  __syncthreads();
+  if (rg == 0 && c < cols) {
+    f32x4 t = part[0][cq];
+#pragma unroll
+    for (int g = 1; g < 8; ++g) t += part[g][cq];
+    *reinterpret_cast<f32x4*>(out + c) = t;
+  }
+}
+
+__global__ __launch_bounds__(256) void zero_fill_kernel(float* __restrict__ p, size_t n) {
+  const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+  if (i < n) p[i] = 0.f;
+}
+
 }  // namespace
+
+size_t key_backward_parts(int B, int N) {
+  return (size_t)B * (size_t)((N + kBackRun * kBackWaves - 1) / (kBackRun * kBackWaves));
+}
+
+size_t key_backward_workspace(int B, int N, int D, int K) {
+  if (B <= 0 || N <= 0 || D <= 0 || K < 1) return 0;
+  return key_backward_parts(B, N) * (size_t)K * D * sizeof(float);
+}
+
+// No token: the taps' and the history's gradients are zero (fill kernels, capturable).
+int key_backward_empty(float* grad_taps, float* grad_history, int B, int D, int K, hipStream_t stream, const char* who) {
+  const size_t cols = (size_t)K * D;
+  hipLaunchKernelGGL(zero_fill_kernel, dim3((unsigned)((cols + 255) / 256)), dim3(256), 0, stream, grad_taps, cols);
+  const size_t nh = (size_t)B * (K - 1) * D;
+  if (grad_history && nh)
+    hipLaunchKernelGGL(zero_fill_kernel, dim3((unsigned)((nh + 255) / 256)), dim3(256), 0, stream, grad_history, nh);
+  return check_launch(who);
+}
+
+// The workgroups' partials of the taps' gradient summed into grad_taps in one pass, in a fixed order.
+int key_backward_sum_taps(float* partial, float* grad_taps, int B, int N, int D, int K, hipStream_t stream,
+                          const char* who) {
+  const size_t cols = (size_t)K * D;
+  const int parts = (int)key_backward_parts(B, N);
+  hipLaunchKernelGGL(tap_sum_kernel, dim3((unsigned)((cols + 15) / 16)), dim3(256), 0, stream, partial, grad_taps,
+                     parts, (int)cols);
+  return check_launch(who);
+}
+
 }  // namespace vsp
+
 
 extern "C" int vsp_key_filter_bf16(const void* z, const float* history, const float* taps, void* keys, int B, int N,
                                    int D, int heads, int K, void* stream) {
@@ -238,4 +267,8 @@ extern "C" int vsp_key_filter_f16(const void* z, const float* history, const flo
 extern "C" int vsp_key_filter_f32(const float* z, const float* history, const float* taps, float* keys, int B, int N,
                                   int D, int heads, int K, void* stream) {
   return vsp::key_filter<float>(z, history, taps, keys, B, N, D, heads, K, stream, "vsp_key_filter_f32");
+}
+
+extern "C" size_t vsp_key_filter_backward_workspace_bytes(int B, int N, int D, int K) {
+  return vsp::key_backward_workspace(B, N, D, K);
 }

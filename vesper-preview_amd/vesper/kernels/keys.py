@@ -1,16 +1,20 @@
-"""The causal key filter and key normalization on MI355X: a HIP kernel behind the reference's contract.
+"""The causal key filter and key normalization on MI355X: HIP kernels behind the reference's contract.
 
-``fused_keys(z, history, taps, heads)`` keeps the signature and result of the reference's
-``vesper/kernels/keys.py:28-32`` (what ``RecurrentSublayer.keys``, ``vesper/column.py:255-289``,
-computes for its key): ``u[t] = sum_r taps[r] * z[t - r]`` with the chunk's predecessors from
-``history``, then ``normalize_keys`` per head, float32 arithmetic, the key in ``z``'s dtype. Where
-the reference runs a Triton kernel, this calls ``vsp_key_filter_{bf16,f16,f32}`` through the C ABI.
+``fused_keys(z, history, taps, heads)`` keeps the signature, result and gradients of the
+reference's ``vesper/kernels/keys.py:28-78`` (what ``RecurrentSublayer.keys``,
+``vesper/column.py:255-289``, computes for its key): ``u[t] = sum_r taps[r] * z[t - r]`` with the
+chunk's predecessors from ``history``, then ``normalize_keys`` per head, float32 arithmetic, the key
+in ``z``'s dtype. Where the reference runs Triton kernels, this calls ``vsp_key_filter_*`` (forward)
+and ``vsp_key_filter_backward_*`` (the gradients of ``z``, ``taps`` and, when it needs one,
+``history``; the normalization's peak held constant as the reference detaches it) through the C ABI.
 
 For: float32, bfloat16 or float16 key inputs on the GPU, a filter of 1 to 8 taps, head widths that
-are powers of two from 8 to 512. Forward only: inputs that need a gradient are refused.
+are powers of two from 8 to 512.
 """
 
 from __future__ import annotations
+
+from typing import Any
 
 import torch
 from torch import Tensor
@@ -20,7 +24,7 @@ from vesper.kernels import _lib
 
 FUSED_KEY_DTYPES = (torch.float32, torch.bfloat16, torch.float16)
 MAX_TAPS = 8
-_ENTRY = {torch.bfloat16: "vsp_key_filter_bf16", torch.float16: "vsp_key_filter_f16", torch.float32: "vsp_key_filter_f32"}
+_SUFFIX = {torch.bfloat16: "bf16", torch.float16: "f16", torch.float32: "f32"}
 
 
 def _aligned(t: Tensor) -> Tensor:
@@ -28,17 +32,7 @@ def _aligned(t: Tensor) -> Tensor:
     return t if t.data_ptr() % 16 == 0 else t.clone()
 
 
-def fused_keys(z: Tensor, history: Tensor, taps: Tensor, heads: int) -> Tensor:
-    """Normalized keys ``[b, n, heads, d / heads]`` in ``z``'s dtype (``z [b, n, d]`` on the GPU).
-
-    ``history [b, K-1, d]`` holds the ``K - 1`` key inputs before the chunk (oldest first) and
-    ``taps [K, d]`` the filter, tap 0 on the current token; both are used in float32.
-
-    Raises:
-        ContractError: on shapes that disagree, a dtype outside float32/bfloat16/float16, tensors
-            off the GPU or on different devices, a filter wider than 8 taps, a head width that is
-            not a power of two in 8..512, or inputs needing a gradient.
-    """
+def _check(z: Tensor, history: Tensor, taps: Tensor, heads: int) -> tuple[int, int, int, int]:
     dims: Dims = {}
     check_shape("z", z, ("b", "n", "d"), dims)
     check_shape("taps", taps, ("K", "d"), dims)
@@ -52,22 +46,72 @@ def fused_keys(z: Tensor, history: Tensor, taps: Tensor, heads: int) -> Tensor:
     for name, t in (("history", history), ("taps", taps)):
         if t.device != z.device:
             raise ContractError(f"{name} is on {t.device}, z on {z.device}")
-    if any(t.requires_grad for t in (z, history, taps)):
-        raise ContractError("fused_keys is forward only here: an input requires a gradient")
     if not 1 <= width <= MAX_TAPS:
         raise ContractError(f"taps: the kernel takes 1..{MAX_TAPS} taps, got {width}")
-    b, n, d = dims["b"], dims["n"], dims["d"]
+    d = dims["d"]
     if heads < 1 or d % heads != 0:
         raise ContractError(f"{d} features are not a multiple of {heads} heads")
     head_dim = d // heads
     if head_dim < 8 or head_dim > 512 or head_dim & (head_dim - 1):
         raise ContractError(f"head width {head_dim}: the kernel takes powers of two 8..512")
-    out = torch.empty(b, n, heads, head_dim, dtype=z.dtype, device=z.device)
-    if b == 0 or n == 0:
+    return dims["b"], dims["n"], d, width
+
+
+class _FusedKeys(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx: Any, z: Tensor, history: Tensor, taps: Tensor, heads: int) -> Tensor:  # noqa: D102
+        b, n, d, width = _check(z, history, taps, heads)
+        zc = _aligned(z)
+        hist = _aligned(history.detach().to(torch.float32))
+        wide = _aligned(taps.detach().to(torch.float32))
+        out = torch.empty(b, n, heads, d // heads, dtype=z.dtype, device=z.device)
+        if b and n:
+            _lib.call(f"vsp_key_filter_{_SUFFIX[z.dtype]}", _lib.ptr(zc), _lib.ptr(hist) if width > 1 else None,
+                      _lib.ptr(wide), _lib.ptr(out), b, n, d, heads, width, _lib.stream_of(z.device))
+        ctx.save_for_backward(zc, hist, wide)
+        ctx.heads = heads
+        ctx.dtypes = (history.dtype, taps.dtype)
         return out
-    zc = _aligned(z)
-    hc = _aligned(history.to(torch.float32))
-    tc = _aligned(taps.to(torch.float32))
-    _lib.call(_ENTRY[z.dtype], _lib.ptr(zc), _lib.ptr(hc) if width > 1 else None, _lib.ptr(tc), _lib.ptr(out),
-              b, n, d, heads, width, _lib.stream_of(z.device))
+
+    @staticmethod
+    def backward(ctx: Any, grad_keys: Tensor) -> tuple[Tensor | None, Tensor | None, Tensor | None, None]:  # noqa: D102
+        zc, hist, wide = ctx.saved_tensors
+        heads: int = ctx.heads
+        b, n, d = zc.shape
+        width = int(wide.shape[0])
+        g = _aligned(grad_keys.to(zc.dtype).reshape(b, n, d))
+        grad_z = torch.empty_like(zc)
+        grad_taps = torch.empty(width, d, dtype=torch.float32, device=zc.device)
+        want_history = ctx.needs_input_grad[1] and width > 1
+        grad_history = torch.empty(b, width - 1, d, dtype=torch.float32, device=zc.device) if want_history else None
+        nbytes = int(_lib.library().vsp_key_filter_backward_workspace_bytes(b, n, d, width))
+        workspace = torch.empty(max(nbytes, 16), dtype=torch.uint8, device=zc.device)
+        _lib.call(f"vsp_key_filter_backward_{_SUFFIX[zc.dtype]}", _lib.ptr(zc),
+                  _lib.ptr(hist) if width > 1 else None, _lib.ptr(wide), _lib.ptr(g), _lib.ptr(grad_z),
+                  _lib.ptr(grad_taps), None if grad_history is None else _lib.ptr(grad_history),
+                  _lib.ptr(workspace), nbytes, b, n, d, heads, width, _lib.stream_of(zc.device))
+        history_dtype, taps_dtype = ctx.dtypes
+        d_history = None
+        if ctx.needs_input_grad[1]:
+            d_history = grad_history.to(history_dtype) if grad_history is not None else torch.zeros(
+                b, 0, d, dtype=history_dtype, device=zc.device)
+        return (grad_z if ctx.needs_input_grad[0] else None, d_history,
+                grad_taps.to(taps_dtype) if ctx.needs_input_grad[2] else None, None)
+
+
+def fused_keys(z: Tensor, history: Tensor, taps: Tensor, heads: int) -> Tensor:
+    """Normalized keys ``[b, n, heads, d / heads]`` in ``z``'s dtype (``z [b, n, d]`` on the GPU).
+
+    ``history [b, K-1, d]`` holds the ``K - 1`` key inputs before the chunk (oldest first) and
+    ``taps [K, d]`` the filter, tap 0 on the current token; both are used in float32. Under autograd
+    the gradients of ``z`` (in its dtype), ``taps`` and ``history`` (in theirs) come from the
+    backward kernel.
+
+    Raises:
+        ContractError: on shapes that disagree, a dtype outside float32/bfloat16/float16, tensors
+            off the GPU or on different devices, a filter wider than 8 taps, or a head width that
+            is not a power of two in 8..512.
+    """
+    _check(z, history, taps, heads)  # the contract first, before autograd records anything
+    out: Tensor = _FusedKeys.apply(z, history, taps, heads)
     return out
