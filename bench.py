@@ -9,7 +9,8 @@ kernel's own rate at its own configuration (attention alone at B=4), the key fil
 scan (B8 T4096 d512 = 8 heads of 64, 4 taps, bf16), the decode rate (256
 single-token steps of batch 64: fp32 delta update of S [64,8,64,64] then attention over a 512-entry
 bf16 KV ring, captured as one HIP graph), the looped column with per-token halting (B4 T2048 d512,
-8 passes), the roofline of the dominant kernel measured with HIP
+8 passes, 4-tap key filter), the column's captured single-token decoder (batch 64, 8 passes), the
+roofline of the dominant kernel measured with HIP
 events on the launch stream inside the timed region, and the CPU oracle timed on a bounded sample
 of the same workload on this host's cores.
 
@@ -271,26 +272,62 @@ def time_decode(torch, reps: int = 5) -> dict:
 
 
 def time_looped(torch, reps: int = 3) -> dict:
-    """The looped column with halting: B4 T2048 d512 H8 d64, 8 passes, window 512, p_halt 0.3."""
+    """The looped column with halting: B4 T2048 d512 H8 d64, 8 passes, window 512, 4-tap key filter,
+    p_halt 0.3."""
     from vesper.loop import LoopedColumn
 
     dev = torch.device("cuda:0")
     b, n, d, h, dk, passes = LOOP_B, LOOP_T, LOOP_D, H, D, LOOP_PASSES
-    column = LoopedColumn.random(d, h, h, dk, WINDOW, passes, seed=11, device=dev)
+    column = LoopedColumn.random(d, h, h, dk, WINDOW, passes, seed=11, device=dev, key_conv=KEY_TAPS)
     g = torch.Generator().manual_seed(12)
     x0 = torch.randn(b, n, d, generator=g).to(dev)
     exits = [(torch.rand(b, n, generator=g) < 0.3).to(dev) for _ in range(passes)]
     states = [torch.zeros(b, h, dk, dk, device=dev) for _ in range(passes)]
-    column.forward(x0, states, exits)  # warm-up
+    histories = [torch.zeros(b, KEY_TAPS - 1, d, device=dev) for _ in range(passes)]
+    column.forward(x0, states, exits, histories)  # warm-up
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     e0.record()
     for _ in range(reps):
-        out = column.forward(x0, states, exits)
+        out = column.forward(x0, states, exits, histories)
     e1.record()
     torch.cuda.synchronize()
     ms = e0.elapsed_time(e1) / reps
     return {"ms": ms, "tok_s": b * n / (ms / 1e3), "mean_passes": float(out.n_iters.float().mean())}
+
+
+def time_column_decode(torch, steps: int = 64) -> dict:
+    """The column's captured single-token decoder: batch 64, d512 (8 heads of 64, 8 KV heads),
+    window 512, 4-tap key filter, all 8 passes dense; rings full (positions 0..511 written), the
+    timed tokens at positions 512 onwards; one step = one HIP graph replay."""
+    from vesper.decode import PER_PASS, CapturedDecoder
+    from vesper.loop import LoopedColumn
+
+    dev = torch.device("cuda:0")
+    b, d, h, dk, passes = DEC_B, LOOP_D, H, D, LOOP_PASSES
+    column = LoopedColumn.random(d, h, h, dk, DEC_W, passes, seed=21, device=dev, key_conv=KEY_TAPS)
+    decoder = CapturedDecoder(column, passes)
+    flat = decoder.start(b)
+    g = torch.Generator().manual_seed(22)
+    for t in range(passes):
+        flat[PER_PASS * t + 2].copy_(torch.randn(b, DEC_W, h, dk, generator=g).to(torch.bfloat16))
+        flat[PER_PASS * t + 3].copy_(torch.randn(b, DEC_W, h, dk, generator=g).to(torch.bfloat16))
+        flat[PER_PASS * t + 4].copy_(torch.arange(DEC_W).expand(b, DEC_W))
+        flat[PER_PASS * t + 5].fill_(True)
+    xs = torch.randn(steps + 8, b, 1, d, generator=g).to(dev)
+    pos = (DEC_W + torch.arange(steps + 8)).view(-1, 1, 1).expand(-1, b, 1).contiguous().to(dev)
+    with torch.no_grad():
+        for i in range(8):  # warm-up, then the capture, then replays
+            _, flat = decoder.step(xs[i], pos[i], flat)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        e0.record()
+        for i in range(8, steps + 8):
+            _, flat = decoder.step(xs[i], pos[i], flat)
+        e1.record()
+        torch.cuda.synchronize()
+    us = e0.elapsed_time(e1) / steps * 1e3
+    return {"us_per_step": us, "tok_s": b / (us / 1e6), "captures": decoder.captures, "replays": decoder.replays}
 
 
 # ---- CPU baseline ---------------------------------------------------------------------------------
@@ -416,6 +453,7 @@ def main() -> int:
     keys_ms, keys_bwd_ms = time_key_filter(torch)
     dec = None if args.no_decode else time_decode(torch)
     looped = None if args.no_loop else time_looped(torch)
+    col_dec = None if args.no_decode else time_column_decode(torch)
 
     scan_dominant = pre["scan_ms"] >= pre["attn_ms"]
     if scan_dominant:
@@ -482,11 +520,19 @@ def main() -> int:
             "hbm_frac": round(step_bytes / (dec["us_per_step"] / 1e6) / 1e9 / HBM_PEAK_GBS, 4),
             "algorithmic_bytes_per_step": step_bytes,
         }
+    if col_dec is not None:
+        result["column_decode"] = {
+            "workload": "captured single-token decode of the looped column: batch 64, d512 H8 d64, 8 passes dense, "
+                        "each pass key filter (4 taps) + fp32 delta step + attention over a full 512-entry bf16 KV "
+                        "ring, bf16 projections; one HIP graph replay per step",
+            "tok_s": round(col_dec["tok_s"], 1), "us_per_step": round(col_dec["us_per_step"], 3),
+            "us_per_pass": round(col_dec["us_per_step"] / LOOP_PASSES, 3),
+        }
     if looped is not None:
         result["looped_column"] = {
-            "workload": "looped column with per-token halting: B4 T2048 d512 H8 d64, 8 passes of delta scan + "
-                        "window attention (w512) with bf16 projections (fixed N(0, 1/512) weights), p_halt 0.3, "
-                        "copy-forward of halted tokens",
+            "workload": "looped column with per-token halting: B4 T2048 d512 H8 d64, 8 passes of key filter (4 taps) "
+                        "+ delta scan + window attention (w512) with bf16 projections (fixed N(0, 1/512) weights), "
+                        "p_halt 0.3, copy-forward of halted tokens",
             "tok_s": round(looped["tok_s"], 1), "ms": round(looped["ms"], 3),
             "mean_active_passes": round(looped["mean_passes"], 3),
         }

@@ -11,9 +11,12 @@ Restated from the reference's pass loop and column:
 - ``mixer_column_step`` is the column's two mixers as ``Column.step`` orders them
   (``vesper/column.py:709-812``): recurrent projections, the carry merges of ``k, v, beta``
   (``:784-789``), the delta scan, the residual; attention projections, the carry merges of the
-  attention keys and values (``:795-796``), window attention, the residual. Norms, the key
-  filter, rotary and the FFN are not part of the mixer path and are left out; queries and keys
-  are L2-normalised (``normalize_keys``) as the scan requires.
+  attention keys and values (``:795-796``), window attention, the residual; optionally the causal
+  key filter before the keys' normalization (``RecurrentSublayer.keys``, ``:255-289``), its
+  history carried per pass. Norms, rotary and the FFN are not part of the mixer path and are left
+  out; queries and keys are L2-normalised (``normalize_keys``) as the scan requires.
+- ``mixer_decode_step`` is the same column one token at a time over per-pass KV rings, at a fixed
+  depth with every pass dense, as ``decode_step`` (``vesper/decode.py:29-46``) runs it.
 
 Rounding points mirror the GPU path (``vesper/loop.py``): the residual stream stays in the wide
 dtype; every matmul takes bf16-rounded operands and returns a bf16-rounded product; the mixers
@@ -28,8 +31,9 @@ from dataclasses import dataclass
 import torch
 from torch import Tensor
 
-from oracle.attention import window_attention
-from oracle.delta import delta_scan_chunked, normalize_keys
+from oracle.attention import kv_ring_write, ring_attend, window_attention
+from oracle.delta import delta_scan_chunked, delta_scan_step, normalize_keys
+from oracle.keys import filter_keys
 
 BF16 = torch.bfloat16
 
@@ -43,6 +47,7 @@ class Written:
     beta: Tensor  # [b, n, h]
     attn_k: Tensor  # [b, n, hkv, dk]
     attn_v: Tensor  # [b, n, hkv, dk]
+    z: Tensor | None = None  # [b, n, h*dk] the key filter's input (with a filter)
 
 
 # step(x, pass_index, state, carry) -> (out, new_state, written); carry = (active, carried Written)
@@ -56,9 +61,10 @@ def _where_tokens(mask: Tensor, a: Tensor, b: Tensor) -> Tensor:
 
 def merge(halts: Tensor, fresh: Written, previous: Written) -> Written:
     """Tokens halting now freeze their fresh projections; the others keep the previous ones (``loop.py:523-537``)."""
+    z = None if fresh.z is None or previous.z is None else _where_tokens(halts, fresh.z, previous.z)
     return Written(*(_where_tokens(halts, f, p) for f, p in zip(
         (fresh.k, fresh.v, fresh.beta, fresh.attn_k, fresh.attn_v),
-        (previous.k, previous.v, previous.beta, previous.attn_k, previous.attn_v))))
+        (previous.k, previous.v, previous.beta, previous.attn_k, previous.attn_v))), z=z)
 
 
 def carry_in(active: Tensor, fresh: Tensor, carried: Tensor) -> Tensor:
@@ -128,35 +134,114 @@ class MixerWeights:
     kv_heads: int
     head_dim: int
     window: int
+    taps: Sequence[Tensor] | None = None  # per pass [K, h*dk]: the causal key filter, or none
 
 
-def mixer_column_step(weights: MixerWeights, masked: bool = True) -> ColumnStep:
+def _keys(weights: MixerWeights, t: int, z: Tensor, history: Tensor | None, rnd: Callable[[Tensor], Tensor]
+          ) -> tuple[Tensor, Tensor | None]:
+    """``RecurrentSublayer.keys`` (``column.py:255-289``): the filter (if any), then ``normalize_keys``."""
+    b, n, _ = z.shape
+    h, dk = weights.heads, weights.head_dim
+    if weights.taps is None:
+        return rnd(normalize_keys(z.view(b, n, h, dk))), history
+    assert history is not None
+    keys, nxt = filter_keys(z, history, weights.taps[t], h)
+    return rnd(keys), nxt
+
+
+def mixer_column_step(weights: MixerWeights, masked: bool = True, bf16: bool = True) -> ColumnStep:
     """The config's column: delta scan then window attention, each with its residual (see module doc).
 
     With ``masked`` the mixers take the active mask (inactive outputs zero, their writes kept);
-    without it they run densely over every token, as the reference's mixers do.
+    without it they run densely over every token, as the reference's mixers do. With a key filter
+    (``weights.taps``) a pass's state is ``(scan state, key history)`` and a halted token's key
+    input is carried into the filter, its key after it (``column.py:779-789``). ``bf16`` False
+    drops the bf16 rounding points (the arithmetic alone, in the inputs' dtype).
     """
     h, hkv, dk, w = weights.heads, weights.kv_heads, weights.head_dim, weights.window
+    rnd = _bf if bf16 else (lambda t: t)
 
-    def step(x: Tensor, t: int, state: Tensor, carry: tuple[Tensor, Written] | None) -> tuple[Tensor, Tensor, Written]:
+    def mm(x: Tensor, m: Tensor) -> Tensor:
+        return _mm(x, m) if bf16 else x @ m
+
+    def step(x: Tensor, t: int, state, carry: tuple[Tensor, Written] | None):
         b, n, _ = x.shape
         active = None if carry is None else carry[0]
         mask = active if masked else None
-        q = _bf(normalize_keys(_mm(x, weights.wq[t]).view(b, n, h, dk)))
-        k = _bf(normalize_keys(_mm(x, weights.wk[t]).view(b, n, h, dk)))
-        v = _mm(x, weights.wv[t]).view(b, n, h, dk)
-        beta = _bf(torch.sigmoid(_mm(x, weights.wb[t])))
+        scan_state, history = state if weights.taps is not None else (state, None)
+        q = rnd(normalize_keys(mm(x, weights.wq[t]).view(b, n, h, dk)))
+        z = mm(x, weights.wk[t]).view(b, n, h * dk)
+        if carry is not None and carry[1].z is not None:
+            z = carry_in(active, z, carry[1].z)
+        k, history = _keys(weights, t, z, history, rnd)
+        v = mm(x, weights.wv[t]).view(b, n, h, dk)
+        beta = rnd(torch.sigmoid(mm(x, weights.wb[t])))
         if carry is not None:
             k, v, beta = (carry_in(active, f, c) for f, c in zip((k, v, beta), (carry[1].k, carry[1].v, carry[1].beta)))
-        r, new_state = delta_scan_chunked(q, k, v, beta, state, 64, active=mask)
-        x1 = x + _bf(r).reshape(b, n, h * dk)
-        aq = _mm(x1, weights.waq[t]).view(b, n, h, dk)
-        ak = _mm(x1, weights.wak[t]).view(b, n, hkv, dk)
-        av = _mm(x1, weights.wav[t]).view(b, n, hkv, dk)
+        r, new_state = delta_scan_chunked(q, k, v, beta, scan_state, 64, active=mask)
+        x1 = x + rnd(r).reshape(b, n, h * dk)
+        aq = mm(x1, weights.waq[t]).view(b, n, h, dk)
+        ak = mm(x1, weights.wak[t]).view(b, n, hkv, dk)
+        av = mm(x1, weights.wav[t]).view(b, n, hkv, dk)
         if carry is not None:
             ak, av = (carry_in(active, f, c) for f, c in zip((ak, av), (carry[1].attn_k, carry[1].attn_v)))
         a = window_attention(aq, ak, av, w, active=mask)
-        x2 = x1 + _bf(a).reshape(b, n, h * dk)
-        return x2, new_state, Written(k=k, v=v, beta=beta, attn_k=ak, attn_v=av)
+        x2 = x1 + rnd(a).reshape(b, n, h * dk)
+        written = Written(k=k, v=v, beta=beta, attn_k=ak, attn_v=av, z=z if weights.taps is not None else None)
+        return x2, (new_state, history) if weights.taps is not None else new_state, written
+
+    return step
+
+
+# one pass's decoding state: (scan state, key history or None, (ring k, ring v, ring pos, ring valid))
+DecodeState = tuple[Tensor, "Tensor | None", tuple[Tensor, Tensor, Tensor, Tensor]]
+
+
+def cold_decode_states(weights: MixerWeights, b: int, dtype: torch.dtype) -> list[DecodeState]:
+    """Zero scan states and key histories, unwritten rings (``init_column_state(..., ring=True)``,
+    ``column.py:465-500``), one per pass."""
+    h, hkv, dk, w = weights.heads, weights.kv_heads, weights.head_dim, weights.window
+    out = []
+    for t in range(len(weights.wq)):
+        hist = None if weights.taps is None else torch.zeros(b, weights.taps[t].shape[0] - 1, h * dk, dtype=dtype)
+        ring = (torch.zeros(b, w, hkv, dk, dtype=dtype), torch.zeros(b, w, hkv, dk, dtype=dtype),
+                torch.zeros(b, w, dtype=torch.long), torch.zeros(b, w, dtype=torch.bool))
+        out.append((torch.zeros(b, h, dk, dk, dtype=dtype), hist, ring))
+    return out
+
+
+def mixer_decode_step(weights: MixerWeights, depth: int, bf16: bool = True
+                      ) -> Callable[[Tensor, Tensor, Sequence[DecodeState]], tuple[Tensor, list[DecodeState]]]:
+    """One token per row through the first ``depth`` passes, every pass dense (``DenseRule``):
+    the column's step with the delta rule's single step (``recurrence.py:143-163``) and attention
+    over the pass's ring followed by the ring write (``attend_ring``, ``attention.py:298-338``),
+    as ``decode_step`` (``vesper/decode.py:29-46``) runs the column. Returns ``(y [b, 1, d], states)``
+    with new state objects for the first ``depth`` passes and the others unchanged."""
+    h, hkv, dk, w = weights.heads, weights.kv_heads, weights.head_dim, weights.window
+    rnd = _bf if bf16 else (lambda t: t)
+
+    def mm(x: Tensor, m: Tensor) -> Tensor:
+        return _mm(x, m) if bf16 else x @ m
+
+    def step(x: Tensor, pos: Tensor, states: Sequence[DecodeState]) -> tuple[Tensor, list[DecodeState]]:
+        b = x.shape[0]
+        new = list(states)
+        for t in range(depth):
+            scan_state, history, (rk, rv, rp, rvalid) = states[t]
+            q = rnd(normalize_keys(mm(x, weights.wq[t]).view(b, 1, h, dk)))
+            z = mm(x, weights.wk[t]).view(b, 1, h * dk)
+            k, history = _keys(weights, t, z, history, rnd)
+            v = mm(x, weights.wv[t]).view(b, 1, h, dk)
+            beta = rnd(torch.sigmoid(mm(x, weights.wb[t])))
+            o, scan_state = delta_scan_step(q[:, 0], k[:, 0], v[:, 0], beta[:, 0], scan_state)
+            x1 = x + rnd(o).reshape(b, 1, h * dk)
+            aq = mm(x1, weights.waq[t]).view(b, 1, h, dk)
+            ak = mm(x1, weights.wak[t]).view(b, 1, hkv, dk)
+            av = mm(x1, weights.wav[t]).view(b, 1, hkv, dk)
+            a = ring_attend(aq, ak, av, pos, rk, rv, rp, rvalid, w)
+            ring = kv_ring_write(rk, rv, rp, rvalid, ak, av, pos)
+            x = x1 + rnd(a).reshape(b, 1, h * dk)
+            new[t] = (scan_state, history, ring)
+        return x, new
 
     return step

@@ -107,3 +107,29 @@ def test_refusals():
         column.forward(x0, states[:1], exits)
     with pytest.raises(ContractError, match="axis"):
         column.forward(x0, states, [torch.zeros(1, 9, dtype=torch.bool, device=GPU)] * 2)
+
+
+def test_the_loop_with_a_key_filter_matches_the_oracle():
+    # halted tokens carry their frozen key input into the filter of later passes and their key
+    # after it (column.py:779-789); each pass keeps its own key history
+    from vesper.loop import LoopedColumn
+
+    b, n, d, h, hkv, dk, w, passes, width = 2, 150, 128, 2, 2, 64, 64, 3, 4
+    column = LoopedColumn.random(d, h, hkv, dk, w, passes, 11, GPU, key_conv=width)
+    g = torch.Generator().manual_seed(12)
+    x0 = torch.randn(b, n, d, generator=g)
+    exits = [torch.rand(b, n, generator=g) < 0.3 for _ in range(passes)]
+    states = [0.02 * torch.randn(b, h, dk, dk, generator=g) for _ in range(passes)]
+    histories = [torch.randn(b, width - 1, d, generator=g) for _ in range(passes)]
+    got = column.forward(x0.to(GPU), [s.to(GPU) for s in states], [e.to(GPU) for e in exits],
+                         [z.to(GPU) for z in histories])
+    ws = {name: [t.to("cpu", torch.float64) for t in column.w[name]] for name in column.w}
+    weights = ol.MixerWeights(**ws, heads=h, kv_heads=hkv, head_dim=dk, window=w,
+                              taps=[t.to("cpu", torch.float64) for t in column.taps])
+    want = ol.loop_forward(x0.double(), ol.mixer_column_step(weights),
+                           [(s.double(), z.double()) for s, z in zip(states, histories)], exits)
+    assert torch.equal(got.n_iters.cpu(), want.n_iters)
+    assert relative_error(got.y, want.y) < 3e-2
+    for t in range(passes):
+        assert relative_error(got.states[t], want.states[t][0]) < 3e-2, t
+        assert relative_error(got.histories[t], want.states[t][1]) < 1e-2, t

@@ -129,3 +129,60 @@ def test_masked_mixers_equal_dense_mixers_for_every_active_token():
     for t in range(passes):
         sel = halt_pass == t
         assert torch.equal(masked.y[sel], masked.per_pass[t][sel])
+
+
+def _filter_weights(d, h, hkv, dk, w, passes, seed, width):
+    base = _mixer_weights(d, h, hkv, dk, w, passes, seed)
+    g = torch.Generator().manual_seed(seed + 100)
+    taps = [(torch.rand(width, h * dk, generator=g, dtype=F64) * 2 - 1) / width**0.5 for _ in range(passes)]
+    return ol.MixerWeights(**{f: getattr(base, f) for f in ("wq", "wk", "wv", "wb", "waq", "wak", "wav")},
+                           heads=h, kv_heads=hkv, head_dim=dk, window=w, taps=taps)
+
+
+@pytest.mark.parametrize("width", [0, 3])
+def test_tokenwise_ring_decoding_equals_the_chunked_forward(width):
+    # the reference's own check of its decoder (tests/test_decode.py:45-76): the chunked forward
+    # over the whole sequence is the truth for the tokenwise ring step; window 6 against 20
+    # tokens, so every ring wraps three times; exact arithmetic here (float64, no bf16 rounding)
+    d, h, hkv, dk, w, passes, depth, b, n = 16, 2, 1, 8, 6, 3, 2, 2, 20
+    weights = (_mixer_weights(d, h, hkv, dk, w, passes, seed=8) if width == 0
+               else _filter_weights(d, h, hkv, dk, w, passes, seed=8, width=width))
+    g = torch.Generator().manual_seed(9)
+    x0 = torch.randn(b, n, d, generator=g, dtype=F64)
+    cold = ol.cold_decode_states(weights, b, F64)
+    chunk_states = [(c[0], c[1]) if width else c[0] for c in cold[:depth]]
+    exits = [torch.zeros(b, n, dtype=torch.bool)] * depth
+    chunked = ol.loop_forward(x0, ol.mixer_column_step(weights, masked=False, bf16=False), chunk_states, exits)
+    step = ol.mixer_decode_step(weights, depth, bf16=False)
+    states = cold
+    for i in range(n):
+        y, states = step(x0[:, i : i + 1], torch.full((b, 1), i, dtype=torch.long), states)
+        torch.testing.assert_close(y, chunked.y[:, i : i + 1], rtol=1e-10, atol=1e-10)
+    for t in range(depth):
+        want = chunked.states[t] if width == 0 else chunked.states[t][0]
+        torch.testing.assert_close(states[t][0], want, rtol=1e-10, atol=1e-12)
+        if width:
+            # the newest K - 1 key inputs (per-token and whole-chunk matmuls round alike to 1e-12)
+            torch.testing.assert_close(states[t][1], chunked.states[t][1], rtol=1e-12, atol=1e-12)
+        assert states[t][2][3].all() and torch.equal(states[t][2][2].sort(dim=1).values,
+                                                      torch.arange(n - w, n).expand(b, w))
+    for t in range(depth, passes):  # passes past the depth are left as they were
+        assert states[t] is cold[t]
+
+
+def test_the_decode_pin_catches_a_planted_mistake():
+    d, h, hkv, dk, w, passes, depth, b, n = 16, 2, 1, 8, 6, 2, 2, 1, 10
+    weights = _filter_weights(d, h, hkv, dk, w, passes, seed=10, width=3)
+    g = torch.Generator().manual_seed(11)
+    x0 = torch.randn(b, n, d, generator=g, dtype=F64)
+    cold = ol.cold_decode_states(weights, b, F64)
+    exits = [torch.zeros(b, n, dtype=torch.bool)] * depth
+    chunked = ol.loop_forward(x0, ol.mixer_column_step(weights, masked=False, bf16=False),
+                              [(c[0], c[1]) for c in cold], exits)
+    step = ol.mixer_decode_step(weights, depth, bf16=False)
+    states, worst = cold, 0.0
+    for i in range(n):
+        # a ring written at the wrong slot age: the token's position one too small
+        y, states = step(x0[:, i : i + 1], torch.full((b, 1), max(i - 1, 0), dtype=torch.long), states)
+        worst = max(worst, float((y - chunked.y[:, i : i + 1]).abs().max()))
+    assert worst > 1e-3

@@ -4,10 +4,12 @@ This is the pass loop of the reference's ``Loop.forward`` (``vesper/loop.py:415-
 a given exit trace (``TraceRule``, ``:203-240``), over a column reduced to its two mixers in the
 order of ``Column.step`` (``vesper/column.py:709-812``):
 
-- recurrent sublayer: projections ``q, k, v, beta`` of the pass input (bf16 matmuls; queries and
-  keys L2-normalised, ``beta = sigmoid``), the carry merges of ``k, v, beta`` for halted tokens
-  (``column.py:784-789``), the delta scan (``vsp_delta_scan_bf16`` with the active mask), the
-  residual;
+- recurrent sublayer: projections ``q, z, v, beta`` of the pass input (bf16 matmuls; queries
+  L2-normalised, ``beta = sigmoid``), the key from the key input ``z`` (``normalize_keys``, after
+  the causal key filter when the column has one, ``column.py:255-289``, with the pass's key
+  history), the carry merges for halted tokens (their key input before the filter, ``k, v, beta``
+  after, ``column.py:779-789``), the delta scan (``vsp_delta_scan_bf16`` with the active mask),
+  the residual;
 - attention sublayer: projections, the carry merges of the attention keys and values
   (``column.py:795-796``), window attention over the chunk (``vsp_window_attn_bf16`` with the
   active mask), the residual.
@@ -15,8 +17,7 @@ order of ``Column.step`` (``vesper/column.py:709-812``):
 The loop zeroes inactive outputs, freezes the projections of tokens as they halt and writes them
 into every later pass's state (copy-forward), and carries halted tokens' hidden states forward
 unchanged (``loop.py:441-453``, ``:523-537``). All passes run even when no token is active any
-more. Norms, the key filter, rotary embeddings and the FFN are not part of the mixer path and
-are left out. The residual stream stays in float32 (autocast's convention); matmuls and mixers run
+more. Norms, rotary embeddings and the FFN are not part of the mixer path and are left out. The residual stream stays in float32 (autocast's convention); matmuls and mixers run
 in bfloat16 with the scan state in float32. Forward only.
 """
 
@@ -28,6 +29,7 @@ from dataclasses import dataclass
 import torch
 from torch import Tensor
 
+from vesper.column import recurrent_keys
 from vesper.contracts import ContractError, Dims, check_shape
 from vesper.kernels.delta_scan import delta_scan_fused
 from vesper.kernels.window_attn import window_attention
@@ -58,12 +60,14 @@ class Written:
     beta: Tensor
     attn_k: Tensor
     attn_v: Tensor
+    z: Tensor | None = None  # the key filter's input, with a filter
 
     def merged(self, halts: Tensor, previous: Written) -> Written:
         """Tokens halting now freeze these projections; the others keep ``previous`` (``loop.py:523-537``)."""
+        z = None if self.z is None or previous.z is None else _where_tokens(halts, self.z, previous.z)
         return Written(*(_where_tokens(halts, a, b) for a, b in zip(
             (self.k, self.v, self.beta, self.attn_k, self.attn_v),
-            (previous.k, previous.v, previous.beta, previous.attn_k, previous.attn_v))))
+            (previous.k, previous.v, previous.beta, previous.attn_k, previous.attn_v))), z=z)
 
 
 @dataclass(frozen=True)
@@ -71,17 +75,19 @@ class LoopResult:
     y: Tensor  # [b, n, d] float32: the hidden state each token halted with
     states: tuple[Tensor, ...]  # the scan state of every pass, [b, h, dk, dk] float32
     n_iters: Tensor  # int32 [b, n]: passes each token was active in
+    histories: tuple[Tensor, ...] | None = None  # each pass's next key history, with a filter
 
 
 class LoopedColumn:
     """One column's mixers run for ``passes`` passes with per-pass projection weights.
 
     Weights are ``[d, out]`` bfloat16 tensors per pass (``x @ w``): ``wq, wk, wv [d, h*dk]``,
-    ``wb [d, h]``, ``waq [d, h*dk]``, ``wak, wav [d, hkv*dk]``.
+    ``wb [d, h]``, ``waq [d, h*dk]``, ``wak, wav [d, hkv*dk]``; optional ``taps`` are the key
+    filter's ``[K, h*dk]`` float32 taps per pass (``wk`` then gives the filter's input).
     """
 
     def __init__(self, weights: dict[str, Sequence[Tensor]], heads: int, kv_heads: int, head_dim: int,
-                 window: int) -> None:
+                 window: int, taps: Sequence[Tensor] | None = None) -> None:
         names = ("wq", "wk", "wv", "wb", "waq", "wak", "wav")
         missing = [n for n in names if n not in weights]
         if missing:
@@ -91,11 +97,21 @@ class LoopedColumn:
             raise ValueError("every weight needs one tensor per pass")
         self.w = {n: list(weights[n]) for n in names}
         self.heads, self.kv_heads, self.head_dim, self.window = heads, kv_heads, head_dim, window
+        if taps is not None and len(taps) != self.passes:
+            raise ValueError("the key filter needs one set of taps per pass")
+        self.taps = None if taps is None else list(taps)
+
+    @property
+    def key_history(self) -> int:
+        """Key inputs a pass carries across a chunk boundary: ``K - 1`` (``column.py:75-77``)."""
+        return 0 if self.taps is None else int(self.taps[0].shape[0]) - 1
 
     @classmethod
     def random(cls, d: int, heads: int, kv_heads: int, head_dim: int, window: int, passes: int, seed: int,
-               device: torch.device) -> LoopedColumn:
-        """Fixed random weights ~ N(0, 1/d) from a CPU generator (the same values on any device)."""
+               device: torch.device, key_conv: int = 0) -> LoopedColumn:
+        """Fixed random weights ~ N(0, 1/d) from a CPU generator (the same values on any device);
+        with ``key_conv`` a filter of that width, taps ~ U(-1/sqrt(K), 1/sqrt(K)) as the
+        reference draws them (``column.py:231-233``)."""
         g = torch.Generator().manual_seed(seed)
         shapes = {"wq": heads * head_dim, "wk": heads * head_dim, "wv": heads * head_dim, "wb": heads,
                   "waq": heads * head_dim, "wak": kv_heads * head_dim, "wav": kv_heads * head_dim}
@@ -103,15 +119,31 @@ class LoopedColumn:
         for _ in range(passes):
             for name, out in shapes.items():
                 weights[name].append((torch.randn(d, out, generator=g) / d**0.5).to(device, BF16))
-        return cls(weights, heads, kv_heads, head_dim, window)
+        taps = None
+        if key_conv:
+            bound = 1.0 / key_conv**0.5
+            taps = [(torch.rand(key_conv, heads * head_dim, generator=g) * (2 * bound) - bound).to(device)
+                    for _ in range(passes)]
+        return cls(weights, heads, kv_heads, head_dim, window, taps)
 
-    def _step(self, x: Tensor, t: int, state: Tensor, active: Tensor | None,
-              carried: Written | None) -> tuple[Tensor, Tensor, Written]:
+    def keys(self, t: int, z: Tensor, history: Tensor | None) -> tuple[Tensor, Tensor | None]:
+        """Pass ``t``'s keys of key inputs ``z [b, n, h*dk]`` (bf16) and the next key history."""
+        b, n, _ = z.shape
+        if self.taps is None:
+            return _normalize(z.view(b, n, self.heads, self.head_dim)).to(BF16), history
+        assert history is not None
+        return recurrent_keys(z, history, self.taps[t], self.heads)
+
+    def _step(self, x: Tensor, t: int, state: Tensor, history: Tensor | None, active: Tensor | None,
+              carried: Written | None) -> tuple[Tensor, Tensor, Tensor | None, Written]:
         b, n, d = x.shape
         h, hkv, dk = self.heads, self.kv_heads, self.head_dim
         xb = x.to(BF16)
         q = _normalize((xb @ self.w["wq"][t]).view(b, n, h, dk)).to(BF16)
-        k = _normalize((xb @ self.w["wk"][t]).view(b, n, h, dk)).to(BF16)
+        z = xb @ self.w["wk"][t]
+        if carried is not None and active is not None and carried.z is not None:
+            z = _where_tokens(active, z, carried.z)  # a halted token's frozen key input, before the filter
+        k, history = self.keys(t, z, history)
         v = (xb @ self.w["wv"][t]).view(b, n, h, dk)
         beta = torch.sigmoid((xb @ self.w["wb"][t]).float()).to(BF16)
         if carried is not None and active is not None:
@@ -129,9 +161,11 @@ class LoopedColumn:
             av = _where_tokens(active, av, carried.attn_v)
         a = window_attention(aq, ak, av, self.window, active=active)
         x2 = x1 + a.reshape(b, n, h * dk).float()
-        return x2, new_state, Written(k=k, v=v, beta=beta, attn_k=ak, attn_v=av)
+        written = Written(k=k, v=v, beta=beta, attn_k=ak, attn_v=av, z=z if self.taps is not None else None)
+        return x2, new_state, history, written
 
-    def forward(self, x0: Tensor, states: Sequence[Tensor], exits: Sequence[Tensor]) -> LoopResult:
+    def forward(self, x0: Tensor, states: Sequence[Tensor], exits: Sequence[Tensor],
+                histories: Sequence[Tensor] | None = None) -> LoopResult:
         """All passes over ``x0 [b, n, d]`` (float32, on the GPU).
 
         Args:
@@ -139,6 +173,7 @@ class LoopedColumn:
             states: one float32 scan state ``[b, h, dk, dk]`` per pass.
             exits: per pass a bool ``[b, n]``: an active token with its exit set halts after the
                 pass; the last pass halts every token still active.
+            histories: with a key filter, one float32 key history ``[b, K-1, h*dk]`` per pass.
 
         Raises:
             ContractError: on shapes or dtypes outside that contract.
@@ -150,6 +185,12 @@ class LoopedColumn:
         for t in range(self.passes):
             check_shape(f"states[{t}]", states[t], ("b", "h", "dk", "dk"), dims, torch.float32)
             check_shape(f"exits[{t}]", exits[t], ("b", "n"), dims, torch.bool)
+        if self.taps is not None:
+            if histories is None or len(histories) != self.passes:
+                raise ContractError(f"a column with a key filter needs {self.passes} key histories")
+            dims["w"] = self.key_history
+            for t in range(self.passes):
+                check_shape(f"histories[{t}]", histories[t], ("b", "w", "d"), dims, torch.float32)
         b, n = dims["b"], dims["n"]
         with torch.no_grad():
             active = torch.ones(b, n, dtype=torch.bool, device=x0.device)
@@ -157,15 +198,18 @@ class LoopedColumn:
             carried: Written | None = None
             x = x0
             new_states = list(states)
+            new_histories: list[Tensor | None] = list(histories) if histories is not None else [None] * self.passes
             for t in range(self.passes):
                 # pass 0 runs with every token active: the unmasked kernels, as the reference's
                 # carry-free first pass
                 mask = None if carried is None else active
-                h, new_states[t], written = self._step(x, t, new_states[t], mask, carried)
+                h, new_states[t], new_histories[t], written = self._step(x, t, new_states[t], new_histories[t], mask,
+                                                                         carried)
                 h = _where_tokens(active, h, torch.zeros_like(h))
                 halts = active & exits[t] if t < self.passes - 1 else active
                 n_iters += active.to(torch.int32)
                 carried = written if carried is None else written.merged(halts, carried)
                 x = _where_tokens(active, h, x)
                 active = active & ~halts
-        return LoopResult(y=x, states=tuple(new_states), n_iters=n_iters)
+        hist_out = tuple(t for t in new_histories if t is not None) if self.taps is not None else None
+        return LoopResult(y=x, states=tuple(new_states), n_iters=n_iters, histories=hist_out)
