@@ -216,6 +216,51 @@ def time_key_filter(torch, reps: int = 50) -> tuple[float, float]:
     return out[0], out[1]
 
 
+def time_attention_backward(torch, reps: int = 20) -> float:
+    """Milliseconds per backward of window attention at B4 T4096 H8 D64 w512 bf16 (the dq and the
+    dk/dv kernels, from a forward's o and log-sum-exp), 20 launches in one HIP graph."""
+    from vesper.kernels import _lib
+
+    dev = torch.device("cuda:0")
+    aq, ak, av = attn_inputs(torch, dev, b=ATTN_B, seed=5)
+    b, n, h, dk = aq.shape
+    o = torch.empty_like(aq)
+    lse = torch.empty(b, h, n, device=dev)
+    up = torch.randn(aq.shape, generator=torch.Generator().manual_seed(6)).to(dev, torch.bfloat16)
+    dq, dkk, dv = torch.empty_like(aq), torch.empty_like(ak), torch.empty_like(av)
+    ws = torch.empty(b * h * n, device=dev)
+    scale = 1.0 / math.sqrt(dk)
+    _lib.call("vsp_window_attn_lse_bf16", _lib.ptr(aq), _lib.ptr(ak), _lib.ptr(av), _lib.ptr(o), _lib.ptr(lse), None,
+              b, n, 0, h, h, dk, WINDOW, scale, _lib.stream_of(dev))
+
+    def run():
+        _lib.call("vsp_window_attn_backward_bf16", _lib.ptr(aq), _lib.ptr(ak), _lib.ptr(av), _lib.ptr(o), _lib.ptr(up),
+                  _lib.ptr(lse), _lib.ptr(ws), _lib.ptr(dq), _lib.ptr(dkk), _lib.ptr(dv), b, n, 0, h, h, dk, WINDOW,
+                  scale, _lib.stream_of(dev))
+
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for _ in range(2):
+            run()
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for _ in range(reps):
+            run()
+    graph.replay()
+    times = []
+    for _ in range(3):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        e0.record()
+        graph.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        times.append(e0.elapsed_time(e1) / reps)
+    return statistics.median(times)
+
+
 def time_decode(torch, reps: int = 5) -> dict:
     from vesper.kernels.delta_scan import delta_scan_step_fused
     from vesper.kernels.ring_attn import RingKVCache, ring_attention
@@ -450,6 +495,7 @@ def main() -> int:
     s_bytes, s_flops = scan_bytes(B, T, H, D), scan_flops(B, T, H, D)
     a_bytes, a_flops = attn_bytes(B, T, H, H, D), attn_flops(B, T, H, D, WINDOW)
     attn4_ms = time_attention_config(torch)
+    attn4_bwd_ms = time_attention_backward(torch)
     keys_ms, keys_bwd_ms = time_key_filter(torch)
     dec = None if args.no_decode else time_decode(torch)
     looped = None if args.no_loop else time_looped(torch)
@@ -497,6 +543,9 @@ def main() -> int:
             "window_attn_b4_tok_s": round(ATTN_B * T / (attn4_ms / 1e3), 1),
             "window_attn_b4_hbm_frac": round(attn_bytes(ATTN_B, T, H, H, D) / (attn4_ms / 1e3) / 1e9 / HBM_PEAK_GBS, 4),
             "window_attn_b4_mfma_frac_bf16": round(attn_flops(ATTN_B, T, H, D, WINDOW) / (attn4_ms / 1e3) / 1e12 / BF16_PEAK_TFLOPS, 4),
+            "window_attn_b4_backward_ms": round(attn4_bwd_ms, 4),
+            # algorithmic backward work: 2.5x the forward's (QK^T again, dP, dQ, dK, dV)
+            "window_attn_b4_backward_mfma_frac_bf16": round(2.5 * attn_flops(ATTN_B, T, H, D, WINDOW) / (attn4_bwd_ms / 1e3) / 1e12 / BF16_PEAK_TFLOPS, 4),
         },
         "roofline": roofline,
     }

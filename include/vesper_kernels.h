@@ -22,7 +22,7 @@
 extern "C" {
 #endif
 
-#define VSP_ABI_VERSION 4
+#define VSP_ABI_VERSION 5
 
 /* Status codes. */
 #define VSP_OK 0
@@ -79,6 +79,27 @@ int vsp_window_attn_bf16(const void* q, const void* keys, const void* values, vo
                          int B, int N, int M, int H, int HKV, int D, int window, float scale, void* stream);
 int vsp_window_attn_f16(const void* q, const void* keys, const void* values, void* o, const uint8_t* active,
                         int B, int N, int M, int H, int HKV, int D, int window, float scale, void* stream);
+/* The same forward, also writing lse [B, H, N] fp32: per query the log-sum-exp of its scaled scores
+ * in log2 units (P = exp2(score * scale * log2(e) - lse)), +inf for an inactive query. */
+int vsp_window_attn_lse_bf16(const void* q, const void* keys, const void* values, void* o, float* lse,
+                             const uint8_t* active, int B, int N, int M, int H, int HKV, int D, int window,
+                             float scale, void* stream);
+int vsp_window_attn_lse_f16(const void* q, const void* keys, const void* values, void* o, float* lse,
+                            const uint8_t* active, int B, int N, int M, int H, int HKV, int D, int window,
+                            float scale, void* stream);
+/* The gradients (the backward of fla-core's `parallel_attn`, which autograd runs for
+ * vesper/kernels/window_attn.py:27-39 under WindowedAttention.attend, vesper/attention.py:373-383):
+ * from dO [B, N, H, D] and the forward's o and lse, dq [B, N, H, D], dk and dv [B, M + N, HKV, D]
+ * (summed over the query heads of each KV head); workspace: B * H * N floats. Deterministic (no
+ * atomics); an inactive query (lse +inf) contributes nothing and gets a zero dq. */
+int vsp_window_attn_backward_bf16(const void* q, const void* keys, const void* values, const void* o,
+                                  const void* dout, const float* lse, float* workspace, void* dq, void* dk,
+                                  void* dv, int B, int N, int M, int H, int HKV, int D, int window, float scale,
+                                  void* stream);
+int vsp_window_attn_backward_f16(const void* q, const void* keys, const void* values, const void* o,
+                                 const void* dout, const float* lse, float* workspace, void* dq, void* dk,
+                                 void* dv, int B, int N, int M, int H, int HKV, int D, int window, float scale,
+                                 void* stream);
 
 /* ---- decode: one new token per row over a KV ring ------------------------------------------
  * q: [B, H, D]; k, v: [B, HKV, D] (the new token); pos: [B] int64, nonnegative;

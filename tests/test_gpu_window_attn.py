@@ -2,7 +2,9 @@
 
 The oracle runs in float64 (float32 at the full headline size) on the same bf16/fp16-valued inputs.
 Bound: relative Frobenius error below 1e-2, and elementwise within the reference's
-``rtol = atol = 3e-2`` (``tests/test_window_attn.py:78``).
+``rtol = atol = 3e-2`` (``tests/test_window_attn.py:78``), for the outputs and for the gradients of
+q, keys and values (the oracle's by autograd, pinned by finite differences in
+``tests/test_oracle_attention.py``).
 """
 
 from __future__ import annotations
@@ -122,8 +124,6 @@ def test_refusals():
         window_attention(dq[:, :, :3], dk_, dv, 4)
     with pytest.raises(ContractError, match="fewer"):
         window_attention(dq, dk_[:, :4], dv[:, :4], 4)
-    with pytest.raises(ContractError, match="forward only"):
-        window_attention(dq.clone().requires_grad_(), dk_, dv, 4)
     with pytest.raises(ValueError, match="window"):
         window_attention(dq, dk_, dv, 0)
 
@@ -148,3 +148,97 @@ def test_repeatable_and_captured_replays_equal_eager():
         assert torch.equal(out, eager), i
         window_attention(q, keys, values, 64)
         torch.cuda.synchronize()
+
+
+def _grads(q, keys, values, w, up, active=None):
+    from vesper.kernels.window_attn import window_attention
+
+    qs, ks, vs = (t.to(GPU).requires_grad_() for t in (q, keys, values))
+    out = window_attention(qs, ks, vs, w, active=None if active is None else active.to(GPU))
+    out.backward(up.to(GPU))
+    return out.detach(), qs.grad, ks.grad, vs.grad
+
+
+def _oracle_grads(q, keys, values, w, up, active=None, dtype=torch.float64):
+    qs, ks, vs = (t.to(dtype).requires_grad_() for t in (q, keys, values))
+    out = oracle_window(qs, ks, vs, w, active=active)
+    out.backward(up.to(dtype))
+    return out.detach(), qs.grad, ks.grad, vs.grad
+
+
+# the reference's gradient cases (tests/test_window_attn.py:67-78): h 4, 2 KV heads, dk 64, window
+# 16, chunks shorter and longer than the window, with no cache, a short one and a full one
+@pytest.mark.parametrize(("n", "m"), [(8, 0), (40, 0), (8, 5), (40, 5), (8, 16), (40, 16)])
+def test_the_gradients_match_the_oracle(n, m):
+    q, keys, values = _inputs(3, n, m, 4, 2, 64, seed=40 + n + m)
+    up = torch.randn(3, n, 4, 64, generator=torch.Generator().manual_seed(n * m + 1)).to(BF16)
+    got = _grads(q, keys, values, 16, up)
+    want = _oracle_grads(q, keys, values, 16, up)
+    for a, b, name in zip(got, want, ("o", "dq", "dk", "dv")):
+        assert relative_error(a, b) < 1e-2, name
+        torch.testing.assert_close(a.float().cpu(), b.float(), rtol=3e-2, atol=3e-2, msg=name)
+
+
+@pytest.mark.parametrize("dk", [16, 32, 64, 128])
+@pytest.mark.parametrize(("h", "hkv"), [(2, 2), (8, 1), (8, 4)])
+@pytest.mark.parametrize("dtype", [BF16, torch.float16])
+def test_the_gradients_for_every_width_and_group(dk, h, hkv, dtype):
+    n, m, w = 150, 30, 48
+    q, keys, values = _inputs(2, n, m, h, hkv, dk, seed=dk + h, dtype=dtype)
+    up = torch.randn(2, n, h, dk, generator=torch.Generator().manual_seed(dk)).to(dtype)
+    got = _grads(q, keys, values, w, up)
+    want = _oracle_grads(q, keys, values, w, up)
+    for a, b, name in zip(got[1:], want[1:], ("dq", "dk", "dv")):
+        assert relative_error(a, b) < 1e-2, name
+
+
+def test_inactive_queries_pass_no_gradient():
+    n = 100
+    q, keys, values = _inputs(2, n, 10, 4, 2, 64, seed=50)
+    active = torch.rand(2, n, generator=torch.Generator().manual_seed(51)) < 0.6
+    up = torch.randn(2, n, 4, 64, generator=torch.Generator().manual_seed(52)).to(BF16)
+    got = _grads(q, keys, values, 32, up, active)
+    want = _oracle_grads(q, keys, values, 32, up, active)
+    assert torch.equal(got[1][~active.to(GPU)], torch.zeros_like(got[1][~active.to(GPU)]))
+    for a, b, name in zip(got[1:], want[1:], ("dq", "dk", "dv")):
+        assert relative_error(a, b) < 1e-2, name
+
+
+def test_the_gradients_at_t4096_w512_against_the_fp32_oracle_and_they_repeat():
+    q, keys, values = _inputs(1, 4096, 0, 8, 8, 64, seed=53)
+    up = torch.randn(1, 4096, 8, 64, generator=torch.Generator().manual_seed(54)).to(BF16)
+    got = _grads(q, keys, values, 512, up)
+    again = _grads(q, keys, values, 512, up)
+    for a, b in zip(got, again):
+        assert torch.equal(a, b)  # deterministic: no atomics
+    want = _oracle_grads(q, keys, values, 512, up, dtype=torch.float32)
+    for a, b, name in zip(got[1:], want[1:], ("dq", "dk", "dv")):
+        assert relative_error(a, b) < 1e-2, name
+
+
+def test_captured_forward_and_backward_equal_eager():
+    from vesper.kernels.window_attn import window_attention
+
+    q, keys, values = (t.to(GPU).requires_grad_() for t in _inputs(2, 300, 16, 8, 2, 64, seed=55))
+    up = torch.randn(2, 300, 8, 64, generator=torch.Generator().manual_seed(56)).to(GPU, BF16)
+
+    def step():
+        out = window_attention(q, keys, values, 64)
+        return (out.detach(), *torch.autograd.grad(out, (q, keys, values), up))
+
+    eager = [t.clone() for t in step()]
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        step()
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        static = step()
+    for _ in range(3):
+        for t in static:
+            t.zero_()
+        graph.replay()
+        torch.cuda.synchronize()
+        for a, b in zip(static, eager):
+            assert torch.equal(a, b)

@@ -186,3 +186,29 @@ def test_planted_mistakes_are_caught(kind: str, monkeypatch: pytest.MonkeyPatch)
     except AssertionError:
         caught.append(True)
     assert caught == [True]
+
+
+def test_the_window_attention_gradients_match_finite_differences() -> None:
+    # the oracle of the backward is autograd through the forward above; finite differences pin it
+    # (grouped heads, a cache in front of the chunk, a window shorter than the keys, an inactive query)
+    g = torch.Generator().manual_seed(31)
+    b, n, m, h, hkv, dk, w = 1, 5, 2, 2, 1, 3, 3
+    q = torch.randn(b, n, h, dk, generator=g, dtype=torch.float64, requires_grad=True)
+    k = torch.randn(b, m + n, hkv, dk, generator=g, dtype=torch.float64, requires_grad=True)
+    v = torch.randn(b, m + n, hkv, dk, generator=g, dtype=torch.float64, requires_grad=True)
+    active = torch.tensor([[True, True, False, True, True]])
+    assert torch.autograd.gradcheck(lambda a, c, e: oa.window_attention(a, c, e, w, active=active), (q, k, v))
+    # an inactive query passes no gradient
+    out = oa.window_attention(q, k, v, w, active=active)
+    gq, _, _ = torch.autograd.grad(out.sum(), (q, k, v))
+    assert torch.equal(gq[:, 2], torch.zeros_like(gq[:, 2]))
+
+
+def test_a_planted_scale_mistake_changes_the_gradients() -> None:
+    g = torch.Generator().manual_seed(32)
+    q = torch.randn(1, 4, 1, 4, generator=g, dtype=torch.float64, requires_grad=True)
+    k = torch.randn(1, 4, 1, 4, generator=g, dtype=torch.float64, requires_grad=True)
+    v = torch.randn(1, 4, 1, 4, generator=g, dtype=torch.float64)
+    (gq,) = torch.autograd.grad(oa.window_attention(q, k, v, 4).sum(), (q,))
+    (wrong,) = torch.autograd.grad(oa.window_attention(2 * q, k, v, 4).sum(), (q,))  # a doubled score scale
+    assert not torch.allclose(gq, wrong, rtol=1e-3)

@@ -20,6 +20,7 @@
 // once per query instead of once per tile (probabilities then reach at most 2^kLazy, which bf16
 // P and the fp32 sums hold exactly as well). Only tiles that cross the causal diagonal, the
 // window's lower edge or the end of the keys are masked.
+#include "attn_mma.h"
 #include "common.h"
 #include "vesper_kernels.h"
 
@@ -28,42 +29,10 @@ namespace {
 
 constexpr float kLazy = 8.f;
 
-template <typename T> struct Mma;
-template <> struct Mma<__bf16> {
-  using V8 = bf16x8;
-  using V4 = bf16x4;
-  __device__ __forceinline__ static f32x4 run(V8 a, V8 b, f32x4 c) {
-    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
-  }
-};
-template <> struct Mma<_Float16> {
-  using V8 = f16x8;
-  using V4 = f16x4;
-  __device__ __forceinline__ static f32x4 run(V8 a, V8 b, f32x4 c) {
-    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
-  }
-};
-
-template <typename T>
-__device__ __forceinline__ typename Mma<T>::V4 read_tr(const T* p) {
-  return read_tr16<typename Mma<T>::V4>(p);
-}
-
-// IEEE maximum (NaN-propagating): v_maximum3_f32 / v_maximum_f32, which need no operand
-// canonicalisation, unlike fmaxf's v_max_f32
-__device__ __forceinline__ float fmax_ieee(float a, float b) { return __builtin_elementwise_maximum(a, b); }
-
-// max over the four lanes l, l ^ 16, l ^ 32, l ^ 48 (the four lane groups of one query)
-__device__ __forceinline__ float max_over_groups(float x) {
-  const auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  x = fmax_ieee(__uint_as_float(a[0]), __uint_as_float(a[1]));
-  const auto c = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  return fmax_ieee(__uint_as_float(c[0]), __uint_as_float(c[1]));
-}
-
 template <typename T, int D>
 __global__ __launch_bounds__(256, D >= 128 ? 2 : 4) void window_attn_kernel(const T* __restrict__ q, const T* __restrict__ keys,
                                                              const T* __restrict__ values, T* __restrict__ o,
+                                                             float* __restrict__ lse,
                                                              const uint8_t* __restrict__ active, int N, int M, int H,
                                                              int HKV, int W, float scale_log2, int nqt) {
   using V8 = typename Mma<T>::V8;
@@ -115,6 +84,7 @@ __global__ __launch_bounds__(256, D >= 128 ? 2 : 4) void window_attn_kernel(cons
       if (qok[qb] && g == 0) {
         T* dst = o + (((size_t)b * N + myq) * H + h) * D;
         for (int d = 0; d < D; ++d) dst[d] = from_f32<T>(0.f);
+        if (lse != nullptr) lse[((size_t)b * H + h) * N + myq] = INFINITY;
       }
     }
     return;
@@ -328,6 +298,10 @@ __global__ __launch_bounds__(256, D >= 128 ? 2 : 4) void window_attn_kernel(cons
     float lt = l_run[qb] + __shfl_xor(l_run[qb], 16);
     lt += __shfl_xor(lt, 32);
     const float inv = (act[qb] && lt > 0.f) ? 1.f / lt : 0.f;
+    // the log-sum-exp in log2 units of the scaled scores, for the backward: P = exp2(s sl2 - lse);
+    // +inf for an inactive query, whose probabilities (and gradients) are then exactly zero
+    if (lse != nullptr && qok[qb] && g == 0)
+      lse[((size_t)b * H + h) * N + wq0 + 16 * qb + lq] = inv > 0.f ? m_used[qb] + log2f(lt) : INFINITY;
     if (qok[qb]) {
       T* dst = o + (((size_t)b * N + wq0 + 16 * qb + lq) * H + h) * D;
 #pragma unroll
@@ -347,8 +321,8 @@ __global__ __launch_bounds__(256, D >= 128 ? 2 : 4) void window_attn_kernel(cons
 bool attn_width(int D) { return D == 16 || D == 32 || D == 64 || D == 128; }
 
 template <typename T>
-int window_attn(const T* q, const T* keys, const T* values, T* o, const uint8_t* active, int B, int N, int M, int H,
-                int HKV, int D, int W, float scale, void* stream_ptr, const char* who) {
+int window_attn(const T* q, const T* keys, const T* values, T* o, float* lse, const uint8_t* active, int B, int N, int M,
+                int H, int HKV, int D, int W, float scale, void* stream_ptr, const char* who) {
   if (B < 0 || N < 0 || M < 0 || H < 1 || HKV < 1) return fail(ERR_ARG, "%s: bad sizes B=%d N=%d M=%d H=%d HKV=%d", who, B, N, M, H, HKV);
   if (H % HKV != 0) return fail(ERR_ARG, "%s: %d query heads are not a multiple of %d KV heads", who, H, HKV);
   if (W < 1) return fail(ERR_ARG, "%s: window must be at least 1, got %d", who, W);
@@ -359,6 +333,7 @@ int window_attn(const T* q, const T* keys, const T* values, T* o, const uint8_t*
   if ((reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(keys) | reinterpret_cast<uintptr_t>(values) |
        reinterpret_cast<uintptr_t>(o)) & 15)
     return fail(ERR_ARG, "%s: q, keys, values and o must be 16-byte aligned", who);
+  if (reinterpret_cast<uintptr_t>(lse) & 3) return fail(ERR_ARG, "%s: lse must be 4-byte aligned", who);
   // one batch row's keys (all KV heads) are addressed with 32-bit byte offsets
   if ((size_t)(M + N) * HKV * D * sizeof(T) >= ((size_t)1 << 32))
     return fail(ERR_UNSUPPORTED, "%s: %d keys x %d KV heads x %d features exceed 4 GiB per batch row", who, M + N, HKV, D);
@@ -367,10 +342,10 @@ int window_attn(const T* q, const T* keys, const T* values, T* o, const uint8_t*
   dim3 grid((unsigned)((size_t)nqt * H * B));
   hipStream_t stream = reinterpret_cast<hipStream_t>(stream_ptr);
   switch (D) {
-    case 16: hipLaunchKernelGGL((window_attn_kernel<T, 16>), grid, dim3(256), 0, stream, q, keys, values, o, active, N, M, H, HKV, W, scale_log2, nqt); break;
-    case 32: hipLaunchKernelGGL((window_attn_kernel<T, 32>), grid, dim3(256), 0, stream, q, keys, values, o, active, N, M, H, HKV, W, scale_log2, nqt); break;
-    case 64: hipLaunchKernelGGL((window_attn_kernel<T, 64>), grid, dim3(256), 0, stream, q, keys, values, o, active, N, M, H, HKV, W, scale_log2, nqt); break;
-    default: hipLaunchKernelGGL((window_attn_kernel<T, 128>), grid, dim3(256), 0, stream, q, keys, values, o, active, N, M, H, HKV, W, scale_log2, nqt); break;
+    case 16: hipLaunchKernelGGL((window_attn_kernel<T, 16>), grid, dim3(256), 0, stream, q, keys, values, o, lse, active, N, M, H, HKV, W, scale_log2, nqt); break;
+    case 32: hipLaunchKernelGGL((window_attn_kernel<T, 32>), grid, dim3(256), 0, stream, q, keys, values, o, lse, active, N, M, H, HKV, W, scale_log2, nqt); break;
+    case 64: hipLaunchKernelGGL((window_attn_kernel<T, 64>), grid, dim3(256), 0, stream, q, keys, values, o, lse, active, N, M, H, HKV, W, scale_log2, nqt); break;
+    default: hipLaunchKernelGGL((window_attn_kernel<T, 128>), grid, dim3(256), 0, stream, q, keys, values, o, lse, active, N, M, H, HKV, W, scale_log2, nqt); break;
   }
   return check_launch(who);
 }
@@ -381,13 +356,29 @@ int window_attn(const T* q, const T* keys, const T* values, T* o, const uint8_t*
 extern "C" int vsp_window_attn_bf16(const void* q, const void* keys, const void* values, void* o, const uint8_t* active,
                                     int B, int N, int M, int H, int HKV, int D, int window, float scale, void* stream) {
   return vsp::window_attn<__bf16>(static_cast<const __bf16*>(q), static_cast<const __bf16*>(keys),
-                                  static_cast<const __bf16*>(values), static_cast<__bf16*>(o), active, B, N, M, H, HKV,
-                                  D, window, scale, stream, "vsp_window_attn_bf16");
+                                  static_cast<const __bf16*>(values), static_cast<__bf16*>(o), nullptr, active, B, N, M,
+                                  H, HKV, D, window, scale, stream, "vsp_window_attn_bf16");
+}
+
+extern "C" int vsp_window_attn_lse_bf16(const void* q, const void* keys, const void* values, void* o, float* lse,
+                                        const uint8_t* active, int B, int N, int M, int H, int HKV, int D, int window,
+                                        float scale, void* stream) {
+  return vsp::window_attn<__bf16>(static_cast<const __bf16*>(q), static_cast<const __bf16*>(keys),
+                                  static_cast<const __bf16*>(values), static_cast<__bf16*>(o), lse, active, B, N, M, H,
+                                  HKV, D, window, scale, stream, "vsp_window_attn_lse_bf16");
 }
 
 extern "C" int vsp_window_attn_f16(const void* q, const void* keys, const void* values, void* o, const uint8_t* active,
                                    int B, int N, int M, int H, int HKV, int D, int window, float scale, void* stream) {
   return vsp::window_attn<_Float16>(static_cast<const _Float16*>(q), static_cast<const _Float16*>(keys),
-                                    static_cast<const _Float16*>(values), static_cast<_Float16*>(o), active, B, N, M,
-                                    H, HKV, D, window, scale, stream, "vsp_window_attn_f16");
+                                    static_cast<const _Float16*>(values), static_cast<_Float16*>(o), nullptr, active, B,
+                                    N, M, H, HKV, D, window, scale, stream, "vsp_window_attn_f16");
+}
+
+extern "C" int vsp_window_attn_lse_f16(const void* q, const void* keys, const void* values, void* o, float* lse,
+                                       const uint8_t* active, int B, int N, int M, int H, int HKV, int D, int window,
+                                       float scale, void* stream) {
+  return vsp::window_attn<_Float16>(static_cast<const _Float16*>(q), static_cast<const _Float16*>(keys),
+                                    static_cast<const _Float16*>(values), static_cast<_Float16*>(o), lse, active, B, N,
+                                    M, H, HKV, D, window, scale, stream, "vsp_window_attn_lse_f16");
 }

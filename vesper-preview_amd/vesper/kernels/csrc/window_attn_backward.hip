@@ -1,0 +1,358 @@
+// Sliding-window causal attention on CDNA4 (gfx950): the gradients.
+//
+// The backward of the prefill kernel (window_attn.hip; reference vesper/kernels/window_attn.py:27-39,
+// run by autograd through WindowedAttention.attend, vesper/attention.py:373-383). With the
+// forward's log-sum-exp `lse` (log2 units of the scaled scores), P = exp2(s * scale_log2 - lse),
+// and per query Dsum = sum_d dO O:
+//   dP = dO V^T,  dS = P (dP - Dsum) scale,  dQ = dS K,  dK = dS^T Q,  dV = P^T dO,
+// dK and dV summed over the query heads that share the KV head. An inactive query's lse is +inf
+// (the forward writes it so): its P, and every gradient through it, is exactly zero.
+//
+// Two kernels and no atomics, so the gradients repeat bitwise:
+// - attn_dq_kernel, one workgroup per (b, h, 64 queries), a wave per 16 queries in registers,
+//   walks the window's 64-key tiles through LDS: S^T = K Q^T and dP^T = V dO^T (16x16x32 MFMA, a
+//   lane holding 16 keys of one query, as the forward), dS^T elementwise, dQ^T += K^T dS^T with
+//   K^T fragments from transposed LDS reads; it also writes Dsum for the second kernel.
+// - attn_dkv_kernel, one workgroup per (b, KV head, 64 keys), a wave per 16 keys in registers,
+//   walks the query heads of the group and the 64-query tiles that see its keys: S = Q K^T and
+//   dP = dO V^T (a lane holding 16 queries of one key), dV^T += dO^T P and dK^T += Q^T dS with dO^T
+//   and Q^T fragments from transposed LDS reads.
+#include "attn_mma.h"
+#include "common.h"
+#include "vesper_kernels.h"
+
+namespace vsp {
+namespace {
+
+template <int D> struct BwdShape {
+  static constexpr int DP = D < 32 ? 32 : D;  // feature extent padded to the MFMA k step
+  static constexpr int KSQ = DP / 32;         // MFMA k steps over the features
+  static constexpr int DT = DP / 16;          // 16-row tiles of a transposed [features x 16] result
+  static constexpr int SEG = DP / 8;          // 16-byte segments per row
+  static constexpr int P = DP + 16;           // LDS pitch (elements) for row and transposed reads
+};
+
+// Rows r0 .. r0 + 63 of a [rows, ld]-strided tensor (features 0 .. D - 1) into LDS [64][P], zero
+// past D and past row `rows`.
+template <typename T, int D>
+__device__ __forceinline__ void stage64(T* dst, const T* src, size_t ld, int r0, int rows) {
+  using Sh = BwdShape<D>;
+  using V8 = typename Mma<T>::V8;
+  for (int sg = threadIdx.x; sg < 64 * Sh::SEG; sg += 256) {
+    const int row = sg / Sh::SEG, part = sg - row * Sh::SEG;
+    V8 v;
+    if (r0 + row < rows && 8 * part < D) {
+      v = *reinterpret_cast<const V8*>(src + (size_t)(r0 + row) * ld + 8 * part);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) v[e] = from_f32<T>(0.f);
+    }
+    *reinterpret_cast<typename Mma<T>::V8*>(dst + row * Sh::P + 8 * part) = v;
+  }
+}
+
+// A fragment of rows rbase + lq, features 32 s + 8 g .. + 7 (row-major LDS tile).
+template <typename T, int D>
+__device__ __forceinline__ typename Mma<T>::V8 row_frag(const T* tile, int rbase, int s) {
+  const int l = threadIdx.x & 63, lq = l & 15, g = l >> 4;
+  return *reinterpret_cast<const typename Mma<T>::V8*>(tile + (rbase + lq) * BwdShape<D>::P + 32 * s + 8 * g);
+}
+
+// The transposed A fragment: lane (lq, g) gets column 16 t + lq of rows r0 + 4 g .. + 3 and
+// r0 + 16 + 4 g .. + 3 (the k order the accumulator-built B fragments use).
+template <typename T, int D>
+__device__ __forceinline__ typename Mma<T>::V8 tr_frag(const T* tile, int r0, int t) {
+  constexpr int P = BwdShape<D>::P;
+  const int l = threadIdx.x & 63, lq = l & 15, g = l >> 4;
+  const T* base = tile + (r0 + 4 * g + (lq >> 2)) * P + 16 * t + 4 * (lq & 3);
+  const auto lo = read_tr<T>(base);
+  const auto hi = read_tr<T>(base + 16 * P);
+  return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+}
+
+template <typename T, int D>
+__global__ __launch_bounds__(256) void attn_dq_kernel(const T* __restrict__ q, const T* __restrict__ keys,
+                                                      const T* __restrict__ values, const T* __restrict__ o,
+                                                      const T* __restrict__ dout, const float* __restrict__ lse,
+                                                      float* __restrict__ dsum, T* __restrict__ dq, int N, int M,
+                                                      int H, int HKV, int W, float scale, float scale_log2, int nqt) {
+  using Sh = BwdShape<D>;
+  using V8 = typename Mma<T>::V8;
+  using V4 = typename Mma<T>::V4;
+  constexpr int KT = 64;
+  __shared__ __align__(16) T sK[KT * Sh::P];
+  __shared__ __align__(16) T sV[KT * Sh::P];
+  const int qt = blockIdx.x % nqt, bh = blockIdx.x / nqt;
+  const int b = bh / H, h = bh - b * H;
+  const int kvh = h / (H / HKV);
+  const int w = threadIdx.x >> 6, l = threadIdx.x & 63;
+  const int lq = l & 15, g = l >> 4;
+  const int S = M + N;
+  const int i = 64 * qt + 16 * w + lq;  // this lane's query
+  const bool qok = i < N;
+  const size_t qrow = (((size_t)b * N + (qok ? i : 0)) * H + h) * D;
+
+  // the query's Q and dO as B fragments (lane (lq, g): features 32 s + 8 g .. + 7), and Dsum
+  V8 qf[Sh::KSQ], df[Sh::KSQ];
+  float part = 0.f;
+#pragma unroll
+  for (int s = 0; s < Sh::KSQ; ++s) {
+    const int f = 32 * s + 8 * g;
+    if (qok && f < D) {
+      qf[s] = *reinterpret_cast<const V8*>(q + qrow + f);
+      df[s] = *reinterpret_cast<const V8*>(dout + qrow + f);
+      const V8 of = *reinterpret_cast<const V8*>(o + qrow + f);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) part += to_f32(df[s][e]) * to_f32(of[e]);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        qf[s][e] = from_f32<T>(0.f);
+        df[s][e] = from_f32<T>(0.f);
+      }
+    }
+  }
+  float dsm = part + __shfl_xor(part, 16);
+  dsm += __shfl_xor(dsm, 32);
+  const float lq_lse = qok ? lse[((size_t)b * H + h) * N + i] : INFINITY;
+  if (qok && g == 0) dsum[((size_t)b * H + h) * N + i] = dsm;
+
+  const int qlo = 64 * qt;
+  const int kfirst = max(0, M + qlo - W + 1), klast = min(S, M + qlo + 64);
+  const int ntiles = (klast - kfirst + KT - 1) / KT;
+  const size_t kv_ld = (size_t)HKV * D;
+  const T* kbase = keys + ((size_t)b * S * HKV + kvh) * D;
+  const T* vbase = values + ((size_t)b * S * HKV + kvh) * D;
+  const int qk = M + i;  // the query's index among the keys
+  const int wlo = M + qlo + 16 * w, whi = wlo + 15;
+
+  f32x4 acc[Sh::DT];
+#pragma unroll
+  for (int t = 0; t < Sh::DT; ++t) acc[t] = zero4();
+  for (int it = 0; it < ntiles; ++it) {
+    const int k0 = kfirst + it * KT;
+    __syncthreads();  // the previous tile's reads are done
+    stage64<T, D>(sK, kbase, kv_ld, k0, S);
+    stage64<T, D>(sV, vbase, kv_ld, k0, S);
+    __syncthreads();
+    if (!(k0 <= whi && k0 + KT - 1 > wlo - W)) continue;  // no query of the wave sees this tile
+    f32x4 sacc[4], pacc[4];
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb) {
+      sacc[kb] = zero4();
+      pacc[kb] = zero4();
+#pragma unroll
+      for (int st = 0; st < Sh::KSQ; ++st) {
+        sacc[kb] = Mma<T>::run(row_frag<T, D>(sK, 16 * kb, st), qf[st], sacc[kb]);
+        pacc[kb] = Mma<T>::run(row_frag<T, D>(sV, 16 * kb, st), df[st], pacc[kb]);
+      }
+    }
+    // lane (lq, g) holds keys k0 + 16 kb + 4 g + r of its query
+    V8 dsb[2];
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int key = k0 + 16 * kb + 4 * g + r;
+        const bool vis = (unsigned)(qk - key) < (unsigned)W;
+        const float p = vis ? __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[kb][r], scale_log2, -lq_lse)) : 0.f;
+        dsb[kb >> 1][4 * (kb & 1) + r] = from_f32<T>(p * (pacc[kb][r] - dsm) * scale);
+      }
+#pragma unroll
+    for (int t = 0; t < Sh::DT; ++t)
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) acc[t] = Mma<T>::run(tr_frag<T, D>(sK, 32 * ks, t), dsb[ks], acc[t]);
+  }
+  if (qok) {
+#pragma unroll
+    for (int t = 0; t < Sh::DT; ++t) {
+      const int d = 16 * t + 4 * g;
+      if (d < D) {
+        V4 v;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) v[r] = from_f32<T>(acc[t][r]);
+        *reinterpret_cast<V4*>(dq + qrow + d) = v;
+      }
+    }
+  }
+}
+
+template <typename T, int D>
+__global__ __launch_bounds__(256) void attn_dkv_kernel(const T* __restrict__ q, const T* __restrict__ keys,
+                                                       const T* __restrict__ values, const T* __restrict__ dout,
+                                                       const float* __restrict__ lse, const float* __restrict__ dsum,
+                                                       T* __restrict__ dk, T* __restrict__ dv, int N, int M, int H,
+                                                       int HKV, int W, float scale, float scale_log2, int nkt) {
+  using Sh = BwdShape<D>;
+  using V8 = typename Mma<T>::V8;
+  using V4 = typename Mma<T>::V4;
+  __shared__ __align__(16) T sQ[64 * Sh::P];
+  __shared__ __align__(16) T sD[64 * Sh::P];
+  __shared__ float sL[64], sS[64];
+  const int kt = blockIdx.x % nkt, bkv = blockIdx.x / nkt;
+  const int b = bkv / HKV, kvh = bkv - b * HKV;
+  const int G = H / HKV;
+  const int w = threadIdx.x >> 6, l = threadIdx.x & 63;
+  const int lq = l & 15, g = l >> 4;
+  const int S = M + N;
+  const int k0 = 64 * kt;
+  const int key = k0 + 16 * w + lq;  // this lane's key
+  const bool kok = key < S;
+  const size_t krow = (((size_t)b * S + (kok ? key : 0)) * HKV + kvh) * D;
+
+  V8 kf[Sh::KSQ], vf[Sh::KSQ];
+#pragma unroll
+  for (int s = 0; s < Sh::KSQ; ++s) {
+    const int f = 32 * s + 8 * g;
+    if (kok && f < D) {
+      kf[s] = *reinterpret_cast<const V8*>(keys + krow + f);
+      vf[s] = *reinterpret_cast<const V8*>(values + krow + f);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        kf[s][e] = from_f32<T>(0.f);
+        vf[s][e] = from_f32<T>(0.f);
+      }
+    }
+  }
+  f32x4 dka[Sh::DT], dva[Sh::DT];
+#pragma unroll
+  for (int t = 0; t < Sh::DT; ++t) {
+    dka[t] = zero4();
+    dva[t] = zero4();
+  }
+  // the queries that see the tile's keys: M + i in [k0, k0 + 63 + W - 1]
+  const int ilo = max(0, k0 - M), ihi = min(N - 1, k0 + 63 + W - 1 - M);
+  const int wk0 = k0 + 16 * w, wk1 = wk0 + 15;
+  const size_t q_ld = (size_t)H * D;
+  for (int j = 0; j < G; ++j) {
+    const int h = kvh * G + j;
+    const T* qbase = q + ((size_t)b * N * H + h) * D;
+    const T* dbase = dout + ((size_t)b * N * H + h) * D;
+    const float* lse_h = lse + ((size_t)b * H + h) * N;
+    const float* dsum_h = dsum + ((size_t)b * H + h) * N;
+    for (int i0 = ilo; i0 <= ihi; i0 += 64) {
+      __syncthreads();  // the previous tile's reads are done
+      stage64<T, D>(sQ, qbase, q_ld, i0, N);
+      stage64<T, D>(sD, dbase, q_ld, i0, N);
+      if (threadIdx.x < 64) {
+        const int ii = i0 + (int)threadIdx.x;
+        sL[threadIdx.x] = ii < N ? lse_h[ii] : INFINITY;
+        sS[threadIdx.x] = ii < N ? dsum_h[ii] : 0.f;
+      }
+      __syncthreads();
+      if (!(M + i0 + 63 >= wk0 && M + i0 <= wk1 + W - 1)) continue;  // no key of the wave is seen
+#pragma unroll
+      for (int qp = 0; qp < 2; ++qp) {
+        V8 pb, dsb;
+#pragma unroll
+        for (int qb = 0; qb < 2; ++qb) {
+          const int r0 = 32 * qp + 16 * qb;
+          f32x4 st = zero4(), dp = zero4();
+#pragma unroll
+          for (int s = 0; s < Sh::KSQ; ++s) {
+            st = Mma<T>::run(row_frag<T, D>(sQ, r0, s), kf[s], st);
+            dp = Mma<T>::run(row_frag<T, D>(sD, r0, s), vf[s], dp);
+          }
+          // lane (lq, g) holds queries r0 + 4 g + r of its key
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int qi = r0 + 4 * g + r;
+            const bool vis = kok && (unsigned)(M + i0 + qi - key) < (unsigned)W;
+            const float p = vis ? __builtin_amdgcn_exp2f(__builtin_fmaf(st[r], scale_log2, -sL[qi])) : 0.f;
+            pb[4 * qb + r] = from_f32<T>(p);
+            dsb[4 * qb + r] = from_f32<T>(p * (dp[r] - sS[qi]) * scale);
+          }
+        }
+#pragma unroll
+        for (int t = 0; t < Sh::DT; ++t) {
+          dva[t] = Mma<T>::run(tr_frag<T, D>(sD, 32 * qp, t), pb, dva[t]);
+          dka[t] = Mma<T>::run(tr_frag<T, D>(sQ, 32 * qp, t), dsb, dka[t]);
+        }
+      }
+    }
+  }
+  if (kok) {
+#pragma unroll
+    for (int t = 0; t < Sh::DT; ++t) {
+      const int d = 16 * t + 4 * g;
+      if (d < D) {
+        V4 a, c;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          a[r] = from_f32<T>(dka[t][r]);
+          c[r] = from_f32<T>(dva[t][r]);
+        }
+        *reinterpret_cast<V4*>(dk + krow + d) = a;
+        *reinterpret_cast<V4*>(dv + krow + d) = c;
+      }
+    }
+  }
+}
+
+template <typename T, int D>
+void launch_backward(const T* q, const T* keys, const T* values, const T* o, const T* dout, const float* lse, float* dsum,
+                     T* dq, T* dk, T* dv, int B, int N, int M, int H, int HKV, int W, float scale, hipStream_t stream) {
+  const float scale_log2 = scale * 1.4426950408889634f;
+  const int nqt = (N + 63) / 64, nkt = (M + N + 63) / 64;
+  hipLaunchKernelGGL((attn_dq_kernel<T, D>), dim3((unsigned)((size_t)nqt * H * B)), dim3(256), 0, stream, q, keys,
+                     values, o, dout, lse, dsum, dq, N, M, H, HKV, W, scale, scale_log2, nqt);
+  hipLaunchKernelGGL((attn_dkv_kernel<T, D>), dim3((unsigned)((size_t)nkt * HKV * B)), dim3(256), 0, stream, q, keys,
+                     values, dout, lse, dsum, dk, dv, N, M, H, HKV, W, scale, scale_log2, nkt);
+}
+
+template <typename T>
+int window_attn_backward(const T* q, const T* keys, const T* values, const T* o, const T* dout, const float* lse,
+                         float* dsum, T* dq, T* dk, T* dv, int B, int N, int M, int H, int HKV, int D, int W,
+                         float scale, void* stream_ptr, const char* who) {
+  if (B < 0 || N < 0 || M < 0 || H < 1 || HKV < 1) return fail(ERR_ARG, "%s: bad sizes B=%d N=%d M=%d H=%d HKV=%d", who, B, N, M, H, HKV);
+  if (H % HKV != 0) return fail(ERR_ARG, "%s: %d query heads are not a multiple of %d KV heads", who, H, HKV);
+  if (W < 1) return fail(ERR_ARG, "%s: window must be at least 1, got %d", who, W);
+  if (!(scale > 0.f)) return fail(ERR_ARG, "%s: the score scale must be positive, got %g", who, (double)scale);
+  if (!(D == 16 || D == 32 || D == 64 || D == 128))
+    return fail(ERR_UNSUPPORTED, "%s: head dimension %d (kernels: 16, 32, 64, 128)", who, D);
+  if (B == 0 || N == 0) return OK;  // no query: the caller's zero dK, dV stand
+  if (!q || !keys || !values || !o || !dout || !lse || !dsum || !dq || !dk || !dv)
+    return fail(ERR_ARG, "%s: null pointer", who);
+  if ((reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(keys) | reinterpret_cast<uintptr_t>(values) |
+       reinterpret_cast<uintptr_t>(o) | reinterpret_cast<uintptr_t>(dout) | reinterpret_cast<uintptr_t>(dq) |
+       reinterpret_cast<uintptr_t>(dk) | reinterpret_cast<uintptr_t>(dv)) & 15)
+    return fail(ERR_ARG, "%s: q, keys, values, o, dO and the gradients must be 16-byte aligned", who);
+  if ((reinterpret_cast<uintptr_t>(lse) | reinterpret_cast<uintptr_t>(dsum)) & 3)
+    return fail(ERR_ARG, "%s: lse and the workspace must be 4-byte aligned", who);
+  hipStream_t stream = reinterpret_cast<hipStream_t>(stream_ptr);
+  switch (D) {
+    case 16: launch_backward<T, 16>(q, keys, values, o, dout, lse, dsum, dq, dk, dv, B, N, M, H, HKV, W, scale, stream); break;
+    case 32: launch_backward<T, 32>(q, keys, values, o, dout, lse, dsum, dq, dk, dv, B, N, M, H, HKV, W, scale, stream); break;
+    case 64: launch_backward<T, 64>(q, keys, values, o, dout, lse, dsum, dq, dk, dv, B, N, M, H, HKV, W, scale, stream); break;
+    default: launch_backward<T, 128>(q, keys, values, o, dout, lse, dsum, dq, dk, dv, B, N, M, H, HKV, W, scale, stream); break;
+  }
+  return check_launch(who);
+}
+
+}  // namespace
+}  // namespace vsp
+
+extern "C" int vsp_window_attn_backward_bf16(const void* q, const void* keys, const void* values, const void* o,
+                                             const void* dout, const float* lse, float* workspace, void* dq, void* dk,
+                                             void* dv, int B, int N, int M, int H, int HKV, int D, int window,
+                                             float scale, void* stream) {
+  using T = __bf16;
+  return vsp::window_attn_backward<T>(static_cast<const T*>(q), static_cast<const T*>(keys),
+                                      static_cast<const T*>(values), static_cast<const T*>(o),
+                                      static_cast<const T*>(dout), lse, workspace, static_cast<T*>(dq),
+                                      static_cast<T*>(dk), static_cast<T*>(dv), B, N, M, H, HKV, D, window, scale,
+                                      stream, "vsp_window_attn_backward_bf16");
+}
+
+extern "C" int vsp_window_attn_backward_f16(const void* q, const void* keys, const void* values, const void* o,
+                                            const void* dout, const float* lse, float* workspace, void* dq, void* dk,
+                                            void* dv, int B, int N, int M, int H, int HKV, int D, int window,
+                                            float scale, void* stream) {
+  using T = _Float16;
+  return vsp::window_attn_backward<T>(static_cast<const T*>(q), static_cast<const T*>(keys),
+                                      static_cast<const T*>(values), static_cast<const T*>(o),
+                                      static_cast<const T*>(dout), lse, workspace, static_cast<T*>(dq),
+                                      static_cast<T*>(dk), static_cast<T*>(dv), B, N, M, H, HKV, D, window, scale,
+                                      stream, "vsp_window_attn_backward_f16");
+}

@@ -11,12 +11,15 @@ the C ABI with the cache offset as an argument, so nothing is padded.
 For: bfloat16 or float16 on the GPU with consecutive positions (the window counts indices, as the
 reference's kernel does; ``WindowedAttention.attend`` checks the positions before calling).
 An optional keyword ``active`` (bool ``[b, n]``) skips inactive queries, whose outputs are zero;
-their keys and values stay visible to every other query. Forward only.
+their keys and values stay visible to every other query. Under autograd the forward also keeps
+each query's log-sum-exp and the backward (``vsp_window_attn_backward_*``) gives the gradients of
+``q``, ``keys`` and ``values`` (an inactive query passes none), as the reference's kernel does.
 """
 
 from __future__ import annotations
 
 import math
+from typing import Any
 
 import torch
 from torch import Tensor
@@ -33,13 +36,59 @@ def _aligned(t: Tensor) -> Tensor:
     return t if t.data_ptr() % 16 == 0 else t.clone()
 
 
+class _WindowAttention(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx: Any, q: Tensor, keys: Tensor, values: Tensor, window: int, mask: Tensor | None) -> Tensor:  # noqa: D102
+        b, n, h, dk = q.shape
+        s, hkv = keys.shape[1], keys.shape[2]
+        m = s - n
+        suffix = "bf16" if q.dtype == torch.bfloat16 else "f16"
+        if n == 0:
+            ctx.save_for_backward(q, keys, values, q, q.new_empty(0))
+            ctx.meta = (window, m)
+            return q.new_zeros(q.shape)
+        qc, kc, vc = _aligned(q.detach()), _aligned(keys.detach()), _aligned(values.detach())
+        o = torch.empty_like(qc)
+        args = (b, n, m, h, hkv, dk, int(window), 1.0 / math.sqrt(dk), _lib.stream_of(q.device))
+        with torch.cuda.device(q.device):
+            if any(ctx.needs_input_grad[:3]):
+                lse = torch.empty(b, h, n, dtype=torch.float32, device=q.device)
+                _lib.call(f"vsp_window_attn_lse_{suffix}", qc.data_ptr(), kc.data_ptr(), vc.data_ptr(), o.data_ptr(),
+                          lse.data_ptr(), _lib.ptr(mask), *args)
+                ctx.save_for_backward(qc, kc, vc, o, lse)
+                ctx.meta = (window, m)
+            else:
+                _lib.call(f"vsp_window_attn_{suffix}", qc.data_ptr(), kc.data_ptr(), vc.data_ptr(), o.data_ptr(),
+                          _lib.ptr(mask), *args)
+        return o
+
+    @staticmethod
+    def backward(ctx: Any, grad_o: Tensor) -> tuple[Tensor | None, ...]:  # noqa: D102
+        qc, kc, vc, o, lse = ctx.saved_tensors
+        window, m = ctx.meta
+        b, n, h, dk = qc.shape
+        hkv = kc.shape[2]
+        if n == 0:
+            return torch.zeros_like(qc), torch.zeros_like(kc), torch.zeros_like(vc), None, None
+        go = _aligned(grad_o.to(qc.dtype))
+        dq, dk_, dv = torch.empty_like(qc), torch.empty_like(kc), torch.empty_like(vc)
+        workspace = torch.empty(b * h * n, dtype=torch.float32, device=qc.device)
+        suffix = "bf16" if qc.dtype == torch.bfloat16 else "f16"
+        with torch.cuda.device(qc.device):
+            _lib.call(f"vsp_window_attn_backward_{suffix}", qc.data_ptr(), kc.data_ptr(), vc.data_ptr(), o.data_ptr(),
+                      go.data_ptr(), lse.data_ptr(), workspace.data_ptr(), dq.data_ptr(), dk_.data_ptr(), dv.data_ptr(),
+                      b, n, m, h, hkv, dk, int(window), 1.0 / math.sqrt(dk), _lib.stream_of(qc.device))
+        return (dq if ctx.needs_input_grad[0] else None, dk_ if ctx.needs_input_grad[1] else None,
+                dv if ctx.needs_input_grad[2] else None, None, None)
+
+
 def window_attention(q: Tensor, keys: Tensor, values: Tensor, window: int, *, active: Tensor | None = None) -> Tensor:
     """Outputs ``[b, n, h, dk]`` of ``q`` over ``keys, values [b, m + n, hkv, dk]``.
 
     Raises:
         ContractError: on shapes that disagree, a dtype other than bfloat16/float16 (or mixed), a
             tensor off the GPU, ``h`` not a multiple of ``hkv``, a head width the kernel does not
-            tile, fewer key rows than queries, or inputs needing a gradient.
+            tile, or fewer key rows than queries.
         ValueError: if ``window`` is below 1.
     """
     if window < 1:
@@ -67,20 +116,11 @@ def window_attention(q: Tensor, keys: Tensor, values: Tensor, window: int, *, ac
         raise ContractError(f"{h} query heads are not a multiple of {hkv} KV heads")
     if dk not in HEAD_DIMS:
         raise ContractError(f"head dimension {dk} is not one the kernel tiles ({HEAD_DIMS})")
-    if torch.is_grad_enabled() and any(t.requires_grad for t in (q, keys, values)):
-        raise ContractError("the HIP window attention is forward only: call it under torch.no_grad()")
     mask = None
     if active is not None:
         check_shape("active", active, ("b", "n"), {"b": b, "n": n}, torch.bool)
         if active.device != q.device:
             raise ContractError(f"active is on {active.device}, q on {q.device}")
         mask = active.contiguous().view(torch.uint8)
-    if n == 0:
-        return q.new_zeros(q.shape)
-    q, keys, values = _aligned(q), _aligned(keys), _aligned(values)
-    o = torch.empty_like(q)
-    entry = "vsp_window_attn_bf16" if q.dtype == torch.bfloat16 else "vsp_window_attn_f16"
-    with torch.cuda.device(q.device):
-        _lib.call(entry, q.data_ptr(), keys.data_ptr(), values.data_ptr(), o.data_ptr(), _lib.ptr(mask), b, n, m, h,
-                  hkv, dk, int(window), 1.0 / math.sqrt(dk), _lib.stream_of(q.device))
-    return o
+    out: Tensor = _WindowAttention.apply(q, keys, values, int(window), mask)
+    return out
