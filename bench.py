@@ -216,6 +216,47 @@ def time_key_filter(torch, reps: int = 50) -> tuple[float, float]:
     return out[0], out[1]
 
 
+def time_scan_backward(torch, reps: int = 10) -> float:
+    """Milliseconds per backward of the delta scan at B8 T4096 H8 d64 bf16 (the four backward
+    kernels through the C ABI), 10 launches in one HIP graph."""
+    from vesper.kernels import _lib
+
+    dev = torch.device("cuda:0")
+    q, k, v, beta, s0 = scan_inputs(torch, dev)
+    up = torch.randn(q.shape, generator=torch.Generator().manual_seed(8)).to(dev, torch.bfloat16)
+    ds = torch.randn(s0.shape, generator=torch.Generator().manual_seed(9)).to(dev)
+    dq, dk, dv, db = (torch.empty_like(t) for t in (q, k, v, beta))
+    d0 = torch.empty_like(s0)
+    nbytes = int(_lib.library().vsp_delta_scan_backward_workspace_bytes(B, T, H, D))
+    ws = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+
+    def run():
+        _lib.call("vsp_delta_scan_backward_bf16", _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(beta), _lib.ptr(s0),
+                  _lib.ptr(up), _lib.ptr(ds), None, _lib.ptr(dq), _lib.ptr(dk), _lib.ptr(dv), _lib.ptr(db),
+                  _lib.ptr(d0), _lib.ptr(ws), nbytes, B, T, H, D, _lib.stream_of(dev))
+
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        run()
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for _ in range(reps):
+            run()
+    graph.replay()
+    times = []
+    for _ in range(3):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        e0.record()
+        graph.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        times.append(e0.elapsed_time(e1) / reps)
+    return statistics.median(times)
+
+
 def time_attention_backward(torch, reps: int = 20) -> float:
     """Milliseconds per backward of window attention at B4 T4096 H8 D64 w512 bf16 (the dq and the
     dk/dv kernels, from a forward's o and log-sum-exp), 20 launches in one HIP graph."""
@@ -496,6 +537,7 @@ def main() -> int:
     a_bytes, a_flops = attn_bytes(B, T, H, H, D), attn_flops(B, T, H, D, WINDOW)
     attn4_ms = time_attention_config(torch)
     attn4_bwd_ms = time_attention_backward(torch)
+    scan_bwd_ms = time_scan_backward(torch)
     keys_ms, keys_bwd_ms = time_key_filter(torch)
     dec = None if args.no_decode else time_decode(torch)
     looped = None if args.no_loop else time_looped(torch)
@@ -538,6 +580,7 @@ def main() -> int:
             "delta_scan_tok_s": round(B * T / (pre["scan_ms"] / 1e3), 1),
             "delta_scan_hbm_frac": round(s_bytes / (pre["scan_ms"] / 1e3) / 1e9 / HBM_PEAK_GBS, 4),
             "delta_scan_mfma_frac_bf16": round(s_flops / (pre["scan_ms"] / 1e3) / 1e12 / BF16_PEAK_TFLOPS, 4),
+            "delta_scan_backward_ms": round(scan_bwd_ms, 4),
             "window_attn_b8_ms": round(pre["attn_ms"], 4),
             "window_attn_b4_ms": round(attn4_ms, 4),
             "window_attn_b4_tok_s": round(ATTN_B * T / (attn4_ms / 1e3), 1),

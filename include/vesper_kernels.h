@@ -22,7 +22,7 @@
 extern "C" {
 #endif
 
-#define VSP_ABI_VERSION 5
+#define VSP_ABI_VERSION 6
 
 /* Status codes. */
 #define VSP_OK 0
@@ -67,6 +67,22 @@ int vsp_delta_step_f32(const float* q, const float* k, const float* v, const flo
                        float* state_out, float* o, const uint8_t* active, int B, int H, int D, void* stream);
 int vsp_delta_step_bf16(const void* q, const void* k, const void* v, const void* beta, const float* state_in,
                         float* state_out, void* o, const uint8_t* active, int B, int H, int D, void* stream);
+
+/* The scan's backward (the gradients fla-core's chunk kernels give vesper/kernels/delta_scan.py:132-187
+ * under autograd): from d_o [B, N, H, D] (the inputs' dtype) and d_state [B, H, D, D] fp32 (the
+ * final state's gradient; NULL for zero), dq, dk, dv [B, N, H, D], dbeta [B, N, H] (the inputs'
+ * dtype) and d_state_in [B, H, D, D] fp32 (the initial state's). active as the forward (an inactive
+ * token's output gradient is ignored). D in {16, 32, 64}; arithmetic in fp32; deterministic.
+ * workspace: vsp_delta_scan_backward_workspace_bytes bytes, 16-byte aligned. N == 0 writes nothing. */
+size_t vsp_delta_scan_backward_workspace_bytes(int B, int N, int H, int D);
+int vsp_delta_scan_backward_bf16(const void* q, const void* k, const void* v, const void* beta, const float* state_in,
+                                 const void* d_o, const float* d_state, const uint8_t* active, void* dq, void* dk,
+                                 void* dv, void* dbeta, float* d_state_in, void* workspace, size_t workspace_bytes,
+                                 int B, int N, int H, int D, void* stream);
+int vsp_delta_scan_backward_f32(const float* q, const float* k, const float* v, const float* beta,
+                                const float* state_in, const float* d_o, const float* d_state, const uint8_t* active,
+                                float* dq, float* dk, float* dv, float* dbeta, float* d_state_in, void* workspace,
+                                size_t workspace_bytes, int B, int N, int H, int D, void* stream);
 
 /* ---- sliding-window causal attention (prefill) -----------------------------------------------
  * q: [B, N, H, D]; keys, values: [B, M + N, HKV, D], the cache's M rows first; o: [B, N, H, D].

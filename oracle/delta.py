@@ -164,3 +164,78 @@ def relative_error(got: Tensor, want: Tensor) -> float:
     den = float(b.square().sum().sqrt())
     num = float((a - b).square().sum().sqrt())
     return num / den if den > 0 else num
+
+
+def delta_scan_chunked_backward(
+    q: Tensor,
+    k: Tensor,
+    v: Tensor,
+    beta: Tensor,
+    state: Tensor,
+    d_o: Tensor,
+    d_state: Tensor | None = None,
+    block: int = 64,
+    active: Tensor | None = None,
+) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor]:
+    """``(dq, dk, dv, dbeta, dstate)`` of ``sum(o * d_o) + sum(state_n * d_state)`` for
+    ``delta_scan_chunked``, written out per block in the WY form (the algebra the scan's backward
+    kernels follow; checked against autograd through ``delta_scan_chunked``).
+
+    Per block, with ``H`` the state at its start, ``G`` the gradient of the state at its end,
+    ``L = (I + A)^-1``, ``T = L diag(beta)``, ``R = V - K H``, ``Delta = T R``, ``P = tril(Q K^T)``:
+    ``dDelta = K G + P^T dO``, ``dR = T^T dDelta`` (= ``dV``), ``dQ = dO H^T + tril(dO Delta^T) K``,
+    ``dT = dDelta R^T``, ``dA = tril(-L^T (dT diag(beta)) L^T, -1)``,
+    ``dK = Delta G^T + tril(dO Delta^T)^T Q - dR H^T + (diag(beta) dA + dA^T diag(beta)) K``,
+    ``dbeta_j = sum_i dT_ij L_ij + sum_m dA_jm (k_j . k_m)``, and the state's gradient at the block's
+    start ``G + Q^T dO - K^T dR``. An inactive token's output gradient is zero (its output is).
+    """
+    _check(q, k, v, beta, state, tokens=True)
+    b, n, h, d = q.shape
+    if active is not None:
+        d_o = torch.where(active[:, :, None, None], d_o, torch.zeros_like(d_o))
+    # the states at the block starts
+    starts, h_state = [], state
+    for s in range(0, n, block):
+        e = min(s + block, n)
+        kb, vb = (x[:, s:e].transpose(1, 2) for x in (k, v))
+        bb = beta[:, s:e].transpose(1, 2)
+        c = e - s
+        lower = torch.tril(bb[..., :, None] * (kb @ kb.transpose(-1, -2)), diagonal=-1)
+        inv = torch.linalg.solve_triangular(torch.eye(c, dtype=q.dtype) + lower,
+                                            torch.eye(c, dtype=q.dtype).expand_as(lower), upper=False,
+                                            unitriangular=True)
+        starts.append(h_state)
+        h_state = h_state + kb.transpose(-1, -2) @ (inv @ (bb[..., None] * (vb - kb @ h_state)))
+    dq, dk, dv = torch.zeros_like(q), torch.zeros_like(k), torch.zeros_like(v)
+    dbeta = torch.zeros_like(beta)
+    grad = torch.zeros_like(state) if d_state is None else d_state.clone()
+    for idx, s in reversed(list(enumerate(range(0, n, block)))):
+        e = min(s + block, n)
+        qb, kb, vb, gob = (x[:, s:e].transpose(1, 2) for x in (q, k, v, d_o))
+        bb = beta[:, s:e].transpose(1, 2)
+        c = e - s
+        hs = starts[idx]
+        gram = kb @ kb.transpose(-1, -2)
+        lower = torch.tril(bb[..., :, None] * gram, diagonal=-1)
+        inv = torch.linalg.solve_triangular(torch.eye(c, dtype=q.dtype) + lower,
+                                            torch.eye(c, dtype=q.dtype).expand_as(lower), upper=False,
+                                            unitriangular=True)
+        t_mat = inv * bb[..., None, :]
+        r = vb - kb @ hs
+        delta = t_mat @ r
+        p = torch.tril(qb @ kb.transpose(-1, -2))
+        d_delta = kb @ grad + p.transpose(-1, -2) @ gob
+        d_r = t_mat.transpose(-1, -2) @ d_delta
+        s2 = torch.tril(gob @ delta.transpose(-1, -2))
+        d_q = gob @ hs.transpose(-1, -2) + s2 @ kb
+        d_t = d_delta @ r.transpose(-1, -2)
+        d_l = torch.tril(d_t * bb[..., None, :])
+        d_a = -torch.tril(inv.transpose(-1, -2) @ d_l @ inv.transpose(-1, -2), diagonal=-1)
+        m = bb[..., :, None] * d_a
+        d_k = (delta @ grad.transpose(-1, -2) + s2.transpose(-1, -2) @ qb - d_r @ hs.transpose(-1, -2)
+               + m @ kb + m.transpose(-1, -2) @ kb)
+        d_b = (d_t * inv).sum(dim=-2) + (d_a * gram).sum(dim=-1)
+        dq[:, s:e], dk[:, s:e], dv[:, s:e] = (x.transpose(1, 2) for x in (d_q, d_k, d_r))
+        dbeta[:, s:e] = d_b.transpose(1, 2)
+        grad = grad + qb.transpose(-1, -2) @ gob - kb.transpose(-1, -2) @ d_r
+    return dq, dk, dv, dbeta, grad

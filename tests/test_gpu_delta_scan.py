@@ -2,7 +2,9 @@
 
 The oracle in float64, fed the same bf16- (or fp32-) valued inputs, is the truth. Tolerances are
 the reference's own (``tests/test_delta_scan_fused.py:34``, ``:255``): relative Frobenius error
-below 1.5e-2 for the bf16 kernel and 1e-5 for the fp32 kernel, on outputs and final states.
+below 1.5e-2 for the bf16 kernel and 1e-5 for the fp32 kernel, on outputs and final states, and on
+the gradients of q, k, v, beta and the initial state (``:87-102``, ``:285-300``; the oracle's by
+autograd through the chunked scan, its WY form pinned in ``tests/test_oracle_delta.py``).
 """
 
 from __future__ import annotations
@@ -161,8 +163,9 @@ def test_refuses_what_the_contract_excludes():
                          torch.zeros(1, 1, 512, 512, device=GPU))
     with pytest.raises(ContractError, match="dtype"):
         delta_scan_fused_fp32(q, k, v, beta, h0)
-    with pytest.raises(ContractError, match="forward only"):
-        delta_scan_fused(q.clone().requires_grad_(), k, v, beta, h0)
+    with pytest.raises(ContractError, match="backward takes head widths"):
+        delta_scan_fused(q.new_zeros(1, 8, 1, 128).requires_grad_(), q.new_zeros(1, 8, 1, 128),
+                         q.new_zeros(1, 8, 1, 128), q.new_zeros(1, 8, 1), torch.zeros(1, 1, 128, 128, device=GPU))
 
 
 def test_active_mask_zeroes_outputs_and_keeps_every_write():
@@ -263,3 +266,112 @@ def test_graph_replays_equal_the_eager_result():
         assert torch.equal(got_s, eager_s), i
         _ = delta_scan_fused(q, k, v, beta, h0)  # eager work between replays
         torch.cuda.synchronize()
+
+
+def _grad_check(fn, inputs, tol, active=None, with_state_grad=True):
+    g = torch.Generator().manual_seed(7)
+    b, n, h, dk = inputs[0].shape
+    d_o = torch.randn(b, n, h, dk, generator=g)
+    d_s = torch.randn(b, h, dk, dk, generator=g)
+    ref_in = [t.cpu().double().requires_grad_() for t in inputs]
+    o_ref, s_ref = delta_scan_chunked(*ref_in, 64, active=active)
+    loss = (o_ref * d_o.double()).sum() + ((s_ref * d_s.double()).sum() if with_state_grad else 0)
+    torch.autograd.backward([loss])
+    fused_in = [t.clone().requires_grad_() for t in inputs]
+    o, s = fn(*fused_in, active=None if active is None else active.to(GPU))
+    loss = (o.float() * d_o.to(GPU)).sum() + ((s * d_s.to(GPU)).sum() if with_state_grad else 0)
+    torch.autograd.backward([loss])
+    for name, got, want in zip(["q", "k", "v", "beta", "state"], fused_in, ref_in):
+        assert got.grad is not None, name
+        assert relative_error(got.grad, want.grad) < tol, (name, relative_error(got.grad, want.grad))
+    return fused_in
+
+
+@pytest.mark.parametrize(("b", "n", "h", "dk"), SIZES[:4])
+def test_every_gradient_matches_the_oracle(b, n, h, dk):
+    from vesper.kernels.delta_scan import delta_scan_fused
+
+    _grad_check(delta_scan_fused, _bf16_inputs(b, n, h, dk), TOL)
+
+
+@pytest.mark.parametrize(("b", "n", "h", "dk"), SIZES[:4])
+def test_fp32_every_gradient_matches_the_oracle_to_float32(b, n, h, dk):
+    from vesper.kernels.delta_scan import delta_scan_fused_fp32
+
+    _grad_check(delta_scan_fused_fp32, _fp32_inputs(b, n, h, dk), TOL_FP32)
+
+
+@pytest.mark.parametrize("dk", [16, 32, 64])
+def test_gradients_with_an_active_mask_and_every_width(dk):
+    from vesper.kernels.delta_scan import delta_scan_fused_fp32
+
+    act = torch.rand(2, 150, generator=torch.Generator().manual_seed(8)) < 0.6
+    _grad_check(delta_scan_fused_fp32, _fp32_inputs(2, 150, 2, dk, seed=dk), TOL_FP32, active=act)
+
+
+def test_fp32_gradients_flow_from_a_state_that_needs_none():
+    # tests/test_delta_scan_fused.py:303-323: a cold or detached state does not require a gradient
+    from vesper.kernels.delta_scan import delta_scan_fused_fp32
+
+    q, k, v, beta, h0 = _fp32_inputs(2, 63, 3, 16)
+    ref_in = [t.cpu().double().requires_grad_() for t in (q, k, v, beta)]
+    o_ref, _ = delta_scan_chunked(*ref_in, h0.cpu().double(), 64)
+    torch.autograd.backward([o_ref.square().sum()])
+    fused_in = [t.clone().requires_grad_() for t in (q, k, v, beta)]
+    state = h0.clone()
+    o, _ = delta_scan_fused_fp32(*fused_in, state)
+    torch.autograd.backward([o.square().sum()])
+    assert not state.requires_grad and state.grad is None
+    for name, got, want in zip(["q", "k", "v", "beta"], fused_in, ref_in):
+        assert relative_error(got.grad, want.grad) < TOL_FP32, name
+
+
+def test_the_gradients_at_b8_t4096_h8_d64_and_they_repeat():
+    from vesper.kernels.delta_scan import delta_scan_fused
+
+    inputs = _bf16_inputs(8, 4096, 8, 64, seed=3)
+    g = torch.Generator().manual_seed(9)
+    d_o = torch.randn(8, 4096, 8, 64, generator=g).to(GPU, BF16)
+
+    def run():
+        ins = [t.clone().requires_grad_() for t in inputs]
+        o, _ = delta_scan_fused(*ins)
+        o.backward(d_o)
+        return [t.grad for t in ins]
+
+    first, again = run(), run()
+    for a, c in zip(first, again):
+        assert torch.equal(a, c)  # deterministic: no atomics
+    ref_in = [t.cpu().float().requires_grad_() for t in inputs]
+    o_ref, _ = delta_scan_chunked(*ref_in, 64)
+    o_ref.backward(d_o.cpu().float())
+    for name, got, want in zip(["q", "k", "v", "beta", "state"], first, ref_in):
+        assert relative_error(got, want.grad) < TOL, name
+
+
+def test_captured_forward_and_backward_equal_eager():
+    from vesper.kernels.delta_scan import delta_scan_fused
+
+    q, k, v, beta, h0 = (t.requires_grad_() for t in _bf16_inputs(2, 200, 2, 64, seed=4))
+    d_o = torch.randn(2, 200, 2, 64, generator=torch.Generator().manual_seed(10)).to(GPU, BF16)
+
+    def step():
+        o, s = delta_scan_fused(q, k, v, beta, h0)
+        return (o.detach(), s.detach(), *torch.autograd.grad(o, (q, k, v, beta, h0), d_o))
+
+    eager = [t.clone() for t in step()]
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        step()
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        static = step()
+    for _ in range(3):
+        for t in static:
+            t.zero_()
+        graph.replay()
+        torch.cuda.synchronize()
+        for a, c in zip(static, eager):
+            assert torch.equal(a, c)

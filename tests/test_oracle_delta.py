@@ -13,6 +13,7 @@ import torch
 
 from conftest import frac_tensor, reference_vectors, scan_inputs
 from oracle import delta as od
+from oracle.delta import delta_scan_chunked, delta_scan_chunked_backward, normalize_keys
 
 F64 = torch.float64
 
@@ -211,3 +212,53 @@ def test_the_rational_case_catches_planted_mistakes(kind: str) -> None:
         outs.append(ot)
     got = torch.stack(outs, 1)
     assert (got - o).abs().max().item() > 1e-3 or (s - h2).abs().max().item() > 1e-3
+
+
+@pytest.mark.parametrize(("b", "n", "h", "dk", "block"), [(2, 1, 2, 4, 64), (2, 63, 3, 8, 64), (1, 130, 2, 8, 64),
+                                                          (2, 70, 2, 4, 16)])
+def test_the_chunked_backward_equals_autograd(b, n, h, dk, block):
+    # the WY-form backward (what the scan's backward kernels compute) against autograd through the
+    # chunked forward: partial blocks, a zero write strength, inactive tokens, a state gradient
+    g = torch.Generator().manual_seed(b * 100 + n)
+    q = torch.randn(b, n, h, dk, generator=g, dtype=torch.float64)
+    k = normalize_keys(torch.randn(b, n, h, dk, generator=g, dtype=torch.float64))
+    v = torch.randn(b, n, h, dk, generator=g, dtype=torch.float64)
+    beta = torch.sigmoid(torch.randn(b, n, h, generator=g, dtype=torch.float64))
+    beta[0, 0, 0] = 0.0
+    h0 = 0.3 * torch.randn(b, h, dk, dk, generator=g, dtype=torch.float64)
+    d_o = torch.randn(b, n, h, dk, generator=g, dtype=torch.float64)
+    d_s = torch.randn(b, h, dk, dk, generator=g, dtype=torch.float64)
+    active = torch.rand(b, n, generator=g) < 0.7
+    ins = [t.clone().requires_grad_() for t in (q, k, v, beta, h0)]
+    o, s = delta_scan_chunked(*ins, block, active=active)
+    ((o * d_o).sum() + (s * d_s).sum()).backward()
+    got = delta_scan_chunked_backward(q, k, v, beta, h0, d_o, d_s, block, active=active)
+    for a, t, name in zip(got, ins, ("q", "k", "v", "beta", "state")):
+        torch.testing.assert_close(a, t.grad, rtol=1e-11, atol=1e-12, msg=name)
+
+
+def test_the_chunked_scan_gradients_match_finite_differences():
+    g = torch.Generator().manual_seed(77)
+    b, n, h, dk = 1, 7, 1, 3
+    q = torch.randn(b, n, h, dk, generator=g, dtype=torch.float64, requires_grad=True)
+    k = normalize_keys(torch.randn(b, n, h, dk, generator=g, dtype=torch.float64)).requires_grad_()
+    v = torch.randn(b, n, h, dk, generator=g, dtype=torch.float64, requires_grad=True)
+    beta = torch.sigmoid(torch.randn(b, n, h, generator=g, dtype=torch.float64)).requires_grad_()
+    h0 = torch.randn(b, h, dk, dk, generator=g, dtype=torch.float64, requires_grad=True)
+    assert torch.autograd.gradcheck(lambda *a: delta_scan_chunked(*a, 3), (q, k, v, beta, h0))
+
+
+def test_a_planted_transpose_in_the_backward_is_caught(monkeypatch):
+    import oracle.delta as od
+
+    g = torch.Generator().manual_seed(78)
+    args = [torch.randn(1, 9, 1, 4, generator=g, dtype=torch.float64) for _ in range(3)]
+    args[1] = normalize_keys(args[1])
+    beta = torch.sigmoid(torch.randn(1, 9, 1, generator=g, dtype=torch.float64))
+    h0 = torch.randn(1, 1, 4, 4, generator=g, dtype=torch.float64)
+    d_o = torch.randn(1, 9, 1, 4, generator=g, dtype=torch.float64)
+    right = od.delta_scan_chunked_backward(*args, beta, h0, d_o, None, 4)
+    real = torch.linalg.solve_triangular
+    monkeypatch.setattr(torch.linalg, "solve_triangular", lambda a, b_, **kw: real(a, b_, **kw).transpose(-1, -2))
+    wrong = od.delta_scan_chunked_backward(*args, beta, h0, d_o, None, 4)
+    assert not torch.allclose(right[1], wrong[1], rtol=1e-3)

@@ -17,7 +17,7 @@ import torch
 HERE = Path(__file__).resolve().parent
 LIBRARY_PATH = HERE / "libvesper_kernels.so"
 HEADER_PATH = HERE.parents[2] / "include" / "vesper_kernels.h"
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 P = ctypes.c_void_p
 I = ctypes.c_int
@@ -35,6 +35,9 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "vsp_delta_step_bf16": (I, [P, P, P, P, P, P, P, P, I, I, I, P]),
     "vsp_window_attn_bf16": (I, [P, P, P, P, P, I, I, I, I, I, I, I, F, P]),
     "vsp_window_attn_f16": (I, [P, P, P, P, P, I, I, I, I, I, I, I, F, P]),
+    "vsp_delta_scan_backward_workspace_bytes": (Z, [I, I, I, I]),
+    "vsp_delta_scan_backward_bf16": (I, [P, P, P, P, P, P, P, P, P, P, P, P, P, P, Z, I, I, I, I, P]),
+    "vsp_delta_scan_backward_f32": (I, [P, P, P, P, P, P, P, P, P, P, P, P, P, P, Z, I, I, I, I, P]),
     "vsp_window_attn_lse_bf16": (I, [P, P, P, P, P, P, I, I, I, I, I, I, I, F, P]),
     "vsp_window_attn_lse_f16": (I, [P, P, P, P, P, P, I, I, I, I, I, I, I, F, P]),
     "vsp_window_attn_backward_bf16": (I, [P, P, P, P, P, P, P, P, P, P, I, I, I, I, I, I, I, F, P]),

@@ -15,11 +15,15 @@ already normalised. Where the reference calls fla-core's Triton kernels, these c
 
 Each takes an optional keyword ``active`` (bool ``[b, n]``, ``[b]`` for the step): inactive tokens
 still write the state; their outputs are zero (``vesper/loop.py:24-26``, ``:441-442``). ``None`` is
-exactly the reference behaviour. The kernels are forward only: inputs that require a gradient are
-refused while grad mode is on.
+exactly the reference behaviour. The two chunked scans are autograd functions: their backward
+(``vsp_delta_scan_backward_*``, head widths 16, 32 and 64) gives the gradients of ``q, k, v, beta``
+and the initial state, as the reference's kernels do; the single step is forward only (inputs
+that require a gradient are refused while grad mode is on).
 """
 
 from __future__ import annotations
+
+from typing import Any
 
 import torch
 from torch import Tensor
@@ -28,6 +32,7 @@ from vesper.contracts import ContractError, Dims, check_shape
 from vesper.kernels import _lib
 
 MAX_HEAD_DIM = 256  # delta_scan.py:41 in the reference; the HIP kernels take any width up to it
+BACKWARD_HEAD_DIMS = (16, 32, 64)  # the widths the backward kernels take
 INPUT_DTYPE = torch.bfloat16  # delta_scan_fused's q, k, v, beta
 FP32_INPUT_DTYPE = torch.float32  # delta_scan_fused_fp32's q, k, v, beta
 STATE_DTYPE = torch.float32
@@ -64,7 +69,7 @@ def _checked_length(q: Tensor, k: Tensor, v: Tensor, beta: Tensor, state: Tensor
 def _refuse_grad(*tensors: Tensor) -> None:
     if torch.is_grad_enabled() and any(t.requires_grad for t in tensors):
         raise ContractError(
-            "the HIP delta scan is forward only (no backward kernel yet): call it under torch.no_grad() "
+            "the HIP delta step is forward only (no backward kernel): call it under torch.no_grad() "
             "or on detached inputs"
         )
 
@@ -85,10 +90,11 @@ def _aligned(t: Tensor) -> Tensor:
 
 
 def _scan(entry: str, q: Tensor, k: Tensor, v: Tensor, beta: Tensor, state: Tensor, active: Tensor | None,
-          fp32: bool) -> tuple[Tensor, Tensor]:
+          fp32: bool, mask: Tensor | None = None) -> tuple[Tensor, Tensor]:
     b, n, h, dk = q.shape
     q, k, v, beta, state = (_aligned(t) for t in (q, k, v, beta, state))
-    mask = _active_mask(active, ("b", "n"), {"b": b, "n": n}, q.device)
+    if mask is None:
+        mask = _active_mask(active, ("b", "n"), {"b": b, "n": n}, q.device)
     o = torch.empty_like(q)
     s_out = torch.empty_like(state)
     lib = _lib.library()
@@ -98,6 +104,56 @@ def _scan(entry: str, q: Tensor, k: Tensor, v: Tensor, beta: Tensor, state: Tens
         _lib.call(entry, q.data_ptr(), k.data_ptr(), v.data_ptr(), beta.data_ptr(), state.data_ptr(), o.data_ptr(),
                   s_out.data_ptr(), _lib.ptr(ws), ws_bytes, _lib.ptr(mask), b, n, h, dk, _lib.stream_of(q.device))
     return o, s_out
+
+
+class _DeltaScan(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx: Any, q: Tensor, k: Tensor, v: Tensor, beta: Tensor, state: Tensor, mask: Tensor | None,
+                fp32: bool) -> tuple[Tensor, Tensor]:  # noqa: D102
+        entry = "vsp_delta_scan_f32" if fp32 else "vsp_delta_scan_bf16"
+        tensors = [t.detach() for t in (q, k, v, beta, state)]
+        o, s_out = _scan(entry, *tensors, None, fp32, mask=mask)
+        if any(ctx.needs_input_grad[:5]):
+            ctx.save_for_backward(*(_aligned(t) for t in tensors), *(() if mask is None else (mask,)))
+            ctx.fp32 = fp32
+            ctx.masked = mask is not None
+        return o, s_out
+
+    @staticmethod
+    def backward(ctx: Any, d_o: Tensor | None, d_state: Tensor | None) -> tuple[Tensor | None, ...]:  # noqa: D102
+        saved = ctx.saved_tensors
+        q, k, v, beta, state = saved[:5]
+        mask = saved[5] if ctx.masked else None
+        b, n, h, dk = q.shape
+        go = torch.zeros_like(q) if d_o is None else _aligned(d_o.to(q.dtype))
+        gs = None if d_state is None else _aligned(d_state.to(STATE_DTYPE))
+        dq, dk_, dv, db = (torch.empty_like(t) for t in (q, k, v, beta))
+        d_state_in = torch.empty_like(state)
+        lib = _lib.library()
+        ws_bytes = int(lib.vsp_delta_scan_backward_workspace_bytes(b, n, h, dk))
+        ws = torch.empty(max(ws_bytes, 16), dtype=torch.uint8, device=q.device)
+        entry = "vsp_delta_scan_backward_f32" if ctx.fp32 else "vsp_delta_scan_backward_bf16"
+        with torch.cuda.device(q.device):
+            _lib.call(entry, q.data_ptr(), k.data_ptr(), v.data_ptr(), beta.data_ptr(), state.data_ptr(),
+                      go.data_ptr(), _lib.ptr(gs), _lib.ptr(mask), dq.data_ptr(), dk_.data_ptr(), dv.data_ptr(),
+                      db.data_ptr(), d_state_in.data_ptr(), ws.data_ptr(), ws_bytes, b, n, h, dk,
+                      _lib.stream_of(q.device))
+        need = ctx.needs_input_grad
+        return (dq if need[0] else None, dk_ if need[1] else None, dv if need[2] else None,
+                db if need[3] else None, d_state_in if need[4] else None, None, None)
+
+
+def _autograd_scan(q: Tensor, k: Tensor, v: Tensor, beta: Tensor, state: Tensor, active: Tensor | None,
+                   fp32: bool) -> tuple[Tensor, Tensor]:
+    b, n, _, dk = q.shape
+    mask = _active_mask(active, ("b", "n"), {"b": b, "n": n}, q.device)
+    if torch.is_grad_enabled() and any(t.requires_grad for t in (q, k, v, beta, state)):
+        if dk not in BACKWARD_HEAD_DIMS:
+            raise ContractError(f"the scan's backward takes head widths {BACKWARD_HEAD_DIMS}, got {dk}")
+        out: tuple[Tensor, Tensor] = _DeltaScan.apply(q, k, v, beta, state, mask, fp32)
+        return out
+    entry = "vsp_delta_scan_f32" if fp32 else "vsp_delta_scan_bf16"
+    return _scan(entry, q, k, v, beta, state, None, fp32, mask=mask)
 
 
 def delta_scan_fused(q: Tensor, k: Tensor, v: Tensor, beta: Tensor, state: Tensor, *,
@@ -116,14 +172,16 @@ def delta_scan_fused(q: Tensor, k: Tensor, v: Tensor, beta: Tensor, state: Tenso
         ``(o, state_n)``: ``o [b, n, h, dk]`` bfloat16 and the final state in float32; with no
         tokens, the empty query tensor and the unchanged state object.
 
+    Under autograd the gradients of ``q, k, v, beta`` (bfloat16) and ``state`` (float32) come from
+    the backward kernels.
+
     Raises:
-        ContractError: on a dtype, shape, device or width outside the contract, or inputs needing
-            a gradient, before any kernel runs.
+        ContractError: on a dtype, shape, device or width outside the contract (with a gradient
+            needed, a head width outside 16, 32, 64), before any kernel runs.
     """
     if _checked_length(q, k, v, beta, state, INPUT_DTYPE) == 0:
         return q, state
-    _refuse_grad(q, k, v, beta, state)
-    return _scan("vsp_delta_scan_bf16", q, k, v, beta, state, active, fp32=False)
+    return _autograd_scan(q, k, v, beta, state, active, fp32=False)
 
 
 def delta_scan_fused_fp32(q: Tensor, k: Tensor, v: Tensor, beta: Tensor, state: Tensor, *,
@@ -134,8 +192,7 @@ def delta_scan_fused_fp32(q: Tensor, k: Tensor, v: Tensor, beta: Tensor, state: 
     """
     if _checked_length(q, k, v, beta, state, FP32_INPUT_DTYPE) == 0:
         return q, state
-    _refuse_grad(q, k, v, beta, state)
-    return _scan("vsp_delta_scan_f32", q, k, v, beta, state, active, fp32=True)
+    return _autograd_scan(q, k, v, beta, state, active, fp32=True)
 
 
 def delta_scan_step_fused(q: Tensor, k: Tensor, v: Tensor, beta: Tensor, state: Tensor, *,
