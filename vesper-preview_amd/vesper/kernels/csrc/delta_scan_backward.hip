@@ -29,17 +29,39 @@ constexpr int kPC = kC + 4;  // pitch (floats) of a [.][64] LDS matrix
 
 // C[16 x 16] += op(X)[16 x K] op(Y)[K x 16] on fp32 MFMA. op(X)[i][k] is X[i * ldx + k] (TA false)
 // or X[k * ldx + i] (TA true, X stored [k][i]); op(Y)[k][j] is Y[k * ldy + j] (TB false) or
-// Y[j * ldy + k] (TB true), times yscale[k] when given. X and Y point at the tile's origin. The
-// result: lane (j, g) holds rows 4 g .. 4 g + 3 of column j.
+// Y[j * ldy + k] (TB true), times yscale[k] when given. X and Y point at the tile's origin (16-byte
+// aligned, pitches multiples of 4). Lane group g supplies k = (K / 4) g + m in step m (the sum's
+// order is free), so a row-contiguous operand comes in 16-byte LDS reads of four k. The result:
+// lane (j, g) holds rows 4 g .. 4 g + 3 of column j.
 template <bool TA, bool TB>
 __device__ __forceinline__ f32x4 mm16(const float* X, int ldx, const float* Y, int ldy, int K, f32x4 acc,
                                       const float* yscale = nullptr) {
-  const int l = threadIdx.x & 63, i = l & 15, kk = l >> 4;
-  for (int k = 0; k < K; k += 4) {
-    const float a = TA ? X[(k + kk) * ldx + i] : X[i * ldx + k + kk];
-    float b = TB ? Y[i * ldy + k + kk] : Y[(k + kk) * ldy + i];
-    if (yscale != nullptr) b *= yscale[k + kk];
-    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, acc, 0, 0, 0);
+  const int l = threadIdx.x & 63, i = l & 15, g = l >> 4;
+  const int KM = K / 4, kb = KM * g;
+  for (int m = 0; m < KM; m += 4) {
+    float a[4], b[4];
+    if constexpr (!TA) {
+      const f32x4 v = *reinterpret_cast<const f32x4*>(X + i * ldx + kb + m);
+#pragma unroll
+      for (int u = 0; u < 4; ++u) a[u] = v[u];
+    } else {
+#pragma unroll
+      for (int u = 0; u < 4; ++u) a[u] = X[(kb + m + u) * ldx + i];
+    }
+    if constexpr (TB) {
+      const f32x4 v = *reinterpret_cast<const f32x4*>(Y + i * ldy + kb + m);
+#pragma unroll
+      for (int u = 0; u < 4; ++u) b[u] = v[u];
+    } else {
+#pragma unroll
+      for (int u = 0; u < 4; ++u) b[u] = Y[(kb + m + u) * ldy + i];
+    }
+    if (yscale != nullptr) {
+#pragma unroll
+      for (int u = 0; u < 4; ++u) b[u] *= yscale[kb + m + u];
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[u], b[u], acc, 0, 0, 0);
   }
   return acc;
 }
@@ -57,16 +79,33 @@ __device__ __forceinline__ int tile_col() { return threadIdx.x & 15; }
 
 // chunk rows t0 .. t0 + 63 of a [B, N, H, D] tensor (head h of batch row b) into LDS [64][ld] as
 // fp32; rows past N are zero, and with `active` so are inactive tokens' rows
+// Loads are unconditional (rows past N re-read row N - 1) and the zeros are selected afterwards, so
+// no load sits behind a per-lane branch (which would make each wait for every earlier one).
+template <typename TIn>
+__device__ __forceinline__ void load4_f32(const TIn* p, float (&x)[4]) {
+  if constexpr (sizeof(TIn) == 2) {
+    typedef TIn V4 __attribute__((ext_vector_type(4)));
+    const V4 v = *reinterpret_cast<const V4*>(p);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) x[j] = to_f32(v[j]);
+  } else {
+    const f32x4 v = *reinterpret_cast<const f32x4*>(p);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) x[j] = v[j];
+  }
+}
+
 template <typename TIn, int D>
 __device__ __forceinline__ void load_rows(float* dst, int ld, const TIn* src, int b, int h, int t0, int N, int H,
                                           const uint8_t* active = nullptr) {
   for (int e = threadIdx.x; e < kC * D / 4; e += blockDim.x) {
     const int row = e / (D / 4), c = 4 * (e - row * (D / 4));
-    const int t = t0 + row;
-    const bool ok = t < N && (active == nullptr || active[(size_t)b * N + t] != 0);
-    const TIn* p = src + (((size_t)b * N + (ok ? t : 0)) * H + h) * D + c;
+    const int t = t0 + row, tc = min(t, N - 1);
+    const bool ok = t < N && (active == nullptr || active[(size_t)b * N + tc] != 0);
+    float x[4];
+    load4_f32(src + (((size_t)b * N + tc) * H + h) * D + c, x);
 #pragma unroll
-    for (int j = 0; j < 4; ++j) dst[row * ld + c + j] = ok ? to_f32(p[j]) : 0.f;
+    for (int j = 0; j < 4; ++j) dst[row * ld + c + j] = ok ? x[j] : 0.f;
   }
 }
 
@@ -74,7 +113,8 @@ template <typename TIn>
 __device__ __forceinline__ void load_beta(float* dst, const TIn* beta, int b, int h, int t0, int N, int H) {
   for (int r = threadIdx.x; r < kC; r += blockDim.x) {
     const int t = t0 + r;
-    dst[r] = t < N ? to_f32(beta[((size_t)b * N + t) * H + h]) : 0.f;
+    const float x = to_f32(beta[((size_t)b * N + min(t, N - 1)) * H + h]);
+    dst[r] = t < N ? x : 0.f;
   }
 }
 
@@ -219,89 +259,160 @@ __global__ __launch_bounds__(256) void scan_bwd_prep_kernel(const TIn* __restric
   }
 }
 
-// the states at the chunk starts, 16 value columns per workgroup (one wave per 16 rows)
+// The two chains: one workgroup per (b, h, 16 value columns), four waves. A wave's A operands come
+// from global memory straight into registers, a chunk ahead of their use; in MFMA step m lane group
+// g supplies k = (K / 4) g + m, so each lane reads K / 4 consecutive elements of its row (the B
+// operands, from LDS, follow the same k order). Only the 16-column state slice and the chunk's
+// [64 x 16] intermediate live in LDS; two barriers per chunk.
+constexpr int kPS = 20;  // LDS pitch (floats) of a 16-column slice
+
+// C[16 x 16] += A B with A from registers (a[m] = A[i][(K / 4) g + m], lane (i, g)) and B
+// row-major in LDS ([k][16], pitch kPS): K / 4 MFMA steps
+template <int KM>
+__device__ __forceinline__ f32x4 mm_reg(const float (&a)[KM], const float* Y, f32x4 acc) {
+  const int l = threadIdx.x & 63, j = l & 15, g = l >> 4;
+#pragma unroll
+  for (int m = 0; m < KM; ++m) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[m], Y[(KM * g + m) * kPS + j], acc, 0, 0, 0);
+  return acc;
+}
+
 template <typename TIn, int D>
-__global__ __launch_bounds__(256) void scan_bwd_states_kernel(const TIn* __restrict__ k,
-                                                              const float* __restrict__ state_in,
-                                                              float* __restrict__ ws, int N, int H, int NC) {
-  constexpr int PD = D + 4, PS = 20, NS = D / 16;
-  __shared__ __align__(16) float sW[kC * PD], sK[kC * PD], sU[kC * PS], sD[kC * PS], sH[D * PS];
-  const int s = blockIdx.x % NS, bh = blockIdx.x / NS;
-  const int b = bh / H, h = bh - b * H;
-  const int w = threadIdx.x >> 6;
-  const float* h0 = state_in + (size_t)bh * D * D;
-  for (int e = threadIdx.x; e < D * 16; e += blockDim.x) sH[(e / 16) * PS + e % 16] = h0[(e / 16) * D + 16 * s + e % 16];
-  for (int c = 0; c < NC; ++c) {
-    const size_t chunk = (size_t)bh * NC + c;
-    __syncthreads();  // sH complete, the previous chunk's reads done
-    float* gH = Ws<D>::Hs(ws, chunk);
-    for (int e = threadIdx.x; e < D * 16; e += blockDim.x) gH[(e / 16) * D + 16 * s + e % 16] = sH[(e / 16) * PS + e % 16];
-    load_mat<D>(sW, PD, Ws<D>::W(ws, chunk), kC);
-    load_rows<TIn, D>(sK, PD, k, b, h, c * kC, N, H);
-    const float* gU = Ws<D>::U(ws, chunk);
-    for (int e = threadIdx.x; e < kC * 16; e += blockDim.x) sU[(e / 16) * PS + e % 16] = gU[(e / 16) * D + 16 * s + e % 16];
-    __syncthreads();
-    // Delta = U - W H (rows 16 w)
-    {
-      const f32x4 acc = mm16<false, false>(sW + 16 * w * PD, PD, sH, PS, D, zero4());
+struct StateOps {
+  float wa[D / 4];  // W row 16 w + i, columns (D / 4) g .. + D / 4
+  float ua[4];      // U rows 16 w + 4 g + r, column 16 s + i
+  float ka[16];     // K^T row 16 w + i (a feature), tokens 16 g .. + 15 (waves w < D / 16)
+};
+
+template <typename TIn, int D>
+__device__ __forceinline__ void load_state_ops(StateOps<TIn, D>& o, const float* ws, const TIn* k, size_t chunk, int b,
+                                               int h, int t0, int N, int H, int s) {
+  const int l = threadIdx.x & 63, i = l & 15, g = l >> 4, w = threadIdx.x >> 6;
+  const float* W = Ws<D>::W(const_cast<float*>(ws), chunk);
+  const float* U = Ws<D>::U(const_cast<float*>(ws), chunk);
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int i = 16 * w + tile_row(r), j = tile_col();
-        sD[i * PS + j] = sU[i * PS + j] - acc[r];
-      }
-    }
-    __syncthreads();
-    // H += K^T Delta (rows 16 w of H, for w < D / 16)
-    if (w < D / 16) {
-      const f32x4 acc = mm16<true, false>(sK + 16 * w, PD, sD, PS, kC, zero4());
+  for (int q = 0; q < D / 16; ++q) {
+    const f32x4 v = *reinterpret_cast<const f32x4*>(W + (16 * w + i) * D + (D / 4) * g + 4 * q);
 #pragma unroll
-      for (int r = 0; r < 4; ++r) sH[(16 * w + tile_row(r)) * PS + tile_col()] += acc[r];
+    for (int e = 0; e < 4; ++e) o.wa[4 * q + e] = v[e];
+  }
+#pragma unroll
+  for (int r = 0; r < 4; ++r) o.ua[r] = U[(16 * w + 4 * g + r) * D + 16 * s + i];
+  if (w < D / 16) {
+#pragma unroll
+    for (int m = 0; m < 16; ++m) {
+      const int t = t0 + 16 * g + m;
+      const float x = to_f32(k[(((size_t)b * N + min(t, N - 1)) * H + h) * D + 16 * w + i]);
+      o.ka[m] = t < N ? x : 0.f;
     }
   }
 }
 
-// the state's gradient at every chunk's end (reverse chain) and at the start
+// the states at the chunk starts: Delta = U - W H, H += K^T Delta
+template <typename TIn, int D>
+__global__ __launch_bounds__(256) void scan_bwd_states_kernel(const TIn* __restrict__ k,
+                                                              const float* __restrict__ state_in,
+                                                              float* __restrict__ ws, int N, int H, int NC) {
+  constexpr int NS = D / 16;
+  __shared__ __align__(16) float sD[kC * kPS], sH[D * kPS];
+  const int s = blockIdx.x % NS, bh = blockIdx.x / NS;
+  const int b = bh / H, h = bh - b * H;
+  const int w = threadIdx.x >> 6, l = threadIdx.x & 63, j = l & 15, g = l >> 4;
+  const float* h0 = state_in + (size_t)bh * D * D;
+  for (int e = threadIdx.x; e < D * 16; e += blockDim.x) sH[(e / 16) * kPS + e % 16] = h0[(e / 16) * D + 16 * s + e % 16];
+  StateOps<TIn, D> ops[2];
+  load_state_ops<TIn, D>(ops[0], ws, k, (size_t)bh * NC, b, h, 0, N, H, s);
+  __syncthreads();
+  auto step = [&](int c, const StateOps<TIn, D>& cur, StateOps<TIn, D>& nxt) {
+    const size_t chunk = (size_t)bh * NC + c;
+    if (c + 1 < NC) load_state_ops<TIn, D>(nxt, ws, k, chunk + 1, b, h, (c + 1) * kC, N, H, s);
+    float* gH = Ws<D>::Hs(ws, chunk);
+    for (int e = threadIdx.x; e < D * 16; e += blockDim.x) gH[(e / 16) * D + 16 * s + e % 16] = sH[(e / 16) * kPS + e % 16];
+    const f32x4 acc = mm_reg<D / 4>(cur.wa, sH, zero4());
+#pragma unroll
+    for (int r = 0; r < 4; ++r) sD[(16 * w + 4 * g + r) * kPS + j] = cur.ua[r] - acc[r];
+    __syncthreads();  // Delta complete; the reads of H are done
+    if (w < D / 16) {
+      const f32x4 dh = mm_reg<16>(cur.ka, sD, zero4());
+#pragma unroll
+      for (int r = 0; r < 4; ++r) sH[(16 * w + 4 * g + r) * kPS + j] += dh[r];
+    }
+    __syncthreads();
+  };
+  for (int c = 0; c < NC; c += 2) {
+    step(c, ops[0], ops[1]);
+    if (c + 1 < NC) step(c + 1, ops[1], ops[0]);
+  }
+}
+
+template <typename TIn, int D>
+struct DStateOps {
+  float ka[D / 4];  // K row 16 w + i (a token), features (D / 4) g .. + D / 4
+  float wta[16];    // W^T row 16 w + i (a feature), tokens 16 g .. + 15 (waves w < D / 16)
+  float ya[4];      // Y rows 16 w + 4 g + r, column 16 s + i (waves w < D / 16)
+};
+
+template <typename TIn, int D>
+__device__ __forceinline__ void load_dstate_ops(DStateOps<TIn, D>& o, const float* ws, const TIn* k, size_t chunk,
+                                                int b, int h, int t0, int N, int H, int s) {
+  const int l = threadIdx.x & 63, i = l & 15, g = l >> 4, w = threadIdx.x >> 6;
+  const int t = t0 + 16 * w + i;
+  const TIn* kr = k + (((size_t)b * N + min(t, N - 1)) * H + h) * D + (D / 4) * g;
+#pragma unroll
+  for (int q = 0; q < D / 16; ++q) {
+    float x[4];
+    load4_f32(kr + 4 * q, x);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) o.ka[4 * q + e] = t < N ? x[e] : 0.f;
+  }
+  if (w < D / 16) {
+    const float* W = Ws<D>::W(const_cast<float*>(ws), chunk);
+    const float* Y = Ws<D>::Y(const_cast<float*>(ws), chunk);
+#pragma unroll
+    for (int m = 0; m < 16; ++m) o.wta[m] = W[(16 * g + m) * D + 16 * w + i];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) o.ya[r] = Y[(16 * w + 4 * g + r) * D + 16 * s + i];
+  }
+}
+
+// the state's gradient at every chunk's end (reverse chain) and at the start: G += Y - W^T (K G)
 template <typename TIn, int D>
 __global__ __launch_bounds__(256) void scan_bwd_dstate_kernel(const TIn* __restrict__ k,
                                                               const float* __restrict__ d_state,
                                                               float* __restrict__ d_state_in, float* __restrict__ ws,
                                                               int N, int H, int NC) {
-  constexpr int PD = D + 4, PS = 20, NS = D / 16;
-  __shared__ __align__(16) float sW[kC * PD], sK[kC * PD], sX[kC * PS], sG[D * PS];
+  constexpr int NS = D / 16;
+  __shared__ __align__(16) float sX[kC * kPS], sG[D * kPS];
   const int s = blockIdx.x % NS, bh = blockIdx.x / NS;
   const int b = bh / H, h = bh - b * H;
-  const int w = threadIdx.x >> 6;
+  const int w = threadIdx.x >> 6, l = threadIdx.x & 63, j = l & 15, g = l >> 4;
   for (int e = threadIdx.x; e < D * 16; e += blockDim.x)
-    sG[(e / 16) * PS + e % 16] = d_state != nullptr ? d_state[(size_t)bh * D * D + (e / 16) * D + 16 * s + e % 16] : 0.f;
-  for (int c = NC - 1; c >= 0; --c) {
-    const size_t chunk = (size_t)bh * NC + c;
-    __syncthreads();
-    float* gG = Ws<D>::dHs(ws, chunk);
-    for (int e = threadIdx.x; e < D * 16; e += blockDim.x) gG[(e / 16) * D + 16 * s + e % 16] = sG[(e / 16) * PS + e % 16];
-    load_mat<D>(sW, PD, Ws<D>::W(ws, chunk), kC);
-    load_rows<TIn, D>(sK, PD, k, b, h, c * kC, N, H);
-    __syncthreads();
-    // X = K G (rows 16 w)
-    {
-      const f32x4 acc = mm16<false, false>(sK + 16 * w * PD, PD, sG, PS, D, zero4());
-#pragma unroll
-      for (int r = 0; r < 4; ++r) sX[(16 * w + tile_row(r)) * PS + tile_col()] = acc[r];
-    }
-    __syncthreads();
-    // G += Y - W^T X (rows 16 w of G)
-    if (w < D / 16) {
-      const float* gY = Ws<D>::Y(ws, chunk);
-      const f32x4 acc = mm16<true, false>(sW + 16 * w, PD, sX, PS, kC, zero4());
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int i = 16 * w + tile_row(r), j = tile_col();
-        sG[i * PS + j] += gY[i * D + 16 * s + j] - acc[r];
-      }
-    }
-  }
+    sG[(e / 16) * kPS + e % 16] = d_state != nullptr ? d_state[(size_t)bh * D * D + (e / 16) * D + 16 * s + e % 16] : 0.f;
+  DStateOps<TIn, D> ops[2];
+  load_dstate_ops<TIn, D>(ops[0], ws, k, (size_t)bh * NC + NC - 1, b, h, (NC - 1) * kC, N, H, s);
   __syncthreads();
+  auto step = [&](int c, const DStateOps<TIn, D>& cur, DStateOps<TIn, D>& nxt) {
+    const size_t chunk = (size_t)bh * NC + c;
+    if (c > 0) load_dstate_ops<TIn, D>(nxt, ws, k, chunk - 1, b, h, (c - 1) * kC, N, H, s);
+    float* gG = Ws<D>::dHs(ws, chunk);
+    for (int e = threadIdx.x; e < D * 16; e += blockDim.x) gG[(e / 16) * D + 16 * s + e % 16] = sG[(e / 16) * kPS + e % 16];
+    const f32x4 x = mm_reg<D / 4>(cur.ka, sG, zero4());
+#pragma unroll
+    for (int r = 0; r < 4; ++r) sX[(16 * w + 4 * g + r) * kPS + j] = x[r];
+    __syncthreads();  // X complete; the reads of G are done
+    if (w < D / 16) {
+      const f32x4 wx = mm_reg<16>(cur.wta, sX, zero4());
+#pragma unroll
+      for (int r = 0; r < 4; ++r) sG[(16 * w + 4 * g + r) * kPS + j] += cur.ya[r] - wx[r];
+    }
+    __syncthreads();
+  };
+  for (int i = 0; i < NC; i += 2) {
+    const int c = NC - 1 - i;
+    step(c, ops[0], ops[1]);
+    if (c > 0) step(c - 1, ops[1], ops[0]);
+  }
   for (int e = threadIdx.x; e < D * 16; e += blockDim.x)
-    d_state_in[(size_t)bh * D * D + (e / 16) * D + 16 * s + e % 16] = sG[(e / 16) * PS + e % 16];
+    d_state_in[(size_t)bh * D * D + (e / 16) * D + 16 * s + e % 16] = sG[(e / 16) * kPS + e % 16];
 }
 
 template <typename TIn, int D>
