@@ -162,6 +162,14 @@ template <int N>
 __device__ __forceinline__ float group_sum(float x) {
   return group_reduce<N>(x, SumOp{});
 }
+// Each lane gets the sum of x over the four lanes of the wave with its index within a 16-lane row
+// (l, l ^ 16, l ^ 32, l ^ 48): a column sum of an MFMA result tile, whose rows sit in lane groups.
+__device__ __forceinline__ float sum_over_rows(float x) {
+  const auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = __uint_as_float(p[0]) + __uint_as_float(p[1]);
+  const auto q = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(q[0]) + __uint_as_float(q[1]);
+}
 template <int N>
 __device__ __forceinline__ float group_max(float x) {
   return group_reduce<N>(x, MaxOp{});

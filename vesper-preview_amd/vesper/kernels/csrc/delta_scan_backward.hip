@@ -77,10 +77,14 @@ __device__ __forceinline__ void wave_sync_lds() {
 __device__ __forceinline__ int tile_row(int r) { return 4 * ((threadIdx.x & 63) >> 4) + r; }
 __device__ __forceinline__ int tile_col() { return threadIdx.x & 15; }
 
-// chunk rows t0 .. t0 + 63 of a [B, N, H, D] tensor (head h of batch row b) into LDS [64][ld] as
-// fp32; rows past N are zero, and with `active` so are inactive tokens' rows
-// Loads are unconditional (rows past N re-read row N - 1) and the zeros are selected afterwards, so
-// no load sits behind a per-lane branch (which would make each wait for every earlier one).
+// Staging into LDS is split in two: fetch() issues a workgroup's global loads into registers,
+// put() converts and writes them to LDS. A kernel fetches every operand before it puts the first,
+// so all its loads are in flight together: with one workgroup per CU nothing else hides a load's
+// latency. Loads are unconditional (rows past N re-read row N - 1, selected to zero in put()), so
+// none sits behind a per-lane branch, which would make it wait for every earlier load. The kernels
+// run 256 threads a workgroup.
+constexpr int kThreads = 256;
+
 template <typename TIn>
 __device__ __forceinline__ void load4_f32(const TIn* p, float (&x)[4]) {
   if constexpr (sizeof(TIn) == 2) {
@@ -95,39 +99,71 @@ __device__ __forceinline__ void load4_f32(const TIn* p, float (&x)[4]) {
   }
 }
 
+// chunk rows t0 .. t0 + 63 of a [B, N, H, D] tensor (head h of batch row b) into LDS [64][ld] as
+// fp32; rows past N are zero, and with `active` so are inactive tokens' rows
 template <typename TIn, int D>
-__device__ __forceinline__ void load_rows(float* dst, int ld, const TIn* src, int b, int h, int t0, int N, int H,
-                                          const uint8_t* active = nullptr) {
-  for (int e = threadIdx.x; e < kC * D / 4; e += blockDim.x) {
-    const int row = e / (D / 4), c = 4 * (e - row * (D / 4));
-    const int t = t0 + row, tc = min(t, N - 1);
-    const bool ok = t < N && (active == nullptr || active[(size_t)b * N + tc] != 0);
-    float x[4];
-    load4_f32(src + (((size_t)b * N + tc) * H + h) * D + c, x);
+struct ChunkRows {
+  typedef TIn V4 __attribute__((ext_vector_type(4)));
+  static constexpr int kIt = kC * D / 4 / kThreads;
+  V4 raw[kIt];
+  uint8_t act[kIt];  // the token's flag; without `active` a byte of src, not looked at
+  bool masked;
+  __device__ __forceinline__ void fetch(const TIn* src, int b, int h, int t0, int N, int H,
+                                        const uint8_t* active = nullptr) {
+    masked = active != nullptr;
+    const uint8_t* flags = masked ? active + (size_t)b * N : reinterpret_cast<const uint8_t*>(src);
 #pragma unroll
-    for (int j = 0; j < 4; ++j) dst[row * ld + c + j] = ok ? x[j] : 0.f;
+    for (int it = 0; it < kIt; ++it) {
+      const int e = threadIdx.x + kThreads * it, row = e / (D / 4), c = 4 * (e % (D / 4));
+      const int tc = min(t0 + row, N - 1);
+      raw[it] = *reinterpret_cast<const V4*>(src + (((size_t)b * N + tc) * H + h) * D + c);
+      act[it] = flags[masked ? tc : 0];
+    }
   }
-}
+  __device__ __forceinline__ void put(float* dst, int ld, int t0, int N) const {
+#pragma unroll
+    for (int it = 0; it < kIt; ++it) {
+      const int e = threadIdx.x + kThreads * it, row = e / (D / 4), c = 4 * (e % (D / 4));
+      const bool ok = t0 + row < N && (!masked || act[it] != 0);
+      f32x4 x;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) x[j] = ok ? to_f32(raw[it][j]) : 0.f;
+      *reinterpret_cast<f32x4*>(dst + row * ld + c) = x;
+    }
+  }
+};
 
+// beta of the chunk's tokens (zero past N) into LDS [64]
 template <typename TIn>
-__device__ __forceinline__ void load_beta(float* dst, const TIn* beta, int b, int h, int t0, int N, int H) {
-  for (int r = threadIdx.x; r < kC; r += blockDim.x) {
-    const int t = t0 + r;
-    const float x = to_f32(beta[((size_t)b * N + min(t, N - 1)) * H + h]);
-    dst[r] = t < N ? x : 0.f;
+struct ChunkBeta {
+  TIn raw;
+  __device__ __forceinline__ void fetch(const TIn* beta, int b, int h, int t0, int N, int H) {
+    raw = beta[((size_t)b * N + min(t0 + (int)(threadIdx.x & (kC - 1)), N - 1)) * H + h];
   }
-}
+  __device__ __forceinline__ void put(float* dst, int t0, int N) const {
+    const int r = threadIdx.x;
+    if (r < kC) dst[r] = t0 + r < N ? to_f32(raw) : 0.f;
+  }
+};
 
-// a [rows][D] fp32 global matrix (row pitch D) into LDS [rows][ld]
-template <int D>
-__device__ __forceinline__ void load_mat(float* dst, int ld, const float* src, int rows) {
-  for (int e = threadIdx.x; e < rows * D / 4; e += blockDim.x) {
-    const int row = e / (D / 4), c = 4 * (e - row * (D / 4));
-    const f32x4 v = *reinterpret_cast<const f32x4*>(src + (size_t)row * D + c);
+// a [R][D] fp32 global matrix (row pitch D) into LDS [R][ld]
+template <int R, int D>
+struct MatRows {
+  static constexpr int kN = R * D / 4, kIt = (kN + kThreads - 1) / kThreads;
+  f32x4 raw[kIt];
+  __device__ __forceinline__ void fetch(const float* src) {
 #pragma unroll
-    for (int j = 0; j < 4; ++j) dst[row * ld + c + j] = v[j];
+    for (int it = 0; it < kIt; ++it)
+      raw[it] = *reinterpret_cast<const f32x4*>(src + 4 * min((int)threadIdx.x + kThreads * it, kN - 1));
   }
-}
+  __device__ __forceinline__ void put(float* dst, int ld) const {
+#pragma unroll
+    for (int it = 0; it < kIt; ++it) {
+      const int e = threadIdx.x + kThreads * it;
+      if (kN % kThreads == 0 || e < kN) *reinterpret_cast<f32x4*>(dst + (4 * e / D) * ld + 4 * e % D) = raw[it];
+    }
+  }
+};
 
 // workspace layout, per (b, h, chunk): L [64][64], W [64][D], U [64][D], Y [D][D], Hs [D][D], dHs [D][D]
 template <int D> struct Ws {
@@ -158,11 +194,20 @@ __global__ __launch_bounds__(256) void scan_bwd_prep_kernel(const TIn* __restric
   const int t0 = c * kC;
   const size_t chunk = blockIdx.x;
   const int w = threadIdx.x >> 6;
-  load_rows<TIn, D>(sK, PD, k, b, h, t0, N, H);
-  load_rows<TIn, D>(sQ, PD, q, b, h, t0, N, H);
-  load_rows<TIn, D>(sO, PD, d_o, b, h, t0, N, H, active);
-  load_rows<TIn, D>(sV, PD, v, b, h, t0, N, H);
-  load_beta(sB, beta, b, h, t0, N, H);
+  {
+    ChunkRows<TIn, D> rk, rq, ro, rv;
+    ChunkBeta<TIn> rb;
+    rk.fetch(k, b, h, t0, N, H);
+    rq.fetch(q, b, h, t0, N, H);
+    ro.fetch(d_o, b, h, t0, N, H, active);
+    rv.fetch(v, b, h, t0, N, H);
+    rb.fetch(beta, b, h, t0, N, H);
+    rk.put(sK, PD, t0, N);
+    rq.put(sQ, PD, t0, N);
+    ro.put(sO, PD, t0, N);
+    rv.put(sV, PD, t0, N);
+    rb.put(sB, t0, N);
+  }
   __syncthreads();
   // A = tril(diag(beta) K K^T, -1)
   for (int ct = 0; ct < 4; ++ct) {
@@ -177,9 +222,10 @@ __global__ __launch_bounds__(256) void scan_bwd_prep_kernel(const TIn* __restric
   // L = (I + A)^-1 by 16x16 blocks: the diagonal blocks (I + A_bb)^-1 by forward substitution (a
   // lane per column of a block), then L_ij = -L_ii sum_{m = j}^{i - 1} A_im L_mj level by level
   // (i - j = 1, 2, 3) on MFMA; the blocks above the diagonal are zero
-  for (int e = threadIdx.x; e < kC * kC; e += blockDim.x) {
-    const int i = e / kC, j = e - i * kC;
-    if (i / 16 < j / 16) sL[i * kPC + j] = 0.f;
+#pragma unroll
+  for (int e = threadIdx.x; e < kC * kC / 4; e += kThreads) {  // four zeros a thread and step
+    const int i = e / (kC / 4), j = 4 * (e % (kC / 4));
+    if (i / 16 < j / 16) *reinterpret_cast<f32x4*>(sL + i * kPC + j) = zero4();
   }
   if (w == 0) {
     const int l = threadIdx.x & 63, blk = l >> 4, col = l & 15;
@@ -216,7 +262,9 @@ __global__ __launch_bounds__(256) void scan_bwd_prep_kernel(const TIn* __restric
     __syncthreads();
   }
   float* gL = Ws<D>::L(ws, chunk);
-  for (int e = threadIdx.x; e < kC * kC; e += blockDim.x) gL[e] = sL[(e / kC) * kPC + (e % kC)];
+#pragma unroll
+  for (int e = threadIdx.x; e < kC * kC / 4; e += kThreads)
+    *reinterpret_cast<f32x4*>(gL + 4 * e) = *reinterpret_cast<const f32x4*>(sL + (e / (kC / 4)) * kPC + 4 * (e % (kC / 4)));
   // W = L diag(beta) K and U = L diag(beta) V (rows 16 w of the wave)
   float* gW = Ws<D>::W(ws, chunk);
   float* gU = Ws<D>::U(ws, chunk);
@@ -276,11 +324,13 @@ __device__ __forceinline__ f32x4 mm_reg(const float (&a)[KM], const float* Y, f3
   return acc;
 }
 
+// The operands hold what was loaded, unconverted: a conversion (or a select) at the load would make
+// the wave wait for the load there, a chunk early.
 template <typename TIn, int D>
 struct StateOps {
   float wa[D / 4];  // W row 16 w + i, columns (D / 4) g .. + D / 4
   float ua[4];      // U rows 16 w + 4 g + r, column 16 s + i
-  float ka[16];     // K^T row 16 w + i (a feature), tokens 16 g .. + 15 (waves w < D / 16)
+  TIn kr[16];       // K^T row 16 min(w, D / 16 - 1) + i (a feature), tokens 16 g .. + 15
 };
 
 template <typename TIn, int D>
@@ -297,14 +347,9 @@ __device__ __forceinline__ void load_state_ops(StateOps<TIn, D>& o, const float*
   }
 #pragma unroll
   for (int r = 0; r < 4; ++r) o.ua[r] = U[(16 * w + 4 * g + r) * D + 16 * s + i];
-  if (w < D / 16) {
+  const int f = 16 * min(w, D / 16 - 1) + i;
 #pragma unroll
-    for (int m = 0; m < 16; ++m) {
-      const int t = t0 + 16 * g + m;
-      const float x = to_f32(k[(((size_t)b * N + min(t, N - 1)) * H + h) * D + 16 * w + i]);
-      o.ka[m] = t < N ? x : 0.f;
-    }
-  }
+  for (int m = 0; m < 16; ++m) o.kr[m] = k[(((size_t)b * N + min(t0 + 16 * g + m, N - 1)) * H + h) * D + f];
 }
 
 // the states at the chunk starts: Delta = U - W H, H += K^T Delta
@@ -318,7 +363,7 @@ __global__ __launch_bounds__(256) void scan_bwd_states_kernel(const TIn* __restr
   const int b = bh / H, h = bh - b * H;
   const int w = threadIdx.x >> 6, l = threadIdx.x & 63, j = l & 15, g = l >> 4;
   const float* h0 = state_in + (size_t)bh * D * D;
-  for (int e = threadIdx.x; e < D * 16; e += blockDim.x) sH[(e / 16) * kPS + e % 16] = h0[(e / 16) * D + 16 * s + e % 16];
+  for (int e = threadIdx.x; e < D * 16; e += kThreads) sH[(e / 16) * kPS + e % 16] = h0[(e / 16) * D + 16 * s + e % 16];
   StateOps<TIn, D> ops[2];
   load_state_ops<TIn, D>(ops[0], ws, k, (size_t)bh * NC, b, h, 0, N, H, s);
   __syncthreads();
@@ -326,13 +371,17 @@ __global__ __launch_bounds__(256) void scan_bwd_states_kernel(const TIn* __restr
     const size_t chunk = (size_t)bh * NC + c;
     if (c + 1 < NC) load_state_ops<TIn, D>(nxt, ws, k, chunk + 1, b, h, (c + 1) * kC, N, H, s);
     float* gH = Ws<D>::Hs(ws, chunk);
-    for (int e = threadIdx.x; e < D * 16; e += blockDim.x) gH[(e / 16) * D + 16 * s + e % 16] = sH[(e / 16) * kPS + e % 16];
+#pragma unroll
+    for (int e = threadIdx.x; e < D * 16; e += kThreads) gH[(e / 16) * D + 16 * s + e % 16] = sH[(e / 16) * kPS + e % 16];
     const f32x4 acc = mm_reg<D / 4>(cur.wa, sH, zero4());
 #pragma unroll
     for (int r = 0; r < 4; ++r) sD[(16 * w + 4 * g + r) * kPS + j] = cur.ua[r] - acc[r];
     __syncthreads();  // Delta complete; the reads of H are done
     if (w < D / 16) {
-      const f32x4 dh = mm_reg<16>(cur.ka, sD, zero4());
+      float ka[16];  // tokens past N contribute nothing
+#pragma unroll
+      for (int m = 0; m < 16; ++m) ka[m] = c * kC + 16 * g + m < N ? to_f32(cur.kr[m]) : 0.f;
+      const f32x4 dh = mm_reg<16>(ka, sD, zero4());
 #pragma unroll
       for (int r = 0; r < 4; ++r) sH[(16 * w + 4 * g + r) * kPS + j] += dh[r];
     }
@@ -346,32 +395,26 @@ __global__ __launch_bounds__(256) void scan_bwd_states_kernel(const TIn* __restr
 
 template <typename TIn, int D>
 struct DStateOps {
-  float ka[D / 4];  // K row 16 w + i (a token), features (D / 4) g .. + D / 4
-  float wta[16];    // W^T row 16 w + i (a feature), tokens 16 g .. + 15 (waves w < D / 16)
-  float ya[4];      // Y rows 16 w + 4 g + r, column 16 s + i (waves w < D / 16)
+  typedef TIn V4 __attribute__((ext_vector_type(4)));
+  V4 kr[D / 16];    // K row 16 w + i (a token), features (D / 4) g .. + D / 4
+  float wta[16];    // W^T row 16 w' + i (a feature), tokens 16 g .. + 15; w' = min(w, D / 16 - 1)
+  float ya[4];      // Y rows 16 w' + 4 g + r, column 16 s + i
 };
 
 template <typename TIn, int D>
 __device__ __forceinline__ void load_dstate_ops(DStateOps<TIn, D>& o, const float* ws, const TIn* k, size_t chunk,
                                                 int b, int h, int t0, int N, int H, int s) {
   const int l = threadIdx.x & 63, i = l & 15, g = l >> 4, w = threadIdx.x >> 6;
-  const int t = t0 + 16 * w + i;
-  const TIn* kr = k + (((size_t)b * N + min(t, N - 1)) * H + h) * D + (D / 4) * g;
+  const TIn* kr = k + (((size_t)b * N + min(t0 + 16 * w + i, N - 1)) * H + h) * D + (D / 4) * g;
 #pragma unroll
-  for (int q = 0; q < D / 16; ++q) {
-    float x[4];
-    load4_f32(kr + 4 * q, x);
+  for (int q = 0; q < D / 16; ++q) o.kr[q] = *reinterpret_cast<const typename DStateOps<TIn, D>::V4*>(kr + 4 * q);
+  const int wf = min(w, D / 16 - 1);
+  const float* W = Ws<D>::W(const_cast<float*>(ws), chunk);
+  const float* Y = Ws<D>::Y(const_cast<float*>(ws), chunk);
 #pragma unroll
-    for (int e = 0; e < 4; ++e) o.ka[4 * q + e] = t < N ? x[e] : 0.f;
-  }
-  if (w < D / 16) {
-    const float* W = Ws<D>::W(const_cast<float*>(ws), chunk);
-    const float* Y = Ws<D>::Y(const_cast<float*>(ws), chunk);
+  for (int m = 0; m < 16; ++m) o.wta[m] = W[(16 * g + m) * D + 16 * wf + i];
 #pragma unroll
-    for (int m = 0; m < 16; ++m) o.wta[m] = W[(16 * g + m) * D + 16 * w + i];
-#pragma unroll
-    for (int r = 0; r < 4; ++r) o.ya[r] = Y[(16 * w + 4 * g + r) * D + 16 * s + i];
-  }
+  for (int r = 0; r < 4; ++r) o.ya[r] = Y[(16 * wf + 4 * g + r) * D + 16 * s + i];
 }
 
 // the state's gradient at every chunk's end (reverse chain) and at the start: G += Y - W^T (K G)
@@ -385,7 +428,7 @@ __global__ __launch_bounds__(256) void scan_bwd_dstate_kernel(const TIn* __restr
   const int s = blockIdx.x % NS, bh = blockIdx.x / NS;
   const int b = bh / H, h = bh - b * H;
   const int w = threadIdx.x >> 6, l = threadIdx.x & 63, j = l & 15, g = l >> 4;
-  for (int e = threadIdx.x; e < D * 16; e += blockDim.x)
+  for (int e = threadIdx.x; e < D * 16; e += kThreads)
     sG[(e / 16) * kPS + e % 16] = d_state != nullptr ? d_state[(size_t)bh * D * D + (e / 16) * D + 16 * s + e % 16] : 0.f;
   DStateOps<TIn, D> ops[2];
   load_dstate_ops<TIn, D>(ops[0], ws, k, (size_t)bh * NC + NC - 1, b, h, (NC - 1) * kC, N, H, s);
@@ -394,8 +437,15 @@ __global__ __launch_bounds__(256) void scan_bwd_dstate_kernel(const TIn* __restr
     const size_t chunk = (size_t)bh * NC + c;
     if (c > 0) load_dstate_ops<TIn, D>(nxt, ws, k, chunk - 1, b, h, (c - 1) * kC, N, H, s);
     float* gG = Ws<D>::dHs(ws, chunk);
-    for (int e = threadIdx.x; e < D * 16; e += blockDim.x) gG[(e / 16) * D + 16 * s + e % 16] = sG[(e / 16) * kPS + e % 16];
-    const f32x4 x = mm_reg<D / 4>(cur.ka, sG, zero4());
+#pragma unroll
+    for (int e = threadIdx.x; e < D * 16; e += kThreads) gG[(e / 16) * D + 16 * s + e % 16] = sG[(e / 16) * kPS + e % 16];
+    float ka[D / 4];  // tokens past N contribute nothing
+    const bool live = c * kC + 16 * w + (threadIdx.x & 15) < N;
+#pragma unroll
+    for (int q = 0; q < D / 16; ++q)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) ka[4 * q + e] = live ? to_f32(cur.kr[q][e]) : 0.f;
+    const f32x4 x = mm_reg<D / 4>(ka, sG, zero4());
 #pragma unroll
     for (int r = 0; r < 4; ++r) sX[(16 * w + 4 * g + r) * kPS + j] = x[r];
     __syncthreads();  // X complete; the reads of G are done
@@ -411,7 +461,7 @@ __global__ __launch_bounds__(256) void scan_bwd_dstate_kernel(const TIn* __restr
     step(c, ops[0], ops[1]);
     if (c > 0) step(c - 1, ops[1], ops[0]);
   }
-  for (int e = threadIdx.x; e < D * 16; e += blockDim.x)
+  for (int e = threadIdx.x; e < D * 16; e += kThreads)
     d_state_in[(size_t)bh * D * D + (e / 16) * D + 16 * s + e % 16] = sG[(e / 16) * kPS + e % 16];
 }
 
@@ -423,7 +473,7 @@ __global__ __launch_bounds__(256) void scan_bwd_chunk_kernel(
   constexpr int P = kPC;  // every buffer is [64][68]
   constexpr int NT = D / 16;
   __shared__ __align__(16) float buf[9][kC * P];
-  __shared__ float sB[kC], sDB[kC];
+  __shared__ float sB[kC], sDB[kC], sPart[4 * kC];
   const int c = blockIdx.x % NC, bh = blockIdx.x / NC;
   const int b = bh / H, h = bh - b * H;
   const int t0 = c * kC;
@@ -431,14 +481,28 @@ __global__ __launch_bounds__(256) void scan_bwd_chunk_kernel(
   const int w = threadIdx.x >> 6;
   float *Bq = buf[0], *Bk = buf[1], *Bo = buf[2], *Br = buf[3], *Bh = buf[4], *Bg = buf[5], *Bl = buf[6];
   float *Bd = buf[7], *Bp = buf[8];
-  load_rows<TIn, D>(Bq, P, q, b, h, t0, N, H);
-  load_rows<TIn, D>(Bk, P, k, b, h, t0, N, H);
-  load_rows<TIn, D>(Bo, P, d_o, b, h, t0, N, H, active);
-  load_rows<TIn, D>(Br, P, v, b, h, t0, N, H);
-  load_mat<D>(Bh, P, Ws<D>::Hs(const_cast<float*>(ws), chunk), D);
-  load_mat<D>(Bg, P, Ws<D>::dHs(const_cast<float*>(ws), chunk), D);
-  load_mat<kC>(Bl, P, Ws<D>::L(const_cast<float*>(ws), chunk), kC);
-  load_beta(sB, beta, b, h, t0, N, H);
+  {
+    ChunkRows<TIn, D> rq, rk, ro, rv;
+    MatRows<D, D> mh, mg;
+    MatRows<kC, kC> ml;
+    ChunkBeta<TIn> rb;
+    rq.fetch(q, b, h, t0, N, H);
+    rk.fetch(k, b, h, t0, N, H);
+    ro.fetch(d_o, b, h, t0, N, H, active);
+    rv.fetch(v, b, h, t0, N, H);
+    mh.fetch(Ws<D>::Hs(const_cast<float*>(ws), chunk));
+    mg.fetch(Ws<D>::dHs(const_cast<float*>(ws), chunk));
+    ml.fetch(Ws<D>::L(const_cast<float*>(ws), chunk));
+    rb.fetch(beta, b, h, t0, N, H);
+    rq.put(Bq, P, t0, N);
+    rk.put(Bk, P, t0, N);
+    ro.put(Bo, P, t0, N);
+    rv.put(Br, P, t0, N);
+    mh.put(Bh, P);
+    mg.put(Bg, P);
+    ml.put(Bl, P);
+    rb.put(sB, t0, N);
+  }
   __syncthreads();
   const int r0 = 16 * w;  // this wave's 16 rows of every [64 x .] result
   // R = V - K H, in place (each tile reads only its own V entries)
@@ -522,24 +586,21 @@ __global__ __launch_bounds__(256) void scan_bwd_chunk_kernel(
     dka[ct] = mm16<true, false>(Bs + r0, P, Bq + 16 * ct, P, kC, dka[ct]);
   }
   __syncthreads();  // H, dO, Q, S2, Delta are done with
-  // dT = dDelta R^T into H's buffer
+  // dT = dDelta R^T. dbeta_j gets sum_i dT_ij L_ij (L is zero above its diagonal): each wave sums
+  // its 16 rows of the column into sPart; dL = tril(dT) diag(beta) goes into H's buffer
   float* Bt = Bh;
   for (int ct = 0; ct < 4; ++ct) {
     const f32x4 acc = mm16<false, true>(Bdd + r0 * P, P, Br + 16 * ct * P, P, D, zero4());
+    const int j = 16 * ct + tile_col();
+    float part = 0.f;
 #pragma unroll
-    for (int r = 0; r < 4; ++r) Bt[(r0 + tile_row(r)) * P + 16 * ct + tile_col()] = acc[r];
-  }
-  __syncthreads();
-  // dbeta from T: sum_i dT_ij L_ij (column j, rows i >= j); then dL = tril(dT diag(beta)) in place
-  for (int j = threadIdx.x; j < kC; j += blockDim.x) {
-    float s = 0.f;
-    for (int i = j; i < kC; ++i) s += Bt[i * P + j] * Bl[i * P + j];
-    sDB[j] = s;
-  }
-  __syncthreads();
-  for (int e = threadIdx.x; e < kC * kC; e += blockDim.x) {
-    const int i = e / kC, j = e - i * kC;
-    Bt[i * P + j] = j <= i ? Bt[i * P + j] * sB[j] : 0.f;
+    for (int r = 0; r < 4; ++r) {
+      const int i = r0 + tile_row(r);
+      part += acc[r] * Bl[i * P + j];
+      Bt[i * P + j] = j <= i ? acc[r] * sB[j] : 0.f;
+    }
+    part = sum_over_rows(part);
+    if ((threadIdx.x & 63) < 16) sPart[w * kC + j] = part;
   }
   __syncthreads();
   // X1 = L^T dL into Q's buffer
@@ -550,30 +611,26 @@ __global__ __launch_bounds__(256) void scan_bwd_chunk_kernel(
     for (int r = 0; r < 4; ++r) Bx[(r0 + tile_row(r)) * P + 16 * ct + tile_col()] = acc[r];
   }
   __syncthreads();
-  // dA = -tril(X1 L^T, -1) into dO's buffer; G2 = K K^T into Delta's buffer
+  // dA = -tril(X1 L^T, -1); dbeta_i gets sum_{m < i} dA_im (k_i . k_m) (a row of the wave's own);
+  // M = diag(beta) dA goes into dO's buffer
   float* Ba = Bo;
-  float* Bk2 = Bd;
+  float rows[4] = {0.f, 0.f, 0.f, 0.f};
   for (int ct = 0; ct < 4; ++ct) {
     const f32x4 acc = mm16<false, true>(Bx + r0 * P, P, Bl + 16 * ct * P, P, kC, zero4());
     const f32x4 gk = mm16<false, true>(Bk + r0 * P, P, Bk + 16 * ct * P, P, D, zero4());
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int i = r0 + tile_row(r), j = 16 * ct + tile_col();
-      Ba[i * P + j] = j < i ? -acc[r] : 0.f;
-      Bk2[i * P + j] = gk[r];
+      const float da = j < i ? -acc[r] : 0.f;
+      rows[r] += da * gk[r];
+      Ba[i * P + j] = da * sB[i];
     }
   }
-  __syncthreads();
-  // dbeta from A: sum_{m < i} dA_im (k_i . k_m); then M = diag(beta) dA in place
-  for (int i = threadIdx.x; i < kC; i += blockDim.x) {
-    float s = 0.f;
-    for (int m = 0; m < i; ++m) s += Ba[i * P + m] * Bk2[i * P + m];
-    sDB[i] += s;
-  }
-  __syncthreads();
-  for (int e = threadIdx.x; e < kC * kC; e += blockDim.x) {
-    const int i = e / kC, j = e - i * kC;
-    Ba[i * P + j] *= sB[i];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const float x = group_sum<16>(rows[r]);
+    const int i = r0 + tile_row(r);
+    if (tile_col() == 0) sDB[i] = ((sPart[i] + sPart[kC + i]) + (sPart[2 * kC + i] + sPart[3 * kC + i])) + x;
   }
   __syncthreads();
   // dK += M K + M^T K, then store
@@ -586,7 +643,7 @@ __global__ __launch_bounds__(256) void scan_bwd_chunk_kernel(
       if (t0 + i < N) dk[(((size_t)b * N + t0 + i) * H + h) * D + j] = from_f32<TIn>(dka[ct][r]);
     }
   }
-  for (int i = threadIdx.x; i < kC; i += blockDim.x)
+  for (int i = threadIdx.x; i < kC; i += kThreads)
     if (t0 + i < N) dbeta[((size_t)b * N + t0 + i) * H + h] = from_f32<TIn>(sDB[i]);
 }
 
