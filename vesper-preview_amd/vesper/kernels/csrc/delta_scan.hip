@@ -401,23 +401,29 @@ __global__ __launch_bounds__(256, 3) void delta_prep_kernel(const TIn* __restric
   const int b = bh / H, h = bh - b * H;
   const int t0 = c * kChunk, nv = min(kChunk, T - t0);
 
+  // Every load is unconditional (tokens past the end re-read the last one, padding features re-read
+  // feature 0) and the zeros are selected once all are issued: a load behind a per-lane branch
+  // would wait for every earlier one.
   typename N::R kn[4][N::NREG];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    const int tok = 16 * i + lq;
-    const TIn* row = k + (((size_t)b * T + t0 + tok) * H + h) * DK;
+    const TIn* row = k + (((size_t)b * T + min(t0 + 16 * i + lq, T - 1)) * H + h) * DK;
 #pragma unroll
     for (int sgi = 0; sgi < N::NREG; ++sgi) {
       const int f = N::feat(sgi);
-      if (tok < nv && f < DK) {
-        kn[i][sgi] = *reinterpret_cast<const typename N::R*>(row + f);
-      } else {
-#pragma unroll
-        for (int e = 0; e < N::PER; ++e) kn[i][sgi][e] = from_f32<E>(0.f);
-      }
+      kn[i][sgi] = *reinterpret_cast<const typename N::R*>(row + (f < DK ? f : 0));
     }
   }
-  const float bl = l < nv ? to_f32(beta[((size_t)b * T + t0 + l) * H + h]) : 0.f;
+  const TIn braw = beta[((size_t)b * T + min(t0 + l, T - 1)) * H + h];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int sgi = 0; sgi < N::NREG; ++sgi) {
+      const bool ok = 16 * i + lq < nv && N::feat(sgi) < DK;
+#pragma unroll
+      for (int e = 0; e < N::PER; ++e) kn[i][sgi][e] = ok ? kn[i][sgi][e] : from_f32<E>(0.f);
+    }
+  const float bl = l < nv ? to_f32(braw) : 0.f;
   E* tc = reinterpret_cast<E*>(&sScr[w][0]);  // compact tiles: tile t = i (i + 1) / 2 + j, row-major
   ut_solve<E, DKP>(kn, bl, &sScr[w][0],
                    [&](int ti, int tj, int r, int cc) { return tc + tile_of(ti, tj) * kTileElems + r * 16 + cc; });

@@ -101,10 +101,10 @@ __device__ __forceinline__ void load4_f32(const TIn* p, float (&x)[4]) {
 
 // chunk rows t0 .. t0 + 63 of a [B, N, H, D] tensor (head h of batch row b) into LDS [64][ld] as
 // fp32; rows past N are zero, and with `active` so are inactive tokens' rows
-template <typename TIn, int D>
+template <typename TIn, int D, int NTH = kThreads>
 struct ChunkRows {
   typedef TIn V4 __attribute__((ext_vector_type(4)));
-  static constexpr int kIt = kC * D / 4 / kThreads;
+  static constexpr int kN = kC * D / 4, kIt = (kN + NTH - 1) / NTH;
   V4 raw[kIt];
   uint8_t act[kIt];  // the token's flag; without `active` a byte of src, not looked at
   bool masked;
@@ -114,7 +114,7 @@ struct ChunkRows {
     const uint8_t* flags = masked ? active + (size_t)b * N : reinterpret_cast<const uint8_t*>(src);
 #pragma unroll
     for (int it = 0; it < kIt; ++it) {
-      const int e = threadIdx.x + kThreads * it, row = e / (D / 4), c = 4 * (e % (D / 4));
+      const int e = min((int)threadIdx.x + NTH * it, kN - 1), row = e / (D / 4), c = 4 * (e % (D / 4));
       const int tc = min(t0 + row, N - 1);
       raw[it] = *reinterpret_cast<const V4*>(src + (((size_t)b * N + tc) * H + h) * D + c);
       act[it] = flags[masked ? tc : 0];
@@ -123,12 +123,12 @@ struct ChunkRows {
   __device__ __forceinline__ void put(float* dst, int ld, int t0, int N) const {
 #pragma unroll
     for (int it = 0; it < kIt; ++it) {
-      const int e = threadIdx.x + kThreads * it, row = e / (D / 4), c = 4 * (e % (D / 4));
+      const int e = threadIdx.x + NTH * it, row = e / (D / 4), c = 4 * (e % (D / 4));
       const bool ok = t0 + row < N && (!masked || act[it] != 0);
       f32x4 x;
 #pragma unroll
       for (int j = 0; j < 4; ++j) x[j] = ok ? to_f32(raw[it][j]) : 0.f;
-      *reinterpret_cast<f32x4*>(dst + row * ld + c) = x;
+      if (kN % NTH == 0 || e < kN) *reinterpret_cast<f32x4*>(dst + row * ld + c) = x;
     }
   }
 };
@@ -147,20 +147,20 @@ struct ChunkBeta {
 };
 
 // a [R][D] fp32 global matrix (row pitch D) into LDS [R][ld]
-template <int R, int D>
+template <int R, int D, int NTH = kThreads>
 struct MatRows {
-  static constexpr int kN = R * D / 4, kIt = (kN + kThreads - 1) / kThreads;
+  static constexpr int kN = R * D / 4, kIt = (kN + NTH - 1) / NTH;
   f32x4 raw[kIt];
   __device__ __forceinline__ void fetch(const float* src) {
 #pragma unroll
     for (int it = 0; it < kIt; ++it)
-      raw[it] = *reinterpret_cast<const f32x4*>(src + 4 * min((int)threadIdx.x + kThreads * it, kN - 1));
+      raw[it] = *reinterpret_cast<const f32x4*>(src + 4 * min((int)threadIdx.x + NTH * it, kN - 1));
   }
   __device__ __forceinline__ void put(float* dst, int ld) const {
 #pragma unroll
     for (int it = 0; it < kIt; ++it) {
-      const int e = threadIdx.x + kThreads * it;
-      if (kN % kThreads == 0 || e < kN) *reinterpret_cast<f32x4*>(dst + (4 * e / D) * ld + 4 * e % D) = raw[it];
+      const int e = threadIdx.x + NTH * it;
+      if (kN % NTH == 0 || e < kN) *reinterpret_cast<f32x4*>(dst + (4 * e / D) * ld + 4 * e % D) = raw[it];
     }
   }
 };
@@ -465,27 +465,32 @@ __global__ __launch_bounds__(256) void scan_bwd_dstate_kernel(const TIn* __restr
     d_state_in[(size_t)bh * D * D + (e / 16) * D + 16 * s + e % 16] = sG[(e / 16) * kPS + e % 16];
 }
 
+// Eight waves: wave w owns row block 16 (w % 4) of every [64 x .] result and every other column
+// tile from w / 4, so two waves share each SIMD and hide each other's LDS and MFMA latency.
+constexpr int kChunkThreads = 512;
+
 template <typename TIn, int D>
-__global__ __launch_bounds__(256) void scan_bwd_chunk_kernel(
+__global__ __launch_bounds__(kChunkThreads) void scan_bwd_chunk_kernel(
     const TIn* __restrict__ q, const TIn* __restrict__ k, const TIn* __restrict__ v, const TIn* __restrict__ beta,
     const TIn* __restrict__ d_o, const uint8_t* __restrict__ active, const float* __restrict__ ws,
     TIn* __restrict__ dq, TIn* __restrict__ dk, TIn* __restrict__ dv, TIn* __restrict__ dbeta, int N, int H, int NC) {
   constexpr int P = kPC;  // every buffer is [64][68]
-  constexpr int NT = D / 16;
+  constexpr int NT = D / 16, NTW = (NT + 1) / 2;  // column tiles of a [64 x D] result; a wave's share
+  constexpr int NTH = kChunkThreads;
   __shared__ __align__(16) float buf[9][kC * P];
-  __shared__ float sB[kC], sDB[kC], sPart[4 * kC];
+  __shared__ float sB[kC], sPart[4 * kC], sRow[2 * kC];
   const int c = blockIdx.x % NC, bh = blockIdx.x / NC;
   const int b = bh / H, h = bh - b * H;
   const int t0 = c * kC;
   const size_t chunk = blockIdx.x;
-  const int w = threadIdx.x >> 6;
+  const int w = threadIdx.x >> 6, rb = w & 3, ch = w >> 2;
   float *Bq = buf[0], *Bk = buf[1], *Bo = buf[2], *Br = buf[3], *Bh = buf[4], *Bg = buf[5], *Bl = buf[6];
   float *Bd = buf[7], *Bp = buf[8];
   {
-    ChunkRows<TIn, D> rq, rk, ro, rv;
-    MatRows<D, D> mh, mg;
-    MatRows<kC, kC> ml;
-    ChunkBeta<TIn> rb;
+    ChunkRows<TIn, D, NTH> rq, rk, ro, rv;
+    MatRows<D, D, NTH> mh, mg;
+    MatRows<kC, kC, NTH> ml;
+    ChunkBeta<TIn> rb_;
     rq.fetch(q, b, h, t0, N, H);
     rk.fetch(k, b, h, t0, N, H);
     ro.fetch(d_o, b, h, t0, N, H, active);
@@ -493,7 +498,7 @@ __global__ __launch_bounds__(256) void scan_bwd_chunk_kernel(
     mh.fetch(Ws<D>::Hs(const_cast<float*>(ws), chunk));
     mg.fetch(Ws<D>::dHs(const_cast<float*>(ws), chunk));
     ml.fetch(Ws<D>::L(const_cast<float*>(ws), chunk));
-    rb.fetch(beta, b, h, t0, N, H);
+    rb_.fetch(beta, b, h, t0, N, H);
     rq.put(Bq, P, t0, N);
     rk.put(Bk, P, t0, N);
     ro.put(Bo, P, t0, N);
@@ -501,18 +506,18 @@ __global__ __launch_bounds__(256) void scan_bwd_chunk_kernel(
     mh.put(Bh, P);
     mg.put(Bg, P);
     ml.put(Bl, P);
-    rb.put(sB, t0, N);
+    rb_.put(sB, t0, N);
   }
   __syncthreads();
-  const int r0 = 16 * w;  // this wave's 16 rows of every [64 x .] result
+  const int r0 = 16 * rb;  // this wave's 16 rows of every [64 x .] result
   // R = V - K H, in place (each tile reads only its own V entries)
-  for (int ct = 0; ct < NT; ++ct) {
+  for (int ct = ch; ct < NT; ct += 2) {
     const f32x4 acc = mm16<false, false>(Bk + r0 * P, P, Bh + 16 * ct, P, D, zero4());
 #pragma unroll
     for (int r = 0; r < 4; ++r) Br[(r0 + tile_row(r)) * P + 16 * ct + tile_col()] -= acc[r];
   }
   // P = tril(Q K^T), diagonal included
-  for (int ct = 0; ct < 4; ++ct) {
+  for (int ct = ch; ct < 4; ct += 2) {
     const f32x4 acc = mm16<false, true>(Bq + r0 * P, P, Bk + 16 * ct * P, P, D, zero4());
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
@@ -522,30 +527,38 @@ __global__ __launch_bounds__(256) void scan_bwd_chunk_kernel(
   }
   __syncthreads();
   // Delta = L diag(beta) R
-  for (int ct = 0; ct < NT; ++ct) {
+  for (int ct = ch; ct < NT; ct += 2) {
     const f32x4 acc = mm16<false, false>(Bl + r0 * P, P, Br + 16 * ct, P, kC, zero4(), sB);
 #pragma unroll
     for (int r = 0; r < 4; ++r) Bd[(r0 + tile_row(r)) * P + 16 * ct + tile_col()] = acc[r];
   }
   __syncthreads();
-  // dK accumulates in registers: the wave's rows r0, every column tile
-  f32x4 dka[NT];
-  // dDelta = K G + P^T dO (registers), dK += Delta G^T
-  f32x4 ddl[NT];
-  for (int ct = 0; ct < NT; ++ct) {
-    ddl[ct] = mm16<false, false>(Bk + r0 * P, P, Bg + 16 * ct, P, D, zero4());
-    ddl[ct] = mm16<true, false>(Bp + r0, P, Bo + 16 * ct, P, kC, ddl[ct]);
-    dka[ct] = mm16<false, true>(Bd + r0 * P, P, Bg + 16 * ct * P, P, D, zero4());
+  // dK accumulates in registers: the wave's rows r0, its column tiles ch, ch + 2
+  f32x4 dka[NTW];
+  // dDelta = K G + P^T dO (registers), dK = Delta G^T
+  f32x4 ddl[NTW];
+#pragma unroll
+  for (int u = 0; u < NTW; ++u) {
+    const int ct = ch + 2 * u;
+    if (ct < NT) {
+      ddl[u] = mm16<false, false>(Bk + r0 * P, P, Bg + 16 * ct, P, D, zero4());
+      ddl[u] = mm16<true, false>(Bp + r0, P, Bo + 16 * ct, P, kC, ddl[u]);
+      dka[u] = mm16<false, true>(Bd + r0 * P, P, Bg + 16 * ct * P, P, D, zero4());
+    }
   }
   __syncthreads();  // the reads of G are done: dDelta goes into its buffer
   float* Bdd = Bg;
-  for (int ct = 0; ct < NT; ++ct)
 #pragma unroll
-    for (int r = 0; r < 4; ++r) Bdd[(r0 + tile_row(r)) * P + 16 * ct + tile_col()] = ddl[ct][r];
+  for (int u = 0; u < NTW; ++u) {
+    const int ct = ch + 2 * u;
+    if (ct < NT)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) Bdd[(r0 + tile_row(r)) * P + 16 * ct + tile_col()] = ddl[u][r];
+  }
   __syncthreads();
   // dR = diag(beta) L^T dDelta into P's buffer (free now); dV = dR
   float* Bdr = Bp;
-  for (int ct = 0; ct < NT; ++ct) {
+  for (int ct = ch; ct < NT; ct += 2) {
     const f32x4 acc = mm16<true, false>(Bl + r0, P, Bdd + 16 * ct, P, kC, zero4());
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
@@ -557,15 +570,19 @@ __global__ __launch_bounds__(256) void scan_bwd_chunk_kernel(
   }
   __syncthreads();
   // dK -= dR H^T
-  for (int ct = 0; ct < NT; ++ct) {
-    const f32x4 acc = mm16<false, true>(Bdr + r0 * P, P, Bh + 16 * ct * P, P, D, zero4());
 #pragma unroll
-    for (int r = 0; r < 4; ++r) dka[ct][r] -= acc[r];
+  for (int u = 0; u < NTW; ++u) {
+    const int ct = ch + 2 * u;
+    if (ct < NT) {
+      const f32x4 acc = mm16<false, true>(Bdr + r0 * P, P, Bh + 16 * ct * P, P, D, zero4());
+#pragma unroll
+      for (int r = 0; r < 4; ++r) dka[u][r] -= acc[r];
+    }
   }
   __syncthreads();  // the reads of dR are done
   // S2 = tril(dO Delta^T), diagonal included, into dR's buffer
   float* Bs = Bp;
-  for (int ct = 0; ct < 4; ++ct) {
+  for (int ct = ch; ct < 4; ct += 2) {
     const f32x4 acc = mm16<false, true>(Bo + r0 * P, P, Bd + 16 * ct * P, P, D, zero4());
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
@@ -575,21 +592,25 @@ __global__ __launch_bounds__(256) void scan_bwd_chunk_kernel(
   }
   __syncthreads();
   // dQ = dO H^T + S2 K; dK += S2^T Q
-  for (int ct = 0; ct < NT; ++ct) {
-    f32x4 acc = mm16<false, true>(Bo + r0 * P, P, Bh + 16 * ct * P, P, D, zero4());
-    acc = mm16<false, false>(Bs + r0 * P, P, Bk + 16 * ct, P, kC, acc);
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int i = r0 + tile_row(r), j = 16 * ct + tile_col();
-      if (t0 + i < N) dq[(((size_t)b * N + t0 + i) * H + h) * D + j] = from_f32<TIn>(acc[r]);
+  for (int u = 0; u < NTW; ++u) {
+    const int ct = ch + 2 * u;
+    if (ct < NT) {
+      f32x4 acc = mm16<false, true>(Bo + r0 * P, P, Bh + 16 * ct * P, P, D, zero4());
+      acc = mm16<false, false>(Bs + r0 * P, P, Bk + 16 * ct, P, kC, acc);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int i = r0 + tile_row(r), j = 16 * ct + tile_col();
+        if (t0 + i < N) dq[(((size_t)b * N + t0 + i) * H + h) * D + j] = from_f32<TIn>(acc[r]);
+      }
+      dka[u] = mm16<true, false>(Bs + r0, P, Bq + 16 * ct, P, kC, dka[u]);
     }
-    dka[ct] = mm16<true, false>(Bs + r0, P, Bq + 16 * ct, P, kC, dka[ct]);
   }
   __syncthreads();  // H, dO, Q, S2, Delta are done with
   // dT = dDelta R^T. dbeta_j gets sum_i dT_ij L_ij (L is zero above its diagonal): each wave sums
-  // its 16 rows of the column into sPart; dL = tril(dT) diag(beta) goes into H's buffer
+  // its 16 rows of its columns into sPart; dL = tril(dT) diag(beta) goes into H's buffer
   float* Bt = Bh;
-  for (int ct = 0; ct < 4; ++ct) {
+  for (int ct = ch; ct < 4; ct += 2) {
     const f32x4 acc = mm16<false, true>(Bdd + r0 * P, P, Br + 16 * ct * P, P, D, zero4());
     const int j = 16 * ct + tile_col();
     float part = 0.f;
@@ -600,22 +621,22 @@ __global__ __launch_bounds__(256) void scan_bwd_chunk_kernel(
       Bt[i * P + j] = j <= i ? acc[r] * sB[j] : 0.f;
     }
     part = sum_over_rows(part);
-    if ((threadIdx.x & 63) < 16) sPart[w * kC + j] = part;
+    if ((threadIdx.x & 63) < 16) sPart[rb * kC + j] = part;
   }
   __syncthreads();
   // X1 = L^T dL into Q's buffer
   float* Bx = Bq;
-  for (int ct = 0; ct < 4; ++ct) {
+  for (int ct = ch; ct < 4; ct += 2) {
     const f32x4 acc = mm16<true, false>(Bl + r0, P, Bt + 16 * ct, P, kC, zero4());
 #pragma unroll
     for (int r = 0; r < 4; ++r) Bx[(r0 + tile_row(r)) * P + 16 * ct + tile_col()] = acc[r];
   }
   __syncthreads();
-  // dA = -tril(X1 L^T, -1); dbeta_i gets sum_{m < i} dA_im (k_i . k_m) (a row of the wave's own);
-  // M = diag(beta) dA goes into dO's buffer
+  // dA = -tril(X1 L^T, -1); dbeta_i gets sum_{m < i} dA_im (k_i . k_m), each wave's columns into
+  // sRow; M = diag(beta) dA goes into dO's buffer
   float* Ba = Bo;
   float rows[4] = {0.f, 0.f, 0.f, 0.f};
-  for (int ct = 0; ct < 4; ++ct) {
+  for (int ct = ch; ct < 4; ct += 2) {
     const f32x4 acc = mm16<false, true>(Bx + r0 * P, P, Bl + 16 * ct * P, P, kC, zero4());
     const f32x4 gk = mm16<false, true>(Bk + r0 * P, P, Bk + 16 * ct * P, P, D, zero4());
 #pragma unroll
@@ -629,22 +650,28 @@ __global__ __launch_bounds__(256) void scan_bwd_chunk_kernel(
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
     const float x = group_sum<16>(rows[r]);
-    const int i = r0 + tile_row(r);
-    if (tile_col() == 0) sDB[i] = ((sPart[i] + sPart[kC + i]) + (sPart[2 * kC + i] + sPart[3 * kC + i])) + x;
+    if (tile_col() == 0) sRow[ch * kC + r0 + tile_row(r)] = x;
   }
   __syncthreads();
   // dK += M K + M^T K, then store
-  for (int ct = 0; ct < NT; ++ct) {
-    dka[ct] = mm16<false, false>(Ba + r0 * P, P, Bk + 16 * ct, P, kC, dka[ct]);
-    dka[ct] = mm16<true, false>(Ba + r0, P, Bk + 16 * ct, P, kC, dka[ct]);
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int i = r0 + tile_row(r), j = 16 * ct + tile_col();
-      if (t0 + i < N) dk[(((size_t)b * N + t0 + i) * H + h) * D + j] = from_f32<TIn>(dka[ct][r]);
+  for (int u = 0; u < NTW; ++u) {
+    const int ct = ch + 2 * u;
+    if (ct < NT) {
+      dka[u] = mm16<false, false>(Ba + r0 * P, P, Bk + 16 * ct, P, kC, dka[u]);
+      dka[u] = mm16<true, false>(Ba + r0, P, Bk + 16 * ct, P, kC, dka[u]);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int i = r0 + tile_row(r), j = 16 * ct + tile_col();
+        if (t0 + i < N) dk[(((size_t)b * N + t0 + i) * H + h) * D + j] = from_f32<TIn>(dka[u][r]);
+      }
     }
   }
-  for (int i = threadIdx.x; i < kC; i += kThreads)
-    if (t0 + i < N) dbeta[((size_t)b * N + t0 + i) * H + h] = from_f32<TIn>(sDB[i]);
+  const int i = threadIdx.x;
+  if (i < kC && t0 + i < N) {
+    const float x = ((sPart[i] + sPart[kC + i]) + (sPart[2 * kC + i] + sPart[3 * kC + i])) + (sRow[i] + sRow[kC + i]);
+    dbeta[((size_t)b * N + t0 + i) * H + h] = from_f32<TIn>(x);
+  }
 }
 
 size_t workspace_floats(int B, int N, int H, int D) {
@@ -664,7 +691,7 @@ void launch(const TIn* q, const TIn* k, const TIn* v, const TIn* beta, const flo
   hipLaunchKernelGGL((scan_bwd_states_kernel<TIn, D>), dim3(slices), dim3(256), 0, stream, k, state_in, ws, N, H, NC);
   hipLaunchKernelGGL((scan_bwd_dstate_kernel<TIn, D>), dim3(slices), dim3(256), 0, stream, k, d_state, d_state_in, ws, N,
                      H, NC);
-  hipLaunchKernelGGL((scan_bwd_chunk_kernel<TIn, D>), dim3(chunks), dim3(256), 0, stream, q, k, v, beta, d_o, active, ws,
+  hipLaunchKernelGGL((scan_bwd_chunk_kernel<TIn, D>), dim3(chunks), dim3(kChunkThreads), 0, stream, q, k, v, beta, d_o, active, ws,
                      dq, dk, dv, dbeta, N, H, NC);
 }
 
