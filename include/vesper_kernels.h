@@ -22,7 +22,7 @@
 extern "C" {
 #endif
 
-#define VSP_ABI_VERSION 6
+#define VSP_ABI_VERSION 7
 
 /* Status codes. */
 #define VSP_OK 0
@@ -59,6 +59,22 @@ int vsp_delta_scan_bf16(const void* q, const void* k, const void* v, const void*
 int vsp_delta_scan_f32(const float* q, const float* k, const float* v, const float* beta, const float* state_in,
                        float* o, float* state_out, void* workspace, size_t workspace_bytes,
                        const uint8_t* active, int B, int T, int H, int D, void* stream);
+
+/* Copy-forward fused into the scan's loads (the carry merges of vesper/column.py:779-789 and
+ * vesper/loop.py:449-452, which select `where(active, fresh, carried)` for k, v and beta before
+ * the scan): as vsp_delta_scan_bf16 / _f32, but where active[b, t] is 0 the token's k, v and beta
+ * rows are read from k_carried, v_carried, beta_carried (same shapes and dtypes as k, v, beta)
+ * instead of k, v, beta. `active` is required; the fresh rows of inactive tokens are never read. */
+int vsp_delta_scan_carried_bf16(const void* q, const void* k, const void* v, const void* beta,
+                                const void* k_carried, const void* v_carried, const void* beta_carried,
+                                const float* state_in, void* o, float* state_out, void* workspace,
+                                size_t workspace_bytes, const uint8_t* active, int B, int T, int H, int D,
+                                void* stream);
+int vsp_delta_scan_carried_f32(const float* q, const float* k, const float* v, const float* beta,
+                               const float* k_carried, const float* v_carried, const float* beta_carried,
+                               const float* state_in, float* o, float* state_out, void* workspace,
+                               size_t workspace_bytes, const uint8_t* active, int B, int T, int H, int D,
+                               void* stream);
 
 /* One decoding token per row (the contract of vesper/recurrence.py:143-163, delta_scan_step):
  * q, k, v: [B, H, D]; beta: [B, H]; state_in, state_out: [B, H, D, D] float32 (may alias, for an

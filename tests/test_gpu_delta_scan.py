@@ -375,3 +375,96 @@ def test_captured_forward_and_backward_equal_eager():
         torch.cuda.synchronize()
         for a, c in zip(static, eager):
             assert torch.equal(a, c)
+
+
+# ---- copy-forward read inside the kernels' loads (carried k, v, beta for inactive tokens) ----
+
+def _carry_case(b, n, h, dk, fp32, seed, frac=0.4):
+    make = _fp32_inputs if fp32 else _bf16_inputs
+    q, k, v, beta, h0 = make(b, n, h, dk, seed)
+    _, kc, vc, bc, _ = make(b, n, h, dk, seed + 7)
+    g = torch.Generator().manual_seed(seed + 11)
+    active = (torch.rand(b, n, generator=g) >= frac).to(GPU)
+    return q, k, v, beta, h0, (kc, vc, bc), active
+
+
+def _merged(k, v, beta, carried, active):
+    keep = active[..., None, None]
+    return (torch.where(keep, k, carried[0]), torch.where(keep, v, carried[1]),
+            torch.where(active[..., None], beta, carried[2]))
+
+
+# widths 16 and 128 take the generic chain, 32 and 64 the bf16 chain, 48 and n = 9 the serial kernel
+@pytest.mark.parametrize("fp32", [False, True])
+@pytest.mark.parametrize(("b", "n", "h", "dk"), [(2, 9, 2, 16), (2, 70, 2, 48), (2, 130, 3, 16), (2, 200, 2, 32),
+                                                 (1, 300, 2, 64), (2, 100, 2, 128)])
+def test_carried_inputs_equal_the_merged_inputs_bitwise(fp32, b, n, h, dk):
+    from vesper.kernels.delta_scan import delta_scan_fused, delta_scan_fused_fp32
+
+    if fp32 and dk == 128:
+        pytest.skip("the fp32 scan runs 128-wide heads token by token: covered at 48")
+    scan = delta_scan_fused_fp32 if fp32 else delta_scan_fused
+    q, k, v, beta, h0, carried, active = _carry_case(b, n, h, dk, fp32, seed=dk + n)
+    # the fresh rows of inactive tokens must never be read: poison them
+    hold = ~active
+    k, v = k.masked_fill(hold[..., None, None], float("nan")), v.masked_fill(hold[..., None, None], float("nan"))
+    beta = beta.masked_fill(hold[..., None], float("nan"))
+    o, s = scan(q, k, v, beta, h0, active=active, carried=carried)
+    o_ref, s_ref = scan(q, *_merged(k, v, beta, carried, active), h0, active=active)
+    torch.cuda.synchronize()
+    assert torch.equal(o, o_ref) and torch.equal(s, s_ref)
+    assert bool(torch.isfinite(s).all())
+
+
+@pytest.mark.parametrize("pattern", ["all_active", "all_held", "alternating", "tail_held"])
+def test_carried_inputs_on_every_flag_pattern_of_a_chunk(pattern):
+    from vesper.kernels.delta_scan import delta_scan_fused
+
+    b, n, h, dk = 2, 190, 2, 64
+    q, k, v, beta, h0, carried, _ = _carry_case(b, n, h, dk, False, seed=3)
+    t = torch.arange(n, device=GPU).expand(b, n)
+    active = {"all_active": t >= 0, "all_held": t < 0, "alternating": t % 2 == 0, "tail_held": t < 150}[pattern]
+    o, s = delta_scan_fused(q, k, v, beta, h0, active=active, carried=carried)
+    o_ref, s_ref = delta_scan_fused(q, *_merged(k, v, beta, carried, active), h0, active=active)
+    torch.cuda.synchronize()
+    assert torch.equal(o, o_ref) and torch.equal(s, s_ref)
+    want, s64 = _oracle(q, *_merged(k, v, beta, carried, active), h0, active=active)
+    assert relative_error(s, s64) < TOL
+
+
+def test_carried_inputs_at_b8_t4096_h8_d64():
+    from vesper.kernels.delta_scan import delta_scan_fused
+
+    q, k, v, beta, h0, carried, active = _carry_case(8, 4096, 8, 64, False, seed=5, frac=0.3)
+    o, s = delta_scan_fused(q, k, v, beta, h0, active=active, carried=carried)
+    o_ref, s_ref = delta_scan_fused(q, *_merged(k, v, beta, carried, active), h0, active=active)
+    torch.cuda.synchronize()
+    assert torch.equal(o, o_ref) and torch.equal(s, s_ref)
+
+
+def test_carried_inputs_under_autograd_route_gradients_to_the_carried_tensors():
+    from vesper.kernels.delta_scan import delta_scan_fused
+
+    q, k, v, beta, h0, carried, active = _carry_case(2, 100, 2, 32, False, seed=9)
+    leaves = [t.clone().requires_grad_() for t in (k, v, beta, *carried)]
+    o, s = delta_scan_fused(q, *leaves[:3], h0, active=active, carried=tuple(leaves[3:]))
+    (o.float().square().sum() + s.square().sum()).backward()
+    ref = [t.clone().requires_grad_() for t in (k, v, beta, *carried)]
+    o2, s2 = delta_scan_fused(q, *_merged(*ref[:3], tuple(ref[3:]), active), h0, active=active)
+    (o2.float().square().sum() + s2.square().sum()).backward()
+    for got, want in zip(leaves, ref):
+        assert torch.equal(got.grad, want.grad)
+    assert not bool(leaves[0].grad[~active].any()) and not bool(leaves[3].grad[active].any())
+
+
+def test_carried_refusals():
+    from vesper.contracts import ContractError
+    from vesper.kernels.delta_scan import delta_scan_fused
+
+    q, k, v, beta, h0, carried, active = _carry_case(1, 20, 2, 16, False, seed=1)
+    with pytest.raises(ContractError, match="active"):
+        delta_scan_fused(q, k, v, beta, h0, carried=carried)
+    with pytest.raises(ContractError, match="carried k"):
+        delta_scan_fused(q, k, v, beta, h0, active=active, carried=(carried[0].float(), *carried[1:]))
+    with pytest.raises(ContractError, match="carried holds"):
+        delta_scan_fused(q, k, v, beta, h0, active=active, carried=carried[:2])

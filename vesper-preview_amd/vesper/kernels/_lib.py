@@ -17,7 +17,7 @@ import torch
 HERE = Path(__file__).resolve().parent
 LIBRARY_PATH = HERE / "libvesper_kernels.so"
 HEADER_PATH = HERE.parents[2] / "include" / "vesper_kernels.h"
-ABI_VERSION = 6
+ABI_VERSION = 7
 
 P = ctypes.c_void_p
 I = ctypes.c_int
@@ -31,6 +31,8 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "vsp_delta_scan_workspace_bytes": (Z, [I, I, I, I, I]),
     "vsp_delta_scan_bf16": (I, [P, P, P, P, P, P, P, P, Z, P, I, I, I, I, P]),
     "vsp_delta_scan_f32": (I, [P, P, P, P, P, P, P, P, Z, P, I, I, I, I, P]),
+    "vsp_delta_scan_carried_bf16": (I, [P, P, P, P, P, P, P, P, P, P, P, Z, P, I, I, I, I, P]),
+    "vsp_delta_scan_carried_f32": (I, [P, P, P, P, P, P, P, P, P, P, P, Z, P, I, I, I, I, P]),
     "vsp_delta_step_f32": (I, [P, P, P, P, P, P, P, P, I, I, I, P]),
     "vsp_delta_step_bf16": (I, [P, P, P, P, P, P, P, P, I, I, I, P]),
     "vsp_window_attn_bf16": (I, [P, P, P, P, P, I, I, I, I, I, I, I, F, P]),

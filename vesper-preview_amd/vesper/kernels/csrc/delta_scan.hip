@@ -27,6 +27,22 @@ namespace {
 
 constexpr int kChunk = 64;
 
+// Copy-forward: where a token is inactive (halted), its k, v and beta are read from the carried
+// tensors (same layout) instead of the fresh ones. All three null: every token reads the fresh ones.
+template <typename TIn>
+struct Carried {
+  const TIn* k;
+  const TIn* v;
+  const TIn* beta;
+  // The source of a token's row: the carried tensor where the token is inactive. The kernels take
+  // CARRY as a template argument, so without carried inputs no address waits for a flag.
+  template <bool CARRY>
+  __device__ __forceinline__ static const TIn* pick(const TIn* fresh, const TIn* held, uint8_t active) {
+    if constexpr (CARRY) return active == 0 ? held : fresh;
+    return fresh;
+  }
+};
+
 // --------------------------------------------------------------------------------------------
 // token-serial kernel
 // --------------------------------------------------------------------------------------------
@@ -35,7 +51,11 @@ __global__ __launch_bounds__(256) void delta_serial_kernel(const TIn* __restrict
                                                            const TIn* __restrict__ v, const TIn* __restrict__ beta,
                                                            const float* __restrict__ s_in, float* __restrict__ s_out,
                                                            TIn* __restrict__ o, const uint8_t* __restrict__ active,
-                                                           int T, int H, int D, int groups) {
+                                                           const TIn* kc, const TIn* vc, const TIn* bc, int T, int H,
+                                                           int D, int groups) {
+  // (scalar pointer arguments: a struct argument would be read through private memory and count as
+  // divergent, which turns every buffer access on it into a loop over lanes)
+  const Carried<TIn> carried{kc, vc, bc};
   constexpr int NT = 16;  // tokens staged per round
   __shared__ float sk[NT][256];
   __shared__ float sq[NT][256];
@@ -65,20 +85,22 @@ __global__ __launch_bounds__(256) void delta_serial_kernel(const TIn* __restrict
   for (int t0 = 0; t0 < T; t0 += NT) {
     const int nt = min(NT, T - t0);
     __syncthreads();
+    if ((int)threadIdx.x < nt) sa[threadIdx.x] = active ? active[(size_t)b * T + t0 + threadIdx.x] : (uint8_t)1;
+    if (carried.k != nullptr) __syncthreads();  // the flags choose each token's source
     for (int i = threadIdx.x; i < nt * D; i += blockDim.x) {
       const int tt = i / D, e = i - tt * D;
       const size_t off = (((size_t)b * T + t0 + tt) * H + h) * D + e;
-      sk[tt][e] = to_f32(k[off]);
+      sk[tt][e] = to_f32((carried.k != nullptr && sa[tt] == 0 ? carried.k : k)[off]);
       sq[tt][e] = to_f32(q[off]);
     }
     for (int i = threadIdx.x; i < nt * 64; i += blockDim.x) {
       const int tt = i >> 6, c = blockIdx.y * 64 + (i & 63);
-      sv[tt][i & 63] = c < D ? to_f32(v[(((size_t)b * T + t0 + tt) * H + h) * D + c]) : 0.f;
+      const TIn* src = carried.k != nullptr && sa[tt] == 0 ? carried.v : v;
+      sv[tt][i & 63] = c < D ? to_f32(src[(((size_t)b * T + t0 + tt) * H + h) * D + c]) : 0.f;
     }
     if ((int)threadIdx.x < nt) {
       const size_t tok = (size_t)b * T + t0 + threadIdx.x;
-      sb[threadIdx.x] = to_f32(beta[tok * H + h]);
-      sa[threadIdx.x] = active ? active[tok] : (uint8_t)1;
+      sb[threadIdx.x] = to_f32((carried.k != nullptr && sa[threadIdx.x] == 0 ? carried.beta : beta)[tok * H + h]);
     }
     __syncthreads();
     for (int tt = 0; tt < nt; ++tt) {
@@ -134,6 +156,15 @@ __global__ __launch_bounds__(256) void delta_serial_kernel(const TIn* __restrict
 // MFMA operand flavours
 // --------------------------------------------------------------------------------------------
 __device__ __forceinline__ int lane_group() { return (threadIdx.x & 63) >> 4; }
+
+// A chunk's 64 active flags as a wave-uniform mask (bit r: token r of the chunk is active), from
+// lanes holding the flag of token 16 i + (lane % 16) in a[i].
+__device__ __forceinline__ uint64_t chunk_mask(const uint8_t (&a)[4]) {
+  uint64_t m = 0;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) m |= (__builtin_amdgcn_ballot_w64(a[i] != 0) & 0xFFFFull) << (16 * i);
+  return m;
+}
 
 // Within a wave, make LDS writes of any lane visible to later LDS reads of any lane.
 __device__ __forceinline__ void wave_sync() {
@@ -383,9 +414,12 @@ __device__ __forceinline__ void ut_solve(const typename Nat<E, DKP>::R (&kn)[4][
 // --------------------------------------------------------------------------------------------
 // chunk preparation: one wave per 64-token chunk, no workgroup barriers
 // --------------------------------------------------------------------------------------------
-template <typename TIn, typename E, int DK>
+template <typename TIn, typename E, int DK, bool CARRY>
 __global__ __launch_bounds__(256, 3) void delta_prep_kernel(const TIn* __restrict__ k, const TIn* __restrict__ beta,
-                                                         E* __restrict__ tmat, int T, int H, int total) {
+                                                         E* __restrict__ tmat, const uint8_t* __restrict__ active,
+                                                         const TIn* kc, const TIn* vc, const TIn* bc, int T, int H,
+                                                         int total) {
+  const Carried<TIn> carried{kc, vc, bc};
   constexpr int DKP = DK < 32 ? 32 : DK;
   using N = Nat<E, DKP>;
   // the compact factor is staged in LDS for 16-byte global stores: it overlays the scratch
@@ -404,17 +438,24 @@ __global__ __launch_bounds__(256, 3) void delta_prep_kernel(const TIn* __restric
   // Every load is unconditional (tokens past the end re-read the last one, padding features re-read
   // feature 0) and the zeros are selected once all are issued: a load behind a per-lane branch
   // would wait for every earlier one.
+  // with carried inputs, the flags of the lane's rows choose their source (loaded first)
+  uint8_t ak[4] = {1, 1, 1, 1}, ab = 1;
+  if constexpr (CARRY) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) ak[i] = active[(size_t)b * T + min(t0 + 16 * i + lq, T - 1)];
+    ab = active[(size_t)b * T + min(t0 + l, T - 1)];
+  }
   typename N::R kn[4][N::NREG];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    const TIn* row = k + (((size_t)b * T + min(t0 + 16 * i + lq, T - 1)) * H + h) * DK;
+    const TIn* row = Carried<TIn>::template pick<CARRY>(k, carried.k, ak[i]) + (((size_t)b * T + min(t0 + 16 * i + lq, T - 1)) * H + h) * DK;
 #pragma unroll
     for (int sgi = 0; sgi < N::NREG; ++sgi) {
       const int f = N::feat(sgi);
       kn[i][sgi] = *reinterpret_cast<const typename N::R*>(row + (f < DK ? f : 0));
     }
   }
-  const TIn braw = beta[((size_t)b * T + min(t0 + l, T - 1)) * H + h];
+  const TIn braw = Carried<TIn>::template pick<CARRY>(beta, carried.beta, ab)[((size_t)b * T + min(t0 + l, T - 1)) * H + h];
 #pragma unroll
   for (int i = 0; i < 4; ++i)
 #pragma unroll
@@ -446,11 +487,12 @@ template <typename E, int DK> struct ChainShape {
   static constexpr int NH = (sizeof(E) == 2 && DK <= 64) ? 7 : 3;
 };
 
-template <typename TIn, typename E, int DK>
+template <typename TIn, typename E, int DK, bool CARRY>
 __global__ __launch_bounds__(64 * (ChainShape<E, DK>::NH + 1)) void delta_chain_kernel(
     const TIn* __restrict__ q, const TIn* __restrict__ k, const TIn* __restrict__ v, const E* __restrict__ tmat,
     const float* __restrict__ s_in, float* __restrict__ s_out, TIn* __restrict__ o, const uint8_t* __restrict__ active,
-    int T, int H) {
+    const TIn* kc, const TIn* vc, const TIn* bc, int T, int H) {
+  const Carried<TIn> carried{kc, vc, bc};
   constexpr int NH = ChainShape<E, DK>::NH;
   constexpr int NW = NH + 1;
   constexpr int BV = 16;
@@ -512,61 +554,65 @@ __global__ __launch_bounds__(64 * (ChainShape<E, DK>::NH + 1)) void delta_chain_
   // 2^31): one VGPR per address keeps the helpers' staging registers from spilling.
   const int rstride = H * DK;
   const size_t bh_base = ((size_t)b * T * H + h) * DK;
-  auto load_rows = [&](NR (&dst)[4][N::NREG], const TIn* base, int c) {
+  // Loads are unconditional (rows past the end re-read the last row, padding features feature 0)
+  // and zeros are selected once all are issued: a load behind a per-lane branch would wait for
+  // every earlier one. Row 16 i + lq of the lane reads `held` where actraw[i] says the token is
+  // inactive and carried inputs are given.
+  auto load_rows = [&](NR (&dst)[4][N::NREG], const TIn* base, const TIn* held, int c) {
     const int nvc = min(kChunk, T - c * kChunk);
-    const TIn* cb = base + bh_base + (size_t)c * kChunk * rstride;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int tok = 16 * i + lq;
+      const int tok = min(16 * i + lq, nvc - 1);
+      const TIn* cb = Carried<TIn>::template pick<CARRY>(base, held, actraw[i]) + bh_base + (size_t)c * kChunk * rstride;
 #pragma unroll
       for (int s = 0; s < N::NREG; ++s) {
         const int f = N::feat(s);
-        if (tok < nvc && f < DK) {
-          dst[i][s] = *reinterpret_cast<const NR*>(cb + (tok * rstride + f));
-        } else {
-#pragma unroll
-          for (int e = 0; e < N::PER; ++e) dst[i][s][e] = from_f32<E>(0.f);
-        }
+        dst[i][s] = *reinterpret_cast<const NR*>(cb + (tok * rstride + (f < DK ? f : 0)));
       }
     }
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int s = 0; s < N::NREG; ++s) {
+        const bool ok = 16 * i + lq < nvc && N::feat(s) < DK;
+#pragma unroll
+        for (int e = 0; e < N::PER; ++e) dst[i][s][e] = ok ? dst[i][s][e] : from_f32<E>(0.f);
+      }
   };
   auto issue_loads = [&](int c) {
-    load_rows(qn, q, c);
-    load_rows(kn, k, c);
+    const int nvc = min(kChunk, T - c * kChunk);
+    // the flags first: with carried inputs they choose the sources of the K and V rows
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      actraw[i] = active != nullptr ? active[(size_t)b * T + (size_t)c * kChunk + min(16 * i + lq, nvc - 1)] : (uint8_t)1;
+    load_rows(qn, q, q, c);
+    load_rows(kn, k, carried.k, c);
     const u32x4* ts = reinterpret_cast<const u32x4*>(tmat + ((size_t)bh * nc + c) * kChunkT);
 #pragma unroll
     for (int j = 0; j < TSEG; ++j) tseg[j] = ts[l + 64 * j];
-    const int nvc = min(kChunk, T - c * kChunk);
     if constexpr (BF) {
-      const TIn* cb = v + bh_base + (size_t)c * kChunk * rstride + v0;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const int tok = 16 * i + lq;
-        if (tok < nvc) {
-          vn[i] = *reinterpret_cast<const bf16x4*>(cb + (tok * rstride + 4 * g));
-        } else {
-#pragma unroll
-          for (int e = 0; e < 4; ++e) vn[i][e] = (__bf16)0.f;
-        }
+        const TIn* cb = Carried<TIn>::template pick<CARRY>(v, carried.v, actraw[i]) + bh_base + (size_t)c * kChunk * rstride + v0;
+        vn[i] = *reinterpret_cast<const bf16x4*>(cb + (min(16 * i + lq, nvc - 1) * rstride + 4 * g));
       }
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) vn[i][e] = 16 * i + lq < nvc ? vn[i][e] : (__bf16)0.f;
     } else {
+      // V segment rows are not the lane's flag rows: their flags come from the chunk's mask
+      uint64_t held_rows = 0;
+      if constexpr (CARRY) held_rows = ~chunk_mask(actraw);
 #pragma unroll
       for (int j = 0; j < VSEG; ++j) {
         const int sg = l + 64 * j, tok = sg / VSPT, part = sg - tok * VSPT;
-        if (tok < nvc) {
-          const TIn* cb = v + bh_base + (size_t)c * kChunk * rstride + v0;
-          vseg[j] = *reinterpret_cast<const u32x4*>(cb + (tok * rstride + part * EPS));
-        } else {
-          vseg[j] = u32x4{0u, 0u, 0u, 0u};
-        }
+        const TIn* cb = (((held_rows >> tok) & 1) ? carried.v : v) + bh_base + (size_t)c * kChunk * rstride + v0;
+        vseg[j] = *reinterpret_cast<const u32x4*>(cb + (min(tok, nvc - 1) * rstride + part * EPS));
       }
-    }
-    if (active != nullptr) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int tok = min(16 * i + lq, nvc - 1);  // clamped: loaded unconditionally, masked later
-        actraw[i] = active[(size_t)b * T + (size_t)c * kChunk + tok];
-      }
+      for (int j = 0; j < VSEG; ++j)
+        if ((l + 64 * j) / VSPT >= nvc) vseg[j] = u32x4{0u, 0u, 0u, 0u};
     }
   };
   auto store_chunk = [&](int c) {
@@ -756,7 +802,7 @@ __global__ __launch_bounds__(64 * (ChainShape<E, DK>::NH + 1)) void delta_chain_
       if (co >= 0 && co % NH == hj) write_output(co);
       if (it >= 0 && it % NH == hj) {  // the idle iteration of chunk it's helper
         if (it + NH < nc) issue_loads(it + NH);
-        if constexpr (!kQInLds) load_rows(qr, q, it);
+        if constexpr (!kQInLds) load_rows(qr, q, q, it);
       }
     }
     __syncthreads();
@@ -842,13 +888,14 @@ __device__ __forceinline__ void flag_wait(const int* f, int want) {
   }
 }
 
-template <typename TIn, int DK>
+template <typename TIn, int DK, bool CARRY>
 __global__ __launch_bounds__(512) void delta_chain_bf16_kernel(const TIn* __restrict__ q, const TIn* __restrict__ k,
                                                                const TIn* __restrict__ v,
                                                                const __bf16* __restrict__ tmat,
                                                                const float* __restrict__ s_in, float* __restrict__ s_out,
                                                                TIn* __restrict__ o, const uint8_t* __restrict__ active,
-                                                               int T, int H) {
+                                                               const TIn* kc, const TIn* vc, const TIn* bc, int T, int H) {
+  const Carried<TIn> carried{kc, vc, bc};
   using E = __bf16;
   static_assert(sizeof(TIn) == 2, "bf16 inputs");
   constexpr int NH = 7;          // helper waves: chunks in flight
@@ -1007,20 +1054,48 @@ __global__ __launch_bounds__(512) void delta_chain_bf16_kernel(const TIn* __rest
   uint8_t actraw[4];
   bf16x8 pt[6];       // P^T per (key block, query tile): (0,0) (0,1) (0,2) (1,2) (0,3) (1,3)
   uint8_t actk[4];
+  // With carried inputs the flags of a chunk pick each K and V row's source when its loads are
+  // issued, so they are loaded one chunk of the helper ahead (actnext: token l of the helper's
+  // next chunk) and kept as a wave-uniform mask per chunk in flight.
+  uint8_t actnext = 1;
 
   // K rows and the V slice go straight into the helper's LDS tiles; Q, T and the active flags into
   // registers. The tiles are zeroed once first, so no uninitialised LDS is ever read.
   for (int i = l; i < 64 * DK / 8; i += 64) *reinterpret_cast<bf16x8*>(&myK[8 * i]) = bf16x8{};
   for (int i = l; i < 64 * BV / 8; i += 64) *reinterpret_cast<bf16x8*>(&myV[8 * i]) = bf16x8{};
   __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the zeros land before any direct load
-  auto issue_loads = [&](int c, bf16x4 (&qa)[4][HB]) {
+  auto issue_loads = [&](int c, bf16x4 (&qa)[4][HB], uint64_t mask) {
     const unsigned cb = (unsigned)c * kChunk * row_bytes;
+    if (!CARRY || mask == ~0ull) {
 #pragma unroll
-    for (int j = 0; j < KSEG; ++j)
-      buffer_load_lds16(rk, &myK[512 * j], (j & 1) ? off_k1 : off_k0, cb + (unsigned)j * (64 / KSEG) * row_bytes);
+      for (int j = 0; j < KSEG; ++j)
+        buffer_load_lds16(rk, &myK[512 * j], (j & 1) ? off_k1 : off_k0, cb + (unsigned)j * (64 / KSEG) * row_bytes);
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
-      buffer_load_lds16(rv, &myV[512 * j], off_v, cb + (unsigned)j * 32 * row_bytes);
+      for (int j = 0; j < 2; ++j)
+        buffer_load_lds16(rv, &myV[512 * j], off_v, cb + (unsigned)j * 32 * row_bytes);
+    } else {
+      // each lane's row from the fresh or the carried tensor by a per-lane address (global direct
+      // loads: a buffer resource chosen per lane would need a loop over lanes). Rows past the end
+      // re-read row T - 1 instead of reading zeros: their T rows and columns are zero, so they add
+      // nothing, and their outputs are dropped.
+      const char* kf = reinterpret_cast<const char*>(k + bh_base);
+      const char* kh = reinterpret_cast<const char*>(carried.k + bh_base);
+      const char* vf = reinterpret_cast<const char*>(v + bh_base + v0);
+      const char* vh = reinterpret_cast<const char*>(carried.v + bh_base + v0);
+#pragma unroll
+      for (int j = 0; j < KSEG; ++j) {
+        const int r = l / KSEG + j * (64 / KSEG);
+        const unsigned seg = ((j & 1) ? off_k1 : off_k0) - (unsigned)(l / KSEG) * row_bytes;
+        const char* src = (((mask >> r) & 1) ? kf : kh) + (size_t)min(c * kChunk + r, T - 1) * row_bytes + seg;
+        load_lds16(src, &myK[512 * j]);
+      }
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const int r = (l >> 1) + 32 * j;
+        const char* src = (((mask >> r) & 1) ? vf : vh) + (size_t)min(c * kChunk + r, T - 1) * row_bytes + 16u * (l & 1);
+        load_lds16(src, &myV[512 * j]);
+      }
+    }
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll
@@ -1030,7 +1105,9 @@ __global__ __launch_bounds__(512) void delta_chain_bf16_kernel(const TIn* __rest
 #pragma unroll
     for (int t = 0; t < kTiles; ++t)
       tl[t] = __builtin_bit_cast(bf16x4, __builtin_amdgcn_raw_buffer_load_b64(rt, off_t + 512u * t, tb, 0));
-    if (active != nullptr) {
+    if constexpr (CARRY) {
+      if (c + NH < nc) actnext = __builtin_amdgcn_raw_buffer_load_b8(ra, (unsigned)l, (unsigned)(c + NH) * kChunk, 0);
+    } else if (active != nullptr) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) actraw[i] = __builtin_amdgcn_raw_buffer_load_b8(ra, (unsigned)(16 * i + lq), (unsigned)c * kChunk, 0);
     }
@@ -1049,14 +1126,20 @@ __global__ __launch_bounds__(512) void delta_chain_bf16_kernel(const TIn* __rest
 
   // Chunk c's operands into state slot c % NSL (once the chain is done with the slot's previous
   // chunk); P^T kept in registers for the output
-  auto form = [&](int c, const bf16x4 (&qa)[4][HB]) {
+  auto form = [&](int c, const bf16x4 (&qa)[4][HB], uint64_t mask, uint64_t& next_mask) {
     const int nvc = min(kChunk, T - c * kChunk);
     const int s = c % NSL;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) actk[i] = (16 * i + lq < nvc && (active == nullptr || actraw[i] != 0)) ? 1 : 0;
     // the direct loads of K and V count as outstanding vector loads until they have written LDS
     __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
     wave_sync();
+    if constexpr (CARRY) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) actk[i] = (16 * i + lq < nvc && ((mask >> (16 * i + lq)) & 1)) ? 1 : 0;
+      next_mask = __builtin_amdgcn_ballot_w64(actnext != 0);  // the helper's next chunk (arrived above)
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) actk[i] = (16 * i + lq < nvc && (active == nullptr || actraw[i] != 0)) ? 1 : 0;
+    }
     // token-major operands: ktf[m][kb] = column 16 m + lq of token rows 32 kb + 4 g (+16)
     bf16x8 ktf[HB][2], vtf[2];
 #pragma unroll
@@ -1139,16 +1222,20 @@ __global__ __launch_bounds__(512) void delta_chain_bf16_kernel(const TIn* __rest
 
   // chunk c: form its operands, issue the loads of chunk c + NH (their latency hidden behind the
   // wait for the chain), then write its output
-  auto run = [&](int c, const bf16x4 (&qc)[4][HB], bf16x4 (&qn)[4][HB]) {
-    form(c, qc);
-    if (c + NH < nc) issue_loads(c + NH, qn);
+  auto run = [&](int c, const bf16x4 (&qc)[4][HB], bf16x4 (&qn)[4][HB], uint64_t mc, uint64_t& mn) {
+    form(c, qc, mc, mn);
+    if (c + NH < nc) issue_loads(c + NH, qn, mn);
     flag_wait<4>(&done, c);
     write_output(c, qc);
   };
-  if (hj < nc) issue_loads(hj, qa0);
+  uint64_t m0 = ~0ull, m1 = ~0ull;  // the flags of the chunks whose loads are in flight
+  if constexpr (CARRY) {
+    if (hj < nc) m0 = __builtin_amdgcn_ballot_w64(__builtin_amdgcn_raw_buffer_load_b8(ra, (unsigned)l, (unsigned)hj * kChunk, 0) != 0);
+  }
+  if (hj < nc) issue_loads(hj, qa0, m0);
   for (int c = hj; c < nc; c += 2 * NH) {
-    run(c, qa0, qa1);
-    if (c + NH < nc) run(c + NH, qa1, qa0);
+    run(c, qa0, qa1, m0, m1);
+    if (c + NH < nc) run(c + NH, qa1, qa0, m1, m0);
   }
 }
 
@@ -1170,11 +1257,12 @@ int check_common(const void* q, const void* k, const void* v, const void* beta, 
 
 template <typename TIn>
 int launch_serial(const TIn* q, const TIn* k, const TIn* v, const TIn* beta, const float* s_in, float* s_out, TIn* o,
-                  const uint8_t* active, int B, int T, int H, int D, hipStream_t stream, const char* who) {
+                  const uint8_t* active, Carried<TIn> carried, int B, int T, int H, int D, hipStream_t stream,
+                  const char* who) {
   const int groups = (D + 63) / 64;
   dim3 grid((unsigned)(B * H), (unsigned)groups);
   hipLaunchKernelGGL(delta_serial_kernel<TIn>, grid, dim3(64 * groups), 0, stream, q, k, v, beta, s_in, s_out, o,
-                     active, T, H, D, groups);
+                     active, carried.k, carried.v, carried.beta, T, H, D, groups);
   return check_launch(who);
 }
 
@@ -1185,28 +1273,45 @@ size_t workspace_bytes(int B, int T, int H, int D, bool fp32) {
   return (size_t)B * H * nc * kChunkT * (fp32 ? sizeof(float) : sizeof(uint16_t));
 }
 
-template <typename TIn, typename E, int DK>
+template <typename TIn, typename E, int DK, bool CARRY>
 void launch_chunked(const TIn* q, const TIn* k, const TIn* v, const TIn* beta, const float* s_in, float* s_out, TIn* o,
-                    E* tmat, const uint8_t* active, int B, int T, int H, hipStream_t stream) {
+                    E* tmat, const uint8_t* active, Carried<TIn> carried, int B, int T, int H, hipStream_t stream) {
   const int nc = (T + kChunk - 1) / kChunk;
   const int total = B * H * nc;
-  hipLaunchKernelGGL((delta_prep_kernel<TIn, E, DK>), dim3((unsigned)((total + 3) / 4)), dim3(256), 0, stream, k, beta,
-                     tmat, T, H, total);
+  hipLaunchKernelGGL((delta_prep_kernel<TIn, E, DK, CARRY>), dim3((unsigned)((total + 3) / 4)), dim3(256), 0, stream, k,
+                     beta, tmat, active, carried.k, carried.v, carried.beta, T, H, total);
   if constexpr (sizeof(E) == 2 && DK >= 32 && DK <= 64) {  // (at 128 the staging registers would spill)
-    hipLaunchKernelGGL((delta_chain_bf16_kernel<TIn, DK>), dim3((unsigned)(B * H * (DK / 16))), dim3(512), 0, stream, q,
-                       k, v, tmat, s_in, s_out, o, active, T, H);
+    hipLaunchKernelGGL((delta_chain_bf16_kernel<TIn, DK, CARRY>), dim3((unsigned)(B * H * (DK / 16))), dim3(512), 0,
+                       stream, q, k, v, tmat, s_in, s_out, o, active, carried.k, carried.v, carried.beta, T, H);
   } else {
-    hipLaunchKernelGGL((delta_chain_kernel<TIn, E, DK>), dim3((unsigned)(B * H * (DK / 16))),
-                       dim3(64 * (ChainShape<E, DK>::NH + 1)), 0, stream, q, k, v, tmat, s_in, s_out, o, active, T, H);
+    hipLaunchKernelGGL((delta_chain_kernel<TIn, E, DK, CARRY>), dim3((unsigned)(B * H * (DK / 16))),
+                       dim3(64 * (ChainShape<E, DK>::NH + 1)), 0, stream, q, k, v, tmat, s_in, s_out, o, active,
+                       carried.k, carried.v, carried.beta, T, H);
   }
+}
+
+template <typename TIn, typename E, int DK>
+void launch_chunked(const TIn* q, const TIn* k, const TIn* v, const TIn* beta, const float* s_in, float* s_out, TIn* o,
+                    E* tmat, const uint8_t* active, Carried<TIn> carried, int B, int T, int H, hipStream_t stream) {
+  if (carried.k != nullptr)
+    launch_chunked<TIn, E, DK, true>(q, k, v, beta, s_in, s_out, o, tmat, active, carried, B, T, H, stream);
+  else
+    launch_chunked<TIn, E, DK, false>(q, k, v, beta, s_in, s_out, o, tmat, active, carried, B, T, H, stream);
 }
 
 template <typename TIn, typename E>
 int delta_scan(const TIn* q, const TIn* k, const TIn* v, const TIn* beta, const float* s_in, TIn* o, float* s_out,
-               void* workspace, size_t ws_bytes, const uint8_t* active, int B, int T, int H, int D, void* stream_ptr,
-               const char* who) {
+               void* workspace, size_t ws_bytes, const uint8_t* active, Carried<TIn> carried, int B, int T, int H, int D,
+               void* stream_ptr, const char* who) {
   int st = check_common(q, k, v, beta, s_in, s_out, o, B, T, H, D, who);
   if (st != OK || B == 0 || H == 0) return st;
+  if (carried.k != nullptr || carried.v != nullptr || carried.beta != nullptr) {
+    if (!carried.k || !carried.v || !carried.beta)
+      return fail(ERR_ARG, "%s: the carried k, v and beta come together", who);
+    if (!active) return fail(ERR_ARG, "%s: carried inputs need the active flags", who);
+    if ((reinterpret_cast<uintptr_t>(carried.k) | reinterpret_cast<uintptr_t>(carried.v)) & 15)
+      return fail(ERR_ARG, "%s: the carried k and v must be 16-byte aligned", who);
+  }
   hipStream_t stream = reinterpret_cast<hipStream_t>(stream_ptr);
   if (T == 0) {
     if (s_in != s_out) {
@@ -1216,7 +1321,7 @@ int delta_scan(const TIn* q, const TIn* k, const TIn* v, const TIn* beta, const 
     return OK;
   }
   const size_t need = workspace_bytes(B, T, H, D, sizeof(E) == 4);
-  if (need == 0) return launch_serial<TIn>(q, k, v, beta, s_in, s_out, o, active, B, T, H, D, stream, who);
+  if (need == 0) return launch_serial<TIn>(q, k, v, beta, s_in, s_out, o, active, carried, B, T, H, D, stream, who);
   if (workspace == nullptr || ws_bytes < need)
     return fail(ERR_ARG, "%s: workspace of %zu bytes given, %zu needed", who, workspace ? ws_bytes : (size_t)0, need);
   // the chunked kernels move q, k, v, o rows and the workspace in 16-byte pieces
@@ -1225,11 +1330,12 @@ int delta_scan(const TIn* q, const TIn* k, const TIn* v, const TIn* beta, const 
     return fail(ERR_ARG, "%s: q, k, v, o and the workspace must be 16-byte aligned", who);
   E* tmat = reinterpret_cast<E*>(workspace);
   switch (D) {
-    case 16: launch_chunked<TIn, E, 16>(q, k, v, beta, s_in, s_out, o, tmat, active, B, T, H, stream); break;
-    case 32: launch_chunked<TIn, E, 32>(q, k, v, beta, s_in, s_out, o, tmat, active, B, T, H, stream); break;
-    case 64: launch_chunked<TIn, E, 64>(q, k, v, beta, s_in, s_out, o, tmat, active, B, T, H, stream); break;
+    case 16: launch_chunked<TIn, E, 16>(q, k, v, beta, s_in, s_out, o, tmat, active, carried, B, T, H, stream); break;
+    case 32: launch_chunked<TIn, E, 32>(q, k, v, beta, s_in, s_out, o, tmat, active, carried, B, T, H, stream); break;
+    case 64: launch_chunked<TIn, E, 64>(q, k, v, beta, s_in, s_out, o, tmat, active, carried, B, T, H, stream); break;
     default:
-      if constexpr (sizeof(E) == 2) launch_chunked<TIn, E, 128>(q, k, v, beta, s_in, s_out, o, tmat, active, B, T, H, stream);
+      if constexpr (sizeof(E) == 2)
+        launch_chunked<TIn, E, 128>(q, k, v, beta, s_in, s_out, o, tmat, active, carried, B, T, H, stream);
       break;
   }
   return check_launch(who);
@@ -1248,7 +1354,7 @@ int delta_step(const TIn* q, const TIn* k, const TIn* v, const TIn* beta, const 
     fast = delta_step_fast_bf16(q, k, v, beta, s_in, s_out, o, active, B, H, D, stream);
   }
   if (fast) return check_launch(who);
-  return launch_serial<TIn>(q, k, v, beta, s_in, s_out, o, active, B, 1, H, D, stream, who);
+  return launch_serial<TIn>(q, k, v, beta, s_in, s_out, o, active, Carried<TIn>{}, B, 1, H, D, stream, who);
 }
 
 }  // namespace
@@ -1266,16 +1372,39 @@ extern "C" int vsp_delta_scan_bf16(const void* q, const void* k, const void* v, 
                                    const uint8_t* active, int B, int T, int H, int D, void* stream) {
   return delta_scan<__bf16, __bf16>(static_cast<const __bf16*>(q), static_cast<const __bf16*>(k),
                                     static_cast<const __bf16*>(v), static_cast<const __bf16*>(beta), state_in,
-                                    static_cast<__bf16*>(o), state_out, workspace, workspace_bytes, active, B, T, H, D,
-                                    stream, "vsp_delta_scan_bf16");
+                                    static_cast<__bf16*>(o), state_out, workspace, workspace_bytes, active,
+                                    vsp::Carried<__bf16>{}, B, T, H, D, stream, "vsp_delta_scan_bf16");
+}
+
+extern "C" int vsp_delta_scan_carried_bf16(const void* q, const void* k, const void* v, const void* beta,
+                                           const void* k_carried, const void* v_carried, const void* beta_carried,
+                                           const float* state_in, void* o, float* state_out, void* workspace,
+                                           size_t workspace_bytes, const uint8_t* active, int B, int T, int H, int D,
+                                           void* stream) {
+  using T16 = __bf16;
+  const vsp::Carried<T16> carried{static_cast<const T16*>(k_carried), static_cast<const T16*>(v_carried),
+                                  static_cast<const T16*>(beta_carried)};
+  return delta_scan<T16, T16>(static_cast<const T16*>(q), static_cast<const T16*>(k), static_cast<const T16*>(v),
+                              static_cast<const T16*>(beta), state_in, static_cast<T16*>(o), state_out, workspace,
+                              workspace_bytes, active, carried, B, T, H, D, stream, "vsp_delta_scan_carried_bf16");
 }
 
 extern "C" int vsp_delta_scan_f32(const float* q, const float* k, const float* v, const float* beta,
                                   const float* state_in, float* o, float* state_out, void* workspace,
                                   size_t workspace_bytes, const uint8_t* active, int B, int T, int H, int D,
                                   void* stream) {
-  return delta_scan<float, float>(q, k, v, beta, state_in, o, state_out, workspace, workspace_bytes, active, B, T, H,
-                                  D, stream, "vsp_delta_scan_f32");
+  return delta_scan<float, float>(q, k, v, beta, state_in, o, state_out, workspace, workspace_bytes, active,
+                                  vsp::Carried<float>{}, B, T, H, D, stream, "vsp_delta_scan_f32");
+}
+
+extern "C" int vsp_delta_scan_carried_f32(const float* q, const float* k, const float* v, const float* beta,
+                                          const float* k_carried, const float* v_carried, const float* beta_carried,
+                                          const float* state_in, float* o, float* state_out, void* workspace,
+                                          size_t workspace_bytes, const uint8_t* active, int B, int T, int H, int D,
+                                          void* stream) {
+  return delta_scan<float, float>(q, k, v, beta, state_in, o, state_out, workspace, workspace_bytes, active,
+                                  vsp::Carried<float>{k_carried, v_carried, beta_carried}, B, T, H, D, stream,
+                                  "vsp_delta_scan_carried_f32");
 }
 
 extern "C" int vsp_delta_step_f32(const float* q, const float* k, const float* v, const float* beta,

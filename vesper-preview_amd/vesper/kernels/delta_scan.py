@@ -15,7 +15,10 @@ already normalised. Where the reference calls fla-core's Triton kernels, these c
 
 Each takes an optional keyword ``active`` (bool ``[b, n]``, ``[b]`` for the step): inactive tokens
 still write the state; their outputs are zero (``vesper/loop.py:24-26``, ``:441-442``). ``None`` is
-exactly the reference behaviour. The two chunked scans are autograd functions: their backward
+exactly the reference behaviour. With ``active``, the chunked scans also take ``carried = (k, v,
+beta)``: the copy-forward of halted tokens (``vesper/column.py:779-789``), read inside the kernels'
+loads (``vsp_delta_scan_carried_*``) where a token is inactive, in place of the ``where`` merges
+before the call. The two chunked scans are autograd functions: their backward
 (``vsp_delta_scan_backward_*``, head widths 16, 32 and 64) gives the gradients of ``q, k, v, beta``
 and the initial state, as the reference's kernels do; the single step is forward only (inputs
 that require a gradient are refused while grad mode is on).
@@ -90,7 +93,8 @@ def _aligned(t: Tensor) -> Tensor:
 
 
 def _scan(entry: str, q: Tensor, k: Tensor, v: Tensor, beta: Tensor, state: Tensor, active: Tensor | None,
-          fp32: bool, mask: Tensor | None = None) -> tuple[Tensor, Tensor]:
+          fp32: bool, mask: Tensor | None = None,
+          carried: tuple[Tensor, Tensor, Tensor] | None = None) -> tuple[Tensor, Tensor]:
     b, n, h, dk = q.shape
     q, k, v, beta, state = (_aligned(t) for t in (q, k, v, beta, state))
     if mask is None:
@@ -101,9 +105,29 @@ def _scan(entry: str, q: Tensor, k: Tensor, v: Tensor, beta: Tensor, state: Tens
     ws_bytes = int(lib.vsp_delta_scan_workspace_bytes(b, n, h, dk, int(fp32)))
     ws = torch.empty(ws_bytes, dtype=torch.uint8, device=q.device) if ws_bytes else None
     with torch.cuda.device(q.device):
-        _lib.call(entry, q.data_ptr(), k.data_ptr(), v.data_ptr(), beta.data_ptr(), state.data_ptr(), o.data_ptr(),
-                  s_out.data_ptr(), _lib.ptr(ws), ws_bytes, _lib.ptr(mask), b, n, h, dk, _lib.stream_of(q.device))
+        if carried is None:
+            _lib.call(entry, q.data_ptr(), k.data_ptr(), v.data_ptr(), beta.data_ptr(), state.data_ptr(), o.data_ptr(),
+                      s_out.data_ptr(), _lib.ptr(ws), ws_bytes, _lib.ptr(mask), b, n, h, dk, _lib.stream_of(q.device))
+        else:
+            kc, vc, bc = (_aligned(t) for t in carried)
+            _lib.call(entry.replace("vsp_delta_scan_", "vsp_delta_scan_carried_"), q.data_ptr(), k.data_ptr(),
+                      v.data_ptr(), beta.data_ptr(), kc.data_ptr(), vc.data_ptr(), bc.data_ptr(), state.data_ptr(),
+                      o.data_ptr(), s_out.data_ptr(), _lib.ptr(ws), ws_bytes, _lib.ptr(mask), b, n, h, dk,
+                      _lib.stream_of(q.device))
     return o, s_out
+
+
+def _checked_carried(carried: tuple[Tensor, Tensor, Tensor], k: Tensor, v: Tensor, beta: Tensor,
+                     active: Tensor | None) -> tuple[Tensor, Tensor, Tensor]:
+    if active is None:
+        raise ContractError("carried inputs need the active mask that says which tokens read them")
+    if len(carried) != 3:
+        raise ContractError(f"carried holds k, v and beta, got {len(carried)} tensors")
+    for name, held, fresh in zip(("k", "v", "beta"), carried, (k, v, beta)):
+        if held.shape != fresh.shape or held.dtype != fresh.dtype or held.device != fresh.device:
+            raise ContractError(f"carried {name}: {tuple(held.shape)} {held.dtype} on {held.device}, "
+                                f"{name} is {tuple(fresh.shape)} {fresh.dtype} on {fresh.device}")
+    return carried
 
 
 class _DeltaScan(torch.autograd.Function):
@@ -144,20 +168,30 @@ class _DeltaScan(torch.autograd.Function):
 
 
 def _autograd_scan(q: Tensor, k: Tensor, v: Tensor, beta: Tensor, state: Tensor, active: Tensor | None,
-                   fp32: bool) -> tuple[Tensor, Tensor]:
+                   fp32: bool, carried: tuple[Tensor, Tensor, Tensor] | None = None) -> tuple[Tensor, Tensor]:
     b, n, _, dk = q.shape
     mask = _active_mask(active, ("b", "n"), {"b": b, "n": n}, q.device)
-    if torch.is_grad_enabled() and any(t.requires_grad for t in (q, k, v, beta, state)):
+    if carried is not None:
+        carried = _checked_carried(carried, k, v, beta, active)
+    grad = torch.is_grad_enabled() and any(t.requires_grad for t in (q, k, v, beta, state, *(carried or ())))
+    if grad and carried is not None and active is not None:
+        # under autograd the merge is explicit, so the gradient reaches the carried tensors
+        keep = active.reshape(b, n, 1, 1)
+        k, v = torch.where(keep, k, carried[0]), torch.where(keep, v, carried[1])
+        beta = torch.where(keep[..., 0], beta, carried[2])
+        carried = None
+    if grad:
         if dk not in BACKWARD_HEAD_DIMS:
             raise ContractError(f"the scan's backward takes head widths {BACKWARD_HEAD_DIMS}, got {dk}")
         out: tuple[Tensor, Tensor] = _DeltaScan.apply(q, k, v, beta, state, mask, fp32)
         return out
     entry = "vsp_delta_scan_f32" if fp32 else "vsp_delta_scan_bf16"
-    return _scan(entry, q, k, v, beta, state, None, fp32, mask=mask)
+    return _scan(entry, q, k, v, beta, state, None, fp32, mask=mask, carried=carried)
 
 
 def delta_scan_fused(q: Tensor, k: Tensor, v: Tensor, beta: Tensor, state: Tensor, *,
-                     active: Tensor | None = None) -> tuple[Tensor, Tensor]:
+                     active: Tensor | None = None,
+                     carried: tuple[Tensor, Tensor, Tensor] | None = None) -> tuple[Tensor, Tensor]:
     """Apply ``n`` tokens to the state with the chunked bfloat16 kernel.
 
     Args:
@@ -167,6 +201,9 @@ def delta_scan_fused(q: Tensor, k: Tensor, v: Tensor, beta: Tensor, state: Tenso
         beta: ``[b, n, h]`` write strengths in [0, 1], bfloat16.
         state: ``[b, h, dk, dk]`` the state before the first token, float32.
         active: optional bool ``[b, n]``; inactive tokens write the state, their outputs are zero.
+        carried: optional ``(k, v, beta)`` shaped as ``k, v, beta`` (needs ``active``): an inactive
+            token writes these rows instead of its fresh ones, as after ``where(active, fresh,
+            carried)`` merges.
 
     Returns:
         ``(o, state_n)``: ``o [b, n, h, dk]`` bfloat16 and the final state in float32; with no
@@ -181,18 +218,19 @@ def delta_scan_fused(q: Tensor, k: Tensor, v: Tensor, beta: Tensor, state: Tenso
     """
     if _checked_length(q, k, v, beta, state, INPUT_DTYPE) == 0:
         return q, state
-    return _autograd_scan(q, k, v, beta, state, active, fp32=False)
+    return _autograd_scan(q, k, v, beta, state, active, fp32=False, carried=carried)
 
 
 def delta_scan_fused_fp32(q: Tensor, k: Tensor, v: Tensor, beta: Tensor, state: Tensor, *,
-                          active: Tensor | None = None) -> tuple[Tensor, Tensor]:
+                          active: Tensor | None = None,
+                          carried: tuple[Tensor, Tensor, Tensor] | None = None) -> tuple[Tensor, Tensor]:
     """Apply ``n`` tokens to the state with float32 inputs, state and arithmetic.
 
     As ``delta_scan_fused`` with every tensor float32; ``o`` is float32.
     """
     if _checked_length(q, k, v, beta, state, FP32_INPUT_DTYPE) == 0:
         return q, state
-    return _autograd_scan(q, k, v, beta, state, active, fp32=True)
+    return _autograd_scan(q, k, v, beta, state, active, fp32=True, carried=carried)
 
 
 def delta_scan_step_fused(q: Tensor, k: Tensor, v: Tensor, beta: Tensor, state: Tensor, *,
