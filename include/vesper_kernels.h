@@ -119,6 +119,17 @@ int vsp_window_attn_lse_bf16(const void* q, const void* keys, const void* values
 int vsp_window_attn_lse_f16(const void* q, const void* keys, const void* values, void* o, float* lse,
                             const uint8_t* active, int B, int N, int M, int H, int HKV, int D, int window,
                             float scale, void* stream);
+/* Copy-forward fused into the tile loads (the carry merges of the attention keys and values,
+ * vesper/column.py:795-796, `where(active, fresh, carried)` before the call): as
+ * vsp_window_attn_bf16 / _f16, but key rows M + t of a token t with active[b, t] == 0 are read from
+ * row t of keys_carried / values_carried ([B, N, HKV, D]: the new rows only; cache rows are never
+ * carried). `active` is required; the fresh key and value rows of inactive tokens are never read. */
+int vsp_window_attn_carried_bf16(const void* q, const void* keys, const void* values, const void* keys_carried,
+                                 const void* values_carried, void* o, const uint8_t* active, int B, int N, int M,
+                                 int H, int HKV, int D, int window, float scale, void* stream);
+int vsp_window_attn_carried_f16(const void* q, const void* keys, const void* values, const void* keys_carried,
+                                const void* values_carried, void* o, const uint8_t* active, int B, int N, int M,
+                                int H, int HKV, int D, int window, float scale, void* stream);
 /* The gradients (the backward of fla-core's `parallel_attn`, which autograd runs for
  * vesper/kernels/window_attn.py:27-39 under WindowedAttention.attend, vesper/attention.py:373-383):
  * from dO [B, N, H, D] and the forward's o and lse, dq [B, N, H, D], dk and dv [B, M + N, HKV, D]

@@ -242,3 +242,91 @@ def test_captured_forward_and_backward_equal_eager():
         torch.cuda.synchronize()
         for a, b in zip(static, eager):
             assert torch.equal(a, b)
+
+
+# ---- copy-forward read inside the tile loads (carried keys and values of inactive tokens) ----
+
+def _carry_case(b, n, m, h, hkv, dk, seed, dtype=BF16, frac=0.4):
+    q, keys, values = (t.to(GPU) for t in _inputs(b, n, m, h, hkv, dk, seed, dtype))
+    g = torch.Generator().manual_seed(seed + 1)
+    kc = torch.randn(b, n, hkv, dk, generator=g).to(GPU, dtype)
+    vc = torch.randn(b, n, hkv, dk, generator=g).to(GPU, dtype)
+    active = (torch.rand(b, n, generator=g) >= frac).to(GPU)
+    return q, keys, values, (kc, vc), active
+
+
+def _merged_kv(keys, values, carried, active):
+    m = keys.shape[1] - active.shape[1]
+    keep = active[..., None, None]
+    return (torch.cat([keys[:, :m], torch.where(keep, keys[:, m:], carried[0])], dim=1),
+            torch.cat([values[:, :m], torch.where(keep, values[:, m:], carried[1])], dim=1))
+
+
+@pytest.mark.parametrize("dtype", [BF16, torch.float16])
+@pytest.mark.parametrize("dk", [16, 32, 64, 128])
+@pytest.mark.parametrize(("n", "m", "w", "h", "hkv"), [(70, 0, 16, 4, 2), (200, 40, 64, 8, 2), (300, 100, 600, 4, 4)])
+def test_carried_keys_and_values_equal_the_merged_ones_bitwise(dtype, dk, n, m, w, h, hkv):
+    from vesper.kernels.window_attn import window_attention
+
+    q, keys, values, carried, active = _carry_case(2, n, m, h, hkv, dk, seed=dk + n, dtype=dtype)
+    # the fresh rows of inactive tokens must never be read: poison them
+    hold = torch.cat([torch.zeros(2, m, dtype=torch.bool, device=GPU), ~active], dim=1)[..., None, None]
+    keys, values = keys.masked_fill(hold, float("nan")), values.masked_fill(hold, float("nan"))
+    got = window_attention(q, keys, values, w, active=active, carried=carried)
+    want = window_attention(q, *_merged_kv(keys, values, carried, active), w, active=active)
+    torch.cuda.synchronize()
+    assert torch.equal(got, want)
+    assert bool(torch.isfinite(got).all())
+
+
+@pytest.mark.parametrize("pattern", ["all_active", "all_held", "alternating", "tail_held"])
+def test_carried_keys_on_every_flag_pattern(pattern):
+    from vesper.kernels.window_attn import window_attention
+
+    b, n, m = 2, 260, 30
+    q, keys, values, carried, _ = _carry_case(b, n, m, 4, 2, 64, seed=4)
+    t = torch.arange(n, device=GPU).expand(b, n)
+    active = {"all_active": t >= 0, "all_held": t < 0, "alternating": t % 2 == 0, "tail_held": t < 200}[pattern]
+    got = window_attention(q, keys, values, 100, active=active, carried=carried)
+    mk, mv = _merged_kv(keys, values, carried, active)
+    want = window_attention(q, mk, mv, 100, active=active)
+    torch.cuda.synchronize()
+    assert torch.equal(got, want)
+    ref = oracle_window(q.double().cpu(), mk.double().cpu(), mv.double().cpu(), 100) * active[..., None, None].cpu()
+    _check(got, ref)
+
+
+def test_carried_keys_at_b4_t4096_h8_d64_w512():
+    from vesper.kernels.window_attn import window_attention
+
+    q, keys, values, carried, active = _carry_case(4, 4096, 0, 8, 8, 64, seed=6, frac=0.3)
+    got = window_attention(q, keys, values, 512, active=active, carried=carried)
+    want = window_attention(q, *_merged_kv(keys, values, carried, active), 512, active=active)
+    torch.cuda.synchronize()
+    assert torch.equal(got, want)
+
+
+def test_carried_keys_under_autograd_route_gradients_to_the_carried_tensors():
+    from vesper.kernels.window_attn import window_attention
+
+    q, keys, values, carried, active = _carry_case(2, 80, 10, 4, 2, 32, seed=8)
+    leaves = [t.clone().requires_grad_() for t in (keys, values, *carried)]
+    window_attention(q, leaves[0], leaves[1], 16, active=active, carried=tuple(leaves[2:])).float().square().sum().backward()
+    ref = [t.clone().requires_grad_() for t in (keys, values, *carried)]
+    window_attention(q, *_merged_kv(ref[0], ref[1], tuple(ref[2:]), active), 16, active=active).float().square().sum().backward()
+    for got, want in zip(leaves, ref):
+        assert torch.equal(got.grad, want.grad)
+    assert not bool(leaves[2].grad[active].any())
+
+
+def test_carried_refusals():
+    from vesper.contracts import ContractError
+    from vesper.kernels.window_attn import window_attention
+
+    q, keys, values, carried, active = _carry_case(1, 20, 4, 2, 2, 16, seed=2)
+    with pytest.raises(ContractError, match="active"):
+        window_attention(q, keys, values, 8, carried=carried)
+    with pytest.raises(ContractError, match="carried keys"):
+        window_attention(q, keys, values, 8, active=active, carried=(keys, carried[1]))
+    with pytest.raises(ContractError, match="carried holds"):
+        window_attention(q, keys, values, 8, active=active, carried=carried[:1])

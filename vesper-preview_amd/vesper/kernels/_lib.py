@@ -42,6 +42,8 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "vsp_delta_scan_backward_f32": (I, [P, P, P, P, P, P, P, P, P, P, P, P, P, P, Z, I, I, I, I, P]),
     "vsp_window_attn_lse_bf16": (I, [P, P, P, P, P, P, I, I, I, I, I, I, I, F, P]),
     "vsp_window_attn_lse_f16": (I, [P, P, P, P, P, P, I, I, I, I, I, I, I, F, P]),
+    "vsp_window_attn_carried_bf16": (I, [P, P, P, P, P, P, P, I, I, I, I, I, I, I, F, P]),
+    "vsp_window_attn_carried_f16": (I, [P, P, P, P, P, P, P, I, I, I, I, I, I, I, F, P]),
     "vsp_window_attn_backward_bf16": (I, [P, P, P, P, P, P, P, P, P, P, I, I, I, I, I, I, I, F, P]),
     "vsp_window_attn_backward_f16": (I, [P, P, P, P, P, P, P, P, P, P, I, I, I, I, I, I, I, F, P]),
     "vsp_ring_attn_workspace_bytes": (Z, [I]),

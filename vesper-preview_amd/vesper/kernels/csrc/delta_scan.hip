@@ -607,8 +607,9 @@ __global__ __launch_bounds__(64 * (ChainShape<E, DK>::NH + 1)) void delta_chain_
 #pragma unroll
       for (int j = 0; j < VSEG; ++j) {
         const int sg = l + 64 * j, tok = sg / VSPT, part = sg - tok * VSPT;
-        const TIn* cb = (((held_rows >> tok) & 1) ? carried.v : v) + bh_base + (size_t)c * kChunk * rstride + v0;
-        vseg[j] = *reinterpret_cast<const u32x4*>(cb + (min(tok, nvc - 1) * rstride + part * EPS));
+        const int tl = min(tok, nvc - 1);  // the row loaded, with its own source flag
+        const TIn* cb = (((held_rows >> tl) & 1) ? carried.v : v) + bh_base + (size_t)c * kChunk * rstride + v0;
+        vseg[j] = *reinterpret_cast<const u32x4*>(cb + (tl * rstride + part * EPS));
       }
 #pragma unroll
       for (int j = 0; j < VSEG; ++j)
@@ -1076,23 +1077,23 @@ __global__ __launch_bounds__(512) void delta_chain_bf16_kernel(const TIn* __rest
     } else {
       // each lane's row from the fresh or the carried tensor by a per-lane address (global direct
       // loads: a buffer resource chosen per lane would need a loop over lanes). Rows past the end
-      // re-read row T - 1 instead of reading zeros: their T rows and columns are zero, so they add
-      // nothing, and their outputs are dropped.
+      // re-read row T - 1 (from that token's own source, so the row is finite) instead of reading
+      // zeros: their T rows and columns are zero, so they add nothing, and their outputs are dropped.
       const char* kf = reinterpret_cast<const char*>(k + bh_base);
       const char* kh = reinterpret_cast<const char*>(carried.k + bh_base);
       const char* vf = reinterpret_cast<const char*>(v + bh_base + v0);
       const char* vh = reinterpret_cast<const char*>(carried.v + bh_base + v0);
 #pragma unroll
       for (int j = 0; j < KSEG; ++j) {
-        const int r = l / KSEG + j * (64 / KSEG);
+        const int t = min(c * kChunk + l / KSEG + j * (64 / KSEG), T - 1);
         const unsigned seg = ((j & 1) ? off_k1 : off_k0) - (unsigned)(l / KSEG) * row_bytes;
-        const char* src = (((mask >> r) & 1) ? kf : kh) + (size_t)min(c * kChunk + r, T - 1) * row_bytes + seg;
+        const char* src = (((mask >> (t - c * kChunk)) & 1) ? kf : kh) + (size_t)t * row_bytes + seg;
         load_lds16(src, &myK[512 * j]);
       }
 #pragma unroll
       for (int j = 0; j < 2; ++j) {
-        const int r = (l >> 1) + 32 * j;
-        const char* src = (((mask >> r) & 1) ? vf : vh) + (size_t)min(c * kChunk + r, T - 1) * row_bytes + 16u * (l & 1);
+        const int t = min(c * kChunk + (l >> 1) + 32 * j, T - 1);
+        const char* src = (((mask >> (t - c * kChunk)) & 1) ? vf : vh) + (size_t)t * row_bytes + 16u * (l & 1);
         load_lds16(src, &myV[512 * j]);
       }
     }

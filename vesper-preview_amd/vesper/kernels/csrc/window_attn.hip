@@ -29,11 +29,15 @@ namespace {
 
 constexpr float kLazy = 8.f;
 
-template <typename T, int D>
-__global__ __launch_bounds__(256, D >= 128 ? 2 : 4) void window_attn_kernel(const T* __restrict__ q, const T* __restrict__ keys,
+// CARRY (copy-forward): key rows M + t of an inactive token t come from keys_c / values_c row t
+// ([B, N, HKV, D], the carried keys and values) instead of keys / values. Its per-lane 64-bit
+// source addresses need more registers: three workgroups per CU at D 64 instead of four.
+template <typename T, int D, bool CARRY>
+__global__ __launch_bounds__(256, D >= 128 ? 2 : (CARRY && D == 64 ? 3 : 4)) void window_attn_kernel(const T* __restrict__ q, const T* __restrict__ keys,
                                                              const T* __restrict__ values, T* __restrict__ o,
                                                              float* __restrict__ lse,
-                                                             const uint8_t* __restrict__ active, int N, int M, int H,
+                                                             const uint8_t* __restrict__ active, const T* keys_c,
+                                                             const T* values_c, int N, int M, int H,
                                                              int HKV, int W, float scale_log2, int nqt) {
   using V8 = typename Mma<T>::V8;
   using V4 = typename Mma<T>::V4;
@@ -112,6 +116,16 @@ __global__ __launch_bounds__(256, D >= 128 ? 2 : 4) void window_attn_kernel(cons
   const size_t kv_row = (size_t)HKV * D;
   const T* kbase = keys + ((size_t)b * S * HKV + kvh) * D;
   const T* vbase = values + ((size_t)b * S * HKV + kvh) * D;
+  // carried rows, indexed by key index (valid from M on)
+  const T* kcbase = CARRY ? keys_c + ((size_t)b * N * HKV + kvh) * D - (size_t)M * kv_row : kbase;
+  const T* vcbase = CARRY ? values_c + ((size_t)b * N * HKV + kvh) * D - (size_t)M * kv_row : vbase;
+  // With carried rows, each tile's 64 source flags (bit r: key k0 + r reads the fresh row) are
+  // loaded one tile ahead (lane l: key k0 + l) and turned into a wave-uniform mask when issued.
+  auto flag_of = [&](int k0) -> uint8_t {
+    const int s = k0 + l;
+    const uint8_t f = active[(size_t)b * N + min(max(s - M, 0), N - 1)];
+    return (s < M || s >= S) ? (uint8_t)1 : f;  // cache rows and rows past the end: fresh
+  };
 
   // staging of one 64-key tile. At D >= 64 through buffer resources over the (b, KV head) rows:
   // each lane's offset within a tile is fixed (computed once), rows past the last key read zeros,
@@ -129,10 +143,23 @@ __global__ __launch_bounds__(256, D >= 128 ? 2 : 4) void window_attn_kernel(cons
     const int rowv = pos / PSEGV, segv = pos - rowv * PSEGV;
     voff[j] = (unsigned)(rowv * kv_row + 8 * (segv < SEG ? segv : 0)) * (unsigned)sizeof(T);
   }
-  auto fetch = [&](int k0, int buf) {
+  auto fetch = [&](int k0, int buf, uint64_t fresh) {
 #pragma unroll
     for (int j = 0; j < NI; ++j) {
-      if constexpr (kDirect) {
+      if constexpr (kDirect && CARRY) {
+        // per-lane sources (global direct loads: a buffer resource cannot differ between lanes);
+        // rows past the last key re-read key S - 1, from that key's own source (masked in the
+        // scores, they must still be finite: probability 0 times the row)
+        const int ins = w + 4 * j;
+        const int pos = ins * 64 + l;
+        const int row = pos / PSEG, seg = pos - row * PSEG;
+        const int rowv = pos / PSEGV, segv = pos - rowv * PSEGV;
+        const int key = min(k0 + row, S - 1), keyv = min(k0 + rowv, S - 1);
+        const size_t sk = (size_t)key * kv_row + 8 * (seg < SEG ? seg : 0);
+        const size_t sv = (size_t)keyv * kv_row + 8 * (segv < SEG ? segv : 0);
+        if (ins < NINS) load_lds16((((fresh >> (key - k0)) & 1) ? kbase : kcbase) + sk, &sK[buf][ins * 64 * 8]);
+        if (ins < NINSV) load_lds16((((fresh >> (keyv - k0)) & 1) ? vbase : vcbase) + sv, &sV[buf][ins * 64 * 8]);
+      } else if constexpr (kDirect) {
         const int ins = w + 4 * j;  // this wave's j-th instruction of the tile
         const unsigned toff = (unsigned)((size_t)k0 * kv_row * sizeof(T));
         if (ins < NINS) buffer_load_lds16(rk, &sK[buf][ins * 64 * 8], koff[j], toff);
@@ -140,10 +167,12 @@ __global__ __launch_bounds__(256, D >= 128 ? 2 : 4) void window_attn_kernel(cons
       } else {
         const int sg = threadIdx.x + 256 * j;
         const int row = sg / SEG, part = sg - row * SEG;
-        const size_t goff = (size_t)min(k0 + row, klast - 1) * kv_row + 8 * part;
+        const int key = min(k0 + row, klast - 1);  // the key loaded, with its own source flag
+        const size_t goff = (size_t)key * kv_row + 8 * part;
+        const bool from_fresh = !CARRY || ((fresh >> ((key - k0) & 63)) & 1);  // (key - k0 < 64 where it loads)
         if (sg < KT * SEG && 8 * part < D) {
-          kreg[j] = *reinterpret_cast<const V8*>(kbase + goff);
-          vreg[j] = *reinterpret_cast<const V8*>(vbase + goff);
+          kreg[j] = *reinterpret_cast<const V8*>((from_fresh ? kbase : kcbase) + goff);
+          vreg[j] = *reinterpret_cast<const V8*>((from_fresh ? vbase : vcbase) + goff);
         } else {
 #pragma unroll
           for (int e = 0; e < 8; ++e) {
@@ -180,14 +209,26 @@ __global__ __launch_bounds__(256, D >= 128 ? 2 : 4) void window_attn_kernel(cons
   // the wave's queries in key-index space: [wlo, whi]
   const int wlo = M + wq0, whi = M + wq0 + 31;
 
-  fetch(kfirst, 0);
+  uint8_t fl = 1;  // CARRY: lane l's flag of the next tile to issue
+  uint64_t fresh = ~0ull;
+  if constexpr (CARRY) {
+    fresh = __builtin_amdgcn_ballot_w64(flag_of(kfirst) != 0);
+    fl = flag_of(kfirst + KT);
+  }
+  fetch(kfirst, 0, fresh);
   stash(0);
   __syncthreads();
   for (int it = 0; it < ntiles; ++it) {
     const int k0 = kfirst + it * KT;
     const int buf = it & 1;
     // the other buffer was last read before the previous barrier
-    if (it + 1 < ntiles) fetch(k0 + KT, buf ^ 1);
+    if (it + 1 < ntiles) {
+      if constexpr (CARRY) {
+        fresh = __builtin_amdgcn_ballot_w64(fl != 0);
+        fl = flag_of(k0 + 2 * KT);
+      }
+      fetch(k0 + KT, buf ^ 1, fresh);
+    }
 
     // skip a tile this wave's queries cannot see (wave-uniform)
     const bool seen = k0 <= whi && k0 + KT - 1 > wlo - W;
@@ -320,9 +361,22 @@ __global__ __launch_bounds__(256, D >= 128 ? 2 : 4) void window_attn_kernel(cons
 
 bool attn_width(int D) { return D == 16 || D == 32 || D == 64 || D == 128; }
 
+template <typename T, bool CARRY>
+void launch_window(dim3 grid, hipStream_t stream, const T* q, const T* keys, const T* values, T* o, float* lse,
+                   const uint8_t* active, const T* kc, const T* vc, int N, int M, int H, int HKV, int D, int W,
+                   float scale_log2, int nqt) {
+  switch (D) {
+    case 16: hipLaunchKernelGGL((window_attn_kernel<T, 16, CARRY>), grid, dim3(256), 0, stream, q, keys, values, o, lse, active, kc, vc, N, M, H, HKV, W, scale_log2, nqt); break;
+    case 32: hipLaunchKernelGGL((window_attn_kernel<T, 32, CARRY>), grid, dim3(256), 0, stream, q, keys, values, o, lse, active, kc, vc, N, M, H, HKV, W, scale_log2, nqt); break;
+    case 64: hipLaunchKernelGGL((window_attn_kernel<T, 64, CARRY>), grid, dim3(256), 0, stream, q, keys, values, o, lse, active, kc, vc, N, M, H, HKV, W, scale_log2, nqt); break;
+    default: hipLaunchKernelGGL((window_attn_kernel<T, 128, CARRY>), grid, dim3(256), 0, stream, q, keys, values, o, lse, active, kc, vc, N, M, H, HKV, W, scale_log2, nqt); break;
+  }
+}
+
 template <typename T>
 int window_attn(const T* q, const T* keys, const T* values, T* o, float* lse, const uint8_t* active, int B, int N, int M,
-                int H, int HKV, int D, int W, float scale, void* stream_ptr, const char* who) {
+                int H, int HKV, int D, int W, float scale, void* stream_ptr, const char* who, const T* kc = nullptr,
+                const T* vc = nullptr) {
   if (B < 0 || N < 0 || M < 0 || H < 1 || HKV < 1) return fail(ERR_ARG, "%s: bad sizes B=%d N=%d M=%d H=%d HKV=%d", who, B, N, M, H, HKV);
   if (H % HKV != 0) return fail(ERR_ARG, "%s: %d query heads are not a multiple of %d KV heads", who, H, HKV);
   if (W < 1) return fail(ERR_ARG, "%s: window must be at least 1, got %d", who, W);
@@ -334,6 +388,12 @@ int window_attn(const T* q, const T* keys, const T* values, T* o, float* lse, co
        reinterpret_cast<uintptr_t>(o)) & 15)
     return fail(ERR_ARG, "%s: q, keys, values and o must be 16-byte aligned", who);
   if (reinterpret_cast<uintptr_t>(lse) & 3) return fail(ERR_ARG, "%s: lse must be 4-byte aligned", who);
+  if (kc != nullptr || vc != nullptr) {
+    if (!kc || !vc) return fail(ERR_ARG, "%s: the carried keys and values come together", who);
+    if (!active) return fail(ERR_ARG, "%s: carried keys and values need the active flags", who);
+    if ((reinterpret_cast<uintptr_t>(kc) | reinterpret_cast<uintptr_t>(vc)) & 15)
+      return fail(ERR_ARG, "%s: the carried keys and values must be 16-byte aligned", who);
+  }
   // one batch row's keys (all KV heads) are addressed with 32-bit byte offsets
   if ((size_t)(M + N) * HKV * D * sizeof(T) >= ((size_t)1 << 32))
     return fail(ERR_UNSUPPORTED, "%s: %d keys x %d KV heads x %d features exceed 4 GiB per batch row", who, M + N, HKV, D);
@@ -341,12 +401,10 @@ int window_attn(const T* q, const T* keys, const T* values, T* o, float* lse, co
   const int nqt = (N + 127) / 128;
   dim3 grid((unsigned)((size_t)nqt * H * B));
   hipStream_t stream = reinterpret_cast<hipStream_t>(stream_ptr);
-  switch (D) {
-    case 16: hipLaunchKernelGGL((window_attn_kernel<T, 16>), grid, dim3(256), 0, stream, q, keys, values, o, lse, active, N, M, H, HKV, W, scale_log2, nqt); break;
-    case 32: hipLaunchKernelGGL((window_attn_kernel<T, 32>), grid, dim3(256), 0, stream, q, keys, values, o, lse, active, N, M, H, HKV, W, scale_log2, nqt); break;
-    case 64: hipLaunchKernelGGL((window_attn_kernel<T, 64>), grid, dim3(256), 0, stream, q, keys, values, o, lse, active, N, M, H, HKV, W, scale_log2, nqt); break;
-    default: hipLaunchKernelGGL((window_attn_kernel<T, 128>), grid, dim3(256), 0, stream, q, keys, values, o, lse, active, N, M, H, HKV, W, scale_log2, nqt); break;
-  }
+  if (kc != nullptr)
+    launch_window<T, true>(grid, stream, q, keys, values, o, lse, active, kc, vc, N, M, H, HKV, D, W, scale_log2, nqt);
+  else
+    launch_window<T, false>(grid, stream, q, keys, values, o, lse, active, kc, vc, N, M, H, HKV, D, W, scale_log2, nqt);
   return check_launch(who);
 }
 
@@ -381,4 +439,24 @@ extern "C" int vsp_window_attn_lse_f16(const void* q, const void* keys, const vo
   return vsp::window_attn<_Float16>(static_cast<const _Float16*>(q), static_cast<const _Float16*>(keys),
                                     static_cast<const _Float16*>(values), static_cast<_Float16*>(o), lse, active, B, N,
                                     M, H, HKV, D, window, scale, stream, "vsp_window_attn_lse_f16");
+}
+
+extern "C" int vsp_window_attn_carried_bf16(const void* q, const void* keys, const void* values, const void* keys_carried,
+                                            const void* values_carried, void* o, const uint8_t* active, int B, int N,
+                                            int M, int H, int HKV, int D, int window, float scale, void* stream) {
+  using T = __bf16;
+  return vsp::window_attn<T>(static_cast<const T*>(q), static_cast<const T*>(keys), static_cast<const T*>(values),
+                             static_cast<T*>(o), nullptr, active, B, N, M, H, HKV, D, window, scale, stream,
+                             "vsp_window_attn_carried_bf16", static_cast<const T*>(keys_carried),
+                             static_cast<const T*>(values_carried));
+}
+
+extern "C" int vsp_window_attn_carried_f16(const void* q, const void* keys, const void* values, const void* keys_carried,
+                                           const void* values_carried, void* o, const uint8_t* active, int B, int N,
+                                           int M, int H, int HKV, int D, int window, float scale, void* stream) {
+  using T = _Float16;
+  return vsp::window_attn<T>(static_cast<const T*>(q), static_cast<const T*>(keys), static_cast<const T*>(values),
+                             static_cast<T*>(o), nullptr, active, B, N, M, H, HKV, D, window, scale, stream,
+                             "vsp_window_attn_carried_f16", static_cast<const T*>(keys_carried),
+                             static_cast<const T*>(values_carried));
 }

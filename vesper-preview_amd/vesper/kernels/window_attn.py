@@ -11,7 +11,11 @@ the C ABI with the cache offset as an argument, so nothing is padded.
 For: bfloat16 or float16 on the GPU with consecutive positions (the window counts indices, as the
 reference's kernel does; ``WindowedAttention.attend`` checks the positions before calling).
 An optional keyword ``active`` (bool ``[b, n]``) skips inactive queries, whose outputs are zero;
-their keys and values stay visible to every other query. Under autograd the forward also keeps
+their keys and values stay visible to every other query. With ``active``, ``carried = (keys,
+values)`` (``[b, n, hkv, dk]``) is the copy-forward of halted tokens (``vesper/column.py:795-796``):
+key rows ``m + t`` of an inactive token ``t`` are read from row ``t`` of the carried tensors inside
+the kernel's tile loads (``vsp_window_attn_carried_*``), in place of ``where`` merges before the
+call. Under autograd the forward also keeps
 each query's log-sum-exp and the backward (``vsp_window_attn_backward_*``) gives the gradients of
 ``q``, ``keys`` and ``values`` (an inactive query passes none), as the reference's kernel does.
 """
@@ -82,13 +86,30 @@ class _WindowAttention(torch.autograd.Function):
                 dv if ctx.needs_input_grad[2] else None, None, None)
 
 
-def window_attention(q: Tensor, keys: Tensor, values: Tensor, window: int, *, active: Tensor | None = None) -> Tensor:
+def _carried_call(q: Tensor, keys: Tensor, values: Tensor, carried: tuple[Tensor, Tensor], window: int,
+                  mask: Tensor) -> Tensor:
+    b, n, h, dk = q.shape
+    s, hkv = keys.shape[1], keys.shape[2]
+    qc, kc, vc = _aligned(q), _aligned(keys), _aligned(values)
+    kh, vh = _aligned(carried[0]), _aligned(carried[1])
+    o = torch.empty_like(qc)
+    suffix = "bf16" if q.dtype == torch.bfloat16 else "f16"
+    with torch.cuda.device(q.device):
+        _lib.call(f"vsp_window_attn_carried_{suffix}", qc.data_ptr(), kc.data_ptr(), vc.data_ptr(), kh.data_ptr(),
+                  vh.data_ptr(), o.data_ptr(), mask.data_ptr(), b, n, s - n, h, hkv, dk, int(window),
+                  1.0 / math.sqrt(dk), _lib.stream_of(q.device))
+    return o
+
+
+def window_attention(q: Tensor, keys: Tensor, values: Tensor, window: int, *, active: Tensor | None = None,
+                     carried: tuple[Tensor, Tensor] | None = None) -> Tensor:
     """Outputs ``[b, n, h, dk]`` of ``q`` over ``keys, values [b, m + n, hkv, dk]``.
 
     Raises:
         ContractError: on shapes that disagree, a dtype other than bfloat16/float16 (or mixed), a
             tensor off the GPU, ``h`` not a multiple of ``hkv``, a head width the kernel does not
-            tile, or fewer key rows than queries.
+            tile, fewer key rows than queries, or carried keys and values without ``active`` or not
+            shaped ``[b, n, hkv, dk]`` in the dtype of ``keys``.
         ValueError: if ``window`` is below 1.
     """
     if window < 1:
@@ -122,5 +143,21 @@ def window_attention(q: Tensor, keys: Tensor, values: Tensor, window: int, *, ac
         if active.device != q.device:
             raise ContractError(f"active is on {active.device}, q on {q.device}")
         mask = active.contiguous().view(torch.uint8)
+    if carried is not None:
+        if active is None or mask is None:
+            raise ContractError("carried keys and values need the active mask that says which tokens read them")
+        if len(carried) != 2:
+            raise ContractError(f"carried holds keys and values, got {len(carried)} tensors")
+        for name, held in zip(("keys", "values"), carried):
+            if held.shape != (b, n, hkv, dk) or held.dtype != q.dtype or held.device != q.device:
+                raise ContractError(f"carried {name}: {tuple(held.shape)} {held.dtype} on {held.device}, "
+                                    f"want {(b, n, hkv, dk)} {q.dtype} on {q.device}")
+        if n > 0 and not (torch.is_grad_enabled() and any(t.requires_grad for t in (q, keys, values, *carried))):
+            return _carried_call(q, keys, values, carried, window, mask)
+        # under autograd the merge is explicit, so the gradient reaches the carried tensors
+        keep = active.reshape(b, n, 1, 1)
+        m = s - n
+        keys = torch.cat([keys[:, :m], torch.where(keep, keys[:, m:], carried[0])], dim=1)
+        values = torch.cat([values[:, :m], torch.where(keep, values[:, m:], carried[1])], dim=1)
     out: Tensor = _WindowAttention.apply(q, keys, values, int(window), mask)
     return out
