@@ -183,6 +183,17 @@ int vsp_key_filter_f16(const void* z, const float* history, const float* taps, v
                        int heads, int K, void* stream);
 int vsp_key_filter_f32(const float* z, const float* history, const float* taps, float* keys, int B, int N, int D,
                        int heads, int K, void* stream);
+/* Copy-forward fused into the filter's loads (the carry merge of the key inputs before the filter,
+ * vesper/column.py:779-782: `where(active, z, z_carried)`): as vsp_key_filter_*, but token t's
+ * input row (as the current token and in the halo of later ones) is z_carried's row t where
+ * active[b, t] == 0. `active` and `z_carried` ([B, N, D], z's dtype) are required; the rows of z
+ * for inactive tokens are never read. */
+int vsp_key_filter_carried_bf16(const void* z, const void* z_carried, const uint8_t* active, const float* history,
+                                const float* taps, void* keys, int B, int N, int D, int heads, int K, void* stream);
+int vsp_key_filter_carried_f16(const void* z, const void* z_carried, const uint8_t* active, const float* history,
+                               const float* taps, void* keys, int B, int N, int D, int heads, int K, void* stream);
+int vsp_key_filter_carried_f32(const float* z, const float* z_carried, const uint8_t* active, const float* history,
+                               const float* taps, float* keys, int B, int N, int D, int heads, int K, void* stream);
 
 /* The key filter's backward (vesper/kernels/keys.py:46-78, `_FusedKeys.backward`, on CUDA
  * vesper/kernels/keys_triton.py:56-177): from grad_keys [B, N, D] (z's dtype), with the
@@ -201,6 +212,16 @@ int vsp_key_filter_backward_f16(const void* z, const float* history, const float
 int vsp_key_filter_backward_f32(const float* z, const float* history, const float* taps, const float* grad_keys,
                                 float* grad_z, float* grad_taps, float* grad_history, void* workspace,
                                 size_t workspace_bytes, int B, int N, int D, int heads, int K, void* stream);
+
+/* ---- copy-forward bookkeeping of the looped column ------------------------------------------
+ * Replaces the row-wise `where` selects of vesper/loop.py:523-537 (`_merge`: tokens halting now
+ * freeze their fresh projections into the carried ones) and vesper/loop.py:441-452 (a halted
+ * token's hidden state carried forward): for each of `count` (0..8) tensors of `rows` rows of
+ * row_bytes[i] bytes, dst[i][r] = src[i][r] where flags[i][r] != 0, in place, one launch; the
+ * rows whose flag is 0 are neither read nor written. src, dst, row_bytes, flags are host arrays of
+ * `count` entries; the device buffers hold rows * row_bytes[i] bytes each. */
+int vsp_copy_rows_where(int count, const void* const* src, void* const* dst, const size_t* row_bytes,
+                        const uint8_t* const* flags, int rows, void* stream);
 
 #ifdef __cplusplus
 }

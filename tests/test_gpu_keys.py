@@ -265,3 +265,53 @@ def test_an_empty_chunk_has_zero_gradients():
     gz, gh, gt = torch.autograd.grad(keys.sum(), (z, history, taps), allow_unused=True)
     assert gz.shape == z.shape
     assert torch.equal(gh, torch.zeros_like(gh)) and torch.equal(gt, torch.zeros_like(gt))
+
+
+# ---- copy-forward inside the filter's loads (carried key inputs of inactive tokens) ----
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+@pytest.mark.parametrize(("n", "width", "head_dim"), [(3, 4, 64), (40, 1, 16), (257, 4, 64), (300, 8, 128)])
+def test_carried_key_inputs_equal_the_merged_ones_bitwise(dtype, n, width, head_dim):
+    from vesper.column import recurrent_keys
+
+    b, heads = 2, 2
+    d = heads * head_dim
+    g = torch.Generator().manual_seed(n + width)
+    z = torch.randn(b, n, d, generator=g).to(GPU, dtype)
+    zc = torch.randn(b, n, d, generator=g).to(GPU, dtype)
+    history = torch.randn(b, width - 1, d, generator=g).to(GPU)
+    taps = _taps(d, width).to(GPU)
+    active = (torch.rand(b, n, generator=g) > 0.4).to(GPU)
+    merged = torch.where(active[..., None], z, zc)
+    poisoned = z.masked_fill(~active[..., None], float("nan"))  # fresh inputs of inactive tokens: never read
+    keys, hist = recurrent_keys(poisoned, history, taps, heads, active=active, carried_z=zc)
+    want_keys, want_hist = recurrent_keys(merged, history, taps, heads)
+    torch.cuda.synchronize()
+    assert torch.equal(keys, want_keys)
+    assert torch.equal(hist, want_hist)
+
+
+def test_carried_key_inputs_at_b8_t4096_d512_h8_k4():
+    from vesper.kernels.keys import fused_keys
+
+    b, n, d, heads = 8, 4096, 512, 8
+    g = torch.Generator().manual_seed(5)
+    z, zc = (torch.randn(b, n, d, generator=g).to(GPU, torch.bfloat16) for _ in range(2))
+    history = torch.randn(b, K - 1, d, generator=g).to(GPU)
+    taps = _taps(d).to(GPU)
+    active = (torch.rand(b, n, generator=g) > 0.3).to(GPU)
+    got = fused_keys(z, history, taps, heads, active=active, carried_z=zc)
+    want = fused_keys(torch.where(active[..., None], z, zc), history, taps, heads)
+    assert torch.equal(got, want)
+
+
+def test_carried_key_inputs_under_autograd_reach_the_carried_tensor():
+    from vesper.kernels.keys import fused_keys
+
+    b, n, d, heads = 2, 50, 64, 1
+    g = torch.Generator().manual_seed(6)
+    z, zc = (torch.randn(b, n, d, generator=g).to(GPU).requires_grad_() for _ in range(2))
+    history = torch.randn(b, K - 1, d, generator=g).to(GPU)
+    active = (torch.rand(b, n, generator=g) > 0.4).to(GPU)
+    fused_keys(z, history, _taps(d).to(GPU), heads, active=active, carried_z=zc).square().sum().backward()
+    assert not bool(z.grad[~active].any()) and not bool(zc.grad[active].any()) and bool(zc.grad.any())

@@ -133,3 +133,74 @@ def test_the_loop_with_a_key_filter_matches_the_oracle():
     for t in range(passes):
         assert relative_error(got.states[t], want.states[t][0]) < 3e-2, t
         assert relative_error(got.histories[t], want.states[t][1]) < 1e-2, t
+
+
+# ---- copy-forward inside the kernels' loads against the where merges ----
+
+def _both_modes(b, n, d, h, hkv, dk, w, passes, seed, key_conv=0, p_halt=0.3):
+    from vesper.loop import LoopedColumn
+
+    fused = LoopedColumn.random(d, h, hkv, dk, w, passes, seed, GPU, key_conv=key_conv)
+    where = LoopedColumn.random(d, h, hkv, dk, w, passes, seed, GPU, key_conv=key_conv, copy_forward="where")
+    g = torch.Generator().manual_seed(seed + 1)
+    x0 = torch.randn(b, n, d, generator=g).to(GPU)
+    exits = [(torch.rand(b, n, generator=g) < p_halt).to(GPU) for _ in range(passes)]
+    states = [(0.02 * torch.randn(b, h, dk, dk, generator=g)).to(GPU) for _ in range(passes)]
+    histories = [torch.randn(b, key_conv - 1, d, generator=g).to(GPU) for _ in range(passes)] if key_conv else None
+    return fused.forward(x0, states, exits, histories), where.forward(x0, states, exits, histories), x0
+
+
+@pytest.mark.parametrize(("key_conv", "p_halt"), [(0, 0.3), (4, 0.3), (4, 0.8), (2, 0.05)])
+def test_fused_copy_forward_equals_the_where_merges_bitwise(key_conv, p_halt):
+    got, want, x0 = _both_modes(2, 300, 128, 2, 2, 64, 64, 4, seed=21 + key_conv, key_conv=key_conv, p_halt=p_halt)
+    assert torch.equal(got.y, want.y)
+    assert torch.equal(got.n_iters, want.n_iters)
+    for a, b in zip(got.states, want.states):
+        assert torch.equal(a, b)
+    if key_conv:
+        for a, b in zip(got.histories, want.histories):
+            assert torch.equal(a, b)
+    assert not torch.equal(got.y, x0.float())  # the input is left as it was, and the passes changed it
+
+
+def test_fused_copy_forward_at_b4_t2048_d512_h8_eight_passes():
+    got, want, _ = _both_modes(4, 2048, 512, 8, 8, 64, 512, 8, seed=31, key_conv=4, p_halt=0.2)
+    assert torch.equal(got.y, want.y) and torch.equal(got.n_iters, want.n_iters)
+    for a, b in zip(got.states, want.states):
+        assert torch.equal(a, b)
+
+
+def test_copy_rows_where_equals_torch_where_bitwise():
+    from vesper.kernels.carry import copy_rows_where
+
+    g = torch.Generator().manual_seed(3)
+    b, n = 3, 77
+    flags = [(torch.rand(b, n, generator=g) < 0.4).to(GPU) for _ in range(3)]
+    shapes = [((b, n, 4, 16), torch.bfloat16), ((b, n, 3), torch.bfloat16), ((b, n, 96), torch.float32),
+              ((b, n, 5), torch.uint8)]
+    items, want = [], []
+    for i, (shape, dtype) in enumerate(shapes):
+        src = (torch.randn(shape, generator=g) * 100).to(dtype).to(GPU)
+        dst = (torch.randn(shape, generator=g) * 100).to(dtype).to(GPU)
+        f = flags[i % 3]
+        want.append(torch.where(f.reshape(b, n, *([1] * (len(shape) - 2))), src, dst))
+        items.append((src, dst, f))
+    copy_rows_where(items)
+    for (_, dst, _), ref in zip(items, want):
+        assert torch.equal(dst, ref)
+
+
+def test_copy_rows_where_refusals():
+    from vesper.contracts import ContractError
+    from vesper.kernels.carry import copy_rows_where
+
+    x = torch.zeros(2, 5, 8, device=GPU)
+    f = torch.ones(2, 5, dtype=torch.bool, device=GPU)
+    with pytest.raises(ContractError, match="at most"):
+        copy_rows_where([(x, x.clone(), f)] * 9)
+    with pytest.raises(ContractError, match="flags"):
+        copy_rows_where([(x, x.clone(), f.float())])
+    with pytest.raises(ContractError, match="contiguous"):
+        copy_rows_where([(x[:, :, :4], x.clone()[:, :, ::2], f)])
+    with pytest.raises(ContractError, match="token rows"):
+        copy_rows_where([(x, x.clone(), f), (x[:1], x[:1].clone(), f[:1])])

@@ -90,14 +90,16 @@ def recurrent_scan(impl: str, q: Tensor, k: Tensor, v: Tensor, beta: Tensor, sta
     return o.to(q.dtype), new_state
 
 
-def recurrent_keys(z: Tensor, history: Tensor, taps: Tensor | None, heads: int) -> tuple[Tensor, Tensor]:
+def recurrent_keys(z: Tensor, history: Tensor, taps: Tensor | None, heads: int, *, active: Tensor | None = None,
+                   carried_z: Tensor | None = None) -> tuple[Tensor, Tensor]:
     """Normalized keys ``[b, n, heads, d / heads]`` of key inputs ``z [b, n, d]`` and the next history.
 
     With a filter (``taps [K, d]``) the key of token ``t`` is ``normalize_keys`` per head of
     ``sum_r taps[r] * z[t - r]``, the positions before the chunk from ``history [b, K-1, d]``
     (oldest first); the next history is the newest ``K - 1`` inputs of ``(history, z)`` as an owned
     float32 copy. With no filter (``taps`` None) the key is ``normalize_keys(z)`` and the history
-    object passes through; so it does for an empty chunk.
+    object passes through; so it does for an empty chunk. ``carried_z`` with ``active`` replaces the
+    key inputs of inactive tokens, in the keys (inside the kernel's loads) and in the next history.
 
     Raises:
         ContractError: as ``fused_keys``.
@@ -107,8 +109,12 @@ def recurrent_keys(z: Tensor, history: Tensor, taps: Tensor | None, heads: int) 
         if n == 0:
             return z.new_empty(b, 0, heads, d // heads), history
         ones = torch.ones(1, d, dtype=torch.float32, device=z.device)
-        return fused_keys(z, z.new_empty(b, 0, d, dtype=torch.float32), ones, heads), history
+        return fused_keys(z, z.new_empty(b, 0, d, dtype=torch.float32), ones, heads, active=active,
+                          carried_z=carried_z), history
     width = int(taps.shape[0])
-    keys = fused_keys(z, history, taps, heads)
-    tail = z[:, max(0, n - (width - 1)):].to(torch.float32)
-    return keys, torch.cat([history.to(torch.float32)[:, n:], tail], dim=1)
+    keys = fused_keys(z, history, taps, heads, active=active, carried_z=carried_z)
+    first = max(0, n - (width - 1))
+    tail = z[:, first:]
+    if carried_z is not None and active is not None:
+        tail = torch.where(active[:, first:, None], tail, carried_z[:, first:])
+    return keys, torch.cat([history.to(torch.float32)[:, n:], tail.to(torch.float32)], dim=1)

@@ -1,0 +1,71 @@
+"""The looped column's copy-forward bookkeeping on MI355X: flagged token rows copied in place.
+
+``copy_rows_where(items)`` performs, for each ``(src, dst, flags)``, ``dst[flags] = src[flags]``
+over the leading ``[b, n]`` token dimensions, every item in one kernel launch
+(``vsp_copy_rows_where``). It stands in for the row-wise ``where`` selects of the reference's
+pass loop: the freezing of the projections of the tokens that halt now into the carried ones
+(``vesper/loop.py:523-537``, ``_merge``) and the carried hidden state of halted tokens
+(``vesper/loop.py:441-452``). Only flagged rows are read and written.
+"""
+
+from __future__ import annotations
+
+import ctypes
+from collections.abc import Sequence
+
+import torch
+from torch import Tensor
+
+from vesper.contracts import ContractError
+from vesper.kernels import _lib
+
+MAX_ITEMS = 8  # tensors per launch
+
+
+def copy_rows_where(items: Sequence[tuple[Tensor, Tensor, Tensor]]) -> None:
+    """``dst[flags] = src[flags]`` in place for each ``(src, dst, flags)``, one launch for all.
+
+    Args:
+        items: up to eight triples on one GPU: ``src`` and ``dst`` of one shape and dtype with
+            leading dimensions ``[b, n]`` (``dst`` contiguous: it is written in place), ``flags``
+            bool ``[b, n]``; every item has the same ``b * n``.
+
+    Raises:
+        ContractError: on more than eight items, shapes, dtypes or devices that disagree, or a
+            ``dst`` that is not contiguous.
+    """
+    if len(items) > MAX_ITEMS:
+        raise ContractError(f"{len(items)} tensors: at most {MAX_ITEMS} per launch")
+    if not items:
+        return
+    device = items[0][1].device
+    rows = None
+    srcs, dsts, flags, sizes = [], [], [], []
+    for i, (src, dst, flag) in enumerate(items):
+        if src.shape != dst.shape or src.dtype != dst.dtype:
+            raise ContractError(f"item {i}: src {tuple(src.shape)} {src.dtype}, dst {tuple(dst.shape)} {dst.dtype}")
+        if flag.dtype != torch.bool or flag.dim() != 2 or tuple(dst.shape[:2]) != tuple(flag.shape):
+            raise ContractError(f"item {i}: flags must be bool {tuple(dst.shape[:2])}, got {tuple(flag.shape)} {flag.dtype}")
+        if any(t.device != device for t in (src, dst, flag)) or device.type != "cuda":
+            raise ContractError(f"item {i}: every tensor must be on one GPU ({device})")
+        if not dst.is_contiguous():
+            raise ContractError(f"item {i}: dst must be contiguous (it is written in place)")
+        n_rows = flag.numel()
+        if rows is None:
+            rows = n_rows
+        elif rows != n_rows:
+            raise ContractError(f"item {i}: {n_rows} token rows, the first item has {rows}")
+        src_c, flag_c = src.contiguous(), flag.contiguous()
+        srcs.append(src_c)
+        dsts.append(dst)
+        flags.append(flag_c)
+        sizes.append(dst.numel() * dst.element_size() // max(n_rows, 1))
+    count = len(items)
+    src_arr = (ctypes.c_void_p * count)(*[t.data_ptr() for t in srcs])
+    dst_arr = (ctypes.c_void_p * count)(*[t.data_ptr() for t in dsts])
+    flag_arr = (ctypes.c_void_p * count)(*[t.data_ptr() for t in flags])
+    size_arr = (ctypes.c_size_t * count)(*sizes)
+    with torch.cuda.device(device):
+        _lib.call("vsp_copy_rows_where", count, ctypes.cast(src_arr, ctypes.c_void_p),
+                  ctypes.cast(dst_arr, ctypes.c_void_p), ctypes.cast(size_arr, ctypes.c_void_p),
+                  ctypes.cast(flag_arr, ctypes.c_void_p), int(rows or 0), _lib.stream_of(device))

@@ -1,0 +1,86 @@
+// The looped column's copy-forward bookkeeping on CDNA4 (gfx950): token rows copied where a flag is set.
+//
+// Reference: vesper/loop.py:523-537 (`_merge`: the tokens halting now freeze their fresh
+// projections into the carried ones, six `where`s per column and pass) and vesper/loop.py:441-452
+// (a halted token's hidden state is carried forward, `where(active, h, x)`). Each is a select over
+// whole token rows. Here one launch copies the flagged rows of up to eight tensors in place,
+// dst[r] = src[r] where flags[r] != 0: only the flagged rows are read and written.
+#include "common.h"
+#include "vesper_kernels.h"
+
+namespace vsp {
+namespace {
+
+constexpr int kMaxItems = 8;
+
+struct CopyItems {
+  const uint8_t* src[kMaxItems];
+  uint8_t* dst[kMaxItems];
+  const uint8_t* flags[kMaxItems];
+  unsigned row_units[kMaxItems];       // copy units per row
+  unsigned unit_log2[kMaxItems];       // a unit is 1 << unit_log2 bytes (1 .. 16)
+  unsigned first_block[kMaxItems + 1]; // the item's first workgroup; first_block[count] = the grid
+  int count;
+};
+
+template <typename U>
+__device__ __forceinline__ void copy_unit(const uint8_t* src, uint8_t* dst, size_t u) {
+  reinterpret_cast<U*>(dst)[u] = reinterpret_cast<const U*>(src)[u];
+}
+
+// 256 consecutive units of one item per workgroup (the item is found from the block index, the
+// same for the whole workgroup)
+__global__ __launch_bounds__(256) void copy_rows_kernel(const CopyItems items, unsigned rows) {
+  int i = 0;
+  while (i + 1 < items.count && blockIdx.x >= items.first_block[i + 1]) ++i;
+  const unsigned per = items.row_units[i];
+  const size_t u = (size_t)(blockIdx.x - items.first_block[i]) * 256 + threadIdx.x;
+  if (u >= (size_t)rows * per) return;
+  if (items.flags[i][u / per] == 0) return;
+  const uint8_t* s = items.src[i];
+  uint8_t* d = items.dst[i];
+  switch (items.unit_log2[i]) {
+    case 4: copy_unit<uint4>(s, d, u); break;
+    case 3: copy_unit<uint2>(s, d, u); break;
+    case 2: copy_unit<uint32_t>(s, d, u); break;
+    case 1: copy_unit<uint16_t>(s, d, u); break;
+    default: copy_unit<uint8_t>(s, d, u); break;
+  }
+}
+
+}  // namespace
+}  // namespace vsp
+
+extern "C" int vsp_copy_rows_where(int count, const void* const* src, void* const* dst, const size_t* row_bytes,
+                                   const uint8_t* const* flags, int rows, void* stream) {
+  using namespace vsp;
+  const char* who = "vsp_copy_rows_where";
+  if (count < 0 || count > kMaxItems) return fail(ERR_ARG, "%s: %d tensors (1 .. %d per launch)", who, count, kMaxItems);
+  if (rows < 0) return fail(ERR_ARG, "%s: %d rows", who, rows);
+  if (count == 0 || rows == 0) return OK;
+  if (!src || !dst || !row_bytes || !flags) return fail(ERR_ARG, "%s: null array", who);
+  CopyItems items{};
+  items.count = count;
+  size_t blocks = 0;
+  for (int i = 0; i < count; ++i) {
+    if (!src[i] || !dst[i] || !flags[i]) return fail(ERR_ARG, "%s: null pointer in tensor %d", who, i);
+    if (row_bytes[i] == 0) return fail(ERR_ARG, "%s: tensor %d has empty rows", who, i);
+    const uintptr_t mix = reinterpret_cast<uintptr_t>(src[i]) | reinterpret_cast<uintptr_t>(dst[i]) | row_bytes[i];
+    unsigned lg = 4;
+    while (lg > 0 && (mix & ((1u << lg) - 1)) != 0) --lg;
+    const size_t per = row_bytes[i] >> lg;
+    if (per > 0xFFFFFFFFu) return fail(ERR_UNSUPPORTED, "%s: rows of %zu bytes", who, row_bytes[i]);
+    items.src[i] = static_cast<const uint8_t*>(src[i]);
+    items.dst[i] = static_cast<uint8_t*>(dst[i]);
+    items.flags[i] = flags[i];
+    items.row_units[i] = (unsigned)per;
+    items.unit_log2[i] = lg;
+    items.first_block[i] = (unsigned)blocks;
+    blocks += ((size_t)rows * per + 255) / 256;
+    if (blocks > 0x7FFFFFFFu) return fail(ERR_UNSUPPORTED, "%s: the copy exceeds the launch grid", who);
+  }
+  items.first_block[count] = (unsigned)blocks;
+  hipLaunchKernelGGL(copy_rows_kernel, dim3((unsigned)blocks), dim3(256), 0, reinterpret_cast<hipStream_t>(stream), items,
+                     (unsigned)rows);
+  return check_launch(who);
+}

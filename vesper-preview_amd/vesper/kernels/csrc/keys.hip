@@ -24,9 +24,14 @@ namespace {
 // row: the token's row offset is scalar, and a lane past D gets a vector offset beyond the range,
 // so its reads return zeros and its writes are dropped (whole heads idle together: D is a multiple
 // of the head width).
-template <typename TZ, int K, int LPH>
+// CARRY (copy-forward of halted tokens' key inputs, vesper/column.py:779-782): token t's input row
+// is zc's row t where active[b, t] == 0, z's row t elsewhere; the rows before the chunk always
+// come from the history. A row's source is wave-uniform (all lanes of a wave hold one token), so
+// both are loaded, the unused one from past its range, and joined bitwise.
+template <typename TZ, int K, int LPH, bool CARRY>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))) void key_filter_kernel(const TZ* __restrict__ z, const float* __restrict__ history,
-                                                         const float* __restrict__ taps, TZ* __restrict__ out, int N,
+                                                         const float* __restrict__ taps, TZ* __restrict__ out,
+                                                         const uint8_t* __restrict__ active, const TZ* zc, int N,
                                                          int D) {
   using Row = Row8<TZ>;
   constexpr int RUN = Row::kRun;
@@ -44,6 +49,19 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))) voi
   constexpr unsigned kPast = 0x80000000u;  // a vector offset past every range (ranges stay below 2^31)
   const unsigned voff = on ? (unsigned)f0 * sizeof(TZ) : kPast;
   const int fl = on ? f0 : 0;  // taps: idle lanes read feature 0's (never stored)
+  // CARRY: lane j holds the flag of token t_begin - (K - 1) + j (clamped into the batch row), so
+  // row t's flag is lane t - t_begin + K - 1 of it, read into a scalar
+  const auto rzc = buffer_rsrc(CARRY ? zc + (size_t)b * N * D : z, batch_bytes);
+  int flags = 1;
+  if constexpr (CARRY) flags = active[(size_t)b * N + min(max(t_begin - (K - 1) + l, 0), N - 1)];
+  auto load_row = [&](unsigned v, unsigned soff, int lane_of_flag) {
+    if constexpr (!CARRY) {
+      return Row::load(rz, v, soff);
+    } else {
+      const bool fresh = __builtin_amdgcn_readlane(flags, lane_of_flag) != 0;
+      return Row::join(Row::load(rz, fresh ? v : kPast, soff), Row::load(rzc, fresh ? kPast : v, soff));
+    }
+  };
 
   // Loads in the order of use (vmcnt counts in issue order): the taps, the K - 1 rows before the
   // run, then the run's rows, so token i waits only for its own row.
@@ -70,7 +88,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))) voi
 #pragma unroll
     for (int r = 1; r < K; ++r) {
       float zr[8], hr[8];
-      Row::unpack(Row::load(rz, vz, first ? 0u : (unsigned)(t_begin - r) * row_bytes), zr);
+      Row::unpack(load_row(vz, first ? 0u : (unsigned)(t_begin - r) * row_bytes, K - 1 - r), zr);
       Row8<float>::unpack(Row8<float>::load(rh, vh, (unsigned)(K - 1 - r) * D * 4u), hr);
 #pragma unroll
       for (int e = 0; e < 8; ++e) win[r - 1][e] = __uint_as_float(__float_as_uint(zr[e]) | __float_as_uint(hr[e]));
@@ -78,7 +96,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))) voi
   }
   typename Row::Raw raw[RUN];  // rows past N (a short last run) re-read row N - 1
 #pragma unroll
-  for (int i = 0; i < RUN; ++i) raw[i] = Row::load(rz, voff, (unsigned)min(t_begin + i, N - 1) * row_bytes);
+  for (int i = 0; i < RUN; ++i) raw[i] = load_row(voff, (unsigned)min(t_begin + i, N - 1) * row_bytes, K - 1 + i);
 
 #pragma unroll
   for (int i = 0; i < RUN; ++i) {
@@ -126,25 +144,38 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))) voi
   }
 }
 
-template <typename TZ, int K>
-void launch_k(const TZ* z, const float* history, const float* taps, TZ* out, int B, int N, int D, int hd,
-              hipStream_t stream) {
+template <typename TZ, int K, bool CARRY>
+void launch_k(const TZ* z, const float* history, const float* taps, TZ* out, const uint8_t* active, const TZ* zc,
+              int B, int N, int D, int hd, hipStream_t stream) {
   constexpr int per_block = 4 * Row8<TZ>::kRun;
   dim3 grid((unsigned)((D / 8 + 63) / 64), (unsigned)((N + per_block - 1) / per_block), (unsigned)B);
+#define VSP_KEY_LAUNCH(LPH)                                                                                          \
+  hipLaunchKernelGGL((key_filter_kernel<TZ, K, LPH, CARRY>), grid, dim3(256), 0, stream, z, history, taps, out, active, \
+                     zc, N, D)
   switch (hd / 8) {
-    case 1: hipLaunchKernelGGL((key_filter_kernel<TZ, K, 1>), grid, dim3(256), 0, stream, z, history, taps, out, N, D); break;
-    case 2: hipLaunchKernelGGL((key_filter_kernel<TZ, K, 2>), grid, dim3(256), 0, stream, z, history, taps, out, N, D); break;
-    case 4: hipLaunchKernelGGL((key_filter_kernel<TZ, K, 4>), grid, dim3(256), 0, stream, z, history, taps, out, N, D); break;
-    case 8: hipLaunchKernelGGL((key_filter_kernel<TZ, K, 8>), grid, dim3(256), 0, stream, z, history, taps, out, N, D); break;
-    case 16: hipLaunchKernelGGL((key_filter_kernel<TZ, K, 16>), grid, dim3(256), 0, stream, z, history, taps, out, N, D); break;
-    case 32: hipLaunchKernelGGL((key_filter_kernel<TZ, K, 32>), grid, dim3(256), 0, stream, z, history, taps, out, N, D); break;
-    default: hipLaunchKernelGGL((key_filter_kernel<TZ, K, 64>), grid, dim3(256), 0, stream, z, history, taps, out, N, D); break;
+    case 1: VSP_KEY_LAUNCH(1); break;
+    case 2: VSP_KEY_LAUNCH(2); break;
+    case 4: VSP_KEY_LAUNCH(4); break;
+    case 8: VSP_KEY_LAUNCH(8); break;
+    case 16: VSP_KEY_LAUNCH(16); break;
+    case 32: VSP_KEY_LAUNCH(32); break;
+    default: VSP_KEY_LAUNCH(64); break;
   }
+#undef VSP_KEY_LAUNCH
+}
+
+template <typename TZ, int K>
+void launch_k(const TZ* z, const float* history, const float* taps, TZ* out, const uint8_t* active, const TZ* zc,
+              int B, int N, int D, int hd, hipStream_t stream) {
+  if (zc != nullptr)
+    launch_k<TZ, K, true>(z, history, taps, out, active, zc, B, N, D, hd, stream);
+  else
+    launch_k<TZ, K, false>(z, history, taps, out, active, zc, B, N, D, hd, stream);
 }
 
 template <typename TZ>
 int key_filter(const TZ* z, const float* history, const float* taps, TZ* out, int B, int N, int D, int heads, int K,
-               void* stream_ptr, const char* who) {
+               void* stream_ptr, const char* who, const uint8_t* active = nullptr, const TZ* zc = nullptr) {
   if (B < 0 || N < 0 || D < 1 || heads < 1) return fail(ERR_ARG, "%s: bad sizes B=%d N=%d D=%d heads=%d", who, B, N, D, heads);
   if (K < 1 || K > 8) return fail(ERR_UNSUPPORTED, "%s: filter width %d (kernels: 1..8)", who, K);
   if (D % heads != 0) return fail(ERR_ARG, "%s: %d features are not a multiple of %d heads", who, D, heads);
@@ -160,16 +191,18 @@ int key_filter(const TZ* z, const float* history, const float* taps, TZ* out, in
   if ((reinterpret_cast<uintptr_t>(z) | reinterpret_cast<uintptr_t>(out) | reinterpret_cast<uintptr_t>(taps) |
        reinterpret_cast<uintptr_t>(history)) & 15)
     return fail(ERR_ARG, "%s: z, history, taps and the output must be 16-byte aligned", who);
+  if (zc != nullptr && (!active || (reinterpret_cast<uintptr_t>(zc) & 15)))
+    return fail(ERR_ARG, "%s: carried key inputs need the active flags and 16-byte alignment", who);
   hipStream_t stream = reinterpret_cast<hipStream_t>(stream_ptr);
   switch (K) {
-    case 1: launch_k<TZ, 1>(z, history, taps, out, B, N, D, hd, stream); break;
-    case 2: launch_k<TZ, 2>(z, history, taps, out, B, N, D, hd, stream); break;
-    case 3: launch_k<TZ, 3>(z, history, taps, out, B, N, D, hd, stream); break;
-    case 4: launch_k<TZ, 4>(z, history, taps, out, B, N, D, hd, stream); break;
-    case 5: launch_k<TZ, 5>(z, history, taps, out, B, N, D, hd, stream); break;
-    case 6: launch_k<TZ, 6>(z, history, taps, out, B, N, D, hd, stream); break;
-    case 7: launch_k<TZ, 7>(z, history, taps, out, B, N, D, hd, stream); break;
-    default: launch_k<TZ, 8>(z, history, taps, out, B, N, D, hd, stream); break;
+    case 1: launch_k<TZ, 1>(z, history, taps, out, active, zc, B, N, D, hd, stream); break;
+    case 2: launch_k<TZ, 2>(z, history, taps, out, active, zc, B, N, D, hd, stream); break;
+    case 3: launch_k<TZ, 3>(z, history, taps, out, active, zc, B, N, D, hd, stream); break;
+    case 4: launch_k<TZ, 4>(z, history, taps, out, active, zc, B, N, D, hd, stream); break;
+    case 5: launch_k<TZ, 5>(z, history, taps, out, active, zc, B, N, D, hd, stream); break;
+    case 6: launch_k<TZ, 6>(z, history, taps, out, active, zc, B, N, D, hd, stream); break;
+    case 7: launch_k<TZ, 7>(z, history, taps, out, active, zc, B, N, D, hd, stream); break;
+    default: launch_k<TZ, 8>(z, history, taps, out, active, zc, B, N, D, hd, stream); break;
   }
   return check_launch(who);
 }
@@ -271,4 +304,27 @@ extern "C" int vsp_key_filter_f32(const float* z, const float* history, const fl
 
 extern "C" size_t vsp_key_filter_backward_workspace_bytes(int B, int N, int D, int K) {
   return vsp::key_backward_workspace(B, N, D, K);
+}
+
+extern "C" int vsp_key_filter_carried_bf16(const void* z, const void* z_carried, const uint8_t* active,
+                                           const float* history, const float* taps, void* keys, int B, int N, int D,
+                                           int heads, int K, void* stream) {
+  return vsp::key_filter<__bf16>(static_cast<const __bf16*>(z), history, taps, static_cast<__bf16*>(keys), B, N, D,
+                                 heads, K, stream, "vsp_key_filter_carried_bf16", active,
+                                 static_cast<const __bf16*>(z_carried));
+}
+
+extern "C" int vsp_key_filter_carried_f16(const void* z, const void* z_carried, const uint8_t* active,
+                                          const float* history, const float* taps, void* keys, int B, int N, int D,
+                                          int heads, int K, void* stream) {
+  return vsp::key_filter<_Float16>(static_cast<const _Float16*>(z), history, taps, static_cast<_Float16*>(keys), B, N,
+                                   D, heads, K, stream, "vsp_key_filter_carried_f16", active,
+                                   static_cast<const _Float16*>(z_carried));
+}
+
+extern "C" int vsp_key_filter_carried_f32(const float* z, const float* z_carried, const uint8_t* active,
+                                          const float* history, const float* taps, float* keys, int B, int N, int D,
+                                          int heads, int K, void* stream) {
+  return vsp::key_filter<float>(z, history, taps, keys, B, N, D, heads, K, stream, "vsp_key_filter_carried_f32", active,
+                                z_carried);
 }

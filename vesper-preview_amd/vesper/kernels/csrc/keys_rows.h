@@ -20,6 +20,8 @@ template <> struct Row8<float> {
   __device__ __forceinline__ static Raw load(__amdgpu_buffer_rsrc_t r, unsigned voff, unsigned soff) {
     return Raw{__builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0), __builtin_amdgcn_raw_buffer_load_b128(r, voff + 16u, soff, 0)};
   }
+  // two loads of which at most one was in range (the other read zeros), joined bitwise: exact
+  __device__ __forceinline__ static Raw join(const Raw& x, const Raw& y) { return Raw{x.a | y.a, x.b | y.b}; }
   __device__ __forceinline__ static void unpack(const Raw& r, float (&x)[8]) {
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
@@ -38,6 +40,7 @@ template <typename H8> struct Row8Half {
   __device__ __forceinline__ static Raw load(__amdgpu_buffer_rsrc_t r, unsigned voff, unsigned soff) {
     return __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0);
   }
+  __device__ __forceinline__ static Raw join(const Raw& x, const Raw& y) { return x | y; }
   __device__ __forceinline__ static void unpack(const Raw& r, float (&x)[8]) {
     const H8 h = __builtin_bit_cast(H8, r);
 #pragma unroll

@@ -10,6 +10,11 @@ and ``vsp_key_filter_backward_*`` (the gradients of ``z``, ``taps`` and, when it
 
 For: float32, bfloat16 or float16 key inputs on the GPU, a filter of 1 to 8 taps, head widths that
 are powers of two from 8 to 512.
+
+With ``active`` and ``carried_z`` (the copy-forward of halted tokens' key inputs, selected before the
+filter, ``vesper/column.py:779-782``) the kernel reads token ``t``'s input row from ``carried_z``
+where ``active[:, t]`` is false, inside its loads (``vsp_key_filter_carried_*``), in place of a
+``where`` merge before the call.
 """
 
 from __future__ import annotations
@@ -99,19 +104,47 @@ class _FusedKeys(torch.autograd.Function):
                 grad_taps.to(taps_dtype) if ctx.needs_input_grad[2] else None, None)
 
 
-def fused_keys(z: Tensor, history: Tensor, taps: Tensor, heads: int) -> Tensor:
+def _carried_keys(z: Tensor, history: Tensor, taps: Tensor, heads: int, active: Tensor, carried_z: Tensor) -> Tensor:
+    b, n, d, width = _check(z, history, taps, heads)
+    zc, held = _aligned(z), _aligned(carried_z)
+    hist = _aligned(history.to(torch.float32))
+    wide = _aligned(taps.to(torch.float32))
+    flags = active.contiguous().view(torch.uint8)
+    out = torch.empty(b, n, heads, d // heads, dtype=z.dtype, device=z.device)
+    if b and n:
+        _lib.call(f"vsp_key_filter_carried_{_SUFFIX[z.dtype]}", _lib.ptr(zc), _lib.ptr(held), _lib.ptr(flags),
+                  _lib.ptr(hist) if width > 1 else None, _lib.ptr(wide), _lib.ptr(out), b, n, d, heads, width,
+                  _lib.stream_of(z.device))
+    return out
+
+
+def fused_keys(z: Tensor, history: Tensor, taps: Tensor, heads: int, *, active: Tensor | None = None,
+               carried_z: Tensor | None = None) -> Tensor:
     """Normalized keys ``[b, n, heads, d / heads]`` in ``z``'s dtype (``z [b, n, d]`` on the GPU).
 
     ``history [b, K-1, d]`` holds the ``K - 1`` key inputs before the chunk (oldest first) and
     ``taps [K, d]`` the filter, tap 0 on the current token; both are used in float32. Under autograd
     the gradients of ``z`` (in its dtype), ``taps`` and ``history`` (in theirs) come from the
-    backward kernel.
+    backward kernel. ``carried_z`` (shaped and typed as ``z``, with ``active`` bool ``[b, n]``)
+    replaces the key inputs of inactive tokens.
 
     Raises:
         ContractError: on shapes that disagree, a dtype outside float32/bfloat16/float16, tensors
             off the GPU or on different devices, a filter wider than 8 taps, or a head width that
-            is not a power of two in 8..512.
+            is not a power of two in 8..512; carried key inputs without ``active`` or unlike ``z``.
     """
     _check(z, history, taps, heads)  # the contract first, before autograd records anything
+    if carried_z is not None:
+        if active is None:
+            raise ContractError("carried key inputs need the active mask that says which tokens read them")
+        if carried_z.shape != z.shape or carried_z.dtype != z.dtype or carried_z.device != z.device:
+            raise ContractError(f"carried_z: {tuple(carried_z.shape)} {carried_z.dtype} on {carried_z.device}, "
+                                f"z is {tuple(z.shape)} {z.dtype} on {z.device}")
+        check_shape("active", active, ("b", "n"), {"b": z.shape[0], "n": z.shape[1]}, torch.bool)
+        if active.device != z.device:
+            raise ContractError(f"active is on {active.device}, z on {z.device}")
+        if not (torch.is_grad_enabled() and any(t.requires_grad for t in (z, history, taps, carried_z))):
+            return _carried_keys(z, history, taps, heads, active, carried_z)
+        z = torch.where(active[..., None], z, carried_z)  # under autograd: the merge, explicit
     out: Tensor = _FusedKeys.apply(z, history, taps, heads)
     return out

@@ -16,8 +16,14 @@ order of ``Column.step`` (``vesper/column.py:709-812``):
 
 The loop zeroes inactive outputs, freezes the projections of tokens as they halt and writes them
 into every later pass's state (copy-forward), and carries halted tokens' hidden states forward
-unchanged (``loop.py:441-453``, ``:523-537``). All passes run even when no token is active any
-more. Norms, rotary embeddings and the FFN are not part of the mixer path and are left out. The residual stream stays in float32 (autocast's convention); matmuls and mixers run
+unchanged (``loop.py:441-453``, ``:523-537``). By default (``copy_forward="fused"``) the kernels read
+the carried rows of inactive tokens inside their loads (the key filter's ``carried_z``, the scan's
+``carried``, the attention's ``carried``) and one launch per pass (``copy_rows_where``) freezes the
+halting tokens' projections into the carried buffers and carries the hidden state, in place of the
+reference's ``where`` merges; ``copy_forward="where"`` runs those merges as torch selects.
+
+All passes run even when no token is active any more. Norms, rotary embeddings and the FFN are not
+part of the mixer path and are left out. The residual stream stays in float32 (autocast's convention); matmuls and mixers run
 in bfloat16 with the scan state in float32. Forward only.
 """
 
@@ -31,6 +37,7 @@ from torch import Tensor
 
 from vesper.column import recurrent_keys
 from vesper.contracts import ContractError, Dims, check_shape
+from vesper.kernels.carry import copy_rows_where
 from vesper.kernels.delta_scan import delta_scan_fused
 from vesper.kernels.window_attn import window_attention
 
@@ -87,7 +94,7 @@ class LoopedColumn:
     """
 
     def __init__(self, weights: dict[str, Sequence[Tensor]], heads: int, kv_heads: int, head_dim: int,
-                 window: int, taps: Sequence[Tensor] | None = None) -> None:
+                 window: int, taps: Sequence[Tensor] | None = None, copy_forward: str = "fused") -> None:
         names = ("wq", "wk", "wv", "wb", "waq", "wak", "wav")
         missing = [n for n in names if n not in weights]
         if missing:
@@ -100,6 +107,9 @@ class LoopedColumn:
         if taps is not None and len(taps) != self.passes:
             raise ValueError("the key filter needs one set of taps per pass")
         self.taps = None if taps is None else list(taps)
+        if copy_forward not in ("fused", "where"):
+            raise ValueError(f"copy_forward is 'fused' or 'where', got {copy_forward!r}")
+        self.copy_forward = copy_forward
 
     @property
     def key_history(self) -> int:
@@ -108,7 +118,7 @@ class LoopedColumn:
 
     @classmethod
     def random(cls, d: int, heads: int, kv_heads: int, head_dim: int, window: int, passes: int, seed: int,
-               device: torch.device, key_conv: int = 0) -> LoopedColumn:
+               device: torch.device, key_conv: int = 0, copy_forward: str = "fused") -> LoopedColumn:
         """Fixed random weights ~ N(0, 1/d) from a CPU generator (the same values on any device);
         with ``key_conv`` a filter of that width, taps ~ U(-1/sqrt(K), 1/sqrt(K)) as the
         reference draws them (``column.py:231-233``)."""
@@ -124,15 +134,17 @@ class LoopedColumn:
             bound = 1.0 / key_conv**0.5
             taps = [(torch.rand(key_conv, heads * head_dim, generator=g) * (2 * bound) - bound).to(device)
                     for _ in range(passes)]
-        return cls(weights, heads, kv_heads, head_dim, window, taps)
+        return cls(weights, heads, kv_heads, head_dim, window, taps, copy_forward)
 
-    def keys(self, t: int, z: Tensor, history: Tensor | None) -> tuple[Tensor, Tensor | None]:
-        """Pass ``t``'s keys of key inputs ``z [b, n, h*dk]`` (bf16) and the next key history."""
+    def keys(self, t: int, z: Tensor, history: Tensor | None, active: Tensor | None = None,
+             carried_z: Tensor | None = None) -> tuple[Tensor, Tensor | None]:
+        """Pass ``t``'s keys of key inputs ``z [b, n, h*dk]`` (bf16) and the next key history
+        (with ``carried_z``, inactive tokens' inputs come from it)."""
         b, n, _ = z.shape
         if self.taps is None:
             return _normalize(z.view(b, n, self.heads, self.head_dim)).to(BF16), history
         assert history is not None
-        return recurrent_keys(z, history, self.taps[t], self.heads)
+        return recurrent_keys(z, history, self.taps[t], self.heads, active=active, carried_z=carried_z)
 
     def _step(self, x: Tensor, t: int, state: Tensor, history: Tensor | None, active: Tensor | None,
               carried: Written | None) -> tuple[Tensor, Tensor, Tensor | None, Written]:
@@ -141,25 +153,37 @@ class LoopedColumn:
         xb = x.to(BF16)
         q = _normalize((xb @ self.w["wq"][t]).view(b, n, h, dk)).to(BF16)
         z = xb @ self.w["wk"][t]
-        if carried is not None and active is not None and carried.z is not None:
+        fused = self.copy_forward == "fused" and carried is not None and active is not None
+        where = self.copy_forward == "where" and carried is not None and active is not None
+        if where and carried is not None and active is not None and carried.z is not None:
             z = _where_tokens(active, z, carried.z)  # a halted token's frozen key input, before the filter
-        k, history = self.keys(t, z, history)
+        if fused and carried is not None and carried.z is not None:
+            k, history = self.keys(t, z, history, active, carried.z)  # the filter reads carried inputs
+        else:
+            k, history = self.keys(t, z, history)
         v = (xb @ self.w["wv"][t]).view(b, n, h, dk)
         beta = torch.sigmoid((xb @ self.w["wb"][t]).float()).to(BF16)
-        if carried is not None and active is not None:
+        if where and carried is not None and active is not None:
             k = _where_tokens(active, k, carried.k)
             v = _where_tokens(active, v, carried.v)
             beta = _where_tokens(active, beta, carried.beta)
-        r, new_state = delta_scan_fused(q, k, v, beta, state, active=active)
+        if fused and carried is not None:  # the scan reads inactive tokens' k, v, beta from the carried ones
+            r, new_state = delta_scan_fused(q, k, v, beta, state, active=active,
+                                            carried=(carried.k, carried.v, carried.beta))
+        else:
+            r, new_state = delta_scan_fused(q, k, v, beta, state, active=active)
         x1 = x + r.reshape(b, n, h * dk).float()
         x1b = x1.to(BF16)
         aq = (x1b @ self.w["waq"][t]).view(b, n, h, dk)
         ak = (x1b @ self.w["wak"][t]).view(b, n, hkv, dk)
         av = (x1b @ self.w["wav"][t]).view(b, n, hkv, dk)
-        if carried is not None and active is not None:
+        if where and carried is not None and active is not None:
             ak = _where_tokens(active, ak, carried.attn_k)
             av = _where_tokens(active, av, carried.attn_v)
-        a = window_attention(aq, ak, av, self.window, active=active)
+        if fused and carried is not None:
+            a = window_attention(aq, ak, av, self.window, active=active, carried=(carried.attn_k, carried.attn_v))
+        else:
+            a = window_attention(aq, ak, av, self.window, active=active)
         x2 = x1 + a.reshape(b, n, h * dk).float()
         written = Written(k=k, v=v, beta=beta, attn_k=ak, attn_v=av, z=z if self.taps is not None else None)
         return x2, new_state, history, written
@@ -205,11 +229,26 @@ class LoopedColumn:
                 mask = None if carried is None else active
                 h, new_states[t], new_histories[t], written = self._step(x, t, new_states[t], new_histories[t], mask,
                                                                          carried)
-                h = _where_tokens(active, h, torch.zeros_like(h))
                 halts = active & exits[t] if t < self.passes - 1 else active
                 n_iters += active.to(torch.int32)
-                carried = written if carried is None else written.merged(halts, carried)
-                x = _where_tokens(active, h, x)
+                if carried is None:  # pass 0: every token active, the fresh projections are the carried ones
+                    carried, x = written, h
+                elif self.copy_forward == "where":
+                    h = _where_tokens(active, h, torch.zeros_like(h))
+                    carried = written.merged(halts, carried)
+                    x = _where_tokens(active, h, x)
+                else:
+                    # one launch: the tokens halting now freeze their fresh projections into the
+                    # carried buffers (none after the last pass), and the active tokens' hidden
+                    # states move into x (x is this loop's own buffer from pass 1 on)
+                    items: list[tuple[Tensor, Tensor, Tensor]] = []
+                    if t < self.passes - 1:
+                        items = [(written.k, carried.k, halts), (written.v, carried.v, halts),
+                                 (written.beta, carried.beta, halts), (written.attn_k, carried.attn_k, halts),
+                                 (written.attn_v, carried.attn_v, halts)]
+                        if written.z is not None and carried.z is not None:
+                            items.append((written.z, carried.z, halts))
+                    copy_rows_where([*items, (h, x, active)])
                 active = active & ~halts
         hist_out = tuple(t for t in new_histories if t is not None) if self.taps is not None else None
         return LoopResult(y=x, states=tuple(new_states), n_iters=n_iters, histories=hist_out)
