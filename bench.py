@@ -359,27 +359,33 @@ def time_decode(torch, reps: int = 5) -> dict:
 
 def time_looped(torch, reps: int = 3) -> dict:
     """The looped column with halting: B4 T2048 d512 H8 d64, 8 passes, window 512, 4-tap key filter,
-    p_halt 0.3."""
+    p_halt 0.3; the copy-forward fused into the kernels' loads (the default) and, for comparison,
+    as where merges."""
     from vesper.loop import LoopedColumn
 
     dev = torch.device("cuda:0")
     b, n, d, h, dk, passes = LOOP_B, LOOP_T, LOOP_D, H, D, LOOP_PASSES
-    column = LoopedColumn.random(d, h, h, dk, WINDOW, passes, seed=11, device=dev, key_conv=KEY_TAPS)
     g = torch.Generator().manual_seed(12)
     x0 = torch.randn(b, n, d, generator=g).to(dev)
     exits = [(torch.rand(b, n, generator=g) < 0.3).to(dev) for _ in range(passes)]
     states = [torch.zeros(b, h, dk, dk, device=dev) for _ in range(passes)]
     histories = [torch.zeros(b, KEY_TAPS - 1, d, device=dev) for _ in range(passes)]
-    column.forward(x0, states, exits, histories)  # warm-up
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    e0.record()
-    for _ in range(reps):
-        out = column.forward(x0, states, exits, histories)
-    e1.record()
-    torch.cuda.synchronize()
-    ms = e0.elapsed_time(e1) / reps
-    return {"ms": ms, "tok_s": b * n / (ms / 1e3), "mean_passes": float(out.n_iters.float().mean())}
+    result = {}
+    for mode in ("fused", "where"):
+        column = LoopedColumn.random(d, h, h, dk, WINDOW, passes, seed=11, device=dev, key_conv=KEY_TAPS,
+                                     copy_forward=mode)
+        column.forward(x0, states, exits, histories)  # warm-up
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        e0.record()
+        for _ in range(reps):
+            out = column.forward(x0, states, exits, histories)
+        e1.record()
+        torch.cuda.synchronize()
+        result[mode] = e0.elapsed_time(e1) / reps
+    ms = result["fused"]
+    return {"ms": ms, "ms_where": result["where"], "tok_s": b * n / (ms / 1e3),
+            "mean_passes": float(out.n_iters.float().mean())}
 
 
 def time_column_decode(torch, steps: int = 64) -> dict:
@@ -626,6 +632,8 @@ def main() -> int:
                         "+ delta scan + window attention (w512) with bf16 projections (fixed N(0, 1/512) weights), "
                         "p_halt 0.3, copy-forward of halted tokens",
             "tok_s": round(looped["tok_s"], 1), "ms": round(looped["ms"], 3),
+            "copy_forward": "fused into the kernels' loads; one row-copy launch per pass",
+            "ms_with_where_merges": round(looped["ms_where"], 3),
             "mean_active_passes": round(looped["mean_passes"], 3),
         }
     if not args.no_cpu_baseline:
