@@ -66,6 +66,19 @@ __device__ __forceinline__ f32x4 mm16(const float* X, int ldx, const float* Y, i
   return acc;
 }
 
+// mm16 over the k blocks kb0 .. kb1 - 1 of 16 (k = 16 kb0 .. 16 kb1 - 1): the part of a product
+// that a triangular operand leaves nonzero. Same operand conventions as mm16.
+template <bool TA, bool TB>
+__device__ __forceinline__ f32x4 mm16k(const float* X, int ldx, const float* Y, int ldy, int kb0, int kb1, f32x4 acc,
+                                       const float* yscale = nullptr) {
+  for (int kb = kb0; kb < kb1; ++kb) {
+    const int k0 = 16 * kb;
+    acc = mm16<TA, TB>(TA ? X + k0 * ldx : X + k0, ldx, TB ? Y + k0 : Y + k0 * ldy, ldy, 16, acc,
+                       yscale != nullptr ? yscale + k0 : nullptr);
+  }
+  return acc;
+}
+
 // Within a wave, LDS writes of any lane are visible to later LDS reads of any lane.
 __device__ __forceinline__ void wave_sync_lds() {
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -465,8 +478,11 @@ __global__ __launch_bounds__(256) void scan_bwd_dstate_kernel(const TIn* __restr
     d_state_in[(size_t)bh * D * D + (e / 16) * D + 16 * s + e % 16] = sG[(e / 16) * kPS + e % 16];
 }
 
-// Eight waves: wave w owns row block 16 (w % 4) of every [64 x .] result and every other column
-// tile from w / 4, so two waves share each SIMD and hide each other's LDS and MFMA latency.
+// Eight waves, two per SIMD, hiding each other's LDS and MFMA latency: wave w owns row block rb
+// of every [64 x .] result and every other column tile from ch = w / 4. Waves w and w + 4 (one
+// SIMD) own row blocks rb and 3 - rb: the triangular products (whose tiles and k ranges grow with
+// the row block) then load every SIMD about evenly. Tiles that a triangular factor makes zero are
+// not computed, and each product runs over the k blocks its triangular operand leaves nonzero.
 constexpr int kChunkThreads = 512;
 
 template <typename TIn, int D>
@@ -483,7 +499,7 @@ __global__ __launch_bounds__(kChunkThreads) void scan_bwd_chunk_kernel(
   const int b = bh / H, h = bh - b * H;
   const int t0 = c * kC;
   const size_t chunk = blockIdx.x;
-  const int w = threadIdx.x >> 6, rb = w & 3, ch = w >> 2;
+  const int w = threadIdx.x >> 6, ch = w >> 2, rb = ch == 0 ? w : 7 - w;
   float *Bq = buf[0], *Bk = buf[1], *Bo = buf[2], *Br = buf[3], *Bh = buf[4], *Bg = buf[5], *Bl = buf[6];
   float *Bd = buf[7], *Bp = buf[8];
   {
@@ -516,9 +532,9 @@ __global__ __launch_bounds__(kChunkThreads) void scan_bwd_chunk_kernel(
 #pragma unroll
     for (int r = 0; r < 4; ++r) Br[(r0 + tile_row(r)) * P + 16 * ct + tile_col()] -= acc[r];
   }
-  // P = tril(Q K^T), diagonal included
+  // P = tril(Q K^T), diagonal included (tiles above the diagonal: zeros)
   for (int ct = ch; ct < 4; ct += 2) {
-    const f32x4 acc = mm16<false, true>(Bq + r0 * P, P, Bk + 16 * ct * P, P, D, zero4());
+    const f32x4 acc = ct <= rb ? mm16<false, true>(Bq + r0 * P, P, Bk + 16 * ct * P, P, D, zero4()) : zero4();
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int i = r0 + tile_row(r), j = 16 * ct + tile_col();
@@ -526,9 +542,9 @@ __global__ __launch_bounds__(kChunkThreads) void scan_bwd_chunk_kernel(
     }
   }
   __syncthreads();
-  // Delta = L diag(beta) R
+  // Delta = L diag(beta) R (L lower triangular: k blocks 0 .. rb)
   for (int ct = ch; ct < NT; ct += 2) {
-    const f32x4 acc = mm16<false, false>(Bl + r0 * P, P, Br + 16 * ct, P, kC, zero4(), sB);
+    const f32x4 acc = mm16k<false, false>(Bl + r0 * P, P, Br + 16 * ct, P, 0, rb + 1, zero4(), sB);
 #pragma unroll
     for (int r = 0; r < 4; ++r) Bd[(r0 + tile_row(r)) * P + 16 * ct + tile_col()] = acc[r];
   }
@@ -542,7 +558,7 @@ __global__ __launch_bounds__(kChunkThreads) void scan_bwd_chunk_kernel(
     const int ct = ch + 2 * u;
     if (ct < NT) {
       ddl[u] = mm16<false, false>(Bk + r0 * P, P, Bg + 16 * ct, P, D, zero4());
-      ddl[u] = mm16<true, false>(Bp + r0, P, Bo + 16 * ct, P, kC, ddl[u]);
+      ddl[u] = mm16k<true, false>(Bp + r0, P, Bo + 16 * ct, P, rb, 4, ddl[u]);  // P^T: k blocks rb .. 3
       dka[u] = mm16<false, true>(Bd + r0 * P, P, Bg + 16 * ct * P, P, D, zero4());
     }
   }
@@ -559,7 +575,7 @@ __global__ __launch_bounds__(kChunkThreads) void scan_bwd_chunk_kernel(
   // dR = diag(beta) L^T dDelta into P's buffer (free now); dV = dR
   float* Bdr = Bp;
   for (int ct = ch; ct < NT; ct += 2) {
-    const f32x4 acc = mm16<true, false>(Bl + r0, P, Bdd + 16 * ct, P, kC, zero4());
+    const f32x4 acc = mm16k<true, false>(Bl + r0, P, Bdd + 16 * ct, P, rb, 4, zero4());  // L^T: k blocks rb .. 3
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int i = r0 + tile_row(r), j = 16 * ct + tile_col();
@@ -580,10 +596,10 @@ __global__ __launch_bounds__(kChunkThreads) void scan_bwd_chunk_kernel(
     }
   }
   __syncthreads();  // the reads of dR are done
-  // S2 = tril(dO Delta^T), diagonal included, into dR's buffer
+  // S2 = tril(dO Delta^T), diagonal included, into dR's buffer (tiles above the diagonal: zeros)
   float* Bs = Bp;
   for (int ct = ch; ct < 4; ct += 2) {
-    const f32x4 acc = mm16<false, true>(Bo + r0 * P, P, Bd + 16 * ct * P, P, D, zero4());
+    const f32x4 acc = ct <= rb ? mm16<false, true>(Bo + r0 * P, P, Bd + 16 * ct * P, P, D, zero4()) : zero4();
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int i = r0 + tile_row(r), j = 16 * ct + tile_col();
@@ -597,21 +613,21 @@ __global__ __launch_bounds__(kChunkThreads) void scan_bwd_chunk_kernel(
     const int ct = ch + 2 * u;
     if (ct < NT) {
       f32x4 acc = mm16<false, true>(Bo + r0 * P, P, Bh + 16 * ct * P, P, D, zero4());
-      acc = mm16<false, false>(Bs + r0 * P, P, Bk + 16 * ct, P, kC, acc);
+      acc = mm16k<false, false>(Bs + r0 * P, P, Bk + 16 * ct, P, 0, rb + 1, acc);  // S2: k blocks 0 .. rb
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int i = r0 + tile_row(r), j = 16 * ct + tile_col();
         if (t0 + i < N) dq[(((size_t)b * N + t0 + i) * H + h) * D + j] = from_f32<TIn>(acc[r]);
       }
-      dka[u] = mm16<true, false>(Bs + r0, P, Bq + 16 * ct, P, kC, dka[u]);
+      dka[u] = mm16k<true, false>(Bs + r0, P, Bq + 16 * ct, P, rb, 4, dka[u]);  // S2^T: k blocks rb .. 3
     }
   }
   __syncthreads();  // H, dO, Q, S2, Delta are done with
   // dT = dDelta R^T. dbeta_j gets sum_i dT_ij L_ij (L is zero above its diagonal): each wave sums
   // its 16 rows of its columns into sPart; dL = tril(dT) diag(beta) goes into H's buffer
   float* Bt = Bh;
-  for (int ct = ch; ct < 4; ct += 2) {
-    const f32x4 acc = mm16<false, true>(Bdd + r0 * P, P, Br + 16 * ct * P, P, D, zero4());
+  for (int ct = ch; ct < 4; ct += 2) {  // (tiles above the diagonal: dL is zero there, and so is L)
+    const f32x4 acc = ct <= rb ? mm16<false, true>(Bdd + r0 * P, P, Br + 16 * ct * P, P, D, zero4()) : zero4();
     const int j = 16 * ct + tile_col();
     float part = 0.f;
 #pragma unroll
@@ -624,10 +640,10 @@ __global__ __launch_bounds__(kChunkThreads) void scan_bwd_chunk_kernel(
     if ((threadIdx.x & 63) < 16) sPart[rb * kC + j] = part;
   }
   __syncthreads();
-  // X1 = L^T dL into Q's buffer
+  // X1 = L^T dL into Q's buffer (L^T upper, dL lower triangular: k blocks max(rb, ct) .. 3)
   float* Bx = Bq;
   for (int ct = ch; ct < 4; ct += 2) {
-    const f32x4 acc = mm16<true, false>(Bl + r0, P, Bt + 16 * ct, P, kC, zero4());
+    const f32x4 acc = mm16k<true, false>(Bl + r0, P, Bt + 16 * ct, P, max(rb, ct), 4, zero4());
 #pragma unroll
     for (int r = 0; r < 4; ++r) Bx[(r0 + tile_row(r)) * P + 16 * ct + tile_col()] = acc[r];
   }
@@ -637,7 +653,13 @@ __global__ __launch_bounds__(kChunkThreads) void scan_bwd_chunk_kernel(
   float* Ba = Bo;
   float rows[4] = {0.f, 0.f, 0.f, 0.f};
   for (int ct = ch; ct < 4; ct += 2) {
-    const f32x4 acc = mm16<false, true>(Bx + r0 * P, P, Bl + 16 * ct * P, P, kC, zero4());
+    if (ct > rb) {  // strictly above the diagonal: dA and M are zero
+#pragma unroll
+      for (int r = 0; r < 4; ++r) Ba[(r0 + tile_row(r)) * P + 16 * ct + tile_col()] = 0.f;
+      continue;
+    }
+    // L^T column block ct: k blocks 0 .. ct
+    const f32x4 acc = mm16k<false, true>(Bx + r0 * P, P, Bl + 16 * ct * P, P, 0, ct + 1, zero4());
     const f32x4 gk = mm16<false, true>(Bk + r0 * P, P, Bk + 16 * ct * P, P, D, zero4());
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
@@ -658,8 +680,8 @@ __global__ __launch_bounds__(kChunkThreads) void scan_bwd_chunk_kernel(
   for (int u = 0; u < NTW; ++u) {
     const int ct = ch + 2 * u;
     if (ct < NT) {
-      dka[u] = mm16<false, false>(Ba + r0 * P, P, Bk + 16 * ct, P, kC, dka[u]);
-      dka[u] = mm16<true, false>(Ba + r0, P, Bk + 16 * ct, P, kC, dka[u]);
+      dka[u] = mm16k<false, false>(Ba + r0 * P, P, Bk + 16 * ct, P, 0, rb + 1, dka[u]);  // M: k blocks 0 .. rb
+      dka[u] = mm16k<true, false>(Ba + r0, P, Bk + 16 * ct, P, rb, 4, dka[u]);         // M^T: k blocks rb .. 3
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int i = r0 + tile_row(r), j = 16 * ct + tile_col();
