@@ -192,8 +192,12 @@ template <int D> struct Ws {
   }
 };
 
+// Eight waves in the chunk kernel's arrangement: wave w owns row block rb (rb and 3 - rb on one
+// SIMD) and every other column tile from ch = w / 4; triangular zeros are skipped.
+constexpr int kPrepThreads = 512;
+
 template <typename TIn, int D>
-__global__ __launch_bounds__(256) void scan_bwd_prep_kernel(const TIn* __restrict__ q, const TIn* __restrict__ k,
+__global__ __launch_bounds__(kPrepThreads) void scan_bwd_prep_kernel(const TIn* __restrict__ q, const TIn* __restrict__ k,
                                                             const TIn* __restrict__ v, const TIn* __restrict__ beta,
                                                             const TIn* __restrict__ d_o,
                                                             const uint8_t* __restrict__ active,
@@ -206,28 +210,29 @@ __global__ __launch_bounds__(256) void scan_bwd_prep_kernel(const TIn* __restric
   const int b = bh / H, h = bh - b * H;
   const int t0 = c * kC;
   const size_t chunk = blockIdx.x;
-  const int w = threadIdx.x >> 6;
+  constexpr int NTH = kPrepThreads, NT = D / 16;
+  const int w = threadIdx.x >> 6, ch = w >> 2, rb = ch == 0 ? w : 7 - w, r0 = 16 * rb;
   {
-    ChunkRows<TIn, D> rk, rq, ro, rv;
-    ChunkBeta<TIn> rb;
+    ChunkRows<TIn, D, NTH> rk, rq, ro, rv;
+    ChunkBeta<TIn> rbeta;
     rk.fetch(k, b, h, t0, N, H);
     rq.fetch(q, b, h, t0, N, H);
     ro.fetch(d_o, b, h, t0, N, H, active);
     rv.fetch(v, b, h, t0, N, H);
-    rb.fetch(beta, b, h, t0, N, H);
+    rbeta.fetch(beta, b, h, t0, N, H);
     rk.put(sK, PD, t0, N);
     rq.put(sQ, PD, t0, N);
     ro.put(sO, PD, t0, N);
     rv.put(sV, PD, t0, N);
-    rb.put(sB, t0, N);
+    rbeta.put(sB, t0, N);
   }
   __syncthreads();
-  // A = tril(diag(beta) K K^T, -1)
-  for (int ct = 0; ct < 4; ++ct) {
-    const f32x4 acc = mm16<false, true>(sK + 16 * w * PD, PD, sK + 16 * ct * PD, PD, D, zero4());
+  // A = tril(diag(beta) K K^T, -1) (tiles above the diagonal: zeros)
+  for (int ct = ch; ct < 4; ct += 2) {
+    const f32x4 acc = ct <= rb ? mm16<false, true>(sK + r0 * PD, PD, sK + 16 * ct * PD, PD, D, zero4()) : zero4();
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      const int i = 16 * w + tile_row(r), j = 16 * ct + tile_col();
+      const int i = r0 + tile_row(r), j = 16 * ct + tile_col();
       sA[i * kPC + j] = i > j ? sB[i] * acc[r] : 0.f;
     }
   }
@@ -236,7 +241,7 @@ __global__ __launch_bounds__(256) void scan_bwd_prep_kernel(const TIn* __restric
   // lane per column of a block), then L_ij = -L_ii sum_{m = j}^{i - 1} A_im L_mj level by level
   // (i - j = 1, 2, 3) on MFMA; the blocks above the diagonal are zero
 #pragma unroll
-  for (int e = threadIdx.x; e < kC * kC / 4; e += kThreads) {  // four zeros a thread and step
+  for (int e = threadIdx.x; e < kC * kC / 4; e += NTH) {  // four zeros a thread and step
     const int i = e / (kC / 4), j = 4 * (e % (kC / 4));
     if (i / 16 < j / 16) *reinterpret_cast<f32x4*>(sL + i * kPC + j) = zero4();
   }
@@ -256,7 +261,7 @@ __global__ __launch_bounds__(256) void scan_bwd_prep_kernel(const TIn* __restric
   }
   __syncthreads();
   for (int lev = 1; lev < 4; ++lev) {
-    const int i = w + lev, j = w;  // block (i, j) of this level, one per wave
+    const int i = w + lev, j = w;  // block (i, j) of this level, one per wave (waves 0 .. 2)
     if (i < 4) {
       f32x4 y = zero4();
       for (int m = j; m < i; ++m)
@@ -276,42 +281,42 @@ __global__ __launch_bounds__(256) void scan_bwd_prep_kernel(const TIn* __restric
   }
   float* gL = Ws<D>::L(ws, chunk);
 #pragma unroll
-  for (int e = threadIdx.x; e < kC * kC / 4; e += kThreads)
+  for (int e = threadIdx.x; e < kC * kC / 4; e += NTH)
     *reinterpret_cast<f32x4*>(gL + 4 * e) = *reinterpret_cast<const f32x4*>(sL + (e / (kC / 4)) * kPC + 4 * (e % (kC / 4)));
-  // W = L diag(beta) K and U = L diag(beta) V (rows 16 w of the wave)
+  // W = L diag(beta) K and U = L diag(beta) V (L lower triangular: k blocks 0 .. rb)
   float* gW = Ws<D>::W(ws, chunk);
   float* gU = Ws<D>::U(ws, chunk);
-  for (int ct = 0; ct < D / 16; ++ct) {
-    const f32x4 aw = mm16<false, false>(sL + 16 * w * kPC, kPC, sK + 16 * ct, PD, kC, zero4(), sB);
-    const f32x4 au = mm16<false, false>(sL + 16 * w * kPC, kPC, sV + 16 * ct, PD, kC, zero4(), sB);
+  for (int ct = ch; ct < NT; ct += 2) {
+    const f32x4 aw = mm16k<false, false>(sL + r0 * kPC, kPC, sK + 16 * ct, PD, 0, rb + 1, zero4(), sB);
+    const f32x4 au = mm16k<false, false>(sL + r0 * kPC, kPC, sV + 16 * ct, PD, 0, rb + 1, zero4(), sB);
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      const int i = 16 * w + tile_row(r), j = 16 * ct + tile_col();
+      const int i = r0 + tile_row(r), j = 16 * ct + tile_col();
       gW[i * D + j] = aw[r];
       gU[i * D + j] = au[r];
       sW[i * PD + j] = aw[r];
     }
   }
-  // P = tril(Q K^T), diagonal included, into sA
-  for (int ct = 0; ct < 4; ++ct) {
-    const f32x4 acc = mm16<false, true>(sQ + 16 * w * PD, PD, sK + 16 * ct * PD, PD, D, zero4());
+  // P = tril(Q K^T), diagonal included, into sA (tiles above the diagonal: zeros)
+  for (int ct = ch; ct < 4; ct += 2) {
+    const f32x4 acc = ct <= rb ? mm16<false, true>(sQ + r0 * PD, PD, sK + 16 * ct * PD, PD, D, zero4()) : zero4();
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      const int i = 16 * w + tile_row(r), j = 16 * ct + tile_col();
+      const int i = r0 + tile_row(r), j = 16 * ct + tile_col();
       sA[i * kPC + j] = j <= i ? acc[r] : 0.f;
     }
   }
   __syncthreads();  // sW, sA complete; sV's reads are done
-  // Z = P^T dO into sV
-  for (int ct = 0; ct < D / 16; ++ct) {
-    const f32x4 acc = mm16<true, false>(sA + 16 * w, kPC, sO + 16 * ct, PD, kC, zero4());
+  // Z = P^T dO into sV (P^T upper triangular: k blocks rb .. 3)
+  for (int ct = ch; ct < NT; ct += 2) {
+    const f32x4 acc = mm16k<true, false>(sA + r0, kPC, sO + 16 * ct, PD, rb, 4, zero4());
 #pragma unroll
-    for (int r = 0; r < 4; ++r) sV[(16 * w + tile_row(r)) * PD + 16 * ct + tile_col()] = acc[r];
+    for (int r = 0; r < 4; ++r) sV[(r0 + tile_row(r)) * PD + 16 * ct + tile_col()] = acc[r];
   }
   __syncthreads();
-  // Y = Q^T dO - W^T Z [D x D]: row tiles of Y over the waves
+  // Y = Q^T dO - W^T Z [D x D]: its tiles over the waves
   float* gY = Ws<D>::Y(ws, chunk);
-  for (int tile = w; tile < (D / 16) * (D / 16); tile += 4) {
+  for (int tile = w; tile < NT * NT; tile += NTH / 64) {
     const int rt = tile / (D / 16), ct = tile - rt * (D / 16);
     f32x4 acc = mm16<true, false>(sQ + 16 * rt, PD, sO + 16 * ct, PD, kC, zero4());
     const f32x4 wz = mm16<true, false>(sW + 16 * rt, PD, sV + 16 * ct, PD, kC, zero4());
@@ -708,7 +713,7 @@ void launch(const TIn* q, const TIn* k, const TIn* v, const TIn* beta, const flo
             float* ws, int B, int N, int H, hipStream_t stream) {
   const int NC = (N + kC - 1) / kC;
   const unsigned chunks = (unsigned)((size_t)B * H * NC), slices = (unsigned)((size_t)B * H * (D / 16));
-  hipLaunchKernelGGL((scan_bwd_prep_kernel<TIn, D>), dim3(chunks), dim3(256), 0, stream, q, k, v, beta, d_o, active, ws,
+  hipLaunchKernelGGL((scan_bwd_prep_kernel<TIn, D>), dim3(chunks), dim3(kPrepThreads), 0, stream, q, k, v, beta, d_o, active, ws,
                      N, H, NC);
   hipLaunchKernelGGL((scan_bwd_states_kernel<TIn, D>), dim3(slices), dim3(256), 0, stream, k, state_in, ws, N, H, NC);
   hipLaunchKernelGGL((scan_bwd_dstate_kernel<TIn, D>), dim3(slices), dim3(256), 0, stream, k, d_state, d_state_in, ws, N,
