@@ -19,7 +19,6 @@ struct CopyItems {
   const uint8_t* flags[kMaxItems];
   unsigned row_units[kMaxItems];       // copy units per row
   unsigned unit_log2[kMaxItems];       // a unit is 1 << unit_log2 bytes (1 .. 16)
-  unsigned first_block[kMaxItems + 1]; // the item's first workgroup; first_block[count] = the grid
   int count;
 };
 
@@ -28,23 +27,26 @@ __device__ __forceinline__ void copy_unit(const uint8_t* src, uint8_t* dst, size
   reinterpret_cast<U*>(dst)[u] = reinterpret_cast<const U*>(src)[u];
 }
 
-// 256 consecutive units of one item per workgroup (the item is found from the block index, the
-// same for the whole workgroup)
+// One token row per wave, every item in turn: a row whose flag is 0 costs one flag read, a flagged
+// row is copied by the wave's lanes in units of 1 << unit_log2 bytes.
 __global__ __launch_bounds__(256) void copy_rows_kernel(const CopyItems items, unsigned rows) {
-  int i = 0;
-  while (i + 1 < items.count && blockIdx.x >= items.first_block[i + 1]) ++i;
-  const unsigned per = items.row_units[i];
-  const size_t u = (size_t)(blockIdx.x - items.first_block[i]) * 256 + threadIdx.x;
-  if (u >= (size_t)rows * per) return;
-  if (items.flags[i][u / per] == 0) return;
-  const uint8_t* s = items.src[i];
-  uint8_t* d = items.dst[i];
-  switch (items.unit_log2[i]) {
-    case 4: copy_unit<uint4>(s, d, u); break;
-    case 3: copy_unit<uint2>(s, d, u); break;
-    case 2: copy_unit<uint32_t>(s, d, u); break;
-    case 1: copy_unit<uint16_t>(s, d, u); break;
-    default: copy_unit<uint8_t>(s, d, u); break;
+  const unsigned row = blockIdx.x * 4u + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+  if (row >= rows) return;
+  for (int i = 0; i < items.count; ++i) {
+    if (items.flags[i][row] == 0) continue;
+    const unsigned per = items.row_units[i];
+    const size_t base = (size_t)row * per;
+    const uint8_t* s = items.src[i];
+    uint8_t* d = items.dst[i];
+    for (unsigned u = lane; u < per; u += 64) {
+      switch (items.unit_log2[i]) {
+        case 4: copy_unit<uint4>(s, d, base + u); break;
+        case 3: copy_unit<uint2>(s, d, base + u); break;
+        case 2: copy_unit<uint32_t>(s, d, base + u); break;
+        case 1: copy_unit<uint16_t>(s, d, base + u); break;
+        default: copy_unit<uint8_t>(s, d, base + u); break;
+      }
+    }
   }
 }
 
@@ -61,7 +63,6 @@ extern "C" int vsp_copy_rows_where(int count, const void* const* src, void* cons
   if (!src || !dst || !row_bytes || !flags) return fail(ERR_ARG, "%s: null array", who);
   CopyItems items{};
   items.count = count;
-  size_t blocks = 0;
   for (int i = 0; i < count; ++i) {
     if (!src[i] || !dst[i] || !flags[i]) return fail(ERR_ARG, "%s: null pointer in tensor %d", who, i);
     if (row_bytes[i] == 0) return fail(ERR_ARG, "%s: tensor %d has empty rows", who, i);
@@ -75,12 +76,8 @@ extern "C" int vsp_copy_rows_where(int count, const void* const* src, void* cons
     items.flags[i] = flags[i];
     items.row_units[i] = (unsigned)per;
     items.unit_log2[i] = lg;
-    items.first_block[i] = (unsigned)blocks;
-    blocks += ((size_t)rows * per + 255) / 256;
-    if (blocks > 0x7FFFFFFFu) return fail(ERR_UNSUPPORTED, "%s: the copy exceeds the launch grid", who);
   }
-  items.first_block[count] = (unsigned)blocks;
-  hipLaunchKernelGGL(copy_rows_kernel, dim3((unsigned)blocks), dim3(256), 0, reinterpret_cast<hipStream_t>(stream), items,
-                     (unsigned)rows);
+  hipLaunchKernelGGL(copy_rows_kernel, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0,
+                     reinterpret_cast<hipStream_t>(stream), items, (unsigned)rows);
   return check_launch(who);
 }
