@@ -32,24 +32,39 @@ template <int D> struct BwdShape {
   static constexpr int P = DP + 16;           // LDS pitch (elements) for row and transposed reads
 };
 
-// Rows r0 .. r0 + 63 of a [rows, ld]-strided tensor (features 0 .. D - 1) into LDS [64][P], zero
-// past D and past row `rows`.
+// Rows r0 .. r0 + 63 of a [rows, ld]-strided tensor (features 0 .. D - 1) staged into LDS [64][P],
+// zero past D and past row `rows`, in two steps: fetch() issues the loads into registers and put()
+// writes them to LDS, so the next tile's loads are in flight while the current one is used. Loads
+// are unconditional (rows past the end re-read the last row, padding features feature 0) and the
+// zeros selected in put(): a load behind a per-lane branch would wait for every earlier one.
 template <typename T, int D>
-__device__ __forceinline__ void stage64(T* dst, const T* src, size_t ld, int r0, int rows) {
+struct Stage64 {
   using Sh = BwdShape<D>;
   using V8 = typename Mma<T>::V8;
-  for (int sg = threadIdx.x; sg < 64 * Sh::SEG; sg += 256) {
-    const int row = sg / Sh::SEG, part = sg - row * Sh::SEG;
-    V8 v;
-    if (r0 + row < rows && 8 * part < D) {
-      v = *reinterpret_cast<const V8*>(src + (size_t)(r0 + row) * ld + 8 * part);
-    } else {
+  static constexpr int kSegs = 64 * Sh::SEG, kIt = (kSegs + 255) / 256;
+  V8 raw[kIt];
+  int r0, rows;
+  __device__ __forceinline__ void fetch(const T* src, size_t ld, int first, int nrows) {
+    r0 = first;
+    rows = nrows;
 #pragma unroll
-      for (int e = 0; e < 8; ++e) v[e] = from_f32<T>(0.f);
+    for (int it = 0; it < kIt; ++it) {
+      const int sg = min((int)threadIdx.x + 256 * it, kSegs - 1), row = sg / Sh::SEG, part = sg - row * Sh::SEG;
+      raw[it] = *reinterpret_cast<const V8*>(src + (size_t)min(r0 + row, rows - 1) * ld + (8 * part < D ? 8 * part : 0));
     }
-    *reinterpret_cast<typename Mma<T>::V8*>(dst + row * Sh::P + 8 * part) = v;
   }
-}
+  __device__ __forceinline__ void put(T* dst) const {
+#pragma unroll
+    for (int it = 0; it < kIt; ++it) {
+      const int sg = threadIdx.x + 256 * it, row = sg / Sh::SEG, part = sg - row * Sh::SEG;
+      const bool ok = r0 + row < rows && 8 * part < D;
+      V8 v;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) v[e] = ok ? raw[it][e] : from_f32<T>(0.f);
+      if (kSegs % 256 == 0 || sg < kSegs) *reinterpret_cast<V8*>(dst + row * Sh::P + 8 * part) = v;
+    }
+  }
+};
 
 // A fragment of rows rbase + lq, features 32 s + 8 g .. + 7 (row-major LDS tile).
 template <typename T, int D>
@@ -80,8 +95,8 @@ __global__ __launch_bounds__(256) void attn_dq_kernel(const T* __restrict__ q, c
   using V8 = typename Mma<T>::V8;
   using V4 = typename Mma<T>::V4;
   constexpr int KT = 64;
-  __shared__ __align__(16) T sK[KT * Sh::P];
-  __shared__ __align__(16) T sV[KT * Sh::P];
+  __shared__ __align__(16) T sK[2][KT * Sh::P];
+  __shared__ __align__(16) T sV[2][KT * Sh::P];
   const int qt = blockIdx.x % nqt, bh = blockIdx.x / nqt;
   const int b = bh / H, h = bh - b * H;
   const int kvh = h / (H / HKV);
@@ -129,13 +144,25 @@ __global__ __launch_bounds__(256) void attn_dq_kernel(const T* __restrict__ q, c
   f32x4 acc[Sh::DT];
 #pragma unroll
   for (int t = 0; t < Sh::DT; ++t) acc[t] = zero4();
+  // double-buffered key tiles: tile it + 1 is fetched into registers while tile it is used, then
+  // written to the other buffer (last read before the previous barrier): one barrier per tile
+  Stage64<T, D> fk, fv;
+  if (ntiles > 0) {
+    fk.fetch(kbase, kv_ld, kfirst, S);
+    fv.fetch(vbase, kv_ld, kfirst, S);
+    fk.put(sK[0]);
+    fv.put(sV[0]);
+  }
+  __syncthreads();
   for (int it = 0; it < ntiles; ++it) {
     const int k0 = kfirst + it * KT;
-    __syncthreads();  // the previous tile's reads are done
-    stage64<T, D>(sK, kbase, kv_ld, k0, S);
-    stage64<T, D>(sV, vbase, kv_ld, k0, S);
-    __syncthreads();
-    if (!(k0 <= whi && k0 + KT - 1 > wlo - W)) continue;  // no query of the wave sees this tile
+    const T* tK = sK[it & 1];
+    const T* tV = sV[it & 1];
+    if (it + 1 < ntiles) {
+      fk.fetch(kbase, kv_ld, k0 + KT, S);
+      fv.fetch(vbase, kv_ld, k0 + KT, S);
+    }
+    if (k0 <= whi && k0 + KT - 1 > wlo - W) {  // some query of the wave sees this tile
     f32x4 sacc[4], pacc[4];
 #pragma unroll
     for (int kb = 0; kb < 4; ++kb) {
@@ -143,8 +170,8 @@ __global__ __launch_bounds__(256) void attn_dq_kernel(const T* __restrict__ q, c
       pacc[kb] = zero4();
 #pragma unroll
       for (int st = 0; st < Sh::KSQ; ++st) {
-        sacc[kb] = Mma<T>::run(row_frag<T, D>(sK, 16 * kb, st), qf[st], sacc[kb]);
-        pacc[kb] = Mma<T>::run(row_frag<T, D>(sV, 16 * kb, st), df[st], pacc[kb]);
+        sacc[kb] = Mma<T>::run(row_frag<T, D>(tK, 16 * kb, st), qf[st], sacc[kb]);
+        pacc[kb] = Mma<T>::run(row_frag<T, D>(tV, 16 * kb, st), df[st], pacc[kb]);
       }
     }
     // lane (lq, g) holds keys k0 + 16 kb + 4 g + r of its query
@@ -161,7 +188,13 @@ __global__ __launch_bounds__(256) void attn_dq_kernel(const T* __restrict__ q, c
 #pragma unroll
     for (int t = 0; t < Sh::DT; ++t)
 #pragma unroll
-      for (int ks = 0; ks < 2; ++ks) acc[t] = Mma<T>::run(tr_frag<T, D>(sK, 32 * ks, t), dsb[ks], acc[t]);
+      for (int ks = 0; ks < 2; ++ks) acc[t] = Mma<T>::run(tr_frag<T, D>(tK, 32 * ks, t), dsb[ks], acc[t]);
+    }
+    if (it + 1 < ntiles) {
+      fk.put(sK[(it + 1) & 1]);
+      fv.put(sV[(it + 1) & 1]);
+    }
+    __syncthreads();
   }
   if (qok) {
 #pragma unroll
@@ -178,7 +211,7 @@ __global__ __launch_bounds__(256) void attn_dq_kernel(const T* __restrict__ q, c
 }
 
 template <typename T, int D>
-__global__ __launch_bounds__(256) void attn_dkv_kernel(const T* __restrict__ q, const T* __restrict__ keys,
+__global__ __launch_bounds__(256, 3) void attn_dkv_kernel(const T* __restrict__ q, const T* __restrict__ keys,
                                                        const T* __restrict__ values, const T* __restrict__ dout,
                                                        const float* __restrict__ lse, const float* __restrict__ dsum,
                                                        T* __restrict__ dk, T* __restrict__ dv, int N, int M, int H,
@@ -186,9 +219,9 @@ __global__ __launch_bounds__(256) void attn_dkv_kernel(const T* __restrict__ q, 
   using Sh = BwdShape<D>;
   using V8 = typename Mma<T>::V8;
   using V4 = typename Mma<T>::V4;
-  __shared__ __align__(16) T sQ[64 * Sh::P];
-  __shared__ __align__(16) T sD[64 * Sh::P];
-  __shared__ float sL[64], sS[64];
+  __shared__ __align__(16) T sQ[2][64 * Sh::P];
+  __shared__ __align__(16) T sD[2][64 * Sh::P];
+  __shared__ float sL[2][64], sS[2][64];
   const int kt = blockIdx.x % nkt, bkv = blockIdx.x / nkt;
   const int b = bkv / HKV, kvh = bkv - b * HKV;
   const int G = H / HKV;
@@ -225,23 +258,42 @@ __global__ __launch_bounds__(256) void attn_dkv_kernel(const T* __restrict__ q, 
   const int ilo = max(0, k0 - M), ihi = min(N - 1, k0 + 63 + W - 1 - M);
   const int wk0 = k0 + 16 * w, wk1 = wk0 + 15;
   const size_t q_ld = (size_t)H * D;
-  for (int j = 0; j < G; ++j) {
-    const int h = kvh * G + j;
-    const T* qbase = q + ((size_t)b * N * H + h) * D;
-    const T* dbase = dout + ((size_t)b * N * H + h) * D;
-    const float* lse_h = lse + ((size_t)b * H + h) * N;
-    const float* dsum_h = dsum + ((size_t)b * H + h) * N;
-    for (int i0 = ilo; i0 <= ihi; i0 += 64) {
-      __syncthreads();  // the previous tile's reads are done
-      stage64<T, D>(sQ, qbase, q_ld, i0, N);
-      stage64<T, D>(sD, dbase, q_ld, i0, N);
-      if (threadIdx.x < 64) {
-        const int ii = i0 + (int)threadIdx.x;
-        sL[threadIdx.x] = ii < N ? lse_h[ii] : INFINITY;
-        sS[threadIdx.x] = ii < N ? dsum_h[ii] : 0.f;
-      }
-      __syncthreads();
-      if (!(M + i0 + 63 >= wk0 && M + i0 <= wk1 + W - 1)) continue;  // no key of the wave is seen
+  // the (query head, 64-query tile) steps of the group, in order; each step's Q and dO tiles (and
+  // its lse, Dsum) are fetched into registers a step ahead and written to the other LDS buffer
+  const int nq = ihi >= ilo ? (ihi - ilo) / 64 + 1 : 0, nsteps = G * nq;
+  Stage64<T, D> fq, fd;
+  float fl = INFINITY, fs = 0.f;
+  auto fetch_step = [&](int step) {
+    const int h = kvh * G + step / nq, i0 = ilo + 64 * (step % nq);
+    fq.fetch(q + ((size_t)b * N * H + h) * D, q_ld, i0, N);
+    fd.fetch(dout + ((size_t)b * N * H + h) * D, q_ld, i0, N);
+    const int ii = min(i0 + (int)(threadIdx.x & 63), N - 1);
+    fl = lse[((size_t)b * H + h) * N + ii];
+    fs = dsum[((size_t)b * H + h) * N + ii];
+  };
+  auto put_step = [&](int step, int buf) {
+    const int i0 = ilo + 64 * (step % nq);
+    fq.put(sQ[buf]);
+    fd.put(sD[buf]);
+    if (threadIdx.x < 64) {
+      const bool in = i0 + (int)threadIdx.x < N;
+      sL[buf][threadIdx.x] = in ? fl : INFINITY;
+      sS[buf][threadIdx.x] = in ? fs : 0.f;
+    }
+  };
+  if (nsteps > 0) {
+    fetch_step(0);
+    put_step(0, 0);
+  }
+  __syncthreads();
+  for (int step = 0; step < nsteps; ++step) {
+    const int buf = step & 1, i0 = ilo + 64 * (step % nq);
+    const T* tQ = sQ[buf];
+    const T* tD = sD[buf];
+    const float* tL = sL[buf];
+    const float* tS = sS[buf];
+    if (step + 1 < nsteps) fetch_step(step + 1);
+    if (M + i0 + 63 >= wk0 && M + i0 <= wk1 + W - 1) {  // some key of the wave is seen
 #pragma unroll
       for (int qp = 0; qp < 2; ++qp) {
         V8 pb, dsb;
@@ -251,26 +303,28 @@ __global__ __launch_bounds__(256) void attn_dkv_kernel(const T* __restrict__ q, 
           f32x4 st = zero4(), dp = zero4();
 #pragma unroll
           for (int s = 0; s < Sh::KSQ; ++s) {
-            st = Mma<T>::run(row_frag<T, D>(sQ, r0, s), kf[s], st);
-            dp = Mma<T>::run(row_frag<T, D>(sD, r0, s), vf[s], dp);
+            st = Mma<T>::run(row_frag<T, D>(tQ, r0, s), kf[s], st);
+            dp = Mma<T>::run(row_frag<T, D>(tD, r0, s), vf[s], dp);
           }
           // lane (lq, g) holds queries r0 + 4 g + r of its key
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
             const int qi = r0 + 4 * g + r;
             const bool vis = kok && (unsigned)(M + i0 + qi - key) < (unsigned)W;
-            const float p = vis ? __builtin_amdgcn_exp2f(__builtin_fmaf(st[r], scale_log2, -sL[qi])) : 0.f;
+            const float p = vis ? __builtin_amdgcn_exp2f(__builtin_fmaf(st[r], scale_log2, -tL[qi])) : 0.f;
             pb[4 * qb + r] = from_f32<T>(p);
-            dsb[4 * qb + r] = from_f32<T>(p * (dp[r] - sS[qi]) * scale);
+            dsb[4 * qb + r] = from_f32<T>(p * (dp[r] - tS[qi]) * scale);
           }
         }
 #pragma unroll
         for (int t = 0; t < Sh::DT; ++t) {
-          dva[t] = Mma<T>::run(tr_frag<T, D>(sD, 32 * qp, t), pb, dva[t]);
-          dka[t] = Mma<T>::run(tr_frag<T, D>(sQ, 32 * qp, t), dsb, dka[t]);
+          dva[t] = Mma<T>::run(tr_frag<T, D>(tD, 32 * qp, t), pb, dva[t]);
+          dka[t] = Mma<T>::run(tr_frag<T, D>(tQ, 32 * qp, t), dsb, dka[t]);
         }
       }
     }
+    if (step + 1 < nsteps) put_step(step + 1, buf ^ 1);
+    __syncthreads();
   }
   if (kok) {
 #pragma unroll
