@@ -1130,8 +1130,14 @@ __global__ __launch_bounds__(512) void delta_chain_bf16_kernel(const TIn* __rest
   auto form = [&](int c, const bf16x4 (&qa)[4][HB], uint64_t mask, uint64_t& next_mask) {
     const int nvc = min(kChunk, T - c * kChunk);
     const int s = c % NSL;
-    // the direct loads of K and V count as outstanding vector loads until they have written LDS
-    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+    // The direct loads of K and V count as outstanding vector memory operations until they have
+    // written LDS. Vector memory operations of a wave complete in issue order, and the only ones
+    // issued after this chunk's loads are the previous chunk's four output stores: waiting for
+    // all but the last four lets those stores drain meanwhile (the helper's first chunk has none).
+    if (c == hj)
+      __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+    else
+      __builtin_amdgcn_s_waitcnt(0x0F74);  // vmcnt(4)
     wave_sync();
     if constexpr (CARRY) {
 #pragma unroll
