@@ -32,8 +32,9 @@ constexpr int kPC = kC + 4;  // pitch (floats) of a [.][64] LDS matrix
 // Y[j * ldy + k] (TB true), times yscale[k] when given. X and Y point at the tile's origin (16-byte
 // aligned, pitches multiples of 4). Lane group g supplies k = (K / 4) g + m in step m (the sum's
 // order is free), so a row-contiguous operand comes in 16-byte LDS reads of four k. The result:
-// lane (j, g) holds rows 4 g .. 4 g + 3 of column j.
-template <bool TA, bool TB>
+// lane (j, g) holds rows 4 g .. 4 g + 3 of column j. BF: the four k of a step are rounded to bf16
+// and multiplied by one 16x16x16 bf16 MFMA (fp32 accumulation) instead of four fp32 ones.
+template <bool TA, bool TB, bool BF = false>
 __device__ __forceinline__ f32x4 mm16(const float* X, int ldx, const float* Y, int ldy, int K, f32x4 acc,
                                       const float* yscale = nullptr) {
   const int l = threadIdx.x & 63, i = l & 15, g = l >> 4;
@@ -60,20 +61,31 @@ __device__ __forceinline__ f32x4 mm16(const float* X, int ldx, const float* Y, i
 #pragma unroll
       for (int u = 0; u < 4; ++u) b[u] *= yscale[kb + m + u];
     }
+    if constexpr (BF) {
+      bf16x4 av, bv;
 #pragma unroll
-    for (int u = 0; u < 4; ++u) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[u], b[u], acc, 0, 0, 0);
+      for (int u = 0; u < 4; ++u) {
+        av[u] = (__bf16)a[u];
+        bv[u] = (__bf16)b[u];
+      }
+      acc = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(s16x4_t, av), __builtin_bit_cast(s16x4_t, bv),
+                                                      acc, 0, 0, 0);
+    } else {
+#pragma unroll
+      for (int u = 0; u < 4; ++u) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[u], b[u], acc, 0, 0, 0);
+    }
   }
   return acc;
 }
 
 // mm16 over the k blocks kb0 .. kb1 - 1 of 16 (k = 16 kb0 .. 16 kb1 - 1): the part of a product
 // that a triangular operand leaves nonzero. Same operand conventions as mm16.
-template <bool TA, bool TB>
+template <bool TA, bool TB, bool BF = false>
 __device__ __forceinline__ f32x4 mm16k(const float* X, int ldx, const float* Y, int ldy, int kb0, int kb1, f32x4 acc,
                                        const float* yscale = nullptr) {
   for (int kb = kb0; kb < kb1; ++kb) {
     const int k0 = 16 * kb;
-    acc = mm16<TA, TB>(TA ? X + k0 * ldx : X + k0, ldx, TB ? Y + k0 : Y + k0 * ldy, ldy, 16, acc,
+    acc = mm16<TA, TB, BF>(TA ? X + k0 * ldx : X + k0, ldx, TB ? Y + k0 : Y + k0 * ldy, ldy, 16, acc,
                        yscale != nullptr ? yscale + k0 : nullptr);
   }
   return acc;
@@ -211,6 +223,7 @@ __global__ __launch_bounds__(kPrepThreads) void scan_bwd_prep_kernel(const TIn* 
   const int t0 = c * kC;
   const size_t chunk = blockIdx.x;
   constexpr int NTH = kPrepThreads, NT = D / 16;
+  constexpr bool BF = sizeof(TIn) == 2;  // bf16 inputs: the products on bf16 MFMA (fp32 accumulation)
   const int w = threadIdx.x >> 6, ch = w >> 2, rb = ch == 0 ? w : 7 - w, r0 = 16 * rb;
   {
     ChunkRows<TIn, D, NTH> rk, rq, ro, rv;
@@ -229,7 +242,7 @@ __global__ __launch_bounds__(kPrepThreads) void scan_bwd_prep_kernel(const TIn* 
   __syncthreads();
   // A = tril(diag(beta) K K^T, -1) (tiles above the diagonal: zeros)
   for (int ct = ch; ct < 4; ct += 2) {
-    const f32x4 acc = ct <= rb ? mm16<false, true>(sK + r0 * PD, PD, sK + 16 * ct * PD, PD, D, zero4()) : zero4();
+    const f32x4 acc = ct <= rb ? mm16<false, true, BF>(sK + r0 * PD, PD, sK + 16 * ct * PD, PD, D, zero4()) : zero4();
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int i = r0 + tile_row(r), j = 16 * ct + tile_col();
@@ -287,8 +300,8 @@ __global__ __launch_bounds__(kPrepThreads) void scan_bwd_prep_kernel(const TIn* 
   float* gW = Ws<D>::W(ws, chunk);
   float* gU = Ws<D>::U(ws, chunk);
   for (int ct = ch; ct < NT; ct += 2) {
-    const f32x4 aw = mm16k<false, false>(sL + r0 * kPC, kPC, sK + 16 * ct, PD, 0, rb + 1, zero4(), sB);
-    const f32x4 au = mm16k<false, false>(sL + r0 * kPC, kPC, sV + 16 * ct, PD, 0, rb + 1, zero4(), sB);
+    const f32x4 aw = mm16k<false, false, BF>(sL + r0 * kPC, kPC, sK + 16 * ct, PD, 0, rb + 1, zero4(), sB);
+    const f32x4 au = mm16k<false, false, BF>(sL + r0 * kPC, kPC, sV + 16 * ct, PD, 0, rb + 1, zero4(), sB);
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int i = r0 + tile_row(r), j = 16 * ct + tile_col();
@@ -299,7 +312,7 @@ __global__ __launch_bounds__(kPrepThreads) void scan_bwd_prep_kernel(const TIn* 
   }
   // P = tril(Q K^T), diagonal included, into sA (tiles above the diagonal: zeros)
   for (int ct = ch; ct < 4; ct += 2) {
-    const f32x4 acc = ct <= rb ? mm16<false, true>(sQ + r0 * PD, PD, sK + 16 * ct * PD, PD, D, zero4()) : zero4();
+    const f32x4 acc = ct <= rb ? mm16<false, true, BF>(sQ + r0 * PD, PD, sK + 16 * ct * PD, PD, D, zero4()) : zero4();
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int i = r0 + tile_row(r), j = 16 * ct + tile_col();
@@ -309,7 +322,7 @@ __global__ __launch_bounds__(kPrepThreads) void scan_bwd_prep_kernel(const TIn* 
   __syncthreads();  // sW, sA complete; sV's reads are done
   // Z = P^T dO into sV (P^T upper triangular: k blocks rb .. 3)
   for (int ct = ch; ct < NT; ct += 2) {
-    const f32x4 acc = mm16k<true, false>(sA + r0, kPC, sO + 16 * ct, PD, rb, 4, zero4());
+    const f32x4 acc = mm16k<true, false, BF>(sA + r0, kPC, sO + 16 * ct, PD, rb, 4, zero4());
 #pragma unroll
     for (int r = 0; r < 4; ++r) sV[(r0 + tile_row(r)) * PD + 16 * ct + tile_col()] = acc[r];
   }
@@ -318,8 +331,8 @@ __global__ __launch_bounds__(kPrepThreads) void scan_bwd_prep_kernel(const TIn* 
   float* gY = Ws<D>::Y(ws, chunk);
   for (int tile = w; tile < NT * NT; tile += NTH / 64) {
     const int rt = tile / (D / 16), ct = tile - rt * (D / 16);
-    f32x4 acc = mm16<true, false>(sQ + 16 * rt, PD, sO + 16 * ct, PD, kC, zero4());
-    const f32x4 wz = mm16<true, false>(sW + 16 * rt, PD, sV + 16 * ct, PD, kC, zero4());
+    f32x4 acc = mm16<true, false, BF>(sQ + 16 * rt, PD, sO + 16 * ct, PD, kC, zero4());
+    const f32x4 wz = mm16<true, false, BF>(sW + 16 * rt, PD, sV + 16 * ct, PD, kC, zero4());
 #pragma unroll
     for (int r = 0; r < 4; ++r) gY[(16 * rt + tile_row(r)) * D + 16 * ct + tile_col()] = acc[r] - wz[r];
   }
@@ -498,6 +511,7 @@ __global__ __launch_bounds__(kChunkThreads) void scan_bwd_chunk_kernel(
   constexpr int P = kPC;  // every buffer is [64][68]
   constexpr int NT = D / 16, NTW = (NT + 1) / 2;  // column tiles of a [64 x D] result; a wave's share
   constexpr int NTH = kChunkThreads;
+  constexpr bool BF = sizeof(TIn) == 2;  // bf16 inputs: the products on bf16 MFMA (fp32 accumulation)
   __shared__ __align__(16) float buf[9][kC * P];
   __shared__ float sB[kC], sPart[4 * kC], sRow[2 * kC];
   const int c = blockIdx.x % NC, bh = blockIdx.x / NC;
@@ -533,13 +547,13 @@ __global__ __launch_bounds__(kChunkThreads) void scan_bwd_chunk_kernel(
   const int r0 = 16 * rb;  // this wave's 16 rows of every [64 x .] result
   // R = V - K H, in place (each tile reads only its own V entries)
   for (int ct = ch; ct < NT; ct += 2) {
-    const f32x4 acc = mm16<false, false>(Bk + r0 * P, P, Bh + 16 * ct, P, D, zero4());
+    const f32x4 acc = mm16<false, false, BF>(Bk + r0 * P, P, Bh + 16 * ct, P, D, zero4());
 #pragma unroll
     for (int r = 0; r < 4; ++r) Br[(r0 + tile_row(r)) * P + 16 * ct + tile_col()] -= acc[r];
   }
   // P = tril(Q K^T), diagonal included (tiles above the diagonal: zeros)
   for (int ct = ch; ct < 4; ct += 2) {
-    const f32x4 acc = ct <= rb ? mm16<false, true>(Bq + r0 * P, P, Bk + 16 * ct * P, P, D, zero4()) : zero4();
+    const f32x4 acc = ct <= rb ? mm16<false, true, BF>(Bq + r0 * P, P, Bk + 16 * ct * P, P, D, zero4()) : zero4();
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int i = r0 + tile_row(r), j = 16 * ct + tile_col();
@@ -549,7 +563,7 @@ __global__ __launch_bounds__(kChunkThreads) void scan_bwd_chunk_kernel(
   __syncthreads();
   // Delta = L diag(beta) R (L lower triangular: k blocks 0 .. rb)
   for (int ct = ch; ct < NT; ct += 2) {
-    const f32x4 acc = mm16k<false, false>(Bl + r0 * P, P, Br + 16 * ct, P, 0, rb + 1, zero4(), sB);
+    const f32x4 acc = mm16k<false, false, BF>(Bl + r0 * P, P, Br + 16 * ct, P, 0, rb + 1, zero4(), sB);
 #pragma unroll
     for (int r = 0; r < 4; ++r) Bd[(r0 + tile_row(r)) * P + 16 * ct + tile_col()] = acc[r];
   }
@@ -562,9 +576,9 @@ __global__ __launch_bounds__(kChunkThreads) void scan_bwd_chunk_kernel(
   for (int u = 0; u < NTW; ++u) {
     const int ct = ch + 2 * u;
     if (ct < NT) {
-      ddl[u] = mm16<false, false>(Bk + r0 * P, P, Bg + 16 * ct, P, D, zero4());
-      ddl[u] = mm16k<true, false>(Bp + r0, P, Bo + 16 * ct, P, rb, 4, ddl[u]);  // P^T: k blocks rb .. 3
-      dka[u] = mm16<false, true>(Bd + r0 * P, P, Bg + 16 * ct * P, P, D, zero4());
+      ddl[u] = mm16<false, false, BF>(Bk + r0 * P, P, Bg + 16 * ct, P, D, zero4());
+      ddl[u] = mm16k<true, false, BF>(Bp + r0, P, Bo + 16 * ct, P, rb, 4, ddl[u]);  // P^T: k blocks rb .. 3
+      dka[u] = mm16<false, true, BF>(Bd + r0 * P, P, Bg + 16 * ct * P, P, D, zero4());
     }
   }
   __syncthreads();  // the reads of G are done: dDelta goes into its buffer
@@ -580,7 +594,7 @@ __global__ __launch_bounds__(kChunkThreads) void scan_bwd_chunk_kernel(
   // dR = diag(beta) L^T dDelta into P's buffer (free now); dV = dR
   float* Bdr = Bp;
   for (int ct = ch; ct < NT; ct += 2) {
-    const f32x4 acc = mm16k<true, false>(Bl + r0, P, Bdd + 16 * ct, P, rb, 4, zero4());  // L^T: k blocks rb .. 3
+    const f32x4 acc = mm16k<true, false, BF>(Bl + r0, P, Bdd + 16 * ct, P, rb, 4, zero4());  // L^T: k blocks rb .. 3
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int i = r0 + tile_row(r), j = 16 * ct + tile_col();
@@ -595,7 +609,7 @@ __global__ __launch_bounds__(kChunkThreads) void scan_bwd_chunk_kernel(
   for (int u = 0; u < NTW; ++u) {
     const int ct = ch + 2 * u;
     if (ct < NT) {
-      const f32x4 acc = mm16<false, true>(Bdr + r0 * P, P, Bh + 16 * ct * P, P, D, zero4());
+      const f32x4 acc = mm16<false, true, BF>(Bdr + r0 * P, P, Bh + 16 * ct * P, P, D, zero4());
 #pragma unroll
       for (int r = 0; r < 4; ++r) dka[u][r] -= acc[r];
     }
@@ -604,7 +618,7 @@ __global__ __launch_bounds__(kChunkThreads) void scan_bwd_chunk_kernel(
   // S2 = tril(dO Delta^T), diagonal included, into dR's buffer (tiles above the diagonal: zeros)
   float* Bs = Bp;
   for (int ct = ch; ct < 4; ct += 2) {
-    const f32x4 acc = ct <= rb ? mm16<false, true>(Bo + r0 * P, P, Bd + 16 * ct * P, P, D, zero4()) : zero4();
+    const f32x4 acc = ct <= rb ? mm16<false, true, BF>(Bo + r0 * P, P, Bd + 16 * ct * P, P, D, zero4()) : zero4();
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int i = r0 + tile_row(r), j = 16 * ct + tile_col();
@@ -617,14 +631,14 @@ __global__ __launch_bounds__(kChunkThreads) void scan_bwd_chunk_kernel(
   for (int u = 0; u < NTW; ++u) {
     const int ct = ch + 2 * u;
     if (ct < NT) {
-      f32x4 acc = mm16<false, true>(Bo + r0 * P, P, Bh + 16 * ct * P, P, D, zero4());
-      acc = mm16k<false, false>(Bs + r0 * P, P, Bk + 16 * ct, P, 0, rb + 1, acc);  // S2: k blocks 0 .. rb
+      f32x4 acc = mm16<false, true, BF>(Bo + r0 * P, P, Bh + 16 * ct * P, P, D, zero4());
+      acc = mm16k<false, false, BF>(Bs + r0 * P, P, Bk + 16 * ct, P, 0, rb + 1, acc);  // S2: k blocks 0 .. rb
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int i = r0 + tile_row(r), j = 16 * ct + tile_col();
         if (t0 + i < N) dq[(((size_t)b * N + t0 + i) * H + h) * D + j] = from_f32<TIn>(acc[r]);
       }
-      dka[u] = mm16k<true, false>(Bs + r0, P, Bq + 16 * ct, P, rb, 4, dka[u]);  // S2^T: k blocks rb .. 3
+      dka[u] = mm16k<true, false, BF>(Bs + r0, P, Bq + 16 * ct, P, rb, 4, dka[u]);  // S2^T: k blocks rb .. 3
     }
   }
   __syncthreads();  // H, dO, Q, S2, Delta are done with
@@ -632,7 +646,7 @@ __global__ __launch_bounds__(kChunkThreads) void scan_bwd_chunk_kernel(
   // its 16 rows of its columns into sPart; dL = tril(dT) diag(beta) goes into H's buffer
   float* Bt = Bh;
   for (int ct = ch; ct < 4; ct += 2) {  // (tiles above the diagonal: dL is zero there, and so is L)
-    const f32x4 acc = ct <= rb ? mm16<false, true>(Bdd + r0 * P, P, Br + 16 * ct * P, P, D, zero4()) : zero4();
+    const f32x4 acc = ct <= rb ? mm16<false, true, BF>(Bdd + r0 * P, P, Br + 16 * ct * P, P, D, zero4()) : zero4();
     const int j = 16 * ct + tile_col();
     float part = 0.f;
 #pragma unroll
@@ -648,7 +662,7 @@ __global__ __launch_bounds__(kChunkThreads) void scan_bwd_chunk_kernel(
   // X1 = L^T dL into Q's buffer (L^T upper, dL lower triangular: k blocks max(rb, ct) .. 3)
   float* Bx = Bq;
   for (int ct = ch; ct < 4; ct += 2) {
-    const f32x4 acc = mm16k<true, false>(Bl + r0, P, Bt + 16 * ct, P, max(rb, ct), 4, zero4());
+    const f32x4 acc = mm16k<true, false, BF>(Bl + r0, P, Bt + 16 * ct, P, max(rb, ct), 4, zero4());
 #pragma unroll
     for (int r = 0; r < 4; ++r) Bx[(r0 + tile_row(r)) * P + 16 * ct + tile_col()] = acc[r];
   }
@@ -664,8 +678,8 @@ __global__ __launch_bounds__(kChunkThreads) void scan_bwd_chunk_kernel(
       continue;
     }
     // L^T column block ct: k blocks 0 .. ct
-    const f32x4 acc = mm16k<false, true>(Bx + r0 * P, P, Bl + 16 * ct * P, P, 0, ct + 1, zero4());
-    const f32x4 gk = mm16<false, true>(Bk + r0 * P, P, Bk + 16 * ct * P, P, D, zero4());
+    const f32x4 acc = mm16k<false, true, BF>(Bx + r0 * P, P, Bl + 16 * ct * P, P, 0, ct + 1, zero4());
+    const f32x4 gk = mm16<false, true, BF>(Bk + r0 * P, P, Bk + 16 * ct * P, P, D, zero4());
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int i = r0 + tile_row(r), j = 16 * ct + tile_col();
@@ -685,8 +699,8 @@ __global__ __launch_bounds__(kChunkThreads) void scan_bwd_chunk_kernel(
   for (int u = 0; u < NTW; ++u) {
     const int ct = ch + 2 * u;
     if (ct < NT) {
-      dka[u] = mm16k<false, false>(Ba + r0 * P, P, Bk + 16 * ct, P, 0, rb + 1, dka[u]);  // M: k blocks 0 .. rb
-      dka[u] = mm16k<true, false>(Ba + r0, P, Bk + 16 * ct, P, rb, 4, dka[u]);         // M^T: k blocks rb .. 3
+      dka[u] = mm16k<false, false, BF>(Ba + r0 * P, P, Bk + 16 * ct, P, 0, rb + 1, dka[u]);  // M: k blocks 0 .. rb
+      dka[u] = mm16k<true, false, BF>(Ba + r0, P, Bk + 16 * ct, P, rb, 4, dka[u]);         // M^T: k blocks rb .. 3
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int i = r0 + tile_row(r), j = 16 * ct + tile_col();
