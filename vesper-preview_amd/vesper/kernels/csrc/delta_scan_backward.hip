@@ -347,11 +347,26 @@ constexpr int kPS = 20;  // LDS pitch (floats) of a 16-column slice
 
 // C[16 x 16] += A B with A from registers (a[m] = A[i][(K / 4) g + m], lane (i, g)) and B
 // row-major in LDS ([k][16], pitch kPS): K / 4 MFMA steps
-template <int KM>
+// BF: each four k rounded to bf16 and multiplied by one 16x16x16 bf16 MFMA (fp32 accumulation).
+template <int KM, bool BF = false>
 __device__ __forceinline__ f32x4 mm_reg(const float (&a)[KM], const float* Y, f32x4 acc) {
   const int l = threadIdx.x & 63, j = l & 15, g = l >> 4;
+  if constexpr (BF) {
 #pragma unroll
-  for (int m = 0; m < KM; ++m) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[m], Y[(KM * g + m) * kPS + j], acc, 0, 0, 0);
+    for (int m = 0; m < KM; m += 4) {
+      bf16x4 av, bv;
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        av[u] = (__bf16)a[m + u];
+        bv[u] = (__bf16)Y[(KM * g + m + u) * kPS + j];
+      }
+      acc = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(s16x4_t, av), __builtin_bit_cast(s16x4_t, bv),
+                                                      acc, 0, 0, 0);
+    }
+  } else {
+#pragma unroll
+    for (int m = 0; m < KM; ++m) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[m], Y[(KM * g + m) * kPS + j], acc, 0, 0, 0);
+  }
   return acc;
 }
 
@@ -404,7 +419,7 @@ __global__ __launch_bounds__(256) void scan_bwd_states_kernel(const TIn* __restr
     float* gH = Ws<D>::Hs(ws, chunk);
 #pragma unroll
     for (int e = threadIdx.x; e < D * 16; e += kThreads) gH[(e / 16) * D + 16 * s + e % 16] = sH[(e / 16) * kPS + e % 16];
-    const f32x4 acc = mm_reg<D / 4>(cur.wa, sH, zero4());
+    const f32x4 acc = mm_reg<D / 4, sizeof(TIn) == 2>(cur.wa, sH, zero4());
 #pragma unroll
     for (int r = 0; r < 4; ++r) sD[(16 * w + 4 * g + r) * kPS + j] = cur.ua[r] - acc[r];
     __syncthreads();  // Delta complete; the reads of H are done
@@ -412,7 +427,7 @@ __global__ __launch_bounds__(256) void scan_bwd_states_kernel(const TIn* __restr
       float ka[16];  // tokens past N contribute nothing
 #pragma unroll
       for (int m = 0; m < 16; ++m) ka[m] = c * kC + 16 * g + m < N ? to_f32(cur.kr[m]) : 0.f;
-      const f32x4 dh = mm_reg<16>(ka, sD, zero4());
+      const f32x4 dh = mm_reg<16, sizeof(TIn) == 2>(ka, sD, zero4());
 #pragma unroll
       for (int r = 0; r < 4; ++r) sH[(16 * w + 4 * g + r) * kPS + j] += dh[r];
     }
@@ -476,12 +491,12 @@ __global__ __launch_bounds__(256) void scan_bwd_dstate_kernel(const TIn* __restr
     for (int q = 0; q < D / 16; ++q)
 #pragma unroll
       for (int e = 0; e < 4; ++e) ka[4 * q + e] = live ? to_f32(cur.kr[q][e]) : 0.f;
-    const f32x4 x = mm_reg<D / 4>(ka, sG, zero4());
+    const f32x4 x = mm_reg<D / 4, sizeof(TIn) == 2>(ka, sG, zero4());
 #pragma unroll
     for (int r = 0; r < 4; ++r) sX[(16 * w + 4 * g + r) * kPS + j] = x[r];
     __syncthreads();  // X complete; the reads of G are done
     if (w < D / 16) {
-      const f32x4 wx = mm_reg<16>(cur.wta, sX, zero4());
+      const f32x4 wx = mm_reg<16, sizeof(TIn) == 2>(cur.wta, sX, zero4());
 #pragma unroll
       for (int r = 0; r < 4; ++r) sG[(16 * w + 4 * g + r) * kPS + j] += cur.ya[r] - wx[r];
     }
