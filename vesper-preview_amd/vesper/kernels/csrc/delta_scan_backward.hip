@@ -344,6 +344,7 @@ __global__ __launch_bounds__(kPrepThreads) void scan_bwd_prep_kernel(const TIn* 
 // operands, from LDS, follow the same k order). Only the 16-column state slice and the chunk's
 // [64 x 16] intermediate live in LDS; two barriers per chunk.
 constexpr int kPS = 20;  // LDS pitch (floats) of a 16-column slice
+constexpr int kRing = 4;  // chunks of chain operands in flight
 
 // C[16 x 16] += A B with A from registers (a[m] = A[i][(K / 4) g + m], lane (i, g)) and B
 // row-major in LDS ([k][16], pitch kPS): K / 4 MFMA steps
@@ -410,12 +411,15 @@ __global__ __launch_bounds__(256) void scan_bwd_states_kernel(const TIn* __restr
   const int w = threadIdx.x >> 6, l = threadIdx.x & 63, j = l & 15, g = l >> 4;
   const float* h0 = state_in + (size_t)bh * D * D;
   for (int e = threadIdx.x; e < D * 16; e += kThreads) sH[(e / 16) * kPS + e % 16] = h0[(e / 16) * D + 16 * s + e % 16];
-  StateOps<TIn, D> ops[2];
-  load_state_ops<TIn, D>(ops[0], ws, k, (size_t)bh * NC, b, h, 0, N, H, s);
+  // a ring of kRing chunks' operands in registers: a slot is refilled with the chunk kRing later
+  // right after its last use, so each chunk's loads have kRing - 1 steps to arrive
+  StateOps<TIn, D> ops[kRing];
+#pragma unroll
+  for (int p = 0; p < kRing; ++p)
+    if (p < NC) load_state_ops<TIn, D>(ops[p], ws, k, (size_t)bh * NC + p, b, h, p * kC, N, H, s);
   __syncthreads();
-  auto step = [&](int c, const StateOps<TIn, D>& cur, StateOps<TIn, D>& nxt) {
+  auto step = [&](int c, StateOps<TIn, D>& cur) {
     const size_t chunk = (size_t)bh * NC + c;
-    if (c + 1 < NC) load_state_ops<TIn, D>(nxt, ws, k, chunk + 1, b, h, (c + 1) * kC, N, H, s);
     float* gH = Ws<D>::Hs(ws, chunk);
 #pragma unroll
     for (int e = threadIdx.x; e < D * 16; e += kThreads) gH[(e / 16) * D + 16 * s + e % 16] = sH[(e / 16) * kPS + e % 16];
@@ -431,11 +435,13 @@ __global__ __launch_bounds__(256) void scan_bwd_states_kernel(const TIn* __restr
 #pragma unroll
       for (int r = 0; r < 4; ++r) sH[(16 * w + 4 * g + r) * kPS + j] += dh[r];
     }
+    if (c + kRing < NC) load_state_ops<TIn, D>(cur, ws, k, chunk + kRing, b, h, (c + kRing) * kC, N, H, s);
     __syncthreads();
   };
-  for (int c = 0; c < NC; c += 2) {
-    step(c, ops[0], ops[1]);
-    if (c + 1 < NC) step(c + 1, ops[1], ops[0]);
+  for (int c = 0; c < NC; c += kRing) {
+#pragma unroll
+    for (int p = 0; p < kRing; ++p)
+      if (c + p < NC) step(c + p, ops[p]);
   }
 }
 
@@ -476,12 +482,14 @@ __global__ __launch_bounds__(256) void scan_bwd_dstate_kernel(const TIn* __restr
   const int w = threadIdx.x >> 6, l = threadIdx.x & 63, j = l & 15, g = l >> 4;
   for (int e = threadIdx.x; e < D * 16; e += kThreads)
     sG[(e / 16) * kPS + e % 16] = d_state != nullptr ? d_state[(size_t)bh * D * D + (e / 16) * D + 16 * s + e % 16] : 0.f;
-  DStateOps<TIn, D> ops[2];
-  load_dstate_ops<TIn, D>(ops[0], ws, k, (size_t)bh * NC + NC - 1, b, h, (NC - 1) * kC, N, H, s);
+  // the register ring of the state chain, walking the chunks backwards
+  DStateOps<TIn, D> ops[kRing];
+#pragma unroll
+  for (int p = 0; p < kRing; ++p)
+    if (p < NC) load_dstate_ops<TIn, D>(ops[p], ws, k, (size_t)bh * NC + NC - 1 - p, b, h, (NC - 1 - p) * kC, N, H, s);
   __syncthreads();
-  auto step = [&](int c, const DStateOps<TIn, D>& cur, DStateOps<TIn, D>& nxt) {
+  auto step = [&](int c, DStateOps<TIn, D>& cur) {
     const size_t chunk = (size_t)bh * NC + c;
-    if (c > 0) load_dstate_ops<TIn, D>(nxt, ws, k, chunk - 1, b, h, (c - 1) * kC, N, H, s);
     float* gG = Ws<D>::dHs(ws, chunk);
 #pragma unroll
     for (int e = threadIdx.x; e < D * 16; e += kThreads) gG[(e / 16) * D + 16 * s + e % 16] = sG[(e / 16) * kPS + e % 16];
@@ -500,12 +508,13 @@ __global__ __launch_bounds__(256) void scan_bwd_dstate_kernel(const TIn* __restr
 #pragma unroll
       for (int r = 0; r < 4; ++r) sG[(16 * w + 4 * g + r) * kPS + j] += cur.ya[r] - wx[r];
     }
+    if (c - kRing >= 0) load_dstate_ops<TIn, D>(cur, ws, k, chunk - kRing, b, h, (c - kRing) * kC, N, H, s);
     __syncthreads();
   };
-  for (int i = 0; i < NC; i += 2) {
-    const int c = NC - 1 - i;
-    step(c, ops[0], ops[1]);
-    if (c > 0) step(c - 1, ops[1], ops[0]);
+  for (int i = 0; i < NC; i += kRing) {
+#pragma unroll
+    for (int p = 0; p < kRing; ++p)
+      if (i + p < NC) step(NC - 1 - i - p, ops[p]);
   }
   for (int e = threadIdx.x; e < D * 16; e += kThreads)
     d_state_in[(size_t)bh * D * D + (e / 16) * D + 16 * s + e % 16] = sG[(e / 16) * kPS + e % 16];
