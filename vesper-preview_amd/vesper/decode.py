@@ -94,10 +94,10 @@ def decode_step(column: LoopedColumn, depth: int, values: Sequence[Tensor],
         for t in range(depth):
             state, history, rk, rv, rp, rvalid = flat[PER_PASS * t: PER_PASS * (t + 1)]
             xb = x.to(BF16)
-            q = _normalize((xb @ column.w["wq"][t]).view(b, 1, h, dk)).to(BF16)
+            q = _normalize(xb @ column.w["wq"][t], h)
             z = xb @ column.w["wk"][t]
             if column.taps is None:
-                k = _normalize(z.view(b, 1, h, dk)).to(BF16)
+                k = _normalize(z, h)
             else:
                 k, nxt = recurrent_keys(z, history, column.taps[t], h)
                 history.copy_(nxt)

@@ -39,19 +39,26 @@ from vesper.column import recurrent_keys
 from vesper.contracts import ContractError, Dims, check_shape
 from vesper.kernels.carry import copy_rows_where
 from vesper.kernels.delta_scan import delta_scan_fused
+from vesper.kernels.keys import fused_keys
 from vesper.kernels.window_attn import window_attention
 
 BF16 = torch.bfloat16
-KEY_NORM_FLOOR = 1e-6  # vesper/recurrence.py:31
 
 
-def _normalize(x: Tensor) -> Tensor:
-    """``normalize_keys`` (``vesper/recurrence.py:91-115``) in float32: divide by the row's peak
-    magnitude (floored at 1e-6), then by the norm of the scaled row floored at one."""
-    x = x.float()
-    peak = x.abs().amax(dim=-1, keepdim=True).clamp_min(KEY_NORM_FLOOR)
-    unit = x / peak
-    return unit / (unit * unit).sum(dim=-1, keepdim=True).clamp_min(1.0).sqrt()
+_ONES: dict[tuple[int, torch.device], Tensor] = {}
+
+
+def _normalize(x: Tensor, heads: int) -> Tensor:
+    """``normalize_keys`` (``vesper/recurrence.py:91-115``) per head of ``x [b, n, heads * dk]``
+    (bfloat16, on the GPU): divide by the head's peak magnitude (floored at 1e-6), then by the norm
+    of the scaled head floored at one, in float32, returned as bfloat16 ``[b, n, heads, dk]``. One
+    launch of the key kernel with a single tap of ones (its filter then passes the input through)
+    instead of a chain of elementwise kernels."""
+    d = x.shape[-1]
+    key = (d, x.device)
+    if key not in _ONES:
+        _ONES[key] = torch.ones(1, d, dtype=torch.float32, device=x.device)
+    return fused_keys(x, x.new_empty(x.shape[0], 0, d, dtype=torch.float32), _ONES[key], heads)
 
 
 def _where_tokens(mask: Tensor, a: Tensor, b: Tensor) -> Tensor:
@@ -142,7 +149,7 @@ class LoopedColumn:
         (with ``carried_z``, inactive tokens' inputs come from it)."""
         b, n, _ = z.shape
         if self.taps is None:
-            return _normalize(z.view(b, n, self.heads, self.head_dim)).to(BF16), history
+            return _normalize(z, self.heads), history
         assert history is not None
         return recurrent_keys(z, history, self.taps[t], self.heads, active=active, carried_z=carried_z)
 
@@ -151,7 +158,7 @@ class LoopedColumn:
         b, n, d = x.shape
         h, hkv, dk = self.heads, self.kv_heads, self.head_dim
         xb = x.to(BF16)
-        q = _normalize((xb @ self.w["wq"][t]).view(b, n, h, dk)).to(BF16)
+        q = _normalize(xb @ self.w["wq"][t], h)
         z = xb @ self.w["wk"][t]
         fused = self.copy_forward == "fused" and carried is not None and active is not None
         where = self.copy_forward == "where" and carried is not None and active is not None
