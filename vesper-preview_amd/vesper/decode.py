@@ -102,9 +102,9 @@ def decode_step(column: LoopedColumn, depth: int, values: Sequence[Tensor],
                 k, nxt = recurrent_keys(z, history, column.taps[t], h)
                 history.copy_(nxt)
             v = (xb @ column.w["wv"][t]).view(b, 1, h, dk)
-            beta = torch.sigmoid((xb @ column.w["wb"][t]).float()).to(BF16)
+            beta = torch.sigmoid(xb @ column.w["wb"][t])  # bf16 in and out, float32 inside
             o, _ = delta_scan_step_fused(q[:, 0], k[:, 0], v[:, 0], beta.view(b, h), state, out_state=state)
-            x1 = x + o.reshape(b, 1, h * dk).float()
+            x1 = x + o.reshape(b, 1, h * dk)  # float32 (promoted in the add)
             x1b = x1.to(BF16)
             aq = (x1b @ column.w["waq"][t]).view(b, 1, h, dk)
             ak = (x1b @ column.w["wak"][t]).view(b, 1, hkv, dk)
@@ -112,7 +112,7 @@ def decode_step(column: LoopedColumn, depth: int, values: Sequence[Tensor],
             ring = RingKVCache(rk, rv, rp, rvalid, column.window)
             a, _ = ring_attention(aq, ak, av, position, ring, inplace=True, check_positions=False,
                                   workspace=workspace)
-            x = x1 + a.reshape(b, 1, h * dk).float()
+            x = x1 + a.reshape(b, 1, h * dk)
     return [x, *flat]
 
 

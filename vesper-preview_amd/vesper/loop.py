@@ -169,7 +169,7 @@ class LoopedColumn:
         else:
             k, history = self.keys(t, z, history)
         v = (xb @ self.w["wv"][t]).view(b, n, h, dk)
-        beta = torch.sigmoid((xb @ self.w["wb"][t]).float()).to(BF16)
+        beta = torch.sigmoid(xb @ self.w["wb"][t])  # bf16 in and out, float32 inside
         if where and carried is not None and active is not None:
             k = _where_tokens(active, k, carried.k)
             v = _where_tokens(active, v, carried.v)
@@ -179,7 +179,7 @@ class LoopedColumn:
                                             carried=(carried.k, carried.v, carried.beta))
         else:
             r, new_state = delta_scan_fused(q, k, v, beta, state, active=active)
-        x1 = x + r.reshape(b, n, h * dk).float()
+        x1 = x + r.reshape(b, n, h * dk)  # float32 (promoted in the add)
         x1b = x1.to(BF16)
         aq = (x1b @ self.w["waq"][t]).view(b, n, h, dk)
         ak = (x1b @ self.w["wak"][t]).view(b, n, hkv, dk)
@@ -191,7 +191,7 @@ class LoopedColumn:
             a = window_attention(aq, ak, av, self.window, active=active, carried=(carried.attn_k, carried.attn_v))
         else:
             a = window_attention(aq, ak, av, self.window, active=active)
-        x2 = x1 + a.reshape(b, n, h * dk).float()
+        x2 = x1 + a.reshape(b, n, h * dk)
         written = Written(k=k, v=v, beta=beta, attn_k=ak, attn_v=av, z=z if self.taps is not None else None)
         return x2, new_state, history, written
 
