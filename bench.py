@@ -374,7 +374,8 @@ def time_looped(torch, reps: int = 3) -> dict:
     for mode in ("fused", "where"):
         column = LoopedColumn.random(d, h, h, dk, WINDOW, passes, seed=11, device=dev, key_conv=KEY_TAPS,
                                      copy_forward=mode)
-        column.forward(x0, states, exits, histories)  # warm-up
+        for _ in range(2):  # warm-up (the first call also sets up the GEMM kernels)
+            column.forward(x0, states, exits, histories)
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         torch.cuda.synchronize()
         e0.record()
@@ -383,9 +384,32 @@ def time_looped(torch, reps: int = 3) -> dict:
         e1.record()
         torch.cuda.synchronize()
         result[mode] = e0.elapsed_time(e1) / reps
+    # the fused forward captured in one HIP graph (as a training or serving loop would run it):
+    # the device time without the host's per-launch cost; the replay must equal the eager result
+    column = LoopedColumn.random(d, h, h, dk, WINDOW, passes, seed=11, device=dev, key_conv=KEY_TAPS)
+    eager = column.forward(x0, states, exits, histories).y.clone()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        column.forward(x0, states, exits, histories)
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        captured = column.forward(x0, states, exits, histories)
+    times = []
+    for _ in range(reps):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        e0.record()
+        graph.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        times.append(e0.elapsed_time(e1))
+        if not torch.equal(captured.y, eager):
+            raise RuntimeError("a replay of the captured looped column differs from the eager forward")
     ms = result["fused"]
-    return {"ms": ms, "ms_where": result["where"], "tok_s": b * n / (ms / 1e3),
-            "mean_passes": float(out.n_iters.float().mean())}
+    return {"ms": ms, "ms_where": result["where"], "ms_captured": statistics.median(times),
+            "tok_s": b * n / (ms / 1e3), "mean_passes": float(out.n_iters.float().mean())}
 
 
 def time_column_decode(torch, steps: int = 64) -> dict:
@@ -634,6 +658,7 @@ def main() -> int:
             "tok_s": round(looped["tok_s"], 1), "ms": round(looped["ms"], 3),
             "copy_forward": "fused into the kernels' loads; one row-copy launch per pass",
             "ms_with_where_merges": round(looped["ms_where"], 3),
+            "ms_captured": round(looped["ms_captured"], 3),
             "mean_active_passes": round(looped["mean_passes"], 3),
         }
     if not args.no_cpu_baseline:

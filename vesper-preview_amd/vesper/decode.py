@@ -89,26 +89,20 @@ def decode_step(column: LoopedColumn, depth: int, values: Sequence[Tensor],
     if not 1 <= depth <= column.passes:
         raise ContractError(f"depth {depth} is outside 1..{column.passes}")
     b = x.shape[0]
-    h, hkv, dk = column.heads, column.kv_heads, column.head_dim
+    h, dk = column.heads, column.head_dim
     with torch.no_grad():
         for t in range(depth):
             state, history, rk, rv, rp, rvalid = flat[PER_PASS * t: PER_PASS * (t + 1)]
-            xb = x.to(BF16)
-            q = _normalize(xb @ column.w["wq"][t], h)
-            z = xb @ column.w["wk"][t]
+            q_in, z, v, beta = column.project_rec(t, x.to(BF16))
+            q = _normalize(q_in, h)
             if column.taps is None:
                 k = _normalize(z, h)
             else:
                 k, nxt = recurrent_keys(z, history, column.taps[t], h)
                 history.copy_(nxt)
-            v = (xb @ column.w["wv"][t]).view(b, 1, h, dk)
-            beta = torch.sigmoid(xb @ column.w["wb"][t])  # bf16 in and out, float32 inside
             o, _ = delta_scan_step_fused(q[:, 0], k[:, 0], v[:, 0], beta.view(b, h), state, out_state=state)
             x1 = x + o.reshape(b, 1, h * dk)  # float32 (promoted in the add)
-            x1b = x1.to(BF16)
-            aq = (x1b @ column.w["waq"][t]).view(b, 1, h, dk)
-            ak = (x1b @ column.w["wak"][t]).view(b, 1, hkv, dk)
-            av = (x1b @ column.w["wav"][t]).view(b, 1, hkv, dk)
+            aq, ak, av = column.project_attn(t, x1.to(BF16))
             ring = RingKVCache(rk, rv, rp, rvalid, column.window)
             a, _ = ring_attention(aq, ak, av, position, ring, inplace=True, check_positions=False,
                                   workspace=workspace)

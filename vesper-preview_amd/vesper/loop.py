@@ -117,6 +117,34 @@ class LoopedColumn:
         if copy_forward not in ("fused", "where"):
             raise ValueError(f"copy_forward is 'fused' or 'where', got {copy_forward!r}")
         self.copy_forward = copy_forward
+        # Each sublayer's projections stacked into one [p, d, h*dk] weight per pass (narrower ones
+        # zero-padded), so one batched GEMM gives each projection as its own contiguous block
+        # instead of one GEMM launch per projection. Built once from ``weights``.
+        hd = heads * head_dim
+
+        def padded(w: Tensor) -> Tensor:
+            return w if w.shape[1] == hd else torch.nn.functional.pad(w, (0, hd - w.shape[1]))
+
+        self.w_rec = [torch.stack([padded(self.w[n][t]) for n in ("wq", "wk", "wv", "wb")]) for t in range(self.passes)]
+        self.w_attn = [torch.stack([padded(self.w[n][t]) for n in ("waq", "wak", "wav")]) for t in range(self.passes)]
+
+    def project_rec(self, t: int, xb: Tensor) -> tuple[Tensor, Tensor, Tensor, Tensor]:
+        """Pass ``t``'s recurrent projections of ``xb [b, n, d]`` (bf16), one batched GEMM:
+        ``q_in [b, n, h*dk]`` (before normalization), ``z [b, n, h*dk]`` (the key input),
+        ``v [b, n, h, dk]``, ``beta = sigmoid [b, n, h]``."""
+        b, n, d = xb.shape
+        h, dk = self.heads, self.head_dim
+        y = torch.matmul(xb.reshape(b * n, d), self.w_rec[t])  # [4, b*n, h*dk], each block contiguous
+        beta = torch.sigmoid(y[3][:, :h]).view(b, n, h)  # bf16 in and out, float32 inside
+        return y[0].view(b, n, h * dk), y[1].view(b, n, h * dk), y[2].view(b, n, h, dk), beta
+
+    def project_attn(self, t: int, xb: Tensor) -> tuple[Tensor, Tensor, Tensor]:
+        """Pass ``t``'s attention projections of ``xb [b, n, d]`` (bf16), one batched GEMM."""
+        b, n, d = xb.shape
+        h, hkv, dk = self.heads, self.kv_heads, self.head_dim
+        y = torch.matmul(xb.reshape(b * n, d), self.w_attn[t])
+        return (y[0].view(b, n, h, dk), y[1][:, :hkv * dk].reshape(b, n, hkv, dk),
+                y[2][:, :hkv * dk].reshape(b, n, hkv, dk))
 
     @property
     def key_history(self) -> int:
@@ -156,10 +184,10 @@ class LoopedColumn:
     def _step(self, x: Tensor, t: int, state: Tensor, history: Tensor | None, active: Tensor | None,
               carried: Written | None) -> tuple[Tensor, Tensor, Tensor | None, Written]:
         b, n, d = x.shape
-        h, hkv, dk = self.heads, self.kv_heads, self.head_dim
+        h, dk = self.heads, self.head_dim
         xb = x.to(BF16)
-        q = _normalize(xb @ self.w["wq"][t], h)
-        z = xb @ self.w["wk"][t]
+        q_in, z, v, beta = self.project_rec(t, xb)
+        q = _normalize(q_in, h)
         fused = self.copy_forward == "fused" and carried is not None and active is not None
         where = self.copy_forward == "where" and carried is not None and active is not None
         if where and carried is not None and active is not None and carried.z is not None:
@@ -168,8 +196,6 @@ class LoopedColumn:
             k, history = self.keys(t, z, history, active, carried.z)  # the filter reads carried inputs
         else:
             k, history = self.keys(t, z, history)
-        v = (xb @ self.w["wv"][t]).view(b, n, h, dk)
-        beta = torch.sigmoid(xb @ self.w["wb"][t])  # bf16 in and out, float32 inside
         if where and carried is not None and active is not None:
             k = _where_tokens(active, k, carried.k)
             v = _where_tokens(active, v, carried.v)
@@ -180,10 +206,7 @@ class LoopedColumn:
         else:
             r, new_state = delta_scan_fused(q, k, v, beta, state, active=active)
         x1 = x + r.reshape(b, n, h * dk)  # float32 (promoted in the add)
-        x1b = x1.to(BF16)
-        aq = (x1b @ self.w["waq"][t]).view(b, n, h, dk)
-        ak = (x1b @ self.w["wak"][t]).view(b, n, hkv, dk)
-        av = (x1b @ self.w["wav"][t]).view(b, n, hkv, dk)
+        aq, ak, av = self.project_attn(t, x1.to(BF16))
         if where and carried is not None and active is not None:
             ak = _where_tokens(active, ak, carried.attn_k)
             av = _where_tokens(active, av, carried.attn_v)
