@@ -1131,10 +1131,11 @@ __global__ __launch_bounds__(512) void delta_chain_bf16_kernel(const TIn* __rest
     const int nvc = min(kChunk, T - c * kChunk);
     const int s = c % NSL;
     // The direct loads of K and V count as outstanding vector memory operations until they have
-    // written LDS. Vector memory operations of a wave complete in issue order, and the only ones
+    // written LDS. Buffer loads and stores of a wave complete in issue order, and the only ones
     // issued after this chunk's loads are the previous chunk's four output stores: waiting for
-    // all but the last four lets those stores drain meanwhile (the helper's first chunk has none).
-    if (c == hj)
+    // all but the last four lets those stores drain meanwhile (the helper's first chunk has none;
+    // the carried variant's per-lane global loads wait for everything).
+    if (CARRY || c == hj)
       __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
     else
       __builtin_amdgcn_s_waitcnt(0x0F74);  // vmcnt(4)
