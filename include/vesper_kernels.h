@@ -22,7 +22,7 @@
 extern "C" {
 #endif
 
-#define VSP_ABI_VERSION 7
+#define VSP_ABI_VERSION 8
 
 /* Status codes. */
 #define VSP_OK 0
@@ -183,17 +183,24 @@ int vsp_key_filter_f16(const void* z, const float* history, const float* taps, v
                        int heads, int K, void* stream);
 int vsp_key_filter_f32(const float* z, const float* history, const float* taps, float* keys, int B, int N, int D,
                        int heads, int K, void* stream);
-/* Copy-forward fused into the filter's loads (the carry merge of the key inputs before the filter,
- * vesper/column.py:779-782: `where(active, z, z_carried)`): as vsp_key_filter_*, but token t's
- * input row (as the current token and in the halo of later ones) is z_carried's row t where
- * active[b, t] == 0. `active` and `z_carried` ([B, N, D], z's dtype) are required; the rows of z
- * for inactive tokens are never read. */
-int vsp_key_filter_carried_bf16(const void* z, const void* z_carried, const uint8_t* active, const float* history,
-                                const float* taps, void* keys, int B, int N, int D, int heads, int K, void* stream);
-int vsp_key_filter_carried_f16(const void* z, const void* z_carried, const uint8_t* active, const float* history,
-                               const float* taps, void* keys, int B, int N, int D, int heads, int K, void* stream);
-int vsp_key_filter_carried_f32(const float* z, const float* z_carried, const uint8_t* active, const float* history,
-                               const float* taps, float* keys, int B, int N, int D, int heads, int K, void* stream);
+/* The whole key step of RecurrentSublayer.keys (vesper/column.py:255-289, which returns the keys
+ * and the next history): the keys as vsp_key_filter_*, optionally
+ * - with the copy-forward fused into the filter's loads (the carry merge of the key inputs before
+ *   the filter, vesper/column.py:779-782, `where(active, z, z_carried)`): token t's input row (as
+ *   the current token and in the halo of later ones) is z_carried's row t where active[b, t] == 0;
+ *   z_carried ([B, N, D], z's dtype) and active go together or are both NULL;
+ * - writing the next history, the newest K - 1 inputs of (history, the chunk as read) in float32,
+ *   into history_out [B, K-1, D] (NULL: not written; it must not overlap history).
+ * The rows of z for inactive tokens are never read. */
+int vsp_key_step_bf16(const void* z, const void* z_carried, const uint8_t* active, const float* history,
+                      const float* taps, void* keys, float* history_out, int B, int N, int D, int heads, int K,
+                      void* stream);
+int vsp_key_step_f16(const void* z, const void* z_carried, const uint8_t* active, const float* history,
+                     const float* taps, void* keys, float* history_out, int B, int N, int D, int heads, int K,
+                     void* stream);
+int vsp_key_step_f32(const float* z, const float* z_carried, const uint8_t* active, const float* history,
+                     const float* taps, float* keys, float* history_out, int B, int N, int D, int heads, int K,
+                     void* stream);
 
 /* The key filter's backward (vesper/kernels/keys.py:46-78, `_FusedKeys.backward`, on CUDA
  * vesper/kernels/keys_triton.py:56-177): from grad_keys [B, N, D] (z's dtype), with the

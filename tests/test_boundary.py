@@ -121,3 +121,12 @@ def test_the_key_filter_refuses_before_launching():
     assert lib.vsp_key_filter_f16(None, None, None, None, 1, 4, 128, 2, 4, None) == 1  # bad argument
     assert "null pointer" in lib.vsp_last_error().decode()
     assert lib.vsp_key_filter_bf16(None, None, None, None, 0, 4, 128, 2, 4, None) == 0  # nothing to do
+    # the key step's next history may not overlap the history it is computed from (refused before
+    # any launch: the addresses are only compared)
+    base = 1 << 20
+    assert lib.vsp_key_step_bf16(base, None, None, base + 4096, base + 8192, base + 12288, base + 4096 + 16,
+                                 1, 4, 128, 2, 4, None) == 1
+    assert "overlaps the history" in lib.vsp_last_error().decode()
+    assert lib.vsp_key_step_bf16(base, base + 64, None, base + 4096, base + 8192, base + 12288, None,
+                                 1, 4, 128, 2, 4, None) == 1
+    assert "active flags" in lib.vsp_last_error().decode()

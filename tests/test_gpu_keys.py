@@ -315,3 +315,26 @@ def test_carried_key_inputs_under_autograd_reach_the_carried_tensor():
     active = (torch.rand(b, n, generator=g) > 0.4).to(GPU)
     fused_keys(z, history, _taps(d).to(GPU), heads, active=active, carried_z=zc).square().sum().backward()
     assert not bool(z.grad[~active].any()) and not bool(zc.grad[active].any()) and bool(zc.grad.any())
+
+
+# ---- the key step: keys and the next history from one launch ----
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize(("n", "width"), [(1, 4), (2, 4), (3, 4), (5, 4), (40, 8), (17, 2), (9, 1)])
+@pytest.mark.parametrize("carry", [False, True])
+def test_the_key_step_writes_the_next_history(dtype, n, width, carry):
+    from vesper.kernels.keys import fused_keys, key_step
+
+    b, heads, d = 2, 2, 128
+    g = torch.Generator().manual_seed(n * 10 + width)
+    z = torch.randn(b, n, d, generator=g).to(GPU, dtype)
+    zc = torch.randn(b, n, d, generator=g).to(GPU, dtype)
+    history = torch.randn(b, width - 1, d, generator=g).to(GPU)
+    taps = _taps(d, width).to(GPU)
+    active = (torch.rand(b, n, generator=g) > 0.4).to(GPU) if carry else None
+    keys, nxt = key_step(z, history, taps, heads, active=active, carried_z=zc if carry else None)
+    merged = torch.where(active[..., None], z, zc) if carry else z
+    want = torch.cat([history, merged.float()], dim=1)[:, n:]  # the newest width - 1 inputs
+    assert nxt.dtype == torch.float32 and nxt.shape == (b, width - 1, d)
+    assert torch.equal(nxt, want)
+    assert torch.equal(keys, fused_keys(merged, history, taps, heads))

@@ -24,7 +24,7 @@ from typing import Literal
 import torch
 from torch import Tensor
 
-from vesper.kernels.keys import fused_keys
+from vesper.kernels.keys import fused_keys, key_step
 from vesper.kernels.delta_scan import (
     FP32_INPUT_DTYPE,
     INPUT_DTYPE,
@@ -111,6 +111,9 @@ def recurrent_keys(z: Tensor, history: Tensor, taps: Tensor | None, heads: int, 
         ones = torch.ones(1, d, dtype=torch.float32, device=z.device)
         return fused_keys(z, z.new_empty(b, 0, d, dtype=torch.float32), ones, heads, active=active,
                           carried_z=carried_z), history
+    inputs = (z, history, taps) if carried_z is None else (z, history, taps, carried_z)
+    if not (torch.is_grad_enabled() and any(t.requires_grad for t in inputs)):
+        return key_step(z, history, taps, heads, active=active, carried_z=carried_z)  # keys and history, one launch
     width = int(taps.shape[0])
     keys = fused_keys(z, history, taps, heads, active=active, carried_z=carried_z)
     first = max(0, n - (width - 1))

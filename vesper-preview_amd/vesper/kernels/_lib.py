@@ -17,7 +17,7 @@ import torch
 HERE = Path(__file__).resolve().parent
 LIBRARY_PATH = HERE / "libvesper_kernels.so"
 HEADER_PATH = HERE.parents[2] / "include" / "vesper_kernels.h"
-ABI_VERSION = 7
+ABI_VERSION = 8
 
 P = ctypes.c_void_p
 I = ctypes.c_int
@@ -52,9 +52,9 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "vsp_key_filter_bf16": (I, [P, P, P, P, I, I, I, I, I, P]),
     "vsp_key_filter_f16": (I, [P, P, P, P, I, I, I, I, I, P]),
     "vsp_key_filter_f32": (I, [P, P, P, P, I, I, I, I, I, P]),
-    "vsp_key_filter_carried_bf16": (I, [P, P, P, P, P, P, I, I, I, I, I, P]),
-    "vsp_key_filter_carried_f16": (I, [P, P, P, P, P, P, I, I, I, I, I, P]),
-    "vsp_key_filter_carried_f32": (I, [P, P, P, P, P, P, I, I, I, I, I, P]),
+    "vsp_key_step_bf16": (I, [P, P, P, P, P, P, P, I, I, I, I, I, P]),
+    "vsp_key_step_f16": (I, [P, P, P, P, P, P, P, I, I, I, I, I, P]),
+    "vsp_key_step_f32": (I, [P, P, P, P, P, P, P, I, I, I, I, I, P]),
     "vsp_copy_rows_where": (I, [I, P, P, P, P, I, P]),
     "vsp_key_filter_backward_workspace_bytes": (Z, [I, I, I, I]),
     "vsp_key_filter_backward_bf16": (I, [P, P, P, P, P, P, P, P, Z, I, I, I, I, I, P]),

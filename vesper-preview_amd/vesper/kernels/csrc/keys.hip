@@ -31,8 +31,8 @@ namespace {
 template <typename TZ, int K, int LPH, bool CARRY>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))) void key_filter_kernel(const TZ* __restrict__ z, const float* __restrict__ history,
                                                          const float* __restrict__ taps, TZ* __restrict__ out,
-                                                         const uint8_t* __restrict__ active, const TZ* zc, int N,
-                                                         int D) {
+                                                         const uint8_t* __restrict__ active, const TZ* zc,
+                                                         float* __restrict__ hist_out, int N, int D) {
   using Row = Row8<TZ>;
   constexpr int RUN = Row::kRun;
   static_assert(RUN >= K - 1, "a run is at least as long as the filter's history");
@@ -93,6 +93,22 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))) voi
 #pragma unroll
       for (int e = 0; e < 8; ++e) win[r - 1][e] = __uint_as_float(__float_as_uint(zr[e]) | __float_as_uint(hr[e]));
     }
+    // The next history (the newest K - 1 inputs of history and chunk): a chunk shorter than K - 1
+    // keeps the history's rows N .. K - 2 first, copied here by the run at the chunk's start (the
+    // history is the kernel's input and hist_out never overlaps it); the chunk's own rows follow
+    // from the run loop below.
+    if (hist_out != nullptr && first && N < K - 1 && on) {
+      const float* src = history + (size_t)b * (K - 1) * D + f0;
+      float* dst = hist_out + (size_t)b * (K - 1) * D + f0;
+#pragma unroll
+      for (int r = 0; r < K - 1; ++r)
+        if (r < K - 1 - N) {
+          const f32x4 a = *reinterpret_cast<const f32x4*>(src + (size_t)(N + r) * D);
+          const f32x4 c = *reinterpret_cast<const f32x4*>(src + (size_t)(N + r) * D + 4);
+          *reinterpret_cast<f32x4*>(dst + (size_t)r * D) = a;
+          *reinterpret_cast<f32x4*>(dst + (size_t)r * D + 4) = c;
+        }
+    }
   }
   typename Row::Raw raw[RUN];  // rows past N (a short last run) re-read row N - 1
 #pragma unroll
@@ -103,6 +119,15 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))) voi
     const int t = t_begin + i;  // past N in a short last run: computed, the store dropped
     float cur[8];
     Row::unpack(raw[i], cur);
+    if constexpr (K > 1) {
+      // the chunk's last K - 1 inputs (as read: carried ones for inactive tokens) into the next history
+      const int r = t - (N - (K - 1));
+      if (hist_out != nullptr && on && t < N && r >= 0) {
+        float* dst = hist_out + ((size_t)b * (K - 1) + r) * D + f0;
+        *reinterpret_cast<f32x4*>(dst) = f32x4{cur[0], cur[1], cur[2], cur[3]};
+        *reinterpret_cast<f32x4*>(dst + 4) = f32x4{cur[4], cur[5], cur[6], cur[7]};
+      }
+    }
     // the filter in the reference's order: taps[0] z[t], then + taps[r] z[t - r] for r = 1, 2, ...
     float u[8];
 #pragma unroll
@@ -146,12 +171,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))) voi
 
 template <typename TZ, int K, bool CARRY>
 void launch_k(const TZ* z, const float* history, const float* taps, TZ* out, const uint8_t* active, const TZ* zc,
-              int B, int N, int D, int hd, hipStream_t stream) {
+              float* hist_out, int B, int N, int D, int hd, hipStream_t stream) {
   constexpr int per_block = 4 * Row8<TZ>::kRun;
   dim3 grid((unsigned)((D / 8 + 63) / 64), (unsigned)((N + per_block - 1) / per_block), (unsigned)B);
 #define VSP_KEY_LAUNCH(LPH)                                                                                          \
   hipLaunchKernelGGL((key_filter_kernel<TZ, K, LPH, CARRY>), grid, dim3(256), 0, stream, z, history, taps, out, active, \
-                     zc, N, D)
+                     zc, hist_out, N, D)
   switch (hd / 8) {
     case 1: VSP_KEY_LAUNCH(1); break;
     case 2: VSP_KEY_LAUNCH(2); break;
@@ -166,16 +191,17 @@ void launch_k(const TZ* z, const float* history, const float* taps, TZ* out, con
 
 template <typename TZ, int K>
 void launch_k(const TZ* z, const float* history, const float* taps, TZ* out, const uint8_t* active, const TZ* zc,
-              int B, int N, int D, int hd, hipStream_t stream) {
+              float* hist_out, int B, int N, int D, int hd, hipStream_t stream) {
   if (zc != nullptr)
-    launch_k<TZ, K, true>(z, history, taps, out, active, zc, B, N, D, hd, stream);
+    launch_k<TZ, K, true>(z, history, taps, out, active, zc, hist_out, B, N, D, hd, stream);
   else
-    launch_k<TZ, K, false>(z, history, taps, out, active, zc, B, N, D, hd, stream);
+    launch_k<TZ, K, false>(z, history, taps, out, active, zc, hist_out, B, N, D, hd, stream);
 }
 
 template <typename TZ>
 int key_filter(const TZ* z, const float* history, const float* taps, TZ* out, int B, int N, int D, int heads, int K,
-               void* stream_ptr, const char* who, const uint8_t* active = nullptr, const TZ* zc = nullptr) {
+               void* stream_ptr, const char* who, const uint8_t* active = nullptr, const TZ* zc = nullptr,
+               float* hist_out = nullptr) {
   if (B < 0 || N < 0 || D < 1 || heads < 1) return fail(ERR_ARG, "%s: bad sizes B=%d N=%d D=%d heads=%d", who, B, N, D, heads);
   if (K < 1 || K > 8) return fail(ERR_UNSUPPORTED, "%s: filter width %d (kernels: 1..8)", who, K);
   if (D % heads != 0) return fail(ERR_ARG, "%s: %d features are not a multiple of %d heads", who, D, heads);
@@ -193,16 +219,22 @@ int key_filter(const TZ* z, const float* history, const float* taps, TZ* out, in
     return fail(ERR_ARG, "%s: z, history, taps and the output must be 16-byte aligned", who);
   if (zc != nullptr && (!active || (reinterpret_cast<uintptr_t>(zc) & 15)))
     return fail(ERR_ARG, "%s: carried key inputs need the active flags and 16-byte alignment", who);
+  if (hist_out != nullptr && K > 1) {
+    const size_t bytes = (size_t)B * (K - 1) * D * sizeof(float);
+    const uintptr_t o = reinterpret_cast<uintptr_t>(hist_out), h0 = reinterpret_cast<uintptr_t>(history);
+    if (o & 15) return fail(ERR_ARG, "%s: the next history must be 16-byte aligned", who);
+    if (o < h0 + bytes && h0 < o + bytes) return fail(ERR_ARG, "%s: the next history overlaps the history", who);
+  }
   hipStream_t stream = reinterpret_cast<hipStream_t>(stream_ptr);
   switch (K) {
-    case 1: launch_k<TZ, 1>(z, history, taps, out, active, zc, B, N, D, hd, stream); break;
-    case 2: launch_k<TZ, 2>(z, history, taps, out, active, zc, B, N, D, hd, stream); break;
-    case 3: launch_k<TZ, 3>(z, history, taps, out, active, zc, B, N, D, hd, stream); break;
-    case 4: launch_k<TZ, 4>(z, history, taps, out, active, zc, B, N, D, hd, stream); break;
-    case 5: launch_k<TZ, 5>(z, history, taps, out, active, zc, B, N, D, hd, stream); break;
-    case 6: launch_k<TZ, 6>(z, history, taps, out, active, zc, B, N, D, hd, stream); break;
-    case 7: launch_k<TZ, 7>(z, history, taps, out, active, zc, B, N, D, hd, stream); break;
-    default: launch_k<TZ, 8>(z, history, taps, out, active, zc, B, N, D, hd, stream); break;
+    case 1: launch_k<TZ, 1>(z, history, taps, out, active, zc, hist_out, B, N, D, hd, stream); break;
+    case 2: launch_k<TZ, 2>(z, history, taps, out, active, zc, hist_out, B, N, D, hd, stream); break;
+    case 3: launch_k<TZ, 3>(z, history, taps, out, active, zc, hist_out, B, N, D, hd, stream); break;
+    case 4: launch_k<TZ, 4>(z, history, taps, out, active, zc, hist_out, B, N, D, hd, stream); break;
+    case 5: launch_k<TZ, 5>(z, history, taps, out, active, zc, hist_out, B, N, D, hd, stream); break;
+    case 6: launch_k<TZ, 6>(z, history, taps, out, active, zc, hist_out, B, N, D, hd, stream); break;
+    case 7: launch_k<TZ, 7>(z, history, taps, out, active, zc, hist_out, B, N, D, hd, stream); break;
+    default: launch_k<TZ, 8>(z, history, taps, out, active, zc, hist_out, B, N, D, hd, stream); break;
   }
   return check_launch(who);
 }
@@ -306,25 +338,25 @@ extern "C" size_t vsp_key_filter_backward_workspace_bytes(int B, int N, int D, i
   return vsp::key_backward_workspace(B, N, D, K);
 }
 
-extern "C" int vsp_key_filter_carried_bf16(const void* z, const void* z_carried, const uint8_t* active,
-                                           const float* history, const float* taps, void* keys, int B, int N, int D,
-                                           int heads, int K, void* stream) {
+extern "C" int vsp_key_step_bf16(const void* z, const void* z_carried, const uint8_t* active, const float* history,
+                                 const float* taps, void* keys, float* history_out, int B, int N, int D, int heads,
+                                 int K, void* stream) {
   return vsp::key_filter<__bf16>(static_cast<const __bf16*>(z), history, taps, static_cast<__bf16*>(keys), B, N, D,
-                                 heads, K, stream, "vsp_key_filter_carried_bf16", active,
-                                 static_cast<const __bf16*>(z_carried));
+                                 heads, K, stream, "vsp_key_step_bf16", active, static_cast<const __bf16*>(z_carried),
+                                 history_out);
 }
 
-extern "C" int vsp_key_filter_carried_f16(const void* z, const void* z_carried, const uint8_t* active,
-                                          const float* history, const float* taps, void* keys, int B, int N, int D,
-                                          int heads, int K, void* stream) {
+extern "C" int vsp_key_step_f16(const void* z, const void* z_carried, const uint8_t* active, const float* history,
+                                const float* taps, void* keys, float* history_out, int B, int N, int D, int heads,
+                                int K, void* stream) {
   return vsp::key_filter<_Float16>(static_cast<const _Float16*>(z), history, taps, static_cast<_Float16*>(keys), B, N,
-                                   D, heads, K, stream, "vsp_key_filter_carried_f16", active,
-                                   static_cast<const _Float16*>(z_carried));
+                                   D, heads, K, stream, "vsp_key_step_f16", active,
+                                   static_cast<const _Float16*>(z_carried), history_out);
 }
 
-extern "C" int vsp_key_filter_carried_f32(const float* z, const float* z_carried, const uint8_t* active,
-                                          const float* history, const float* taps, float* keys, int B, int N, int D,
-                                          int heads, int K, void* stream) {
-  return vsp::key_filter<float>(z, history, taps, keys, B, N, D, heads, K, stream, "vsp_key_filter_carried_f32", active,
-                                z_carried);
+extern "C" int vsp_key_step_f32(const float* z, const float* z_carried, const uint8_t* active, const float* history,
+                                const float* taps, float* keys, float* history_out, int B, int N, int D, int heads,
+                                int K, void* stream) {
+  return vsp::key_filter<float>(z, history, taps, keys, B, N, D, heads, K, stream, "vsp_key_step_f32", active,
+                                z_carried, history_out);
 }

@@ -13,8 +13,9 @@ are powers of two from 8 to 512.
 
 With ``active`` and ``carried_z`` (the copy-forward of halted tokens' key inputs, selected before the
 filter, ``vesper/column.py:779-782``) the kernel reads token ``t``'s input row from ``carried_z``
-where ``active[:, t]`` is false, inside its loads (``vsp_key_filter_carried_*``), in place of a
-``where`` merge before the call.
+where ``active[:, t]`` is false, inside its loads, in place of a ``where`` merge before the call.
+``key_step`` returns the next key history too, written by the same kernel launch
+(``vsp_key_step_*``): the whole of ``RecurrentSublayer.keys`` (``vesper/column.py:255-289``).
 """
 
 from __future__ import annotations
@@ -104,18 +105,51 @@ class _FusedKeys(torch.autograd.Function):
                 grad_taps.to(taps_dtype) if ctx.needs_input_grad[2] else None, None)
 
 
-def _carried_keys(z: Tensor, history: Tensor, taps: Tensor, heads: int, active: Tensor, carried_z: Tensor) -> Tensor:
+def _key_step(z: Tensor, history: Tensor, taps: Tensor, heads: int, active: Tensor | None,
+              carried_z: Tensor | None, want_history: bool) -> tuple[Tensor, Tensor | None]:
     b, n, d, width = _check(z, history, taps, heads)
-    zc, held = _aligned(z), _aligned(carried_z)
+    zc = _aligned(z)
+    held = None if carried_z is None else _aligned(carried_z)
+    flags = None if carried_z is None or active is None else active.contiguous().view(torch.uint8)
     hist = _aligned(history.to(torch.float32))
     wide = _aligned(taps.to(torch.float32))
-    flags = active.contiguous().view(torch.uint8)
     out = torch.empty(b, n, heads, d // heads, dtype=z.dtype, device=z.device)
+    nxt = torch.empty(b, width - 1, d, dtype=torch.float32, device=z.device) if want_history else None
     if b and n:
-        _lib.call(f"vsp_key_filter_carried_{_SUFFIX[z.dtype]}", _lib.ptr(zc), _lib.ptr(held), _lib.ptr(flags),
-                  _lib.ptr(hist) if width > 1 else None, _lib.ptr(wide), _lib.ptr(out), b, n, d, heads, width,
-                  _lib.stream_of(z.device))
-    return out
+        _lib.call(f"vsp_key_step_{_SUFFIX[z.dtype]}", _lib.ptr(zc), _lib.ptr(held), _lib.ptr(flags),
+                  _lib.ptr(hist) if width > 1 else None, _lib.ptr(wide), _lib.ptr(out),
+                  _lib.ptr(nxt) if width > 1 else None, b, n, d, heads, width, _lib.stream_of(z.device))
+    return out, nxt
+
+
+def _check_carried(z: Tensor, active: Tensor | None, carried_z: Tensor) -> None:
+    if active is None:
+        raise ContractError("carried key inputs need the active mask that says which tokens read them")
+    if carried_z.shape != z.shape or carried_z.dtype != z.dtype or carried_z.device != z.device:
+        raise ContractError(f"carried_z: {tuple(carried_z.shape)} {carried_z.dtype} on {carried_z.device}, "
+                            f"z is {tuple(z.shape)} {z.dtype} on {z.device}")
+    check_shape("active", active, ("b", "n"), {"b": z.shape[0], "n": z.shape[1]}, torch.bool)
+    if active.device != z.device:
+        raise ContractError(f"active is on {active.device}, z on {z.device}")
+
+
+def key_step(z: Tensor, history: Tensor, taps: Tensor, heads: int, *, active: Tensor | None = None,
+             carried_z: Tensor | None = None) -> tuple[Tensor, Tensor]:
+    """The keys and the next key history of key inputs ``z [b, n, d]`` (``n >= 1``), no gradient.
+
+    As ``fused_keys`` for the keys; the next history is the newest ``K - 1`` inputs of ``(history,
+    z)`` (with ``carried_z``, the carried rows of inactive tokens) as a new float32 ``[b, K-1, d]``
+    tensor, written by the same launch.
+
+    Raises:
+        ContractError: as ``fused_keys``.
+    """
+    _check(z, history, taps, heads)
+    if carried_z is not None:
+        _check_carried(z, active, carried_z)
+    keys, nxt = _key_step(z, history, taps, heads, active, carried_z, want_history=True)
+    assert nxt is not None
+    return keys, nxt
 
 
 def fused_keys(z: Tensor, history: Tensor, taps: Tensor, heads: int, *, active: Tensor | None = None,
@@ -135,16 +169,10 @@ def fused_keys(z: Tensor, history: Tensor, taps: Tensor, heads: int, *, active: 
     """
     _check(z, history, taps, heads)  # the contract first, before autograd records anything
     if carried_z is not None:
-        if active is None:
-            raise ContractError("carried key inputs need the active mask that says which tokens read them")
-        if carried_z.shape != z.shape or carried_z.dtype != z.dtype or carried_z.device != z.device:
-            raise ContractError(f"carried_z: {tuple(carried_z.shape)} {carried_z.dtype} on {carried_z.device}, "
-                                f"z is {tuple(z.shape)} {z.dtype} on {z.device}")
-        check_shape("active", active, ("b", "n"), {"b": z.shape[0], "n": z.shape[1]}, torch.bool)
-        if active.device != z.device:
-            raise ContractError(f"active is on {active.device}, z on {z.device}")
+        _check_carried(z, active, carried_z)
         if not (torch.is_grad_enabled() and any(t.requires_grad for t in (z, history, taps, carried_z))):
-            return _carried_keys(z, history, taps, heads, active, carried_z)
+            return _key_step(z, history, taps, heads, active, carried_z, want_history=False)[0]
+        assert active is not None
         z = torch.where(active[..., None], z, carried_z)  # under autograd: the merge, explicit
     out: Tensor = _FusedKeys.apply(z, history, taps, heads)
     return out
