@@ -213,8 +213,8 @@ __global__ __launch_bounds__(64 * NW) void attn_dq_kernel(const T* __restrict__ 
   }
 }
 
-template <typename T, int D, int NW, int MINWG>
-__global__ __launch_bounds__(64 * NW, MINWG) void attn_dkv_kernel(const T* __restrict__ q, const T* __restrict__ keys,
+template <typename T, int D, int NW, int WAVES_PER_SIMD>
+__global__ __launch_bounds__(64 * NW, WAVES_PER_SIMD) void attn_dkv_kernel(const T* __restrict__ q, const T* __restrict__ keys,
                                                        const T* __restrict__ values, const T* __restrict__ dout,
                                                        const float* __restrict__ lse, const float* __restrict__ dsum,
                                                        T* __restrict__ dk, T* __restrict__ dv, int N, int M, int H,
@@ -351,13 +351,15 @@ template <typename T, int D>
 void launch_backward(const T* q, const T* keys, const T* values, const T* o, const T* dout, const float* lse, float* dsum,
                      T* dq, T* dk, T* dv, int B, int N, int M, int H, int HKV, int W, float scale, hipStream_t stream) {
   const float scale_log2 = scale * 1.4426950408889634f;
-  constexpr int kDqWaves = 8, kDkvWaves = 8, kDkvMinWG = 2;  // 16 queries, 16 keys a wave
+  // waves a workgroup (16 queries, 16 keys a wave); the dK/dV kernel's bound asks for 2 waves a
+  // SIMD at least (256 VGPRs), its D 64 instance takes 126 and so runs 4 (two workgroups a CU)
+  constexpr int kDqWaves = 8, kDkvWaves = 8, kDkvWavesPerSimd = 2;
   const int nqt = (N + 16 * kDqWaves - 1) / (16 * kDqWaves);
   const int nkt = (M + N + 16 * kDkvWaves - 1) / (16 * kDkvWaves);
   hipLaunchKernelGGL((attn_dq_kernel<T, D, kDqWaves>), dim3((unsigned)((size_t)nqt * H * B)), dim3(64 * kDqWaves), 0,
                      stream, q, keys,
                      values, o, dout, lse, dsum, dq, N, M, H, HKV, W, scale, scale_log2, nqt);
-  hipLaunchKernelGGL((attn_dkv_kernel<T, D, kDkvWaves, kDkvMinWG>), dim3((unsigned)((size_t)nkt * HKV * B)),
+  hipLaunchKernelGGL((attn_dkv_kernel<T, D, kDkvWaves, kDkvWavesPerSimd>), dim3((unsigned)((size_t)nkt * HKV * B)),
                      dim3(64 * kDkvWaves), 0, stream, q, keys,
                      values, dout, lse, dsum, dk, dv, N, M, H, HKV, W, scale, scale_log2, nkt);
 }
