@@ -22,7 +22,7 @@
 extern "C" {
 #endif
 
-#define VSP_ABI_VERSION 8
+#define VSP_ABI_VERSION 9
 
 /* Status codes. */
 #define VSP_OK 0
@@ -35,6 +35,27 @@ const char* vsp_last_error(void);
 
 /* VSP_ABI_VERSION of the loaded library. */
 int vsp_abi_version(void);
+
+/* Set-up, once per process before the first kernel call (later calls return at once): allocates
+ * the fault record below in pinned host memory. No counterpart in the reference, whose kernels
+ * come from a library that needs none. */
+int vsp_init(void);
+
+/* The fault record of the bounded waits. Kernels whose waves hand work to each other through LDS
+ * flags (the bf16 scan's chain) poll those flags a bounded number of times; a wait that gives up
+ * sets its kernel family's bit here and the kernel writes NaN in place of its later outputs, so a
+ * broken hand-over neither hangs the device nor passes as a result. vsp_fault_bits reads the
+ * record without any device synchronisation (it shows the faults of kernels that have completed);
+ * bit 0: the scan chain. The bits stay set until vsp_clear_faults. No counterpart in the
+ * reference: its library's kernels have no inter-wave hand-over. */
+unsigned vsp_fault_bits(void);
+void vsp_clear_faults(void);
+
+/* Polls a bounded wait makes before it gives up (default 2^19, seconds of waiting; a negative
+ * value restores the default); returns the previous limit. Taken at each launch. For tests of the
+ * fault path: a limit of 0 makes a wait whose flag is not yet set give up at once, while every
+ * kernel still runs to its end. */
+int vsp_set_wait_limit(int polls);
 
 /* ---- delta-rule scan ------------------------------------------------------------------------
  * Per batch row b and head h, with the state H [D, D] read as H^T q, each token applies

@@ -14,7 +14,8 @@ Restated from the reference's pass loop and column:
   attention keys and values (``:795-796``), window attention, the residual; optionally the causal
   key filter before the keys' normalization (``RecurrentSublayer.keys``, ``:255-289``), its
   history carried per pass. Norms, rotary and the FFN are not part of the mixer path and are left
-  out; queries and keys are L2-normalised (``normalize_keys``) as the scan requires.
+  out; keys are L2-normalised (``normalize_keys``) as the scan requires, queries are not
+  (``RecurrentSublayer.project``, ``column.py:236-253``; ``docs/model-card.md:26``).
 - ``mixer_decode_step`` is the same column one token at a time over per-pass KV rings, at a fixed
   depth with every pass dense, as ``decode_step`` (``vesper/decode.py:29-46``) runs it.
 
@@ -169,7 +170,7 @@ def mixer_column_step(weights: MixerWeights, masked: bool = True, bf16: bool = T
         active = None if carry is None else carry[0]
         mask = active if masked else None
         scan_state, history = state if weights.taps is not None else (state, None)
-        q = rnd(normalize_keys(mm(x, weights.wq[t]).view(b, n, h, dk)))
+        q = mm(x, weights.wq[t]).view(b, n, h, dk)
         z = mm(x, weights.wk[t]).view(b, n, h * dk)
         if carry is not None and carry[1].z is not None:
             z = carry_in(active, z, carry[1].z)
@@ -228,7 +229,7 @@ def mixer_decode_step(weights: MixerWeights, depth: int, bf16: bool = True
         new = list(states)
         for t in range(depth):
             scan_state, history, (rk, rv, rp, rvalid) = states[t]
-            q = rnd(normalize_keys(mm(x, weights.wq[t]).view(b, 1, h, dk)))
+            q = mm(x, weights.wq[t]).view(b, 1, h, dk)
             z = mm(x, weights.wk[t]).view(b, 1, h * dk)
             k, history = _keys(weights, t, z, history, rnd)
             v = mm(x, weights.wv[t]).view(b, 1, h, dk)

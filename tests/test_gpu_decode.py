@@ -114,6 +114,29 @@ def test_the_captured_step_equals_the_eager_step_bitwise_across_the_capture(key_
     assert decoder.replays == n - WARM_STEPS
 
 
+def test_a_call_of_another_batch_after_the_capture_is_refused_and_the_graph_still_matches_eager():
+    from vesper.contracts import ContractError
+    from vesper.decode import WARM_STEPS, CapturedDecoder, cold_states, decode_step
+
+    column = _column(0)
+    b, depth = 2, 2
+    x = _inputs(b, WARM_STEPS + 4, 64, seed=7).to(GPU)
+    decoder = CapturedDecoder(column, depth)
+    flat, eager_flat = decoder.start(b), cold_states(column, b, GPU)
+    for i in range(WARM_STEPS + 4):
+        if i == WARM_STEPS + 2:  # captured by now: a wider batch is refused before the graph's buffers change
+            assert decoder.captures == 1
+            wide = decoder.start(b + 1)
+            with pytest.raises(ContractError, match="captured"):
+                decoder.step(_inputs(b + 1, 1, 64, seed=8).to(GPU), _at(i, b + 1), wide)
+        y, flat = decoder.step(x[:, i : i + 1], _at(i, b), flat)
+        eager = decode_step(column, depth, [x[:, i : i + 1], _at(i, b), *eager_flat])
+        assert torch.equal(y, eager[0]), i
+        for got, want in zip(flat, eager[1:]):
+            assert torch.equal(got, want), i
+        eager_flat = eager[1:]
+
+
 def test_a_second_generation_on_one_decoder_starts_truly_cold():
     from vesper.decode import CapturedDecoder, cold_states, decode_step
 

@@ -184,7 +184,7 @@ def test_active_mask_zeroes_outputs_and_keeps_every_write():
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, BF16])
-@pytest.mark.parametrize("dk", [16, 32, 64, 100, 128])
+@pytest.mark.parametrize("dk", [16, 32, 48, 64, 100, 128, 256])
 def test_the_decode_step_matches_the_oracle_step(dtype, dk):
     from vesper.kernels.delta_scan import delta_scan_step_fused
 
@@ -468,3 +468,33 @@ def test_carried_refusals():
         delta_scan_fused(q, k, v, beta, h0, active=active, carried=(carried[0].float(), *carried[1:]))
     with pytest.raises(ContractError, match="carried holds"):
         delta_scan_fused(q, k, v, beta, h0, active=active, carried=carried[:2])
+
+
+def test_a_wait_that_gives_up_is_recorded_and_refused_and_its_outputs_are_nan():
+    """The chain's bounded hand-over waits, made to give up from the host (a limit of 0 polls): the
+    kernel still runs to its end, the fault record says so, every later call raises until the record
+    is cleared, and the broken workgroups' outputs are NaN; with the default limit the next call is
+    right again."""
+    from vesper.kernels import _lib
+    from vesper.kernels.delta_scan import delta_scan_fused
+
+    q, k, v, beta, h0 = _bf16_inputs(1, 4096, 2, 64)
+    _lib.check_faults(synchronize=True)
+    previous = _lib.set_wait_limit(0)
+    try:
+        o, s = delta_scan_fused(q, k, v, beta, h0)
+        torch.cuda.synchronize()
+    finally:
+        _lib.set_wait_limit(previous)
+    try:
+        with pytest.raises(_lib.KernelLibraryError, match="bounded wait gave up"):
+            _lib.check_faults()
+        with pytest.raises(_lib.KernelLibraryError, match="bounded wait gave up"):
+            delta_scan_fused(q, k, v, beta, h0)
+        assert bool(torch.isnan(s).any()) or bool(torch.isnan(o.float()).any())
+    finally:
+        _lib.clear_faults()
+    o, s = delta_scan_fused(q, k, v, beta, h0)
+    _lib.check_faults(synchronize=True)
+    o_ref, s_ref = _oracle(q, k, v, beta, h0)
+    assert relative_error(o, o_ref) < TOL and relative_error(s, s_ref) < TOL

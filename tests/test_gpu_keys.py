@@ -114,6 +114,40 @@ def test_no_filter_is_the_plain_normalization_and_keeps_the_history():
     assert keys.shape == (2, 0, 2, 64) and after is history
 
 
+def test_the_reference_normalization_edge_rows_through_the_kernel():
+    # tests/test_recurrence_review.py:37-87 of the reference, through the key kernel's path without
+    # a filter (recurrent_keys with no taps): a row whose peak is a huge or tiny finite value
+    # normalizes to exactly a unit vector in its own dtype; a row under the 1e-6 floor is exactly
+    # u / 1e-6 (float32, as the oracle's division in float32 gives it); a zero row stays zero. Head
+    # width 8 (the kernel's narrowest), the peak at several features and signs.
+    from conftest import frac_tensor, reference_vectors
+    from vesper.column import recurrent_keys
+
+    c = reference_vectors()["normalize_keys"]
+    for dtype_name, magnitude in c["magnitudes_by_dtype"]["rows"]:
+        if dtype_name == "float64":
+            continue  # no float64 kernel
+        dtype = getattr(torch, dtype_name)
+        z = torch.zeros(1, 4, 16, dtype=dtype)
+        want = torch.zeros(1, 4, 2, 8, dtype=dtype)
+        for t, (feature, sign) in enumerate([(0, 1.0), (5, -1.0), (9, 1.0), (15, -1.0)]):
+            z[0, t, feature] = sign * float(magnitude)
+            want[0, t, feature // 8, feature % 8] = sign
+        keys, _ = recurrent_keys(z.to(GPU), torch.zeros(1, 0, 16, device=GPU), None, 2)
+        assert torch.equal(keys.cpu(), want), dtype_name
+    small = frac_tensor(c["small_floor"]["k"], torch.float32)  # [[3e-8, 4e-8]]
+    z = torch.zeros(1, 2, 8)
+    z[0, 0, :2] = small[0]
+    z[0, 1, 6:] = -small[0]
+    keys, _ = recurrent_keys(z.to(GPU), torch.zeros(1, 0, 8, device=GPU), None, 1)
+    assert torch.equal(keys.cpu(), normalize_keys(z.view(1, 2, 1, 8)))
+    want = frac_tensor(c["small_floor"]["want"])[0]
+    torch.testing.assert_close(keys[0, 0, 0, :2].cpu().double(), want, rtol=1e-7, atol=0)
+    zero = torch.zeros(1, 3, 8)
+    keys, _ = recurrent_keys(zero.to(GPU), torch.zeros(1, 0, 8, device=GPU), None, 1)
+    assert torch.equal(keys.cpu(), zero.view(1, 3, 1, 8))
+
+
 def test_captured_replays_equal_eager():
     from vesper.kernels.keys import fused_keys
 

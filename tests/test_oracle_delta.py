@@ -166,6 +166,10 @@ def test_normalize_keys_known_answers() -> None:
         assert torch.allclose(od.normalize_keys(k), want, rtol=1e-12, atol=0), case
     wide = torch.ones(1, c["wide_ones_fp16"]["n"], dtype=torch.float16)
     assert torch.equal(od.normalize_keys(wide), torch.full_like(wide, 1 / 256))
+    for dtype_name, magnitude in c["magnitudes_by_dtype"]["rows"]:
+        dtype = getattr(torch, dtype_name)
+        k = torch.tensor([[float(magnitude), 0.0]], dtype=dtype)
+        assert torch.equal(od.normalize_keys(k), torch.tensor([[1.0, 0.0]], dtype=dtype)), dtype_name
 
 
 def test_write_strength_known_answers() -> None:

@@ -186,3 +186,33 @@ def test_the_decode_pin_catches_a_planted_mistake():
         y, states = step(x0[:, i : i + 1], torch.full((b, 1), max(i - 1, 0), dtype=torch.long), states)
         worst = max(worst, float((y - chunked.y[:, i : i + 1]).abs().max()))
     assert worst > 1e-3
+
+
+def test_the_scan_reads_the_raw_query():
+    # RecurrentSublayer.project (column.py:236-253) hands F.linear(x, w_q) to the scan unchanged:
+    # "q is not normalized" (docs/model-card.md:26). Unit-scale weights give queries of norm well
+    # above one, where normalizing them would change the output. Zero attention values make the
+    # attention sublayer add nothing, so the step's output minus its input is the scan's read.
+    from oracle.delta import delta_scan_serial, normalize_keys
+
+    d, h, dk, n = 8, 2, 4, 5
+    g = torch.Generator().manual_seed(9)
+
+    def mats(out):
+        return [torch.randn(d, out, generator=g, dtype=F64)]
+
+    weights = ol.MixerWeights(wq=mats(h * dk), wk=mats(h * dk), wv=mats(h * dk), wb=mats(h), waq=mats(h * dk),
+                              wak=mats(h * dk), wav=[torch.zeros(d, h * dk, dtype=F64)], heads=h, kv_heads=h,
+                              head_dim=dk, window=4)
+    x = torch.randn(1, n, d, generator=g, dtype=F64)
+    s0 = torch.zeros(1, h, dk, dk, dtype=F64)
+    y, _, _ = ol.mixer_column_step(weights, masked=False, bf16=False)(x, 0, s0, None)
+    q = (x @ weights.wq[0]).view(1, n, h, dk)
+    k = normalize_keys((x @ weights.wk[0]).view(1, n, h, dk))
+    v = (x @ weights.wv[0]).view(1, n, h, dk)
+    beta = torch.sigmoid(x @ weights.wb[0])
+    o, _ = delta_scan_serial(q, k, v, beta, s0)
+    assert float(q.norm(dim=-1).min()) > 1.0
+    assert torch.allclose(y - x, o.reshape(1, n, h * dk), rtol=0, atol=1e-12)
+    o_normalized, _ = delta_scan_serial(normalize_keys(q), k, v, beta, s0)
+    assert float((o_normalized - o).abs().max()) > 1e-2

@@ -94,7 +94,7 @@ def decode_step(column: LoopedColumn, depth: int, values: Sequence[Tensor],
         for t in range(depth):
             state, history, rk, rv, rp, rvalid = flat[PER_PASS * t: PER_PASS * (t + 1)]
             q_in, z, v, beta = column.project_rec(t, x.to(BF16))
-            q = _normalize(q_in, h)
+            q = q_in.view(b, 1, h, dk)  # the scan's query is not normalized (column.py:247)
             if column.taps is None:
                 k = _normalize(z, h)
             else:
@@ -153,7 +153,14 @@ class CapturedDecoder:
         """One token per row (``x [b, 1, d]`` float32 at ``position`` int64 ``[b, 1]``): ``(y, flat)``."""
         values = [x, position, *flat]
         _check(self.column, x, position, flat)
-        if self._workspace is None or self._workspace.shape[0] != x.shape[0]:
+        if self._graph is not None:
+            # the graph holds the captured workspace and buffers: a call of another shape is refused
+            # before anything the graph uses is touched
+            for mine, given in zip(self._static, values):
+                if mine.shape != given.shape or mine.dtype != given.dtype:
+                    raise ContractError(f"the decoder was captured for {tuple(mine.shape)} {mine.dtype}, "
+                                        f"got {tuple(given.shape)} {given.dtype}")
+        elif self._workspace is None or self._workspace.shape[0] != x.shape[0]:
             self._workspace = torch.zeros(x.shape[0], dtype=torch.int32, device=self.device)
         if self.eager < WARM_STEPS:
             self.eager += 1
@@ -171,9 +178,6 @@ class CapturedDecoder:
             self._graph = graph
             self.captures += 1
         for mine, given in zip(self._static, values):
-            if mine.shape != given.shape or mine.dtype != given.dtype:
-                raise ContractError(f"the decoder was captured for {tuple(mine.shape)} {mine.dtype}, "
-                                    f"got {tuple(given.shape)} {given.dtype}")
             if mine.data_ptr() != given.data_ptr():
                 mine.copy_(given)
         self._graph.replay()

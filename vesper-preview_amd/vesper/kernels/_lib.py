@@ -17,7 +17,7 @@ import torch
 HERE = Path(__file__).resolve().parent
 LIBRARY_PATH = HERE / "libvesper_kernels.so"
 HEADER_PATH = HERE.parents[2] / "include" / "vesper_kernels.h"
-ABI_VERSION = 8
+ABI_VERSION = 9
 
 P = ctypes.c_void_p
 I = ctypes.c_int
@@ -28,6 +28,10 @@ F = ctypes.c_float
 SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "vsp_last_error": (ctypes.c_char_p, []),
     "vsp_abi_version": (I, []),
+    "vsp_init": (I, []),
+    "vsp_fault_bits": (ctypes.c_uint, []),
+    "vsp_clear_faults": (None, []),
+    "vsp_set_wait_limit": (I, [I]),
     "vsp_delta_scan_workspace_bytes": (Z, [I, I, I, I, I]),
     "vsp_delta_scan_bf16": (I, [P, P, P, P, P, P, P, P, Z, P, I, I, I, I, P]),
     "vsp_delta_scan_f32": (I, [P, P, P, P, P, P, P, P, Z, P, I, I, I, I, P]),
@@ -87,8 +91,36 @@ def library() -> ctypes.CDLL:
     version = lib.vsp_abi_version()
     if version != ABI_VERSION:
         raise KernelLibraryError(f"{LIBRARY_PATH} has ABI {version}, this package needs {ABI_VERSION}")
+    if torch.cuda.is_available() and lib.vsp_init() != 0:
+        raise KernelLibraryError(f"vsp_init failed: {lib.vsp_last_error().decode('utf-8', 'replace')}")
     _LIB = lib
     return lib
+
+
+FAULT_NAMES = {0: "the bf16 scan's chunk hand-over"}
+
+
+def check_faults(synchronize: bool = False) -> None:
+    """Raise ``KernelLibraryError`` if a kernel's bounded wait has given up since the last
+    ``clear_faults`` (its outputs from then on are NaN). Without ``synchronize`` it sees kernels
+    that have completed; with it, every kernel queued on the current device so far."""
+    lib = library()
+    if synchronize and torch.cuda.is_available():
+        torch.cuda.synchronize()
+    bits = lib.vsp_fault_bits()
+    if bits:
+        names = ", ".join(FAULT_NAMES.get(i, f"kernel family {i}") for i in range(32) if bits >> i & 1)
+        raise KernelLibraryError(f"a bounded wait gave up in {names}: its results are invalid (NaN); "
+                                 "clear_faults() resets the record")
+
+
+def clear_faults() -> None:
+    library().vsp_clear_faults()
+
+
+def set_wait_limit(polls: int) -> int:
+    """Polls a bounded wait makes before giving up (negative: the default); returns the previous."""
+    return int(library().vsp_set_wait_limit(polls))
 
 
 def available() -> bool:
@@ -118,6 +150,8 @@ def stream_of(device: torch.device) -> int:
 def call(name: str, *args: object) -> None:
     """Call an entry point and turn a nonzero status into ``KernelLibraryError``."""
     lib = library()
+    if lib.vsp_fault_bits():  # a fault of an earlier call: its results, and what used them, are invalid
+        check_faults()
     status = getattr(lib, name)(*args)
     if status != 0:
         message = lib.vsp_last_error().decode("utf-8", "replace")

@@ -27,6 +27,22 @@ int check_launch(const char* what);
 
 enum Status { OK = 0, ERR_ARG = 1, ERR_UNSUPPORTED = 2, ERR_LAUNCH = 3 };
 
+// ---- bounded waits and the fault record --------------------------------------------------------
+// Kernels whose waves hand work to each other through LDS flags wait with a bounded number of
+// polls. A wait that gives up stores 1 into its kernel family's word of the fault record (pinned
+// host memory, set up by vsp_init; the host reads it without a device synchronisation), and the
+// kernel writes NaN in place of its later outputs: a broken hand-over can neither hang the device
+// nor pass unnoticed. The limit is a kernel argument, so a test can make the waits give up from
+// the host (vsp_set_wait_limit) while every kernel still runs to its end.
+enum FaultFamily { FAULT_SCAN_CHAIN = 0, kFaultWords = 16 };
+unsigned* fault_record();  // device address of the fault words; null before vsp_init
+int wait_limit();          // polls before a bounded wait gives up
+
+__device__ __forceinline__ void record_fault(unsigned* record, int family) {
+  // a plain (system-scope) store of a constant: no atomic read-modify-write on host memory
+  if (record != nullptr) __hip_atomic_store(record + family, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+
 // ---- launchers shared between translation units ------------------------------------------------
 // The register-resident single-token delta step (delta_step.hip) for head widths 16, 32, 64 and
 // 128; false when the width or the state's alignment needs the general token-serial kernel.

@@ -49,7 +49,7 @@ struct Carried {
 template <typename TIn>
 __global__ __launch_bounds__(256) void delta_serial_kernel(const TIn* __restrict__ q, const TIn* __restrict__ k,
                                                            const TIn* __restrict__ v, const TIn* __restrict__ beta,
-                                                           const float* __restrict__ s_in, float* __restrict__ s_out,
+                                                           const float* s_in, float* s_out,  // may alias
                                                            TIn* __restrict__ o, const uint8_t* __restrict__ active,
                                                            const TIn* kc, const TIn* vc, const TIn* bc, int T, int H,
                                                            int D, int groups) {
@@ -878,13 +878,15 @@ __device__ __forceinline__ int flag_peek(const int* f) {
   __atomic_signal_fence(__ATOMIC_SEQ_CST);
   return value;
 }
-// Wait until *f >= want, polling every 64 * SLEEP cycles. The spin limit (2^19 polls) is never
-// reached while the hand-over protocol holds; it only keeps a broken protocol from hanging the
-// device.
+// Wait until *f >= want, polling every 64 * SLEEP cycles, at most `limit` polls after the first
+// look. The limit (2^19 polls by default, seconds) is never reached while the hand-over protocol
+// holds; a wait that gives up returns false, and the caller records the fault (record_fault) and
+// marks the workgroup broken, so its later outputs are written as NaN.
 template <int SLEEP = 1>
-__device__ __forceinline__ void flag_wait(const int* f, int want) {
-  for (int spin = 0; spin < (1 << 19); ++spin) {
-    if (flag_peek(f) >= want) return;
+__device__ __forceinline__ bool flag_wait(const int* f, int want, int limit) {
+  for (int spin = 0;; ++spin) {
+    if (flag_peek(f) >= want) return true;
+    if (spin >= limit) return false;
     __builtin_amdgcn_s_sleep(SLEEP);
   }
 }
@@ -895,7 +897,8 @@ __global__ __launch_bounds__(512) void delta_chain_bf16_kernel(const TIn* __rest
                                                                const __bf16* __restrict__ tmat,
                                                                const float* __restrict__ s_in, float* __restrict__ s_out,
                                                                TIn* __restrict__ o, const uint8_t* __restrict__ active,
-                                                               const TIn* kc, const TIn* vc, const TIn* bc, int T, int H) {
+                                                               const TIn* kc, const TIn* vc, const TIn* bc, int T, int H,
+                                                               unsigned* fault, int wait_limit) {
   const Carried<TIn> carried{kc, vc, bc};
   using E = __bf16;
   static_assert(sizeof(TIn) == 2, "bf16 inputs");
@@ -916,7 +919,7 @@ __global__ __launch_bounds__(512) void delta_chain_bf16_kernel(const TIn* __rest
   __shared__ __align__(16) float sU[NSL][4 * 64 * 4]; // U: token tile ti, accumulator layout
   __shared__ __align__(16) E sHo[NSL][BV * PK];       // H^T of the slice before the chunk: row = value column
   __shared__ __align__(16) E sD[NSL][2 * FR];         // Delta: token block kb, as the output's operand
-  __shared__ int staged[NSL], consumed[NSL], done;
+  __shared__ int staged[NSL], consumed[NSL], done, broken;
 
   const int lg = xcd_logical_block(blockIdx.x, gridDim.x);
   const int slice = lg % NS, bh = lg / NS;
@@ -937,8 +940,24 @@ __global__ __launch_bounds__(512) void delta_chain_bf16_kernel(const TIn* __rest
   auto put_frag = [&](E* base, int f, const bf16x8& x) { *reinterpret_cast<bf16x8*>(base + f * FR + 8 * l) = x; };
 
   if (threadIdx.x < NSL) staged[threadIdx.x] = consumed[threadIdx.x] = -1;
-  if (threadIdx.x == 0) done = -1;
+  if (threadIdx.x == 0) {
+    done = -1;
+    broken = 0;
+  }
   __syncthreads();
+  // a bounded wait that gave up: the fault is recorded and the workgroup's later outputs are NaN
+  auto await = [&](const int* f, int want) {
+    if (!flag_wait<1>(f, want, wait_limit)) {
+      record_fault(fault, FAULT_SCAN_CHAIN);
+      flag_release(&broken, 1);
+    }
+  };
+  auto await_slow = [&](const int* f, int want) {
+    if (!flag_wait<4>(f, want, wait_limit)) {
+      record_fault(fault, FAULT_SCAN_CHAIN);
+      flag_release(&broken, 1);
+    }
+  };
 
   if (wave == 0) {
     // ---- the chain: Delta = U - W H, H <- H + K^T Delta per chunk ----
@@ -970,8 +989,8 @@ __global__ __launch_bounds__(512) void delta_chain_bf16_kernel(const TIn* __rest
     auto ready = [&](int c, int st, int cs) {
       const int s = c % NSL;
       if (st < c || cs < c - NSL) {
-        flag_wait(&staged[s], c);
-        flag_wait(&consumed[s], c - NSL);
+        await(&staged[s], c);
+        await(&consumed[s], c - NSL);
       }
     };
 
@@ -1017,10 +1036,12 @@ __global__ __launch_bounds__(512) void delta_chain_bf16_kernel(const TIn* __rest
 #pragma unroll
         for (int kb = 0; kb < 2; ++kb) hreg[m] = mfma_bf16(kt[m][kb], db[kb], hreg[m]);
     }
+    const bool bad = flag_peek(&broken) != 0;
 #pragma unroll
     for (int m = 0; m < HB; ++m)
 #pragma unroll
-      for (int r = 0; r < 4; ++r) s_out[((size_t)bh * DK + 16 * m + 4 * g + r) * DK + v0 + lq] = hreg[m][r];
+      for (int r = 0; r < 4; ++r)
+        s_out[((size_t)bh * DK + 16 * m + 4 * g + r) * DK + v0 + lq] = bad ? __builtin_nanf("") : hreg[m][r];
     return;
   }
 
@@ -1177,7 +1198,7 @@ __global__ __launch_bounds__(512) void delta_chain_bf16_kernel(const TIn* __rest
     const bf16x4 z4{};
     const bf16x8 tf[6] = {join4(tl[0], z4), join4(tl[1], tl[2]), join4(tl[3], tl[4]),
                           join4(tl[5], z4), join4(tl[6], tl[7]), join4(tl[8], tl[9])};
-    flag_wait<4>(&done, c - NSL);  // the chain is done with the slot's previous chunk
+    await_slow(&done, c - NSL);  // the chain is done with the slot's previous chunk
     // W^T = K^T T^T (dk tile m, token tile ti): its tile pairs over dk are the chain's -W operand
 #pragma unroll
     for (int ti = 0; ti < 4; ++ti) {
@@ -1211,6 +1232,7 @@ __global__ __launch_bounds__(512) void delta_chain_bf16_kernel(const TIn* __rest
     for (int kb = 0; kb < KBF; ++kb) hf[kb] = acc_frag(&sHo[s][lq * PK + 32 * kb]);
     const bf16x8 d0 = frag_at(sD[s], 0), d1 = frag_at(sD[s], 1);
     flag_release(&consumed[s], c);  // after the reads above: the chain may reuse the slot
+    const bool bad = flag_peek(&broken) != 0;
     const unsigned cb = (unsigned)c * kChunk * row_bytes;
 #pragma unroll
     for (int J = 0; J < 4; ++J) {
@@ -1223,7 +1245,7 @@ __global__ __launch_bounds__(512) void delta_chain_bf16_kernel(const TIn* __rest
       typedef TIn O4 __attribute__((ext_vector_type(4)));
       O4 w4;
 #pragma unroll
-      for (int r = 0; r < 4; ++r) w4[r] = from_f32<TIn>(on ? acc[r] : 0.f);
+      for (int r = 0; r < 4; ++r) w4[r] = from_f32<TIn>(bad ? __builtin_nanf("") : (on ? acc[r] : 0.f));
       __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, w4), ro, off_q, cb + 16u * J * row_bytes, 0);
     }
   };
@@ -1233,7 +1255,7 @@ __global__ __launch_bounds__(512) void delta_chain_bf16_kernel(const TIn* __rest
   auto run = [&](int c, const bf16x4 (&qc)[4][HB], bf16x4 (&qn)[4][HB], uint64_t mc, uint64_t& mn) {
     form(c, qc, mc, mn);
     if (c + NH < nc) issue_loads(c + NH, qn, mn);
-    flag_wait<4>(&done, c);
+    await_slow(&done, c);
     write_output(c, qc);
   };
   uint64_t m0 = ~0ull, m1 = ~0ull;  // the flags of the chunks whose loads are in flight
@@ -1290,7 +1312,8 @@ void launch_chunked(const TIn* q, const TIn* k, const TIn* v, const TIn* beta, c
                      beta, tmat, active, carried.k, carried.v, carried.beta, T, H, total);
   if constexpr (sizeof(E) == 2 && DK >= 32 && DK <= 64) {  // (at 128 the staging registers would spill)
     hipLaunchKernelGGL((delta_chain_bf16_kernel<TIn, DK, CARRY>), dim3((unsigned)(B * H * (DK / 16))), dim3(512), 0,
-                       stream, q, k, v, tmat, s_in, s_out, o, active, carried.k, carried.v, carried.beta, T, H);
+                       stream, q, k, v, tmat, s_in, s_out, o, active, carried.k, carried.v, carried.beta, T, H,
+                       fault_record(), wait_limit());
   } else {
     hipLaunchKernelGGL((delta_chain_kernel<TIn, E, DK, CARRY>), dim3((unsigned)(B * H * (DK / 16))),
                        dim3(64 * (ChainShape<E, DK>::NH + 1)), 0, stream, q, k, v, tmat, s_in, s_out, o, active,

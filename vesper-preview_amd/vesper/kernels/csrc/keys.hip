@@ -145,17 +145,22 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))) voi
 #pragma unroll
       for (int e = 0; e < 8; ++e) win[0][e] = cur[e];
     }
-    // normalize_keys per head: s = u / max(peak, floor), key = s / sqrt(max(|s|^2, 1)); each
-    // division is a reciprocal (v_rcp / v_rsq, 1 ulp) per token and lane times the 8 features,
-    // far inside float32's 2e-5 bound
+    // normalize_keys per head: s = u / max(peak, floor), key = s / sqrt(max(|s|^2, 1)). The first
+    // division is a reciprocal (v_rcp, 1 ulp) refined by one Newton step on the residual
+    // (r = u - s0 * scale by FMA, s = s0 + r / scale), which gives the correctly rounded quotient
+    // here: the peak component of a row scales to exactly 1 and a row under the floor to exactly
+    // u / 1e-6, as the reference's division does. The second is v_rsq (1 ulp) times the 8
+    // features, far inside float32's 2e-5 bound, and exact where the norm is floored at one.
     float peak = 0.f;
 #pragma unroll
     for (int e = 0; e < 8; ++e) peak = __builtin_fmaxf(peak, fabsf(u[e]));
-    const float inv_scale = __builtin_amdgcn_rcpf(__builtin_fmaxf(group_max<LPH>(peak), kKeyFloor));
+    const float scale = __builtin_fmaxf(group_max<LPH>(peak), kKeyFloor);
+    const float inv_scale = __builtin_amdgcn_rcpf(scale);
     float ss = 0.f;
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-      u[e] = u[e] * inv_scale;
+      const float s0 = u[e] * inv_scale;
+      u[e] = __builtin_fmaf(__builtin_fmaf(-s0, scale, u[e]), inv_scale, s0);
       ss += u[e] * u[e];
     }
     const float inv_den = __builtin_amdgcn_rsqf(__builtin_fmaxf(group_sum<LPH>(ss), 1.f));

@@ -135,11 +135,12 @@ def _check_carried(z: Tensor, active: Tensor | None, carried_z: Tensor) -> None:
 
 def key_step(z: Tensor, history: Tensor, taps: Tensor, heads: int, *, active: Tensor | None = None,
              carried_z: Tensor | None = None) -> tuple[Tensor, Tensor]:
-    """The keys and the next key history of key inputs ``z [b, n, d]`` (``n >= 1``), no gradient.
+    """The keys and the next key history of key inputs ``z [b, n, d]``, no gradient.
 
     As ``fused_keys`` for the keys; the next history is the newest ``K - 1`` inputs of ``(history,
     z)`` (with ``carried_z``, the carried rows of inactive tokens) as a new float32 ``[b, K-1, d]``
-    tensor, written by the same launch.
+    tensor, written by the same launch. An empty chunk (``n == 0``) returns empty keys and the
+    history unchanged, as ``RecurrentSublayer.keys`` does (``column.py:275-277``).
 
     Raises:
         ContractError: as ``fused_keys``.
@@ -147,6 +148,9 @@ def key_step(z: Tensor, history: Tensor, taps: Tensor, heads: int, *, active: Te
     _check(z, history, taps, heads)
     if carried_z is not None:
         _check_carried(z, active, carried_z)
+    if z.shape[1] == 0:
+        b, _, d = z.shape
+        return z.new_empty(b, 0, heads, d // heads), history
     keys, nxt = _key_step(z, history, taps, heads, active, carried_z, want_history=True)
     assert nxt is not None
     return keys, nxt

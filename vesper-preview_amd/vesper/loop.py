@@ -4,8 +4,8 @@ This is the pass loop of the reference's ``Loop.forward`` (``vesper/loop.py:415-
 a given exit trace (``TraceRule``, ``:203-240``), over a column reduced to its two mixers in the
 order of ``Column.step`` (``vesper/column.py:709-812``):
 
-- recurrent sublayer: projections ``q, z, v, beta`` of the pass input (bf16 matmuls; queries
-  L2-normalised, ``beta = sigmoid``), the key from the key input ``z`` (``normalize_keys``, after
+- recurrent sublayer: projections ``q, z, v, beta`` of the pass input (bf16 matmuls; the query
+  is not normalized, ``column.py:247``; ``beta = sigmoid``), the key from the key input ``z`` (``normalize_keys``, after
   the causal key filter when the column has one, ``column.py:255-289``, with the pass's key
   history), the carry merges for halted tokens (their key input before the filter, ``k, v, beta``
   after, ``column.py:779-789``), the delta scan (``vsp_delta_scan_bf16`` with the active mask),
@@ -187,7 +187,7 @@ class LoopedColumn:
         h, dk = self.heads, self.head_dim
         xb = x.to(BF16)
         q_in, z, v, beta = self.project_rec(t, xb)
-        q = _normalize(q_in, h)
+        q = q_in.view(b, n, h, dk)  # the scan's query is not normalized (column.py:247)
         fused = self.copy_forward == "fused" and carried is not None and active is not None
         where = self.copy_forward == "where" and carried is not None and active is not None
         if where and carried is not None and active is not None and carried.z is not None:
