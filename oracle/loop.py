@@ -9,12 +9,14 @@ Restated from the reference's pass loop and column:
   their place (copy-forward); a halted token's hidden state is carried forward unchanged
   (``:452``); the last pass halts every token still active.
 - ``mixer_column_step`` is the column's two mixers as ``Column.step`` orders them
-  (``vesper/column.py:709-812``): recurrent projections, the carry merges of ``k, v, beta``
-  (``:784-789``), the delta scan, the residual; attention projections, the carry merges of the
+  (``vesper/column.py:709-812``): the pre-normalization (``RMSNorm`` with its gain at one), the
+  recurrent projections, the carry merges of ``k, v, beta``
+  (``:784-789``), the delta scan, the residual; the pre-normalization and the attention
+  projections, the carry merges of the
   attention keys and values (``:795-796``), window attention, the residual; optionally the causal
   key filter before the keys' normalization (``RecurrentSublayer.keys``, ``:255-289``), its
-  history carried per pass. Norms, rotary and the FFN are not part of the mixer path and are left
-  out; keys are L2-normalised (``normalize_keys``) as the scan requires, queries are not
+  history carried per pass. Rotary and the FFN are not part of the mixer path and are left out;
+  keys are L2-normalised (``normalize_keys``) as the scan requires, queries are not
   (``RecurrentSublayer.project``, ``column.py:236-253``; ``docs/model-card.md:26``).
 - ``mixer_decode_step`` is the same column one token at a time over per-pass KV rings, at a fixed
   depth with every pass dense, as ``decode_step`` (``vesper/decode.py:29-46``) runs it.
@@ -110,6 +112,22 @@ def loop_forward(x0: Tensor, step: ColumnStep, states: Sequence[Tensor], exits: 
     return LoopOutput(y=x, states=tuple(new_states), n_iters=n_iters, per_pass=tuple(per_pass))
 
 
+RMS_EPS = 1e-6  # column.py:55
+RMS_SCALE_FLOOR = 1e-3  # column.py:56
+
+
+def rms_norm(x: Tensor) -> Tensor:
+    """``RMSNorm`` with its gain at one (its initial value), ``column.py:146-188``: ``x / sqrt(mean(x^2)
+    + 1e-6)``, computed scale-safely (each row divided by its peak magnitude floored at 1e-3 first),
+    in the input's dtype or float32, whichever is wider. The pre-normalization of both sublayers in
+    ``Column.step`` (``column.py:779``, ``:793``)."""
+    wide = x.to(torch.promote_types(x.dtype, torch.float32))
+    scale = wide.abs().amax(dim=-1, keepdim=True).clamp_min(RMS_SCALE_FLOOR)
+    scaled = wide / scale
+    rms = torch.sqrt(scaled.square().mean(dim=-1, keepdim=True) + RMS_EPS / (scale * scale))
+    return (scaled / rms).to(x.dtype)
+
+
 def _bf(t: Tensor) -> Tensor:
     """Round to bfloat16 and come back to the wide dtype."""
     return t.to(BF16).to(t.dtype)
@@ -170,20 +188,22 @@ def mixer_column_step(weights: MixerWeights, masked: bool = True, bf16: bool = T
         active = None if carry is None else carry[0]
         mask = active if masked else None
         scan_state, history = state if weights.taps is not None else (state, None)
-        q = mm(x, weights.wq[t]).view(b, n, h, dk)
-        z = mm(x, weights.wk[t]).view(b, n, h * dk)
+        xn = rms_norm(x)
+        q = mm(xn, weights.wq[t]).view(b, n, h, dk)
+        z = mm(xn, weights.wk[t]).view(b, n, h * dk)
         if carry is not None and carry[1].z is not None:
             z = carry_in(active, z, carry[1].z)
         k, history = _keys(weights, t, z, history, rnd)
-        v = mm(x, weights.wv[t]).view(b, n, h, dk)
-        beta = rnd(torch.sigmoid(mm(x, weights.wb[t])))
+        v = mm(xn, weights.wv[t]).view(b, n, h, dk)
+        beta = rnd(torch.sigmoid(mm(xn, weights.wb[t])))
         if carry is not None:
             k, v, beta = (carry_in(active, f, c) for f, c in zip((k, v, beta), (carry[1].k, carry[1].v, carry[1].beta)))
         r, new_state = delta_scan_chunked(q, k, v, beta, scan_state, 64, active=mask)
         x1 = x + rnd(r).reshape(b, n, h * dk)
-        aq = mm(x1, weights.waq[t]).view(b, n, h, dk)
-        ak = mm(x1, weights.wak[t]).view(b, n, hkv, dk)
-        av = mm(x1, weights.wav[t]).view(b, n, hkv, dk)
+        x1n = rms_norm(x1)
+        aq = mm(x1n, weights.waq[t]).view(b, n, h, dk)
+        ak = mm(x1n, weights.wak[t]).view(b, n, hkv, dk)
+        av = mm(x1n, weights.wav[t]).view(b, n, hkv, dk)
         if carry is not None:
             ak, av = (carry_in(active, f, c) for f, c in zip((ak, av), (carry[1].attn_k, carry[1].attn_v)))
         a = window_attention(aq, ak, av, w, active=mask)
@@ -229,16 +249,18 @@ def mixer_decode_step(weights: MixerWeights, depth: int, bf16: bool = True
         new = list(states)
         for t in range(depth):
             scan_state, history, (rk, rv, rp, rvalid) = states[t]
-            q = mm(x, weights.wq[t]).view(b, 1, h, dk)
-            z = mm(x, weights.wk[t]).view(b, 1, h * dk)
+            xn = rms_norm(x)
+            q = mm(xn, weights.wq[t]).view(b, 1, h, dk)
+            z = mm(xn, weights.wk[t]).view(b, 1, h * dk)
             k, history = _keys(weights, t, z, history, rnd)
-            v = mm(x, weights.wv[t]).view(b, 1, h, dk)
-            beta = rnd(torch.sigmoid(mm(x, weights.wb[t])))
+            v = mm(xn, weights.wv[t]).view(b, 1, h, dk)
+            beta = rnd(torch.sigmoid(mm(xn, weights.wb[t])))
             o, scan_state = delta_scan_step(q[:, 0], k[:, 0], v[:, 0], beta[:, 0], scan_state)
             x1 = x + rnd(o).reshape(b, 1, h * dk)
-            aq = mm(x1, weights.waq[t]).view(b, 1, h, dk)
-            ak = mm(x1, weights.wak[t]).view(b, 1, hkv, dk)
-            av = mm(x1, weights.wav[t]).view(b, 1, hkv, dk)
+            x1n = rms_norm(x1)
+            aq = mm(x1n, weights.waq[t]).view(b, 1, h, dk)
+            ak = mm(x1n, weights.wak[t]).view(b, 1, hkv, dk)
+            av = mm(x1n, weights.wav[t]).view(b, 1, hkv, dk)
             a = ring_attend(aq, ak, av, pos, rk, rv, rp, rvalid, w)
             ring = kv_ring_write(rk, rv, rp, rvalid, ak, av, pos)
             x = x1 + rnd(a).reshape(b, 1, h * dk)

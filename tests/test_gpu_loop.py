@@ -93,6 +93,19 @@ def test_config_size_two_passes_match_the_fp32_oracle():
         assert relative_error(got.states[t], want.states[t]) < 3e-2, t
 
 
+def test_eight_passes_at_b4_t768_d512_h8_w512_match_the_oracle():
+    # the config's depth and widths (8 passes, d 512, 8 heads of 64, window 512) at a shorter
+    # sequence, so the float64 oracle finishes in seconds; the window still slides
+    b, n, d, h, dk, w, passes = 4, 768, 512, 8, 64, 512, 8
+    column, x0, exits, states = _setup(b, n, d, h, h, dk, w, passes, seed=13)
+    got = column.forward(x0.to(GPU), [s.to(GPU) for s in states], [e.to(GPU) for e in exits])
+    want = _oracle(column, x0, exits, states)
+    assert torch.equal(got.n_iters.cpu(), want.n_iters)
+    assert relative_error(got.y, want.y) < 3e-2
+    for t in range(passes):
+        assert relative_error(got.states[t], want.states[t]) < 3e-2, t
+
+
 def test_refusals():
     from vesper.contracts import ContractError
     from vesper.loop import LoopedColumn

@@ -187,3 +187,53 @@ def test_refusals():
         ring_attention(q.float(), q, q, torch.tensor([[1]], device=GPU), ring)
     with pytest.raises(ContractError, match="axis"):
         ring_attention(q, q, q, torch.tensor([[1, 2]], device=GPU), ring)
+
+
+def test_decode_config_256_steps_delta_and_ring_against_the_chunked_oracles():
+    """The decode workload at its full size: batch 64, H 8, d 64, 256 steps, each the delta rule's
+    single step on the fp32 state [64, 8, 64, 64] (S0 ~ N(0, 0.02^2)) and attention over a bf16 KV
+    ring of 512 entries prefilled at positions 0..511, the step at position 512 + s writing slot
+    s (every slot of the first half is overwritten). The truth: the chunked delta scan over the 256
+    tokens (the same recurrence) and window attention with the 512 prefilled rows as the cache
+    (the ring's visible entries are the window's keys), both on the CPU."""
+    from oracle.delta import delta_scan_chunked, normalize_keys
+    from vesper.kernels.delta_scan import delta_scan_step_fused
+    from vesper.kernels.ring_attn import RingKVCache, ring_attention
+
+    b, h, dk, w, steps = 64, 8, 64, 512, 256
+    g = torch.Generator().manual_seed(11)
+    s0 = 0.02 * torch.randn(b, h, dk, dk, generator=g)
+    q = torch.randn(b, steps, h, dk, generator=g)
+    k = normalize_keys(torch.randn(b, steps, h, dk, generator=g))
+    q = normalize_keys(q)
+    v = torch.randn(b, steps, h, dk, generator=g)
+    beta = torch.sigmoid(torch.randn(b, steps, h, generator=g))
+    rk = torch.randn(b, w, h, dk, generator=g).to(BF16)
+    rv = torch.randn(b, w, h, dk, generator=g).to(BF16)
+    aq = torch.randn(b, steps, h, dk, generator=g).to(BF16)
+    ak = torch.randn(b, steps, h, dk, generator=g).to(BF16)
+    av = torch.randn(b, steps, h, dk, generator=g).to(BF16)
+
+    state = s0.to(GPU)
+    ring = RingKVCache(rk.to(GPU), rv.to(GPU), torch.arange(w).expand(b, w).contiguous().to(GPU),
+                       torch.ones(b, w, dtype=torch.bool, device=GPU), w)
+    dq, dkk, dv, db = (t.to(GPU) for t in (q, k, v, beta))
+    daq, dak, dav = (t.to(GPU) for t in (aq, ak, av))
+    outs, atts = [], []
+    with torch.no_grad():
+        for s in range(steps):
+            o, _ = delta_scan_step_fused(dq[:, s], dkk[:, s], dv[:, s], db[:, s], state, out_state=state)
+            a, _ = ring_attention(daq[:, s : s + 1], dak[:, s : s + 1], dav[:, s : s + 1],
+                                  torch.full((b, 1), w + s, device=GPU), ring, inplace=True, check_positions=False)
+            outs.append(o)
+            atts.append(a)
+    o_ref, s_ref = delta_scan_chunked(q.double(), k.double(), v.double(), beta.double(), s0.double(), 64)
+    assert relative_error(torch.stack(outs, dim=1), o_ref) < 1e-5
+    assert relative_error(state, s_ref) < 1e-5
+    keys = torch.cat([rk, ak], dim=1).float()
+    values = torch.cat([rv, av], dim=1).float()
+    a_ref = oa.window_attention(aq.float(), keys, values, w)
+    assert relative_error(torch.cat(atts, dim=1), a_ref) < 1e-2
+    # the ring now holds positions 256..767: slots 0..255 rewritten with the new tokens
+    assert torch.equal(ring.pos[:, :steps].cpu(), torch.arange(w, w + steps).expand(b, steps))
+    assert torch.equal(ring.k[:, :steps].cpu(), ak) and torch.equal(ring.v[:, steps:].cpu(), rv[:, steps:])

@@ -207,10 +207,11 @@ def test_the_scan_reads_the_raw_query():
     x = torch.randn(1, n, d, generator=g, dtype=F64)
     s0 = torch.zeros(1, h, dk, dk, dtype=F64)
     y, _, _ = ol.mixer_column_step(weights, masked=False, bf16=False)(x, 0, s0, None)
-    q = (x @ weights.wq[0]).view(1, n, h, dk)
-    k = normalize_keys((x @ weights.wk[0]).view(1, n, h, dk))
-    v = (x @ weights.wv[0]).view(1, n, h, dk)
-    beta = torch.sigmoid(x @ weights.wb[0])
+    xn = x / x.square().mean(dim=-1, keepdim=True).add(1e-6).sqrt()  # RMSNorm, gain one (column.py:146-188)
+    q = (xn @ weights.wq[0]).view(1, n, h, dk)
+    k = normalize_keys((xn @ weights.wk[0]).view(1, n, h, dk))
+    v = (xn @ weights.wv[0]).view(1, n, h, dk)
+    beta = torch.sigmoid(xn @ weights.wb[0])
     o, _ = delta_scan_serial(q, k, v, beta, s0)
     assert float(q.norm(dim=-1).min()) > 1.0
     assert torch.allclose(y - x, o.reshape(1, n, h * dk), rtol=0, atol=1e-12)

@@ -29,7 +29,7 @@ from vesper.column import recurrent_keys
 from vesper.contracts import ContractError, Dims, check_shape
 from vesper.kernels.delta_scan import delta_scan_step_fused
 from vesper.kernels.ring_attn import RingKVCache, ring_attention
-from vesper.loop import BF16, LoopedColumn, _normalize
+from vesper.loop import BF16, LoopedColumn, _normalize, rms_norm_bf16
 
 WARM_STEPS = 3  # eager calls before the capture (vesper/graphs.py:99)
 PER_PASS = 6  # flat tensors per pass: scan state, key history, ring keys, values, positions, valid
@@ -93,7 +93,7 @@ def decode_step(column: LoopedColumn, depth: int, values: Sequence[Tensor],
     with torch.no_grad():
         for t in range(depth):
             state, history, rk, rv, rp, rvalid = flat[PER_PASS * t: PER_PASS * (t + 1)]
-            q_in, z, v, beta = column.project_rec(t, x.to(BF16))
+            q_in, z, v, beta = column.project_rec(t, rms_norm_bf16(x))
             q = q_in.view(b, 1, h, dk)  # the scan's query is not normalized (column.py:247)
             if column.taps is None:
                 k = _normalize(z, h)
@@ -102,7 +102,7 @@ def decode_step(column: LoopedColumn, depth: int, values: Sequence[Tensor],
                 history.copy_(nxt)
             o, _ = delta_scan_step_fused(q[:, 0], k[:, 0], v[:, 0], beta.view(b, h), state, out_state=state)
             x1 = x + o.reshape(b, 1, h * dk)  # float32 (promoted in the add)
-            aq, ak, av = column.project_attn(t, x1.to(BF16))
+            aq, ak, av = column.project_attn(t, rms_norm_bf16(x1))
             ring = RingKVCache(rk, rv, rp, rvalid, column.window)
             a, _ = ring_attention(aq, ak, av, position, ring, inplace=True, check_positions=False,
                                   workspace=workspace)

@@ -4,13 +4,14 @@ This is the pass loop of the reference's ``Loop.forward`` (``vesper/loop.py:415-
 a given exit trace (``TraceRule``, ``:203-240``), over a column reduced to its two mixers in the
 order of ``Column.step`` (``vesper/column.py:709-812``):
 
-- recurrent sublayer: projections ``q, z, v, beta`` of the pass input (bf16 matmuls; the query
+- recurrent sublayer: the pre-normalization (``RMSNorm`` with its gain at one, ``column.py:146-188``),
+  projections ``q, z, v, beta`` of the pass input (bf16 matmuls; the query
   is not normalized, ``column.py:247``; ``beta = sigmoid``), the key from the key input ``z`` (``normalize_keys``, after
   the causal key filter when the column has one, ``column.py:255-289``, with the pass's key
   history), the carry merges for halted tokens (their key input before the filter, ``k, v, beta``
   after, ``column.py:779-789``), the delta scan (``vsp_delta_scan_bf16`` with the active mask),
   the residual;
-- attention sublayer: projections, the carry merges of the attention keys and values
+- attention sublayer: the pre-normalization, projections, the carry merges of the attention keys and values
   (``column.py:795-796``), window attention over the chunk (``vsp_window_attn_bf16`` with the
   active mask), the residual.
 
@@ -22,8 +23,8 @@ the carried rows of inactive tokens inside their loads (the key filter's ``carri
 halting tokens' projections into the carried buffers and carries the hidden state, in place of the
 reference's ``where`` merges; ``copy_forward="where"`` runs those merges as torch selects.
 
-All passes run even when no token is active any more. Norms, rotary embeddings and the FFN are not
-part of the mixer path and are left out. The residual stream stays in float32 (autocast's convention); matmuls and mixers run
+All passes run even when no token is active any more. Rotary embeddings and the FFN are not part
+of the mixer path and are left out. The residual stream stays in float32 (autocast's convention); matmuls and mixers run
 in bfloat16 with the scan state in float32. Forward only.
 """
 
@@ -59,6 +60,21 @@ def _normalize(x: Tensor, heads: int) -> Tensor:
     if key not in _ONES:
         _ONES[key] = torch.ones(1, d, dtype=torch.float32, device=x.device)
     return fused_keys(x, x.new_empty(x.shape[0], 0, d, dtype=torch.float32), _ONES[key], heads)
+
+
+RMS_EPS = 1e-6  # column.py:55
+RMS_SCALE_FLOOR = 1e-3  # column.py:56
+
+
+def rms_norm_bf16(x: Tensor) -> Tensor:
+    """The sublayers' pre-normalization, ``RMSNorm`` with its gain at one (``column.py:146-188``):
+    ``x / sqrt(mean(x^2) + 1e-6)`` of the float32 residual stream ``x [..., d]``, each row first
+    divided by its peak magnitude floored at 1e-3 (scale-safe, as the reference computes it), in
+    float32, returned in bfloat16 for the projections."""
+    scale = x.abs().amax(dim=-1, keepdim=True).clamp_min(RMS_SCALE_FLOOR)
+    scaled = x / scale
+    rms = torch.sqrt(scaled.square().mean(dim=-1, keepdim=True) + RMS_EPS / (scale * scale))
+    return (scaled / rms).to(BF16)
 
 
 def _where_tokens(mask: Tensor, a: Tensor, b: Tensor) -> Tensor:
@@ -185,7 +201,7 @@ class LoopedColumn:
               carried: Written | None) -> tuple[Tensor, Tensor, Tensor | None, Written]:
         b, n, d = x.shape
         h, dk = self.heads, self.head_dim
-        xb = x.to(BF16)
+        xb = rms_norm_bf16(x)
         q_in, z, v, beta = self.project_rec(t, xb)
         q = q_in.view(b, n, h, dk)  # the scan's query is not normalized (column.py:247)
         fused = self.copy_forward == "fused" and carried is not None and active is not None
@@ -206,7 +222,7 @@ class LoopedColumn:
         else:
             r, new_state = delta_scan_fused(q, k, v, beta, state, active=active)
         x1 = x + r.reshape(b, n, h * dk)  # float32 (promoted in the add)
-        aq, ak, av = self.project_attn(t, x1.to(BF16))
+        aq, ak, av = self.project_attn(t, rms_norm_bf16(x1))
         if where and carried is not None and active is not None:
             ak = _where_tokens(active, ak, carried.attn_k)
             av = _where_tokens(active, av, carried.attn_v)
