@@ -37,8 +37,9 @@ const char* vsp_last_error(void);
 int vsp_abi_version(void);
 
 /* Set-up, once per process before the first kernel call (later calls return at once): allocates
- * the fault record below in pinned host memory. No counterpart in the reference, whose kernels
- * come from a library that needs none. */
+ * the fault record below in pinned host memory, and on every visible device takes the address of
+ * the static scratch of vsp_ring_attn_noalloc_bf16 (with that device current) and zeroes it. No
+ * counterpart in the reference, whose kernels come from a library that needs none. */
 int vsp_init(void);
 
 /* The fault record of the bounded waits. Kernels whose waves hand work to each other through LDS
@@ -187,6 +188,19 @@ int vsp_ring_attn_f16(const void* q, const void* k, const void* v, const int64_t
                       int64_t* ring_pos, uint8_t* ring_valid, void* o, const uint8_t* active, void* workspace,
                       size_t workspace_bytes, int B, int H, int HKV, int D, int window, float scale, int write,
                       void* stream);
+
+/* vsp_ring_attn_bf16 with no workspace argument and no allocation of any kind: the per-row arrival
+ * counters live in a static device array of 65536 counters (256 KiB per GPU, held until the
+ * process ends), whose per-device address vsp_init takes and zeroes. No counterpart in the
+ * reference: it is for callers that cannot allocate (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc). B at most 65536 (larger B is refused with
+ * VSP_ERR_ARG); vsp_init must have run. Every call that writes the ring leaves the counters zero.
+ * All calls on one GPU share the array: calls that overlap in time on one GPU (two streams)
+ * race, so they must be ordered. */
+int vsp_ring_attn_noalloc_bf16(const void* q, const void* k, const void* v, const int64_t* pos, void* ring_k,
+                               void* ring_v, int64_t* ring_pos, uint8_t* ring_valid, void* o,
+                               const uint8_t* active, int B, int H, int HKV, int D, int window, float scale,
+                               int write, void* stream);
 
 /* ---- the causal key filter and key normalization (before the scan) --------------------------
  * z: [B, N, D] key inputs (bf16, f16 or fp32); history: [B, K-1, D] fp32, the K-1 inputs before

@@ -53,6 +53,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "vsp_ring_attn_workspace_bytes": (Z, [I]),
     "vsp_ring_attn_bf16": (I, [P, P, P, P, P, P, P, P, P, P, P, Z, I, I, I, I, I, F, I, P]),
     "vsp_ring_attn_f16": (I, [P, P, P, P, P, P, P, P, P, P, P, Z, I, I, I, I, I, F, I, P]),
+    "vsp_ring_attn_noalloc_bf16": (I, [P, P, P, P, P, P, P, P, P, P, I, I, I, I, I, F, I, P]),
     "vsp_key_filter_bf16": (I, [P, P, P, P, I, I, I, I, I, P]),
     "vsp_key_filter_f16": (I, [P, P, P, P, I, I, I, I, I, P]),
     "vsp_key_filter_f32": (I, [P, P, P, P, I, I, I, I, I, P]),

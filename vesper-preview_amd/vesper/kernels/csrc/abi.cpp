@@ -61,6 +61,8 @@ extern "C" int vsp_init(void) {
     g_fault_host = static_cast<unsigned*>(host);
     g_fault_device = static_cast<unsigned*>(dev);
   }
+  const int st = vsp::ring_scratch_init();
+  if (st != vsp::OK) return st;
   g_initialised = true;
   g_last_error[0] = '\0';
   return vsp::OK;

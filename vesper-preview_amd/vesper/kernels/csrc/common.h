@@ -38,6 +38,11 @@ enum FaultFamily { FAULT_SCAN_CHAIN = 0, kFaultWords = 16 };
 unsigned* fault_record();  // device address of the fault words; null before vsp_init
 int wait_limit();          // polls before a bounded wait gives up
 
+// The allocation-free ring attention entry's static scratch (decode.hip): rows of one call at most,
+// and its per-device set-up, run by vsp_init.
+constexpr int kNoAllocMaxRows = 1 << 16;
+int ring_scratch_init();
+
 __device__ __forceinline__ void record_fault(unsigned* record, int family) {
   // a plain (system-scope) store of a constant: no atomic read-modify-write on host memory
   if (record != nullptr) __hip_atomic_store(record + family, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);

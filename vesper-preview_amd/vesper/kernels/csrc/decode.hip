@@ -291,9 +291,63 @@ int ring_attn(const T* q, const T* knew, const T* vnew, const int64_t* pos, T* r
 }
 
 }  // namespace
+
+// ---- the allocation-free entry's static scratch -------------------------------------------------
+// The per-row arrival counters of the in-kernel ring write, for callers that cannot allocate (code
+// under graph capture, serving loops): a file-scope device array, one copy per GPU, alive until the
+// process ends. Host code never passes the array's name to a kernel (in host code it is a host-side
+// stand-in, not a device address): ring_scratch_init takes each device's address with
+// hipGetSymbolAddress, with that device current, and the entry point uses that address.
+constexpr int kMaxDevices = 64;
+__device__ __align__(256) uint32_t scratch[kNoAllocMaxRows];
+uint32_t* g_scratch[kMaxDevices] = {};
+
+int ring_scratch_init() {
+  int count = 0, current = 0;
+  hipError_t err = hipGetDeviceCount(&count);
+  if (err != hipSuccess) return fail(ERR_LAUNCH, "vsp_init: hipGetDeviceCount: %s", hipGetErrorString(err));
+  err = hipGetDevice(&current);
+  if (err != hipSuccess) return fail(ERR_LAUNCH, "vsp_init: hipGetDevice: %s", hipGetErrorString(err));
+  for (int d = 0; d < count && d < kMaxDevices; ++d) {
+    if (g_scratch[d] != nullptr) continue;
+    err = hipSetDevice(d);
+    void* ptr = nullptr;
+    if (err == hipSuccess) err = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    // the counters start at zero; every call that writes the ring leaves them zero again
+    if (err == hipSuccess) err = hipMemset(ptr, 0, sizeof(scratch));
+    if (err != hipSuccess) {
+      (void)hipSetDevice(current);
+      return fail(ERR_LAUNCH, "vsp_init: static scratch on device %d: %s", d, hipGetErrorString(err));
+    }
+    g_scratch[d] = static_cast<uint32_t*>(ptr);
+  }
+  err = hipSetDevice(current);
+  if (err != hipSuccess) return fail(ERR_LAUNCH, "vsp_init: hipSetDevice: %s", hipGetErrorString(err));
+  return OK;
+}
+
 }  // namespace vsp
 
 extern "C" size_t vsp_ring_attn_workspace_bytes(int B) { return B > 0 ? (size_t)B * sizeof(uint32_t) : 0; }
+
+extern "C" int vsp_ring_attn_noalloc_bf16(const void* q, const void* k, const void* v, const int64_t* pos,
+                                          void* ring_k, void* ring_v, int64_t* ring_pos, uint8_t* ring_valid, void* o,
+                                          const uint8_t* active, int B, int H, int HKV, int D, int window, float scale,
+                                          int write, void* stream) {
+  const char* who = "vsp_ring_attn_noalloc_bf16";
+  if (B > vsp::kNoAllocMaxRows)
+    return vsp::fail(vsp::ERR_ARG, "%s: %d rows exceed the static scratch's %d", who, B, vsp::kNoAllocMaxRows);
+  int device = 0;
+  const hipError_t err = hipGetDevice(&device);
+  if (err != hipSuccess) return vsp::fail(vsp::ERR_LAUNCH, "%s: hipGetDevice: %s", who, hipGetErrorString(err));
+  if (device < 0 || device >= vsp::kMaxDevices || vsp::g_scratch[device] == nullptr)
+    return vsp::fail(vsp::ERR_ARG, "%s: vsp_init has not set up device %d", who, device);
+  return vsp::ring_attn<__bf16>(static_cast<const __bf16*>(q), static_cast<const __bf16*>(k),
+                                static_cast<const __bf16*>(v), pos, static_cast<__bf16*>(ring_k),
+                                static_cast<__bf16*>(ring_v), ring_pos, ring_valid, static_cast<__bf16*>(o), active,
+                                vsp::g_scratch[device], sizeof(uint32_t) * (size_t)vsp::kNoAllocMaxRows, B, H, HKV, D,
+                                window, scale, write, stream, who);
+}
 
 extern "C" int vsp_ring_attn_bf16(const void* q, const void* k, const void* v, const int64_t* pos, void* ring_k,
                                   void* ring_v, int64_t* ring_pos, uint8_t* ring_valid, void* o,
