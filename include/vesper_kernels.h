@@ -255,6 +255,14 @@ int vsp_key_filter_backward_f32(const float* z, const float* history, const floa
                                 float* grad_z, float* grad_taps, float* grad_history, void* workspace,
                                 size_t workspace_bytes, int B, int N, int D, int heads, int K, void* stream);
 
+/* ---- the sublayers' pre-normalization of the looped column -----------------------------------
+ * RMSNorm (vesper/column.py:146-188): out = x / sqrt(mean(x^2) + 1e-6) * gain per row of `d`
+ * floats, computed scale-safely as the reference does (each row divided by its peak magnitude
+ * floored at 1e-3 first); x: [rows, d] float32, gain: [d] float32 or NULL (all ones), out:
+ * [rows, d] bf16, the projections' operand. d a multiple of 8 in 8..2048; x, gain, out 16-byte
+ * aligned. */
+int vsp_rms_norm_bf16(const float* x, const float* gain, void* out, int rows, int d, void* stream);
+
 /* ---- copy-forward bookkeeping of the looped column ------------------------------------------
  * Replaces the row-wise `where` selects of vesper/loop.py:523-537 (`_merge`: tokens halting now
  * freeze their fresh projections into the carried ones) and vesper/loop.py:441-452 (a halted

@@ -86,12 +86,16 @@ def test_the_product_path_does_not_import_the_oracle():
 
 
 def test_the_scan_switch_refuses_what_it_cannot_run():
-    # the reference's names and refusals (vesper/column.py:382-405); "reference" is not shipped
+    # the reference's names and refusals (vesper/column.py:382-426): "reference" runs anywhere but
+    # not captured on the GPU; the fused scans need the GPU
     from vesper.column import SCAN_IMPLS, check_capturable_scan, check_scan
 
     assert SCAN_IMPLS == ("reference", "fused", "fused-fp32")
-    with pytest.raises(ValueError, match="does not ship"):
-        check_scan("reference", torch.device("cpu"))
+    assert check_scan("reference", torch.device("cpu")) == "reference"
+    assert check_scan("reference", torch.device("cuda")) == "reference"
+    assert check_capturable_scan("reference", torch.device("cpu")) == "reference"
+    with pytest.raises(ValueError, match="cannot run as a captured graph"):
+        check_capturable_scan("reference", torch.device("cuda"))
     with pytest.raises(ValueError, match="must be one of"):
         check_scan("triton", torch.device("cpu"))
     with pytest.raises(ValueError, match="needs the model on CUDA"):
@@ -130,3 +134,54 @@ def test_the_key_filter_refuses_before_launching():
     assert lib.vsp_key_step_bf16(base, base + 64, None, base + 4096, base + 8192, base + 12288, None,
                                  1, 4, 128, 2, 4, None) == 1
     assert "active flags" in lib.vsp_last_error().decode()
+
+
+def test_set_scan_and_scan_of_over_a_model():
+    # column.py:353-380, :428-441: one choice for every recurrent sublayer; refused before any change
+    from torch import nn
+
+    from vesper.column import RecurrentSublayer, scan_of, set_scan
+
+    g = torch.Generator().manual_seed(0)
+    model = nn.Sequential(RecurrentSublayer(32, 2, generator=g), nn.Linear(4, 4), RecurrentSublayer(32, 2, generator=g))
+    assert scan_of(model) == "reference"
+    assert set_scan(model, "reference") == 2
+    with pytest.raises(ValueError, match="needs the model on CUDA"):
+        set_scan(model, "fused")
+    assert scan_of(model) == "reference"  # unchanged by the refused call
+    with pytest.raises(ValueError, match="must be one of"):
+        set_scan(model, "triton")
+    with pytest.raises(ValueError, match="no recurrent sublayer"):
+        set_scan(nn.Linear(4, 4), "reference")
+    model[2].scan_impl = "fused"
+    with pytest.raises(ValueError, match="expected exactly one"):
+        scan_of(model)
+    with pytest.raises(ValueError, match="expected exactly one"):
+        scan_of(nn.Linear(4, 4))
+
+
+def test_the_reference_scan_backend_equals_the_oracle_scan():
+    # the "reference" choice of RecurrentSublayer.scan (column.py:316-326): the chunked scan in the
+    # promoted dtype, then W_o; checked against the oracle's chunked scan (itself pinned by the
+    # reference's rational known answers) and against the token-serial recurrence
+    from oracle.delta import delta_scan_chunked, delta_scan_serial, normalize_keys
+    from vesper.column import RecurrentSublayer
+
+    g = torch.Generator().manual_seed(1)
+    layer = RecurrentSublayer(32, 2, block=8, generator=g).double()
+    x = torch.randn(2, 21, 32, generator=g, dtype=torch.float64)
+    q, z, v, beta = layer.project(x)
+    k = normalize_keys(z.view(2, 21, 2, 16))
+    s0 = 0.1 * torch.randn(2, 2, 16, 16, generator=g, dtype=torch.float64)
+    y, s1 = layer.scan(q, k, v, beta, s0)
+    o_ref, s_ref = delta_scan_chunked(q, k, v, beta, s0, 64)
+    o_ser, s_ser = delta_scan_serial(q, k, v, beta, s0)
+    torch.testing.assert_close(y, o_ref.flatten(2) @ layer.w_o.T, rtol=1e-10, atol=1e-10)
+    torch.testing.assert_close(s1, s_ref, rtol=1e-10, atol=1e-10)
+    torch.testing.assert_close(s1, s_ser, rtol=1e-10, atol=1e-10)
+    # bf16 projections run the scan in float32, as the reference promotes them; the reads return
+    # in the projections' dtype
+    from vesper.column import recurrent_scan
+
+    o16, s32 = recurrent_scan("reference", *(t.to(torch.bfloat16) for t in (q, k, v, beta)), s0.float())
+    assert o16.dtype == torch.bfloat16 and s32.dtype == torch.float32

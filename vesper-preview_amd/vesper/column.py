@@ -1,28 +1,32 @@
-"""The column's scan switch, for the HIP scans: which delta-rule kernel a recurrent sublayer runs.
+"""The column's recurrent sublayer and scan switch on MI355X: which delta-rule scan runs, and where.
 
-Mirrors the reference's backend selection (``vesper/column.py:47-53``, ``:291-326``,
-``:382-426``) with the same names and the same refusals, so a driver written against the
-reference keeps its checks:
+Mirrors the reference's backend selection (``vesper/column.py:47-53``, ``:192-352``,
+``:353-441``) with the same names, the same refusals and the same messages' key phrases, so a
+driver written against the reference keeps its checks:
 
 - ``ScanImpl`` / ``SCAN_IMPLS`` / ``FUSED_INPUT_DTYPES``: "fused" runs ``delta_scan_fused``
   (bfloat16 inputs, float32 state), "fused-fp32" runs ``delta_scan_fused_fp32`` (float32
-  throughout). "reference" names the reference's pure-PyTorch scan (``vesper/recurrence.py``),
-  which this build does not ship: asking for it is refused with a message saying so.
-- ``check_scan`` / ``check_capturable_scan``: the device checks of a choice, before any step.
-- ``recurrent_scan``: the kernel part of ``RecurrentSublayer.scan`` (``column.py:308-315``):
-  cast ``q, k, v, beta`` to the choice's input dtype and the state to float32 with autocast off,
-  run the kernel, return the reads in the projections' dtype and the new float32 state. The
-  output projection ``W_o`` stays with the caller.
-- ``recurrent_keys``: ``RecurrentSublayer.keys`` (``column.py:255-289``) on the key filter kernel:
-  the normalized keys and the next key history, for a filter or none.
+  throughout), both HIP kernels; "reference" runs ``vesper.recurrence.delta_scan_chunked``, the
+  plain PyTorch chunked scan, on whatever device the tensors are on (the reference's eager truth
+  and CPU path; never chosen implicitly, never a fallback of the HIP scans).
+- ``check_scan`` / ``check_capturable_scan``: the device checks of a choice, before any step;
+  "reference" passes ``check_scan`` anywhere and is refused by ``check_capturable_scan`` on the
+  GPU (a triangular solve per block is not a capturable scan).
+- ``set_scan`` / ``scan_of``: one choice for every ``RecurrentSublayer`` of a model.
+- ``RecurrentSublayer``: the projections around the scan: ``project`` (``q``, the key input
+  ``z``, ``v``, ``beta = sigmoid(W_beta x)``), ``keys`` (the causal key filter and
+  ``normalize_keys``, ``recurrent_keys``), ``scan`` (the chosen scan and ``W_o``).
+- ``recurrent_scan``: the scan part of ``RecurrentSublayer.scan`` (``column.py:291-326``).
+- ``recurrent_keys``: ``RecurrentSublayer.keys`` (``column.py:255-289``) on the key filter kernel.
 """
 
 from __future__ import annotations
 
+import math
 from typing import Literal
 
 import torch
-from torch import Tensor
+from torch import Tensor, nn
 
 from vesper.kernels.keys import fused_keys, key_step
 from vesper.kernels.delta_scan import (
@@ -33,10 +37,11 @@ from vesper.kernels.delta_scan import (
     delta_scan_fused_fp32,
     fused_scan_available,
 )
+from vesper.recurrence import delta_scan_chunked
 
 ScanImpl = Literal["reference", "fused", "fused-fp32"]
 SCAN_IMPLS: tuple[ScanImpl, ...] = ("reference", "fused", "fused-fp32")
-# what each HIP scan takes its q, k, v, beta in
+# what each HIP scan takes its q, k, v, beta in; the reference takes promote_types(dtype, float32)
 FUSED_INPUT_DTYPES: dict[ScanImpl, torch.dtype] = {
     "fused": INPUT_DTYPE,
     "fused-fp32": FP32_INPUT_DTYPE,
@@ -46,15 +51,15 @@ FUSED_INPUT_DTYPES: dict[ScanImpl, torch.dtype] = {
 def check_scan(impl: str, device: torch.device) -> ScanImpl:
     """The one check of a scan choice against the device it would run on; returns it typed.
 
+    "reference" runs anywhere (``column.py:382-405``); the HIP scans need the GPU and the built
+    kernel library.
+
     Raises:
-        ValueError: if ``impl`` is not one of ``SCAN_IMPLS``; for "reference" (not shipped by this
-            build); for a HIP scan off the GPU or without the built kernel library.
+        ValueError: if ``impl`` is not one of ``SCAN_IMPLS``, or a fused scan off the GPU or
+            without the built kernel library.
     """
     if impl == "reference":
-        raise ValueError(
-            "the reference scan is the pure-PyTorch path of vesper/recurrence.py, which this build does "
-            "not ship; use fused or fused-fp32"
-        )
+        return "reference"
     if impl not in FUSED_INPUT_DTYPES:
         raise ValueError(f"scan must be one of {SCAN_IMPLS}, got {impl!r}")
     if device.type != "cuda":
@@ -65,29 +70,137 @@ def check_scan(impl: str, device: torch.device) -> ScanImpl:
 
 
 def check_capturable_scan(impl: str, device: torch.device) -> ScanImpl:
-    """``check_scan``: both HIP scans run inside a captured HIP graph (no allocation in the library,
-    no host synchronisation), so every choice that passes it can be captured."""
-    return check_scan(impl, device)
+    """``check_scan``, and the choice must run inside a captured HIP graph on the GPU
+    (``column.py:408-426``): both HIP scans do (no allocation in the library, no host
+    synchronisation); the reference scan on the GPU is refused.
+
+    Raises:
+        ValueError: as ``check_scan``, or the reference scan on the GPU.
+    """
+    chosen = check_scan(impl, device)
+    if chosen == "reference" and device.type == "cuda":
+        raise ValueError("the reference scan cannot run as a captured graph (a triangular solve per block); "
+                         "on the GPU use fused or fused-fp32")
+    return chosen
+
+
+def set_scan(model: nn.Module, impl: str) -> int:
+    """Choose the scan implementation of every ``RecurrentSublayer`` in ``model`` (``column.py:353-380``).
+
+    Every parameter's device is checked with ``check_scan`` before any sublayer changes.
+
+    Returns:
+        The number of sublayers set.
+
+    Raises:
+        ValueError: if ``impl`` is not one of ``SCAN_IMPLS``, if ``model`` has no recurrent
+            sublayer, or if a fused scan is asked where it cannot run.
+    """
+    if impl not in SCAN_IMPLS:
+        raise ValueError(f"scan must be one of {SCAN_IMPLS}, got {impl!r}")
+    sublayers = [m for m in model.modules() if isinstance(m, RecurrentSublayer)]
+    if not sublayers:
+        raise ValueError("the model has no recurrent sublayer to set")
+    chosen: ScanImpl = "reference"
+    for device in sorted({p.device for p in model.parameters()}, key=str):
+        chosen = check_scan(impl, device)
+    for sublayer in sublayers:
+        sublayer.scan_impl = chosen
+    return len(sublayers)
+
+
+def scan_of(model: nn.Module) -> ScanImpl:
+    """The scan implementation every ``RecurrentSublayer`` in ``model`` uses (``column.py:428-441``).
+
+    Raises:
+        ValueError: if the model has no recurrent sublayer or its sublayers disagree.
+    """
+    impls = {m.scan_impl for m in model.modules() if isinstance(m, RecurrentSublayer)}
+    if len(impls) != 1:
+        raise ValueError(f"recurrent sublayers use {sorted(impls)} scan implementations, expected exactly one")
+    return impls.pop()
 
 
 def recurrent_scan(impl: str, q: Tensor, k: Tensor, v: Tensor, beta: Tensor, state: Tensor, *,
-                   active: Tensor | None = None) -> tuple[Tensor, Tensor]:
+                   active: Tensor | None = None, block: int = 64) -> tuple[Tensor, Tensor]:
     """The scan of ``RecurrentSublayer.scan`` without its output projection: ``(o, state')``.
 
     ``q, k, v [b, n, h, dk]`` and ``beta [b, n, h]`` in the projections' dtype; ``state
-    [b, h, dk, dk]`` in any float dtype. Returns ``o`` in ``q``'s dtype and the state in float32.
+    [b, h, dk, dk]``. The HIP scans take their input dtype with autocast off and return ``o`` in
+    ``q``'s dtype and the state in float32; the reference scan runs in ``promote_types(dtype,
+    float32)`` (``column.py:316-325``) and returns its state in that dtype.
 
     Raises:
         ValueError: as ``check_scan``.
         ContractError: from the kernel's contract check.
     """
     chosen = check_scan(impl, q.device)
+    if chosen == "reference":
+        compute = torch.promote_types(q.dtype, torch.float32)
+        with torch.autocast(device_type=q.device.type, enabled=False):
+            o, new_state = delta_scan_chunked(q.to(compute), k.to(compute), v.to(compute), beta.to(compute),
+                                              state.to(compute), block, active=active)
+        return o.to(q.dtype), new_state
     kernel = delta_scan_fused if chosen == "fused" else delta_scan_fused_fp32
     dtype = FUSED_INPUT_DTYPES[chosen]
     with torch.autocast(device_type=q.device.type, enabled=False):
         o, new_state = kernel(q.to(dtype), k.to(dtype), v.to(dtype), beta.to(dtype), state.to(STATE_DTYPE),
                               active=active)
     return o.to(q.dtype), new_state
+
+
+class RecurrentSublayer(nn.Module):
+    """The projections around the delta-rule scan (``column.py:192-352``).
+
+    ``w_q, w_k, w_v, w_o`` of ``[d, d]`` and ``w_beta`` of ``[h, d]``, drawn ``N(0, 1/d)`` in that
+    order, then the optional causal key filter ``conv_k [K, d]`` ~ ``U(-1/sqrt(K), 1/sqrt(K))``
+    (``column.py:216-233``). ``scan_impl`` is module state (``set_scan``), never a parameter.
+    """
+
+    def __init__(self, d: int, heads: int, key_conv: int = 0, block: int = 64,
+                 generator: torch.Generator | None = None) -> None:
+        super().__init__()
+        if d % heads != 0:
+            raise ValueError(f"heads ({heads}) must divide d ({d})")
+        if block < 1:
+            raise ValueError(f"block must be at least 1, got {block}")
+        self.heads, self.head_dim, self.block, self.key_conv = heads, d // heads, block, key_conv
+        self.scan_impl: ScanImpl = "reference"
+        std = 1.0 / math.sqrt(d)
+        self.w_q = nn.Parameter(torch.randn(d, d, generator=generator) * std)
+        self.w_k = nn.Parameter(torch.randn(d, d, generator=generator) * std)
+        self.w_v = nn.Parameter(torch.randn(d, d, generator=generator) * std)
+        self.w_o = nn.Parameter(torch.randn(d, d, generator=generator) * std)
+        self.w_beta = nn.Parameter(torch.randn(heads, d, generator=generator) * std)
+        self.conv_k: nn.Parameter | None = None
+        if key_conv:
+            bound = 1.0 / math.sqrt(key_conv)
+            self.conv_k = nn.Parameter(torch.rand(key_conv, d, generator=generator) * (2 * bound) - bound)
+
+    def project(self, x: Tensor) -> tuple[Tensor, Tensor, Tensor, Tensor]:
+        """``[b, n, d]`` to ``q [b, n, h, dk]`` (not normalized), the key input ``z [b, n, d]``,
+        ``v [b, n, h, dk]`` and ``beta = sigmoid(W_beta x) [b, n, h]`` (``column.py:236-253``)."""
+        b, n, _ = x.shape
+        q = nn.functional.linear(x, self.w_q).view(b, n, self.heads, self.head_dim)
+        z = nn.functional.linear(x, self.w_k)
+        v = nn.functional.linear(x, self.w_v).view(b, n, self.heads, self.head_dim)
+        return q, z, v, torch.sigmoid(nn.functional.linear(x, self.w_beta))
+
+    def keys(self, z: Tensor, history: Tensor) -> tuple[Tensor, Tensor]:
+        """Normalized keys and the next key history (``column.py:255-289``) on the key kernel."""
+        return recurrent_keys(z, history, self.conv_k, self.heads)
+
+    def scan(self, q: Tensor, k: Tensor, v: Tensor, beta: Tensor, state: Tensor) -> tuple[Tensor, Tensor]:
+        """The chosen scan and the output projection: ``(y [b, n, d], state')`` (``column.py:291-326``)."""
+        o, new_state = recurrent_scan(self.scan_impl, q, k, v, beta, state, block=self.block)
+        return nn.functional.linear(o.flatten(2), self.w_o), new_state
+
+    def forward(self, x: Tensor, state: Tensor, history: Tensor) -> tuple[Tensor, Tensor, Tensor]:
+        """Project, make the keys, scan: ``(y, state', history')`` (``column.py:328-350``)."""
+        q, z, v, beta = self.project(x)
+        k, history_next = self.keys(z, history)
+        y, state_next = self.scan(q, k, v, beta, state)
+        return y, state_next, history_next
 
 
 def recurrent_keys(z: Tensor, history: Tensor, taps: Tensor | None, heads: int, *, active: Tensor | None = None,

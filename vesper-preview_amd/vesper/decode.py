@@ -29,7 +29,8 @@ from vesper.column import recurrent_keys
 from vesper.contracts import ContractError, Dims, check_shape
 from vesper.kernels.delta_scan import delta_scan_step_fused
 from vesper.kernels.ring_attn import RingKVCache, ring_attention
-from vesper.loop import BF16, LoopedColumn, _normalize, rms_norm_bf16
+from vesper.kernels.norm import rms_norm_bf16
+from vesper.loop import BF16, LoopedColumn, _normalize
 
 WARM_STEPS = 3  # eager calls before the capture (vesper/graphs.py:99)
 PER_PASS = 6  # flat tensors per pass: scan state, key history, ring keys, values, positions, valid

@@ -61,6 +61,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "vsp_key_step_f16": (I, [P, P, P, P, P, P, P, I, I, I, I, I, P]),
     "vsp_key_step_f32": (I, [P, P, P, P, P, P, P, I, I, I, I, I, P]),
     "vsp_copy_rows_where": (I, [I, P, P, P, P, I, P]),
+    "vsp_rms_norm_bf16": (I, [P, P, P, I, I, P]),
     "vsp_key_filter_backward_workspace_bytes": (Z, [I, I, I, I]),
     "vsp_key_filter_backward_bf16": (I, [P, P, P, P, P, P, P, P, Z, I, I, I, I, I, P]),
     "vsp_key_filter_backward_f16": (I, [P, P, P, P, P, P, P, P, Z, I, I, I, I, I, P]),

@@ -41,6 +41,7 @@ from vesper.contracts import ContractError, Dims, check_shape
 from vesper.kernels.carry import copy_rows_where
 from vesper.kernels.delta_scan import delta_scan_fused
 from vesper.kernels.keys import fused_keys
+from vesper.kernels.norm import rms_norm_bf16
 from vesper.kernels.window_attn import window_attention
 
 BF16 = torch.bfloat16
@@ -60,21 +61,6 @@ def _normalize(x: Tensor, heads: int) -> Tensor:
     if key not in _ONES:
         _ONES[key] = torch.ones(1, d, dtype=torch.float32, device=x.device)
     return fused_keys(x, x.new_empty(x.shape[0], 0, d, dtype=torch.float32), _ONES[key], heads)
-
-
-RMS_EPS = 1e-6  # column.py:55
-RMS_SCALE_FLOOR = 1e-3  # column.py:56
-
-
-def rms_norm_bf16(x: Tensor) -> Tensor:
-    """The sublayers' pre-normalization, ``RMSNorm`` with its gain at one (``column.py:146-188``):
-    ``x / sqrt(mean(x^2) + 1e-6)`` of the float32 residual stream ``x [..., d]``, each row first
-    divided by its peak magnitude floored at 1e-3 (scale-safe, as the reference computes it), in
-    float32, returned in bfloat16 for the projections."""
-    scale = x.abs().amax(dim=-1, keepdim=True).clamp_min(RMS_SCALE_FLOOR)
-    scaled = x / scale
-    rms = torch.sqrt(scaled.square().mean(dim=-1, keepdim=True) + RMS_EPS / (scale * scale))
-    return (scaled / rms).to(BF16)
 
 
 def _where_tokens(mask: Tensor, a: Tensor, b: Tensor) -> Tensor:
