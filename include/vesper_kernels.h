@@ -98,6 +98,28 @@ int vsp_delta_scan_carried_f32(const float* q, const float* k, const float* v, c
                                size_t workspace_bytes, const uint8_t* active, int B, int T, int H, int D,
                                void* stream);
 
+/* The scan with beta given as write-strength logits: the reference's `write_strength`
+ * (vesper/recurrence.py:34-88) applied in the scan's own beta loads, so beta is never written to
+ * memory: beta = sigmoid(logit + ln(1 + alpha m[b, t])), exactly 0 where 1 + alpha m is 0;
+ * m: [B, T] float32 or NULL (no modulator: beta = sigmoid(logit)); alpha finite and >= 0; the
+ * caller holds 1 + alpha m >= 0 (the reference refuses a negative factor). Otherwise as
+ * vsp_delta_scan_bf16 / _f32, logits in beta's place and dtype. */
+int vsp_delta_scan_logits_bf16(const void* q, const void* k, const void* v, const void* logits, const float* m,
+                               float alpha, const float* state_in, void* o, float* state_out, void* workspace,
+                               size_t workspace_bytes, const uint8_t* active, int B, int T, int H, int D,
+                               void* stream);
+int vsp_delta_scan_logits_f32(const float* q, const float* k, const float* v, const float* logits, const float* m,
+                              float alpha, const float* state_in, float* o, float* state_out, void* workspace,
+                              size_t workspace_bytes, const uint8_t* active, int B, int T, int H, int D,
+                              void* stream);
+
+/* The write strength alone (vesper/recurrence.py:34-88): beta [rows, H] from logits [rows, H]
+ * (same dtype) and the per-row modulator m [rows] float32 (or NULL), as above. */
+int vsp_write_strength_bf16(const void* logits, const float* m, float alpha, void* beta, int rows, int H,
+                            void* stream);
+int vsp_write_strength_f32(const float* logits, const float* m, float alpha, float* beta, int rows, int H,
+                           void* stream);
+
 /* One decoding token per row (the contract of vesper/recurrence.py:143-163, delta_scan_step):
  * q, k, v: [B, H, D]; beta: [B, H]; state_in, state_out: [B, H, D, D] float32 (may alias, for an
  * in-place decode); o: [B, H, D]; active: [B] or NULL. */
@@ -165,6 +187,29 @@ int vsp_window_attn_backward_f16(const void* q, const void* keys, const void* va
                                  const void* dout, const float* lse, float* workspace, void* dq, void* dk,
                                  void* dv, int B, int N, int M, int H, int HKV, int D, int window, float scale,
                                  void* stream);
+
+/* ---- the attention window across chunks and the rotary embedding ---------------------------
+ * The chronological window (vesper/attention.py:30-59, 142-175, `KVCache`, `kv_cache_push`): from
+ * a cache of M <= window entries (cache_k, cache_v [B, M, HKV, D], cache_pos [B, M] int64, oldest
+ * first) and a chunk of N (k, v [B, N, HKV, D], pos [B, N]), write the newest min(M + N, window)
+ * entries, oldest first, into out_k, out_v [B, keep, HKV, D] and out_pos [B, keep] (fresh buffers;
+ * the inputs are not changed). elem_bytes 2 (bf16/f16) or 4 (fp32); one launch for all three. */
+int vsp_kv_cache_push(const void* cache_k, const void* cache_v, const int64_t* cache_pos, const void* k,
+                      const void* v, const int64_t* pos, void* out_k, void* out_v, int64_t* out_pos, int B, int M,
+                      int N, int HKV, int D, int elem_bytes, int window, void* stream);
+
+/* Rotary position embedding (vesper/attention.py:178-217, `rotary`, as `WindowedAttention.project`
+ * applies it to q and k, attention.py:292): q [B, N, H, D] and k [B, N, HKV, D] (HKV may be 0 and
+ * k, k_out NULL) at int64 positions pos [B, N]; pair j of a token at position p turns by the angle
+ * p * inv_freq[j] (inv_freq: [D / 2] float64 on the device, base^(-2j/D) as the host computes it),
+ * in float64; cos and sin are cast to the dtype, and the rotation is computed in it with every
+ * product and sum rounded to it. The outputs may be the inputs (in place). D even, <= 1024. */
+int vsp_rotary_qk_bf16(const void* q, const void* k, const int64_t* pos, const double* inv_freq, void* q_out,
+                       void* k_out, int B, int N, int H, int HKV, int D, void* stream);
+int vsp_rotary_qk_f16(const void* q, const void* k, const int64_t* pos, const double* inv_freq, void* q_out,
+                      void* k_out, int B, int N, int H, int HKV, int D, void* stream);
+int vsp_rotary_qk_f32(const float* q, const float* k, const int64_t* pos, const double* inv_freq, float* q_out,
+                      float* k_out, int B, int N, int H, int HKV, int D, void* stream);
 
 /* ---- decode: one new token per row over a KV ring ------------------------------------------
  * q: [B, H, D]; k, v: [B, HKV, D] (the new token); pos: [B] int64, nonnegative;

@@ -14,6 +14,9 @@ Semantics restated from the reference:
   token per row over a ring whose visibility is ``valid`` and the position mask, never slot
   order; the new key is attended once from its argument and then written to slot ``p % w``.
 - ``kv_cache_push`` (``vesper/attention.py:142-175``): keep the newest ``min(m + n, w)`` entries.
+- ``rotary`` (``vesper/attention.py:178-217``): pairs ``(x[2j], x[2j+1])`` rotated by
+  ``pos * base^(-2j/dk)``, the phases in float64, ``cos`` and ``sin`` cast to ``x``'s dtype and the
+  rotation computed in that dtype.
 
 An optional ``active`` (bool ``[b, n]``) zeroes the outputs of inactive queries; their keys and
 values stay visible to every other query (``vesper/loop.py:24-26``, ``:441-442``).
@@ -173,3 +176,23 @@ def kv_ring_write(
     npos[rows, slot] = pos[:, 0]
     nvalid[rows, slot] = True
     return nk, nv, npos, nvalid
+
+
+def rotary(x: Tensor, pos: Tensor, base: float) -> Tensor:
+    """Rotary position embedding of ``x [b, n, heads, dk]`` at int64 positions ``pos [b, n]``
+    (``vesper/attention.py:178-217``): the inverse frequencies ``base^(-2j/dk)`` and the angles
+    ``pos * inv_freq`` in float64, their ``cos`` and ``sin`` cast to ``x.dtype``, then
+    ``(x1 cos - x2 sin, x1 sin + x2 cos)`` per pair in ``x.dtype``. ``pos = 0`` returns ``x``."""
+    b, n, _, dk = x.shape
+    if pos.shape != (b, n) or pos.dtype != torch.long:
+        raise ValueError(f"pos must be int64 {(b, n)}, got {pos.dtype} {tuple(pos.shape)}")
+    if dk % 2 != 0:
+        raise ValueError(f"dk must be even for rotary pairs, got {dk}")
+    if not 1.0 < base < float("inf"):
+        raise ValueError(f"rotary base must be finite and above 1, got {base}")
+    exponent = torch.arange(0, dk // 2, dtype=torch.float64) * (2.0 / dk)
+    angle = pos.to(torch.float64)[:, :, None] * base ** (-exponent)
+    cos = angle.cos().to(x.dtype)[:, :, None, :]
+    sin = angle.sin().to(x.dtype)[:, :, None, :]
+    x1, x2 = x[..., 0::2], x[..., 1::2]
+    return torch.stack([x1 * cos - x2 * sin, x1 * sin + x2 * cos], dim=-1).flatten(-2)

@@ -15,7 +15,9 @@ Restated from the reference's pass loop and column:
   projections, the carry merges of the
   attention keys and values (``:795-796``), window attention, the residual; optionally the causal
   key filter before the keys' normalization (``RecurrentSublayer.keys``, ``:255-289``), its
-  history carried per pass. Rotary and the FFN are not part of the mixer path and are left out;
+  history carried per pass; optionally the rotary embedding of the attention's queries and keys
+  at positions 0..n-1 (``WindowedAttention.project``, ``attention.py:292``). The FFN is not part
+  of the mixer path and is left out;
   keys are L2-normalised (``normalize_keys``) as the scan requires, queries are not
   (``RecurrentSublayer.project``, ``column.py:236-253``; ``docs/model-card.md:26``).
 - ``mixer_decode_step`` is the same column one token at a time over per-pass KV rings, at a fixed
@@ -34,7 +36,7 @@ from dataclasses import dataclass
 import torch
 from torch import Tensor
 
-from oracle.attention import kv_ring_write, ring_attend, window_attention
+from oracle.attention import kv_ring_write, ring_attend, rotary, window_attention
 from oracle.delta import delta_scan_chunked, delta_scan_step, normalize_keys
 from oracle.keys import filter_keys
 
@@ -154,6 +156,7 @@ class MixerWeights:
     head_dim: int
     window: int
     taps: Sequence[Tensor] | None = None  # per pass [K, h*dk]: the causal key filter, or none
+    rotary_base: float | None = None  # the attention's rotary embedding of q and k, or none
 
 
 def _keys(weights: MixerWeights, t: int, z: Tensor, history: Tensor | None, rnd: Callable[[Tensor], Tensor]
@@ -204,6 +207,9 @@ def mixer_column_step(weights: MixerWeights, masked: bool = True, bf16: bool = T
         aq = mm(x1n, weights.waq[t]).view(b, n, h, dk)
         ak = mm(x1n, weights.wak[t]).view(b, n, hkv, dk)
         av = mm(x1n, weights.wav[t]).view(b, n, hkv, dk)
+        if weights.rotary_base is not None:  # WindowedAttention.project (attention.py:292), positions 0..n-1
+            pos = torch.arange(n).expand(b, n)
+            aq, ak = rnd(rotary(aq, pos, weights.rotary_base)), rnd(rotary(ak, pos, weights.rotary_base))
         if carry is not None:
             ak, av = (carry_in(active, f, c) for f, c in zip((ak, av), (carry[1].attn_k, carry[1].attn_v)))
         a = window_attention(aq, ak, av, w, active=mask)
@@ -261,6 +267,8 @@ def mixer_decode_step(weights: MixerWeights, depth: int, bf16: bool = True
             aq = mm(x1n, weights.waq[t]).view(b, 1, h, dk)
             ak = mm(x1n, weights.wak[t]).view(b, 1, hkv, dk)
             av = mm(x1n, weights.wav[t]).view(b, 1, hkv, dk)
+            if weights.rotary_base is not None:
+                aq, ak = rnd(rotary(aq, pos, weights.rotary_base)), rnd(rotary(ak, pos, weights.rotary_base))
             a = ring_attend(aq, ak, av, pos, rk, rv, rp, rvalid, w)
             ring = kv_ring_write(rk, rv, rp, rvalid, ak, av, pos)
             x = x1 + rnd(a).reshape(b, 1, h * dk)

@@ -36,7 +36,7 @@ def _weights(column, dtype=F64):
     ws = {name: [t.to("cpu", dtype) for t in column.w[name]] for name in column.w}
     taps = None if column.taps is None else [t.to("cpu", dtype) for t in column.taps]
     return ol.MixerWeights(**ws, heads=column.heads, kv_heads=column.kv_heads, head_dim=column.head_dim,
-                           window=column.window, taps=taps)
+                           window=column.window, taps=taps, rotary_base=column.rotary_base)
 
 
 def _inputs(b, n, d, seed):

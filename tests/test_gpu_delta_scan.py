@@ -9,6 +9,8 @@ autograd through the chunked scan, its WY form pinned in ``tests/test_oracle_del
 
 from __future__ import annotations
 
+import math
+
 import pytest
 import torch
 
@@ -498,3 +500,87 @@ def test_a_wait_that_gives_up_is_recorded_and_refused_and_its_outputs_are_nan():
     _lib.check_faults(synchronize=True)
     o_ref, s_ref = _oracle(q, k, v, beta, h0)
     assert relative_error(o, o_ref) < TOL and relative_error(s, s_ref) < TOL
+
+
+# ---- the write strength (recurrence.py:34-88): alone, and inside the scan's beta loads ----------
+
+def _modulator(b, n, seed, alpha=0.5):
+    g = torch.Generator().manual_seed(seed)
+    m = torch.rand(b, n, generator=g) * 4 - 1  # [-1, 3]: 1 + alpha m in [0.5, 2.5]
+    m[0, :3] = -1.0 / alpha  # factor exactly zero: an exact zero write
+    return m
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, BF16])
+def test_the_write_strength_matches_the_oracle_and_the_reference_vectors(dtype):
+    from conftest import frac_tensor, reference_vectors
+    from oracle.delta import write_strength as oracle_strength
+    from vesper.kernels.delta_scan import write_strength
+
+    g = torch.Generator().manual_seed(4)
+    logits = (3 * torch.randn(3, 50, 4, generator=g)).to(dtype)
+    tol = 1e-6 if dtype == torch.float32 else 2 ** -8
+    got = write_strength(logits.to(GPU))
+    torch.testing.assert_close(got.cpu().double(), oracle_strength(logits.double()), rtol=tol, atol=1e-7)
+    m = _modulator(3, 50, 5)
+    got = write_strength(logits.to(GPU), m.to(GPU), 0.5)
+    want = oracle_strength(logits.double(), m.double(), 0.5)
+    torch.testing.assert_close(got.cpu().double(), want, rtol=tol, atol=1e-7)
+    assert bool((got[0, :3] == 0).all())  # exact zeros where 1 + alpha m = 0
+    c = reference_vectors()["write_strength"]
+    ends = write_strength(frac_tensor(c["logits"], torch.float32).to(GPU))
+    assert torch.equal(ends.cpu(), frac_tensor(c["want"], torch.float32))
+    o = c["odds_case"]
+    beta0 = float(frac_tensor([o["beta"]])[0])
+    logit = torch.tensor([[[math.log(beta0 / (1 - beta0))]]], dtype=torch.float32)
+    odds = write_strength(logit.to(GPU), torch.tensor([[float(frac_tensor([o["m"]])[0])]], device=GPU),
+                          float(frac_tensor([o["alpha"]])[0]))
+    assert abs(float(odds) - float(frac_tensor([o["want"]])[0])) < 1e-6
+
+
+def test_the_write_strength_refusals_and_gradients():
+    from oracle.delta import write_strength as oracle_strength
+    from vesper.kernels.delta_scan import write_strength
+
+    logits = torch.randn(2, 6, 3, device=GPU)
+    m = torch.rand(2, 6, device=GPU)
+    with pytest.raises(ValueError, match="alpha must be given"):
+        write_strength(logits, m)
+    with pytest.raises(ValueError, match="non-negative"):
+        write_strength(logits, m, -0.5)
+    with pytest.raises(ValueError, match="must not be negative"):
+        write_strength(logits, m - 3.0, 1.0)
+    g = torch.Generator().manual_seed(6)
+    lg = torch.randn(2, 9, 3, generator=g, dtype=torch.float64)
+    mm = _modulator(2, 9, 7).double()
+    up = torch.randn(2, 9, 3, generator=g, dtype=torch.float64)
+    lg_ref, m_ref = lg.clone().requires_grad_(), mm.clone().requires_grad_()
+    (oracle_strength(lg_ref, m_ref, 0.5) * up).sum().backward()
+    lg_gpu, m_gpu = lg.float().to(GPU).requires_grad_(), mm.float().to(GPU).requires_grad_()
+    (write_strength(lg_gpu, m_gpu, 0.5) * up.float().to(GPU)).sum().backward()
+    torch.testing.assert_close(lg_gpu.grad.cpu().double(), lg_ref.grad, rtol=1e-5, atol=1e-6)
+    torch.testing.assert_close(m_gpu.grad.cpu().double(), m_ref.grad, rtol=1e-5, atol=1e-6)
+
+
+@pytest.mark.parametrize("fp32", [False, True])
+@pytest.mark.parametrize(("b", "n", "h", "dk"), [(2, 9, 3, 64), (2, 130, 3, 64), (1, 200, 2, 16)])
+def test_the_scan_with_the_write_strength_in_its_loads_matches_the_oracle(fp32, b, n, h, dk):
+    from oracle.delta import write_strength as oracle_strength
+    from vesper.kernels.delta_scan import delta_scan_fused_logits
+
+    q, k, v, _, h0 = scan_inputs(b, n, h, dk, seed=8)
+    logits = torch.randn(b, n, h, generator=torch.Generator().manual_seed(9))
+    m = _modulator(b, n, 10)
+    dtype = torch.float32 if fp32 else BF16
+    q, k, v, logits = (t.to(dtype) for t in (q, k, v, logits))
+    beta = oracle_strength(logits.double(), m.double(), 0.5)
+    o_ref, s_ref = delta_scan_chunked(q.double(), k.double(), v.double(), beta, h0.double(), 64)
+    dev = [t.to(GPU) for t in (q, k, v, logits, h0)]
+    o, s = delta_scan_fused_logits(*dev, m=m.to(GPU), alpha=0.5)
+    tol = TOL_FP32 if fp32 else TOL
+    assert relative_error(o, o_ref) < tol and relative_error(s, s_ref) < tol
+    # no modulator: beta = sigmoid(logits)
+    o, s = delta_scan_fused_logits(*dev)
+    o_ref, s_ref = delta_scan_chunked(q.double(), k.double(), v.double(), torch.sigmoid(logits.double()),
+                                      h0.double(), 64)
+    assert relative_error(o, o_ref) < tol and relative_error(s, s_ref) < tol

@@ -35,7 +35,7 @@ def _setup(b, n, d, h, hkv, dk, w, passes, seed, p_halt=0.3):
 def _oracle(column, x0, exits, states, dtype=torch.float64):
     ws = {name: [t.to("cpu", dtype) for t in column.w[name]] for name in column.w}
     weights = ol.MixerWeights(**ws, heads=column.heads, kv_heads=column.kv_heads, head_dim=column.head_dim,
-                              window=column.window)
+                              window=column.window, rotary_base=column.rotary_base)
     return ol.loop_forward(x0.to(dtype), ol.mixer_column_step(weights), [s.to(dtype) for s in states], exits)
 
 
@@ -138,7 +138,7 @@ def test_the_loop_with_a_key_filter_matches_the_oracle():
                          [z.to(GPU) for z in histories])
     ws = {name: [t.to("cpu", torch.float64) for t in column.w[name]] for name in column.w}
     weights = ol.MixerWeights(**ws, heads=h, kv_heads=hkv, head_dim=dk, window=w,
-                              taps=[t.to("cpu", torch.float64) for t in column.taps])
+                              taps=[t.to("cpu", torch.float64) for t in column.taps], rotary_base=column.rotary_base)
     want = ol.loop_forward(x0.double(), ol.mixer_column_step(weights),
                            [(s.double(), z.double()) for s, z in zip(states, histories)], exits)
     assert torch.equal(got.n_iters.cpu(), want.n_iters)

@@ -212,3 +212,58 @@ def test_a_planted_scale_mistake_changes_the_gradients() -> None:
     (gq,) = torch.autograd.grad(oa.window_attention(q, k, v, 4).sum(), (q,))
     (wrong,) = torch.autograd.grad(oa.window_attention(2 * q, k, v, 4).sum(), (q,))  # a doubled score scale
     assert not torch.allclose(gq, wrong, rtol=1e-3)
+
+
+def test_rotary_pairs_match_the_reference_scalar_trig():
+    # tests/test_attention_independent.py:66-79: at position 2, pair 0 turns by 2 rad, pair 1 by
+    # 2 / sqrt(base) (base^(-2/4)); a planted mistake (the pair's partner of the wrong sign, or
+    # base^(-j/dk)) fails it
+    from conftest import reference_vectors
+
+    c = reference_vectors()["rotary"]
+    base = float(c["base"])
+    pos = torch.full((1, 1), c["position"], dtype=torch.long)
+    for case in c["pairs"]:
+        x = torch.tensor([[[[float(v) for v in case["x"]]]]], dtype=torch.float64)
+        want = torch.tensor([float(v) for v in case["want"]], dtype=torch.float64)
+        assert torch.allclose(oa.rotary(x, pos, base)[0, 0, 0], want, rtol=0, atol=1e-12)
+    x = torch.tensor([[[[1.0, 0.0, 1.0, 0.0]]]], dtype=torch.float64)
+    wrong = torch.stack([x[..., 0::2], x[..., 1::2]], dim=-1).flatten(-2)  # no rotation at all
+    assert not torch.allclose(oa.rotary(x, pos, base), wrong, atol=1e-3)
+
+
+def test_rotary_keeps_norms_is_the_identity_at_zero_and_keeps_phases_in_float64():
+    from conftest import reference_vectors
+
+    g = torch.Generator().manual_seed(4)
+    x = torch.randn(1, 5, 2, 16, generator=g, dtype=torch.float64)
+    pos = torch.arange(5).expand(1, 5)
+    r = oa.rotary(x, pos, 10000.0)
+    assert (r.square().sum(-1) - x.square().sum(-1)).abs().max().item() < 1e-12
+    assert torch.equal(oa.rotary(x, torch.zeros(1, 5, dtype=torch.long), 10000.0), x)
+    # scores depend on position differences only (tests/test_attention.py:106-111)
+    q, k = torch.randn(1, 6, 1, 16, generator=g, dtype=torch.float64), torch.randn(1, 6, 1, 16, generator=g,
+                                                                                    dtype=torch.float64)
+    p0 = torch.arange(6).expand(1, 6)
+    s0 = oa.rotary(q, p0, 10000.0)[0, :, 0] @ oa.rotary(k, p0, 10000.0)[0, :, 0].T
+    s1 = oa.rotary(q, p0 + 1000, 10000.0)[0, :, 0] @ oa.rotary(k, p0 + 1000, 10000.0)[0, :, 0].T
+    assert (s1 - s0).abs().max().item() < 1e-9
+    for dtype_name, position, atol in reference_vectors()["rotary"]["precision"]:
+        dtype = getattr(torch, dtype_name)
+        x = torch.zeros(1, 2, 1, 2, dtype=dtype)
+        x[..., 0] = 1.0
+        r = oa.rotary(x, torch.tensor([[position, position + 1]]), 10000.0)
+        want = torch.tensor([[math.cos(position), math.sin(position)], [math.cos(position + 1), math.sin(position + 1)]],
+                            dtype=torch.float64)
+        assert r.dtype == dtype and not torch.equal(r[0, 0], r[0, 1])
+        assert torch.allclose(r[0, :, 0, :].double(), want, rtol=0, atol=float(atol)), dtype_name
+
+
+def test_rotary_refusals():
+    x = torch.zeros(1, 2, 1, 4)
+    with pytest.raises(ValueError, match="int64"):
+        oa.rotary(x, torch.zeros(2, 2, dtype=torch.long), 10000.0)
+    with pytest.raises(ValueError, match="even"):
+        oa.rotary(torch.zeros(1, 2, 1, 3), torch.zeros(1, 2, dtype=torch.long), 10000.0)
+    with pytest.raises(ValueError, match="above 1"):
+        oa.rotary(x, torch.zeros(1, 2, dtype=torch.long), float("nan"))

@@ -8,6 +8,7 @@ beta 1/2, output = the state read; no attention and no residual, so the rational
 
 from __future__ import annotations
 
+import dataclasses
 from fractions import Fraction
 
 import pytest
@@ -139,14 +140,17 @@ def _filter_weights(d, h, hkv, dk, w, passes, seed, width):
                            heads=h, kv_heads=hkv, head_dim=dk, window=w, taps=taps)
 
 
-@pytest.mark.parametrize("width", [0, 3])
-def test_tokenwise_ring_decoding_equals_the_chunked_forward(width):
+@pytest.mark.parametrize(("width", "rotary_base"), [(0, None), (3, None), (3, 10000.0)])
+def test_tokenwise_ring_decoding_equals_the_chunked_forward(width, rotary_base):
     # the reference's own check of its decoder (tests/test_decode.py:45-76): the chunked forward
     # over the whole sequence is the truth for the tokenwise ring step; window 6 against 20
-    # tokens, so every ring wraps three times; exact arithmetic here (float64, no bf16 rounding)
+    # tokens, so every ring wraps three times; exact arithmetic here (float64, no bf16 rounding);
+    # with rotary, the token at position i turns as the chunk's row i does
     d, h, hkv, dk, w, passes, depth, b, n = 16, 2, 1, 8, 6, 3, 2, 2, 20
     weights = (_mixer_weights(d, h, hkv, dk, w, passes, seed=8) if width == 0
                else _filter_weights(d, h, hkv, dk, w, passes, seed=8, width=width))
+    if rotary_base is not None:
+        weights = dataclasses.replace(weights, rotary_base=rotary_base)
     g = torch.Generator().manual_seed(9)
     x0 = torch.randn(b, n, d, generator=g, dtype=F64)
     cold = ol.cold_decode_states(weights, b, F64)

@@ -103,7 +103,7 @@ def decode_step(column: LoopedColumn, depth: int, values: Sequence[Tensor],
                 history.copy_(nxt)
             o, _ = delta_scan_step_fused(q[:, 0], k[:, 0], v[:, 0], beta.view(b, h), state, out_state=state)
             x1 = x + o.reshape(b, 1, h * dk)  # float32 (promoted in the add)
-            aq, ak, av = column.project_attn(t, rms_norm_bf16(x1))
+            aq, ak, av = column.project_attn(t, rms_norm_bf16(x1), position)
             ring = RingKVCache(rk, rv, rp, rvalid, column.window)
             a, _ = ring_attention(aq, ak, av, position, ring, inplace=True, check_positions=False,
                                   workspace=workspace)

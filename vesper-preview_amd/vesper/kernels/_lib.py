@@ -37,6 +37,10 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "vsp_delta_scan_f32": (I, [P, P, P, P, P, P, P, P, Z, P, I, I, I, I, P]),
     "vsp_delta_scan_carried_bf16": (I, [P, P, P, P, P, P, P, P, P, P, P, Z, P, I, I, I, I, P]),
     "vsp_delta_scan_carried_f32": (I, [P, P, P, P, P, P, P, P, P, P, P, Z, P, I, I, I, I, P]),
+    "vsp_delta_scan_logits_bf16": (I, [P, P, P, P, P, F, P, P, P, P, Z, P, I, I, I, I, P]),
+    "vsp_delta_scan_logits_f32": (I, [P, P, P, P, P, F, P, P, P, P, Z, P, I, I, I, I, P]),
+    "vsp_write_strength_bf16": (I, [P, P, F, P, I, I, P]),
+    "vsp_write_strength_f32": (I, [P, P, F, P, I, I, P]),
     "vsp_delta_step_f32": (I, [P, P, P, P, P, P, P, P, I, I, I, P]),
     "vsp_delta_step_bf16": (I, [P, P, P, P, P, P, P, P, I, I, I, P]),
     "vsp_window_attn_bf16": (I, [P, P, P, P, P, I, I, I, I, I, I, I, F, P]),
@@ -61,6 +65,10 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "vsp_key_step_f16": (I, [P, P, P, P, P, P, P, I, I, I, I, I, P]),
     "vsp_key_step_f32": (I, [P, P, P, P, P, P, P, I, I, I, I, I, P]),
     "vsp_copy_rows_where": (I, [I, P, P, P, P, I, P]),
+    "vsp_kv_cache_push": (I, [P, P, P, P, P, P, P, P, P, I, I, I, I, I, I, I, P]),
+    "vsp_rotary_qk_bf16": (I, [P, P, P, P, P, P, I, I, I, I, I, P]),
+    "vsp_rotary_qk_f16": (I, [P, P, P, P, P, P, I, I, I, I, I, P]),
+    "vsp_rotary_qk_f32": (I, [P, P, P, P, P, P, I, I, I, I, I, P]),
     "vsp_rms_norm_bf16": (I, [P, P, P, I, I, P]),
     "vsp_key_filter_backward_workspace_bytes": (Z, [I, I, I, I]),
     "vsp_key_filter_backward_bf16": (I, [P, P, P, P, P, P, P, P, Z, I, I, I, I, I, P]),

@@ -56,6 +56,21 @@ bool delta_step_fast_f32(const float* q, const float* k, const float* v, const f
 bool delta_step_fast_bf16(const __bf16* q, const __bf16* k, const __bf16* v, const __bf16* beta, const float* s_in,
                           float* s_out, __bf16* o, const uint8_t* active, int B, int H, int D, hipStream_t stream);
 
+// ---- the write strength (vesper/recurrence.py:34-88) -------------------------------------------
+// beta = sigmoid(logit + ln(1 + alpha m)) of a write-strength logit and the token's modulator m,
+// exactly 0 where 1 + alpha m is 0 (a negative factor is refused by the host); without a
+// modulator (m null) sigmoid(logit). In float32, the factor floored at the smallest normal
+// before the logarithm as the reference floors it.
+__device__ __forceinline__ float write_strength(float logit, const float* m, size_t token, float alpha) {
+  float x = logit;
+  if (m != nullptr) {
+    const float f = 1.f + alpha * m[token];
+    if (!(f > 0.f)) return 0.f;
+    x += logf(__builtin_fmaxf(f, 1.17549435e-38f));
+  }
+  return 1.f / (1.f + expf(-x));
+}
+
 // ---- element conversions ----------------------------------------------------------------------
 __device__ __forceinline__ float to_f32(float x) { return x; }
 __device__ __forceinline__ float to_f32(__bf16 x) { return (float)x; }

@@ -52,7 +52,8 @@ __global__ __launch_bounds__(256) void delta_serial_kernel(const TIn* __restrict
                                                            const float* s_in, float* s_out,  // may alias
                                                            TIn* __restrict__ o, const uint8_t* __restrict__ active,
                                                            const TIn* kc, const TIn* vc, const TIn* bc, int T, int H,
-                                                           int D, int groups) {
+                                                           int D, int groups, const float* mod_m, float mod_alpha,
+                                                           int beta_logits) {
   // (scalar pointer arguments: a struct argument would be read through private memory and count as
   // divergent, which turns every buffer access on it into a loop over lanes)
   const Carried<TIn> carried{kc, vc, bc};
@@ -100,7 +101,8 @@ __global__ __launch_bounds__(256) void delta_serial_kernel(const TIn* __restrict
     }
     if ((int)threadIdx.x < nt) {
       const size_t tok = (size_t)b * T + t0 + threadIdx.x;
-      sb[threadIdx.x] = to_f32((carried.k != nullptr && sa[threadIdx.x] == 0 ? carried.beta : beta)[tok * H + h]);
+      const float raw = to_f32((carried.k != nullptr && sa[threadIdx.x] == 0 ? carried.beta : beta)[tok * H + h]);
+      sb[threadIdx.x] = beta_logits ? write_strength(raw, mod_m, tok, mod_alpha) : raw;
     }
     __syncthreads();
     for (int tt = 0; tt < nt; ++tt) {
@@ -418,7 +420,7 @@ template <typename TIn, typename E, int DK, bool CARRY>
 __global__ __launch_bounds__(256, 3) void delta_prep_kernel(const TIn* __restrict__ k, const TIn* __restrict__ beta,
                                                          E* __restrict__ tmat, const uint8_t* __restrict__ active,
                                                          const TIn* kc, const TIn* vc, const TIn* bc, int T, int H,
-                                                         int total) {
+                                                         int total, const float* mod_m, float mod_alpha, int beta_logits) {
   const Carried<TIn> carried{kc, vc, bc};
   constexpr int DKP = DK < 32 ? 32 : DK;
   using N = Nat<E, DKP>;
@@ -464,7 +466,10 @@ __global__ __launch_bounds__(256, 3) void delta_prep_kernel(const TIn* __restric
 #pragma unroll
       for (int e = 0; e < N::PER; ++e) kn[i][sgi][e] = ok ? kn[i][sgi][e] : from_f32<E>(0.f);
     }
-  const float bl = l < nv ? to_f32(braw) : 0.f;
+  // the write strength from its logit (and the token's modulator) where the entry takes logits
+  const float braw_f = beta_logits ? write_strength(to_f32(braw), mod_m, (size_t)b * T + min(t0 + l, T - 1), mod_alpha)
+                                   : to_f32(braw);
+  const float bl = l < nv ? braw_f : 0.f;
   E* tc = reinterpret_cast<E*>(&sScr[w][0]);  // compact tiles: tile t = i (i + 1) / 2 + j, row-major
   ut_solve<E, DKP>(kn, bl, &sScr[w][0],
                    [&](int ti, int tj, int r, int cc) { return tc + tile_of(ti, tj) * kTileElems + r * 16 + cc; });
@@ -1272,6 +1277,14 @@ __global__ __launch_bounds__(512) void delta_chain_bf16_kernel(const TIn* __rest
 // --------------------------------------------------------------------------------------------
 // host side
 // --------------------------------------------------------------------------------------------
+// beta given as write-strength logits (with an optional per-token modulator), turned into beta in the
+// kernels' loads (recurrence.py:34-88)
+struct Strength {
+  const float* m = nullptr;
+  float alpha = 0.f;
+  int logits = 0;
+};
+
 bool chunked_width(int D, bool fp32) { return D == 16 || D == 32 || D == 64 || (D == 128 && !fp32); }
 constexpr int kSerialBelow = 16;  // shorter sequences run token by token
 
@@ -1288,11 +1301,12 @@ int check_common(const void* q, const void* k, const void* v, const void* beta, 
 template <typename TIn>
 int launch_serial(const TIn* q, const TIn* k, const TIn* v, const TIn* beta, const float* s_in, float* s_out, TIn* o,
                   const uint8_t* active, Carried<TIn> carried, int B, int T, int H, int D, hipStream_t stream,
-                  const char* who) {
+                  const char* who, Strength strength = {}) {
   const int groups = (D + 63) / 64;
   dim3 grid((unsigned)(B * H), (unsigned)groups);
   hipLaunchKernelGGL(delta_serial_kernel<TIn>, grid, dim3(64 * groups), 0, stream, q, k, v, beta, s_in, s_out, o,
-                     active, carried.k, carried.v, carried.beta, T, H, D, groups);
+                     active, carried.k, carried.v, carried.beta, T, H, D, groups, strength.m, strength.alpha,
+                     strength.logits);
   return check_launch(who);
 }
 
@@ -1305,11 +1319,13 @@ size_t workspace_bytes(int B, int T, int H, int D, bool fp32) {
 
 template <typename TIn, typename E, int DK, bool CARRY>
 void launch_chunked(const TIn* q, const TIn* k, const TIn* v, const TIn* beta, const float* s_in, float* s_out, TIn* o,
-                    E* tmat, const uint8_t* active, Carried<TIn> carried, int B, int T, int H, hipStream_t stream) {
+                    E* tmat, const uint8_t* active, Carried<TIn> carried, int B, int T, int H, hipStream_t stream,
+                    Strength strength) {
   const int nc = (T + kChunk - 1) / kChunk;
   const int total = B * H * nc;
   hipLaunchKernelGGL((delta_prep_kernel<TIn, E, DK, CARRY>), dim3((unsigned)((total + 3) / 4)), dim3(256), 0, stream, k,
-                     beta, tmat, active, carried.k, carried.v, carried.beta, T, H, total);
+                     beta, tmat, active, carried.k, carried.v, carried.beta, T, H, total, strength.m, strength.alpha,
+                     strength.logits);
   if constexpr (sizeof(E) == 2 && DK >= 32 && DK <= 64) {  // (at 128 the staging registers would spill)
     hipLaunchKernelGGL((delta_chain_bf16_kernel<TIn, DK, CARRY>), dim3((unsigned)(B * H * (DK / 16))), dim3(512), 0,
                        stream, q, k, v, tmat, s_in, s_out, o, active, carried.k, carried.v, carried.beta, T, H,
@@ -1323,17 +1339,18 @@ void launch_chunked(const TIn* q, const TIn* k, const TIn* v, const TIn* beta, c
 
 template <typename TIn, typename E, int DK>
 void launch_chunked(const TIn* q, const TIn* k, const TIn* v, const TIn* beta, const float* s_in, float* s_out, TIn* o,
-                    E* tmat, const uint8_t* active, Carried<TIn> carried, int B, int T, int H, hipStream_t stream) {
+                    E* tmat, const uint8_t* active, Carried<TIn> carried, int B, int T, int H, hipStream_t stream,
+                    Strength strength) {
   if (carried.k != nullptr)
-    launch_chunked<TIn, E, DK, true>(q, k, v, beta, s_in, s_out, o, tmat, active, carried, B, T, H, stream);
+    launch_chunked<TIn, E, DK, true>(q, k, v, beta, s_in, s_out, o, tmat, active, carried, B, T, H, stream, strength);
   else
-    launch_chunked<TIn, E, DK, false>(q, k, v, beta, s_in, s_out, o, tmat, active, carried, B, T, H, stream);
+    launch_chunked<TIn, E, DK, false>(q, k, v, beta, s_in, s_out, o, tmat, active, carried, B, T, H, stream, strength);
 }
 
 template <typename TIn, typename E>
 int delta_scan(const TIn* q, const TIn* k, const TIn* v, const TIn* beta, const float* s_in, TIn* o, float* s_out,
                void* workspace, size_t ws_bytes, const uint8_t* active, Carried<TIn> carried, int B, int T, int H, int D,
-               void* stream_ptr, const char* who) {
+               void* stream_ptr, const char* who, Strength strength = {}) {
   int st = check_common(q, k, v, beta, s_in, s_out, o, B, T, H, D, who);
   if (st != OK || B == 0 || H == 0) return st;
   if (carried.k != nullptr || carried.v != nullptr || carried.beta != nullptr) {
@@ -1352,7 +1369,8 @@ int delta_scan(const TIn* q, const TIn* k, const TIn* v, const TIn* beta, const 
     return OK;
   }
   const size_t need = workspace_bytes(B, T, H, D, sizeof(E) == 4);
-  if (need == 0) return launch_serial<TIn>(q, k, v, beta, s_in, s_out, o, active, carried, B, T, H, D, stream, who);
+  if (need == 0)
+    return launch_serial<TIn>(q, k, v, beta, s_in, s_out, o, active, carried, B, T, H, D, stream, who, strength);
   if (workspace == nullptr || ws_bytes < need)
     return fail(ERR_ARG, "%s: workspace of %zu bytes given, %zu needed", who, workspace ? ws_bytes : (size_t)0, need);
   // the chunked kernels move q, k, v, o rows and the workspace in 16-byte pieces
@@ -1361,12 +1379,12 @@ int delta_scan(const TIn* q, const TIn* k, const TIn* v, const TIn* beta, const 
     return fail(ERR_ARG, "%s: q, k, v, o and the workspace must be 16-byte aligned", who);
   E* tmat = reinterpret_cast<E*>(workspace);
   switch (D) {
-    case 16: launch_chunked<TIn, E, 16>(q, k, v, beta, s_in, s_out, o, tmat, active, carried, B, T, H, stream); break;
-    case 32: launch_chunked<TIn, E, 32>(q, k, v, beta, s_in, s_out, o, tmat, active, carried, B, T, H, stream); break;
-    case 64: launch_chunked<TIn, E, 64>(q, k, v, beta, s_in, s_out, o, tmat, active, carried, B, T, H, stream); break;
+    case 16: launch_chunked<TIn, E, 16>(q, k, v, beta, s_in, s_out, o, tmat, active, carried, B, T, H, stream, strength); break;
+    case 32: launch_chunked<TIn, E, 32>(q, k, v, beta, s_in, s_out, o, tmat, active, carried, B, T, H, stream, strength); break;
+    case 64: launch_chunked<TIn, E, 64>(q, k, v, beta, s_in, s_out, o, tmat, active, carried, B, T, H, stream, strength); break;
     default:
       if constexpr (sizeof(E) == 2)
-        launch_chunked<TIn, E, 128>(q, k, v, beta, s_in, s_out, o, tmat, active, carried, B, T, H, stream);
+        launch_chunked<TIn, E, 128>(q, k, v, beta, s_in, s_out, o, tmat, active, carried, B, T, H, stream, strength);
       break;
   }
   return check_launch(who);
@@ -1450,4 +1468,34 @@ extern "C" int vsp_delta_step_bf16(const void* q, const void* k, const void* v, 
   return delta_step<__bf16>(static_cast<const __bf16*>(q), static_cast<const __bf16*>(k),
                             static_cast<const __bf16*>(v), static_cast<const __bf16*>(beta), state_in, state_out,
                             static_cast<__bf16*>(o), active, B, H, D, stream, "vsp_delta_step_bf16");
+}
+
+extern "C" int vsp_delta_scan_logits_bf16(const void* q, const void* k, const void* v, const void* logits,
+                                          const float* m, float alpha, const float* state_in, void* o,
+                                          float* state_out, void* workspace, size_t workspace_bytes,
+                                          const uint8_t* active, int B, int T, int H, int D, void* stream) {
+  if (!(alpha >= 0.f) || alpha == __builtin_inff())
+    return vsp::fail(vsp::ERR_ARG, "vsp_delta_scan_logits_bf16: alpha %g is not finite and non-negative", alpha);
+  vsp::Strength strength;
+  strength.m = m;
+  strength.alpha = alpha;
+  strength.logits = 1;
+  return delta_scan<__bf16, __bf16>(static_cast<const __bf16*>(q), static_cast<const __bf16*>(k),
+                                    static_cast<const __bf16*>(v), static_cast<const __bf16*>(logits), state_in,
+                                    static_cast<__bf16*>(o), state_out, workspace, workspace_bytes, active,
+                                    vsp::Carried<__bf16>{}, B, T, H, D, stream, "vsp_delta_scan_logits_bf16", strength);
+}
+
+extern "C" int vsp_delta_scan_logits_f32(const float* q, const float* k, const float* v, const float* logits,
+                                         const float* m, float alpha, const float* state_in, float* o,
+                                         float* state_out, void* workspace, size_t workspace_bytes,
+                                         const uint8_t* active, int B, int T, int H, int D, void* stream) {
+  if (!(alpha >= 0.f) || alpha == __builtin_inff())
+    return vsp::fail(vsp::ERR_ARG, "vsp_delta_scan_logits_f32: alpha %g is not finite and non-negative", alpha);
+  vsp::Strength strength;
+  strength.m = m;
+  strength.alpha = alpha;
+  strength.logits = 1;
+  return delta_scan<float, float>(q, k, v, logits, state_in, o, state_out, workspace, workspace_bytes, active,
+                                  vsp::Carried<float>{}, B, T, H, D, stream, "vsp_delta_scan_logits_f32", strength);
 }

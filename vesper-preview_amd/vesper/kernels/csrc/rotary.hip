@@ -1,0 +1,99 @@
+// Rotary position embedding on CDNA4 (gfx950): the attention's queries and keys rotated in one launch.
+//
+// Reference: vesper/attention.py:178-217 (`rotary`) as `WindowedAttention.project` applies it to q
+// and k (attention.py:292): pairs (x[2j], x[2j+1]) of a token at position p turn by
+// p * base^(-2j/dk); the angle is computed in float64, only cos and sin are cast to the
+// activations' dtype, and the rotation x1 cos - x2 sin, x1 sin + x2 cos is computed in that dtype
+// (each product and the sum rounded to it, as torch evaluates it). The inverse frequencies
+// base^(-2j/dk) arrive as a float64 table the host computed exactly as the reference does.
+//
+// One wave per token row (b, n): lane j owns pair j (and j + 64, ...), computes its cos and sin once
+// and turns that pair in every query head and every key head of the row. q and k may be rotated in
+// place (each element is read and written by one thread).
+#include "common.h"
+#include "vesper_kernels.h"
+
+namespace vsp {
+namespace {
+
+// x1 c - x2 s and x1 s + x2 c with every operation rounded to T (no contraction into FMAs)
+template <typename T>
+__device__ __forceinline__ void turn(const T* src, T* dst, T c, T s) {
+#pragma clang fp contract(off)
+  typedef T P2 __attribute__((ext_vector_type(2)));
+  const P2 x = *reinterpret_cast<const P2*>(src);
+  const float x1 = to_f32(x[0]), x2 = to_f32(x[1]), cf = to_f32(c), sf = to_f32(s);
+  const float a = to_f32(from_f32<T>(x1 * cf)), b = to_f32(from_f32<T>(x2 * sf));
+  const float e = to_f32(from_f32<T>(x1 * sf)), f = to_f32(from_f32<T>(x2 * cf));
+  P2 y;
+  y[0] = from_f32<T>(a - b);
+  y[1] = from_f32<T>(e + f);
+  *reinterpret_cast<P2*>(dst) = y;
+}
+
+template <typename T>
+__device__ __forceinline__ T from_f64(double v) {
+  if constexpr (sizeof(T) == 4) return (float)v;
+  else return (T)(float)v;
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void rotary_qk_kernel(const T* q, const T* k, const int64_t* __restrict__ pos,
+                                                        const double* __restrict__ inv_freq, T* qo, T* ko, int rows,
+                                                        int H, int HKV, int D) {
+  const int row = blockIdx.x * 4 + (int)(threadIdx.x >> 6), lane = threadIdx.x & 63;
+  if (row >= rows) return;
+  const double p = (double)pos[row];
+  const int half = D / 2;
+  for (int j = lane; j < half; j += 64) {
+    const double angle = p * inv_freq[j];
+    const T c = from_f64<T>(cos(angle)), s = from_f64<T>(sin(angle));
+    for (int hh = 0; hh < H; ++hh) {
+      const size_t off = ((size_t)row * H + hh) * D + 2 * j;
+      turn<T>(q + off, qo + off, c, s);
+    }
+    for (int hh = 0; hh < HKV; ++hh) {
+      const size_t off = ((size_t)row * HKV + hh) * D + 2 * j;
+      turn<T>(k + off, ko + off, c, s);
+    }
+  }
+}
+
+template <typename T>
+int rotary_qk(const T* q, const T* k, const int64_t* pos, const double* inv_freq, T* qo, T* ko, int B, int N, int H,
+              int HKV, int D, void* stream, const char* who) {
+  if (B < 0 || N < 0 || H < 0 || HKV < 0) return fail(ERR_ARG, "%s: negative size", who);
+  if (D < 2 || D % 2 != 0 || D > 1024) return fail(ERR_ARG, "%s: head dimension %d (even, 2..1024)", who, D);
+  if ((size_t)B * N == 0 || H + HKV == 0) return OK;
+  if (!pos || !inv_freq || (H > 0 && (!q || !qo)) || (HKV > 0 && (!k || !ko)))
+    return fail(ERR_ARG, "%s: null pointer", who);
+  if ((reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(k) | reinterpret_cast<uintptr_t>(qo) |
+       reinterpret_cast<uintptr_t>(ko)) & (2 * sizeof(T) - 1))
+    return fail(ERR_ARG, "%s: q, k and the outputs must be aligned to a pair", who);
+  const int rows = B * N;
+  hipLaunchKernelGGL(rotary_qk_kernel<T>, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0,
+                     reinterpret_cast<hipStream_t>(stream), q, k, pos, inv_freq, qo, ko, rows, H, HKV, D);
+  return check_launch(who);
+}
+
+}  // namespace
+}  // namespace vsp
+
+extern "C" int vsp_rotary_qk_bf16(const void* q, const void* k, const int64_t* pos, const double* inv_freq, void* q_out,
+                                  void* k_out, int B, int N, int H, int HKV, int D, void* stream) {
+  return vsp::rotary_qk<__bf16>(static_cast<const __bf16*>(q), static_cast<const __bf16*>(k), pos, inv_freq,
+                                static_cast<__bf16*>(q_out), static_cast<__bf16*>(k_out), B, N, H, HKV, D, stream,
+                                "vsp_rotary_qk_bf16");
+}
+
+extern "C" int vsp_rotary_qk_f16(const void* q, const void* k, const int64_t* pos, const double* inv_freq, void* q_out,
+                                 void* k_out, int B, int N, int H, int HKV, int D, void* stream) {
+  return vsp::rotary_qk<_Float16>(static_cast<const _Float16*>(q), static_cast<const _Float16*>(k), pos, inv_freq,
+                                  static_cast<_Float16*>(q_out), static_cast<_Float16*>(k_out), B, N, H, HKV, D, stream,
+                                  "vsp_rotary_qk_f16");
+}
+
+extern "C" int vsp_rotary_qk_f32(const float* q, const float* k, const int64_t* pos, const double* inv_freq,
+                                 float* q_out, float* k_out, int B, int N, int H, int HKV, int D, void* stream) {
+  return vsp::rotary_qk<float>(q, k, pos, inv_freq, q_out, k_out, B, N, H, HKV, D, stream, "vsp_rotary_qk_f32");
+}

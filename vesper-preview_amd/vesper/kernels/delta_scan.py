@@ -281,3 +281,116 @@ def delta_scan_step_fused(q: Tensor, k: Tensor, v: Tensor, beta: Tensor, state: 
         _lib.call(entry, q.data_ptr(), k.data_ptr(), v.data_ptr(), beta.data_ptr(), state.data_ptr(),
                   out_state.data_ptr(), o.data_ptr(), _lib.ptr(mask), b, h, dk, _lib.stream_of(q.device))
     return o, out_state
+
+
+# ---- the write strength (vesper/recurrence.py:34-88), alone and inside the scan's loads ----------
+
+def _checked_modulator(logits: Tensor, m: Tensor | None, alpha: float | None) -> float:
+    """The reference's refusals of a modulator (``recurrence.py:68-84``); returns alpha (0 without m)."""
+    if m is None:
+        return 0.0
+    if alpha is None:
+        raise ValueError("alpha must be given with a modulator (configs/*.yaml: learning.alpha)")
+    if not 0.0 <= alpha < float("inf"):
+        raise ValueError(f"alpha must be finite and non-negative, got {alpha}")
+    dims: Dims = {}
+    check_shape("logits", logits, ("b", "n", "h"), dims)
+    check_shape("m", m, ("b", "n"), dims, torch.float32)
+    if m.device != logits.device:
+        raise ContractError(f"m is on {m.device}, logits on {logits.device}")
+    factor = 1.0 + alpha * m
+    if bool((factor < 0).any().item()):
+        raise ValueError(f"1 + alpha m must not be negative; alpha {alpha}, smallest m {m.min().item()}")
+    return float(alpha)
+
+
+class _WriteStrength(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx: Any, logits: Tensor, m: Tensor | None, alpha: float) -> Tensor:  # noqa: D102
+        lg = _aligned(logits.detach())
+        mm = None if m is None else m.detach().contiguous()
+        beta = torch.empty_like(lg)
+        rows = lg.numel() // lg.shape[-1] if lg.dim() else 1
+        entry = "vsp_write_strength_f32" if lg.dtype == torch.float32 else "vsp_write_strength_bf16"
+        with torch.cuda.device(lg.device):
+            _lib.call(entry, lg.data_ptr(), _lib.ptr(mm), float(alpha), beta.data_ptr(), rows, lg.shape[-1],
+                      _lib.stream_of(lg.device))
+        ctx.save_for_backward(beta, *(() if mm is None else (mm,)))
+        ctx.alpha = alpha
+        return beta
+
+    @staticmethod
+    def backward(ctx: Any, g: Tensor) -> tuple[Tensor | None, ...]:  # noqa: D102
+        beta, *rest = ctx.saved_tensors
+        b32 = beta.float()
+        slope = g.float() * b32 * (1.0 - b32)  # d sigmoid; zero where the factor is zero (beta = 0)
+        d_logits = slope.to(beta.dtype)
+        d_m = None
+        if rest and ctx.needs_input_grad[1]:
+            factor = 1.0 + ctx.alpha * rest[0]
+            d_m = torch.where(factor > 0, (slope * ctx.alpha / factor.clamp_min(torch.finfo(torch.float32).tiny)[..., None]
+                                           ).sum(dim=-1), torch.zeros_like(factor))
+        return d_logits if ctx.needs_input_grad[0] else None, d_m, None
+
+
+def write_strength(logits: Tensor, m: Tensor | None = None, alpha: float | None = None) -> Tensor:
+    """``beta`` in [0, 1] from the write-strength logits, modulated when ``m`` is given
+    (``vesper/recurrence.py:34-88``): ``sigmoid(logits)``, or ``sigmoid(logits + ln(1 + alpha m))``
+    with an exact zero where ``1 + alpha m`` is zero. On the GPU (``vsp_write_strength_*``), in
+    ``logits``' dtype (bfloat16 or float32); under autograd the gradients of ``logits`` and ``m``.
+
+    Args:
+        logits: ``[b, n, h]`` (any shape without ``m``), bfloat16 or float32, on the GPU.
+        m: optional float32 ``[b, n]`` modulator, broadcast over heads.
+        alpha: the modulation strength, required with ``m``, finite and non-negative.
+
+    Raises:
+        ContractError: on a dtype, shape or device outside that; ValueError: as the reference
+            (``m`` without ``alpha``, a negative or non-finite ``alpha``, ``1 + alpha m < 0``).
+    """
+    if logits.dtype not in (torch.float32, torch.bfloat16):
+        raise ContractError(f"logits: dtype must be torch.float32 or torch.bfloat16, got {logits.dtype}")
+    if logits.device.type != "cuda":
+        raise ContractError(f"the write strength kernel runs on CUDA only, got logits on {logits.device}")
+    a = _checked_modulator(logits, m, alpha)
+    if logits.numel() == 0:
+        return torch.empty_like(logits)
+    return _WriteStrength.apply(logits, m, a)
+
+
+def delta_scan_fused_logits(q: Tensor, k: Tensor, v: Tensor, logits: Tensor, state: Tensor, *,
+                            m: Tensor | None = None, alpha: float | None = None,
+                            active: Tensor | None = None) -> tuple[Tensor, Tensor]:
+    """``delta_scan_fused(q, k, v, write_strength(logits, m, alpha), state)`` with the write strength
+    computed inside the scan's beta loads (``vsp_delta_scan_logits_*``): ``beta`` is never
+    written to memory. bfloat16 inputs run the bf16 scan, float32 inputs the fp32 scan; ``beta``
+    stays float32 inside both (the separate path rounds it to the inputs' dtype first).
+
+    Under autograd it is the composition above (the write strength's gradient and the scan's
+    backward kernels).
+
+    Raises:
+        ContractError / ValueError: as ``delta_scan_fused`` and ``write_strength``.
+    """
+    fp32 = q.dtype == torch.float32
+    if _checked_length(q, k, v, logits, state, FP32_INPUT_DTYPE if fp32 else INPUT_DTYPE) == 0:
+        return q, state
+    a = _checked_modulator(logits, m, alpha)
+    if torch.is_grad_enabled() and any(t.requires_grad for t in (q, k, v, logits, state, *(() if m is None else (m,)))):
+        beta = write_strength(logits, m, alpha)
+        return (delta_scan_fused_fp32 if fp32 else delta_scan_fused)(q, k, v, beta, state, active=active)
+    b, n, h, dk = q.shape
+    q, k, v, logits, state = (_aligned(t) for t in (q, k, v, logits, state))
+    mm = None if m is None else m.contiguous()
+    mask = _active_mask(active, ("b", "n"), {"b": b, "n": n}, q.device)
+    o = torch.empty_like(q)
+    s_out = torch.empty_like(state)
+    lib = _lib.library()
+    ws_bytes = int(lib.vsp_delta_scan_workspace_bytes(b, n, h, dk, int(fp32)))
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=q.device) if ws_bytes else None
+    entry = "vsp_delta_scan_logits_f32" if fp32 else "vsp_delta_scan_logits_bf16"
+    with torch.cuda.device(q.device):
+        _lib.call(entry, q.data_ptr(), k.data_ptr(), v.data_ptr(), logits.data_ptr(), _lib.ptr(mm), a,
+                  state.data_ptr(), o.data_ptr(), s_out.data_ptr(), _lib.ptr(ws), ws_bytes, _lib.ptr(mask),
+                  b, n, h, dk, _lib.stream_of(q.device))
+    return o, s_out

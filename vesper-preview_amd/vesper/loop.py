@@ -11,7 +11,9 @@ order of ``Column.step`` (``vesper/column.py:709-812``):
   history), the carry merges for halted tokens (their key input before the filter, ``k, v, beta``
   after, ``column.py:779-789``), the delta scan (``vsp_delta_scan_bf16`` with the active mask),
   the residual;
-- attention sublayer: the pre-normalization, projections, the carry merges of the attention keys and values
+- attention sublayer: the pre-normalization, projections, the rotary embedding of the queries and
+  keys at positions 0..n-1 (``attention.py:178-217, 292``; one launch, ``vsp_rotary_qk_bf16``), the
+  carry merges of the attention keys and values
   (``column.py:795-796``), window attention over the chunk (``vsp_window_attn_bf16`` with the
   active mask), the residual.
 
@@ -23,8 +25,8 @@ the carried rows of inactive tokens inside their loads (the key filter's ``carri
 halting tokens' projections into the carried buffers and carries the hidden state, in place of the
 reference's ``where`` merges; ``copy_forward="where"`` runs those merges as torch selects.
 
-All passes run even when no token is active any more. Rotary embeddings and the FFN are not part
-of the mixer path and are left out. The residual stream stays in float32 (autocast's convention); matmuls and mixers run
+All passes run even when no token is active any more. The FFN is not part of the mixer path and
+is left out. The residual stream stays in float32 (autocast's convention); matmuls and mixers run
 in bfloat16 with the scan state in float32. Forward only.
 """
 
@@ -36,6 +38,7 @@ from dataclasses import dataclass
 import torch
 from torch import Tensor
 
+from vesper.attention import rotary_qk
 from vesper.column import recurrent_keys
 from vesper.contracts import ContractError, Dims, check_shape
 from vesper.kernels.carry import copy_rows_where
@@ -103,7 +106,8 @@ class LoopedColumn:
     """
 
     def __init__(self, weights: dict[str, Sequence[Tensor]], heads: int, kv_heads: int, head_dim: int,
-                 window: int, taps: Sequence[Tensor] | None = None, copy_forward: str = "fused") -> None:
+                 window: int, taps: Sequence[Tensor] | None = None, copy_forward: str = "fused",
+                 rotary_base: float | None = 10000.0) -> None:
         names = ("wq", "wk", "wv", "wb", "waq", "wak", "wav")
         missing = [n for n in names if n not in weights]
         if missing:
@@ -119,6 +123,8 @@ class LoopedColumn:
         if copy_forward not in ("fused", "where"):
             raise ValueError(f"copy_forward is 'fused' or 'where', got {copy_forward!r}")
         self.copy_forward = copy_forward
+        self.rotary_base = rotary_base
+        self._positions: dict[tuple[int, int, torch.device], Tensor] = {}
         # Each sublayer's projections stacked into one [p, d, h*dk] weight per pass (narrower ones
         # zero-padded), so one batched GEMM gives each projection as its own contiguous block
         # instead of one GEMM launch per projection. Built once from ``weights``.
@@ -140,13 +146,23 @@ class LoopedColumn:
         beta = torch.sigmoid(y[3][:, :h]).view(b, n, h)  # bf16 in and out, float32 inside
         return y[0].view(b, n, h * dk), y[1].view(b, n, h * dk), y[2].view(b, n, h, dk), beta
 
-    def project_attn(self, t: int, xb: Tensor) -> tuple[Tensor, Tensor, Tensor]:
-        """Pass ``t``'s attention projections of ``xb [b, n, d]`` (bf16), one batched GEMM."""
+    def project_attn(self, t: int, xb: Tensor, pos: Tensor | None = None) -> tuple[Tensor, Tensor, Tensor]:
+        """Pass ``t``'s attention projections of ``xb [b, n, d]`` (bf16), one batched GEMM, with the
+        queries and keys rotated at positions ``pos [b, n]`` (default ``0..n-1``) in one launch
+        when the column has a rotary base (``WindowedAttention.project``, ``attention.py:269-292``)."""
         b, n, d = xb.shape
         h, hkv, dk = self.heads, self.kv_heads, self.head_dim
         y = torch.matmul(xb.reshape(b * n, d), self.w_attn[t])
-        return (y[0].view(b, n, h, dk), y[1][:, :hkv * dk].reshape(b, n, hkv, dk),
-                y[2][:, :hkv * dk].reshape(b, n, hkv, dk))
+        aq, ak = y[0].view(b, n, h, dk), y[1][:, :hkv * dk].reshape(b, n, hkv, dk)
+        if self.rotary_base is not None:
+            if pos is None:
+                key = (b, n, xb.device)
+                pos = self._positions.get(key)
+                if pos is None:
+                    pos = torch.arange(n, device=xb.device).expand(b, n).contiguous()
+                    self._positions[key] = pos
+            aq, ak = rotary_qk(aq, ak, pos, self.rotary_base)
+        return aq, ak, y[2][:, :hkv * dk].reshape(b, n, hkv, dk)
 
     @property
     def key_history(self) -> int:
@@ -155,7 +171,8 @@ class LoopedColumn:
 
     @classmethod
     def random(cls, d: int, heads: int, kv_heads: int, head_dim: int, window: int, passes: int, seed: int,
-               device: torch.device, key_conv: int = 0, copy_forward: str = "fused") -> LoopedColumn:
+               device: torch.device, key_conv: int = 0, copy_forward: str = "fused",
+               rotary_base: float | None = 10000.0) -> LoopedColumn:
         """Fixed random weights ~ N(0, 1/d) from a CPU generator (the same values on any device);
         with ``key_conv`` a filter of that width, taps ~ U(-1/sqrt(K), 1/sqrt(K)) as the
         reference draws them (``column.py:231-233``)."""
@@ -171,7 +188,7 @@ class LoopedColumn:
             bound = 1.0 / key_conv**0.5
             taps = [(torch.rand(key_conv, heads * head_dim, generator=g) * (2 * bound) - bound).to(device)
                     for _ in range(passes)]
-        return cls(weights, heads, kv_heads, head_dim, window, taps, copy_forward)
+        return cls(weights, heads, kv_heads, head_dim, window, taps, copy_forward, rotary_base)
 
     def keys(self, t: int, z: Tensor, history: Tensor | None, active: Tensor | None = None,
              carried_z: Tensor | None = None) -> tuple[Tensor, Tensor | None]:
