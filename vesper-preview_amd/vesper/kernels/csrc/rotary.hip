@@ -31,10 +31,19 @@ __device__ __forceinline__ void turn(const T* src, T* dst, T c, T s) {
   *reinterpret_cast<P2*>(dst) = y;
 }
 
+// double to T through float, as torch casts a float64 tensor to a 16-bit one (two roundings). The
+// float is pinned in a register first: otherwise the two conversions are folded into one direct
+// (singly rounded) double-to-half conversion, which differs where the float lands exactly on a
+// half-way point between two 16-bit values.
 template <typename T>
 __device__ __forceinline__ T from_f64(double v) {
-  if constexpr (sizeof(T) == 4) return (float)v;
-  else return (T)(float)v;
+  float f = (float)v;
+  if constexpr (sizeof(T) == 4) {
+    return f;
+  } else {
+    asm volatile("" : "+v"(f));
+    return (T)f;
+  }
 }
 
 template <typename T>
