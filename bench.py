@@ -446,12 +446,237 @@ def time_column_decode(torch, steps: int = 64) -> dict:
     return {"us_per_step": us, "tok_s": b / (us / 1e6), "captures": decoder.captures, "replays": decoder.replays}
 
 
+# ---- per-launch medians, warm and cold ---------------------------------------------------------------
+def _medians(torch, calls, reps: int) -> list[float]:
+    """GPU milliseconds of each of ``reps`` calls (``calls(i)`` runs call i), median-ready: the
+    device is first held busy by a spin kernel long enough for the host to enqueue every call with
+    its events, so no event pair times the host."""
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(reps)]
+    torch.cuda.synchronize()
+    torch.cuda._sleep(50_000_000)  # tens of ms of device time ahead of the host
+    for i in range(reps):
+        ev[i][0].record()
+        calls(i)
+        ev[i][1].record()
+    torch.cuda.synchronize()
+    return [a.elapsed_time(b) for a, b in ev]
+
+
+def time_cold_warm(torch, reps: int = 52) -> dict:
+    """Median milliseconds per launch over ``reps`` launches after 10 warm-ups, warm (one resident
+    input set) and cold (input sets rotated so that more than 512 MB lie between two uses of a
+    set, beyond the 256 MB MALL): the bf16 scan at B8 T4096 H8 d64, window attention at B8 and B4
+    T4096 H8 D64 w512, and the float32 scan at B2 T512 H4 d64 and B8 T4096 H8 d64."""
+    from vesper.kernels.delta_scan import delta_scan_fused, delta_scan_fused_fp32
+    from vesper.kernels.window_attn import window_attention
+
+    dev = torch.device("cuda:0")
+    out: dict = {}
+    with torch.no_grad():
+        sets = [scan_inputs(torch, dev, seed=10 + i) for i in range(4)]  # 4 x 137 MB
+        fn = lambda i, s=sets: delta_scan_fused(*s[i % len(s)])  # noqa: E731
+        for i in range(10):
+            fn(i)
+        out["delta_scan_bf16_b8_warm_ms"] = statistics.median(_medians(torch, lambda i: fn(0), reps))
+        out["delta_scan_bf16_b8_cold_ms"] = statistics.median(_medians(torch, fn, reps))
+        del sets
+        for b, name in ((B, "b8"), (ATTN_B, "b4")):
+            asets = [attn_inputs(torch, dev, b=b, seed=20 + i) for i in range(8 if b == ATTN_B else 5)]
+            afn = lambda i, s=asets: window_attention(*s[i % len(s)], WINDOW)  # noqa: E731
+            for i in range(10):
+                afn(i)
+            out[f"window_attn_{name}_warm_ms"] = statistics.median(_medians(torch, lambda i: afn(0), reps))
+            out[f"window_attn_{name}_cold_ms"] = statistics.median(_medians(torch, afn, reps))
+            del asets
+        for (b, t, h), name in (((2, 512, 4), "c1_b2_t512_h4"), ((B, T, H), "b8_t4096_h8")):
+            s32 = [x.float() for x in scan_inputs(torch, dev, b=b, t=t, h=h, seed=30)]
+            for _ in range(10):
+                delta_scan_fused_fp32(*s32)
+            out[f"delta_scan_fp32_{name}_warm_ms"] = statistics.median(
+                _medians(torch, lambda i: delta_scan_fused_fp32(*s32), reps))
+            del s32
+    return out
+
+
+def time_decode_cold(torch, sets: int = 8) -> float:
+    """Microseconds per decode step (delta step + ring attention, batch 64) with ``sets``
+    independent states and rings (72 MiB each, 576 MB in all) used in turn, so consecutive uses of
+    one set are 504 MB apart: the 256 MB MALL cannot serve them. 256 steps in one HIP graph."""
+    from vesper.kernels.delta_scan import delta_scan_step_fused
+    from vesper.kernels.ring_attn import RingKVCache, ring_attention
+
+    dev = torch.device("cuda:0")
+    g = torch.Generator().manual_seed(31)
+    b, h, d, w, n = DEC_B, H, D, DEC_W, DEC_STEPS
+    states = [(0.02 * torch.randn(b, h, d, d, generator=g)).to(dev) for _ in range(sets)]
+    rings = [RingKVCache(torch.randn(b, w, h, d, generator=g).to(dev, torch.bfloat16),
+                         torch.randn(b, w, h, d, generator=g).to(dev, torch.bfloat16),
+                         torch.arange(w).expand(b, w).contiguous().to(dev),
+                         torch.ones(b, w, dtype=torch.bool, device=dev), w) for _ in range(sets)]
+    counters = [torch.zeros(b, dtype=torch.int32, device=dev) for _ in range(sets)]
+    dq = torch.randn(n, b, h, d, generator=g)
+    dq = (dq / dq.norm(dim=-1, keepdim=True)).to(dev)
+    dbeta = torch.sigmoid(torch.randn(n, b, h, generator=g)).to(dev)
+    aq = torch.randn(n, b, 1, h, d, generator=g).to(dev, torch.bfloat16)
+    pos = (w + torch.arange(n) // sets).view(n, 1, 1).expand(n, b, 1).contiguous().to(dev)
+
+    def run_all():
+        for s in range(n):
+            j = s % sets
+            delta_scan_step_fused(dq[s], dq[s], dq[s], dbeta[s], states[j], out_state=states[j])
+            ring_attention(aq[s], aq[s], aq[s], pos[s], rings[j], inplace=True, check_positions=False,
+                           workspace=counters[j])
+
+    with torch.no_grad():
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            run_all()
+        torch.cuda.current_stream().wait_stream(side)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            run_all()
+        times = []
+        for _ in range(5):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            torch.cuda.synchronize()
+            e0.record()
+            graph.replay()
+            e1.record()
+            torch.cuda.synchronize()
+            times.append(e0.elapsed_time(e1))
+    return 1e3 * statistics.median(times) / n
+
+
+def time_published_shapes(torch, reps: int = 20) -> dict:
+    """Forward plus backward at the shapes the reference quotes its kernels on (context only, taken
+    on other GPUs): window attention at b16, chunk 1024 after a 512-row cache, 8 heads over 2 KV
+    heads, dk 64, window 512 (vesper/kernels/window_attn.py:10-13: 1.46 ms on an RTX 5090); the
+    scan at b32 n88 h2 dk16 in bf16 and in fp32 (vesper/kernels/delta_scan.py:22-24: about 2 and
+    1 ms on an RTX 5060 Ti). Eager autograd calls, median milliseconds of ``reps``."""
+    from vesper.kernels.delta_scan import delta_scan_fused, delta_scan_fused_fp32
+    from vesper.kernels.window_attn import window_attention
+
+    dev = torch.device("cuda:0")
+    g = torch.Generator().manual_seed(41)
+    out = {}
+    b, n, m, h, hkv, dk = 16, 1024, 512, 8, 2, 64
+    q = torch.randn(b, n, h, dk, generator=g).to(dev, torch.bfloat16).requires_grad_()
+    keys = torch.randn(b, m + n, hkv, dk, generator=g).to(dev, torch.bfloat16).requires_grad_()
+    vals = torch.randn(b, m + n, hkv, dk, generator=g).to(dev, torch.bfloat16).requires_grad_()
+    up = torch.randn(b, n, h, dk, generator=g).to(dev, torch.bfloat16)
+
+    def attn():
+        window_attention(q, keys, vals, m).backward(up)
+
+    def timed(fn) -> float:
+        for _ in range(3):
+            fn()
+        times = []
+        for _ in range(reps):
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            fn()
+            torch.cuda.synchronize()
+            times.append(1e3 * (time.perf_counter() - t0))
+        return statistics.median(times)
+
+    out["window_attn_fwd_bwd_b16_n1024_m512_h8_hkv2_dk64_ms"] = round(timed(attn), 4)
+    for fp32, name in ((False, "bf16"), (True, "fp32")):
+        dtype = torch.float32 if fp32 else torch.bfloat16
+        sb, sn, sh, sd = 32, 88, 2, 16
+        qs = torch.randn(sb, sn, sh, sd, generator=g)
+        ks = torch.randn(sb, sn, sh, sd, generator=g)
+        ks = ks / ks.norm(dim=-1, keepdim=True)
+        ins = [t.to(dev, dtype).requires_grad_() for t in (qs, ks, torch.randn(sb, sn, sh, sd, generator=g),
+                                                             torch.sigmoid(torch.randn(sb, sn, sh, generator=g)))]
+        s0 = torch.zeros(sb, sh, sd, sd, device=dev, requires_grad=True)
+        kernel = delta_scan_fused_fp32 if fp32 else delta_scan_fused
+
+        def scan():
+            o, s = kernel(*ins, s0)
+            (o.float().sum() + s.sum()).backward()
+
+        out[f"delta_scan_{name}_fwd_bwd_b32_n88_h2_dk16_ms"] = round(timed(scan), 4)
+    return out
+
+
 # ---- CPU baseline ---------------------------------------------------------------------------------
+def cpu_info(torch) -> dict:
+    """The host the CPU legs ran on: logical CPUs, the model name lscpu reports, torch's threading."""
+    model = platform.processor() or "unknown"
+    try:
+        import subprocess
+
+        text = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10, check=False).stdout
+        for line in text.splitlines():
+            if line.strip().startswith("Model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except (OSError, subprocess.SubprocessError):
+        pass
+    info = " ".join(torch.__config__.parallel_info().split())
+    return {"cpu_count": os.cpu_count(), "model": model, "parallel_info": info[:400]}
+
+
+def cpu_legs(torch) -> dict:
+    """The oracle on the host for the decode workload (8 warm-up steps, then the 256 steps of batch
+    64: delta step on the fp32 state + ring attention over 512 bf16-valued entries and the ring
+    write) and the looped column (one batch row of B4 T2048 d512 H8, 8 passes, halting 0.3, in
+    float32), on all of the host's cores."""
+    from oracle import loop as ol
+    from oracle.attention import kv_ring_write, ring_attend
+    from oracle.delta import delta_scan_step
+
+    torch.set_num_threads(os.cpu_count() or 1)
+    g = torch.Generator().manual_seed(3)
+    b, h, d, w, n = DEC_B, H, D, DEC_W, DEC_STEPS
+    state = 0.02 * torch.randn(b, h, d, d, generator=g)
+    rk = torch.randn(b, w, h, d, generator=g).to(torch.bfloat16).float()
+    rv = torch.randn(b, w, h, d, generator=g).to(torch.bfloat16).float()
+    rpos = torch.arange(w).expand(b, w).contiguous()
+    valid = torch.ones(b, w, dtype=torch.bool)
+    out = {}
+    t0 = 0.0
+    for s in range(n + 8):
+        if s == 8:
+            t0 = time.perf_counter()
+        q = torch.randn(b, h, d, generator=g)
+        q = q / q.norm(dim=-1, keepdim=True)
+        beta = torch.sigmoid(torch.randn(b, h, generator=g))
+        _, state = delta_scan_step(q, q, q, beta, state)
+        aq = torch.randn(b, 1, h, d, generator=g).to(torch.bfloat16).float()
+        p = torch.full((b, 1), w + s)
+        ring_attend(aq, aq, aq, p, rk, rv, rpos, valid, w)
+        rk, rv, rpos, valid = kv_ring_write(rk, rv, rpos, valid, aq, aq, p)
+    dt = time.perf_counter() - t0
+    out["decode"] = {"tok_s": round(b * n / dt, 1), "s_256_steps": round(dt, 3),
+                     "sample": "the 256-step decode workload in full after 8 warm-up steps (oracle, fp32)"}
+    lb, ln, ld, passes = 1, LOOP_T, LOOP_D, LOOP_PASSES
+    gw = torch.Generator().manual_seed(11)
+    mats = lambda o: [(torch.randn(ld, o, generator=gw) / ld**0.5).to(torch.bfloat16).float() for _ in range(passes)]  # noqa: E731
+    weights = ol.MixerWeights(wq=mats(H * D), wk=mats(H * D), wv=mats(H * D), wb=mats(H), waq=mats(H * D),
+                              wak=mats(H * D), wav=mats(H * D), heads=H, kv_heads=H, head_dim=D, window=WINDOW,
+                              rotary_base=10000.0)
+    gx = torch.Generator().manual_seed(12)
+    x0 = torch.randn(lb, ln, ld, generator=gx)
+    exits = [torch.rand(lb, ln, generator=gx) < 0.3 for _ in range(passes)]
+    states = [torch.zeros(lb, H, D, D) for _ in range(passes)]
+    t0 = time.perf_counter()
+    ol.loop_forward(x0, ol.mixer_column_step(weights, bf16=False), states, exits)
+    dt = time.perf_counter() - t0
+    out["looped_column"] = {"tok_s": round(lb * ln / dt, 1), "s": round(dt, 3),
+                            "sample": "one batch row of the looped-column workload (T2048 d512 H8, 8 passes, "
+                                      "p_halt 0.3, no key filter), oracle in float32, one run"}
+    return out
+
+
+# ---- CPU baseline (the headline's) ----------------------------------------------------------------
 def cpu_baseline(torch) -> dict:
     from oracle.attention import window_attention as oracle_window
     from oracle.delta import delta_scan_chunked
 
-    threads = max(1, min(16, os.cpu_count() or 1))
+    threads = os.cpu_count() or 1
     torch.set_num_threads(threads)
     sb = B  # the whole step's batch
     q, k, v, beta, s0 = scan_inputs(torch, torch.device("cpu"), b=sb)
@@ -466,18 +691,11 @@ def cpu_baseline(torch) -> dict:
         if i:  # the first run warms up
             times.append(time.perf_counter() - t0)
     t = statistics.median(times)
-    model = platform.processor() or "unknown"
-    try:
-        with open("/proc/cpuinfo", encoding="utf-8") as f:
-            for line in f:
-                if line.startswith("model name"):
-                    model = line.split(":", 1)[1].strip()
-                    break
-    except OSError:
-        pass
+    host = cpu_info(torch)
     return {"value": sb * T / t, "unit": "tok/s", "cores": torch.get_num_threads(), "kind": "port",
             "sample": f"one full step on the CPU: oracle delta_scan_chunked + window_attention in fp32 on the "
-                      f"same inputs (B={sb}, T={T}, H={H}, d={D}, w={WINDOW}), median of 5 after 1 warm-up, {model}"}
+                      f"same inputs (B={sb}, T={T}, H={H}, d={D}, w={WINDOW}), median of 5 after 1 warm-up, "
+                      f"{host['model']}", **host}
 
 
 def traffic_probe(torch) -> None:
@@ -570,22 +788,27 @@ def main() -> int:
     scan_bwd_ms = time_scan_backward(torch)
     keys_ms, keys_bwd_ms = time_key_filter(torch)
     dec = None if args.no_decode else time_decode(torch)
+    dec_cold_us = None if args.no_decode else time_decode_cold(torch)
+    cold_warm = time_cold_warm(torch)
+    published = time_published_shapes(torch)
     looped = None if args.no_loop else time_looped(torch)
     col_dec = None if args.no_decode else time_column_decode(torch)
 
-    scan_dominant = pre["scan_ms"] >= pre["attn_ms"]
+    # the dominant kernel by its median launch time over the timed steps (a mean can carry a few
+    # slow first launches)
+    scan_dominant = pre["scan_ms_median"] >= pre["attn_ms_median"]
     if scan_dominant:
-        name, ms, nbytes, flops = "delta_scan (prep + chain kernels)", pre["scan_ms"], s_bytes, s_flops
+        name, ms, nbytes, flops = "delta_scan (prep + chain kernels)", pre["scan_ms_median"], s_bytes, s_flops
         traffic = traffic_from_profiles("delta_scan")
     else:
-        name, ms, nbytes, flops = "window_attn_kernel", pre["attn_ms"], a_bytes, a_flops
+        name, ms, nbytes, flops = "window_attn_kernel", pre["attn_ms_median"], a_bytes, a_flops
         traffic = traffic_from_profiles("window_attn")
     achieved = nbytes / (ms / 1e3) / 1e9
     roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic, "kernel": name,
                 "algorithmic_bytes": nbytes, "algorithmic_flops": flops,
                 "mfma_frac_bf16": round(flops / (ms / 1e3) / 1e12 / BF16_PEAK_TFLOPS, 4),
-                "avg_launch_ms": round(ms, 4)}
+                "avg_launch_ms": round(ms, 4), "launch_ms_statistic": "median over the timed steps"}
 
     result = {
         "metric": "delta-scan+window-attn prefill tok/s @T=4096; decode tok/s; % of roofline",
@@ -607,6 +830,8 @@ def main() -> int:
         },
         "kernels": {
             "delta_scan_ms": round(pre["scan_ms"], 4),
+            "delta_scan_ms_median": round(pre["scan_ms_median"], 4),
+            "window_attn_b8_ms_median": round(pre["attn_ms_median"], 4),
             "delta_scan_tok_s": round(B * T / (pre["scan_ms"] / 1e3), 1),
             "delta_scan_hbm_frac": round(s_bytes / (pre["scan_ms"] / 1e3) / 1e9 / HBM_PEAK_GBS, 4),
             "delta_scan_mfma_frac_bf16": round(s_flops / (pre["scan_ms"] / 1e3) / 1e12 / BF16_PEAK_TFLOPS, 4),
@@ -661,8 +886,25 @@ def main() -> int:
             "ms_captured": round(looped["ms_captured"], 3),
             "mean_active_passes": round(looped["mean_passes"], 3),
         }
+    result["cold_warm"] = {
+        "method": "median of 52 launches after 10 warm-ups; warm: one input set; cold: input sets rotated "
+                  "so more than 512 MB lie between two uses of a set (the MALL is 256 MB)",
+        **{k: round(v, 4) for k, v in cold_warm.items()},
+        "delta_scan_bf16_b8_cold_hbm_frac": round(s_bytes / (cold_warm["delta_scan_bf16_b8_cold_ms"] / 1e3) / 1e9
+                                                  / HBM_PEAK_GBS, 4),
+    }
+    result["kernels"]["delta_scan_fp32_c1_b2_t512_h4_ms"] = round(cold_warm["delta_scan_fp32_c1_b2_t512_h4_warm_ms"], 4)
+    result["kernels"]["delta_scan_fp32_b8_t4096_h8_ms"] = round(cold_warm["delta_scan_fp32_b8_t4096_h8_warm_ms"], 4)
+    result["published_shapes"] = {"note": "context only: the reference quotes these on NVIDIA cards "
+                                          "(window_attn.py:10-13, delta_scan.py:22-24)", **published}
+    if dec is not None and dec_cold_us is not None:
+        step_bytes = decode_step_bytes(DEC_B, H, D, DEC_W)
+        result["decode"]["cold_us_per_step"] = round(dec_cold_us, 3)
+        result["decode"]["cold_hbm_frac"] = round(step_bytes / (dec_cold_us / 1e6) / 1e9 / HBM_PEAK_GBS, 4)
+        result["decode"]["cold_tok_s"] = round(DEC_B / (dec_cold_us / 1e6), 1)
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(torch)
+        result["cpu_legs"] = cpu_legs(torch)
     log(f"prefill step {pre['step_ms']:.3f} ms (scan {pre['scan_ms']:.3f}, attn {pre['attn_ms']:.3f}), wall {pre['wall_s']:.2f} s")
     print(json.dumps(result), flush=True)
     return 0
