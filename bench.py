@@ -10,9 +10,11 @@ scan (B8 T4096 d512 = 8 heads of 64, 4 taps, bf16), the decode rate (256
 single-token steps of batch 64: fp32 delta update of S [64,8,64,64] then attention over a 512-entry
 bf16 KV ring, captured as one HIP graph), the looped column with per-token halting (B4 T2048 d512,
 8 passes, 4-tap key filter), the column's captured single-token decoder (batch 64, 8 passes), the
-roofline of the dominant kernel measured with HIP
-events on the launch stream inside the timed region, and the CPU oracle timed on a bounded sample
-of the same workload on this host's cores.
+roofline of the dominant kernel measured with HIP events on the launch stream inside the timed
+region, per-launch medians warm and cold (input sets rotated past the 256 MB MALL) for the scan
+(bf16 and fp32), attention and decode, forward plus backward at the shapes the reference quotes its
+kernels on, and the CPU oracle timed on bounded samples of the same workloads on all of this host's
+cores.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
 """
