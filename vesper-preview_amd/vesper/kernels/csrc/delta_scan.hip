@@ -937,10 +937,9 @@ __global__ __launch_bounds__(512) void delta_chain_bf16_kernel(const TIn* __rest
   const int rstride = H * DK;
   const size_t bh_base = ((size_t)b * T * H + h) * DK;
 
-  // the Acc-layout A fragment of a row-major LDS row: k = 4 g + r and 16 + 4 g + r
-  auto acc_frag = [&](const E* arow) {
-    return join4(*reinterpret_cast<const bf16x4*>(arow + 4 * g), *reinterpret_cast<const bf16x4*>(arow + 16 + 4 * g));
-  };
+  // the A fragment of a row-major LDS row over one 32-wide k block in the natural k order: lane
+  // group g holds k = 8 g .. 8 g + 7 (one 16-byte read)
+  auto row_frag = [&](const E* arow) { return *reinterpret_cast<const bf16x8*>(arow + 8 * g); };
   auto frag_at = [&](const E* base, int f) { return *reinterpret_cast<const bf16x8*>(base + f * FR + 8 * l); };
   auto put_frag = [&](E* base, int f, const bf16x8& x) { *reinterpret_cast<bf16x8*>(base + f * FR + 8 * l) = x; };
 
@@ -1068,15 +1067,18 @@ __global__ __launch_bounds__(512) void delta_chain_bf16_kernel(const TIn* __rest
   auto kswz = [](int row) { return KSEG == 8 ? ((((row >> 1) & 3) << 1) | ((row >> 3) & 1)) : ((row >> 2) & 3); };
   // lane offsets: row lq, features 4 g (q, o); row lq, T tile columns 4 g; the direct-load segments
   // (K: for even and odd instructions, whose rows differ in the swizzle's row-bit 3)
-  const unsigned off_q = (unsigned)lq * row_bytes + 8u * g;
+  const unsigned off_q = (unsigned)lq * row_bytes + 8u * g;    // the output's row lq, columns 4 g
+  const unsigned off_qn = (unsigned)lq * row_bytes + 16u * g;  // Q row lq, features 8 g (16-byte pieces)
   const unsigned off_t = (unsigned)(lq * 16 + 4 * g) * 2u;
   const unsigned off_k0 = (unsigned)(l / KSEG) * row_bytes + 16u * (unsigned)((l % KSEG) ^ kswz(l / KSEG));
   const unsigned off_k1 = (unsigned)(l / KSEG) * row_bytes + 16u * (unsigned)((l % KSEG) ^ kswz(64 / KSEG + l / KSEG));
   const unsigned off_v = (unsigned)(l >> 1) * row_bytes + 16u * (unsigned)(l & 1);
 
-  // Q in the Q^T accumulator layout, qa[J][I] = Q[16 J + lq][16 I + 4 g .. + 3], for two chunks: the
-  // one being formed and written, and the one whose loads are in flight
-  bf16x4 qa0[4][HB], qa1[4][HB];
+  // Q as B fragments in the natural k order, qa[J][kb] = Q[16 J + lq][32 kb + 8 g .. + 7] (each a
+  // 16-byte load: a wave instruction covers 16 rows in 64-byte runs), for two chunks: the one being
+  // formed and written, and the one whose loads are in flight. The K and H^T fragments it meets in
+  // the products are read in the same k order.
+  bf16x8 qa0[4][KBF], qa1[4][KBF];
   bf16x4 tl[kTiles];  // the compact T tiles: row lq, columns 4 g .. + 3
   uint8_t actraw[4];
   bf16x8 pt[6];       // P^T per (key block, query tile): (0,0) (0,1) (0,2) (1,2) (0,3) (1,3)
@@ -1091,7 +1093,7 @@ __global__ __launch_bounds__(512) void delta_chain_bf16_kernel(const TIn* __rest
   for (int i = l; i < 64 * DK / 8; i += 64) *reinterpret_cast<bf16x8*>(&myK[8 * i]) = bf16x8{};
   for (int i = l; i < 64 * BV / 8; i += 64) *reinterpret_cast<bf16x8*>(&myV[8 * i]) = bf16x8{};
   __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the zeros land before any direct load
-  auto issue_loads = [&](int c, bf16x4 (&qa)[4][HB], uint64_t mask) {
+  auto issue_loads = [&](int c, bf16x8 (&qa)[4][KBF], uint64_t mask) {
     const unsigned cb = (unsigned)c * kChunk * row_bytes;
     if (!CARRY || mask == ~0ull) {
 #pragma unroll
@@ -1126,8 +1128,8 @@ __global__ __launch_bounds__(512) void delta_chain_bf16_kernel(const TIn* __rest
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll
-      for (int m = 0; m < HB; ++m)
-        qa[i][m] = __builtin_bit_cast(bf16x4, __builtin_amdgcn_raw_buffer_load_b64(rq, off_q + 32u * m, cb + 16u * i * row_bytes, 0));
+      for (int kb = 0; kb < KBF; ++kb)
+        qa[i][kb] = __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(rq, off_qn + 64u * kb, cb + 16u * i * row_bytes, 0));
     const unsigned tb = (unsigned)c * kChunkT * 2u;
 #pragma unroll
     for (int t = 0; t < kTiles; ++t)
@@ -1143,9 +1145,8 @@ __global__ __launch_bounds__(512) void delta_chain_bf16_kernel(const TIn* __rest
   // element offset of (row, column) in a helper's K tile: unpadded rows, 16-byte segments XOR-swizzled
   // by row bits so that both the row-fragment and the transposed reads spread over the 64 banks
   auto kat = [&](int row, int col) { return row * DK + (((col >> 3) ^ kswz(row)) << 3) + (col & 7); };
-  auto kfrag = [&](int row, int kb) {  // the Acc-layout A fragment of K row `row`, dk block kb
-    return join4(*reinterpret_cast<const bf16x4*>(&myK[kat(row, 32 * kb + 4 * g)]),
-                 *reinterpret_cast<const bf16x4*>(&myK[kat(row, 32 * kb + 16 + 4 * g)]));
+  auto kfrag = [&](int row, int kb) {  // the A fragment of K row `row`, dk block kb, natural k order
+    return *reinterpret_cast<const bf16x8*>(&myK[kat(row, 32 * kb + 8 * g)]);
   };
   auto ktr = [&](int r0, int m) {  // column 16 m + lq of token rows r0 + 4 g .. + 3 (transposed read)
     return read_tr16<bf16x4>(&myK[kat(r0 + 4 * g + (lq >> 2), 16 * m + 4 * (lq & 3))]);
@@ -1153,7 +1154,7 @@ __global__ __launch_bounds__(512) void delta_chain_bf16_kernel(const TIn* __rest
 
   // Chunk c's operands into state slot c % NSL (once the chain is done with the slot's previous
   // chunk); P^T kept in registers for the output
-  auto form = [&](int c, const bf16x4 (&qa)[4][HB], uint64_t mask, uint64_t& next_mask) {
+  auto form = [&](int c, const bf16x8 (&qa)[4][KBF], uint64_t mask, uint64_t& next_mask) {
     const int nvc = min(kChunk, T - c * kChunk);
     const int s = c % NSL;
     // The direct loads of K and V count as outstanding vector memory operations until they have
@@ -1186,7 +1187,7 @@ __global__ __launch_bounds__(512) void delta_chain_bf16_kernel(const TIn* __rest
     auto ptile = [&](int jj, int ii) {
       f32x4 acc = zero4();
 #pragma unroll
-      for (int kb = 0; kb < KBF; ++kb) acc = mfma_bf16(kfrag(16 * jj + lq, kb), join4(qa[ii][2 * kb], qa[ii][2 * kb + 1]), acc);
+      for (int kb = 0; kb < KBF; ++kb) acc = mfma_bf16(kfrag(16 * jj + lq, kb), qa[ii][kb], acc);
       if (jj == ii) {
 #pragma unroll
         for (int r = 0; r < 4; ++r) acc[r] = (4 * g + r <= lq) ? acc[r] : 0.f;
@@ -1230,11 +1231,11 @@ __global__ __launch_bounds__(512) void delta_chain_bf16_kernel(const TIn* __rest
 
   // O^T = H^T Q^T + Delta^T P^T for chunk c, from state slot c % NSL; rows past the sequence's end
   // fall outside the output's buffer range and are dropped
-  auto write_output = [&](int c, const bf16x4 (&qa)[4][HB]) {
+  auto write_output = [&](int c, const bf16x8 (&qa)[4][KBF]) {
     const int s = c % NSL;
     bf16x8 hf[KBF];
 #pragma unroll
-    for (int kb = 0; kb < KBF; ++kb) hf[kb] = acc_frag(&sHo[s][lq * PK + 32 * kb]);
+    for (int kb = 0; kb < KBF; ++kb) hf[kb] = row_frag(&sHo[s][lq * PK + 32 * kb]);
     const bf16x8 d0 = frag_at(sD[s], 0), d1 = frag_at(sD[s], 1);
     flag_release(&consumed[s], c);  // after the reads above: the chain may reuse the slot
     const bool bad = flag_peek(&broken) != 0;
@@ -1245,7 +1246,7 @@ __global__ __launch_bounds__(512) void delta_chain_bf16_kernel(const TIn* __rest
       f32x4 acc = mfma_bf16(d0, pt[p0], zero4());
       if (J >= 2) acc = mfma_bf16(d1, pt[p0 + 1], acc);
 #pragma unroll
-      for (int kb = 0; kb < KBF; ++kb) acc = mfma_bf16(hf[kb], join4(qa[J][2 * kb], qa[J][2 * kb + 1]), acc);
+      for (int kb = 0; kb < KBF; ++kb) acc = mfma_bf16(hf[kb], qa[J][kb], acc);
       const bool on = actk[J] != 0;
       typedef TIn O4 __attribute__((ext_vector_type(4)));
       O4 w4;
@@ -1257,7 +1258,7 @@ __global__ __launch_bounds__(512) void delta_chain_bf16_kernel(const TIn* __rest
 
   // chunk c: form its operands, issue the loads of chunk c + NH (their latency hidden behind the
   // wait for the chain), then write its output
-  auto run = [&](int c, const bf16x4 (&qc)[4][HB], bf16x4 (&qn)[4][HB], uint64_t mc, uint64_t& mn) {
+  auto run = [&](int c, const bf16x8 (&qc)[4][KBF], bf16x8 (&qn)[4][KBF], uint64_t mc, uint64_t& mn) {
     form(c, qc, mc, mn);
     if (c + NH < nc) issue_loads(c + NH, qn, mn);
     await_slow(&done, c);
