@@ -266,3 +266,24 @@ def test_a_planted_transpose_in_the_backward_is_caught(monkeypatch):
     monkeypatch.setattr(torch.linalg, "solve_triangular", lambda a, b_, **kw: real(a, b_, **kw).transpose(-1, -2))
     wrong = od.delta_scan_chunked_backward(*args, beta, h0, d_o, None, 4)
     assert not torch.allclose(right[1], wrong[1], rtol=1e-3)
+
+
+def test_write_strength_is_the_scaled_odds_closed_form() -> None:
+    # sigmoid(l + ln(1 + a m)) = s (1 + a m) / (1 + s a m) with s = sigmoid(l): the write odds
+    # s / (1 - s) multiplied by 1 + a m; 1 + a m = 0 gives an exact zero, m = 0 the plain sigmoid
+    g = torch.Generator().manual_seed(11)
+    logits = torch.randn(3, 5, 4, generator=g, dtype=F64) * 3
+    m = torch.rand(3, 5, generator=g, dtype=F64) * 4
+    alpha = 0.75
+    s = torch.sigmoid(logits)
+    am = (alpha * m)[..., None]
+    want = s * (1 + am) / (1 + s * am)
+    assert (od.write_strength(logits, m, alpha) - want).abs().max().item() < 1e-14
+    assert torch.equal(od.write_strength(logits, torch.zeros(3, 5, dtype=F64), alpha), s)
+    edge = torch.full((3, 5), -1.0 / alpha, dtype=F64)
+    assert not bool(od.write_strength(logits, edge, alpha).any())
+    more = od.write_strength(logits, m + 0.5, alpha)
+    assert bool((more > od.write_strength(logits, m, alpha)).all())
+    # a planted mistake: the factor added to the probability instead of scaling the odds
+    wrong = torch.sigmoid(logits) * (1 + am)
+    assert not torch.allclose(wrong, want, atol=1e-3)

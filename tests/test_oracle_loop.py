@@ -221,3 +221,22 @@ def test_the_scan_reads_the_raw_query():
     assert torch.allclose(y - x, o.reshape(1, n, h * dk), rtol=0, atol=1e-12)
     o_normalized, _ = delta_scan_serial(normalize_keys(q), k, v, beta, s0)
     assert float((o_normalized - o).abs().max()) > 1e-2
+
+
+def test_rms_norm_against_the_plain_formula_and_its_edges():
+    # column.py:146-188 with unit gain: x / sqrt(mean(x^2) + 1e-6); the oracle divides by the
+    # row's peak first, which changes nothing in exact arithmetic and keeps float32 finite
+    x = torch.tensor([[3.0, 4.0], [0.0, 0.0], [1e-5, -2e-5], [0.5, -0.5]], dtype=F64)
+    plain = x / torch.sqrt(x.square().mean(-1, keepdim=True) + 1e-6)
+    assert (ol.rms_norm(x) - plain).abs().max().item() < 1e-14
+    assert not bool(ol.rms_norm(x)[1].any())
+    # a row far below sqrt(eps) is scaled by about 1 / 1e-3, not blown up to unit size
+    assert abs(float(ol.rms_norm(x)[2, 1]) - (-2e-5 / 1e-3)) < 1e-5
+    g = torch.Generator().manual_seed(3)
+    big = torch.randn(6, 512, generator=g, dtype=torch.float32) * 1e30  # squares overflow float32
+    out = ol.rms_norm(big)
+    assert torch.isfinite(out).all()
+    assert (out.double().square().mean(-1) - 1).abs().max().item() < 1e-5
+    # a planted mistake: eps dropped (the tiny row would come out at unit size)
+    no_eps = x / torch.sqrt(x.square().mean(-1, keepdim=True)).clamp_min(1e-300)
+    assert not torch.allclose(no_eps[2], ol.rms_norm(x)[2], atol=1e-3)
