@@ -355,15 +355,29 @@ __device__ __forceinline__ void ut_solve(const typename Nat<E, DKP>::R (&kn)[4][
   }
   wave_sync();
 
-  // fp32 16x16x16 products; k permuted as 4g + r so accumulator tiles serve as B operands
+  // 16x16x16 products; k permuted as 4g + r so accumulator tiles serve as B operands. For bf16
+  // inputs (whose factor is stored in bf16) one bf16 16x16x16 MFMA with fp32 accumulation; for fp32
+  // inputs four fp32 16x16x4 MFMAs, keeping the fp32 entry's precision
   auto mm = [&](const float* atile_lds, const f32x4* areg, const float* btile_lds, const f32x4* breg, f32x4 acc) {
+    if constexpr (sizeof(E) == 2) {
+      typedef short s16x4_v __attribute__((ext_vector_type(4)));
+      bf16x4 a4, b4;
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const float av = areg ? (*areg)[r] : atile_lds[lq * TP + 4 * g + r];
-      const float bv = breg ? (*breg)[r] : btile_lds[(4 * g + r) * TP + lq];
-      acc = __builtin_amdgcn_mfma_f32_16x16x4f32(av, bv, acc, 0, 0, 0);
+      for (int r = 0; r < 4; ++r) {
+        a4[r] = (__bf16)(areg ? (*areg)[r] : atile_lds[lq * TP + 4 * g + r]);
+        b4[r] = (__bf16)(breg ? (*breg)[r] : btile_lds[(4 * g + r) * TP + lq]);
+      }
+      return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(s16x4_v, a4), __builtin_bit_cast(s16x4_v, b4),
+                                                       acc, 0, 0, 0);
+    } else {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float av = areg ? (*areg)[r] : atile_lds[lq * TP + 4 * g + r];
+        const float bv = breg ? (*breg)[r] : btile_lds[(4 * g + r) * TP + lq];
+        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(av, bv, acc, 0, 0, 0);
+      }
+      return acc;
     }
-    return acc;
   };
   auto xd = [&](int blk) { return (const float*)(Xd + blk * 16 * TP); };
   auto ao = [&](int i, int j) { return &aoff[i * (i - 1) / 2 + j]; };
