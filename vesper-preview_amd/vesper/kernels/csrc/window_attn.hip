@@ -59,8 +59,11 @@ __global__ __launch_bounds__(256, D >= 128 ? 2 : (CARRY && D == 64 ? 3 : 4)) voi
   constexpr bool kDirect = D >= 64;
   constexpr int NINS = KT * PSEG / 64, NINSV = KT * PSEGV / 64;  // wave instructions per K, V tile
   constexpr int NI = kDirect ? (NINSV + 3) / 4 : (KT * SEG + 255) / 256;
-  __shared__ __align__(16) T sK[2][KT * PK];
-  __shared__ __align__(16) T sV[2][KT * PV];
+  // Separate variables per buffer, each tile's buffers fixed at compile time (the tile loop runs
+  // two tiles an iteration): the compiler then tells the direct loads into one buffer from the
+  // reads of the other and does not wait for the next tile's loads before reading this one.
+  __shared__ __align__(16) T sK0[KT * PK], sK1[KT * PK];
+  __shared__ __align__(16) T sV0[KT * PV], sV1[KT * PV];
 
   const int lg = xcd_logical_block(blockIdx.x, gridDim.x);
   const int qt = lg % nqt, bh = lg / nqt;
@@ -143,7 +146,7 @@ __global__ __launch_bounds__(256, D >= 128 ? 2 : (CARRY && D == 64 ? 3 : 4)) voi
     const int rowv = pos / PSEGV, segv = pos - rowv * PSEGV;
     voff[j] = (unsigned)(rowv * kv_row + 8 * (segv < SEG ? segv : 0)) * (unsigned)sizeof(T);
   }
-  auto fetch = [&](int k0, int buf, uint64_t fresh) {
+  auto fetch = [&](int k0, T* Kn, T* Vn, uint64_t fresh) {
 #pragma unroll
     for (int j = 0; j < NI; ++j) {
       if constexpr (kDirect && CARRY) {
@@ -157,13 +160,13 @@ __global__ __launch_bounds__(256, D >= 128 ? 2 : (CARRY && D == 64 ? 3 : 4)) voi
         const int key = min(k0 + row, S - 1), keyv = min(k0 + rowv, S - 1);
         const size_t sk = (size_t)key * kv_row + 8 * (seg < SEG ? seg : 0);
         const size_t sv = (size_t)keyv * kv_row + 8 * (segv < SEG ? segv : 0);
-        if (ins < NINS) load_lds16((((fresh >> (key - k0)) & 1) ? kbase : kcbase) + sk, &sK[buf][ins * 64 * 8]);
-        if (ins < NINSV) load_lds16((((fresh >> (keyv - k0)) & 1) ? vbase : vcbase) + sv, &sV[buf][ins * 64 * 8]);
+        if (ins < NINS) load_lds16((((fresh >> (key - k0)) & 1) ? kbase : kcbase) + sk, Kn + ins * 64 * 8);
+        if (ins < NINSV) load_lds16((((fresh >> (keyv - k0)) & 1) ? vbase : vcbase) + sv, Vn + ins * 64 * 8);
       } else if constexpr (kDirect) {
         const int ins = w + 4 * j;  // this wave's j-th instruction of the tile
         const unsigned toff = (unsigned)((size_t)k0 * kv_row * sizeof(T));
-        if (ins < NINS) buffer_load_lds16(rk, &sK[buf][ins * 64 * 8], koff[j], toff);
-        if (ins < NINSV) buffer_load_lds16(rv, &sV[buf][ins * 64 * 8], voff[j], toff);
+        if (ins < NINS) buffer_load_lds16(rk, Kn + ins * 64 * 8, koff[j], toff);
+        if (ins < NINSV) buffer_load_lds16(rv, Vn + ins * 64 * 8, voff[j], toff);
       } else {
         const int sg = threadIdx.x + 256 * j;
         const int row = sg / SEG, part = sg - row * SEG;
@@ -183,15 +186,15 @@ __global__ __launch_bounds__(256, D >= 128 ? 2 : (CARRY && D == 64 ? 3 : 4)) voi
       }
     }
   };
-  auto stash = [&](int buf) {
+  auto stash = [&](T* Kn, T* Vn) {
     if constexpr (!kDirect) {
 #pragma unroll
       for (int j = 0; j < NI; ++j) {
         const int sg = threadIdx.x + 256 * j;
         if (sg < KT * SEG) {
           const int row = sg / SEG, part = sg - row * SEG;
-          *reinterpret_cast<V8*>(&sK[buf][row * PK + 8 * part]) = kreg[j];
-          *reinterpret_cast<V8*>(&sV[buf][row * PV + 8 * part]) = vreg[j];
+          *reinterpret_cast<V8*>(Kn + row * PK + 8 * part) = kreg[j];
+          *reinterpret_cast<V8*>(Vn + row * PV + 8 * part) = vreg[j];
         }
       }
     }
@@ -215,27 +218,25 @@ __global__ __launch_bounds__(256, D >= 128 ? 2 : (CARRY && D == 64 ? 3 : 4)) voi
     fresh = __builtin_amdgcn_ballot_w64(flag_of(kfirst) != 0);
     fl = flag_of(kfirst + KT);
   }
-  fetch(kfirst, 0, fresh);
-  stash(0);
+  fetch(kfirst, sK0, sV0, fresh);
+  stash(sK0, sV0);
+  if constexpr (kDirect) __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's direct loads
   __syncthreads();
-  for (int it = 0; it < ntiles; ++it) {
+  // one tile: K, V in Kt, Vt; the next tile's loads go to Kn, Vn (last read before the previous barrier)
+  auto tile = [&](int it, const T* Kt, const T* Vt, T* Kn, T* Vn) {
     const int k0 = kfirst + it * KT;
-    const int buf = it & 1;
-    // the other buffer was last read before the previous barrier
     if (it + 1 < ntiles) {
       if constexpr (CARRY) {
         fresh = __builtin_amdgcn_ballot_w64(fl != 0);
         fl = flag_of(k0 + 2 * KT);
       }
-      fetch(k0 + KT, buf ^ 1, fresh);
+      fetch(k0 + KT, Kn, Vn, fresh);
     }
 
     // skip a tile this wave's queries cannot see (wave-uniform)
     const bool seen = k0 <= whi && k0 + KT - 1 > wlo - W;
     if (seen) {
       const bool full = k0 + KT - 1 <= wlo && k0 > whi - W && k0 + KT <= klast;
-      const T* Kt = sK[buf];
-      const T* Vt = sV[buf];
       f32x4 sacc[QB][4];
 #pragma unroll
       for (int kb = 0; kb < 4; ++kb) {
@@ -330,9 +331,16 @@ __global__ __launch_bounds__(256, D >= 128 ? 2 : (CARRY && D == 64 ? 3 : 4)) voi
         }
       }
     }
-    if (it + 1 < ntiles) stash(buf ^ 1);
-    __syncthreads();  // (the direct loads into buf ^ 1 are waited for before it)
+    if (it + 1 < ntiles) stash(Kn, Vn);
+    if constexpr (kDirect) __builtin_amdgcn_s_waitcnt(0x0F70);  // the next tile's direct loads
+    __syncthreads();
+  };
+  int it = 0;
+  for (; it + 1 < ntiles; it += 2) {
+    tile(it, sK0, sV0, sK1, sV1);
+    tile(it + 1, sK1, sV1, sK0, sV0);
   }
+  if (it < ntiles) tile(it, sK0, sV0, sK1, sV1);
 
 #pragma unroll
   for (int qb = 0; qb < QB; ++qb) {
