@@ -200,15 +200,20 @@ __global__ __launch_bounds__(256, D >= 128 ? 2 : (CARRY && D == 64 ? 3 : 4)) voi
     }
   };
 
-  float m_used[QB], l_run[QB];
-  f32x4 oacc[QB][DT];
+  // lacc: the row sums of the probabilities as rounded for the P V product, by one more MFMA per
+  // key step with an all-ones A operand (every lane then holds its query's sum, and no VALU adds)
+  float m_used[QB];
+  f32x4 oacc[QB][DT], lacc[QB];
 #pragma unroll
   for (int qb = 0; qb < QB; ++qb) {
     m_used[qb] = -1e30f;  // finite: exp2 of a masked score minus it is exactly 0
-    l_run[qb] = 0.f;
+    lacc[qb] = zero4();
 #pragma unroll
     for (int t = 0; t < DT; ++t) oacc[qb][t] = zero4();
   }
+  V8 ones;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) ones[j] = from_f32<T>(1.f);
   // the wave's queries in key-index space: [wlo, whi]
   const int wlo = M + wq0, whi = M + wq0 + 31;
 
@@ -236,7 +241,10 @@ __global__ __launch_bounds__(256, D >= 128 ? 2 : (CARRY && D == 64 ? 3 : 4)) voi
     // skip a tile this wave's queries cannot see (wave-uniform)
     const bool seen = k0 <= whi && k0 + KT - 1 > wlo - W;
     if (seen) {
-      const bool full = k0 + KT - 1 <= wlo && k0 > whi - W && k0 + KT <= klast;
+      // masks only where needed: the causal edge (some key after some query of the wave, or keys
+      // past the last one) and the window's lower edge (some key too old for the wave's last query)
+      const bool cmask = k0 + KT - 1 > wlo || k0 + KT > klast;
+      const bool wmask = k0 <= whi - W;
       f32x4 sacc[QB][4];
 #pragma unroll
       for (int kb = 0; kb < 4; ++kb) {
@@ -255,17 +263,22 @@ __global__ __launch_bounds__(256, D >= 128 ? 2 : (CARRY && D == 64 ? 3 : 4)) voi
       float mt[QB];
 #pragma unroll
       for (int qb = 0; qb < QB; ++qb) {
-        if (!full) {
-          // key k0 + 16 kb + 4 g + r is visible to query qidx iff 0 <= qidx - key < W; for every
-          // query that is stored, qidx < klast, so keys at or past klast are never visible
-          const int c0 = wlo + 16 * qb + lq - k0 - 4 * g;
+        // key k0 + 4 g + e (e = 16 kb + r) is visible to query qidx iff qidx - W < key <= qidx, that
+        // is iff c - W < e <= c with c = qidx - k0 - 4 g (each test one compare with a constant);
+        // every query that is stored has qidx < klast, so keys at or past klast fail the first
+        const int c = wlo + 16 * qb + lq - k0 - 4 * g;
+        if (cmask) {
 #pragma unroll
           for (int kb = 0; kb < 4; ++kb)
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-              const bool vis = (unsigned)(c0 - 16 * kb - r) < (unsigned)W;
-              sacc[qb][kb][r] = vis ? sacc[qb][kb][r] : -INFINITY;
-            }
+            for (int r = 0; r < 4; ++r) sacc[qb][kb][r] = 16 * kb + r <= c ? sacc[qb][kb][r] : -INFINITY;
+        }
+        if (wmask) {
+          const int cw = c - W;
+#pragma unroll
+          for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) sacc[qb][kb][r] = 16 * kb + r > cw ? sacc[qb][kb][r] : -INFINITY;
         }
         mt[qb] = sacc[qb][0][0];
 #pragma unroll
@@ -285,14 +298,12 @@ __global__ __launch_bounds__(256, D >= 128 ? 2 : (CARRY && D == 64 ? 3 : 4)) voi
         for (int qb = 0; qb < QB; ++qb) {
           const float mn = need[qb] ? mt[qb] : m_used[qb];
           const float alpha = __builtin_amdgcn_exp2f(m_used[qb] - mn);
-          l_run[qb] *= alpha;
+          lacc[qb] *= alpha;
 #pragma unroll
           for (int t = 0; t < DT; ++t) oacc[qb][t] *= alpha;
           m_used[qb] = mn;
         }
       }
-      using P2 = typename Dot2<T>::P2;
-      const P2 one2 = {from_f32<T>(1.f), from_f32<T>(1.f)};
 #pragma unroll
       for (int qb = 0; qb < QB; ++qb) {
         float p[4][4];
@@ -307,14 +318,6 @@ __global__ __launch_bounds__(256, D >= 128 ? 2 : (CARRY && D == 64 ? 3 : 4)) voi
             pb[qb][ks][j] = from_f32<T>(p[2 * ks][j]);
             pb[qb][ks][4 + j] = from_f32<T>(p[2 * ks + 1][j]);
           }
-        // the row sum of the probabilities as rounded for the P V product, two per v_dot2
-        float ps0 = 0.f, ps1 = 0.f;
-#pragma unroll
-        for (int j = 0; j < 8; j += 2) {
-          ps0 = Dot2<T>::run(P2{pb[qb][0][j], pb[qb][0][j + 1]}, one2, ps0);
-          ps1 = Dot2<T>::run(P2{pb[qb][1][j], pb[qb][1][j + 1]}, one2, ps1);
-        }
-        l_run[qb] += ps0 + ps1;
       }
       // O^T += V^T P^T: A fragments of V^T by transposed LDS reads (lane (lq, g) gets column
       // 16 t + lq of key rows 32 ks + 4 g .. +3 and 32 ks + 16 + 4 g .. +3)
@@ -330,6 +333,10 @@ __global__ __launch_bounds__(256, D >= 128 ? 2 : (CARRY && D == 64 ? 3 : 4)) voi
           for (int qb = 0; qb < QB; ++qb) oacc[qb][t] = Mma<T>::run(a, pb[qb][ks], oacc[qb][t]);
         }
       }
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+        for (int qb = 0; qb < QB; ++qb) lacc[qb] = Mma<T>::run(ones, pb[qb][ks], lacc[qb]);
     }
     if (it + 1 < ntiles) stash(Kn, Vn);
     if constexpr (kDirect) __builtin_amdgcn_s_waitcnt(0x0F70);  // the next tile's direct loads
@@ -344,8 +351,7 @@ __global__ __launch_bounds__(256, D >= 128 ? 2 : (CARRY && D == 64 ? 3 : 4)) voi
 
 #pragma unroll
   for (int qb = 0; qb < QB; ++qb) {
-    float lt = l_run[qb] + __shfl_xor(l_run[qb], 16);
-    lt += __shfl_xor(lt, 32);
+    const float lt = lacc[qb][0];
     const float inv = (act[qb] && lt > 0.f) ? 1.f / lt : 0.f;
     // the log-sum-exp in log2 units of the scaled scores, for the backward: P = exp2(s sl2 - lse);
     // +inf for an inactive query, whose probabilities (and gradients) are then exactly zero
