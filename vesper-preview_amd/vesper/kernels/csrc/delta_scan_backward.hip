@@ -11,12 +11,16 @@
 // and the state's gradient at the chunk's start G + Q^T dO - K^T dR = G - W^T (K G) + Y with
 // W = T K, Y = Q^T dO - W^T P^T dO.
 //
-// Four kernels, all arithmetic in fp32 (16x16x4 MFMA, operands staged in LDS), no atomics:
-// - scan_bwd_prep_kernel, per (b, h, chunk): L, W, U = T V and Y into the workspace;
-// - scan_bwd_states_kernel, per (b, h, 16 value columns): the states at the chunk starts, by the
-//   forward chain Delta = U - W H, H += K^T Delta (value columns evolve independently);
-// - scan_bwd_dstate_kernel, per (b, h, 16 value columns): the reverse chain of the state's
-//   gradient, recorded at every chunk's end, and the initial state's gradient;
+// Both chains are one matrix product per chunk: with U = T V, N = -K^T W and B = K^T U,
+//   H_next = H + N H + B        (forward: the state at the next chunk's start),
+//   G_start = G + N^T G + Y     (reverse: the state's gradient at the chunk's start).
+// Three kernels, no atomics (fp32 arithmetic; bf16 inputs multiply on bf16 MFMA):
+// - scan_bwd_prep_kernel, per (b, h, chunk): L, N and N^T (bf16, in the chains' MFMA operand
+//   order), B and Y (fp32, in the chains' accumulator order) into the workspace;
+// - scan_bwd_chains_kernel, one wave per (b, h, 16 value columns) and direction (value columns
+//   evolve independently): the states at the chunk starts and the state's gradients at the
+//   chunk ends, and the initial state's gradient; the state slice stays in MFMA accumulators and
+//   N's fragments come straight from global memory into a register ring, several chunks ahead;
 // - scan_bwd_chunk_kernel, per (b, h, chunk): every token gradient of the chunk.
 #include "common.h"
 #include "vesper_kernels.h"
@@ -190,19 +194,62 @@ struct MatRows {
   }
 };
 
-// workspace layout, per (b, h, chunk): L [64][64], W [64][D], U [64][D], Y [D][D], Hs [D][D], dHs [D][D]
-template <int D> struct Ws {
-  static constexpr size_t kL = (size_t)kC * kC, kW = (size_t)kC * D, kS = (size_t)D * D;
-  static constexpr size_t kPer = kL + 2 * kW + 3 * kS;
-  __device__ __forceinline__ static float* L(float* ws, size_t chunk) { return ws + chunk * kPer; }
-  __device__ __forceinline__ static float* W(float* ws, size_t chunk) { return ws + chunk * kPer + kL; }
-  __device__ __forceinline__ static float* U(float* ws, size_t chunk) { return ws + chunk * kPer + kL + kW; }
-  __device__ __forceinline__ static float* Y(float* ws, size_t chunk) { return ws + chunk * kPer + kL + 2 * kW; }
-  __device__ __forceinline__ static float* Hs(float* ws, size_t chunk) { return ws + chunk * kPer + kL + 2 * kW + kS; }
-  __device__ __forceinline__ static float* dHs(float* ws, size_t chunk) {
-    return ws + chunk * kPer + kL + 2 * kW + 2 * kS;
+// a [D][D] fp32 matrix stored in accumulator order (accfrag: value slice s = column tile) into
+// LDS [D][ld], row-major
+template <int D, int NTH = kThreads>
+struct AccRows {
+  static constexpr int NT = D / 16, kN = D * D / 4, kIt = (kN + NTH - 1) / NTH;
+  f32x4 raw[kIt];
+  __device__ __forceinline__ void fetch(const float* src) {
+#pragma unroll
+    for (int it = 0; it < kIt; ++it)
+      raw[it] = *reinterpret_cast<const f32x4*>(src + 4 * min((int)threadIdx.x + NTH * it, kN - 1));
+  }
+  __device__ __forceinline__ void put(float* dst, int ld) const {
+#pragma unroll
+    for (int it = 0; it < kIt; ++it) {
+      const int e = threadIdx.x + NTH * it;  // = (s NT + rt) 64 + lane
+      if (kN % NTH == 0 || e < kN) {
+        const int lane = e & 63, st = e >> 6, sl = st / NT, rt = st - sl * NT;
+        const int row = 16 * rt + 4 * (lane >> 4), col = 16 * sl + (lane & 15);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) dst[(row + r) * ld + col] = raw[it][r];
+      }
+    }
   }
 };
+
+// workspace layout, per (b, h, chunk), in floats: L [64][64]; NF, NR [D][D] (the chains' A
+// operands: bf16 on the bf16 entry, in the first half of each block, fp32 on the fp32 one); B, Y,
+// Hs, dHs [D][D] in accumulator order
+template <int D> struct Ws {
+  static constexpr size_t kL = (size_t)kC * kC, kS = (size_t)D * D;
+  static constexpr size_t kPer = kL + 6 * kS;
+  __device__ __forceinline__ static float* L(float* ws, size_t chunk) { return ws + chunk * kPer; }
+  // N's A-operand fragments for the forward chain (NF) and N^T's for the reverse one (NR)
+  __device__ __forceinline__ static float* NF(float* ws, size_t chunk) { return ws + chunk * kPer + kL; }
+  __device__ __forceinline__ static float* NR(float* ws, size_t chunk) { return ws + chunk * kPer + kL + kS; }
+  __device__ __forceinline__ static float* B(float* ws, size_t chunk) { return ws + chunk * kPer + kL + 2 * kS; }
+  __device__ __forceinline__ static float* Y(float* ws, size_t chunk) { return ws + chunk * kPer + kL + 3 * kS; }
+  __device__ __forceinline__ static float* Hs(float* ws, size_t chunk) { return ws + chunk * kPer + kL + 4 * kS; }
+  __device__ __forceinline__ static float* dHs(float* ws, size_t chunk) { return ws + chunk * kPer + kL + 5 * kS; }
+};
+
+typedef unsigned v4u32_t __attribute__((ext_vector_type(4)));
+
+// Chain operand orders (16x16x16 bf16 MFMA, or four 16x16x4 fp32 ones in k order 4 g + u: lane
+// (i, g) of an A fragment holds row i, k = 4 g .. 4 g + 3; an accumulator's lane (j, g) holds rows
+// 4 g .. 4 g + 3 of column j):
+// - afrag: the four elements of A tile (rt, kt) for lane l; two k tiles of a row tile side by
+//   side, so a lane reads a pair of bf16 tiles with one 16-byte load (D 16: one tile);
+// - accfrag: the four floats of accumulator tile rt of value slice s for lane l.
+template <int NT>
+__device__ __forceinline__ size_t afrag(int rt, int kt, int l) {
+  if constexpr (NT == 1) return (size_t)l * 4;
+  else return ((size_t)(rt * (NT / 2) + kt / 2) * 64 + l) * 8 + (kt & 1) * 4;
+}
+template <int NT>
+__device__ __forceinline__ size_t accfrag(int s, int rt, int l) { return ((size_t)(s * NT + rt) * 64 + l) * 4; }
 
 // Eight waves in the chunk kernel's arrangement: wave w owns row block rb (rb and 3 - rb on one
 // SIMD) and every other column tile from ch = w / 4; triangular zeros are skipped.
@@ -215,7 +262,7 @@ __global__ __launch_bounds__(kPrepThreads) void scan_bwd_prep_kernel(const TIn* 
                                                             const uint8_t* __restrict__ active,
                                                             float* __restrict__ ws, int N, int H, int NC) {
   constexpr int PD = D + 4;
-  __shared__ __align__(16) float sK[kC * PD], sQ[kC * PD], sO[kC * PD], sV[kC * PD], sW[kC * PD];
+  __shared__ __align__(16) float sK[kC * PD], sQ[kC * PD], sO[kC * PD], sV[kC * PD], sW[kC * PD], sU[kC * PD];
   __shared__ __align__(16) float sA[kC * kPC], sL[kC * kPC];
   __shared__ float sB[kC];
   const int c = blockIdx.x % NC, bh = blockIdx.x / NC;
@@ -297,17 +344,14 @@ __global__ __launch_bounds__(kPrepThreads) void scan_bwd_prep_kernel(const TIn* 
   for (int e = threadIdx.x; e < kC * kC / 4; e += NTH)
     *reinterpret_cast<f32x4*>(gL + 4 * e) = *reinterpret_cast<const f32x4*>(sL + (e / (kC / 4)) * kPC + 4 * (e % (kC / 4)));
   // W = L diag(beta) K and U = L diag(beta) V (L lower triangular: k blocks 0 .. rb)
-  float* gW = Ws<D>::W(ws, chunk);
-  float* gU = Ws<D>::U(ws, chunk);
   for (int ct = ch; ct < NT; ct += 2) {
     const f32x4 aw = mm16k<false, false, BF>(sL + r0 * kPC, kPC, sK + 16 * ct, PD, 0, rb + 1, zero4(), sB);
     const f32x4 au = mm16k<false, false, BF>(sL + r0 * kPC, kPC, sV + 16 * ct, PD, 0, rb + 1, zero4(), sB);
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int i = r0 + tile_row(r), j = 16 * ct + tile_col();
-      gW[i * D + j] = aw[r];
-      gU[i * D + j] = au[r];
       sW[i * PD + j] = aw[r];
+      sU[i * PD + j] = au[r];
     }
   }
   // P = tril(Q K^T), diagonal included, into sA (tiles above the diagonal: zeros)
@@ -327,197 +371,179 @@ __global__ __launch_bounds__(kPrepThreads) void scan_bwd_prep_kernel(const TIn* 
     for (int r = 0; r < 4; ++r) sV[(r0 + tile_row(r)) * PD + 16 * ct + tile_col()] = acc[r];
   }
   __syncthreads();
-  // Y = Q^T dO - W^T Z [D x D]: its tiles over the waves
+  // the chains' operands, tile (rt, ct) of each [D x D] product over the waves: Y = Q^T dO - W^T Z
+  // and B = K^T U in accumulator order (value slice ct); N = -K^T W into NR and N^T = -W^T K into
+  // NF, each accumulator tile (rt, ct) being A tile (ct, rt) of the other's transpose
   float* gY = Ws<D>::Y(ws, chunk);
+  float* gB = Ws<D>::B(ws, chunk);
+  float* gNF = Ws<D>::NF(ws, chunk);
+  float* gNR = Ws<D>::NR(ws, chunk);
+  const int l = threadIdx.x & 63;
   for (int tile = w; tile < NT * NT; tile += NTH / 64) {
-    const int rt = tile / (D / 16), ct = tile - rt * (D / 16);
-    f32x4 acc = mm16<true, false, BF>(sQ + 16 * rt, PD, sO + 16 * ct, PD, kC, zero4());
+    const int rt = tile / NT, ct = tile - rt * NT;
+    const f32x4 qo = mm16<true, false, BF>(sQ + 16 * rt, PD, sO + 16 * ct, PD, kC, zero4());
     const f32x4 wz = mm16<true, false, BF>(sW + 16 * rt, PD, sV + 16 * ct, PD, kC, zero4());
+    const f32x4 ku = mm16<true, false, BF>(sK + 16 * rt, PD, sU + 16 * ct, PD, kC, zero4());
+    const f32x4 kw = mm16<true, false, BF>(sK + 16 * rt, PD, sW + 16 * ct, PD, kC, zero4());
+    const f32x4 wk = mm16<true, false, BF>(sW + 16 * rt, PD, sK + 16 * ct, PD, kC, zero4());
+    *reinterpret_cast<f32x4*>(gY + accfrag<NT>(ct, rt, l)) = qo - wz;
+    *reinterpret_cast<f32x4*>(gB + accfrag<NT>(ct, rt, l)) = ku;
+    if constexpr (BF) {
+      bf16x4 nr, nf;
 #pragma unroll
-    for (int r = 0; r < 4; ++r) gY[(16 * rt + tile_row(r)) * D + 16 * ct + tile_col()] = acc[r] - wz[r];
+      for (int r = 0; r < 4; ++r) {
+        nr[r] = (__bf16)(-kw[r]);
+        nf[r] = (__bf16)(-wk[r]);
+      }
+      *reinterpret_cast<bf16x4*>(reinterpret_cast<__bf16*>(gNR) + afrag<NT>(ct, rt, l)) = nr;
+      *reinterpret_cast<bf16x4*>(reinterpret_cast<__bf16*>(gNF) + afrag<NT>(ct, rt, l)) = nf;
+    } else {
+      *reinterpret_cast<f32x4*>(gNR + afrag<NT>(ct, rt, l)) = -kw;
+      *reinterpret_cast<f32x4*>(gNF + afrag<NT>(ct, rt, l)) = -wk;
+    }
   }
 }
 
-// The two chains: one workgroup per (b, h, 16 value columns), four waves. A wave's A operands come
-// from global memory straight into registers, a chunk ahead of their use; in MFMA step m lane group
-// g supplies k = (K / 4) g + m, so each lane reads K / 4 consecutive elements of its row (the B
-// operands, from LDS, follow the same k order). Only the 16-column state slice and the chunk's
-// [64 x 16] intermediate live in LDS; two barriers per chunk.
-constexpr int kPS = 20;  // LDS pitch (floats) of a 16-column slice
-constexpr int kRing = 4;  // chunks of chain operands in flight
+// The chains, one wave each: logical blocks [0, S) walk the states forward, [S, 2 S) the state's
+// gradient backward (S = B H D / 16 value slices). A step records the slice (the state at the
+// chunk's start, or its gradient at the chunk's end) and applies X += A bf16(X) + C with the
+// chunk's A (N or N^T) and C (B or Y): every B operand of the product is the lane's own
+// accumulator, rounded, so the chain needs no data from other lanes. The operands of kRing chunks
+// are in flight in registers: a slot is refilled with the chunk kRing later right after its use
+// (unconditionally, the last chunk again past the end, so that no load sits behind a branch).
+template <int D, bool BF>
+struct ChainShape {
+  static constexpr int NT = D / 16;
+  // chunks of operands in flight: as many as the registers hold without spills
+  static constexpr int kRing = BF ? (D >= 64 ? 6 : 12) : (D >= 64 ? 2 : (D >= 32 ? 8 : 12));
+};
 
-// C[16 x 16] += A B with A from registers (a[m] = A[i][(K / 4) g + m], lane (i, g)) and B
-// row-major in LDS ([k][16], pitch kPS): K / 4 MFMA steps
-// BF: each four k rounded to bf16 and multiplied by one 16x16x16 bf16 MFMA (fp32 accumulation).
-template <int KM, bool BF = false>
-__device__ __forceinline__ f32x4 mm_reg(const float (&a)[KM], const float* Y, f32x4 acc) {
-  const int l = threadIdx.x & 63, j = l & 15, g = l >> 4;
-  if constexpr (BF) {
+template <int NT, bool BF>
+struct ChainOps {
+  static constexpr int kA = BF ? 2 : 4;  // dwords per A tile and lane
+  uint32_t a[kA * NT * NT];  // A tile (rt, kt): a[kA (rt NT + kt)] .. + kA - 1, four bf16 or fp32
+  f32x4 add[NT];             // the added term's accumulator tiles
+};
+
+// A chain's loads and stores go through one buffer resource over its (b, h) chunks: the chunk's
+// offset is a scalar, a lane's offset within the chunk a constant.
+template <int D, bool BF>
+__device__ __forceinline__ void load_chain_ops(ChainOps<D / 16, BF>& o, __amdgpu_buffer_rsrc_t rs, unsigned a_off,
+                                               unsigned add_off, unsigned chunk_off, int s, int l) {
+  constexpr int NT = D / 16;
+#if defined(__HIP_DEVICE_COMPILE__)
+  if constexpr (!BF) {
 #pragma unroll
-    for (int m = 0; m < KM; m += 4) {
-      bf16x4 av, bv;
+    for (int rt = 0; rt < NT; ++rt)
 #pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        av[u] = (__bf16)a[m + u];
-        bv[u] = (__bf16)Y[(KM * g + m + u) * kPS + j];
+      for (int kt = 0; kt < NT; ++kt) {
+        const auto v = __builtin_amdgcn_raw_buffer_load_b128(rs, a_off + 4 * (unsigned)afrag<NT>(rt, kt, l), chunk_off, 0);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) o.a[4 * (rt * NT + kt) + e] = v[e];
       }
-      acc = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(s16x4_t, av), __builtin_bit_cast(s16x4_t, bv),
-                                                      acc, 0, 0, 0);
-    }
+  } else if constexpr (NT == 1) {
+    const auto v = __builtin_amdgcn_raw_buffer_load_b64(rs, a_off + 2 * (unsigned)afrag<NT>(0, 0, l), chunk_off, 0);
+    o.a[0] = v[0];
+    o.a[1] = v[1];
   } else {
 #pragma unroll
-    for (int m = 0; m < KM; ++m) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[m], Y[(KM * g + m) * kPS + j], acc, 0, 0, 0);
-  }
-  return acc;
-}
-
-// The operands hold what was loaded, unconverted: a conversion (or a select) at the load would make
-// the wave wait for the load there, a chunk early.
-template <typename TIn, int D>
-struct StateOps {
-  float wa[D / 4];  // W row 16 w + i, columns (D / 4) g .. + D / 4
-  float ua[4];      // U rows 16 w + 4 g + r, column 16 s + i
-  TIn kr[16];       // K^T row 16 min(w, D / 16 - 1) + i (a feature), tokens 16 g .. + 15
-};
-
-template <typename TIn, int D>
-__device__ __forceinline__ void load_state_ops(StateOps<TIn, D>& o, const float* ws, const TIn* k, size_t chunk, int b,
-                                               int h, int t0, int N, int H, int s) {
-  const int l = threadIdx.x & 63, i = l & 15, g = l >> 4, w = threadIdx.x >> 6;
-  const float* W = Ws<D>::W(const_cast<float*>(ws), chunk);
-  const float* U = Ws<D>::U(const_cast<float*>(ws), chunk);
+    for (int rt = 0; rt < NT; ++rt)
 #pragma unroll
-  for (int q = 0; q < D / 16; ++q) {
-    const f32x4 v = *reinterpret_cast<const f32x4*>(W + (16 * w + i) * D + (D / 4) * g + 4 * q);
+      for (int kt = 0; kt < NT; kt += 2) {
+        const auto v = __builtin_amdgcn_raw_buffer_load_b128(rs, a_off + 2 * (unsigned)afrag<NT>(rt, kt, l), chunk_off, 0);
 #pragma unroll
-    for (int e = 0; e < 4; ++e) o.wa[4 * q + e] = v[e];
+        for (int e = 0; e < 4; ++e) o.a[2 * (rt * NT + kt) + e] = v[e];
+      }
   }
 #pragma unroll
-  for (int r = 0; r < 4; ++r) o.ua[r] = U[(16 * w + 4 * g + r) * D + 16 * s + i];
-  const int f = 16 * min(w, D / 16 - 1) + i;
-#pragma unroll
-  for (int m = 0; m < 16; ++m) o.kr[m] = k[(((size_t)b * N + min(t0 + 16 * g + m, N - 1)) * H + h) * D + f];
+  for (int rt = 0; rt < NT; ++rt) {
+    const auto v = __builtin_amdgcn_raw_buffer_load_b128(rs, add_off + 4 * (unsigned)accfrag<NT>(s, rt, l), chunk_off, 0);
+    o.add[rt] = __builtin_bit_cast(f32x4, v);
+  }
+#endif
 }
 
-// the states at the chunk starts: Delta = U - W H, H += K^T Delta
 template <typename TIn, int D>
-__global__ __launch_bounds__(256) void scan_bwd_states_kernel(const TIn* __restrict__ k,
-                                                              const float* __restrict__ state_in,
-                                                              float* __restrict__ ws, int N, int H, int NC) {
-  constexpr int NS = D / 16;
-  __shared__ __align__(16) float sD[kC * kPS], sH[D * kPS];
-  const int s = blockIdx.x % NS, bh = blockIdx.x / NS;
-  const int b = bh / H, h = bh - b * H;
-  const int w = threadIdx.x >> 6, l = threadIdx.x & 63, j = l & 15, g = l >> 4;
-  const float* h0 = state_in + (size_t)bh * D * D;
-  for (int e = threadIdx.x; e < D * 16; e += kThreads) sH[(e / 16) * kPS + e % 16] = h0[(e / 16) * D + 16 * s + e % 16];
-  // a ring of kRing chunks' operands in registers: a slot is refilled with the chunk kRing later
-  // right after its last use, so each chunk's loads have kRing - 1 steps to arrive
-  StateOps<TIn, D> ops[kRing];
+__global__ __launch_bounds__(64) void scan_bwd_chains_kernel(const float* __restrict__ state_in,
+                                                             const float* __restrict__ d_state,
+                                                             float* __restrict__ d_state_in, float* __restrict__ ws,
+                                                             int NC, int S) {
+  constexpr bool BF = sizeof(TIn) == 2;  // bf16 A operands and 16x16x16 bf16 MFMA; else fp32 ones
+  constexpr int NT = ChainShape<D, BF>::NT, R = ChainShape<D, BF>::kRing;
+  constexpr unsigned kPerB = (unsigned)(Ws<D>::kPer * sizeof(float));  // bytes per chunk
+  constexpr unsigned kLB = (unsigned)(Ws<D>::kL * sizeof(float)), kSB = (unsigned)(Ws<D>::kS * sizeof(float));
+  const int lg = xcd_logical_block(blockIdx.x, gridDim.x);
+  const bool rev = lg >= S;
+  const int sl = rev ? lg - S : lg;
+  const int s = sl % NT, bh = sl / NT;
+  const int l = threadIdx.x & 63, j = l & 15, g = l >> 4;
+  // offsets within a chunk: the A fragments (NF or NR), the added term (B or Y), the record (Hs or dHs)
+  const unsigned a_off = rev ? kLB + kSB : kLB;
+  const unsigned add_off = rev ? kLB + 3 * kSB : kLB + 2 * kSB;
+  const unsigned rec_off = rev ? kLB + 5 * kSB : kLB + 4 * kSB;
+  const __amdgpu_buffer_rsrc_t rs = buffer_rsrc(ws + (size_t)bh * NC * Ws<D>::kPer, (unsigned)NC * kPerB);
+  const float* init = rev ? d_state : state_in;  // (no gradient of the final state: zeros)
+  f32x4 acc[NT];
 #pragma unroll
-  for (int p = 0; p < kRing; ++p)
-    if (p < NC) load_state_ops<TIn, D>(ops[p], ws, k, (size_t)bh * NC + p, b, h, p * kC, N, H, s);
-  __syncthreads();
-  auto step = [&](int c, StateOps<TIn, D>& cur) {
-    const size_t chunk = (size_t)bh * NC + c;
-    float* gH = Ws<D>::Hs(ws, chunk);
+  for (int rt = 0; rt < NT; ++rt)
 #pragma unroll
-    for (int e = threadIdx.x; e < D * 16; e += kThreads) gH[(e / 16) * D + 16 * s + e % 16] = sH[(e / 16) * kPS + e % 16];
-    const f32x4 acc = mm_reg<D / 4, sizeof(TIn) == 2>(cur.wa, sH, zero4());
-#pragma unroll
-    for (int r = 0; r < 4; ++r) sD[(16 * w + 4 * g + r) * kPS + j] = cur.ua[r] - acc[r];
-    __syncthreads();  // Delta complete; the reads of H are done
-    if (w < D / 16) {
-      float ka[16];  // tokens past N contribute nothing
-#pragma unroll
-      for (int m = 0; m < 16; ++m) ka[m] = c * kC + 16 * g + m < N ? to_f32(cur.kr[m]) : 0.f;
-      const f32x4 dh = mm_reg<16, sizeof(TIn) == 2>(ka, sD, zero4());
-#pragma unroll
-      for (int r = 0; r < 4; ++r) sH[(16 * w + 4 * g + r) * kPS + j] += dh[r];
-    }
-    if (c + kRing < NC) load_state_ops<TIn, D>(cur, ws, k, chunk + kRing, b, h, (c + kRing) * kC, N, H, s);
-    __syncthreads();
+    for (int r = 0; r < 4; ++r)
+      acc[rt][r] = init != nullptr ? init[(size_t)bh * D * D + (16 * rt + 4 * g + r) * D + 16 * s + j] : 0.f;
+  auto chunk_off = [&](int i) { return (unsigned)(rev ? NC - 1 - i : i) * kPerB; };  // the i-th chunk visited
+  auto load = [&](ChainOps<NT, BF>& o, int i) {
+    load_chain_ops<D, BF>(o, rs, a_off, add_off, chunk_off(min(i, NC - 1)), s, l);
   };
-  for (int c = 0; c < NC; c += kRing) {
+  ChainOps<NT, BF> ops[R];
 #pragma unroll
-    for (int p = 0; p < kRing; ++p)
-      if (c + p < NC) step(c + p, ops[p]);
-  }
-}
-
-template <typename TIn, int D>
-struct DStateOps {
-  typedef TIn V4 __attribute__((ext_vector_type(4)));
-  V4 kr[D / 16];    // K row 16 w + i (a token), features (D / 4) g .. + D / 4
-  float wta[16];    // W^T row 16 w' + i (a feature), tokens 16 g .. + 15; w' = min(w, D / 16 - 1)
-  float ya[4];      // Y rows 16 w' + 4 g + r, column 16 s + i
-};
-
-template <typename TIn, int D>
-__device__ __forceinline__ void load_dstate_ops(DStateOps<TIn, D>& o, const float* ws, const TIn* k, size_t chunk,
-                                                int b, int h, int t0, int N, int H, int s) {
-  const int l = threadIdx.x & 63, i = l & 15, g = l >> 4, w = threadIdx.x >> 6;
-  const TIn* kr = k + (((size_t)b * N + min(t0 + 16 * w + i, N - 1)) * H + h) * D + (D / 4) * g;
+  for (int p = 0; p < R; ++p) load(ops[p], p);
+  auto step = [&](int i, ChainOps<NT, BF>& cur) {
+    const unsigned co = chunk_off(i);
+    s16x4_t xb[NT];
+    f32x4 xf[NT];
 #pragma unroll
-  for (int q = 0; q < D / 16; ++q) o.kr[q] = *reinterpret_cast<const typename DStateOps<TIn, D>::V4*>(kr + 4 * q);
-  const int wf = min(w, D / 16 - 1);
-  const float* W = Ws<D>::W(const_cast<float*>(ws), chunk);
-  const float* Y = Ws<D>::Y(const_cast<float*>(ws), chunk);
+    for (int kt = 0; kt < NT; ++kt) {
+#if defined(__HIP_DEVICE_COMPILE__)
+      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(v4u32_t, acc[kt]), rs,
+                                             rec_off + 4 * (unsigned)accfrag<NT>(s, kt, l), co, 0);
+#endif
+      xf[kt] = acc[kt];
+      bf16x4 t;
 #pragma unroll
-  for (int m = 0; m < 16; ++m) o.wta[m] = W[(16 * g + m) * D + 16 * wf + i];
-#pragma unroll
-  for (int r = 0; r < 4; ++r) o.ya[r] = Y[(16 * wf + 4 * g + r) * D + 16 * s + i];
-}
-
-// the state's gradient at every chunk's end (reverse chain) and at the start: G += Y - W^T (K G)
-template <typename TIn, int D>
-__global__ __launch_bounds__(256) void scan_bwd_dstate_kernel(const TIn* __restrict__ k,
-                                                              const float* __restrict__ d_state,
-                                                              float* __restrict__ d_state_in, float* __restrict__ ws,
-                                                              int N, int H, int NC) {
-  constexpr int NS = D / 16;
-  __shared__ __align__(16) float sX[kC * kPS], sG[D * kPS];
-  const int s = blockIdx.x % NS, bh = blockIdx.x / NS;
-  const int b = bh / H, h = bh - b * H;
-  const int w = threadIdx.x >> 6, l = threadIdx.x & 63, j = l & 15, g = l >> 4;
-  for (int e = threadIdx.x; e < D * 16; e += kThreads)
-    sG[(e / 16) * kPS + e % 16] = d_state != nullptr ? d_state[(size_t)bh * D * D + (e / 16) * D + 16 * s + e % 16] : 0.f;
-  // the register ring of the state chain, walking the chunks backwards
-  DStateOps<TIn, D> ops[kRing];
-#pragma unroll
-  for (int p = 0; p < kRing; ++p)
-    if (p < NC) load_dstate_ops<TIn, D>(ops[p], ws, k, (size_t)bh * NC + NC - 1 - p, b, h, (NC - 1 - p) * kC, N, H, s);
-  __syncthreads();
-  auto step = [&](int c, DStateOps<TIn, D>& cur) {
-    const size_t chunk = (size_t)bh * NC + c;
-    float* gG = Ws<D>::dHs(ws, chunk);
-#pragma unroll
-    for (int e = threadIdx.x; e < D * 16; e += kThreads) gG[(e / 16) * D + 16 * s + e % 16] = sG[(e / 16) * kPS + e % 16];
-    float ka[D / 4];  // tokens past N contribute nothing
-    const bool live = c * kC + 16 * w + (threadIdx.x & 15) < N;
-#pragma unroll
-    for (int q = 0; q < D / 16; ++q)
-#pragma unroll
-      for (int e = 0; e < 4; ++e) ka[4 * q + e] = live ? to_f32(cur.kr[q][e]) : 0.f;
-    const f32x4 x = mm_reg<D / 4, sizeof(TIn) == 2>(ka, sG, zero4());
-#pragma unroll
-    for (int r = 0; r < 4; ++r) sX[(16 * w + 4 * g + r) * kPS + j] = x[r];
-    __syncthreads();  // X complete; the reads of G are done
-    if (w < D / 16) {
-      const f32x4 wx = mm_reg<16, sizeof(TIn) == 2>(cur.wta, sX, zero4());
-#pragma unroll
-      for (int r = 0; r < 4; ++r) sG[(16 * w + 4 * g + r) * kPS + j] += cur.ya[r] - wx[r];
+      for (int r = 0; r < 4; ++r) t[r] = (__bf16)acc[kt][r];
+      xb[kt] = __builtin_bit_cast(s16x4_t, t);
     }
-    if (c - kRing >= 0) load_dstate_ops<TIn, D>(cur, ws, k, chunk - kRing, b, h, (c - kRing) * kC, N, H, s);
-    __syncthreads();
-  };
-  for (int i = 0; i < NC; i += kRing) {
 #pragma unroll
-    for (int p = 0; p < kRing; ++p)
-      if (i + p < NC) step(NC - 1 - i - p, ops[p]);
+    for (int rt = 0; rt < NT; ++rt) {
+      acc[rt] += cur.add[rt];
+#pragma unroll
+      for (int kt = 0; kt < NT; ++kt) {
+        const uint32_t* a = cur.a + ChainOps<NT, BF>::kA * (rt * NT + kt);
+        if constexpr (BF) {
+          const uint2 a2 = {a[0], a[1]};
+          acc[rt] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(s16x4_t, a2), xb[kt], acc[rt], 0, 0, 0);
+        } else {
+#pragma unroll
+          for (int u = 0; u < 4; ++u)
+            acc[rt] = __builtin_amdgcn_mfma_f32_16x16x4f32(__builtin_bit_cast(float, a[u]), xf[kt][u], acc[rt], 0, 0, 0);
+        }
+      }
+    }
+    load(cur, i + R);
+  };
+  int i = 0;
+  for (; i + R <= NC; i += R) {
+#pragma unroll
+    for (int p = 0; p < R; ++p) step(i + p, ops[p]);
   }
-  for (int e = threadIdx.x; e < D * 16; e += kThreads)
-    d_state_in[(size_t)bh * D * D + (e / 16) * D + 16 * s + e % 16] = sG[(e / 16) * kPS + e % 16];
+#pragma unroll
+  for (int p = 0; p < R; ++p)
+    if (i + p < NC) step(i + p, ops[p]);
+  if (rev) {
+#pragma unroll
+    for (int rt = 0; rt < NT; ++rt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) d_state_in[(size_t)bh * D * D + (16 * rt + 4 * g + r) * D + 16 * s + j] = acc[rt][r];
+  }
 }
 
 // Eight waves, two per SIMD, hiding each other's LDS and MFMA latency: wave w owns row block rb
@@ -547,7 +573,7 @@ __global__ __launch_bounds__(kChunkThreads) void scan_bwd_chunk_kernel(
   float *Bd = buf[7], *Bp = buf[8];
   {
     ChunkRows<TIn, D, NTH> rq, rk, ro, rv;
-    MatRows<D, D, NTH> mh, mg;
+    AccRows<D, NTH> mh, mg;
     MatRows<kC, kC, NTH> ml;
     ChunkBeta<TIn> rb_;
     rq.fetch(q, b, h, t0, N, H);
@@ -741,7 +767,7 @@ __global__ __launch_bounds__(kChunkThreads) void scan_bwd_chunk_kernel(
 
 size_t workspace_floats(int B, int N, int H, int D) {
   const size_t nc = (size_t)(N + kC - 1) / kC;
-  const size_t per = (size_t)kC * kC + 2 * (size_t)kC * D + 3 * (size_t)D * D;
+  const size_t per = (size_t)kC * kC + 6 * (size_t)D * D;
   return (size_t)B * H * nc * per;
 }
 
@@ -753,9 +779,8 @@ void launch(const TIn* q, const TIn* k, const TIn* v, const TIn* beta, const flo
   const unsigned chunks = (unsigned)((size_t)B * H * NC), slices = (unsigned)((size_t)B * H * (D / 16));
   hipLaunchKernelGGL((scan_bwd_prep_kernel<TIn, D>), dim3(chunks), dim3(kPrepThreads), 0, stream, q, k, v, beta, d_o, active, ws,
                      N, H, NC);
-  hipLaunchKernelGGL((scan_bwd_states_kernel<TIn, D>), dim3(slices), dim3(256), 0, stream, k, state_in, ws, N, H, NC);
-  hipLaunchKernelGGL((scan_bwd_dstate_kernel<TIn, D>), dim3(slices), dim3(256), 0, stream, k, d_state, d_state_in, ws, N,
-                     H, NC);
+  hipLaunchKernelGGL((scan_bwd_chains_kernel<TIn, D>), dim3(2 * slices), dim3(64), 0, stream, state_in, d_state,
+                     d_state_in, ws, NC, (int)slices);
   hipLaunchKernelGGL((scan_bwd_chunk_kernel<TIn, D>), dim3(chunks), dim3(kChunkThreads), 0, stream, q, k, v, beta, d_o, active, ws,
                      dq, dk, dv, dbeta, N, H, NC);
 }

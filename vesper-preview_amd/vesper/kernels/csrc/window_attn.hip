@@ -230,6 +230,13 @@ __global__ __launch_bounds__(256, D >= 128 ? 2 : (CARRY && D == 64 ? 3 : 4)) voi
   // one tile: K, V in Kt, Vt; the next tile's loads go to Kn, Vn (last read before the previous barrier)
   auto tile = [&](int it, const T* Kt, const T* Vt, T* Kn, T* Vn) {
     const int k0 = kfirst + it * KT;
+    // a wave in the first half of its tiles issues ahead of those in their second half: the four
+    // workgroups of a CU then finish closer together (issue goes oldest-first otherwise, and the
+    // last workgroup would run its final tiles alone on the CU)
+    if (2 * it < ntiles)
+      __builtin_amdgcn_s_setprio(1);
+    else
+      __builtin_amdgcn_s_setprio(0);
     if (it + 1 < ntiles) {
       if constexpr (CARRY) {
         fresh = __builtin_amdgcn_ballot_w64(fl != 0);
