@@ -765,6 +765,279 @@ __global__ __launch_bounds__(kChunkThreads) void scan_bwd_chunk_kernel(
   }
 }
 
+// ---- the chunk kernel on bf16 LDS tiles (bf16 entry, head widths 32 and 64) ------------------
+// Operands live in LDS as bf16 row-major tiles and feed 16x16x32 MFMAs in one of two forms, with
+// the same k order (k0 + 8 g + e for lane group g, element e) so that any two combine:
+// - frow(X, ld, r0, k0): row r0 + lq of X, k along its columns (one 16-byte read);
+// - fcol(X, ld, c0, k0): column c0 + lq of X, k along its rows (two transposed 8-byte reads).
+// A product's A operand is frow(X) for X or fcol(X) for X^T; its B operand fcol(Y) for Y or
+// frow(Y) for Y^T. Results (lane (j, g) holds rows 4 g .. 4 g + 3 of column j) go back to LDS as
+// bf16, the rounding the fp32-staged kernel applied when it multiplied them.
+__device__ __forceinline__ bf16x8 frow(const __bf16* X, int ld, int r0, int k0) {
+  const int l = threadIdx.x & 63, lq = l & 15, g = l >> 4;
+  return *reinterpret_cast<const bf16x8*>(X + (r0 + lq) * ld + k0 + 8 * g);
+}
+__device__ __forceinline__ bf16x8 fcol(const __bf16* X, int ld, int c0, int k0) {
+  const int l = threadIdx.x & 63, lq = l & 15, g = l >> 4;
+  const __bf16* p = X + (k0 + 8 * g + (lq >> 2)) * ld + c0 + 4 * (lq & 3);
+  const bf16x4 lo = read_tr16<bf16x4>(p), hi = read_tr16<bf16x4>(p + 4 * ld);
+  return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+}
+__device__ __forceinline__ f32x4 mma32(bf16x8 a, bf16x8 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+// an accumulator tile into a bf16 tile at (r0, c0)
+__device__ __forceinline__ void put_tile(__bf16* X, int ld, int r0, int c0, f32x4 acc) {
+#pragma unroll
+  for (int r = 0; r < 4; ++r) X[(r0 + tile_row(r)) * ld + c0 + tile_col()] = (__bf16)acc[r];
+}
+// an accumulator tile into rows t0 + r0 .. of a [B, N, H, D] tensor (rows past N skipped)
+template <typename TIn, int D>
+__device__ __forceinline__ void store_rows(TIn* dst, int b, int h, int t0, int N, int H, int r0, int c0, f32x4 acc) {
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int t = t0 + r0 + tile_row(r);
+    if (t < N) dst[(((size_t)b * N + t) * H + h) * D + c0 + tile_col()] = from_f32<TIn>(acc[r]);
+  }
+}
+
+// chunk rows t0 .. t0 + 63 of a [B, N, H, D] bf16 tensor into LDS [64][ld] bf16; rows past N,
+// and with `active` inactive tokens' rows, are zero. 16 bytes a thread and step.
+template <int D, int NTH>
+struct ChunkRows16 {
+  static constexpr int kN = kC * D / 8, kIt = (kN + NTH - 1) / NTH;
+  bf16x8 raw[kIt];
+  bool ok[kIt];
+  __device__ __forceinline__ void fetch(const __bf16* src, int b, int h, int t0, int N, int H,
+                                        const uint8_t* active = nullptr) {
+#pragma unroll
+    for (int it = 0; it < kIt; ++it) {
+      const int e = min((int)threadIdx.x + NTH * it, kN - 1), row = e / (D / 8), c = 8 * (e % (D / 8));
+      const int tc = min(t0 + row, N - 1);
+      raw[it] = *reinterpret_cast<const bf16x8*>(src + (((size_t)b * N + tc) * H + h) * D + c);
+      ok[it] = t0 + row < N && (active == nullptr || active[(size_t)b * N + tc] != 0);
+    }
+  }
+  __device__ __forceinline__ void put(__bf16* dst, int ld) const {
+#pragma unroll
+    for (int it = 0; it < kIt; ++it) {
+      const int e = threadIdx.x + NTH * it, row = e / (D / 8), c = 8 * (e % (D / 8));
+      bf16x8 x = raw[it];
+      if (!ok[it]) {
+#pragma unroll
+        for (int u = 0; u < 8; ++u) x[u] = (__bf16)0.f;
+      }
+      if (kN % NTH == 0 || e < kN) *reinterpret_cast<bf16x8*>(dst + row * ld + c) = x;
+    }
+  }
+};
+
+// a [D][D] fp32 record in accumulator order into LDS [D][ld] bf16, row-major
+template <int D, int NTH>
+struct AccRows16 {
+  static constexpr int NT = D / 16, kN = D * D / 4, kIt = (kN + NTH - 1) / NTH;
+  f32x4 raw[kIt];
+  __device__ __forceinline__ void fetch(const float* src) {
+#pragma unroll
+    for (int it = 0; it < kIt; ++it)
+      raw[it] = *reinterpret_cast<const f32x4*>(src + 4 * min((int)threadIdx.x + NTH * it, kN - 1));
+  }
+  __device__ __forceinline__ void put(__bf16* dst, int ld) const {
+#pragma unroll
+    for (int it = 0; it < kIt; ++it) {
+      const int e = threadIdx.x + NTH * it;  // = (s NT + rt) 64 + lane
+      if (kN % NTH == 0 || e < kN) {
+        const int lane = e & 63, st = e >> 6, sl = st / NT, rt = st - sl * NT;
+        const int row = 16 * rt + 4 * (lane >> 4), col = 16 * sl + (lane & 15);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) dst[(row + r) * ld + col] = (__bf16)raw[it][r];
+      }
+    }
+  }
+};
+
+// Eight waves: wave w owns row block rb of every [64 x .] result (rb and 3 - rb on one SIMD) and
+// every other column tile from ch = w / 4. Triangular factors bound each product's k range (in
+// steps of 32) and leave tiles above the diagonal zero.
+template <int D>
+__global__ __launch_bounds__(kChunkThreads) void scan_bwd_chunk_bf16_kernel(
+    const __bf16* __restrict__ q, const __bf16* __restrict__ k, const __bf16* __restrict__ v,
+    const __bf16* __restrict__ beta, const __bf16* __restrict__ d_o, const uint8_t* __restrict__ active,
+    const float* __restrict__ ws, __bf16* __restrict__ dq, __bf16* __restrict__ dk, __bf16* __restrict__ dv,
+    __bf16* __restrict__ dbeta, int N, int H, int NC) {
+  using T = __bf16;
+  constexpr int NT = D / 16;  // column tiles of a [64 x D] result
+  constexpr int NTH = kChunkThreads;
+  constexpr int LD = D + 8, L6 = kC + 8, LF = kC + 4;  // pitches: [64][D] and [D][D], [64][64], fp32 [64][64]
+  __shared__ __align__(16) T sQ[kC * LD], sK[kC * LD], sO[kC * LD], sR[kC * LD], sD[kC * LD], sDD[kC * LD],
+      sDR[kC * LD];
+  __shared__ __align__(16) T sH[D * LD], sG[D * LD];
+  __shared__ __align__(16) T sT[kC * L6], sL[kC * L6], sP[kC * L6], sM[kC * L6];
+  __shared__ __align__(16) float sLf[kC * LF];
+  __shared__ float sB[kC], sPart[4 * kC], sRow[2 * kC];
+  T* sX1 = sT;   // X1 = L^T dL once T is done with
+  T* sS2 = sP;   // S2 = tril(dO Delta^T) once P is done with
+  T* sDL = sM;   // dL, then M = diag(beta) dA
+  const int c = blockIdx.x % NC, bh = blockIdx.x / NC;
+  const int b = bh / H, h = bh - b * H;
+  const int t0 = c * kC;
+  const size_t chunk = blockIdx.x;
+  const int w = threadIdx.x >> 6, ch = w >> 2, rb = ch == 0 ? w : 7 - w, r0 = 16 * rb;
+  const int khi = (rb + 2) / 2 * 32;  // k range of a lower triangular A operand for row block rb
+  const int klo = rb / 2 * 32;        // and of an upper triangular one
+  {
+    ChunkRows16<D, NTH> rq, rk, ro, rv;
+    AccRows16<D, NTH> mh, mg;
+    MatRows<kC, kC, NTH> ml;
+    ChunkBeta<T> rbeta;
+    rq.fetch(q, b, h, t0, N, H);
+    rk.fetch(k, b, h, t0, N, H);
+    ro.fetch(d_o, b, h, t0, N, H, active);
+    rv.fetch(v, b, h, t0, N, H);
+    mh.fetch(Ws<D>::Hs(const_cast<float*>(ws), chunk));
+    mg.fetch(Ws<D>::dHs(const_cast<float*>(ws), chunk));
+    ml.fetch(Ws<D>::L(const_cast<float*>(ws), chunk));
+    rbeta.fetch(beta, b, h, t0, N, H);
+    rq.put(sQ, LD);
+    rk.put(sK, LD);
+    ro.put(sO, LD);
+    rv.put(sR, LD);
+    mh.put(sH, LD);
+    mg.put(sG, LD);
+    ml.put(sLf, LF);
+    rbeta.put(sB, t0, N);
+  }
+  __syncthreads();
+  // L and T = L diag(beta) in bf16
+  for (int e = threadIdx.x; e < kC * kC / 4; e += NTH) {
+    const int i = e / (kC / 4), j = 4 * (e % (kC / 4));
+    const f32x4 x = *reinterpret_cast<const f32x4*>(sLf + i * LF + j);
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      sL[i * L6 + j + u] = (T)x[u];
+      sT[i * L6 + j + u] = (T)(x[u] * sB[j + u]);
+    }
+  }
+  // R = V - K H in place (each lane reads only its own V entries)
+  for (int ct = ch; ct < NT; ct += 2) {
+    f32x4 acc = zero4();
+    for (int kk = 0; kk < D; kk += 32) acc = mma32(frow(sK, LD, r0, kk), fcol(sH, LD, 16 * ct, kk), acc);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      T& x = sR[(r0 + tile_row(r)) * LD + 16 * ct + tile_col()];
+      x = (T)((float)x - acc[r]);
+    }
+  }
+  // P = tril(Q K^T), diagonal included
+  for (int ct = ch; ct < 4; ct += 2) {
+    f32x4 acc = zero4();
+    if (ct <= rb)
+      for (int kk = 0; kk < D; kk += 32) acc = mma32(frow(sQ, LD, r0, kk), frow(sK, LD, 16 * ct, kk), acc);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) acc[r] = 16 * ct + tile_col() <= r0 + tile_row(r) ? acc[r] : 0.f;
+    put_tile(sP, L6, r0, 16 * ct, acc);
+  }
+  __syncthreads();
+  // Delta = T R; dDelta = K G + P^T dO
+  for (int ct = ch; ct < NT; ct += 2) {
+    f32x4 d = zero4(), dd = zero4();
+    for (int kk = 0; kk < khi; kk += 32) d = mma32(frow(sT, L6, r0, kk), fcol(sR, LD, 16 * ct, kk), d);
+    for (int kk = 0; kk < D; kk += 32) dd = mma32(frow(sK, LD, r0, kk), fcol(sG, LD, 16 * ct, kk), dd);
+    for (int kk = klo; kk < kC; kk += 32) dd = mma32(fcol(sP, L6, r0, kk), fcol(sO, LD, 16 * ct, kk), dd);
+    put_tile(sD, LD, r0, 16 * ct, d);
+    put_tile(sDD, LD, r0, 16 * ct, dd);
+  }
+  __syncthreads();
+  // dR = T^T dDelta (= dV; kept negated for dK); S2 = tril(dO Delta^T) over P; dT = dDelta R^T:
+  // dbeta_j gets sum_i dT_ij L_ij (column sums per row block into sPart), dL = tril(dT) diag(beta)
+  for (int ct = ch; ct < NT; ct += 2) {
+    f32x4 acc = zero4();
+    for (int kk = klo; kk < kC; kk += 32) acc = mma32(fcol(sT, L6, r0, kk), fcol(sDD, LD, 16 * ct, kk), acc);
+    store_rows<T, D>(dv, b, h, t0, N, H, r0, 16 * ct, acc);
+    put_tile(sDR, LD, r0, 16 * ct, -acc);
+  }
+  for (int ct = ch; ct < 4; ct += 2) {
+    f32x4 s2 = zero4(), dt = zero4();
+    if (ct <= rb) {
+      for (int kk = 0; kk < D; kk += 32) {
+        s2 = mma32(frow(sO, LD, r0, kk), frow(sD, LD, 16 * ct, kk), s2);
+        dt = mma32(frow(sDD, LD, r0, kk), frow(sR, LD, 16 * ct, kk), dt);
+      }
+    }
+    const int j = 16 * ct + tile_col();
+    float part = 0.f;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int i = r0 + tile_row(r);
+      part += dt[r] * sLf[i * LF + j];
+      s2[r] = j <= i ? s2[r] : 0.f;
+      dt[r] = j <= i ? dt[r] * sB[j] : 0.f;
+    }
+    part = sum_over_rows(part);
+    if ((threadIdx.x & 63) < 16) sPart[rb * kC + j] = part;
+    put_tile(sS2, L6, r0, 16 * ct, s2);
+    put_tile(sDL, L6, r0, 16 * ct, dt);
+  }
+  __syncthreads();
+  // dQ = dO H^T + S2 K; X1 = L^T dL over T (L^T upper, dL lower: k from max(rb, ct))
+  for (int ct = ch; ct < NT; ct += 2) {
+    f32x4 acc = zero4();
+    for (int kk = 0; kk < D; kk += 32) acc = mma32(frow(sO, LD, r0, kk), frow(sH, LD, 16 * ct, kk), acc);
+    for (int kk = 0; kk < khi; kk += 32) acc = mma32(frow(sS2, L6, r0, kk), fcol(sK, LD, 16 * ct, kk), acc);
+    store_rows<T, D>(dq, b, h, t0, N, H, r0, 16 * ct, acc);
+  }
+  for (int ct = ch; ct < 4; ct += 2) {  // (T was last read before the previous barrier)
+    f32x4 x1 = zero4();
+    for (int kk = max(rb, ct) / 2 * 32; kk < kC; kk += 32)
+      x1 = mma32(fcol(sL, L6, r0, kk), fcol(sDL, L6, 16 * ct, kk), x1);
+    put_tile(sX1, L6, r0, 16 * ct, x1);
+  }
+  __syncthreads();
+  // dA = -tril(X1 L^T, -1) (L^T[k][j] nonzero for k <= j); dbeta_i gets sum_m dA_im (k_i . k_m)
+  // (row sums per column half into sRow); M = diag(beta) dA over dL
+  float rows[4] = {0.f, 0.f, 0.f, 0.f};
+  for (int ct = ch; ct < 4; ct += 2) {
+    f32x4 da = zero4(), gk = zero4();
+    if (ct <= rb) {
+      for (int kk = 0; kk < (ct + 2) / 2 * 32; kk += 32) da = mma32(frow(sX1, L6, r0, kk), frow(sL, L6, 16 * ct, kk), da);
+      for (int kk = 0; kk < D; kk += 32) gk = mma32(frow(sK, LD, r0, kk), frow(sK, LD, 16 * ct, kk), gk);
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int i = r0 + tile_row(r), j = 16 * ct + tile_col();
+      da[r] = j < i ? -da[r] : 0.f;
+      rows[r] += da[r] * gk[r];
+      da[r] *= sB[i];
+    }
+    put_tile(sM, L6, r0, 16 * ct, da);
+  }
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const float x = group_sum<16>(rows[r]);
+    if (tile_col() == 0) sRow[ch * kC + r0 + tile_row(r)] = x;
+  }
+  __syncthreads();
+  // dK = Delta G^T + S2^T Q - dR H^T + M K + M^T K
+  for (int ct = ch; ct < NT; ct += 2) {
+    f32x4 acc = zero4();
+    for (int kk = 0; kk < D; kk += 32) {
+      acc = mma32(frow(sD, LD, r0, kk), frow(sG, LD, 16 * ct, kk), acc);
+      acc = mma32(frow(sDR, LD, r0, kk), frow(sH, LD, 16 * ct, kk), acc);
+    }
+    for (int kk = klo; kk < kC; kk += 32) {
+      acc = mma32(fcol(sS2, L6, r0, kk), fcol(sQ, LD, 16 * ct, kk), acc);
+      acc = mma32(fcol(sM, L6, r0, kk), fcol(sK, LD, 16 * ct, kk), acc);
+    }
+    for (int kk = 0; kk < khi; kk += 32) acc = mma32(frow(sM, L6, r0, kk), fcol(sK, LD, 16 * ct, kk), acc);
+    store_rows<T, D>(dk, b, h, t0, N, H, r0, 16 * ct, acc);
+  }
+  const int i = threadIdx.x;
+  if (i < kC && t0 + i < N) {
+    const float x = ((sPart[i] + sPart[kC + i]) + (sPart[2 * kC + i] + sPart[3 * kC + i])) + (sRow[i] + sRow[kC + i]);
+    dbeta[((size_t)b * N + t0 + i) * H + h] = (T)x;
+  }
+}
+
 size_t workspace_floats(int B, int N, int H, int D) {
   const size_t nc = (size_t)(N + kC - 1) / kC;
   const size_t per = (size_t)kC * kC + 6 * (size_t)D * D;
@@ -781,8 +1054,12 @@ void launch(const TIn* q, const TIn* k, const TIn* v, const TIn* beta, const flo
                      N, H, NC);
   hipLaunchKernelGGL((scan_bwd_chains_kernel<TIn, D>), dim3(2 * slices), dim3(64), 0, stream, state_in, d_state,
                      d_state_in, ws, NC, (int)slices);
-  hipLaunchKernelGGL((scan_bwd_chunk_kernel<TIn, D>), dim3(chunks), dim3(kChunkThreads), 0, stream, q, k, v, beta, d_o, active, ws,
-                     dq, dk, dv, dbeta, N, H, NC);
+  if constexpr (sizeof(TIn) == 2 && D >= 32)
+    hipLaunchKernelGGL((scan_bwd_chunk_bf16_kernel<D>), dim3(chunks), dim3(kChunkThreads), 0, stream, q, k, v, beta, d_o,
+                       active, ws, dq, dk, dv, dbeta, N, H, NC);
+  else
+    hipLaunchKernelGGL((scan_bwd_chunk_kernel<TIn, D>), dim3(chunks), dim3(kChunkThreads), 0, stream, q, k, v, beta, d_o,
+                       active, ws, dq, dk, dv, dbeta, N, H, NC);
 }
 
 template <typename TIn>
