@@ -1038,6 +1038,171 @@ __global__ __launch_bounds__(kChunkThreads) void scan_bwd_chunk_bf16_kernel(
   }
 }
 
+// The prep kernel on bf16 LDS tiles (bf16 entry, head widths 32 and 64). The UT solve stays in
+// fp32; once it is done its two fp32 buffers hold the bf16 T and P, and W and U, so that the
+// kernel's LDS (about 74 KB at D 64) lets two workgroups share a CU.
+template <int D>
+__global__ __launch_bounds__(kPrepThreads) void scan_bwd_prep_bf16_kernel(
+    const __bf16* __restrict__ q, const __bf16* __restrict__ k, const __bf16* __restrict__ v,
+    const __bf16* __restrict__ beta, const __bf16* __restrict__ d_o, const uint8_t* __restrict__ active,
+    float* __restrict__ ws, int N, int H, int NC) {
+  using T = __bf16;
+  constexpr int NT = D / 16, NTH = kPrepThreads;
+  constexpr int LD = D + 8, L6 = kC + 8, PF = kC + 8;  // pitches: [64][D] bf16, [64][64] bf16, [64][64] fp32
+  static_assert(2 * kC * L6 * sizeof(T) == kC * PF * sizeof(float) && 2 * kC * LD * sizeof(T) <= kC * PF * sizeof(float),
+                "T and P, then W and U, fit the fp32 buffers of the solve");
+  __shared__ __align__(16) T sQ[kC * LD], sK[kC * LD], sV[kC * LD], sO[kC * LD];
+  __shared__ __align__(16) float sA[kC * PF], sL[kC * PF];
+  __shared__ float sB[kC];
+  T* sT = reinterpret_cast<T*>(sA);  // T = L diag(beta), then P beside it, once A is done with
+  T* sP = sT + kC * L6;
+  T* sW = reinterpret_cast<T*>(sL);  // W and U once L is in bf16 (T) and in the workspace
+  T* sU = sW + kC * LD;
+  T* sZ = sV;                        // Z = P^T dO once U is done
+  const int c = blockIdx.x % NC, bh = blockIdx.x / NC;
+  const int b = bh / H, h = bh - b * H;
+  const int t0 = c * kC;
+  const size_t chunk = blockIdx.x;
+  const int w = threadIdx.x >> 6, ch = w >> 2, rb = ch == 0 ? w : 7 - w, r0 = 16 * rb;
+  const int khi = (rb + 2) / 2 * 32, klo = rb / 2 * 32;
+  {
+    ChunkRows16<D, NTH> rq, rk, rv, ro;
+    ChunkBeta<T> rbeta;
+    rk.fetch(k, b, h, t0, N, H);
+    rq.fetch(q, b, h, t0, N, H);
+    ro.fetch(d_o, b, h, t0, N, H, active);
+    rv.fetch(v, b, h, t0, N, H);
+    rbeta.fetch(beta, b, h, t0, N, H);
+    rk.put(sK, LD);
+    rq.put(sQ, LD);
+    ro.put(sO, LD);
+    rv.put(sV, LD);
+    rbeta.put(sB, t0, N);
+  }
+  __syncthreads();
+  // A = tril(diag(beta) K K^T, -1) in fp32
+  for (int ct = ch; ct < 4; ct += 2) {
+    f32x4 acc = zero4();
+    if (ct <= rb)
+      for (int kk = 0; kk < D; kk += 32) acc = mma32(frow(sK, LD, r0, kk), frow(sK, LD, 16 * ct, kk), acc);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int i = r0 + tile_row(r), j = 16 * ct + tile_col();
+      sA[i * PF + j] = i > j ? sB[i] * acc[r] : 0.f;
+    }
+  }
+  __syncthreads();
+  // L = (I + A)^-1: the diagonal 16x16 blocks by forward substitution (a lane per column of a
+  // block), then L_ij = -L_ii sum_{m = j}^{i - 1} A_im L_mj level by level on fp32 MFMA
+#pragma unroll
+  for (int e = threadIdx.x; e < kC * kC / 4; e += NTH) {
+    const int i = e / (kC / 4), j = 4 * (e % (kC / 4));
+    if (i / 16 < j / 16) *reinterpret_cast<f32x4*>(sL + i * PF + j) = zero4();
+  }
+  if (w == 0) {
+    const int l = threadIdx.x & 63, blk = l >> 4, col = l & 15;
+    const float* ab = sA + 16 * blk * PF + 16 * blk;
+    float x[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      float sum = i == col ? 1.f : 0.f;
+#pragma unroll
+      for (int m = 0; m < i; ++m) sum -= ab[i * PF + m] * x[m];
+      x[i] = sum;
+    }
+#pragma unroll
+    for (int i = 0; i < 16; ++i) sL[(16 * blk + i) * PF + 16 * blk + col] = x[i];
+  }
+  __syncthreads();
+  for (int lev = 1; lev < 4; ++lev) {
+    const int i = w + lev, j = w;
+    if (i < 4) {
+      f32x4 y = zero4();
+      for (int m = j; m < i; ++m)
+        y = mm16<false, false>(sA + 16 * i * PF + 16 * m, PF, sL + 16 * m * PF + 16 * j, PF, 16, y);
+      float* dst = sL + 16 * i * PF + 16 * j;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) dst[tile_row(r) * PF + tile_col()] = y[r];
+      wave_sync_lds();
+      const f32x4 x = mm16<false, false>(sL + 16 * i * PF + 16 * i, PF, dst, PF, 16, zero4());
+      wave_sync_lds();
+#pragma unroll
+      for (int r = 0; r < 4; ++r) dst[tile_row(r) * PF + tile_col()] = -x[r];
+    }
+    __syncthreads();
+  }
+  // L into the workspace; T = L diag(beta) in bf16 over A
+  float* gL = Ws<D>::L(ws, chunk);
+  for (int e = threadIdx.x; e < kC * kC / 4; e += NTH) {
+    const int i = e / (kC / 4), j = 4 * (e % (kC / 4));
+    const f32x4 x = *reinterpret_cast<const f32x4*>(sL + i * PF + j);
+    *reinterpret_cast<f32x4*>(gL + 4 * e) = x;
+    bf16x4 t;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) t[u] = (T)(x[u] * sB[j + u]);
+    *reinterpret_cast<bf16x4*>(sT + i * L6 + j) = t;
+  }
+  __syncthreads();
+  // W = T K and U = T V over L; P = tril(Q K^T) beside T
+  for (int ct = ch; ct < NT; ct += 2) {
+    f32x4 aw = zero4(), au = zero4();
+    for (int kk = 0; kk < khi; kk += 32) {
+      const bf16x8 a = frow(sT, L6, r0, kk);
+      aw = mma32(a, fcol(sK, LD, 16 * ct, kk), aw);
+      au = mma32(a, fcol(sV, LD, 16 * ct, kk), au);
+    }
+    put_tile(sW, LD, r0, 16 * ct, aw);
+    put_tile(sU, LD, r0, 16 * ct, au);
+  }
+  for (int ct = ch; ct < 4; ct += 2) {
+    f32x4 acc = zero4();
+    if (ct <= rb)
+      for (int kk = 0; kk < D; kk += 32) acc = mma32(frow(sQ, LD, r0, kk), frow(sK, LD, 16 * ct, kk), acc);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) acc[r] = 16 * ct + tile_col() <= r0 + tile_row(r) ? acc[r] : 0.f;
+    put_tile(sP, L6, r0, 16 * ct, acc);
+  }
+  __syncthreads();
+  // Z = P^T dO over V (P^T upper triangular)
+  for (int ct = ch; ct < NT; ct += 2) {
+    f32x4 acc = zero4();
+    for (int kk = klo; kk < kC; kk += 32) acc = mma32(fcol(sP, L6, r0, kk), fcol(sO, LD, 16 * ct, kk), acc);
+    put_tile(sZ, LD, r0, 16 * ct, acc);
+  }
+  __syncthreads();
+  // the chains' operands, tile (rt, ct) of each [D x D] product: Y = Q^T dO - W^T Z and B = K^T U
+  // in accumulator order, N = -K^T W into NR and N^T = -W^T K into NF (A tile (ct, rt) of each)
+  float* gY = Ws<D>::Y(ws, chunk);
+  float* gB = Ws<D>::B(ws, chunk);
+  __bf16* gNF = reinterpret_cast<__bf16*>(Ws<D>::NF(ws, chunk));
+  __bf16* gNR = reinterpret_cast<__bf16*>(Ws<D>::NR(ws, chunk));
+  const int l = threadIdx.x & 63;
+  for (int tile = w; tile < NT * NT; tile += NTH / 64) {
+    const int rt = tile / NT, ct = tile - rt * NT;
+    f32x4 y = zero4(), bb = zero4(), kw = zero4(), wk = zero4();
+#pragma unroll
+    for (int kk = 0; kk < kC; kk += 32) {
+      const bf16x8 qa = fcol(sQ, LD, 16 * rt, kk), wa = fcol(sW, LD, 16 * rt, kk), ka = fcol(sK, LD, 16 * rt, kk);
+      const bf16x8 zb = fcol(sZ, LD, 16 * ct, kk), wb = fcol(sW, LD, 16 * ct, kk), kb = fcol(sK, LD, 16 * ct, kk);
+      y = mma32(qa, fcol(sO, LD, 16 * ct, kk), y);
+      y = mma32(wa, -zb, y);
+      bb = mma32(ka, fcol(sU, LD, 16 * ct, kk), bb);
+      kw = mma32(ka, wb, kw);
+      wk = mma32(wa, kb, wk);
+    }
+    *reinterpret_cast<f32x4*>(gY + accfrag<NT>(ct, rt, l)) = y;
+    *reinterpret_cast<f32x4*>(gB + accfrag<NT>(ct, rt, l)) = bb;
+    bf16x4 nr, nf;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      nr[r] = (T)(-kw[r]);
+      nf[r] = (T)(-wk[r]);
+    }
+    *reinterpret_cast<bf16x4*>(gNR + afrag<NT>(ct, rt, l)) = nr;
+    *reinterpret_cast<bf16x4*>(gNF + afrag<NT>(ct, rt, l)) = nf;
+  }
+}
+
 size_t workspace_floats(int B, int N, int H, int D) {
   const size_t nc = (size_t)(N + kC - 1) / kC;
   const size_t per = (size_t)kC * kC + 6 * (size_t)D * D;
@@ -1050,8 +1215,12 @@ void launch(const TIn* q, const TIn* k, const TIn* v, const TIn* beta, const flo
             float* ws, int B, int N, int H, hipStream_t stream) {
   const int NC = (N + kC - 1) / kC;
   const unsigned chunks = (unsigned)((size_t)B * H * NC), slices = (unsigned)((size_t)B * H * (D / 16));
-  hipLaunchKernelGGL((scan_bwd_prep_kernel<TIn, D>), dim3(chunks), dim3(kPrepThreads), 0, stream, q, k, v, beta, d_o, active, ws,
-                     N, H, NC);
+  if constexpr (sizeof(TIn) == 2 && D >= 32)
+    hipLaunchKernelGGL((scan_bwd_prep_bf16_kernel<D>), dim3(chunks), dim3(kPrepThreads), 0, stream, q, k, v, beta, d_o,
+                       active, ws, N, H, NC);
+  else
+    hipLaunchKernelGGL((scan_bwd_prep_kernel<TIn, D>), dim3(chunks), dim3(kPrepThreads), 0, stream, q, k, v, beta, d_o,
+                       active, ws, N, H, NC);
   hipLaunchKernelGGL((scan_bwd_chains_kernel<TIn, D>), dim3(2 * slices), dim3(64), 0, stream, state_in, d_state,
                      d_state_in, ws, NC, (int)slices);
   if constexpr (sizeof(TIn) == 2 && D >= 32)
