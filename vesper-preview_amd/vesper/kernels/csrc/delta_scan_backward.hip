@@ -220,8 +220,8 @@ struct AccRows {
 };
 
 // workspace layout, per (b, h, chunk), in floats: L [64][64]; NF, NR [D][D] (the chains' A
-// operands: bf16 on the bf16 entry, in the first half of each block, fp32 on the fp32 one); B, Y,
-// Hs, dHs [D][D] in accumulator order
+// operands); B, Y, Hs, dHs [D][D] in accumulator order. On the bf16 entry at head widths 32 and
+// 64, L, NF, NR, Hs and dHs hold bf16 (in the first half of their blocks).
 template <int D> struct Ws {
   static constexpr size_t kL = (size_t)kC * kC, kS = (size_t)D * D;
   static constexpr size_t kPer = kL + 6 * kS;
@@ -236,6 +236,7 @@ template <int D> struct Ws {
 };
 
 typedef unsigned v4u32_t __attribute__((ext_vector_type(4)));
+typedef unsigned v2u32_t __attribute__((ext_vector_type(2)));
 
 // Chain operand orders (16x16x16 bf16 MFMA, or four 16x16x4 fp32 ones in k order 4 g + u: lane
 // (i, g) of an A fragment holds row i, k = 4 g .. 4 g + 3; an accumulator's lane (j, g) holds rows
@@ -502,15 +503,19 @@ __global__ __launch_bounds__(64) void scan_bwd_chains_kernel(const float* __rest
     f32x4 xf[NT];
 #pragma unroll
     for (int kt = 0; kt < NT; ++kt) {
-#if defined(__HIP_DEVICE_COMPILE__)
-      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(v4u32_t, acc[kt]), rs,
-                                             rec_off + 4 * (unsigned)accfrag<NT>(s, kt, l), co, 0);
-#endif
       xf[kt] = acc[kt];
       bf16x4 t;
 #pragma unroll
       for (int r = 0; r < 4; ++r) t[r] = (__bf16)acc[kt][r];
       xb[kt] = __builtin_bit_cast(s16x4_t, t);
+#if defined(__HIP_DEVICE_COMPILE__)
+      if constexpr (BF && D >= 32)  // the record as the bf16 chunk kernel multiplies it
+        __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(v2u32_t, t), rs,
+                                              rec_off + 2 * (unsigned)accfrag<NT>(s, kt, l), co, 0);
+      else
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(v4u32_t, acc[kt]), rs,
+                                               rec_off + 4 * (unsigned)accfrag<NT>(s, kt, l), co, 0);
+#endif
     }
 #pragma unroll
     for (int rt = 0; rt < NT; ++rt) {
@@ -832,15 +837,15 @@ struct ChunkRows16 {
   }
 };
 
-// a [D][D] fp32 record in accumulator order into LDS [D][ld] bf16, row-major
+// a [D][D] bf16 record in accumulator order into LDS [D][ld] bf16, row-major
 template <int D, int NTH>
 struct AccRows16 {
   static constexpr int NT = D / 16, kN = D * D / 4, kIt = (kN + NTH - 1) / NTH;
-  f32x4 raw[kIt];
-  __device__ __forceinline__ void fetch(const float* src) {
+  bf16x4 raw[kIt];
+  __device__ __forceinline__ void fetch(const __bf16* src) {
 #pragma unroll
     for (int it = 0; it < kIt; ++it)
-      raw[it] = *reinterpret_cast<const f32x4*>(src + 4 * min((int)threadIdx.x + NTH * it, kN - 1));
+      raw[it] = *reinterpret_cast<const bf16x4*>(src + 4 * min((int)threadIdx.x + NTH * it, kN - 1));
   }
   __device__ __forceinline__ void put(__bf16* dst, int ld) const {
 #pragma unroll
@@ -850,7 +855,7 @@ struct AccRows16 {
         const int lane = e & 63, st = e >> 6, sl = st / NT, rt = st - sl * NT;
         const int row = 16 * rt + 4 * (lane >> 4), col = 16 * sl + (lane & 15);
 #pragma unroll
-        for (int r = 0; r < 4; ++r) dst[(row + r) * ld + col] = (__bf16)raw[it][r];
+        for (int r = 0; r < 4; ++r) dst[(row + r) * ld + col] = raw[it][r];
       }
     }
   }
@@ -868,12 +873,11 @@ __global__ __launch_bounds__(kChunkThreads) void scan_bwd_chunk_bf16_kernel(
   using T = __bf16;
   constexpr int NT = D / 16;  // column tiles of a [64 x D] result
   constexpr int NTH = kChunkThreads;
-  constexpr int LD = D + 8, L6 = kC + 8, LF = kC + 4;  // pitches: [64][D] and [D][D], [64][64], fp32 [64][64]
+  constexpr int LD = D + 8, L6 = kC + 8;  // pitches: [64][D] and [D][D], [64][64]
   __shared__ __align__(16) T sQ[kC * LD], sK[kC * LD], sO[kC * LD], sR[kC * LD], sD[kC * LD], sDD[kC * LD],
       sDR[kC * LD];
   __shared__ __align__(16) T sH[D * LD], sG[D * LD];
   __shared__ __align__(16) T sT[kC * L6], sL[kC * L6], sP[kC * L6], sM[kC * L6];
-  __shared__ __align__(16) float sLf[kC * LF];
   __shared__ float sB[kC], sPart[4 * kC], sRow[2 * kC];
   T* sX1 = sT;   // X1 = L^T dL once T is done with
   T* sS2 = sP;   // S2 = tril(dO Delta^T) once P is done with
@@ -888,15 +892,15 @@ __global__ __launch_bounds__(kChunkThreads) void scan_bwd_chunk_bf16_kernel(
   {
     ChunkRows16<D, NTH> rq, rk, ro, rv;
     AccRows16<D, NTH> mh, mg;
-    MatRows<kC, kC, NTH> ml;
     ChunkBeta<T> rbeta;
+    const T* gL = reinterpret_cast<const T*>(Ws<D>::L(const_cast<float*>(ws), chunk));
+    const bf16x8 lraw = *reinterpret_cast<const bf16x8*>(gL + 8 * threadIdx.x);  // [64][64]: 8 a thread
     rq.fetch(q, b, h, t0, N, H);
     rk.fetch(k, b, h, t0, N, H);
     ro.fetch(d_o, b, h, t0, N, H, active);
     rv.fetch(v, b, h, t0, N, H);
-    mh.fetch(Ws<D>::Hs(const_cast<float*>(ws), chunk));
-    mg.fetch(Ws<D>::dHs(const_cast<float*>(ws), chunk));
-    ml.fetch(Ws<D>::L(const_cast<float*>(ws), chunk));
+    mh.fetch(reinterpret_cast<const T*>(Ws<D>::Hs(const_cast<float*>(ws), chunk)));
+    mg.fetch(reinterpret_cast<const T*>(Ws<D>::dHs(const_cast<float*>(ws), chunk)));
     rbeta.fetch(beta, b, h, t0, N, H);
     rq.put(sQ, LD);
     rk.put(sK, LD);
@@ -904,19 +908,18 @@ __global__ __launch_bounds__(kChunkThreads) void scan_bwd_chunk_bf16_kernel(
     rv.put(sR, LD);
     mh.put(sH, LD);
     mg.put(sG, LD);
-    ml.put(sLf, LF);
+    *reinterpret_cast<bf16x8*>(sL + (threadIdx.x >> 3) * L6 + 8 * (threadIdx.x & 7)) = lraw;
     rbeta.put(sB, t0, N);
   }
+  static_assert(kChunkThreads * 8 == kC * kC, "one 16-byte piece of L a thread");
   __syncthreads();
-  // L and T = L diag(beta) in bf16
-  for (int e = threadIdx.x; e < kC * kC / 4; e += NTH) {
-    const int i = e / (kC / 4), j = 4 * (e % (kC / 4));
-    const f32x4 x = *reinterpret_cast<const f32x4*>(sLf + i * LF + j);
+  // T = L diag(beta)
+  for (int e = threadIdx.x; e < kC * kC / 8; e += NTH) {
+    const int i = e / (kC / 8), j = 8 * (e % (kC / 8));
+    bf16x8 x = *reinterpret_cast<const bf16x8*>(sL + i * L6 + j);
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      sL[i * L6 + j + u] = (T)x[u];
-      sT[i * L6 + j + u] = (T)(x[u] * sB[j + u]);
-    }
+    for (int u = 0; u < 8; ++u) x[u] = (T)((float)x[u] * sB[j + u]);
+    *reinterpret_cast<bf16x8*>(sT + i * L6 + j) = x;
   }
   // R = V - K H in place (each lane reads only its own V entries)
   for (int ct = ch; ct < NT; ct += 2) {
@@ -969,7 +972,7 @@ __global__ __launch_bounds__(kChunkThreads) void scan_bwd_chunk_bf16_kernel(
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int i = r0 + tile_row(r);
-      part += dt[r] * sLf[i * LF + j];
+      part += dt[r] * (float)sL[i * L6 + j];
       s2[r] = j <= i ? s2[r] : 0.f;
       dt[r] = j <= i ? dt[r] * sB[j] : 0.f;
     }
@@ -1131,15 +1134,18 @@ __global__ __launch_bounds__(kPrepThreads) void scan_bwd_prep_bf16_kernel(
     }
     __syncthreads();
   }
-  // L into the workspace; T = L diag(beta) in bf16 over A
-  float* gL = Ws<D>::L(ws, chunk);
+  // L into the workspace in bf16 (as the chunk kernel multiplies it); T = L diag(beta) in bf16 over A
+  T* gL = reinterpret_cast<T*>(Ws<D>::L(ws, chunk));
   for (int e = threadIdx.x; e < kC * kC / 4; e += NTH) {
     const int i = e / (kC / 4), j = 4 * (e % (kC / 4));
     const f32x4 x = *reinterpret_cast<const f32x4*>(sL + i * PF + j);
-    *reinterpret_cast<f32x4*>(gL + 4 * e) = x;
-    bf16x4 t;
+    bf16x4 lb, t;
 #pragma unroll
-    for (int u = 0; u < 4; ++u) t[u] = (T)(x[u] * sB[j + u]);
+    for (int u = 0; u < 4; ++u) {
+      lb[u] = (T)x[u];
+      t[u] = (T)((float)lb[u] * sB[j + u]);
+    }
+    *reinterpret_cast<bf16x4*>(gL + 4 * e) = lb;
     *reinterpret_cast<bf16x4*>(sT + i * L6 + j) = t;
   }
   __syncthreads();
