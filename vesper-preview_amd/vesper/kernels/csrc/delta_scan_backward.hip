@@ -869,7 +869,7 @@ __global__ __launch_bounds__(kChunkThreads) void scan_bwd_chunk_bf16_kernel(
     const __bf16* __restrict__ q, const __bf16* __restrict__ k, const __bf16* __restrict__ v,
     const __bf16* __restrict__ beta, const __bf16* __restrict__ d_o, const uint8_t* __restrict__ active,
     const float* __restrict__ ws, __bf16* __restrict__ dq, __bf16* __restrict__ dk, __bf16* __restrict__ dv,
-    __bf16* __restrict__ dbeta, int N, int H, int NC) {
+    __bf16* __restrict__ dbeta, int N, int H, int NC, int total) {
   using T = __bf16;
   constexpr int NT = D / 16;  // column tiles of a [64 x D] result
   constexpr int NTH = kChunkThreads;
@@ -882,26 +882,35 @@ __global__ __launch_bounds__(kChunkThreads) void scan_bwd_chunk_bf16_kernel(
   T* sX1 = sT;   // X1 = L^T dL once T is done with
   T* sS2 = sP;   // S2 = tril(dO Delta^T) once P is done with
   T* sDL = sM;   // dL, then M = diag(beta) dA
-  const int c = blockIdx.x % NC, bh = blockIdx.x / NC;
-  const int b = bh / H, h = bh - b * H;
-  const int t0 = c * kC;
-  const size_t chunk = blockIdx.x;
   const int w = threadIdx.x >> 6, ch = w >> 2, rb = ch == 0 ? w : 7 - w, r0 = 16 * rb;
   const int khi = (rb + 2) / 2 * 32;  // k range of a lower triangular A operand for row block rb
   const int klo = rb / 2 * 32;        // and of an upper triangular one
-  {
-    ChunkRows16<D, NTH> rq, rk, ro, rv;
-    AccRows16<D, NTH> mh, mg;
-    ChunkBeta<T> rbeta;
-    const T* gL = reinterpret_cast<const T*>(Ws<D>::L(const_cast<float*>(ws), chunk));
-    const bf16x8 lraw = *reinterpret_cast<const bf16x8*>(gL + 8 * threadIdx.x);  // [64][64]: 8 a thread
+  // A workgroup walks chunks blockIdx.x, + gridDim.x, ...: the next chunk's operands are loaded
+  // into registers while the current one is computed.
+  ChunkRows16<D, NTH> rq, rk, ro, rv;
+  AccRows16<D, NTH> mh, mg;
+  ChunkBeta<T> rbeta;
+  bf16x8 lraw;
+  auto fetch = [&](int cid) {
+    const int c = cid % NC, bh = cid / NC;
+    const int b = bh / H, h = bh - b * H;
+    const int t0 = c * kC;
+    const T* gL = reinterpret_cast<const T*>(Ws<D>::L(const_cast<float*>(ws), cid));
+    lraw = *reinterpret_cast<const bf16x8*>(gL + 8 * threadIdx.x);  // [64][64]: 8 a thread
     rq.fetch(q, b, h, t0, N, H);
     rk.fetch(k, b, h, t0, N, H);
     ro.fetch(d_o, b, h, t0, N, H, active);
     rv.fetch(v, b, h, t0, N, H);
-    mh.fetch(reinterpret_cast<const T*>(Ws<D>::Hs(const_cast<float*>(ws), chunk)));
-    mg.fetch(reinterpret_cast<const T*>(Ws<D>::dHs(const_cast<float*>(ws), chunk)));
+    mh.fetch(reinterpret_cast<const T*>(Ws<D>::Hs(const_cast<float*>(ws), cid)));
+    mg.fetch(reinterpret_cast<const T*>(Ws<D>::dHs(const_cast<float*>(ws), cid)));
     rbeta.fetch(beta, b, h, t0, N, H);
+  };
+  fetch(blockIdx.x);
+  for (int cid = blockIdx.x; cid < total; cid += gridDim.x) {
+  const int c = cid % NC, bh = cid / NC;
+  const int b = bh / H, h = bh - b * H;
+  const int t0 = c * kC;
+  {
     rq.put(sQ, LD);
     rk.put(sK, LD);
     ro.put(sO, LD);
@@ -913,6 +922,7 @@ __global__ __launch_bounds__(kChunkThreads) void scan_bwd_chunk_bf16_kernel(
   }
   static_assert(kChunkThreads * 8 == kC * kC, "one 16-byte piece of L a thread");
   __syncthreads();
+  fetch(min(cid + (int)gridDim.x, total - 1));  // (the last chunk again past the end: no branch)
   // T = L diag(beta)
   for (int e = threadIdx.x; e < kC * kC / 8; e += NTH) {
     const int i = e / (kC / 8), j = 8 * (e % (kC / 8));
@@ -1038,6 +1048,8 @@ __global__ __launch_bounds__(kChunkThreads) void scan_bwd_chunk_bf16_kernel(
   if (i < kC && t0 + i < N) {
     const float x = ((sPart[i] + sPart[kC + i]) + (sPart[2 * kC + i] + sPart[3 * kC + i])) + (sRow[i] + sRow[kC + i]);
     dbeta[((size_t)b * N + t0 + i) * H + h] = (T)x;
+  }
+  __syncthreads();  // every read of this chunk's LDS is done before the next one is put
   }
 }
 
@@ -1215,6 +1227,16 @@ size_t workspace_floats(int B, int N, int H, int D) {
   return (size_t)B * H * nc * per;
 }
 
+// workgroups that stay resident at `per_cu` a CU on the current device
+unsigned persistent_blocks(int per_cu) {
+  static int cus[64] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256u * per_cu;
+  if (cus[dev] == 0 && hipDeviceGetAttribute(&cus[dev], hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+    cus[dev] = 256;
+  return (unsigned)cus[dev] * per_cu;
+}
+
 template <typename TIn, int D>
 void launch(const TIn* q, const TIn* k, const TIn* v, const TIn* beta, const float* state_in, const TIn* d_o,
             const float* d_state, const uint8_t* active, TIn* dq, TIn* dk, TIn* dv, TIn* dbeta, float* d_state_in,
@@ -1230,8 +1252,9 @@ void launch(const TIn* q, const TIn* k, const TIn* v, const TIn* beta, const flo
   hipLaunchKernelGGL((scan_bwd_chains_kernel<TIn, D>), dim3(2 * slices), dim3(64), 0, stream, state_in, d_state,
                      d_state_in, ws, NC, (int)slices);
   if constexpr (sizeof(TIn) == 2 && D >= 32)
-    hipLaunchKernelGGL((scan_bwd_chunk_bf16_kernel<D>), dim3(chunks), dim3(kChunkThreads), 0, stream, q, k, v, beta, d_o,
-                       active, ws, dq, dk, dv, dbeta, N, H, NC);
+    hipLaunchKernelGGL((scan_bwd_chunk_bf16_kernel<D>), dim3(min(chunks, persistent_blocks(1))),
+                       dim3(kChunkThreads), 0, stream, q, k, v, beta, d_o, active, ws, dq, dk, dv, dbeta, N, H, NC,
+                       (int)chunks);
   else
     hipLaunchKernelGGL((scan_bwd_chunk_kernel<TIn, D>), dim3(chunks), dim3(kChunkThreads), 0, stream, q, k, v, beta, d_o,
                        active, ws, dq, dk, dv, dbeta, N, H, NC);
