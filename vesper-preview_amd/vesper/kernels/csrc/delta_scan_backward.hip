@@ -862,8 +862,9 @@ struct AccRows16 {
 };
 
 // Eight waves: wave w owns row block rb of every [64 x .] result (rb and 3 - rb on one SIMD) and
-// every other column tile from ch = w / 4. Triangular factors bound each product's k range (in
-// steps of 32) and leave tiles above the diagonal zero.
+// every other column tile from ch = w / 4. Products run over their full k range, unrolled: the
+// triangular factors hold exact zeros where they vanish, and straight-line code lets the compiler
+// issue a stage's LDS reads ahead of its MFMAs.
 template <int D>
 __global__ __launch_bounds__(kChunkThreads) void scan_bwd_chunk_bf16_kernel(
     const __bf16* __restrict__ q, const __bf16* __restrict__ k, const __bf16* __restrict__ v,
@@ -883,8 +884,6 @@ __global__ __launch_bounds__(kChunkThreads) void scan_bwd_chunk_bf16_kernel(
   T* sS2 = sP;   // S2 = tril(dO Delta^T) once P is done with
   T* sDL = sM;   // dL, then M = diag(beta) dA
   const int w = threadIdx.x >> 6, ch = w >> 2, rb = ch == 0 ? w : 7 - w, r0 = 16 * rb;
-  const int khi = (rb + 2) / 2 * 32;  // k range of a lower triangular A operand for row block rb
-  const int klo = rb / 2 * 32;        // and of an upper triangular one
   // A workgroup walks chunks blockIdx.x, + gridDim.x, ...: the next chunk's operands are loaded
   // into registers while the current one is computed.
   ChunkRows16<D, NTH> rq, rk, ro, rv;
@@ -932,8 +931,11 @@ __global__ __launch_bounds__(kChunkThreads) void scan_bwd_chunk_bf16_kernel(
     *reinterpret_cast<bf16x8*>(sT + i * L6 + j) = x;
   }
   // R = V - K H in place (each lane reads only its own V entries)
-  for (int ct = ch; ct < NT; ct += 2) {
+  #pragma unroll
+  for (int u_ = 0; u_ < NT / 2; ++u_) {
+    const int ct = ch + 2 * u_;
     f32x4 acc = zero4();
+    #pragma unroll
     for (int kk = 0; kk < D; kk += 32) acc = mma32(frow(sK, LD, r0, kk), fcol(sH, LD, 16 * ct, kk), acc);
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
@@ -942,9 +944,12 @@ __global__ __launch_bounds__(kChunkThreads) void scan_bwd_chunk_bf16_kernel(
     }
   }
   // P = tril(Q K^T), diagonal included
-  for (int ct = ch; ct < 4; ct += 2) {
+  #pragma unroll
+  for (int u_ = 0; u_ < 2; ++u_) {
+    const int ct = ch + 2 * u_;
     f32x4 acc = zero4();
     if (ct <= rb)
+      #pragma unroll
       for (int kk = 0; kk < D; kk += 32) acc = mma32(frow(sQ, LD, r0, kk), frow(sK, LD, 16 * ct, kk), acc);
 #pragma unroll
     for (int r = 0; r < 4; ++r) acc[r] = 16 * ct + tile_col() <= r0 + tile_row(r) ? acc[r] : 0.f;
@@ -952,26 +957,37 @@ __global__ __launch_bounds__(kChunkThreads) void scan_bwd_chunk_bf16_kernel(
   }
   __syncthreads();
   // Delta = T R; dDelta = K G + P^T dO
-  for (int ct = ch; ct < NT; ct += 2) {
+  #pragma unroll
+  for (int u_ = 0; u_ < NT / 2; ++u_) {
+    const int ct = ch + 2 * u_;
     f32x4 d = zero4(), dd = zero4();
-    for (int kk = 0; kk < khi; kk += 32) d = mma32(frow(sT, L6, r0, kk), fcol(sR, LD, 16 * ct, kk), d);
+    #pragma unroll
+    for (int kk = 0; kk < kC; kk += 32) d = mma32(frow(sT, L6, r0, kk), fcol(sR, LD, 16 * ct, kk), d);
+    #pragma unroll
     for (int kk = 0; kk < D; kk += 32) dd = mma32(frow(sK, LD, r0, kk), fcol(sG, LD, 16 * ct, kk), dd);
-    for (int kk = klo; kk < kC; kk += 32) dd = mma32(fcol(sP, L6, r0, kk), fcol(sO, LD, 16 * ct, kk), dd);
+    #pragma unroll
+    for (int kk = 0; kk < kC; kk += 32) dd = mma32(fcol(sP, L6, r0, kk), fcol(sO, LD, 16 * ct, kk), dd);
     put_tile(sD, LD, r0, 16 * ct, d);
     put_tile(sDD, LD, r0, 16 * ct, dd);
   }
   __syncthreads();
   // dR = T^T dDelta (= dV; kept negated for dK); S2 = tril(dO Delta^T) over P; dT = dDelta R^T:
   // dbeta_j gets sum_i dT_ij L_ij (column sums per row block into sPart), dL = tril(dT) diag(beta)
-  for (int ct = ch; ct < NT; ct += 2) {
+  #pragma unroll
+  for (int u_ = 0; u_ < NT / 2; ++u_) {
+    const int ct = ch + 2 * u_;
     f32x4 acc = zero4();
-    for (int kk = klo; kk < kC; kk += 32) acc = mma32(fcol(sT, L6, r0, kk), fcol(sDD, LD, 16 * ct, kk), acc);
+    #pragma unroll
+    for (int kk = 0; kk < kC; kk += 32) acc = mma32(fcol(sT, L6, r0, kk), fcol(sDD, LD, 16 * ct, kk), acc);
     store_rows<T, D>(dv, b, h, t0, N, H, r0, 16 * ct, acc);
     put_tile(sDR, LD, r0, 16 * ct, -acc);
   }
-  for (int ct = ch; ct < 4; ct += 2) {
+  #pragma unroll
+  for (int u_ = 0; u_ < 2; ++u_) {
+    const int ct = ch + 2 * u_;
     f32x4 s2 = zero4(), dt = zero4();
     if (ct <= rb) {
+      #pragma unroll
       for (int kk = 0; kk < D; kk += 32) {
         s2 = mma32(frow(sO, LD, r0, kk), frow(sD, LD, 16 * ct, kk), s2);
         dt = mma32(frow(sDD, LD, r0, kk), frow(sR, LD, 16 * ct, kk), dt);
@@ -993,15 +1009,22 @@ __global__ __launch_bounds__(kChunkThreads) void scan_bwd_chunk_bf16_kernel(
   }
   __syncthreads();
   // dQ = dO H^T + S2 K; X1 = L^T dL over T (L^T upper, dL lower: k from max(rb, ct))
-  for (int ct = ch; ct < NT; ct += 2) {
+  #pragma unroll
+  for (int u_ = 0; u_ < NT / 2; ++u_) {
+    const int ct = ch + 2 * u_;
     f32x4 acc = zero4();
+    #pragma unroll
     for (int kk = 0; kk < D; kk += 32) acc = mma32(frow(sO, LD, r0, kk), frow(sH, LD, 16 * ct, kk), acc);
-    for (int kk = 0; kk < khi; kk += 32) acc = mma32(frow(sS2, L6, r0, kk), fcol(sK, LD, 16 * ct, kk), acc);
+    #pragma unroll
+    for (int kk = 0; kk < kC; kk += 32) acc = mma32(frow(sS2, L6, r0, kk), fcol(sK, LD, 16 * ct, kk), acc);
     store_rows<T, D>(dq, b, h, t0, N, H, r0, 16 * ct, acc);
   }
-  for (int ct = ch; ct < 4; ct += 2) {  // (T was last read before the previous barrier)
+  #pragma unroll
+  for (int u_ = 0; u_ < 2; ++u_) {  // (T was last read before the previous barrier)
+    const int ct = ch + 2 * u_;
     f32x4 x1 = zero4();
-    for (int kk = max(rb, ct) / 2 * 32; kk < kC; kk += 32)
+    #pragma unroll
+    for (int kk = 0; kk < kC; kk += 32)
       x1 = mma32(fcol(sL, L6, r0, kk), fcol(sDL, L6, 16 * ct, kk), x1);
     put_tile(sX1, L6, r0, 16 * ct, x1);
   }
@@ -1009,10 +1032,14 @@ __global__ __launch_bounds__(kChunkThreads) void scan_bwd_chunk_bf16_kernel(
   // dA = -tril(X1 L^T, -1) (L^T[k][j] nonzero for k <= j); dbeta_i gets sum_m dA_im (k_i . k_m)
   // (row sums per column half into sRow); M = diag(beta) dA over dL
   float rows[4] = {0.f, 0.f, 0.f, 0.f};
-  for (int ct = ch; ct < 4; ct += 2) {
+  #pragma unroll
+  for (int u_ = 0; u_ < 2; ++u_) {
+    const int ct = ch + 2 * u_;
     f32x4 da = zero4(), gk = zero4();
     if (ct <= rb) {
-      for (int kk = 0; kk < (ct + 2) / 2 * 32; kk += 32) da = mma32(frow(sX1, L6, r0, kk), frow(sL, L6, 16 * ct, kk), da);
+      #pragma unroll
+      for (int kk = 0; kk < kC; kk += 32) da = mma32(frow(sX1, L6, r0, kk), frow(sL, L6, 16 * ct, kk), da);
+      #pragma unroll
       for (int kk = 0; kk < D; kk += 32) gk = mma32(frow(sK, LD, r0, kk), frow(sK, LD, 16 * ct, kk), gk);
     }
 #pragma unroll
@@ -1031,17 +1058,22 @@ __global__ __launch_bounds__(kChunkThreads) void scan_bwd_chunk_bf16_kernel(
   }
   __syncthreads();
   // dK = Delta G^T + S2^T Q - dR H^T + M K + M^T K
-  for (int ct = ch; ct < NT; ct += 2) {
+  #pragma unroll
+  for (int u_ = 0; u_ < NT / 2; ++u_) {
+    const int ct = ch + 2 * u_;
     f32x4 acc = zero4();
+    #pragma unroll
     for (int kk = 0; kk < D; kk += 32) {
       acc = mma32(frow(sD, LD, r0, kk), frow(sG, LD, 16 * ct, kk), acc);
       acc = mma32(frow(sDR, LD, r0, kk), frow(sH, LD, 16 * ct, kk), acc);
     }
-    for (int kk = klo; kk < kC; kk += 32) {
+    #pragma unroll
+    for (int kk = 0; kk < kC; kk += 32) {
       acc = mma32(fcol(sS2, L6, r0, kk), fcol(sQ, LD, 16 * ct, kk), acc);
       acc = mma32(fcol(sM, L6, r0, kk), fcol(sK, LD, 16 * ct, kk), acc);
     }
-    for (int kk = 0; kk < khi; kk += 32) acc = mma32(frow(sM, L6, r0, kk), fcol(sK, LD, 16 * ct, kk), acc);
+    #pragma unroll
+    for (int kk = 0; kk < kC; kk += 32) acc = mma32(frow(sM, L6, r0, kk), fcol(sK, LD, 16 * ct, kk), acc);
     store_rows<T, D>(dk, b, h, t0, N, H, r0, 16 * ct, acc);
   }
   const int i = threadIdx.x;
@@ -1079,7 +1111,6 @@ __global__ __launch_bounds__(kPrepThreads) void scan_bwd_prep_bf16_kernel(
   const int t0 = c * kC;
   const size_t chunk = blockIdx.x;
   const int w = threadIdx.x >> 6, ch = w >> 2, rb = ch == 0 ? w : 7 - w, r0 = 16 * rb;
-  const int khi = (rb + 2) / 2 * 32, klo = rb / 2 * 32;
   {
     ChunkRows16<D, NTH> rq, rk, rv, ro;
     ChunkBeta<T> rbeta;
@@ -1096,9 +1127,12 @@ __global__ __launch_bounds__(kPrepThreads) void scan_bwd_prep_bf16_kernel(
   }
   __syncthreads();
   // A = tril(diag(beta) K K^T, -1) in fp32
-  for (int ct = ch; ct < 4; ct += 2) {
+  #pragma unroll
+  for (int u_ = 0; u_ < 2; ++u_) {
+    const int ct = ch + 2 * u_;
     f32x4 acc = zero4();
     if (ct <= rb)
+      #pragma unroll
       for (int kk = 0; kk < D; kk += 32) acc = mma32(frow(sK, LD, r0, kk), frow(sK, LD, 16 * ct, kk), acc);
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
@@ -1129,10 +1163,12 @@ __global__ __launch_bounds__(kPrepThreads) void scan_bwd_prep_bf16_kernel(
     for (int i = 0; i < 16; ++i) sL[(16 * blk + i) * PF + 16 * blk + col] = x[i];
   }
   __syncthreads();
+  #pragma unroll
   for (int lev = 1; lev < 4; ++lev) {
     const int i = w + lev, j = w;
     if (i < 4) {
       f32x4 y = zero4();
+      #pragma unroll
       for (int m = j; m < i; ++m)
         y = mm16<false, false>(sA + 16 * i * PF + 16 * m, PF, sL + 16 * m * PF + 16 * j, PF, 16, y);
       float* dst = sL + 16 * i * PF + 16 * j;
@@ -1162,9 +1198,12 @@ __global__ __launch_bounds__(kPrepThreads) void scan_bwd_prep_bf16_kernel(
   }
   __syncthreads();
   // W = T K and U = T V over L; P = tril(Q K^T) beside T
-  for (int ct = ch; ct < NT; ct += 2) {
+  #pragma unroll
+  for (int u_ = 0; u_ < NT / 2; ++u_) {
+    const int ct = ch + 2 * u_;
     f32x4 aw = zero4(), au = zero4();
-    for (int kk = 0; kk < khi; kk += 32) {
+    #pragma unroll
+    for (int kk = 0; kk < kC; kk += 32) {
       const bf16x8 a = frow(sT, L6, r0, kk);
       aw = mma32(a, fcol(sK, LD, 16 * ct, kk), aw);
       au = mma32(a, fcol(sV, LD, 16 * ct, kk), au);
@@ -1172,9 +1211,12 @@ __global__ __launch_bounds__(kPrepThreads) void scan_bwd_prep_bf16_kernel(
     put_tile(sW, LD, r0, 16 * ct, aw);
     put_tile(sU, LD, r0, 16 * ct, au);
   }
-  for (int ct = ch; ct < 4; ct += 2) {
+  #pragma unroll
+  for (int u_ = 0; u_ < 2; ++u_) {
+    const int ct = ch + 2 * u_;
     f32x4 acc = zero4();
     if (ct <= rb)
+      #pragma unroll
       for (int kk = 0; kk < D; kk += 32) acc = mma32(frow(sQ, LD, r0, kk), frow(sK, LD, 16 * ct, kk), acc);
 #pragma unroll
     for (int r = 0; r < 4; ++r) acc[r] = 16 * ct + tile_col() <= r0 + tile_row(r) ? acc[r] : 0.f;
@@ -1182,9 +1224,12 @@ __global__ __launch_bounds__(kPrepThreads) void scan_bwd_prep_bf16_kernel(
   }
   __syncthreads();
   // Z = P^T dO over V (P^T upper triangular)
-  for (int ct = ch; ct < NT; ct += 2) {
+  #pragma unroll
+  for (int u_ = 0; u_ < NT / 2; ++u_) {
+    const int ct = ch + 2 * u_;
     f32x4 acc = zero4();
-    for (int kk = klo; kk < kC; kk += 32) acc = mma32(fcol(sP, L6, r0, kk), fcol(sO, LD, 16 * ct, kk), acc);
+    #pragma unroll
+    for (int kk = 0; kk < kC; kk += 32) acc = mma32(fcol(sP, L6, r0, kk), fcol(sO, LD, 16 * ct, kk), acc);
     put_tile(sZ, LD, r0, 16 * ct, acc);
   }
   __syncthreads();
@@ -1195,6 +1240,7 @@ __global__ __launch_bounds__(kPrepThreads) void scan_bwd_prep_bf16_kernel(
   __bf16* gNF = reinterpret_cast<__bf16*>(Ws<D>::NF(ws, chunk));
   __bf16* gNR = reinterpret_cast<__bf16*>(Ws<D>::NR(ws, chunk));
   const int l = threadIdx.x & 63;
+  #pragma unroll
   for (int tile = w; tile < NT * NT; tile += NTH / 64) {
     const int rt = tile / NT, ct = tile - rt * NT;
     f32x4 y = zero4(), bb = zero4(), kw = zero4(), wk = zero4();
