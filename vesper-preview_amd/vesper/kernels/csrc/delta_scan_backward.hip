@@ -220,8 +220,8 @@ struct AccRows {
 };
 
 // workspace layout, per (b, h, chunk), in floats: L [64][64]; NF, NR [D][D] (the chains' A
-// operands); B, Y, Hs, dHs [D][D] in accumulator order. On the bf16 entry at head widths 32 and
-// 64, L, NF, NR, Hs and dHs hold bf16 (in the first half of their blocks).
+// operands); B, Y, Hs, dHs [D][D] in accumulator order. On the bf16 entry NF, NR, B and Y hold
+// bf16, and so do L, Hs and dHs at head widths 32 and 64 (in the first half of their blocks).
 template <int D> struct Ws {
   static constexpr size_t kL = (size_t)kC * kC, kS = (size_t)D * D;
   static constexpr size_t kPer = kL + 6 * kS;
@@ -387,18 +387,22 @@ __global__ __launch_bounds__(kPrepThreads) void scan_bwd_prep_kernel(const TIn* 
     const f32x4 ku = mm16<true, false, BF>(sK + 16 * rt, PD, sU + 16 * ct, PD, kC, zero4());
     const f32x4 kw = mm16<true, false, BF>(sK + 16 * rt, PD, sW + 16 * ct, PD, kC, zero4());
     const f32x4 wk = mm16<true, false, BF>(sW + 16 * rt, PD, sK + 16 * ct, PD, kC, zero4());
-    *reinterpret_cast<f32x4*>(gY + accfrag<NT>(ct, rt, l)) = qo - wz;
-    *reinterpret_cast<f32x4*>(gB + accfrag<NT>(ct, rt, l)) = ku;
     if constexpr (BF) {
-      bf16x4 nr, nf;
+      bf16x4 nr, nf, yb, bb;
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         nr[r] = (__bf16)(-kw[r]);
         nf[r] = (__bf16)(-wk[r]);
+        yb[r] = (__bf16)(qo[r] - wz[r]);
+        bb[r] = (__bf16)ku[r];
       }
+      *reinterpret_cast<bf16x4*>(reinterpret_cast<__bf16*>(gY) + accfrag<NT>(ct, rt, l)) = yb;
+      *reinterpret_cast<bf16x4*>(reinterpret_cast<__bf16*>(gB) + accfrag<NT>(ct, rt, l)) = bb;
       *reinterpret_cast<bf16x4*>(reinterpret_cast<__bf16*>(gNR) + afrag<NT>(ct, rt, l)) = nr;
       *reinterpret_cast<bf16x4*>(reinterpret_cast<__bf16*>(gNF) + afrag<NT>(ct, rt, l)) = nf;
     } else {
+      *reinterpret_cast<f32x4*>(gY + accfrag<NT>(ct, rt, l)) = qo - wz;
+      *reinterpret_cast<f32x4*>(gB + accfrag<NT>(ct, rt, l)) = ku;
       *reinterpret_cast<f32x4*>(gNR + afrag<NT>(ct, rt, l)) = -kw;
       *reinterpret_cast<f32x4*>(gNF + afrag<NT>(ct, rt, l)) = -wk;
     }
@@ -422,8 +426,18 @@ struct ChainShape {
 template <int NT, bool BF>
 struct ChainOps {
   static constexpr int kA = BF ? 2 : 4;  // dwords per A tile and lane
-  uint32_t a[kA * NT * NT];  // A tile (rt, kt): a[kA (rt NT + kt)] .. + kA - 1, four bf16 or fp32
-  f32x4 add[NT];             // the added term's accumulator tiles
+  uint32_t a[kA * NT * NT];   // A tile (rt, kt): a[kA (rt NT + kt)] .. + kA - 1, four bf16 or fp32
+  uint32_t add[kA * NT];      // the added term's accumulator tiles, four bf16 or fp32 a tile
+  __device__ __forceinline__ f32x4 add_tile(int rt) const {
+    if constexpr (BF) {
+      const uint2 v = {add[2 * rt], add[2 * rt + 1]};
+      const bf16x4 x = __builtin_bit_cast(bf16x4, v);
+      return f32x4{(float)x[0], (float)x[1], (float)x[2], (float)x[3]};
+    } else {
+      const uint4 v = {add[4 * rt], add[4 * rt + 1], add[4 * rt + 2], add[4 * rt + 3]};
+      return __builtin_bit_cast(f32x4, v);
+    }
+  }
 };
 
 // A chain's loads and stores go through one buffer resource over its (b, h) chunks: the chunk's
@@ -458,8 +472,15 @@ __device__ __forceinline__ void load_chain_ops(ChainOps<D / 16, BF>& o, __amdgpu
   }
 #pragma unroll
   for (int rt = 0; rt < NT; ++rt) {
-    const auto v = __builtin_amdgcn_raw_buffer_load_b128(rs, add_off + 4 * (unsigned)accfrag<NT>(s, rt, l), chunk_off, 0);
-    o.add[rt] = __builtin_bit_cast(f32x4, v);
+    if constexpr (BF) {
+      const auto v = __builtin_amdgcn_raw_buffer_load_b64(rs, add_off + 2 * (unsigned)accfrag<NT>(s, rt, l), chunk_off, 0);
+      o.add[2 * rt] = v[0];
+      o.add[2 * rt + 1] = v[1];
+    } else {
+      const auto v = __builtin_amdgcn_raw_buffer_load_b128(rs, add_off + 4 * (unsigned)accfrag<NT>(s, rt, l), chunk_off, 0);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) o.add[4 * rt + e] = v[e];
+    }
   }
 #endif
 }
@@ -519,7 +540,7 @@ __global__ __launch_bounds__(64) void scan_bwd_chains_kernel(const float* __rest
     }
 #pragma unroll
     for (int rt = 0; rt < NT; ++rt) {
-      acc[rt] += cur.add[rt];
+      acc[rt] += cur.add_tile(rt);
 #pragma unroll
       for (int kt = 0; kt < NT; ++kt) {
         const uint32_t* a = cur.a + ChainOps<NT, BF>::kA * (rt * NT + kt);
@@ -1254,14 +1275,16 @@ __global__ __launch_bounds__(kPrepThreads) void scan_bwd_prep_bf16_kernel(
       kw = mma32(ka, wb, kw);
       wk = mma32(wa, kb, wk);
     }
-    *reinterpret_cast<f32x4*>(gY + accfrag<NT>(ct, rt, l)) = y;
-    *reinterpret_cast<f32x4*>(gB + accfrag<NT>(ct, rt, l)) = bb;
-    bf16x4 nr, nf;
+    bf16x4 nr, nf, yb, bbb;
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       nr[r] = (T)(-kw[r]);
       nf[r] = (T)(-wk[r]);
+      yb[r] = (T)y[r];
+      bbb[r] = (T)bb[r];
     }
+    *reinterpret_cast<bf16x4*>(reinterpret_cast<T*>(gY) + accfrag<NT>(ct, rt, l)) = yb;
+    *reinterpret_cast<bf16x4*>(reinterpret_cast<T*>(gB) + accfrag<NT>(ct, rt, l)) = bbb;
     *reinterpret_cast<bf16x4*>(gNR + afrag<NT>(ct, rt, l)) = nr;
     *reinterpret_cast<bf16x4*>(gNF + afrag<NT>(ct, rt, l)) = nf;
   }
