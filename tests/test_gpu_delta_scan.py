@@ -296,6 +296,16 @@ def test_every_gradient_matches_the_oracle(b, n, h, dk):
     _grad_check(delta_scan_fused, _bf16_inputs(b, n, h, dk), TOL)
 
 
+@pytest.mark.parametrize("dk", [32, 64])
+def test_bf16_gradients_over_several_chunks_with_an_active_mask(dk):
+    # five chunks (the last one partial), three heads: the chains' hand-over from chunk to chunk
+    # in both directions, at the widths of the bf16 tile kernels
+    from vesper.kernels.delta_scan import delta_scan_fused
+
+    act = torch.rand(2, 300, generator=torch.Generator().manual_seed(11)) < 0.7
+    _grad_check(delta_scan_fused, _bf16_inputs(2, 300, 3, dk, seed=dk), TOL, active=act)
+
+
 @pytest.mark.parametrize(("b", "n", "h", "dk"), SIZES[:4])
 def test_fp32_every_gradient_matches_the_oracle_to_float32(b, n, h, dk):
     from vesper.kernels.delta_scan import delta_scan_fused_fp32
