@@ -165,9 +165,12 @@ def test_refuses_what_the_contract_excludes():
                          torch.zeros(1, 1, 512, 512, device=GPU))
     with pytest.raises(ContractError, match="dtype"):
         delta_scan_fused_fp32(q, k, v, beta, h0)
-    with pytest.raises(ContractError, match="backward takes head widths"):
-        delta_scan_fused(q.new_zeros(1, 8, 1, 128).requires_grad_(), q.new_zeros(1, 8, 1, 128),
-                         q.new_zeros(1, 8, 1, 128), q.new_zeros(1, 8, 1), torch.zeros(1, 1, 128, 128, device=GPU))
+    with pytest.raises(ContractError, match="backward takes head widths up to 128"):
+        delta_scan_fused(q.new_zeros(1, 8, 1, 192).requires_grad_(), q.new_zeros(1, 8, 1, 192),
+                         q.new_zeros(1, 8, 1, 192), q.new_zeros(1, 8, 1), torch.zeros(1, 1, 192, 192, device=GPU))
+    f = torch.zeros(1, 8, 1, 128, device=GPU)
+    with pytest.raises(ContractError, match="backward takes head widths up to 64"):
+        delta_scan_fused_fp32(f.clone().requires_grad_(), f, f, f[..., 0], torch.zeros(1, 1, 128, 128, device=GPU))
 
 
 def test_active_mask_zeroes_outputs_and_keeps_every_write():
@@ -304,6 +307,25 @@ def test_bf16_gradients_over_several_chunks_with_an_active_mask(dk):
 
     act = torch.rand(2, 300, generator=torch.Generator().manual_seed(11)) < 0.7
     _grad_check(delta_scan_fused, _bf16_inputs(2, 300, 3, dk, seed=dk), TOL, active=act)
+
+
+def test_bf16_gradients_at_width_128_over_several_chunks_with_an_active_mask():
+    # width 128: the chunk kernel reads the states' fragments from the chains' records (both
+    # orientations) instead of LDS tiles
+    from vesper.kernels.delta_scan import delta_scan_fused
+
+    act = torch.rand(1, 200, generator=torch.Generator().manual_seed(12)) < 0.7
+    _grad_check(delta_scan_fused, _bf16_inputs(1, 200, 2, 128, seed=128), TOL, active=act)
+
+
+@pytest.mark.parametrize(("dk", "fp32"), [(48, False), (100, False), (24, True), (48, True)])
+def test_gradients_at_widths_the_kernels_take_zero_padded(dk, fp32):
+    # a width between the kernels' (16, 32, 64, 128 on the bf16 entry; up to 64 on the fp32 one)
+    # runs padded with zero features and value columns: the same outputs and gradients
+    from vesper.kernels.delta_scan import delta_scan_fused, delta_scan_fused_fp32
+
+    fn, make, tol = (delta_scan_fused_fp32, _fp32_inputs, TOL_FP32) if fp32 else (delta_scan_fused, _bf16_inputs, TOL)
+    _grad_check(fn, make(2, 130, 2, dk, seed=dk), tol)
 
 
 @pytest.mark.parametrize(("b", "n", "h", "dk"), SIZES[:4])

@@ -420,7 +420,7 @@ template <int D, bool BF>
 struct ChainShape {
   static constexpr int NT = D / 16;
   // chunks of operands in flight: as many as the registers hold without spills
-  static constexpr int kRing = BF ? (D >= 64 ? 6 : 12) : (D >= 64 ? 2 : (D >= 32 ? 8 : 12));
+  static constexpr int kRing = BF ? (D >= 128 ? 2 : (D >= 64 ? 6 : 12)) : (D >= 64 ? 2 : (D >= 32 ? 8 : 12));
 };
 
 template <int NT, bool BF>
@@ -492,6 +492,11 @@ __global__ __launch_bounds__(64) void scan_bwd_chains_kernel(const float* __rest
                                                              int NC, int S) {
   constexpr bool BF = sizeof(TIn) == 2;  // bf16 A operands and 16x16x16 bf16 MFMA; else fp32 ones
   constexpr int NT = ChainShape<D, BF>::NT, R = ChainShape<D, BF>::kRing;
+  // At D 128 the chunk kernel reads the records as MFMA fragments from global memory, in both
+  // orientations: each step also records its slice transposed (through a 16x16 LDS tile), in
+  // the second half of the record's block.
+  constexpr bool kRowRec = BF && D >= 128;
+  __shared__ __align__(16) __bf16 sTr[kRowRec ? NT * 16 * 16 : 1];
   constexpr unsigned kPerB = (unsigned)(Ws<D>::kPer * sizeof(float));  // bytes per chunk
   constexpr unsigned kLB = (unsigned)(Ws<D>::kL * sizeof(float)), kSB = (unsigned)(Ws<D>::kS * sizeof(float));
   const int lg = xcd_logical_block(blockIdx.x, gridDim.x);
@@ -537,6 +542,23 @@ __global__ __launch_bounds__(64) void scan_bwd_chains_kernel(const float* __rest
         __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(v4u32_t, acc[kt]), rs,
                                                rec_off + 4 * (unsigned)accfrag<NT>(s, kt, l), co, 0);
 #endif
+      if constexpr (kRowRec) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) sTr[kt * 256 + (4 * g + r) * 16 + j] = t[r];
+      }
+    }
+    if constexpr (kRowRec) {
+      // tile (kt, s) of the slice transposed: lane (j, g) takes row j, columns 4 g .. 4 g + 3
+      wave_sync_lds();
+#pragma unroll
+      for (int kt = 0; kt < NT; ++kt) {
+        const bf16x4 x = *reinterpret_cast<const bf16x4*>(sTr + kt * 256 + j * 16 + 4 * g);
+#if defined(__HIP_DEVICE_COMPILE__)
+        __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(v2u32_t, x), rs,
+                                              rec_off + kSB / 2 + 2 * (unsigned)accfrag<NT>(s, kt, l), co, 0);
+#endif
+      }
+      wave_sync_lds();
     }
 #pragma unroll
     for (int rt = 0; rt < NT; ++rt) {
@@ -809,6 +831,14 @@ __device__ __forceinline__ bf16x8 fcol(const __bf16* X, int ld, int c0, int k0) 
   const bf16x4 lo = read_tr16<bf16x4>(p), hi = read_tr16<bf16x4>(p + 4 * ld);
   return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
 }
+// the A operand in the k order of a pair of 16-row accumulator tiles (k0 + 4 g .. + 3, then
+// k0 + 16 + 4 g .. + 3): row r0 + lq of X by two 8-byte reads
+__device__ __forceinline__ bf16x8 frow2(const __bf16* X, int ld, int r0, int k0) {
+  const int l = threadIdx.x & 63, lq = l & 15, g = l >> 4;
+  const __bf16* p = X + (r0 + lq) * ld + k0 + 4 * g;
+  const bf16x4 lo = *reinterpret_cast<const bf16x4*>(p), hi = *reinterpret_cast<const bf16x4*>(p + 16);
+  return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+}
 __device__ __forceinline__ f32x4 mma32(bf16x8 a, bf16x8 b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
 }
@@ -896,9 +926,16 @@ __global__ __launch_bounds__(kChunkThreads) void scan_bwd_chunk_bf16_kernel(
   constexpr int NT = D / 16;  // column tiles of a [64 x D] result
   constexpr int NTH = kChunkThreads;
   constexpr int LD = D + 8, L6 = kC + 8;  // pitches: [64][D] and [D][D], [64][64]
-  __shared__ __align__(16) T sQ[kC * LD], sK[kC * LD], sO[kC * LD], sR[kC * LD], sD[kC * LD], sDD[kC * LD],
-      sDR[kC * LD];
-  __shared__ __align__(16) T sH[D * LD], sG[D * LD];
+  // Up to D 64 the states H and G are LDS tiles. At D 128 they would not fit: their fragments come
+  // from the chains' records in global memory (column order for H and G as B operands, the
+  // transposed records for H^T and G^T), whose k order within 32 is 4 g .. 4 g + 3 of each 16-row
+  // tile, so the A operands they meet are read in that order too (frow2); and -dR goes over R.
+  constexpr bool kHGinLDS = D <= 64;
+  __shared__ __align__(16) T sQ[kC * LD], sK[kC * LD], sO[kC * LD], sR[kC * LD], sD[kC * LD], sDD[kC * LD];
+  __shared__ __align__(16) T sDRx[kHGinLDS ? kC * LD : 1];
+  __shared__ __align__(16) T sH[kHGinLDS ? D * LD : 1], sG[kHGinLDS ? D * LD : 1];
+  T* sDR = kHGinLDS ? sDRx : sR;
+  constexpr int kU = kHGinLDS ? NT / 2 : 1;  // column tiles unrolled (D 128: one, for the registers)
   __shared__ __align__(16) T sT[kC * L6], sL[kC * L6], sP[kC * L6], sM[kC * L6];
   __shared__ float sB[kC], sPart[4 * kC], sRow[2 * kC];
   T* sX1 = sT;   // X1 = L^T dL once T is done with
@@ -908,7 +945,7 @@ __global__ __launch_bounds__(kChunkThreads) void scan_bwd_chunk_bf16_kernel(
   // A workgroup walks chunks blockIdx.x, + gridDim.x, ...: the next chunk's operands are loaded
   // into registers while the current one is computed.
   ChunkRows16<D, NTH> rq, rk, ro, rv;
-  AccRows16<D, NTH> mh, mg;
+  AccRows16<kHGinLDS ? D : 16, NTH> mh, mg;
   ChunkBeta<T> rbeta;
   bf16x8 lraw;
   auto fetch = [&](int cid) {
@@ -921,28 +958,58 @@ __global__ __launch_bounds__(kChunkThreads) void scan_bwd_chunk_bf16_kernel(
     rk.fetch(k, b, h, t0, N, H);
     ro.fetch(d_o, b, h, t0, N, H, active);
     rv.fetch(v, b, h, t0, N, H);
-    mh.fetch(reinterpret_cast<const T*>(Ws<D>::Hs(const_cast<float*>(ws), cid)));
-    mg.fetch(reinterpret_cast<const T*>(Ws<D>::dHs(const_cast<float*>(ws), cid)));
+    if constexpr (kHGinLDS) {
+      mh.fetch(reinterpret_cast<const T*>(Ws<D>::Hs(const_cast<float*>(ws), cid)));
+      mg.fetch(reinterpret_cast<const T*>(Ws<D>::dHs(const_cast<float*>(ws), cid)));
+    }
     rbeta.fetch(beta, b, h, t0, N, H);
   };
-  fetch(blockIdx.x);
+  // (at D 128 the registers go to the states' fragments: each chunk loads its own operands)
+  if constexpr (kHGinLDS) fetch(blockIdx.x);
   for (int cid = blockIdx.x; cid < total; cid += gridDim.x) {
+  if constexpr (!kHGinLDS) fetch(cid);
   const int c = cid % NC, bh = cid / NC;
   const int b = bh / H, h = bh - b * H;
   const int t0 = c * kC;
+  // the states' fragments: B operands of X H (hcol) and X H^T (hrow), and the A operands they meet
+  const T* gH = reinterpret_cast<const T*>(Ws<D>::Hs(const_cast<float*>(ws), cid));
+  const T* gG = reinterpret_cast<const T*>(Ws<D>::dHs(const_cast<float*>(ws), cid));
+  const int lane = threadIdx.x & 63;
+  auto bcol = [&](const T* rec, const T* tile, int ct, int kk) -> bf16x8 {
+    if constexpr (kHGinLDS) {
+      return fcol(tile, LD, 16 * ct, kk);
+    } else {
+      const bf16x4 lo = *reinterpret_cast<const bf16x4*>(rec + accfrag<NT>(ct, kk / 16, lane));
+      const bf16x4 hi = *reinterpret_cast<const bf16x4*>(rec + accfrag<NT>(ct, kk / 16 + 1, lane));
+      return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+    }
+  };
+  auto brow = [&](const T* rec, const T* tile, int ct, int kk) -> bf16x8 {
+    if constexpr (kHGinLDS) {
+      return frow(tile, LD, 16 * ct, kk);
+    } else {
+      const T* rr = rec + Ws<D>::kS;  // the transposed record
+      const bf16x4 lo = *reinterpret_cast<const bf16x4*>(rr + accfrag<NT>(kk / 16, ct, lane));
+      const bf16x4 hi = *reinterpret_cast<const bf16x4*>(rr + accfrag<NT>(kk / 16 + 1, ct, lane));
+      return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+    }
+  };
+  auto arow = [&](const T* X, int kk) -> bf16x8 { return kHGinLDS ? frow(X, LD, r0, kk) : frow2(X, LD, r0, kk); };
   {
     rq.put(sQ, LD);
     rk.put(sK, LD);
     ro.put(sO, LD);
     rv.put(sR, LD);
-    mh.put(sH, LD);
-    mg.put(sG, LD);
+    if constexpr (kHGinLDS) {
+      mh.put(sH, LD);
+      mg.put(sG, LD);
+    }
     *reinterpret_cast<bf16x8*>(sL + (threadIdx.x >> 3) * L6 + 8 * (threadIdx.x & 7)) = lraw;
     rbeta.put(sB, t0, N);
   }
   static_assert(kChunkThreads * 8 == kC * kC, "one 16-byte piece of L a thread");
   __syncthreads();
-  fetch(min(cid + (int)gridDim.x, total - 1));  // (the last chunk again past the end: no branch)
+  if constexpr (kHGinLDS) fetch(min(cid + (int)gridDim.x, total - 1));  // (the last chunk again past the end)
   // T = L diag(beta)
   for (int e = threadIdx.x; e < kC * kC / 8; e += NTH) {
     const int i = e / (kC / 8), j = 8 * (e % (kC / 8));
@@ -952,12 +1019,12 @@ __global__ __launch_bounds__(kChunkThreads) void scan_bwd_chunk_bf16_kernel(
     *reinterpret_cast<bf16x8*>(sT + i * L6 + j) = x;
   }
   // R = V - K H in place (each lane reads only its own V entries)
-  #pragma unroll
+#pragma unroll kU
   for (int u_ = 0; u_ < NT / 2; ++u_) {
     const int ct = ch + 2 * u_;
     f32x4 acc = zero4();
     #pragma unroll
-    for (int kk = 0; kk < D; kk += 32) acc = mma32(frow(sK, LD, r0, kk), fcol(sH, LD, 16 * ct, kk), acc);
+    for (int kk = 0; kk < D; kk += 32) acc = mma32(arow(sK, kk), bcol(gH, sH, ct, kk), acc);
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       T& x = sR[(r0 + tile_row(r)) * LD + 16 * ct + tile_col()];
@@ -978,31 +1045,23 @@ __global__ __launch_bounds__(kChunkThreads) void scan_bwd_chunk_bf16_kernel(
   }
   __syncthreads();
   // Delta = T R; dDelta = K G + P^T dO
-  #pragma unroll
+#pragma unroll kU
   for (int u_ = 0; u_ < NT / 2; ++u_) {
     const int ct = ch + 2 * u_;
     f32x4 d = zero4(), dd = zero4();
     #pragma unroll
     for (int kk = 0; kk < kC; kk += 32) d = mma32(frow(sT, L6, r0, kk), fcol(sR, LD, 16 * ct, kk), d);
     #pragma unroll
-    for (int kk = 0; kk < D; kk += 32) dd = mma32(frow(sK, LD, r0, kk), fcol(sG, LD, 16 * ct, kk), dd);
+    for (int kk = 0; kk < D; kk += 32) dd = mma32(arow(sK, kk), bcol(gG, sG, ct, kk), dd);
     #pragma unroll
     for (int kk = 0; kk < kC; kk += 32) dd = mma32(fcol(sP, L6, r0, kk), fcol(sO, LD, 16 * ct, kk), dd);
     put_tile(sD, LD, r0, 16 * ct, d);
     put_tile(sDD, LD, r0, 16 * ct, dd);
   }
   __syncthreads();
-  // dR = T^T dDelta (= dV; kept negated for dK); S2 = tril(dO Delta^T) over P; dT = dDelta R^T:
-  // dbeta_j gets sum_i dT_ij L_ij (column sums per row block into sPart), dL = tril(dT) diag(beta)
-  #pragma unroll
-  for (int u_ = 0; u_ < NT / 2; ++u_) {
-    const int ct = ch + 2 * u_;
-    f32x4 acc = zero4();
-    #pragma unroll
-    for (int kk = 0; kk < kC; kk += 32) acc = mma32(fcol(sT, L6, r0, kk), fcol(sDD, LD, 16 * ct, kk), acc);
-    store_rows<T, D>(dv, b, h, t0, N, H, r0, 16 * ct, acc);
-    put_tile(sDR, LD, r0, 16 * ct, -acc);
-  }
+  // S2 = tril(dO Delta^T) over P; dT = dDelta R^T: dbeta_j gets sum_i dT_ij L_ij (column sums per
+  // row block into sPart), dL = tril(dT) diag(beta); then dR = T^T dDelta (= dV; kept negated for
+  // dK, over R at D 128 once every dT tile has read R)
   #pragma unroll
   for (int u_ = 0; u_ < 2; ++u_) {
     const int ct = ch + 2 * u_;
@@ -1028,14 +1087,24 @@ __global__ __launch_bounds__(kChunkThreads) void scan_bwd_chunk_bf16_kernel(
     put_tile(sS2, L6, r0, 16 * ct, s2);
     put_tile(sDL, L6, r0, 16 * ct, dt);
   }
-  __syncthreads();
-  // dQ = dO H^T + S2 K; X1 = L^T dL over T (L^T upper, dL lower: k from max(rb, ct))
-  #pragma unroll
+  if constexpr (!kHGinLDS) __syncthreads();
+#pragma unroll kU
   for (int u_ = 0; u_ < NT / 2; ++u_) {
     const int ct = ch + 2 * u_;
     f32x4 acc = zero4();
     #pragma unroll
-    for (int kk = 0; kk < D; kk += 32) acc = mma32(frow(sO, LD, r0, kk), frow(sH, LD, 16 * ct, kk), acc);
+    for (int kk = 0; kk < kC; kk += 32) acc = mma32(fcol(sT, L6, r0, kk), fcol(sDD, LD, 16 * ct, kk), acc);
+    store_rows<T, D>(dv, b, h, t0, N, H, r0, 16 * ct, acc);
+    put_tile(sDR, LD, r0, 16 * ct, -acc);
+  }
+  __syncthreads();
+  // dQ = dO H^T + S2 K; X1 = L^T dL over T (L^T upper, dL lower: k from max(rb, ct))
+#pragma unroll kU
+  for (int u_ = 0; u_ < NT / 2; ++u_) {
+    const int ct = ch + 2 * u_;
+    f32x4 acc = zero4();
+    #pragma unroll
+    for (int kk = 0; kk < D; kk += 32) acc = mma32(arow(sO, kk), brow(gH, sH, ct, kk), acc);
     #pragma unroll
     for (int kk = 0; kk < kC; kk += 32) acc = mma32(frow(sS2, L6, r0, kk), fcol(sK, LD, 16 * ct, kk), acc);
     store_rows<T, D>(dq, b, h, t0, N, H, r0, 16 * ct, acc);
@@ -1079,14 +1148,14 @@ __global__ __launch_bounds__(kChunkThreads) void scan_bwd_chunk_bf16_kernel(
   }
   __syncthreads();
   // dK = Delta G^T + S2^T Q - dR H^T + M K + M^T K
-  #pragma unroll
+#pragma unroll kU
   for (int u_ = 0; u_ < NT / 2; ++u_) {
     const int ct = ch + 2 * u_;
     f32x4 acc = zero4();
     #pragma unroll
     for (int kk = 0; kk < D; kk += 32) {
-      acc = mma32(frow(sD, LD, r0, kk), frow(sG, LD, 16 * ct, kk), acc);
-      acc = mma32(frow(sDR, LD, r0, kk), frow(sH, LD, 16 * ct, kk), acc);
+      acc = mma32(arow(sD, kk), brow(gG, sG, ct, kk), acc);
+      acc = mma32(arow(sDR, kk), brow(gH, sH, ct, kk), acc);
     }
     #pragma unroll
     for (int kk = 0; kk < kC; kk += 32) {
@@ -1106,9 +1175,9 @@ __global__ __launch_bounds__(kChunkThreads) void scan_bwd_chunk_bf16_kernel(
   }
 }
 
-// The prep kernel on bf16 LDS tiles (bf16 entry, head widths 32 and 64). The UT solve stays in
-// fp32; once it is done its two fp32 buffers hold the bf16 T and P, and W and U, so that the
-// kernel's LDS (about 74 KB at D 64) lets two workgroups share a CU.
+// The prep kernel on bf16 LDS tiles (bf16 entry, head widths 32, 64 and 128). The UT solve stays
+// in fp32; once it is done its two fp32 buffers hold the bf16 T and P, and (up to D 64) W and U,
+// so that the kernel's LDS (about 74 KB at D 64) lets two workgroups share a CU.
 template <int D>
 __global__ __launch_bounds__(kPrepThreads) void scan_bwd_prep_bf16_kernel(
     const __bf16* __restrict__ q, const __bf16* __restrict__ k, const __bf16* __restrict__ v,
@@ -1117,14 +1186,15 @@ __global__ __launch_bounds__(kPrepThreads) void scan_bwd_prep_bf16_kernel(
   using T = __bf16;
   constexpr int NT = D / 16, NTH = kPrepThreads;
   constexpr int LD = D + 8, L6 = kC + 8, PF = kC + 8;  // pitches: [64][D] bf16, [64][64] bf16, [64][64] fp32
-  static_assert(2 * kC * L6 * sizeof(T) == kC * PF * sizeof(float) && 2 * kC * LD * sizeof(T) <= kC * PF * sizeof(float),
-                "T and P, then W and U, fit the fp32 buffers of the solve");
+  static_assert(2 * kC * L6 * sizeof(T) == kC * PF * sizeof(float), "T and P fit the fp32 buffer of A");
+  constexpr bool kWUinL = 2 * kC * LD * sizeof(T) <= kC * PF * sizeof(float);  // W and U fit L's (D <= 64)
   __shared__ __align__(16) T sQ[kC * LD], sK[kC * LD], sV[kC * LD], sO[kC * LD];
   __shared__ __align__(16) float sA[kC * PF], sL[kC * PF];
+  __shared__ __align__(16) T sWU[kWUinL ? 1 : 2 * kC * LD];
   __shared__ float sB[kC];
   T* sT = reinterpret_cast<T*>(sA);  // T = L diag(beta), then P beside it, once A is done with
   T* sP = sT + kC * L6;
-  T* sW = reinterpret_cast<T*>(sL);  // W and U once L is in bf16 (T) and in the workspace
+  T* sW = kWUinL ? reinterpret_cast<T*>(sL) : sWU;  // W and U, over L once L is in bf16 (T) and saved
   T* sU = sW + kC * LD;
   T* sZ = sV;                        // Z = P^T dO once U is done
   const int c = blockIdx.x % NC, bh = blockIdx.x / NC;
@@ -1335,10 +1405,15 @@ int scan_backward(const TIn* q, const TIn* k, const TIn* v, const TIn* beta, con
                   float* d_state_in, void* workspace, size_t workspace_bytes, int B, int N, int H, int D,
                   void* stream_ptr, const char* who) {
   if (B < 0 || N < 0 || H < 1) return fail(ERR_ARG, "%s: bad sizes B=%d N=%d H=%d", who, B, N, H);
-  if (!(D == 16 || D == 32 || D == 64)) return fail(ERR_UNSUPPORTED, "%s: head dimension %d (backward: 16, 32, 64)", who, D);
+  constexpr bool bf16 = sizeof(TIn) == 2;
+  if (!(D == 16 || D == 32 || D == 64 || (D == 128 && bf16)))
+    return fail(ERR_UNSUPPORTED, "%s: head dimension %d (backward: 16, 32, 64%s)", who, D, bf16 ? ", 128" : "");
   if (B == 0 || N == 0) return OK;  // no token: the caller's state gradient passes through
   if (!q || !k || !v || !beta || !state_in || !d_o || !dq || !dk || !dv || !dbeta || !d_state_in)
     return fail(ERR_ARG, "%s: null pointer", who);
+  // the chains address one (b, h)'s chunks of the workspace with 32-bit byte offsets
+  if ((size_t)((N + kC - 1) / kC) * ((size_t)kC * kC + 6 * (size_t)D * D) * sizeof(float) >= ((size_t)1 << 32))
+    return fail(ERR_UNSUPPORTED, "%s: %d tokens of width %d exceed the 4 GiB workspace a head", who, N, D);
   const size_t need = workspace_floats(B, N, H, D) * sizeof(float);
   if (!workspace || workspace_bytes < need)
     return fail(ERR_ARG, "%s: workspace of %zu bytes, %zu needed", who, workspace_bytes, need);
@@ -1350,7 +1425,11 @@ int scan_backward(const TIn* q, const TIn* k, const TIn* v, const TIn* beta, con
   switch (D) {
     case 16: launch<TIn, 16>(q, k, v, beta, state_in, d_o, d_state, active, dq, dk, dv, dbeta, d_state_in, ws, B, N, H, stream); break;
     case 32: launch<TIn, 32>(q, k, v, beta, state_in, d_o, d_state, active, dq, dk, dv, dbeta, d_state_in, ws, B, N, H, stream); break;
-    default: launch<TIn, 64>(q, k, v, beta, state_in, d_o, d_state, active, dq, dk, dv, dbeta, d_state_in, ws, B, N, H, stream); break;
+    case 64: launch<TIn, 64>(q, k, v, beta, state_in, d_o, d_state, active, dq, dk, dv, dbeta, d_state_in, ws, B, N, H, stream); break;
+    default:
+      if constexpr (bf16)
+        launch<TIn, 128>(q, k, v, beta, state_in, d_o, d_state, active, dq, dk, dv, dbeta, d_state_in, ws, B, N, H, stream);
+      break;
   }
   return check_launch(who);
 }

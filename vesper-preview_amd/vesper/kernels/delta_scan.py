@@ -19,9 +19,10 @@ exactly the reference behaviour. With ``active``, the chunked scans also take ``
 beta)``: the copy-forward of halted tokens (``vesper/column.py:779-789``), read inside the kernels'
 loads (``vsp_delta_scan_carried_*``) where a token is inactive, in place of the ``where`` merges
 before the call. The two chunked scans are autograd functions: their backward
-(``vsp_delta_scan_backward_*``, head widths 16, 32 and 64) gives the gradients of ``q, k, v, beta``
-and the initial state, as the reference's kernels do; the single step is forward only (inputs
-that require a gradient are refused while grad mode is on).
+(``vsp_delta_scan_backward_*``: head widths 16, 32, 64 and, on the bf16 entry, 128; a narrower
+width runs zero-padded to the next of these, which leaves every output and gradient unchanged)
+gives the gradients of ``q, k, v, beta`` and the initial state, as the reference's kernels do; the
+single step is forward only (inputs that require a gradient are refused while grad mode is on).
 """
 
 from __future__ import annotations
@@ -35,7 +36,8 @@ from vesper.contracts import ContractError, Dims, check_shape
 from vesper.kernels import _lib
 
 MAX_HEAD_DIM = 256  # delta_scan.py:41 in the reference; the HIP kernels take any width up to it
-BACKWARD_HEAD_DIMS = (16, 32, 64)  # the widths the backward kernels take
+# the widths the backward kernels take, on the bf16 and on the fp32 entry
+BACKWARD_HEAD_DIMS = {False: (16, 32, 64, 128), True: (16, 32, 64)}
 INPUT_DTYPE = torch.bfloat16  # delta_scan_fused's q, k, v, beta
 FP32_INPUT_DTYPE = torch.float32  # delta_scan_fused_fp32's q, k, v, beta
 STATE_DTYPE = torch.float32
@@ -181,10 +183,20 @@ def _autograd_scan(q: Tensor, k: Tensor, v: Tensor, beta: Tensor, state: Tensor,
         beta = torch.where(keep[..., 0], beta, carried[2])
         carried = None
     if grad:
-        if dk not in BACKWARD_HEAD_DIMS:
-            raise ContractError(f"the scan's backward takes head widths {BACKWARD_HEAD_DIMS}, got {dk}")
-        out: tuple[Tensor, Tensor] = _DeltaScan.apply(q, k, v, beta, state, mask, fp32)
-        return out
+        widths = BACKWARD_HEAD_DIMS[fp32]
+        width = next((w for w in widths if w >= dk), None)
+        if width is None:
+            raise ContractError(f"the scan's backward takes head widths up to {widths[-1]}, got {dk}")
+        if width == dk:
+            out: tuple[Tensor, Tensor] = _DeltaScan.apply(q, k, v, beta, state, mask, fp32)
+            return out
+        # zero features of q and k and zero value columns add exact zeros to every product, so the
+        # padded scan's outputs and gradients are the unpadded ones (the padding's are dropped)
+        pad = width - dk
+        qp, kp, vp = (torch.nn.functional.pad(t, (0, pad)) for t in (q, k, v))
+        sp = torch.nn.functional.pad(state, (0, pad, 0, pad))
+        o, s = _DeltaScan.apply(qp, kp, vp, beta, sp, mask, fp32)
+        return o[..., :dk].contiguous(), s[..., :dk, :dk].contiguous()
     entry = "vsp_delta_scan_f32" if fp32 else "vsp_delta_scan_bf16"
     return _scan(entry, q, k, v, beta, state, None, fp32, mask=mask, carried=carried)
 
