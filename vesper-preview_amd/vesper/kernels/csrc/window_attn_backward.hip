@@ -166,6 +166,9 @@ __global__ __launch_bounds__(64 * NW) void attn_dq_kernel(const T* __restrict__ 
       fv.fetch(vbase, kv_ld, k0 + KT, S);
     }
     if (k0 <= whi && k0 + KT - 1 > wlo - W) {  // some query of the wave sees this tile
+    // every key of the tile visible to every query of the wave: no masks (an inactive query's
+    // or a query past N has lse +inf, so its P is 0 without one)
+    const bool full = k0 + KT - 1 <= wlo && k0 > whi - W;
     f32x4 sacc[4], pacc[4];
 #pragma unroll
     for (int kb = 0; kb < 4; ++kb) {
@@ -177,17 +180,24 @@ __global__ __launch_bounds__(64 * NW) void attn_dq_kernel(const T* __restrict__ 
         pacc[kb] = Mma<T>::run(row_frag<T, D>(tV, 16 * kb, st), df[st], pacc[kb]);
       }
     }
-    // lane (lq, g) holds keys k0 + 16 kb + 4 g + r of its query
+    // lane (lq, g) holds keys k0 + 16 kb + 4 g + r of its query; dS without the scale (applied to
+    // dQ at the end)
+    float p[4][4];
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) p[kb][r] = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[kb][r], scale_log2, -lq_lse));
+    if (!full) {
+#pragma unroll
+      for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) p[kb][r] = (unsigned)(qk - (k0 + 16 * kb + 4 * g + r)) < (unsigned)W ? p[kb][r] : 0.f;
+    }
     V8 dsb[2];
 #pragma unroll
     for (int kb = 0; kb < 4; ++kb)
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int key = k0 + 16 * kb + 4 * g + r;
-        const bool vis = (unsigned)(qk - key) < (unsigned)W;
-        const float p = vis ? __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[kb][r], scale_log2, -lq_lse)) : 0.f;
-        dsb[kb >> 1][4 * (kb & 1) + r] = from_f32<T>(p * (pacc[kb][r] - dsm) * scale);
-      }
+      for (int r = 0; r < 4; ++r) dsb[kb >> 1][4 * (kb & 1) + r] = from_f32<T>(p[kb][r] * (pacc[kb][r] - dsm));
 #pragma unroll
     for (int t = 0; t < Sh::DT; ++t)
 #pragma unroll
@@ -206,7 +216,7 @@ __global__ __launch_bounds__(64 * NW) void attn_dq_kernel(const T* __restrict__ 
       if (d < D) {
         V4 v;
 #pragma unroll
-        for (int r = 0; r < 4; ++r) v[r] = from_f32<T>(acc[t][r]);
+        for (int r = 0; r < 4; ++r) v[r] = from_f32<T>(acc[t][r] * scale);
         *reinterpret_cast<V4*>(dq + qrow + d) = v;
       }
     }
@@ -224,7 +234,7 @@ __global__ __launch_bounds__(64 * NW, WAVES_PER_SIMD) void attn_dkv_kernel(const
   using V4 = typename Mma<T>::V4;
   __shared__ __align__(16) T sQ[2][64 * Sh::P];
   __shared__ __align__(16) T sD[2][64 * Sh::P];
-  __shared__ float sL[2][64], sS[2][64];
+  __shared__ __align__(16) float sL[2][64], sS[2][64];
   const int kt = blockIdx.x % nkt, bkv = blockIdx.x / nkt;
   const int b = bkv / HKV, kvh = bkv - b * HKV;
   const int G = H / HKV;
@@ -297,6 +307,9 @@ __global__ __launch_bounds__(64 * NW, WAVES_PER_SIMD) void attn_dkv_kernel(const
     const float* tS = sS[buf];
     if (step + 1 < nsteps) fetch_step(step + 1);
     if (M + i0 + 63 >= wk0 && M + i0 <= wk1 + W - 1) {  // some key of the wave is seen
+      // every query of the step sees every key of the wave: no masks (queries past N or inactive
+      // have lse +inf; keys past the end are never stored)
+      const bool full = M + i0 >= wk1 && M + i0 + 63 - wk0 < W;
 #pragma unroll
       for (int qp = 0; qp < 2; ++qp) {
         V8 pb, dsb;
@@ -309,14 +322,21 @@ __global__ __launch_bounds__(64 * NW, WAVES_PER_SIMD) void attn_dkv_kernel(const
             st = Mma<T>::run(row_frag<T, D>(tQ, r0, s), kf[s], st);
             dp = Mma<T>::run(row_frag<T, D>(tD, r0, s), vf[s], dp);
           }
-          // lane (lq, g) holds queries r0 + 4 g + r of its key
+          // lane (lq, g) holds queries r0 + 4 g + r of its key; dS without the scale (applied to dK
+          // at the end)
+          const f32x4 lv = *reinterpret_cast<const f32x4*>(tL + r0 + 4 * g);
+          const f32x4 sv = *reinterpret_cast<const f32x4*>(tS + r0 + 4 * g);
+          float p[4];
+#pragma unroll
+          for (int r = 0; r < 4; ++r) p[r] = __builtin_amdgcn_exp2f(__builtin_fmaf(st[r], scale_log2, -lv[r]));
+          if (!full) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) p[r] = (unsigned)(M + i0 + r0 + 4 * g + r - key) < (unsigned)W ? p[r] : 0.f;
+          }
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
-            const int qi = r0 + 4 * g + r;
-            const bool vis = kok && (unsigned)(M + i0 + qi - key) < (unsigned)W;
-            const float p = vis ? __builtin_amdgcn_exp2f(__builtin_fmaf(st[r], scale_log2, -tL[qi])) : 0.f;
-            pb[4 * qb + r] = from_f32<T>(p);
-            dsb[4 * qb + r] = from_f32<T>(p * (dp[r] - tS[qi]) * scale);
+            pb[4 * qb + r] = from_f32<T>(p[r]);
+            dsb[4 * qb + r] = from_f32<T>(p[r] * (dp[r] - sv[r]));
           }
         }
 #pragma unroll
@@ -337,7 +357,7 @@ __global__ __launch_bounds__(64 * NW, WAVES_PER_SIMD) void attn_dkv_kernel(const
         V4 a, c;
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          a[r] = from_f32<T>(dka[t][r]);
+          a[r] = from_f32<T>(dka[t][r] * scale);
           c[r] = from_f32<T>(dva[t][r]);
         }
         *reinterpret_cast<V4*>(dk + krow + d) = a;
