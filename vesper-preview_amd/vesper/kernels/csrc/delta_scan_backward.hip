@@ -878,12 +878,10 @@ struct ChunkRows16 {
 #pragma unroll
     for (int it = 0; it < kIt; ++it) {
       const int e = threadIdx.x + NTH * it, row = e / (D / 8), c = 8 * (e % (D / 8));
-      bf16x8 x = raw[it];
-      if (!ok[it]) {
-#pragma unroll
-        for (int u = 0; u < 8; ++u) x[u] = (__bf16)0.f;
-      }
-      if (kN % NTH == 0 || e < kN) *reinterpret_cast<bf16x8*>(dst + row * ld + c) = x;
+      const uint4 x = __builtin_bit_cast(uint4, raw[it]);  // zeros selected as four 32-bit words
+      const bool o = ok[it];
+      const uint4 y = {o ? x.x : 0u, o ? x.y : 0u, o ? x.z : 0u, o ? x.w : 0u};
+      if (kN % NTH == 0 || e < kN) *reinterpret_cast<uint4*>(dst + row * ld + c) = y;
     }
   }
 };

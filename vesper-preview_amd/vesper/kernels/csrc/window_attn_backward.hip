@@ -61,10 +61,10 @@ struct Stage64 {
     for (int it = 0; it < kIt; ++it) {
       const int sg = threadIdx.x + NTH * it, row = sg / Sh::SEG, part = sg - row * Sh::SEG;
       const bool ok = r0 + row < rows && 8 * part < D;
-      V8 v;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) v[e] = ok ? raw[it][e] : from_f32<T>(0.f);
-      if (kSegs % NTH == 0 || sg < kSegs) *reinterpret_cast<V8*>(dst + row * Sh::P + 8 * part) = v;
+      // the zeros selected as four 32-bit words (the 16 bytes as one unit, not eight elements)
+      const uint4 x = __builtin_bit_cast(uint4, raw[it]);
+      const uint4 v = {ok ? x.x : 0u, ok ? x.y : 0u, ok ? x.z : 0u, ok ? x.w : 0u};
+      if (kSegs % NTH == 0 || sg < kSegs) *reinterpret_cast<uint4*>(dst + row * Sh::P + 8 * part) = v;
     }
   }
 };
