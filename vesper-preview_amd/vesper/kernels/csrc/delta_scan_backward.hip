@@ -251,6 +251,13 @@ __device__ __forceinline__ size_t afrag(int rt, int kt, int l) {
 }
 template <int NT>
 __device__ __forceinline__ size_t accfrag(int s, int rt, int l) { return ((size_t)(s * NT + rt) * 64 + l) * 4; }
+// - accfrag2: the same for bf16 with two row tiles of a slice side by side (one 16-byte access for
+//   a lane's pair; D 16: one tile): the chains' added terms and their records on the bf16 entry.
+template <int NT>
+__device__ __forceinline__ size_t accfrag2(int s, int rt, int l) {
+  if constexpr (NT == 1) return (size_t)l * 4;
+  else return ((size_t)(s * (NT / 2) + rt / 2) * 64 + l) * 8 + (rt & 1) * 4;
+}
 
 // Eight waves in the chunk kernel's arrangement: wave w owns row block rb (rb and 3 - rb on one
 // SIMD) and every other column tile from ch = w / 4; triangular zeros are skipped.
@@ -396,8 +403,8 @@ __global__ __launch_bounds__(kPrepThreads) void scan_bwd_prep_kernel(const TIn* 
         yb[r] = (__bf16)(qo[r] - wz[r]);
         bb[r] = (__bf16)ku[r];
       }
-      *reinterpret_cast<bf16x4*>(reinterpret_cast<__bf16*>(gY) + accfrag<NT>(ct, rt, l)) = yb;
-      *reinterpret_cast<bf16x4*>(reinterpret_cast<__bf16*>(gB) + accfrag<NT>(ct, rt, l)) = bb;
+      *reinterpret_cast<bf16x4*>(reinterpret_cast<__bf16*>(gY) + accfrag2<NT>(ct, rt, l)) = yb;
+      *reinterpret_cast<bf16x4*>(reinterpret_cast<__bf16*>(gB) + accfrag2<NT>(ct, rt, l)) = bb;
       *reinterpret_cast<bf16x4*>(reinterpret_cast<__bf16*>(gNR) + afrag<NT>(ct, rt, l)) = nr;
       *reinterpret_cast<bf16x4*>(reinterpret_cast<__bf16*>(gNF) + afrag<NT>(ct, rt, l)) = nf;
     } else {
@@ -470,10 +477,19 @@ __device__ __forceinline__ void load_chain_ops(ChainOps<D / 16, BF>& o, __amdgpu
         for (int e = 0; e < 4; ++e) o.a[2 * (rt * NT + kt) + e] = v[e];
       }
   }
+  if constexpr (BF && NT >= 2) {
+#pragma unroll
+    for (int rt = 0; rt < NT; rt += 2) {  // a pair of row tiles a load
+      const auto v = __builtin_amdgcn_raw_buffer_load_b128(rs, add_off + 2 * (unsigned)accfrag2<NT>(s, rt, l), chunk_off, 0);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) o.add[2 * rt + e] = v[e];
+    }
+  }
 #pragma unroll
   for (int rt = 0; rt < NT; ++rt) {
-    if constexpr (BF) {
-      const auto v = __builtin_amdgcn_raw_buffer_load_b64(rs, add_off + 2 * (unsigned)accfrag<NT>(s, rt, l), chunk_off, 0);
+    if constexpr (BF && NT >= 2) {
+    } else if constexpr (BF) {
+      const auto v = __builtin_amdgcn_raw_buffer_load_b64(rs, add_off + 2 * (unsigned)accfrag2<NT>(s, rt, l), chunk_off, 0);
       o.add[2 * rt] = v[0];
       o.add[2 * rt + 1] = v[1];
     } else {
@@ -527,6 +543,7 @@ __global__ __launch_bounds__(64) void scan_bwd_chains_kernel(const float* __rest
     const unsigned co = chunk_off(i);
     s16x4_t xb[NT];
     f32x4 xf[NT];
+    bf16x4 tprev;
 #pragma unroll
     for (int kt = 0; kt < NT; ++kt) {
       xf[kt] = acc[kt];
@@ -535,12 +552,17 @@ __global__ __launch_bounds__(64) void scan_bwd_chains_kernel(const float* __rest
       for (int r = 0; r < 4; ++r) t[r] = (__bf16)acc[kt][r];
       xb[kt] = __builtin_bit_cast(s16x4_t, t);
 #if defined(__HIP_DEVICE_COMPILE__)
-      if constexpr (BF && D >= 32)  // the record as the bf16 chunk kernel multiplies it
-        __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(v2u32_t, t), rs,
-                                              rec_off + 2 * (unsigned)accfrag<NT>(s, kt, l), co, 0);
-      else
+      if constexpr (BF && D >= 32) {  // the record as the bf16 chunk kernel multiplies it, a pair a store
+        if (kt & 1) {
+          const v4u32_t pr = {__builtin_bit_cast(v2u32_t, tprev)[0], __builtin_bit_cast(v2u32_t, tprev)[1],
+                               __builtin_bit_cast(v2u32_t, t)[0], __builtin_bit_cast(v2u32_t, t)[1]};
+          __builtin_amdgcn_raw_buffer_store_b128(pr, rs, rec_off + 2 * (unsigned)accfrag2<NT>(s, kt - 1, l), co, 0);
+        }
+        tprev = t;
+      } else {
         __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(v4u32_t, acc[kt]), rs,
                                                rec_off + 4 * (unsigned)accfrag<NT>(s, kt, l), co, 0);
+      }
 #endif
       if constexpr (kRowRec) {
 #pragma unroll
@@ -886,25 +908,30 @@ struct ChunkRows16 {
   }
 };
 
-// a [D][D] bf16 record in accumulator order into LDS [D][ld] bf16, row-major
+// a [D][D] bf16 record in accumulator order (accfrag2: pairs of row tiles) into LDS [D][ld] bf16,
+// row-major
 template <int D, int NTH>
 struct AccRows16 {
-  static constexpr int NT = D / 16, kN = D * D / 4, kIt = (kN + NTH - 1) / NTH;
-  bf16x4 raw[kIt];
+  static constexpr int NT = D / 16, NP = NT >= 2 ? NT / 2 : 1, EU = NT >= 2 ? 8 : 4;  // elements a unit
+  static constexpr int kN = D * D / EU, kIt = (kN + NTH - 1) / NTH;
+  typedef __bf16 U __attribute__((ext_vector_type(EU)));
+  U raw[kIt];
   __device__ __forceinline__ void fetch(const __bf16* src) {
 #pragma unroll
-    for (int it = 0; it < kIt; ++it)
-      raw[it] = *reinterpret_cast<const bf16x4*>(src + 4 * min((int)threadIdx.x + NTH * it, kN - 1));
+    for (int it = 0; it < kIt; ++it) raw[it] = *reinterpret_cast<const U*>(src + EU * min((int)threadIdx.x + NTH * it, kN - 1));
   }
   __device__ __forceinline__ void put(__bf16* dst, int ld) const {
 #pragma unroll
     for (int it = 0; it < kIt; ++it) {
-      const int e = threadIdx.x + NTH * it;  // = (s NT + rt) 64 + lane
+      const int e = threadIdx.x + NTH * it;  // = (slice NP + pair) 64 + lane
       if (kN % NTH == 0 || e < kN) {
-        const int lane = e & 63, st = e >> 6, sl = st / NT, rt = st - sl * NT;
-        const int row = 16 * rt + 4 * (lane >> 4), col = 16 * sl + (lane & 15);
+        const int lane = e & 63, st = e >> 6, sl = st / NP, m = st - sl * NP;
 #pragma unroll
-        for (int r = 0; r < 4; ++r) dst[(row + r) * ld + col] = raw[it][r];
+        for (int u = 0; u < EU / 4; ++u) {
+          const int row = 16 * (2 * m + u) + 4 * (lane >> 4), col = 16 * sl + (lane & 15);
+#pragma unroll
+          for (int r = 0; r < 4; ++r) dst[(row + r) * ld + col] = raw[it][4 * u + r];
+        }
       }
     }
   }
@@ -977,9 +1004,7 @@ __global__ __launch_bounds__(kChunkThreads) void scan_bwd_chunk_bf16_kernel(
     if constexpr (kHGinLDS) {
       return fcol(tile, LD, 16 * ct, kk);
     } else {
-      const bf16x4 lo = *reinterpret_cast<const bf16x4*>(rec + accfrag<NT>(ct, kk / 16, lane));
-      const bf16x4 hi = *reinterpret_cast<const bf16x4*>(rec + accfrag<NT>(ct, kk / 16 + 1, lane));
-      return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+      return *reinterpret_cast<const bf16x8*>(rec + accfrag2<NT>(ct, kk / 16, lane));  // tiles kk/16, +1
     }
   };
   auto brow = [&](const T* rec, const T* tile, int ct, int kk) -> bf16x8 {
@@ -1351,8 +1376,8 @@ __global__ __launch_bounds__(kPrepThreads) void scan_bwd_prep_bf16_kernel(
       yb[r] = (T)y[r];
       bbb[r] = (T)bb[r];
     }
-    *reinterpret_cast<bf16x4*>(reinterpret_cast<T*>(gY) + accfrag<NT>(ct, rt, l)) = yb;
-    *reinterpret_cast<bf16x4*>(reinterpret_cast<T*>(gB) + accfrag<NT>(ct, rt, l)) = bbb;
+    *reinterpret_cast<bf16x4*>(reinterpret_cast<T*>(gY) + accfrag2<NT>(ct, rt, l)) = yb;
+    *reinterpret_cast<bf16x4*>(reinterpret_cast<T*>(gB) + accfrag2<NT>(ct, rt, l)) = bbb;
     *reinterpret_cast<bf16x4*>(gNR + afrag<NT>(ct, rt, l)) = nr;
     *reinterpret_cast<bf16x4*>(gNF + afrag<NT>(ct, rt, l)) = nf;
   }
