@@ -1354,32 +1354,50 @@ __global__ __launch_bounds__(kPrepThreads) void scan_bwd_prep_bf16_kernel(
   __bf16* gNF = reinterpret_cast<__bf16*>(Ws<D>::NF(ws, chunk));
   __bf16* gNR = reinterpret_cast<__bf16*>(Ws<D>::NR(ws, chunk));
   const int l = threadIdx.x & 63;
-  #pragma unroll
-  for (int tile = w; tile < NT * NT; tile += NTH / 64) {
-    const int rt = tile / NT, ct = tile - rt * NT;
-    f32x4 y = zero4(), bb = zero4(), kw = zero4(), wk = zero4();
+  // a wave takes row tiles of one column tile, two at a time: each column fragment it reads (of
+  // dO, Z, U, W, K) then serves both
+  constexpr int RPW = NT * NT >= 8 ? NT * NT / 8 : 1;  // row tiles a wave
+  constexpr int RSTEP = NT >= 8 ? 1 : 8 / NT;          // between a wave's row tiles
+  constexpr int RG = RPW >= 2 ? 2 : 1;                 // row tiles at a time
+  if (NT * NT >= 8 || w < NT * NT) {
+    const int ct = w % NT, rt0 = w / NT;
 #pragma unroll
-    for (int kk = 0; kk < kC; kk += 32) {
-      const bf16x8 qa = fcol(sQ, LD, 16 * rt, kk), wa = fcol(sW, LD, 16 * rt, kk), ka = fcol(sK, LD, 16 * rt, kk);
-      const bf16x8 zb = fcol(sZ, LD, 16 * ct, kk), wb = fcol(sW, LD, 16 * ct, kk), kb = fcol(sK, LD, 16 * ct, kk);
-      y = mma32(qa, fcol(sO, LD, 16 * ct, kk), y);
-      y = mma32(wa, -zb, y);
-      bb = mma32(ka, fcol(sU, LD, 16 * ct, kk), bb);
-      kw = mma32(ka, wb, kw);
-      wk = mma32(wa, kb, wk);
-    }
-    bf16x4 nr, nf, yb, bbb;
+    for (int j0 = 0; j0 < RPW; j0 += RG) {
+      f32x4 y[RG], bb[RG], kw[RG], wk[RG];
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      nr[r] = (T)(-kw[r]);
-      nf[r] = (T)(-wk[r]);
-      yb[r] = (T)y[r];
-      bbb[r] = (T)bb[r];
+      for (int j = 0; j < RG; ++j) y[j] = bb[j] = kw[j] = wk[j] = zero4();
+#pragma unroll
+      for (int kk = 0; kk < kC; kk += 32) {
+        const bf16x8 ob = fcol(sO, LD, 16 * ct, kk), zb = -fcol(sZ, LD, 16 * ct, kk), ub = fcol(sU, LD, 16 * ct, kk);
+        const bf16x8 wb = fcol(sW, LD, 16 * ct, kk), kb = fcol(sK, LD, 16 * ct, kk);
+#pragma unroll
+        for (int j = 0; j < RG; ++j) {
+          const int rt = rt0 + RSTEP * (j0 + j);
+          const bf16x8 qa = fcol(sQ, LD, 16 * rt, kk), wa = fcol(sW, LD, 16 * rt, kk), ka = fcol(sK, LD, 16 * rt, kk);
+          y[j] = mma32(qa, ob, y[j]);
+          y[j] = mma32(wa, zb, y[j]);
+          bb[j] = mma32(ka, ub, bb[j]);
+          kw[j] = mma32(ka, wb, kw[j]);
+          wk[j] = mma32(wa, kb, wk[j]);
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < RG; ++j) {
+        const int rt = rt0 + RSTEP * (j0 + j);
+        bf16x4 nr, nf, yb, bbb;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          nr[r] = (T)(-kw[j][r]);
+          nf[r] = (T)(-wk[j][r]);
+          yb[r] = (T)y[j][r];
+          bbb[r] = (T)bb[j][r];
+        }
+        *reinterpret_cast<bf16x4*>(reinterpret_cast<T*>(gY) + accfrag2<NT>(ct, rt, l)) = yb;
+        *reinterpret_cast<bf16x4*>(reinterpret_cast<T*>(gB) + accfrag2<NT>(ct, rt, l)) = bbb;
+        *reinterpret_cast<bf16x4*>(gNR + afrag<NT>(ct, rt, l)) = nr;
+        *reinterpret_cast<bf16x4*>(gNF + afrag<NT>(ct, rt, l)) = nf;
+      }
     }
-    *reinterpret_cast<bf16x4*>(reinterpret_cast<T*>(gY) + accfrag2<NT>(ct, rt, l)) = yb;
-    *reinterpret_cast<bf16x4*>(reinterpret_cast<T*>(gB) + accfrag2<NT>(ct, rt, l)) = bbb;
-    *reinterpret_cast<bf16x4*>(gNR + afrag<NT>(ct, rt, l)) = nr;
-    *reinterpret_cast<bf16x4*>(gNF + afrag<NT>(ct, rt, l)) = nf;
   }
 }
 
