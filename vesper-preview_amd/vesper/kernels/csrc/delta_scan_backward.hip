@@ -540,6 +540,9 @@ __global__ __launch_bounds__(64) void scan_bwd_chains_kernel(const float* __rest
 #pragma unroll
   for (int p = 0; p < R; ++p) load(ops[p], p);
   auto step = [&](int i, ChainOps<NT, BF>& cur) {
+    // the records' stores carry the chunk's offset in the vector offset (scalar offset 0): the
+    // compiler puts no wait state after a wide buffer store with a scalar offset before its data
+    // registers are written again, and on gfx950 such a store can then write the new value
     const unsigned co = chunk_off(i);
     s16x4_t xb[NT];
     f32x4 xf[NT];
@@ -556,12 +559,12 @@ __global__ __launch_bounds__(64) void scan_bwd_chains_kernel(const float* __rest
         if (kt & 1) {
           const v4u32_t pr = {__builtin_bit_cast(v2u32_t, tprev)[0], __builtin_bit_cast(v2u32_t, tprev)[1],
                                __builtin_bit_cast(v2u32_t, t)[0], __builtin_bit_cast(v2u32_t, t)[1]};
-          __builtin_amdgcn_raw_buffer_store_b128(pr, rs, rec_off + 2 * (unsigned)accfrag2<NT>(s, kt - 1, l), co, 0);
+          __builtin_amdgcn_raw_buffer_store_b128(pr, rs, co + rec_off + 2 * (unsigned)accfrag2<NT>(s, kt - 1, l), 0, 0);
         }
         tprev = t;
       } else {
         __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(v4u32_t, acc[kt]), rs,
-                                               rec_off + 4 * (unsigned)accfrag<NT>(s, kt, l), co, 0);
+                                               co + rec_off + 4 * (unsigned)accfrag<NT>(s, kt, l), 0, 0);
       }
 #endif
       if constexpr (kRowRec) {
@@ -577,7 +580,7 @@ __global__ __launch_bounds__(64) void scan_bwd_chains_kernel(const float* __rest
         const bf16x4 x = *reinterpret_cast<const bf16x4*>(sTr + kt * 256 + j * 16 + 4 * g);
 #if defined(__HIP_DEVICE_COMPILE__)
         __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(v2u32_t, x), rs,
-                                              rec_off + kSB / 2 + 2 * (unsigned)accfrag<NT>(s, kt, l), co, 0);
+                                              co + rec_off + kSB / 2 + 2 * (unsigned)accfrag<NT>(s, kt, l), 0, 0);
 #endif
       }
       wave_sync_lds();
