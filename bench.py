@@ -218,9 +218,12 @@ def time_key_filter(torch, reps: int = 50) -> tuple[float, float]:
     return out[0], out[1]
 
 
-def time_scan_backward(torch, reps: int = 10) -> float:
-    """Milliseconds per backward of the delta scan at B8 T4096 H8 d64 bf16 (the four backward
-    kernels through the C ABI), 10 launches in one HIP graph."""
+def time_scan_backward(torch, reps: int = 10) -> dict:
+    """The delta scan's backward at B8 T4096 H8 d64 bf16 through the C ABI, 10 launches in one HIP
+    graph (median milliseconds of 3 replays): as autograd runs it (``recorded_ms``: the forward
+    recorded each chunk's starting state, so only the state gradient's chain runs; the forward
+    with the records is timed the same way, ``forward_recording_ms``), and the backward that
+    recomputes the states itself (``alone_ms``)."""
     from vesper.kernels import _lib
 
     dev = torch.device("cuda:0")
@@ -229,34 +232,55 @@ def time_scan_backward(torch, reps: int = 10) -> float:
     ds = torch.randn(s0.shape, generator=torch.Generator().manual_seed(9)).to(dev)
     dq, dk, dv, db = (torch.empty_like(t) for t in (q, k, v, beta))
     d0 = torch.empty_like(s0)
-    nbytes = int(_lib.library().vsp_delta_scan_backward_workspace_bytes(B, T, H, D))
+    lib = _lib.library()
+    nbytes = int(lib.vsp_delta_scan_backward_workspace_bytes(B, T, H, D))
     ws = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+    fbytes = int(lib.vsp_delta_scan_workspace_bytes(B, T, H, D, 0))
+    fws = torch.empty(fbytes, dtype=torch.uint8, device=dev)
+    rbytes = int(lib.vsp_delta_scan_records_bytes(B, T, H, D))
+    rec = torch.empty(rbytes, dtype=torch.uint8, device=dev)
+    o, s1 = torch.empty_like(q), torch.empty_like(s0)
+    p = _lib.ptr
+    # (the stream is looked up at each call: under capture it is the capturing one)
+    grads = lambda: [p(dq), p(dk), p(dv), p(db), p(d0), p(ws), nbytes, B, T, H, D, _lib.stream_of(dev)]  # noqa: E731
 
-    def run():
-        _lib.call("vsp_delta_scan_backward_bf16", _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(beta), _lib.ptr(s0),
-                  _lib.ptr(up), _lib.ptr(ds), None, _lib.ptr(dq), _lib.ptr(dk), _lib.ptr(dv), _lib.ptr(db),
-                  _lib.ptr(d0), _lib.ptr(ws), nbytes, B, T, H, D, _lib.stream_of(dev))
+    def forward():
+        _lib.call("vsp_delta_scan_record_bf16", p(q), p(k), p(v), p(beta), p(s0), p(o), p(s1), p(fws), fbytes, None,
+                  p(rec), rbytes, B, T, H, D, _lib.stream_of(dev))
 
-    side = torch.cuda.Stream()
-    side.wait_stream(torch.cuda.current_stream())
-    with torch.cuda.stream(side):
-        run()
-    torch.cuda.current_stream().wait_stream(side)
-    graph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(graph):
-        for _ in range(reps):
+    def recorded():
+        _lib.call("vsp_delta_scan_backward_recorded_bf16", p(q), p(k), p(v), p(beta), p(s0), p(up), p(ds), None,
+                  p(rec), rbytes, *grads())
+
+    def alone():
+        _lib.call("vsp_delta_scan_backward_bf16", p(q), p(k), p(v), p(beta), p(s0), p(up), p(ds), None, *grads())
+
+    def timed(run):
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
             run()
-    graph.replay()
-    times = []
-    for _ in range(3):
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        torch.cuda.synchronize()
-        e0.record()
+        torch.cuda.current_stream().wait_stream(side)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            for _ in range(reps):
+                run()
         graph.replay()
-        e1.record()
-        torch.cuda.synchronize()
-        times.append(e0.elapsed_time(e1) / reps)
-    return statistics.median(times)
+        times = []
+        for _ in range(3):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            torch.cuda.synchronize()
+            e0.record()
+            graph.replay()
+            e1.record()
+            torch.cuda.synchronize()
+            times.append(e0.elapsed_time(e1) / reps)
+        return statistics.median(times)
+
+    out = {"forward_recording_ms": timed(forward)}  # (also leaves the records the backward reads)
+    out["recorded_ms"] = timed(recorded)
+    out["alone_ms"] = timed(alone)
+    return out
 
 
 def time_attention_backward(torch, reps: int = 20) -> float:
@@ -787,7 +811,7 @@ def main() -> int:
     a_bytes, a_flops = attn_bytes(B, T, H, H, D), attn_flops(B, T, H, D, WINDOW)
     attn4_ms = time_attention_config(torch)
     attn4_bwd_ms = time_attention_backward(torch)
-    scan_bwd_ms = time_scan_backward(torch)
+    scan_bwd = time_scan_backward(torch)
     keys_ms, keys_bwd_ms = time_key_filter(torch)
     dec = None if args.no_decode else time_decode(torch)
     dec_cold_us = None if args.no_decode else time_decode_cold(torch)
@@ -837,7 +861,10 @@ def main() -> int:
             "delta_scan_tok_s": round(B * T / (pre["scan_ms"] / 1e3), 1),
             "delta_scan_hbm_frac": round(s_bytes / (pre["scan_ms"] / 1e3) / 1e9 / HBM_PEAK_GBS, 4),
             "delta_scan_mfma_frac_bf16": round(s_flops / (pre["scan_ms"] / 1e3) / 1e12 / BF16_PEAK_TFLOPS, 4),
-            "delta_scan_backward_ms": round(scan_bwd_ms, 4),
+            "delta_scan_backward_ms": round(scan_bwd["recorded_ms"], 4),
+            "delta_scan_backward_note": "autograd's path: the states at the chunks' starts recorded by the forward",
+            "delta_scan_forward_recording_ms": round(scan_bwd["forward_recording_ms"], 4),
+            "delta_scan_backward_recomputing_states_ms": round(scan_bwd["alone_ms"], 4),
             "window_attn_b8_ms": round(pre["attn_ms"], 4),
             "window_attn_b4_ms": round(attn4_ms, 4),
             "window_attn_b4_tok_s": round(ATTN_B * T / (attn4_ms / 1e3), 1),

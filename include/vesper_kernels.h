@@ -77,6 +77,19 @@ int vsp_delta_scan_bf16(const void* q, const void* k, const void* v, const void*
                         void* o, float* state_out, void* workspace, size_t workspace_bytes,
                         const uint8_t* active, int B, int T, int H, int D, void* stream);
 
+/* vsp_delta_scan_bf16 that also records, for the backward, the state at each 64-token chunk's
+ * start: `records` receives vsp_delta_scan_records_bytes(B, T, H, D) bytes (16-byte aligned), one
+ * [D x D] bf16 block a (b, h, chunk), in the order vsp_delta_scan_backward_recorded_bf16 reads.
+ * Records exist for D in {32, 64} on the chunked path (T >= 16); the size is 0 otherwise and the
+ * call is refused (VSP_ERR_UNSUPPORTED). The state the forward carries in fp32 is recorded rounded
+ * to bf16, the precision the backward multiplies it at. No counterpart in the reference: the
+ * autograd path of vesper/kernels/delta_scan.py:132-153 keeps what its backward needs itself. */
+size_t vsp_delta_scan_records_bytes(int B, int T, int H, int D);
+int vsp_delta_scan_record_bf16(const void* q, const void* k, const void* v, const void* beta, const float* state_in,
+                               void* o, float* state_out, void* workspace, size_t workspace_bytes,
+                               const uint8_t* active, void* records, size_t records_bytes, int B, int T, int H,
+                               int D, void* stream);
+
 /* float32 q, k, v, beta, state and o. */
 int vsp_delta_scan_f32(const float* q, const float* k, const float* v, const float* beta, const float* state_in,
                        float* o, float* state_out, void* workspace, size_t workspace_bytes,
@@ -144,6 +157,14 @@ int vsp_delta_scan_backward_f32(const float* q, const float* k, const float* v, 
                                 const float* state_in, const float* d_o, const float* d_state, const uint8_t* active,
                                 float* dq, float* dk, float* dv, float* dbeta, float* d_state_in, void* workspace,
                                 size_t workspace_bytes, int B, int N, int H, int D, void* stream);
+/* vsp_delta_scan_backward_bf16 given the forward's records (vsp_delta_scan_record_bf16 on the same
+ * inputs): the states at the chunks' starts are read from them instead of being recomputed, so only
+ * the state's gradient runs as a chain. D in {32, 64}; records_bytes as vsp_delta_scan_records_bytes. */
+int vsp_delta_scan_backward_recorded_bf16(const void* q, const void* k, const void* v, const void* beta,
+                                          const float* state_in, const void* d_o, const float* d_state,
+                                          const uint8_t* active, const void* records, size_t records_bytes, void* dq,
+                                          void* dk, void* dv, void* dbeta, float* d_state_in, void* workspace,
+                                          size_t workspace_bytes, int B, int N, int H, int D, void* stream);
 
 /* ---- sliding-window causal attention (prefill) -----------------------------------------------
  * q: [B, N, H, D]; keys, values: [B, M + N, HKV, D], the cache's M rows first; o: [B, N, H, D].

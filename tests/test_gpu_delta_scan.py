@@ -616,3 +616,114 @@ def test_the_scan_with_the_write_strength_in_its_loads_matches_the_oracle(fp32, 
     o_ref, s_ref = delta_scan_chunked(q.double(), k.double(), v.double(), torch.sigmoid(logits.double()),
                                       h0.double(), 64)
     assert relative_error(o, o_ref) < tol and relative_error(s, s_ref) < tol
+
+
+# ---- the forward's records of the chunks' starting states, and the backward that reads them ----
+
+def _unpack_records(rec: torch.Tensor, b: int, h: int, nc: int, dk: int) -> torch.Tensor:
+    """The records' [D x D] blocks as states [b, h, nc, D, D]: element ((s (NT/2) + rt/2) 64 + l) 8 +
+    (rt % 2) 4 + r of a block is row 16 rt + 4 (l / 16) + r, column 16 s + l % 16 (NT = D / 16)."""
+    nt = dk // 16
+    x = rec.view(BF16).float().cpu().view(b * h * nc, nt, nt // 2, 4, 16, 2, 4)  # s, rt/2, g, j, rt%2, r
+    # rows 16 (2 p + e) + 4 g + r, columns 16 s + j
+    x = x.permute(0, 2, 5, 3, 6, 1, 4).reshape(b * h * nc, dk, dk)
+    return x.view(b, h, nc, dk, dk)
+
+
+def _record_forward(q, k, v, beta, h0):
+    from vesper.kernels import _lib
+
+    b, n, h, dk = q.shape
+    lib = _lib.library()
+    nbytes = int(lib.vsp_delta_scan_records_bytes(b, n, h, dk))
+    wbytes = int(lib.vsp_delta_scan_workspace_bytes(b, n, h, dk, 0))
+    rec = torch.empty(nbytes, dtype=torch.uint8, device=GPU)
+    ws = torch.empty(wbytes, dtype=torch.uint8, device=GPU)
+    o, s = torch.empty_like(q), torch.empty_like(h0)
+    _lib.call("vsp_delta_scan_record_bf16", *(_lib.ptr(t) for t in (q, k, v, beta, h0, o, s, ws)), wbytes, None,
+              _lib.ptr(rec), nbytes, b, n, h, dk, _lib.stream_of(GPU))
+    return o, s, rec
+
+
+@pytest.mark.parametrize("dk", [32, 64])
+def test_the_forward_records_each_chunks_starting_state(dk):
+    """The records hold the state before chunk c: the oracle's final state over the first 64 c tokens
+    (the initial state itself, rounded to bf16, for chunk 0), to bf16 precision; the forward's
+    outputs are the plain forward's bit for bit."""
+    from vesper.kernels.delta_scan import delta_scan_fused
+
+    b, n, h = 2, 200, 3
+    q, k, v, beta, h0 = _bf16_inputs(b, n, h, dk, seed=dk + 5)
+    o, s, rec = _record_forward(q, k, v, beta, h0)
+    o_plain, s_plain = delta_scan_fused(q, k, v, beta, h0)
+    assert torch.equal(o, o_plain) and torch.equal(s, s_plain)
+    nc = (n + 63) // 64
+    states = _unpack_records(rec, b, h, nc, dk)
+    assert torch.equal(states[:, :, 0], h0.cpu().to(BF16).float())
+    for c in range(1, nc):
+        _, want = _oracle(q[:, : 64 * c], k[:, : 64 * c], v[:, : 64 * c], beta[:, : 64 * c], h0)
+        assert relative_error(states[:, :, c], want) < 1e-2, c
+
+
+@pytest.mark.parametrize("dk", [32, 64])
+def test_the_backward_from_the_records_and_the_backward_alone_agree(dk):
+    """vsp_delta_scan_backward_recorded_bf16 (the autograd path at widths 32 and 64) and
+    vsp_delta_scan_backward_bf16 (which recomputes the states) on one input with an active mask: dv
+    and the initial state's gradient do not read the states and are equal bit for bit; both sets of
+    gradients match the oracle's."""
+    from oracle.delta import delta_scan_chunked
+    from vesper.kernels import _lib
+
+    b, n, h = 2, 300, 3
+    q, k, v, beta, h0 = _bf16_inputs(b, n, h, dk, seed=dk + 9)
+    active = torch.rand(b, n, generator=torch.Generator().manual_seed(4)) < 0.7
+    mask = active.to(GPU).view(torch.uint8)
+    g = torch.Generator().manual_seed(5)
+    d_o = torch.randn(b, n, h, dk, generator=g).to(BF16)
+    d_s = torch.randn(b, h, dk, dk, generator=g)
+    lib = _lib.library()
+    nbytes = int(lib.vsp_delta_scan_records_bytes(b, n, h, dk))
+    wbytes = int(lib.vsp_delta_scan_workspace_bytes(b, n, h, dk, 0))
+    rec = torch.empty(nbytes, dtype=torch.uint8, device=GPU)
+    ws = torch.empty(wbytes, dtype=torch.uint8, device=GPU)
+    o, s = torch.empty_like(q), torch.empty_like(h0)
+    _lib.call("vsp_delta_scan_record_bf16", *(_lib.ptr(t) for t in (q, k, v, beta, h0, o, s, ws)), wbytes,
+              _lib.ptr(mask), _lib.ptr(rec), nbytes, b, n, h, dk, _lib.stream_of(GPU))
+    go, gs = d_o.to(GPU), d_s.to(GPU)
+    bbytes = int(lib.vsp_delta_scan_backward_workspace_bytes(b, n, h, dk))
+    bws = torch.empty(bbytes, dtype=torch.uint8, device=GPU)
+    grads = {}
+    for name in ("recorded", "alone"):
+        out = [torch.empty_like(t) for t in (q, k, v, beta, h0)]
+        head = [_lib.ptr(t) for t in (q, k, v, beta, h0, go, gs, mask)]
+        tail = [_lib.ptr(t) for t in out] + [_lib.ptr(bws), bbytes, b, n, h, dk, _lib.stream_of(GPU)]
+        if name == "recorded":
+            _lib.call("vsp_delta_scan_backward_recorded_bf16", *head, _lib.ptr(rec), nbytes, *tail)
+        else:
+            _lib.call("vsp_delta_scan_backward_bf16", *head, *tail)
+        grads[name] = out
+    torch.cuda.synchronize()
+    assert torch.equal(grads["recorded"][2], grads["alone"][2])
+    assert torch.equal(grads["recorded"][4], grads["alone"][4])
+    ref_in = [t.cpu().double().requires_grad_() for t in (q, k, v, beta, h0)]
+    o_ref, s_ref = delta_scan_chunked(*ref_in, 64, active=active)
+    torch.autograd.backward([(o_ref * d_o.double() * active[..., None, None]).sum() + (s_ref * d_s.double()).sum()])
+    for name, got in grads.items():
+        for what, x, want in zip(["q", "k", "v", "beta", "state"], got, ref_in):
+            assert relative_error(x, want.grad) < TOL, (name, what, relative_error(x, want.grad))
+
+
+def test_record_refusals():
+    from vesper.kernels import _lib
+    from vesper.kernels._lib import KernelLibraryError
+
+    lib = _lib.library()
+    assert int(lib.vsp_delta_scan_records_bytes(1, 200, 2, 16)) == 0  # widths 32 and 64 only
+    assert int(lib.vsp_delta_scan_records_bytes(1, 8, 2, 64)) == 0    # the serial path keeps none
+    assert int(lib.vsp_delta_scan_records_bytes(1, 200, 2, 64)) == 4 * 2 * 64 * 64 * 2
+    q, k, v, beta, h0 = _bf16_inputs(1, 200, 2, 16)
+    o, s = torch.empty_like(q), torch.empty_like(h0)
+    ws = torch.empty(int(lib.vsp_delta_scan_workspace_bytes(1, 200, 2, 16, 0)), dtype=torch.uint8, device=GPU)
+    with pytest.raises(KernelLibraryError, match="no records"):
+        _lib.call("vsp_delta_scan_record_bf16", *(_lib.ptr(t) for t in (q, k, v, beta, h0, o, s, ws)), ws.numel(),
+                  None, _lib.ptr(ws), ws.numel(), 1, 200, 2, 16, _lib.stream_of(GPU))

@@ -35,6 +35,8 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "vsp_delta_scan_workspace_bytes": (Z, [I, I, I, I, I]),
     "vsp_delta_scan_bf16": (I, [P, P, P, P, P, P, P, P, Z, P, I, I, I, I, P]),
     "vsp_delta_scan_f32": (I, [P, P, P, P, P, P, P, P, Z, P, I, I, I, I, P]),
+    "vsp_delta_scan_records_bytes": (Z, [I, I, I, I]),
+    "vsp_delta_scan_record_bf16": (I, [P, P, P, P, P, P, P, P, Z, P, P, Z, I, I, I, I, P]),
     "vsp_delta_scan_carried_bf16": (I, [P, P, P, P, P, P, P, P, P, P, P, Z, P, I, I, I, I, P]),
     "vsp_delta_scan_carried_f32": (I, [P, P, P, P, P, P, P, P, P, P, P, Z, P, I, I, I, I, P]),
     "vsp_delta_scan_logits_bf16": (I, [P, P, P, P, P, F, P, P, P, P, Z, P, I, I, I, I, P]),
@@ -48,6 +50,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "vsp_delta_scan_backward_workspace_bytes": (Z, [I, I, I, I]),
     "vsp_delta_scan_backward_bf16": (I, [P, P, P, P, P, P, P, P, P, P, P, P, P, P, Z, I, I, I, I, P]),
     "vsp_delta_scan_backward_f32": (I, [P, P, P, P, P, P, P, P, P, P, P, P, P, P, Z, I, I, I, I, P]),
+    "vsp_delta_scan_backward_recorded_bf16": (I, [P, P, P, P, P, P, P, P, P, Z, P, P, P, P, P, P, Z, I, I, I, I, P]),
     "vsp_window_attn_lse_bf16": (I, [P, P, P, P, P, P, I, I, I, I, I, I, I, F, P]),
     "vsp_window_attn_lse_f16": (I, [P, P, P, P, P, P, I, I, I, I, I, I, I, F, P]),
     "vsp_window_attn_carried_bf16": (I, [P, P, P, P, P, P, P, I, I, I, I, I, I, I, F, P]),

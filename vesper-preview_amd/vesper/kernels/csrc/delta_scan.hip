@@ -917,7 +917,8 @@ __global__ __launch_bounds__(512) void delta_chain_bf16_kernel(const TIn* __rest
                                                                const float* __restrict__ s_in, float* __restrict__ s_out,
                                                                TIn* __restrict__ o, const uint8_t* __restrict__ active,
                                                                const TIn* kc, const TIn* vc, const TIn* bc, int T, int H,
-                                                               unsigned* fault, int wait_limit) {
+                                                               __bf16* __restrict__ hrec, unsigned* fault,
+                                                               int wait_limit) {
   const Carried<TIn> carried{kc, vc, bc};
   using E = __bf16;
   static_assert(sizeof(TIn) == 2, "bf16 inputs");
@@ -1021,6 +1022,13 @@ __global__ __launch_bounds__(512) void delta_chain_bf16_kernel(const TIn* __rest
       bf16x8 hb[KBF];
 #pragma unroll
       for (int kb = 0; kb < KBF; ++kb) hb[kb] = pack_acc(hreg[2 * kb], hreg[2 * kb + 1]);
+      if (hrec != nullptr) {
+        // the state at the chunk's start for the backward, as bf16 accumulator tiles in pairs of
+        // row tiles (tiles 2 kb and 2 kb + 1 of the slice: one 16-byte store a lane and pair)
+        __bf16* rec = hrec + ((size_t)bh * nc + it) * (DK * DK) + (size_t)slice * KBF * FR + 8 * l;
+#pragma unroll
+        for (int kb = 0; kb < KBF; ++kb) *reinterpret_cast<bf16x8*>(rec + kb * FR) = hb[kb];
+      }
 #pragma unroll
       for (int kb = 0; kb < KBF; ++kb) {  // H^T rows: value column lq, dk 32 kb + 4 g (+16)
         *reinterpret_cast<bf16x4*>(&sHo[s][lq * PK + 32 * kb + 4 * g]) = __builtin_shufflevector(hb[kb], hb[kb], 0, 1, 2, 3);
@@ -1335,7 +1343,7 @@ size_t workspace_bytes(int B, int T, int H, int D, bool fp32) {
 template <typename TIn, typename E, int DK, bool CARRY>
 void launch_chunked(const TIn* q, const TIn* k, const TIn* v, const TIn* beta, const float* s_in, float* s_out, TIn* o,
                     E* tmat, const uint8_t* active, Carried<TIn> carried, int B, int T, int H, hipStream_t stream,
-                    Strength strength) {
+                    Strength strength, __bf16* hrec) {
   const int nc = (T + kChunk - 1) / kChunk;
   const int total = B * H * nc;
   hipLaunchKernelGGL((delta_prep_kernel<TIn, E, DK, CARRY>), dim3((unsigned)((total + 3) / 4)), dim3(256), 0, stream, k,
@@ -1344,7 +1352,7 @@ void launch_chunked(const TIn* q, const TIn* k, const TIn* v, const TIn* beta, c
   if constexpr (sizeof(E) == 2 && DK >= 32 && DK <= 64) {  // (at 128 the staging registers would spill)
     hipLaunchKernelGGL((delta_chain_bf16_kernel<TIn, DK, CARRY>), dim3((unsigned)(B * H * (DK / 16))), dim3(512), 0,
                        stream, q, k, v, tmat, s_in, s_out, o, active, carried.k, carried.v, carried.beta, T, H,
-                       fault_record(), wait_limit());
+                       hrec, fault_record(), wait_limit());
   } else {
     hipLaunchKernelGGL((delta_chain_kernel<TIn, E, DK, CARRY>), dim3((unsigned)(B * H * (DK / 16))),
                        dim3(64 * (ChainShape<E, DK>::NH + 1)), 0, stream, q, k, v, tmat, s_in, s_out, o, active,
@@ -1355,17 +1363,19 @@ void launch_chunked(const TIn* q, const TIn* k, const TIn* v, const TIn* beta, c
 template <typename TIn, typename E, int DK>
 void launch_chunked(const TIn* q, const TIn* k, const TIn* v, const TIn* beta, const float* s_in, float* s_out, TIn* o,
                     E* tmat, const uint8_t* active, Carried<TIn> carried, int B, int T, int H, hipStream_t stream,
-                    Strength strength) {
+                    Strength strength, __bf16* hrec) {
   if (carried.k != nullptr)
-    launch_chunked<TIn, E, DK, true>(q, k, v, beta, s_in, s_out, o, tmat, active, carried, B, T, H, stream, strength);
+    launch_chunked<TIn, E, DK, true>(q, k, v, beta, s_in, s_out, o, tmat, active, carried, B, T, H, stream, strength,
+                                     hrec);
   else
-    launch_chunked<TIn, E, DK, false>(q, k, v, beta, s_in, s_out, o, tmat, active, carried, B, T, H, stream, strength);
+    launch_chunked<TIn, E, DK, false>(q, k, v, beta, s_in, s_out, o, tmat, active, carried, B, T, H, stream, strength,
+                                      hrec);
 }
 
 template <typename TIn, typename E>
 int delta_scan(const TIn* q, const TIn* k, const TIn* v, const TIn* beta, const float* s_in, TIn* o, float* s_out,
                void* workspace, size_t ws_bytes, const uint8_t* active, Carried<TIn> carried, int B, int T, int H, int D,
-               void* stream_ptr, const char* who, Strength strength = {}) {
+               void* stream_ptr, const char* who, Strength strength = {}, __bf16* hrec = nullptr) {
   int st = check_common(q, k, v, beta, s_in, s_out, o, B, T, H, D, who);
   if (st != OK || B == 0 || H == 0) return st;
   if (carried.k != nullptr || carried.v != nullptr || carried.beta != nullptr) {
@@ -1394,12 +1404,12 @@ int delta_scan(const TIn* q, const TIn* k, const TIn* v, const TIn* beta, const 
     return fail(ERR_ARG, "%s: q, k, v, o and the workspace must be 16-byte aligned", who);
   E* tmat = reinterpret_cast<E*>(workspace);
   switch (D) {
-    case 16: launch_chunked<TIn, E, 16>(q, k, v, beta, s_in, s_out, o, tmat, active, carried, B, T, H, stream, strength); break;
-    case 32: launch_chunked<TIn, E, 32>(q, k, v, beta, s_in, s_out, o, tmat, active, carried, B, T, H, stream, strength); break;
-    case 64: launch_chunked<TIn, E, 64>(q, k, v, beta, s_in, s_out, o, tmat, active, carried, B, T, H, stream, strength); break;
+    case 16: launch_chunked<TIn, E, 16>(q, k, v, beta, s_in, s_out, o, tmat, active, carried, B, T, H, stream, strength, hrec); break;
+    case 32: launch_chunked<TIn, E, 32>(q, k, v, beta, s_in, s_out, o, tmat, active, carried, B, T, H, stream, strength, hrec); break;
+    case 64: launch_chunked<TIn, E, 64>(q, k, v, beta, s_in, s_out, o, tmat, active, carried, B, T, H, stream, strength, hrec); break;
     default:
       if constexpr (sizeof(E) == 2)
-        launch_chunked<TIn, E, 128>(q, k, v, beta, s_in, s_out, o, tmat, active, carried, B, T, H, stream, strength);
+        launch_chunked<TIn, E, 128>(q, k, v, beta, s_in, s_out, o, tmat, active, carried, B, T, H, stream, strength, hrec);
       break;
   }
   return check_launch(who);
@@ -1438,6 +1448,33 @@ extern "C" int vsp_delta_scan_bf16(const void* q, const void* k, const void* v, 
                                     static_cast<const __bf16*>(v), static_cast<const __bf16*>(beta), state_in,
                                     static_cast<__bf16*>(o), state_out, workspace, workspace_bytes, active,
                                     vsp::Carried<__bf16>{}, B, T, H, D, stream, "vsp_delta_scan_bf16");
+}
+
+// The chunk-start states the bf16 forward can record for the backward: widths 32 and 64 on the
+// chunked path, one [D x D] bf16 block a (b, h, chunk) in the backward's accumulator-pair order.
+extern "C" size_t vsp_delta_scan_records_bytes(int B, int T, int H, int D) {
+  if (!(D == 32 || D == 64) || vsp::workspace_bytes(B, T, H, D, false) == 0) return 0;
+  const size_t nc = (size_t)(T + vsp::kChunk - 1) / vsp::kChunk;
+  return (size_t)B * H * nc * D * D * sizeof(uint16_t);
+}
+
+extern "C" int vsp_delta_scan_record_bf16(const void* q, const void* k, const void* v, const void* beta,
+                                          const float* state_in, void* o, float* state_out, void* workspace,
+                                          size_t workspace_bytes, const uint8_t* active, void* records,
+                                          size_t records_bytes, int B, int T, int H, int D, void* stream) {
+  const char* who = "vsp_delta_scan_record_bf16";
+  const size_t need = vsp_delta_scan_records_bytes(B, T, H, D);
+  if (need == 0)
+    return vsp::fail(vsp::ERR_UNSUPPORTED, "%s: no records at B=%d T=%d H=%d D=%d (widths 32 and 64, T >= %d)", who, B,
+                     T, H, D, vsp::kSerialBelow);
+  if (records == nullptr || records_bytes < need || (reinterpret_cast<uintptr_t>(records) & 15))
+    return vsp::fail(vsp::ERR_ARG, "%s: records of %zu bytes (16-byte aligned) needed, %zu given", who, need,
+                     records ? records_bytes : (size_t)0);
+  return delta_scan<__bf16, __bf16>(static_cast<const __bf16*>(q), static_cast<const __bf16*>(k),
+                                    static_cast<const __bf16*>(v), static_cast<const __bf16*>(beta), state_in,
+                                    static_cast<__bf16*>(o), state_out, workspace, workspace_bytes, active,
+                                    vsp::Carried<__bf16>{}, B, T, H, D, stream, who, vsp::Strength{},
+                                    static_cast<__bf16*>(records));
 }
 
 extern "C" int vsp_delta_scan_carried_bf16(const void* q, const void* k, const void* v, const void* beta,

@@ -505,7 +505,7 @@ template <typename TIn, int D>
 __global__ __launch_bounds__(64) void scan_bwd_chains_kernel(const float* __restrict__ state_in,
                                                              const float* __restrict__ d_state,
                                                              float* __restrict__ d_state_in, float* __restrict__ ws,
-                                                             int NC, int S) {
+                                                             int NC, int S, int lg0) {
   constexpr bool BF = sizeof(TIn) == 2;  // bf16 A operands and 16x16x16 bf16 MFMA; else fp32 ones
   constexpr int NT = ChainShape<D, BF>::NT, R = ChainShape<D, BF>::kRing;
   // At D 128 the chunk kernel reads the records as MFMA fragments from global memory, in both
@@ -515,7 +515,8 @@ __global__ __launch_bounds__(64) void scan_bwd_chains_kernel(const float* __rest
   __shared__ __align__(16) __bf16 sTr[kRowRec ? NT * 16 * 16 : 1];
   constexpr unsigned kPerB = (unsigned)(Ws<D>::kPer * sizeof(float));  // bytes per chunk
   constexpr unsigned kLB = (unsigned)(Ws<D>::kL * sizeof(float)), kSB = (unsigned)(Ws<D>::kS * sizeof(float));
-  const int lg = xcd_logical_block(blockIdx.x, gridDim.x);
+  // (lg0 = S: the reverse chains only, the states having been recorded by the forward)
+  const int lg = xcd_logical_block(blockIdx.x, gridDim.x) + lg0;
   const bool rev = lg >= S;
   const int sl = rev ? lg - S : lg;
   const int s = sl % NT, bh = sl / NT;
@@ -948,8 +949,8 @@ template <int D>
 __global__ __launch_bounds__(kChunkThreads) void scan_bwd_chunk_bf16_kernel(
     const __bf16* __restrict__ q, const __bf16* __restrict__ k, const __bf16* __restrict__ v,
     const __bf16* __restrict__ beta, const __bf16* __restrict__ d_o, const uint8_t* __restrict__ active,
-    const float* __restrict__ ws, __bf16* __restrict__ dq, __bf16* __restrict__ dk, __bf16* __restrict__ dv,
-    __bf16* __restrict__ dbeta, int N, int H, int NC, int total) {
+    const float* __restrict__ ws, const __bf16* __restrict__ hrec, __bf16* __restrict__ dq, __bf16* __restrict__ dk,
+    __bf16* __restrict__ dv, __bf16* __restrict__ dbeta, int N, int H, int NC, int total) {
   using T = __bf16;
   constexpr int NT = D / 16;  // column tiles of a [64 x D] result
   constexpr int NTH = kChunkThreads;
@@ -987,7 +988,9 @@ __global__ __launch_bounds__(kChunkThreads) void scan_bwd_chunk_bf16_kernel(
     ro.fetch(d_o, b, h, t0, N, H, active);
     rv.fetch(v, b, h, t0, N, H);
     if constexpr (kHGinLDS) {
-      mh.fetch(reinterpret_cast<const T*>(Ws<D>::Hs(const_cast<float*>(ws), cid)));
+      // the chunk's starting state: the forward's record when it kept one, else the chain's
+      mh.fetch(hrec != nullptr ? hrec + (size_t)cid * (D * D)
+                               : reinterpret_cast<const T*>(Ws<D>::Hs(const_cast<float*>(ws), cid)));
       mg.fetch(reinterpret_cast<const T*>(Ws<D>::dHs(const_cast<float*>(ws), cid)));
     }
     rbeta.fetch(beta, b, h, t0, N, H);
@@ -1204,7 +1207,7 @@ __global__ __launch_bounds__(kChunkThreads) void scan_bwd_chunk_bf16_kernel(
 // The prep kernel on bf16 LDS tiles (bf16 entry, head widths 32, 64 and 128). The UT solve stays
 // in fp32; once it is done its two fp32 buffers hold the bf16 T and P, and (up to D 64) W and U,
 // so that the kernel's LDS (about 74 KB at D 64) lets two workgroups share a CU.
-template <int D>
+template <int D, bool REC>
 __global__ __launch_bounds__(kPrepThreads) void scan_bwd_prep_bf16_kernel(
     const __bf16* __restrict__ q, const __bf16* __restrict__ k, const __bf16* __restrict__ v,
     const __bf16* __restrict__ beta, const __bf16* __restrict__ d_o, const uint8_t* __restrict__ active,
@@ -1351,7 +1354,8 @@ __global__ __launch_bounds__(kPrepThreads) void scan_bwd_prep_bf16_kernel(
   }
   __syncthreads();
   // the chains' operands, tile (rt, ct) of each [D x D] product: Y = Q^T dO - W^T Z and B = K^T U
-  // in accumulator order, N = -K^T W into NR and N^T = -W^T K into NF (A tile (ct, rt) of each)
+  // in accumulator order, N = -K^T W into NR and N^T = -W^T K into NF (A tile (ct, rt) of each);
+  // with the forward's records (REC) only the reverse chain runs, so B and N^T are not formed
   float* gY = Ws<D>::Y(ws, chunk);
   float* gB = Ws<D>::B(ws, chunk);
   __bf16* gNF = reinterpret_cast<__bf16*>(Ws<D>::NF(ws, chunk));
@@ -1379,9 +1383,11 @@ __global__ __launch_bounds__(kPrepThreads) void scan_bwd_prep_bf16_kernel(
           const bf16x8 qa = fcol(sQ, LD, 16 * rt, kk), wa = fcol(sW, LD, 16 * rt, kk), ka = fcol(sK, LD, 16 * rt, kk);
           y[j] = mma32(qa, ob, y[j]);
           y[j] = mma32(wa, zb, y[j]);
-          bb[j] = mma32(ka, ub, bb[j]);
           kw[j] = mma32(ka, wb, kw[j]);
-          wk[j] = mma32(wa, kb, wk[j]);
+          if constexpr (!REC) {
+            bb[j] = mma32(ka, ub, bb[j]);
+            wk[j] = mma32(wa, kb, wk[j]);
+          }
         }
       }
 #pragma unroll
@@ -1396,9 +1402,11 @@ __global__ __launch_bounds__(kPrepThreads) void scan_bwd_prep_bf16_kernel(
           bbb[r] = (T)bb[j][r];
         }
         *reinterpret_cast<bf16x4*>(reinterpret_cast<T*>(gY) + accfrag2<NT>(ct, rt, l)) = yb;
-        *reinterpret_cast<bf16x4*>(reinterpret_cast<T*>(gB) + accfrag2<NT>(ct, rt, l)) = bbb;
         *reinterpret_cast<bf16x4*>(gNR + afrag<NT>(ct, rt, l)) = nr;
-        *reinterpret_cast<bf16x4*>(gNF + afrag<NT>(ct, rt, l)) = nf;
+        if constexpr (!REC) {
+          *reinterpret_cast<bf16x4*>(reinterpret_cast<T*>(gB) + accfrag2<NT>(ct, rt, l)) = bbb;
+          *reinterpret_cast<bf16x4*>(gNF + afrag<NT>(ct, rt, l)) = nf;
+        }
       }
     }
   }
@@ -1420,24 +1428,31 @@ unsigned persistent_blocks(int per_cu) {
   return (unsigned)cus[dev] * per_cu;
 }
 
+// hrec: the chunk-start states the forward recorded (bf16, widths 32 and 64), or null: then the
+// forward chain runs here as well.
 template <typename TIn, int D>
 void launch(const TIn* q, const TIn* k, const TIn* v, const TIn* beta, const float* state_in, const TIn* d_o,
             const float* d_state, const uint8_t* active, TIn* dq, TIn* dk, TIn* dv, TIn* dbeta, float* d_state_in,
-            float* ws, int B, int N, int H, hipStream_t stream) {
+            float* ws, int B, int N, int H, hipStream_t stream, const __bf16* hrec = nullptr) {
   const int NC = (N + kC - 1) / kC;
   const unsigned chunks = (unsigned)((size_t)B * H * NC), slices = (unsigned)((size_t)B * H * (D / 16));
-  if constexpr (sizeof(TIn) == 2 && D >= 32)
-    hipLaunchKernelGGL((scan_bwd_prep_bf16_kernel<D>), dim3(chunks), dim3(kPrepThreads), 0, stream, q, k, v, beta, d_o,
-                       active, ws, N, H, NC);
-  else
+  if constexpr (sizeof(TIn) == 2 && D >= 32) {
+    if (hrec != nullptr)
+      hipLaunchKernelGGL((scan_bwd_prep_bf16_kernel<D, true>), dim3(chunks), dim3(kPrepThreads), 0, stream, q, k, v,
+                         beta, d_o, active, ws, N, H, NC);
+    else
+      hipLaunchKernelGGL((scan_bwd_prep_bf16_kernel<D, false>), dim3(chunks), dim3(kPrepThreads), 0, stream, q, k, v,
+                         beta, d_o, active, ws, N, H, NC);
+  } else {
     hipLaunchKernelGGL((scan_bwd_prep_kernel<TIn, D>), dim3(chunks), dim3(kPrepThreads), 0, stream, q, k, v, beta, d_o,
                        active, ws, N, H, NC);
-  hipLaunchKernelGGL((scan_bwd_chains_kernel<TIn, D>), dim3(2 * slices), dim3(64), 0, stream, state_in, d_state,
-                     d_state_in, ws, NC, (int)slices);
+  }
+  hipLaunchKernelGGL((scan_bwd_chains_kernel<TIn, D>), dim3(hrec != nullptr ? slices : 2 * slices), dim3(64), 0, stream,
+                     state_in, d_state, d_state_in, ws, NC, (int)slices, hrec != nullptr ? (int)slices : 0);
   if constexpr (sizeof(TIn) == 2 && D >= 32)
     hipLaunchKernelGGL((scan_bwd_chunk_bf16_kernel<D>), dim3(min(chunks, persistent_blocks(1))),
-                       dim3(kChunkThreads), 0, stream, q, k, v, beta, d_o, active, ws, dq, dk, dv, dbeta, N, H, NC,
-                       (int)chunks);
+                       dim3(kChunkThreads), 0, stream, q, k, v, beta, d_o, active, ws, hrec, dq, dk, dv, dbeta, N, H,
+                       NC, (int)chunks);
   else
     hipLaunchKernelGGL((scan_bwd_chunk_kernel<TIn, D>), dim3(chunks), dim3(kChunkThreads), 0, stream, q, k, v, beta, d_o,
                        active, ws, dq, dk, dv, dbeta, N, H, NC);
@@ -1447,7 +1462,7 @@ template <typename TIn>
 int scan_backward(const TIn* q, const TIn* k, const TIn* v, const TIn* beta, const float* state_in, const TIn* d_o,
                   const float* d_state, const uint8_t* active, TIn* dq, TIn* dk, TIn* dv, TIn* dbeta,
                   float* d_state_in, void* workspace, size_t workspace_bytes, int B, int N, int H, int D,
-                  void* stream_ptr, const char* who) {
+                  void* stream_ptr, const char* who, const __bf16* hrec = nullptr) {
   if (B < 0 || N < 0 || H < 1) return fail(ERR_ARG, "%s: bad sizes B=%d N=%d H=%d", who, B, N, H);
   constexpr bool bf16 = sizeof(TIn) == 2;
   if (!(D == 16 || D == 32 || D == 64 || (D == 128 && bf16)))
@@ -1468,8 +1483,8 @@ int scan_backward(const TIn* q, const TIn* k, const TIn* v, const TIn* beta, con
   float* ws = static_cast<float*>(workspace);
   switch (D) {
     case 16: launch<TIn, 16>(q, k, v, beta, state_in, d_o, d_state, active, dq, dk, dv, dbeta, d_state_in, ws, B, N, H, stream); break;
-    case 32: launch<TIn, 32>(q, k, v, beta, state_in, d_o, d_state, active, dq, dk, dv, dbeta, d_state_in, ws, B, N, H, stream); break;
-    case 64: launch<TIn, 64>(q, k, v, beta, state_in, d_o, d_state, active, dq, dk, dv, dbeta, d_state_in, ws, B, N, H, stream); break;
+    case 32: launch<TIn, 32>(q, k, v, beta, state_in, d_o, d_state, active, dq, dk, dv, dbeta, d_state_in, ws, B, N, H, stream, hrec); break;
+    case 64: launch<TIn, 64>(q, k, v, beta, state_in, d_o, d_state, active, dq, dk, dv, dbeta, d_state_in, ws, B, N, H, stream, hrec); break;
     default:
       if constexpr (bf16)
         launch<TIn, 128>(q, k, v, beta, state_in, d_o, d_state, active, dq, dk, dv, dbeta, d_state_in, ws, B, N, H, stream);
@@ -1506,4 +1521,26 @@ extern "C" int vsp_delta_scan_backward_f32(const float* q, const float* k, const
                                            int H, int D, void* stream) {
   return vsp::scan_backward<float>(q, k, v, beta, state_in, d_o, d_state, active, dq, dk, dv, dbeta, d_state_in,
                                    workspace, workspace_bytes, B, N, H, D, stream, "vsp_delta_scan_backward_f32");
+}
+
+extern "C" int vsp_delta_scan_backward_recorded_bf16(const void* q, const void* k, const void* v, const void* beta,
+                                                     const float* state_in, const void* d_o, const float* d_state,
+                                                     const uint8_t* active, const void* records, size_t records_bytes,
+                                                     void* dq, void* dk, void* dv, void* dbeta, float* d_state_in,
+                                                     void* workspace, size_t workspace_bytes, int B, int N, int H,
+                                                     int D, void* stream) {
+  using T = __bf16;
+  const char* who = "vsp_delta_scan_backward_recorded_bf16";
+  if (B > 0 && N > 0 && H > 0) {
+    if (D != 32 && D != 64) return vsp::fail(vsp::ERR_UNSUPPORTED, "%s: head dimension %d (records: 32, 64)", who, D);
+    const size_t need = (size_t)B * H * ((N + vsp::kC - 1) / vsp::kC) * D * D * sizeof(T);
+    if (records == nullptr || records_bytes < need || (reinterpret_cast<uintptr_t>(records) & 15))
+      return vsp::fail(vsp::ERR_ARG, "%s: records of %zu bytes (16-byte aligned) needed, %zu given", who, need,
+                       records ? records_bytes : (size_t)0);
+  }
+  return vsp::scan_backward<T>(static_cast<const T*>(q), static_cast<const T*>(k), static_cast<const T*>(v),
+                               static_cast<const T*>(beta), state_in, static_cast<const T*>(d_o), d_state, active,
+                               static_cast<T*>(dq), static_cast<T*>(dk), static_cast<T*>(dv), static_cast<T*>(dbeta),
+                               d_state_in, workspace, workspace_bytes, B, N, H, D, stream, who,
+                               static_cast<const T*>(records));
 }

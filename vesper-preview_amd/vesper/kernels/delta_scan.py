@@ -95,8 +95,8 @@ def _aligned(t: Tensor) -> Tensor:
 
 
 def _scan(entry: str, q: Tensor, k: Tensor, v: Tensor, beta: Tensor, state: Tensor, active: Tensor | None,
-          fp32: bool, mask: Tensor | None = None,
-          carried: tuple[Tensor, Tensor, Tensor] | None = None) -> tuple[Tensor, Tensor]:
+          fp32: bool, mask: Tensor | None = None, carried: tuple[Tensor, Tensor, Tensor] | None = None,
+          records: Tensor | None = None) -> tuple[Tensor, Tensor]:
     b, n, h, dk = q.shape
     q, k, v, beta, state = (_aligned(t) for t in (q, k, v, beta, state))
     if mask is None:
@@ -107,7 +107,11 @@ def _scan(entry: str, q: Tensor, k: Tensor, v: Tensor, beta: Tensor, state: Tens
     ws_bytes = int(lib.vsp_delta_scan_workspace_bytes(b, n, h, dk, int(fp32)))
     ws = torch.empty(ws_bytes, dtype=torch.uint8, device=q.device) if ws_bytes else None
     with torch.cuda.device(q.device):
-        if carried is None:
+        if records is not None:  # the bf16 forward that also keeps the chunks' starting states
+            _lib.call("vsp_delta_scan_record_bf16", q.data_ptr(), k.data_ptr(), v.data_ptr(), beta.data_ptr(),
+                      state.data_ptr(), o.data_ptr(), s_out.data_ptr(), _lib.ptr(ws), ws_bytes, _lib.ptr(mask),
+                      records.data_ptr(), records.numel(), b, n, h, dk, _lib.stream_of(q.device))
+        elif carried is None:
             _lib.call(entry, q.data_ptr(), k.data_ptr(), v.data_ptr(), beta.data_ptr(), state.data_ptr(), o.data_ptr(),
                       s_out.data_ptr(), _lib.ptr(ws), ws_bytes, _lib.ptr(mask), b, n, h, dk, _lib.stream_of(q.device))
         else:
@@ -138,11 +142,19 @@ class _DeltaScan(torch.autograd.Function):
                 fp32: bool) -> tuple[Tensor, Tensor]:  # noqa: D102
         entry = "vsp_delta_scan_f32" if fp32 else "vsp_delta_scan_bf16"
         tensors = [t.detach() for t in (q, k, v, beta, state)]
-        o, s_out = _scan(entry, *tensors, None, fp32, mask=mask)
-        if any(ctx.needs_input_grad[:5]):
-            ctx.save_for_backward(*(_aligned(t) for t in tensors), *(() if mask is None else (mask,)))
+        grad = any(ctx.needs_input_grad[:5])
+        # the bf16 forward at widths 32 and 64 keeps the chunks' starting states for the backward,
+        # which then runs only the state gradient's chain
+        b, n, h, dk = q.shape
+        nrec = 0 if fp32 or not grad else int(_lib.library().vsp_delta_scan_records_bytes(b, n, h, dk))
+        records = torch.empty(nrec, dtype=torch.uint8, device=q.device) if nrec else None
+        o, s_out = _scan(entry, *tensors, None, fp32, mask=mask, records=records)
+        if grad:
+            ctx.save_for_backward(*(_aligned(t) for t in tensors), *(() if mask is None else (mask,)),
+                                  *(() if records is None else (records,)))
             ctx.fp32 = fp32
             ctx.masked = mask is not None
+            ctx.recorded = records is not None
         return o, s_out
 
     @staticmethod
@@ -150,6 +162,7 @@ class _DeltaScan(torch.autograd.Function):
         saved = ctx.saved_tensors
         q, k, v, beta, state = saved[:5]
         mask = saved[5] if ctx.masked else None
+        records = saved[-1] if ctx.recorded else None
         b, n, h, dk = q.shape
         go = torch.zeros_like(q) if d_o is None else _aligned(d_o.to(q.dtype))
         gs = None if d_state is None else _aligned(d_state.to(STATE_DTYPE))
@@ -160,10 +173,17 @@ class _DeltaScan(torch.autograd.Function):
         ws = torch.empty(max(ws_bytes, 16), dtype=torch.uint8, device=q.device)
         entry = "vsp_delta_scan_backward_f32" if ctx.fp32 else "vsp_delta_scan_backward_bf16"
         with torch.cuda.device(q.device):
-            _lib.call(entry, q.data_ptr(), k.data_ptr(), v.data_ptr(), beta.data_ptr(), state.data_ptr(),
-                      go.data_ptr(), _lib.ptr(gs), _lib.ptr(mask), dq.data_ptr(), dk_.data_ptr(), dv.data_ptr(),
-                      db.data_ptr(), d_state_in.data_ptr(), ws.data_ptr(), ws_bytes, b, n, h, dk,
-                      _lib.stream_of(q.device))
+            if records is not None:
+                _lib.call("vsp_delta_scan_backward_recorded_bf16", q.data_ptr(), k.data_ptr(), v.data_ptr(),
+                          beta.data_ptr(), state.data_ptr(), go.data_ptr(), _lib.ptr(gs), _lib.ptr(mask),
+                          records.data_ptr(), records.numel(), dq.data_ptr(), dk_.data_ptr(), dv.data_ptr(),
+                          db.data_ptr(), d_state_in.data_ptr(), ws.data_ptr(), ws_bytes, b, n, h, dk,
+                          _lib.stream_of(q.device))
+            else:
+                _lib.call(entry, q.data_ptr(), k.data_ptr(), v.data_ptr(), beta.data_ptr(), state.data_ptr(),
+                          go.data_ptr(), _lib.ptr(gs), _lib.ptr(mask), dq.data_ptr(), dk_.data_ptr(), dv.data_ptr(),
+                          db.data_ptr(), d_state_in.data_ptr(), ws.data_ptr(), ws_bytes, b, n, h, dk,
+                          _lib.stream_of(q.device))
         need = ctx.needs_input_grad
         return (dq if need[0] else None, dk_ if need[1] else None, dv if need[2] else None,
                 db if need[3] else None, d_state_in if need[4] else None, None, None)
