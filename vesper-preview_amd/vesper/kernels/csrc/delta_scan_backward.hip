@@ -868,18 +868,52 @@ __device__ __forceinline__ bf16x8 frow2(const __bf16* X, int ld, int r0, int k0)
 __device__ __forceinline__ f32x4 mma32(bf16x8 a, bf16x8 b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
 }
-// an accumulator tile into a bf16 tile at (r0, c0)
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+template <int N> using vec_u32 = unsigned __attribute__((ext_vector_type(N)));
+// An accumulator tile in bf16 as 32-bit pairs of columns: lane (j, g) holds rows 4 g .. 4 g + 3 of
+// column j; after one exchange with the lane of column j ^ 1 (a DPP swap) the even lane holds rows
+// 4 g, 4 g + 1 and the odd lane rows 4 g + 2, 4 g + 3 of columns j & ~1 and (j & ~1) + 1, so a
+// tile goes out in two 4-byte writes a lane instead of four 2-byte ones (in LDS: no two lanes in
+// one 32-bit word, and the 64 lanes of a write on 64 distinct banks at the tiles' pitches).
+// Returns the two words and sets `row` to the first one's row within the tile. pair_words takes the
+// lane's four bf16 values as two words (rows 4 g, 4 g + 1 and rows 4 g + 2, 4 g + 3).
+__device__ __forceinline__ uint2 pair_words(uint32_t lo, uint32_t hi, int& row) {
+  const int l = threadIdx.x & 63, odd = l & 1;
+  const uint32_t own = odd ? hi : lo, send = odd ? lo : hi;
+  // quad_perm [1, 0, 3, 2]: the word of the neighbouring column
+  const uint32_t recv = (uint32_t)__builtin_amdgcn_mov_dpp((int)send, 0xB1, 0xF, 0xF, false);
+  const uint32_t first = odd ? recv : own, second = odd ? own : recv;
+  row = 4 * (l >> 4) + 2 * odd;
+  return uint2{__builtin_amdgcn_perm(second, first, 0x05040100u), __builtin_amdgcn_perm(second, first, 0x07060302u)};
+}
+__device__ __forceinline__ uint2 pair_cols(f32x4 acc, int& row) {
+  const bf16x2_t lo2 = {(__bf16)acc[0], (__bf16)acc[1]}, hi2 = {(__bf16)acc[2], (__bf16)acc[3]};
+  return pair_words(__builtin_bit_cast(uint32_t, lo2), __builtin_bit_cast(uint32_t, hi2), row);
+}
+// an accumulator tile into a bf16 tile at (r0, c0) (ld and c0 even)
 __device__ __forceinline__ void put_tile(__bf16* X, int ld, int r0, int c0, f32x4 acc) {
-#pragma unroll
-  for (int r = 0; r < 4; ++r) X[(r0 + tile_row(r)) * ld + c0 + tile_col()] = (__bf16)acc[r];
+  int row;
+  const uint2 w = pair_cols(acc, row);
+  __bf16* p = X + (r0 + row) * ld + c0 + (tile_col() & ~1);
+  *reinterpret_cast<uint32_t*>(p) = w.x;
+  *reinterpret_cast<uint32_t*>(p + ld) = w.y;
 }
 // an accumulator tile into rows t0 + r0 .. of a [B, N, H, D] tensor (rows past N skipped)
 template <typename TIn, int D>
 __device__ __forceinline__ void store_rows(TIn* dst, int b, int h, int t0, int N, int H, int r0, int c0, f32x4 acc) {
+  if constexpr (sizeof(TIn) == 2) {
+    int row;
+    const uint2 w = pair_cols(acc, row);
+    const int t = t0 + r0 + row;
+    TIn* p = dst + (((size_t)b * N + t) * H + h) * D + c0 + (tile_col() & ~1);
+    if (t < N) *reinterpret_cast<uint32_t*>(p) = w.x;
+    if (t + 1 < N) *reinterpret_cast<uint32_t*>(p + (size_t)H * D) = w.y;
+  } else {
 #pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    const int t = t0 + r0 + tile_row(r);
-    if (t < N) dst[(((size_t)b * N + t) * H + h) * D + c0 + tile_col()] = from_f32<TIn>(acc[r]);
+    for (int r = 0; r < 4; ++r) {
+      const int t = t0 + r0 + tile_row(r);
+      if (t < N) dst[(((size_t)b * N + t) * H + h) * D + c0 + tile_col()] = from_f32<TIn>(acc[r]);
+    }
   }
 }
 
@@ -913,7 +947,7 @@ struct ChunkRows16 {
 };
 
 // a [D][D] bf16 record in accumulator order (accfrag2: pairs of row tiles) into LDS [D][ld] bf16,
-// row-major
+// row-major (column pairs exchanged as put_tile does: a lane's units are the record's lane's)
 template <int D, int NTH>
 struct AccRows16 {
   static constexpr int NT = D / 16, NP = NT >= 2 ? NT / 2 : 1, EU = NT >= 2 ? 8 : 4;  // elements a unit
@@ -930,11 +964,14 @@ struct AccRows16 {
       const int e = threadIdx.x + NTH * it;  // = (slice NP + pair) 64 + lane
       if (kN % NTH == 0 || e < kN) {
         const int lane = e & 63, st = e >> 6, sl = st / NP, m = st - sl * NP;
+        const auto words = __builtin_bit_cast(vec_u32<EU / 2>, raw[it]);
 #pragma unroll
         for (int u = 0; u < EU / 4; ++u) {
-          const int row = 16 * (2 * m + u) + 4 * (lane >> 4), col = 16 * sl + (lane & 15);
-#pragma unroll
-          for (int r = 0; r < 4; ++r) dst[(row + r) * ld + col] = raw[it][4 * u + r];
+          int row;
+          const uint2 w = pair_words(words[2 * u], words[2 * u + 1], row);
+          __bf16* p = dst + (16 * (2 * m + u) + row) * ld + 16 * sl + ((lane & 15) & ~1);
+          *reinterpret_cast<uint32_t*>(p) = w.x;
+          *reinterpret_cast<uint32_t*>(p + ld) = w.y;
         }
       }
     }
