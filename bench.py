@@ -765,6 +765,32 @@ def traffic_probe(torch) -> None:
     print(json.dumps({"copy_bytes": COPY_BYTES}), flush=True)
 
 
+def traffic_probe_backward(torch) -> None:
+    """The copy of known size, then one training step of each mixer under autograd at its bench
+    shape (the scan at B8 T4096 H8 d64 bf16: the forward recording the chunks' starting states and
+    the backward reading them; window attention at B4 T4096 H8 D64 w512), for `rocprofv3 --pmc`."""
+    from vesper.kernels.delta_scan import delta_scan_fused
+    from vesper.kernels.window_attn import window_attention
+
+    dev = torch.device("cuda:0")
+    src = torch.ones(COPY_BYTES // 4, dtype=torch.float32, device=dev)
+    dst = torch.empty_like(src)
+    inputs = [t.requires_grad_() for t in scan_inputs(torch, dev)]
+    g = torch.Generator().manual_seed(8)
+    d_o = torch.randn(inputs[0].shape, generator=g).to(dev, torch.bfloat16)
+    d_s = torch.randn(inputs[4].shape, generator=g).to(dev)
+    aq, ak, av = (t.requires_grad_() for t in attn_inputs(torch, dev, b=ATTN_B))
+    d_a = torch.randn(aq.shape, generator=g).to(dev, torch.bfloat16)
+    with torch.no_grad():
+        dst.copy_(src)
+    o, s = delta_scan_fused(*inputs)
+    torch.autograd.backward([o, s], [d_o, d_s])
+    a = window_attention(aq, ak, av, WINDOW)
+    torch.autograd.backward([a], [d_a])
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_bytes": COPY_BYTES}), flush=True)
+
+
 def traffic_from_profiles(kernel: str) -> float | None:
     path = ROOT / "profiles" / "hbm_traffic.json"
     if not path.exists():
@@ -784,6 +810,8 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-decode", action="store_true")
     ap.add_argument("--no-loop", action="store_true")
+    ap.add_argument("--traffic-probe-backward", action="store_true",
+                    help="one training step of each mixer after a copy of known size, for rocprofv3 --pmc")
     ap.add_argument("--traffic-probe", action="store_true",
                     help="launch each kernel once plus a calibration copy, for rocprofv3 --pmc runs")
     args = ap.parse_args()
@@ -803,6 +831,9 @@ def main() -> int:
     _lib.library()  # fail loudly if the kernels are not built
     if args.traffic_probe:
         traffic_probe(torch)
+        return 0
+    if args.traffic_probe_backward:
+        traffic_probe_backward(torch)
         return 0
 
     pre = time_prefill(torch, args.steps, args.warmup)

@@ -991,7 +991,10 @@ __global__ __launch_bounds__(kChunkThreads) void scan_bwd_chunk_bf16_kernel(
   using T = __bf16;
   constexpr int NT = D / 16;  // column tiles of a [64 x D] result
   constexpr int NTH = kChunkThreads;
-  constexpr int LD = D + 8, L6 = kC + 8;  // pitches: [64][D] and [D][D], [64][64]
+  // pitches: [64][D] and [D][D], [64][64]; up to D 64 rows 40 banks apart (the row fragments'
+  // 16-byte reads then meet no bank twice: each two groups of eight lanes in one cycle cover the 64
+  // banks), at D 128 (LDS-bound) 68
+  constexpr int LD = D <= 64 ? D + 16 : D + 8, L6 = D <= 64 ? kC + 16 : kC + 8;
   // Up to D 64 the states H and G are LDS tiles. At D 128 they would not fit: their fragments come
   // from the chains' records in global memory (column order for H and G as B operands, the
   // transposed records for H^T and G^T), whose k order within 32 is 4 g .. 4 g + 3 of each 16-row
