@@ -48,10 +48,14 @@ __global__ __launch_bounds__(256, D >= 128 ? 2 : (CARRY && D == 64 ? 3 : 4)) voi
   constexpr int DT = DP / 16;          // 16-row tiles of O^T
   constexpr int KSQ = DP / 32;         // k steps over features
   constexpr int SEG = DP / 8;          // 16-byte segments per row
-  // LDS pitches (elements) against bank conflicts on the 64 banks: K rows carry one 16-byte pad
-  // segment (the 16 rows of a 16-byte row-fragment read start 36 banks apart at D 64), V rows two
-  // (the 8 rows of a transposed read start 8, 24 or 40 banks apart and cover all 64 banks)
-  constexpr int PK = DP + 8, PSEG = SEG + 1;
+  // LDS layouts against bank conflicts on the 64 banks. A 16-byte row-fragment read serves lanes
+  // 0-7 and 16-23 (then 8-15 and 24-31, ...) in one pass: at D 64 the K rows are unpadded and
+  // their 16-byte segments XOR-swizzled by row (segment s of row r at s ^ 2 ((r >> 1) & 3)), so
+  // the 16 lanes of a pass, rows 0-7 at two segments each, meet every bank once; a 36-bank pitch
+  // (one pad segment, kept at other widths) costs these reads a second pass. V rows carry two pad
+  // segments (the 8 rows of a transposed read start 8, 24 or 40 banks apart and cover all 64).
+  constexpr bool kSwzK = D == 64;
+  constexpr int PK = kSwzK ? DP : DP + 8, PSEG = kSwzK ? SEG : SEG + 1;
   constexpr int PV = DP + 16, PSEGV = SEG + 2;
   // At D >= 64 the tiles go from global memory straight into LDS: a wave instruction fills 1 KiB
   // of consecutive segments (pad segments re-read a real one and are never used); narrower heads,
@@ -65,6 +69,7 @@ __global__ __launch_bounds__(256, D >= 128 ? 2 : (CARRY && D == 64 ? 3 : 4)) voi
   __shared__ __align__(16) T sK0[KT * PK], sK1[KT * PK];
   __shared__ __align__(16) T sV0[KT * PV], sV1[KT * PV];
 
+  auto kswz = [](int row) { return kSwzK ? 2 * ((row >> 1) & 3) : 0; };  // K's segment swizzle
   const int lg = xcd_logical_block(blockIdx.x, gridDim.x);
   const int qt = lg % nqt, bh = lg / nqt;
   const int b = bh / H, h = bh - b * H;
@@ -141,8 +146,8 @@ __global__ __launch_bounds__(256, D >= 128 ? 2 : (CARRY && D == 64 ? 3 : 4)) voi
 #pragma unroll
   for (int j = 0; j < (kDirect ? NI : 1); ++j) {
     const int pos = (w + 4 * j) * 64 + l;  // padded segment position in the tile
-    const int row = pos / PSEG, seg = pos - row * PSEG;
-    koff[j] = (unsigned)(row * kv_row + 8 * (seg < SEG ? seg : 0)) * (unsigned)sizeof(T);
+    const int row = pos / PSEG, seg = pos - row * PSEG;  // LDS position: the segment it holds is seg ^ kswz(row)
+    koff[j] = (unsigned)(row * kv_row + 8 * (seg < SEG ? seg ^ kswz(row) : 0)) * (unsigned)sizeof(T);
     const int rowv = pos / PSEGV, segv = pos - rowv * PSEGV;
     voff[j] = (unsigned)(rowv * kv_row + 8 * (segv < SEG ? segv : 0)) * (unsigned)sizeof(T);
   }
@@ -158,7 +163,7 @@ __global__ __launch_bounds__(256, D >= 128 ? 2 : (CARRY && D == 64 ? 3 : 4)) voi
         const int row = pos / PSEG, seg = pos - row * PSEG;
         const int rowv = pos / PSEGV, segv = pos - rowv * PSEGV;
         const int key = min(k0 + row, S - 1), keyv = min(k0 + rowv, S - 1);
-        const size_t sk = (size_t)key * kv_row + 8 * (seg < SEG ? seg : 0);
+        const size_t sk = (size_t)key * kv_row + 8 * (seg < SEG ? seg ^ kswz(row) : 0);
         const size_t sv = (size_t)keyv * kv_row + 8 * (segv < SEG ? segv : 0);
         if (ins < NINS) load_lds16((((fresh >> (key - k0)) & 1) ? kbase : kcbase) + sk, Kn + ins * 64 * 8);
         if (ins < NINSV) load_lds16((((fresh >> (keyv - k0)) & 1) ? vbase : vcbase) + sv, Vn + ins * 64 * 8);
@@ -259,7 +264,7 @@ __global__ __launch_bounds__(256, D >= 128 ? 2 : (CARRY && D == 64 ? 3 : 4)) voi
         for (int qb = 0; qb < QB; ++qb) sacc[qb][kb] = zero4();
 #pragma unroll
         for (int st = 0; st < KSQ; ++st) {
-          const V8 a = *reinterpret_cast<const V8*>(Kt + (16 * kb + lq) * PK + 32 * st + 8 * g);
+          const V8 a = *reinterpret_cast<const V8*>(Kt + (16 * kb + lq) * PK + 8 * ((4 * st + g) ^ kswz(lq)));
 #pragma unroll
           for (int qb = 0; qb < QB; ++qb) sacc[qb][kb] = Mma<T>::run(a, qf[qb][st], sacc[qb][kb]);
         }
