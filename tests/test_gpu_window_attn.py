@@ -126,6 +126,42 @@ def test_refusals():
         window_attention(dq, dk_[:, :4], dv[:, :4], 4)
     with pytest.raises(ValueError, match="window"):
         window_attention(dq, dk_, dv, 0)
+    wide = torch.zeros(1, 8, 4, 136, dtype=BF16, device=GPU)
+    with pytest.raises(ContractError, match="exceeds"):
+        window_attention(wide, wide[:, :, :2], wide[:, :, :2], 4)
+
+
+@pytest.mark.parametrize("dk", [8, 24, 48, 96])
+def test_widths_between_the_kernels_run_zero_padded(dk):
+    """A head width the kernels do not tile runs with zero features up to the next one (scale
+    1 / sqrt(dk) kept): outputs and gradients against the oracle at that width, with a cache, grouped
+    KV heads and an active mask, and with carried keys and values."""
+    from vesper.kernels.window_attn import window_attention
+
+    n, m, w, h, hkv = 150, 30, 48, 4, 2
+    q, keys, values = _inputs(2, n, m, h, hkv, dk, seed=dk + 3)
+    active = torch.rand(2, n, generator=torch.Generator().manual_seed(dk)) < 0.7
+    want = oracle_window(q.double(), keys.double(), values.double(), w, active=active)
+    got = window_attention(q.to(GPU), keys.to(GPU), values.to(GPU), w, active=active.to(GPU))
+    assert got.shape == q.shape
+    _check(got, want)
+    up = torch.randn(2, n, h, dk, generator=torch.Generator().manual_seed(dk + 1)).to(BF16)
+    g_got = _grads(q, keys, values, w, up)
+    g_want = _oracle_grads(q, keys, values, w, up)
+    for a, b, name in zip(g_got, g_want, ("o", "dq", "dk", "dv")):
+        assert relative_error(a, b) < 1e-2, name
+    # carried keys and values: equal to the where-merged inputs
+    g = torch.Generator().manual_seed(dk + 2)
+    ck = torch.randn(2, n, hkv, dk, generator=g).to(BF16)
+    cv = torch.randn(2, n, hkv, dk, generator=g).to(BF16)
+    keep = active.reshape(2, n, 1, 1)
+    mk = torch.cat([keys[:, :m], torch.where(keep, keys[:, m:], ck)], dim=1)
+    mv = torch.cat([values[:, :m], torch.where(keep, values[:, m:], cv)], dim=1)
+    with torch.no_grad():
+        fused = window_attention(q.to(GPU), keys.to(GPU), values.to(GPU), w, active=active.to(GPU),
+                                 carried=(ck.to(GPU), cv.to(GPU)))
+        merged = window_attention(q.to(GPU), mk.to(GPU), mv.to(GPU), w, active=active.to(GPU))
+    assert torch.equal(fused, merged)
 
 
 def test_repeatable_and_captured_replays_equal_eager():

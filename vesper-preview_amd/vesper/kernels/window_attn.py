@@ -42,25 +42,26 @@ def _aligned(t: Tensor) -> Tensor:
 
 class _WindowAttention(torch.autograd.Function):
     @staticmethod
-    def forward(ctx: Any, q: Tensor, keys: Tensor, values: Tensor, window: int, mask: Tensor | None) -> Tensor:  # noqa: D102
+    def forward(ctx: Any, q: Tensor, keys: Tensor, values: Tensor, window: int, mask: Tensor | None,
+                scale: float) -> Tensor:  # noqa: D102
         b, n, h, dk = q.shape
         s, hkv = keys.shape[1], keys.shape[2]
         m = s - n
         suffix = "bf16" if q.dtype == torch.bfloat16 else "f16"
         if n == 0:
             ctx.save_for_backward(q, keys, values, q, q.new_empty(0))
-            ctx.meta = (window, m)
+            ctx.meta = (window, m, scale)
             return q.new_zeros(q.shape)
         qc, kc, vc = _aligned(q.detach()), _aligned(keys.detach()), _aligned(values.detach())
         o = torch.empty_like(qc)
-        args = (b, n, m, h, hkv, dk, int(window), 1.0 / math.sqrt(dk), _lib.stream_of(q.device))
+        args = (b, n, m, h, hkv, dk, int(window), scale, _lib.stream_of(q.device))
         with torch.cuda.device(q.device):
             if any(ctx.needs_input_grad[:3]):
                 lse = torch.empty(b, h, n, dtype=torch.float32, device=q.device)
                 _lib.call(f"vsp_window_attn_lse_{suffix}", qc.data_ptr(), kc.data_ptr(), vc.data_ptr(), o.data_ptr(),
                           lse.data_ptr(), _lib.ptr(mask), *args)
                 ctx.save_for_backward(qc, kc, vc, o, lse)
-                ctx.meta = (window, m)
+                ctx.meta = (window, m, scale)
             else:
                 _lib.call(f"vsp_window_attn_{suffix}", qc.data_ptr(), kc.data_ptr(), vc.data_ptr(), o.data_ptr(),
                           _lib.ptr(mask), *args)
@@ -69,11 +70,11 @@ class _WindowAttention(torch.autograd.Function):
     @staticmethod
     def backward(ctx: Any, grad_o: Tensor) -> tuple[Tensor | None, ...]:  # noqa: D102
         qc, kc, vc, o, lse = ctx.saved_tensors
-        window, m = ctx.meta
+        window, m, scale = ctx.meta
         b, n, h, dk = qc.shape
         hkv = kc.shape[2]
         if n == 0:
-            return torch.zeros_like(qc), torch.zeros_like(kc), torch.zeros_like(vc), None, None
+            return torch.zeros_like(qc), torch.zeros_like(kc), torch.zeros_like(vc), None, None, None
         go = _aligned(grad_o.to(qc.dtype))
         dq, dk_, dv = torch.empty_like(qc), torch.empty_like(kc), torch.empty_like(vc)
         workspace = torch.empty(b * h * n, dtype=torch.float32, device=qc.device)
@@ -81,13 +82,13 @@ class _WindowAttention(torch.autograd.Function):
         with torch.cuda.device(qc.device):
             _lib.call(f"vsp_window_attn_backward_{suffix}", qc.data_ptr(), kc.data_ptr(), vc.data_ptr(), o.data_ptr(),
                       go.data_ptr(), lse.data_ptr(), workspace.data_ptr(), dq.data_ptr(), dk_.data_ptr(), dv.data_ptr(),
-                      b, n, m, h, hkv, dk, int(window), 1.0 / math.sqrt(dk), _lib.stream_of(qc.device))
+                      b, n, m, h, hkv, dk, int(window), scale, _lib.stream_of(qc.device))
         return (dq if ctx.needs_input_grad[0] else None, dk_ if ctx.needs_input_grad[1] else None,
-                dv if ctx.needs_input_grad[2] else None, None, None)
+                dv if ctx.needs_input_grad[2] else None, None, None, None)
 
 
 def _carried_call(q: Tensor, keys: Tensor, values: Tensor, carried: tuple[Tensor, Tensor], window: int,
-                  mask: Tensor) -> Tensor:
+                  mask: Tensor, scale: float) -> Tensor:
     b, n, h, dk = q.shape
     s, hkv = keys.shape[1], keys.shape[2]
     qc, kc, vc = _aligned(q), _aligned(keys), _aligned(values)
@@ -96,8 +97,8 @@ def _carried_call(q: Tensor, keys: Tensor, values: Tensor, carried: tuple[Tensor
     suffix = "bf16" if q.dtype == torch.bfloat16 else "f16"
     with torch.cuda.device(q.device):
         _lib.call(f"vsp_window_attn_carried_{suffix}", qc.data_ptr(), kc.data_ptr(), vc.data_ptr(), kh.data_ptr(),
-                  vh.data_ptr(), o.data_ptr(), mask.data_ptr(), b, n, s - n, h, hkv, dk, int(window),
-                  1.0 / math.sqrt(dk), _lib.stream_of(q.device))
+                  vh.data_ptr(), o.data_ptr(), mask.data_ptr(), b, n, s - n, h, hkv, dk, int(window), scale,
+                  _lib.stream_of(q.device))
     return o
 
 
@@ -108,8 +109,10 @@ def window_attention(q: Tensor, keys: Tensor, values: Tensor, window: int, *, ac
     Raises:
         ContractError: on shapes that disagree, a dtype other than bfloat16/float16 (or mixed), a
             tensor off the GPU, ``h`` not a multiple of ``hkv``, a head width the kernel does not
-            tile, fewer key rows than queries, or carried keys and values without ``active`` or not
-            shaped ``[b, n, hkv, dk]`` in the dtype of ``keys``.
+            tile (above 128; narrower widths between the kernels' 16, 32, 64 and 128 run with zero
+            features added up to the next one, which change no score and no output), fewer key rows
+            than queries, or carried keys and values without ``active`` or not shaped
+            ``[b, n, hkv, dk]`` in the dtype of ``keys``.
         ValueError: if ``window`` is below 1.
     """
     if window < 1:
@@ -135,8 +138,9 @@ def window_attention(q: Tensor, keys: Tensor, values: Tensor, window: int, *, ac
         raise ContractError(f"keys hold {s} positions, fewer than the {n} queries")
     if h % hkv != 0:
         raise ContractError(f"{h} query heads are not a multiple of {hkv} KV heads")
-    if dk not in HEAD_DIMS:
-        raise ContractError(f"head dimension {dk} is not one the kernel tiles ({HEAD_DIMS})")
+    width = next((w for w in HEAD_DIMS if w >= dk), None)
+    if width is None:
+        raise ContractError(f"head dimension {dk} exceeds the kernel's {HEAD_DIMS[-1]}")
     mask = None
     if active is not None:
         check_shape("active", active, ("b", "n"), {"b": b, "n": n}, torch.bool)
@@ -153,11 +157,24 @@ def window_attention(q: Tensor, keys: Tensor, values: Tensor, window: int, *, ac
                 raise ContractError(f"carried {name}: {tuple(held.shape)} {held.dtype} on {held.device}, "
                                     f"want {(b, n, hkv, dk)} {q.dtype} on {q.device}")
         if n > 0 and not (torch.is_grad_enabled() and any(t.requires_grad for t in (q, keys, values, *carried))):
-            return _carried_call(q, keys, values, carried, window, mask)
+            if width != dk:
+                pad = (0, width - dk)
+                q, keys, values = (torch.nn.functional.pad(t, pad) for t in (q, keys, values))
+                carried = (torch.nn.functional.pad(carried[0], pad), torch.nn.functional.pad(carried[1], pad))
+                return _carried_call(q, keys, values, carried, window, mask, 1.0 / math.sqrt(dk))[..., :dk].contiguous()
+            return _carried_call(q, keys, values, carried, window, mask, 1.0 / math.sqrt(dk))
         # under autograd the merge is explicit, so the gradient reaches the carried tensors
         keep = active.reshape(b, n, 1, 1)
         m = s - n
         keys = torch.cat([keys[:, :m], torch.where(keep, keys[:, m:], carried[0])], dim=1)
         values = torch.cat([values[:, :m], torch.where(keep, values[:, m:], carried[1])], dim=1)
-    out: Tensor = _WindowAttention.apply(q, keys, values, int(window), mask)
+    if width != dk:
+        # zero features of q, keys and values add zero to every score and give zero outputs there
+        # (the scale stays 1 / sqrt(dk)); the padding's outputs are dropped, its gradients never
+        # reach the inputs
+        pad = (0, width - dk)
+        qp, kp, vp = (torch.nn.functional.pad(t, pad) for t in (q, keys, values))
+        padded: Tensor = _WindowAttention.apply(qp, kp, vp, int(window), mask, 1.0 / math.sqrt(dk))
+        return padded[..., :dk].contiguous()
+    out: Tensor = _WindowAttention.apply(q, keys, values, int(window), mask, 1.0 / math.sqrt(dk))
     return out
