@@ -100,7 +100,10 @@ __global__ __launch_bounds__(64 * NW) void attn_dq_kernel(const T* __restrict__ 
   constexpr int KT = 64;
   __shared__ __align__(16) T sK[2][KT * Sh::P];
   __shared__ __align__(16) T sV[2][KT * Sh::P];
-  const int qt = blockIdx.x % nqt, bh = blockIdx.x / nqt;
+  // consecutive query tiles of a head on one XCD: their key windows overlap, so most of each
+  // tile's K and V reads hit that XCD's L2
+  const int lg = xcd_logical_block(blockIdx.x, gridDim.x);
+  const int qt = lg % nqt, bh = lg / nqt;
   const int b = bh / H, h = bh - b * H;
   const int kvh = h / (H / HKV);
   const int w = threadIdx.x >> 6, l = threadIdx.x & 63;
@@ -235,7 +238,9 @@ __global__ __launch_bounds__(64 * NW, WAVES_PER_SIMD) void attn_dkv_kernel(const
   __shared__ __align__(16) T sQ[2][64 * Sh::P];
   __shared__ __align__(16) T sD[2][64 * Sh::P];
   __shared__ __align__(16) float sL[2][64], sS[2][64];
-  const int kt = blockIdx.x % nkt, bkv = blockIdx.x / nkt;
+  // consecutive key tiles of a KV head on one XCD: their query ranges overlap (L2 hits for Q, dO)
+  const int lg = xcd_logical_block(blockIdx.x, gridDim.x);
+  const int kt = lg % nkt, bkv = lg / nkt;
   const int b = bkv / HKV, kvh = bkv - b * HKV;
   const int G = H / HKV;
   const int w = threadIdx.x >> 6, l = threadIdx.x & 63;
