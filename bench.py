@@ -4,7 +4,8 @@
 A step is one prefill pass of both mixers over one batch of synthetic input: the delta-rule scan
 (B=8, T=4096, H=8, d=64; bf16 q/k/v/beta, fp32 state with S0 ~ N(0, 0.02^2), chunk 64) followed by
 sliding-window causal attention over the same batch shape (window 512, bf16). ``value`` is prefill
-tokens/s = B*T / (time of one step), inputs resident in HBM. Beside it the line carries each
+tokens/s = B*T / (time of one step), inputs resident in HBM, the timed steps run as one captured HIP
+graph (the eager loop's time, with the host's gaps between launches, is reported beside it). Beside it the line carries each
 kernel's own rate at its own configuration (attention alone at B=4), the key filter that feeds the
 scan (B8 T4096 d512 = 8 heads of 64, 4 taps, bf16), the decode rate (256
 single-token steps of batch 64: fp32 delta update of S [64,8,64,64] then attention over a 512-entry
@@ -112,37 +113,86 @@ def attn_inputs(torch, dev, b=B, t=T, h=H, d=D, seed=1):
 
 
 # ---- GPU legs -------------------------------------------------------------------------------------
+def captured_ms(torch, fn, count: int, replays: int = 1) -> float:
+    """Milliseconds per call of ``fn`` with ``count`` calls captured in one HIP graph: the graph is
+    replayed once untimed, then ``replays`` times back to back between two events on the stream
+    (median per-call time when ``replays`` > 1 is taken over single replays)."""
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        fn()
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for _ in range(count):
+            fn()
+    graph.replay()
+    torch.cuda.synchronize()
+    times = []
+    for _ in range(replays):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        graph.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        times.append(e0.elapsed_time(e1) / count)
+    return statistics.median(times)
+
+
 def time_prefill(torch, steps: int, warmup: int) -> dict:
+    """The prefill step (the scan, then window attention, over the bench batch). The timed steps
+    run as one HIP graph of ``steps`` steps (each step's kernels launched back to back by the
+    device, as a captured training or serving loop runs them), between a synchronize and events on
+    the stream; the scan and the attention alone are timed the same way (graphs of 10 launches,
+    median of 5 replays). The eager loop (one Python call per mixer, events around each) is timed
+    too: its gaps between launches are the host's."""
     from vesper.kernels.delta_scan import delta_scan_fused
     from vesper.kernels.window_attn import window_attention
 
     dev = torch.device("cuda:0")
     q, k, v, beta, s0 = scan_inputs(torch, dev)
     aq, ak, av = attn_inputs(torch, dev)
+
+    def scan():
+        delta_scan_fused(q, k, v, beta, s0)
+
+    def attn():
+        window_attention(aq, ak, av, WINDOW)
+
+    def step():
+        scan()
+        attn()
+
     with torch.no_grad():
         for _ in range(warmup):
-            delta_scan_fused(q, k, v, beta, s0)
-            window_attention(aq, ak, av, WINDOW)
-        ev = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(steps)]
+            step()
         torch.cuda.synchronize()
-        t0 = time.perf_counter()
+        # eager: events around each call
+        ev = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(steps)]
         for i in range(steps):
             ev[i][0].record()
-            delta_scan_fused(q, k, v, beta, s0)
+            scan()
             ev[i][1].record()
-            window_attention(aq, ak, av, WINDOW)
+            attn()
             ev[i][2].record()
         torch.cuda.synchronize()
+        # captured: exactly `steps` steps in one graph, timed over one replay
+        t0 = time.perf_counter()
+        step_ms = captured_ms(torch, step, steps)
         wall = time.perf_counter() - t0
-    scan_ms = [e[0].elapsed_time(e[1]) for e in ev]
-    attn_ms = [e[1].elapsed_time(e[2]) for e in ev]
-    step_ms = [e[0].elapsed_time(e[2]) for e in ev]
-    return {"wall_s": wall, "scan_ms": statistics.mean(scan_ms), "attn_ms": statistics.mean(attn_ms),
-            "step_ms": statistics.mean(step_ms), "scan_ms_median": statistics.median(scan_ms),
-            "attn_ms_median": statistics.median(attn_ms)}
+        scan_ms = captured_ms(torch, scan, 10, 5)
+        attn_ms = captured_ms(torch, attn, 10, 5)
+    e_scan = [e[0].elapsed_time(e[1]) for e in ev]
+    e_attn = [e[1].elapsed_time(e[2]) for e in ev]
+    e_step = [e[0].elapsed_time(e[2]) for e in ev]
+    return {"wall_s": wall, "step_ms": step_ms, "scan_ms": scan_ms, "attn_ms": attn_ms,
+            "eager_step_ms": statistics.median(e_step), "eager_scan_ms": statistics.median(e_scan),
+            "eager_attn_ms": statistics.median(e_attn)}
 
 
-def time_attention_config(torch, reps: int = 20) -> float:
+def time_attention_config(torch) -> float:
+    """Milliseconds per launch of window attention at B4 T4096 H8 D64 w512 (bf16), in a HIP graph
+    of 10 launches (median of 5 replays)."""
     from vesper.kernels.window_attn import window_attention
 
     dev = torch.device("cuda:0")
@@ -150,14 +200,7 @@ def time_attention_config(torch, reps: int = 20) -> float:
     with torch.no_grad():
         for _ in range(3):
             window_attention(aq, ak, av, WINDOW)
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        torch.cuda.synchronize()
-        e0.record()
-        for _ in range(reps):
-            window_attention(aq, ak, av, WINDOW)
-        e1.record()
-        torch.cuda.synchronize()
-    return e0.elapsed_time(e1) / reps
+        return captured_ms(torch, lambda: window_attention(aq, ak, av, WINDOW), 10, 5)
 
 
 def time_key_filter(torch, reps: int = 50) -> tuple[float, float]:
@@ -851,21 +894,21 @@ def main() -> int:
     looped = None if args.no_loop else time_looped(torch)
     col_dec = None if args.no_decode else time_column_decode(torch)
 
-    # the dominant kernel by its median launch time over the timed steps (a mean can carry a few
-    # slow first launches)
-    scan_dominant = pre["scan_ms_median"] >= pre["attn_ms_median"]
+    # the dominant kernel by its time per launch in a graph of 10 launches (median of 5 replays)
+    scan_dominant = pre["scan_ms"] >= pre["attn_ms"]
     if scan_dominant:
-        name, ms, nbytes, flops = "delta_scan (prep + chain kernels)", pre["scan_ms_median"], s_bytes, s_flops
+        name, ms, nbytes, flops = "delta_scan (prep + chain kernels)", pre["scan_ms"], s_bytes, s_flops
         traffic = traffic_from_profiles("delta_scan")
     else:
-        name, ms, nbytes, flops = "window_attn_kernel", pre["attn_ms_median"], a_bytes, a_flops
+        name, ms, nbytes, flops = "window_attn_kernel", pre["attn_ms"], a_bytes, a_flops
         traffic = traffic_from_profiles("window_attn")
     achieved = nbytes / (ms / 1e3) / 1e9
     roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic, "kernel": name,
                 "algorithmic_bytes": nbytes, "algorithmic_flops": flops,
                 "mfma_frac_bf16": round(flops / (ms / 1e3) / 1e12 / BF16_PEAK_TFLOPS, 4),
-                "avg_launch_ms": round(ms, 4), "launch_ms_statistic": "median over the timed steps"}
+                "avg_launch_ms": round(ms, 4),
+                "launch_ms_statistic": "per launch in a HIP graph of 10, median of 5 replays"}
 
     result = {
         "metric": "delta-scan+window-attn prefill tok/s @T=4096; decode tok/s; % of roofline",
@@ -887,8 +930,9 @@ def main() -> int:
         },
         "kernels": {
             "delta_scan_ms": round(pre["scan_ms"], 4),
-            "delta_scan_ms_median": round(pre["scan_ms_median"], 4),
-            "window_attn_b8_ms_median": round(pre["attn_ms_median"], 4),
+            "prefill_step_eager_ms": round(pre["eager_step_ms"], 4),
+            "delta_scan_eager_ms": round(pre["eager_scan_ms"], 4),
+            "window_attn_b8_eager_ms": round(pre["eager_attn_ms"], 4),
             "delta_scan_tok_s": round(B * T / (pre["scan_ms"] / 1e3), 1),
             "delta_scan_hbm_frac": round(s_bytes / (pre["scan_ms"] / 1e3) / 1e9 / HBM_PEAK_GBS, 4),
             "delta_scan_mfma_frac_bf16": round(s_flops / (pre["scan_ms"] / 1e3) / 1e12 / BF16_PEAK_TFLOPS, 4),
@@ -965,7 +1009,8 @@ def main() -> int:
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(torch)
         result["cpu_legs"] = cpu_legs(torch)
-    log(f"prefill step {pre['step_ms']:.3f} ms (scan {pre['scan_ms']:.3f}, attn {pre['attn_ms']:.3f}), wall {pre['wall_s']:.2f} s")
+    log(f"prefill step {pre['step_ms']:.4f} ms captured, {pre['eager_step_ms']:.4f} eager (scan {pre['scan_ms']:.4f}, "
+        f"attn {pre['attn_ms']:.4f}), wall {pre['wall_s']:.2f} s")
     print(json.dumps(result), flush=True)
     return 0
 
