@@ -226,7 +226,7 @@ __global__ __launch_bounds__(64 * NW) void attn_dq_kernel(const T* __restrict__ 
   }
 }
 
-template <typename T, int D, int NW, int WAVES_PER_SIMD>
+template <typename T, int D, int NW, int WAVES_PER_SIMD, int KB>
 __global__ __launch_bounds__(64 * NW, WAVES_PER_SIMD) void attn_dkv_kernel(const T* __restrict__ q, const T* __restrict__ keys,
                                                        const T* __restrict__ values, const T* __restrict__ dout,
                                                        const float* __restrict__ lse, const float* __restrict__ dsum,
@@ -246,35 +246,42 @@ __global__ __launch_bounds__(64 * NW, WAVES_PER_SIMD) void attn_dkv_kernel(const
   const int w = threadIdx.x >> 6, l = threadIdx.x & 63;
   const int lq = l & 15, g = l >> 4;
   const int S = M + N;
-  const int k0 = 16 * NW * kt;
-  const int key = k0 + 16 * w + lq;  // this lane's key
-  const bool kok = key < S;
-  const size_t krow = (((size_t)b * S + (kok ? key : 0)) * HKV + kvh) * D;
-
-  V8 kf[Sh::KSQ], vf[Sh::KSQ];
+  // each wave holds KB blocks of 16 keys, so every Q or dO fragment it reads from LDS feeds KB
+  // MFMAs (and a workgroup's staged query tiles serve 16 NW KB keys)
+  const int k0 = 16 * NW * KB * kt;
+  int key[KB];
+  bool kok[KB];
+  size_t krow[KB];
+  V8 kf[KB][Sh::KSQ], vf[KB][Sh::KSQ];
+  f32x4 dka[KB][Sh::DT], dva[KB][Sh::DT];
 #pragma unroll
-  for (int s = 0; s < Sh::KSQ; ++s) {
-    const int f = 32 * s + 8 * g;
-    if (kok && f < D) {
-      kf[s] = *reinterpret_cast<const V8*>(keys + krow + f);
-      vf[s] = *reinterpret_cast<const V8*>(values + krow + f);
-    } else {
+  for (int kb = 0; kb < KB; ++kb) {
+    key[kb] = k0 + 16 * (KB * w + kb) + lq;  // this lane's key of block kb
+    kok[kb] = key[kb] < S;
+    krow[kb] = (((size_t)b * S + (kok[kb] ? key[kb] : 0)) * HKV + kvh) * D;
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        kf[s][e] = from_f32<T>(0.f);
-        vf[s][e] = from_f32<T>(0.f);
+    for (int s = 0; s < Sh::KSQ; ++s) {
+      const int f = 32 * s + 8 * g;
+      if (kok[kb] && f < D) {
+        kf[kb][s] = *reinterpret_cast<const V8*>(keys + krow[kb] + f);
+        vf[kb][s] = *reinterpret_cast<const V8*>(values + krow[kb] + f);
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          kf[kb][s][e] = from_f32<T>(0.f);
+          vf[kb][s][e] = from_f32<T>(0.f);
+        }
       }
     }
-  }
-  f32x4 dka[Sh::DT], dva[Sh::DT];
 #pragma unroll
-  for (int t = 0; t < Sh::DT; ++t) {
-    dka[t] = zero4();
-    dva[t] = zero4();
+    for (int t = 0; t < Sh::DT; ++t) {
+      dka[kb][t] = zero4();
+      dva[kb][t] = zero4();
+    }
   }
-  // the queries that see the tile's keys: M + i in [k0, k0 + 63 + W - 1]
-  const int ilo = max(0, k0 - M), ihi = min(N - 1, k0 + 16 * NW - 1 + W - 1 - M);
-  const int wk0 = k0 + 16 * w, wk1 = wk0 + 15;
+  // the queries that see the tile's keys: M + i in [k0, k0 + 16 NW KB - 1 + W - 1]
+  const int ilo = max(0, k0 - M), ihi = min(N - 1, k0 + 16 * NW * KB - 1 + W - 1 - M);
+  const int wk0 = k0 + 16 * KB * w, wk1 = wk0 + 16 * KB - 1;
   const size_t q_ld = (size_t)H * D;
   // the (query head, 64-query tile) steps of the group, in order; each step's Q and dO tiles (and
   // its lse, Dsum) are fetched into registers a step ahead and written to the other LDS buffer
@@ -317,56 +324,73 @@ __global__ __launch_bounds__(64 * NW, WAVES_PER_SIMD) void attn_dkv_kernel(const
       const bool full = M + i0 >= wk1 && M + i0 + 63 - wk0 < W;
 #pragma unroll
       for (int qp = 0; qp < 2; ++qp) {
-        V8 pb, dsb;
+        V8 pb[KB], dsb[KB];
 #pragma unroll
         for (int qb = 0; qb < 2; ++qb) {
           const int r0 = 32 * qp + 16 * qb;
-          f32x4 st = zero4(), dp = zero4();
+          f32x4 st[KB], dp[KB];
+#pragma unroll
+          for (int kb = 0; kb < KB; ++kb) st[kb] = dp[kb] = zero4();
 #pragma unroll
           for (int s = 0; s < Sh::KSQ; ++s) {
-            st = Mma<T>::run(row_frag<T, D>(tQ, r0, s), kf[s], st);
-            dp = Mma<T>::run(row_frag<T, D>(tD, r0, s), vf[s], dp);
+            const V8 qa = row_frag<T, D>(tQ, r0, s), da = row_frag<T, D>(tD, r0, s);
+#pragma unroll
+            for (int kb = 0; kb < KB; ++kb) {
+              st[kb] = Mma<T>::run(qa, kf[kb][s], st[kb]);
+              dp[kb] = Mma<T>::run(da, vf[kb][s], dp[kb]);
+            }
           }
           // lane (lq, g) holds queries r0 + 4 g + r of its key; dS without the scale (applied to dK
           // at the end)
           const f32x4 lv = *reinterpret_cast<const f32x4*>(tL + r0 + 4 * g);
           const f32x4 sv = *reinterpret_cast<const f32x4*>(tS + r0 + 4 * g);
-          float p[4];
 #pragma unroll
-          for (int r = 0; r < 4; ++r) p[r] = __builtin_amdgcn_exp2f(__builtin_fmaf(st[r], scale_log2, -lv[r]));
-          if (!full) {
+          for (int kb = 0; kb < KB; ++kb) {
+            float p[4];
 #pragma unroll
-            for (int r = 0; r < 4; ++r) p[r] = (unsigned)(M + i0 + r0 + 4 * g + r - key) < (unsigned)W ? p[r] : 0.f;
-          }
+            for (int r = 0; r < 4; ++r) p[r] = __builtin_amdgcn_exp2f(__builtin_fmaf(st[kb][r], scale_log2, -lv[r]));
+            if (!full) {
 #pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            pb[4 * qb + r] = from_f32<T>(p[r]);
-            dsb[4 * qb + r] = from_f32<T>(p[r] * (dp[r] - sv[r]));
+              for (int r = 0; r < 4; ++r)
+                p[r] = (unsigned)(M + i0 + r0 + 4 * g + r - key[kb]) < (unsigned)W ? p[r] : 0.f;
+            }
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              pb[kb][4 * qb + r] = from_f32<T>(p[r]);
+              dsb[kb][4 * qb + r] = from_f32<T>(p[r] * (dp[kb][r] - sv[r]));
+            }
           }
         }
 #pragma unroll
         for (int t = 0; t < Sh::DT; ++t) {
-          dva[t] = Mma<T>::run(tr_frag<T, D>(tD, 32 * qp, t), pb, dva[t]);
-          dka[t] = Mma<T>::run(tr_frag<T, D>(tQ, 32 * qp, t), dsb, dka[t]);
+          const V8 da = tr_frag<T, D>(tD, 32 * qp, t), qa = tr_frag<T, D>(tQ, 32 * qp, t);
+#pragma unroll
+          for (int kb = 0; kb < KB; ++kb) {
+            dva[kb][t] = Mma<T>::run(da, pb[kb], dva[kb][t]);
+            dka[kb][t] = Mma<T>::run(qa, dsb[kb], dka[kb][t]);
+          }
         }
       }
     }
     if (step + 1 < nsteps) put_step(step + 1, buf ^ 1);
     __syncthreads();
   }
-  if (kok) {
 #pragma unroll
-    for (int t = 0; t < Sh::DT; ++t) {
-      const int d = 16 * t + 4 * g;
-      if (d < D) {
-        V4 a, c;
+  for (int kb = 0; kb < KB; ++kb) {
+    if (kok[kb]) {
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          a[r] = from_f32<T>(dka[t][r] * scale);
-          c[r] = from_f32<T>(dva[t][r]);
+      for (int t = 0; t < Sh::DT; ++t) {
+        const int d = 16 * t + 4 * g;
+        if (d < D) {
+          V4 a, c;
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            a[r] = from_f32<T>(dka[kb][t][r] * scale);
+            c[r] = from_f32<T>(dva[kb][t][r]);
+          }
+          *reinterpret_cast<V4*>(dk + krow[kb] + d) = a;
+          *reinterpret_cast<V4*>(dv + krow[kb] + d) = c;
         }
-        *reinterpret_cast<V4*>(dk + krow + d) = a;
-        *reinterpret_cast<V4*>(dv + krow + d) = c;
       }
     }
   }
@@ -376,15 +400,18 @@ template <typename T, int D>
 void launch_backward(const T* q, const T* keys, const T* values, const T* o, const T* dout, const float* lse, float* dsum,
                      T* dq, T* dk, T* dv, int B, int N, int M, int H, int HKV, int W, float scale, hipStream_t stream) {
   const float scale_log2 = scale * 1.4426950408889634f;
-  // waves a workgroup (16 queries, 16 keys a wave); the dK/dV kernel's bound asks for 2 waves a
-  // SIMD at least (256 VGPRs), its D 64 instance takes 126 and so runs 4 (two workgroups a CU)
-  constexpr int kDqWaves = 8, kDkvWaves = 8, kDkvWavesPerSimd = 2;
+  // waves a workgroup (16 queries a dQ wave, 16 KB keys a dK/dV wave); the dK/dV kernel's bound
+  // asks for 2 waves a SIMD at least (256 VGPRs): its D 64 instance takes 126 and so runs 4 (two
+  // workgroups a CU). Two key blocks a wave (each Q, dO fragment feeding two MFMAs) took 202
+  // VGPRs, halving that, and ran slower (dK/dV 67 -> 77 us at B4 T4096 H8 d64 w512).
+  constexpr int kDqWaves = 8, kDkvWaves = 8, kDkvWavesPerSimd = 2, kDkvBlocks = 1;
   const int nqt = (N + 16 * kDqWaves - 1) / (16 * kDqWaves);
-  const int nkt = (M + N + 16 * kDkvWaves - 1) / (16 * kDkvWaves);
+  const int nkt = (M + N + 16 * kDkvWaves * kDkvBlocks - 1) / (16 * kDkvWaves * kDkvBlocks);
   hipLaunchKernelGGL((attn_dq_kernel<T, D, kDqWaves>), dim3((unsigned)((size_t)nqt * H * B)), dim3(64 * kDqWaves), 0,
                      stream, q, keys,
                      values, o, dout, lse, dsum, dq, N, M, H, HKV, W, scale, scale_log2, nqt);
-  hipLaunchKernelGGL((attn_dkv_kernel<T, D, kDkvWaves, kDkvWavesPerSimd>), dim3((unsigned)((size_t)nkt * HKV * B)),
+  hipLaunchKernelGGL((attn_dkv_kernel<T, D, kDkvWaves, kDkvWavesPerSimd, kDkvBlocks>),
+                     dim3((unsigned)((size_t)nkt * HKV * B)),
                      dim3(64 * kDkvWaves), 0, stream, q, keys,
                      values, dout, lse, dsum, dk, dv, N, M, H, HKV, W, scale, scale_log2, nkt);
 }
