@@ -982,15 +982,24 @@ struct AccRows16 {
 // every other column tile from ch = w / 4. Products run over their full k range, unrolled: the
 // triangular factors hold exact zeros where they vanish, and straight-line code lets the compiler
 // issue a stage's LDS reads ahead of its MFMAs.
+// Threads of the bf16 chunk kernel: eight waves (two a SIMD, two tiles of every [64 x 64] product
+// each). Sixteen at width 64 (four a SIMD, one tile each) measured slower: the 128-register bound
+// of four waves a SIMD spilled (chunk kernel 115 -> 139 us at B8 T4096 H8 d64).
+template <int D> struct ChunkShape {
+  static constexpr int NTH = 512;
+  static constexpr int NW = NTH / 64;
+  static constexpr int NCH = NW / 4;  // column groups: a wave's column tiles are ch, ch + NCH, ...
+};
+
 template <int D>
-__global__ __launch_bounds__(kChunkThreads) void scan_bwd_chunk_bf16_kernel(
+__global__ __launch_bounds__(ChunkShape<D>::NTH) void scan_bwd_chunk_bf16_kernel(
     const __bf16* __restrict__ q, const __bf16* __restrict__ k, const __bf16* __restrict__ v,
     const __bf16* __restrict__ beta, const __bf16* __restrict__ d_o, const uint8_t* __restrict__ active,
     const float* __restrict__ ws, const __bf16* __restrict__ hrec, __bf16* __restrict__ dq, __bf16* __restrict__ dk,
     __bf16* __restrict__ dv, __bf16* __restrict__ dbeta, int N, int H, int NC, int total) {
   using T = __bf16;
   constexpr int NT = D / 16;  // column tiles of a [64 x D] result
-  constexpr int NTH = kChunkThreads;
+  constexpr int NTH = ChunkShape<D>::NTH, NCH = ChunkShape<D>::NCH;
   // pitches: [64][D] and [D][D], [64][64]; up to D 64 rows 40 banks apart (the row fragments'
   // 16-byte reads then meet no bank twice: each two groups of eight lanes in one cycle cover the 64
   // banks), at D 128 (LDS-bound) 68
@@ -1004,13 +1013,15 @@ __global__ __launch_bounds__(kChunkThreads) void scan_bwd_chunk_bf16_kernel(
   __shared__ __align__(16) T sDRx[kHGinLDS ? kC * LD : 1];
   __shared__ __align__(16) T sH[kHGinLDS ? D * LD : 1], sG[kHGinLDS ? D * LD : 1];
   T* sDR = kHGinLDS ? sDRx : sR;
-  constexpr int kU = kHGinLDS ? NT / 2 : 1;  // column tiles unrolled (D 128: one, for the registers)
+  constexpr int kU = kHGinLDS ? NT / NCH : 1;  // column tiles unrolled (D 128: one, for the registers)
   __shared__ __align__(16) T sT[kC * L6], sL[kC * L6], sP[kC * L6], sM[kC * L6];
-  __shared__ float sB[kC], sPart[4 * kC], sRow[2 * kC];
+  __shared__ float sB[kC], sPart[4 * kC], sRow[NCH * kC];
   T* sX1 = sT;   // X1 = L^T dL once T is done with
   T* sS2 = sP;   // S2 = tril(dO Delta^T) once P is done with
   T* sDL = sM;   // dL, then M = diag(beta) dA
-  const int w = threadIdx.x >> 6, ch = w >> 2, rb = ch == 0 ? w : 7 - w, r0 = 16 * rb;
+  // wave w: column group ch = w / 4 and row block rb; the waves of one SIMD (w, w + 4, ...) take
+  // row blocks rb and 3 - rb in turn, which evens out the triangular products' work
+  const int w = threadIdx.x >> 6, ch = w >> 2, rb = (ch & 1) == 0 ? (w & 3) : 3 - (w & 3), r0 = 16 * rb;
   // A workgroup walks chunks blockIdx.x, + gridDim.x, ...: the next chunk's operands are loaded
   // into registers while the current one is computed.
   ChunkRows16<D, NTH> rq, rk, ro, rv;
@@ -1022,7 +1033,7 @@ __global__ __launch_bounds__(kChunkThreads) void scan_bwd_chunk_bf16_kernel(
     const int b = bh / H, h = bh - b * H;
     const int t0 = c * kC;
     const T* gL = reinterpret_cast<const T*>(Ws<D>::L(const_cast<float*>(ws), cid));
-    lraw = *reinterpret_cast<const bf16x8*>(gL + 8 * threadIdx.x);  // [64][64]: 8 a thread
+    lraw = *reinterpret_cast<const bf16x8*>(gL + 8 * min((int)threadIdx.x, kC * kC / 8 - 1));  // [64][64]: 8 a thread
     rq.fetch(q, b, h, t0, N, H);
     rk.fetch(k, b, h, t0, N, H);
     ro.fetch(d_o, b, h, t0, N, H, active);
@@ -1073,10 +1084,10 @@ __global__ __launch_bounds__(kChunkThreads) void scan_bwd_chunk_bf16_kernel(
       mh.put(sH, LD);
       mg.put(sG, LD);
     }
-    *reinterpret_cast<bf16x8*>(sL + (threadIdx.x >> 3) * L6 + 8 * (threadIdx.x & 7)) = lraw;
+    if (threadIdx.x < kC * kC / 8) *reinterpret_cast<bf16x8*>(sL + (threadIdx.x >> 3) * L6 + 8 * (threadIdx.x & 7)) = lraw;
     rbeta.put(sB, t0, N);
   }
-  static_assert(kChunkThreads * 8 == kC * kC, "one 16-byte piece of L a thread");
+  static_assert(NTH * 8 >= kC * kC, "one 16-byte piece of L a thread at most");
   __syncthreads();
   if constexpr (kHGinLDS) fetch(min(cid + (int)gridDim.x, total - 1));  // (the last chunk again past the end)
   // T = L diag(beta)
@@ -1089,8 +1100,8 @@ __global__ __launch_bounds__(kChunkThreads) void scan_bwd_chunk_bf16_kernel(
   }
   // R = V - K H in place (each lane reads only its own V entries)
 #pragma unroll kU
-  for (int u_ = 0; u_ < NT / 2; ++u_) {
-    const int ct = ch + 2 * u_;
+  for (int u_ = 0; u_ < NT / NCH; ++u_) {
+    const int ct = ch + NCH * u_;
     f32x4 acc = zero4();
     #pragma unroll
     for (int kk = 0; kk < D; kk += 32) acc = mma32(arow(sK, kk), bcol(gH, sH, ct, kk), acc);
@@ -1102,8 +1113,8 @@ __global__ __launch_bounds__(kChunkThreads) void scan_bwd_chunk_bf16_kernel(
   }
   // P = tril(Q K^T), diagonal included
   #pragma unroll
-  for (int u_ = 0; u_ < 2; ++u_) {
-    const int ct = ch + 2 * u_;
+  for (int u_ = 0; u_ < 4 / NCH; ++u_) {
+    const int ct = ch + NCH * u_;
     f32x4 acc = zero4();
     if (ct <= rb)
       #pragma unroll
@@ -1115,8 +1126,8 @@ __global__ __launch_bounds__(kChunkThreads) void scan_bwd_chunk_bf16_kernel(
   __syncthreads();
   // Delta = T R; dDelta = K G + P^T dO
 #pragma unroll kU
-  for (int u_ = 0; u_ < NT / 2; ++u_) {
-    const int ct = ch + 2 * u_;
+  for (int u_ = 0; u_ < NT / NCH; ++u_) {
+    const int ct = ch + NCH * u_;
     f32x4 d = zero4(), dd = zero4();
     #pragma unroll
     for (int kk = 0; kk < kC; kk += 32) d = mma32(frow(sT, L6, r0, kk), fcol(sR, LD, 16 * ct, kk), d);
@@ -1132,8 +1143,8 @@ __global__ __launch_bounds__(kChunkThreads) void scan_bwd_chunk_bf16_kernel(
   // row block into sPart), dL = tril(dT) diag(beta); then dR = T^T dDelta (= dV; kept negated for
   // dK, over R at D 128 once every dT tile has read R)
   #pragma unroll
-  for (int u_ = 0; u_ < 2; ++u_) {
-    const int ct = ch + 2 * u_;
+  for (int u_ = 0; u_ < 4 / NCH; ++u_) {
+    const int ct = ch + NCH * u_;
     f32x4 s2 = zero4(), dt = zero4();
     if (ct <= rb) {
       #pragma unroll
@@ -1158,8 +1169,8 @@ __global__ __launch_bounds__(kChunkThreads) void scan_bwd_chunk_bf16_kernel(
   }
   if constexpr (!kHGinLDS) __syncthreads();
 #pragma unroll kU
-  for (int u_ = 0; u_ < NT / 2; ++u_) {
-    const int ct = ch + 2 * u_;
+  for (int u_ = 0; u_ < NT / NCH; ++u_) {
+    const int ct = ch + NCH * u_;
     f32x4 acc = zero4();
     #pragma unroll
     for (int kk = 0; kk < kC; kk += 32) acc = mma32(fcol(sT, L6, r0, kk), fcol(sDD, LD, 16 * ct, kk), acc);
@@ -1169,8 +1180,8 @@ __global__ __launch_bounds__(kChunkThreads) void scan_bwd_chunk_bf16_kernel(
   __syncthreads();
   // dQ = dO H^T + S2 K; X1 = L^T dL over T (L^T upper, dL lower: k from max(rb, ct))
 #pragma unroll kU
-  for (int u_ = 0; u_ < NT / 2; ++u_) {
-    const int ct = ch + 2 * u_;
+  for (int u_ = 0; u_ < NT / NCH; ++u_) {
+    const int ct = ch + NCH * u_;
     f32x4 acc = zero4();
     #pragma unroll
     for (int kk = 0; kk < D; kk += 32) acc = mma32(arow(sO, kk), brow(gH, sH, ct, kk), acc);
@@ -1179,8 +1190,8 @@ __global__ __launch_bounds__(kChunkThreads) void scan_bwd_chunk_bf16_kernel(
     store_rows<T, D>(dq, b, h, t0, N, H, r0, 16 * ct, acc);
   }
   #pragma unroll
-  for (int u_ = 0; u_ < 2; ++u_) {  // (T was last read before the previous barrier)
-    const int ct = ch + 2 * u_;
+  for (int u_ = 0; u_ < 4 / NCH; ++u_) {  // (T was last read before the previous barrier)
+    const int ct = ch + NCH * u_;
     f32x4 x1 = zero4();
     #pragma unroll
     for (int kk = 0; kk < kC; kk += 32)
@@ -1192,8 +1203,8 @@ __global__ __launch_bounds__(kChunkThreads) void scan_bwd_chunk_bf16_kernel(
   // (row sums per column half into sRow); M = diag(beta) dA over dL
   float rows[4] = {0.f, 0.f, 0.f, 0.f};
   #pragma unroll
-  for (int u_ = 0; u_ < 2; ++u_) {
-    const int ct = ch + 2 * u_;
+  for (int u_ = 0; u_ < 4 / NCH; ++u_) {
+    const int ct = ch + NCH * u_;
     f32x4 da = zero4(), gk = zero4();
     if (ct <= rb) {
       #pragma unroll
@@ -1218,8 +1229,8 @@ __global__ __launch_bounds__(kChunkThreads) void scan_bwd_chunk_bf16_kernel(
   __syncthreads();
   // dK = Delta G^T + S2^T Q - dR H^T + M K + M^T K
 #pragma unroll kU
-  for (int u_ = 0; u_ < NT / 2; ++u_) {
-    const int ct = ch + 2 * u_;
+  for (int u_ = 0; u_ < NT / NCH; ++u_) {
+    const int ct = ch + NCH * u_;
     f32x4 acc = zero4();
     #pragma unroll
     for (int kk = 0; kk < D; kk += 32) {
@@ -1237,7 +1248,10 @@ __global__ __launch_bounds__(kChunkThreads) void scan_bwd_chunk_bf16_kernel(
   }
   const int i = threadIdx.x;
   if (i < kC && t0 + i < N) {
-    const float x = ((sPart[i] + sPart[kC + i]) + (sPart[2 * kC + i] + sPart[3 * kC + i])) + (sRow[i] + sRow[kC + i]);
+    float rs = sRow[i];
+#pragma unroll
+    for (int c2 = 1; c2 < NCH; ++c2) rs += sRow[c2 * kC + i];
+    const float x = ((sPart[i] + sPart[kC + i]) + (sPart[2 * kC + i] + sPart[3 * kC + i])) + rs;
     dbeta[((size_t)b * N + t0 + i) * H + h] = (T)x;
   }
   __syncthreads();  // every read of this chunk's LDS is done before the next one is put
@@ -1491,7 +1505,7 @@ void launch(const TIn* q, const TIn* k, const TIn* v, const TIn* beta, const flo
                      state_in, d_state, d_state_in, ws, NC, (int)slices, hrec != nullptr ? (int)slices : 0);
   if constexpr (sizeof(TIn) == 2 && D >= 32)
     hipLaunchKernelGGL((scan_bwd_chunk_bf16_kernel<D>), dim3(min(chunks, persistent_blocks(1))),
-                       dim3(kChunkThreads), 0, stream, q, k, v, beta, d_o, active, ws, hrec, dq, dk, dv, dbeta, N, H,
+                       dim3(ChunkShape<D>::NTH), 0, stream, q, k, v, beta, d_o, active, ws, hrec, dq, dk, dv, dbeta, N, H,
                        NC, (int)chunks);
   else
     hipLaunchKernelGGL((scan_bwd_chunk_kernel<TIn, D>), dim3(chunks), dim3(kChunkThreads), 0, stream, q, k, v, beta, d_o,
