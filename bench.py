@@ -879,20 +879,28 @@ def main() -> int:
         traffic_probe_backward(torch)
         return 0
 
-    pre = time_prefill(torch, args.steps, args.warmup)
+    def leg(fn, *a):
+        """A leg's result, once every kernel it queued (graph replays included) has completed with no
+        bounded wait giving up: a replay whose scan hand-over gave up writes NaN and must not pass
+        as a timing."""
+        out = fn(torch, *a)
+        _lib.check_faults(synchronize=True)
+        return out
+
+    pre = leg(time_prefill, args.steps, args.warmup)
     tok_s = B * T / (pre["step_ms"] / 1e3)
     s_bytes, s_flops = scan_bytes(B, T, H, D), scan_flops(B, T, H, D)
     a_bytes, a_flops = attn_bytes(B, T, H, H, D), attn_flops(B, T, H, D, WINDOW)
-    attn4_ms = time_attention_config(torch)
-    attn4_bwd_ms = time_attention_backward(torch)
-    scan_bwd = time_scan_backward(torch)
-    keys_ms, keys_bwd_ms = time_key_filter(torch)
-    dec = None if args.no_decode else time_decode(torch)
-    dec_cold_us = None if args.no_decode else time_decode_cold(torch)
-    cold_warm = time_cold_warm(torch)
-    published = time_published_shapes(torch)
-    looped = None if args.no_loop else time_looped(torch)
-    col_dec = None if args.no_decode else time_column_decode(torch)
+    attn4_ms = leg(time_attention_config)
+    attn4_bwd_ms = leg(time_attention_backward)
+    scan_bwd = leg(time_scan_backward)
+    keys_ms, keys_bwd_ms = leg(time_key_filter)
+    dec = None if args.no_decode else leg(time_decode)
+    dec_cold_us = None if args.no_decode else leg(time_decode_cold)
+    cold_warm = leg(time_cold_warm)
+    published = leg(time_published_shapes)
+    looped = None if args.no_loop else leg(time_looped)
+    col_dec = None if args.no_decode else leg(time_column_decode)
 
     # the dominant kernel by its time per launch in a graph of 10 launches (median of 5 replays)
     scan_dominant = pre["scan_ms"] >= pre["attn_ms"]
@@ -909,6 +917,17 @@ def main() -> int:
                 "mfma_frac_bf16": round(flops / (ms / 1e3) / 1e12 / BF16_PEAK_TFLOPS, 4),
                 "avg_launch_ms": round(ms, 4),
                 "launch_ms_statistic": "per launch in a HIP graph of 10, median of 5 replays"}
+    # both prefill kernels, whichever dominates this run (their times are close)
+    roofline["per_kernel"] = {
+        "delta_scan": {"ms": round(pre["scan_ms"], 4),
+                       "hbm_frac": round(s_bytes / (pre["scan_ms"] / 1e3) / 1e9 / HBM_PEAK_GBS, 4),
+                       "mfma_frac_bf16": round(s_flops / (pre["scan_ms"] / 1e3) / 1e12 / BF16_PEAK_TFLOPS, 4),
+                       "traffic": traffic_from_profiles("delta_scan")},
+        "window_attn": {"ms": round(pre["attn_ms"], 4),
+                        "hbm_frac": round(a_bytes / (pre["attn_ms"] / 1e3) / 1e9 / HBM_PEAK_GBS, 4),
+                        "mfma_frac_bf16": round(a_flops / (pre["attn_ms"] / 1e3) / 1e12 / BF16_PEAK_TFLOPS, 4),
+                        "traffic": traffic_from_profiles("window_attn")},
+    }
 
     result = {
         "metric": "delta-scan+window-attn prefill tok/s @T=4096; decode tok/s; % of roofline",

@@ -37,9 +37,10 @@ const char* vsp_last_error(void);
 int vsp_abi_version(void);
 
 /* Set-up, once per process before the first kernel call (later calls return at once): allocates
- * the fault record below in pinned host memory, and on every visible device takes the address of
- * the static scratch of vsp_ring_attn_noalloc_bf16 (with that device current) and zeroes it. No
- * counterpart in the reference, whose kernels come from a library that needs none. */
+ * the fault record below in pinned host memory, and on the current device only takes the address
+ * of the static scratch of vsp_ring_attn_noalloc_bf16 and zeroes it (another device is set up by
+ * that entry's first call on it; no other device is touched). No counterpart in the reference,
+ * whose kernels come from a library that needs none. */
 int vsp_init(void);
 
 /* The fault record of the bounded waits. Kernels whose waves hand work to each other through LDS
@@ -115,8 +116,10 @@ int vsp_delta_scan_carried_f32(const float* q, const float* k, const float* v, c
  * (vesper/recurrence.py:34-88) applied in the scan's own beta loads, so beta is never written to
  * memory: beta = sigmoid(logit + ln(1 + alpha m[b, t])), exactly 0 where 1 + alpha m is 0;
  * m: [B, T] float32 or NULL (no modulator: beta = sigmoid(logit)); alpha finite and >= 0; the
- * caller holds 1 + alpha m >= 0 (the reference refuses a negative factor). Otherwise as
- * vsp_delta_scan_bf16 / _f32, logits in beta's place and dtype. */
+ * caller holds 1 + alpha m >= 0 (the reference refuses a negative factor). beta is computed in
+ * float32 and rounded to the inputs' dtype, as the reference column casts it before its scan
+ * (vesper/column.py:313). Otherwise as vsp_delta_scan_bf16 / _f32, logits in beta's place and
+ * dtype. */
 int vsp_delta_scan_logits_bf16(const void* q, const void* k, const void* v, const void* logits, const float* m,
                                float alpha, const float* state_in, void* o, float* state_out, void* workspace,
                                size_t workspace_bytes, const uint8_t* active, int B, int T, int H, int D,
@@ -258,7 +261,8 @@ int vsp_ring_attn_f16(const void* q, const void* k, const void* v, const int64_t
 
 /* vsp_ring_attn_bf16 with no workspace argument and no allocation of any kind: the per-row arrival
  * counters live in a static device array of 65536 counters (256 KiB per GPU, held until the
- * process ends), whose per-device address vsp_init takes and zeroes. No counterpart in the
+ * process ends), whose address vsp_init takes and zeroes for the device current at set-up, and
+ * this entry's first call on any other device (zeroed by a kernel on `stream`). No counterpart in the
  * reference: it is for callers that cannot allocate (code under HIP graph capture, tight serving
  * loops, harnesses that forbid hipMalloc). B at most 65536 (larger B is refused with
  * VSP_ERR_ARG); vsp_init must have run. Every call that writes the ring leaves the counters zero.

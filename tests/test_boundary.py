@@ -21,6 +21,26 @@ def test_the_library_exports_every_declared_symbol():
     assert lib.vsp_abi_version() == _lib.ABI_VERSION
 
 
+def test_the_library_never_switches_devices():
+    """The library works on the caller's current device only: it imports no HIP call that changes
+    or enumerates devices, so loading it (vsp_init) and calling any entry point cannot create a
+    context on another GPU."""
+    import shutil
+    import subprocess
+
+    from vesper.kernels import _lib
+
+    nm = shutil.which("nm")
+    if nm is None:
+        pytest.skip("binutils' nm is not installed")
+    out = subprocess.run([nm, "-D", "--undefined-only", str(_lib.LIBRARY_PATH)], capture_output=True, text=True,
+                         check=True).stdout
+    imported = {line.split()[-1].split("@")[0] for line in out.splitlines() if line.strip()}
+    assert "hipGetDevice" in imported  # the check sees the HIP imports at all
+    for call in ("hipSetDevice", "hipGetDeviceCount", "hipDeviceReset", "hipDevicePrimaryCtxRetain"):
+        assert call not in imported, call
+
+
 def test_the_workspace_size_covers_every_chunk():
     from vesper.kernels import _lib
 

@@ -428,15 +428,14 @@ def _merged(k, v, beta, carried, active):
             torch.where(active[..., None], beta, carried[2]))
 
 
-# widths 16 and 128 take the generic chain, 32 and 64 the bf16 chain, 48 and n = 9 the serial kernel
+# widths 16 and 128 take the generic chain (the fp32 entry runs 128 token by token), 32 and 64 the bf16
+# chain, 48 and n = 9 the serial kernel
 @pytest.mark.parametrize("fp32", [False, True])
 @pytest.mark.parametrize(("b", "n", "h", "dk"), [(2, 9, 2, 16), (2, 70, 2, 48), (2, 130, 3, 16), (2, 200, 2, 32),
                                                  (1, 300, 2, 64), (2, 100, 2, 128)])
 def test_carried_inputs_equal_the_merged_inputs_bitwise(fp32, b, n, h, dk):
     from vesper.kernels.delta_scan import delta_scan_fused, delta_scan_fused_fp32
 
-    if fp32 and dk == 128:
-        pytest.skip("the fp32 scan runs 128-wide heads token by token: covered at 48")
     scan = delta_scan_fused_fp32 if fp32 else delta_scan_fused
     q, k, v, beta, h0, carried, active = _carry_case(b, n, h, dk, fp32, seed=dk + n)
     # the fresh rows of inactive tokens must never be read: poison them
@@ -592,6 +591,59 @@ def test_the_write_strength_refusals_and_gradients():
     (write_strength(lg_gpu, m_gpu, 0.5) * up.float().to(GPU)).sum().backward()
     torch.testing.assert_close(lg_gpu.grad.cpu().double(), lg_ref.grad, rtol=1e-5, atol=1e-6)
     torch.testing.assert_close(m_gpu.grad.cpu().double(), m_ref.grad, rtol=1e-5, atol=1e-6)
+
+
+def test_bf16_logits_with_a_modulator_give_float32_beta_and_gradients():
+    """bf16 logits plus the float32 shift ln(1 + alpha m) promote to float32 in the reference
+    (recurrence.py:84-88): beta comes out float32, and its gradient is taken from the unrounded
+    beta, so saturated logits (where a bf16 beta would round to 1) keep their nonzero slope."""
+    from oracle.delta import write_strength as oracle_strength
+    from vesper.kernels.delta_scan import write_strength
+
+    g = torch.Generator().manual_seed(11)
+    lg = (3 * torch.randn(2, 40, 3, generator=g)).to(BF16)
+    # saturating logits (tokens 0-2 of row 0 have 1 + alpha m = 0, an exact zero write)
+    lg[0, 3:11, 0] = torch.tensor([6.5, 7.0, 8.0, 9.0, 10.0, 12.0, 4.0, 5.5], dtype=BF16)
+    mm = _modulator(2, 40, 12)
+    up = torch.randn(2, 40, 3, generator=g)
+    lg_ref = lg.double().requires_grad_()
+    m_ref = mm.double().requires_grad_()
+    want = oracle_strength(lg_ref, m_ref, 0.5)
+    (want * up.double()).sum().backward()
+    lg_gpu, m_gpu = lg.to(GPU).requires_grad_(), mm.to(GPU).requires_grad_()
+    beta = write_strength(lg_gpu, m_gpu, 0.5)
+    assert beta.dtype == torch.float32
+    torch.testing.assert_close(beta.detach().cpu().double(), want.detach(), rtol=1e-6, atol=1e-7)
+    (beta * up.to(GPU)).sum().backward()
+    assert lg_gpu.grad.dtype == BF16
+    # the logits' gradient is rounded to bf16 once (the reference casts the float32 gradient back);
+    # the absolute term is an ulp of a float32 beta near 1 (~6e-8) times |up|, which 1 - beta carries
+    torch.testing.assert_close(lg_gpu.grad.cpu().double(), lg_ref.grad, rtol=2 ** -8, atol=3e-7)
+    assert bool((lg_gpu.grad[0, 3:11, 0] != 0).all())  # saturated logits keep a slope
+    assert not bool(lg_gpu.grad[0, :3].any())  # a zero write has a zero gradient
+    torch.testing.assert_close(m_gpu.grad.cpu().double(), m_ref.grad, rtol=1e-5, atol=1e-6)
+
+
+@pytest.mark.parametrize("fp32", [False, True])
+@pytest.mark.parametrize("with_m", [False, True])
+def test_the_scan_from_logits_gives_the_same_outputs_with_and_without_autograd(fp32, with_m):
+    """The no-grad path computes beta inside the scan's loads, the autograd path through
+    write_strength and delta_scan_fused; both round beta to the inputs' dtype, so both see the
+    same beta and their forward outputs agree bitwise."""
+    from vesper.kernels.delta_scan import delta_scan_fused_logits
+
+    b, n, h, dk = 2, 200, 3, 64
+    q, k, v, _, h0 = scan_inputs(b, n, h, dk, seed=13)
+    logits = 2 * torch.randn(b, n, h, generator=torch.Generator().manual_seed(14))
+    dtype = torch.float32 if fp32 else BF16
+    q, k, v, logits = (t.to(dtype).to(GPU) for t in (q, k, v, logits))
+    h0 = h0.to(GPU)
+    kw = {"m": _modulator(b, n, 15).to(GPU), "alpha": 0.5} if with_m else {}
+    with torch.no_grad():
+        o_plain, s_plain = delta_scan_fused_logits(q, k, v, logits, h0, **kw)
+    o_grad, s_grad = delta_scan_fused_logits(q, k, v, logits.clone().requires_grad_(), h0, **kw)
+    assert torch.equal(o_grad.detach(), o_plain)
+    assert torch.equal(s_grad.detach(), s_plain)
 
 
 @pytest.mark.parametrize("fp32", [False, True])

@@ -4,7 +4,7 @@ Parity: relative Frobenius error of the halted hidden states and of every pass's
 3e-2 (the reference's attention bound; eight bf16 mixer passes compound their roundings), the
 per-token pass counts exact. At the full config size: exact size-independent properties
 (determinism, pass counts from the exit trace, early-halting tokens bitwise equal to a one-pass
-run) and an fp32-oracle parity check over two passes.
+run) and fp32-oracle parity checks over two passes and over all eight.
 """
 
 from __future__ import annotations
@@ -88,6 +88,19 @@ def test_config_size_two_passes_match_the_fp32_oracle():
     column, x0, exits, states = _setup(b, n, d, h, h, dk, w, passes, seed=9)
     got = column.forward(x0.to(GPU), [s.to(GPU) for s in states], [e.to(GPU) for e in exits])
     want = _oracle(column, x0, exits, states, dtype=torch.float32)
+    assert relative_error(got.y, want.y) < 3e-2
+    for t in range(passes):
+        assert relative_error(got.states[t], want.states[t]) < 3e-2, t
+
+
+def test_config_size_eight_passes_match_the_fp32_oracle():
+    # the full config: B4 T2048 d512, 8 heads of 64, window 512, all 8 passes with halting 0.3
+    b, n, d, h, dk, w, passes = 4, 2048, 512, 8, 64, 512, 8
+    column, x0, exits, states = _setup(b, n, d, h, h, dk, w, passes, seed=17)
+    got = column.forward(x0.to(GPU), [s.to(GPU) for s in states], [e.to(GPU) for e in exits])
+    want = _oracle(column, x0, exits, states, dtype=torch.float32)
+    assert torch.equal(got.n_iters.cpu(), want.n_iters)
+    assert torch.equal(got.n_iters.cpu(), _expected_iters(exits, passes))
     assert relative_error(got.y, want.y) < 3e-2
     for t in range(passes):
         assert relative_error(got.states[t], want.states[t]) < 3e-2, t

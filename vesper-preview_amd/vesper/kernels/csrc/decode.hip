@@ -20,6 +20,7 @@
 // per-row arrival counter in the caller's workspace) writes them and resets the counter to zero:
 // every workgroup of the row has read the old position and flag by then, whatever order the
 // workgroups ran in.
+#include <mutex>
 #include <type_traits>
 
 #include "common.h"
@@ -304,35 +305,61 @@ int ring_attn(const T* q, const T* knew, const T* vnew, const int64_t* pos, T* r
 // The per-row arrival counters of the in-kernel ring write, for callers that cannot allocate (code
 // under graph capture, serving loops): a file-scope device array, one copy per GPU, alive until the
 // process ends. Host code never passes the array's name to a kernel (in host code it is a host-side
-// stand-in, not a device address): ring_scratch_init takes each device's address with
-// hipGetSymbolAddress, with that device current, and the entry point uses that address.
+// stand-in, not a device address): ring_scratch_init takes the current device's address with
+// hipGetSymbolAddress and the entry point uses that address. Only the current device is touched:
+// vsp_init sets up the device current when it runs, and the entry point sets up any other device
+// on its first call there (a process that uses one GPU never creates a context on another).
 constexpr int kMaxDevices = 64;
 __device__ __align__(256) uint32_t scratch[kNoAllocMaxRows];
 uint32_t* g_scratch[kMaxDevices] = {};
+std::mutex g_scratch_mutex;
 
-int ring_scratch_init() {
-  int count = 0, current = 0;
-  hipError_t err = hipGetDeviceCount(&count);
-  if (err != hipSuccess) return fail(ERR_LAUNCH, "vsp_init: hipGetDeviceCount: %s", hipGetErrorString(err));
-  err = hipGetDevice(&current);
-  if (err != hipSuccess) return fail(ERR_LAUNCH, "vsp_init: hipGetDevice: %s", hipGetErrorString(err));
-  for (int d = 0; d < count && d < kMaxDevices; ++d) {
-    if (g_scratch[d] != nullptr) continue;
-    err = hipSetDevice(d);
-    void* ptr = nullptr;
-    if (err == hipSuccess) err = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
-    // the counters start at zero; every call that writes the ring leaves them zero again
-    if (err == hipSuccess) err = hipMemset(ptr, 0, sizeof(scratch));
-    if (err != hipSuccess) {
-      (void)hipSetDevice(current);
-      return fail(ERR_LAUNCH, "vsp_init: static scratch on device %d: %s", d, hipGetErrorString(err));
-    }
-    g_scratch[d] = static_cast<uint32_t*>(ptr);
-  }
-  err = hipSetDevice(current);
-  if (err != hipSuccess) return fail(ERR_LAUNCH, "vsp_init: hipSetDevice: %s", hipGetErrorString(err));
-  return OK;
+// zeroes the counters on a stream (a kernel, not a memset: the first call on a device may be
+// captured into a graph)
+__global__ __launch_bounds__(256) void zero_counters_kernel(uint32_t* c, int n) {
+  const int i = blockIdx.x * 256 + threadIdx.x;
+  if (i < n) c[i] = 0u;
 }
+
+// The current device's scratch address, set up on first use; null (with the error set) on failure.
+// `stream` null: zeroed synchronously (vsp_init); otherwise zeroed by a kernel on that stream,
+// ahead of the caller's launch.
+uint32_t* scratch_of_current(hipStream_t stream, bool sync_zero) {
+  int device = 0;
+  hipError_t err = hipGetDevice(&device);
+  if (err != hipSuccess) {
+    fail(ERR_LAUNCH, "static scratch: hipGetDevice: %s", hipGetErrorString(err));
+    return nullptr;
+  }
+  if (device < 0 || device >= kMaxDevices) {
+    fail(ERR_UNSUPPORTED, "static scratch: device %d beyond the %d this build tracks", device, kMaxDevices);
+    return nullptr;
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (g_scratch[device] != nullptr) return g_scratch[device];
+  void* ptr = nullptr;
+  err = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+  if (err != hipSuccess) {
+    fail(ERR_LAUNCH, "static scratch on device %d: hipGetSymbolAddress: %s", device, hipGetErrorString(err));
+    return nullptr;
+  }
+  // the counters start at zero; every call that writes the ring leaves them zero again
+  if (sync_zero) {
+    err = hipMemset(ptr, 0, sizeof(scratch));
+  } else {
+    hipLaunchKernelGGL(zero_counters_kernel, dim3((kNoAllocMaxRows + 255) / 256), dim3(256), 0, stream,
+                       static_cast<uint32_t*>(ptr), kNoAllocMaxRows);
+    err = hipGetLastError();
+  }
+  if (err != hipSuccess) {
+    fail(ERR_LAUNCH, "static scratch on device %d: zeroing: %s", device, hipGetErrorString(err));
+    return nullptr;
+  }
+  g_scratch[device] = static_cast<uint32_t*>(ptr);
+  return g_scratch[device];
+}
+
+int ring_scratch_init() { return scratch_of_current(nullptr, true) != nullptr ? OK : ERR_LAUNCH; }
 
 }  // namespace vsp
 
@@ -345,15 +372,12 @@ extern "C" int vsp_ring_attn_noalloc_bf16(const void* q, const void* k, const vo
   const char* who = "vsp_ring_attn_noalloc_bf16";
   if (B > vsp::kNoAllocMaxRows)
     return vsp::fail(vsp::ERR_ARG, "%s: %d rows exceed the static scratch's %d", who, B, vsp::kNoAllocMaxRows);
-  int device = 0;
-  const hipError_t err = hipGetDevice(&device);
-  if (err != hipSuccess) return vsp::fail(vsp::ERR_LAUNCH, "%s: hipGetDevice: %s", who, hipGetErrorString(err));
-  if (device < 0 || device >= vsp::kMaxDevices || vsp::g_scratch[device] == nullptr)
-    return vsp::fail(vsp::ERR_ARG, "%s: vsp_init has not set up device %d", who, device);
+  uint32_t* counters = vsp::scratch_of_current(reinterpret_cast<hipStream_t>(stream), false);
+  if (counters == nullptr) return vsp::ERR_LAUNCH;
   return vsp::ring_attn<__bf16>(static_cast<const __bf16*>(q), static_cast<const __bf16*>(k),
                                 static_cast<const __bf16*>(v), pos, static_cast<__bf16*>(ring_k),
                                 static_cast<__bf16*>(ring_v), ring_pos, ring_valid, static_cast<__bf16*>(o), active,
-                                vsp::g_scratch[device], sizeof(uint32_t) * (size_t)vsp::kNoAllocMaxRows, B, H, HKV, D,
+                                counters, sizeof(uint32_t) * (size_t)vsp::kNoAllocMaxRows, B, H, HKV, D,
                                 window, scale, write, stream, who);
 }
 

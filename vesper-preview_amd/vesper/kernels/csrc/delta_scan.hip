@@ -102,7 +102,9 @@ __global__ __launch_bounds__(256) void delta_serial_kernel(const TIn* __restrict
     if ((int)threadIdx.x < nt) {
       const size_t tok = (size_t)b * T + t0 + threadIdx.x;
       const float raw = to_f32((carried.k != nullptr && sa[threadIdx.x] == 0 ? carried.beta : beta)[tok * H + h]);
-      sb[threadIdx.x] = beta_logits ? write_strength(raw, mod_m, tok, mod_alpha) : raw;
+      // beta from its logit is rounded to the inputs' dtype, as the reference column casts it
+      // before its scan (column.py:313)
+      sb[threadIdx.x] = beta_logits ? to_f32(from_f32<TIn>(write_strength(raw, mod_m, tok, mod_alpha))) : raw;
     }
     __syncthreads();
     for (int tt = 0; tt < nt; ++tt) {
@@ -480,9 +482,11 @@ __global__ __launch_bounds__(256, 3) void delta_prep_kernel(const TIn* __restric
 #pragma unroll
       for (int e = 0; e < N::PER; ++e) kn[i][sgi][e] = ok ? kn[i][sgi][e] : from_f32<E>(0.f);
     }
-  // the write strength from its logit (and the token's modulator) where the entry takes logits
-  const float braw_f = beta_logits ? write_strength(to_f32(braw), mod_m, (size_t)b * T + min(t0 + l, T - 1), mod_alpha)
-                                   : to_f32(braw);
+  // the write strength from its logit (and the token's modulator) where the entry takes logits,
+  // rounded to the inputs' dtype as the reference column casts beta before its scan (column.py:313)
+  const float braw_f =
+      beta_logits ? to_f32(from_f32<TIn>(write_strength(to_f32(braw), mod_m, (size_t)b * T + min(t0 + l, T - 1), mod_alpha)))
+                  : to_f32(braw);
   const float bl = l < nv ? braw_f : 0.f;
   E* tc = reinterpret_cast<E*>(&sScr[w][0]);  // compact tiles: tile t = i (i + 1) / 2 + j, row-major
   ut_solve<E, DKP>(kn, bl, &sScr[w][0],

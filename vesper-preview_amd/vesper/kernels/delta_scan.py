@@ -339,8 +339,13 @@ def _checked_modulator(logits: Tensor, m: Tensor | None, alpha: float | None) ->
 class _WriteStrength(torch.autograd.Function):
     @staticmethod
     def forward(ctx: Any, logits: Tensor, m: Tensor | None, alpha: float) -> Tensor:  # noqa: D102
+        ctx.logits_dtype = logits.dtype
         lg = _aligned(logits.detach())
         mm = None if m is None else m.detach().contiguous()
+        if mm is not None:
+            # logits + ln(1 + alpha m) promotes to float32 in the reference (recurrence.py:84-88), so
+            # beta and its gradient are float32 there: the fp32 kernel on the exactly widened logits
+            lg = lg.float()
         beta = torch.empty_like(lg)
         rows = lg.numel() // lg.shape[-1] if lg.dim() else 1
         entry = "vsp_write_strength_f32" if lg.dtype == torch.float32 else "vsp_write_strength_bf16"
@@ -356,7 +361,7 @@ class _WriteStrength(torch.autograd.Function):
         beta, *rest = ctx.saved_tensors
         b32 = beta.float()
         slope = g.float() * b32 * (1.0 - b32)  # d sigmoid; zero where the factor is zero (beta = 0)
-        d_logits = slope.to(beta.dtype)
+        d_logits = slope.to(ctx.logits_dtype)
         d_m = None
         if rest and ctx.needs_input_grad[1]:
             factor = 1.0 + ctx.alpha * rest[0]
@@ -368,8 +373,10 @@ class _WriteStrength(torch.autograd.Function):
 def write_strength(logits: Tensor, m: Tensor | None = None, alpha: float | None = None) -> Tensor:
     """``beta`` in [0, 1] from the write-strength logits, modulated when ``m`` is given
     (``vesper/recurrence.py:34-88``): ``sigmoid(logits)``, or ``sigmoid(logits + ln(1 + alpha m))``
-    with an exact zero where ``1 + alpha m`` is zero. On the GPU (``vsp_write_strength_*``), in
-    ``logits``' dtype (bfloat16 or float32); under autograd the gradients of ``logits`` and ``m``.
+    with an exact zero where ``1 + alpha m`` is zero. On the GPU (``vsp_write_strength_*``):
+    without ``m`` in ``logits``' dtype (bfloat16 or float32), with the float32 ``m`` in float32, as
+    the reference's sum with the float32 shift promotes it; under autograd the gradients of
+    ``logits`` (in its dtype) and ``m``.
 
     Args:
         logits: ``[b, n, h]`` (any shape without ``m``), bfloat16 or float32, on the GPU.
@@ -396,7 +403,8 @@ def delta_scan_fused_logits(q: Tensor, k: Tensor, v: Tensor, logits: Tensor, sta
     """``delta_scan_fused(q, k, v, write_strength(logits, m, alpha), state)`` with the write strength
     computed inside the scan's beta loads (``vsp_delta_scan_logits_*``): ``beta`` is never
     written to memory. bfloat16 inputs run the bf16 scan, float32 inputs the fp32 scan; ``beta``
-    stays float32 inside both (the separate path rounds it to the inputs' dtype first).
+    is computed in float32 and rounded to the inputs' dtype, as the reference column casts it
+    before its scan (``column.py:313``), so with and without autograd the scan sees the same beta.
 
     Under autograd it is the composition above (the write strength's gradient and the scan's
     backward kernels).
@@ -409,7 +417,7 @@ def delta_scan_fused_logits(q: Tensor, k: Tensor, v: Tensor, logits: Tensor, sta
         return q, state
     a = _checked_modulator(logits, m, alpha)
     if torch.is_grad_enabled() and any(t.requires_grad for t in (q, k, v, logits, state, *(() if m is None else (m,)))):
-        beta = write_strength(logits, m, alpha)
+        beta = write_strength(logits, m, alpha).to(q.dtype)
         return (delta_scan_fused_fp32 if fp32 else delta_scan_fused)(q, k, v, beta, state, active=active)
     b, n, h, dk = q.shape
     q, k, v, logits, state = (_aligned(t) for t in (q, k, v, logits, state))
