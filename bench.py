@@ -671,6 +671,89 @@ def time_published_shapes(torch, reps: int = 20) -> dict:
 
 
 # ---- CPU baseline ---------------------------------------------------------------------------------
+def probe_library():
+    """``libvesper_probe.so`` (bench.py's HBM streaming probes, built beside the kernel library)."""
+    import ctypes
+
+    from vesper.kernels import build as kbuild
+
+    if not kbuild.PROBE_LIBRARY.exists():
+        raise RuntimeError(f"{kbuild.PROBE_LIBRARY} is not built: run __graft_entry__.build()")
+    lib = ctypes.CDLL(str(kbuild.PROBE_LIBRARY))
+    lib.vsp_probe_stream.restype = ctypes.c_int
+    lib.vsp_probe_stream.argtypes = [ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int,
+                                     ctypes.c_void_p]
+    return lib
+
+
+PROBE_MODES = {"read": 0, "copy": 1, "fill": 2, "read_nt": 3, "copy_nt": 4, "fill_nt": 5}
+
+
+def time_hbm_ceiling(torch, sweep: bool = False) -> dict:
+    """What HBM gives to the simplest access patterns, from hand-written streaming kernels
+    (``libvesper_probe.so``: 16-byte pieces, a grid-stride loop with several pieces in flight per
+    thread). Cold: 1 GiB buffers (four times the 256 MB MALL, so every pass misses it), read,
+    copied and filled, per launch in a HIP graph of 5 (median of 3 replays); TB/s counts bytes read
+    plus bytes written. Then the decode step's own pattern: its 8.39 MB fp32 state (b64 H8 64x64)
+    read and written back in place, warm (one buffer) and cold (64 buffers rotated, 537 MB). With
+    ``sweep`` every mode and workgroup count; otherwise the counts the sweep found best."""
+    lib = probe_library()
+    dev = torch.device("cuda:0")
+    gib = 1 << 30
+    a = torch.empty(gib, dtype=torch.uint8, device=dev)
+    b = torch.empty(gib, dtype=torch.uint8, device=dev)
+    a.fill_(1)
+    b.fill_(2)
+    sink = torch.zeros(16384 * 256, dtype=torch.int32, device=dev)
+
+    def launch(mode: str, src, dst, nbytes: int, blocks: int) -> None:
+        # torch's current stream at each call: under capture that is the capturing stream
+        st = lib.vsp_probe_stream(PROBE_MODES[mode], src, dst, nbytes, blocks, torch.cuda.current_stream(dev).cuda_stream)
+        if st != 0:
+            raise RuntimeError(f"vsp_probe_stream({mode}, {nbytes}, {blocks}) returned {st}")
+
+    out: dict = {}
+    block_counts = (1024, 2048, 4096, 8192, 16384) if sweep else (4096,)
+    modes = ("read", "copy", "fill", "read_nt", "copy_nt", "fill_nt") if sweep else ("read", "copy", "fill")
+    for mode in modes:
+        best = None
+        for blocks in block_counts:
+            if mode.startswith("read"):
+                fn = lambda: launch(mode, a.data_ptr(), sink.data_ptr(), gib, blocks)  # noqa: E731
+                moved = gib
+            elif mode.startswith("copy"):
+                fn = lambda: launch(mode, a.data_ptr(), b.data_ptr(), gib, blocks)  # noqa: E731
+                moved = 2 * gib
+            else:
+                fn = lambda: launch(mode, None, b.data_ptr(), gib, blocks)  # noqa: E731
+                moved = gib
+            ms = captured_ms(torch, fn, 5, 3)
+            tbs = moved / (ms / 1e3) / 1e12
+            if sweep:
+                out[f"{mode}_1GiB_blocks{blocks}_tbs"] = round(tbs, 3)
+            if best is None or tbs > best[0]:
+                best = (tbs, blocks, ms)
+        out[f"{mode}_1GiB_cold_tbs"] = round(best[0], 3)
+        out[f"{mode}_1GiB_cold_blocks"] = best[1]
+    del b
+    # the decode step's state: 8.39 MB read and written in place (copy onto itself)
+    state_bytes = 64 * 8 * 64 * 64 * 4
+    nbuf = 64
+    bufs = a[: nbuf * state_bytes].view(nbuf, state_bytes)
+    for blocks in ((256, 512, 1024, 2048) if sweep else (1024,)):
+        warm = captured_ms(torch, lambda: launch("copy", bufs[0].data_ptr(), bufs[0].data_ptr(), state_bytes, blocks),
+                           20, 3)
+        it = iter(range(10**9))
+        cold = captured_ms(torch, lambda: (lambda i: launch("copy", bufs[i % nbuf].data_ptr(), bufs[i % nbuf].data_ptr(),
+                                                             state_bytes, blocks))(next(it)), nbuf, 3)
+        key = f"state_8p39MB_inplace_blocks{blocks}" if sweep else "state_8p39MB_inplace"
+        out[f"{key}_warm_us"] = round(warm * 1e3, 3)
+        out[f"{key}_cold_us"] = round(cold * 1e3, 3)
+        out[f"{key}_warm_tbs"] = round(2 * state_bytes / (warm / 1e3) / 1e12, 3)
+        out[f"{key}_cold_tbs"] = round(2 * state_bytes / (cold / 1e3) / 1e12, 3)
+    return out
+
+
 def cpu_info(torch) -> dict:
     """The host the CPU legs ran on: logical CPUs, the model name lscpu reports, torch's threading."""
     model = platform.processor() or "unknown"
@@ -857,6 +940,8 @@ def main() -> int:
                     help="one training step of each mixer after a copy of known size, for rocprofv3 --pmc")
     ap.add_argument("--traffic-probe", action="store_true",
                     help="launch each kernel once plus a calibration copy, for rocprofv3 --pmc runs")
+    ap.add_argument("--hbm-ceiling", action="store_true",
+                    help="only the HBM streaming probes, every mode and workgroup count (one JSON line)")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -877,6 +962,9 @@ def main() -> int:
         return 0
     if args.traffic_probe_backward:
         traffic_probe_backward(torch)
+        return 0
+    if args.hbm_ceiling:
+        print(json.dumps({"hbm_ceiling": time_hbm_ceiling(torch, sweep=True)}), flush=True)
         return 0
 
     def leg(fn, *a):

@@ -20,6 +20,9 @@ CSRC = HERE / "csrc"
 INCLUDE = HERE.parents[2] / "include"
 OBJDIR = HERE / "_build"
 LIBRARY = HERE / "libvesper_kernels.so"
+# bench.py's HBM streaming probes: measurement only, kept out of the mixers' library
+PROBE_SOURCE = HERE / "probe" / "hbm_probe.hip"
+PROBE_LIBRARY = HERE / "libvesper_probe.so"
 ARCH = os.environ.get("VSP_OFFLOAD_ARCH", "gfx950")
 
 # -packed-fp32-ops off: hipcc must not emit packed fp32 VALU forms in these kernels
@@ -72,7 +75,19 @@ def build(verbose: bool = False) -> Path:
     os.replace(tmp, LIBRARY)
     if verbose:
         print(f"built {LIBRARY} from {len(srcs)} sources", file=sys.stderr)
+    build_probe()
     return LIBRARY
+
+
+def build_probe() -> Path:
+    """Compile bench.py's HBM streaming probes into ``libvesper_probe.so``; returns its path."""
+    tmp = PROBE_LIBRARY.with_suffix(".so.tmp")
+    cmd = [hipcc(), *HIP_FLAGS, "-shared", "-Wl,--no-undefined", "-o", str(tmp), str(PROBE_SOURCE)]
+    proc = subprocess.run(cmd, capture_output=True, text=True, check=False)
+    if proc.returncode != 0:
+        raise RuntimeError(f"hipcc failed on {PROBE_SOURCE.name}:\n{proc.stderr[-6000:]}")
+    os.replace(tmp, PROBE_LIBRARY)
+    return PROBE_LIBRARY
 
 
 if __name__ == "__main__":
