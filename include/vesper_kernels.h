@@ -22,7 +22,7 @@
 extern "C" {
 #endif
 
-#define VSP_ABI_VERSION 9
+#define VSP_ABI_VERSION 10
 
 /* Status codes. */
 #define VSP_OK 0
@@ -258,6 +258,20 @@ int vsp_ring_attn_f16(const void* q, const void* k, const void* v, const int64_t
                       int64_t* ring_pos, uint8_t* ring_valid, void* o, const uint8_t* active, void* workspace,
                       size_t workspace_bytes, int B, int H, int HKV, int D, int window, float scale, int write,
                       void* stream);
+
+/* The same with the ring's keys and values in float32 (ring_k, ring_v: [B, window, HKV, D] fp32,
+ * 16-byte aligned), the ring the reference's CapturedDecoder allocates (vesper/decode.py:81,85 with
+ * vesper/column.py:492) and attend_ring casts to the query dtype (vesper/attention.py:325): each
+ * ring element is rounded to q's dtype (nearest even) as it is read, and the new token is written
+ * into its slot widened to float32. q, k, v, o in bf16 (fp16 for the _f16 entry). */
+int vsp_ring_attn_bf16_ring_f32(const void* q, const void* k, const void* v, const int64_t* pos, float* ring_k,
+                                float* ring_v, int64_t* ring_pos, uint8_t* ring_valid, void* o, const uint8_t* active,
+                                void* workspace, size_t workspace_bytes, int B, int H, int HKV, int D, int window,
+                                float scale, int write, void* stream);
+int vsp_ring_attn_f16_ring_f32(const void* q, const void* k, const void* v, const int64_t* pos, float* ring_k,
+                               float* ring_v, int64_t* ring_pos, uint8_t* ring_valid, void* o, const uint8_t* active,
+                               void* workspace, size_t workspace_bytes, int B, int H, int HKV, int D, int window,
+                               float scale, int write, void* stream);
 
 /* vsp_ring_attn_bf16 with no workspace argument and no allocation of any kind: the per-row arrival
  * counters live in a static device array of 65536 counters (256 KiB per GPU, held until the

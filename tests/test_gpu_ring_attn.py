@@ -67,6 +67,47 @@ def test_random_rings_match_the_oracle(dtype, dk, h, hkv):
     assert torch.equal(after.pos.cpu(), npos) and torch.equal(after.valid.cpu(), nvalid)
 
 
+@pytest.mark.parametrize("dtype", [BF16, torch.float16])
+@pytest.mark.parametrize(("h", "hkv", "dk"), [(8, 8, 64), (8, 2, 128), (4, 4, 16)])
+def test_a_float32_ring_reads_as_the_ring_cast_to_the_query_dtype(dtype, h, hkv, dk):
+    """The reference decoder's rings are float32 (decode.py:81,85; column.py:492) and attend_ring
+    casts them to the query dtype (attention.py:325): over a float32 ring the outputs equal, bitwise,
+    those over the same ring rounded to q's dtype, and the new token lands in its slot widened to
+    float32 (every other slot untouched)."""
+    from vesper.kernels.ring_attn import RingKVCache, ring_attention
+
+    b, w = 5, 40
+    rk, rv, rpos, valid, p = _random_ring(b, w, hkv, dk, seed=71 + dk, dtype=torch.float32)
+    g = torch.Generator().manual_seed(72)
+    q = torch.randn(b, 1, h, dk, generator=g).to(dtype)
+    k = torch.randn(b, 1, hkv, dk, generator=g).to(dtype)
+    v = torch.randn(b, 1, hkv, dk, generator=g).to(dtype)
+    wide = RingKVCache(*(t.to(GPU) for t in (rk, rv, rpos, valid)), w)
+    narrow = RingKVCache(rk.to(GPU, dtype), rv.to(GPU, dtype), rpos.to(GPU), valid.to(GPU), w)
+    dq, dk_, dv, dp = (t.to(GPU) for t in (q, k, v, p))
+    o32, after32 = ring_attention(dq, dk_, dv, dp, wide)
+    o16, after16 = ring_attention(dq, dk_, dv, dp, narrow)
+    assert torch.equal(o32, o16)
+    assert after32.k.dtype == torch.float32 and after32.v.dtype == torch.float32
+    nk, nv, npos, nvalid = oa.kv_ring_write(rk, rv, rpos, valid, k.float(), v.float(), p)
+    assert torch.equal(after32.k.cpu(), nk) and torch.equal(after32.v.cpu(), nv)
+    assert torch.equal(after32.pos.cpu(), npos) and torch.equal(after32.valid.cpu(), nvalid)
+    assert torch.equal(after16.pos, after32.pos)
+    want = oa.ring_attend(q.double(), k.double(), v.double(), p, rk.to(dtype).double(), rv.to(dtype).double(),
+                          rpos, valid, w)
+    assert relative_error(o32, want) < 1e-2
+
+
+def test_a_ring_of_another_dtype_is_refused():
+    from vesper.contracts import ContractError
+    from vesper.kernels.ring_attn import kv_ring_empty, ring_attention
+
+    ring = kv_ring_empty(1, 1, 16, 4, torch.float16, GPU)
+    q = torch.zeros(1, 1, 1, 16, dtype=BF16, device=GPU)
+    with pytest.raises(ContractError, match="dtype"):
+        ring_attention(q, q, q, torch.ones(1, 1, dtype=torch.long, device=GPU), ring)
+
+
 def test_decoding_steps_equal_the_whole_chunk_window():
     # 3w + 5 single-token steps from an empty ring equal the window attention over the whole chunk
     from vesper.kernels.ring_attn import kv_ring_empty, ring_attention

@@ -17,7 +17,7 @@ import torch
 HERE = Path(__file__).resolve().parent
 LIBRARY_PATH = HERE / "libvesper_kernels.so"
 HEADER_PATH = HERE.parents[2] / "include" / "vesper_kernels.h"
-ABI_VERSION = 9
+ABI_VERSION = 10
 
 P = ctypes.c_void_p
 I = ctypes.c_int
@@ -60,6 +60,8 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "vsp_ring_attn_workspace_bytes": (Z, [I]),
     "vsp_ring_attn_bf16": (I, [P, P, P, P, P, P, P, P, P, P, P, Z, I, I, I, I, I, F, I, P]),
     "vsp_ring_attn_f16": (I, [P, P, P, P, P, P, P, P, P, P, P, Z, I, I, I, I, I, F, I, P]),
+    "vsp_ring_attn_bf16_ring_f32": (I, [P, P, P, P, P, P, P, P, P, P, P, Z, I, I, I, I, I, F, I, P]),
+    "vsp_ring_attn_f16_ring_f32": (I, [P, P, P, P, P, P, P, P, P, P, P, Z, I, I, I, I, I, F, I, P]),
     "vsp_ring_attn_noalloc_bf16": (I, [P, P, P, P, P, P, P, P, P, P, I, I, I, I, I, F, I, P]),
     "vsp_key_filter_bf16": (I, [P, P, P, P, I, I, I, I, I, P]),
     "vsp_key_filter_f16": (I, [P, P, P, P, I, I, I, I, I, P]),

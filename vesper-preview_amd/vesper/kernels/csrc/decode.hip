@@ -36,15 +36,46 @@ constexpr int kMaxGroup = 8;
 // (many waves per CU with few loads each stream the window faster than fewer waves with many loads:
 // 24.6 against 25.1 us per decode step with the ring read from HBM); wider groups run 256 threads
 // with eight keys each, so the per-head softmax states still fit in registers.
+template <typename T> struct Ring8 {
+  typedef T V8 __attribute__((ext_vector_type(8)));
+};
+
 template <int GM> struct RingShape {
   static constexpr int NT = GM <= 2 ? 1024 : 256;  // threads
   static constexpr int KPT = GM <= 2 ? 4 : 8;      // keys per thread per batch
 };
 
-template <typename T, int D, int GM>
+// Eight ring elements as the queries' type: the ring's own type is either the queries' (one 16-byte
+// load) or float32 (two, each element rounded to nearest even, as the reference's autocast casts an
+// fp32 ring to the query dtype, attention.py:325).
+template <typename T, typename R>
+__device__ __forceinline__ typename Ring8<T>::V8 load_ring8(const R* p) {
+  typedef typename Ring8<T>::V8 V8;
+  if constexpr (sizeof(R) == sizeof(T)) {
+    return *reinterpret_cast<const V8*>(p);
+  } else {
+    const float4 a = reinterpret_cast<const float4*>(p)[0], b = reinterpret_cast<const float4*>(p)[1];
+    V8 x;
+    x[0] = from_f32<T>(a.x); x[1] = from_f32<T>(a.y); x[2] = from_f32<T>(a.z); x[3] = from_f32<T>(a.w);
+    x[4] = from_f32<T>(b.x); x[5] = from_f32<T>(b.y); x[6] = from_f32<T>(b.z); x[7] = from_f32<T>(b.w);
+    return x;
+  }
+}
+// The new token's eight elements into the ring (widened exactly when the ring is float32).
+template <typename T, typename R>
+__device__ __forceinline__ void store_ring8(R* p, const typename Ring8<T>::V8& x) {
+  if constexpr (sizeof(R) == sizeof(T)) {
+    *reinterpret_cast<typename Ring8<T>::V8*>(p) = x;
+  } else {
+    reinterpret_cast<float4*>(p)[0] = make_float4(to_f32(x[0]), to_f32(x[1]), to_f32(x[2]), to_f32(x[3]));
+    reinterpret_cast<float4*>(p)[1] = make_float4(to_f32(x[4]), to_f32(x[5]), to_f32(x[6]), to_f32(x[7]));
+  }
+}
+
+template <typename T, typename R, int D, int GM>
 __global__ __launch_bounds__(RingShape<GM>::NT) void ring_attn_kernel(
     const T* __restrict__ q, const T* __restrict__ knew, const T* __restrict__ vnew, const int64_t* __restrict__ pos,
-    T* ring_k, T* ring_v, int64_t* ring_pos, uint8_t* ring_valid, T* __restrict__ o, const uint8_t* __restrict__ active,
+    R* ring_k, R* ring_v, int64_t* ring_pos, uint8_t* ring_valid, T* __restrict__ o, const uint8_t* __restrict__ active,
     uint32_t* __restrict__ counters, int H, int HKV, int W, float scale_log2, int write) {
   constexpr int NT = RingShape<GM>::NT;
   constexpr int NW = NT / 64;              // waves
@@ -118,8 +149,8 @@ __global__ __launch_bounds__(RingShape<GM>::NT) void ring_attn_kernel(
       return group_sum<KL>(s) * scale_log2;
     };
 
-    const T* kb = ring_k + head_off;
-    const T* vb = ring_v + head_off;
+    const R* kb = ring_k + head_off;
+    const R* vb = ring_v + head_off;
     for (int j0 = 0; j0 < W; j0 += BATCH) {
       // positions and flags first, then every key and value load of the batch: waiting for the
       // first does not wait for the rest (the load counter retires in order)
@@ -135,8 +166,8 @@ __global__ __launch_bounds__(RingShape<GM>::NT) void ring_attn_kernel(
 #pragma unroll
       for (int i = 0; i < KPT; ++i) {
         const int j = min(j0 + kg + i * KPP, W - 1);  // keys past W re-read row W - 1, masked below
-        kr[i] = *reinterpret_cast<const V8*>(kb + (size_t)j * row_stride);
-        vr[i] = *reinterpret_cast<const V8*>(vb + (size_t)j * row_stride);
+        kr[i] = load_ring8<T>(kb + (size_t)j * row_stride);
+        vr[i] = load_ring8<T>(vb + (size_t)j * row_stride);
       }
       if (j0 == 0) {  // the group's query heads (heads past G are zero: their results are never stored)
         const T* qb = q + ((size_t)b * H + (size_t)kvh * G) * D;
@@ -247,10 +278,10 @@ __global__ __launch_bounds__(RingShape<GM>::NT) void ring_attn_kernel(
   const size_t dst = ((size_t)b * W + slot) * row_stride + (size_t)kvh * D;
   const size_t src = ((size_t)b * HKV + kvh) * D;
   if (tid < KL) {
-    *reinterpret_cast<V8*>(ring_k + dst + 8 * tid) = *reinterpret_cast<const V8*>(knew + src + 8 * tid);
+    store_ring8<T>(ring_k + dst + 8 * tid, *reinterpret_cast<const V8*>(knew + src + 8 * tid));
   } else if (tid < 2 * KL) {
     const int pp = tid - KL;
-    *reinterpret_cast<V8*>(ring_v + dst + 8 * pp) = *reinterpret_cast<const V8*>(vnew + src + 8 * pp);
+    store_ring8<T>(ring_v + dst + 8 * pp, *reinterpret_cast<const V8*>(vnew + src + 8 * pp));
   }
 }
 
@@ -258,8 +289,8 @@ bool ring_width(int D) { return D == 16 || D == 32 || D == 64 || D == 128; }
 
 bool aligned16(const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15) == 0; }
 
-template <typename T>
-int ring_attn(const T* q, const T* knew, const T* vnew, const int64_t* pos, T* ring_k, T* ring_v, int64_t* ring_pos,
+template <typename T, typename R = T>
+int ring_attn(const T* q, const T* knew, const T* vnew, const int64_t* pos, R* ring_k, R* ring_v, int64_t* ring_pos,
               uint8_t* ring_valid, T* o, const uint8_t* active, void* workspace, size_t ws_bytes, int B, int H, int HKV,
               int D, int W, float scale, int write, void* stream_ptr, const char* who) {
   if (B < 0 || H < 1 || HKV < 1 || W < 1) return fail(ERR_ARG, "%s: bad sizes B=%d H=%d HKV=%d W=%d", who, B, H, HKV, W);
@@ -285,10 +316,10 @@ int ring_attn(const T* q, const T* knew, const T* vnew, const int64_t* pos, T* r
   };
   auto by_group = [&](auto dtag) {
     constexpr int Dc = decltype(dtag)::value;
-    if (G == 1) go(ring_attn_kernel<T, Dc, 1>, RingShape<1>::NT);
-    else if (G == 2) go(ring_attn_kernel<T, Dc, 2>, RingShape<2>::NT);
-    else if (G <= 4) go(ring_attn_kernel<T, Dc, 4>, RingShape<4>::NT);
-    else go(ring_attn_kernel<T, Dc, 8>, RingShape<8>::NT);
+    if (G == 1) go(ring_attn_kernel<T, R, Dc, 1>, RingShape<1>::NT);
+    else if (G == 2) go(ring_attn_kernel<T, R, Dc, 2>, RingShape<2>::NT);
+    else if (G <= 4) go(ring_attn_kernel<T, R, Dc, 4>, RingShape<4>::NT);
+    else go(ring_attn_kernel<T, R, Dc, 8>, RingShape<8>::NT);
   };
   switch (D) {
     case 16: by_group(std::integral_constant<int, 16>{}); break;
@@ -401,4 +432,30 @@ extern "C" int vsp_ring_attn_f16(const void* q, const void* k, const void* v, co
                                   static_cast<_Float16*>(ring_v), ring_pos, ring_valid, static_cast<_Float16*>(o),
                                   active, workspace, workspace_bytes, B, H, HKV, D, window, scale, write, stream,
                                   "vsp_ring_attn_f16");
+}
+
+// The ring in float32 with bf16 / fp16 queries: the ring the reference's captured decoder allocates
+// (init_states(1, torch.float32, ...), vesper/decode.py:81,85; column.py:492), whose keys and values
+// attend_ring casts to the queries' dtype (attention.py:325). Each ring element is rounded to the
+// queries' dtype as it is loaded; the new token is written into its slot widened to float32.
+extern "C" int vsp_ring_attn_bf16_ring_f32(const void* q, const void* k, const void* v, const int64_t* pos,
+                                           float* ring_k, float* ring_v, int64_t* ring_pos, uint8_t* ring_valid,
+                                           void* o, const uint8_t* active, void* workspace, size_t workspace_bytes,
+                                           int B, int H, int HKV, int D, int window, float scale, int write,
+                                           void* stream) {
+  return vsp::ring_attn<__bf16, float>(static_cast<const __bf16*>(q), static_cast<const __bf16*>(k),
+                                       static_cast<const __bf16*>(v), pos, ring_k, ring_v, ring_pos, ring_valid,
+                                       static_cast<__bf16*>(o), active, workspace, workspace_bytes, B, H, HKV, D,
+                                       window, scale, write, stream, "vsp_ring_attn_bf16_ring_f32");
+}
+
+extern "C" int vsp_ring_attn_f16_ring_f32(const void* q, const void* k, const void* v, const int64_t* pos,
+                                          float* ring_k, float* ring_v, int64_t* ring_pos, uint8_t* ring_valid,
+                                          void* o, const uint8_t* active, void* workspace, size_t workspace_bytes,
+                                          int B, int H, int HKV, int D, int window, float scale, int write,
+                                          void* stream) {
+  return vsp::ring_attn<_Float16, float>(static_cast<const _Float16*>(q), static_cast<const _Float16*>(k),
+                                         static_cast<const _Float16*>(v), pos, ring_k, ring_v, ring_pos, ring_valid,
+                                         static_cast<_Float16*>(o), active, workspace, workspace_bytes, B, H, HKV, D,
+                                         window, scale, write, stream, "vsp_ring_attn_f16_ring_f32");
 }

@@ -66,7 +66,9 @@ def ring_attention(q: Tensor, k: Tensor, v: Tensor, pos: Tensor, cache: RingKVCa
         q: ``[b, 1, h, dk]`` rotated queries, bfloat16 or float16.
         k, v: ``[b, 1, hkv, dk]`` the new token's rotated key and value, q's dtype.
         pos: ``[b, 1]`` int64 nonnegative positions.
-        cache: the ring (its keys and values in q's dtype).
+        cache: the ring, its keys and values in q's dtype or in float32 (the reference decoder's
+            allocation; each element is then rounded to q's dtype as it is read, and the new token
+            is written widened to float32).
         active: optional bool ``[b]``; an inactive row's output is zero, its token is still written.
         inplace: write into ``cache``'s tensors instead of a copy.
         check_positions: hold ``pos >= 0`` with ``require`` (a device assert under graph capture).
@@ -88,9 +90,15 @@ def ring_attention(q: Tensor, k: Tensor, v: Tensor, pos: Tensor, cache: RingKVCa
     check_shape("cache.valid", cache.valid, ("b", "w"), dims, torch.bool)
     if q.dtype not in (torch.bfloat16, torch.float16):
         raise ContractError(f"q: dtype must be bfloat16 or float16, got {q.dtype}")
-    for name, t in (("k", k), ("v", v), ("cache.k", cache.k), ("cache.v", cache.v)):
+    for name, t in (("k", k), ("v", v)):
         if t.dtype != q.dtype:
             raise ContractError(f"{name}: dtype must be {q.dtype}, got {t.dtype}")
+    # the ring in q's dtype, or in float32 as the reference's decoder allocates it (decode.py:81,85;
+    # column.py:492): then each element is rounded to q's dtype as it is read (attention.py:325)
+    ring_dtype = cache.k.dtype
+    if ring_dtype not in (q.dtype, torch.float32) or cache.v.dtype != ring_dtype:
+        raise ContractError(f"cache.k, cache.v: dtype must be {q.dtype} or torch.float32 (both alike), got "
+                            f"{cache.k.dtype} and {cache.v.dtype}")
     if q.device.type != "cuda":
         raise ContractError(f"the ring attention kernel runs on CUDA only, got q on {q.device}")
     for name, t in (("k", k), ("v", v), ("pos", pos), ("cache.k", cache.k), ("cache.v", cache.v),
@@ -132,6 +140,8 @@ def ring_attention(q: Tensor, k: Tensor, v: Tensor, pos: Tensor, cache: RingKVCa
         if counters.numel() < b:
             raise ContractError(f"workspace holds {counters.numel()} counters, {b} rows need {b}")
     entry = "vsp_ring_attn_bf16" if q.dtype == torch.bfloat16 else "vsp_ring_attn_f16"
+    if ring_dtype == torch.float32:
+        entry += "_ring_f32"
     with torch.cuda.device(q.device):
         _lib.call(entry, q.data_ptr(), k.data_ptr(), v.data_ptr(), pos.data_ptr(), ring.k.data_ptr(),
                   ring.v.data_ptr(), ring.pos.data_ptr(), ring.valid.data_ptr(), o.data_ptr(), _lib.ptr(mask),
