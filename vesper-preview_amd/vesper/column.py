@@ -49,14 +49,15 @@ FUSED_INPUT_DTYPES: dict[ScanImpl, torch.dtype] = {
 
 
 def check_scan(impl: str, device: torch.device) -> ScanImpl:
-    """The one check of a scan choice against the device it would run on; returns it typed.
+    """Validate ``impl`` for a model whose parameters live on ``device`` and return it as a
+    ``ScanImpl`` (the contract of ``column.py:382-405``).
 
-    "reference" runs anywhere (``column.py:382-405``); the HIP scans need the GPU and the built
-    kernel library.
+    The PyTorch "reference" scan is accepted on any device; "fused" and "fused-fp32" are this
+    package's HIP kernels, so they need a GPU device and ``libvesper_kernels.so`` loaded.
 
     Raises:
-        ValueError: if ``impl`` is not one of ``SCAN_IMPLS``, or a fused scan off the GPU or
-            without the built kernel library.
+        ValueError: for a name outside ``SCAN_IMPLS``; for a HIP scan on a non-GPU device or when
+            the kernel library is not available.
     """
     if impl == "reference":
         return "reference"
@@ -70,12 +71,13 @@ def check_scan(impl: str, device: torch.device) -> ScanImpl:
 
 
 def check_capturable_scan(impl: str, device: torch.device) -> ScanImpl:
-    """``check_scan``, and the choice must run inside a captured HIP graph on the GPU
-    (``column.py:408-426``): both HIP scans do (no allocation in the library, no host
-    synchronisation); the reference scan on the GPU is refused.
+    """Like ``check_scan``, for a caller that will replay the scan from a captured HIP graph
+    (``column.py:408-426``). The HIP scans allocate nothing and never synchronise with the host,
+    so either captures; the PyTorch scan on a GPU does not (it solves a triangular system per
+    block) and is turned down there.
 
     Raises:
-        ValueError: as ``check_scan``, or the reference scan on the GPU.
+        ValueError: whatever ``check_scan`` raises, and for "reference" on a GPU device.
     """
     chosen = check_scan(impl, device)
     if chosen == "reference" and device.type == "cuda":
@@ -85,16 +87,17 @@ def check_capturable_scan(impl: str, device: torch.device) -> ScanImpl:
 
 
 def set_scan(model: nn.Module, impl: str) -> int:
-    """Choose the scan implementation of every ``RecurrentSublayer`` in ``model`` (``column.py:353-380``).
+    """Switch every ``RecurrentSublayer`` of ``model`` to the scan ``impl`` (``column.py:353-380``).
 
-    Every parameter's device is checked with ``check_scan`` before any sublayer changes.
+    The choice is validated with ``check_scan`` for the device of each parameter first, so a
+    refused choice leaves the model as it was.
 
     Returns:
-        The number of sublayers set.
+        How many sublayers now use ``impl``.
 
     Raises:
-        ValueError: if ``impl`` is not one of ``SCAN_IMPLS``, if ``model`` has no recurrent
-            sublayer, or if a fused scan is asked where it cannot run.
+        ValueError: for a name outside ``SCAN_IMPLS``, a model without recurrent sublayers, or a
+            HIP scan on a device where ``check_scan`` turns it down.
     """
     if impl not in SCAN_IMPLS:
         raise ValueError(f"scan must be one of {SCAN_IMPLS}, got {impl!r}")
@@ -110,10 +113,11 @@ def set_scan(model: nn.Module, impl: str) -> int:
 
 
 def scan_of(model: nn.Module) -> ScanImpl:
-    """The scan implementation every ``RecurrentSublayer`` in ``model`` uses (``column.py:428-441``).
+    """The one scan implementation shared by all of ``model``'s ``RecurrentSublayer`` modules
+    (``column.py:428-441``).
 
     Raises:
-        ValueError: if the model has no recurrent sublayer or its sublayers disagree.
+        ValueError: when there is no recurrent sublayer, or when they do not all use the same scan.
     """
     impls = {m.scan_impl for m in model.modules() if isinstance(m, RecurrentSublayer)}
     if len(impls) != 1:

@@ -49,7 +49,8 @@ def fused_scan_available() -> bool:
 
 
 def _checked_length(q: Tensor, k: Tensor, v: Tensor, beta: Tensor, state: Tensor, input_dtype: torch.dtype) -> int:
-    """The one contract check of the scans (reference ``delta_scan.py:93-119``); returns ``n``.
+    """Shape, dtype, device and width checks shared by both scan entries (the contract of the
+    reference's ``delta_scan.py:93-119``, with its error texts); returns the token count ``n``.
 
     Raises:
         ContractError: on a shape or dtype mismatch, a tensor off the GPU or on another device than
@@ -224,22 +225,24 @@ def _autograd_scan(q: Tensor, k: Tensor, v: Tensor, beta: Tensor, state: Tensor,
 def delta_scan_fused(q: Tensor, k: Tensor, v: Tensor, beta: Tensor, state: Tensor, *,
                      active: Tensor | None = None,
                      carried: tuple[Tensor, Tensor, Tensor] | None = None) -> tuple[Tensor, Tensor]:
-    """Apply ``n`` tokens to the state with the chunked bfloat16 kernel.
+    """Run the delta rule over a block of ``n`` tokens on the bf16 HIP kernels (chunked WY/UT form,
+    fp32 state), the drop-in for ``vesper/kernels/delta_scan.py:132-153``.
 
     Args:
-        q: ``[b, n, h, dk]`` queries, bfloat16, on the GPU.
-        k: ``[b, n, h, dk]`` keys, bfloat16, L2 norm at most one.
-        v: ``[b, n, h, dk]`` values, bfloat16.
-        beta: ``[b, n, h]`` write strengths in [0, 1], bfloat16.
-        state: ``[b, h, dk, dk]`` the state before the first token, float32.
-        active: optional bool ``[b, n]``; inactive tokens write the state, their outputs are zero.
-        carried: optional ``(k, v, beta)`` shaped as ``k, v, beta`` (needs ``active``): an inactive
-            token writes these rows instead of its fresh ones, as after ``where(active, fresh,
-            carried)`` merges.
+        q: the queries ``[b, n, h, dk]`` in bfloat16, resident on the GPU.
+        k: the keys, same shape and dtype; the caller normalizes them (norm at most one).
+        v: the values, same shape and dtype.
+        beta: per token and head ``[b, n, h]``, bfloat16, each in [0, 1].
+        state: the fp32 state ``[b, h, dk, dk]`` the block starts from, read as ``H^T q``.
+        active: optional bool ``[b, n]``: a token marked False still updates the state, but its
+            output row is zero.
+        carried: optional ``(k, v, beta)`` with the shapes of ``k, v, beta`` (requires ``active``):
+            rows that an inactive token writes in place of its fresh ones, the same result as
+            merging with ``where(active, fresh, carried)`` first.
 
     Returns:
-        ``(o, state_n)``: ``o [b, n, h, dk]`` bfloat16 and the final state in float32; with no
-        tokens, the empty query tensor and the unchanged state object.
+        ``(o, state_n)``: the outputs ``[b, n, h, dk]`` in bfloat16 and the fp32 state after the
+        block; for ``n == 0`` the (empty) ``q`` tensor itself and the same ``state`` object.
 
     Under autograd the gradients of ``q, k, v, beta`` (bfloat16) and ``state`` (float32) come from
     the backward kernels.
