@@ -173,7 +173,7 @@ int vsp_delta_scan_backward_recorded_bf16(const void* q, const void* k, const vo
  * q: [B, N, H, D]; keys, values: [B, M + N, HKV, D], the cache's M rows first; o: [B, N, H, D].
  * Query i sits at key index M + i and attends key indices [M + i - window + 1, M + i]; softmax in
  * fp32 with `scale` (1/sqrt(D) for the reference); query head h reads KV head h / (H / HKV).
- * D in {16, 32, 64, 128}; H a multiple of HKV; active: [B, N] or NULL.
+ * D in {16, 32, 64, 128, 256}; H a multiple of HKV; active: [B, N] or NULL.
  * Replaces the fla-core 0.5.2 `parallel_attn` call of vesper/kernels/window_attn.py:27-39
  * (`window_attention`), without the zero query rows the reference pads the cache with. */
 int vsp_window_attn_bf16(const void* q, const void* keys, const void* values, void* o, const uint8_t* active,

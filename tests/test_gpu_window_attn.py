@@ -49,7 +49,7 @@ def test_the_kernel_equals_the_oracle_window(n, m):
 
 
 @pytest.mark.parametrize("dtype", [BF16, torch.float16])
-@pytest.mark.parametrize("dk", [16, 32, 64, 128])
+@pytest.mark.parametrize("dk", [16, 32, 64, 128, 256])
 @pytest.mark.parametrize(("n", "m", "w"), [(1, 0, 1), (70, 3, 7), (130, 64, 64), (300, 100, 100), (200, 40, 600)])
 def test_widths_windows_and_offsets(dtype, dk, n, m, w):
     from vesper.kernels.window_attn import window_attention
@@ -126,12 +126,12 @@ def test_refusals():
         window_attention(dq, dk_[:, :4], dv[:, :4], 4)
     with pytest.raises(ValueError, match="window"):
         window_attention(dq, dk_, dv, 0)
-    wide = torch.zeros(1, 8, 4, 136, dtype=BF16, device=GPU)
+    wide = torch.zeros(1, 8, 4, 264, dtype=BF16, device=GPU)
     with pytest.raises(ContractError, match="exceeds"):
         window_attention(wide, wide[:, :, :2], wide[:, :, :2], 4)
 
 
-@pytest.mark.parametrize("dk", [8, 24, 48, 96])
+@pytest.mark.parametrize("dk", [8, 24, 48, 96, 192])
 def test_widths_between_the_kernels_run_zero_padded(dk):
     """A head width the kernels do not tile runs with zero features up to the next one (scale
     1 / sqrt(dk) kept): outputs and gradients against the oracle at that width, with a cache, grouped
@@ -215,7 +215,7 @@ def test_the_gradients_match_the_oracle(n, m):
         torch.testing.assert_close(a.float().cpu(), b.float(), rtol=3e-2, atol=3e-2, msg=name)
 
 
-@pytest.mark.parametrize("dk", [16, 32, 64, 128])
+@pytest.mark.parametrize("dk", [16, 32, 64, 128, 256])
 @pytest.mark.parametrize(("h", "hkv"), [(2, 2), (8, 1), (8, 4)])
 @pytest.mark.parametrize("dtype", [BF16, torch.float16])
 def test_the_gradients_for_every_width_and_group(dk, h, hkv, dtype):
@@ -299,7 +299,7 @@ def _merged_kv(keys, values, carried, active):
 
 
 @pytest.mark.parametrize("dtype", [BF16, torch.float16])
-@pytest.mark.parametrize("dk", [16, 32, 64, 128])
+@pytest.mark.parametrize("dk", [16, 32, 64, 128, 256])
 @pytest.mark.parametrize(("n", "m", "w", "h", "hkv"), [(70, 0, 16, 4, 2), (200, 40, 64, 8, 2), (300, 100, 600, 4, 4)])
 def test_carried_keys_and_values_equal_the_merged_ones_bitwise(dtype, dk, n, m, w, h, hkv):
     from vesper.kernels.window_attn import window_attention

@@ -33,7 +33,7 @@ constexpr float kLazy = 8.f;
 // ([B, N, HKV, D], the carried keys and values) instead of keys / values. Its per-lane 64-bit
 // source addresses need more registers: three workgroups per CU at D 64 instead of four.
 template <typename T, int D, bool CARRY>
-__global__ __launch_bounds__(256, D >= 128 ? 2 : (CARRY && D == 64 ? 3 : 4)) void window_attn_kernel(const T* __restrict__ q, const T* __restrict__ keys,
+__global__ __launch_bounds__(256, D >= 256 ? 1 : (D >= 128 ? 2 : (CARRY && D == 64 ? 3 : 4))) void window_attn_kernel(const T* __restrict__ q, const T* __restrict__ keys,
                                                              const T* __restrict__ values, T* __restrict__ o,
                                                              float* __restrict__ lse,
                                                              const uint8_t* __restrict__ active, const T* keys_c,
@@ -385,7 +385,7 @@ __global__ __launch_bounds__(256, D >= 128 ? 2 : (CARRY && D == 64 ? 3 : 4)) voi
   }
 }
 
-bool attn_width(int D) { return D == 16 || D == 32 || D == 64 || D == 128; }
+bool attn_width(int D) { return D == 16 || D == 32 || D == 64 || D == 128 || D == 256; }
 
 template <typename T, bool CARRY>
 void launch_window(dim3 grid, hipStream_t stream, const T* q, const T* keys, const T* values, T* o, float* lse,
@@ -395,7 +395,8 @@ void launch_window(dim3 grid, hipStream_t stream, const T* q, const T* keys, con
     case 16: hipLaunchKernelGGL((window_attn_kernel<T, 16, CARRY>), grid, dim3(256), 0, stream, q, keys, values, o, lse, active, kc, vc, N, M, H, HKV, W, scale_log2, nqt); break;
     case 32: hipLaunchKernelGGL((window_attn_kernel<T, 32, CARRY>), grid, dim3(256), 0, stream, q, keys, values, o, lse, active, kc, vc, N, M, H, HKV, W, scale_log2, nqt); break;
     case 64: hipLaunchKernelGGL((window_attn_kernel<T, 64, CARRY>), grid, dim3(256), 0, stream, q, keys, values, o, lse, active, kc, vc, N, M, H, HKV, W, scale_log2, nqt); break;
-    default: hipLaunchKernelGGL((window_attn_kernel<T, 128, CARRY>), grid, dim3(256), 0, stream, q, keys, values, o, lse, active, kc, vc, N, M, H, HKV, W, scale_log2, nqt); break;
+    case 128: hipLaunchKernelGGL((window_attn_kernel<T, 128, CARRY>), grid, dim3(256), 0, stream, q, keys, values, o, lse, active, kc, vc, N, M, H, HKV, W, scale_log2, nqt); break;
+    default: hipLaunchKernelGGL((window_attn_kernel<T, 256, CARRY>), grid, dim3(256), 0, stream, q, keys, values, o, lse, active, kc, vc, N, M, H, HKV, W, scale_log2, nqt); break;
   }
 }
 
@@ -407,7 +408,7 @@ int window_attn(const T* q, const T* keys, const T* values, T* o, float* lse, co
   if (H % HKV != 0) return fail(ERR_ARG, "%s: %d query heads are not a multiple of %d KV heads", who, H, HKV);
   if (W < 1) return fail(ERR_ARG, "%s: window must be at least 1, got %d", who, W);
   if (!(scale > 0.f)) return fail(ERR_ARG, "%s: the score scale must be positive, got %g", who, (double)scale);
-  if (!attn_width(D)) return fail(ERR_UNSUPPORTED, "%s: head dimension %d (kernels: 16, 32, 64, 128)", who, D);
+  if (!attn_width(D)) return fail(ERR_UNSUPPORTED, "%s: head dimension %d (kernels: 16, 32, 64, 128, 256)", who, D);
   if (B == 0 || N == 0) return OK;
   if (!q || !keys || !values || !o) return fail(ERR_ARG, "%s: null pointer", who);
   if ((reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(keys) | reinterpret_cast<uintptr_t>(values) |

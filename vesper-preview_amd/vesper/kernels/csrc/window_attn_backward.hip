@@ -424,8 +424,8 @@ int window_attn_backward(const T* q, const T* keys, const T* values, const T* o,
   if (H % HKV != 0) return fail(ERR_ARG, "%s: %d query heads are not a multiple of %d KV heads", who, H, HKV);
   if (W < 1) return fail(ERR_ARG, "%s: window must be at least 1, got %d", who, W);
   if (!(scale > 0.f)) return fail(ERR_ARG, "%s: the score scale must be positive, got %g", who, (double)scale);
-  if (!(D == 16 || D == 32 || D == 64 || D == 128))
-    return fail(ERR_UNSUPPORTED, "%s: head dimension %d (kernels: 16, 32, 64, 128)", who, D);
+  if (!(D == 16 || D == 32 || D == 64 || D == 128 || D == 256))
+    return fail(ERR_UNSUPPORTED, "%s: head dimension %d (kernels: 16, 32, 64, 128, 256)", who, D);
   if (B == 0 || N == 0) return OK;  // no query: the caller's zero dK, dV stand
   if (!q || !keys || !values || !o || !dout || !lse || !dsum || !dq || !dk || !dv)
     return fail(ERR_ARG, "%s: null pointer", who);
@@ -440,7 +440,8 @@ int window_attn_backward(const T* q, const T* keys, const T* values, const T* o,
     case 16: launch_backward<T, 16>(q, keys, values, o, dout, lse, dsum, dq, dk, dv, B, N, M, H, HKV, W, scale, stream); break;
     case 32: launch_backward<T, 32>(q, keys, values, o, dout, lse, dsum, dq, dk, dv, B, N, M, H, HKV, W, scale, stream); break;
     case 64: launch_backward<T, 64>(q, keys, values, o, dout, lse, dsum, dq, dk, dv, B, N, M, H, HKV, W, scale, stream); break;
-    default: launch_backward<T, 128>(q, keys, values, o, dout, lse, dsum, dq, dk, dv, B, N, M, H, HKV, W, scale, stream); break;
+    case 128: launch_backward<T, 128>(q, keys, values, o, dout, lse, dsum, dq, dk, dv, B, N, M, H, HKV, W, scale, stream); break;
+    default: launch_backward<T, 256>(q, keys, values, o, dout, lse, dsum, dq, dk, dv, B, N, M, H, HKV, W, scale, stream); break;
   }
   return check_launch(who);
 }

@@ -32,7 +32,7 @@ from vesper.contracts import ContractError, Dims, check_shape
 from vesper.kernels import _lib
 
 WINDOW_KERNEL_DTYPES = (torch.bfloat16, torch.float16)
-HEAD_DIMS = (16, 32, 64, 128)
+HEAD_DIMS = (16, 32, 64, 128, 256)
 
 
 def _aligned(t: Tensor) -> Tensor:
@@ -109,7 +109,7 @@ def window_attention(q: Tensor, keys: Tensor, values: Tensor, window: int, *, ac
     Raises:
         ContractError: on shapes that disagree, a dtype other than bfloat16/float16 (or mixed), a
             tensor off the GPU, ``h`` not a multiple of ``hkv``, a head width the kernel does not
-            tile (above 128; narrower widths between the kernels' 16, 32, 64 and 128 run with zero
+            tile (above 256; narrower widths between the kernels' 16, 32, 64, 128 and 256 run with zero
             features added up to the next one, which change no score and no output), fewer key rows
             than queries, or carried keys and values without ``active`` or not shaped
             ``[b, n, hkv, dk]`` in the dtype of ``keys``.
