@@ -148,9 +148,13 @@ int vsp_delta_step_bf16(const void* q, const void* k, const void* v, const void*
  * under autograd): from d_o [B, N, H, D] (the inputs' dtype) and d_state [B, H, D, D] fp32 (the
  * final state's gradient; NULL for zero), dq, dk, dv [B, N, H, D], dbeta [B, N, H] (the inputs'
  * dtype) and d_state_in [B, H, D, D] fp32 (the initial state's). active as the forward (an inactive
- * token's output gradient is ignored). D in {16, 32, 64, 128} (bf16) or {16, 32, 64} (fp32); fp32
- * accumulation (the bf16 entry multiplies on bf16 MFMA); deterministic.
- * workspace: vsp_delta_scan_backward_workspace_bytes bytes, 16-byte aligned. N == 0 writes nothing. */
+ * token's output gradient is ignored). D: any multiple of 16 up to 256. {16, 32, 64, 128} (bf16)
+ * and {16, 32, 64} (fp32) run the tiled chunk kernels; other widths run the wide backward (the
+ * forward recomputed token by token to checkpoint each chunk's starting state, then per-chunk and
+ * per-value-group kernels whose partial sums are added in a fixed order). fp32 accumulation (the
+ * bf16 entry multiplies on bf16 MFMA); deterministic.
+ * workspace: vsp_delta_scan_backward_workspace_bytes bytes (the larger of both at D = 128), 16-byte
+ * aligned. N == 0 writes nothing. */
 size_t vsp_delta_scan_backward_workspace_bytes(int B, int N, int H, int D);
 int vsp_delta_scan_backward_bf16(const void* q, const void* k, const void* v, const void* beta, const float* state_in,
                                  const void* d_o, const float* d_state, const uint8_t* active, void* dq, void* dk,

@@ -51,6 +51,17 @@ def test_the_workspace_size_covers_every_chunk():
     assert lib.vsp_delta_scan_workspace_bytes(2, 130, 3, 128, 1) == 0  # fp32 at 128 runs token by token
     assert lib.vsp_delta_scan_workspace_bytes(2, 130, 3, 48, 1) == 0  # token-serial width
     assert lib.vsp_delta_scan_workspace_bytes(2, 10, 3, 64, 0) == 0  # short sequences are serial
+    # the backward: six [D, D] blocks and one [64, 64] block a chunk on the tiled widths; the wide
+    # backward keeps per head a [D, D] state a chunk, the state's gradient and the final state, and
+    # per chunk three [64, 64] blocks (L, P, the Gram matrix) and per value group of 64 columns two
+    # [64, 64] and two [64, D] partial sums
+    tiled = 2 * 3 * 3 * (64 * 64 + 6 * 64 * 64) * 4
+    assert lib.vsp_delta_scan_backward_workspace_bytes(2, 130, 3, 64) == tiled
+    wide = 2 * ((3 + 2) * 192 * 192 + 3 * (3 * 64 * 64 + 3 * (2 * 64 * 64 + 2 * 64 * 192))) * 4
+    assert lib.vsp_delta_scan_backward_workspace_bytes(1, 130, 2, 192) == wide
+    assert lib.vsp_delta_scan_backward_workspace_bytes(1, 130, 2, 128) == 2 * 3 * (64 * 64 + 6 * 128 * 128) * 4
+    assert lib.vsp_delta_scan_backward_workspace_bytes(1, 130, 2, 200) == 0  # not a multiple of 16
+    assert lib.vsp_delta_scan_backward_workspace_bytes(1, 130, 2, 272) == 0  # above 256
     assert lib.vsp_ring_attn_workspace_bytes(64) == 64 * 4  # one arrival counter per row
     assert lib.vsp_ring_attn_workspace_bytes(0) == 0
 

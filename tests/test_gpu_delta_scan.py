@@ -165,12 +165,9 @@ def test_refuses_what_the_contract_excludes():
                          torch.zeros(1, 1, 512, 512, device=GPU))
     with pytest.raises(ContractError, match="dtype"):
         delta_scan_fused_fp32(q, k, v, beta, h0)
-    with pytest.raises(ContractError, match="backward takes head widths up to 128"):
-        delta_scan_fused(q.new_zeros(1, 8, 1, 192).requires_grad_(), q.new_zeros(1, 8, 1, 192),
-                         q.new_zeros(1, 8, 1, 192), q.new_zeros(1, 8, 1), torch.zeros(1, 1, 192, 192, device=GPU))
-    f = torch.zeros(1, 8, 1, 128, device=GPU)
-    with pytest.raises(ContractError, match="backward takes head widths up to 64"):
-        delta_scan_fused_fp32(f.clone().requires_grad_(), f, f, f[..., 0], torch.zeros(1, 1, 128, 128, device=GPU))
+    f = torch.zeros(1, 8, 1, 264, device=GPU)
+    with pytest.raises(ContractError, match="exceeds"):
+        delta_scan_fused_fp32(f.clone().requires_grad_(), f, f, f[..., 0], torch.zeros(1, 1, 264, 264, device=GPU))
 
 
 def test_active_mask_zeroes_outputs_and_keeps_every_write():
@@ -326,6 +323,29 @@ def test_gradients_at_widths_the_kernels_take_zero_padded(dk, fp32):
 
     fn, make, tol = (delta_scan_fused_fp32, _fp32_inputs, TOL_FP32) if fp32 else (delta_scan_fused, _bf16_inputs, TOL)
     _grad_check(fn, make(2, 130, 2, dk, seed=dk), tol)
+
+
+@pytest.mark.parametrize(("dk", "fp32"), [(192, False), (200, False), (256, False), (80, True), (128, True),
+                                         (256, True)])
+def test_gradients_of_heads_wider_than_the_tiled_kernels(dk, fp32):
+    # the wide backward (chunk-start states checkpointed by the token-serial forward, value groups
+    # of 64, 32 or 16 columns, partial sums added in a fixed order): three chunks, the last partial,
+    # with an active mask; 200 runs zero-padded to 208 (value groups of 16)
+    from vesper.kernels.delta_scan import backward_width, delta_scan_fused, delta_scan_fused_fp32
+
+    assert backward_width(dk, fp32) == (208 if dk == 200 else dk)
+    fn, make, tol = (delta_scan_fused_fp32, _fp32_inputs, TOL_FP32) if fp32 else (delta_scan_fused, _bf16_inputs, TOL)
+    act = torch.rand(2, 150, generator=torch.Generator().manual_seed(dk)) < 0.7
+    first = _grad_check(fn, make(2, 150, 2, dk, seed=dk), tol, active=act)
+    # deterministic: a second backward over the same inputs gives the same bits
+    again = [t.detach().clone().requires_grad_() for t in first]
+    o, s = fn(*again, active=act.to(GPU))
+    g = torch.Generator().manual_seed(7)
+    d_o = torch.randn(o.shape, generator=g).to(GPU)
+    d_s = torch.randn(s.shape, generator=g).to(GPU)
+    torch.autograd.backward([(o.float() * d_o).sum() + (s * d_s).sum()])
+    for name, a, b_ in zip(["q", "k", "v", "beta", "state"], first, again):
+        assert torch.equal(a.grad, b_.grad), name
 
 
 @pytest.mark.parametrize(("b", "n", "h", "dk"), SIZES[:4])

@@ -18,6 +18,7 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+typedef short s16x4_t __attribute__((ext_vector_type(4)));
 
 namespace vsp {
 
@@ -55,6 +56,23 @@ bool delta_step_fast_f32(const float* q, const float* k, const float* v, const f
                          float* s_out, float* o, const uint8_t* active, int B, int H, int D, hipStream_t stream);
 bool delta_step_fast_bf16(const __bf16* q, const __bf16* k, const __bf16* v, const __bf16* beta, const float* s_in,
                           float* s_out, __bf16* o, const uint8_t* active, int B, int H, int D, hipStream_t stream);
+
+// The token-serial forward's states at each 64-token chunk's start (delta_scan.hip), and the
+// backward at head widths the chunked backward does not tile (delta_scan_backward_wide.hip).
+int delta_scan_checkpoints_bf16(const __bf16* q, const __bf16* k, const __bf16* v, const __bf16* beta,
+                                const float* s_in, float* s_out, float* ckpt, int B, int T, int H, int D,
+                                hipStream_t stream);
+int delta_scan_checkpoints_f32(const float* q, const float* k, const float* v, const float* beta, const float* s_in,
+                               float* s_out, float* ckpt, int B, int T, int H, int D, hipStream_t stream);
+size_t wide_backward_workspace_bytes(int B, int N, int H, int D);
+int scan_backward_wide_bf16(const __bf16* q, const __bf16* k, const __bf16* v, const __bf16* beta,
+                            const float* state_in, const __bf16* d_o, const float* d_state, const uint8_t* active,
+                            __bf16* dq, __bf16* dk, __bf16* dv, __bf16* dbeta, float* d_state_in, void* workspace,
+                            size_t workspace_bytes, int B, int N, int H, int D, hipStream_t stream, const char* who);
+int scan_backward_wide_f32(const float* q, const float* k, const float* v, const float* beta, const float* state_in,
+                           const float* d_o, const float* d_state, const uint8_t* active, float* dq, float* dk,
+                           float* dv, float* dbeta, float* d_state_in, void* workspace, size_t workspace_bytes, int B,
+                           int N, int H, int D, hipStream_t stream, const char* who);
 
 // ---- the write strength (vesper/recurrence.py:34-88) -------------------------------------------
 // beta = sigmoid(logit + ln(1 + alpha m)) of a write-strength logit and the token's modulator m,
@@ -161,6 +179,57 @@ __device__ __forceinline__ void store_tile_t(E* base, int ld, f32x4 acc) {
   for (int r = 0; r < 4; ++r) base[c * ld + r0 + r] = from_f32<E>(acc[r]);
 }
 
+// C[16 x 16] += op(X)[16 x K] op(Y)[K x 16] on fp32 MFMA. op(X)[i][k] is X[i * ldx + k] (TA false)
+// or X[k * ldx + i] (TA true, X stored [k][i]); op(Y)[k][j] is Y[k * ldy + j] (TB false) or
+// Y[j * ldy + k] (TB true), times yscale[k] when given. X and Y point at the tile's origin (16-byte
+// aligned, pitches multiples of 4). Lane group g supplies k = (K / 4) g + m in step m (the sum's
+// order is free), so a row-contiguous operand comes in 16-byte LDS reads of four k. The result:
+// lane (j, g) holds rows 4 g .. 4 g + 3 of column j. BF: the four k of a step are rounded to bf16
+// and multiplied by one 16x16x16 bf16 MFMA (fp32 accumulation) instead of four fp32 ones.
+template <bool TA, bool TB, bool BF = false>
+__device__ __forceinline__ f32x4 mm16(const float* X, int ldx, const float* Y, int ldy, int K, f32x4 acc,
+                                      const float* yscale = nullptr) {
+  const int l = threadIdx.x & 63, i = l & 15, g = l >> 4;
+  const int KM = K / 4, kb = KM * g;
+  for (int m = 0; m < KM; m += 4) {
+    float a[4], b[4];
+    if constexpr (!TA) {
+      const f32x4 v = *reinterpret_cast<const f32x4*>(X + i * ldx + kb + m);
+#pragma unroll
+      for (int u = 0; u < 4; ++u) a[u] = v[u];
+    } else {
+#pragma unroll
+      for (int u = 0; u < 4; ++u) a[u] = X[(kb + m + u) * ldx + i];
+    }
+    if constexpr (TB) {
+      const f32x4 v = *reinterpret_cast<const f32x4*>(Y + i * ldy + kb + m);
+#pragma unroll
+      for (int u = 0; u < 4; ++u) b[u] = v[u];
+    } else {
+#pragma unroll
+      for (int u = 0; u < 4; ++u) b[u] = Y[(kb + m + u) * ldy + i];
+    }
+    if (yscale != nullptr) {
+#pragma unroll
+      for (int u = 0; u < 4; ++u) b[u] *= yscale[kb + m + u];
+    }
+    if constexpr (BF) {
+      bf16x4 av, bv;
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        av[u] = (__bf16)a[u];
+        bv[u] = (__bf16)b[u];
+      }
+      acc = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(s16x4_t, av), __builtin_bit_cast(s16x4_t, bv),
+                                                      acc, 0, 0, 0);
+    } else {
+#pragma unroll
+      for (int u = 0; u < 4; ++u) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[u], b[u], acc, 0, 0, 0);
+    }
+  }
+  return acc;
+}
+
 // ---- lane reductions through DPP (a VALU modifier: no LDS traffic, unlike ds_bpermute) --------
 template <int CTRL>
 __device__ __forceinline__ float dpp_f32(float x) {
@@ -216,7 +285,6 @@ __device__ __forceinline__ float group_max(float x) {
 // 4e + i / 4 (e = 0..3). So when lane j of a group addresses row r0 + j / 4, column c0 + 4 (j % 4)
 // of a row-major tile of 16-bit elements, lane i receives column c0 + i of rows r0 .. r0 + 3: the
 // k-contiguous operand fragment of an MFMA whose k index runs down the tile's rows.
-typedef short s16x4_t __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) s16x4_t lds_s16x4_t;
 template <typename V4, typename T>
 __device__ __forceinline__ V4 read_tr16(const T* p) {

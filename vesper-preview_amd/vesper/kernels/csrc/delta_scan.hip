@@ -53,7 +53,7 @@ __global__ __launch_bounds__(256) void delta_serial_kernel(const TIn* __restrict
                                                            TIn* __restrict__ o, const uint8_t* __restrict__ active,
                                                            const TIn* kc, const TIn* vc, const TIn* bc, int T, int H,
                                                            int D, int groups, const float* mod_m, float mod_alpha,
-                                                           int beta_logits) {
+                                                           int beta_logits, float* ckpt) {
   // (scalar pointer arguments: a struct argument would be read through private memory and count as
   // divergent, which turns every buffer access on it into a loop over lanes)
   const Carried<TIn> carried{kc, vc, bc};
@@ -108,6 +108,15 @@ __global__ __launch_bounds__(256) void delta_serial_kernel(const TIn* __restrict
     }
     __syncthreads();
     for (int tt = 0; tt < nt; ++tt) {
+      if (ckpt != nullptr && ((t0 + tt) & 63) == 0) {
+        // the state at a 64-token chunk's start, for the backward: [b, h][chunk][row][column]
+        float* dst = ckpt + ((size_t)bh * ((T + 63) >> 6) + ((t0 + tt) >> 6)) * D * D;
+#pragma unroll
+        for (int r = 0; r < 64; ++r) {
+          const int row = wv * 64 + r;
+          if (col_ok && row < D) dst[(size_t)row * D + col] = st[r];
+        }
+      }
       const float* kr = &sk[tt][wv * 64];
       const float* qr = &sq[tt][wv * 64];
       float p0 = 0.f, p1 = 0.f, p2 = 0.f, p3 = 0.f;
@@ -145,7 +154,7 @@ __global__ __launch_bounds__(256) void delta_serial_kernel(const TIn* __restrict
         out = 0.f;
         for (int g = 0; g < groups; ++g) out += red[1][g][lane];
       }
-      if (wv == 0 && col_ok)
+      if (wv == 0 && col_ok && o != nullptr)
         o[(((size_t)b * T + t0 + tt) * H + h) * D + col] = from_f32<TIn>(sa[tt] ? out : 0.f);
     }
   }
@@ -1333,7 +1342,7 @@ int launch_serial(const TIn* q, const TIn* k, const TIn* v, const TIn* beta, con
   dim3 grid((unsigned)(B * H), (unsigned)groups);
   hipLaunchKernelGGL(delta_serial_kernel<TIn>, grid, dim3(64 * groups), 0, stream, q, k, v, beta, s_in, s_out, o,
                      active, carried.k, carried.v, carried.beta, T, H, D, groups, strength.m, strength.alpha,
-                     strength.logits);
+                     strength.logits, (float*)nullptr);
   return check_launch(who);
 }
 
@@ -1436,6 +1445,30 @@ int delta_step(const TIn* q, const TIn* k, const TIn* v, const TIn* beta, const 
 }
 
 }  // namespace
+
+// The states at every 64-token chunk's start (ckpt: [B, H, ceil(T / 64), D, D] fp32), from the
+// token-serial forward with its outputs dropped; s_out receives the final state. For the backward
+// at head widths the chunked kernels do not tile.
+int delta_scan_checkpoints_bf16(const __bf16* q, const __bf16* k, const __bf16* v, const __bf16* beta,
+                                const float* s_in, float* s_out, float* ckpt, int B, int T, int H, int D,
+                                hipStream_t stream) {
+  const int groups = (D + 63) / 64;
+  hipLaunchKernelGGL(delta_serial_kernel<__bf16>, dim3((unsigned)(B * H), (unsigned)groups), dim3(64 * groups), 0,
+                     stream, q, k, v, beta, s_in, s_out, (__bf16*)nullptr, (const uint8_t*)nullptr,
+                     (const __bf16*)nullptr, (const __bf16*)nullptr, (const __bf16*)nullptr, T, H, D, groups,
+                     (const float*)nullptr, 0.f, 0, ckpt);
+  return OK;
+}
+int delta_scan_checkpoints_f32(const float* q, const float* k, const float* v, const float* beta, const float* s_in,
+                               float* s_out, float* ckpt, int B, int T, int H, int D, hipStream_t stream) {
+  const int groups = (D + 63) / 64;
+  hipLaunchKernelGGL(delta_serial_kernel<float>, dim3((unsigned)(B * H), (unsigned)groups), dim3(64 * groups), 0,
+                     stream, q, k, v, beta, s_in, s_out, (float*)nullptr, (const uint8_t*)nullptr,
+                     (const float*)nullptr, (const float*)nullptr, (const float*)nullptr, T, H, D, groups,
+                     (const float*)nullptr, 0.f, 0, ckpt);
+  return OK;
+}
+
 }  // namespace vsp
 
 using vsp::delta_scan;

@@ -31,57 +31,6 @@ namespace {
 constexpr int kC = 64;       // tokens per chunk
 constexpr int kPC = kC + 4;  // pitch (floats) of a [.][64] LDS matrix
 
-// C[16 x 16] += op(X)[16 x K] op(Y)[K x 16] on fp32 MFMA. op(X)[i][k] is X[i * ldx + k] (TA false)
-// or X[k * ldx + i] (TA true, X stored [k][i]); op(Y)[k][j] is Y[k * ldy + j] (TB false) or
-// Y[j * ldy + k] (TB true), times yscale[k] when given. X and Y point at the tile's origin (16-byte
-// aligned, pitches multiples of 4). Lane group g supplies k = (K / 4) g + m in step m (the sum's
-// order is free), so a row-contiguous operand comes in 16-byte LDS reads of four k. The result:
-// lane (j, g) holds rows 4 g .. 4 g + 3 of column j. BF: the four k of a step are rounded to bf16
-// and multiplied by one 16x16x16 bf16 MFMA (fp32 accumulation) instead of four fp32 ones.
-template <bool TA, bool TB, bool BF = false>
-__device__ __forceinline__ f32x4 mm16(const float* X, int ldx, const float* Y, int ldy, int K, f32x4 acc,
-                                      const float* yscale = nullptr) {
-  const int l = threadIdx.x & 63, i = l & 15, g = l >> 4;
-  const int KM = K / 4, kb = KM * g;
-  for (int m = 0; m < KM; m += 4) {
-    float a[4], b[4];
-    if constexpr (!TA) {
-      const f32x4 v = *reinterpret_cast<const f32x4*>(X + i * ldx + kb + m);
-#pragma unroll
-      for (int u = 0; u < 4; ++u) a[u] = v[u];
-    } else {
-#pragma unroll
-      for (int u = 0; u < 4; ++u) a[u] = X[(kb + m + u) * ldx + i];
-    }
-    if constexpr (TB) {
-      const f32x4 v = *reinterpret_cast<const f32x4*>(Y + i * ldy + kb + m);
-#pragma unroll
-      for (int u = 0; u < 4; ++u) b[u] = v[u];
-    } else {
-#pragma unroll
-      for (int u = 0; u < 4; ++u) b[u] = Y[(kb + m + u) * ldy + i];
-    }
-    if (yscale != nullptr) {
-#pragma unroll
-      for (int u = 0; u < 4; ++u) b[u] *= yscale[kb + m + u];
-    }
-    if constexpr (BF) {
-      bf16x4 av, bv;
-#pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        av[u] = (__bf16)a[u];
-        bv[u] = (__bf16)b[u];
-      }
-      acc = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(s16x4_t, av), __builtin_bit_cast(s16x4_t, bv),
-                                                      acc, 0, 0, 0);
-    } else {
-#pragma unroll
-      for (int u = 0; u < 4; ++u) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[u], b[u], acc, 0, 0, 0);
-    }
-  }
-  return acc;
-}
-
 // mm16 over the k blocks kb0 .. kb1 - 1 of 16 (k = 16 kb0 .. 16 kb1 - 1): the part of a product
 // that a triangular operand leaves nonzero. Same operand conventions as mm16.
 template <bool TA, bool TB, bool BF = false>
@@ -1519,8 +1468,16 @@ int scan_backward(const TIn* q, const TIn* k, const TIn* v, const TIn* beta, con
                   void* stream_ptr, const char* who, const __bf16* hrec = nullptr) {
   if (B < 0 || N < 0 || H < 1) return fail(ERR_ARG, "%s: bad sizes B=%d N=%d H=%d", who, B, N, H);
   constexpr bool bf16 = sizeof(TIn) == 2;
-  if (!(D == 16 || D == 32 || D == 64 || (D == 128 && bf16)))
-    return fail(ERR_UNSUPPORTED, "%s: head dimension %d (backward: 16, 32, 64%s)", who, D, bf16 ? ", 128" : "");
+  if (!(D == 16 || D == 32 || D == 64 || (D == 128 && bf16))) {
+    // widths the chunked kernels do not tile: the wide backward (multiples of 16 up to 256)
+    if (hrec != nullptr) return fail(ERR_UNSUPPORTED, "%s: head dimension %d with records", who, D);
+    if constexpr (bf16)
+      return scan_backward_wide_bf16(q, k, v, beta, state_in, d_o, d_state, active, dq, dk, dv, dbeta, d_state_in,
+                                     workspace, workspace_bytes, B, N, H, D, static_cast<hipStream_t>(stream_ptr), who);
+    else
+      return scan_backward_wide_f32(q, k, v, beta, state_in, d_o, d_state, active, dq, dk, dv, dbeta, d_state_in,
+                                    workspace, workspace_bytes, B, N, H, D, static_cast<hipStream_t>(stream_ptr), who);
+  }
   if (B == 0 || N == 0) return OK;  // no token: the caller's state gradient passes through
   if (!q || !k || !v || !beta || !state_in || !d_o || !dq || !dk || !dv || !dbeta || !d_state_in)
     return fail(ERR_ARG, "%s: null pointer", who);
@@ -1552,7 +1509,10 @@ int scan_backward(const TIn* q, const TIn* k, const TIn* v, const TIn* beta, con
 
 extern "C" size_t vsp_delta_scan_backward_workspace_bytes(int B, int N, int H, int D) {
   if (B <= 0 || N <= 0 || H <= 0 || D <= 0) return 0;
-  return vsp::workspace_floats(B, N, H, D) * sizeof(float);
+  const size_t tiled = vsp::workspace_floats(B, N, H, D) * sizeof(float);
+  if (D == 16 || D == 32 || D == 64) return tiled;
+  const size_t wide = vsp::wide_backward_workspace_bytes(B, N, H, D);  // 0 where it does not run
+  return D == 128 ? (tiled > wide ? tiled : wide) : wide;  // 128: tiled for bf16, wide for fp32
 }
 
 extern "C" int vsp_delta_scan_backward_bf16(const void* q, const void* k, const void* v, const void* beta,

@@ -19,10 +19,12 @@ exactly the reference behaviour. With ``active``, the chunked scans also take ``
 beta)``: the copy-forward of halted tokens (``vesper/column.py:779-789``), read inside the kernels'
 loads (``vsp_delta_scan_carried_*``) where a token is inactive, in place of the ``where`` merges
 before the call. The two chunked scans are autograd functions: their backward
-(``vsp_delta_scan_backward_*``: head widths 16, 32, 64 and, on the bf16 entry, 128; a narrower
-width runs zero-padded to the next of these, which leaves every output and gradient unchanged)
-gives the gradients of ``q, k, v, beta`` and the initial state, as the reference's kernels do; the
-single step is forward only (inputs that require a gradient are refused while grad mode is on).
+(``vsp_delta_scan_backward_*``) gives the gradients of ``q, k, v, beta`` and the initial state at
+every width up to ``MAX_HEAD_DIM``, as the reference's kernels do. Its chunked kernels tile widths
+16, 32, 64 and, on the bf16 entry, 128; wider heads run a wide backward (state checkpoints from the
+token-serial forward, then chunk and value-group kernels) that takes multiples of 16. A width in
+between runs zero-padded to the next width taken, which leaves every output and gradient unchanged.
+The single step is forward only (inputs that require a gradient are refused while grad mode is on).
 """
 
 from __future__ import annotations
@@ -36,8 +38,16 @@ from vesper.contracts import ContractError, Dims, check_shape
 from vesper.kernels import _lib
 
 MAX_HEAD_DIM = 256  # delta_scan.py:41 in the reference; the HIP kernels take any width up to it
-# the widths the backward kernels take, on the bf16 and on the fp32 entry
+# the widths the tiled backward kernels take, on the bf16 and on the fp32 entry; wider heads take
+# the wide backward at any multiple of 16 up to MAX_HEAD_DIM
 BACKWARD_HEAD_DIMS = {False: (16, 32, 64, 128), True: (16, 32, 64)}
+
+
+def backward_width(dk: int, fp32: bool) -> int:
+    """The width the backward runs a head of width ``dk`` at (zero-padded up to it): the next tiled
+    width, else the next multiple of 16."""
+    tiled = next((w for w in BACKWARD_HEAD_DIMS[fp32] if w >= dk), None)
+    return tiled if tiled is not None else -(-dk // 16) * 16
 INPUT_DTYPE = torch.bfloat16  # delta_scan_fused's q, k, v, beta
 FP32_INPUT_DTYPE = torch.float32  # delta_scan_fused_fp32's q, k, v, beta
 STATE_DTYPE = torch.float32
@@ -204,10 +214,7 @@ def _autograd_scan(q: Tensor, k: Tensor, v: Tensor, beta: Tensor, state: Tensor,
         beta = torch.where(keep[..., 0], beta, carried[2])
         carried = None
     if grad:
-        widths = BACKWARD_HEAD_DIMS[fp32]
-        width = next((w for w in widths if w >= dk), None)
-        if width is None:
-            raise ContractError(f"the scan's backward takes head widths up to {widths[-1]}, got {dk}")
+        width = backward_width(dk, fp32)
         if width == dk:
             out: tuple[Tensor, Tensor] = _DeltaScan.apply(q, k, v, beta, state, mask, fp32)
             return out
@@ -248,8 +255,8 @@ def delta_scan_fused(q: Tensor, k: Tensor, v: Tensor, beta: Tensor, state: Tenso
     the backward kernels.
 
     Raises:
-        ContractError: on a dtype, shape, device or width outside the contract (with a gradient
-            needed, a head width outside 16, 32, 64), before any kernel runs.
+        ContractError: on a dtype, shape, device or width outside the contract, before any kernel
+            runs.
     """
     if _checked_length(q, k, v, beta, state, INPUT_DTYPE) == 0:
         return q, state
