@@ -22,7 +22,7 @@
 extern "C" {
 #endif
 
-#define VSP_ABI_VERSION 10
+#define VSP_ABI_VERSION 11
 
 /* Status codes. */
 #define VSP_OK 0
@@ -325,6 +325,23 @@ int vsp_key_step_f16(const void* z, const void* z_carried, const uint8_t* active
 int vsp_key_step_f32(const float* z, const float* z_carried, const uint8_t* active, const float* history,
                      const float* taps, float* keys, float* history_out, int B, int N, int D, int heads, int K,
                      void* stream);
+
+/* normalize_keys (vesper/recurrence.py:91-115) on `rows` rows of any width, x and y [rows, width]
+ * contiguous in one dtype: y = s / max(||s||, 1), s = x / max(max |x|, 1e-6), float32 arithmetic
+ * (the peak division correctly rounded, so the peak component becomes exactly 1), rounded to the
+ * dtype. The row form for widths the key filter does not take (above 512, or not a power of two),
+ * up to the reference's 65536-wide rows (tests/test_recurrence_review.py:61-64). The backward
+ * gives grad_x from grad_y with the peak held constant (recurrence.py:103-105). One wave a row;
+ * deterministic. rows == 0 or width == 0 writes nothing. */
+int vsp_normalize_keys_bf16(const void* x, void* y, int64_t rows, int width, void* stream);
+int vsp_normalize_keys_f16(const void* x, void* y, int64_t rows, int width, void* stream);
+int vsp_normalize_keys_f32(const float* x, float* y, int64_t rows, int width, void* stream);
+int vsp_normalize_keys_backward_bf16(const void* x, const void* grad_y, void* grad_x, int64_t rows, int width,
+                                     void* stream);
+int vsp_normalize_keys_backward_f16(const void* x, const void* grad_y, void* grad_x, int64_t rows, int width,
+                                    void* stream);
+int vsp_normalize_keys_backward_f32(const float* x, const float* grad_y, float* grad_x, int64_t rows, int width,
+                                    void* stream);
 
 /* The key filter's backward (vesper/kernels/keys.py:46-78, `_FusedKeys.backward`, on CUDA
  * vesper/kernels/keys_triton.py:56-177): from grad_keys [B, N, D] (z's dtype), with the

@@ -372,3 +372,95 @@ def test_the_key_step_writes_the_next_history(dtype, n, width, carry):
     assert nxt.dtype == torch.float32 and nxt.shape == (b, width - 1, d)
     assert torch.equal(nxt, want)
     assert torch.equal(keys, fused_keys(merged, history, taps, heads))
+
+
+# ---- normalize_keys alone, on rows of any width (vsp_normalize_keys_*) ---------------------------
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("width", [1, 3, 64, 100, 513, 4096, 65536])
+def test_normalize_keys_on_rows_of_any_width(width, dtype):
+    from vesper.kernels.keys import normalize_keys as fused
+
+    g = torch.Generator().manual_seed(width)
+    rows = 3 if width >= 4096 else 37
+    k = (torch.randn(rows, width, generator=g) * torch.logspace(-8, 3, rows)[:, None]).to(dtype)
+    k[0] = 0  # a zero row stays zero
+    got = fused(k.to(GPU))
+    assert got.dtype == dtype and got.shape == k.shape
+    bound = _bound(dtype)
+    torch.testing.assert_close(got.cpu().double(), normalize_keys(k.double()), rtol=bound, atol=bound)
+    assert torch.equal(fused(k.to(GPU)), got)  # repeatable
+    # leading dimensions are rows: a [2, rows / 2 ...] view gives the same rows
+    if rows % 2 == 0:
+        assert torch.equal(fused(k.to(GPU).view(2, rows // 2, width)).view(rows, width), got)
+
+
+def test_normalize_keys_reference_rows():
+    # tests/test_recurrence_review.py:50-87 of the reference: 65536 float16 ones give exactly 1/256
+    # each (the squared norm accumulated without overflow); a row whose peak is huge or tiny in its
+    # dtype is exactly a unit vector; a row under the 1e-6 floor is u / 1e-6; a zero row stays zero
+    from conftest import frac_tensor, reference_vectors
+    from vesper.kernels.keys import normalize_keys as fused
+
+    c = reference_vectors()["normalize_keys"]
+    assert c["wide_ones_fp16"]["n"] == 65536 and c["wide_ones_fp16"]["want_each"] == "1/256"
+    ones = torch.ones(1, 65536, dtype=torch.float16, device=GPU)
+    assert torch.equal(fused(ones), torch.full_like(ones, 1 / 256))
+    for dtype_name, magnitude in c["magnitudes_by_dtype"]["rows"]:
+        if dtype_name == "float64":
+            continue  # no float64 kernel
+        dtype = getattr(torch, dtype_name)
+        key = torch.tensor(((float(magnitude), 0.0),), dtype=dtype, device=GPU)
+        assert torch.equal(fused(key), torch.tensor(((1.0, 0.0),), dtype=dtype, device=GPU)), dtype_name
+    small = frac_tensor(c["small_floor"]["k"], torch.float32).to(GPU)
+    torch.testing.assert_close(fused(small).cpu().double(), frac_tensor(c["small_floor"]["want"]), rtol=1e-7, atol=0)
+    zero = torch.zeros(1, 3, device=GPU)
+    assert torch.equal(fused(zero), zero)
+
+
+def test_normalize_keys_gradients():
+    # the reference's independent derivative (tests/test_recurrence_review.py:67-72): at (s, 2 s),
+    # d((x + y) / sqrt(x^2 + y^2)) = (2, -1) / (5 sqrt 5) / s; then random rows at several widths
+    # against the oracle's autograd in float64, and rows under the floor (gradient g / 1e-6)
+    import math
+
+    from vesper.kernels.keys import normalize_keys as fused
+
+    for s in (1.0, 1e30):
+        key = torch.tensor(((s, 2 * s),), device=GPU, requires_grad=True)
+        (grad,) = torch.autograd.grad(fused(key).sum(), (key,))
+        want = torch.tensor(((2.0, -1.0),), dtype=torch.float64) / (5 * math.sqrt(5)) / s
+        torch.testing.assert_close(grad.cpu().double(), want, rtol=1e-6, atol=0)
+    g = torch.Generator().manual_seed(3)
+    for width, dtype, tol in ((7, torch.float32, 1e-5), (1000, torch.float32, 1e-5), (70000, torch.float32, 1e-5),
+                              (600, torch.bfloat16, 2e-2), (600, torch.float16, 4e-3)):
+        # rows under the floor, small, unit and large (float16: 1e-9 underflows to zero, whose
+        # gradient g / 1e-6 would overflow it)
+        tiny = 1e-4 if dtype == torch.float16 else 1e-9
+        k = (torch.randn(5, width, generator=g) * torch.tensor([tiny, 1e-3, 1.0, 10.0, 1e4])[:, None]).to(dtype)
+        up = torch.randn(5, width, generator=g).to(dtype)
+        kg = k.to(GPU).requires_grad_()
+        (grad,) = torch.autograd.grad((fused(kg).float() * up.to(GPU).float()).sum(), (kg,))
+        kr = k.double().requires_grad_()
+        (want,) = torch.autograd.grad((normalize_keys(kr) * up.double()).sum(), (kr,))
+        assert grad.dtype == dtype
+        for row in range(5):  # each row on its own scale
+            scale = want[row].abs().max().item()
+            torch.testing.assert_close(grad[row].cpu().double() / scale, want[row] / scale, rtol=tol, atol=tol)
+
+
+def test_normalize_keys_empty_and_refusals():
+    # tests/test_recurrence_review.py:81-87: empty arrays keep their shape, with a gradient
+    from vesper.contracts import ContractError
+    from vesper.kernels.keys import normalize_keys as fused
+
+    for shape in ((0, 3), (2, 0)):
+        key = torch.empty(shape, device=GPU, requires_grad=True)
+        out = fused(key)
+        assert out.shape == key.shape
+        (grad,) = torch.autograd.grad(out.sum(), (key,))
+        assert grad.shape == key.shape
+    with pytest.raises(ContractError, match="CUDA only"):
+        fused(torch.ones(2, 3))
+    with pytest.raises(ContractError, match="dtype"):
+        fused(torch.ones(2, 3, dtype=torch.float64, device=GPU))

@@ -17,12 +17,13 @@ import torch
 HERE = Path(__file__).resolve().parent
 LIBRARY_PATH = HERE / "libvesper_kernels.so"
 HEADER_PATH = HERE.parents[2] / "include" / "vesper_kernels.h"
-ABI_VERSION = 10
+ABI_VERSION = 11
 
 P = ctypes.c_void_p
 I = ctypes.c_int
 Z = ctypes.c_size_t
 F = ctypes.c_float
+L = ctypes.c_int64
 
 # every entry point of include/vesper_kernels.h: (return type, argument types)
 SIGNATURES: dict[str, tuple[object, list[object]]] = {
@@ -79,6 +80,12 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "vsp_key_filter_backward_bf16": (I, [P, P, P, P, P, P, P, P, Z, I, I, I, I, I, P]),
     "vsp_key_filter_backward_f16": (I, [P, P, P, P, P, P, P, P, Z, I, I, I, I, I, P]),
     "vsp_key_filter_backward_f32": (I, [P, P, P, P, P, P, P, P, Z, I, I, I, I, I, P]),
+    "vsp_normalize_keys_bf16": (I, [P, P, L, I, P]),
+    "vsp_normalize_keys_f16": (I, [P, P, L, I, P]),
+    "vsp_normalize_keys_f32": (I, [P, P, L, I, P]),
+    "vsp_normalize_keys_backward_bf16": (I, [P, P, P, L, I, P]),
+    "vsp_normalize_keys_backward_f16": (I, [P, P, P, L, I, P]),
+    "vsp_normalize_keys_backward_f32": (I, [P, P, P, L, I, P]),
 }
 
 

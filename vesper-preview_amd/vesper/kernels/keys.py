@@ -16,6 +16,10 @@ filter, ``vesper/column.py:779-782``) the kernel reads token ``t``'s input row f
 where ``active[:, t]`` is false, inside its loads, in place of a ``where`` merge before the call.
 ``key_step`` returns the next key history too, written by the same kernel launch
 (``vsp_key_step_*``): the whole of ``RecurrentSublayer.keys`` (``vesper/column.py:255-289``).
+
+``normalize_keys(k)`` is the reference's ``vesper/recurrence.py:91-115`` alone on rows of any width
+(``vsp_normalize_keys_*``, one wave a row, with its gradient), for rows the filter's head widths
+do not cover: wider than 512, or not a power of two.
 """
 
 from __future__ import annotations
@@ -179,4 +183,52 @@ def fused_keys(z: Tensor, history: Tensor, taps: Tensor, heads: int, *, active: 
         assert active is not None
         z = torch.where(active[..., None], z, carried_z)  # under autograd: the merge, explicit
     out: Tensor = _FusedKeys.apply(z, history, taps, heads)
+    return out
+
+
+class _NormalizeKeys(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx: Any, k: Tensor) -> Tensor:  # noqa: D102
+        x = _aligned(k.detach())
+        y = torch.empty_like(x)
+        width = x.shape[-1]
+        with torch.cuda.device(x.device):
+            _lib.call(f"vsp_normalize_keys_{_SUFFIX[x.dtype]}", x.data_ptr(), y.data_ptr(), x.numel() // width,
+                      width, _lib.stream_of(x.device))
+        ctx.save_for_backward(x)
+        return y
+
+    @staticmethod
+    def backward(ctx: Any, grad: Tensor) -> Tensor:  # noqa: D102
+        (x,) = ctx.saved_tensors
+        g = _aligned(grad.to(x.dtype))
+        gx = torch.empty_like(x)
+        width = x.shape[-1]
+        with torch.cuda.device(x.device):
+            _lib.call(f"vsp_normalize_keys_backward_{_SUFFIX[x.dtype]}", x.data_ptr(), g.data_ptr(), gx.data_ptr(),
+                      x.numel() // width, width, _lib.stream_of(x.device))
+        return gx
+
+
+def normalize_keys(k: Tensor) -> Tensor:
+    """``k / max(||k||_2, 1e-6)`` per row of ``k [..., dk]`` on the GPU, at any width
+    (``vesper/recurrence.py:91-115``): the row divided by its peak magnitude (floored at 1e-6, held
+    constant under autograd), then by the scaled row's norm floored at one, in float32, returned in
+    ``k``'s dtype (float32, bfloat16 or float16). An empty ``k`` comes back as it is.
+
+    Raises:
+        ContractError: on a tensor off the GPU, a dtype outside float32/bfloat16/float16, or a
+            zero-dimensional tensor.
+    """
+    if k.dim() == 0:
+        raise ContractError("normalize_keys needs at least one dimension (the key features)")
+    if k.dtype not in FUSED_KEY_DTYPES:
+        raise ContractError(f"k: dtype must be float32, bfloat16 or float16, got {k.dtype}")
+    if k.device.type != "cuda":
+        raise ContractError(f"the key normalization kernel runs on CUDA only, got k on {k.device}")
+    if k.shape[-1] >= 2**31:
+        raise ContractError(f"rows of {k.shape[-1]} features exceed the kernel's int32 width")
+    if k.numel() == 0:
+        return k
+    out: Tensor = _NormalizeKeys.apply(k)
     return out
