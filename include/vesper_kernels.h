@@ -22,7 +22,7 @@
 extern "C" {
 #endif
 
-#define VSP_ABI_VERSION 11
+#define VSP_ABI_VERSION 12
 
 /* Status codes. */
 #define VSP_OK 0
@@ -58,6 +58,16 @@ void vsp_clear_faults(void);
  * fault path: a limit of 0 makes a wait whose flag is not yet set give up at once, while every
  * kernel still runs to its end. */
 int vsp_set_wait_limit(int polls);
+
+/* Which form of the bf16 scan runs at head width 64 (with or without carried inputs): 0 the
+ * value-slice chains, one workgroup per 16 value columns of a head over the whole sequence; 1 the
+ * segmented scan, whose workgroups each carry one head's whole state through one segment of the
+ * sequence, the segments joined by their affine maps H -> X + M H; 2 (the default, and any other
+ * value) by shape: the chains while B * H * 4 workgroups fit one a CU (256), the segments beyond.
+ * Both compute the same scan to the bf16 tolerance; returns the previous setting. Taken at each
+ * call. No counterpart in the reference (its library has one kernel); for tests and measurements
+ * of both forms. */
+int vsp_set_scan_segments(int form);
 
 /* ---- delta-rule scan ------------------------------------------------------------------------
  * Per batch row b and head h, with the state H [D, D] read as H^T q, each token applies

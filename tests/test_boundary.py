@@ -45,8 +45,17 @@ def test_the_workspace_size_covers_every_chunk():
     from vesper.kernels import _lib
 
     lib = _lib.library()
-    # ten 16x16 lower tiles of the UT factor per 64-token chunk
-    assert lib.vsp_delta_scan_workspace_bytes(8, 4096, 8, 64, 0) == 8 * 8 * 64 * 2560 * 2
+    # ten 16x16 lower tiles of the UT factor per 64-token chunk; the bf16 scan at width 64 adds, per
+    # head, the affine maps (X and M, fp32 [64, 64] each) of every segment but the last and a copy of
+    # S0: at B8 H8 four segments of sixteen chunks, at B1 H2 T4096 sixteen of four, at B2 H1 T520 two
+    # of five, and none where a head has fewer than eight chunks or B H reaches 256
+    seg = lambda heads, maps: heads * (maps * 2 + 1) * 64 * 64 * 4  # noqa: E731
+    assert lib.vsp_delta_scan_workspace_bytes(8, 4096, 8, 64, 0) == 8 * 8 * 64 * 2560 * 2 + seg(64, 3)
+    assert lib.vsp_delta_scan_workspace_bytes(1, 4096, 2, 64, 0) == 2 * 64 * 2560 * 2 + seg(2, 15)
+    assert lib.vsp_delta_scan_workspace_bytes(2, 520, 1, 64, 0) == 2 * 9 * 2560 * 2 + seg(2, 1)
+    assert lib.vsp_delta_scan_workspace_bytes(1, 300, 1, 64, 0) == 5 * 2560 * 2
+    assert lib.vsp_delta_scan_workspace_bytes(32, 4096, 8, 64, 0) == 32 * 8 * 64 * 2560 * 2
+    assert lib.vsp_delta_scan_workspace_bytes(8, 4096, 8, 32, 0) == 8 * 8 * 64 * 2560 * 2
     assert lib.vsp_delta_scan_workspace_bytes(2, 130, 3, 16, 1) == 2 * 3 * 3 * 2560 * 4
     assert lib.vsp_delta_scan_workspace_bytes(2, 130, 3, 128, 1) == 0  # fp32 at 128 runs token by token
     assert lib.vsp_delta_scan_workspace_bytes(2, 130, 3, 48, 1) == 0  # token-serial width

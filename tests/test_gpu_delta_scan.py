@@ -185,6 +185,112 @@ def test_active_mask_zeroes_outputs_and_keeps_every_write():
         assert relative_error(o, o_ref) < tol and relative_error(s, s_ref) < tol
 
 
+# ---- the bf16 scan at head width 64 in both its forms: segmented (segments of whole-head state
+# joined by their affine maps H -> X + M H) and as value-slice chains over the whole sequence ------
+
+# (b, n, h): 16, 4, 2 and 1 segments a head (at least four chunks a segment, B H segments near 256),
+# every one with a partial last chunk
+SEGMENTED = [(1, 4096 - 37, 2), (3, 1000, 3), (2, 520, 1), (1, 300, 1)]
+
+
+def _scan_form(segments: int, fn, *args, **kwargs):
+    from vesper.kernels import _lib
+
+    previous = _lib.set_scan_segments(segments)
+    try:
+        out = fn(*args, **kwargs)
+        torch.cuda.synchronize()
+    finally:
+        _lib.set_scan_segments(previous)
+    return out
+
+
+@pytest.mark.parametrize("segments", [True, False])
+@pytest.mark.parametrize(("b", "n", "h"), SEGMENTED)
+def test_both_forms_of_the_bf16_scan_match_the_oracle(segments, b, n, h):
+    from vesper.kernels.delta_scan import delta_scan_fused
+
+    q, k, v, beta, h0 = _bf16_inputs(b, n, h, 64, seed=n)
+    o_ref, s_ref = _oracle(q, k, v, beta, h0)
+    o, s = _scan_form(segments, delta_scan_fused, q, k, v, beta, h0)
+    assert relative_error(o, o_ref) < TOL and relative_error(s, s_ref) < TOL
+
+
+@pytest.mark.parametrize(("b", "n", "h"), [(16, 700, 8), (8, 200, 8)])
+def test_the_form_picked_by_shape_matches_the_oracle(b, n, h):
+    # B H = 128 takes the segments (two of six chunks at n = 700), B H = 64 the value-slice chains
+    from vesper.kernels.delta_scan import delta_scan_fused
+
+    q, k, v, beta, h0 = _bf16_inputs(b, n, h, 64, seed=b)
+    o_ref, s_ref = _oracle(q, k, v, beta, h0)
+    o, s = _scan_form(2, delta_scan_fused, q, k, v, beta, h0)
+    assert relative_error(o, o_ref) < TOL and relative_error(s, s_ref) < TOL
+
+
+@pytest.mark.parametrize(("b", "n", "h"), SEGMENTED[:2])
+def test_the_segmented_scan_with_an_active_mask(b, n, h):
+    from vesper.kernels.delta_scan import delta_scan_fused
+
+    q, k, v, beta, h0 = _bf16_inputs(b, n, h, 64, seed=n + 1)
+    act = torch.rand(b, n, generator=torch.Generator().manual_seed(n)) < 0.6
+    o_ref, s_ref = _oracle(q, k, v, beta, h0, act)
+    o, s = _scan_form(True, delta_scan_fused, q, k, v, beta, h0, active=act.to(GPU))
+    o_all, s_all = _scan_form(True, delta_scan_fused, q, k, v, beta, h0)
+    assert torch.equal(s, s_all) and torch.equal(o[act.to(GPU)], o_all[act.to(GPU)])
+    assert bool((o[~act.to(GPU)] == 0).all())
+    assert relative_error(o, o_ref) < TOL and relative_error(s, s_ref) < TOL
+
+
+def test_the_segmented_scan_writes_the_final_state_over_the_initial_one():
+    """state_out may alias state_in (include/vesper_kernels.h): with sixteen segments the last one
+    writes the final state while the first starts from a copy of S0, so the result is the one with
+    separate buffers, bit for bit."""
+    from vesper.kernels import _lib
+
+    previous = _lib.set_scan_segments(1)
+    try:
+        _in_place_case()
+    finally:
+        _lib.set_scan_segments(previous)
+
+
+def _in_place_case():
+    from vesper.kernels import _lib
+
+    b, n, h, dk = 1, 4096, 2, 64
+    q, k, v, beta, h0 = _bf16_inputs(b, n, h, dk, seed=3)
+    lib = _lib.library()
+    wbytes = int(lib.vsp_delta_scan_workspace_bytes(b, n, h, dk, 0))
+    ws = torch.empty(wbytes, dtype=torch.uint8, device=GPU)
+    o1, s1 = torch.empty_like(q), torch.empty_like(h0)
+    _lib.call("vsp_delta_scan_bf16", *(_lib.ptr(t) for t in (q, k, v, beta, h0, o1, s1, ws)), wbytes, None, b, n, h,
+              dk, _lib.stream_of(GPU))
+    s2 = h0.clone()
+    o2 = torch.empty_like(q)
+    _lib.call("vsp_delta_scan_bf16", *(_lib.ptr(t) for t in (q, k, v, beta, s2, o2, s2, ws)), wbytes, None, b, n, h,
+              dk, _lib.stream_of(GPU))
+    torch.cuda.synchronize()
+    assert torch.equal(o1, o2) and torch.equal(s1, s2)
+    o_ref, s_ref = _oracle(q, k, v, beta, h0)
+    assert relative_error(o1, o_ref) < TOL and relative_error(s1, s_ref) < TOL
+
+
+def test_the_segmented_records_hold_each_chunks_starting_state():
+    """Records over ten chunks in two segments of five: the second segment's states come from the
+    first one's map."""
+    b, n, h, dk = 1, 600, 2, 64
+    q, k, v, beta, h0 = _bf16_inputs(b, n, h, dk, seed=11)
+    o, s, rec = _scan_form(True, _record_forward, q, k, v, beta, h0)
+    nc = (n + 63) // 64
+    states = _unpack_records(rec, b, h, nc, dk)
+    assert torch.equal(states[:, :, 0], h0.cpu().to(BF16).float())
+    for c in range(1, nc):
+        _, want = _oracle(q[:, : 64 * c], k[:, : 64 * c], v[:, : 64 * c], beta[:, : 64 * c], h0)
+        assert relative_error(states[:, :, c], want) < 1e-2, c
+    o_ref, s_ref = _oracle(q, k, v, beta, h0)
+    assert relative_error(o, o_ref) < TOL and relative_error(s, s_ref) < TOL
+
+
 @pytest.mark.parametrize("dtype", [torch.float32, BF16])
 @pytest.mark.parametrize("dk", [16, 32, 48, 64, 100, 128, 256])
 def test_the_decode_step_matches_the_oracle_step(dtype, dk):

@@ -17,7 +17,7 @@ import torch
 HERE = Path(__file__).resolve().parent
 LIBRARY_PATH = HERE / "libvesper_kernels.so"
 HEADER_PATH = HERE.parents[2] / "include" / "vesper_kernels.h"
-ABI_VERSION = 11
+ABI_VERSION = 12
 
 P = ctypes.c_void_p
 I = ctypes.c_int
@@ -33,6 +33,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "vsp_fault_bits": (ctypes.c_uint, []),
     "vsp_clear_faults": (None, []),
     "vsp_set_wait_limit": (I, [I]),
+    "vsp_set_scan_segments": (I, [I]),
     "vsp_delta_scan_workspace_bytes": (Z, [I, I, I, I, I]),
     "vsp_delta_scan_bf16": (I, [P, P, P, P, P, P, P, P, Z, P, I, I, I, I, P]),
     "vsp_delta_scan_f32": (I, [P, P, P, P, P, P, P, P, Z, P, I, I, I, I, P]),
@@ -143,6 +144,13 @@ def clear_faults() -> None:
 def set_wait_limit(polls: int) -> int:
     """Polls a bounded wait makes before giving up (negative: the default); returns the previous."""
     return int(library().vsp_set_wait_limit(polls))
+
+
+def set_scan_segments(form: int) -> int:
+    """The form of the bf16 scan at head width 64: 0 (or False) value-slice chains over the whole
+    sequence, 1 (or True) segments joined by their affine maps, 2 by shape (the default); returns
+    the previous setting."""
+    return int(library().vsp_set_scan_segments(int(form)))
 
 
 def available() -> bool:

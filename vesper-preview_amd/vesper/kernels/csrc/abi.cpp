@@ -18,6 +18,7 @@ bool g_initialised = false;
 unsigned* g_fault_host = nullptr;    // the fault record: kFaultWords words of pinned host memory
 unsigned* g_fault_device = nullptr;  // its address for kernels
 std::atomic<int> g_wait_limit{1 << 19};
+std::atomic<int> g_scan_segments{2};
 }  // namespace
 
 namespace vsp {
@@ -39,6 +40,7 @@ int check_launch(const char* what) {
 
 unsigned* fault_record() { return g_fault_device; }
 int wait_limit() { return g_wait_limit.load(std::memory_order_relaxed); }
+int scan_segments() { return g_scan_segments.load(std::memory_order_relaxed); }
 
 }  // namespace vsp
 
@@ -83,6 +85,10 @@ extern "C" void vsp_clear_faults(void) {
 
 extern "C" int vsp_set_wait_limit(int polls) {
   return g_wait_limit.exchange(polls < 0 ? (1 << 19) : polls, std::memory_order_relaxed);
+}
+
+extern "C" int vsp_set_scan_segments(int form) {
+  return g_scan_segments.exchange(form == 0 || form == 1 ? form : 2, std::memory_order_relaxed);
 }
 
 extern "C" int vsp_abi_version(void) { return VSP_ABI_VERSION; }

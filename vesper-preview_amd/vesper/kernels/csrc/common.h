@@ -38,6 +38,11 @@ enum Status { OK = 0, ERR_ARG = 1, ERR_UNSUPPORTED = 2, ERR_LAUNCH = 3 };
 enum FaultFamily { FAULT_SCAN_CHAIN = 0, kFaultWords = 16 };
 unsigned* fault_record();  // device address of the fault words; null before vsp_init
 int wait_limit();          // polls before a bounded wait gives up
+// The form of the bf16 scan at head width 64: 0 value-slice chains over the whole sequence
+// (delta_chain_bf16_kernel), 1 segments of whole-head state joined by their affine maps
+// (delta_seg_kernel), 2 (the default) by shape. Both compute the same scan; vsp_set_scan_segments
+// sets it.
+int scan_segments();
 
 // The allocation-free ring attention entry's static scratch (decode.hip): rows of one call at most,
 // and its per-device set-up, run by vsp_init.

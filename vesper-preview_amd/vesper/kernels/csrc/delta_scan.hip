@@ -1310,6 +1310,8 @@ __global__ __launch_bounds__(512) void delta_chain_bf16_kernel(const TIn* __rest
   }
 }
 
+#include "scan_segments.h"
+
 // --------------------------------------------------------------------------------------------
 // host side
 // --------------------------------------------------------------------------------------------
@@ -1350,7 +1352,31 @@ size_t workspace_bytes(int B, int T, int H, int D, bool fp32) {
   if (B <= 0 || H <= 0 || T < kSerialBelow || !chunked_width(D, fp32)) return 0;
   if ((size_t)T * H * D >= ((size_t)1 << 31)) return 0;  // 32-bit row offsets in the chain kernel
   const size_t nc = (size_t)(T + kChunk - 1) / kChunk;
-  return (size_t)B * H * nc * kChunkT * (fp32 ? sizeof(float) : sizeof(uint16_t));
+  size_t bytes = (size_t)B * H * nc * kChunkT * (fp32 ? sizeof(float) : sizeof(uint16_t));
+  if (!fp32 && D == 64) {  // the segmented scan's maps and the copies of S0 follow the UT factors
+    const SegShape sh = seg_shape(B, H, T);
+    if (sh.nseg > 1) bytes += (size_t)B * H * ((sh.nseg - 1) * kSegMapBytes + 64 * 64 * sizeof(float));
+  }
+  return bytes;
+}
+
+// The segmented scan (bf16, head width 64): the map pass over every segment but the last, then the
+// output pass over all of them. tmat is the workspace's start; the maps follow the UT factors.
+template <bool CARRY>
+void launch_segments(const __bf16* q, const __bf16* k, const __bf16* v, const float* s_in, float* s_out, __bf16* o,
+                     __bf16* tmat, const uint8_t* active, Carried<__bf16> carried, int B, int T, int H,
+                     hipStream_t stream, __bf16* hrec) {
+  const SegShape sh = seg_shape(B, H, T);
+  const size_t nc = (size_t)(T + kChunk - 1) / kChunk;
+  float* maps = reinterpret_cast<float*>(tmat + (size_t)B * H * nc * kChunkT);
+  float* s0copy = maps + (size_t)B * H * (sh.nseg - 1) * (kSegMapBytes / sizeof(float));
+  if (sh.nseg > 1)
+    hipLaunchKernelGGL((delta_seg_kernel<kSegMaps, CARRY>), dim3((unsigned)(B * H * (sh.nseg - 1))), dim3(512), 0,
+                       stream, q, k, v, tmat, s_in, s_out, o, active, maps, s0copy, T, H, sh.nseg, sh.seglen,
+                       (__bf16*)nullptr, fault_record(), wait_limit(), carried.k, carried.v);
+  hipLaunchKernelGGL((delta_seg_kernel<kSegOutputs, CARRY>), dim3((unsigned)(B * H * sh.nseg)), dim3(512), 0, stream,
+                     q, k, v, tmat, s_in, s_out, o, active, maps, s0copy, T, H, sh.nseg, sh.seglen, hrec,
+                     fault_record(), wait_limit(), carried.k, carried.v);
 }
 
 template <typename TIn, typename E, int DK, bool CARRY>
@@ -1362,6 +1388,15 @@ void launch_chunked(const TIn* q, const TIn* k, const TIn* v, const TIn* beta, c
   hipLaunchKernelGGL((delta_prep_kernel<TIn, E, DK, CARRY>), dim3((unsigned)((total + 3) / 4)), dim3(256), 0, stream, k,
                      beta, tmat, active, carried.k, carried.v, carried.beta, T, H, total, strength.m, strength.alpha,
                      strength.logits);
+  if constexpr (std::is_same<TIn, __bf16>::value && DK == 64) {
+    // by shape: the value-slice chains while they fit one workgroup a CU (B H D/16 <= kSegBlocks),
+    // where their four CUs a head outrun one whole-head workgroup a segment; the segments beyond
+    const int form = scan_segments();
+    if (form == 1 || (form == 2 && B * H * (DK / 16) > kSegBlocks)) {
+      launch_segments<CARRY>(q, k, v, s_in, s_out, o, tmat, active, carried, B, T, H, stream, hrec);
+      return;
+    }
+  }
   if constexpr (sizeof(E) == 2 && DK >= 32 && DK <= 64) {  // (at 128 the staging registers would spill)
     hipLaunchKernelGGL((delta_chain_bf16_kernel<TIn, DK, CARRY>), dim3((unsigned)(B * H * (DK / 16))), dim3(512), 0,
                        stream, q, k, v, tmat, s_in, s_out, o, active, carried.k, carried.v, carried.beta, T, H,
