@@ -22,7 +22,7 @@
 extern "C" {
 #endif
 
-#define VSP_ABI_VERSION 12
+#define VSP_ABI_VERSION 13
 
 /* Status codes. */
 #define VSP_OK 0
@@ -213,6 +213,17 @@ int vsp_window_attn_carried_bf16(const void* q, const void* keys, const void* va
 int vsp_window_attn_carried_f16(const void* q, const void* keys, const void* values, const void* keys_carried,
                                 const void* values_carried, void* o, const uint8_t* active, int B, int N, int M,
                                 int H, int HKV, int D, int window, float scale, void* stream);
+/* vsp_window_attn_* over a cache and a chunk held apart: key rows below M come from cache_keys /
+ * cache_values [B, M, HKV, D] and key row M + t from keys / values [B, N, HKV, D] (the chunk's own),
+ * so the kernel branch of WindowedAttention.attend (vesper/attention.py:373-383, which concatenates
+ * the cache's and the chunk's keys before the fla-core call) needs no copy of either. Outputs equal
+ * vsp_window_attn_* over the concatenated keys bit for bit. With M = 0 the cache pointers may be NULL. */
+int vsp_window_attn_cached_bf16(const void* q, const void* cache_keys, const void* cache_values, const void* keys,
+                                const void* values, void* o, const uint8_t* active, int B, int N, int M, int H,
+                                int HKV, int D, int window, float scale, void* stream);
+int vsp_window_attn_cached_f16(const void* q, const void* cache_keys, const void* cache_values, const void* keys,
+                               const void* values, void* o, const uint8_t* active, int B, int N, int M, int H,
+                               int HKV, int D, int window, float scale, void* stream);
 /* The gradients (the backward of fla-core's `parallel_attn`, which autograd runs for
  * vesper/kernels/window_attn.py:27-39 under WindowedAttention.attend, vesper/attention.py:373-383):
  * from dO [B, N, H, D] and the forward's o and lse, dq [B, N, H, D], dk and dv [B, M + N, HKV, D]

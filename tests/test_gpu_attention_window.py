@@ -148,6 +148,28 @@ def test_a_second_4096_token_chunk_with_a_full_window_cache_at_b4_h8_d64_w512():
     assert torch.equal(cache.pos.cpu(), pos[:, -w:])
 
 
+@pytest.mark.parametrize("dtype", [BF16, torch.float16])
+@pytest.mark.parametrize("dk", [16, 32, 64, 128, 256])
+@pytest.mark.parametrize(("m", "n", "w"), [(1, 70, 64), (37, 130, 64), (64, 200, 64), (100, 64, 128), (300, 700, 512),
+                                            (512, 300, 512), (511, 1, 512)])
+def test_the_cache_and_the_chunk_as_two_sources_equal_their_concatenation_bitwise(dtype, dk, m, n, w):
+    """vsp_window_attn_cached_*: key rows below m from the cache, the rest from the chunk, with the
+    tile across row m (m not a multiple of 64, or straddling the window) read row by row; outputs
+    equal the one-tensor kernel over the concatenated keys bit for bit, GQA included."""
+    from vesper.kernels.window_attn import window_attention, window_attention_cached
+
+    b, h, hkv = 2, 4, 2
+    g = torch.Generator().manual_seed(m + n + dk)
+    q = torch.randn(b, n, h, dk, generator=g).to(dtype).to(GPU)
+    ck, cv = (torch.randn(b, m, hkv, dk, generator=g).to(dtype).to(GPU) for _ in range(2))
+    k, v = (torch.randn(b, n, hkv, dk, generator=g).to(dtype).to(GPU) for _ in range(2))
+    with torch.no_grad():
+        got = window_attention_cached(q, ck, cv, k, v, w)
+        want = window_attention(q, torch.cat([ck, k], 1), torch.cat([cv, v], 1), w)
+    torch.cuda.synchronize()
+    assert torch.equal(got, want)
+
+
 def test_attend_refuses_positions_that_are_not_consecutive():
     from vesper.attention import attend, kv_cache_empty
     from vesper.contracts import ContractError

@@ -25,7 +25,7 @@ from torch import Tensor
 
 from vesper.contracts import ContractError, Dims, check_shape, require
 from vesper.kernels import _lib
-from vesper.kernels.window_attn import window_attention
+from vesper.kernels.window_attn import window_attention_cached
 
 _SUFFIX = {torch.bfloat16: "bf16", torch.float16: "f16", torch.float32: "f32"}
 
@@ -204,7 +204,8 @@ def attend(q: Tensor, k: Tensor, v: Tensor, pos: Tensor, cache: KVCache) -> tupl
     rotated ``k``, ``v [b, n, hkv, dk]`` at consecutive positions ``pos [b, n]``; returns the
     attention output ``[b, n, h, dk]`` (before the output projection) and the pushed cache. The
     kernel branch of ``WindowedAttention.attend`` (``attention.py:373-383``): the cache's ``m``
-    rows then the chunk's as the keys of ``window_attention``, which places query ``i`` at key
+    rows then the chunk's as the keys of ``window_attention`` (read from the two tensors in place,
+    ``window_attention_cached``, not concatenated first), which places query ``i`` at key
     index ``m + i``. A chunk of zero tokens returns an empty output and the cache unchanged.
 
     Raises:
@@ -224,9 +225,9 @@ def attend(q: Tensor, k: Tensor, v: Tensor, pos: Tensor, cache: KVCache) -> tupl
     kpos = torch.cat([cache.pos, pos], dim=1)
     if kpos.shape[1] > 1:
         require((kpos[:, 1:] - kpos[:, :-1] == 1).all().reshape(1), "attend: cache and chunk positions must be consecutive")
-    keys = torch.cat([cache.k.to(q.dtype), k.to(q.dtype)], dim=1)
-    vals = torch.cat([cache.v.to(q.dtype), v.to(q.dtype)], dim=1)
-    o = window_attention(q, keys, vals, cache.window)
+    # the cache's rows and the chunk's as two sources of one kernel call (no concatenated copy)
+    o = window_attention_cached(q, cache.k.to(q.dtype), cache.v.to(q.dtype), k.to(q.dtype), v.to(q.dtype),
+                                cache.window)
     return o, kv_cache_push(cache, k, v, pos)
 
 

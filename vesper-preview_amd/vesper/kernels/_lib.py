@@ -17,7 +17,7 @@ import torch
 HERE = Path(__file__).resolve().parent
 LIBRARY_PATH = HERE / "libvesper_kernels.so"
 HEADER_PATH = HERE.parents[2] / "include" / "vesper_kernels.h"
-ABI_VERSION = 12
+ABI_VERSION = 13
 
 P = ctypes.c_void_p
 I = ctypes.c_int
@@ -57,6 +57,8 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "vsp_window_attn_lse_f16": (I, [P, P, P, P, P, P, I, I, I, I, I, I, I, F, P]),
     "vsp_window_attn_carried_bf16": (I, [P, P, P, P, P, P, P, I, I, I, I, I, I, I, F, P]),
     "vsp_window_attn_carried_f16": (I, [P, P, P, P, P, P, P, I, I, I, I, I, I, I, F, P]),
+    "vsp_window_attn_cached_bf16": (I, [P, P, P, P, P, P, P, I, I, I, I, I, I, I, F, P]),
+    "vsp_window_attn_cached_f16": (I, [P, P, P, P, P, P, P, I, I, I, I, I, I, I, F, P]),
     "vsp_window_attn_backward_bf16": (I, [P, P, P, P, P, P, P, P, P, P, I, I, I, I, I, I, I, F, P]),
     "vsp_window_attn_backward_f16": (I, [P, P, P, P, P, P, P, P, P, P, I, I, I, I, I, I, I, F, P]),
     "vsp_ring_attn_workspace_bytes": (Z, [I]),

@@ -29,11 +29,20 @@ namespace {
 
 constexpr float kLazy = 8.f;
 
-// CARRY (copy-forward): key rows M + t of an inactive token t come from keys_c / values_c row t
-// ([B, N, HKV, D], the carried keys and values) instead of keys / values. Its per-lane 64-bit
-// source addresses need more registers: three workgroups per CU at D 64 instead of four.
-template <typename T, int D, bool CARRY>
-__global__ __launch_bounds__(256, D >= 256 ? 1 : (D >= 128 ? 2 : (CARRY && D == 64 ? 3 : 4))) void window_attn_kernel(const T* __restrict__ q, const T* __restrict__ keys,
+// Where the key rows come from (SRC):
+//  * kSrcPlain: keys / values [B, M + N, HKV, D], the cache's M rows first;
+//  * kSrcCarried (copy-forward): as plain, but key rows M + t of an inactive token t come from
+//    keys_c / values_c row t ([B, N, HKV, D], the carried keys and values);
+//  * kSrcCached: rows below M from keys / values as the cache alone ([B, M, HKV, D]) and rows M + t
+//    from keys_c / values_c row t (the chunk's own keys and values, [B, N, HKV, D]), so a chunk
+//    attends over a cache without the two being copied into one tensor first. Whole tiles on either
+//    side go through a buffer resource over their tensor; the one tile across row M picks each
+//    row's source by a per-lane address.
+// The per-lane 64-bit source addresses need more registers: three workgroups per CU at D 64
+// instead of four.
+constexpr int kSrcPlain = 0, kSrcCarried = 1, kSrcCached = 2;
+template <typename T, int D, int SRC>
+__global__ __launch_bounds__(256, D >= 256 ? 1 : (D >= 128 ? 2 : (SRC != kSrcPlain && D == 64 ? 3 : 4))) void window_attn_kernel(const T* __restrict__ q, const T* __restrict__ keys,
                                                              const T* __restrict__ values, T* __restrict__ o,
                                                              float* __restrict__ lse,
                                                              const uint8_t* __restrict__ active, const T* keys_c,
@@ -41,6 +50,7 @@ __global__ __launch_bounds__(256, D >= 256 ? 1 : (D >= 128 ? 2 : (CARRY && D == 
                                                              int HKV, int W, float scale_log2, int nqt) {
   using V8 = typename Mma<T>::V8;
   using V4 = typename Mma<T>::V4;
+  constexpr bool CARRY = SRC == kSrcCarried, CACHED = SRC == kSrcCached;
   constexpr int QT = 128;              // queries per workgroup
   constexpr int QB = 2;                // 16-query blocks per wave
   constexpr int KT = 64;               // keys per tile
@@ -122,11 +132,15 @@ __global__ __launch_bounds__(256, D >= 256 ? 1 : (D >= 128 ? 2 : (CARRY && D == 
   const int klast = min(S, M + qbase + QT);
   const int ntiles = (klast - kfirst + KT - 1) / KT;
   const size_t kv_row = (size_t)HKV * D;
-  const T* kbase = keys + ((size_t)b * S * HKV + kvh) * D;
-  const T* vbase = values + ((size_t)b * S * HKV + kvh) * D;
-  // carried rows, indexed by key index (valid from M on)
-  const T* kcbase = CARRY ? keys_c + ((size_t)b * N * HKV + kvh) * D - (size_t)M * kv_row : kbase;
-  const T* vcbase = CARRY ? values_c + ((size_t)b * N * HKV + kvh) * D - (size_t)M * kv_row : vbase;
+  const T* kbase = keys + ((size_t)b * (CACHED ? M : S) * HKV + kvh) * D;
+  const T* vbase = values + ((size_t)b * (CACHED ? M : S) * HKV + kvh) * D;
+  // carried (or the chunk's own) rows, indexed by key index (valid from M on)
+  const T* kcbase = CARRY || CACHED ? keys_c + ((size_t)b * N * HKV + kvh) * D - (size_t)M * kv_row : kbase;
+  const T* vcbase = CARRY || CACHED ? values_c + ((size_t)b * N * HKV + kvh) * D - (size_t)M * kv_row : vbase;
+  // cached: bit r of a tile's mask says key k0 + r is a cache row
+  auto cache_rows = [&](int k0) -> uint64_t {
+    return k0 >= M ? 0ull : (M - k0 >= 64 ? ~0ull : ((1ull << (M - k0)) - 1ull));
+  };
   // With carried rows, each tile's 64 source flags (bit r: key k0 + r reads the fresh row) are
   // loaded one tile ahead (lane l: key k0 + l) and turned into a wave-uniform mask when issued.
   auto flag_of = [&](int k0) -> uint8_t {
@@ -140,8 +154,14 @@ __global__ __launch_bounds__(256, D >= 256 ? 1 : (D >= 128 ? 2 : (CARRY && D == 
   // and keys past klast that do load are masked in the scores (weight 0 in the output). Narrower
   // heads: keys past klast re-read key klast - 1.
   V8 kreg[kDirect ? 1 : NI], vreg[kDirect ? 1 : NI];
-  const unsigned kv_bytes = (unsigned)(((size_t)(S - 1) * kv_row + D) * sizeof(T));
+  const unsigned kv_bytes =
+      CACHED ? (M > 0 ? (unsigned)(((size_t)(M - 1) * kv_row + D) * sizeof(T)) : 0u)
+             : (unsigned)(((size_t)(S - 1) * kv_row + D) * sizeof(T));
   const __amdgpu_buffer_rsrc_t rk = buffer_rsrc(kbase, kv_bytes), rv = buffer_rsrc(vbase, kv_bytes);
+  // cached: the chunk's rows, from key index M on
+  const unsigned kvc_bytes = CACHED ? (unsigned)(((size_t)(N - 1) * kv_row + D) * sizeof(T)) : 0u;
+  const __amdgpu_buffer_rsrc_t rkc = buffer_rsrc(kcbase + (size_t)M * kv_row, kvc_bytes);
+  const __amdgpu_buffer_rsrc_t rvc = buffer_rsrc(vcbase + (size_t)M * kv_row, kvc_bytes);
   unsigned koff[kDirect ? NI : 1], voff[kDirect ? NI : 1];
 #pragma unroll
   for (int j = 0; j < (kDirect ? NI : 1); ++j) {
@@ -152,9 +172,22 @@ __global__ __launch_bounds__(256, D >= 256 ? 1 : (D >= 128 ? 2 : (CARRY && D == 
     voff[j] = (unsigned)(rowv * kv_row + 8 * (segv < SEG ? segv : 0)) * (unsigned)sizeof(T);
   }
   auto fetch = [&](int k0, T* Kn, T* Vn, uint64_t fresh) {
+    if constexpr (CACHED) fresh = cache_rows(k0);
+    // cached: a whole tile on one side of row M loads through that tensor's buffer resource
+    const bool whole = CACHED && (k0 >= M || k0 + KT <= M);
 #pragma unroll
     for (int j = 0; j < NI; ++j) {
-      if constexpr (kDirect && CARRY) {
+      if constexpr (kDirect && CACHED) {
+        if (whole) {
+          const int ins = w + 4 * j;
+          const bool chunk = k0 >= M;
+          const unsigned toff = (unsigned)((size_t)(chunk ? k0 - M : k0) * kv_row * sizeof(T));
+          if (ins < NINS) buffer_load_lds16(chunk ? rkc : rk, Kn + ins * 64 * 8, koff[j], toff);
+          if (ins < NINSV) buffer_load_lds16(chunk ? rvc : rv, Vn + ins * 64 * 8, voff[j], toff);
+          continue;
+        }
+      }
+      if constexpr (kDirect && (CARRY || CACHED)) {
         // per-lane sources (global direct loads: a buffer resource cannot differ between lanes);
         // rows past the last key re-read key S - 1, from that key's own source (masked in the
         // scores, they must still be finite: probability 0 times the row)
@@ -177,7 +210,7 @@ __global__ __launch_bounds__(256, D >= 256 ? 1 : (D >= 128 ? 2 : (CARRY && D == 
         const int row = sg / SEG, part = sg - row * SEG;
         const int key = min(k0 + row, klast - 1);  // the key loaded, with its own source flag
         const size_t goff = (size_t)key * kv_row + 8 * part;
-        const bool from_fresh = !CARRY || ((fresh >> ((key - k0) & 63)) & 1);  // (key - k0 < 64 where it loads)
+        const bool from_fresh = !(CARRY || CACHED) || ((fresh >> ((key - k0) & 63)) & 1);  // (key - k0 < 64 where it loads)
         if (sg < KT * SEG && 8 * part < D) {
           kreg[j] = *reinterpret_cast<const V8*>((from_fresh ? kbase : kcbase) + goff);
           vreg[j] = *reinterpret_cast<const V8*>((from_fresh ? vbase : vcbase) + goff);
@@ -387,35 +420,40 @@ __global__ __launch_bounds__(256, D >= 256 ? 1 : (D >= 128 ? 2 : (CARRY && D == 
 
 bool attn_width(int D) { return D == 16 || D == 32 || D == 64 || D == 128 || D == 256; }
 
-template <typename T, bool CARRY>
+template <typename T, int SRC>
 void launch_window(dim3 grid, hipStream_t stream, const T* q, const T* keys, const T* values, T* o, float* lse,
                    const uint8_t* active, const T* kc, const T* vc, int N, int M, int H, int HKV, int D, int W,
                    float scale_log2, int nqt) {
   switch (D) {
-    case 16: hipLaunchKernelGGL((window_attn_kernel<T, 16, CARRY>), grid, dim3(256), 0, stream, q, keys, values, o, lse, active, kc, vc, N, M, H, HKV, W, scale_log2, nqt); break;
-    case 32: hipLaunchKernelGGL((window_attn_kernel<T, 32, CARRY>), grid, dim3(256), 0, stream, q, keys, values, o, lse, active, kc, vc, N, M, H, HKV, W, scale_log2, nqt); break;
-    case 64: hipLaunchKernelGGL((window_attn_kernel<T, 64, CARRY>), grid, dim3(256), 0, stream, q, keys, values, o, lse, active, kc, vc, N, M, H, HKV, W, scale_log2, nqt); break;
-    case 128: hipLaunchKernelGGL((window_attn_kernel<T, 128, CARRY>), grid, dim3(256), 0, stream, q, keys, values, o, lse, active, kc, vc, N, M, H, HKV, W, scale_log2, nqt); break;
-    default: hipLaunchKernelGGL((window_attn_kernel<T, 256, CARRY>), grid, dim3(256), 0, stream, q, keys, values, o, lse, active, kc, vc, N, M, H, HKV, W, scale_log2, nqt); break;
+    case 16: hipLaunchKernelGGL((window_attn_kernel<T, 16, SRC>), grid, dim3(256), 0, stream, q, keys, values, o, lse, active, kc, vc, N, M, H, HKV, W, scale_log2, nqt); break;
+    case 32: hipLaunchKernelGGL((window_attn_kernel<T, 32, SRC>), grid, dim3(256), 0, stream, q, keys, values, o, lse, active, kc, vc, N, M, H, HKV, W, scale_log2, nqt); break;
+    case 64: hipLaunchKernelGGL((window_attn_kernel<T, 64, SRC>), grid, dim3(256), 0, stream, q, keys, values, o, lse, active, kc, vc, N, M, H, HKV, W, scale_log2, nqt); break;
+    case 128: hipLaunchKernelGGL((window_attn_kernel<T, 128, SRC>), grid, dim3(256), 0, stream, q, keys, values, o, lse, active, kc, vc, N, M, H, HKV, W, scale_log2, nqt); break;
+    default: hipLaunchKernelGGL((window_attn_kernel<T, 256, SRC>), grid, dim3(256), 0, stream, q, keys, values, o, lse, active, kc, vc, N, M, H, HKV, W, scale_log2, nqt); break;
   }
 }
 
 template <typename T>
 int window_attn(const T* q, const T* keys, const T* values, T* o, float* lse, const uint8_t* active, int B, int N, int M,
                 int H, int HKV, int D, int W, float scale, void* stream_ptr, const char* who, const T* kc = nullptr,
-                const T* vc = nullptr) {
+                const T* vc = nullptr, bool cached = false) {
   if (B < 0 || N < 0 || M < 0 || H < 1 || HKV < 1) return fail(ERR_ARG, "%s: bad sizes B=%d N=%d M=%d H=%d HKV=%d", who, B, N, M, H, HKV);
   if (H % HKV != 0) return fail(ERR_ARG, "%s: %d query heads are not a multiple of %d KV heads", who, H, HKV);
   if (W < 1) return fail(ERR_ARG, "%s: window must be at least 1, got %d", who, W);
   if (!(scale > 0.f)) return fail(ERR_ARG, "%s: the score scale must be positive, got %g", who, (double)scale);
   if (!attn_width(D)) return fail(ERR_UNSUPPORTED, "%s: head dimension %d (kernels: 16, 32, 64, 128, 256)", who, D);
   if (B == 0 || N == 0) return OK;
-  if (!q || !keys || !values || !o) return fail(ERR_ARG, "%s: null pointer", who);
+  // (a cached call with no cache rows may pass null for them)
+  if (!q || !o || ((!keys || !values) && !(cached && M == 0))) return fail(ERR_ARG, "%s: null pointer", who);
   if ((reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(keys) | reinterpret_cast<uintptr_t>(values) |
        reinterpret_cast<uintptr_t>(o)) & 15)
     return fail(ERR_ARG, "%s: q, keys, values and o must be 16-byte aligned", who);
   if (reinterpret_cast<uintptr_t>(lse) & 3) return fail(ERR_ARG, "%s: lse must be 4-byte aligned", who);
-  if (kc != nullptr || vc != nullptr) {
+  if (cached) {
+    if (!kc || !vc) return fail(ERR_ARG, "%s: null pointer", who);
+    if ((reinterpret_cast<uintptr_t>(kc) | reinterpret_cast<uintptr_t>(vc)) & 15)
+      return fail(ERR_ARG, "%s: the chunk's keys and values must be 16-byte aligned", who);
+  } else if (kc != nullptr || vc != nullptr) {
     if (!kc || !vc) return fail(ERR_ARG, "%s: the carried keys and values come together", who);
     if (!active) return fail(ERR_ARG, "%s: carried keys and values need the active flags", who);
     if ((reinterpret_cast<uintptr_t>(kc) | reinterpret_cast<uintptr_t>(vc)) & 15)
@@ -428,10 +466,15 @@ int window_attn(const T* q, const T* keys, const T* values, T* o, float* lse, co
   const int nqt = (N + 127) / 128;
   dim3 grid((unsigned)((size_t)nqt * H * B));
   hipStream_t stream = reinterpret_cast<hipStream_t>(stream_ptr);
-  if (kc != nullptr)
-    launch_window<T, true>(grid, stream, q, keys, values, o, lse, active, kc, vc, N, M, H, HKV, D, W, scale_log2, nqt);
+  if (cached)
+    launch_window<T, kSrcCached>(grid, stream, q, keys, values, o, lse, active, kc, vc, N, M, H, HKV, D, W, scale_log2,
+                                 nqt);
+  else if (kc != nullptr)
+    launch_window<T, kSrcCarried>(grid, stream, q, keys, values, o, lse, active, kc, vc, N, M, H, HKV, D, W, scale_log2,
+                                  nqt);
   else
-    launch_window<T, false>(grid, stream, q, keys, values, o, lse, active, kc, vc, N, M, H, HKV, D, W, scale_log2, nqt);
+    launch_window<T, kSrcPlain>(grid, stream, q, keys, values, o, lse, active, kc, vc, N, M, H, HKV, D, W, scale_log2,
+                                nqt);
   return check_launch(who);
 }
 
@@ -486,4 +529,24 @@ extern "C" int vsp_window_attn_carried_f16(const void* q, const void* keys, cons
                              static_cast<T*>(o), nullptr, active, B, N, M, H, HKV, D, window, scale, stream,
                              "vsp_window_attn_carried_f16", static_cast<const T*>(keys_carried),
                              static_cast<const T*>(values_carried));
+}
+
+extern "C" int vsp_window_attn_cached_bf16(const void* q, const void* cache_keys, const void* cache_values,
+                                           const void* keys, const void* values, void* o, const uint8_t* active, int B,
+                                           int N, int M, int H, int HKV, int D, int window, float scale, void* stream) {
+  using T = __bf16;
+  return vsp::window_attn<T>(static_cast<const T*>(q), static_cast<const T*>(cache_keys),
+                             static_cast<const T*>(cache_values), static_cast<T*>(o), nullptr, active, B, N, M, H, HKV, D,
+                             window, scale, stream, "vsp_window_attn_cached_bf16", static_cast<const T*>(keys),
+                             static_cast<const T*>(values), true);
+}
+
+extern "C" int vsp_window_attn_cached_f16(const void* q, const void* cache_keys, const void* cache_values,
+                                          const void* keys, const void* values, void* o, const uint8_t* active, int B,
+                                          int N, int M, int H, int HKV, int D, int window, float scale, void* stream) {
+  using T = _Float16;
+  return vsp::window_attn<T>(static_cast<const T*>(q), static_cast<const T*>(cache_keys),
+                             static_cast<const T*>(cache_values), static_cast<T*>(o), nullptr, active, B, N, M, H, HKV, D,
+                             window, scale, stream, "vsp_window_attn_cached_f16", static_cast<const T*>(keys),
+                             static_cast<const T*>(values), true);
 }

@@ -178,3 +178,42 @@ def window_attention(q: Tensor, keys: Tensor, values: Tensor, window: int, *, ac
         return padded[..., :dk].contiguous()
     out: Tensor = _WindowAttention.apply(q, keys, values, int(window), mask, 1.0 / math.sqrt(dk))
     return out
+
+
+def window_attention_cached(q: Tensor, cache_keys: Tensor, cache_values: Tensor, keys: Tensor, values: Tensor,
+                            window: int) -> Tensor:
+    """``window_attention(q, cat([cache_keys, keys], 1), cat([cache_values, values], 1), window)``
+    with the cache's rows ``[b, m, hkv, dk]`` and the chunk's ``[b, n, hkv, dk]`` held apart: the
+    kernel (``vsp_window_attn_cached_*``) reads each key row from its own tensor, so neither is
+    copied, and the outputs are the concatenated call's bit for bit. Under autograd, and at head
+    widths between the kernels', the concatenated call runs (its backward takes one key tensor).
+
+    Raises:
+        ContractError / ValueError: as ``window_attention``, for shapes or dtypes that disagree.
+    """
+    if window < 1:
+        raise ValueError(f"window must be at least 1, got {window}")
+    dims: Dims = {}
+    check_shape("q", q, ("b", "n", "h", "dk"), dims)
+    check_shape("cache_keys", cache_keys, ("b", "m", "hkv", "dk"), dims)
+    check_shape("cache_values", cache_values, ("b", "m", "hkv", "dk"), dims)
+    check_shape("keys", keys, ("b", "n", "hkv", "dk"), dims)
+    check_shape("values", values, ("b", "n", "hkv", "dk"), dims)
+    b, n, h, dk = q.shape
+    m, hkv = dims["m"], dims["hkv"]
+    tensors = (q, cache_keys, cache_values, keys, values)
+    needs_grad = torch.is_grad_enabled() and any(t.requires_grad for t in tensors)
+    plain = (m == 0 or n == 0 or needs_grad or dk not in HEAD_DIMS or h % hkv != 0 or q.dtype not in WINDOW_KERNEL_DTYPES
+             or any(t.dtype != q.dtype or t.device != q.device for t in tensors) or q.device.type != "cuda")
+    if plain:  # the one-tensor call, which also raises whatever the arguments break
+        if m == 0:
+            return window_attention(q, keys, values, window)
+        return window_attention(q, torch.cat([cache_keys, keys], 1), torch.cat([cache_values, values], 1), window)
+    qc, ck, cv, kc, vc = (_aligned(t) for t in tensors)
+    o = torch.empty_like(qc)
+    suffix = "bf16" if q.dtype == torch.bfloat16 else "f16"
+    with torch.cuda.device(q.device):
+        _lib.call(f"vsp_window_attn_cached_{suffix}", qc.data_ptr(), ck.data_ptr(), cv.data_ptr(), kc.data_ptr(),
+                  vc.data_ptr(), o.data_ptr(), None, b, n, m, h, hkv, dk, int(window), 1.0 / math.sqrt(dk),
+                  _lib.stream_of(q.device))
+    return o
