@@ -1240,12 +1240,12 @@ __global__ __launch_bounds__(kPrepThreads) void scan_bwd_prep_bf16_kernel(
     rk.fetch(k, b, h, t0, N, H);
     rq.fetch(q, b, h, t0, N, H);
     ro.fetch(d_o, b, h, t0, N, H, active);
-    rv.fetch(v, b, h, t0, N, H);
+    if constexpr (!REC) rv.fetch(v, b, h, t0, N, H);  // V only for U = T V and B = K^T U (the state chain)
     rbeta.fetch(beta, b, h, t0, N, H);
     rk.put(sK, LD);
     rq.put(sQ, LD);
     ro.put(sO, LD);
-    rv.put(sV, LD);
+    if constexpr (!REC) rv.put(sV, LD);
     rbeta.put(sB, t0, N);
   }
   __syncthreads();
@@ -1320,7 +1320,7 @@ __global__ __launch_bounds__(kPrepThreads) void scan_bwd_prep_bf16_kernel(
     *reinterpret_cast<bf16x4*>(sT + i * L6 + j) = t;
   }
   __syncthreads();
-  // W = T K and U = T V over L; P = tril(Q K^T) beside T
+  // W = T K and (for the state chain) U = T V over L; P = tril(Q K^T) beside T
   #pragma unroll
   for (int u_ = 0; u_ < NT / 2; ++u_) {
     const int ct = ch + 2 * u_;
@@ -1329,10 +1329,10 @@ __global__ __launch_bounds__(kPrepThreads) void scan_bwd_prep_bf16_kernel(
     for (int kk = 0; kk < kC; kk += 32) {
       const bf16x8 a = frow(sT, L6, r0, kk);
       aw = mma32(a, fcol(sK, LD, 16 * ct, kk), aw);
-      au = mma32(a, fcol(sV, LD, 16 * ct, kk), au);
+      if constexpr (!REC) au = mma32(a, fcol(sV, LD, 16 * ct, kk), au);
     }
     put_tile(sW, LD, r0, 16 * ct, aw);
-    put_tile(sU, LD, r0, 16 * ct, au);
+    if constexpr (!REC) put_tile(sU, LD, r0, 16 * ct, au);
   }
   #pragma unroll
   for (int u_ = 0; u_ < 2; ++u_) {
@@ -1378,8 +1378,9 @@ __global__ __launch_bounds__(kPrepThreads) void scan_bwd_prep_bf16_kernel(
       for (int j = 0; j < RG; ++j) y[j] = bb[j] = kw[j] = wk[j] = zero4();
 #pragma unroll
       for (int kk = 0; kk < kC; kk += 32) {
-        const bf16x8 ob = fcol(sO, LD, 16 * ct, kk), zb = -fcol(sZ, LD, 16 * ct, kk), ub = fcol(sU, LD, 16 * ct, kk);
-        const bf16x8 wb = fcol(sW, LD, 16 * ct, kk), kb = fcol(sK, LD, 16 * ct, kk);
+        const bf16x8 ob = fcol(sO, LD, 16 * ct, kk), zb = -fcol(sZ, LD, 16 * ct, kk);
+        const bf16x8 ub = REC ? bf16x8{} : fcol(sU, LD, 16 * ct, kk);
+        const bf16x8 wb = fcol(sW, LD, 16 * ct, kk), kb = REC ? bf16x8{} : fcol(sK, LD, 16 * ct, kk);
 #pragma unroll
         for (int j = 0; j < RG; ++j) {
           const int rt = rt0 + RSTEP * (j0 + j);
