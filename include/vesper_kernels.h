@@ -269,7 +269,7 @@ int vsp_rotary_qk_f32(const float* q, const float* k, const int64_t* pos, const 
  * (keys, values, position, valid flag) in place, after every read of the call, by the same launch.
  * The contract of vesper/attention.py:298-338 (`attend_ring`, without the projections) and
  * vesper/attention.py:104-139 (`kv_ring_write`); the reference runs masked SDPA there.
- * D in {16, 32, 64, 128}; at most 8 query heads per KV head; q, k, v and the ring's keys and
+ * D a multiple of 8 up to 256; at most 8 query heads per KV head; q, k, v and the ring's keys and
  * values 16-byte aligned; active: [B] or NULL (an inactive row reads zeros and still writes its
  * token). `workspace` (needed when `write` is nonzero) holds vsp_ring_attn_workspace_bytes(B)
  * bytes of per-row arrival counters: zero before the first call, and every call leaves it zero.

@@ -130,6 +130,34 @@ def test_two_chunks_through_the_cache_equal_the_whole_sequence():
     assert torch.equal(cache.k.cpu(), k[:, -w:])
 
 
+def test_float32_attend_takes_the_blocked_branch_and_chunks_equal_the_whole_sequence():
+    # float32 activations (attention.py:384-407): two chunks through the cache against the oracle
+    # over the whole sequence, and the gradients of q, k, v (float32 against float64 on the CPU)
+    from vesper.attention import attend, kv_cache_empty
+
+    b, h, hkv, dk, w = 2, 4, 2, 32, 48
+    g = torch.Generator().manual_seed(5)
+    n1, n2 = 70, 131
+    q = torch.randn(b, n1 + n2, h, dk, generator=g)
+    k, v = (torch.randn(b, n1 + n2, hkv, dk, generator=g) for _ in range(2))
+    dout = torch.randn(b, n1 + n2, h, dk, generator=g)
+    pos = torch.arange(n1 + n2).expand(b, n1 + n2).contiguous()
+    qg, kg, vg = (t.to(GPU).requires_grad_() for t in (q, k, v))
+    cache = kv_cache_empty(b, hkv, dk, w, torch.float32, GPU)
+    o1, cache = attend(qg[:, :n1], kg[:, :n1], vg[:, :n1], pos[:, :n1].to(GPU), cache)
+    o2, cache = attend(qg[:, n1:], kg[:, n1:], vg[:, n1:], pos[:, n1:].to(GPU), cache)
+    got = torch.cat([o1, o2], dim=1)
+    (got * dout.to(GPU)).sum().backward()
+    qd, kd, vd = (t.double().requires_grad_() for t in (q, k, v))
+    want = oa.window_attention(qd, kd, vd, w)
+    (want * dout.double()).sum().backward()
+    assert got.dtype == torch.float32 and cache.k.shape[1] == w
+    torch.testing.assert_close(got.detach().cpu().double(), want.detach(), rtol=1e-5, atol=1e-5)
+    for name, a, e in (("q", qg, qd), ("k", kg, kd), ("v", vg, vd)):
+        torch.testing.assert_close(a.grad.cpu().double(), e.grad, rtol=1e-4, atol=1e-4, msg=name)
+    assert torch.equal(cache.k.detach().cpu(), k[:, -w:]) and torch.equal(cache.pos.cpu(), pos[:, -w:])
+
+
 def test_a_second_4096_token_chunk_with_a_full_window_cache_at_b4_h8_d64_w512():
     # the prefill attention config's shape, continued: chunk 2 of 4096 tokens over the 512-entry
     # cache chunk 1 left, against the oracle over the 8192-token sequence (float32 on the CPU)

@@ -98,6 +98,43 @@ def test_a_float32_ring_reads_as_the_ring_cast_to_the_query_dtype(dtype, h, hkv,
     assert relative_error(o32, want) < 1e-2
 
 
+@pytest.mark.parametrize("ring_dtype", [BF16, torch.float32])
+@pytest.mark.parametrize("dk", [8, 24, 40, 96, 136, 200, 248, 256])
+@pytest.mark.parametrize(("h", "hkv"), [(8, 8), (4, 2), (8, 1)])
+def test_rings_of_every_width_up_to_256_match_the_oracle(ring_dtype, dk, h, hkv):
+    """Head widths past the four first ones: 8 and 256 run their own shape; the widths that are not
+    powers of two run the next power of two's lanes with the lanes past the width idle (nothing
+    read or written there: the slots' neighbours in the ring row stay untouched)."""
+    from vesper.kernels.ring_attn import RingKVCache, ring_attention
+
+    b, w = 3, 45
+    rk, rv, rpos, valid, p = _random_ring(b, w, hkv, dk, seed=3 * dk + h, dtype=ring_dtype)
+    g = torch.Generator().manual_seed(dk)
+    q = torch.randn(b, 1, h, dk, generator=g).to(BF16)
+    k = torch.randn(b, 1, hkv, dk, generator=g).to(BF16)
+    v = torch.randn(b, 1, hkv, dk, generator=g).to(BF16)
+    want = oa.ring_attend(q.double(), k.double(), v.double(), p, rk.to(BF16).double(), rv.to(BF16).double(),
+                          rpos, valid, w)
+    ring = RingKVCache(*(t.to(GPU) for t in (rk, rv, rpos, valid)), w)
+    o, after = ring_attention(q.to(GPU), k.to(GPU), v.to(GPU), p.to(GPU), ring)
+    assert relative_error(o, want) < 1e-2
+    torch.testing.assert_close(o.float().cpu(), want.float(), rtol=3e-2, atol=3e-2)
+    nk, nv, npos, nvalid = oa.kv_ring_write(rk, rv, rpos, valid, k.to(ring_dtype), v.to(ring_dtype), p)
+    assert torch.equal(after.k.cpu(), nk) and torch.equal(after.v.cpu(), nv)
+    assert torch.equal(after.pos.cpu(), npos) and torch.equal(after.valid.cpu(), nvalid)
+
+
+def test_widths_the_kernel_does_not_take_are_refused():
+    from vesper.contracts import ContractError
+    from vesper.kernels.ring_attn import kv_ring_empty, ring_attention
+
+    for dk in (12, 264):
+        ring = kv_ring_empty(1, 1, dk, 8, BF16, GPU)
+        q = torch.zeros(1, 1, 1, dk, dtype=BF16, device=GPU)
+        with pytest.raises(ContractError, match="multiples of 8"):
+            ring_attention(q, q, q, torch.tensor([[1]], device=GPU), ring)
+
+
 def test_a_ring_of_another_dtype_is_refused():
     from vesper.contracts import ContractError
     from vesper.kernels.ring_attn import kv_ring_empty, ring_attention

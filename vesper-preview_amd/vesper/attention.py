@@ -9,9 +9,10 @@ Mirrors the pieces of the reference's ``vesper/attention.py`` around the window 
   ``:292``): one launch rotates the queries and keys of a chunk (``vsp_rotary_qk_*``); phases in
   float64, the rotation in the activations' dtype, as the reference computes it. Differentiable:
   the backward is the rotation by the opposite angle (the same kernel at negated positions).
-- ``attend`` (``WindowedAttention.attend``'s kernel branch, ``attention.py:340-407``, without the
-  output projection): the chunk's queries over the cache and the chunk through
-  ``window_attention`` (the cache's rows first, ``window_attn.py:36``), then the pushed cache.
+- ``attend`` (``WindowedAttention.attend``, ``attention.py:340-407``, without the output
+  projection): the chunk's queries over the cache and the chunk through ``window_attention`` (the
+  cache's rows first, ``window_attn.py:36``) in bfloat16 / float16, the reference's blocked eager
+  branch for float32; then the pushed cache.
 """
 
 from __future__ import annotations
@@ -25,7 +26,7 @@ from torch import Tensor
 
 from vesper.contracts import ContractError, Dims, check_shape, require
 from vesper.kernels import _lib
-from vesper.kernels.window_attn import window_attention_cached
+from vesper.kernels.window_attn import WINDOW_KERNEL_DTYPES, window_attention_cached
 
 _SUFFIX = {torch.bfloat16: "bf16", torch.float16: "f16", torch.float32: "f32"}
 
@@ -201,16 +202,27 @@ def rotary_qk(q: Tensor, k: Tensor, pos: Tensor, base: float) -> tuple[Tensor, T
 
 def attend(q: Tensor, k: Tensor, v: Tensor, pos: Tensor, cache: KVCache) -> tuple[Tensor, KVCache]:
     """Windowed softmax of a chunk's rotated ``q [b, n, h, dk]`` over the cache and the chunk's
-    rotated ``k``, ``v [b, n, hkv, dk]`` at consecutive positions ``pos [b, n]``; returns the
-    attention output ``[b, n, h, dk]`` (before the output projection) and the pushed cache. The
-    kernel branch of ``WindowedAttention.attend`` (``attention.py:373-383``): the cache's ``m``
-    rows then the chunk's as the keys of ``window_attention`` (read from the two tensors in place,
-    ``window_attention_cached``, not concatenated first), which places query ``i`` at key
-    index ``m + i``. A chunk of zero tokens returns an empty output and the cache unchanged.
+    rotated ``k``, ``v [b, n, hkv, dk]`` at positions ``pos [b, n]``; returns the attention output
+    ``[b, n, h, dk]`` (before the output projection) and the pushed cache. The two branches of
+    ``WindowedAttention.attend`` (``attention.py:340-407``):
+
+    - bfloat16 / float16 on the GPU (``:373-383``): the cache's ``m`` rows then the chunk's as the
+      keys of ``window_attention`` (read from the two tensors in place,
+      ``window_attention_cached``, not concatenated first), which places query ``i`` at key index
+      ``m + i``; positions must be consecutive across the cache and the chunk.
+    - float32 (any other dtype) on the GPU (``:384-407``, the reference's eager branch): blocks of
+      ``window`` queries, each over the keys its first query can still see, masked by position
+      (``kpos <= qpos < kpos + window``), through torch's ``scaled_dot_product_attention`` with
+      the key heads shared by ``h / hkv`` query heads; differentiable.
+
+    Tensors off the GPU are refused (the cache push, like the kernel, runs on CUDA).
+
+    A chunk of zero tokens returns an empty output and the cache unchanged.
 
     Raises:
-        ContractError: on shapes or dtypes that disagree; positions that are not consecutive
-            across the cache and the chunk (eagerly; a device assert under graph capture).
+        ContractError: on shapes or dtypes that disagree; on the kernel branch, positions that are
+            not consecutive across the cache and the chunk (eagerly; a device assert under graph
+            capture).
     """
     dims: Dims = {}
     check_shape("q", q, ("b", "n", "h", "dk"), dims)
@@ -222,6 +234,8 @@ def attend(q: Tensor, k: Tensor, v: Tensor, pos: Tensor, cache: KVCache) -> tupl
     check_shape("cache.pos", cache.pos, ("b", "m"), dims, torch.long)
     if dims["n"] == 0:
         return q.new_zeros(q.shape), cache
+    if q.is_cuda and q.dtype not in WINDOW_KERNEL_DTYPES:
+        return _attend_blocked(q, k, v, pos, cache), kv_cache_push(cache, k, v, pos)
     kpos = torch.cat([cache.pos, pos], dim=1)
     if kpos.shape[1] > 1:
         require((kpos[:, 1:] - kpos[:, :-1] == 1).all().reshape(1), "attend: cache and chunk positions must be consecutive")
@@ -229,6 +243,31 @@ def attend(q: Tensor, k: Tensor, v: Tensor, pos: Tensor, cache: KVCache) -> tupl
     o = window_attention_cached(q, cache.k.to(q.dtype), cache.v.to(q.dtype), k.to(q.dtype), v.to(q.dtype),
                                 cache.window)
     return o, kv_cache_push(cache, k, v, pos)
+
+
+def _attend_blocked(q: Tensor, k: Tensor, v: Tensor, pos: Tensor, cache: KVCache) -> Tensor:
+    """``attend``'s eager branch (``attention.py:384-407``): query block ``[s, s + w)`` attends the
+    chunk's keys from ``s - w + 1`` on, plus the cache while ``s < w`` (older entries are out of every
+    query's window by then), under the position mask. The keys and values are taken in q's dtype
+    (the cache may be wider: an empty float32 cache promotes what is pushed onto it)."""
+    n, w = q.shape[1], cache.window
+    ck, cv = cache.k.to(q.dtype), cache.v.to(q.dtype)
+    kc, vc = k.to(q.dtype), v.to(q.dtype)
+    outs: list[Tensor] = []
+    for s in range(0, n, w):
+        e = min(s + w, n)
+        first = max(0, s - w + 1)
+        keys, vals, kpos = kc[:, first:e], vc[:, first:e], pos[:, first:e]
+        if s < w:
+            keys, vals = torch.cat([ck, keys], dim=1), torch.cat([cv, vals], dim=1)
+            kpos = torch.cat([cache.pos, kpos], dim=1)
+        qpos = pos[:, s:e]
+        visible = (kpos[:, None, :] <= qpos[:, :, None]) & (kpos[:, None, :] > qpos[:, :, None] - w)
+        block = torch.nn.functional.scaled_dot_product_attention(
+            q[:, s:e].transpose(1, 2), keys.transpose(1, 2), vals.transpose(1, 2), attn_mask=visible[:, None],
+            enable_gqa=True)
+        outs.append(block.transpose(1, 2))
+    return torch.cat(outs, dim=1)
 
 
 def scale_of(dk: int) -> float:

@@ -8,7 +8,8 @@
 //
 // ring_attn_kernel: one workgroup per (b, KV head) serves the G = H / HKV query heads of that
 // group, so each ring row is read from HBM once per step. D/8 lanes share a key row (16-byte
-// pieces); a thread takes KPT keys of a batch and issues all of their K and V loads before any
+// pieces; D is the head width rounded up to a power of two, and with PAD the lanes past the real
+// width dk load nothing and hold zeros); a thread takes KPT keys of a batch and issues all of their K and V loads before any
 // arithmetic, so the whole window of the head is in flight at once (W = 512 at D = 64 is one
 // batch). Each thread keeps, per query head, an online softmax over its own keys (running max,
 // sum and weighted values, base-2 exponent); the partial states merge across the key groups of a
@@ -72,11 +73,11 @@ __device__ __forceinline__ void store_ring8(R* p, const typename Ring8<T>::V8& x
   }
 }
 
-template <typename T, typename R, int D, int GM>
+template <typename T, typename R, int D, int GM, bool PAD>
 __global__ __launch_bounds__(RingShape<GM>::NT) void ring_attn_kernel(
     const T* __restrict__ q, const T* __restrict__ knew, const T* __restrict__ vnew, const int64_t* __restrict__ pos,
     R* ring_k, R* ring_v, int64_t* ring_pos, uint8_t* ring_valid, T* __restrict__ o, const uint8_t* __restrict__ active,
-    uint32_t* __restrict__ counters, int H, int HKV, int W, float scale_log2, int write) {
+    uint32_t* __restrict__ counters, int H, int HKV, int W, float scale_log2, int write, int dk_arg) {
   constexpr int NT = RingShape<GM>::NT;
   constexpr int NW = NT / 64;              // waves
   constexpr int KL = D / 8;                // lanes per key row
@@ -95,10 +96,12 @@ __global__ __launch_bounds__(RingShape<GM>::NT) void ring_attn_kernel(
   const int G = H / HKV;
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int part = tid % KL, kg = tid / KL;
+  const int dk = PAD ? dk_arg : D;       // the real head width (a multiple of 8, at most D)
+  const bool live = !PAD || 8 * part < dk;  // this lane's 8 features exist
   const int64_t p = pos[b];
-  const size_t row_stride = (size_t)HKV * D;
-  const size_t head_off = ((size_t)b * W * HKV + kvh) * D + 8 * part;
-  T* out = o + ((size_t)b * H + (size_t)kvh * G) * D;
+  const size_t row_stride = (size_t)HKV * dk;
+  const size_t head_off = ((size_t)b * W * HKV + kvh) * dk + 8 * part;
+  T* out = o + ((size_t)b * H + (size_t)kvh * G) * dk;
   // An inactive row is computed like an active one and stores zeros, so no wait on its flag delays
   // the row's loads; its token is still written.
   {
@@ -166,23 +169,31 @@ __global__ __launch_bounds__(RingShape<GM>::NT) void ring_attn_kernel(
 #pragma unroll
       for (int i = 0; i < KPT; ++i) {
         const int j = min(j0 + kg + i * KPP, W - 1);  // keys past W re-read row W - 1, masked below
-        kr[i] = load_ring8<T>(kb + (size_t)j * row_stride);
-        vr[i] = load_ring8<T>(vb + (size_t)j * row_stride);
+        if (live) {
+          kr[i] = load_ring8<T>(kb + (size_t)j * row_stride);
+          vr[i] = load_ring8<T>(vb + (size_t)j * row_stride);
+        } else {
+#pragma unroll
+          for (int e = 0; e < 8; ++e) kr[i][e] = vr[i][e] = from_f32<T>(0.f);
+        }
       }
       if (j0 == 0) {  // the group's query heads (heads past G are zero: their results are never stored)
-        const T* qb = q + ((size_t)b * H + (size_t)kvh * G) * D;
+        const T* qb = q + ((size_t)b * H + (size_t)kvh * G) * dk;
         if constexpr (kQReg) {
 #pragma unroll
           for (int gi = 0; gi < GM; ++gi) {
-            if (gi < G) {
-              qr[gi] = *reinterpret_cast<const V8*>(qb + gi * D + 8 * part);
+            if (gi < G && live) {
+              qr[gi] = *reinterpret_cast<const V8*>(qb + gi * dk + 8 * part);
             } else {
 #pragma unroll
               for (int e = 0; e < 8; ++e) qr[gi][e] = from_f32<T>(0.f);
             }
           }
         } else {
-          for (int i = tid; i < GM * D; i += NT) sq[i / D][i % D] = i / D < G ? qb[i] : from_f32<T>(0.f);
+          for (int i = tid; i < GM * D; i += NT) {
+            const int gi = i / D, d = i % D;
+            sq[gi][d] = gi < G && d < dk ? qb[gi * dk + d] : from_f32<T>(0.f);
+          }
         }
       }
       __syncthreads();  // the previous batch's flags are read (and sq is written)
@@ -222,9 +233,14 @@ __global__ __launch_bounds__(RingShape<GM>::NT) void ring_attn_kernel(
       fold(sc, vr, KPT);
     }
     if (kg == 0) {  // the new token, always visible
-      const V8 kn = *reinterpret_cast<const V8*>(knew + ((size_t)b * HKV + kvh) * D + 8 * part);
-      V8 vn[KPT];
-      vn[0] = *reinterpret_cast<const V8*>(vnew + ((size_t)b * HKV + kvh) * D + 8 * part);
+      V8 kn, vn[KPT];
+      if (live) {
+        kn = *reinterpret_cast<const V8*>(knew + ((size_t)b * HKV + kvh) * dk + 8 * part);
+        vn[0] = *reinterpret_cast<const V8*>(vnew + ((size_t)b * HKV + kvh) * dk + 8 * part);
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) kn[e] = vn[0][e] = from_f32<T>(0.f);
+      }
       float sc[GM][KPT];
 #pragma unroll
       for (int gi = 0; gi < GM; ++gi) sc[gi][0] = dot(gi, kn);
@@ -256,8 +272,8 @@ __global__ __launch_bounds__(RingShape<GM>::NT) void ring_attn_kernel(
     }
     __syncthreads();
     const bool on = active == nullptr || active[b] != 0;
-    for (int i = tid; i < G * D; i += NT) {
-      const int gi = i / D, d = i - gi * D;
+    for (int i = tid; i < G * dk; i += NT) {
+      const int gi = i / dk, d = i - gi * dk;
       float mx = smerge[0][gi][0];
 #pragma unroll
       for (int w = 1; w < NW; ++w) mx = fmaxf(mx, smerge[w][gi][0]);
@@ -275,17 +291,19 @@ __global__ __launch_bounds__(RingShape<GM>::NT) void ring_attn_kernel(
   if (!write || p < 0) return;  // a negative position is refused by the host wrapper
   __syncthreads();              // every read of this workgroup is done
   const int slot = (int)(p % W);
-  const size_t dst = ((size_t)b * W + slot) * row_stride + (size_t)kvh * D;
-  const size_t src = ((size_t)b * HKV + kvh) * D;
+  const size_t dst = ((size_t)b * W + slot) * row_stride + (size_t)kvh * dk;
+  const size_t src = ((size_t)b * HKV + kvh) * dk;
   if (tid < KL) {
-    store_ring8<T>(ring_k + dst + 8 * tid, *reinterpret_cast<const V8*>(knew + src + 8 * tid));
+    if (8 * tid < dk) store_ring8<T>(ring_k + dst + 8 * tid, *reinterpret_cast<const V8*>(knew + src + 8 * tid));
   } else if (tid < 2 * KL) {
     const int pp = tid - KL;
-    store_ring8<T>(ring_v + dst + 8 * pp, *reinterpret_cast<const V8*>(vnew + src + 8 * pp));
+    if (8 * pp < dk) store_ring8<T>(ring_v + dst + 8 * pp, *reinterpret_cast<const V8*>(vnew + src + 8 * pp));
   }
 }
 
-bool ring_width(int D) { return D == 16 || D == 32 || D == 64 || D == 128; }
+// Head widths the ring kernel takes: multiples of 8 (16-byte rows) up to 256; the powers of two run
+// their own shape, the others the next power of two's lanes with the lanes past the width idle.
+bool ring_width(int D) { return D >= 8 && D <= 256 && D % 8 == 0; }
 
 bool aligned16(const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15) == 0; }
 
@@ -296,7 +314,7 @@ int ring_attn(const T* q, const T* knew, const T* vnew, const int64_t* pos, R* r
   if (B < 0 || H < 1 || HKV < 1 || W < 1) return fail(ERR_ARG, "%s: bad sizes B=%d H=%d HKV=%d W=%d", who, B, H, HKV, W);
   if (H % HKV != 0) return fail(ERR_ARG, "%s: %d query heads are not a multiple of %d KV heads", who, H, HKV);
   if (H / HKV > kMaxGroup) return fail(ERR_UNSUPPORTED, "%s: %d query heads per KV head (at most %d)", who, H / HKV, kMaxGroup);
-  if (!ring_width(D)) return fail(ERR_UNSUPPORTED, "%s: head dimension %d (kernels: 16, 32, 64, 128)", who, D);
+  if (!ring_width(D)) return fail(ERR_UNSUPPORTED, "%s: head dimension %d (kernels: multiples of 8 up to 256)", who, D);
   if (B == 0) return OK;
   if (!q || !knew || !vnew || !pos || !ring_k || !ring_v || !ring_pos || !ring_valid || !o)
     return fail(ERR_ARG, "%s: null pointer", who);
@@ -312,21 +330,29 @@ int ring_attn(const T* q, const T* knew, const T* vnew, const int64_t* pos, R* r
   const int G = H / HKV;
   auto go = [&](auto kern, int nt) {
     hipLaunchKernelGGL(kern, grid, dim3(nt), 0, stream, q, knew, vnew, pos, ring_k, ring_v, ring_pos, ring_valid, o,
-                       active, counters, H, HKV, W, scale_log2, write);
+                       active, counters, H, HKV, W, scale_log2, write, D);
   };
-  auto by_group = [&](auto dtag) {
+  auto by_group = [&](auto dtag, auto padtag) {
     constexpr int Dc = decltype(dtag)::value;
-    if (G == 1) go(ring_attn_kernel<T, R, Dc, 1>, RingShape<1>::NT);
-    else if (G == 2) go(ring_attn_kernel<T, R, Dc, 2>, RingShape<2>::NT);
-    else if (G <= 4) go(ring_attn_kernel<T, R, Dc, 4>, RingShape<4>::NT);
-    else go(ring_attn_kernel<T, R, Dc, 8>, RingShape<8>::NT);
+    constexpr bool Pc = decltype(padtag)::value;
+    if (G == 1) go(ring_attn_kernel<T, R, Dc, 1, Pc>, RingShape<1>::NT);
+    else if (G == 2) go(ring_attn_kernel<T, R, Dc, 2, Pc>, RingShape<2>::NT);
+    else if (G <= 4) go(ring_attn_kernel<T, R, Dc, 4, Pc>, RingShape<4>::NT);
+    else go(ring_attn_kernel<T, R, Dc, 8, Pc>, RingShape<8>::NT);
   };
-  switch (D) {
-    case 16: by_group(std::integral_constant<int, 16>{}); break;
-    case 32: by_group(std::integral_constant<int, 32>{}); break;
-    case 64: by_group(std::integral_constant<int, 64>{}); break;
-    default: by_group(std::integral_constant<int, 128>{}); break;
-  }
+  auto by_width = [&](auto padtag) {
+    const int Dp = D <= 8 ? 8 : D <= 16 ? 16 : D <= 32 ? 32 : D <= 64 ? 64 : D <= 128 ? 128 : 256;
+    switch (Dp) {
+      case 8: by_group(std::integral_constant<int, 8>{}, padtag); break;
+      case 16: by_group(std::integral_constant<int, 16>{}, padtag); break;
+      case 32: by_group(std::integral_constant<int, 32>{}, padtag); break;
+      case 64: by_group(std::integral_constant<int, 64>{}, padtag); break;
+      case 128: by_group(std::integral_constant<int, 128>{}, padtag); break;
+      default: by_group(std::integral_constant<int, 256>{}, padtag); break;
+    }
+  };
+  if ((D & (D - 1)) == 0) by_width(std::false_type{});
+  else by_width(std::true_type{});
   return check_launch(who);
 }
 

@@ -24,7 +24,7 @@ from torch import Tensor
 from vesper.contracts import ContractError, Dims, check_shape, require
 from vesper.kernels import _lib
 
-HEAD_DIMS = (16, 32, 64, 128)
+MAX_HEAD_DIM = 256  # head widths: multiples of 8 (16-byte rows) up to this
 MAX_GROUP = 8
 
 
@@ -109,8 +109,8 @@ def ring_attention(q: Tensor, k: Tensor, v: Tensor, pos: Tensor, cache: RingKVCa
     hkv = dims["hkv"]
     if h % hkv != 0 or h // hkv > MAX_GROUP:
         raise ContractError(f"{h} query heads over {hkv} KV heads: need a multiple, at most {MAX_GROUP} per KV head")
-    if dk not in HEAD_DIMS:
-        raise ContractError(f"head dimension {dk} is not one the kernel tiles ({HEAD_DIMS})")
+    if dk % 8 != 0 or not 8 <= dk <= MAX_HEAD_DIM:
+        raise ContractError(f"head dimension {dk}: the kernel takes multiples of 8 up to {MAX_HEAD_DIM}")
     if torch.is_grad_enabled() and any(t.requires_grad for t in (q, k, v)):
         raise ContractError("the HIP ring attention is forward only: call it under torch.no_grad()")
     if check_positions and b > 0:
