@@ -22,7 +22,7 @@
 extern "C" {
 #endif
 
-#define VSP_ABI_VERSION 13
+#define VSP_ABI_VERSION 14
 
 /* Status codes. */
 #define VSP_OK 0
@@ -389,6 +389,20 @@ int vsp_key_filter_backward_f32(const float* z, const float* history, const floa
  * [rows, d] bf16, the projections' operand. d a multiple of 8 in 8..2048; x, gain, out 16-byte
  * aligned. */
 int vsp_rms_norm_bf16(const float* x, const float* gain, void* out, int rows, int d, void* stream);
+
+/* The decode step's projection of that normalized stream, fused (the looped column's per-pass
+ * projections, vesper/column.py:192-260 and vesper/attention.py:269-292, for a decode step of M
+ * single-token rows): s = x + residual (float32; residual [M, d] bf16 or NULL) is written to
+ * sum_out ([M, d] float32, or NULL; it must not overlap x), z = RMSNorm(s, gain) in bf16 exactly as
+ * vsp_rms_norm_bf16 computes it, and for each of the nblk (1..4) weight blocks
+ * out_j = z W_j [:, :used_j] (bf16, [M, used_j] contiguous, fp32 accumulation), W_j [d, cols] the
+ * block's weight passed transposed: weights_t [nblk, cols, d] bf16. Block sigmoid_block (or -1 for
+ * none) is stored as the logistic of its bf16-rounded product (the write strength). d a multiple
+ * of 32 in 32..2048; 1 <= used_j <= cols; x, residual, sum_out, gain and weights_t 16-byte
+ * aligned, the outputs 4-byte aligned. */
+int vsp_decode_proj_bf16(const float* x, const void* residual, float* sum_out, const float* gain,
+                         const void* weights_t, int nblk, int cols, int d, int M, int used0, int used1, int used2,
+                         int used3, void* out0, void* out1, void* out2, void* out3, int sigmoid_block, void* stream);
 
 /* ---- copy-forward bookkeeping of the looped column ------------------------------------------
  * Replaces the row-wise `where` selects of vesper/loop.py:523-537 (`_merge`: tokens halting now

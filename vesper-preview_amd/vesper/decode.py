@@ -29,7 +29,8 @@ from vesper.column import recurrent_keys
 from vesper.contracts import ContractError, Dims, check_shape
 from vesper.kernels.delta_scan import delta_scan_step_fused
 from vesper.kernels.ring_attn import RingKVCache, ring_attention
-from vesper.kernels.norm import rms_norm_bf16
+from vesper.attention import rotary_qk
+from vesper.kernels.norm import decode_projection
 from vesper.loop import BF16, LoopedColumn, _normalize
 
 WARM_STEPS = 3  # eager calls before the capture (vesper/graphs.py:99)
@@ -89,25 +90,44 @@ def decode_step(column: LoopedColumn, depth: int, values: Sequence[Tensor],
     _check(column, x, position, flat)
     if not 1 <= depth <= column.passes:
         raise ContractError(f"depth {depth} is outside 1..{column.passes}")
-    b = x.shape[0]
-    h, dk = column.heads, column.head_dim
+    b, d = x.shape[0], x.shape[2]
+    h, hkv, dk = column.heads, column.kv_heads, column.head_dim
+    hd = h * dk
     with torch.no_grad():
+        # the residual stream between the sublayers: each projection adds the previous mixer's
+        # output to it, normalizes and projects in one launch (vsp_decode_proj_bf16)
+        xs = x.reshape(b, d)
+        pending = None  # the previous pass's attention output, added by the next projection
         for t in range(depth):
             state, history, rk, rv, rp, rvalid = flat[PER_PASS * t: PER_PASS * (t + 1)]
-            q_in, z, v, beta = column.project_rec(t, rms_norm_bf16(x))
+            w_rec, w_attn = column.decode_weights(t)
+            if pending is None:
+                q_in, z, v, beta = decode_projection(xs, w_rec, (hd, hd, hd, h), sigmoid_block=3)
+            else:
+                nxt_x = torch.empty_like(xs)
+                q_in, z, v, beta = decode_projection(xs, w_rec, (hd, hd, hd, h), residual=pending, sum_out=nxt_x,
+                                                     sigmoid_block=3)
+                xs = nxt_x
             q = q_in.view(b, 1, h, dk)  # the scan's query is not normalized (column.py:247)
+            z = z.view(b, 1, hd)
             if column.taps is None:
                 k = _normalize(z, h)
             else:
                 k, nxt = recurrent_keys(z, history, column.taps[t], h)
                 history.copy_(nxt)
-            o, _ = delta_scan_step_fused(q[:, 0], k[:, 0], v[:, 0], beta.view(b, h), state, out_state=state)
-            x1 = x + o.reshape(b, 1, h * dk)  # float32 (promoted in the add)
-            aq, ak, av = column.project_attn(t, rms_norm_bf16(x1), position)
+            o, _ = delta_scan_step_fused(q[:, 0], k[:, 0], v.view(b, h, dk), beta, state, out_state=state)
+            x1 = torch.empty_like(xs)
+            aq, ak, av = decode_projection(xs, w_attn, (hd, hkv * dk, hkv * dk), residual=o.reshape(b, hd),
+                                           sum_out=x1)
+            xs = x1
+            aq, ak = aq.view(b, 1, h, dk), ak.view(b, 1, hkv, dk)
+            if column.rotary_base is not None:
+                aq, ak = rotary_qk(aq, ak, position, column.rotary_base)
             ring = RingKVCache(rk, rv, rp, rvalid, column.window)
-            a, _ = ring_attention(aq, ak, av, position, ring, inplace=True, check_positions=False,
+            a, _ = ring_attention(aq, ak, av.view(b, 1, hkv, dk), position, ring, inplace=True, check_positions=False,
                                   workspace=workspace)
-            x = x1 + a.reshape(b, 1, h * dk)
+            pending = a.reshape(b, hd)
+        x = (xs + pending).view(b, 1, d)  # float32 (promoted in the add)
     return [x, *flat]
 
 

@@ -46,3 +46,72 @@ def rms_norm_bf16(x: Tensor, gain: Tensor | None = None) -> Tensor:
     with torch.cuda.device(x.device):
         _lib.call("vsp_rms_norm_bf16", xc.data_ptr(), _lib.ptr(g), out.data_ptr(), rows, d, _lib.stream_of(x.device))
     return out
+
+
+def decode_projection(x: Tensor, weights_t: Tensor, used: tuple[int, ...], *, residual: Tensor | None = None,
+                      sum_out: Tensor | None = None, gain: Tensor | None = None,
+                      sigmoid_block: int | None = None) -> list[Tensor]:
+    """A decode step's sublayer projections in one launch (``vsp_decode_proj_bf16``): the residual
+    sum ``s = x + residual`` (written into ``sum_out`` when given), ``z = RMSNorm(s, gain)`` in
+    bfloat16 exactly as ``rms_norm_bf16`` computes it, and ``z W_j[:, :used_j]`` for each block of
+    the stacked projection weight (``vesper/column.py:192-260``, ``vesper/attention.py:269-292``).
+
+    Args:
+        x: float32 ``[M, d]`` (one row a token), ``d`` a multiple of 32 in 32..2048.
+        weights_t: bf16 ``[p, cols, d]``: the stacked ``[p, d, cols]`` weight, each block transposed.
+        used: the columns kept of each of the ``p`` (1..4) blocks.
+        residual: optional bf16 ``[M, d]`` added to ``x`` (the previous mixer's output).
+        sum_out: optional float32 ``[M, d]`` that receives ``s`` (not ``x`` itself).
+        gain: optional float32 ``[d]`` (the norm's weight; ones when omitted).
+        sigmoid_block: the block whose outputs pass through the logistic function (the write strength).
+
+    Returns:
+        one bf16 ``[M, used_j]`` tensor per block.
+
+    Raises:
+        ContractError: on shapes, dtypes or devices outside that contract.
+    """
+    if x.dim() != 2 or x.dtype != torch.float32 or x.device.type != "cuda":
+        raise ContractError(f"x: float32 [M, d] on CUDA, got {tuple(x.shape)} {x.dtype} on {x.device}")
+    m, d = x.shape
+    if weights_t.dim() != 3 or weights_t.dtype != torch.bfloat16 or weights_t.shape[2] != d:
+        raise ContractError(f"weights_t: bf16 [p, cols, {d}], got {tuple(weights_t.shape)} {weights_t.dtype}")
+    p, cols = weights_t.shape[0], weights_t.shape[1]
+    if len(used) != p or not 1 <= p <= 4 or any(not 1 <= u <= cols for u in used):
+        raise ContractError(f"used: {p} widths in 1..{cols}, got {tuple(used)}")
+    if d % 32 or not 32 <= d <= 2048:
+        raise ContractError(f"x: width {d} is not a multiple of 32 in 32..2048")
+    tensors = [("weights_t", weights_t)]
+    if residual is not None:
+        if residual.shape != (m, d) or residual.dtype != torch.bfloat16:
+            raise ContractError(f"residual: bf16 [{m}, {d}], got {tuple(residual.shape)} {residual.dtype}")
+        tensors.append(("residual", residual))
+    if sum_out is not None:
+        if sum_out.shape != (m, d) or sum_out.dtype != torch.float32 or not sum_out.is_contiguous():
+            raise ContractError(f"sum_out: contiguous float32 [{m}, {d}], got {tuple(sum_out.shape)} {sum_out.dtype}")
+        if sum_out.data_ptr() == x.data_ptr():
+            raise ContractError("sum_out must not be x")
+        tensors.append(("sum_out", sum_out))
+    if gain is not None:
+        if gain.shape != (d,) or gain.dtype != torch.float32:
+            raise ContractError(f"gain: float32 [{d}], got {tuple(gain.shape)} {gain.dtype}")
+        tensors.append(("gain", gain))
+    for name, t in tensors:
+        if t.device != x.device:
+            raise ContractError(f"{name} is on {t.device}, x on {x.device}")
+    if sigmoid_block is not None and not 0 <= sigmoid_block < p:
+        raise ContractError(f"sigmoid_block {sigmoid_block} is not one of the {p} blocks")
+    xc, wc = x.contiguous(), weights_t.contiguous()
+    rc = None if residual is None else residual.contiguous()
+    gc = None if gain is None else gain.contiguous()
+    for name, t in (("x", xc), ("weights_t", wc), ("residual", rc), ("sum_out", sum_out), ("gain", gc)):
+        if t is not None and t.data_ptr() % 16:
+            raise ContractError(f"{name} must be 16-byte aligned")
+    outs = [torch.empty(m, u, dtype=torch.bfloat16, device=x.device) for u in used]
+    ptrs = [o.data_ptr() for o in outs] + [0] * (4 - p)
+    widths = list(used) + [1] * (4 - p)
+    with torch.cuda.device(x.device):
+        _lib.call("vsp_decode_proj_bf16", xc.data_ptr(), _lib.ptr(rc), _lib.ptr(sum_out), _lib.ptr(gc), wc.data_ptr(),
+                  p, cols, d, m, *widths, *ptrs, -1 if sigmoid_block is None else sigmoid_block,
+                  _lib.stream_of(x.device))
+    return outs

@@ -135,6 +135,7 @@ class LoopedColumn:
 
         self.w_rec = [torch.stack([padded(self.w[n][t]) for n in ("wq", "wk", "wv", "wb")]) for t in range(self.passes)]
         self.w_attn = [torch.stack([padded(self.w[n][t]) for n in ("waq", "wak", "wav")]) for t in range(self.passes)]
+        self._decode_w: dict[int, tuple[Tensor, Tensor]] = {}
 
     def project_rec(self, t: int, xb: Tensor) -> tuple[Tensor, Tensor, Tensor, Tensor]:
         """Pass ``t``'s recurrent projections of ``xb [b, n, d]`` (bf16), one batched GEMM:
@@ -145,6 +146,14 @@ class LoopedColumn:
         y = torch.matmul(xb.reshape(b * n, d), self.w_rec[t])  # [4, b*n, h*dk], each block contiguous
         beta = torch.sigmoid(y[3][:, :h]).view(b, n, h)  # bf16 in and out, float32 inside
         return y[0].view(b, n, h * dk), y[1].view(b, n, h * dk), y[2].view(b, n, h, dk), beta
+
+    def decode_weights(self, t: int) -> tuple[Tensor, Tensor]:
+        """Pass ``t``'s stacked recurrent and attention weights with each block transposed
+        (``[p, h*dk, d]``), the operand layout of the decode step's fused projection; made once."""
+        if t not in self._decode_w:
+            self._decode_w[t] = (self.w_rec[t].transpose(1, 2).contiguous(),
+                                 self.w_attn[t].transpose(1, 2).contiguous())
+        return self._decode_w[t]
 
     def project_attn(self, t: int, xb: Tensor, pos: Tensor | None = None) -> tuple[Tensor, Tensor, Tensor]:
         """Pass ``t``'s attention projections of ``xb [b, n, d]`` (bf16), one batched GEMM, with the
