@@ -7,8 +7,10 @@
 // (each product and the sum rounded to it, as torch evaluates it). The inverse frequencies
 // base^(-2j/dk) arrive as a float64 table the host computed exactly as the reference does.
 //
-// One wave per token row (b, n): lane j owns pair j (and j + 64, ...), computes its cos and sin once
-// and turns that pair in every query head and every key head of the row. q and k may be rotated in
+// A workgroup takes four token rows (b, n): first its threads compute each (row, pair)'s cos and
+// sin once into LDS (the float64 part), then every (row, head, pair) turn of the rows' query and
+// key heads is an independent piece of work spread over all 256 threads, consecutive threads on
+// consecutive pairs, four pieces' loads issued before their arithmetic. q and k may be rotated in
 // place (each element is read and written by one thread).
 #include "common.h"
 #include "vesper_kernels.h"
@@ -16,12 +18,15 @@
 namespace vsp {
 namespace {
 
+template <typename T> struct Pair {
+  typedef T P2 __attribute__((ext_vector_type(2)));
+};
+
 // x1 c - x2 s and x1 s + x2 c with every operation rounded to T (no contraction into FMAs)
 template <typename T>
-__device__ __forceinline__ void turn(const T* src, T* dst, T c, T s) {
+__device__ __forceinline__ void turn(typename Pair<T>::P2 x, T* dst, T c, T s) {
 #pragma clang fp contract(off)
-  typedef T P2 __attribute__((ext_vector_type(2)));
-  const P2 x = *reinterpret_cast<const P2*>(src);
+  typedef typename Pair<T>::P2 P2;
   const float x1 = to_f32(x[0]), x2 = to_f32(x[1]), cf = to_f32(c), sf = to_f32(s);
   const float a = to_f32(from_f32<T>(x1 * cf)), b = to_f32(from_f32<T>(x2 * sf));
   const float e = to_f32(from_f32<T>(x1 * sf)), f = to_f32(from_f32<T>(x2 * cf));
@@ -46,25 +51,43 @@ __device__ __forceinline__ T from_f64(double v) {
   }
 }
 
+constexpr int kRotRows = 4;  // token rows a workgroup
+
 template <typename T>
 __global__ __launch_bounds__(256) void rotary_qk_kernel(const T* q, const T* k, const int64_t* __restrict__ pos,
                                                         const double* __restrict__ inv_freq, T* qo, T* ko, int rows,
                                                         int H, int HKV, int D) {
-  const int row = blockIdx.x * 4 + (int)(threadIdx.x >> 6), lane = threadIdx.x & 63;
-  if (row >= rows) return;
-  const double p = (double)pos[row];
-  const int half = D / 2;
-  for (int j = lane; j < half; j += 64) {
-    const double angle = p * inv_freq[j];
-    const T c = from_f64<T>(cos(angle)), s = from_f64<T>(sin(angle));
-    for (int hh = 0; hh < H; ++hh) {
-      const size_t off = ((size_t)row * H + hh) * D + 2 * j;
-      turn<T>(q + off, qo + off, c, s);
+  __shared__ T cs[kRotRows][512], sn[kRotRows][512];
+  const int half = D / 2, row0 = blockIdx.x * kRotRows;
+  const int nrows = min(kRotRows, rows - row0);
+  for (int e = threadIdx.x; e < nrows * half; e += 256) {
+    const int r = e / half, j = e - r * half;
+    const double angle = (double)pos[row0 + r] * inv_freq[j];
+    cs[r][j] = from_f64<T>(cos(angle));
+    sn[r][j] = from_f64<T>(sin(angle));
+  }
+  __syncthreads();
+  // piece t: row r = t / (heads * half), head hh, pair j (heads: the H query heads, then the HKV
+  // key heads)
+  const int heads = H + HKV, per_row = heads * half, total = nrows * per_row;
+  for (int t0 = threadIdx.x; t0 < total; t0 += 4 * 256) {
+    typename Pair<T>::P2 xv[4];
+    size_t off[4];
+    bool isq[4];
+    int rr[4], jj[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int t = min(t0 + 256 * u, total - 1);
+      const int r = t / per_row, rem = t - r * per_row, hh = rem / half, j = rem - hh * half;
+      isq[u] = hh < H;
+      off[u] = isq[u] ? ((size_t)(row0 + r) * H + hh) * D + 2 * j : ((size_t)(row0 + r) * HKV + (hh - H)) * D + 2 * j;
+      rr[u] = r;
+      jj[u] = j;
+      xv[u] = *reinterpret_cast<const typename Pair<T>::P2*>((isq[u] ? q : k) + off[u]);
     }
-    for (int hh = 0; hh < HKV; ++hh) {
-      const size_t off = ((size_t)row * HKV + hh) * D + 2 * j;
-      turn<T>(k + off, ko + off, c, s);
-    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+      if (t0 + 256 * u < total) turn<T>(xv[u], (isq[u] ? qo : ko) + off[u], cs[rr[u]][jj[u]], sn[rr[u]][jj[u]]);
   }
 }
 
@@ -80,7 +103,7 @@ int rotary_qk(const T* q, const T* k, const int64_t* pos, const double* inv_freq
        reinterpret_cast<uintptr_t>(ko)) & (2 * sizeof(T) - 1))
     return fail(ERR_ARG, "%s: q, k and the outputs must be aligned to a pair", who);
   const int rows = B * N;
-  hipLaunchKernelGGL(rotary_qk_kernel<T>, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0,
+  hipLaunchKernelGGL(rotary_qk_kernel<T>, dim3((unsigned)((rows + kRotRows - 1) / kRotRows)), dim3(256), 0,
                      reinterpret_cast<hipStream_t>(stream), q, k, pos, inv_freq, qo, ko, rows, H, HKV, D);
   return check_launch(who);
 }
