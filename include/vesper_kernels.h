@@ -335,7 +335,9 @@ int vsp_key_filter_f32(const float* z, const float* history, const float* taps, 
  *   the current token and in the halo of later ones) is z_carried's row t where active[b, t] == 0;
  *   z_carried ([B, N, D], z's dtype) and active go together or are both NULL;
  * - writing the next history, the newest K - 1 inputs of (history, the chunk as read) in float32,
- *   into history_out [B, K-1, D] (NULL: not written; it must not overlap history).
+ *   into history_out [B, K-1, D] (NULL: not written; it must not overlap history, or it is history
+ *   itself for a chunk of at most 16 tokens with bf16/fp16 z, 8 with fp32 z: the in-place update
+ *   of a decode step).
  * The rows of z for inactive tokens are never read. */
 int vsp_key_step_bf16(const void* z, const void* z_carried, const uint8_t* active, const float* history,
                       const float* taps, void* keys, float* history_out, int B, int N, int D, int heads, int K,

@@ -374,6 +374,42 @@ def test_the_key_step_writes_the_next_history(dtype, n, width, carry):
     assert torch.equal(keys, fused_keys(merged, history, taps, heads))
 
 
+_IN_PLACE = [(1, 4), (1, 2), (1, 8), (3, 4), (7, 8), (8, 4), (2, 1)]
+
+
+@pytest.mark.parametrize(("dtype", "n", "width"), [(torch.float32, n, w) for n, w in _IN_PLACE]
+                         + [(torch.bfloat16, n, w) for n, w in _IN_PLACE + [(16, 8)]])
+@pytest.mark.parametrize("carry", [False, True])
+def test_the_key_step_updates_a_history_in_place(dtype, n, width, carry):
+    """A decode step's update: the next history written over the history it was computed from
+    equals the out-of-place step's, keys included, bit for bit (chunks up to 8 tokens with float32
+    inputs, 16 with bf16)."""
+    from vesper.kernels.keys import key_step
+
+    b, heads, d = 3, 2, 256
+    g = torch.Generator().manual_seed(n * 100 + width)
+    z = torch.randn(b, n, d, generator=g).to(GPU, dtype)
+    zc = torch.randn(b, n, d, generator=g).to(GPU, dtype)
+    history = torch.randn(b, width - 1, d, generator=g).to(GPU)
+    taps = _taps(d, width).to(GPU)
+    active = (torch.rand(b, n, generator=g) > 0.4).to(GPU) if carry else None
+    want_keys, want_next = key_step(z, history, taps, heads, active=active, carried_z=zc if carry else None)
+    inplace = history.clone()
+    keys, nxt = key_step(z, inplace, taps, heads, active=active, carried_z=zc if carry else None, in_place=True)
+    assert nxt is inplace
+    assert torch.equal(inplace, want_next) and torch.equal(keys, want_keys)
+
+
+def test_an_in_place_history_refuses_a_long_chunk():
+    from vesper.contracts import ContractError
+    from vesper.kernels.keys import key_step
+
+    z = torch.zeros(1, 17, 64, dtype=torch.bfloat16, device=GPU)
+    history = torch.zeros(1, 3, 64, device=GPU)
+    with pytest.raises(ContractError, match="at most 16"):
+        key_step(z, history, _taps(64, 4).to(GPU), 1, in_place=True)
+
+
 # ---- normalize_keys alone, on rows of any width (vsp_normalize_keys_*) ---------------------------
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])

@@ -25,12 +25,12 @@ from collections.abc import Sequence
 import torch
 from torch import Tensor
 
-from vesper.column import recurrent_keys
+from vesper.attention import rotary_qk
 from vesper.contracts import ContractError, Dims, check_shape
 from vesper.kernels.delta_scan import delta_scan_step_fused
-from vesper.kernels.ring_attn import RingKVCache, ring_attention
-from vesper.attention import rotary_qk
+from vesper.kernels.keys import key_step
 from vesper.kernels.norm import decode_projection
+from vesper.kernels.ring_attn import RingKVCache, ring_attention
 from vesper.loop import BF16, LoopedColumn, _normalize
 
 WARM_STEPS = 3  # eager calls before the capture (vesper/graphs.py:99)
@@ -112,9 +112,8 @@ def decode_step(column: LoopedColumn, depth: int, values: Sequence[Tensor],
             z = z.view(b, 1, hd)
             if column.taps is None:
                 k = _normalize(z, h)
-            else:
-                k, nxt = recurrent_keys(z, history, column.taps[t], h)
-                history.copy_(nxt)
+            else:  # the key history updated in place by the filter's launch
+                k, _ = key_step(z, history, column.taps[t], h, in_place=True)
             o, _ = delta_scan_step_fused(q[:, 0], k[:, 0], v.view(b, h, dk), beta, state, out_state=state)
             x1 = torch.empty_like(xs)
             aq, ak, av = decode_projection(xs, w_attn, (hd, hkv * dk, hkv * dk), residual=o.reshape(b, hd),

@@ -29,10 +29,10 @@ namespace {
 // come from the history. A row's source is wave-uniform (all lanes of a wave hold one token), so
 // both are loaded, the unused one from past its range, and joined bitwise.
 template <typename TZ, int K, int LPH, bool CARRY>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))) void key_filter_kernel(const TZ* __restrict__ z, const float* __restrict__ history,
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))) void key_filter_kernel(const TZ* __restrict__ z, const float* history,
                                                          const float* __restrict__ taps, TZ* __restrict__ out,
                                                          const uint8_t* __restrict__ active, const TZ* zc,
-                                                         float* __restrict__ hist_out, int N, int D) {
+                                                         float* hist_out, int N, int D) {
   using Row = Row8<TZ>;
   constexpr int RUN = Row::kRun;
   static_assert(RUN >= K - 1, "a run is at least as long as the filter's history");
@@ -93,21 +93,27 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))) voi
 #pragma unroll
       for (int e = 0; e < 8; ++e) win[r - 1][e] = __uint_as_float(__float_as_uint(zr[e]) | __float_as_uint(hr[e]));
     }
+    // The next history may be the history itself (a chunk within one run: then this wave alone
+    // reads and writes these features of the batch row); its rows were all read into win above, so
+    // every load has to land before the first store.
+    if (hist_out == history && hist_out != nullptr) {
+      __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+      asm volatile("" ::: "memory");
+    }
     // The next history (the newest K - 1 inputs of history and chunk): a chunk shorter than K - 1
-    // keeps the history's rows N .. K - 2 first, copied here by the run at the chunk's start (the
-    // history is the kernel's input and hist_out never overlaps it); the chunk's own rows follow
-    // from the run loop below.
+    // keeps the history's rows N .. K - 2 first, written here from win (win[r - 1] holds history
+    // row K - 1 - r in the chunk's first run) by the run at the chunk's start; the chunk's own rows
+    // follow from the run loop below.
     if (hist_out != nullptr && first && N < K - 1 && on) {
-      const float* src = history + (size_t)b * (K - 1) * D + f0;
       float* dst = hist_out + (size_t)b * (K - 1) * D + f0;
 #pragma unroll
-      for (int r = 0; r < K - 1; ++r)
-        if (r < K - 1 - N) {
-          const f32x4 a = *reinterpret_cast<const f32x4*>(src + (size_t)(N + r) * D);
-          const f32x4 c = *reinterpret_cast<const f32x4*>(src + (size_t)(N + r) * D + 4);
-          *reinterpret_cast<f32x4*>(dst + (size_t)r * D) = a;
-          *reinterpret_cast<f32x4*>(dst + (size_t)r * D + 4) = c;
+      for (int i = 0; i < K - 1; ++i) {
+        const int r = K - 2 - i - N;  // history row K - 2 - i lands in row r of the next one
+        if (r >= 0) {
+          *reinterpret_cast<f32x4*>(dst + (size_t)r * D) = f32x4{win[i][0], win[i][1], win[i][2], win[i][3]};
+          *reinterpret_cast<f32x4*>(dst + (size_t)r * D + 4) = f32x4{win[i][4], win[i][5], win[i][6], win[i][7]};
         }
+      }
     }
   }
   typename Row::Raw raw[RUN];  // rows past N (a short last run) re-read row N - 1
@@ -228,7 +234,10 @@ int key_filter(const TZ* z, const float* history, const float* taps, TZ* out, in
     const size_t bytes = (size_t)B * (K - 1) * D * sizeof(float);
     const uintptr_t o = reinterpret_cast<uintptr_t>(hist_out), h0 = reinterpret_cast<uintptr_t>(history);
     if (o & 15) return fail(ERR_ARG, "%s: the next history must be 16-byte aligned", who);
-    if (o < h0 + bytes && h0 < o + bytes) return fail(ERR_ARG, "%s: the next history overlaps the history", who);
+    // in place only where one run holds a batch row's tokens (one wave reads and writes each feature)
+    if (o == h0 ? N > Row8<TZ>::kRun : (o < h0 + bytes && h0 < o + bytes))
+      return fail(ERR_ARG, "%s: the next history overlaps the history (in place: at most %d tokens)", who,
+                  Row8<TZ>::kRun);
   }
   hipStream_t stream = reinterpret_cast<hipStream_t>(stream_ptr);
   switch (K) {

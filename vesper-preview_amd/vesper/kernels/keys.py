@@ -110,15 +110,18 @@ class _FusedKeys(torch.autograd.Function):
 
 
 def _key_step(z: Tensor, history: Tensor, taps: Tensor, heads: int, active: Tensor | None,
-              carried_z: Tensor | None, want_history: bool) -> tuple[Tensor, Tensor | None]:
+              carried_z: Tensor | None, want_history: bool, in_place: bool = False) -> tuple[Tensor, Tensor | None]:
     b, n, d, width = _check(z, history, taps, heads)
     zc = _aligned(z)
     held = None if carried_z is None else _aligned(carried_z)
     flags = None if carried_z is None or active is None else active.contiguous().view(torch.uint8)
-    hist = _aligned(history.to(torch.float32))
+    hist = history if in_place else _aligned(history.to(torch.float32))
     wide = _aligned(taps.to(torch.float32))
     out = torch.empty(b, n, heads, d // heads, dtype=z.dtype, device=z.device)
-    nxt = torch.empty(b, width - 1, d, dtype=torch.float32, device=z.device) if want_history else None
+    if in_place:
+        nxt = history
+    else:
+        nxt = torch.empty(b, width - 1, d, dtype=torch.float32, device=z.device) if want_history else None
     if b and n:
         _lib.call(f"vsp_key_step_{_SUFFIX[z.dtype]}", _lib.ptr(zc), _lib.ptr(held), _lib.ptr(flags),
                   _lib.ptr(hist) if width > 1 else None, _lib.ptr(wide), _lib.ptr(out),
@@ -138,24 +141,33 @@ def _check_carried(z: Tensor, active: Tensor | None, carried_z: Tensor) -> None:
 
 
 def key_step(z: Tensor, history: Tensor, taps: Tensor, heads: int, *, active: Tensor | None = None,
-             carried_z: Tensor | None = None) -> tuple[Tensor, Tensor]:
+             carried_z: Tensor | None = None, in_place: bool = False) -> tuple[Tensor, Tensor]:
     """The keys and the next key history of key inputs ``z [b, n, d]``, no gradient.
 
     As ``fused_keys`` for the keys; the next history is the newest ``K - 1`` inputs of ``(history,
     z)`` (with ``carried_z``, the carried rows of inactive tokens) as a new float32 ``[b, K-1, d]``
-    tensor, written by the same launch. An empty chunk (``n == 0``) returns empty keys and the
-    history unchanged, as ``RecurrentSublayer.keys`` does (``column.py:275-277``).
+    tensor, written by the same launch; with ``in_place`` it is written into ``history`` itself
+    (a contiguous float32 tensor) and that tensor returned: a decode step's update, for chunks of
+    at most 16 tokens (8 with float32 ``z``). An empty chunk (``n == 0``) returns empty keys and
+    the history unchanged, as ``RecurrentSublayer.keys`` does (``column.py:275-277``).
 
     Raises:
-        ContractError: as ``fused_keys``.
+        ContractError: as ``fused_keys``; ``in_place`` with a history that is not contiguous
+            float32 or a chunk longer than that.
     """
     _check(z, history, taps, heads)
+    if in_place:
+        limit = 8 if z.dtype == torch.float32 else 16
+        if history.dtype != torch.float32 or not history.is_contiguous() or history.data_ptr() % 16:
+            raise ContractError("an in-place history must be a contiguous, 16-byte aligned float32 tensor")
+        if z.shape[1] > limit:
+            raise ContractError(f"an in-place history takes chunks of at most {limit} tokens, got {z.shape[1]}")
     if carried_z is not None:
         _check_carried(z, active, carried_z)
     if z.shape[1] == 0:
         b, _, d = z.shape
         return z.new_empty(b, 0, heads, d // heads), history
-    keys, nxt = _key_step(z, history, taps, heads, active, carried_z, want_history=True)
+    keys, nxt = _key_step(z, history, taps, heads, active, carried_z, want_history=True, in_place=in_place)
     assert nxt is not None
     return keys, nxt
 
