@@ -22,7 +22,7 @@
 extern "C" {
 #endif
 
-#define VSP_ABI_VERSION 14
+#define VSP_ABI_VERSION 15
 
 /* Status codes. */
 #define VSP_OK 0
@@ -401,10 +401,15 @@ int vsp_rms_norm_bf16(const float* x, const float* gain, void* out, int rows, in
  * block's weight passed transposed: weights_t [nblk, cols, d] bf16. Block sigmoid_block (or -1 for
  * none) is stored as the logistic of its bf16-rounded product (the write strength). d a multiple
  * of 32 in 32..2048; 1 <= used_j <= cols; x, residual, sum_out, gain and weights_t 16-byte
- * aligned, the outputs 4-byte aligned. */
+ * aligned, the outputs 4-byte aligned. Blocks j with bit j of rotate_mask set are rotated as they
+ * are stored, as vsp_rotary_qk_bf16 rotates them (heads of rotary_dk columns, token m at
+ * positions[m] (int64 [M]), inv_freq the float64 [rotary_dk / 2] table): bitwise the separate
+ * launch's q and k; used_j a multiple of rotary_dk. */
 int vsp_decode_proj_bf16(const float* x, const void* residual, float* sum_out, const float* gain,
                          const void* weights_t, int nblk, int cols, int d, int M, int used0, int used1, int used2,
-                         int used3, void* out0, void* out1, void* out2, void* out3, int sigmoid_block, void* stream);
+                         int used3, void* out0, void* out1, void* out2, void* out3, int sigmoid_block,
+                         const int64_t* positions, const double* inv_freq, int rotate_mask, int rotary_dk,
+                         void* stream);
 
 /* ---- copy-forward bookkeeping of the looped column ------------------------------------------
  * Replaces the row-wise `where` selects of vesper/loop.py:523-537 (`_merge`: tokens halting now

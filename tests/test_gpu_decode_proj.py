@@ -97,3 +97,25 @@ def test_refusals():
         decode_projection(x, wt, (32, 33))
     with pytest.raises(ContractError, match="must not be x"):
         decode_projection(x, wt, (32, 32), residual=torch.zeros(4, 64, dtype=BF16, device=GPU), sum_out=x)
+
+
+@pytest.mark.parametrize(("m", "h", "hkv", "dk"), [(64, 8, 8, 64), (5, 4, 2, 32), (17, 2, 1, 128)])
+def test_rotation_as_stored_equals_the_rotary_launch_bitwise(m, h, hkv, dk):
+    """q and k rotated by the projection's stores equal the projection then rotary_qk, bit for bit
+    (the rotary kernel is pinned against the reference's scalar-trig pairs)."""
+    from vesper.attention import rotary_inv_freq, rotary_qk
+    from vesper.kernels.norm import decode_projection
+
+    g = torch.Generator().manual_seed(m + dk)
+    d, cols = 256, h * dk
+    x = torch.randn(m, d, generator=g).to(GPU)
+    w = (torch.randn(3, d, cols, generator=g) / d ** 0.5).to(BF16).to(GPU)
+    wt = w.transpose(1, 2).contiguous()
+    used = (h * dk, hkv * dk, hkv * dk)
+    pos = torch.randint(0, 100_000, (m,), generator=g).to(GPU)
+    plain = decode_projection(x, wt, used)
+    rot = decode_projection(x, wt, used, rotary=(pos, rotary_inv_freq(10000.0, dk, GPU), dk, (0, 1)))
+    want_q, want_k = rotary_qk(plain[0].view(m, 1, h, dk), plain[1].view(m, 1, hkv, dk), pos.view(m, 1), 10000.0)
+    assert torch.equal(rot[0].view(m, 1, h, dk), want_q)
+    assert torch.equal(rot[1].view(m, 1, hkv, dk), want_k)
+    assert torch.equal(rot[2], plain[2])

@@ -115,6 +115,11 @@ def _inv_freq(base: float, dk: int, device: torch.device) -> Tensor:
     return table
 
 
+def rotary_inv_freq(base: float, dk: int, device: torch.device) -> Tensor:
+    """The float64 table ``base^(-2j/dk)`` the rotary kernels read (``attention.py:211-212``)."""
+    return _inv_freq(base, dk, device)
+
+
 def _check_rotary(x: Tensor, pos: Tensor, base: float, name: str = "x") -> int:
     dims: Dims = {}
     check_shape(name, x, ("b", "n", "heads", "dk"), dims)

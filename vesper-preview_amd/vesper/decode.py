@@ -25,7 +25,7 @@ from collections.abc import Sequence
 import torch
 from torch import Tensor
 
-from vesper.attention import rotary_qk
+from vesper.attention import rotary_inv_freq
 from vesper.contracts import ContractError, Dims, check_shape
 from vesper.kernels.delta_scan import delta_scan_step_fused
 from vesper.kernels.keys import key_step
@@ -98,6 +98,9 @@ def decode_step(column: LoopedColumn, depth: int, values: Sequence[Tensor],
         # output to it, normalizes and projects in one launch (vsp_decode_proj_bf16)
         xs = x.reshape(b, d)
         pending = None  # the previous pass's attention output, added by the next projection
+        rotary = None
+        if column.rotary_base is not None:
+            rotary = (position.reshape(b), rotary_inv_freq(column.rotary_base, dk, x.device), dk, (0, 1))
         for t in range(depth):
             state, history, rk, rv, rp, rvalid = flat[PER_PASS * t: PER_PASS * (t + 1)]
             w_rec, w_attn = column.decode_weights(t)
@@ -117,11 +120,9 @@ def decode_step(column: LoopedColumn, depth: int, values: Sequence[Tensor],
             o, _ = delta_scan_step_fused(q[:, 0], k[:, 0], v.view(b, h, dk), beta, state, out_state=state)
             x1 = torch.empty_like(xs)
             aq, ak, av = decode_projection(xs, w_attn, (hd, hkv * dk, hkv * dk), residual=o.reshape(b, hd),
-                                           sum_out=x1)
+                                           sum_out=x1, rotary=rotary)  # q and k rotated as stored
             xs = x1
             aq, ak = aq.view(b, 1, h, dk), ak.view(b, 1, hkv, dk)
-            if column.rotary_base is not None:
-                aq, ak = rotary_qk(aq, ak, position, column.rotary_base)
             ring = RingKVCache(rk, rv, rp, rvalid, column.window)
             a, _ = ring_attention(aq, ak, av.view(b, 1, hkv, dk), position, ring, inplace=True, check_positions=False,
                                   workspace=workspace)

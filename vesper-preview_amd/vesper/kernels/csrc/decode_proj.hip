@@ -18,8 +18,11 @@
 // partial tiles are summed in a fixed order through LDS. A block whose used width is narrow (the
 // write strength's h columns) takes one column group. One block may have its outputs passed
 // through the logistic function (the write strength, rounded to bf16 first as the separate
-// sigmoid would see it).
+// sigmoid would see it), and blocks may be rotated as they are stored (the attention's q and k:
+// a thread stores two adjacent columns of one token, a rotary pair, turned by the rotary kernel's
+// own arithmetic, so the result is bitwise the separate launch's).
 #include "common.h"
+#include "rotary_math.h"
 #include "vesper_kernels.h"
 
 namespace vsp {
@@ -40,7 +43,10 @@ template <int NSEG>
 __global__ __launch_bounds__(256) void decode_proj_kernel(const float* __restrict__ x, const __bf16* __restrict__ res,
                                                           float* __restrict__ sum_out, const float* __restrict__ gain,
                                                           const __bf16* __restrict__ wt, int M, int d, int cols,
-                                                          ProjBlocks blk, int sig_block) {
+                                                          ProjBlocks blk, int sig_block,
+                                                          const int64_t* __restrict__ pos,
+                                                          const double* __restrict__ inv_freq, int rot_mask,
+                                                          int rot_dk) {
   constexpr int PITCH = 512 * NSEG + 16;  // bf16 elements a row of z: rows 8 banks apart
   constexpr int KSMAX = NSEG * 4;         // k steps of 32 a wave takes, at most
   __shared__ __align__(16) __bf16 sz[16][PITCH];
@@ -168,6 +174,10 @@ __global__ __launch_bounds__(256) void decode_proj_kernel(const float* __restric
       b0 = (__bf16)(1.f / (1.f + expf(-(float)b0)));
       b1 = (__bf16)(1.f / (1.f + expf(-(float)b1)));
     }
+    if ((rot_mask >> nb) & 1) {  // columns col, col + 1: pair (col % dk) / 2 of a head
+      const double angle = (double)pos[m] * inv_freq[(col % rot_dk) >> 1];
+      rot_pair<__bf16>(b0, b1, rot_from_f64<__bf16>(cos(angle)), rot_from_f64<__bf16>(sin(angle)), b0, b1);
+    }
     __bf16* orow = blk.out[nb] + (size_t)m * used;
     orow[col] = b0;
     if (col + 1 < used) orow[col + 1] = b1;
@@ -180,13 +190,21 @@ __global__ __launch_bounds__(256) void decode_proj_kernel(const float* __restric
 extern "C" int vsp_decode_proj_bf16(const float* x, const void* residual, float* sum_out, const float* gain,
                                     const void* weights_t, int nblk, int cols, int d, int M, int used0, int used1,
                                     int used2, int used3, void* out0, void* out1, void* out2, void* out3,
-                                    int sigmoid_block, void* stream) {
+                                    int sigmoid_block, const int64_t* positions, const double* inv_freq,
+                                    int rotate_mask, int rotary_dk, void* stream) {
   using namespace vsp;
   const char* who = "vsp_decode_proj_bf16";
   if (nblk < 1 || nblk > kMaxBlocks) return fail(ERR_ARG, "%s: %d weight blocks (1..%d)", who, nblk, kMaxBlocks);
   if (d < 32 || d > 2048 || d % 32 != 0) return fail(ERR_ARG, "%s: width %d (a multiple of 32 in 32..2048)", who, d);
   if (M < 0 || cols < 1) return fail(ERR_ARG, "%s: bad sizes M=%d cols=%d", who, M, cols);
   if (sigmoid_block < -1 || sigmoid_block >= nblk) return fail(ERR_ARG, "%s: sigmoid block %d", who, sigmoid_block);
+  if (rotate_mask < 0 || rotate_mask >= (1 << nblk)) return fail(ERR_ARG, "%s: rotate mask %d", who, rotate_mask);
+  if (rotate_mask != 0) {
+    if (!positions || !inv_freq) return fail(ERR_ARG, "%s: rotation without positions or frequencies", who);
+    if (rotary_dk < 2 || rotary_dk % 2 != 0) return fail(ERR_ARG, "%s: rotary head width %d", who, rotary_dk);
+    if (sigmoid_block >= 0 && ((rotate_mask >> sigmoid_block) & 1))
+      return fail(ERR_ARG, "%s: block %d both rotated and passed through the logistic", who, sigmoid_block);
+  }
   const int used_in[kMaxBlocks] = {used0, used1, used2, used3};
   void* out_in[kMaxBlocks] = {out0, out1, out2, out3};
   ProjBlocks blk{};
@@ -199,6 +217,8 @@ extern "C" int vsp_decode_proj_bf16(const float* x, const void* residual, float*
       return fail(ERR_ARG, "%s: block %d uses %d of its %d columns", who, j, used_in[j], cols);
     if (out_in[j] == nullptr) return fail(ERR_ARG, "%s: null output for block %d", who, j);
     if (reinterpret_cast<uintptr_t>(out_in[j]) & 3) return fail(ERR_ARG, "%s: output %d must be 4-byte aligned", who, j);
+    if (((rotate_mask >> j) & 1) && used_in[j] % rotary_dk != 0)
+      return fail(ERR_ARG, "%s: rotated block %d's %d columns are not whole heads of %d", who, j, used_in[j], rotary_dk);
     blk.used[j] = used_in[j];
     blk.out[j] = static_cast<__bf16*>(out_in[j]);
     groups += (used_in[j] + 31) / 32;
@@ -214,10 +234,13 @@ extern "C" int vsp_decode_proj_bf16(const float* x, const void* residual, float*
   const __bf16* r = static_cast<const __bf16*>(residual);
   const __bf16* w = static_cast<const __bf16*>(weights_t);
   if (d <= 512)
-    hipLaunchKernelGGL(decode_proj_kernel<1>, grid, dim3(256), 0, s, x, r, sum_out, gain, w, M, d, cols, blk, sigmoid_block);
+    hipLaunchKernelGGL(decode_proj_kernel<1>, grid, dim3(256), 0, s, x, r, sum_out, gain, w, M, d, cols, blk, sigmoid_block,
+                       positions, inv_freq, rotate_mask, rotary_dk);
   else if (d <= 1024)
-    hipLaunchKernelGGL(decode_proj_kernel<2>, grid, dim3(256), 0, s, x, r, sum_out, gain, w, M, d, cols, blk, sigmoid_block);
+    hipLaunchKernelGGL(decode_proj_kernel<2>, grid, dim3(256), 0, s, x, r, sum_out, gain, w, M, d, cols, blk, sigmoid_block,
+                       positions, inv_freq, rotate_mask, rotary_dk);
   else
-    hipLaunchKernelGGL(decode_proj_kernel<4>, grid, dim3(256), 0, s, x, r, sum_out, gain, w, M, d, cols, blk, sigmoid_block);
+    hipLaunchKernelGGL(decode_proj_kernel<4>, grid, dim3(256), 0, s, x, r, sum_out, gain, w, M, d, cols, blk, sigmoid_block,
+                       positions, inv_freq, rotate_mask, rotary_dk);
   return check_launch(who);
 }

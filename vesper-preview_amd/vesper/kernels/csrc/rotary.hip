@@ -13,6 +13,7 @@
 // consecutive pairs, four pieces' loads issued before their arithmetic. q and k may be rotated in
 // place (each element is read and written by one thread).
 #include "common.h"
+#include "rotary_math.h"
 #include "vesper_kernels.h"
 
 namespace vsp {
@@ -22,33 +23,15 @@ template <typename T> struct Pair {
   typedef T P2 __attribute__((ext_vector_type(2)));
 };
 
-// x1 c - x2 s and x1 s + x2 c with every operation rounded to T (no contraction into FMAs)
+// the pair x turned (rot_pair) and stored at dst
 template <typename T>
 __device__ __forceinline__ void turn(typename Pair<T>::P2 x, T* dst, T c, T s) {
-#pragma clang fp contract(off)
-  typedef typename Pair<T>::P2 P2;
-  const float x1 = to_f32(x[0]), x2 = to_f32(x[1]), cf = to_f32(c), sf = to_f32(s);
-  const float a = to_f32(from_f32<T>(x1 * cf)), b = to_f32(from_f32<T>(x2 * sf));
-  const float e = to_f32(from_f32<T>(x1 * sf)), f = to_f32(from_f32<T>(x2 * cf));
-  P2 y;
-  y[0] = from_f32<T>(a - b);
-  y[1] = from_f32<T>(e + f);
-  *reinterpret_cast<P2*>(dst) = y;
-}
-
-// double to T through float, as torch casts a float64 tensor to a 16-bit one (two roundings). The
-// float is pinned in a register first: otherwise the two conversions are folded into one direct
-// (singly rounded) double-to-half conversion, which differs where the float lands exactly on a
-// half-way point between two 16-bit values.
-template <typename T>
-__device__ __forceinline__ T from_f64(double v) {
-  float f = (float)v;
-  if constexpr (sizeof(T) == 4) {
-    return f;
-  } else {
-    asm volatile("" : "+v"(f));
-    return (T)f;
-  }
+  typename Pair<T>::P2 y;
+  T y1, y2;
+  rot_pair<T>(x[0], x[1], c, s, y1, y2);
+  y[0] = y1;
+  y[1] = y2;
+  *reinterpret_cast<typename Pair<T>::P2*>(dst) = y;
 }
 
 constexpr int kRotRows = 4;  // token rows a workgroup
@@ -63,8 +46,8 @@ __global__ __launch_bounds__(256) void rotary_qk_kernel(const T* q, const T* k, 
   for (int e = threadIdx.x; e < nrows * half; e += 256) {
     const int r = e / half, j = e - r * half;
     const double angle = (double)pos[row0 + r] * inv_freq[j];
-    cs[r][j] = from_f64<T>(cos(angle));
-    sn[r][j] = from_f64<T>(sin(angle));
+    cs[r][j] = rot_from_f64<T>(cos(angle));
+    sn[r][j] = rot_from_f64<T>(sin(angle));
   }
   __syncthreads();
   // piece t: row r = t / (heads * half), head hh, pair j (heads: the H query heads, then the HKV

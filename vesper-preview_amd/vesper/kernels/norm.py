@@ -50,7 +50,8 @@ def rms_norm_bf16(x: Tensor, gain: Tensor | None = None) -> Tensor:
 
 def decode_projection(x: Tensor, weights_t: Tensor, used: tuple[int, ...], *, residual: Tensor | None = None,
                       sum_out: Tensor | None = None, gain: Tensor | None = None,
-                      sigmoid_block: int | None = None) -> list[Tensor]:
+                      sigmoid_block: int | None = None,
+                      rotary: tuple[Tensor, Tensor, int, tuple[int, ...]] | None = None) -> list[Tensor]:
     """A decode step's sublayer projections in one launch (``vsp_decode_proj_bf16``): the residual
     sum ``s = x + residual`` (written into ``sum_out`` when given), ``z = RMSNorm(s, gain)`` in
     bfloat16 exactly as ``rms_norm_bf16`` computes it, and ``z W_j[:, :used_j]`` for each block of
@@ -64,6 +65,10 @@ def decode_projection(x: Tensor, weights_t: Tensor, used: tuple[int, ...], *, re
         sum_out: optional float32 ``[M, d]`` that receives ``s`` (not ``x`` itself).
         gain: optional float32 ``[d]`` (the norm's weight; ones when omitted).
         sigmoid_block: the block whose outputs pass through the logistic function (the write strength).
+        rotary: ``(positions, inv_freq, dk, blocks)``: the blocks rotated as they are stored, as
+            ``rotary_qk`` rotates queries and keys (heads of ``dk`` columns, token ``m`` at
+            ``positions[m]`` int64 ``[M]``, ``inv_freq`` the float64 ``[dk / 2]`` table), bitwise
+            the separate launch's result.
 
     Returns:
         one bf16 ``[M, used_j]`` tensor per block.
@@ -101,6 +106,18 @@ def decode_projection(x: Tensor, weights_t: Tensor, used: tuple[int, ...], *, re
             raise ContractError(f"{name} is on {t.device}, x on {x.device}")
     if sigmoid_block is not None and not 0 <= sigmoid_block < p:
         raise ContractError(f"sigmoid_block {sigmoid_block} is not one of the {p} blocks")
+    rot_pos, rot_freq, rot_dk, rot_mask = None, None, 0, 0
+    if rotary is not None:
+        rot_pos, rot_freq, rot_dk, blocks = rotary
+        if rot_pos.shape != (m,) or rot_pos.dtype != torch.long or rot_pos.device != x.device:
+            raise ContractError(f"rotary positions: int64 [{m}] on {x.device}, got {tuple(rot_pos.shape)} {rot_pos.dtype}")
+        if rot_freq.shape != (rot_dk // 2,) or rot_freq.dtype != torch.float64 or rot_freq.device != x.device:
+            raise ContractError(f"rotary frequencies: float64 [{rot_dk // 2}] on {x.device}")
+        for j in blocks:
+            if not 0 <= j < p or used[j] % rot_dk or j == sigmoid_block:
+                raise ContractError(f"block {j} cannot be rotated in heads of {rot_dk}")
+            rot_mask |= 1 << j
+        rot_pos, rot_freq = rot_pos.contiguous(), rot_freq.contiguous()
     xc, wc = x.contiguous(), weights_t.contiguous()
     rc = None if residual is None else residual.contiguous()
     gc = None if gain is None else gain.contiguous()
@@ -113,5 +130,5 @@ def decode_projection(x: Tensor, weights_t: Tensor, used: tuple[int, ...], *, re
     with torch.cuda.device(x.device):
         _lib.call("vsp_decode_proj_bf16", xc.data_ptr(), _lib.ptr(rc), _lib.ptr(sum_out), _lib.ptr(gc), wc.data_ptr(),
                   p, cols, d, m, *widths, *ptrs, -1 if sigmoid_block is None else sigmoid_block,
-                  _lib.stream_of(x.device))
+                  _lib.ptr(rot_pos), _lib.ptr(rot_freq), rot_mask, rot_dk, _lib.stream_of(x.device))
     return outs
