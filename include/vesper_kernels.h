@@ -22,7 +22,7 @@
 extern "C" {
 #endif
 
-#define VSP_ABI_VERSION 15
+#define VSP_ABI_VERSION 16
 
 /* Status codes. */
 #define VSP_OK 0
@@ -153,6 +153,18 @@ int vsp_delta_step_f32(const float* q, const float* k, const float* v, const flo
                        float* state_out, float* o, const uint8_t* active, int B, int H, int D, void* stream);
 int vsp_delta_step_bf16(const void* q, const void* k, const void* v, const void* beta, const float* state_in,
                         float* state_out, void* o, const uint8_t* active, int B, int H, int D, void* stream);
+
+/* The decode step's key filter folded into the bf16 step (the looped column's per-pass decode:
+ * vesper/column.py:255-289 for the key, vesper/recurrence.py:118-163 for the step): the key of each
+ * (b, h) is formed from the key inputs z [B, H*D] bf16 with the K filter taps (taps [K, H*D]
+ * float32, tap 0 on the token) over the history (history [B, K-1, H*D] float32, oldest first;
+ * NULL when K = 1) and normalized per head, exactly as vsp_key_step_bf16 forms and rounds it, and
+ * the next history is written over the history; then the step as vsp_delta_step_bf16 with that
+ * key. Bitwise the two launches' results. D in {16, 32, 64, 128}, K in 1..8; z, taps, history and
+ * the states 16-byte aligned; state_out may be state_in. */
+int vsp_delta_step_keys_bf16(const void* q, const void* z, const void* v, const void* beta, float* history,
+                             const float* taps, int K, const float* state_in, float* state_out, void* o,
+                             const uint8_t* active, int B, int H, int D, void* stream);
 
 /* The scan's backward (the gradients fla-core's chunk kernels give vesper/kernels/delta_scan.py:132-187
  * under autograd): from d_o [B, N, H, D] (the inputs' dtype) and d_state [B, H, D, D] fp32 (the

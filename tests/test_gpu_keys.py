@@ -410,6 +410,31 @@ def test_an_in_place_history_refuses_a_long_chunk():
         key_step(z, history, _taps(64, 4).to(GPU), 1, in_place=True)
 
 
+@pytest.mark.parametrize("dk", [16, 32, 64, 128])
+@pytest.mark.parametrize("width", [1, 2, 4, 8])
+@pytest.mark.parametrize("inactive", [False, True])
+def test_the_key_filter_inside_the_delta_step_equals_the_two_launches(dk, width, inactive):
+    """vsp_delta_step_keys_bf16: the decode step's key formed inside the delta step's launch gives
+    the key step's history and the delta step's output and state bit for bit."""
+    from vesper.kernels.delta_scan import delta_scan_step_fused, delta_scan_step_keys
+    from vesper.kernels.keys import key_step
+
+    b, h = 3, 4
+    g = torch.Generator().manual_seed(dk * 10 + width)
+    q, v = (torch.randn(b, h, dk, generator=g).to(torch.bfloat16).to(GPU) for _ in range(2))
+    z = torch.randn(b, 1, h * dk, generator=g).to(torch.bfloat16).to(GPU)
+    beta = torch.rand(b, h, generator=g).to(torch.bfloat16).to(GPU)
+    history = torch.randn(b, width - 1, h * dk, generator=g).to(GPU)
+    taps = _taps(h * dk, width).to(GPU)
+    state = (0.1 * torch.randn(b, h, dk, dk, generator=g)).to(GPU)
+    active = torch.tensor([True, False, True], device=GPU) if inactive else None
+    keys, want_hist = key_step(z, history, taps, h)
+    want_o, want_state = delta_scan_step_fused(q, keys[:, 0], v, beta, state, active=active)
+    hist, st = history.clone(), state.clone()
+    o = delta_scan_step_keys(q, z[:, 0], v, beta, hist, taps, st, active=active)
+    assert torch.equal(o, want_o) and torch.equal(st, want_state) and torch.equal(hist, want_hist)
+
+
 # ---- normalize_keys alone, on rows of any width (vsp_normalize_keys_*) ---------------------------
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])

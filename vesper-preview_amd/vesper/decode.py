@@ -27,8 +27,7 @@ from torch import Tensor
 
 from vesper.attention import rotary_inv_freq
 from vesper.contracts import ContractError, Dims, check_shape
-from vesper.kernels.delta_scan import delta_scan_step_fused
-from vesper.kernels.keys import key_step
+from vesper.kernels.delta_scan import delta_scan_step_fused, delta_scan_step_keys
 from vesper.kernels.norm import decode_projection
 from vesper.kernels.ring_attn import RingKVCache, ring_attention
 from vesper.loop import BF16, LoopedColumn, _normalize
@@ -111,13 +110,12 @@ def decode_step(column: LoopedColumn, depth: int, values: Sequence[Tensor],
                 q_in, z, v, beta = decode_projection(xs, w_rec, (hd, hd, hd, h), residual=pending, sum_out=nxt_x,
                                                      sigmoid_block=3)
                 xs = nxt_x
-            q = q_in.view(b, 1, h, dk)  # the scan's query is not normalized (column.py:247)
-            z = z.view(b, 1, hd)
+            q = q_in.view(b, h, dk)  # the scan's query is not normalized (column.py:247)
             if column.taps is None:
-                k = _normalize(z, h)
-            else:  # the key history updated in place by the filter's launch
-                k, _ = key_step(z, history, column.taps[t], h, in_place=True)
-            o, _ = delta_scan_step_fused(q[:, 0], k[:, 0], v.view(b, h, dk), beta, state, out_state=state)
+                k = _normalize(z.view(b, 1, hd), h)
+                o, _ = delta_scan_step_fused(q, k[:, 0], v.view(b, h, dk), beta, state, out_state=state)
+            else:  # the key filter inside the step's launch, the history updated in place
+                o = delta_scan_step_keys(q, z, v.view(b, h, dk), beta, history, column.taps[t], state)
             x1 = torch.empty_like(xs)
             aq, ak, av = decode_projection(xs, w_attn, (hd, hkv * dk, hkv * dk), residual=o.reshape(b, hd),
                                            sum_out=x1, rotary=rotary)  # q and k rotated as stored

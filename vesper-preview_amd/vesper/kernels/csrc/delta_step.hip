@@ -11,7 +11,17 @@
 // loads are issued before any arithmetic, so a workgroup has its whole 16 KiB row block in flight
 // at once. The column sums over row groups reduce with lane shuffles inside a wave and through LDS
 // across waves, in a fixed order (bitwise repeatable).
+//
+// With a key filter of K taps (the decode step's key, vsp_delta_step_keys_bf16) the workgroup
+// forms its head's key itself before the step: the first wave filters the head's key inputs z
+// with the taps over the key history and normalizes the result (vesper/column.py:255-289 with
+// vesper/recurrence.py:91-115), with the key filter kernel's arithmetic (the same order of terms,
+// the same reductions over D/8-lane groups, the key rounded to bf16 as that kernel stores it), so
+// the step is bitwise the two launches'; it writes the next history over the history (its own
+// head's features, read into registers first). The state's loads are issued before, so the
+// filter runs while they arrive.
 #include "common.h"
+#include "keys_rows.h"
 #include "vesper_kernels.h"
 
 namespace vsp {
@@ -25,14 +35,18 @@ template <int D> struct StepShape {
   static constexpr int NW = NT / 64;                             // waves
 };
 
-template <typename TIn, int D>
+template <typename TIn, int D, int K = 0>
 __global__ __launch_bounds__(StepShape<D>::NT) void delta_step_kernel(
     const TIn* __restrict__ q, const TIn* __restrict__ k, const TIn* __restrict__ v, const TIn* __restrict__ beta,
-    const float* s_in, float* s_out, TIn* __restrict__ o, const uint8_t* __restrict__ active, int H) {
-  // s_in and s_out may alias (an in-place step): each thread writes exactly the elements it read
+    const float* s_in, float* s_out, TIn* __restrict__ o, const uint8_t* __restrict__ active, int H,
+    float* history = nullptr, const float* __restrict__ taps = nullptr) {
+  // s_in and s_out may alias (an in-place step): each thread writes exactly the elements it read.
+  // K > 0: k holds the key inputs z [B, H * D] and the key is filtered here (history [B, K-1, H*D],
+  // taps [K, H*D], both float32).
   using S = StepShape<D>;
   constexpr int CPR = S::CPR, RG = S::RG, RPT = S::RPT, NW = S::NW;
   __shared__ float red[NW][3][D];
+  __shared__ float skey[K > 0 ? D : 1];
 
   const int bh = blockIdx.x;
   const int t = threadIdx.x, lane = t & 63, wv = t >> 6;
@@ -42,12 +56,67 @@ __global__ __launch_bounds__(StepShape<D>::NT) void delta_step_kernel(
   float4 st[RPT];
 #pragma unroll
   for (int j = 0; j < RPT; ++j) st[j] = reinterpret_cast<const float4*>(s_in + base + (size_t)(rg + RG * j) * D)[cb];
+  if constexpr (K > 0) {
+    // the first wave forms the key: lane l takes features 8 (l % LPH) .. + 7 of the head (the lanes
+    // past LPH repeat a group; only the first group stores)
+    constexpr int LPH = D / 8;
+    if (t < 64) {
+      const int fc = t % LPH, b = bh / H, DT = H * D;
+      const size_t fo = (size_t)(bh - b * H) * D + 8 * fc;
+      float cur[8], tp[K][8], win[K > 1 ? K - 1 : 1][8];
+      load8_f32(k + (size_t)b * DT + fo, cur);
+#pragma unroll
+      for (int r = 0; r < K; ++r) load8_f32(taps + (size_t)r * DT + fo, tp[r]);
+      float* hb = history + (size_t)b * (K - 1) * DT + fo;
+#pragma unroll
+      for (int r = 1; r < K; ++r) load8_f32(hb + (size_t)(K - 1 - r) * DT, win[r - 1]);  // input t - r
+      // the filter in the reference's order: taps[0] z[t], then + taps[r] z[t - r] for r = 1, 2, ...
+      float u[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        float acc = tp[0][e] * cur[e];
+#pragma unroll
+        for (int r = 1; r < K; ++r) acc = acc + tp[r][e] * win[r - 1][e];
+        u[e] = acc;
+      }
+      // normalize_keys over the head: s = u / max(peak, floor), key = s / sqrt(max(|s|^2, 1))
+      float peak = 0.f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) peak = __builtin_fmaxf(peak, fabsf(u[e]));
+      const float scale = __builtin_fmaxf(group_max<LPH>(peak), kKeyFloor);
+      const float inv_scale = __builtin_amdgcn_rcpf(scale);
+      float ss = 0.f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float s0 = u[e] * inv_scale;
+        u[e] = __builtin_fmaf(__builtin_fmaf(-s0, scale, u[e]), inv_scale, s0);
+        ss += u[e] * u[e];
+      }
+      const float inv_den = __builtin_amdgcn_rsqf(__builtin_fmaxf(group_sum<LPH>(ss), 1.f));
+      if (t < LPH) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) skey[8 * fc + e] = to_f32(from_f32<TIn>(u[e] * inv_den));
+        // the next history: rows 1 .. K - 2 move down one, the token's inputs become row K - 2
+#pragma unroll
+        for (int i = 0; i + 1 < K - 1; ++i) {
+          const float* src = win[K - 3 - i];  // old row i + 1
+          *reinterpret_cast<float4*>(hb + (size_t)i * DT) = make_float4(src[0], src[1], src[2], src[3]);
+          *reinterpret_cast<float4*>(hb + (size_t)i * DT + 4) = make_float4(src[4], src[5], src[6], src[7]);
+        }
+        if constexpr (K > 1) {
+          *reinterpret_cast<float4*>(hb + (size_t)(K - 2) * DT) = make_float4(cur[0], cur[1], cur[2], cur[3]);
+          *reinterpret_cast<float4*>(hb + (size_t)(K - 2) * DT + 4) = make_float4(cur[4], cur[5], cur[6], cur[7]);
+        }
+      }
+    }
+    __syncthreads();
+  }
   const TIn* kp = k + (size_t)bh * D;
   const TIn* qp = q + (size_t)bh * D;
   float kr[RPT], qr[RPT];
 #pragma unroll
   for (int j = 0; j < RPT; ++j) {
-    kr[j] = to_f32(kp[rg + RG * j]);
+    kr[j] = K > 0 ? skey[rg + RG * j] : to_f32(kp[rg + RG * j]);
     qr[j] = to_f32(qp[rg + RG * j]);
   }
   float vv[4];
@@ -144,6 +213,30 @@ bool step_fast(const TIn* q, const TIn* k, const TIn* v, const TIn* beta, const 
   }
 }
 
+template <int D, int K>
+void launch_step_keys(const __bf16* q, const __bf16* z, const __bf16* v, const __bf16* beta, float* history,
+                      const float* taps, const float* s_in, float* s_out, __bf16* o, const uint8_t* active, int B,
+                      int H, hipStream_t stream) {
+  hipLaunchKernelGGL((delta_step_kernel<__bf16, D, K>), dim3((unsigned)(B * H)), dim3(StepShape<D>::NT), 0, stream, q,
+                     z, v, beta, s_in, s_out, o, active, H, history, taps);
+}
+
+template <int D>
+void step_keys_by_width(int K, const __bf16* q, const __bf16* z, const __bf16* v, const __bf16* beta,
+                        float* history, const float* taps, const float* s_in, float* s_out, __bf16* o,
+                        const uint8_t* active, int B, int H, hipStream_t stream) {
+  switch (K) {
+    case 1: launch_step_keys<D, 1>(q, z, v, beta, history, taps, s_in, s_out, o, active, B, H, stream); break;
+    case 2: launch_step_keys<D, 2>(q, z, v, beta, history, taps, s_in, s_out, o, active, B, H, stream); break;
+    case 3: launch_step_keys<D, 3>(q, z, v, beta, history, taps, s_in, s_out, o, active, B, H, stream); break;
+    case 4: launch_step_keys<D, 4>(q, z, v, beta, history, taps, s_in, s_out, o, active, B, H, stream); break;
+    case 5: launch_step_keys<D, 5>(q, z, v, beta, history, taps, s_in, s_out, o, active, B, H, stream); break;
+    case 6: launch_step_keys<D, 6>(q, z, v, beta, history, taps, s_in, s_out, o, active, B, H, stream); break;
+    case 7: launch_step_keys<D, 7>(q, z, v, beta, history, taps, s_in, s_out, o, active, B, H, stream); break;
+    default: launch_step_keys<D, 8>(q, z, v, beta, history, taps, s_in, s_out, o, active, B, H, stream); break;
+  }
+}
+
 }  // namespace
 
 // The register-resident step for head widths 16, 32, 64 and 128; false when the width (or the
@@ -160,3 +253,31 @@ bool delta_step_fast_bf16(const __bf16* q, const __bf16* k, const __bf16* v, con
 }
 
 }  // namespace vsp
+
+extern "C" int vsp_delta_step_keys_bf16(const void* q, const void* z, const void* v, const void* beta, float* history,
+                                        const float* taps, int K, const float* state_in, float* state_out, void* o,
+                                        const uint8_t* active, int B, int H, int D, void* stream) {
+  using namespace vsp;
+  const char* who = "vsp_delta_step_keys_bf16";
+  if (B < 0 || H < 1) return fail(ERR_ARG, "%s: bad sizes B=%d H=%d", who, B, H);
+  if (D != 16 && D != 32 && D != 64 && D != 128)
+    return fail(ERR_UNSUPPORTED, "%s: head dimension %d (kernels: 16, 32, 64, 128)", who, D);
+  if (K < 1 || K > 8) return fail(ERR_UNSUPPORTED, "%s: filter width %d (kernels: 1..8)", who, K);
+  if (B == 0) return OK;
+  if (!q || !z || !v || !beta || !taps || !state_in || !state_out || !o || (K > 1 && !history))
+    return fail(ERR_ARG, "%s: null pointer", who);
+  if ((reinterpret_cast<uintptr_t>(z) | reinterpret_cast<uintptr_t>(taps) | reinterpret_cast<uintptr_t>(history) |
+       reinterpret_cast<uintptr_t>(state_in) | reinterpret_cast<uintptr_t>(state_out)) & 15)
+    return fail(ERR_ARG, "%s: z, taps, history and the states must be 16-byte aligned", who);
+  hipStream_t stream_h = reinterpret_cast<hipStream_t>(stream);
+  const __bf16 *qb = static_cast<const __bf16*>(q), *zb = static_cast<const __bf16*>(z);
+  const __bf16 *vb = static_cast<const __bf16*>(v), *bb = static_cast<const __bf16*>(beta);
+  __bf16* ob = static_cast<__bf16*>(o);
+  switch (D) {
+    case 16: step_keys_by_width<16>(K, qb, zb, vb, bb, history, taps, state_in, state_out, ob, active, B, H, stream_h); break;
+    case 32: step_keys_by_width<32>(K, qb, zb, vb, bb, history, taps, state_in, state_out, ob, active, B, H, stream_h); break;
+    case 64: step_keys_by_width<64>(K, qb, zb, vb, bb, history, taps, state_in, state_out, ob, active, B, H, stream_h); break;
+    default: step_keys_by_width<128>(K, qb, zb, vb, bb, history, taps, state_in, state_out, ob, active, B, H, stream_h); break;
+  }
+  return check_launch(who);
+}

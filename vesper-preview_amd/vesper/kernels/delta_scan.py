@@ -325,6 +325,68 @@ def delta_scan_step_fused(q: Tensor, k: Tensor, v: Tensor, beta: Tensor, state: 
     return o, out_state
 
 
+def delta_scan_step_keys(q: Tensor, z: Tensor, v: Tensor, beta: Tensor, history: Tensor, taps: Tensor, state: Tensor,
+                         *, active: Tensor | None = None, out_state: Tensor | None = None) -> Tensor:
+    """A decode step's key filter and delta step in one launch (``vsp_delta_step_keys_bf16``): each
+    head's key is the normalized filter of the key inputs ``z`` over the key ``history``
+    (``vesper/column.py:255-289``), formed and rounded as ``key_step`` forms it, the next history
+    is written over ``history``, and the step runs as ``delta_scan_step_fused`` with that key:
+    bitwise the two launches' results.
+
+    Args:
+        q, v: ``[b, h, dk]`` bfloat16; ``beta [b, h]`` bfloat16.
+        z: ``[b, h * dk]`` bfloat16 key inputs of the token.
+        history: ``[b, K-1, h * dk]`` contiguous float32, updated in place.
+        taps: ``[K, h * dk]`` float32 (``K`` in 1..8, tap 0 on the token).
+        state: ``[b, h, dk, dk]`` float32; ``out_state`` may be ``state`` itself.
+        active: optional bool ``[b]``; an inactive row writes the state and reads zero.
+
+    Returns:
+        ``o [b, h, dk]`` bfloat16 (the new state is in ``out_state``, by default ``state``).
+
+    Raises:
+        ContractError: on shapes, dtypes or devices outside that contract, or a head width other
+            than 16, 32, 64 or 128.
+    """
+    dims: Dims = {}
+    check_shape("q", q, ("b", "h", "dk"), dims, torch.bfloat16)
+    check_shape("v", v, ("b", "h", "dk"), dims, torch.bfloat16)
+    check_shape("beta", beta, ("b", "h"), dims, torch.bfloat16)
+    check_shape("state", state, ("b", "h", "dk", "dk"), dims, STATE_DTYPE)
+    b, h, dk = q.shape
+    dims["hd"] = h * dk
+    check_shape("z", z, ("b", "hd"), dims, torch.bfloat16)
+    check_shape("taps", taps, ("K", "hd"), dims, torch.float32)
+    width = dims["K"]
+    dims["hist"] = width - 1
+    check_shape("history", history, ("b", "hist", "hd"), dims, torch.float32)
+    if dk not in (16, 32, 64, 128) or not 1 <= width <= 8:
+        raise ContractError(f"head dimension {dk} (16, 32, 64, 128) or filter width {width} (1..8) not taken")
+    for name, t in (("z", z), ("v", v), ("beta", beta), ("history", history), ("taps", taps), ("state", state)):
+        if t.device != q.device or t.device.type != "cuda":
+            raise ContractError(f"{name} is on {t.device}, q on {q.device} (CUDA only)")
+    _refuse_grad(q, z, v, beta, history, taps, state)
+    if out_state is None:
+        out_state = state
+    for name, t in (("history", history), ("state", state), ("out_state", out_state)):
+        if not t.is_contiguous() or t.data_ptr() % 16:
+            raise ContractError(f"{name} must be contiguous and 16-byte aligned")
+    if out_state.shape != state.shape or out_state.dtype != STATE_DTYPE or out_state.device != q.device:
+        raise ContractError("out_state must be shaped, typed and placed like state")
+    q, v, beta = (t.contiguous() for t in (q, v, beta))
+    zc, tc = z.contiguous(), taps.contiguous()
+    for name, t in (("z", zc), ("taps", tc)):
+        if t.data_ptr() % 16:
+            raise ContractError(f"{name} must be 16-byte aligned")
+    mask = _active_mask(active, ("b",), dims, q.device)
+    o = torch.empty_like(q)
+    with torch.cuda.device(q.device):
+        _lib.call("vsp_delta_step_keys_bf16", q.data_ptr(), zc.data_ptr(), v.data_ptr(), beta.data_ptr(),
+                  history.data_ptr() if width > 1 else None, tc.data_ptr(), width, state.data_ptr(),
+                  out_state.data_ptr(), o.data_ptr(), _lib.ptr(mask), b, h, dk, _lib.stream_of(q.device))
+    return o
+
+
 # ---- the write strength (vesper/recurrence.py:34-88), alone and inside the scan's loads ----------
 
 def _checked_modulator(logits: Tensor, m: Tensor | None, alpha: float | None) -> float:
