@@ -73,71 +73,88 @@ __global__ __launch_bounds__(256) void decode_proj_kernel(const float* __restric
       if (w + 4 * i < ksteps) af[j][i] = *reinterpret_cast<const bf16x8*>(wr + 32 * (w + 4 * i));
   }
 
-  // the norm: wave w takes rows 4w .. 4w + 3 of the 16 (one wave a row, lane segments 8 (lane + 64 j))
-  for (int i = 0; i < 4; ++i) {
-    const int rl = 4 * w + i, m = mb * 16 + rl;
-    if (m >= M) {
+  // the norm: wave w takes rows 4w .. 4w + 3 of the 16 (one wave a row, lane segments 8 (lane + 64 j));
+  // every row's loads are issued before the first row's reductions
+  constexpr int RA = NSEG == 1 ? 4 : (NSEG == 2 ? 2 : 1);  // rows whose loads are in flight together
+  for (int i0 = 0; i0 < 4; i0 += RA) {
+    float e[RA][NSEG][8];
+#pragma unroll
+    for (int ii = 0; ii < RA; ++ii) {
+      const int m = mb * 16 + 4 * w + i0 + ii;
+      const size_t ro = (size_t)min(m, M - 1) * d;  // rows past M read row M - 1 (never used)
 #pragma unroll
       for (int j = 0; j < NSEG; ++j) {
         const int f = 8 * (l + 64 * j);
-        if (f < d) *reinterpret_cast<bf16x8*>(&sz[rl][f]) = bf16x8{};
-      }
-      continue;
-    }
-    const float* xr = x + (size_t)m * d;
-    float v[NSEG][8];
-    float peak = 0.f;
+        const int fs = f < d ? f : 0;
+        const float4 a = reinterpret_cast<const float4*>(x + ro + fs)[0];
+        const float4 b = reinterpret_cast<const float4*>(x + ro + fs)[1];
+        e[ii][j][0] = a.x; e[ii][j][1] = a.y; e[ii][j][2] = a.z; e[ii][j][3] = a.w;
+        e[ii][j][4] = b.x; e[ii][j][5] = b.y; e[ii][j][6] = b.z; e[ii][j][7] = b.w;
+        if (res != nullptr) {
+          const bf16x8 rv = *reinterpret_cast<const bf16x8*>(res + ro + fs);
 #pragma unroll
-    for (int j = 0; j < NSEG; ++j) {
-      const int f = 8 * (l + 64 * j);
-      const bool ok = f < d;
-      const float4 a = reinterpret_cast<const float4*>(xr + (ok ? f : 0))[0];
-      const float4 b = reinterpret_cast<const float4*>(xr + (ok ? f : 0))[1];
-      float e[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
-      if (res != nullptr) {
-        const bf16x8 rv = *reinterpret_cast<const bf16x8*>(res + (size_t)m * d + (ok ? f : 0));
-#pragma unroll
-        for (int k = 0; k < 8; ++k) e[k] += (float)rv[k];
-      }
-      if (ok && sum_out != nullptr && gid == 0) {
-        reinterpret_cast<float4*>(sum_out + (size_t)m * d + f)[0] = make_float4(e[0], e[1], e[2], e[3]);
-        reinterpret_cast<float4*>(sum_out + (size_t)m * d + f)[1] = make_float4(e[4], e[5], e[6], e[7]);
-      }
-#pragma unroll
-      for (int k = 0; k < 8; ++k) {
-        v[j][k] = ok ? e[k] : 0.f;
-        peak = __builtin_fmaxf(peak, fabsf(v[j][k]));
+          for (int k = 0; k < 8; ++k) e[ii][j][k] += (float)rv[k];
+        }
       }
     }
-    const float scale = __builtin_fmaxf(group_max<64>(peak), kProjRmsScaleFloor);
-    const float inv_scale = __builtin_amdgcn_rcpf(scale);
-    float ss = 0.f;
 #pragma unroll
-    for (int j = 0; j < NSEG; ++j)
+    for (int ii = 0; ii < RA; ++ii) {
+      const int rl = 4 * w + i0 + ii, m = mb * 16 + rl;
+      if (m >= M) {
 #pragma unroll
-      for (int k = 0; k < 8; ++k) {
-        const float s0 = v[j][k] * inv_scale;
-        v[j][k] = __builtin_fmaf(__builtin_fmaf(-s0, scale, v[j][k]), inv_scale, s0);
-        ss += v[j][k] * v[j][k];
+        for (int j = 0; j < NSEG; ++j) {
+          const int f = 8 * (l + 64 * j);
+          if (f < d) *reinterpret_cast<bf16x8*>(&sz[rl][f]) = bf16x8{};
+        }
+        continue;
       }
-    const float mean = group_sum<64>(ss) / (float)d;
-    const float inv_rms = 1.f / __builtin_sqrtf(mean + kProjRmsEps / (scale * scale));
+      float v[NSEG][8];
+      float peak = 0.f;
 #pragma unroll
-    for (int j = 0; j < NSEG; ++j) {
-      const int f = 8 * (l + 64 * j);
-      if (f >= d) continue;
-      bf16x8 o;
-      if (gain != nullptr) {
-        const float4 ga = reinterpret_cast<const float4*>(gain + f)[0];
-        const float4 gb = reinterpret_cast<const float4*>(gain + f)[1];
-        const float gg[8] = {ga.x, ga.y, ga.z, ga.w, gb.x, gb.y, gb.z, gb.w};
+      for (int j = 0; j < NSEG; ++j) {
+        const int f = 8 * (l + 64 * j);
+        const bool ok = f < d;
+        if (ok && sum_out != nullptr && gid == 0) {
+          float* so = sum_out + (size_t)m * d + f;
+          reinterpret_cast<float4*>(so)[0] = make_float4(e[ii][j][0], e[ii][j][1], e[ii][j][2], e[ii][j][3]);
+          reinterpret_cast<float4*>(so)[1] = make_float4(e[ii][j][4], e[ii][j][5], e[ii][j][6], e[ii][j][7]);
+        }
 #pragma unroll
-        for (int k = 0; k < 8; ++k) o[k] = (__bf16)(v[j][k] * inv_rms * gg[k]);
-      } else {
-#pragma unroll
-        for (int k = 0; k < 8; ++k) o[k] = (__bf16)(v[j][k] * inv_rms);
+        for (int k = 0; k < 8; ++k) {
+          v[j][k] = ok ? e[ii][j][k] : 0.f;
+          peak = __builtin_fmaxf(peak, fabsf(v[j][k]));
+        }
       }
-      *reinterpret_cast<bf16x8*>(&sz[rl][f]) = o;
+      const float scale = __builtin_fmaxf(group_max<64>(peak), kProjRmsScaleFloor);
+      const float inv_scale = __builtin_amdgcn_rcpf(scale);
+      float ss = 0.f;
+#pragma unroll
+      for (int j = 0; j < NSEG; ++j)
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+          const float s0 = v[j][k] * inv_scale;
+          v[j][k] = __builtin_fmaf(__builtin_fmaf(-s0, scale, v[j][k]), inv_scale, s0);
+          ss += v[j][k] * v[j][k];
+        }
+      const float mean = group_sum<64>(ss) / (float)d;
+      const float inv_rms = 1.f / __builtin_sqrtf(mean + kProjRmsEps / (scale * scale));
+#pragma unroll
+      for (int j = 0; j < NSEG; ++j) {
+        const int f = 8 * (l + 64 * j);
+        if (f >= d) continue;
+        bf16x8 o;
+        if (gain != nullptr) {
+          const float4 ga = reinterpret_cast<const float4*>(gain + f)[0];
+          const float4 gb = reinterpret_cast<const float4*>(gain + f)[1];
+          const float gg[8] = {ga.x, ga.y, ga.z, ga.w, gb.x, gb.y, gb.z, gb.w};
+#pragma unroll
+          for (int k = 0; k < 8; ++k) o[k] = (__bf16)(v[j][k] * inv_rms * gg[k]);
+        } else {
+#pragma unroll
+          for (int k = 0; k < 8; ++k) o[k] = (__bf16)(v[j][k] * inv_rms);
+        }
+        *reinterpret_cast<bf16x8*>(&sz[rl][f]) = o;
+      }
     }
   }
   __syncthreads();
