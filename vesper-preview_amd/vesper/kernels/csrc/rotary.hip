@@ -8,9 +8,10 @@
 // base^(-2j/dk) arrive as a float64 table the host computed exactly as the reference does.
 //
 // A workgroup takes four token rows (b, n): first its threads compute each (row, pair)'s cos and
-// sin once into LDS (the float64 part), then every (row, head, pair) turn of the rows' query and
-// key heads is an independent piece of work spread over all 256 threads, consecutive threads on
-// consecutive pairs, four pieces' loads issued before their arithmetic. q and k may be rotated in
+// sin once into LDS (the float64 part), then the rows' query and key heads are cut into pieces of
+// consecutive pairs (16 bytes where the head width and alignment allow, else one pair), each an
+// independent piece of work spread over all 256 threads, consecutive threads on consecutive
+// pieces, four pieces' loads issued before their arithmetic. q and k may be rotated in
 // place (each element is read and written by one thread).
 #include "common.h"
 #include "rotary_math.h"
@@ -19,30 +20,41 @@
 namespace vsp {
 namespace {
 
-template <typename T> struct Pair {
-  typedef T P2 __attribute__((ext_vector_type(2)));
+// PP consecutive pairs of one head as one vector access (16 bytes where the rows allow it)
+template <typename T, int PP> struct Pieces {
+  typedef T V __attribute__((ext_vector_type(2 * PP)));
 };
-
-// the pair x turned (rot_pair) and stored at dst
-template <typename T>
-__device__ __forceinline__ void turn(typename Pair<T>::P2 x, T* dst, T c, T s) {
-  typename Pair<T>::P2 y;
-  T y1, y2;
-  rot_pair<T>(x[0], x[1], c, s, y1, y2);
-  y[0] = y1;
-  y[1] = y2;
-  *reinterpret_cast<typename Pair<T>::P2*>(dst) = y;
-}
 
 constexpr int kRotRows = 4;  // token rows a workgroup
 
-template <typename T>
+template <typename T, int PP>
 __global__ __launch_bounds__(256) void rotary_qk_kernel(const T* q, const T* k, const int64_t* __restrict__ pos,
                                                         const double* __restrict__ inv_freq, T* qo, T* ko, int rows,
                                                         int H, int HKV, int D) {
   __shared__ T cs[kRotRows][512], sn[kRotRows][512];
   const int half = D / 2, row0 = blockIdx.x * kRotRows;
   const int nrows = min(kRotRows, rows - row0);
+  // piece t: row r = t / (heads * groups), head hh, pairs PP g .. PP g + PP - 1 (heads: the H query
+  // heads, then the HKV key heads)
+  typedef typename Pieces<T, PP>::V V;
+  const int groups = half / PP, heads = H + HKV, per_row = heads * groups, total = nrows * per_row;
+  V xv[4];
+  size_t off[4];
+  bool isq[4];
+  int rr[4], jj[4];
+  auto load_round = [&](int t0) {
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int t = min(t0 + 256 * u, total - 1);
+      const int r = t / per_row, rem = t - r * per_row, hh = rem / groups, j = PP * (rem - hh * groups);
+      isq[u] = hh < H;
+      off[u] = isq[u] ? ((size_t)(row0 + r) * H + hh) * D + 2 * j : ((size_t)(row0 + r) * HKV + (hh - H)) * D + 2 * j;
+      rr[u] = r;
+      jj[u] = j;
+      xv[u] = *reinterpret_cast<const V*>((isq[u] ? q : k) + off[u]);
+    }
+  };
+  load_round(threadIdx.x);  // the first pieces' loads do not wait for the cos and sin
   for (int e = threadIdx.x; e < nrows * half; e += 256) {
     const int r = e / half, j = e - r * half;
     const double angle = (double)pos[row0 + r] * inv_freq[j];
@@ -50,27 +62,21 @@ __global__ __launch_bounds__(256) void rotary_qk_kernel(const T* q, const T* k, 
     sn[r][j] = rot_from_f64<T>(sin(angle));
   }
   __syncthreads();
-  // piece t: row r = t / (heads * half), head hh, pair j (heads: the H query heads, then the HKV
-  // key heads)
-  const int heads = H + HKV, per_row = heads * half, total = nrows * per_row;
   for (int t0 = threadIdx.x; t0 < total; t0 += 4 * 256) {
-    typename Pair<T>::P2 xv[4];
-    size_t off[4];
-    bool isq[4];
-    int rr[4], jj[4];
+    if (t0 != (int)threadIdx.x) load_round(t0);
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
-      const int t = min(t0 + 256 * u, total - 1);
-      const int r = t / per_row, rem = t - r * per_row, hh = rem / half, j = rem - hh * half;
-      isq[u] = hh < H;
-      off[u] = isq[u] ? ((size_t)(row0 + r) * H + hh) * D + 2 * j : ((size_t)(row0 + r) * HKV + (hh - H)) * D + 2 * j;
-      rr[u] = r;
-      jj[u] = j;
-      xv[u] = *reinterpret_cast<const typename Pair<T>::P2*>((isq[u] ? q : k) + off[u]);
-    }
+      if (t0 + 256 * u >= total) continue;
+      V y;
 #pragma unroll
-    for (int u = 0; u < 4; ++u)
-      if (t0 + 256 * u < total) turn<T>(xv[u], (isq[u] ? qo : ko) + off[u], cs[rr[u]][jj[u]], sn[rr[u]][jj[u]]);
+      for (int i = 0; i < PP; ++i) {
+        T y1, y2;
+        rot_pair<T>(xv[u][2 * i], xv[u][2 * i + 1], cs[rr[u]][jj[u] + i], sn[rr[u]][jj[u] + i], y1, y2);
+        y[2 * i] = y1;
+        y[2 * i + 1] = y2;
+      }
+      *reinterpret_cast<V*>((isq[u] ? qo : ko) + off[u]) = y;
+    }
   }
 }
 
@@ -86,8 +92,16 @@ int rotary_qk(const T* q, const T* k, const int64_t* pos, const double* inv_freq
        reinterpret_cast<uintptr_t>(ko)) & (2 * sizeof(T) - 1))
     return fail(ERR_ARG, "%s: q, k and the outputs must be aligned to a pair", who);
   const int rows = B * N;
-  hipLaunchKernelGGL(rotary_qk_kernel<T>, dim3((unsigned)((rows + kRotRows - 1) / kRotRows)), dim3(256), 0,
-                     reinterpret_cast<hipStream_t>(stream), q, k, pos, inv_freq, qo, ko, rows, H, HKV, D);
+  // 16-byte pieces (PW pairs) where every row of pairs splits into them and the tensors are aligned
+  constexpr int PW = 8 / sizeof(T);
+  const bool wide = (D / 2) % PW == 0 && ((reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(k) |
+                                          reinterpret_cast<uintptr_t>(qo) | reinterpret_cast<uintptr_t>(ko)) & 15) == 0;
+  const dim3 grid((unsigned)((rows + kRotRows - 1) / kRotRows));
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  if (wide)
+    hipLaunchKernelGGL((rotary_qk_kernel<T, PW>), grid, dim3(256), 0, s, q, k, pos, inv_freq, qo, ko, rows, H, HKV, D);
+  else
+    hipLaunchKernelGGL((rotary_qk_kernel<T, 1>), grid, dim3(256), 0, s, q, k, pos, inv_freq, qo, ko, rows, H, HKV, D);
   return check_launch(who);
 }
 
