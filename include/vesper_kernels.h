@@ -22,7 +22,7 @@
 extern "C" {
 #endif
 
-#define VSP_ABI_VERSION 16
+#define VSP_ABI_VERSION 18
 
 /* Status codes. */
 #define VSP_OK 0
@@ -403,6 +403,12 @@ int vsp_key_filter_backward_f32(const float* z, const float* history, const floa
  * [rows, d] bf16, the projections' operand. d a multiple of 8 in 8..2048; x, gain, out 16-byte
  * aligned. */
 int vsp_rms_norm_bf16(const float* x, const float* gain, void* out, int rows, int d, void* stream);
+/* The same norm of s = x + residual (residual [rows, d] bf16, added in float32 as the column's
+ * residual add does: vesper/column.py:779-796), with s also written to sum_out ([rows, d] float32,
+ * or NULL; it must not overlap x): the add and the norm in one launch, bitwise the two launches'.
+ * x, residual, sum_out, gain and out 16-byte aligned. */
+int vsp_add_rms_norm_bf16(const float* x, const void* residual, float* sum_out, const float* gain, void* out, int rows,
+                          int d, void* stream);
 
 /* The decode step's projection of that normalized stream, fused (the looped column's per-pass
  * projections, vesper/column.py:192-260 and vesper/attention.py:269-292, for a decode step of M
@@ -432,6 +438,13 @@ int vsp_decode_proj_bf16(const float* x, const void* residual, float* sum_out, c
  * `count` entries; the device buffers hold rows * row_bytes[i] bytes each. */
 int vsp_copy_rows_where(int count, const void* const* src, void* const* dst, const size_t* row_bytes,
                         const uint8_t* const* flags, int rows, void* stream);
+
+/* The pass loop's halting bookkeeping for one pass (vesper/loop.py:441-452; the pass count of the
+ * loop's LoopResult): over count tokens (bool bytes), halts = active & exits (exits NULL: every
+ * active token halts, the last pass), n_iters += active (int32, in place), next = active & !halts.
+ * One launch for the five elementwise steps; halts and next must not be active. */
+int vsp_halt_step(const uint8_t* active, const uint8_t* exits, int* n_iters, uint8_t* halts, uint8_t* next, int count,
+                  void* stream);
 
 #ifdef __cplusplus
 }

@@ -230,3 +230,20 @@ def test_copy_rows_where_refusals():
         copy_rows_where([(x[:, :, :4], x.clone()[:, :, ::2], f)])
     with pytest.raises(ContractError, match="token rows"):
         copy_rows_where([(x, x.clone(), f), (x[:1], x[:1].clone(), f[:1])])
+
+
+def test_the_halting_step_matches_the_elementwise_steps():
+    # vsp_halt_step: halts = active & exits (all active on the last pass), n_iters += active,
+    # next = active & ~halts, against the torch steps it replaces
+    from vesper.kernels.carry import halt_step
+
+    g = torch.Generator().manual_seed(9)
+    for last in (False, True):
+        active = (torch.rand(3, 1000, generator=g) < 0.6).to(GPU)
+        exits = (torch.rand(3, 1000, generator=g) < 0.3).to(GPU)
+        n_iters = torch.randint(0, 5, (3, 1000), generator=g, dtype=torch.int32).to(GPU)
+        want_halts = active if last else active & exits
+        want_iters = n_iters + active.to(torch.int32)
+        halts, nxt = halt_step(active, None if last else exits, n_iters)
+        assert torch.equal(halts, want_halts) and torch.equal(n_iters, want_iters)
+        assert torch.equal(nxt, active & ~want_halts)

@@ -49,3 +49,22 @@ def test_refusals():
         rms_norm_bf16(torch.zeros(2, 60, device=GPU))
     with pytest.raises(ContractError, match="gain"):
         rms_norm_bf16(torch.zeros(2, 64, device=GPU), torch.ones(32, device=GPU))
+
+
+@pytest.mark.parametrize("d", [8, 64, 512, 1000, 2048])
+@pytest.mark.parametrize("with_gain", [False, True])
+def test_the_residual_add_inside_the_norm_equals_the_two_launches_bitwise(d, with_gain):
+    """vsp_add_rms_norm_bf16: x + r (bf16 r added in float32) normalized in one launch equals the
+    add followed by the norm, and the sum it writes equals the add, bit for bit."""
+    from vesper.kernels.norm import rms_norm_bf16
+
+    g = torch.Generator().manual_seed(d)
+    x = (torch.randn(37, d, generator=g) * torch.logspace(-3, 3, 37)[:, None]).to(GPU)
+    r = torch.randn(37, d, generator=g).to(torch.bfloat16).to(GPU)
+    gain = (0.5 + torch.rand(d, generator=g)).to(GPU) if with_gain else None
+    s = torch.empty_like(x)
+    got = rms_norm_bf16(x, gain, residual=r, sum_out=s)
+    want_s = x + r.float()
+    assert torch.equal(s, want_s)
+    assert torch.equal(got, rms_norm_bf16(want_s, gain))
+    assert torch.equal(rms_norm_bf16(x, gain, residual=r), got)  # without the sum written

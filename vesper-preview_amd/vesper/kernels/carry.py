@@ -69,3 +69,32 @@ def copy_rows_where(items: Sequence[tuple[Tensor, Tensor, Tensor]]) -> None:
         _lib.call("vsp_copy_rows_where", count, ctypes.cast(src_arr, ctypes.c_void_p),
                   ctypes.cast(dst_arr, ctypes.c_void_p), ctypes.cast(size_arr, ctypes.c_void_p),
                   ctypes.cast(flag_arr, ctypes.c_void_p), int(rows or 0), _lib.stream_of(device))
+
+
+def halt_step(active: Tensor, exits: Tensor | None, n_iters: Tensor) -> tuple[Tensor, Tensor]:
+    """One pass's halting bookkeeping in one launch (``vsp_halt_step``): ``halts = active & exits``
+    (every active token when ``exits`` is None, the last pass), ``n_iters += active`` in place, and
+    the next pass's ``active & ~halts``; returns ``(halts, next_active)``.
+
+    Args:
+        active: bool ``[b, n]``; exits: bool ``[b, n]`` or None; n_iters: contiguous int32 ``[b, n]``.
+
+    Raises:
+        ContractError: on shapes, dtypes or devices that disagree.
+    """
+    shape = tuple(active.shape)
+    if active.dtype != torch.bool or active.device.type != "cuda":
+        raise ContractError(f"active: bool on CUDA, got {active.dtype} on {active.device}")
+    if exits is not None and (tuple(exits.shape) != shape or exits.dtype != torch.bool or exits.device != active.device):
+        raise ContractError(f"exits: bool {shape} on {active.device}")
+    if (tuple(n_iters.shape) != shape or n_iters.dtype != torch.int32 or n_iters.device != active.device
+            or not n_iters.is_contiguous()):
+        raise ContractError(f"n_iters: contiguous int32 {shape} on {active.device}")
+    a = active.contiguous()
+    e = None if exits is None else exits.contiguous()
+    halts = torch.empty_like(a)
+    nxt = torch.empty_like(a)
+    with torch.cuda.device(active.device):
+        _lib.call("vsp_halt_step", a.data_ptr(), _lib.ptr(e), n_iters.data_ptr(), halts.data_ptr(), nxt.data_ptr(),
+                  a.numel(), _lib.stream_of(active.device))
+    return halts, nxt

@@ -81,3 +81,38 @@ extern "C" int vsp_copy_rows_where(int count, const void* const* src, void* cons
                      reinterpret_cast<hipStream_t>(stream), items, (unsigned)rows);
   return check_launch(who);
 }
+
+namespace vsp {
+namespace {
+
+// The pass loop's halting bookkeeping for one pass (vesper/loop.py:441-452 with the pass count of
+// column.py's loop): halts = active & exits (every active token on the last pass, exits NULL),
+// n_iters += active, next = active & !halts. One thread per token.
+__global__ __launch_bounds__(256) void halt_step_kernel(const uint8_t* __restrict__ active,
+                                                        const uint8_t* __restrict__ exits,
+                                                        int* __restrict__ n_iters, uint8_t* __restrict__ halts,
+                                                        uint8_t* __restrict__ next, int count) {
+  const int i = blockIdx.x * 256 + threadIdx.x;
+  if (i >= count) return;
+  const uint8_t a = active[i] != 0;
+  const uint8_t h = a & (exits == nullptr ? (uint8_t)1 : (uint8_t)(exits[i] != 0));
+  n_iters[i] += a;
+  halts[i] = h;
+  next[i] = a & (uint8_t)!h;
+}
+
+}  // namespace
+}  // namespace vsp
+
+extern "C" int vsp_halt_step(const uint8_t* active, const uint8_t* exits, int* n_iters, uint8_t* halts, uint8_t* next,
+                             int count, void* stream) {
+  using namespace vsp;
+  const char* who = "vsp_halt_step";
+  if (count < 0) return fail(ERR_ARG, "%s: %d tokens", who, count);
+  if (count == 0) return OK;
+  if (!active || !n_iters || !halts || !next) return fail(ERR_ARG, "%s: null pointer", who);
+  if (next == active || halts == active) return fail(ERR_ARG, "%s: the outputs must not be the active flags", who);
+  hipLaunchKernelGGL(halt_step_kernel, dim3((unsigned)((count + 255) / 256)), dim3(256), 0,
+                     reinterpret_cast<hipStream_t>(stream), active, exits, n_iters, halts, next, count);
+  return check_launch(who);
+}

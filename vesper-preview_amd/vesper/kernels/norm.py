@@ -14,12 +14,18 @@ from vesper.contracts import ContractError
 from vesper.kernels import _lib
 
 
-def rms_norm_bf16(x: Tensor, gain: Tensor | None = None) -> Tensor:
+def rms_norm_bf16(x: Tensor, gain: Tensor | None = None, *, residual: Tensor | None = None,
+                  sum_out: Tensor | None = None) -> Tensor:
     """``RMSNorm`` over the last axis of float32 ``x [..., d]`` on the GPU, as bfloat16.
 
     Args:
         x: float32, its last axis ``d`` a multiple of 8 in 8..2048.
         gain: optional float32 ``[d]`` (the norm's weight; ones when omitted).
+        residual: optional bfloat16 tensor shaped like ``x``: the norm is then of ``x + residual``
+            (added in float32, the column's residual add), in the same launch
+            (``vsp_add_rms_norm_bf16``), bitwise the add followed by the norm.
+        sum_out: with ``residual``, an optional contiguous float32 tensor shaped like ``x`` (not
+            ``x`` itself) that receives ``x + residual``.
 
     Raises:
         ContractError: on a dtype, width or device outside that contract.
@@ -43,8 +49,28 @@ def rms_norm_bf16(x: Tensor, gain: Tensor | None = None) -> Tensor:
             g = g.clone()
     out = torch.empty(x.shape, dtype=torch.bfloat16, device=x.device)
     rows = xc.numel() // d
+    if residual is None:
+        if sum_out is not None:
+            raise ContractError("sum_out needs a residual")
+        with torch.cuda.device(x.device):
+            _lib.call("vsp_rms_norm_bf16", xc.data_ptr(), _lib.ptr(g), out.data_ptr(), rows, d,
+                      _lib.stream_of(x.device))
+        return out
+    if residual.shape != x.shape or residual.dtype != torch.bfloat16 or residual.device != x.device:
+        raise ContractError(f"residual: bf16 {tuple(x.shape)} on {x.device}, got {tuple(residual.shape)} "
+                            f"{residual.dtype} on {residual.device}")
+    rc = residual.contiguous()
+    if rc.data_ptr() % 16:
+        rc = rc.clone()
+    if sum_out is not None:
+        if (sum_out.shape != x.shape or sum_out.dtype != torch.float32 or sum_out.device != x.device
+                or not sum_out.is_contiguous() or sum_out.data_ptr() % 16):
+            raise ContractError(f"sum_out: contiguous, aligned float32 {tuple(x.shape)} on {x.device}")
+        if sum_out.data_ptr() == xc.data_ptr():
+            raise ContractError("sum_out must not be x")
     with torch.cuda.device(x.device):
-        _lib.call("vsp_rms_norm_bf16", xc.data_ptr(), _lib.ptr(g), out.data_ptr(), rows, d, _lib.stream_of(x.device))
+        _lib.call("vsp_add_rms_norm_bf16", xc.data_ptr(), rc.data_ptr(), _lib.ptr(sum_out), _lib.ptr(g),
+                  out.data_ptr(), rows, d, _lib.stream_of(x.device))
     return out
 
 

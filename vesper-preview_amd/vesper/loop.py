@@ -41,7 +41,7 @@ from torch import Tensor
 from vesper.attention import rotary_qk
 from vesper.column import recurrent_keys
 from vesper.contracts import ContractError, Dims, check_shape
-from vesper.kernels.carry import copy_rows_where
+from vesper.kernels.carry import copy_rows_where, halt_step
 from vesper.kernels.delta_scan import delta_scan_fused
 from vesper.kernels.keys import fused_keys
 from vesper.kernels.norm import rms_norm_bf16
@@ -233,8 +233,9 @@ class LoopedColumn:
                                             carried=(carried.k, carried.v, carried.beta))
         else:
             r, new_state = delta_scan_fused(q, k, v, beta, state, active=active)
-        x1 = x + r.reshape(b, n, h * dk)  # float32 (promoted in the add)
-        aq, ak, av = self.project_attn(t, rms_norm_bf16(x1))
+        # x1 = x + r (float32, promoted in the add) and its norm, in one launch
+        x1 = torch.empty_like(x)
+        aq, ak, av = self.project_attn(t, rms_norm_bf16(x, residual=r.reshape(b, n, h * dk), sum_out=x1))
         if where and carried is not None and active is not None:
             ak = _where_tokens(active, ak, carried.attn_k)
             av = _where_tokens(active, av, carried.attn_v)
@@ -287,8 +288,9 @@ class LoopedColumn:
                 mask = None if carried is None else active
                 h, new_states[t], new_histories[t], written = self._step(x, t, new_states[t], new_histories[t], mask,
                                                                          carried)
-                halts = active & exits[t] if t < self.passes - 1 else active
-                n_iters += active.to(torch.int32)
+                # halts = active & exit (all active on the last pass), n_iters += active, and the
+                # next pass's active & ~halts: one launch
+                halts, next_active = halt_step(active, exits[t] if t < self.passes - 1 else None, n_iters)
                 if carried is None:  # pass 0: every token active, the fresh projections are the carried ones
                     carried, x = written, h
                 elif self.copy_forward == "where":
@@ -307,6 +309,6 @@ class LoopedColumn:
                         if written.z is not None and carried.z is not None:
                             items.append((written.z, carried.z, halts))
                     copy_rows_where([*items, (h, x, active)])
-                active = active & ~halts
+                active = next_active
         hist_out = tuple(t for t in new_histories if t is not None) if self.taps is not None else None
         return LoopResult(y=x, states=tuple(new_states), n_iters=n_iters, histories=hist_out)
