@@ -48,17 +48,19 @@ template <int GM> struct RingShape {
 
 // Eight ring elements as the queries' type: the ring's own type is either the queries' (one 16-byte
 // load) or float32 (two, each element rounded to nearest even, as the reference's autocast casts an
-// fp32 ring to the query dtype, attention.py:325).
+// fp32 ring to the query dtype, attention.py:325). The loads are nontemporal: a decode step reads
+// each ring once, and a column's rings (one a pass) together outgrow the MALL, so they stream.
 template <typename T, typename R>
 __device__ __forceinline__ typename Ring8<T>::V8 load_ring8(const R* p) {
   typedef typename Ring8<T>::V8 V8;
   if constexpr (sizeof(R) == sizeof(T)) {
-    return *reinterpret_cast<const V8*>(p);
+    return __builtin_nontemporal_load(reinterpret_cast<const V8*>(p));
   } else {
-    const float4 a = reinterpret_cast<const float4*>(p)[0], b = reinterpret_cast<const float4*>(p)[1];
+    const f32x4 a = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(p));
+    const f32x4 b = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(p) + 1);
     V8 x;
-    x[0] = from_f32<T>(a.x); x[1] = from_f32<T>(a.y); x[2] = from_f32<T>(a.z); x[3] = from_f32<T>(a.w);
-    x[4] = from_f32<T>(b.x); x[5] = from_f32<T>(b.y); x[6] = from_f32<T>(b.z); x[7] = from_f32<T>(b.w);
+    x[0] = from_f32<T>(a[0]); x[1] = from_f32<T>(a[1]); x[2] = from_f32<T>(a[2]); x[3] = from_f32<T>(a[3]);
+    x[4] = from_f32<T>(b[0]); x[5] = from_f32<T>(b[1]); x[6] = from_f32<T>(b[2]); x[7] = from_f32<T>(b[3]);
     return x;
   }
 }
