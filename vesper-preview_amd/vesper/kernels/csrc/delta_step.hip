@@ -53,9 +53,12 @@ __global__ __launch_bounds__(StepShape<D>::NT) void delta_step_kernel(
   const int cb = t % CPR, rg = t / CPR;
   const size_t base = (size_t)bh * D * D;
 
-  float4 st[RPT];
+  // the state streams (read once, written once a step; a decoder's states outgrow the caches):
+  // nontemporal loads and stores
+  f32x4 st[RPT];
 #pragma unroll
-  for (int j = 0; j < RPT; ++j) st[j] = reinterpret_cast<const float4*>(s_in + base + (size_t)(rg + RG * j) * D)[cb];
+  for (int j = 0; j < RPT; ++j)
+    st[j] = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(s_in + base + (size_t)(rg + RG * j) * D) + cb);
   if constexpr (K > 0) {
     // the first wave forms the key: lane l takes features 8 (l % LPH) .. + 7 of the head (the lanes
     // past LPH repeat a group; only the first group stores)
@@ -128,7 +131,7 @@ __global__ __launch_bounds__(StepShape<D>::NT) void delta_step_kernel(
   float pk[4] = {0.f, 0.f, 0.f, 0.f}, pq[4] = {0.f, 0.f, 0.f, 0.f}, kq = 0.f;
 #pragma unroll
   for (int j = 0; j < RPT; ++j) {
-    const float e[4] = {st[j].x, st[j].y, st[j].z, st[j].w};
+    const float e[4] = {st[j][0], st[j][1], st[j][2], st[j][3]};
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
       pk[c] += e[c] * kr[j];
@@ -177,12 +180,12 @@ __global__ __launch_bounds__(StepShape<D>::NT) void delta_step_kernel(
   for (int c = 0; c < 4; ++c) u[c] = bt * (vv[c] - pk[c]);
 #pragma unroll
   for (int j = 0; j < RPT; ++j) {
-    float4 w4;
-    w4.x = st[j].x + kr[j] * u[0];
-    w4.y = st[j].y + kr[j] * u[1];
-    w4.z = st[j].z + kr[j] * u[2];
-    w4.w = st[j].w + kr[j] * u[3];
-    reinterpret_cast<float4*>(s_out + base + (size_t)(rg + RG * j) * D)[cb] = w4;
+    f32x4 w4;
+    w4[0] = st[j][0] + kr[j] * u[0];
+    w4[1] = st[j][1] + kr[j] * u[1];
+    w4[2] = st[j][2] + kr[j] * u[2];
+    w4[3] = st[j][3] + kr[j] * u[3];
+    __builtin_nontemporal_store(w4, reinterpret_cast<f32x4*>(s_out + base + (size_t)(rg + RG * j) * D) + cb);
   }
   if (rg == 0) {
     const bool on = active == nullptr || active[bh / H] != 0;
