@@ -22,7 +22,7 @@
 extern "C" {
 #endif
 
-#define VSP_ABI_VERSION 18
+#define VSP_ABI_VERSION 19
 
 /* Status codes. */
 #define VSP_OK 0
@@ -445,6 +445,13 @@ int vsp_copy_rows_where(int count, const void* const* src, void* const* dst, con
  * One launch for the five elementwise steps; halts and next must not be active. */
 int vsp_halt_step(const uint8_t* active, const uint8_t* exits, int* n_iters, uint8_t* halts, uint8_t* next, int count,
                   void* stream);
+
+/* The residual stream after a pass's attention for the rows still in the loop (vesper/loop.py:452
+ * with the column's residual add): x[r] = x1[r] + a[r] (x1, x float32 [rows, d]; a bf16 [rows, d],
+ * added in float32) where flags[r] != 0, every row when flags is NULL; other rows of x are left
+ * as they are. d a multiple of 8; x1, a, x 16-byte aligned; x must not overlap x1 or a. */
+int vsp_residual_rows_where(const float* x1, const void* a, float* x, const uint8_t* flags, int rows, int d,
+                            void* stream);
 
 #ifdef __cplusplus
 }

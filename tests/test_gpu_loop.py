@@ -247,3 +247,19 @@ def test_the_halting_step_matches_the_elementwise_steps():
         halts, nxt = halt_step(active, None if last else exits, n_iters)
         assert torch.equal(halts, want_halts) and torch.equal(n_iters, want_iters)
         assert torch.equal(nxt, active & ~want_halts)
+
+
+def test_the_residual_rows_match_the_add_and_the_row_copy():
+    # vsp_residual_rows_where: x[r] = x1[r] + a[r] on flagged rows (all rows without flags), the
+    # other rows untouched, bit for bit the torch add followed by the row selection
+    from vesper.kernels.carry import residual_rows_where
+
+    g = torch.Generator().manual_seed(10)
+    x1 = torch.randn(3, 100, 520, generator=g).to(GPU)
+    a = torch.randn(3, 100, 520, generator=g).to(torch.bfloat16).to(GPU)
+    flags = (torch.rand(3, 100, generator=g) < 0.5).to(GPU)
+    for fl in (flags, None):
+        x = torch.randn(3, 100, 520, generator=g).to(GPU)
+        want = x1 + a if fl is None else torch.where(fl[..., None], x1 + a, x)
+        residual_rows_where(x1, a, x, fl)
+        assert torch.equal(x, want)

@@ -98,3 +98,38 @@ def halt_step(active: Tensor, exits: Tensor | None, n_iters: Tensor) -> tuple[Te
         _lib.call("vsp_halt_step", a.data_ptr(), _lib.ptr(e), n_iters.data_ptr(), halts.data_ptr(), nxt.data_ptr(),
                   a.numel(), _lib.stream_of(active.device))
     return halts, nxt
+
+
+def residual_rows_where(x1: Tensor, a: Tensor, x: Tensor, flags: Tensor | None) -> None:
+    """``x[r] = x1[r] + a[r]`` in place for the token rows with ``flags[r]`` set (every row when
+    ``flags`` is None), one launch (``vsp_residual_rows_where``): the residual add after a pass's
+    attention written straight into the loop's hidden state, only for the tokens still in the
+    loop (``vesper/loop.py:452``).
+
+    Args:
+        x1: float32 ``[b, n, d]``; a: bfloat16 ``[b, n, d]`` (added in float32); x: contiguous
+            float32 ``[b, n, d]``, written in place (not ``x1``); flags: bool ``[b, n]`` or None.
+
+    Raises:
+        ContractError: on shapes, dtypes or devices that disagree.
+    """
+    if x1.dim() != 3 or x1.dtype != torch.float32 or x1.device.type != "cuda":
+        raise ContractError(f"x1: float32 [b, n, d] on CUDA, got {tuple(x1.shape)} {x1.dtype} on {x1.device}")
+    if a.shape != x1.shape or a.dtype != torch.bfloat16 or a.device != x1.device:
+        raise ContractError(f"a: bf16 {tuple(x1.shape)}, got {tuple(a.shape)} {a.dtype}")
+    if x.shape != x1.shape or x.dtype != torch.float32 or x.device != x1.device or not x.is_contiguous():
+        raise ContractError(f"x: contiguous float32 {tuple(x1.shape)} on {x1.device}")
+    if x.data_ptr() == x1.data_ptr():
+        raise ContractError("x must not be x1")
+    if flags is not None and (tuple(flags.shape) != tuple(x1.shape[:2]) or flags.dtype != torch.bool
+                              or flags.device != x1.device):
+        raise ContractError(f"flags: bool {tuple(x1.shape[:2])} on {x1.device}")
+    x1c, ac = x1.contiguous(), a.contiguous()
+    for name, t in (("x1", x1c), ("a", ac), ("x", x)):
+        if t.data_ptr() % 16:
+            raise ContractError(f"{name} must be 16-byte aligned")
+    fl = None if flags is None else flags.contiguous().view(torch.uint8)
+    b, n, d = x1.shape
+    with torch.cuda.device(x1.device):
+        _lib.call("vsp_residual_rows_where", x1c.data_ptr(), ac.data_ptr(), x.data_ptr(), _lib.ptr(fl), b * n, d,
+                  _lib.stream_of(x1.device))

@@ -116,3 +116,45 @@ extern "C" int vsp_halt_step(const uint8_t* active, const uint8_t* exits, int* n
                      reinterpret_cast<hipStream_t>(stream), active, exits, n_iters, halts, next, count);
   return check_launch(who);
 }
+
+namespace vsp {
+namespace {
+
+// The residual stream after a pass's attention, for the rows still in the loop: x[r] = x1[r] + a[r]
+// (x1 float32, a the attention's bf16 output, added in float32 as the column's residual add) where
+// flags[r] != 0 (every row when flags is NULL); other rows of x keep what they hold (the halted
+// tokens' carried hidden states, vesper/loop.py:452). One wave a row, 16-byte pieces.
+__global__ __launch_bounds__(256) void residual_rows_kernel(const float* __restrict__ x1, const __bf16* __restrict__ a,
+                                                            float* __restrict__ x, const uint8_t* __restrict__ flags,
+                                                            int rows, int d) {
+  const int row = blockIdx.x * 4 + (int)(threadIdx.x >> 6), lane = threadIdx.x & 63;
+  if (row >= rows) return;
+  if (flags != nullptr && flags[row] == 0) return;
+  const size_t base = (size_t)row * d;
+  for (int f = 8 * lane; f < d; f += 512) {
+    const float4 u = reinterpret_cast<const float4*>(x1 + base + f)[0];
+    const float4 w = reinterpret_cast<const float4*>(x1 + base + f)[1];
+    const bf16x8 r = *reinterpret_cast<const bf16x8*>(a + base + f);
+    reinterpret_cast<float4*>(x + base + f)[0] =
+        make_float4(u.x + (float)r[0], u.y + (float)r[1], u.z + (float)r[2], u.w + (float)r[3]);
+    reinterpret_cast<float4*>(x + base + f)[1] =
+        make_float4(w.x + (float)r[4], w.y + (float)r[5], w.z + (float)r[6], w.w + (float)r[7]);
+  }
+}
+
+}  // namespace
+}  // namespace vsp
+
+extern "C" int vsp_residual_rows_where(const float* x1, const void* a, float* x, const uint8_t* flags, int rows, int d,
+                                       void* stream) {
+  using namespace vsp;
+  const char* who = "vsp_residual_rows_where";
+  if (rows < 0 || d < 8 || d % 8 != 0) return fail(ERR_ARG, "%s: rows %d, width %d (a multiple of 8)", who, rows, d);
+  if (rows == 0) return OK;
+  if (!x1 || !a || !x) return fail(ERR_ARG, "%s: null pointer", who);
+  if ((reinterpret_cast<uintptr_t>(x1) | reinterpret_cast<uintptr_t>(a) | reinterpret_cast<uintptr_t>(x)) & 15)
+    return fail(ERR_ARG, "%s: x1, a and x must be 16-byte aligned", who);
+  hipLaunchKernelGGL(residual_rows_kernel, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0,
+                     reinterpret_cast<hipStream_t>(stream), x1, static_cast<const __bf16*>(a), x, flags, rows, d);
+  return check_launch(who);
+}

@@ -41,7 +41,7 @@ from torch import Tensor
 from vesper.attention import rotary_qk
 from vesper.column import recurrent_keys
 from vesper.contracts import ContractError, Dims, check_shape
-from vesper.kernels.carry import copy_rows_where, halt_step
+from vesper.kernels.carry import copy_rows_where, halt_step, residual_rows_where
 from vesper.kernels.delta_scan import delta_scan_fused
 from vesper.kernels.keys import fused_keys
 from vesper.kernels.norm import rms_norm_bf16
@@ -210,7 +210,10 @@ class LoopedColumn:
         return recurrent_keys(z, history, self.taps[t], self.heads, active=active, carried_z=carried_z)
 
     def _step(self, x: Tensor, t: int, state: Tensor, history: Tensor | None, active: Tensor | None,
-              carried: Written | None) -> tuple[Tensor, Tensor, Tensor | None, Written]:
+              carried: Written | None) -> tuple[tuple[Tensor, Tensor], Tensor, Tensor | None, Written]:
+        """One pass over ``x``; returns ``(x1, a)`` (the hidden state after the recurrent sublayer
+        and the attention's output: the pass's output is ``x1 + a``), the new state and history, and
+        the projections the pass wrote."""
         b, n, d = x.shape
         h, dk = self.heads, self.head_dim
         xb = rms_norm_bf16(x)
@@ -243,9 +246,8 @@ class LoopedColumn:
             a = window_attention(aq, ak, av, self.window, active=active, carried=(carried.attn_k, carried.attn_v))
         else:
             a = window_attention(aq, ak, av, self.window, active=active)
-        x2 = x1 + a.reshape(b, n, h * dk)
         written = Written(k=k, v=v, beta=beta, attn_k=ak, attn_v=av, z=z if self.taps is not None else None)
-        return x2, new_state, history, written
+        return (x1, a.reshape(b, n, h * dk)), new_state, history, written
 
     def forward(self, x0: Tensor, states: Sequence[Tensor], exits: Sequence[Tensor],
                 histories: Sequence[Tensor] | None = None) -> LoopResult:
@@ -286,21 +288,24 @@ class LoopedColumn:
                 # pass 0 runs with every token active: the unmasked kernels, as the reference's
                 # carry-free first pass
                 mask = None if carried is None else active
-                h, new_states[t], new_histories[t], written = self._step(x, t, new_states[t], new_histories[t], mask,
-                                                                         carried)
+                (x1, a), new_states[t], new_histories[t], written = self._step(x, t, new_states[t],
+                                                                               new_histories[t], mask, carried)
                 # halts = active & exit (all active on the last pass), n_iters += active, and the
                 # next pass's active & ~halts: one launch
                 halts, next_active = halt_step(active, exits[t] if t < self.passes - 1 else None, n_iters)
                 if carried is None:  # pass 0: every token active, the fresh projections are the carried ones
-                    carried, x = written, h
+                    carried = written
+                    x = torch.empty_like(x1)  # this loop's own buffer from here on
+                    residual_rows_where(x1, a, x, None)
                 elif self.copy_forward == "where":
+                    h = x1 + a
                     h = _where_tokens(active, h, torch.zeros_like(h))
                     carried = written.merged(halts, carried)
                     x = _where_tokens(active, h, x)
                 else:
                     # one launch: the tokens halting now freeze their fresh projections into the
-                    # carried buffers (none after the last pass), and the active tokens' hidden
-                    # states move into x (x is this loop's own buffer from pass 1 on)
+                    # carried buffers (none after the last pass); then the active tokens' hidden
+                    # states x1 + a go straight into x (this loop's own buffer from pass 1 on)
                     items: list[tuple[Tensor, Tensor, Tensor]] = []
                     if t < self.passes - 1:
                         items = [(written.k, carried.k, halts), (written.v, carried.v, halts),
@@ -308,7 +313,8 @@ class LoopedColumn:
                                  (written.attn_v, carried.attn_v, halts)]
                         if written.z is not None and carried.z is not None:
                             items.append((written.z, carried.z, halts))
-                    copy_rows_where([*items, (h, x, active)])
+                    copy_rows_where(items)
+                    residual_rows_where(x1, a, x, active)
                 active = next_active
         hist_out = tuple(t for t in new_histories if t is not None) if self.taps is not None else None
         return LoopResult(y=x, states=tuple(new_states), n_iters=n_iters, histories=hist_out)
