@@ -22,7 +22,7 @@
 extern "C" {
 #endif
 
-#define VSP_ABI_VERSION 19
+#define VSP_ABI_VERSION 20
 
 /* Status codes. */
 #define VSP_OK 0
@@ -428,6 +428,18 @@ int vsp_decode_proj_bf16(const float* x, const void* residual, float* sum_out, c
                          int used3, void* out0, void* out1, void* out2, void* out3, int sigmoid_block,
                          const int64_t* positions, const double* inv_freq, int rotate_mask, int rotary_dk,
                          void* stream);
+
+/* The same stacked projections for a prefill (the looped column's per-pass projections of M
+ * tokens' normalized input, vesper/column.py:192-260 and vesper/attention.py:269-292): for each of
+ * the nblk (1..4) weight blocks out_j = z W_j [:, :used_j] (bf16, [M, used_j] contiguous, fp32
+ * accumulation), z [M, d] bf16, W_j [d, cols] the block's weight passed transposed: weights_t
+ * [nblk, cols, d] bf16. Only the used columns are computed. Block sigmoid_block (or -1) is stored
+ * as the logistic of its bf16-rounded product, as vsp_decode_proj_bf16 stores it. d a multiple of
+ * 64 in 64..16384, 1 <= used_j <= cols, z and each weight block under 4 GiB (with a 256-row
+ * margin), z, weights_t and the outputs 16-byte aligned (the outputs may be NULL when M is 0). */
+int vsp_project_bf16(const void* z, const void* weights_t, int nblk, int cols, int d, int M, int used0, int used1,
+                     int used2, int used3, void* out0, void* out1, void* out2, void* out3, int sigmoid_block,
+                     void* stream);
 
 /* ---- copy-forward bookkeeping of the looped column ------------------------------------------
  * Replaces the row-wise `where` selects of vesper/loop.py:523-537 (`_merge`: tokens halting now

@@ -17,7 +17,7 @@ import torch
 HERE = Path(__file__).resolve().parent
 LIBRARY_PATH = HERE / "libvesper_kernels.so"
 HEADER_PATH = HERE.parents[2] / "include" / "vesper_kernels.h"
-ABI_VERSION = 19
+ABI_VERSION = 20
 
 P = ctypes.c_void_p
 I = ctypes.c_int
@@ -84,6 +84,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "vsp_residual_rows_where": (I, [P, P, P, P, I, I, P]),
     "vsp_delta_step_keys_bf16": (I, [P, P, P, P, P, P, I, P, P, P, P, I, I, I, P]),
     "vsp_decode_proj_bf16": (I, [P, P, P, P, P, I, I, I, I, I, I, I, I, P, P, P, P, I, P, P, I, I, P]),
+    "vsp_project_bf16": (I, [P, P, I, I, I, I, I, I, I, I, P, P, P, P, I, P]),
     "vsp_key_filter_backward_workspace_bytes": (Z, [I, I, I, I]),
     "vsp_key_filter_backward_bf16": (I, [P, P, P, P, P, P, P, P, Z, I, I, I, I, I, P]),
     "vsp_key_filter_backward_f16": (I, [P, P, P, P, P, P, P, P, Z, I, I, I, I, I, P]),

@@ -158,3 +158,52 @@ def decode_projection(x: Tensor, weights_t: Tensor, used: tuple[int, ...], *, re
                   p, cols, d, m, *widths, *ptrs, -1 if sigmoid_block is None else sigmoid_block,
                   _lib.ptr(rot_pos), _lib.ptr(rot_freq), rot_mask, rot_dk, _lib.stream_of(x.device))
     return outs
+
+
+def projection(z: Tensor, weights_t: Tensor, used: tuple[int, ...], *,
+               sigmoid_block: int | None = None) -> list[Tensor]:
+    """A prefill's sublayer projections in one launch (``vsp_project_bf16``): ``z W_j[:, :used_j]``
+    for each block of the stacked projection weight (``vesper/column.py:192-260``,
+    ``vesper/attention.py:269-292``), each block computed over the columns it uses only.
+
+    Args:
+        z: bf16 ``[M, d]``, the normalized input (one row a token), ``d`` a multiple of 64 in
+            64..16384.
+        weights_t: bf16 ``[p, cols, d]``: the stacked ``[p, d, cols]`` weight, each block transposed.
+        used: the columns kept of each of the ``p`` (1..4) blocks.
+        sigmoid_block: the block whose outputs pass through the logistic function (the write
+            strength), as ``decode_projection`` stores it.
+
+    Returns:
+        one bf16 ``[M, used_j]`` tensor per block.
+
+    Raises:
+        ContractError: on shapes, dtypes or devices outside that contract.
+    """
+    if z.dim() != 2 or z.dtype != torch.bfloat16 or z.device.type != "cuda":
+        raise ContractError(f"z: bf16 [M, d] on CUDA, got {tuple(z.shape)} {z.dtype} on {z.device}")
+    m, d = z.shape
+    if weights_t.dim() != 3 or weights_t.dtype != torch.bfloat16 or weights_t.shape[2] != d:
+        raise ContractError(f"weights_t: bf16 [p, cols, {d}], got {tuple(weights_t.shape)} {weights_t.dtype}")
+    if weights_t.device != z.device:
+        raise ContractError(f"weights_t is on {weights_t.device}, z on {z.device}")
+    p, cols = weights_t.shape[0], weights_t.shape[1]
+    if len(used) != p or not 1 <= p <= 4 or any(not 1 <= u <= cols for u in used):
+        raise ContractError(f"used: {p} widths in 1..{cols}, got {tuple(used)}")
+    if d % 64 or not 64 <= d <= 16384:
+        raise ContractError(f"z: width {d} is not a multiple of 64 in 64..16384")
+    if (m + 256) * d * 2 >= 1 << 32 or (cols + 256) * d * 2 >= 1 << 32:
+        raise ContractError(f"z [{m}, {d}] or a weight block of {cols} columns over 4 GiB")
+    if sigmoid_block is not None and not 0 <= sigmoid_block < p:
+        raise ContractError(f"sigmoid_block {sigmoid_block} is not one of the {p} blocks")
+    zc, wc = z.contiguous(), weights_t.contiguous()
+    for name, t in (("z", zc), ("weights_t", wc)):
+        if t.data_ptr() % 16:
+            raise ContractError(f"{name} must be 16-byte aligned")
+    outs = [torch.empty(m, u, dtype=torch.bfloat16, device=z.device) for u in used]
+    ptrs = [o.data_ptr() for o in outs] + [0] * (4 - p)
+    widths = list(used) + [1] * (4 - p)
+    with torch.cuda.device(z.device):
+        _lib.call("vsp_project_bf16", zc.data_ptr(), wc.data_ptr(), p, cols, d, m, *widths, *ptrs,
+                  -1 if sigmoid_block is None else sigmoid_block, _lib.stream_of(z.device))
+    return outs

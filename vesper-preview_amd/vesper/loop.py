@@ -5,13 +5,13 @@ a given exit trace (``TraceRule``, ``:203-240``), over a column reduced to its t
 order of ``Column.step`` (``vesper/column.py:709-812``):
 
 - recurrent sublayer: the pre-normalization (``RMSNorm`` with its gain at one, ``column.py:146-188``),
-  projections ``q, z, v, beta`` of the pass input (bf16 matmuls; the query
+  projections ``q, z, v, beta`` of the pass input (one ``vsp_project_bf16`` launch; the query
   is not normalized, ``column.py:247``; ``beta = sigmoid``), the key from the key input ``z`` (``normalize_keys``, after
   the causal key filter when the column has one, ``column.py:255-289``, with the pass's key
   history), the carry merges for halted tokens (their key input before the filter, ``k, v, beta``
   after, ``column.py:779-789``), the delta scan (``vsp_delta_scan_bf16`` with the active mask),
   the residual;
-- attention sublayer: the pre-normalization, projections, the rotary embedding of the queries and
+- attention sublayer: the pre-normalization, projections (one launch), the rotary embedding of the queries and
   keys at positions 0..n-1 (``attention.py:178-217, 292``; one launch, ``vsp_rotary_qk_bf16``), the
   carry merges of the attention keys and values
   (``column.py:795-796``), window attention over the chunk (``vsp_window_attn_bf16`` with the
@@ -44,7 +44,7 @@ from vesper.contracts import ContractError, Dims, check_shape
 from vesper.kernels.carry import copy_rows_where, halt_step, residual_rows_where
 from vesper.kernels.delta_scan import delta_scan_fused
 from vesper.kernels.keys import fused_keys
-from vesper.kernels.norm import rms_norm_bf16
+from vesper.kernels.norm import projection, rms_norm_bf16
 from vesper.kernels.window_attn import window_attention
 
 BF16 = torch.bfloat16
@@ -138,14 +138,27 @@ class LoopedColumn:
         self._decode_w: dict[int, tuple[Tensor, Tensor]] = {}
 
     def project_rec(self, t: int, xb: Tensor) -> tuple[Tensor, Tensor, Tensor, Tensor]:
-        """Pass ``t``'s recurrent projections of ``xb [b, n, d]`` (bf16), one batched GEMM:
+        """Pass ``t``'s recurrent projections of ``xb [b, n, d]`` (bf16), one launch:
         ``q_in [b, n, h*dk]`` (before normalization), ``z [b, n, h*dk]`` (the key input),
         ``v [b, n, h, dk]``, ``beta = sigmoid [b, n, h]``."""
         b, n, d = xb.shape
         h, dk = self.heads, self.head_dim
-        y = torch.matmul(xb.reshape(b * n, d), self.w_rec[t])  # [4, b*n, h*dk], each block contiguous
-        beta = torch.sigmoid(y[3][:, :h]).view(b, n, h)  # bf16 in and out, float32 inside
-        return y[0].view(b, n, h * dk), y[1].view(b, n, h * dk), y[2].view(b, n, h, dk), beta
+        hd = h * dk
+        q_in, z, v, beta = self._project(xb.reshape(b * n, d), t, 0, (hd, hd, hd, h), sigmoid_block=3)
+        return q_in.view(b, n, hd), z.view(b, n, hd), v.view(b, n, h, dk), beta.view(b, n, h)
+
+    def _project(self, xb: Tensor, t: int, which: int, used: tuple[int, ...],
+                 sigmoid_block: int | None = None) -> list[Tensor]:
+        """The blocks of pass ``t``'s stacked weight (``which``: 0 recurrent, 1 attention) applied
+        to ``xb [M, d]``, each as its own ``[M, used_j]`` tensor: one ``vsp_project_bf16`` launch
+        when ``d`` is a multiple of 64, else the batched library GEMM over the padded stack."""
+        if xb.shape[1] % 64 == 0:
+            return projection(xb, self.decode_weights(t)[which], used, sigmoid_block=sigmoid_block)
+        y = torch.matmul(xb, (self.w_rec if which == 0 else self.w_attn)[t])
+        outs = [y[j][:, :u].contiguous() for j, u in enumerate(used)]
+        if sigmoid_block is not None:  # bf16 in and out, float32 inside
+            outs[sigmoid_block] = torch.sigmoid(outs[sigmoid_block])
+        return outs
 
     def decode_weights(self, t: int) -> tuple[Tensor, Tensor]:
         """Pass ``t``'s stacked recurrent and attention weights with each block transposed
@@ -156,13 +169,13 @@ class LoopedColumn:
         return self._decode_w[t]
 
     def project_attn(self, t: int, xb: Tensor, pos: Tensor | None = None) -> tuple[Tensor, Tensor, Tensor]:
-        """Pass ``t``'s attention projections of ``xb [b, n, d]`` (bf16), one batched GEMM, with the
+        """Pass ``t``'s attention projections of ``xb [b, n, d]`` (bf16), one launch, with the
         queries and keys rotated at positions ``pos [b, n]`` (default ``0..n-1``) in one launch
         when the column has a rotary base (``WindowedAttention.project``, ``attention.py:269-292``)."""
         b, n, d = xb.shape
         h, hkv, dk = self.heads, self.kv_heads, self.head_dim
-        y = torch.matmul(xb.reshape(b * n, d), self.w_attn[t])
-        aq, ak = y[0].view(b, n, h, dk), y[1][:, :hkv * dk].reshape(b, n, hkv, dk)
+        yq, yk, yv = self._project(xb.reshape(b * n, d), t, 1, (h * dk, hkv * dk, hkv * dk))
+        aq, ak = yq.view(b, n, h, dk), yk.view(b, n, hkv, dk)
         if self.rotary_base is not None:
             if pos is None:
                 key = (b, n, xb.device)
@@ -171,7 +184,7 @@ class LoopedColumn:
                     pos = torch.arange(n, device=xb.device).expand(b, n).contiguous()
                     self._positions[key] = pos
             aq, ak = rotary_qk(aq, ak, pos, self.rotary_base)
-        return aq, ak, y[2][:, :hkv * dk].reshape(b, n, hkv, dk)
+        return aq, ak, yv.view(b, n, hkv, dk)
 
     @property
     def key_history(self) -> int:
