@@ -349,18 +349,19 @@ __device__ __forceinline__ void ut_solve(const typename Nat<E, DKP>::R (&kn)[4][
   }
   wave_sync();
 
-  // diagonal blocks: lane (blk, col) solves (I + A_bb) x = e_col by forward substitution
+  // diagonal blocks: lane (blk, col) solves (I + A_bb) x = e_col by forward substitution, column by
+  // column (once x_j is known it leaves every later row's sum, each row's terms in the order of j),
+  // so the rows' updates are independent and the dependent chain is 15 steps long
   {
     const int blk = g, col = lq;
     const float* ab = Ad + blk * 16 * TP;
     float x[16];
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      float sum = (i == col) ? 1.f : 0.f;
+    for (int i = 0; i < 16; ++i) x[i] = (i == col) ? 1.f : 0.f;
 #pragma unroll
-      for (int j = 0; j < i; ++j) sum -= ab[i * TP + j] * x[j];
-      x[i] = sum;
-    }
+    for (int j = 0; j < 16; ++j)
+#pragma unroll
+      for (int i = j + 1; i < 16; ++i) x[i] -= ab[i * TP + j] * x[j];
 #pragma unroll
     for (int i = 0; i < 16; ++i) Xd[blk * 16 * TP + i * TP + col] = x[i];
   }
