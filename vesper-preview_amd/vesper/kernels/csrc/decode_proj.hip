@@ -11,16 +11,20 @@
 //   z = RMSNorm(s) in bf16, the arithmetic of vsp_rms_norm_bf16 (bitwise the same z)
 //   y_j = z W_j for each block j of the stacked weight, only its first used_j columns
 //
-// Workgroup = 16 rows x 32 output columns of one block: four waves each normalize four of the
+// Workgroup = 16 rows x 32 output columns of one block: eight waves each normalize two of the
 // rows (one wave a row, as the norm kernel) into LDS, then each wave forms the 16x32 tile over
-// every fourth 32-wide step of the d inputs (16x16x32 bf16 MFMA, the transposed weight
-// [p, h*dk, d] giving the A fragments as 16-byte loads issued before the norm), and the four
+// every eighth 32-wide step of the d inputs (16x16x32 bf16 MFMA, the transposed weight
+// [p, h*dk, d] giving the A fragments as 16-byte loads issued before the norm), and the eight
 // partial tiles are summed in a fixed order through LDS. A block whose used width is narrow (the
 // write strength's h columns) takes one column group. One block may have its outputs passed
 // through the logistic function (the write strength, rounded to bf16 first as the separate
 // sigmoid would see it), and blocks may be rotated as they are stored (the attention's q and k:
 // a thread stores two adjacent columns of one token, a rotary pair, turned by the rotary kernel's
-// own arithmetic, so the result is bitwise the separate launch's).
+// own arithmetic, so the result is bitwise the separate launch's; its float64 cos and sin are
+// formed while the loads are in flight). The launch is a chain of latencies (timestamps per phase
+// in a timing copy, four waves: the loads 43 %, the norm of four rows a wave 36 %, the products
+// 10 %, the float64 cos and sin a further 13 % on the attention's launch): eight waves halve the
+// norm's rows a wave.
 #include "common.h"
 #include "rotary_math.h"
 #include "vesper_kernels.h"
@@ -31,6 +35,8 @@ namespace {
 constexpr float kProjRmsEps = 1e-6f;         // column.py:55
 constexpr float kProjRmsScaleFloor = 1e-3f;  // column.py:56
 constexpr int kMaxBlocks = 4;
+constexpr int kProjWaves = 8;                   // waves a workgroup
+constexpr int kProjRowsPerWave = 16 / kProjWaves;  // rows of the norm a wave takes
 
 struct ProjBlocks {
   int nblk;
@@ -40,7 +46,7 @@ struct ProjBlocks {
 };
 
 template <int NSEG>
-__global__ __launch_bounds__(256) void decode_proj_kernel(const float* __restrict__ x, const __bf16* __restrict__ res,
+__global__ __launch_bounds__(64 * kProjWaves) void decode_proj_kernel(const float* __restrict__ x, const __bf16* __restrict__ res,
                                                           float* __restrict__ sum_out, const float* __restrict__ gain,
                                                           const __bf16* __restrict__ wt, int M, int d, int cols,
                                                           ProjBlocks blk, int sig_block,
@@ -48,9 +54,9 @@ __global__ __launch_bounds__(256) void decode_proj_kernel(const float* __restric
                                                           const double* __restrict__ inv_freq, int rot_mask,
                                                           int rot_dk) {
   constexpr int PITCH = 512 * NSEG + 16;  // bf16 elements a row of z: rows 8 banks apart
-  constexpr int KSMAX = NSEG * 4;         // k steps of 32 a wave takes, at most
+  constexpr int KSMAX = 16 * NSEG / kProjWaves;  // k steps of 32 a wave takes, at most
   __shared__ __align__(16) __bf16 sz[16][PITCH];
-  __shared__ f32x4 part[4][2][64];
+  __shared__ f32x4 part[kProjWaves][2][64];
 
   const int gid = blockIdx.x, mb = blockIdx.y;
   int nb = 0;
@@ -59,7 +65,7 @@ __global__ __launch_bounds__(256) void decode_proj_kernel(const float* __restric
     if (j < blk.nblk && gid >= blk.start[j]) nb = j;
   const int c0 = (gid - blk.start[nb]) * 32;  // first output column of this workgroup in block nb
   const int w = threadIdx.x >> 6, l = threadIdx.x & 63, lq = l & 15, g = l >> 4;
-  const int ksteps = d / 32;  // wave w takes the steps w, w + 4, w + 8, ...
+  const int ksteps = d / 32;  // wave w takes the steps w, w + 8, w + 16, ...
 
   // the weight fragments first (they do not depend on x): A[n][k] = W_nb[k][c0 + 16 j + n] from the
   // transposed weight; columns past the block's width re-read its last row (never stored)
@@ -70,17 +76,32 @@ __global__ __launch_bounds__(256) void decode_proj_kernel(const float* __restric
     const __bf16* wr = wt + ((size_t)nb * cols + n) * d + 8 * g;
 #pragma unroll
     for (int i = 0; i < KSMAX; ++i)
-      if (w + 4 * i < ksteps) af[j][i] = *reinterpret_cast<const bf16x8*>(wr + 32 * (w + 4 * i));
+      if (w + kProjWaves * i < ksteps) af[j][i] = *reinterpret_cast<const bf16x8*>(wr + 32 * (w + kProjWaves * i));
   }
 
-  // the norm: wave w takes rows 4w .. 4w + 3 of the 16 (one wave a row, lane segments 8 (lane + 64 j));
+  // The store's thread: thread t < 256 stores two adjacent columns of one row (tile j = t / 128,
+  // lane ln = (t % 128) / 2: row lq, columns 4 g .. 4 g + 3; pair p = t % 2). A rotated block's cos
+  // and sin for that pair are formed now, while the loads are in flight.
+  const int t = threadIdx.x, j = (t >> 7) & 1, ln = (t & 127) >> 1, p = t & 1;
+  const int m = mb * 16 + (ln & 15);
+  const int col = c0 + 16 * j + 4 * (ln >> 4) + 2 * p;
+  const int used = blk.used[nb];
+  const bool rot = (rot_mask >> nb) & 1;
+  __bf16 rc = (__bf16)0.f, rs = (__bf16)0.f;
+  if (rot && t < 256 && m < M && col < used) {  // columns col, col + 1: pair (col % dk) / 2 of a head
+    const double angle = (double)pos[m] * inv_freq[(col % rot_dk) >> 1];
+    rc = rot_from_f64<__bf16>(cos(angle));
+    rs = rot_from_f64<__bf16>(sin(angle));
+  }
+
+  // the norm: wave w takes rows 2w, 2w + 1 of the 16 (one wave a row, lane segments 8 (lane + 64 j));
   // every row's loads are issued before the first row's reductions
-  constexpr int RA = NSEG == 1 ? 4 : (NSEG == 2 ? 2 : 1);  // rows whose loads are in flight together
-  for (int i0 = 0; i0 < 4; i0 += RA) {
+  constexpr int RA = NSEG <= 2 ? kProjRowsPerWave : 1;  // rows whose loads are in flight together
+  for (int i0 = 0; i0 < kProjRowsPerWave; i0 += RA) {
     float e[RA][NSEG][8];
 #pragma unroll
     for (int ii = 0; ii < RA; ++ii) {
-      const int m = mb * 16 + 4 * w + i0 + ii;
+      const int m = mb * 16 + kProjRowsPerWave * w + i0 + ii;
       const size_t ro = (size_t)min(m, M - 1) * d;  // rows past M read row M - 1 (never used)
 #pragma unroll
       for (int j = 0; j < NSEG; ++j) {
@@ -99,7 +120,7 @@ __global__ __launch_bounds__(256) void decode_proj_kernel(const float* __restric
     }
 #pragma unroll
     for (int ii = 0; ii < RA; ++ii) {
-      const int rl = 4 * w + i0 + ii, m = mb * 16 + rl;
+      const int rl = kProjRowsPerWave * w + i0 + ii, m = mb * 16 + rl;
       if (m >= M) {
 #pragma unroll
         for (int j = 0; j < NSEG; ++j) {
@@ -163,8 +184,8 @@ __global__ __launch_bounds__(256) void decode_proj_kernel(const float* __restric
   f32x4 acc[2] = {zero4(), zero4()};
 #pragma unroll
   for (int i = 0; i < KSMAX; ++i) {
-    if (w + 4 * i < ksteps) {
-      const bf16x8 bz = *reinterpret_cast<const bf16x8*>(&sz[lq][32 * (w + 4 * i) + 8 * g]);
+    if (w + kProjWaves * i < ksteps) {
+      const bf16x8 bz = *reinterpret_cast<const bf16x8*>(&sz[lq][32 * (w + kProjWaves * i) + 8 * g]);
 #pragma unroll
       for (int j = 0; j < 2; ++j) acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[j][i], bz, acc[j], 0, 0, 0);
     }
@@ -173,16 +194,11 @@ __global__ __launch_bounds__(256) void decode_proj_kernel(const float* __restric
   part[w][1][l] = acc[1];
   __syncthreads();
 
-  // the four waves' partial tiles summed in a fixed order; thread t stores two adjacent columns of
-  // one row: tile j = t / 128, lane ln = (t % 128) / 2 (row lq, columns 4 g .. 4 g + 3), pair p = t % 2
-  const int t = threadIdx.x, j = t >> 7, ln = (t & 127) >> 1, p = t & 1;
-  const int m = mb * 16 + (ln & 15);
-  const int col = c0 + 16 * j + 4 * (ln >> 4) + 2 * p;
-  const int used = blk.used[nb];
-  if (m < M && col < used) {
+  // the waves' partial tiles summed in a fixed order by the store's threads
+  if (t < 256 && m < M && col < used) {
     float y0 = 0.f, y1 = 0.f;
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
+    for (int q = 0; q < kProjWaves; ++q) {
       y0 += part[q][j][ln][2 * p];
       y1 += part[q][j][ln][2 * p + 1];
     }
@@ -191,10 +207,7 @@ __global__ __launch_bounds__(256) void decode_proj_kernel(const float* __restric
       b0 = (__bf16)(1.f / (1.f + expf(-(float)b0)));
       b1 = (__bf16)(1.f / (1.f + expf(-(float)b1)));
     }
-    if ((rot_mask >> nb) & 1) {  // columns col, col + 1: pair (col % dk) / 2 of a head
-      const double angle = (double)pos[m] * inv_freq[(col % rot_dk) >> 1];
-      rot_pair<__bf16>(b0, b1, rot_from_f64<__bf16>(cos(angle)), rot_from_f64<__bf16>(sin(angle)), b0, b1);
-    }
+    if (rot) rot_pair<__bf16>(b0, b1, rc, rs, b0, b1);
     __bf16* orow = blk.out[nb] + (size_t)m * used;
     orow[col] = b0;
     if (col + 1 < used) orow[col + 1] = b1;
@@ -251,13 +264,13 @@ extern "C" int vsp_decode_proj_bf16(const float* x, const void* residual, float*
   const __bf16* r = static_cast<const __bf16*>(residual);
   const __bf16* w = static_cast<const __bf16*>(weights_t);
   if (d <= 512)
-    hipLaunchKernelGGL(decode_proj_kernel<1>, grid, dim3(256), 0, s, x, r, sum_out, gain, w, M, d, cols, blk, sigmoid_block,
+    hipLaunchKernelGGL(decode_proj_kernel<1>, grid, dim3(64 * kProjWaves), 0, s, x, r, sum_out, gain, w, M, d, cols, blk, sigmoid_block,
                        positions, inv_freq, rotate_mask, rotary_dk);
   else if (d <= 1024)
-    hipLaunchKernelGGL(decode_proj_kernel<2>, grid, dim3(256), 0, s, x, r, sum_out, gain, w, M, d, cols, blk, sigmoid_block,
+    hipLaunchKernelGGL(decode_proj_kernel<2>, grid, dim3(64 * kProjWaves), 0, s, x, r, sum_out, gain, w, M, d, cols, blk, sigmoid_block,
                        positions, inv_freq, rotate_mask, rotary_dk);
   else
-    hipLaunchKernelGGL(decode_proj_kernel<4>, grid, dim3(256), 0, s, x, r, sum_out, gain, w, M, d, cols, blk, sigmoid_block,
+    hipLaunchKernelGGL(decode_proj_kernel<4>, grid, dim3(64 * kProjWaves), 0, s, x, r, sum_out, gain, w, M, d, cols, blk, sigmoid_block,
                        positions, inv_freq, rotate_mask, rotary_dk);
   return check_launch(who);
 }
