@@ -461,6 +461,20 @@ def test_fp32_every_gradient_matches_the_oracle_to_float32(b, n, h, dk):
     _grad_check(delta_scan_fused_fp32, _fp32_inputs(b, n, h, dk), TOL_FP32)
 
 
+# the shape the reference quotes both fused scans at (kernels/delta_scan.py:22-24, "stage-1 size":
+# b 32, n 88, h 2, dk 16), forward and every gradient against the float64 oracle; the reference
+# reports about 2e-7 relative for its fp32 scan there
+def test_the_reference_benchmark_shape_b32_n88_h2_d16():
+    from vesper.kernels.delta_scan import delta_scan_fused, delta_scan_fused_fp32
+
+    for fn, inputs, tol in ((delta_scan_fused, _bf16_inputs(32, 88, 2, 16, seed=88), TOL),
+                            (delta_scan_fused_fp32, _fp32_inputs(32, 88, 2, 16, seed=88), TOL_FP32)):
+        o, s = fn(*inputs)
+        o_ref, s_ref = _oracle(*inputs)
+        assert relative_error(o, o_ref) < tol and relative_error(s, s_ref) < tol
+        _grad_check(fn, inputs, tol)
+
+
 @pytest.mark.parametrize("dk", [16, 32, 64])
 def test_gradients_with_an_active_mask_and_every_width(dk):
     from vesper.kernels.delta_scan import delta_scan_fused_fp32

@@ -252,6 +252,18 @@ def test_the_gradients_at_t4096_w512_against_the_fp32_oracle_and_they_repeat():
         assert relative_error(a, b) < 1e-2, name
 
 
+# the shape the reference quotes its kernel at (kernels/window_attn.py:10-13: b 16, a 1024-token
+# chunk after a 512-row cache, 8 query heads over 2 KV heads, dk 64, window 512), forward and
+# every gradient against the float32 oracle (the reference reports 2-4e-3 relative for its kernel)
+def test_the_reference_benchmark_shape_b16_n1024_m512_h8_hkv2_d64():
+    q, keys, values = _inputs(16, 1024, 512, 8, 2, 64, seed=57)
+    up = torch.randn(16, 1024, 8, 64, generator=torch.Generator().manual_seed(58)).to(BF16)
+    got = _grads(q, keys, values, 512, up)
+    want = _oracle_grads(q, keys, values, 512, up, dtype=torch.float32)
+    for a, b, name in zip(got, want, ("o", "dq", "dk", "dv")):
+        assert relative_error(a, b) < 1e-2, (name, relative_error(a, b))
+
+
 def test_captured_forward_and_backward_equal_eager():
     from vesper.kernels.window_attn import window_attention
 
