@@ -146,6 +146,21 @@ def test_no_tokens_return_the_state_unchanged():
     assert o is q and s is h0
 
 
+def test_beta_one_with_the_key_as_query_reads_back_the_value_at_full_size():
+    # the delta rule's defining overwrite (reference tests/test_recurrence.py:48-56): with beta = 1,
+    # reading k right after writing (k, v) returns v whatever the state held, so o = v at every
+    # token of B8 T4096 H8 d64 (bf16 keys hold k.k = 1 only to their rounding, about 4e-3)
+    from vesper.kernels.delta_scan import delta_scan_fused, delta_scan_fused_fp32
+
+    _, k, v, beta, h0 = scan_inputs(8, 4096, 8, 64, seed=9)
+    k = normalize_keys(k)
+    ones = torch.ones_like(beta)
+    for fn, dtype, tol in ((delta_scan_fused, BF16, TOL), (delta_scan_fused_fp32, torch.float32, 1e-5)):
+        kd, vd = k.to(GPU, dtype), v.to(GPU, dtype)
+        o, _ = fn(kd, kd, vd, ones.to(GPU, dtype), h0.to(GPU))
+        assert relative_error(o, vd) < tol, (dtype, relative_error(o, vd))
+
+
 def test_refuses_what_the_contract_excludes():
     from vesper.contracts import ContractError
     from vesper.kernels.delta_scan import delta_scan_fused, delta_scan_fused_fp32
