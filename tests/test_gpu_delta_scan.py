@@ -161,6 +161,26 @@ def test_beta_one_with_the_key_as_query_reads_back_the_value_at_full_size():
         assert relative_error(o, vd) < tol, (dtype, relative_error(o, vd))
 
 
+def test_causality_holds_bitwise_at_full_size():
+    # later inputs never reach earlier outputs (the reference's causality property,
+    # tests/test_recurrence.py:30-104): inputs changed from token p on (inside a chunk) leave every
+    # output before p unchanged bit for bit, on both scan kernels at B8 T4096 H8 d64
+    from vesper.kernels.delta_scan import delta_scan_fused, delta_scan_fused_fp32
+
+    p = 2021
+    for fn, inputs in ((delta_scan_fused, _bf16_inputs(8, 4096, 8, 64, seed=21)),
+                       (delta_scan_fused_fp32, _fp32_inputs(8, 4096, 8, 64, seed=21))):
+        o, s = fn(*inputs)
+        q, k, v, beta, h0 = (t.clone() for t in inputs)
+        g = torch.Generator().manual_seed(22)
+        v[:, p:] += torch.randn(v[:, p:].shape, generator=g).to(GPU, v.dtype)
+        q[:, p:] = -q[:, p:]
+        beta[:, p:] = 1 - beta[:, p:]
+        o2, s2 = fn(q, k, v, beta, h0)
+        assert torch.equal(o2[:, :p], o[:, :p]) and not torch.equal(o2[:, p:], o[:, p:])
+        assert not torch.equal(s2, s)
+
+
 def test_refuses_what_the_contract_excludes():
     from vesper.contracts import ContractError
     from vesper.kernels.delta_scan import delta_scan_fused, delta_scan_fused_fp32

@@ -79,6 +79,29 @@ def test_headline_config_b4_t4096_h8_d64_w512():
     _check(got, want)
 
 
+def test_causality_and_the_window_edge_hold_bitwise_at_b4_t4096_h8_d64_w512():
+    # the reference's causality and window-boundary properties (tests/test_attention.py:58-147) at
+    # the attention config: keys and values changed from position p on leave every earlier query's
+    # output unchanged bit for bit, and changed before position p leave every query from p + w - 1 on
+    from vesper.kernels.window_attn import window_attention
+
+    q, keys, values = (t.to(GPU) for t in _inputs(4, 4096, 0, 8, 8, 64, seed=59))
+    base = window_attention(q, keys, values, 512)
+    p, w = 2000, 512
+    noise = torch.randn(keys.shape, generator=torch.Generator().manual_seed(60)).to(GPU, BF16)
+    late_k, late_v = keys.clone(), values.clone()
+    late_k[:, p:] += noise[:, p:]
+    late_v[:, p:] -= noise[:, p:]
+    after = window_attention(q, late_k, late_v, w)
+    assert torch.equal(after[:, :p], base[:, :p]) and not torch.equal(after[:, p:], base[:, p:])
+    early_k, early_v = keys.clone(), values.clone()
+    early_k[:, :p] += noise[:, :p]
+    early_v[:, :p] -= noise[:, :p]
+    after = window_attention(q, early_k, early_v, w)
+    assert torch.equal(after[:, p + w - 1:], base[:, p + w - 1:])
+    assert not torch.equal(after[:, p + w - 2], base[:, p + w - 2])
+
+
 def test_active_mask_skips_inactive_queries_only():
     from vesper.kernels.window_attn import window_attention
 
